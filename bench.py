@@ -1,0 +1,350 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X HERM hot path (one GPU).
+
+Headline ("C2"): one step = fused RMSNorm-SiLU of
+x bf16 [32768, 512] + surprise of 32768 tokens from fp32 logits [32768, 256]
++ admission above the 0.9 quantile of the scores. ``value`` is HERM tokens/s
+over K steps with every input resident in HBM. Each step reads a different
+one of several input sets (>= 512 MiB in total) so that the 256 MiB Infinity
+Cache cannot hold the working set; the step is captured once per input set in
+a HIP graph and replayed (its three kernels are launch-bound at this size).
+
+Also measured and reported (same JSON line, "kernels"): the C1/C3 affine scan,
+the C3 RMSNorm-SiLU, and the C4 MoE route/permute/grouped-GEMM/combine, each as
+average kernel time from HIP events, GB/s or TFLOP/s, and the roofline fraction.
+The CPU baseline is the oracle's single-threaded C port of the same C2 step
+(and, as an extra, the reference's PyTorch formulas on all host cores).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _path in (ROOT, ROOT / "koemi-5hom_amd"):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+C2_TOKENS = 16 * 2048
+
+# Algorithmic bytes / FLOPs per launch.
+C2_NORM_BYTES = 32768 * 512 * 2 * 2 + 512 * 2 + 32768 * 4            # x read, y write, gamma, inv
+C2_SURPRISE_BYTES = 32768 * 256 * 4 + 32768 * 8 + 32768 + 32768 * 4   # logits, targets, valid, s
+C2_ADMISSION_BYTES = 32768 * 4 + 32768 + 32768 + 4                     # s, valid, mask, tau
+C1_SCAN_BYTES = 12 * 4 * 1024 * 256 + 4 * 256 * 4
+C3_SCAN_BYTES = 12 * 32 * 4096 * 1024 + 32 * 1024 * 4
+C3_NORM_BYTES = 131072 * 1024 * 2 * 2 + 1024 * 2 + 131072 * 4
+C4_T, C4_D, C4_H, C4_E, C4_K = 32768, 1024, 2816, 16, 2
+C4_PAIRS = C4_T * C4_K
+C4_ROUTE_BYTES = C4_T * (8 + 8 + 1) + C4_PAIRS * 8
+C4_PERMUTE_BYTES = C4_T * C4_D * 2 + C4_PAIRS * C4_D * 2 + C4_PAIRS * 8 + C4_T + 2 * C4_PAIRS * 8 + (C4_E + 1) * 8
+C4_GEMM_FLOP = 6 * C4_D * C4_H * C4_PAIRS
+C4_COMBINE_BYTES = C4_PAIRS * C4_D * 2 + C4_T * C4_D * 2 + C4_PAIRS * 8 + (C4_E + 1) * 8
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="1,3,4", help="extra configurations to measure (comma list of 1,3,4; '' for none)")
+    ap.add_argument("--kernel-iters", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def roofline(achieved: float, peak: float, unit: str, bound: str, traffic) -> dict:
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if any."""
+
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.is_file():
+        return None
+    try:
+        return json.loads(path.read_text()).get(kernel, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures a single GPU: this build has no multi-GPU path and every box has one GPU; "
+              "run with --gpus 1", file=sys.stderr, flush=True)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from koemi_amd import core, dense, moe, think, workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stream = torch.cuda.current_stream(device)
+
+    def events_ms(fn, iters: int, warmup: int = 3) -> float:
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            fn()
+        end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) / iters
+
+    # ------------------------------------------------------------- headline C2
+    log("generating C2 input sets")
+    per_set = C2_NORM_BYTES + C2_SURPRISE_BYTES + C2_ADMISSION_BYTES
+    n_sets = max(2, math.ceil(512 * 2**20 / per_set))
+    sets = []
+    for i in range(n_sets):
+        c = workloads.config2(seed=1002 + i)
+        d = {
+            "x": c.x.to(device), "gamma": c.gamma.to(device), "logits": c.logits.to(device),
+            "targets": c.targets.to(device), "valid": c.valid.to(device),
+        }
+        sets.append(d)
+    eps, q = 1e-6, 0.9
+
+    def step(d):
+        y, inv = core.rmsnorm_silu_forward(d["x"], d["gamma"], eps)
+        s = think.surprise_from_logits(d["logits"], d["targets"], d["valid"])
+        mask, tau = think.salience_admission(s, d["valid"], quantile=q)
+        d["out"] = (y, inv, s, mask, tau)
+
+    # eager reference outputs for the graph check
+    for d in sets:
+        step(d)
+    torch.cuda.synchronize()
+    eager = [tuple(t.clone() for t in d["out"]) for d in sets]
+
+    log(f"capturing {n_sets} step graphs")
+    graphs = []
+    pool = torch.cuda.graph_pool_handle()
+    for d in sets:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=pool):
+            step(d)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for i, g in enumerate(graphs):  # every replay must reproduce the eager outputs
+        g.replay()
+        torch.cuda.synchronize()
+        for got, want in zip(sets[i]["out"], eager[i]):
+            assert torch.equal(got, want), "graph replay differs from the eager step"
+
+    for i in range(args.warmup):
+        graphs[i % n_sets].replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} C2 steps")
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(args.steps):
+        graphs[i % n_sets].replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(end)
+    ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
+    value = C2_TOKENS / (ms_per_step / 1000.0)
+    for i, g in enumerate(graphs[: min(2, n_sets)]):
+        for got, want in zip(sets[i]["out"], eager[i]):
+            assert torch.equal(got, want), "graph replay differs from the eager step after timing"
+
+    # Per-kernel times of the step, each replayed alone from its own graph.
+    def kernel_graph(fn_for_set):
+        gs = []
+        for d in sets:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                fn_for_set(d)
+            gs.append(g)
+        torch.cuda.synchronize()
+        counter = [0]
+
+        def replay():
+            gs[counter[0] % n_sets].replay()
+            counter[0] += 1
+
+        return events_ms(replay, max(args.steps, 50), warmup=5)
+
+    log("timing C2 kernels")
+    for d in sets:
+        d["s"] = d["out"][2]
+    c2_times = {
+        "rmsnorm_silu": kernel_graph(lambda d: core.rmsnorm_silu_forward(d["x"], d["gamma"], eps)),
+        "surprise_rows": kernel_graph(lambda d: think.surprise_from_logits(d["logits"], d["targets"], d["valid"])),
+        "quantile_admission": kernel_graph(lambda d: think.salience_admission(d["s"], d["valid"], quantile=q)),
+    }
+    c2_bytes = {"rmsnorm_silu": C2_NORM_BYTES, "surprise_rows": C2_SURPRISE_BYTES, "quantile_admission": C2_ADMISSION_BYTES}
+    kernels = {}
+    for name, ms in c2_times.items():
+        gbs = c2_bytes[name] / (ms / 1000.0) / 1e9
+        kernels[f"C2.{name}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    dominant = max(c2_times, key=c2_times.get)
+    dom_gbs = c2_bytes[dominant] / (c2_times[dominant] / 1000.0) / 1e9
+    eager_ms = events_ms(lambda: step(sets[0]), 20)
+    del graphs
+    for d in sets:
+        d.pop("out", None)
+
+    # ------------------------------------------------------------ other configs
+    extra = [c for c in args.configs.split(",") if c.strip()]
+    if "1" in extra:
+        log("C1 scan")
+        c1 = workloads.to_device(workloads.config1(), device)
+        g1 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g1, pool=pool):
+            dense.scan_forward(c1.retention, c1.increment, c1.initial)
+        ms = events_ms(g1.replay, 100)
+        kernels["C1.affine_scan"] = {"ms": round(ms, 5), "GB/s": round(C1_SCAN_BYTES / ms / 1e6, 1),
+                                     "frac_hbm": round(C1_SCAN_BYTES / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                     "note": "12.6 MB working set is launch-bound and fits the Infinity Cache"}
+        del c1, g1
+    if "3" in extra:
+        log("C3 scan + norm (generating 1 GiB of inputs)")
+        c3 = workloads.to_device(workloads.config3(), device)
+        ms = events_ms(lambda: dense.scan_forward(c3.retention, c3.increment, c3.initial), args.kernel_iters)
+        gbs = C3_SCAN_BYTES / ms / 1e6
+        kernels["C3.affine_scan"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                     "tokens_per_s": round(32 * 4096 / (ms / 1000.0))}
+        h = dense.scan_forward(c3.retention, c3.increment, c3.initial).to(torch.bfloat16).view(-1, 1024)
+        del c3
+        gamma = workloads.config3(batch=1, seq=1, width=1024).gamma.to(device)
+        ms = events_ms(lambda: core.rmsnorm_silu_forward(h, gamma, 1e-6), args.kernel_iters)
+        gbs = C3_NORM_BYTES / ms / 1e6
+        kernels["C3.rmsnorm_silu"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del h
+    if "4" in extra:
+        log("C4 MoE (generating inputs)")
+        c4 = workloads.to_device(workloads.config4(), device)
+        ms = events_ms(lambda: moe.route_topk_valid(c4.token_ids, c4.previous_token_ids, c4.valid, expert_count=16,
+                                                    top_k=2, validate=False), args.kernel_iters)
+        kernels["C4.route_hash"] = {"ms": round(ms, 5), "GB/s": round(C4_ROUTE_BYTES / ms / 1e6, 1)}
+        a_l, w_l = moe.route_topk_learned(c4.router_logits, c4.valid, top_k=2)
+        assign = moe.route_topk_valid(c4.token_ids, c4.previous_token_ids, c4.valid, expert_count=16, top_k=2)
+        ms = events_ms(lambda: moe.permute_topk(c4.context, assign, c4.valid, expert_count=16, validate=False), args.kernel_iters)
+        gbs = C4_PERMUTE_BYTES / ms / 1e6
+        kernels["C4.permute"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        sc, rows, experts, offsets, sw = moe.permute_topk(c4.context, a_l, c4.valid, expert_count=16, pair_weights=w_l)
+        weights = (c4.gate_weights, c4.gate_biases, c4.value_weights, c4.value_biases, c4.output_weights, c4.output_biases)
+        ms = events_ms(lambda: moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights, validate=False),
+                       max(5, args.kernel_iters // 2))
+        tflops = C4_GEMM_FLOP / ms / 1e9
+        kernels["C4.grouped_glu_ffn"] = {"ms": round(ms, 5), "TFLOP/s": round(tflops, 1),
+                                         "frac_mfma_bf16": round(tflops / BF16_PEAK_TFLOPS, 4)}
+        y = moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights, validate=False)
+        ms = events_ms(lambda: moe.combine_topk(y, rows, offsets, token_count=C4_T, top_k=2, pair_weights=sw,
+                                                validate=False), args.kernel_iters)
+        gbs = C4_COMBINE_BYTES / ms / 1e6
+        kernels["C4.combine"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        # practical bf16 GEMM ceiling of the platform library at the same total shape
+        a_mat = torch.randn((C4_PAIRS, C4_D), device=device, dtype=torch.bfloat16)
+        b_mat = torch.randn((C4_D, 2 * C4_H), device=device, dtype=torch.bfloat16)
+        ms = events_ms(lambda: torch.matmul(a_mat, b_mat), 10)
+        kernels["hipblaslt_reference_gemm"] = {"shape": [C4_PAIRS, C4_D, 2 * C4_H],
+                                               "TFLOP/s": round(2 * C4_PAIRS * C4_D * 2 * C4_H / ms / 1e9, 1)}
+        del c4, sc, y, a_mat, b_mat
+
+    # ------------------------------------------------------------ CPU baseline
+    cpu_baseline = None
+    extras = {}
+    if not args.no_cpu_baseline:
+        import oracle
+
+        log("CPU baseline (oracle C port, 1 thread)")
+        c = workloads.config2()
+        x32 = c.x.float().numpy()
+        g32 = c.gamma.float().numpy()
+        logits, targets, valid = c.logits.numpy(), c.targets.numpy(), c.valid.numpy()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.rmsnorm_silu_f32(x32, g32, eps)
+            s_cpu = oracle.surprise_rows(logits, targets, valid)
+            oracle.admission(s_cpu, valid, q=q)
+            reps += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= args.cpu_seconds or reps >= 1000:
+                break
+        cpu_value = reps * C2_TOKENS / elapsed
+        cpu_baseline = {"value": round(cpu_value, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+                        "sample": f"{reps} full C2 steps (32768 tokens each) with the oracle's C port, {elapsed:.1f} s"}
+        # the reference's PyTorch formulas on all host cores
+        import torch.nn.functional as F
+
+        threads = len(os.sched_getaffinity(0))
+        torch.set_num_threads(threads)
+        x_t, g_t = c.x.float(), c.gamma.float()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            F.silu(x_t * torch.rsqrt(x_t.square().mean(dim=-1, keepdim=True) + eps) * g_t)
+            nll = F.cross_entropy(c.logits, c.targets, reduction="none")
+            s_t = torch.where(c.valid, 1.0 - torch.exp(-(nll / math.log(256))), torch.zeros(()))
+            s_t > torch.quantile(s_t, q)
+            reps += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= args.cpu_seconds / 2 or reps >= 1000:
+                break
+        extras["cpu_torch_reference_formulas"] = {"value": round(reps * C2_TOKENS / elapsed, 1), "unit": "tokens/s",
+                                                  "cores": threads, "sample": f"{reps} C2 steps, fp32 torch CPU"}
+
+    result = {
+        "metric": "HERM tokens/s on 1 MI355X (C2: fused RMSNorm-SiLU + surprise + 0.9-quantile admission)",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: RMSNorm-SiLU of x bf16 [32768,512] (eps 1e-6) + surprise from logits fp32 [32768,256] "
+                        "+ admission above the 0.9 quantile; seeded inputs, rotated over "
+                        f"{n_sets} HBM-resident sets (> Infinity Cache); step = 3 kernels replayed from a HIP graph",
+            "tokens_per_step": C2_TOKENS,
+            "compute": "bf16 activations, fp32 arithmetic in every kernel",
+            "input_sets": n_sets,
+        },
+        "roofline": {**roofline(dom_gbs, HBM_PEAK_GBS, "GB/s", "hbm", load_traffic(f"C2.{dominant}")),
+                     "kernel": f"C2.{dominant}", "algorithmic_bytes": c2_bytes[dominant],
+                     "avg_ms": round(c2_times[dominant], 5)},
+        "cpu_baseline": cpu_baseline,
+        "eager_ms_per_step": round(eager_ms, 5),
+        "kernels": kernels,
+        **extras,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,214 @@
+/*
+ * koemi_hip.h — C ABI of the MI355X (gfx950) HERM hot-path kernels.
+ *
+ * Every entry point takes plain device pointers, element counts and an opaque
+ * HIP stream (a hipStream_t passed as void*; NULL is the null stream). Inputs
+ * are borrowed, outputs and workspaces are caller-allocated device memory. The
+ * library never allocates device memory itself: operations that need scratch
+ * space export a *_workspace_bytes() query and take a workspace pointer.
+ *
+ * All tensors are dense row-major and contiguous. Booleans are one byte
+ * (0 or 1, the torch.bool layout). Every entry point returns KOEMI_OK (0) or a
+ * KOEMI_ERR_* status; koemi_last_error() then returns a message for the
+ * calling host thread. Work is enqueued asynchronously on `stream`.
+ *
+ * Reference interfaces (Koemi-5HOM, src/koemi/cuda_kernels/...) that each
+ * group of entry points replaces are cited next to the declarations.
+ */
+#ifndef KOEMI_HIP_H
+#define KOEMI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the torch dtype each one mirrors in parentheses). */
+enum koemi_dtype {
+    KOEMI_F32 = 0,  /* torch.float32  */
+    KOEMI_F16 = 1,  /* torch.float16  */
+    KOEMI_BF16 = 2, /* torch.bfloat16 */
+    KOEMI_F64 = 3,  /* torch.float64  */
+    KOEMI_I32 = 4,  /* torch.int32    */
+    KOEMI_I64 = 5,  /* torch.int64    */
+    KOEMI_BOOL = 6  /* torch.bool     */
+};
+
+enum koemi_status {
+    KOEMI_OK = 0,
+    KOEMI_ERR_INVALID = 1,     /* argument violates the operator contract          */
+    KOEMI_ERR_UNSUPPORTED = 2, /* dtype / size outside what this build implements  */
+    KOEMI_ERR_LAUNCH = 3       /* the HIP runtime rejected a kernel launch          */
+};
+
+typedef void* koemi_stream_t;
+
+/* ABI version, mirrors KOEMI_CUDA_ABI_VERSION = 1
+ * (cuda_kernels/loader.py:32; core/rmsnorm_silu.cpp:74; moe/moe_kernels.cpp:257). */
+int koemi_abi_version(void);
+
+/* Message describing the last failure on the calling host thread ("" if none). */
+const char* koemi_last_error(void);
+
+/* ---------------------------------------------------------------- dense --- */
+/* Replaces the pybind `forward(a, b, h0) -> h` of dense/affine_scan.cu:119-167
+ * (front dense/affine_scan.py:51-98). h_t = a_t * h_{t-1} + b_t over t in
+ * [0, sequence), h_{-1} = initial. increment/states are [batch, sequence,
+ * features]; retention is the same shape, or [batch, sequence] when
+ * broadcast_retention != 0; initial is [batch, features]. dtype is one of
+ * F32/F16/BF16/F64; accumulation is fp32 (fp64 for F64). */
+int koemi_affine_scan_forward(const void* retention, const void* increment, const void* initial,
+                              void* states, int64_t batch, int64_t sequence, int64_t features,
+                              int broadcast_retention, int dtype, koemi_stream_t stream);
+
+/* Replaces the pybind `backward(a, h0, h, dh) -> (da, db, dh0)` of
+ * dense/affine_scan.cu:169-226. grad_retention is always full shape
+ * [batch, sequence, features]; the caller reduces it for broadcast retention
+ * (dense/affine_scan.py:233-255). */
+int koemi_affine_scan_backward(const void* retention, const void* initial, const void* states,
+                               const void* grad_states, void* grad_retention, void* grad_increment,
+                               void* grad_initial, int64_t batch, int64_t sequence,
+                               int64_t features, int broadcast_retention, int dtype,
+                               koemi_stream_t stream);
+
+/* ----------------------------------------------------------------- core --- */
+/* Replaces `rmsnorm_silu_forward(x, w, eps) -> [y, inverse_rms]` of
+ * core/rmsnorm_silu.cpp:56-59 / rmsnorm_silu.cu:203-217.
+ * inv = rsqrt(mean(x^2) + eps) per row (fp32), y = silu(x * inv * w).
+ * x, y: [rows, hidden]; weight: [hidden]; dtype F32/F16/BF16. */
+int koemi_rmsnorm_silu_forward(const void* input, const void* weight, void* output,
+                               float* inverse_rms, int64_t rows, int64_t hidden, double eps,
+                               int dtype, koemi_stream_t stream);
+
+/* Replaces `rmsnorm_silu_backward(g, x, w, inv, eps) -> [dx, dw]` of
+ * core/rmsnorm_silu.cpp:61-69 / rmsnorm_silu.cu:219-245. The weight gradient is
+ * reduced deterministically in two stages (no atomics) through the workspace. */
+size_t koemi_rmsnorm_silu_backward_workspace_bytes(int64_t rows, int64_t hidden);
+int koemi_rmsnorm_silu_backward(const void* grad_output, const void* input, const void* weight,
+                                const float* inverse_rms, void* grad_input, void* grad_weight,
+                                int64_t rows, int64_t hidden, int dtype, void* workspace,
+                                size_t workspace_bytes, koemi_stream_t stream);
+
+/* ---------------------------------------------------------------- think --- */
+/* Row kernel of think/surprise_kernel.cu:84-134 (`causal_surprise` forward
+ * after its logits GEMM). For each row r with valid[r]:
+ *   z_j = logits[r, j] (+ bias[j]),  nll = log(sum_j exp(z_j - max)) + max - z_t,
+ *   surprise[r] = 1 - exp(-nll / log_vocab);   invalid rows -> 0.
+ * logits fp32 [rows, vocab]; bias [vocab] of `dtype` or NULL; targets int64;
+ * surprise [rows] of `dtype` (F32/F16/BF16). The summation order and the
+ * exp/log routines are fixed (see surprise.hip), so results are reproducible
+ * bit for bit. log_vocab is float(log(vocab)) as the reference computes it. */
+int koemi_surprise_rows_forward(const float* logits, const void* bias, const int64_t* target_ids,
+                                const uint8_t* valid_mask, void* surprise, int64_t rows,
+                                int64_t vocab, float log_vocab, int dtype, koemi_stream_t stream);
+
+/* Row kernel of think/surprise_kernel.cu:136-192: d logits for an upstream
+ * gradient on surprise. grad_logits fp32 [rows, vocab]; invalid rows -> 0. */
+int koemi_surprise_rows_backward(const float* logits, const void* bias, const int64_t* target_ids,
+                                 const uint8_t* valid_mask, const void* grad_surprise,
+                                 float* grad_logits, int64_t rows, int64_t vocab, float log_vocab,
+                                 int dtype, koemi_stream_t stream);
+
+/* Salience admission with a fixed threshold (model/network.py:349):
+ * admission[i] = valid[i] && surprise[i] > threshold. surprise of `dtype`. */
+int koemi_admission_threshold(const void* surprise, const uint8_t* valid_mask, uint8_t* admission,
+                              int64_t count, float threshold, int dtype, koemi_stream_t stream);
+
+/* Admission at a quantile of the scores: tau = torch.quantile(surprise, q)
+ * with linear interpolation (rank = float(q) * (count - 1) in fp32), then
+ * admission[i] = valid[i] && surprise[i] > tau. tau is written to
+ * *threshold_out (device memory). Exact order-statistic selection on device,
+ * no host round trip. surprise fp32, count >= 1. */
+size_t koemi_admission_quantile_workspace_bytes(int64_t count);
+int koemi_admission_quantile(const float* surprise, const uint8_t* valid_mask, uint8_t* admission,
+                             float* threshold_out, int64_t count, float quantile, void* workspace,
+                             size_t workspace_bytes, koemi_stream_t stream);
+
+/* ------------------------------------------------------------------ moe --- */
+/* Replaces `route_topk(tok, prev, valid, E, k)` of moe/moe_kernels.cpp:193-201
+ * with the int64 semantics of the PyTorch oracle (model/experts.py:283-289):
+ * h = mix32(tok * 1000003 + prev * 97409); a[t, s] = (h + s * 0x9E3779B9) mod E
+ * for valid tokens, -1 otherwise. ids are I32 or I64 (`id_dtype`).
+ * *duplicate_flag (device int32, caller-zeroed) is set to 1 when a valid token
+ * received the same expert in two slots (moe/__init__.py:113-125, 171-175). */
+int koemi_moe_route_hash(const void* token_ids, const void* previous_token_ids,
+                         const uint8_t* valid_mask, int id_dtype, int64_t* assignments,
+                         int32_t* duplicate_flag, int64_t tokens, int64_t expert_count,
+                         int64_t top_k, koemi_stream_t stream);
+
+/* Learned top-k gate of model/router.py:46-49: p = softmax(logits) in fp32,
+ * (weights, assignments) = topk(p, k) in descending order, ties to the lower
+ * expert index; invalid tokens get assignment -1 and weight 0.
+ * router_logits fp32 [tokens, expert_count], expert_count <= 1024. */
+int koemi_moe_route_learned(const float* router_logits, const uint8_t* valid_mask,
+                            int64_t* assignments, float* weights, int64_t tokens,
+                            int64_t expert_count, int64_t top_k, koemi_stream_t stream);
+
+/* Contract checks of moe/__init__.py:113-125, 213-220 on device:
+ * flags[0] |= 1 if a valid assignment is outside [0, expert_count),
+ * flags[1] |= 1 if a valid token repeats an expert. flags: caller-zeroed int32[2]. */
+int koemi_moe_check_assignments(const void* assignments, int assignment_dtype,
+                                const uint8_t* valid_mask, int32_t* flags, int64_t tokens,
+                                int64_t top_k, int64_t expert_count, koemi_stream_t stream);
+
+/* Per-expert activation counts (model/network.py:48-70):
+ * counts[e] = #{(t, s): valid[t] && assignments[t, s] == e}. counts int64 [E]
+ * (overwritten; no zeroing needed). */
+int koemi_moe_expert_counts(const void* assignments, int assignment_dtype,
+                            const uint8_t* valid_mask, int64_t* counts, int64_t tokens,
+                            int64_t top_k, int64_t expert_count, koemi_stream_t stream);
+
+/* Replaces `permute_topk(ctx, assignments, valid, E)` of
+ * moe/moe_kernels.cu:390-499: pair key = expert (E for an invalid token, an
+ * out-of-range expert or a repeated slot); pairs are stably sorted by key;
+ * segment_offsets[E + 1] is the exclusive prefix of the per-expert counts
+ * (segment_offsets[E] = valid pairs); sorted_rows = pair / top_k;
+ * sorted_experts = key; sorted_context[i] = context[sorted_rows[i]] for
+ * i < segment_offsets[E], zero afterwards. pair_weights [tokens, top_k] fp32
+ * (or NULL) is permuted the same way into sorted_weights (0 past the valid
+ * pairs). Context dtype F32/F16/BF16; assignments I32/I64. expert_count <= 4095. */
+size_t koemi_moe_permute_workspace_bytes(int64_t tokens, int64_t top_k, int64_t expert_count);
+int koemi_moe_permute(const void* context, int context_dtype, const void* assignments,
+                      int assignment_dtype, const uint8_t* valid_mask, const float* pair_weights,
+                      void* sorted_context, int64_t* sorted_rows, int64_t* sorted_experts,
+                      int64_t* segment_offsets, float* sorted_weights, int64_t tokens,
+                      int64_t width, int64_t top_k, int64_t expert_count, void* workspace,
+                      size_t workspace_bytes, koemi_stream_t stream);
+
+/* Replaces `grouped_expert_mlp(...)` of moe/moe_kernels.cu:501-558: for each
+ * sorted pair i < segment_offsets[E] with expert e = sorted_experts[i]:
+ *   y_i = W_o[e] (silu(W_g[e] x_i + b_g[e]) * (W_v[e] x_i + b_v[e])) + b_o[e];
+ * rows past the valid pairs are zero. Weights: gate/value [E, hidden, width],
+ * their biases [E, hidden], output [E, width, hidden], its bias [E, width].
+ * BF16 runs on bf16 MFMA (fp32 accumulation, the GLU product rounded to bf16
+ * between the two GEMMs); F32/F16 run a fp32-accumulating scalar path.
+ * The tile scheduler reads segment_offsets on device (no host sync). */
+size_t koemi_moe_grouped_mlp_workspace_bytes(int64_t pairs, int64_t width, int64_t hidden,
+                                             int64_t expert_count, int dtype);
+int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* sorted_experts,
+                          const int64_t* segment_offsets, const void* gate_weights,
+                          const void* gate_biases, const void* value_weights,
+                          const void* value_biases, const void* output_weights,
+                          const void* output_biases, void* output, int64_t pairs, int64_t width,
+                          int64_t hidden, int64_t expert_count, int dtype, void* workspace,
+                          size_t workspace_bytes, koemi_stream_t stream);
+
+/* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
+ * without atomics: combined[t] = sum over the valid sorted pairs i of token t,
+ * in ascending i, of y_i * w_i in fp32, w_i = pair_weights[i] (sorted order)
+ * or 1/top_k when pair_weights is NULL; tokens without pairs get 0. Output in
+ * `dtype` (the expert_outputs dtype). num_segments = len(segment_offsets) - 1. */
+size_t koemi_moe_combine_workspace_bytes(int64_t tokens, int64_t top_k);
+int koemi_moe_combine(const void* expert_outputs, const int64_t* sorted_rows,
+                      const int64_t* segment_offsets, const float* pair_weights, void* combined,
+                      int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
+                      int64_t num_segments, int dtype, void* workspace, size_t workspace_bytes,
+                      koemi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KOEMI_HIP_H */

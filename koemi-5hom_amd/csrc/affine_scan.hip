@@ -1,0 +1,278 @@
+// Affine scan h_t = a_t * h_{t-1} + b_t for gfx950.
+//
+// Reference semantics: src/koemi/cuda_kernels/dense/affine_scan.cu:17-106 (one
+// thread walks one column through the whole sequence). Here the scan is
+// two-level so that a column is worked on by NSEG waves at once:
+//
+//   * A workgroup owns 64 consecutive state columns of one batch row (lane =
+//     column, so every global access of a wave is one contiguous 64-element
+//     row segment) and walks the sequence in chunks of CH = NSEG * S steps.
+//   * Inside a chunk, wave w scans its S consecutive steps serially in
+//     registers, producing the segment transfer (P = prod a, B = local scan).
+//   * The NSEG segment transfers are composed through LDS,
+//     (a2, b2) o (a1, b1) = (a2 a1, a2 b1 + b2), starting from the carried
+//     state of the previous chunk, which stays in a register for the whole
+//     sequence (no inter-workgroup traffic, no second pass over a and b).
+//   * The next chunk's a/b are loaded before the current chunk is combined, so
+//     two chunks of loads are in flight per wave.
+//
+// HBM traffic is the algorithmic minimum: read a and b once, write h once.
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+constexpr int kScanSteps = 8;     // S: serial steps per wave per chunk
+constexpr int kScanSegments = 8;  // NSEG: waves per workgroup
+
+template <typename T, typename A, int S, bool BCAST>
+__device__ __forceinline__ void scan_load(const T* __restrict__ a_col, const T* __restrict__ b_col,
+                                          int64_t a_stride, int64_t F, int64_t L, int64_t t_first,
+                                          bool col_ok, A (&ra)[S], A (&rb)[S]) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const int64_t t = t_first + i;
+        const bool ok = col_ok && t < L;
+        ra[i] = ok ? static_cast<A>(a_col[t * a_stride]) : A(1);
+        rb[i] = ok ? static_cast<A>(b_col[t * F]) : A(0);
+    }
+}
+
+template <typename T, int S, int NSEG, bool BCAST>
+__global__ __launch_bounds__(kWave * NSEG) void scan_forward_kernel(
+    const T* __restrict__ a, const T* __restrict__ b, const T* __restrict__ h0, T* __restrict__ h,
+    int64_t L, int64_t F, int64_t col_tiles) {
+    using A = typename AccOf<T>::type;
+    constexpr int CH = S * NSEG;
+    __shared__ A seg_p[NSEG][kWave];
+    __shared__ A seg_b[NSEG][kWave];
+
+    const int lane = lane_id();
+    const int seg = static_cast<int>(threadIdx.x) / kWave;
+    const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
+    const int64_t f = (static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane;
+    const bool col_ok = f < F;
+    const int64_t fc = col_ok ? f : 0;
+
+    const T* a_col = BCAST ? a + bi * L : a + bi * L * F + fc;
+    const int64_t a_stride = BCAST ? 1 : F;
+    const T* b_col = b + bi * L * F + fc;
+    T* h_col = h + bi * L * F + fc;
+
+    A carry = col_ok ? static_cast<A>(h0[bi * F + fc]) : A(0);
+
+    A ra[S], rb[S], na[S], nb[S];
+    scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, static_cast<int64_t>(seg) * S, col_ok,
+                              ra, rb);
+    for (int64_t t0 = 0; t0 < L; t0 += CH) {
+        const int64_t t_seg = t0 + static_cast<int64_t>(seg) * S;
+        const bool more = t0 + CH < L;
+        if (more) {
+            scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, t_seg + CH, col_ok, na, nb);
+        }
+        // Segment-local inclusive scan from a zero state: (prod a, local h).
+        A p = A(1), q = A(0);
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            q = ra[i] * q + rb[i];
+            p = p * ra[i];
+            ra[i] = p;
+            rb[i] = q;
+        }
+        seg_p[seg][lane] = p;
+        seg_b[seg][lane] = q;
+        __syncthreads();
+        // Compose the carried state through the segments before this one.
+        A c = carry, c_in = carry;
+#pragma unroll
+        for (int j = 0; j < NSEG; ++j) {
+            if (j == seg) c_in = c;
+            c = seg_p[j][lane] * c + seg_b[j][lane];
+        }
+        carry = c;
+        if (col_ok) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const int64_t t = t_seg + i;
+                if (t < L) h_col[t * F] = static_cast<T>(ra[i] * c_in + rb[i]);
+            }
+        }
+        __syncthreads();
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                ra[i] = na[i];
+                rb[i] = nb[i];
+            }
+        }
+    }
+}
+
+// Reverse-time adjoint of the scan (dense/affine_scan.cu:58-106):
+//   g_t = dh_t + a_{t+1} g_{t+1},  db_t = g_t,  da_t = g_t h_{t-1},  dh0 = a_0 g_0.
+// In reversed time u = L-1-t this is a forward scan with coefficient a_{t+1}
+// and increment dh_t, so it reuses the same two-level structure.
+template <typename T, int S, int NSEG, bool BCAST>
+__global__ __launch_bounds__(kWave * NSEG) void scan_backward_kernel(
+    const T* __restrict__ a, const T* __restrict__ h0, const T* __restrict__ h,
+    const T* __restrict__ dh, T* __restrict__ da, T* __restrict__ db, T* __restrict__ dh0,
+    int64_t L, int64_t F, int64_t col_tiles) {
+    using A = typename AccOf<T>::type;
+    constexpr int CH = S * NSEG;
+    __shared__ A seg_p[NSEG][kWave];
+    __shared__ A seg_b[NSEG][kWave];
+
+    const int lane = lane_id();
+    const int seg = static_cast<int>(threadIdx.x) / kWave;
+    const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
+    const int64_t f = (static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane;
+    const bool col_ok = f < F;
+    const int64_t fc = col_ok ? f : 0;
+
+    const T* a_col = BCAST ? a + bi * L : a + bi * L * F + fc;
+    const int64_t a_stride = BCAST ? 1 : F;
+    const int64_t base = bi * L * F + fc;
+    const A h_init = col_ok ? static_cast<A>(h0[bi * F + fc]) : A(0);
+
+    A carry = A(0);
+    for (int64_t u0 = 0; u0 < L; u0 += CH) {
+        const int64_t u_seg = u0 + static_cast<int64_t>(seg) * S;
+        A ra[S], rb[S], hp[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const int64_t t = L - 1 - (u_seg + i);
+            const bool ok = col_ok && t >= 0;
+            ra[i] = (ok && t + 1 < L) ? static_cast<A>(a_col[(t + 1) * a_stride]) : A(1);
+            rb[i] = ok ? static_cast<A>(dh[base + t * F]) : A(0);
+            hp[i] = ok ? (t > 0 ? static_cast<A>(h[base + (t - 1) * F]) : h_init) : A(0);
+        }
+        A p = A(1), q = A(0);
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            q = ra[i] * q + rb[i];
+            p = p * ra[i];
+            ra[i] = p;
+            rb[i] = q;
+        }
+        seg_p[seg][lane] = p;
+        seg_b[seg][lane] = q;
+        __syncthreads();
+        A c = carry, c_in = carry;
+#pragma unroll
+        for (int j = 0; j < NSEG; ++j) {
+            if (j == seg) c_in = c;
+            c = seg_p[j][lane] * c + seg_b[j][lane];
+        }
+        carry = c;
+        if (col_ok) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const int64_t t = L - 1 - (u_seg + i);
+                if (t >= 0) {
+                    const A g = ra[i] * c_in + rb[i];
+                    db[base + t * F] = static_cast<T>(g);
+                    da[base + t * F] = static_cast<T>(g * hp[i]);
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (col_ok && seg == 0) {
+        dh0[bi * F + fc] = static_cast<T>(static_cast<A>(a_col[0]) * carry);
+    }
+}
+
+template <typename T, bool BCAST>
+int launch_forward(const void* a, const void* b, const void* h0, void* h, int64_t B, int64_t L,
+                   int64_t F, hipStream_t stream) {
+    const int64_t col_tiles = (F + kWave - 1) / kWave;
+    const int64_t blocks = B * col_tiles;
+    if (blocks > 0x7fffffff) return fail(KOEMI_ERR_UNSUPPORTED, "affine scan grid too large");
+    hipLaunchKernelGGL((scan_forward_kernel<T, kScanSteps, kScanSegments, BCAST>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kWave * kScanSegments), 0, stream,
+                       static_cast<const T*>(a), static_cast<const T*>(b),
+                       static_cast<const T*>(h0), static_cast<T*>(h), L, F, col_tiles);
+    return check_launch("koemi_affine_scan_forward");
+}
+
+template <typename T, bool BCAST>
+int launch_backward(const void* a, const void* h0, const void* h, const void* dh, void* da,
+                    void* db, void* dh0, int64_t B, int64_t L, int64_t F, hipStream_t stream) {
+    const int64_t col_tiles = (F + kWave - 1) / kWave;
+    const int64_t blocks = B * col_tiles;
+    if (blocks > 0x7fffffff) return fail(KOEMI_ERR_UNSUPPORTED, "affine scan grid too large");
+    hipLaunchKernelGGL((scan_backward_kernel<T, kScanSteps, kScanSegments, BCAST>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(kWave * kScanSegments), 0, stream,
+                       static_cast<const T*>(a), static_cast<const T*>(h0),
+                       static_cast<const T*>(h), static_cast<const T*>(dh), static_cast<T*>(da),
+                       static_cast<T*>(db), static_cast<T*>(dh0), L, F, col_tiles);
+    return check_launch("koemi_affine_scan_backward");
+}
+
+int check_scan_args(const void* a, const void* b, const void* h0, const void* h, int64_t B,
+                    int64_t L, int64_t F, int dtype) {
+    if (B < 0 || L < 0 || F < 0) return fail(KOEMI_ERR_INVALID, "affine scan sizes must be non-negative");
+    if (dtype != KOEMI_F32 && dtype != KOEMI_F64 && dtype != KOEMI_F16 && dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "affine scan does not support dtype %s", dtype_name(dtype));
+    if (B * L * F > 0 && (!a || !b || !h0 || !h))
+        return fail(KOEMI_ERR_INVALID, "affine scan received a null pointer");
+    return KOEMI_OK;
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_affine_scan_forward(const void* retention, const void* increment,
+                                         const void* initial, void* states, int64_t batch,
+                                         int64_t sequence, int64_t features,
+                                         int broadcast_retention, int dtype,
+                                         koemi_stream_t stream) {
+    int st = check_scan_args(retention, increment, initial, states, batch, sequence, features, dtype);
+    if (st != KOEMI_OK) return st;
+    if (batch * sequence * features == 0) return KOEMI_OK;
+    hipStream_t s = as_stream(stream);
+    const bool bc = broadcast_retention != 0;
+    switch (dtype) {
+        case KOEMI_F32:
+            return bc ? launch_forward<float, true>(retention, increment, initial, states, batch, sequence, features, s)
+                      : launch_forward<float, false>(retention, increment, initial, states, batch, sequence, features, s);
+        case KOEMI_F64:
+            return bc ? launch_forward<double, true>(retention, increment, initial, states, batch, sequence, features, s)
+                      : launch_forward<double, false>(retention, increment, initial, states, batch, sequence, features, s);
+        case KOEMI_F16:
+            return bc ? launch_forward<f16, true>(retention, increment, initial, states, batch, sequence, features, s)
+                      : launch_forward<f16, false>(retention, increment, initial, states, batch, sequence, features, s);
+        default:
+            return bc ? launch_forward<bf16, true>(retention, increment, initial, states, batch, sequence, features, s)
+                      : launch_forward<bf16, false>(retention, increment, initial, states, batch, sequence, features, s);
+    }
+}
+
+extern "C" int koemi_affine_scan_backward(const void* retention, const void* initial,
+                                          const void* states, const void* grad_states,
+                                          void* grad_retention, void* grad_increment,
+                                          void* grad_initial, int64_t batch, int64_t sequence,
+                                          int64_t features, int broadcast_retention, int dtype,
+                                          koemi_stream_t stream) {
+    int st = check_scan_args(retention, states, initial, grad_states, batch, sequence, features, dtype);
+    if (st != KOEMI_OK) return st;
+    if (batch * sequence * features > 0 && (!grad_retention || !grad_increment || !grad_initial))
+        return fail(KOEMI_ERR_INVALID, "affine scan backward received a null gradient pointer");
+    if (batch * sequence * features == 0) return KOEMI_OK;
+    hipStream_t s = as_stream(stream);
+    const bool bc = broadcast_retention != 0;
+#define KOEMI_SCAN_BWD(T)                                                                          \
+    (bc ? launch_backward<T, true>(retention, initial, states, grad_states, grad_retention,        \
+                                   grad_increment, grad_initial, batch, sequence, features, s)    \
+        : launch_backward<T, false>(retention, initial, states, grad_states, grad_retention,       \
+                                    grad_increment, grad_initial, batch, sequence, features, s))
+    switch (dtype) {
+        case KOEMI_F32: return KOEMI_SCAN_BWD(float);
+        case KOEMI_F64: return KOEMI_SCAN_BWD(double);
+        case KOEMI_F16: return KOEMI_SCAN_BWD(f16);
+        default: return KOEMI_SCAN_BWD(bf16);
+    }
+#undef KOEMI_SCAN_BWD
+}

@@ -1,0 +1,96 @@
+// Shared device/host helpers for the gfx950 HERM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/koemi_hip.h"
+
+namespace koemi {
+
+// ----------------------------------------------------------------- errors ---
+// Per-host-thread message for koemi_last_error(); set_error returns the status
+// so entry points can `return fail(...)`.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+template <typename... Args>
+inline int fail(int status, const char* fmt, Args... args) {
+    set_error(fmt, args...);
+    return status;
+}
+inline int fail(int status, const char* msg) {
+    set_error("%s", msg);
+    return status;
+}
+
+// Checks the launch that was just enqueued.
+inline int check_launch(const char* what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        return fail(KOEMI_ERR_LAUNCH, "%s: kernel launch failed: %s", what, hipGetErrorString(err));
+    }
+    return KOEMI_OK;
+}
+
+inline hipStream_t as_stream(koemi_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------ element types ---
+using bf16 = __bf16;
+using f16 = _Float16;
+
+template <typename T> struct AccOf { using type = float; };
+template <> struct AccOf<double> { using type = double; };
+
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// ------------------------------------------------------------ wave helpers ---
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ float wave_sum_xor(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max_xor(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+__device__ __forceinline__ uint64_t lanemask_lt() {
+    const int l = lane_id();
+    return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+// Number of blocks for `items` work items of `per_block` each, clamped to a grid size
+// the runtime accepts.
+inline unsigned grid_for(int64_t items, int64_t per_block) {
+    int64_t b = (items + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    return static_cast<unsigned>(b);
+}
+
+inline bool float_dtype(int dt) { return dt == KOEMI_F32 || dt == KOEMI_F16 || dt == KOEMI_BF16; }
+inline bool index_dtype(int dt) { return dt == KOEMI_I32 || dt == KOEMI_I64; }
+inline const char* dtype_name(int dt) {
+    switch (dt) {
+        case KOEMI_F32: return "float32";
+        case KOEMI_F16: return "float16";
+        case KOEMI_BF16: return "bfloat16";
+        case KOEMI_F64: return "float64";
+        case KOEMI_I32: return "int32";
+        case KOEMI_I64: return "int64";
+        case KOEMI_BOOL: return "bool";
+        default: return "unknown";
+    }
+}
+
+}  // namespace koemi

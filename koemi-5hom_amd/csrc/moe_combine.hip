@@ -1,0 +1,188 @@
+// Deterministic MoE combine for gfx950.
+//
+// Reference: cuda_kernels/moe/moe_kernels.cu:201-229, 560-582 — fp32 atomicAdd
+// of y / top_k into a zeroed fp32 [tokens, width] buffer, then a cast. That
+// costs a zero-fill, read-modify-write atomics and a cast pass, and the sum
+// order depends on scheduling for top_k > 2. Here:
+//
+//   1. invert sorted_rows: each valid sorted position i records itself under
+//      its token (one int atomic per pair, used only to claim a slot);
+//   2. one wave per token sorts its (at most top_k) positions ascending, sums
+//      y_i * w_i in fp32 in that order and writes the row once in the output
+//      dtype.
+//
+// HBM traffic is one read of every valid expert output row and one write of
+// every token row.
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+constexpr int kCombineWaves = 4;
+constexpr int kMaxTopK = 256;
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+__global__ void zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+__global__ void invert_rows_kernel(const int64_t* __restrict__ sorted_rows, const int64_t* __restrict__ valid_end,
+                                   int32_t* __restrict__ cnt, int64_t* __restrict__ pos, int64_t pairs, int64_t tokens,
+                                   int64_t k) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t valid = min(*valid_end, pairs);
+    if (i >= valid) return;
+    const int64_t t = sorted_rows[i];
+    if (t < 0 || t >= tokens) return;
+    const int32_t slot = atomicAdd(&cnt[t], 1);
+    if (slot < k) pos[t * k + slot] = i;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kWave * kCombineWaves) void combine_rows_kernel(
+    const T* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
+    const float* __restrict__ pair_w, T* __restrict__ out, int64_t tokens, int64_t k, int64_t D) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
+    if (t >= tokens) return;
+    const int lane = lane_id();
+    const int n = min(static_cast<int64_t>(cnt[t]), k);
+    const int64_t* mine = pos + t * k;
+    const float inv_k_div = static_cast<float>(k);
+    if constexpr (VEC) {
+        constexpr int N = 16 / sizeof(T);
+        union V {
+            uint4 raw;
+            T e[N];
+        };
+        const int64_t nvec = D / N;
+        for (int64_t v0 = 0; v0 < nvec; v0 += 2 * kWave) {
+            float acc[2][N];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int q = 0; q < N; ++q) acc[u][q] = 0.0f;
+            int64_t last = -1;
+            for (int r = 0; r < n; ++r) {
+                // r-th smallest position of this token (n <= k, k small).
+                int64_t best = INT64_MAX;
+                for (int j = 0; j < n; ++j) {
+                    const int64_t pj = mine[j];
+                    if (pj > last && pj < best) best = pj;
+                }
+                last = best;
+                const float w = pair_w ? pair_w[best] : 0.0f;
+                const T* row = y + best * D;
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int64_t v = v0 + u * kWave + lane;
+                    if (v < nvec) {
+                        V in;
+                        in.raw = reinterpret_cast<const uint4*>(row)[v];
+#pragma unroll
+                        for (int q = 0; q < N; ++q) {
+                            const float f = to_f32(in.e[q]);
+                            acc[u][q] += pair_w ? f * w : f / inv_k_div;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int64_t v = v0 + u * kWave + lane;
+                if (v < nvec) {
+                    V o;
+#pragma unroll
+                    for (int q = 0; q < N; ++q) o.e[q] = from_f32<T>(acc[u][q]);
+                    reinterpret_cast<uint4*>(out + t * D)[v] = o.raw;
+                }
+            }
+        }
+    } else {
+        for (int64_t c = lane; c < D; c += kWave) {
+            float acc = 0.0f;
+            int64_t last = -1;
+            for (int r = 0; r < n; ++r) {
+                int64_t best = INT64_MAX;
+                for (int j = 0; j < n; ++j) {
+                    const int64_t pj = mine[j];
+                    if (pj > last && pj < best) best = pj;
+                }
+                last = best;
+                const float f = to_f32(y[best * D + c]);
+                acc += pair_w ? f * pair_w[best] : f / inv_k_div;
+            }
+            out[t * D + c] = from_f32<T>(acc);
+        }
+    }
+}
+
+struct CombineWorkspace {
+    size_t cnt_off, pos_off, total;
+};
+inline CombineWorkspace combine_workspace(int64_t tokens, int64_t k) {
+    CombineWorkspace w;
+    w.cnt_off = 0;
+    w.pos_off = align256(static_cast<size_t>(tokens) * sizeof(int32_t));
+    w.total = w.pos_off + align256(static_cast<size_t>(tokens) * static_cast<size_t>(k) * sizeof(int64_t));
+    return w;
+}
+
+template <typename T>
+int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, const float* pair_w, void* out,
+                        int64_t tokens, int64_t k, int64_t D, hipStream_t s) {
+    const bool vec = (D * static_cast<int64_t>(sizeof(T))) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+    if (vec)
+        hipLaunchKernelGGL((combine_rows_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(y), cnt, pos, pair_w,
+                           static_cast<T*>(out), tokens, k, D);
+    else
+        hipLaunchKernelGGL((combine_rows_kernel<T, false>), grid, block, 0, s, static_cast<const T*>(y), cnt, pos, pair_w,
+                           static_cast<T*>(out), tokens, k, D);
+    return check_launch("koemi_moe_combine(rows)");
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" size_t koemi_moe_combine_workspace_bytes(int64_t tokens, int64_t top_k) {
+    if (tokens < 1 || top_k < 1) return 0;
+    return combine_workspace(tokens, top_k).total;
+}
+
+extern "C" int koemi_moe_combine(const void* expert_outputs, const int64_t* sorted_rows,
+                                 const int64_t* segment_offsets, const float* pair_weights, void* combined,
+                                 int64_t pairs, int64_t width, int64_t tokens, int64_t top_k, int64_t num_segments,
+                                 int dtype, void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    if (tokens < 1 || width < 1 || pairs < 0) return fail(KOEMI_ERR_INVALID, "combine needs tokens >= 1, width >= 1");
+    if (top_k < 1 || top_k > kMaxTopK) return fail(KOEMI_ERR_INVALID, "top_k must be in [1, %d]", kMaxTopK);
+    if (num_segments < 1) return fail(KOEMI_ERR_INVALID, "segment_offsets must have at least two entries");
+    if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "combine does not support dtype %s", dtype_name(dtype));
+    if (!segment_offsets || !combined || (pairs > 0 && (!expert_outputs || !sorted_rows)))
+        return fail(KOEMI_ERR_INVALID, "combine received a null pointer");
+    const CombineWorkspace ws = combine_workspace(tokens, top_k);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "combine workspace too small: need %zu bytes", ws.total);
+    char* base = static_cast<char*>(workspace);
+    int32_t* cnt = reinterpret_cast<int32_t*>(base + ws.cnt_off);
+    int64_t* pos = reinterpret_cast<int64_t*>(base + ws.pos_off);
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(tokens, 256)), dim3(256), 0, s, cnt, tokens);
+    int st = check_launch("koemi_moe_combine(zero)");
+    if (st != KOEMI_OK) return st;
+    if (pairs > 0) {
+        hipLaunchKernelGGL(invert_rows_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, s, sorted_rows,
+                           segment_offsets + num_segments, cnt, pos, pairs, tokens, top_k);
+        st = check_launch("koemi_moe_combine(invert)");
+        if (st != KOEMI_OK) return st;
+    }
+    switch (dtype) {
+        case KOEMI_F32: return launch_combine_rows<float>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);
+        case KOEMI_F16: return launch_combine_rows<f16>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);
+        default: return launch_combine_rows<bf16>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);
+    }
+}

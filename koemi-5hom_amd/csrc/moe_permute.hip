@@ -1,0 +1,293 @@
+// Stable MoE permutation for gfx950: a counting sort of (token, slot) pairs by
+// expert that reproduces the order of a stable argsort bit for bit.
+//
+// Reference: cuda_kernels/moe/moe_kernels.cu:68-145, 390-499 (pair keys, CUB
+// 64-bit radix sort, histogram, scan, gathers) and the stable-argsort oracle of
+// model/experts.py:171-216. With E experts the key needs only log2(E+1) bits,
+// so instead of eight radix passes over 64-bit keys this runs:
+//
+//   1. count   : one wave per chunk of kChunk pairs builds its per-expert
+//                histogram in LDS (counts are order-independent);
+//   2. scan    : one workgroup turns the [chunks, E+1] counts into
+//                segment_offsets and the first destination of every
+//                (chunk, expert) — chunk order then pair order is stability;
+//   3. scatter : each chunk walks its pairs in order, 64 at a time; lanes with
+//                the same key are grouped with ballots, ranked by popcount of
+//                the lower lanes, and advance an LDS cursor per key. Writes
+//                sorted_rows / sorted_experts / sorted_weights and the pair ->
+//                position map;
+//   4. gather  : one wave per token reads its context row once and writes it to
+//                each of its k positions (zero rows for invalid pairs, which
+//                all land past segment_offsets[E]).
+//
+// Every destination is computed, none is claimed by an atomic, so the output
+// does not depend on scheduling.
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+constexpr int kChunk = 512;          // pairs per count/scatter wave
+constexpr int kMaxExperts = 4095;    // LDS holds E+1 cursors (scan: E+1 int64)
+constexpr int kScanThreads = 1024;
+
+inline int64_t num_chunks(int64_t pairs) { return (pairs + kChunk - 1) / kChunk; }
+
+// Workspace layout (byte offsets, 256-aligned).
+struct PermuteWorkspace {
+    size_t counts_off, dest_off, total;
+};
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline PermuteWorkspace permute_workspace(int64_t tokens, int64_t k, int64_t E) {
+    const int64_t pairs = tokens * k;
+    PermuteWorkspace w;
+    w.counts_off = 0;
+    w.dest_off = align256(static_cast<size_t>(num_chunks(pairs) > 0 ? num_chunks(pairs) : 1) * (E + 1) * sizeof(int32_t));
+    w.total = w.dest_off + align256(static_cast<size_t>(pairs > 0 ? pairs : 1) * sizeof(int64_t));
+    return w;
+}
+
+// Pair key (moe_kernels.cu:68-91): expert for a valid token whose slot holds an
+// in-range expert not already used by an earlier slot, else the sentinel E.
+template <typename I>
+__device__ __forceinline__ int32_t pair_key(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+                                            int64_t p, int64_t k, int64_t E) {
+    const int64_t t = p / k;
+    const int64_t s = p - t * k;
+    const int64_t e = static_cast<int64_t>(a[p]);
+    bool ok = valid[t] && e >= 0 && e < E;
+    for (int64_t r = 0; r < s && ok; ++r) ok = static_cast<int64_t>(a[t * k + r]) != e;
+    return static_cast<int32_t>(ok ? e : E);
+}
+
+template <typename I>
+__global__ __launch_bounds__(kWave) void permute_count_kernel(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+                                                              int32_t* __restrict__ counts, int64_t pairs, int64_t k,
+                                                              int64_t E) {
+    extern __shared__ int32_t hist[];
+    const int64_t chunk = blockIdx.x;
+    for (int64_t e = threadIdx.x; e <= E; e += kWave) hist[e] = 0;
+    __syncthreads();
+    const int64_t p0 = chunk * kChunk;
+    const int64_t p1 = min(pairs, p0 + kChunk);
+    for (int64_t p = p0 + threadIdx.x; p < p1; p += kWave) atomicAdd(&hist[pair_key(a, valid, p, k, E)], 1);
+    __syncthreads();
+    int32_t* row = counts + chunk * (E + 1);
+    for (int64_t e = threadIdx.x; e <= E; e += kWave) row[e] = hist[e];
+}
+
+// counts[c][e] -> first destination of (chunk c, key e); offsets[e] = first
+// position of key e, offsets[E] = number of valid pairs.
+__global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __restrict__ counts,
+                                                                    int64_t* __restrict__ offsets, int64_t chunks,
+                                                                    int64_t E) {
+    extern __shared__ int64_t key_total[];  // E+1 entries
+    const int tid = threadIdx.x;
+    for (int64_t e = tid; e <= E; e += kScanThreads) {
+        int64_t run = 0;
+        for (int64_t c = 0; c < chunks; ++c) {
+            const int32_t v = counts[c * (E + 1) + e];
+            counts[c * (E + 1) + e] = static_cast<int32_t>(run);
+            run += v;
+        }
+        key_total[e] = run;
+    }
+    __syncthreads();
+    // Exclusive scan of key_total over E+1 keys: each thread scans a contiguous span.
+    __shared__ int64_t span_sum[kScanThreads];
+    const int64_t n = E + 1;
+    const int64_t per = (n + kScanThreads - 1) / kScanThreads;
+    const int64_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
+    int64_t s = 0;
+    for (int64_t e = b0; e < b1; ++e) s += key_total[e];
+    span_sum[tid] = s;
+    __syncthreads();
+    if (tid == 0) {
+        int64_t run = 0;
+        for (int i = 0; i < kScanThreads; ++i) {
+            const int64_t v = span_sum[i];
+            span_sum[i] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    int64_t run = span_sum[tid];
+    for (int64_t e = b0; e < b1; ++e) {
+        const int64_t v = key_total[e];
+        key_total[e] = run;
+        run += v;
+    }
+    __syncthreads();
+    for (int64_t e = tid; e <= E; e += kScanThreads) {
+        offsets[e] = key_total[e];
+        const int64_t base = key_total[e];
+        for (int64_t c = 0; c < chunks; ++c) counts[c * (E + 1) + e] += static_cast<int32_t>(base);
+    }
+}
+
+template <typename I>
+__global__ __launch_bounds__(kWave) void permute_scatter_kernel(
+    const I* __restrict__ a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
+    const int32_t* __restrict__ bases, int64_t* __restrict__ sorted_rows, int64_t* __restrict__ sorted_experts,
+    float* __restrict__ sorted_w, int64_t* __restrict__ dest, int64_t pairs, int64_t k, int64_t E) {
+    extern __shared__ int32_t cursor[];
+    const int64_t chunk = blockIdx.x;
+    const int lane = lane_id();
+    for (int64_t e = lane; e <= E; e += kWave) cursor[e] = bases[chunk * (E + 1) + e];
+    __syncthreads();
+    const int64_t p0 = chunk * kChunk;
+    const int64_t p1 = min(pairs, p0 + kChunk);
+    for (int64_t g = p0; g < p1; g += kWave) {
+        const int64_t p = g + lane;
+        const bool active = p < p1;
+        const int32_t key = active ? pair_key(a, valid, p, k, E) : -1;
+        // Group the lanes by key: peers = lanes of this group with my key.
+        uint64_t remaining = __ballot(active);
+        uint64_t peers = 0;
+        while (remaining) {
+            const int leader = __ffsll(static_cast<unsigned long long>(remaining)) - 1;
+            const int32_t lkey = __shfl(key, leader, kWave);
+            const uint64_t same = __ballot(active && key == lkey);
+            if (active && key == lkey) peers = same;
+            remaining &= ~same;
+        }
+        const int rank = __popcll(peers & lanemask_lt());
+        int64_t d = 0;
+        if (active) d = static_cast<int64_t>(cursor[key]) + rank;
+        __syncthreads();
+        if (active && rank == 0) cursor[key] += __popcll(peers);
+        __syncthreads();
+        if (active) {
+            sorted_rows[d] = p / k;
+            sorted_experts[d] = key;
+            if (sorted_w) sorted_w[d] = (key < E) ? pair_w[p] : 0.0f;
+            dest[p] = d;
+        }
+    }
+}
+
+// One wave per token: context row read once, written to each of the k positions.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __restrict__ ctx,
+                                                                   const int64_t* __restrict__ dest,
+                                                                   const int64_t* __restrict__ offsets_end,
+                                                                   T* __restrict__ out, int64_t tokens, int64_t k,
+                                                                   int64_t D) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    if (t >= tokens) return;
+    const int lane = lane_id();
+    const int64_t valid_pairs = *offsets_end;
+    const T* src = ctx + t * D;
+    if constexpr (VEC) {
+        constexpr int N = 16 / sizeof(T);
+        const int64_t nvec = D / N;
+        for (int64_t v0 = 0; v0 < nvec; v0 += kWave * 4) {
+            uint4 buf[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t v = v0 + u * kWave + lane;
+                buf[u] = v < nvec ? reinterpret_cast<const uint4*>(src)[v] : make_uint4(0, 0, 0, 0);
+            }
+            for (int64_t s = 0; s < k; ++s) {
+                const int64_t d = dest[t * k + s];
+                uint4* dst = reinterpret_cast<uint4*>(out + d * D);
+                const bool keep = d < valid_pairs;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int64_t v = v0 + u * kWave + lane;
+                    if (v < nvec) dst[v] = keep ? buf[u] : make_uint4(0, 0, 0, 0);
+                }
+            }
+        }
+    } else {
+        for (int64_t s = 0; s < k; ++s) {
+            const int64_t d = dest[t * k + s];
+            const bool keep = d < valid_pairs;
+            for (int64_t c = lane; c < D; c += kWave) out[d * D + c] = keep ? src[c] : static_cast<T>(0.0f);
+        }
+    }
+}
+
+template <typename I>
+int run_index_phase(const void* assignments, const uint8_t* valid, const float* pair_w, int64_t* sorted_rows,
+                    int64_t* sorted_experts, int64_t* offsets, float* sorted_w, int32_t* counts, int64_t* dest,
+                    int64_t pairs, int64_t k, int64_t E, hipStream_t s) {
+    const I* a = static_cast<const I*>(assignments);
+    const int64_t chunks = num_chunks(pairs);
+    const size_t hist_bytes = static_cast<size_t>(E + 1) * sizeof(int32_t);
+    hipLaunchKernelGGL(permute_count_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
+                       valid, counts, pairs, k, E);
+    int st = check_launch("koemi_moe_permute(count)");
+    if (st != KOEMI_OK) return st;
+    hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(kScanThreads), static_cast<size_t>(E + 1) * sizeof(int64_t), s,
+                       counts, offsets, chunks, E);
+    st = check_launch("koemi_moe_permute(scan)");
+    if (st != KOEMI_OK) return st;
+    hipLaunchKernelGGL(permute_scatter_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
+                       valid, pair_w, counts, sorted_rows, sorted_experts, sorted_w, dest, pairs, k, E);
+    return check_launch("koemi_moe_permute(scatter)");
+}
+
+template <typename T>
+int run_gather(const void* ctx, const int64_t* dest, const int64_t* offsets_end, void* out, int64_t tokens, int64_t k,
+               int64_t D, hipStream_t s) {
+    const bool vec = (D * static_cast<int64_t>(sizeof(T))) % 16 == 0 && reinterpret_cast<uintptr_t>(ctx) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    const dim3 grid(grid_for(tokens, 4)), block(kWave * 4);
+    if (vec)
+        hipLaunchKernelGGL((permute_gather_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(ctx), dest,
+                           offsets_end, static_cast<T*>(out), tokens, k, D);
+    else
+        hipLaunchKernelGGL((permute_gather_kernel<T, false>), grid, block, 0, s, static_cast<const T*>(ctx), dest,
+                           offsets_end, static_cast<T*>(out), tokens, k, D);
+    return check_launch("koemi_moe_permute(gather)");
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" size_t koemi_moe_permute_workspace_bytes(int64_t tokens, int64_t top_k, int64_t expert_count) {
+    if (tokens < 0 || top_k < 1 || expert_count < 1) return 0;
+    return permute_workspace(tokens, top_k, expert_count).total;
+}
+
+extern "C" int koemi_moe_permute(const void* context, int context_dtype, const void* assignments,
+                                 int assignment_dtype, const uint8_t* valid_mask, const float* pair_weights,
+                                 void* sorted_context, int64_t* sorted_rows, int64_t* sorted_experts,
+                                 int64_t* segment_offsets, float* sorted_weights, int64_t tokens, int64_t width,
+                                 int64_t top_k, int64_t expert_count, void* workspace, size_t workspace_bytes,
+                                 koemi_stream_t stream) {
+    if (tokens < 1 || width < 1) return fail(KOEMI_ERR_INVALID, "context dimensions must be positive");
+    if (top_k < 1 || top_k > 256) return fail(KOEMI_ERR_INVALID, "assignments top_k is outside [1, 256]");
+    if (expert_count < 1 || top_k > expert_count) return fail(KOEMI_ERR_INVALID, "top_k must not exceed expert_count");
+    if (expert_count > kMaxExperts) return fail(KOEMI_ERR_UNSUPPORTED, "permute supports at most %d experts", kMaxExperts);
+    if (!float_dtype(context_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "context must be float32, float16 or bfloat16");
+    if (!index_dtype(assignment_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "assignments must be int32 or int64");
+    if ((pair_weights == nullptr) != (sorted_weights == nullptr))
+        return fail(KOEMI_ERR_INVALID, "pair_weights and sorted_weights must both be given or both be null");
+    if (!context || !assignments || !valid_mask || !sorted_context || !sorted_rows || !sorted_experts || !segment_offsets)
+        return fail(KOEMI_ERR_INVALID, "permute received a null pointer");
+    const PermuteWorkspace ws = permute_workspace(tokens, top_k, expert_count);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "permute workspace too small: need %zu bytes", ws.total);
+    if (num_chunks(tokens * top_k) > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many pairs");
+    char* base = static_cast<char*>(workspace);
+    int32_t* counts = reinterpret_cast<int32_t*>(base + ws.counts_off);
+    int64_t* dest = reinterpret_cast<int64_t*>(base + ws.dest_off);
+    hipStream_t s = as_stream(stream);
+    const int64_t pairs = tokens * top_k;
+    int st = (assignment_dtype == KOEMI_I32)
+                 ? run_index_phase<int32_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                                            segment_offsets, sorted_weights, counts, dest, pairs, top_k, expert_count, s)
+                 : run_index_phase<int64_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                                            segment_offsets, sorted_weights, counts, dest, pairs, top_k, expert_count, s);
+    if (st != KOEMI_OK) return st;
+    const int64_t* offsets_end = segment_offsets + expert_count;
+    switch (context_dtype) {
+        case KOEMI_F32: return run_gather<float>(context, dest, offsets_end, sorted_context, tokens, top_k, width, s);
+        case KOEMI_F16: return run_gather<f16>(context, dest, offsets_end, sorted_context, tokens, top_k, width, s);
+        default: return run_gather<bf16>(context, dest, offsets_end, sorted_context, tokens, top_k, width, s);
+    }
+}

@@ -1,0 +1,228 @@
+// MoE routing for gfx950: content-hash top-k, learned softmax top-k, device-side
+// contract checks and per-expert activation counts.
+//
+// Reference: model/experts.py:30-38, 283-289 (hash route in int64),
+// cuda_kernels/moe/moe_kernels.cu:33-66 (native route), model/router.py:43-59
+// (learned gate), cuda_kernels/moe/__init__.py:113-125, 213-220 (checks) and
+// model/network.py:48-70 (activation counts). All of it is integer work or a
+// 16-wide softmax per token: one thread per token, no HBM-heavy traffic.
+#include "common.hpp"
+#include "detmath.hpp"
+
+namespace koemi {
+namespace {
+
+// mix32 of experts.py:30-38. The product tok * 1000003 + prev * 97409 is taken
+// modulo 2^64 (the int64 tensor arithmetic of the reference) and only its low
+// 32 bits are used, so unsigned 64-bit arithmetic gives the same bits.
+__device__ __forceinline__ uint32_t content_hash(int64_t token, int64_t previous) {
+    const uint64_t mixed = static_cast<uint64_t>(token) * 1000003ull + static_cast<uint64_t>(previous) * 97409ull;
+    uint32_t v = static_cast<uint32_t>(mixed);
+    v ^= v >> 16;
+    v *= 0x45D9F3Bu;
+    v ^= v >> 16;
+    v *= 0x45D9F3Bu;
+    return v ^ (v >> 16);
+}
+
+template <typename I>
+__global__ void route_hash_kernel(const I* __restrict__ tok, const I* __restrict__ prev,
+                                  const uint8_t* __restrict__ valid, int64_t* __restrict__ out,
+                                  int32_t* __restrict__ dup_flag, int64_t T, int64_t E, int64_t k) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    int64_t* row = out + t * k;
+    if (!valid[t]) {
+        for (int64_t s = 0; s < k; ++s) row[s] = -1;
+        return;
+    }
+    const uint64_t h = content_hash(static_cast<int64_t>(tok[t]), static_cast<int64_t>(prev[t]));
+    bool dup = false;
+    for (int64_t s = 0; s < k; ++s) {
+        // int64 sum of experts.py:288 (no 32-bit wraparound): h < 2^32, s * 0x9E3779B9 < 2^40.
+        const int64_t e = static_cast<int64_t>((h + static_cast<uint64_t>(s) * 0x9E3779B9ull) % static_cast<uint64_t>(E));
+        for (int64_t r = 0; r < s; ++r) dup |= (row[r] == e);
+        row[s] = e;
+    }
+    if (dup) atomicOr(dup_flag, 1);
+}
+
+// softmax(logits) then top-k in descending probability, ties to the lower index
+// (router.py:46-49). Probabilities use the fixed exp of detmath.hpp and a
+// left-to-right sum so that weights are reproducible bit for bit.
+__global__ void route_learned_kernel(const float* __restrict__ logits, const uint8_t* __restrict__ valid,
+                                     int64_t* __restrict__ out_idx, float* __restrict__ out_w, int64_t T,
+                                     int64_t E, int64_t k) {
+#pragma clang fp contract(off)
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    int64_t* idx = out_idx + t * k;
+    float* wt = out_w + t * k;
+    if (!valid[t]) {
+        for (int64_t s = 0; s < k; ++s) {
+            idx[s] = -1;
+            wt[s] = 0.0f;
+        }
+        return;
+    }
+    const float* l = logits + t * E;
+    float m = -__builtin_inff();
+    for (int64_t j = 0; j < E; ++j) m = fmaxf(m, l[j]);
+    float sum = 0.0f;
+    for (int64_t j = 0; j < E; ++j) sum = sum + detmath::det_expf(l[j] - m);
+    float prev_p = __builtin_inff();
+    int64_t prev_j = -1;
+    for (int64_t s = 0; s < k; ++s) {
+        int64_t best = -1;
+        float best_p = 0.0f;
+        for (int64_t j = 0; j < E; ++j) {
+            const float p = detmath::det_expf(l[j] - m) / sum;
+            const bool after_prev = (p < prev_p) || (p == prev_p && j > prev_j);
+            if (after_prev && (best < 0 || p > best_p)) {
+                best = j;
+                best_p = p;
+            }
+        }
+        idx[s] = best;
+        wt[s] = best < 0 ? 0.0f : best_p;
+        prev_p = best_p;
+        prev_j = best;
+    }
+}
+
+template <typename I>
+__global__ void check_assignments_kernel(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+                                         int32_t* __restrict__ flags, int64_t T, int64_t k, int64_t E) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= T || !valid[t]) return;
+    const I* row = a + t * k;
+    bool out_of_range = false, dup = false;
+    for (int64_t s = 0; s < k; ++s) {
+        const int64_t e = static_cast<int64_t>(row[s]);
+        out_of_range |= (e < 0 || e >= E);
+        for (int64_t r = 0; r < s; ++r) dup |= (static_cast<int64_t>(row[r]) == e);
+    }
+    if (out_of_range) atomicOr(flags, 1);
+    if (dup) atomicOr(flags + 1, 1);
+}
+
+constexpr int kCountThreads = 256;
+constexpr int kCountLdsBins = 4096;
+
+template <typename I>
+__global__ __launch_bounds__(kCountThreads) void expert_counts_kernel(
+    const I* __restrict__ a, const uint8_t* __restrict__ valid, unsigned long long* __restrict__ counts,
+    int64_t T, int64_t k, int64_t E) {
+    __shared__ uint32_t hist[kCountLdsBins];
+    const bool use_lds = E <= kCountLdsBins;
+    if (use_lds) {
+        for (int64_t e = threadIdx.x; e < E; e += kCountThreads) hist[e] = 0;
+        __syncthreads();
+    }
+    const int64_t pairs = T * k;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kCountThreads;
+    for (int64_t p = static_cast<int64_t>(blockIdx.x) * kCountThreads + threadIdx.x; p < pairs; p += stride) {
+        const int64_t t = p / k;
+        const int64_t e = static_cast<int64_t>(a[p]);
+        if (valid[t] && e >= 0 && e < E) {
+            if (use_lds) atomicAdd(&hist[e], 1u);
+            else atomicAdd(&counts[e], 1ull);
+        }
+    }
+    if (use_lds) {
+        __syncthreads();
+        for (int64_t e = threadIdx.x; e < E; e += kCountThreads)
+            if (hist[e]) atomicAdd(&counts[e], static_cast<unsigned long long>(hist[e]));
+    }
+}
+
+__global__ void zero_i64_kernel(int64_t* __restrict__ p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_moe_route_hash(const void* token_ids, const void* previous_token_ids,
+                                    const uint8_t* valid_mask, int id_dtype, int64_t* assignments,
+                                    int32_t* duplicate_flag, int64_t tokens, int64_t expert_count,
+                                    int64_t top_k, koemi_stream_t stream) {
+    if (tokens < 0) return fail(KOEMI_ERR_INVALID, "token count must be non-negative");
+    if (expert_count < 1 || top_k < 1 || top_k > expert_count)
+        return fail(KOEMI_ERR_INVALID, "route needs 1 <= top_k <= expert_count");
+    if (!index_dtype(id_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "token ids must be int32 or int64");
+    if (tokens == 0) return KOEMI_OK;
+    if (!token_ids || !previous_token_ids || !valid_mask || !assignments || !duplicate_flag)
+        return fail(KOEMI_ERR_INVALID, "route received a null pointer");
+    const dim3 grid(grid_for(tokens, 256)), block(256);
+    hipStream_t s = as_stream(stream);
+    if (id_dtype == KOEMI_I32)
+        hipLaunchKernelGGL(route_hash_kernel<int32_t>, grid, block, 0, s, static_cast<const int32_t*>(token_ids),
+                           static_cast<const int32_t*>(previous_token_ids), valid_mask, assignments, duplicate_flag,
+                           tokens, expert_count, top_k);
+    else
+        hipLaunchKernelGGL(route_hash_kernel<int64_t>, grid, block, 0, s, static_cast<const int64_t*>(token_ids),
+                           static_cast<const int64_t*>(previous_token_ids), valid_mask, assignments, duplicate_flag,
+                           tokens, expert_count, top_k);
+    return check_launch("koemi_moe_route_hash");
+}
+
+extern "C" int koemi_moe_route_learned(const float* router_logits, const uint8_t* valid_mask,
+                                       int64_t* assignments, float* weights, int64_t tokens,
+                                       int64_t expert_count, int64_t top_k, koemi_stream_t stream) {
+    if (tokens < 0) return fail(KOEMI_ERR_INVALID, "token count must be non-negative");
+    if (expert_count < 1 || top_k < 1 || top_k > expert_count)
+        return fail(KOEMI_ERR_INVALID, "learned route needs 1 <= top_k <= expert_count");
+    if (expert_count > 1024) return fail(KOEMI_ERR_UNSUPPORTED, "learned route supports at most 1024 experts");
+    if (tokens == 0) return KOEMI_OK;
+    if (!router_logits || !valid_mask || !assignments || !weights)
+        return fail(KOEMI_ERR_INVALID, "learned route received a null pointer");
+    hipLaunchKernelGGL(route_learned_kernel, dim3(grid_for(tokens, 256)), dim3(256), 0, as_stream(stream),
+                       router_logits, valid_mask, assignments, weights, tokens, expert_count, top_k);
+    return check_launch("koemi_moe_route_learned");
+}
+
+extern "C" int koemi_moe_check_assignments(const void* assignments, int assignment_dtype,
+                                           const uint8_t* valid_mask, int32_t* flags, int64_t tokens,
+                                           int64_t top_k, int64_t expert_count, koemi_stream_t stream) {
+    if (tokens < 0 || top_k < 1 || expert_count < 1) return fail(KOEMI_ERR_INVALID, "invalid assignment check sizes");
+    if (!index_dtype(assignment_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "assignments must be int32 or int64");
+    if (tokens == 0) return KOEMI_OK;
+    if (!assignments || !valid_mask || !flags) return fail(KOEMI_ERR_INVALID, "assignment check received a null pointer");
+    const dim3 grid(grid_for(tokens, 256)), block(256);
+    hipStream_t s = as_stream(stream);
+    if (assignment_dtype == KOEMI_I32)
+        hipLaunchKernelGGL(check_assignments_kernel<int32_t>, grid, block, 0, s, static_cast<const int32_t*>(assignments),
+                           valid_mask, flags, tokens, top_k, expert_count);
+    else
+        hipLaunchKernelGGL(check_assignments_kernel<int64_t>, grid, block, 0, s, static_cast<const int64_t*>(assignments),
+                           valid_mask, flags, tokens, top_k, expert_count);
+    return check_launch("koemi_moe_check_assignments");
+}
+
+extern "C" int koemi_moe_expert_counts(const void* assignments, int assignment_dtype,
+                                       const uint8_t* valid_mask, int64_t* counts, int64_t tokens,
+                                       int64_t top_k, int64_t expert_count, koemi_stream_t stream) {
+    if (tokens < 0 || top_k < 1 || expert_count < 1) return fail(KOEMI_ERR_INVALID, "invalid expert count sizes");
+    if (!index_dtype(assignment_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "assignments must be int32 or int64");
+    if (!counts) return fail(KOEMI_ERR_INVALID, "expert counts received a null pointer");
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(zero_i64_kernel, dim3(grid_for(expert_count, 256)), dim3(256), 0, s, counts, expert_count);
+    int st = check_launch("koemi_moe_expert_counts");
+    if (st != KOEMI_OK || tokens == 0) return st;
+    if (!assignments || !valid_mask) return fail(KOEMI_ERR_INVALID, "expert counts received a null pointer");
+    int64_t blocks = (tokens * top_k + kCountThreads * 16 - 1) / (kCountThreads * 16);
+    if (blocks < 1) blocks = 1;
+    if (blocks > 1024) blocks = 1024;
+    unsigned long long* c = reinterpret_cast<unsigned long long*>(counts);
+    if (assignment_dtype == KOEMI_I32)
+        hipLaunchKernelGGL(expert_counts_kernel<int32_t>, dim3(static_cast<unsigned>(blocks)), dim3(kCountThreads), 0, s,
+                           static_cast<const int32_t*>(assignments), valid_mask, c, tokens, top_k, expert_count);
+    else
+        hipLaunchKernelGGL(expert_counts_kernel<int64_t>, dim3(static_cast<unsigned>(blocks)), dim3(kCountThreads), 0, s,
+                           static_cast<const int64_t*>(assignments), valid_mask, c, tokens, top_k, expert_count);
+    return check_launch("koemi_moe_expert_counts");
+}

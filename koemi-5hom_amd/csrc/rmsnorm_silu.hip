@@ -1,0 +1,272 @@
+// Fused RMSNorm + SiLU for gfx950.
+//
+// Reference: src/koemi/cuda_kernels/core/rmsnorm_silu.cu:62-132 (one block per
+// row, two global passes over x). Here one wave owns a row and keeps it in
+// registers: each lane loads NV 16-byte vectors (8 bf16/f16 or 4 fp32 values),
+// the sum of squares is reduced with a xor butterfly, and y = silu(x * inv * w)
+// is produced from the same registers, so x is read from HBM exactly once and y
+// written once. Rows whose width does not fit that layout use a generic
+// block-per-row path.
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+constexpr int kNormWaves = 4;
+
+__device__ __forceinline__ float silu(float v) {
+    // v * sigmoid(v) with the hardware exp2 and reciprocal (1 ulp each).
+    const float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+__device__ __forceinline__ float silu_grad(float v) {
+    const float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+    const float sg = __builtin_amdgcn_rcpf(1.0f + e);
+    return sg * (1.0f + v * (1.0f - sg));
+}
+
+template <typename T>
+struct Vec16 {
+    static constexpr int N = 16 / sizeof(T);
+    union {
+        uint4 raw;
+        T e[N];
+    };
+};
+
+// NV vectors per lane; row width H must satisfy H % N == 0 and H <= NV*64*N.
+template <typename T, int NV>
+__global__ __launch_bounds__(kWave * kNormWaves) void rmsnorm_silu_fwd_wave(
+    const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y, float* __restrict__ inv_out,
+    int64_t rows, int H, float eps) {
+    constexpr int N = Vec16<T>::N;
+    const int lane = lane_id();
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const T* xr = x + row * H;
+    T* yr = y + row * H;
+    Vec16<T> xv[NV], wv[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int c = (v * kWave + lane) * N;
+        if (c < H) {
+            xv[v].raw = *reinterpret_cast<const uint4*>(xr + c);
+            wv[v].raw = *reinterpret_cast<const uint4*>(w + c);
+        } else {
+            xv[v].raw = make_uint4(0, 0, 0, 0);
+            wv[v].raw = make_uint4(0, 0, 0, 0);
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const float f = to_f32(xv[v].e[i]);
+            ss = __builtin_fmaf(f, f, ss);
+        }
+    ss = wave_sum_xor(ss);
+    const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
+    if (lane == 0) inv_out[row] = inv;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int c = (v * kWave + lane) * N;
+        if (c < H) {
+            Vec16<T> o;
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                o.e[i] = from_f32<T>(silu(to_f32(xv[v].e[i]) * inv * to_f32(wv[v].e[i])));
+            *reinterpret_cast<uint4*>(yr + c) = o.raw;
+        }
+    }
+}
+
+// Generic path: one 256-thread block per row, two passes over the row.
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_silu_fwd_block(const T* __restrict__ x,
+                                                              const T* __restrict__ w,
+                                                              T* __restrict__ y,
+                                                              float* __restrict__ inv_out,
+                                                              int64_t rows, int H, float eps) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    if (row >= rows) return;
+    const T* xr = x + row * H;
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < H; c += 256) {
+        const float f = to_f32(xr[c]);
+        ss = __builtin_fmaf(f, f, ss);
+    }
+    ss = wave_sum_xor(ss);
+    if (lane_id() == 0) red[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
+    if (threadIdx.x == 0) inv_out[row] = inv;
+    for (int c = threadIdx.x; c < H; c += 256)
+        y[row * H + c] = from_f32<T>(silu(to_f32(xr[c]) * inv * to_f32(w[c])));
+}
+
+// ------------------------------------------------------------------ backward --
+// dx = inv * d * w - x * inv^3 / H * sum_c(d_c w_c x_c),  d = g * silu'(x inv w),
+// dw = sum_rows d * x * inv. Stage 1 writes one fp32 partial row of dw per
+// workgroup; stage 2 sums the partials in a fixed order (deterministic).
+constexpr int kBwdBlockRows = 32;    // rows per workgroup in stage 1 (upper bound on partial count)
+constexpr int kBwdMaxBlocks = 1024;
+
+inline int64_t bwd_blocks(int64_t rows) {
+    int64_t b = (rows + kBwdBlockRows - 1) / kBwdBlockRows;
+    if (b > kBwdMaxBlocks) b = kBwdMaxBlocks;
+    if (b < 1) b = 1;
+    return b;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_silu_bwd_stage1(
+    const T* __restrict__ g, const T* __restrict__ x, const T* __restrict__ w,
+    const float* __restrict__ inv_rms, T* __restrict__ dx, float* __restrict__ partial,
+    int64_t rows, int H) {
+    __shared__ float red[4];
+    __shared__ float total;
+    const int64_t blocks = gridDim.x;
+    float* part = partial + static_cast<int64_t>(blockIdx.x) * H;
+    for (int c = threadIdx.x; c < H; c += 256) part[c] = 0.0f;
+    for (int64_t row = blockIdx.x; row < rows; row += blocks) {
+        const T* xr = x + row * H;
+        const T* gr = g + row * H;
+        const float inv = inv_rms[row];
+        float dot = 0.0f;
+        for (int c = threadIdx.x; c < H; c += 256) {
+            const float xf = to_f32(xr[c]), wf = to_f32(w[c]);
+            const float d = to_f32(gr[c]) * silu_grad(xf * inv * wf);
+            dot = __builtin_fmaf(d * wf, xf, dot);
+        }
+        dot = wave_sum_xor(dot);
+        __syncthreads();
+        if (lane_id() == 0) red[threadIdx.x / kWave] = dot;
+        __syncthreads();
+        if (threadIdx.x == 0) total = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();
+        const float corr = inv * inv * inv / static_cast<float>(H) * total;
+        for (int c = threadIdx.x; c < H; c += 256) {
+            const float xf = to_f32(xr[c]), wf = to_f32(w[c]);
+            const float nrm = xf * inv;
+            const float d = to_f32(gr[c]) * silu_grad(nrm * wf);
+            dx[row * H + c] = from_f32<T>(inv * d * wf - xf * corr);
+            part[c] += d * nrm;  // this thread is the only writer of part[c]
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_silu_bwd_stage2(const float* __restrict__ partial,
+                                                               T* __restrict__ dw, int64_t blocks,
+                                                               int H) {
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= H) return;
+    float acc = 0.0f;
+    for (int64_t b = 0; b < blocks; ++b) acc += partial[b * H + c];
+    dw[c] = from_f32<T>(acc);
+}
+
+template <typename T>
+int launch_forward(const void* x, const void* w, void* y, float* inv, int64_t rows, int64_t H,
+                   float eps, hipStream_t stream) {
+    constexpr int N = Vec16<T>::N;
+    const T* xp = static_cast<const T*>(x);
+    const T* wp = static_cast<const T*>(w);
+    T* yp = static_cast<T*>(y);
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(w) % 16 == 0) &&
+                         (reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    const int Hi = static_cast<int>(H);
+    const dim3 wgrid(grid_for(rows, kNormWaves)), wblock(kWave * kNormWaves);
+    if (aligned && H % N == 0) {
+        const int64_t vecs = H / N;  // vectors per row
+        if (vecs <= kWave * 1) {
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 1>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
+            return check_launch("koemi_rmsnorm_silu_forward");
+        }
+        if (vecs <= kWave * 2) {
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 2>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
+            return check_launch("koemi_rmsnorm_silu_forward");
+        }
+        if (vecs <= kWave * 4) {
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 4>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
+            return check_launch("koemi_rmsnorm_silu_forward");
+        }
+        if (vecs <= kWave * 8) {
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 8>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
+            return check_launch("koemi_rmsnorm_silu_forward");
+        }
+    }
+    if (rows > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu: too many rows for the generic path");
+    hipLaunchKernelGGL(rmsnorm_silu_fwd_block<T>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, xp, wp, yp, inv, rows, Hi, eps);
+    return check_launch("koemi_rmsnorm_silu_forward");
+}
+
+template <typename T>
+int launch_backward(const void* g, const void* x, const void* w, const float* inv, void* dx,
+                    void* dw, int64_t rows, int64_t H, float* partial, hipStream_t stream) {
+    const int64_t blocks = bwd_blocks(rows);
+    hipLaunchKernelGGL(rmsnorm_silu_bwd_stage1<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       static_cast<const T*>(g), static_cast<const T*>(x), static_cast<const T*>(w), inv,
+                       static_cast<T*>(dx), partial, rows, static_cast<int>(H));
+    int st = check_launch("koemi_rmsnorm_silu_backward");
+    if (st != KOEMI_OK) return st;
+    hipLaunchKernelGGL(rmsnorm_silu_bwd_stage2<T>, dim3(grid_for(H, 256)), dim3(256), 0, stream, partial,
+                       static_cast<T*>(dw), blocks, static_cast<int>(H));
+    return check_launch("koemi_rmsnorm_silu_backward");
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_rmsnorm_silu_forward(const void* input, const void* weight, void* output,
+                                          float* inverse_rms, int64_t rows, int64_t hidden,
+                                          double eps, int dtype, koemi_stream_t stream) {
+    if (rows < 0 || hidden < 1) return fail(KOEMI_ERR_INVALID, "rmsnorm_silu needs rows >= 0 and a positive hidden dimension");
+    if (hidden > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu hidden dimension too large");
+    if (!(eps > 0.0)) return fail(KOEMI_ERR_INVALID, "eps must be finite and positive");
+    if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu does not support dtype %s", dtype_name(dtype));
+    if (rows == 0) return KOEMI_OK;
+    if (!input || !weight || !output || !inverse_rms) return fail(KOEMI_ERR_INVALID, "rmsnorm_silu received a null pointer");
+    hipStream_t s = as_stream(stream);
+    const float e = static_cast<float>(eps);
+    switch (dtype) {
+        case KOEMI_F32: return launch_forward<float>(input, weight, output, inverse_rms, rows, hidden, e, s);
+        case KOEMI_F16: return launch_forward<f16>(input, weight, output, inverse_rms, rows, hidden, e, s);
+        default: return launch_forward<bf16>(input, weight, output, inverse_rms, rows, hidden, e, s);
+    }
+}
+
+extern "C" size_t koemi_rmsnorm_silu_backward_workspace_bytes(int64_t rows, int64_t hidden) {
+    if (rows < 0 || hidden < 1) return 0;
+    return static_cast<size_t>(bwd_blocks(rows)) * static_cast<size_t>(hidden) * sizeof(float);
+}
+
+extern "C" int koemi_rmsnorm_silu_backward(const void* grad_output, const void* input,
+                                           const void* weight, const float* inverse_rms,
+                                           void* grad_input, void* grad_weight, int64_t rows,
+                                           int64_t hidden, int dtype, void* workspace,
+                                           size_t workspace_bytes, koemi_stream_t stream) {
+    if (rows < 0 || hidden < 1) return fail(KOEMI_ERR_INVALID, "rmsnorm_silu backward needs rows >= 0 and a positive hidden dimension");
+    if (hidden > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu hidden dimension too large");
+    if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu does not support dtype %s", dtype_name(dtype));
+    if (!grad_weight) return fail(KOEMI_ERR_INVALID, "rmsnorm_silu backward received a null pointer");
+    if (rows > 0 && (!grad_output || !input || !weight || !inverse_rms || !grad_input))
+        return fail(KOEMI_ERR_INVALID, "rmsnorm_silu backward received a null pointer");
+    const size_t need = koemi_rmsnorm_silu_backward_workspace_bytes(rows, hidden);
+    if (workspace_bytes < need || (need > 0 && !workspace))
+        return fail(KOEMI_ERR_INVALID, "rmsnorm_silu backward workspace too small: need %zu bytes", need);
+    hipStream_t s = as_stream(stream);
+    float* partial = static_cast<float*>(workspace);
+    switch (dtype) {
+        case KOEMI_F32: return launch_backward<float>(grad_output, input, weight, inverse_rms, grad_input, grad_weight, rows, hidden, partial, s);
+        case KOEMI_F16: return launch_backward<f16>(grad_output, input, weight, inverse_rms, grad_input, grad_weight, rows, hidden, partial, s);
+        default: return launch_backward<bf16>(grad_output, input, weight, inverse_rms, grad_input, grad_weight, rows, hidden, partial, s);
+    }
+}

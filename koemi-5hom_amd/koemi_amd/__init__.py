@@ -1,0 +1,48 @@
+"""MI355X (gfx950) HERM hot path behind Koemi-5HOM's operator fronts.
+
+Module map (reference front -> this package):
+
+* ``koemi.cuda_kernels.dense``  -> ``koemi_amd.dense``     (dense_affine_scan)
+* ``koemi.model.cuda_scan``     -> ``koemi_amd.cuda_scan`` (cuda_affine_scan)
+* ``koemi.cuda_kernels.core``   -> ``koemi_amd.core``      (fused_rmsnorm_silu)
+* ``koemi.cuda_kernels.think``  -> ``koemi_amd.think``     (causal_surprise, ...)
+* ``koemi.cuda_kernels.moe``    -> ``koemi_amd.moe``       (route/permute/grouped MLP/combine)
+* ``koemi.cuda_kernels.loader`` -> ``koemi_amd.loader``
+
+Every operator runs a hand-written HIP kernel from ``libkoemi_hip.so``
+(C ABI in ``include/koemi_hip.h``); none falls back to CPU or to PyTorch.
+"""
+
+from koemi_amd.core import fused_rmsnorm_silu, load_core_extension
+from koemi_amd.cuda_scan import cuda_affine_scan, diagnose_cuda_affine_scan
+from koemi_amd.dense import dense_affine_scan, native_cuda_available
+from koemi_amd.moe import (
+    combine_topk,
+    expert_activation_counts,
+    grouped_expert_mlp_inference,
+    load_native_extension,
+    permute_topk,
+    route_topk_learned,
+    route_topk_valid,
+)
+from koemi_amd.think import benchmark_causal_surprise, causal_surprise, salience_admission, surprise_from_logits
+
+__all__ = [
+    "benchmark_causal_surprise",
+    "causal_surprise",
+    "combine_topk",
+    "cuda_affine_scan",
+    "dense_affine_scan",
+    "diagnose_cuda_affine_scan",
+    "expert_activation_counts",
+    "fused_rmsnorm_silu",
+    "grouped_expert_mlp_inference",
+    "load_core_extension",
+    "load_native_extension",
+    "native_cuda_available",
+    "permute_topk",
+    "route_topk_learned",
+    "route_topk_valid",
+    "salience_admission",
+    "surprise_from_logits",
+]

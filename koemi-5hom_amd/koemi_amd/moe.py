@@ -1,0 +1,561 @@
+"""MoE fronts on the gfx950 HIP kernels: route, permute, grouped GLU-FFN, combine.
+
+Mirrors ``src/koemi/cuda_kernels/moe/__init__.py`` of the reference (names,
+positional/keyword layout, return tuples, exception classes, validation order
+and messages). The contract checks that the reference runs as several
+``.item()`` synchronisations (moe/__init__.py:113-125, 213-220, 293-301,
+345-353) run here as one device check and one read-back; ``validate=False``
+(keyword-only, build-side) skips them for already checked inputs, like
+``validate_targets=False`` of the think front.
+
+Build-side keyword-only extensions (absent from the reference signatures):
+
+* ``permute_topk(..., pair_weights=None)`` also returns the weights permuted
+  into sorted order, for the learned gate;
+* ``combine_topk(..., pair_weights=None)`` weighs each sorted pair by its gate
+  probability (router.py:73) instead of ``1 / top_k`` (moe_kernels.cu:226-228);
+* ``route_topk_learned`` — softmax top-k gate of router.py:46-49;
+* ``expert_activation_counts`` — per-expert counts of network.py:48-70.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import Tensor
+
+from koemi_amd import _native
+
+__all__ = [
+    "CudaMoeUnavailableError",
+    "CudaMoeValidationError",
+    "combine_topk",
+    "expert_activation_counts",
+    "grouped_expert_mlp_inference",
+    "load_native_extension",
+    "permute_topk",
+    "route_topk_learned",
+    "route_topk_valid",
+]
+
+_MAX_PERMUTE_EXPERTS = 4095
+
+
+class CudaMoeUnavailableError(RuntimeError):
+    """Raised when the MoE kernels cannot run (no GPU or no kernel library)."""
+
+
+class CudaMoeValidationError(ValueError):
+    """Raised when a MoE operation receives an unsafe contract."""
+
+
+def _require_library() -> None:
+    if not torch.cuda.is_available():
+        raise CudaMoeUnavailableError("Koemi MoE kernels require torch.cuda.is_available() == True")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise CudaMoeUnavailableError(f"Koemi MoE kernel library is unavailable: {error}") from error
+
+
+def _require_cuda_tensor(tensor: Tensor, name: str) -> None:
+    if not isinstance(tensor, Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not tensor.is_cuda:
+        raise CudaMoeValidationError(f"{name} must be a CUDA tensor")
+    if not tensor.is_contiguous():
+        raise CudaMoeValidationError(f"{name} must be contiguous")
+
+
+def _require_same_cuda_device(tensors: dict[str, Tensor]) -> None:
+    devices = {tensor.device for tensor in tensors.values()}
+    if len(devices) != 1:
+        rendered = ", ".join(sorted(str(device) for device in devices))
+        raise CudaMoeValidationError(f"all MoE tensors must use one CUDA device, found {rendered}")
+
+
+def _require_supported_context_dtype(tensor: Tensor, name: str) -> None:
+    if tensor.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise CudaMoeValidationError(f"{name} must use float32, float16, or bfloat16; found {tensor.dtype}")
+
+
+def _require_positive_bounded(value: int, name: str, upper_bound: int) -> int:
+    if isinstance(value, bool) or not isinstance(value, int) or value < 1:
+        raise CudaMoeValidationError(f"{name} must be a positive integer")
+    if value > upper_bound:
+        raise CudaMoeValidationError(f"{name} exceeds the CUDA MoE limit of {upper_bound}")
+    return value
+
+
+def _require_inference_only(tensors: dict[str, Tensor]) -> None:
+    gradient_tensors = [name for name, tensor in tensors.items() if tensor.requires_grad]
+    if gradient_tensors:
+        raise RuntimeError("the native MoE path is inference-only; tensors require gradients: " + ", ".join(gradient_tensors))
+
+
+def _aligned(tensor: Tensor) -> Tensor:
+    """Contiguous tensor whose first element is 16-byte aligned (vector loads)."""
+
+    return tensor if tensor.data_ptr() % 16 == 0 else tensor.clone()
+
+
+def _assignment_flags(assignments: Tensor, valid_mask: Tensor, expert_count: int) -> tuple[bool, bool]:
+    """(any valid assignment out of range, any valid token repeating an expert)."""
+
+    flags = torch.zeros((2,), device=assignments.device, dtype=torch.int32)
+    tokens, top_k = assignments.shape
+    with torch.cuda.device(assignments.device):
+        _native.call(
+            "koemi_moe_check_assignments",
+            assignments.data_ptr(),
+            _native.dtype_code(assignments.dtype),
+            valid_mask.data_ptr(),
+            flags.data_ptr(),
+            tokens,
+            top_k,
+            expert_count,
+            _native.stream_of(assignments.device),
+        )
+    out_of_range, duplicate = flags.tolist()
+    return bool(out_of_range), bool(duplicate)
+
+
+def route_topk_valid(
+    token_ids: Tensor,
+    previous_token_ids: Tensor,
+    valid_mask: Tensor,
+    *,
+    expert_count: int,
+    top_k: int,
+    validate: bool = True,
+) -> Tensor:
+    """Route tokens with HERM's content hash and reject duplicate valid slots
+    (reference moe/__init__.py:128-176; int64 hash semantics of experts.py:283-289).
+
+    Returns ``token_ids.shape + (top_k,)`` int64; invalid rows contain ``-1``.
+    """
+
+    tensors = {"token_ids": token_ids, "previous_token_ids": previous_token_ids, "valid_mask": valid_mask}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    if token_ids.dtype not in (torch.int32, torch.int64):
+        raise CudaMoeValidationError("token_ids must use int32 or int64")
+    if previous_token_ids.dtype != token_ids.dtype:
+        raise CudaMoeValidationError("token_ids and previous_token_ids must use one dtype")
+    if valid_mask.dtype != torch.bool:
+        raise CudaMoeValidationError("valid_mask must use boolean dtype")
+    if token_ids.shape != previous_token_ids.shape or token_ids.shape != valid_mask.shape:
+        raise CudaMoeValidationError("routing tensors must have equal shapes")
+    expert_count = _require_positive_bounded(expert_count, "expert_count", 1 << 20)
+    top_k = _require_positive_bounded(top_k, "top_k", 256)
+    if top_k > expert_count:
+        raise CudaMoeValidationError("top_k must not exceed expert_count")
+    _require_library()
+    count = token_ids.numel()
+    assignments = torch.empty((count, top_k), device=token_ids.device, dtype=torch.int64)
+    duplicate = torch.zeros((1,), device=token_ids.device, dtype=torch.int32)
+    if count:
+        with torch.cuda.device(token_ids.device):
+            _native.call(
+                "koemi_moe_route_hash",
+                token_ids.data_ptr(),
+                previous_token_ids.data_ptr(),
+                valid_mask.data_ptr(),
+                _native.dtype_code(token_ids.dtype),
+                assignments.data_ptr(),
+                duplicate.data_ptr(),
+                count,
+                expert_count,
+                top_k,
+                _native.stream_of(token_ids.device),
+            )
+    assignments = assignments.reshape(*token_ids.shape, top_k)
+    if validate and count and top_k >= 2 and bool(duplicate.item()):
+        raise CudaMoeValidationError("MoE routing produced duplicate experts for a valid token")
+    return assignments
+
+
+def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int) -> tuple[Tensor, Tensor]:
+    """Learned softmax top-k gate (router.py:46-49): returns int64 assignments and
+    fp32 weights of shape ``router_logits.shape[:-1] + (top_k,)``, descending by
+    probability (ties to the lower expert index); invalid rows get -1 and 0."""
+
+    tensors = {"router_logits": router_logits, "valid_mask": valid_mask}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    if router_logits.dtype != torch.float32:
+        raise CudaMoeValidationError("router_logits must use float32")
+    if router_logits.ndim < 1 or valid_mask.shape != router_logits.shape[:-1]:
+        raise CudaMoeValidationError("valid_mask must match router_logits.shape[:-1]")
+    if valid_mask.dtype != torch.bool:
+        raise CudaMoeValidationError("valid_mask must use boolean dtype")
+    expert_count = _require_positive_bounded(int(router_logits.shape[-1]), "expert_count", 1024)
+    top_k = _require_positive_bounded(top_k, "top_k", 256)
+    if top_k > expert_count:
+        raise CudaMoeValidationError("top_k must not exceed expert_count")
+    _require_library()
+    count = valid_mask.numel()
+    assignments = torch.empty((count, top_k), device=router_logits.device, dtype=torch.int64)
+    weights = torch.empty((count, top_k), device=router_logits.device, dtype=torch.float32)
+    if count:
+        with torch.cuda.device(router_logits.device):
+            _native.call(
+                "koemi_moe_route_learned",
+                router_logits.data_ptr(),
+                valid_mask.data_ptr(),
+                assignments.data_ptr(),
+                weights.data_ptr(),
+                count,
+                expert_count,
+                top_k,
+                _native.stream_of(router_logits.device),
+            )
+    shape = (*valid_mask.shape, top_k)
+    return assignments.reshape(shape), weights.reshape(shape)
+
+
+def expert_activation_counts(assignments: Tensor, valid_mask: Tensor, *, expert_count: int) -> Tensor:
+    """int64 ``[expert_count]`` counts of valid in-range assignments (network.py:48-70)."""
+
+    tensors = {"assignments": assignments, "valid_mask": valid_mask}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    if assignments.dtype not in (torch.int32, torch.int64):
+        raise CudaMoeValidationError("assignments must use int32 or int64")
+    if assignments.ndim < 1 or valid_mask.shape != assignments.shape[:-1] or valid_mask.dtype != torch.bool:
+        raise CudaMoeValidationError("valid_mask must be boolean with shape assignments.shape[:-1]")
+    expert_count = _require_positive_bounded(expert_count, "expert_count", 1 << 20)
+    _require_library()
+    top_k = int(assignments.shape[-1])
+    counts = torch.empty((expert_count,), device=assignments.device, dtype=torch.int64)
+    with torch.cuda.device(assignments.device):
+        _native.call(
+            "koemi_moe_expert_counts",
+            assignments.data_ptr(),
+            _native.dtype_code(assignments.dtype),
+            valid_mask.data_ptr(),
+            counts.data_ptr(),
+            valid_mask.numel(),
+            max(top_k, 1),
+            expert_count,
+            _native.stream_of(assignments.device),
+        )
+    return counts
+
+
+def permute_topk(
+    context: Tensor,
+    assignments: Tensor,
+    valid_mask: Tensor,
+    *,
+    expert_count: int,
+    pair_weights: Tensor | None = None,
+    validate: bool = True,
+) -> tuple[Tensor, ...]:
+    """Sort valid token-expert pairs into stable expert segments
+    (reference moe/__init__.py:179-228).
+
+    Returns ``(sorted_context, sorted_rows, sorted_experts, segment_offsets)``;
+    invalid pairs follow all expert segments with the sentinel expert
+    ``expert_count`` and zero context rows. With ``pair_weights`` ([tokens,
+    top_k] float32) a fifth tensor, the weights in sorted order, is returned.
+    """
+
+    tensors = {"context": context, "assignments": assignments, "valid_mask": valid_mask}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    _require_supported_context_dtype(context, "context")
+    if context.ndim < 2 or context.shape[-1] < 1:
+        raise CudaMoeValidationError("context must have at least two dimensions and a non-empty width")
+    if assignments.ndim != 2 or assignments.shape[0] != context.numel() // context.shape[-1]:
+        raise CudaMoeValidationError("assignments must have shape [token_count, top_k]")
+    if assignments.dtype not in (torch.int32, torch.int64):
+        raise CudaMoeValidationError("assignments must use int32 or int64")
+    if valid_mask.ndim != 1 or valid_mask.shape[0] != assignments.shape[0]:
+        raise CudaMoeValidationError("valid_mask must have shape [token_count]")
+    expert_count = _require_positive_bounded(expert_count, "expert_count", 1 << 20)
+    top_k = _require_positive_bounded(int(assignments.shape[1]), "top_k", 256)
+    if top_k > expert_count:
+        raise CudaMoeValidationError("top_k must not exceed expert_count")
+    if expert_count > _MAX_PERMUTE_EXPERTS:
+        raise CudaMoeValidationError(f"expert_count exceeds the HIP MoE permute limit of {_MAX_PERMUTE_EXPERTS}")
+    if pair_weights is not None:
+        _require_cuda_tensor(pair_weights, "pair_weights")
+        if pair_weights.shape != assignments.shape or pair_weights.dtype != torch.float32:
+            raise CudaMoeValidationError("pair_weights must be float32 with the shape of assignments")
+        if pair_weights.device != context.device:
+            raise CudaMoeValidationError("all MoE tensors must use one CUDA device")
+    _require_library()
+    if validate and assignments.shape[0] > 0:
+        out_of_range, duplicate = _assignment_flags(assignments, valid_mask, expert_count)
+        if out_of_range:
+            raise CudaMoeValidationError("valid MoE assignments must be in [0, expert_count)")
+        if duplicate and top_k >= 2:
+            raise CudaMoeValidationError("MoE permutation received duplicate experts for a valid token")
+    flat = _aligned(context.reshape(-1, context.shape[-1]))
+    tokens, width = flat.shape
+    pairs = tokens * top_k
+    device = context.device
+    sorted_context = torch.empty((pairs, width), device=device, dtype=context.dtype)
+    sorted_rows = torch.empty((pairs,), device=device, dtype=torch.int64)
+    sorted_experts = torch.empty((pairs,), device=device, dtype=torch.int64)
+    segment_offsets = torch.empty((expert_count + 1,), device=device, dtype=torch.int64)
+    sorted_weights = torch.empty((pairs,), device=device, dtype=torch.float32) if pair_weights is not None else None
+    if tokens == 0:
+        raise CudaMoeValidationError("context dimensions must be positive")
+    workspace_bytes = _native.query("koemi_moe_permute_workspace_bytes", tokens, top_k, expert_count)
+    workspace = torch.empty((workspace_bytes,), device=device, dtype=torch.uint8)
+    with torch.cuda.device(device):
+        _native.call(
+            "koemi_moe_permute",
+            flat.data_ptr(),
+            _native.dtype_code(flat.dtype),
+            assignments.data_ptr(),
+            _native.dtype_code(assignments.dtype),
+            valid_mask.data_ptr(),
+            _native.ptr(pair_weights),
+            sorted_context.data_ptr(),
+            sorted_rows.data_ptr(),
+            sorted_experts.data_ptr(),
+            segment_offsets.data_ptr(),
+            _native.ptr(sorted_weights),
+            tokens,
+            width,
+            top_k,
+            expert_count,
+            workspace.data_ptr(),
+            workspace_bytes,
+            _native.stream_of(device),
+        )
+    if sorted_weights is not None:
+        return sorted_context, sorted_rows, sorted_experts, segment_offsets, sorted_weights
+    return sorted_context, sorted_rows, sorted_experts, segment_offsets
+
+
+def grouped_expert_mlp_inference(
+    sorted_context: Tensor,
+    sorted_experts: Tensor,
+    segment_offsets: Tensor,
+    gate_weights: Tensor,
+    gate_biases: Tensor,
+    value_weights: Tensor,
+    value_biases: Tensor,
+    output_weights: Tensor,
+    output_biases: Tensor,
+    *,
+    validate: bool = True,
+) -> Tensor:
+    """Grouped gated MLP for sorted MoE pairs (reference moe/__init__.py:231-312).
+
+    Inference-only. Weights ``[E, H, D]``, ``[E, H]``, ``[E, H, D]``, ``[E, H]``,
+    ``[E, D, H]``, ``[E, D]``; bf16 runs on MFMA with fp32 accumulation.
+    """
+
+    tensors = {
+        "sorted_context": sorted_context,
+        "sorted_experts": sorted_experts,
+        "segment_offsets": segment_offsets,
+        "gate_weights": gate_weights,
+        "gate_biases": gate_biases,
+        "value_weights": value_weights,
+        "value_biases": value_biases,
+        "output_weights": output_weights,
+        "output_biases": output_biases,
+    }
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    _require_supported_context_dtype(sorted_context, "sorted_context")
+    _require_inference_only(tensors)
+    if sorted_context.ndim != 2:
+        raise CudaMoeValidationError("sorted_context must have shape [pair_count, width]")
+    if sorted_experts.ndim != 1 or sorted_experts.shape[0] != sorted_context.shape[0]:
+        raise CudaMoeValidationError("sorted_experts must have shape [pair_count]")
+    if sorted_experts.dtype != torch.int64:
+        raise CudaMoeValidationError("sorted_experts must use int64")
+    if segment_offsets.dtype != torch.int64 or segment_offsets.ndim != 1:
+        raise CudaMoeValidationError("segment_offsets must be a one-dimensional int64 tensor")
+    if gate_weights.ndim != 3 or value_weights.ndim != 3 or output_weights.ndim != 3:
+        raise CudaMoeValidationError("expert weights must be three-dimensional")
+    expert_count, hidden_width, input_width = gate_weights.shape
+    if input_width != sorted_context.shape[1]:
+        raise CudaMoeValidationError("gate weight input width does not match sorted_context")
+    if value_weights.shape != (expert_count, hidden_width, input_width):
+        raise CudaMoeValidationError("value weights do not match gate weight shapes")
+    if output_weights.shape[0] != expert_count or output_weights.shape[1] != input_width:
+        raise CudaMoeValidationError("output weights do not match expert and output widths")
+    if output_weights.shape[2] != hidden_width:
+        raise CudaMoeValidationError("output weight hidden width does not match gate weights")
+    if gate_biases.shape != (expert_count, hidden_width):
+        raise CudaMoeValidationError("gate biases do not match gate weights")
+    if value_biases.shape != (expert_count, hidden_width):
+        raise CudaMoeValidationError("value biases do not match value weights")
+    if output_biases.shape != (expert_count, input_width):
+        raise CudaMoeValidationError("output biases do not match output weights")
+    if segment_offsets.shape[0] != expert_count + 1:
+        raise CudaMoeValidationError("segment_offsets must have expert_count + 1 entries")
+    floating = [t for t in tensors.values() if t is not sorted_experts and t is not segment_offsets]
+    if any(tensor.dtype != sorted_context.dtype for tensor in floating):
+        raise CudaMoeValidationError("all grouped MLP floating tensors must use one dtype")
+    _require_library()
+    pairs = int(sorted_context.shape[0])
+    if validate:
+        offsets = segment_offsets.tolist()
+        valid_pair_count = int(offsets[-1])
+        if valid_pair_count < 0 or valid_pair_count > pairs:
+            raise CudaMoeValidationError("segment_offsets final value is outside pair_count")
+        if valid_pair_count:
+            selected = sorted_experts[:valid_pair_count]
+            bad = torch.stack(((selected < 0).any(), (selected >= expert_count).any())).tolist()
+            if any(bad):
+                raise CudaMoeValidationError("sorted expert ids are outside the expert catalog")
+        if any(b < a for a, b in zip(offsets, offsets[1:])) or offsets[0] < 0:
+            raise CudaMoeValidationError("segment_offsets must be non-decreasing")
+    output = torch.empty_like(sorted_context)
+    if pairs == 0:
+        return output
+    x = _aligned(sorted_context)
+    weights = [_aligned(t) for t in (gate_weights, gate_biases, value_weights, value_biases, output_weights, output_biases)]
+    workspace_bytes = _native.query(
+        "koemi_moe_grouped_mlp_workspace_bytes",
+        pairs,
+        input_width,
+        hidden_width,
+        expert_count,
+        _native.dtype_code(sorted_context.dtype),
+    )
+    workspace = torch.empty((workspace_bytes,), device=sorted_context.device, dtype=torch.uint8)
+    with torch.cuda.device(sorted_context.device):
+        _native.call(
+            "koemi_moe_grouped_mlp",
+            x.data_ptr(),
+            sorted_experts.data_ptr(),
+            segment_offsets.data_ptr(),
+            *(w.data_ptr() for w in weights),
+            output.data_ptr(),
+            pairs,
+            input_width,
+            hidden_width,
+            expert_count,
+            _native.dtype_code(sorted_context.dtype),
+            workspace.data_ptr(),
+            workspace_bytes,
+            _native.stream_of(sorted_context.device),
+        )
+    return output
+
+
+def combine_topk(
+    expert_outputs: Tensor,
+    sorted_rows: Tensor,
+    segment_offsets: Tensor,
+    *,
+    token_count: int,
+    top_k: int,
+    pair_weights: Tensor | None = None,
+    validate: bool = True,
+) -> Tensor:
+    """Combine sorted expert outputs into token rows using ``1 / top_k``, or the
+    per-pair ``pair_weights`` (sorted order, float32) of a learned gate
+    (reference moe/__init__.py:315-360). Deterministic: no atomics in the sum."""
+
+    tensors = {"expert_outputs": expert_outputs, "sorted_rows": sorted_rows, "segment_offsets": segment_offsets}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    _require_supported_context_dtype(expert_outputs, "expert_outputs")
+    _require_inference_only(tensors)
+    if expert_outputs.ndim != 2:
+        raise CudaMoeValidationError("expert_outputs must have shape [pair_count, width]")
+    if sorted_rows.dtype != torch.int64 or sorted_rows.ndim != 1:
+        raise CudaMoeValidationError("sorted_rows must be a one-dimensional int64 tensor")
+    if sorted_rows.shape[0] != expert_outputs.shape[0]:
+        raise CudaMoeValidationError("sorted_rows must match expert_outputs pair_count")
+    if segment_offsets.dtype != torch.int64 or segment_offsets.ndim != 1:
+        raise CudaMoeValidationError("segment_offsets must be a one-dimensional int64 tensor")
+    token_count = _require_positive_bounded(token_count, "token_count", 1 << 31)
+    top_k = _require_positive_bounded(top_k, "top_k", 256)
+    if segment_offsets.shape[0] < 2:
+        raise CudaMoeValidationError("segment_offsets must have at least two entries")
+    if expert_outputs.shape[1] < 1:
+        raise CudaMoeValidationError("expert_outputs must have shape [pair_count, width]")
+    if pair_weights is not None:
+        _require_cuda_tensor(pair_weights, "pair_weights")
+        if pair_weights.shape != sorted_rows.shape or pair_weights.dtype != torch.float32:
+            raise CudaMoeValidationError("pair_weights must be float32 of shape [pair_count]")
+    _require_library()
+    pairs = int(expert_outputs.shape[0])
+    if validate:
+        valid_pair_count = int(segment_offsets[-1].item())
+        if valid_pair_count < 0 or valid_pair_count > pairs:
+            raise CudaMoeValidationError("segment_offsets final value is outside pair_count")
+        if valid_pair_count:
+            selected = sorted_rows[:valid_pair_count]
+            bad = torch.stack(((selected < 0).any(), (selected >= token_count).any())).tolist()
+            if any(bad):
+                raise CudaMoeValidationError("sorted rows are outside token_count")
+    width = int(expert_outputs.shape[1])
+    y = _aligned(expert_outputs)
+    combined = torch.empty((token_count, width), device=expert_outputs.device, dtype=expert_outputs.dtype)
+    workspace_bytes = _native.query("koemi_moe_combine_workspace_bytes", token_count, top_k)
+    workspace = torch.empty((workspace_bytes,), device=expert_outputs.device, dtype=torch.uint8)
+    with torch.cuda.device(expert_outputs.device):
+        _native.call(
+            "koemi_moe_combine",
+            y.data_ptr(),
+            sorted_rows.data_ptr(),
+            segment_offsets.data_ptr(),
+            _native.ptr(pair_weights),
+            combined.data_ptr(),
+            pairs,
+            width,
+            token_count,
+            top_k,
+            int(segment_offsets.shape[0]) - 1,
+            _native.dtype_code(expert_outputs.dtype),
+            workspace.data_ptr(),
+            workspace_bytes,
+            _native.stream_of(expert_outputs.device),
+        )
+    return combined
+
+
+class _MoeExtension:
+    """Object with the operator names of the reference's pybind MoE module
+    (moe_kernels.cpp:256-262), over the C ABI."""
+
+    KOEMI_CUDA_ABI_VERSION = _native.ABI_VERSION
+
+    @staticmethod
+    def route_topk(token_ids: Tensor, previous_token_ids: Tensor, valid_mask: Tensor, expert_count: int, top_k: int) -> Tensor:
+        return route_topk_valid(
+            token_ids, previous_token_ids, valid_mask, expert_count=expert_count, top_k=top_k, validate=False
+        ).reshape(-1, top_k)
+
+    @staticmethod
+    def permute_topk(context: Tensor, assignments: Tensor, valid_mask: Tensor, expert_count: int) -> list[Tensor]:
+        return list(permute_topk(context, assignments, valid_mask, expert_count=expert_count, validate=False))
+
+    @staticmethod
+    def grouped_expert_mlp(*tensors: Tensor) -> Tensor:
+        return grouped_expert_mlp_inference(*tensors, validate=False)
+
+    @staticmethod
+    def combine_topk(expert_outputs: Tensor, sorted_rows: Tensor, segment_offsets: Tensor, token_count: int, top_k: int) -> Tensor:
+        return combine_topk(expert_outputs, sorted_rows, segment_offsets, token_count=token_count, top_k=top_k, validate=False)
+
+
+_MOE_EXTENSION = _MoeExtension()
+
+
+def load_native_extension() -> Any:
+    """Load the prebuilt kernel library (reference moe/__init__.py:24-70);
+    returns an object exposing the reference's native op names."""
+
+    _require_library()
+    return _MOE_EXTENSION

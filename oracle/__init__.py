@@ -1,0 +1,371 @@
+"""CPU oracle of the Koemi-5HOM HERM hot path (numpy + the C restatement).
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
+checker or the CPU baseline — never as the thing measured or shipped. The
+product package ``koemi_amd`` does not import it and has no CPU fallback.
+
+Each function names the reference lines it restates. Pinning (which checks in
+tests/test_oracle.py fix each function beyond its own formula) is listed in the
+module docstring of that test file.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+from oracle.build import LIBRARY, build
+
+PAD_TOKEN_ID = 256  # configuration/settings.py:10-11
+
+# ----------------------------------------------------------------- C library
+
+_LIB: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The C restatement, built on first use if the shared object is missing."""
+
+    global _LIB
+    if _LIB is None:
+        if not LIBRARY.is_file():
+            build()
+        handle = ctypes.CDLL(str(LIBRARY))
+        handle.oracle_det_expf.restype = c_float
+        handle.oracle_det_expf.argtypes = [c_float]
+        handle.oracle_det_logf.restype = c_float
+        handle.oracle_det_logf.argtypes = [c_float]
+        handle.oracle_quantile.restype = c_float
+        handle.oracle_quantile.argtypes = [c_void_p, c_int64, c_float]
+        for name in ("oracle_scan_sequential_f32", "oracle_scan_sequential_f64"):
+            fn = getattr(handle, name)
+            fn.restype = None
+            fn.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int]
+        handle.oracle_surprise_rows.restype = None
+        handle.oracle_surprise_rows.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float]
+        handle.oracle_route_learned.restype = None
+        handle.oracle_route_learned.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64]
+        for name in ("oracle_det_expf_array", "oracle_det_logf_array"):
+            fn = getattr(handle, name)
+            fn.restype = None
+            fn.argtypes = [c_void_p, c_void_p, c_int64]
+        handle.oracle_rmsnorm_silu_f32.restype = None
+        handle.oracle_rmsnorm_silu_f32.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float]
+        _LIB = handle
+    return _LIB
+
+
+def _p(array: np.ndarray | None) -> int | None:
+    return None if array is None else array.ctypes.data
+
+
+# ---------------------------------------------------------------- bfloat16
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    """bfloat16 bit patterns (uint16) -> float32."""
+
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(values: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest even; NaN kept quiet."""
+
+    u = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(values)
+    if nan.any():
+        rounded = rounded.copy()
+        rounded[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return rounded
+
+
+def round_bf16(values: np.ndarray) -> np.ndarray:
+    return bf16_to_f32(f32_to_bf16(np.asarray(values, dtype=np.float32)))
+
+
+# -------------------------------------------------------------------- scan
+
+def scan_sequential(retention: np.ndarray, increment: np.ndarray, initial: np.ndarray | None = None) -> np.ndarray:
+    """h_t = a_t * h_{t-1} + b_t in the input dtype (float32 or float64), h_{-1} =
+    initial (zeros if None). Retention is full-shape or [B, L] (+ trailing 1s).
+    Restates tests/model/test_scan.py:10-16 and tests/cuda/test_dense_cuda.py:21-33."""
+
+    dtype = increment.dtype
+    assert dtype in (np.float32, np.float64)
+    b = np.ascontiguousarray(increment)
+    B, L = b.shape[:2]
+    F = int(np.prod(b.shape[2:])) if b.ndim > 2 else 1
+    a = np.ascontiguousarray(retention, dtype=dtype)
+    broadcast = a.size == B * L and b.size != B * L
+    if not broadcast and a.shape != b.shape:
+        a = np.ascontiguousarray(np.broadcast_to(a, b.shape))
+    h0 = np.zeros((B, F), dtype=dtype) if initial is None else np.ascontiguousarray(initial, dtype=dtype).reshape(B, F)
+    out = np.empty_like(b)
+    fn = lib().oracle_scan_sequential_f32 if dtype == np.float32 else lib().oracle_scan_sequential_f64
+    fn(_p(a), _p(b), _p(h0), _p(out), B, L, F, int(broadcast))
+    return out
+
+
+def scan_hillis_steele(retention: np.ndarray, increment: np.ndarray, initial: np.ndarray | None = None) -> np.ndarray:
+    """The model-path window scan of model/scan.py:17-30 (log2 L doubling rounds),
+    vectorized over the state columns; used as the second CPU baseline."""
+
+    coefficient = np.broadcast_to(retention, increment.shape).astype(increment.dtype)
+    value = increment.copy()
+    length = increment.shape[1]
+    offset = 1
+    while offset < length:
+        shifted_c = np.concatenate((np.ones_like(coefficient[:, :offset]), coefficient[:, : length - offset]), axis=1)
+        shifted_v = np.concatenate((np.zeros_like(value[:, :offset]), value[:, : length - offset]), axis=1)
+        value = coefficient * shifted_v + value
+        coefficient = coefficient * shifted_c
+        offset *= 2
+    if initial is None:
+        return value
+    return value + coefficient * initial[:, None]
+
+
+# ------------------------------------------------------------ rmsnorm-silu
+
+def rmsnorm_silu_f64(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> tuple[np.ndarray, np.ndarray]:
+    """silu(x * rsqrt(mean(x^2) + eps) * w) in float64 (test_core_cuda.py:70-71,
+    layers.py:14-16 followed by silu). Returns (y, inverse_rms)."""
+
+    xf = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt(np.mean(xf * xf, axis=-1) + eps)
+    v = xf * inv[:, None] * np.asarray(weight, dtype=np.float64)
+    return v / (1.0 + np.exp(-v)), inv
+
+
+def rmsnorm_silu_f32(x: np.ndarray, weight: np.ndarray, eps: float = 1e-6) -> tuple[np.ndarray, np.ndarray]:
+    """fp32 port of the fused forward (core/rmsnorm_silu.cu:62-91), for the CPU baseline."""
+
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weight, dtype=np.float32)
+    rows, hidden = x.shape
+    y = np.empty_like(x)
+    inv = np.empty((rows,), dtype=np.float32)
+    lib().oracle_rmsnorm_silu_f32(_p(x), _p(w), _p(y), _p(inv), rows, hidden, c_float(eps))
+    return y, inv
+
+
+# --------------------------------------------------------------- surprise
+
+def log_vocab_f32(vocab: int) -> float:
+    return float(np.float32(math.log(float(np.float32(vocab)))))
+
+
+def det_expf(x: float) -> float:
+    return float(lib().oracle_det_expf(float(x)))
+
+
+def det_logf(x: float) -> float:
+    return float(lib().oracle_det_logf(float(x)))
+
+
+def det_expf_array(x: np.ndarray) -> np.ndarray:
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(xs)
+    lib().oracle_det_expf_array(_p(xs), _p(out), xs.size)
+    return out
+
+
+def det_logf_array(x: np.ndarray) -> np.ndarray:
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(xs)
+    lib().oracle_det_logf_array(_p(xs), _p(out), xs.size)
+    return out
+
+
+def surprise_rows(
+    logits: np.ndarray, targets: np.ndarray, valid: np.ndarray, bias: np.ndarray | None = None
+) -> np.ndarray:
+    """Per-row surprise with the kernel's rounding steps (network.py:677-688;
+    surprise_kernel.cu:84-134). logits float32 [R, V]."""
+
+    z = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, vocab = z.shape
+    t = np.ascontiguousarray(targets, dtype=np.int64).reshape(rows)
+    v = np.ascontiguousarray(valid, dtype=np.uint8).reshape(rows)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.empty((rows,), dtype=np.float32)
+    lib().oracle_surprise_rows(_p(z), _p(b), _p(t), _p(v), _p(out), rows, vocab, c_float(log_vocab_f32(vocab)))
+    return out
+
+
+def surprise_rows_f64(logits: np.ndarray, targets: np.ndarray, valid: np.ndarray) -> np.ndarray:
+    """Surprise in float64 via a max-shifted logsumexp (reference_causal_surprise,
+    tests/cuda/test_think_cuda.py:19-32), as the accuracy yardstick."""
+
+    z = np.asarray(logits, dtype=np.float64)
+    m = z.max(axis=-1, keepdims=True)
+    lse = np.log(np.exp(z - m).sum(axis=-1)) + m[..., 0]
+    zt = np.take_along_axis(z, np.asarray(targets, dtype=np.int64)[..., None], axis=-1)[..., 0]
+    s = 1.0 - np.exp(-(lse - zt) / math.log(z.shape[-1]))
+    return np.where(np.asarray(valid, dtype=bool), s, 0.0)
+
+
+def quantile(scores: np.ndarray, q: float) -> float:
+    s = np.ascontiguousarray(scores, dtype=np.float32).reshape(-1)
+    return float(lib().oracle_quantile(_p(s), s.size, c_float(q)))
+
+
+def admission(scores: np.ndarray, valid: np.ndarray, *, threshold: float | None = None, q: float | None = None) -> tuple[np.ndarray, float]:
+    """valid & (s > tau) with strict '>' (network.py:349); tau fixed or the q-quantile."""
+
+    s = np.asarray(scores, dtype=np.float32)
+    tau = float(np.float32(threshold)) if threshold is not None else quantile(s, q)
+    return np.asarray(valid, dtype=bool) & (s > np.float32(tau)), tau
+
+
+# ------------------------------------------------------------------- MoE
+
+TOKEN_HASH_FACTOR = 1_000_003          # experts.py:12
+PREVIOUS_TOKEN_HASH_FACTOR = 97_409    # experts.py:13
+HASH_MIX_MULTIPLIER = 0x45D9F3B        # experts.py:15
+SLOT_OFFSET = 0x9E3779B9               # experts.py:288
+
+
+def content_hash(token_ids: np.ndarray, previous_token_ids: np.ndarray) -> np.ndarray:
+    """experts.py:30-38 in int64 arithmetic (two's-complement wrap of the
+    products, masked to 32 bits)."""
+
+    mask = np.int64(0xFFFFFFFF)
+    with np.errstate(over="ignore"):
+        v = (np.asarray(token_ids, dtype=np.int64) * TOKEN_HASH_FACTOR
+             + np.asarray(previous_token_ids, dtype=np.int64) * PREVIOUS_TOKEN_HASH_FACTOR) & mask
+        v = v ^ (v >> 16)
+        v = (v * HASH_MIX_MULTIPLIER) & mask
+        v = v ^ (v >> 16)
+        v = (v * HASH_MIX_MULTIPLIER) & mask
+    return v ^ (v >> 16)
+
+
+def route_hash(token_ids: np.ndarray, previous_token_ids: np.ndarray, valid: np.ndarray, expert_count: int, top_k: int) -> np.ndarray:
+    """assign_top_k of experts.py:283-289: (hash + s * 0x9E3779B9) mod E in int64; invalid -> -1."""
+
+    h = content_hash(token_ids, previous_token_ids)
+    offsets = np.arange(top_k, dtype=np.int64) * SLOT_OFFSET
+    a = np.remainder(h[..., None] + offsets, expert_count)
+    return np.where(np.asarray(valid, dtype=bool)[..., None], a, -1).astype(np.int64)
+
+
+def route_learned(router_logits: np.ndarray, valid: np.ndarray, top_k: int) -> tuple[np.ndarray, np.ndarray]:
+    """router.py:46-49 with the kernel's rounding steps: (assignments, weights)."""
+
+    z = np.ascontiguousarray(router_logits, dtype=np.float32)
+    E = z.shape[-1]
+    T = z.size // E
+    v = np.ascontiguousarray(valid, dtype=np.uint8).reshape(T)
+    idx = np.empty((T, top_k), dtype=np.int64)
+    w = np.empty((T, top_k), dtype=np.float32)
+    lib().oracle_route_learned(_p(z), _p(v), _p(idx), _p(w), T, E, top_k)
+    shape = tuple(z.shape[:-1]) + (top_k,)
+    return idx.reshape(shape), w.reshape(shape)
+
+
+def expert_counts(assignments: np.ndarray, valid: np.ndarray, expert_count: int) -> np.ndarray:
+    """network.py:48-70: counts of valid, in-range assignments per expert."""
+
+    a = np.asarray(assignments, dtype=np.int64)
+    counted = np.asarray(valid, dtype=bool)[..., None] & (a >= 0) & (a < expert_count)
+    return np.bincount(a[counted].reshape(-1), minlength=expert_count).astype(np.int64)
+
+
+def pair_keys(assignments: np.ndarray, valid: np.ndarray, expert_count: int) -> np.ndarray:
+    """Sort key per (token, slot) pair (moe_kernels.cu:68-91; experts.py:183-191):
+    the expert, or expert_count for an invalid token, an out-of-range expert or a
+    slot repeating an earlier slot's expert."""
+
+    a = np.asarray(assignments, dtype=np.int64)
+    T, k = a.shape
+    ok = np.asarray(valid, dtype=bool)[:, None] & (a >= 0) & (a < expert_count)
+    for s in range(1, k):
+        ok[:, s] &= ~(a[:, :s] == a[:, s : s + 1]).any(axis=1)
+    return np.where(ok, a, expert_count).reshape(-1)
+
+
+def permute(context: np.ndarray, assignments: np.ndarray, valid: np.ndarray, expert_count: int,
+            pair_weights: np.ndarray | None = None):
+    """permute_topk contract (moe/__init__.py:179-228; moe_kernels.cu:390-499):
+    stable argsort of the pair keys (experts.py:189-197). Returns
+    (sorted_context, sorted_rows, sorted_experts, segment_offsets[, sorted_weights])."""
+
+    T, k = np.asarray(assignments).shape
+    keys = pair_keys(assignments, valid, expert_count)
+    order = np.argsort(keys, kind="stable")
+    sorted_keys = keys[order]
+    counts = np.bincount(keys, minlength=expert_count + 1)
+    offsets = np.zeros(expert_count + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(counts[:expert_count])
+    rows = order // k
+    ctx = np.asarray(context).reshape(T, -1)
+    sorted_ctx = ctx[rows].copy()
+    sorted_ctx[offsets[-1]:] = 0
+    result = [sorted_ctx, rows.astype(np.int64), sorted_keys.astype(np.int64), offsets]
+    if pair_weights is not None:
+        sw = np.asarray(pair_weights, dtype=np.float32).reshape(-1)[order].copy()
+        sw[offsets[-1]:] = 0.0
+        result.append(sw)
+    return tuple(result)
+
+
+def grouped_mlp(sorted_context: np.ndarray, sorted_experts: np.ndarray, offsets: np.ndarray,
+                gate_w, gate_b, value_w, value_b, out_w, out_b, *, dtype=np.float64,
+                round_hidden_bf16: bool = False) -> np.ndarray:
+    """Per-expert GLU FFN over the sorted segments (GatedFeedForward, layers.py:27-29;
+    moe_kernels.cu:147-199): y = W_o (silu(W_g x + b_g) * (W_v x + b_v)) + b_o,
+    rows past offsets[-1] zero. With round_hidden_bf16 the GLU product is rounded
+    to bfloat16 before the second product, as the bf16 MFMA path stores it."""
+
+    x = np.asarray(sorted_context, dtype=dtype)
+    out = np.zeros((x.shape[0], np.asarray(out_w).shape[1]), dtype=dtype)
+    off = np.asarray(offsets, dtype=np.int64)
+    for e in range(off.shape[0] - 1):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi <= lo:
+            continue
+        xe = x[lo:hi]
+        g = xe @ np.asarray(gate_w[e], dtype=dtype).T + np.asarray(gate_b[e], dtype=dtype)
+        v = xe @ np.asarray(value_w[e], dtype=dtype).T + np.asarray(value_b[e], dtype=dtype)
+        h = g / (1.0 + np.exp(-g)) * v
+        if round_hidden_bf16:
+            h = round_bf16(h.astype(np.float32)).astype(dtype)
+        out[lo:hi] = h @ np.asarray(out_w[e], dtype=dtype).T + np.asarray(out_b[e], dtype=dtype)
+    return out
+
+
+def combine(expert_outputs: np.ndarray, sorted_rows: np.ndarray, offsets: np.ndarray, token_count: int,
+            top_k: int, pair_weights: np.ndarray | None = None) -> np.ndarray:
+    """combine_topk (moe_kernels.cu:201-229; router.py:73): out[t] = sum over valid
+    sorted pairs of y * (1/k or w), accumulated in float32 in ascending pair order."""
+
+    y = np.asarray(expert_outputs, dtype=np.float32)
+    out = np.zeros((token_count, y.shape[1]), dtype=np.float32)
+    valid_pairs = int(np.asarray(offsets)[-1])
+    for i in range(valid_pairs):
+        t = int(sorted_rows[i])
+        contribution = y[i] * np.float32(pair_weights[i]) if pair_weights is not None else y[i] / np.float32(top_k)
+        out[t] = out[t] + contribution
+    return out
+
+
+def previous_token_ids(input_ids: np.ndarray, valid: np.ndarray, carried: np.ndarray) -> np.ndarray:
+    """network.py:742-750: the previous valid token of each position, or the carried
+    last token before the first valid one."""
+
+    B, L = input_ids.shape
+    out = np.empty_like(input_ids)
+    for b in range(B):
+        last = carried[b]
+        for t in range(L):
+            out[b, t] = last
+            if valid[b, t]:
+                last = input_ids[b, t]
+    return out
+

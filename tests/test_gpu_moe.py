@@ -1,0 +1,215 @@
+"""GPU parity of the MoE fronts: route, permute, grouped GLU-FFN, combine.
+
+* routing indices, learned top-k indices, expert counts, permutation order,
+  sorted rows/experts, segment offsets and sorted context: bit-exact against the
+  oracle (C4: T = 32768, D = 1024 bf16, E = 16, k = 2; hash and learned gates);
+* learned gate weights: bit-exact against the oracle (same exp and sum order),
+  within 1e-6 relative of torch softmax;
+* grouped MLP: fp32 path 2e-4 (tests/cuda/test_moe_cuda.py:113); bf16 MFMA path
+  against the float64 oracle with the GLU product rounded to bf16 as the kernel
+  stores it: |err| <= 2^-7 |y| + 2e-3 max|y| per element (bf16 output rounding
+  plus fp32-accumulation order), max abs / rel printed;
+* combine: bit-exact against the oracle's ascending-order fp32 sum rounded once.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from koemi_amd import moe, workloads
+
+pytestmark = pytest.mark.gpu
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "kats.json").read_text())
+
+
+def bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------------- route
+
+
+def test_route_matches_reference_test_and_kat(device):
+    tok = torch.tensor([[1, 2, 99], [7, 3, 4]], device=device)
+    prev = torch.tensor([[0, 1, 2], [6, 7, 8]], device=device)
+    valid = torch.tensor([[True, True, False], [True, False, True]], device=device)
+    got = moe.route_topk_valid(tok, prev, valid, expert_count=8, top_k=2)
+    want = oracle.route_hash(tok.cpu().numpy(), prev.cpu().numpy(), valid.cpu().numpy(), 8, 2)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    kat = GOLDEN["network_hash_route"]
+    t = torch.tensor(kat["token_ids"], device=device)
+    p = torch.tensor(kat["previous_token_ids"], device=device)
+    v = t != 256
+    a = moe.route_topk_valid(t, p, v, expert_count=kat["expert_count"], top_k=1)
+    assert a[..., 0].tolist() == kat["expert_indices"]
+    counts = moe.expert_activation_counts(a, v, expert_count=kat["expert_count"])
+    assert counts.tolist() == kat["activation_counts"]
+
+
+@pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
+def test_config4_hash_route_bit_exact(device, id_dtype):
+    c = workloads.config4()
+    got = moe.route_topk_valid(c.token_ids.to(device, id_dtype), c.previous_token_ids.to(device, id_dtype),
+                               c.valid.to(device), expert_count=16, top_k=2)
+    want = oracle.route_hash(c.token_ids.numpy(), c.previous_token_ids.numpy(), c.valid.numpy(), 16, 2)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    counts = moe.expert_activation_counts(got, c.valid.to(device), expert_count=16)
+    np.testing.assert_array_equal(counts.cpu().numpy(), oracle.expert_counts(want, c.valid.numpy(), 16))
+
+
+def test_route_rejects_duplicate_slots(device):
+    tok = torch.arange(64, device=device)
+    with pytest.raises(moe.CudaMoeValidationError, match="duplicate experts"):
+        moe.route_topk_valid(tok, tok, torch.ones(64, dtype=torch.bool, device=device), expert_count=3, top_k=2)
+
+
+def test_config4_learned_route_bit_exact(device):
+    c = workloads.config4()
+    valid = c.valid.clone()
+    valid[::97] = False
+    idx, w = moe.route_topk_learned(c.router_logits.to(device), valid.to(device), top_k=2)
+    want_idx, want_w = oracle.route_learned(c.router_logits.numpy(), valid.numpy(), 2)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_array_equal(w.cpu().numpy(), want_w)
+    ref_w, ref_idx = c.router_logits.softmax(-1).topk(2, dim=-1)
+    v = valid.numpy()
+    np.testing.assert_array_equal(idx.cpu().numpy()[v], ref_idx.numpy()[v])
+    np.testing.assert_allclose(w.cpu().numpy()[v], ref_w.numpy()[v], rtol=1e-6)
+
+
+# ----------------------------------------------------------------- permute
+
+
+def test_permute_known_answer(device):
+    kat = GOLDEN["permute_stable_pairs"]
+    ctx = torch.arange(kat["context_rows"] * kat["context_width"], dtype=torch.float32).reshape(kat["context_rows"], -1)
+    sc, rows, experts, offsets = moe.permute_topk(ctx.to(device), torch.tensor(kat["assignments"], device=device),
+                                                  torch.tensor(kat["valid"], device=device), expert_count=kat["expert_count"])
+    assert rows.tolist() == kat["sorted_rows"] and experts.tolist() == kat["sorted_experts"]
+    assert offsets.tolist() == kat["segment_offsets"]
+    z = kat["zero_rows_from"]
+    assert torch.equal(sc[:z].cpu(), ctx[torch.tensor(kat["sorted_rows"][:z])])
+    assert torch.equal(sc[z:].cpu(), torch.zeros_like(sc[z:].cpu()))
+    outputs = sc + 10.0
+    combined = moe.combine_topk(outputs, rows, offsets, token_count=3, top_k=2)
+    expected = torch.zeros_like(ctx)
+    for pair in range(kat["segment_offsets"][-1]):
+        expected[rows[pair].item()] += outputs[pair].cpu() / 2.0
+    assert torch.equal(combined.cpu(), expected)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_permute_random_with_invalid_and_repeats(device, dtype):
+    g = torch.Generator().manual_seed(71)
+    T, k, E, D = 5000, 3, 13, 72
+    a = torch.randint(-1, E + 1, (T, k), generator=g)
+    valid = torch.rand((T,), generator=g) > 0.2
+    ctx = torch.randn((T, D), generator=g).to(dtype)
+    w = torch.rand((T, k), generator=g)
+    got = moe.permute_topk(ctx.to(device), a.to(device), valid.to(device), expert_count=E, pair_weights=w.to(device), validate=False)
+    want = oracle.permute(ctx.float().numpy(), a.numpy(), valid.numpy(), E, pair_weights=w.numpy())
+    np.testing.assert_array_equal(got[0].float().cpu().numpy(), want[0])
+    for g_t, w_t in zip(got[1:], want[1:]):
+        np.testing.assert_array_equal(g_t.cpu().numpy(), w_t)
+
+
+def test_config4_permute_bit_exact(device):
+    c = workloads.config4()
+    a = oracle.route_hash(c.token_ids.numpy(), c.previous_token_ids.numpy(), c.valid.numpy(), 16, 2)
+    got = moe.permute_topk(c.context.to(device), torch.from_numpy(a).to(device), c.valid.to(device), expert_count=16)
+    want = oracle.permute(c.context.view(torch.int16).numpy(), a, c.valid.numpy(), 16)
+    assert torch.equal(got[0].view(torch.int16).cpu(), torch.from_numpy(want[0]))
+    for g_t, w_t in zip(got[1:], want[1:]):
+        np.testing.assert_array_equal(g_t.cpu().numpy(), w_t)
+
+
+# ------------------------------------------------------------- grouped MLP
+
+
+def test_grouped_mlp_fp32_matches_reference_rows(device):
+    torch.manual_seed(3)
+    E, D, H, P = 2, 4, 3, 3
+    x = torch.randn(P, D, device=device)
+    experts = torch.tensor([0, 0, 1], device=device)
+    offsets = torch.tensor([0, 2, 3], device=device)
+    gw, gb = torch.randn(E, H, D, device=device), torch.randn(E, H, device=device)
+    vw, vb = torch.randn_like(gw), torch.randn_like(gb)
+    ow, ob = torch.randn(E, D, H, device=device), torch.randn(E, D, device=device)
+    got = moe.grouped_expert_mlp_inference(x, experts, offsets, gw, gb, vw, vb, ow, ob)
+    rows = []
+    for row, e in enumerate(experts.tolist()):
+        gate = F.linear(x[row], gw[e], gb[e])
+        value = F.linear(x[row], vw[e], vb[e])
+        rows.append(F.linear(F.silu(gate) * value, ow[e], ob[e]))
+    torch.testing.assert_close(got, torch.stack(rows), rtol=2e-4, atol=2e-4)
+
+
+def check_bf16_mlp(got: torch.Tensor, want: np.ndarray, name: str):
+    g = got.float().cpu().numpy()
+    err = np.abs(g - want)
+    scale = np.abs(want).max()
+    print(f"{name}: max_abs={err.max():.3e} max|y|={scale:.3e} max_rel_to_scale={err.max() / scale:.3e}", flush=True)
+    assert np.all(err <= 2.0**-7 * np.abs(want) + 2e-3 * scale)
+
+
+@pytest.mark.parametrize("sizes", [(0, 5, 300, 0, 57), (128, 128, 1, 255, 3), (1000, 0, 0, 17, 2)])
+def test_grouped_mlp_bf16_mfma_ragged_segments(device, sizes):
+    g = torch.Generator().manual_seed(sum(sizes))
+    E, D, H = len(sizes), 256, 384
+    offsets = np.concatenate([[0], np.cumsum(sizes)])
+    P = int(offsets[-1]) + 7  # trailing rows past the valid pairs
+    x = torch.randn((P, D), generator=g).to(torch.bfloat16)
+    experts = torch.full((P,), E, dtype=torch.int64)
+    for e in range(E):
+        experts[offsets[e]:offsets[e + 1]] = e
+    ws = [(0.05 * torch.randn(s, generator=g)).to(torch.bfloat16) for s in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    got = moe.grouped_expert_mlp_inference(x.to(device), experts.to(device), torch.from_numpy(offsets).to(device),
+                                           *(w.to(device) for w in ws))
+    want = oracle.grouped_mlp(x.float().numpy(), experts.numpy(), offsets, *(w.float().numpy() for w in ws),
+                              round_hidden_bf16=True)
+    check_bf16_mlp(got, want, f"grouped MLP bf16 sizes={sizes}")
+    assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
+
+
+def run_config4_pipeline(device, c, learned: bool):
+    ctx = c.context.to(device)
+    valid = c.valid.to(device)
+    if learned:
+        a, w = moe.route_topk_learned(c.router_logits.to(device), valid, top_k=2)
+        sc, rows, experts, offsets, sw = moe.permute_topk(ctx, a, valid, expert_count=16, pair_weights=w)
+    else:
+        a = moe.route_topk_valid(c.token_ids.to(device), c.previous_token_ids.to(device), valid, expert_count=16, top_k=2)
+        sc, rows, experts, offsets = moe.permute_topk(ctx, a, valid, expert_count=16)
+        sw = None
+    y = moe.grouped_expert_mlp_inference(sc, experts, offsets, c.gate_weights.to(device), c.gate_biases.to(device),
+                                         c.value_weights.to(device), c.value_biases.to(device),
+                                         c.output_weights.to(device), c.output_biases.to(device))
+    out = moe.combine_topk(y, rows, offsets, token_count=ctx.shape[0], top_k=2, pair_weights=sw)
+    return sc, rows, experts, offsets, sw, y, out
+
+
+@pytest.mark.parametrize("learned", [False, True])
+def test_config4_pipeline(device, learned):
+    c = workloads.config4()
+    sc, rows, experts, offsets, sw, y, out = run_config4_pipeline(device, c, learned)
+    off = offsets.cpu().numpy()
+    # sampled rows of the expert outputs against the oracle (fp32 numpy matmul)
+    sample = np.concatenate([np.arange(off[e], min(off[e] + 96, off[e + 1])) for e in range(16)])
+    sample = np.concatenate([sample, np.arange(max(0, off[-1] - 64), off[-1])])
+    x = sc.float().cpu().numpy()[sample]
+    sub_experts = experts.cpu().numpy()[sample]
+    sub_offsets = np.concatenate([[0], np.cumsum(np.bincount(sub_experts, minlength=16)[:16])])
+    ws = [t.float().numpy() for t in (c.gate_weights, c.gate_biases, c.value_weights, c.value_biases, c.output_weights, c.output_biases)]
+    want = oracle.grouped_mlp(x, sub_experts, sub_offsets, *ws, dtype=np.float32, round_hidden_bf16=True)
+    check_bf16_mlp(y[torch.from_numpy(sample).to(device)], want, f"C4 grouped MLP ({'learned' if learned else 'hash'})")
+    # combine bit-exact against the oracle on the kernel's own expert outputs
+    want_out = oracle.combine(y.float().cpu().numpy(), rows.cpu().numpy(), off, c.context.shape[0], 2,
+                              None if sw is None else sw.cpu().numpy())
+    np.testing.assert_array_equal(out.cpu().view(torch.int16).numpy(), oracle.f32_to_bf16(want_out).view(np.int16))

@@ -1,0 +1,159 @@
+"""GPU parity of surprise scoring and salience admission.
+
+* causal_surprise (prior-state front): forward 3e-4, backward 2e-3
+  (tests/cuda/test_think_cuda.py:89, 118-120), invalid rows exactly 0,
+  causality.
+* surprise_from_logits: bit-identical to the C oracle (same exp/log routines
+  and summation order), and within a few fp32 ulp of the float64 formula.
+* admission: tau and the mask bit-identical to the oracle (torch.quantile
+  semantics); any disagreement with a mask computed from torch's own
+  cross_entropy scores is confined to tokens within 4 ulp of tau.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from koemi_amd import think, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def reference_causal_surprise(prior, weight, bias, targets, valid):
+    logits = torch.matmul(prior.float(), weight.float().transpose(0, 1)) + bias.float()
+    nll = torch.logsumexp(logits, dim=-1) - logits.gather(-1, targets.unsqueeze(-1)).squeeze(-1)
+    s = 1.0 - torch.exp(-nll / math.log(weight.shape[0]))
+    return torch.where(valid, s, torch.zeros_like(s)).to(prior.dtype)
+
+
+def build_inputs(device, requires_grad=False):
+    torch.manual_seed(17)
+    prior = torch.randn(2, 7, 8)
+    weight = torch.randn(19, 8)
+    bias = torch.randn(19)
+    targets = torch.randint(0, 19, (2, 7))
+    valid = torch.ones(2, 7, dtype=torch.bool)
+    valid[0, -1] = False
+    out = [prior, weight, bias]
+    out = [t.to(device).requires_grad_(requires_grad) for t in out]
+    return (*out, targets.to(device), valid.to(device))
+
+
+def test_causal_surprise_forward(device):
+    inputs = build_inputs(device)
+    got = think.causal_surprise(*inputs)
+    want = reference_causal_surprise(*inputs)
+    torch.testing.assert_close(got, want, rtol=3e-4, atol=3e-4)
+    assert got[0, -1].item() == 0.0
+
+
+def test_causal_surprise_backward(device):
+    p, w, b, t, v = build_inputs(device, requires_grad=True)
+    out = think.causal_surprise(p, w, b, t, v)
+    grads = torch.autograd.grad(out.square().sum(), (p, w, b))
+    rp, rw, rb = (x.detach().cpu().double().requires_grad_() for x in (p, w, b))
+    ref = reference_causal_surprise(rp, rw, rb, t.cpu(), v.cpu()).double()
+    ref_grads = torch.autograd.grad(ref.square().sum(), (rp, rw, rb))
+    for got, want in zip(grads, ref_grads):
+        torch.testing.assert_close(got.cpu(), want.float(), rtol=2e-3, atol=2e-3)
+    assert torch.equal(grads[0][0, -1].cpu(), torch.zeros(8))
+
+
+def test_causal_surprise_is_causal(device):
+    inputs = build_inputs(device)
+    base = think.causal_surprise(*inputs)
+    changed_prior = inputs[0].clone()
+    changed_prior[:, 4:] = torch.randn_like(changed_prior[:, 4:]) * 100.0
+    changed_targets = inputs[3].clone()
+    changed_targets[:, 4:] = (changed_targets[:, 4:] + 7) % 19
+    changed = think.causal_surprise(changed_prior, inputs[1], inputs[2], changed_targets, inputs[4])
+    assert torch.equal(changed[:, :4], base[:, :4])
+
+
+def test_benchmark_reports_synchronized_latency(device):
+    m = think.benchmark_causal_surprise(*build_inputs(device), warmup_iterations=2, measured_iterations=5)
+    assert m.position_count == 14 and m.measured_iterations == 5 and m.latency_milliseconds > 0
+
+
+@pytest.mark.parametrize("vocab", [2, 19, 256, 257, 1000, 1030])
+def test_surprise_rows_bit_identical_to_oracle(device, vocab):
+    rng = np.random.default_rng(vocab)
+    logits = rng.normal(0, 2, (333, vocab)).astype(np.float32)
+    bias = rng.normal(0, 1, vocab).astype(np.float32)
+    targets = rng.integers(0, vocab, 333)
+    valid = rng.random(333) > 0.1
+    got = think.surprise_from_logits(
+        torch.from_numpy(logits).to(device), torch.from_numpy(targets).to(device), torch.from_numpy(valid).to(device),
+        content_bias=torch.from_numpy(bias).to(device),
+    ).cpu().numpy()
+    want = oracle.surprise_rows(logits, targets, valid, bias)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_config2_surprise_and_quantile_admission_bit_exact(device):
+    c = workloads.config2()
+    s = think.surprise_from_logits(c.logits.to(device), c.targets.to(device), c.valid.to(device))
+    mask, tau = think.salience_admission(s, c.valid.to(device), quantile=c.quantile)
+    s_cpu = s.cpu().numpy()
+    want_s = oracle.surprise_rows(c.logits.numpy(), c.targets.numpy(), c.valid.numpy())
+    np.testing.assert_array_equal(s_cpu, want_s)
+    want_mask, want_tau = oracle.admission(want_s, c.valid.numpy(), q=c.quantile)
+    assert float(tau) == want_tau
+    assert float(tau) == float(torch.quantile(torch.from_numpy(want_s), c.quantile))
+    np.testing.assert_array_equal(mask.cpu().numpy(), want_mask)
+    admitted = int(mask.sum())
+    # float64 accuracy of the scores
+    f64 = oracle.surprise_rows_f64(c.logits.numpy(), c.targets.numpy(), c.valid.numpy())
+    max_abs = float(np.abs(s_cpu - f64).max())
+    # torch's own path (network.py:681-687) and its mask
+    nll = F.cross_entropy(c.logits, c.targets, reduction="none")
+    torch_s = (1.0 - torch.exp(-(nll / math.log(256)))).numpy()
+    torch_tau = float(torch.quantile(torch.from_numpy(torch_s), c.quantile))
+    torch_mask = torch_s > torch_tau
+    differ = np.nonzero(torch_mask != want_mask)[0]
+    near = np.abs(torch_s[differ] - torch_tau) <= 4 * np.spacing(np.float32(torch_tau))
+    print(f"C2 admission: admitted={admitted} tau={float(tau):.9g} max_abs_vs_f64={max_abs:.3e} "
+          f"mask_diff_vs_torch_path={differ.size}", flush=True)
+    assert max_abs <= 4 * np.spacing(np.float32(1.0))
+    assert near.all()
+    assert admitted == int(np.sum(want_s > want_tau))
+
+
+@pytest.mark.parametrize("case", ["single", "pair", "ties", "constant", "negative", "wide", "nan", "large"])
+@pytest.mark.parametrize("q", [0.0, 0.25, 0.9, 1.0])
+def test_quantile_admission_edge_cases(device, case, q):
+    rng = np.random.default_rng(sum(map(ord, case)))
+    scores = {
+        "single": np.array([0.4]),
+        "pair": np.array([0.9, 0.1]),
+        "ties": np.repeat([0.2, 0.5, 0.7], 333),
+        "constant": np.full(1000, 0.625),
+        "negative": rng.normal(0, 10, 5000),
+        "wide": np.concatenate([rng.uniform(0, 1, 4000), [1e-30, 3e38, -3e38, 0.0, -0.0]]),
+        "nan": np.array([0.1, np.nan, 0.5, 0.7]),
+        "large": rng.uniform(0.5, 0.9, 300_000),
+    }[case].astype(np.float32)
+    valid = rng.random(scores.size) > 0.2
+    mask, tau = think.salience_admission(torch.from_numpy(scores).to(device), torch.from_numpy(valid).to(device), quantile=q)
+    want_mask, want_tau = oracle.admission(scores, valid, q=q)
+    if math.isnan(want_tau):
+        assert math.isnan(float(tau))
+    else:
+        assert float(tau) == want_tau
+    np.testing.assert_array_equal(mask.cpu().numpy(), want_mask)
+
+
+def test_fixed_threshold_admission_is_strict(device):
+    s = torch.tensor([0.7, 0.75, 0.8, 0.9], device=device)
+    valid = torch.tensor([True, True, True, False], device=device)
+    mask, tau = think.salience_admission(s, valid, threshold=0.75)
+    assert mask.tolist() == [False, False, True, False] and float(tau) == 0.75
+    for dtype in (torch.bfloat16, torch.float16):
+        m, _ = think.salience_admission(s.to(dtype), valid, threshold=0.75)
+        assert m.tolist() == [False, False, True, False]

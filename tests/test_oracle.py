@@ -1,0 +1,390 @@
+"""Pins of the CPU oracle (CPU only).
+
+The oracle is only trusted as far as these checks fix it. For each oracle
+function, the checks below are chosen so that a plausible slip (dropped term,
+wrong sign, swapped operand, wrong rounding order) fails at least one:
+
+* exp/log (the fixed routines behind the bit-exact surprise and router):
+  <= 2 ulp from float64 math over a dense sweep; exact special values.
+* scan_sequential: brute-force Python recurrence (tiny shapes); closed forms
+  a=0 -> h=b, a=1,b=0 -> h=h0, constant (a,b) -> geometric series; fp32 path
+  bit-identical to a torch fp32 loop (test_dense_cuda.py:21-33); finiteness at
+  the bounded retention range (test_scan.py:40-45); Hillis-Steele agrees
+  (test_scan.py:20-30 sizes).
+* rmsnorm_silu: torch float64 closed form (test_core_cuda.py:70-71); constant
+  rows; fp32 port within the reference tolerance 2e-5.
+* surprise_rows: float64 logsumexp formula and torch cross_entropy
+  (network.py:677-688) within a few ulp; uniform logits -> 1 - 1/e; invalid
+  -> exactly 0; bias[65] = 12 monotonic known case (test_network.py:61-70).
+* quantile: torch.quantile (linear) on many sizes / q; NaN propagation.
+* hash route: the network KAT (test_network.py:95-101) and the dispatch
+  properties of test_dispatch.py:50-108; uint32-vs-int64 closed form (E power
+  of two agrees, E = 6 does not).
+* learned route: torch softmax + topk indices, weights to 1e-6; exact ties.
+* permute: the stable-pairs KAT and torch.argsort(stable=True) on random data.
+* grouped_mlp / combine: torch per-row loops of test_moe_cuda.py:79-113.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "kats.json").read_text())
+
+
+def ulp_error(got: np.ndarray, want64: np.ndarray) -> np.ndarray:
+    want32 = want64.astype(np.float32)
+    spacing = np.spacing(np.abs(want32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - want64) / spacing
+
+
+# ----------------------------------------------------------------- exp / log
+
+
+def test_det_exp_within_two_ulp_over_the_used_range():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.uniform(-86.0, 88.0, 400_000), rng.uniform(-1, 1, 100_000), np.arange(-86, 89)]).astype(np.float32)
+    got = oracle.det_expf_array(x)
+    assert ulp_error(got, np.exp(x.astype(np.float64))).max() <= 2.0
+
+
+def test_det_exp_special_values():
+    assert oracle.det_expf(0.0) == 1.0
+    assert oracle.det_expf(-100.0) == 0.0
+    assert math.isinf(oracle.det_expf(100.0))
+    assert math.isnan(oracle.det_expf(float("nan")))
+
+
+def test_det_log_within_two_ulp():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([np.exp(rng.uniform(-80, 80, 400_000)), rng.uniform(0.5, 2.0, 100_000), [1.0, 2.0, 256.0]]).astype(np.float32)
+    got = oracle.det_logf_array(x)
+    want = np.log(x.astype(np.float64))
+    err = np.abs(got - want)
+    # relative ulp except near log(1) = 0 where the absolute error is what matters
+    ok = (ulp_error(got, want) <= 2.0) | (err <= 2 * np.spacing(np.float32(1.0)) * np.abs(x.astype(np.float64) - 1.0) + 1e-12)
+    assert ok.all()
+    assert oracle.det_logf(1.0) == 0.0
+    assert math.isinf(oracle.det_logf(0.0)) and oracle.det_logf(0.0) < 0
+
+
+# ---------------------------------------------------------------------- scan
+
+
+def brute_force_scan(a, b, h0):
+    B, L = b.shape[:2]
+    out = np.empty_like(b)
+    for bi in range(B):
+        state = h0[bi].copy()
+        for t in range(L):
+            state = a[bi, t] * state + b[bi, t]
+            out[bi, t] = state
+    return out
+
+
+@pytest.mark.parametrize("shape", [(3, 1, 5), (3, 2, 5), (4, 17, 8), (2, 96, 48)])
+def test_scan_matches_brute_force_float64(shape):
+    rng = np.random.default_rng(2)
+    a = rng.uniform(0.004, 0.994, shape)
+    b = rng.standard_normal(shape)
+    h0 = rng.standard_normal((shape[0], shape[2]))
+    np.testing.assert_array_equal(oracle.scan_sequential(a, b, h0), brute_force_scan(a, b, h0))
+
+
+def test_scan_broadcast_retention_matches_expanded():
+    rng = np.random.default_rng(3)
+    a = rng.uniform(0.05, 0.95, (2, 29, 1, 1))
+    b = rng.standard_normal((2, 29, 4, 8))
+    h0 = rng.standard_normal((2, 4, 8))
+    expanded = oracle.scan_sequential(np.broadcast_to(a, b.shape).copy(), b, h0)
+    np.testing.assert_array_equal(oracle.scan_sequential(a, b, h0).reshape(b.shape), expanded.reshape(b.shape))
+
+
+def test_scan_closed_forms():
+    rng = np.random.default_rng(4)
+    b = rng.standard_normal((2, 50, 3))
+    h0 = rng.standard_normal((2, 3))
+    np.testing.assert_array_equal(oracle.scan_sequential(np.zeros_like(b), b, h0), b)
+    np.testing.assert_array_equal(oracle.scan_sequential(np.ones_like(b), np.zeros_like(b), h0), np.broadcast_to(h0[:, None], b.shape))
+    a_c, b_c = 0.9, 0.3
+    h = oracle.scan_sequential(np.full_like(b, a_c), np.full_like(b, b_c), h0)
+    t = np.arange(1, 51)[None, :, None]
+    closed = a_c**t * h0[:, None] + b_c * (1 - a_c**t) / (1 - a_c)
+    np.testing.assert_allclose(h, closed, rtol=1e-12, atol=1e-12)
+
+
+def test_scan_fp32_is_the_torch_fp32_recurrence_bit_for_bit():
+    torch.manual_seed(101)
+    a = torch.rand((2, 37, 64)) * 0.9 + 0.05
+    b = torch.randn((2, 37, 64))
+    h0 = torch.randn((2, 64))
+    state, states = h0, []
+    for t in range(b.shape[1]):  # test_dense_cuda.py:21-33
+        state = a[:, t] * state + b[:, t]
+        states.append(state)
+    expected = torch.stack(states, dim=1).numpy()
+    np.testing.assert_array_equal(oracle.scan_sequential(a.numpy(), b.numpy(), h0.numpy()), expected)
+
+
+def test_scan_stays_finite_at_the_bounded_retention_range():
+    b = np.random.default_rng(5).standard_normal((1, 2048, 8)).astype(np.float32)
+    for value in (2.0**-8, 1.0 - 2.0**-8):
+        assert np.isfinite(oracle.scan_sequential(np.full_like(b, value), b, np.zeros((1, 8), np.float32))).all()
+
+
+@pytest.mark.parametrize("shape", [(3, 1, 5), (4, 17, 8), (2, 96, 48)])
+def test_hillis_steele_window_scan_agrees(shape):
+    rng = np.random.default_rng(6)
+    a = (rng.uniform(0, 1, shape) * 0.99 + 0.004).astype(np.float32)
+    b = rng.standard_normal(shape).astype(np.float32)
+    h0 = rng.standard_normal((shape[0], shape[2])).astype(np.float32)
+    np.testing.assert_allclose(oracle.scan_hillis_steele(a, b, h0), oracle.scan_sequential(a, b, h0), atol=1e-5)
+
+
+# ------------------------------------------------------------- rmsnorm-silu
+
+
+def test_rmsnorm_silu_matches_the_torch_closed_form():
+    torch.manual_seed(11)
+    x = torch.randn((5, 257), dtype=torch.float64)
+    w = torch.randn((257,), dtype=torch.float64)
+    expected = F.silu(x * torch.rsqrt(x.square().mean(dim=-1, keepdim=True) + 1e-6) * w)
+    y, inv = oracle.rmsnorm_silu_f64(x.numpy(), w.numpy())
+    np.testing.assert_allclose(y, expected.numpy(), rtol=1e-12, atol=1e-14)
+    np.testing.assert_allclose(inv, torch.rsqrt(x.square().mean(dim=-1) + 1e-6).numpy(), rtol=1e-14)
+
+
+def test_rmsnorm_silu_constant_rows():
+    c, eps = -0.37, 1e-6
+    x = np.full((2, 16), c)
+    w = np.linspace(0.5, 1.5, 16)
+    y, _ = oracle.rmsnorm_silu_f64(x, w, eps)
+    v = np.sign(c) * w * abs(c) / math.sqrt(c * c + eps)
+    np.testing.assert_allclose(y[0], v / (1 + np.exp(-v)), rtol=1e-13)
+
+
+def test_rmsnorm_silu_fp32_port_within_reference_tolerance():
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((64, 512)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(512)).astype(np.float32)
+    y32, inv32 = oracle.rmsnorm_silu_f32(x, w)
+    y64, inv64 = oracle.rmsnorm_silu_f64(x, w)
+    np.testing.assert_allclose(y32, y64, atol=2e-5, rtol=2e-5)
+    np.testing.assert_allclose(inv32, inv64, rtol=2e-6)
+
+
+def test_bf16_round_trip_and_rounding():
+    values = np.array([1.0, 1.00390625, 1.005859375, -2.5, 3.0e38, 1e-40], dtype=np.float32)
+    torch_bits = torch.from_numpy(values).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(oracle.f32_to_bf16(values), torch_bits)
+
+
+# ------------------------------------------------------------------ surprise
+
+
+def test_surprise_matches_float64_and_torch_cross_entropy():
+    g = torch.Generator().manual_seed(21)
+    logits = 2.0 * torch.randn((2048, 256), generator=g)
+    targets = torch.randint(0, 256, (2048,), generator=g)
+    valid = torch.rand((2048,), generator=g) > 0.1
+    got = oracle.surprise_rows(logits.numpy(), targets.numpy(), valid.numpy())
+    want64 = oracle.surprise_rows_f64(logits.numpy(), targets.numpy(), valid.numpy())
+    assert np.abs(got - want64).max() <= 4 * np.spacing(np.float32(1.0))
+    # reference model path: cross_entropy / log(V), 1 - exp(-.), zero where invalid
+    nll = F.cross_entropy(logits, targets, reduction="none")
+    ref = torch.where(valid, 1.0 - torch.exp(-(nll / math.log(256))), torch.zeros(()))
+    assert np.abs(got - ref.numpy()).max() <= 3e-6
+    assert (got[~valid.numpy()] == 0).all()
+
+
+@pytest.mark.parametrize("vocab", [2, 19, 257, 1000, 1030])
+def test_surprise_ragged_vocabularies(vocab):
+    rng = np.random.default_rng(vocab)
+    logits = rng.normal(0, 3, (64, vocab)).astype(np.float32)
+    bias = rng.normal(0, 1, vocab).astype(np.float32)
+    targets = rng.integers(0, vocab, 64)
+    valid = np.ones(64, dtype=bool)
+    got = oracle.surprise_rows(logits, targets, valid, bias)
+    want = oracle.surprise_rows_f64(logits.astype(np.float64) + bias.astype(np.float32).astype(np.float64), targets, valid)
+    assert np.abs(got - want).max() <= 8 * np.spacing(np.float32(1.0))
+
+
+def test_surprise_uniform_logits_is_one_minus_inverse_e():
+    s = oracle.surprise_rows(np.zeros((4, 256), np.float32), np.array([0, 7, 100, 255]), np.ones(4, bool))
+    assert np.abs(s - (1 - math.exp(-1))).max() <= 2 * np.spacing(np.float32(0.63))
+
+
+def test_surprise_bias_known_case():
+    kat = GOLDEN["surprise_bias_monotonic"]
+    bias = np.zeros(kat["vocab"], np.float32)
+    bias[kat["bias_index"]] = kat["bias_value"]
+    s = oracle.surprise_rows(np.zeros((2, kat["vocab"]), np.float32), np.array(kat["tokens"]), np.ones(2, bool), bias)
+    assert s[0] < s[1]
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 100, 1001, 32768])
+@pytest.mark.parametrize("q", [0.0, 0.1, 0.5, 0.9, 0.999, 1.0])
+def test_quantile_matches_torch(n, q):
+    values = torch.rand((n,), generator=torch.Generator().manual_seed(n)) * 0.3 + 0.55
+    got = oracle.quantile(values.numpy(), q)
+    want = float(torch.quantile(values, q))
+    assert got == want or abs(got - want) <= np.spacing(np.float32(want))
+
+
+def test_quantile_with_ties_and_nan():
+    v = np.array([0.5, 0.5, 0.5, 0.7, 0.7], np.float32)
+    assert oracle.quantile(v, 0.5) == float(torch.quantile(torch.from_numpy(v), 0.5))
+    assert math.isnan(oracle.quantile(np.array([0.1, float("nan"), 0.3], np.float32), 0.9))
+
+
+def test_admission_is_strictly_above_the_threshold():
+    s = np.array([0.7, 0.75, 0.8, 0.9], np.float32)
+    mask, _ = oracle.admission(s, np.array([True, True, True, False]), threshold=0.75)
+    assert mask.tolist() == [False, False, True, False]
+
+
+# ------------------------------------------------------------------------ MoE
+
+
+def test_network_hash_route_known_answer():
+    kat = GOLDEN["network_hash_route"]
+    tok, prev = np.array(kat["token_ids"]), np.array(kat["previous_token_ids"])
+    valid = tok != oracle.PAD_TOKEN_ID
+    a = oracle.route_hash(tok, prev, valid, kat["expert_count"], kat["top_k"])
+    assert a[..., 0].tolist() == kat["expert_indices"]
+    assert oracle.expert_counts(a, valid, kat["expert_count"]).tolist() == kat["activation_counts"]
+
+
+def test_hash_route_properties_of_the_reference_dispatch_tests():
+    six = oracle.route_hash(np.array([[97, 98, 99]]), np.array([[32, 97, 98]]), np.ones((1, 3), bool), 128, 6)
+    assert all(len(set(row)) == 6 for row in six[0].tolist())
+    tokens = np.arange(1, 256)
+    reachable = set(oracle.route_hash(tokens, tokens - 1, np.ones(255, bool), 64, 1)[:, 0].tolist())
+    assert len(reachable) >= 48
+    mixed = oracle.content_hash(tokens, tokens - 1)
+    affine = tokens * 1_000_003 + (tokens - 1) * 97_409
+    for e in (4, 64):
+        assert len(set((mixed % e).tolist())) > len(set((affine % e).tolist()))
+    all_tokens = np.arange(0, 257)
+    assert (oracle.content_hash(all_tokens, np.full_like(all_tokens, 256)) >= 0).all()
+    padded = oracle.route_hash(np.array([65, 256, 66]), np.array([32, 65, 256]), np.array([True, False, True]), 8, 1)
+    assert padded[1, 0] == -1 and padded[0, 0] >= 0 and padded[2, 0] >= 0
+
+
+def test_hash_route_against_torch_int64_expression():
+    g = torch.Generator().manual_seed(31)
+    tok = torch.randint(0, 257, (4096,), generator=g)
+    prev = torch.randint(0, 257, (4096,), generator=g)
+    value = (tok * 1_000_003 + prev * 97_409) & 0xFFFFFFFF  # experts.py:30-38, in torch int64
+    value = value ^ (value >> 16)
+    value = (value * 0x45D9F3B) & 0xFFFFFFFF
+    value = value ^ (value >> 16)
+    value = (value * 0x45D9F3B) & 0xFFFFFFFF
+    value = value ^ (value >> 16)
+    expected = (value.unsqueeze(-1) + torch.arange(3) * 0x9E3779B9).remainder(16)
+    got = oracle.route_hash(tok.numpy(), prev.numpy(), np.ones(4096, bool), 16, 3)
+    np.testing.assert_array_equal(got, expected.numpy())
+
+
+def test_uint32_slot_offsets_agree_only_for_power_of_two_expert_counts():
+    tokens = np.arange(40_000) % 257
+    prev = (np.arange(40_000) * 7) % 257
+    h = oracle.content_hash(tokens, prev)
+    for experts, expect_equal in ((16, True), (128, True), (6, False)):
+        wide = (h + 0x9E3779B9) % experts
+        wrapped = ((h + 0x9E3779B9) & 0xFFFFFFFF) % experts
+        assert bool((wide == wrapped).all()) == expect_equal
+
+
+def test_learned_route_matches_torch_softmax_topk():
+    g = torch.Generator().manual_seed(41)
+    logits = torch.randn((4096, 16), generator=g)
+    valid = torch.rand((4096,), generator=g) > 0.05
+    probs = logits.softmax(dim=-1)
+    w_ref, idx_ref = probs.topk(2, dim=-1)
+    idx, w = oracle.route_learned(logits.numpy(), valid.numpy(), 2)
+    v = valid.numpy()
+    np.testing.assert_array_equal(idx[v], idx_ref.numpy()[v])
+    np.testing.assert_allclose(w[v], w_ref.numpy()[v], rtol=1e-6, atol=0)
+    assert (idx[~v] == -1).all() and (w[~v] == 0).all()
+    assert oracle.expert_counts(idx, v, 16).sum() == v.sum() * 2
+
+
+def test_learned_route_ties_go_to_the_lower_index():
+    logits = np.zeros((1, 8), np.float32)
+    logits[0, [2, 5, 6]] = 1.0
+    idx, w = oracle.route_learned(logits, np.ones(1, bool), 3)
+    assert idx[0].tolist() == [2, 5, 6] and w[0, 0] == w[0, 1] == w[0, 2]
+
+
+def test_permute_known_answer():
+    kat = GOLDEN["permute_stable_pairs"]
+    ctx = np.arange(kat["context_rows"] * kat["context_width"], dtype=np.float32).reshape(kat["context_rows"], -1)
+    sc, rows, experts, offsets = oracle.permute(ctx, np.array(kat["assignments"]), np.array(kat["valid"]), kat["expert_count"])
+    assert rows.tolist() == kat["sorted_rows"]
+    assert experts.tolist() == kat["sorted_experts"]
+    assert offsets.tolist() == kat["segment_offsets"]
+    k = len(kat["assignments"][0])
+    np.testing.assert_array_equal(sc[: kat["zero_rows_from"]], ctx[np.array(kat["sorted_pairs"][: kat["zero_rows_from"]]) // k])
+    assert (sc[kat["zero_rows_from"]:] == 0).all()
+
+
+def test_permute_matches_torch_stable_argsort_with_invalid_and_repeated_slots():
+    g = torch.Generator().manual_seed(51)
+    T, k, E = 3000, 3, 11
+    assignments = torch.randint(-1, E + 1, (T, k), generator=g)
+    valid = torch.rand((T,), generator=g) > 0.2
+    ctx = torch.randn((T, 5), generator=g)
+    # experts.py:181-196 in torch
+    pair_rows = torch.arange(T).repeat_interleave(k)
+    pair_experts = assignments.reshape(-1)
+    slots = torch.arange(k)
+    repeated = (assignments.unsqueeze(-1) == assignments.unsqueeze(-2)) & (slots.unsqueeze(0) < slots.unsqueeze(1))
+    first = ~repeated.any(dim=-1)
+    pair_valid = pair_experts.ge(0) & pair_experts.lt(E) & valid.repeat_interleave(k) & first.reshape(-1)
+    keys = torch.where(pair_valid, pair_experts, torch.full((), E))
+    order = torch.argsort(keys, stable=True)
+    sc, rows, experts, offsets = oracle.permute(ctx.numpy(), assignments.numpy(), valid.numpy(), E)
+    np.testing.assert_array_equal(rows, pair_rows[order].numpy())
+    np.testing.assert_array_equal(experts, keys[order].numpy())
+    counts = torch.bincount(keys, minlength=E + 1)
+    np.testing.assert_array_equal(offsets[1:], torch.cumsum(counts[:E], 0).numpy())
+    n_valid = int(offsets[-1])
+    np.testing.assert_array_equal(sc[:n_valid], ctx[pair_rows[order][:n_valid]].numpy())
+    assert (sc[n_valid:] == 0).all()
+
+
+def test_grouped_mlp_and_combine_match_the_reference_loops():
+    g = torch.Generator().manual_seed(61)
+    E, D, H, P = 3, 8, 6, 10
+    x = torch.randn((P, D), generator=g, dtype=torch.float64)
+    experts = torch.tensor([0, 0, 0, 1, 2, 2, 2, 2, 3, 3])
+    offsets = torch.tensor([0, 3, 4, 8])
+    gw, vw = torch.randn((E, H, D), generator=g, dtype=torch.float64), torch.randn((E, H, D), generator=g, dtype=torch.float64)
+    gb, vb = torch.randn((E, H), generator=g, dtype=torch.float64), torch.randn((E, H), generator=g, dtype=torch.float64)
+    ow, ob = torch.randn((E, D, H), generator=g, dtype=torch.float64), torch.randn((E, D), generator=g, dtype=torch.float64)
+    got = oracle.grouped_mlp(x.numpy(), experts.numpy(), offsets.numpy(), gw.numpy(), gb.numpy(), vw.numpy(), vb.numpy(), ow.numpy(), ob.numpy())
+    rows = []
+    for row, e in enumerate(experts[:8].tolist()):  # test_moe_cuda.py:106-112
+        gate = F.linear(x[row], gw[e], gb[e])
+        value = F.linear(x[row], vw[e], vb[e])
+        rows.append(F.linear(F.silu(gate) * value, ow[e], ob[e]))
+    np.testing.assert_allclose(got[:8], torch.stack(rows).numpy(), rtol=1e-12, atol=1e-12)
+    assert (got[8:] == 0).all()
+    # combine: test_moe_cuda.py:79-82
+    y = torch.randn((P, D), generator=g)
+    sorted_rows = torch.tensor([0, 1, 2, 0, 1, 3, 2, 3, 4, 4])
+    combined = oracle.combine(y.numpy(), sorted_rows.numpy(), offsets.numpy(), 5, 2)
+    expected = torch.zeros((5, D))
+    for pair in range(8):
+        expected[sorted_rows[pair]] += y[pair] / 2.0
+    np.testing.assert_array_equal(combined, expected.numpy())
