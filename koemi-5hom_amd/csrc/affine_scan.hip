@@ -22,19 +22,36 @@
 namespace koemi {
 namespace {
 
-constexpr int kScanSteps = 8;     // S: serial steps per wave per chunk
-constexpr int kScanSegments = 8;  // NSEG: waves per workgroup
+#ifndef KOEMI_SCAN_STEPS
+#define KOEMI_SCAN_STEPS 8
+#endif
+#ifndef KOEMI_SCAN_SEGMENTS
+#define KOEMI_SCAN_SEGMENTS 8
+#endif
+constexpr int kScanSteps = KOEMI_SCAN_STEPS;        // S: serial steps per wave per chunk
+constexpr int kScanSegments = KOEMI_SCAN_SEGMENTS;  // NSEG: waves per workgroup
 
+// Loads are unconditional (the position is clamped into the sequence) and the
+// identity element is selected afterwards: loads under divergent branches would
+// force the compiler to wait for every outstanding load, including the prefetch
+// of the next chunk.
 template <typename T, typename A, int S, bool BCAST>
 __device__ __forceinline__ void scan_load(const T* __restrict__ a_col, const T* __restrict__ b_col,
                                           int64_t a_stride, int64_t F, int64_t L, int64_t t_first,
                                           bool col_ok, A (&ra)[S], A (&rb)[S]) {
+    T va[S], vb[S];
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int64_t t = t_first + i;
-        const bool ok = col_ok && t < L;
-        ra[i] = ok ? static_cast<A>(a_col[t * a_stride]) : A(1);
-        rb[i] = ok ? static_cast<A>(b_col[t * F]) : A(0);
+        const int64_t tc = t < L ? t : L - 1;
+        va[i] = a_col[tc * a_stride];
+        vb[i] = b_col[tc * F];
+    }
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const bool ok = col_ok && t_first + i < L;
+        ra[i] = ok ? static_cast<A>(va[i]) : A(1);
+        rb[i] = ok ? static_cast<A>(vb[i]) : A(0);
     }
 }
 
@@ -61,15 +78,9 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_kernel(
 
     A carry = col_ok ? static_cast<A>(h0[bi * F + fc]) : A(0);
 
-    A ra[S], rb[S], na[S], nb[S];
-    scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, static_cast<int64_t>(seg) * S, col_ok,
-                              ra, rb);
-    for (int64_t t0 = 0; t0 < L; t0 += CH) {
+    // Scan one chunk held in (ra, rb), starting at t0, and write its states.
+    auto process = [&](A (&ra)[S], A (&rb)[S], int64_t t0) {
         const int64_t t_seg = t0 + static_cast<int64_t>(seg) * S;
-        const bool more = t0 + CH < L;
-        if (more) {
-            scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, t_seg + CH, col_ok, na, nb);
-        }
         // Segment-local inclusive scan from a zero state: (prod a, local h).
         A p = A(1), q = A(0);
 #pragma unroll
@@ -98,13 +109,19 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_kernel(
             }
         }
         __syncthreads();
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < S; ++i) {
-                ra[i] = na[i];
-                rb[i] = nb[i];
-            }
-        }
+    };
+
+    // Two register buffers, alternated by a two-chunk loop body, so that the
+    // next chunk's loads are always in flight while the current one is scanned.
+    A xa[S], xb[S], ya[S], yb[S];
+    const int64_t seg_off = static_cast<int64_t>(seg) * S;
+    scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, seg_off, col_ok, xa, xb);
+    for (int64_t t0 = 0; t0 < L; t0 += 2 * CH) {
+        scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, t0 + CH + seg_off, col_ok, ya, yb);
+        process(xa, xb, t0);
+        if (t0 + CH >= L) break;
+        scan_load<T, A, S, BCAST>(a_col, b_col, a_stride, F, L, t0 + 2 * CH + seg_off, col_ok, xa, xb);
+        process(ya, yb, t0 + CH);
     }
 }
 
@@ -138,13 +155,24 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_backward_kernel(
     for (int64_t u0 = 0; u0 < L; u0 += CH) {
         const int64_t u_seg = u0 + static_cast<int64_t>(seg) * S;
         A ra[S], rb[S], hp[S];
+        T va[S], vg[S], vh[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {  // unconditional, clamped loads (see scan_load)
+            const int64_t t = L - 1 - (u_seg + i);
+            const int64_t tc = t < 0 ? 0 : t;
+            const int64_t ta = tc + 1 < L ? tc + 1 : L - 1;
+            const int64_t tp = tc > 0 ? tc - 1 : 0;
+            va[i] = a_col[ta * a_stride];
+            vg[i] = dh[base + tc * F];
+            vh[i] = h[base + tp * F];
+        }
 #pragma unroll
         for (int i = 0; i < S; ++i) {
             const int64_t t = L - 1 - (u_seg + i);
             const bool ok = col_ok && t >= 0;
-            ra[i] = (ok && t + 1 < L) ? static_cast<A>(a_col[(t + 1) * a_stride]) : A(1);
-            rb[i] = ok ? static_cast<A>(dh[base + t * F]) : A(0);
-            hp[i] = ok ? (t > 0 ? static_cast<A>(h[base + (t - 1) * F]) : h_init) : A(0);
+            ra[i] = (ok && t + 1 < L) ? static_cast<A>(va[i]) : A(1);
+            rb[i] = ok ? static_cast<A>(vg[i]) : A(0);
+            hp[i] = ok ? (t > 0 ? static_cast<A>(vh[i]) : h_init) : A(0);
         }
         A p = A(1), q = A(0);
 #pragma unroll

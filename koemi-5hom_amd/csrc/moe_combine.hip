@@ -118,6 +118,100 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_rows_kernel(
     }
 }
 
+// top_k <= KMAX: the token's positions live in registers, sorted ascending by
+// a compare-exchange network, and every row load of a vector step is issued
+// before the first add (loads are unconditional at clamped addresses; rows
+// beyond the token's count reuse its first row and are skipped in the sum).
+template <int KMAX>
+__device__ __forceinline__ void sort_positions(int64_t (&p)[KMAX]) {
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i)
+#pragma unroll
+        for (int j = 0; j + 1 < KMAX - i; ++j) {
+            const int64_t lo = min(p[j], p[j + 1]), hi = max(p[j], p[j + 1]);
+            p[j] = lo;
+            p[j + 1] = hi;
+        }
+}
+
+template <typename T, int KMAX, bool VEC>
+__global__ __launch_bounds__(kWave * kCombineWaves) void combine_rows_small_kernel(
+    const T* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
+    const float* __restrict__ pair_w, T* __restrict__ out, int64_t tokens, int64_t k, int64_t D) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
+    if (t >= tokens) return;
+    const int lane = lane_id();
+    const int n = static_cast<int>(min(static_cast<int64_t>(cnt[t]), k));
+    int64_t p[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        const int64_t pj = pos[t * k + min(static_cast<int64_t>(j), k - 1)];
+        p[j] = j < n ? pj : INT64_MAX;
+    }
+    sort_positions<KMAX>(p);
+    const float kf = static_cast<float>(k);
+    T* orow = out + t * D;
+    if (n == 0) {
+        for (int64_t c = lane; c < D; c += kWave) orow[c] = from_f32<T>(0.0f);
+        return;
+    }
+    const T* rows[KMAX];
+    float w[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        const int64_t pj = j < n ? p[j] : p[0];
+        rows[j] = y + pj * D;
+        w[j] = pair_w ? pair_w[pj] : 0.0f;
+    }
+    if constexpr (VEC) {
+        constexpr int N = 16 / sizeof(T);
+        union V {
+            uint4 raw;
+            T e[N];
+        };
+        const int64_t nvec = D / N;
+        for (int64_t v0 = 0; v0 < nvec; v0 += kWave) {
+            const int64_t v = v0 + lane;
+            const int64_t vc = v < nvec ? v : nvec - 1;
+            V in[KMAX];
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) in[j].raw = reinterpret_cast<const uint4*>(rows[j])[vc];
+            float acc[N];
+#pragma unroll
+            for (int q = 0; q < N; ++q) acc[q] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) {
+                if (j < n) {
+#pragma unroll
+                    for (int q = 0; q < N; ++q) {
+                        const float f = to_f32(in[j].e[q]);
+                        acc[q] += pair_w ? f * w[j] : f / kf;
+                    }
+                }
+            }
+            if (v < nvec) {
+                V o;
+#pragma unroll
+                for (int q = 0; q < N; ++q) o.e[q] = from_f32<T>(acc[q]);
+                reinterpret_cast<uint4*>(orow)[v] = o.raw;
+            }
+        }
+    } else {
+        for (int64_t c0 = 0; c0 < D; c0 += kWave) {
+            const int64_t c = c0 + lane;
+            const int64_t cc = c < D ? c : D - 1;
+            float in[KMAX];
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) in[j] = to_f32(rows[j][cc]);
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j)
+                if (j < n) acc += pair_w ? in[j] * w[j] : in[j] / kf;
+            if (c < D) orow[c] = from_f32<T>(acc);
+        }
+    }
+}
+
 struct CombineWorkspace {
     size_t cnt_off, pos_off, total;
 };
@@ -135,6 +229,20 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
     const bool vec = (D * static_cast<int64_t>(sizeof(T))) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 16 == 0;
     const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+#define KOEMI_COMBINE_SMALL(KMAX)                                                                                   \
+    if (k <= KMAX) {                                                                                                \
+        if (vec)                                                                                                    \
+            hipLaunchKernelGGL((combine_rows_small_kernel<T, KMAX, true>), grid, block, 0, s,                       \
+                               static_cast<const T*>(y), cnt, pos, pair_w, static_cast<T*>(out), tokens, k, D);      \
+        else                                                                                                        \
+            hipLaunchKernelGGL((combine_rows_small_kernel<T, KMAX, false>), grid, block, 0, s,                      \
+                               static_cast<const T*>(y), cnt, pos, pair_w, static_cast<T*>(out), tokens, k, D);      \
+        return check_launch("koemi_moe_combine(rows)");                                                             \
+    }
+    KOEMI_COMBINE_SMALL(2)
+    KOEMI_COMBINE_SMALL(4)
+    KOEMI_COMBINE_SMALL(8)
+#undef KOEMI_COMBINE_SMALL
     if (vec)
         hipLaunchKernelGGL((combine_rows_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(y), cnt, pos, pair_w,
                            static_cast<T*>(out), tokens, k, D);

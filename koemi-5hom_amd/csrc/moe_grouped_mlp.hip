@@ -38,9 +38,10 @@ struct MlpWorkspace {
     int64_t max_slots;
 };
 
-// The MFMA path keeps H in bf16; the SIMT path keeps it in fp32.
+// The MFMA path (both GEMM K dimensions multiples of kBK) keeps H in bf16; the
+// SIMT path keeps it in fp32.
 inline bool mfma_shape(int64_t width, int64_t hidden, int dtype) {
-    return dtype == KOEMI_BF16 && width % 8 == 0 && hidden % 8 == 0;
+    return dtype == KOEMI_BF16 && width % kBK == 0 && hidden % kBK == 0;
 }
 
 inline MlpWorkspace mlp_workspace(int64_t pairs, int64_t width, int64_t hidden, int64_t E, int dtype) {
@@ -60,28 +61,75 @@ __device__ __forceinline__ float silu_f(float v) {
     return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// slot -> (expert, first row) for every BM-row tile of every expert segment.
-// Segment bounds are clamped to [0, pairs] so that malformed offsets can never
-// address rows outside the operands.
-__global__ void build_schedule_kernel(const int64_t* __restrict__ offsets, int64_t E, int64_t pairs,
-                                      int64_t max_slots, int32_t* __restrict__ slot_expert,
-                                      int64_t* __restrict__ slot_row, int64_t* __restrict__ slot_end) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    int64_t slot = 0;
-    for (int64_t e = 0; e < E; ++e) {
-        const int64_t lo = min(max(offsets[e], int64_t(0)), pairs);
-        const int64_t hi = min(max(offsets[e + 1], lo), pairs);
-        for (int64_t r = lo; r < hi && slot < max_slots; r += kBM) {
-            slot_expert[slot] = static_cast<int32_t>(e);
-            slot_row[slot] = r;
-            slot_end[slot] = hi;
-            ++slot;
+// slot -> (expert, first row, segment end) for every BM-row tile of every
+// expert segment, built by one workgroup: per-expert tile counts, their
+// exclusive prefix in LDS, then a binary search per slot. Segment bounds are
+// clamped to [0, pairs] so that malformed offsets can never address rows
+// outside the operands.
+constexpr int kSchedThreads = 1024;
+constexpr int64_t kMaxScheduleExperts = 8191;  // (E + 1) int32 tile prefixes stay within 32 KiB of LDS
+
+__device__ __forceinline__ void segment_bounds(const int64_t* __restrict__ offsets, int64_t e, int64_t pairs,
+                                               int64_t& lo, int64_t& hi) {
+    lo = min(max(offsets[e], int64_t(0)), pairs);
+    hi = min(max(offsets[e + 1], lo), pairs);
+}
+
+__global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
+    const int64_t* __restrict__ offsets, int64_t E, int64_t pairs, int64_t max_slots,
+    int32_t* __restrict__ slot_expert, int64_t* __restrict__ slot_row, int64_t* __restrict__ slot_end) {
+    extern __shared__ int32_t first_tile[];  // E + 1 entries
+    __shared__ int32_t span_sum[kSchedThreads];
+    const int tid = threadIdx.x;
+    const int64_t n = E + 1;
+    for (int64_t e = tid; e < E; e += kSchedThreads) {
+        int64_t lo, hi;
+        segment_bounds(offsets, e, pairs, lo, hi);
+        first_tile[e] = static_cast<int32_t>((hi - lo + kBM - 1) / kBM);
+    }
+    if (tid == 0) first_tile[E] = 0;
+    __syncthreads();
+    const int64_t per = (n + kSchedThreads - 1) / kSchedThreads;
+    const int64_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
+    int32_t sum = 0;
+    for (int64_t e = b0; e < b1; ++e) sum += first_tile[e];
+    span_sum[tid] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t run = 0;
+        for (int i = 0; i < kSchedThreads; ++i) {
+            const int32_t v = span_sum[i];
+            span_sum[i] = run;
+            run += v;
         }
     }
-    for (; slot < max_slots; ++slot) {
-        slot_expert[slot] = -1;
-        slot_row[slot] = 0;
-        slot_end[slot] = 0;
+    __syncthreads();
+    int32_t run = span_sum[tid];
+    for (int64_t e = b0; e < b1; ++e) {
+        const int32_t v = first_tile[e];
+        first_tile[e] = run;
+        run += v;
+    }
+    __syncthreads();
+    const int64_t total = first_tile[E];
+    for (int64_t slot = tid; slot < max_slots; slot += kSchedThreads) {
+        if (slot >= total) {
+            slot_expert[slot] = -1;
+            slot_row[slot] = 0;
+            slot_end[slot] = 0;
+            continue;
+        }
+        int64_t lo_e = 0, hi_e = E - 1;  // largest e with first_tile[e] <= slot
+        while (lo_e < hi_e) {
+            const int64_t mid = (lo_e + hi_e + 1) / 2;
+            if (first_tile[mid] <= slot) lo_e = mid;
+            else hi_e = mid - 1;
+        }
+        int64_t lo, hi;
+        segment_bounds(offsets, lo_e, pairs, lo, hi);
+        slot_expert[slot] = static_cast<int32_t>(lo_e);
+        slot_row[slot] = lo + (slot - first_tile[lo_e]) * kBM;
+        slot_end[slot] = hi;
     }
 }
 
@@ -113,27 +161,22 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const bf16* We0 = W0 + static_cast<int64_t>(e) * n_out * K;
     const bf16* We1 = GLU ? W1 + static_cast<int64_t>(e) * n_out * K : nullptr;
 
-    // Global load assignment: 4 16-byte chunks of A and 4 of B per thread.
+    // Global load assignment: 4 16-byte chunks of A and 4 of B per thread. The
+    // loads are unconditional at clamped addresses (a branch around a load would
+    // make the compiler wait for the prefetch too); rows past the segment or the
+    // output width only feed discarded outputs. K is a multiple of kBK.
     uint4 ra[4], rb[4];
     auto load_tiles = [&](int64_t k0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = tid + i * kGemmThreads;
             const int r = c >> 3, cc = (c & 7) * 8;
-            const int64_t grow = row0 + r;
-            const bool ok_a = grow < row_end && k0 + cc < K;
-            ra[i] = ok_a ? *reinterpret_cast<const uint4*>(A + grow * K + k0 + cc) : make_uint4(0, 0, 0, 0);
-            const bf16* src;
-            int64_t n;
-            if (GLU) {
-                n = n0 + (r & 63);
-                src = (r < 64 ? We0 : We1);
-            } else {
-                n = n0 + r;
-                src = We0;
-            }
-            const bool ok_b = n < n_out && k0 + cc < K;
-            rb[i] = ok_b ? *reinterpret_cast<const uint4*>(src + n * K + k0 + cc) : make_uint4(0, 0, 0, 0);
+            const int64_t kc = k0 + cc;
+            const int64_t grow = min(row0 + r, row_end - 1);
+            ra[i] = *reinterpret_cast<const uint4*>(A + grow * K + kc);
+            const bf16* src = (GLU && r >= 64) ? We1 : We0;
+            const int64_t n = min(GLU ? n0 + (r & 63) : n0 + r, n_out - 1);
+            rb[i] = *reinterpret_cast<const uint4*>(src + n * K + kc);
         }
     };
     auto store_tiles = [&]() {
@@ -270,14 +313,17 @@ __global__ __launch_bounds__(256) void glu_output_simt_kernel(
     }
 }
 
-// Rows past the valid pairs are zero (moe_kernels.cu:512, 167-169).
+// Rows past the valid pairs are zero (moe_kernels.cu:512, 167-169); a
+// grid-stride loop over only those rows.
 template <typename T>
 __global__ void zero_tail_rows_kernel(T* __restrict__ y, const int64_t* __restrict__ valid_end, int64_t pairs,
                                       int64_t D) {
-    const int64_t p = blockIdx.x;
-    if (p >= pairs || p < *valid_end) return;
-    for (int64_t c = threadIdx.x; c < D; c += blockDim.x) y[p * D + c] = static_cast<T>(0.0f);
+    const int64_t start = min(max(*valid_end, int64_t(0)), pairs);
+    for (int64_t p = start + blockIdx.x; p < pairs; p += gridDim.x)
+        for (int64_t c = threadIdx.x; c < D; c += blockDim.x) y[p * D + c] = static_cast<T>(0.0f);
 }
+
+inline unsigned tail_blocks(int64_t pairs) { return static_cast<unsigned>(pairs < 1024 ? (pairs > 0 ? pairs : 1) : 1024); }
 
 template <typename T>
 int run_simt(const void* x, const int64_t* experts, const int64_t* offsets, const void* Wg, const void* bg,
@@ -294,7 +340,7 @@ int run_simt(const void* x, const int64_t* experts, const int64_t* offsets, cons
                        static_cast<const T*>(bo), static_cast<T*>(y), D, Hd);
     st = check_launch("koemi_moe_grouped_mlp(output)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL(zero_tail_rows_kernel<T>, grid, block, 0, s, static_cast<T*>(y), offsets + E, P, D);
+    hipLaunchKernelGGL(zero_tail_rows_kernel<T>, dim3(tail_blocks(P)), block, 0, s, static_cast<T*>(y), offsets + E, P, D);
     return check_launch("koemi_moe_grouped_mlp(zero)");
 }
 
@@ -306,8 +352,10 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
     int64_t* slot_end = reinterpret_cast<int64_t*>(base + ws.slot_end_off);
     if (ws.max_slots > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-    hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(64), 0, s, offsets, E, P, ws.max_slots, slot_expert,
-                       slot_row, slot_end);
+    if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
+                                             static_cast<long long>(kMaxScheduleExperts));
+    hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
+                       s, offsets, E, P, ws.max_slots, slot_expert, slot_row, slot_end);
     int st = check_launch("koemi_moe_grouped_mlp(schedule)");
     if (st != KOEMI_OK) return st;
     const unsigned slots = static_cast<unsigned>(ws.max_slots);
@@ -321,8 +369,8 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
                        static_cast<bf16*>(y), slot_expert, slot_row, slot_end, D, Hd);
     st = check_launch("koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(static_cast<unsigned>(P)), dim3(256), 0, s,
-                       static_cast<bf16*>(y), offsets + E, P, D);
+    hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
+                       offsets + E, P, D);
     return check_launch("koemi_moe_grouped_mlp(zero)");
 }
 

@@ -27,9 +27,10 @@
 namespace koemi {
 namespace {
 
-constexpr int kChunk = 512;          // pairs per count/scatter wave
+constexpr int kChunk = 128;          // pairs per count/scatter wave
 constexpr int kMaxExperts = 4095;    // LDS holds E+1 cursors (scan: E+1 int64)
 constexpr int kScanThreads = 1024;
+constexpr int kScanPerLane = 8;      // chunks per lane per scan block
 
 inline int64_t num_chunks(int64_t pairs) { return (pairs + kChunk - 1) / kChunk; }
 
@@ -47,17 +48,30 @@ inline PermuteWorkspace permute_workspace(int64_t tokens, int64_t k, int64_t E) 
     return w;
 }
 
-// Pair key (moe_kernels.cu:68-91): expert for a valid token whose slot holds an
-// in-range expert not already used by an earlier slot, else the sentinel E.
+// Pair key (moe_kernels.cu:68-91) of pair g + lane: the expert for a valid token
+// whose slot holds an in-range expert not already used by an earlier slot of the
+// same token, else the sentinel E; -1 for lanes past p1. Earlier slots of a
+// token are read from the lanes that hold them (pairs are token-major), with a
+// memory read only when a token straddles the start of the 64-pair group.
 template <typename I>
-__device__ __forceinline__ int32_t pair_key(const I* __restrict__ a, const uint8_t* __restrict__ valid,
-                                            int64_t p, int64_t k, int64_t E) {
-    const int64_t t = p / k;
-    const int64_t s = p - t * k;
-    const int64_t e = static_cast<int64_t>(a[p]);
-    bool ok = valid[t] && e >= 0 && e < E;
-    for (int64_t r = 0; r < s && ok; ++r) ok = static_cast<int64_t>(a[t * k + r]) != e;
-    return static_cast<int32_t>(ok ? e : E);
+__device__ __forceinline__ int32_t group_key(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+                                             int64_t g, int64_t p1, int64_t k, int64_t E) {
+    const int lane = lane_id();
+    const int64_t p = g + lane;
+    const bool active = p < p1;
+    const int64_t pc = active ? p : p1 - 1;
+    const int64_t e = static_cast<int64_t>(a[pc]);
+    const int64_t t = pc / k;
+    const int64_t s = pc - t * k;
+    bool ok = active && valid[t] && e >= 0 && e < E;
+    for (int64_t r = 1; r < k; ++r) {
+        const int64_t above = __shfl_up(e, static_cast<unsigned>(r < kWave ? r : 0), kWave);
+        if (r <= s) {
+            const int64_t earlier = (r < kWave && lane >= r) ? above : static_cast<int64_t>(a[pc - r]);
+            ok = ok && earlier != e;
+        }
+    }
+    return active ? static_cast<int32_t>(ok ? e : E) : -1;
 }
 
 template <typename I>
@@ -70,32 +84,43 @@ __global__ __launch_bounds__(kWave) void permute_count_kernel(const I* __restric
     __syncthreads();
     const int64_t p0 = chunk * kChunk;
     const int64_t p1 = min(pairs, p0 + kChunk);
-    for (int64_t p = p0 + threadIdx.x; p < p1; p += kWave) atomicAdd(&hist[pair_key(a, valid, p, k, E)], 1);
+    for (int64_t g = p0; g < p1; g += kWave) {
+        const int32_t key = group_key(a, valid, g, p1, k, E);
+        if (key >= 0) atomicAdd(&hist[key], 1);
+    }
     __syncthreads();
     int32_t* row = counts + chunk * (E + 1);
     for (int64_t e = threadIdx.x; e <= E; e += kWave) row[e] = hist[e];
 }
 
 // counts[c][e] -> first destination of (chunk c, key e); offsets[e] = first
-// position of key e, offsets[E] = number of valid pairs.
+// position of key e, offsets[E] = number of valid pairs. Each wave owns keys;
+// a key's chunk counts are scanned kScanPerLane per lane with a wave prefix.
 __global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __restrict__ counts,
                                                                     int64_t* __restrict__ offsets, int64_t chunks,
                                                                     int64_t E) {
     extern __shared__ int64_t key_total[];  // E+1 entries
-    const int tid = threadIdx.x;
-    for (int64_t e = tid; e <= E; e += kScanThreads) {
-        int64_t run = 0;
-        for (int64_t c = 0; c < chunks; ++c) {
-            const int32_t v = counts[c * (E + 1) + e];
-            counts[c * (E + 1) + e] = static_cast<int32_t>(run);
-            run += v;
+    __shared__ int64_t span_sum[kScanThreads];
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    constexpr int kWaves = kScanThreads / kWave;
+    const int64_t n = E + 1;
+    // Sweep 1: total per key.
+    for (int64_t key = wave; key < n; key += kWaves) {
+        int64_t sum = 0;
+        for (int64_t c0 = 0; c0 < chunks; c0 += kWave * kScanPerLane) {
+            int32_t v[kScanPerLane];
+            const int64_t cl = c0 + static_cast<int64_t>(lane) * kScanPerLane;
+#pragma unroll
+            for (int j = 0; j < kScanPerLane; ++j) v[j] = counts[(cl + j < chunks ? cl + j : chunks - 1) * n + key];
+#pragma unroll
+            for (int j = 0; j < kScanPerLane; ++j) sum += (cl + j < chunks) ? v[j] : 0;
         }
-        key_total[e] = run;
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+        if (lane == 0) key_total[key] = sum;
     }
     __syncthreads();
-    // Exclusive scan of key_total over E+1 keys: each thread scans a contiguous span.
-    __shared__ int64_t span_sum[kScanThreads];
-    const int64_t n = E + 1;
+    // Exclusive scan over keys: each thread scans a contiguous span.
     const int64_t per = (n + kScanThreads - 1) / kScanThreads;
     const int64_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
     int64_t s = 0;
@@ -118,10 +143,38 @@ __global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __r
         run += v;
     }
     __syncthreads();
-    for (int64_t e = tid; e <= E; e += kScanThreads) {
-        offsets[e] = key_total[e];
-        const int64_t base = key_total[e];
-        for (int64_t c = 0; c < chunks; ++c) counts[c * (E + 1) + e] += static_cast<int32_t>(base);
+    for (int64_t e = tid; e < n; e += kScanThreads) offsets[e] = key_total[e];
+    // Sweep 2: exclusive scan of each key's counts over the chunks, from the key's offset.
+    for (int64_t key = wave; key < n; key += kWaves) {
+        int64_t base = key_total[key];
+        for (int64_t c0 = 0; c0 < chunks; c0 += kWave * kScanPerLane) {
+            int32_t v[kScanPerLane];
+            const int64_t cl = c0 + static_cast<int64_t>(lane) * kScanPerLane;
+#pragma unroll
+            for (int j = 0; j < kScanPerLane; ++j) {
+                const int64_t c = cl + j;
+                v[j] = counts[(c < chunks ? c : chunks - 1) * n + key];
+            }
+            int64_t local = 0;
+#pragma unroll
+            for (int j = 0; j < kScanPerLane; ++j) local += (cl + j < chunks) ? v[j] : 0;
+            int64_t incl = local;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const int64_t up = __shfl_up(incl, off, kWave);
+                if (lane >= off) incl += up;
+            }
+            int64_t pos = base + incl - local;
+#pragma unroll
+            for (int j = 0; j < kScanPerLane; ++j) {
+                const int64_t c = cl + j;
+                if (c < chunks) {
+                    counts[c * n + key] = static_cast<int32_t>(pos);
+                    pos += v[j];
+                }
+            }
+            base += __shfl(incl, kWave - 1, kWave);
+        }
     }
 }
 
@@ -139,8 +192,8 @@ __global__ __launch_bounds__(kWave) void permute_scatter_kernel(
     const int64_t p1 = min(pairs, p0 + kChunk);
     for (int64_t g = p0; g < p1; g += kWave) {
         const int64_t p = g + lane;
-        const bool active = p < p1;
-        const int32_t key = active ? pair_key(a, valid, p, k, E) : -1;
+        const int32_t key = group_key(a, valid, g, p1, k, E);
+        const bool active = key >= 0;
         // Group the lanes by key: peers = lanes of this group with my key.
         uint64_t remaining = __ballot(active);
         uint64_t peers = 0;
@@ -166,7 +219,6 @@ __global__ __launch_bounds__(kWave) void permute_scatter_kernel(
     }
 }
 
-// One wave per token: context row read once, written to each of the k positions.
 template <typename T, bool VEC>
 __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __restrict__ ctx,
                                                                    const int64_t* __restrict__ dest,
@@ -184,9 +236,9 @@ __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __re
         for (int64_t v0 = 0; v0 < nvec; v0 += kWave * 4) {
             uint4 buf[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < 4; ++u) {  // unconditional loads at clamped indices
                 const int64_t v = v0 + u * kWave + lane;
-                buf[u] = v < nvec ? reinterpret_cast<const uint4*>(src)[v] : make_uint4(0, 0, 0, 0);
+                buf[u] = reinterpret_cast<const uint4*>(src)[v < nvec ? v : nvec - 1];
             }
             for (int64_t s = 0; s < k; ++s) {
                 const int64_t d = dest[t * k + s];

@@ -36,48 +36,72 @@ struct Vec16 {
 };
 
 // NV vectors per lane; row width H must satisfy H % N == 0 and H <= NV*64*N.
-template <typename T, int NV>
+// Each wave handles ROWS consecutive rows and issues all of their loads before
+// any arithmetic, so ROWS*NV 16-byte loads per lane are in flight at once.
+template <typename T, int NV, int ROWS>
 __global__ __launch_bounds__(kWave * kNormWaves) void rmsnorm_silu_fwd_wave(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y, float* __restrict__ inv_out,
     int64_t rows, int H, float eps) {
     constexpr int N = Vec16<T>::N;
     const int lane = lane_id();
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * kNormWaves + threadIdx.x / kWave;
-    if (row >= rows) return;
-    const T* xr = x + row * H;
-    T* yr = y + row * H;
-    Vec16<T> xv[NV], wv[NV];
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kNormWaves + threadIdx.x / kWave) * ROWS;
+    if (row0 >= rows) return;
+    // Unconditional loads at clamped addresses (no branch around a load), zeroed
+    // afterwards where out of range, so all of them are in flight together.
+    Vec16<T> xv[ROWS][NV], wv[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         const int c = (v * kWave + lane) * N;
-        if (c < H) {
-            xv[v].raw = *reinterpret_cast<const uint4*>(xr + c);
-            wv[v].raw = *reinterpret_cast<const uint4*>(w + c);
-        } else {
-            xv[v].raw = make_uint4(0, 0, 0, 0);
-            wv[v].raw = make_uint4(0, 0, 0, 0);
-        }
+        wv[v].raw = *reinterpret_cast<const uint4*>(w + min(c, H - N));
     }
-    float ss = 0.0f;
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
+    for (int r = 0; r < ROWS; ++r)
 #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const float f = to_f32(xv[v].e[i]);
-            ss = __builtin_fmaf(f, f, ss);
+        for (int v = 0; v < NV; ++v) {
+            const int c = (v * kWave + lane) * N;
+            const int64_t rr = min(row0 + r, rows - 1);
+            xv[r][v].raw = *reinterpret_cast<const uint4*>(x + rr * H + min(c, H - N));
         }
-    ss = wave_sum_xor(ss);
-    const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
-    if (lane == 0) inv_out[row] = inv;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
         const int c = (v * kWave + lane) * N;
-        if (c < H) {
-            Vec16<T> o;
+        if (c >= H) wv[v].raw = make_uint4(0, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < N; ++i)
-                o.e[i] = from_f32<T>(silu(to_f32(xv[v].e[i]) * inv * to_f32(wv[v].e[i])));
-            *reinterpret_cast<uint4*>(yr + c) = o.raw;
+        for (int r = 0; r < ROWS; ++r)
+            if (c >= H || row0 + r >= rows) xv[r][v].raw = make_uint4(0, 0, 0, 0);
+    }
+    float ss[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        ss[r] = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const float f = to_f32(xv[r][v].e[i]);
+                ss[r] = __builtin_fmaf(f, f, ss[r]);
+            }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) ss[r] += __shfl_xor(ss[r], off, kWave);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (row0 + r >= rows) break;
+        const float inv = rsqrtf(ss[r] / static_cast<float>(H) + eps);
+        if (lane == r) inv_out[row0 + r] = inv;
+        T* yr = y + (row0 + r) * H;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int c = (v * kWave + lane) * N;
+            if (c < H) {
+                Vec16<T> o;
+#pragma unroll
+                for (int i = 0; i < N; ++i)
+                    o.e[i] = from_f32<T>(silu(to_f32(xv[r][v].e[i]) * inv * to_f32(wv[v].e[i])));
+                *reinterpret_cast<uint4*>(yr + c) = o.raw;
+            }
         }
     }
 }
@@ -181,25 +205,18 @@ int launch_forward(const void* x, const void* w, void* y, float* inv, int64_t ro
                          (reinterpret_cast<uintptr_t>(w) % 16 == 0) &&
                          (reinterpret_cast<uintptr_t>(y) % 16 == 0);
     const int Hi = static_cast<int>(H);
-    const dim3 wgrid(grid_for(rows, kNormWaves)), wblock(kWave * kNormWaves);
+    const dim3 wblock(kWave * kNormWaves);
     if (aligned && H % N == 0) {
         const int64_t vecs = H / N;  // vectors per row
-        if (vecs <= kWave * 1) {
-            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 1>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
-            return check_launch("koemi_rmsnorm_silu_forward");
-        }
-        if (vecs <= kWave * 2) {
-            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 2>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
-            return check_launch("koemi_rmsnorm_silu_forward");
-        }
-        if (vecs <= kWave * 4) {
-            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 4>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
-            return check_launch("koemi_rmsnorm_silu_forward");
-        }
-        if (vecs <= kWave * 8) {
-            hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, 8>), wgrid, wblock, 0, stream, xp, wp, yp, inv, rows, Hi, eps);
-            return check_launch("koemi_rmsnorm_silu_forward");
-        }
+#define KOEMI_NORM_LAUNCH(NV, ROWS)                                                                      \
+    hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, NV, ROWS>), dim3(grid_for(rows, kNormWaves * ROWS)), wblock, 0, \
+                       stream, xp, wp, yp, inv, rows, Hi, eps);                                           \
+    return check_launch("koemi_rmsnorm_silu_forward")
+        if (vecs <= kWave * 1) { KOEMI_NORM_LAUNCH(1, 4); }
+        if (vecs <= kWave * 2) { KOEMI_NORM_LAUNCH(2, 2); }
+        if (vecs <= kWave * 4) { KOEMI_NORM_LAUNCH(4, 1); }
+        if (vecs <= kWave * 8) { KOEMI_NORM_LAUNCH(8, 1); }
+#undef KOEMI_NORM_LAUNCH
     }
     if (rows > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "rmsnorm_silu: too many rows for the generic path");
     hipLaunchKernelGGL(rmsnorm_silu_fwd_block<T>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream, xp, wp, yp, inv, rows, Hi, eps);
