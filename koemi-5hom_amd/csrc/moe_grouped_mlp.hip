@@ -24,12 +24,29 @@ namespace {
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
-constexpr int kBM = 128;
-constexpr int kBN = 128;
-constexpr int kBK = 64;
-constexpr int kPad = 8;  // bf16 elements of row padding in LDS (conflict-free 16 B fragment reads)
-constexpr int kLdsStride = kBK + kPad;
+// Block tile 256 (pairs) x 256 (B rows), four waves in 2x2, each owning a
+// 128x128 sub-tile as 4x4 MFMA 32x32 tiles (256 fp32 accumulators). K advances
+// in 32-wide tiles through a ring of four LDS stages (32 KiB each: A then B)
+// filled by global_load_lds_dwordx4, which writes each lane's 16 bytes straight
+// into LDS at M0 + 16 * lane without passing through registers; two tiles are
+// in flight while one is multiplied, and the fragments of the next K step are
+// read while the current one is multiplied. A stage row is 64 bytes (four
+// 16-byte K groups); group g of row r sits at slot g ^ ((r >> 2) & 3), so the
+// sixteen rows read by any sixteen consecutive lanes fill 256 distinct bytes
+// of banks (conflict-free 16-byte fragment reads).
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 32;
+#ifndef KOEMI_GEMM_STAGES
+#define KOEMI_GEMM_STAGES 4
+#endif
+constexpr int kStages = KOEMI_GEMM_STAGES;
 constexpr int kGemmThreads = 256;
+constexpr uint32_t kStageBytes = 2u * kBM * kBK * 2u;  // A and B, bf16
+constexpr uint32_t kOperandBytes = kBM * kBK * 2u;
+constexpr int kGroupM = 4;  // tile slots per group in the launch order
+// Rows are 64 bytes; the K step of the fronts' MFMA shape check.
+constexpr int kKAlign = 64;
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
@@ -38,10 +55,10 @@ struct MlpWorkspace {
     int64_t max_slots;
 };
 
-// The MFMA path (both GEMM K dimensions multiples of kBK) keeps H in bf16; the
+// The MFMA path (both GEMM K dimensions multiples of kKAlign) keeps H in bf16; the
 // SIMT path keeps it in fp32.
 inline bool mfma_shape(int64_t width, int64_t hidden, int dtype) {
-    return dtype == KOEMI_BF16 && width % kBK == 0 && hidden % kBK == 0;
+    return dtype == KOEMI_BF16 && width % kKAlign == 0 && hidden % kKAlign == 0;
 }
 
 inline MlpWorkspace mlp_workspace(int64_t pairs, int64_t width, int64_t hidden, int64_t E, int dtype) {
@@ -133,140 +150,202 @@ __global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
     }
 }
 
-// One 128x128 output tile (GLU: 128 rows x 64 hidden units) per workgroup; four
-// waves in a 2x2 arrangement, each owning 64 rows x 64 B-rows as 2x2 MFMA
-// 32x32 tiles. The next K tile is fetched into registers while the current one
-// is multiplied out of LDS.
+// Byte offset of K group g (16 bytes) of row r inside one operand stage.
+__device__ __forceinline__ int slot_swizzle(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ uint32_t stage_slot(int r, int g) {
+    return static_cast<uint32_t>(r * (kBK * 2) + ((g ^ slot_swizzle(r)) << 4));
+}
+
+// Asynchronous 16-byte-per-lane copy global -> LDS (lane l writes M0 + 16 l).
+// Issued through inline assembly so that the compiler does not order every
+// later LDS read after it (it cannot tell the ring stages apart); completion is
+// tracked explicitly with vmcnt. M0 is restored afterwards.
+__device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* src) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds_byte_addr)), "v"(src)
+        : "memory");
+}
+
+// Waits until at most n tiles of this wave's stage copies are outstanding
+// (eight copies per tile and wave), then joins the workgroup.
+__device__ __forceinline__ void wait_tiles_and_sync(int64_t n) {
+    if (n >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One 256x256 tile per workgroup. GLU: B rows 0..127 are gate rows and
+// 128..255 the value rows of hidden units [h0, h0 + 128), so wave (wm, wn) holds
+// gate and value accumulators of the same 128 rows x 64 hidden units and forms
+// silu(g + b_g) * (u + b_v) in registers. Plain: 256 consecutive output
+// columns. The MFMA is issued with the weight fragment as its first operand,
+// so each lane's accumulators are four consecutive output columns of one row
+// (8-byte stores). Launch order: workgroup i runs on XCD i % 8; tiles are
+// renumbered so that every XCD owns a contiguous range, traversed in groups of
+// kGroupM slots (all column tiles of a group before the next), which keeps the
+// A rows and B columns of concurrently running tiles in that XCD's L2.
 template <bool GLU>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
-    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K) {
-    __shared__ __attribute__((aligned(16))) bf16 As[kBM * kLdsStride];
-    __shared__ __attribute__((aligned(16))) bf16 Bs[kBN * kLdsStride];
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t slots, int64_t n_tiles,
+    int64_t per_xcd) {
+    __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
 
-    const int e = slot_expert[blockIdx.x];
+    const int64_t logical = static_cast<int64_t>(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    const int64_t group = kGroupM * n_tiles;
+    const int64_t gi = logical / group;
+    const int64_t first_slot = gi * kGroupM;
+    if (first_slot >= slots) return;
+    const int64_t gm = min(static_cast<int64_t>(kGroupM), slots - first_slot);
+    const int64_t within = logical - gi * group;
+    const int64_t slot = first_slot + within % gm;
+    const int64_t tile_n = within / gm;
+    const int e = slot_expert[slot];
     if (e < 0) return;
-    const int64_t row0 = slot_row[blockIdx.x];
-    const int64_t row_end = slot_end[blockIdx.x];
+    const int64_t row0 = slot_row[slot];
+    const int64_t row_end = slot_end[slot];
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = tid / kWave;
     const int wm = wave >> 1, wn = wave & 1;
+    const int64_t n0 = GLU ? tile_n * (kBN / 2) : tile_n * kBN;
 
-    // B rows of this tile: GLU -> 64 gate rows then 64 value rows of hidden units
-    // [h0, h0 + 64); plain -> 128 consecutive output columns from n0.
-    const int64_t n0 = GLU ? static_cast<int64_t>(blockIdx.y) * (kBN / 2) : static_cast<int64_t>(blockIdx.y) * kBN;
-    const bf16* We0 = W0 + static_cast<int64_t>(e) * n_out * K;
-    const bf16* We1 = GLU ? W1 + static_cast<int64_t>(e) * n_out * K : nullptr;
-
-    // Global load assignment: 4 16-byte chunks of A and 4 of B per thread. The
-    // loads are unconditional at clamped addresses (a branch around a load would
-    // make the compiler wait for the prefetch too); rows past the segment or the
-    // output width only feed discarded outputs. K is a multiple of kBK.
-    uint4 ra[4], rb[4];
-    auto load_tiles = [&](int64_t k0) {
+    // Stage copies: wave w fills 1 KiB chunks 4w..4w+3 (16 rows each) of A and
+    // of B; lane l of a chunk copies row l / 4 of it, K group (l % 4) ^ swizzle.
+    // Rows past the segment or the output width are clamped (they only feed
+    // discarded outputs). Offsets are 32-bit and relative to per-tile bases
+    // (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves 0-1
+    // copy gate rows, waves 2-3 value rows.
+    const bf16* a_base = A + row0 * K;
+    const bf16* b_base = ((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K;
+    const int a_rows = static_cast<int>(row_end - row0);
+    int a_off[4], b_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (wave * 4 + i) * 16 + (lane >> 2);
+        const int g = (lane & 3) ^ slot_swizzle(r);
+        a_off[i] = min(r, a_rows - 1) * static_cast<int>(K) + g * 8;
+        const int64_t n = GLU ? min(n0 + (r & 127), n_out - 1) : min(n0 + r, n_out - 1);
+        b_off[i] = static_cast<int>(n) * static_cast<int>(K) + g * 8;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+    auto issue = [&](int64_t kt, int stage) {
+        const uint32_t a_dst = lds0 + stage * kStageBytes + wave * 4 * 1024;
+        const int64_t k0 = kt * kBK;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int r = c >> 3, cc = (c & 7) * 8;
-            const int64_t kc = k0 + cc;
-            const int64_t grow = min(row0 + r, row_end - 1);
-            ra[i] = *reinterpret_cast<const uint4*>(A + grow * K + kc);
-            const bf16* src = (GLU && r >= 64) ? We1 : We0;
-            const int64_t n = min(GLU ? n0 + (r & 63) : n0 + r, n_out - 1);
-            rb[i] = *reinterpret_cast<const uint4*>(src + n * K + kc);
-        }
-    };
-    auto store_tiles = [&]() {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = tid + i * kGemmThreads;
-            const int r = c >> 3, cc = (c & 7) * 8;
-            *reinterpret_cast<uint4*>(As + r * kLdsStride + cc) = ra[i];
-            *reinterpret_cast<uint4*>(Bs + r * kLdsStride + cc) = rb[i];
+            lds_dma16(a_dst + i * 1024, a_base + a_off[i] + k0);
+            lds_dma16(a_dst + kOperandBytes + i * 1024, b_base + b_off[i] + k0);
         }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    // B-row base of each of the wave's two n-tiles.
-    int brow[2];
-    if (GLU) {
-        brow[0] = wn * 32;       // gate rows of hidden units h0 + wn*32 ...
-        brow[1] = 64 + wn * 32;  // value rows of the same hidden units
-    } else {
-        brow[0] = wn * 64;
-        brow[1] = wn * 64 + 32;
+    // Fragment rows: A rows of the wave's four m-tiles, B rows of its four
+    // n-tiles (GLU: two gate, two value).
+    const int fr = lane & 31;
+    const int fg = lane >> 5;
+    int a_row[4], b_row[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        a_row[t] = wm * 128 + t * 32 + fr;
+        b_row[t] = (GLU ? ((t < 2) ? wn * 64 + t * 32 : 128 + wn * 64 + (t - 2) * 32) : wn * 128 + t * 32) + fr;
     }
-    const int frag_row = lane & 31;
-    const int frag_k = (lane >> 5) * 8;
 
-    load_tiles(0);
-    for (int64_t k0 = 0; k0 < K; k0 += kBK) {
-        store_tiles();
-        __syncthreads();
-        if (k0 + kBK < K) load_tiles(k0 + kBK);
+    auto read_frags = [&](int64_t kt, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
+        const char* As = lds + (kt % kStages) * kStageBytes;
+        const char* Bs = As + kOperandBytes;
 #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 16) {
-            bf16x8 af[2], bfr[2];
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-                af[mt] = *reinterpret_cast<const bf16x8*>(As + (wm * 64 + mt * 32 + frag_row) * kLdsStride + kk + frag_k);
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-                bfr[nt] = *reinterpret_cast<const bf16x8*>(Bs + (brow[nt] + frag_row) * kLdsStride + kk + frag_k);
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0);
+        for (int t = 0; t < 4; ++t) {
+            af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
+            bfr[t] = *reinterpret_cast<const bf16x8*>(Bs + stage_slot(b_row[t], kk * 2 + fg));
         }
-        __syncthreads();
+    };
+    auto multiply = [&](const bf16x8 (&af)[4], const bf16x8 (&bfr)[4]) {
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    };
+
+    // K is a multiple of 64, so nk >= 2.
+    const int64_t nk = K / kBK;
+#pragma unroll
+    for (int p = 0; p < kStages - 1; ++p)
+        if (p < nk) issue(p, p);
+    wait_tiles_and_sync(min(static_cast<int64_t>(kStages - 2), nk - 1));
+    bf16x8 a0[4], b0[4], a1[4], b1[4];
+    read_frags(0, 0, a0, b0);
+    for (int64_t kt = 0; kt < nk; ++kt) {
+        // Tile kt + 1 has landed for every wave, and every wave is done with
+        // the stage of tile kt - 1, which the next copy overwrites.
+        wait_tiles_and_sync(min(static_cast<int64_t>(kStages - 3), nk - 2 - kt));
+        if (kt + kStages - 1 < nk) issue(kt + kStages - 1, static_cast<int>((kt + kStages - 1) % kStages));
+        read_frags(kt, 1, a1, b1);
+        multiply(a0, b0);
+        if (kt + 1 < nk) read_frags(kt + 1, 0, a0, b0);
+        multiply(a1, b1);
     }
 
-    // Epilogue. Accumulator element v of lane l is row (l/32)*4 + v%4 + (v/4)*8,
-    // column l%32 of its 32x32 tile.
-    const int col_in_tile = lane & 31;
-    const int row_base = (lane >> 5) * 4;
-    if (GLU) {
-        const int64_t h = n0 + wn * 32 + col_in_tile;
-        if (h < n_out) {
-            const float bg = to_f32(bias0[static_cast<int64_t>(e) * n_out + h]);
-            const float bv = to_f32(bias1[static_cast<int64_t>(e) * n_out + h]);
+    // Epilogue. Accumulator element v of lane l: row (of the tile) l % 32,
+    // column 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its 32x32 tile. The biases
+    // of the lane's columns are read once, before the row loop.
+    const int col4 = fg * 4;
+    constexpr int kBiasTiles = GLU ? 2 : 4;
+    float b0v[kBiasTiles][16], b1v[GLU ? 2 : 1][16];
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+    for (int nt = 0; nt < kBiasTiles; ++nt)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t grow = row0 + wm * 64 + mt * 32 + row_base + (v & 3) + (v >> 2) * 8;
-                    if (grow < row_end) {
-                        const float g = acc[mt][0][v] + bg;
-                        const float u = acc[mt][1][v] + bv;
-                        C[grow * n_out + h] = from_f32<bf16>(silu_f(g) * u);
+        for (int v = 0; v < 16; ++v) {
+            const int64_t col = (GLU ? n0 + wn * 64 : n0 + wn * 128) + nt * 32 + col4 + (v >> 2) * 8 + (v & 3);
+            const int64_t cc = static_cast<int64_t>(e) * n_out + min(col, n_out - 1);
+            b0v[nt][v] = to_f32(bias0[cc]);
+            if constexpr (GLU) b1v[nt][v] = to_f32(bias1[cc]);
+        }
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int64_t grow = row0 + wm * 128 + mt * 32 + fr;
+        if (grow >= row_end) continue;
+        bf16* crow = C + grow * n_out;
+#pragma unroll
+        for (int nt = 0; nt < kBiasTiles; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = (GLU ? n0 + wn * 64 : n0 + wn * 128) + nt * 32 + col4 + j * 8;
+                if (col >= n_out) continue;
+                union {
+                    uint2 raw;
+                    bf16 e[4];
+                } o;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if constexpr (GLU) {
+                        const float g = acc[mt][nt][j * 4 + q] + b0v[nt][j * 4 + q];
+                        const float u = acc[mt][nt + 2][j * 4 + q] + b1v[nt][j * 4 + q];
+                        o.e[q] = from_f32<bf16>(silu_f(g) * u);
+                    } else {
+                        o.e[q] = from_f32<bf16>(acc[mt][nt][j * 4 + q] + b0v[nt][j * 4 + q]);
                     }
                 }
-        }
-    } else {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            const int64_t col = n0 + wn * 64 + nt * 32 + col_in_tile;
-            if (col >= n_out) continue;
-            const float bo = to_f32(bias0[static_cast<int64_t>(e) * n_out + col]);
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t grow = row0 + wm * 64 + mt * 32 + row_base + (v & 3) + (v >> 2) * 8;
-                    if (grow < row_end) C[grow * n_out + col] = from_f32<bf16>(acc[mt][nt][v] + bo);
-                }
-        }
+                *reinterpret_cast<uint2*>(crow + col) = o.raw;
+            }
     }
 }
 
@@ -352,22 +431,30 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
     int64_t* slot_end = reinterpret_cast<int64_t*>(base + ws.slot_end_off);
     if (ws.max_slots > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
+    if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
     if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
                                              static_cast<long long>(kMaxScheduleExperts));
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
                        s, offsets, E, P, ws.max_slots, slot_expert, slot_row, slot_end);
     int st = check_launch("koemi_moe_grouped_mlp(schedule)");
     if (st != KOEMI_OK) return st;
-    const unsigned slots = static_cast<unsigned>(ws.max_slots);
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<true>), dim3(slots, grid_for(Hd, kBN / 2)), dim3(kGemmThreads), 0, s,
-                       static_cast<const bf16*>(x), static_cast<const bf16*>(Wg), static_cast<const bf16*>(Wv),
-                       static_cast<const bf16*>(bg), static_cast<const bf16*>(bv), H, slot_expert, slot_row, slot_end, Hd, D);
-    st = check_launch("koemi_moe_grouped_mlp(gemm1)");
+    const int64_t slots = ws.max_slots;
+    auto launch = [&](auto kernel, const bf16* a, const void* w0, const void* w1, const void* b0, const void* b1,
+                      bf16* c, int64_t n_out, int64_t K, int64_t n_tiles, const char* what) {
+        const int64_t tiles = slots * n_tiles;
+        const int64_t per_xcd = (tiles + 7) / 8;
+        if (per_xcd * 8 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kGemmThreads), 0, s, a,
+                           static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
+                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
+                           per_xcd);
+        return check_launch(what);
+    };
+    st = launch(grouped_gemm_bf16_kernel<true>, static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D,
+                (Hd + kBN / 2 - 1) / (kBN / 2), "koemi_moe_grouped_mlp(gemm1)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL((grouped_gemm_bf16_kernel<false>), dim3(slots, grid_for(D, kBN)), dim3(kGemmThreads), 0, s, H,
-                       static_cast<const bf16*>(Wo), nullptr, static_cast<const bf16*>(bo), nullptr,
-                       static_cast<bf16*>(y), slot_expert, slot_row, slot_end, D, Hd);
-    st = check_launch("koemi_moe_grouped_mlp(gemm2)");
+    st = launch(grouped_gemm_bf16_kernel<false>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd,
+                (D + kBN - 1) / kBN, "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
     hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
                        offsets + E, P, D);
