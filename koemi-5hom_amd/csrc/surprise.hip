@@ -219,18 +219,24 @@ __global__ void admission_threshold_kernel(const T* __restrict__ s, const uint8_
 }
 
 // ---------------------------------------------------------- quantile select ---
-// Exact k-th order statistic of n fp32 scores in one workgroup, by repeated
-// bucket refinement over the order-preserving 32-bit key of each float:
-// every pass histograms the keys inside the current [lo, hi] key range into
-// at most 4096 buckets of width 2^shift in LDS and keeps the bucket that holds
-// the target rank. The key range shrinks 2048-fold or more per pass, so three
-// passes reach a single key (two for the usual spread of scores).
+// Exact order statistics of n fp32 scores in one workgroup, over the
+// order-preserving 32-bit key of each float. One pass histograms all keys
+// into at most 4096 buckets of width 2^shift spanning [min, max] (LDS atomics)
+// and finds, by a prefix over the buckets, the buckets holding ranks k_lo and
+// k_hi. When those buckets are small (the usual case: a few dozen scores) their
+// keys are gathered into LDS and each candidate counts the smaller and equal
+// candidates, which names the key of each rank exactly. Crowded buckets (many
+// ties, or a few extreme outliers stretching the range) fall back to repeated
+// refinement: each further pass histograms the keys inside the current bucket,
+// shrinking the key range 2048-fold or more.
 //
-// For n <= 1024 * NPT the keys are loaded once into registers (all loads in
-// flight together) and every pass runs from registers; larger inputs re-read the
-// scores from L2 in each pass.
+// For n <= 1024 * 32 the scores and valid flags are loaded once into
+// registers (all loads in flight together), four consecutive elements per
+// thread and group so that the mask is written four bytes at a time; larger
+// inputs re-read the scores from L2 in each pass.
 constexpr int kSelThreads = 1024;
 constexpr int kSelBuckets = 4096;
+constexpr int kSelList = 512;  // candidates gathered per rank
 
 __device__ __forceinline__ uint32_t order_key(float f) {
     const uint32_t u = detmath::float_to_bits(f);
@@ -242,68 +248,94 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 }
 
 struct SelShared {
-    uint32_t hist[kSelBuckets];
-    uint32_t wave_tmp[kSelThreads / kWave];
-    uint32_t result[4];
+    uint32_t hist[kSelBuckets + kWave];  // one spill slot per lane for keys outside the range
+    uint32_t list[2][kSelList];
+    uint32_t wave_tmp[3][kSelThreads / kWave];
+    uint32_t result[8];
 };
 
-__device__ uint32_t block_sum_u32(uint32_t v, SelShared& sh) {
+// Sum, min and max over the workgroup in one exchange.
+__device__ void block_count_min_max(uint32_t& cnt, uint32_t& kmin, uint32_t& kmax, SelShared& sh) {
     const int lane = lane_id(), w = threadIdx.x / kWave;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    for (int off = 32; off > 0; off >>= 1) {
+        cnt += __shfl_xor(cnt, off, kWave);
+        kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(kmin, off, kWave)));
+        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(kmax, off, kWave)));
+    }
+    if (lane == 0) {
+        sh.wave_tmp[0][w] = cnt;
+        sh.wave_tmp[1][w] = kmin;
+        sh.wave_tmp[2][w] = kmax;
+    }
     __syncthreads();
-    if (lane == 0) sh.wave_tmp[w] = v;
-    __syncthreads();
-    uint32_t total = 0;
-    for (int i = 0; i < kSelThreads / kWave; ++i) total += sh.wave_tmp[i];
-    return total;
-}
-
-__device__ uint32_t block_min_u32(uint32_t v, SelShared& sh) {
-    const int lane = lane_id(), w = threadIdx.x / kWave;
+    cnt = 0;
+    kmin = 0xffffffffu;
+    kmax = 0;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = min(v, static_cast<uint32_t>(__shfl_xor(v, off, kWave)));
+    for (int i = 0; i < kSelThreads / kWave; ++i) {
+        cnt += sh.wave_tmp[0][i];
+        kmin = min(kmin, sh.wave_tmp[1][i]);
+        kmax = max(kmax, sh.wave_tmp[2][i]);
+    }
     __syncthreads();
-    if (lane == 0) sh.wave_tmp[w] = v;
-    __syncthreads();
-    uint32_t r = 0xffffffffu;
-    for (int i = 0; i < kSelThreads / kWave; ++i) r = min(r, sh.wave_tmp[i]);
-    return r;
 }
 
-__device__ uint32_t block_max_u32(uint32_t v, SelShared& sh) {
-    const int lane = lane_id(), w = threadIdx.x / kWave;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, off, kWave)));
-    __syncthreads();
-    if (lane == 0) sh.wave_tmp[w] = v;
-    __syncthreads();
-    uint32_t r = 0;
-    for (int i = 0; i < kSelThreads / kWave; ++i) r = max(r, sh.wave_tmp[i]);
-    return r;
-}
-
-// Scores held in registers: element j of thread tid is index j * kSelThreads + tid.
-template <int NPT>
+// Scores held in registers: group g of thread tid holds elements
+// 4 * (g * kSelThreads + tid) + c, c < 4.
+template <int NPT, bool VEC>
 struct RegisterKeys {
+    static_assert(NPT % 4 == 0 && NPT <= 32, "four elements per group; 128 VGPRs at 1024 threads");
+    static constexpr int kGroups = NPT / 4;
     uint32_t key[NPT];
     uint64_t present;  // bit j: index in range and score not NaN
-    __device__ void load(const float* __restrict__ s, int64_t n) {
+    uint64_t ok;       // bit j: valid flag
+    __device__ static int64_t index(int g, int c) {
+        return (static_cast<int64_t>(g) * kSelThreads + threadIdx.x) * 4 + c;
+    }
+    __device__ void load(const float* __restrict__ s, const uint8_t* __restrict__ valid, int64_t n) {
         float v[NPT];
+        uint32_t vw[kGroups];
+        // Unconditional loads at clamped indices; VEC: n % 4 == 0, the scores
+        // are 16-byte and the flags 4-byte aligned, so each group is one
+        // 16-byte and one 4-byte load.
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) {  // unconditional loads at clamped indices
-            const int64_t i = static_cast<int64_t>(j) * kSelThreads + threadIdx.x;
-            v[j] = s[i < n ? i : n - 1];
+        for (int g = 0; g < kGroups; ++g) {
+            if constexpr (VEC) {
+                const int64_t i = index(g, 0);
+                const int64_t ic = i < n ? i : n - 4;
+                const float4 f = *reinterpret_cast<const float4*>(s + ic);
+                v[g * 4 + 0] = f.x;
+                v[g * 4 + 1] = f.y;
+                v[g * 4 + 2] = f.z;
+                v[g * 4 + 3] = f.w;
+                vw[g] = *reinterpret_cast<const uint32_t*>(valid + ic);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t i = index(g, c);
+                    v[g * 4 + c] = s[i < n ? i : n - 1];
+                }
+                uint32_t w = 0;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int64_t i = index(g, c);
+                    w |= static_cast<uint32_t>(valid[i < n ? i : n - 1]) << (8 * c);
+                }
+                vw[g] = w;
+            }
         }
-#pragma unroll
-        for (int j = 0; j < NPT; ++j)
-            if (static_cast<int64_t>(j) * kSelThreads + threadIdx.x >= n) v[j] = __builtin_nanf("");
         present = 0;
+        ok = 0;
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) {
-            key[j] = order_key(v[j]);
-            if (v[j] == v[j]) present |= (1ull << j);
-        }
+        for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int j = g * 4 + c;
+                key[j] = order_key(v[j]);
+                if (index(g, c) < n && v[j] == v[j]) present |= (1ull << j);
+                if ((vw[g] >> (8 * c)) & 0xffu) ok |= (1ull << j);
+            }
     }
     template <class F>
     __device__ void visit(F f) const {
@@ -311,18 +343,30 @@ struct RegisterKeys {
         for (int j = 0; j < NPT; ++j)
             if ((present >> j) & 1ull) f(key[j]);
     }
-    __device__ void write_mask(const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm, int64_t n, float tau) const {
-        uint8_t ok[NPT];
+    // Every slot, with its presence flag (no branch per element).
+    template <class F>
+    __device__ void visit_all(F f) const {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) {
-            const int64_t i = static_cast<int64_t>(j) * kSelThreads + threadIdx.x;
-            ok[j] = valid[i < n ? i : n - 1];
-        }
+        for (int j = 0; j < NPT; ++j) f(key[j], ((present >> j) & 1ull) != 0);
+    }
+    __device__ void write_mask(uint8_t* __restrict__ adm, int64_t n, float tau) const {
 #pragma unroll
-        for (int j = 0; j < NPT; ++j) {
-            const int64_t i = static_cast<int64_t>(j) * kSelThreads + threadIdx.x;
-            const bool above = ((present >> j) & 1ull) && key_to_float(key[j]) > tau;
-            if (i < n) adm[i] = (ok[j] && above) ? 1 : 0;
+        for (int g = 0; g < kGroups; ++g) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int j = g * 4 + c;
+                const bool on = ((ok >> j) & 1ull) && ((present >> j) & 1ull) && key_to_float(key[j]) > tau;
+                w |= static_cast<uint32_t>(on) << (8 * c);
+            }
+            const int64_t i0 = index(g, 0);
+            if constexpr (VEC) {
+                if (i0 < n) *reinterpret_cast<uint32_t*>(adm + i0) = w;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (i0 + c < n) adm[i0 + c] = static_cast<uint8_t>((w >> (8 * c)) & 0xffu);
+            }
         }
     }
 };
@@ -330,9 +374,11 @@ struct RegisterKeys {
 // Scores re-read from memory in every pass (any n).
 struct MemoryKeys {
     const float* s;
+    const uint8_t* valid;
     int64_t n;
-    __device__ void load(const float* __restrict__ src, int64_t count) {
+    __device__ void load(const float* __restrict__ src, const uint8_t* __restrict__ flags, int64_t count) {
         s = src;
+        valid = flags;
         n = count;
     }
     template <class F>
@@ -351,67 +397,135 @@ struct MemoryKeys {
             if (v == v) f(order_key(v));
         }
     }
-    __device__ void write_mask(const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm, int64_t count, float tau) const {
+    template <class F>
+    __device__ void visit_all(F f) const {
+        visit([&](uint32_t k) { f(k, true); });
+    }
+    __device__ void write_mask(uint8_t* __restrict__ adm, int64_t count, float tau) const {
         for (int64_t i = threadIdx.x; i < count; i += kSelThreads) adm[i] = (valid[i] && s[i] > tau) ? 1 : 0;
     }
 };
 
-// Key of the element with 0-based rank `target` among the (non-NaN) keys.
+// Histograms the keys in [lo, hi] into kSelBuckets buckets of width 2^shift and
+// finds the bucket holding each of the ranks t0 <= t1 (ranks count from the
+// start of the range, after `below` smaller keys). Results in sh.result:
+// [0] bucket of t0, [1] keys before it, [2] its size, [3..5] the same for t1.
+template <class Keys>
+__device__ void bucket_pass(const Keys& keys, uint32_t lo, uint32_t hi, int shift, uint32_t below, uint32_t t0,
+                            uint32_t t1, SelShared& sh) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kSelBuckets + kWave; i += kSelThreads) sh.hist[i] = 0;
+    __syncthreads();
+    const uint32_t spill = kSelBuckets + lane_id();
+    keys.visit_all([&](uint32_t k, bool present) {
+        const bool in = present && k >= lo && k <= hi;
+        atomicAdd(&sh.hist[in ? (k - lo) >> shift : spill], 1u);
+    });
+    __syncthreads();
+    // Exclusive prefix over buckets: each thread owns 4 consecutive buckets.
+    constexpr int kPer = kSelBuckets / kSelThreads;
+    uint32_t local[kPer];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        local[q] = sh.hist[tid * kPer + q];
+        mine += local[q];
+    }
+    const int lane = lane_id(), w = tid / kWave;
+    uint32_t incl = mine;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t up = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += up;
+    }
+    if (lane == kWave - 1) sh.wave_tmp[0][w] = incl;
+    __syncthreads();
+    uint32_t wave_base = 0;
+    for (int i = 0; i < w; ++i) wave_base += sh.wave_tmp[0][i];
+    uint32_t run = below + wave_base + incl - mine;  // keys before my first bucket
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        if (t0 >= run && t0 < run + local[q]) {
+            sh.result[0] = static_cast<uint32_t>(tid * kPer + q);
+            sh.result[1] = run;
+            sh.result[2] = local[q];
+        }
+        if (t1 >= run && t1 < run + local[q]) {
+            sh.result[3] = static_cast<uint32_t>(tid * kPer + q);
+            sh.result[4] = run;
+            sh.result[5] = local[q];
+        }
+        run += local[q];
+    }
+    __syncthreads();
+}
+
+// Key of the element with 0-based rank `target` among the (non-NaN) keys, by
+// repeated bucket refinement.
 template <class Keys>
 __device__ uint32_t select_rank(const Keys& keys, uint32_t lo, uint32_t hi, uint32_t target, SelShared& sh) {
-    const int tid = threadIdx.x;
-    uint32_t below = 0;  // elements with key < lo
+    uint32_t below = 0;  // keys < lo
     for (int pass = 0; pass < 8 && lo < hi; ++pass) {
-        // Bucket width 2^shift with (hi - lo) >> shift < kSelBuckets (12-bit buckets).
         const uint32_t span = hi - lo;
         const int shift = span < kSelBuckets ? 0 : 32 - __builtin_clz(span) - 12;
-        for (int i = tid; i < kSelBuckets; i += kSelThreads) sh.hist[i] = 0;
-        __syncthreads();
-        const uint32_t lo_k = lo, hi_k = hi;
-        keys.visit([&](uint32_t k) {
-            if (k >= lo_k && k <= hi_k) atomicAdd(&sh.hist[(k - lo_k) >> shift], 1u);
-        });
-        __syncthreads();
-        // Exclusive prefix over buckets: each thread owns 4 consecutive buckets.
-        constexpr int kPer = kSelBuckets / kSelThreads;
-        uint32_t local[kPer];
-        uint32_t mine = 0;
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            local[q] = sh.hist[tid * kPer + q];
-            mine += local[q];
-        }
-        const int lane = lane_id(), w = tid / kWave;
-        uint32_t incl = mine;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const uint32_t up = __shfl_up(incl, off, kWave);
-            if (lane >= off) incl += up;
-        }
-        __syncthreads();
-        if (lane == kWave - 1) sh.wave_tmp[w] = incl;
-        __syncthreads();
-        uint32_t wave_base = 0;
-        for (int i = 0; i < w; ++i) wave_base += sh.wave_tmp[i];
-        uint32_t run = below + wave_base + incl - mine;  // elements before my first bucket
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            if (target >= run && target < run + local[q]) {
-                sh.result[0] = static_cast<uint32_t>(tid * kPer + q);
-                sh.result[1] = run;
-            }
-            run += local[q];
-        }
-        __syncthreads();
+        bucket_pass(keys, lo, hi, shift, below, target, target, sh);
         const uint32_t b = sh.result[0];
         below = sh.result[1];
+        __syncthreads();
         const uint64_t new_lo = static_cast<uint64_t>(lo) + (static_cast<uint64_t>(b) << shift);
         const uint64_t new_hi = new_lo + (uint64_t(1) << shift) - 1;
         lo = static_cast<uint32_t>(new_lo);
         hi = static_cast<uint32_t>(new_hi < hi ? new_hi : hi);
-        __syncthreads();
     }
     return lo;
+}
+
+// Keys of ranks t0 and t1 = t0 or t0 + 1 among the keys in [kmin, kmax].
+template <class Keys>
+__device__ void select_two_ranks(const Keys& keys, uint32_t kmin, uint32_t kmax, uint32_t t0, uint32_t t1,
+                                 SelShared& sh, uint32_t& key0, uint32_t& key1) {
+    const int tid = threadIdx.x;
+    const uint32_t span = kmax - kmin;
+    const int shift = span < kSelBuckets ? 0 : 32 - __builtin_clz(span) - 12;
+    bucket_pass(keys, kmin, kmax, shift, 0, t0, t1, sh);
+    const uint32_t b0 = sh.result[0], below0 = sh.result[1], n0 = sh.result[2];
+    const uint32_t b1 = sh.result[3], below1 = sh.result[4], n1 = sh.result[5];
+    __syncthreads();
+    if (n0 > kSelList || n1 > kSelList) {  // crowded bucket: refine
+        key0 = select_rank(keys, kmin, kmax, t0, sh);
+        key1 = (t1 == t0) ? key0 : select_rank(keys, kmin, kmax, t1, sh);
+        return;
+    }
+    // Gather the candidates of both buckets (list 1 only when they differ).
+    if (tid < 2) sh.result[6 + tid] = 0;
+    __syncthreads();
+    const uint32_t lo = kmin;
+    keys.visit([&](uint32_t k) {
+        const uint32_t b = (k - lo) >> shift;
+        if (b == b0) sh.list[0][atomicAdd(&sh.result[6], 1u)] = k;
+        else if (b == b1) sh.list[1][atomicAdd(&sh.result[7], 1u)] = k;
+    });
+    __syncthreads();
+    // Threads [0, 512) rank list 0 for t0, threads [512, 1024) the list of t1.
+    const int half = tid / kSelList;
+    const int idx = tid % kSelList;
+    const uint32_t* list = (half == 1 && b1 != b0) ? sh.list[1] : sh.list[0];
+    const uint32_t m = (half == 1 && b1 != b0) ? n1 : n0;
+    const uint32_t r = half == 0 ? t0 - below0 : t1 - below1;
+    if (static_cast<uint32_t>(idx) < m) {
+        const uint32_t x = list[idx];
+        uint32_t less = 0, equal = 0;
+        for (uint32_t j = 0; j < m; ++j) {
+            const uint32_t y = list[j];
+            less += y < x;
+            equal += y == x;
+        }
+        if (less <= r && r < less + equal) sh.result[half] = x;  // equal keys write the same value
+    }
+    __syncthreads();
+    key0 = sh.result[0];
+    key1 = sh.result[1];
+    __syncthreads();
 }
 
 template <class Keys>
@@ -420,34 +534,21 @@ __global__ __launch_bounds__(kSelThreads) void quantile_admission_kernel(
     float* __restrict__ tau_out, int64_t n, int64_t k_lo, int64_t k_hi, float weight) {
     __shared__ SelShared sh;
     Keys keys;
-    keys.load(s, n);
+    keys.load(s, valid, n);
     uint32_t counted = 0, kmin = 0xffffffffu, kmax = 0;
     keys.visit([&](uint32_t k) {
         ++counted;
         kmin = min(kmin, k);
         kmax = max(kmax, k);
     });
-    counted = block_sum_u32(counted, sh);
-    kmin = block_min_u32(kmin, sh);
-    kmax = block_max_u32(kmax, sh);
+    block_count_min_max(counted, kmin, kmax, sh);
     float tau;
     if (static_cast<int64_t>(counted) != n) {
         tau = __builtin_nanf("");  // a NaN score: torch.quantile propagates NaN
     } else {
-        const uint32_t key_lo = select_rank(keys, kmin, kmax, static_cast<uint32_t>(k_lo), sh);
-        uint32_t key_hi = key_lo;
-        if (k_hi != k_lo) {
-            // rank k_hi is key_lo again when more than k_hi elements are <= key_lo,
-            // otherwise the smallest key above key_lo.
-            uint32_t le = 0, above_min = 0xffffffffu;
-            keys.visit([&](uint32_t k) {
-                if (k <= key_lo) ++le;
-                else above_min = min(above_min, k);
-            });
-            le = block_sum_u32(le, sh);
-            above_min = block_min_u32(above_min, sh);
-            key_hi = (le > static_cast<uint32_t>(k_hi)) ? key_lo : above_min;
-        }
+        uint32_t key_lo, key_hi;
+        select_two_ranks(keys, kmin, kmax, static_cast<uint32_t>(k_lo), static_cast<uint32_t>(k_hi), sh, key_lo,
+                         key_hi);
         const float v_lo = key_to_float(key_lo);
         const float v_hi = key_to_float(key_hi);
         // torch.lerp: small weights interpolate from the start, large from the end.
@@ -455,7 +556,7 @@ __global__ __launch_bounds__(kSelThreads) void quantile_admission_kernel(
                             : __builtin_fmaf(weight - 1.0f, v_hi - v_lo, v_hi);
     }
     if (threadIdx.x == 0) *tau_out = tau;
-    keys.write_mask(valid, adm, n, tau);
+    keys.write_mask(adm, n, tau);
 }
 
 template <typename T>
@@ -574,17 +675,20 @@ extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* va
     const int64_t k_hi = static_cast<int64_t>(__builtin_ceilf(rank));
     const float weight = rank - static_cast<float>(k_lo);
     const hipStream_t s = as_stream(stream);
-    if (count <= 16LL * kSelThreads)
-        hipLaunchKernelGGL(quantile_admission_kernel<RegisterKeys<16>>, dim3(1), dim3(kSelThreads), 0, s,
-                           surprise, valid_mask, admission, threshold_out, count, k_lo, k_hi, weight);
-    else if (count <= 32LL * kSelThreads)
-        hipLaunchKernelGGL(quantile_admission_kernel<RegisterKeys<32>>, dim3(1), dim3(kSelThreads), 0, s,
-                           surprise, valid_mask, admission, threshold_out, count, k_lo, k_hi, weight);
-    else if (count <= 64LL * kSelThreads)
-        hipLaunchKernelGGL(quantile_admission_kernel<RegisterKeys<64>>, dim3(1), dim3(kSelThreads), 0, s,
-                           surprise, valid_mask, admission, threshold_out, count, k_lo, k_hi, weight);
-    else
-        hipLaunchKernelGGL(quantile_admission_kernel<MemoryKeys>, dim3(1), dim3(kSelThreads), 0, s,
-                           surprise, valid_mask, admission, threshold_out, count, k_lo, k_hi, weight);
+    const bool vec = count % 4 == 0 && reinterpret_cast<uintptr_t>(surprise) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(valid_mask) % 4 == 0 && reinterpret_cast<uintptr_t>(admission) % 4 == 0;
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission, threshold_out,
+                           count, k_lo, k_hi, weight);
+    };
+    if (count <= 16LL * kSelThreads) {
+        if (vec) launch(quantile_admission_kernel<RegisterKeys<16, true>>);
+        else launch(quantile_admission_kernel<RegisterKeys<16, false>>);
+    } else if (count <= 32LL * kSelThreads) {
+        if (vec) launch(quantile_admission_kernel<RegisterKeys<32, true>>);
+        else launch(quantile_admission_kernel<RegisterKeys<32, false>>);
+    } else {
+        launch(quantile_admission_kernel<MemoryKeys>);
+    }
     return check_launch("koemi_admission_quantile");
 }

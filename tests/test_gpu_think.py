@@ -125,7 +125,11 @@ def test_config2_surprise_and_quantile_admission_bit_exact(device):
     assert admitted == int(np.sum(want_s > want_tau))
 
 
-@pytest.mark.parametrize("case", ["single", "pair", "ties", "constant", "negative", "wide", "nan", "large"])
+@pytest.mark.parametrize(
+    "case",
+    ["single", "pair", "ties", "ties_aligned", "constant", "negative", "wide", "nan", "normal_32k", "odd_32k",
+     "ties_32k", "outliers_32k", "large"],
+)
 @pytest.mark.parametrize("q", [0.0, 0.25, 0.9, 1.0])
 def test_quantile_admission_edge_cases(device, case, q):
     rng = np.random.default_rng(sum(map(ord, case)))
@@ -137,6 +141,11 @@ def test_quantile_admission_edge_cases(device, case, q):
         "negative": rng.normal(0, 10, 5000),
         "wide": np.concatenate([rng.uniform(0, 1, 4000), [1e-30, 3e38, -3e38, 0.0, -0.0]]),
         "nan": np.array([0.1, np.nan, 0.5, 0.7]),
+        "ties_aligned": np.repeat([0.2, 0.5, 0.7], 400),
+        "normal_32k": rng.normal(0.63, 0.05, 32768),
+        "odd_32k": rng.normal(0.63, 0.05, 32767),
+        "ties_32k": rng.choice([0.25, 0.5, 0.75], 32768),
+        "outliers_32k": np.concatenate([rng.normal(0.63, 0.05, 32764), [1e-30, 3e38, -3e38, -0.0]]),
         "large": rng.uniform(0.5, 0.9, 300_000),
     }[case].astype(np.float32)
     valid = rng.random(scores.size) > 0.2
