@@ -65,6 +65,11 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run each HBM kernel a few times at its config plus a device copy of known size, for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (prints nothing else)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two --pmc passes over --traffic-probe into profiles/traffic.json")
     return ap.parse_args()
 
 
@@ -85,8 +90,107 @@ def load_traffic(kernel: str):
         return None
 
 
+# Kernels of the traffic probe: name fragment in the rocprofv3 kernel name -> bench key
+# and algorithmic bytes per launch.
+# (Names with __bf16 template arguments appear mangled or oddly demangled.)
+TRAFFIC_KERNELS = {
+    ("fwd_waveIDF16bLi1ELi4E", "rmsnorm_silu_fwd_wave<__bf16, 1, 4>", "rmsnorm_silu_fwd_wave<bool _Accum, int, E, 4>"):
+        ("C2.rmsnorm_silu", C2_NORM_BYTES),
+    ("surprise_rows_kernel",): ("C2.surprise_rows", C2_SURPRISE_BYTES),
+    ("scan_forward_kernel",): ("C3.affine_scan", C3_SCAN_BYTES),
+    ("fwd_waveIDF16bLi2ELi2E", "rmsnorm_silu_fwd_wave<__bf16, 2, 2>"): ("C3.rmsnorm_silu", C3_NORM_BYTES),
+    ("permute_gather_kernel",): ("C4.permute_gather", C4_T * C4_D * 2 + C4_PAIRS * C4_D * 2 + C4_PAIRS * 8),
+    ("combine_rows_small_kernel",): ("C4.combine_rows", C4_PAIRS * C4_D * 2 + C4_T * C4_D * 2 + C4_PAIRS * 8),
+}
+COPY_BYTES = 512 * 2**20  # the calibration copy reads and writes this many bytes
+
+
+def traffic_probe() -> int:
+    """Launch each HBM kernel at its configuration (and one device copy of known size)."""
+
+    import torch
+
+    from koemi_amd import core, dense, moe, think, workloads
+
+    device = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    c2 = workloads.config2()
+    x, gamma = c2.x.to(device), c2.gamma.to(device)
+    logits, targets, valid = c2.logits.to(device), c2.targets.to(device), c2.valid.to(device)
+    for _ in range(3):
+        core.rmsnorm_silu_forward(x, gamma, 1e-6)
+        think.surprise_from_logits(logits, targets, valid)
+    c3 = workloads.to_device(workloads.config3(), device)
+    for _ in range(3):
+        h = dense.scan_forward(c3.retention, c3.increment, c3.initial)
+    hb = h.to(torch.bfloat16).view(-1, 1024)
+    del c3, h
+    g3 = workloads.config3(batch=1, seq=1, width=1024).gamma.to(device)
+    for _ in range(3):
+        core.rmsnorm_silu_forward(hb, g3, 1e-6)
+    del hb
+    c4 = workloads.to_device(workloads.config4(), device)
+    a_l, w_l = moe.route_topk_learned(c4.router_logits, c4.valid, top_k=2)
+    for _ in range(3):
+        sc, rows, experts, offsets, sw = moe.permute_topk(c4.context, a_l, c4.valid, expert_count=16, pair_weights=w_l)
+    for _ in range(3):
+        moe.combine_topk(sc, rows, offsets, token_count=C4_T, top_k=2, pair_weights=sw)
+    torch.cuda.synchronize()
+    return 0
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
+    """profiles/traffic.json from rocprofv3 counter_collection.csv files of FETCH_SIZE and WRITE_SIZE."""
+
+    import csv
+    import statistics
+
+    def per_kernel(directory: str, counter: str) -> dict:
+        rows = []
+        for path in Path(directory).rglob("*counter_collection.csv"):
+            with path.open() as fh:
+                rows += [r for r in csv.DictReader(fh) if r["Counter_Name"] == counter]
+        out = {}
+        for r in rows:
+            out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return out
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+
+    def find(table: dict, fragments):
+        vals = [v for name, vs in table.items() if any(f in name for f in fragments) for v in vs]
+        return statistics.median(vals) if vals else None
+
+    # The calibration copy is the largest device-to-device copy (hipMemcpy's blit kernel).
+    copy_fetch = max(v for name, vs in fetch.items() if "copyBuffer" in name for v in vs)
+    copy_write = max(v for name, vs in write.items() if "copyBuffer" in name for v in vs)
+    fetch_scale = COPY_BYTES / (copy_fetch * 1024.0)
+    write_scale = COPY_BYTES / (copy_write * 1024.0)
+    result = {"_calibration": {"copy_bytes": COPY_BYTES, "copy_fetch_kib": copy_fetch, "copy_write_kib": copy_write,
+                               "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}}
+    for fragments, (key, algorithmic) in TRAFFIC_KERNELS.items():
+        f, w = find(fetch, fragments), find(write, fragments)
+        if f is None or w is None:
+            continue
+        read_b = f * 1024.0 * fetch_scale
+        write_b = w * 1024.0 * write_scale
+        result[key] = {"fetch_kib": f, "write_kib": w, "bytes_per_launch": round(read_b + write_b),
+                       "algorithmic_bytes": algorithmic, "ratio": round((read_b + write_b) / algorithmic, 4)}
+    out = ROOT / "profiles" / "traffic.json"
+    out.write_text(json.dumps(result, indent=1) + "\n")
+    print(json.dumps(result, indent=1))
+    return 0
+
+
 def main() -> int:
     args = parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
+    if args.traffic_probe:
+        return traffic_probe()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures a single GPU: this build has no multi-GPU path and every box has one GPU; "

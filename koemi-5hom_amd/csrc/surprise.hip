@@ -255,6 +255,7 @@ struct SelShared {
 };
 
 // Sum, min and max over the workgroup in one exchange.
+template <int THREADS = kSelThreads>
 __device__ void block_count_min_max(uint32_t& cnt, uint32_t& kmin, uint32_t& kmax, SelShared& sh) {
     const int lane = lane_id(), w = threadIdx.x / kWave;
 #pragma unroll
@@ -273,7 +274,7 @@ __device__ void block_count_min_max(uint32_t& cnt, uint32_t& kmin, uint32_t& kma
     kmin = 0xffffffffu;
     kmax = 0;
 #pragma unroll
-    for (int i = 0; i < kSelThreads / kWave; ++i) {
+    for (int i = 0; i < THREADS / kWave; ++i) {
         cnt += sh.wave_tmp[0][i];
         kmin = min(kmin, sh.wave_tmp[1][i]);
         kmax = max(kmax, sh.wave_tmp[2][i]);
@@ -410,20 +411,21 @@ struct MemoryKeys {
 // finds the bucket holding each of the ranks t0 <= t1 (ranks count from the
 // start of the range, after `below` smaller keys). Results in sh.result:
 // [0] bucket of t0, [1] keys before it, [2] its size, [3..5] the same for t1.
-template <class Keys>
+template <class Keys, int THREADS = kSelThreads, int BUCKETS = kSelBuckets>
 __device__ void bucket_pass(const Keys& keys, uint32_t lo, uint32_t hi, int shift, uint32_t below, uint32_t t0,
                             uint32_t t1, SelShared& sh) {
+    static_assert(BUCKETS <= kSelBuckets && BUCKETS % THREADS == 0, "bucket layout");
     const int tid = threadIdx.x;
-    for (int i = tid; i < kSelBuckets + kWave; i += kSelThreads) sh.hist[i] = 0;
+    for (int i = tid; i < BUCKETS + kWave; i += THREADS) sh.hist[i] = 0;
     __syncthreads();
-    const uint32_t spill = kSelBuckets + lane_id();
+    const uint32_t spill = BUCKETS + lane_id();
     keys.visit_all([&](uint32_t k, bool present) {
         const bool in = present && k >= lo && k <= hi;
         atomicAdd(&sh.hist[in ? (k - lo) >> shift : spill], 1u);
     });
     __syncthreads();
-    // Exclusive prefix over buckets: each thread owns 4 consecutive buckets.
-    constexpr int kPer = kSelBuckets / kSelThreads;
+    // Exclusive prefix over buckets: each thread owns kPer consecutive buckets.
+    constexpr int kPer = BUCKETS / THREADS;
     uint32_t local[kPer];
     uint32_t mine = 0;
 #pragma unroll
@@ -559,6 +561,322 @@ __global__ __launch_bounds__(kSelThreads) void quantile_admission_kernel(
     keys.write_mask(adm, n, tau);
 }
 
+// ----------------------------------------------- two-kernel quantile select ---
+// For larger n the per-element work is spread over many workgroups:
+//
+//   partition (grid, 4096 scores per workgroup): every workgroup reads the same
+//     strided sample of 1024 scores and, from its bucket histogram, the same
+//     two pivot keys p_lo <= p_hi bracketing sample ranks a few standard
+//     deviations either side of the target ranks. Each workgroup then splits
+//     its own scores into below p_lo (mask 0), above p_hi (mask = valid) and
+//     candidates, writes the decided mask bytes, and records its counts and
+//     its candidates (key; index in the workgroup with the valid flag in bit
+//     31) in its own workspace slot (no atomics, so the workspace needs no
+//     clearing).
+//   finish (one workgroup): every thread loads the records and its share of
+//     every slot at once (one memory round trip), checks that the target
+//     ranks lie among the candidates, selects their keys exactly from the
+//     candidates gathered in LDS, forms tau, checks p_lo <= tau <= p_hi (which
+//     makes every decided mask byte correct) and writes the candidates' mask
+//     bytes. If a check fails (a NaN score, a sample far off the data, too
+//     many candidates) it falls back to the exact single-workgroup select over
+//     all scores and rewrites the whole mask.
+constexpr int kPartThreads = 1024;
+constexpr int kPartPerThread = 4;
+constexpr int kPartScores = kPartThreads * kPartPerThread;  // per workgroup
+constexpr int kPartCand = kPartThreads;                      // candidate slots per workgroup
+constexpr int kPartMaxGroups = 32;                           // finish: one slot entry per thread and group
+static_assert(kPartMaxGroups * kPartScores <= (1 << 22), "32-bit sample index arithmetic");
+constexpr int kSampleBuckets = 1024;
+constexpr int kFinishCand = 8192;                            // candidates gathered in LDS
+constexpr int64_t kPartitionMin = 8192;                      // smaller inputs: one workgroup
+
+struct PartWorkspace {
+    size_t header_off, record_off, key_off, index_off, total;
+};
+inline PartWorkspace part_workspace(int64_t n) {
+    const int64_t groups = (n + kPartScores - 1) / kPartScores;
+    PartWorkspace w;
+    w.header_off = 0;
+    w.record_off = 256;
+    w.key_off = w.record_off + ((static_cast<size_t>(groups) * 4 * sizeof(uint32_t) + 255) & ~size_t(255));
+    w.index_off = w.key_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
+    w.total = w.index_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
+    return w;
+}
+
+// One sample key per thread: element floor(tid * n / 1024) (n > 1024 and
+// tid * n < 2^32 on the partitioned path, so 32-bit arithmetic is exact).
+struct SampleKeys {
+    uint32_t key;
+    bool present;
+    __device__ void load(const float* __restrict__ s, int64_t n) {
+        const uint32_t src = static_cast<uint32_t>(threadIdx.x) * static_cast<uint32_t>(n) / kPartThreads;
+        const float v = s[src];
+        key = order_key(v);
+        present = v == v;
+    }
+    template <class F>
+    __device__ void visit(F f) const {
+        if (present) f(key);
+    }
+    template <class F>
+    __device__ void visit_all(F f) const {
+        f(key, present);
+    }
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
+    const float* __restrict__ s, const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm, int64_t n,
+    int64_t k_lo, int64_t k_hi, uint32_t* __restrict__ header, uint32_t* __restrict__ records,
+    uint32_t* __restrict__ cand_key, uint32_t* __restrict__ cand_index) {
+    __shared__ SelShared sh;
+    const int tid = threadIdx.x;
+    // Own scores and the sample are loaded together.
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kPartScores + static_cast<int64_t>(tid) * kPartPerThread;
+    float v[kPartPerThread];
+    uint32_t vw = 0;
+    if constexpr (VEC) {
+        const int64_t ic = base < n ? base : n - kPartPerThread;
+        const float4 f = *reinterpret_cast<const float4*>(s + ic);
+        v[0] = f.x;
+        v[1] = f.y;
+        v[2] = f.z;
+        v[3] = f.w;
+        vw = *reinterpret_cast<const uint32_t*>(valid + ic);
+    } else {
+#pragma unroll
+        for (int c = 0; c < kPartPerThread; ++c) {
+            const int64_t i = base + c < n ? base + c : n - 1;
+            v[c] = s[i];
+            vw |= static_cast<uint32_t>(valid[i]) << (8 * c);
+        }
+    }
+    SampleKeys sample;
+    sample.load(s, n);
+
+    // Pivots from the sample (identical in every workgroup).
+    uint32_t m = sample.present ? 1u : 0u, smin = sample.present ? sample.key : 0xffffffffu,
+             smax = sample.present ? sample.key : 0u;
+    block_count_min_max<kPartThreads>(m, smin, smax, sh);
+    uint32_t p_lo = 0, p_hi = 0xffffffffu;
+    if (m > 0) {
+        const float frac0 = static_cast<float>(k_lo) / static_cast<float>(n);
+        const float frac1 = static_cast<float>(k_hi) / static_cast<float>(n);
+        const float sd = __builtin_sqrtf(static_cast<float>(m) * frac0 * (1.0f - frac0));
+        const float margin = 4.0f * sd + 4.0f;
+        const float r0f = frac0 * static_cast<float>(m) - margin;
+        const float r1f = frac1 * static_cast<float>(m) + margin;
+        const uint32_t r0 = r0f <= 0.0f ? 0u : min(static_cast<uint32_t>(r0f), m - 1);
+        const uint32_t r1 = r1f >= static_cast<float>(m - 1) ? m - 1 : static_cast<uint32_t>(r1f);
+        const uint32_t span = smax - smin;
+        const int shift = span < kSampleBuckets ? 0 : 32 - __builtin_clz(span) - 10;
+        bucket_pass<SampleKeys, kPartThreads, kSampleBuckets>(sample, smin, smax, shift, 0, r0, r1, sh);
+        const uint32_t b0 = sh.result[0], b1 = sh.result[3];
+        __syncthreads();
+        // Ranks at the sample's ends open the range to the whole key space.
+        p_lo = r0 == 0 ? 0u : smin + (b0 << shift);
+        const uint64_t top = static_cast<uint64_t>(smin) + ((static_cast<uint64_t>(b1) + 1) << shift) - 1;
+        p_hi = r1 == m - 1 ? 0xffffffffu : static_cast<uint32_t>(top < smax ? top : smax);
+    }
+    if (blockIdx.x == 0 && tid == 0) {
+        header[0] = p_lo;
+        header[1] = p_hi;
+    }
+
+    // Classify own scores; decided mask bytes are written now.
+    uint32_t below = 0, nan = 0, cand = 0, cand_bits = 0, out = 0;
+#pragma unroll
+    for (int c = 0; c < kPartPerThread; ++c) {
+        if (base + c >= n) continue;
+        const uint32_t k = order_key(v[c]);
+        if (v[c] != v[c]) {
+            ++nan;
+        } else if (k < p_lo) {
+            ++below;
+        } else if (k > p_hi) {
+            out |= ((vw >> (8 * c)) & 0xffu ? 1u : 0u) << (8 * c);
+        } else {
+            ++cand;
+            cand_bits |= 1u << c;
+        }
+    }
+    if constexpr (VEC) {
+        if (base < n) *reinterpret_cast<uint32_t*>(adm + base) = out;
+    } else {
+#pragma unroll
+        for (int c = 0; c < kPartPerThread; ++c)
+            if (base + c < n && !((cand_bits >> c) & 1u)) adm[base + c] = static_cast<uint8_t>((out >> (8 * c)) & 0xffu);
+    }
+    // Exclusive scan of the candidate counts over the workgroup; totals.
+    const int lane = lane_id(), w = tid / kWave;
+    uint32_t incl = cand;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t up = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += up;
+    }
+    uint32_t below_sum = below, nan_sum = nan;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        below_sum += __shfl_xor(below_sum, off, kWave);
+        nan_sum += __shfl_xor(nan_sum, off, kWave);
+    }
+    if (lane == kWave - 1) sh.wave_tmp[0][w] = incl;
+    if (lane == 0) {
+        sh.wave_tmp[1][w] = below_sum;
+        sh.wave_tmp[2][w] = nan_sum;
+    }
+    __syncthreads();
+    uint32_t pos = incl - cand, total = 0, below_total = 0, nan_total = 0;
+#pragma unroll
+    for (int i = 0; i < kPartThreads / kWave; ++i) {
+        if (i < w) pos += sh.wave_tmp[0][i];
+        total += sh.wave_tmp[0][i];
+        below_total += sh.wave_tmp[1][i];
+        nan_total += sh.wave_tmp[2][i];
+    }
+    uint32_t* keys_out = cand_key + static_cast<int64_t>(blockIdx.x) * kPartCand;
+    uint32_t* index_out = cand_index + static_cast<int64_t>(blockIdx.x) * kPartCand;
+#pragma unroll
+    for (int c = 0; c < kPartPerThread; ++c) {
+        if ((cand_bits >> c) & 1u) {
+            if (pos < kPartCand) {
+                keys_out[pos] = order_key(v[c]);
+                const uint32_t ok = ((vw >> (8 * c)) & 0xffu) ? 0x80000000u : 0u;
+                index_out[pos] = static_cast<uint32_t>(tid * kPartPerThread + c) | ok;
+            }
+            ++pos;
+        }
+    }
+    if (tid == 0) {
+        uint32_t* rec = records + static_cast<int64_t>(blockIdx.x) * 4;
+        rec[0] = below_total;
+        rec[1] = total;
+        rec[2] = nan_total;
+    }
+}
+
+// Candidate keys gathered in LDS.
+struct LdsKeys {
+    const uint32_t* key;
+    uint32_t m;
+    template <class F>
+    __device__ void visit(F f) const {
+        for (uint32_t i = threadIdx.x; i < m; i += kSelThreads) f(key[i]);
+    }
+    template <class F>
+    __device__ void visit_all(F f) const {
+        visit([&](uint32_t k) { f(k, true); });
+    }
+};
+
+__global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
+    const float* __restrict__ s, const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm,
+    float* __restrict__ tau_out, int64_t n, int64_t k_lo, int64_t k_hi, float weight,
+    const uint32_t* __restrict__ header, const uint32_t* __restrict__ records, const uint32_t* __restrict__ cand_key,
+    const uint32_t* __restrict__ cand_index, int groups) {
+    __shared__ SelShared sh;
+    __shared__ uint32_t keys[kFinishCand];
+    const int tid = threadIdx.x;
+    // One round trip: lane g of every wave loads record g (vector loads, all in
+    // flight together), every thread loads entry `tid` of every slot (in bounds
+    // whatever the counts), and the pivots.
+    const int lane = lane_id();
+    const int rg = lane < groups ? lane : groups - 1;
+    uint32_t rec_below = records[rg * 4 + 0];
+    uint32_t rec_cand = records[rg * 4 + 1];
+    uint32_t rec_nan = records[rg * 4 + 2];
+    uint32_t key[kPartMaxGroups], index[kPartMaxGroups];
+#pragma unroll
+    for (int g = 0; g < kPartMaxGroups; ++g) {
+        const int gc = g < groups ? g : groups - 1;
+        key[g] = cand_key[static_cast<int64_t>(gc) * kPartCand + tid];
+        index[g] = cand_index[static_cast<int64_t>(gc) * kPartCand + tid];
+    }
+    if (lane >= groups) rec_below = rec_cand = rec_nan = 0;
+    uint32_t below = rec_below, cand = rec_cand, bad = (rec_nan != 0 || rec_cand > kPartCand) ? 1u : 0u;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        below += __shfl_xor(below, off, kWave);
+        cand += __shfl_xor(cand, off, kWave);
+        bad |= __shfl_xor(bad, off, kWave);
+    }
+    uint32_t count[kPartMaxGroups];
+#pragma unroll
+    for (int g = 0; g < kPartMaxGroups; ++g) count[g] = __shfl(rec_cand, g, kWave);  // 0 past `groups`
+    const uint32_t p_lo = header[0], p_hi = header[1];
+    const bool fast = bad == 0 && cand <= kFinishCand && static_cast<int64_t>(below) <= k_lo &&
+                      k_hi < static_cast<int64_t>(below) + static_cast<int64_t>(cand);
+    float tau = 0.0f;
+    bool decided = false;
+    if (fast) {
+        uint32_t off = 0;
+#pragma unroll
+        for (int g = 0; g < kPartMaxGroups; ++g) {
+            if (static_cast<uint32_t>(tid) < count[g]) keys[off + tid] = key[g];
+            off += count[g];
+        }
+        __syncthreads();
+        LdsKeys lk{keys, cand};
+        uint32_t cnt = 0, kmin = 0xffffffffu, kmax = 0;
+        lk.visit([&](uint32_t k) {
+            ++cnt;
+            kmin = min(kmin, k);
+            kmax = max(kmax, k);
+        });
+        block_count_min_max(cnt, kmin, kmax, sh);
+        uint32_t key_lo, key_hi;
+        select_two_ranks(lk, kmin, kmax, static_cast<uint32_t>(k_lo - below), static_cast<uint32_t>(k_hi - below), sh,
+                         key_lo, key_hi);
+        const float v_lo = key_to_float(key_lo);
+        const float v_hi = key_to_float(key_hi);
+        tau = weight < 0.5f ? __builtin_fmaf(weight, v_hi - v_lo, v_lo)
+                            : __builtin_fmaf(weight - 1.0f, v_hi - v_lo, v_hi);
+        // Every decided byte is right when tau lies in [p_lo, p_hi]; for tau = ±0
+        // both zero keys must lie inside too (+0 > -0 is false for floats).
+        const uint32_t tk = order_key(tau);
+        decided = tau == tau && tk >= p_lo && tk <= p_hi;
+        if (tau == 0.0f) decided = decided && order_key(-0.0f) >= p_lo && order_key(0.0f) <= p_hi;
+        if (decided) {
+            // Mask bytes of the candidates (every other byte was decided by the partition).
+#pragma unroll
+            for (int g = 0; g < kPartMaxGroups; ++g) {
+                if (static_cast<uint32_t>(tid) < count[g]) {
+                    const int64_t i = static_cast<int64_t>(g) * kPartScores + (index[g] & 0x7fffffffu);
+                    adm[i] = ((index[g] >> 31) && key_to_float(key[g]) > tau) ? 1 : 0;
+                }
+            }
+        }
+    }
+    if (!decided) {
+        // Exact select over all scores from memory, and the whole mask.
+        MemoryKeys mk;
+        mk.load(s, valid, n);
+        uint32_t counted = 0, kmin = 0xffffffffu, kmax = 0;
+        mk.visit([&](uint32_t k) {
+            ++counted;
+            kmin = min(kmin, k);
+            kmax = max(kmax, k);
+        });
+        block_count_min_max(counted, kmin, kmax, sh);
+        if (static_cast<int64_t>(counted) != n) {
+            tau = __builtin_nanf("");
+        } else {
+            uint32_t key_lo, key_hi;
+            select_two_ranks(mk, kmin, kmax, static_cast<uint32_t>(k_lo), static_cast<uint32_t>(k_hi), sh, key_lo,
+                             key_hi);
+            const float v_lo = key_to_float(key_lo);
+            const float v_hi = key_to_float(key_hi);
+            tau = weight < 0.5f ? __builtin_fmaf(weight, v_hi - v_lo, v_lo)
+                                : __builtin_fmaf(weight - 1.0f, v_hi - v_lo, v_hi);
+        }
+        mk.write_mask(adm, n, tau);
+    }
+    if (tid == 0) *tau_out = tau;
+}
+
 template <typename T>
 int launch_rows(const float* logits, const void* bias, const int64_t* targets, const uint8_t* valid,
                 void* out, int64_t rows, int64_t V, float log_vocab, hipStream_t stream) {
@@ -653,17 +971,20 @@ extern "C" int koemi_admission_threshold(const void* surprise, const uint8_t* va
     return check_launch("koemi_admission_threshold");
 }
 
+// Inputs handled by the two-kernel path (more use the single workgroup).
+inline bool partitioned(int64_t count) {
+    return count > kPartitionMin && count <= static_cast<int64_t>(kPartMaxGroups) * kPartScores;
+}
+
 extern "C" size_t koemi_admission_quantile_workspace_bytes(int64_t count) {
-    (void)count;
-    return 0;
+    if (!partitioned(count)) return 0;
+    return part_workspace(count).total;
 }
 
 extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* valid_mask,
                                         uint8_t* admission, float* threshold_out, int64_t count,
                                         float quantile, void* workspace, size_t workspace_bytes,
                                         koemi_stream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     if (count < 1) return fail(KOEMI_ERR_INVALID, "quantile admission needs at least one score");
     if (count > 0xffffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "quantile admission supports at most 2^32-1 scores");
     if (!(quantile >= 0.0f && quantile <= 1.0f)) return fail(KOEMI_ERR_INVALID, "quantile must lie in [0, 1]");
@@ -681,14 +1002,33 @@ extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* va
         hipLaunchKernelGGL(kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission, threshold_out,
                            count, k_lo, k_hi, weight);
     };
-    if (count <= 16LL * kSelThreads) {
-        if (vec) launch(quantile_admission_kernel<RegisterKeys<16, true>>);
-        else launch(quantile_admission_kernel<RegisterKeys<16, false>>);
-    } else if (count <= 32LL * kSelThreads) {
-        if (vec) launch(quantile_admission_kernel<RegisterKeys<32, true>>);
-        else launch(quantile_admission_kernel<RegisterKeys<32, false>>);
-    } else {
-        launch(quantile_admission_kernel<MemoryKeys>);
+    if (count <= kPartitionMin) {
+        if (vec) launch(quantile_admission_kernel<RegisterKeys<8, true>>);
+        else launch(quantile_admission_kernel<RegisterKeys<8, false>>);
+        return check_launch("koemi_admission_quantile");
     }
+    if (!partitioned(count)) {
+        launch(quantile_admission_kernel<MemoryKeys>);
+        return check_launch("koemi_admission_quantile");
+    }
+    const PartWorkspace pw = part_workspace(count);
+    if (!workspace || workspace_bytes < pw.total)
+        return fail(KOEMI_ERR_INVALID, "quantile admission workspace too small: need %zu bytes", pw.total);
+    const int groups = static_cast<int>((count + kPartScores - 1) / kPartScores);
+    char* ws = static_cast<char*>(workspace);
+    uint32_t* header = reinterpret_cast<uint32_t*>(ws + pw.header_off);
+    uint32_t* records = reinterpret_cast<uint32_t*>(ws + pw.record_off);
+    uint32_t* cand_key = reinterpret_cast<uint32_t*>(ws + pw.key_off);
+    uint32_t* cand_index = reinterpret_cast<uint32_t*>(ws + pw.index_off);
+    if (vec)
+        hipLaunchKernelGGL(quantile_partition_kernel<true>, dim3(static_cast<unsigned>(groups)), dim3(kPartThreads), 0,
+                           s, surprise, valid_mask, admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
+    else
+        hipLaunchKernelGGL(quantile_partition_kernel<false>, dim3(static_cast<unsigned>(groups)), dim3(kPartThreads), 0,
+                           s, surprise, valid_mask, admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
+    const int st = check_launch("koemi_admission_quantile(partition)");
+    if (st != KOEMI_OK) return st;
+    hipLaunchKernelGGL(quantile_finish_kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission,
+                       threshold_out, count, k_lo, k_hi, weight, header, records, cand_key, cand_index, groups);
     return check_launch("koemi_admission_quantile");
 }

@@ -128,7 +128,7 @@ def test_config2_surprise_and_quantile_admission_bit_exact(device):
 @pytest.mark.parametrize(
     "case",
     ["single", "pair", "ties", "ties_aligned", "constant", "negative", "wide", "nan", "normal_32k", "odd_32k",
-     "ties_32k", "outliers_32k", "large"],
+     "ties_32k", "outliers_32k", "zeros_32k", "sorted_32k", "large"],
 )
 @pytest.mark.parametrize("q", [0.0, 0.25, 0.9, 1.0])
 def test_quantile_admission_edge_cases(device, case, q):
@@ -146,6 +146,8 @@ def test_quantile_admission_edge_cases(device, case, q):
         "odd_32k": rng.normal(0.63, 0.05, 32767),
         "ties_32k": rng.choice([0.25, 0.5, 0.75], 32768),
         "outliers_32k": np.concatenate([rng.normal(0.63, 0.05, 32764), [1e-30, 3e38, -3e38, -0.0]]),
+        "zeros_32k": rng.choice(np.array([-0.0, 0.0, 0.5, -1.0]), 32768),
+        "sorted_32k": np.sort(rng.normal(0.63, 0.05, 32768)),
         "large": rng.uniform(0.5, 0.9, 300_000),
     }[case].astype(np.float32)
     valid = rng.random(scores.size) > 0.2
