@@ -19,6 +19,8 @@
 // HBM traffic is the algorithmic minimum: read a and b once, write h once.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace koemi {
 namespace {
 
@@ -125,6 +127,128 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_kernel(
     }
 }
 
+// fp32, full-shape retention, F % VEC == 0 and 16-byte aligned rows: each lane
+// owns VEC adjacent columns (one VEC-wide vector load per step), so a wave
+// reads 64 * VEC * 4 contiguous bytes of every step row. Same two-level
+// structure and rounding as scan_forward_kernel (each column is scanned by the
+// same operations in the same order).
+template <int VEC>
+struct FloatVec;
+template <>
+struct FloatVec<2> {
+    using type = float2;
+    __device__ static void split(const float2& v, float (&o)[2]) { o[0] = v.x; o[1] = v.y; }
+    __device__ static float2 join(const float (&o)[2]) { return make_float2(o[0], o[1]); }
+};
+template <>
+struct FloatVec<4> {
+    using type = float4;
+    __device__ static void split(const float4& v, float (&o)[4]) { o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w; }
+    __device__ static float4 join(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
+};
+
+template <int S, int NSEG, int VEC>
+__global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
+    int64_t L, int64_t F, int64_t col_tiles) {
+    using V = typename FloatVec<VEC>::type;
+    constexpr int CH = S * NSEG;
+    __shared__ float seg_p[NSEG][VEC][kWave];
+    __shared__ float seg_b[NSEG][VEC][kWave];
+
+    const int lane = lane_id();
+    const int seg = static_cast<int>(threadIdx.x) / kWave;
+    const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
+    const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane) * VEC;
+    const bool col_ok = f < F;
+    const int64_t fc = col_ok ? f : 0;
+    const float* a_col = a + bi * L * F + fc;
+    const float* b_col = b + bi * L * F + fc;
+    float* h_col = h + bi * L * F + fc;
+
+    float carry[VEC];
+    {
+        const V c0 = *reinterpret_cast<const V*>(h0 + bi * F + fc);
+        FloatVec<VEC>::split(c0, carry);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) carry[c] = col_ok ? carry[c] : 0.0f;
+    }
+
+    auto load = [&](int64_t t_first, float (&ra)[S][VEC], float (&rb)[S][VEC]) {
+        V va[S], vb[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) {  // unconditional loads at clamped positions
+            const int64_t t = t_first + i;
+            const int64_t tc = t < L ? t : L - 1;
+            va[i] = *reinterpret_cast<const V*>(a_col + tc * F);
+            vb[i] = *reinterpret_cast<const V*>(b_col + tc * F);
+        }
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const bool ok = col_ok && t_first + i < L;
+            FloatVec<VEC>::split(va[i], ra[i]);
+            FloatVec<VEC>::split(vb[i], rb[i]);
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) {
+                ra[i][c] = ok ? ra[i][c] : 1.0f;
+                rb[i][c] = ok ? rb[i][c] : 0.0f;
+            }
+        }
+    };
+
+    auto process = [&](float (&ra)[S][VEC], float (&rb)[S][VEC], int64_t t0) {
+        const int64_t t_seg = t0 + static_cast<int64_t>(seg) * S;
+        float c_in[VEC];
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+            float p = 1.0f, q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                q = ra[i][c] * q + rb[i][c];
+                p = p * ra[i][c];
+                ra[i][c] = p;
+                rb[i][c] = q;
+            }
+            seg_p[seg][c][lane] = p;
+            seg_b[seg][c][lane] = q;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+            float cc = carry[c], ci = carry[c];
+#pragma unroll
+            for (int j = 0; j < NSEG; ++j) {
+                if (j == seg) ci = cc;
+                cc = seg_p[j][c][lane] * cc + seg_b[j][c][lane];
+            }
+            carry[c] = cc;
+            c_in[c] = ci;
+        }
+        if (col_ok) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const int64_t t = t_seg + i;
+                float o[VEC];
+#pragma unroll
+                for (int c = 0; c < VEC; ++c) o[c] = ra[i][c] * c_in[c] + rb[i][c];
+                if (t < L) *reinterpret_cast<V*>(h_col + t * F) = FloatVec<VEC>::join(o);
+            }
+        }
+        __syncthreads();
+    };
+
+    float xa[S][VEC], xb[S][VEC], ya[S][VEC], yb[S][VEC];
+    const int64_t seg_off = static_cast<int64_t>(seg) * S;
+    load(seg_off, xa, xb);
+    for (int64_t t0 = 0; t0 < L; t0 += 2 * CH) {
+        load(t0 + CH + seg_off, ya, yb);
+        process(xa, xb, t0);
+        if (t0 + CH >= L) break;
+        load(t0 + 2 * CH + seg_off, xa, xb);
+        process(ya, yb, t0 + CH);
+    }
+}
+
 // Reverse-time adjoint of the scan (dense/affine_scan.cu:58-106):
 //   g_t = dh_t + a_{t+1} g_{t+1},  db_t = g_t,  da_t = g_t h_{t-1},  dh0 = a_0 g_0.
 // In reversed time u = L-1-t this is a forward scan with coefficient a_{t+1}
@@ -210,9 +334,30 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_backward_kernel(
     }
 }
 
+#ifndef KOEMI_SCAN_VEC
+#define KOEMI_SCAN_VEC 2
+#endif
+
 template <typename T, bool BCAST>
 int launch_forward(const void* a, const void* b, const void* h0, void* h, int64_t B, int64_t L,
                    int64_t F, hipStream_t stream) {
+    if constexpr (std::is_same<T, float>::value && !BCAST && KOEMI_SCAN_VEC > 1) {
+        constexpr int VEC = KOEMI_SCAN_VEC;
+        const bool wide = F % VEC == 0 && reinterpret_cast<uintptr_t>(a) % (4 * VEC) == 0 &&
+                          reinterpret_cast<uintptr_t>(b) % (4 * VEC) == 0 &&
+                          reinterpret_cast<uintptr_t>(h) % (4 * VEC) == 0 &&
+                          reinterpret_cast<uintptr_t>(h0) % (4 * VEC) == 0;
+        if (wide) {
+            const int64_t tiles = (F / VEC + kWave - 1) / kWave;
+            const int64_t blocks = B * tiles;
+            if (blocks > 0x7fffffff) return fail(KOEMI_ERR_UNSUPPORTED, "affine scan grid too large");
+            hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC>),
+                               dim3(static_cast<unsigned>(blocks)), dim3(kWave * kScanSegments), 0, stream,
+                               static_cast<const float*>(a), static_cast<const float*>(b),
+                               static_cast<const float*>(h0), static_cast<float*>(h), L, F, tiles);
+            return check_launch("koemi_affine_scan_forward");
+        }
+    }
     const int64_t col_tiles = (F + kWave - 1) / kWave;
     const int64_t blocks = B * col_tiles;
     if (blocks > 0x7fffffff) return fail(KOEMI_ERR_UNSUPPORTED, "affine scan grid too large");

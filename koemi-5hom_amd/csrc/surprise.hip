@@ -4,14 +4,15 @@
 // after an fp32 logits GEMM), model/network.py:677-688 (surprise definition)
 // and network.py:349 (admission = valid & surprise > threshold).
 //
-// One wave owns one row of logits. A lane holds elements j = k*256 + lane*4 + p
-// (chunk k, component p) and reads them with one 16-byte load per chunk, so a
-// 256-logit row is a single coalesced 1 KiB wave load kept in registers: the row
-// is read from HBM once (max, sum-exp and the target logit all come from
-// registers). The sum of exponentials is accumulated per lane in (k, p) order and
-// then combined by a xor butterfly over the 64 lanes; with the exp/log routines
-// of detmath.hpp this fixes every rounding step, which is what lets the
-// admission mask be reproduced exactly on the host.
+// Rows of up to 256 logits take a quarter wave each (16 lanes, four rows per
+// wave side by side); longer rows take a whole wave, a lane holding elements
+// j = k*256 + lane*4 + p (chunk k, component p). Either way a row is read from
+// HBM once with 16-byte loads and kept in registers (max, sum-exp and the
+// target logit all come from registers). The sum of exponentials is
+// accumulated per lane in a fixed element order and then combined by a xor
+// butterfly over the row's lanes; with the exp/log routines of detmath.hpp this
+// fixes every rounding step, which is what lets the admission mask be
+// reproduced exactly on the host.
 #include "common.hpp"
 #include "detmath.hpp"
 
@@ -159,6 +160,83 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
         }
         out[row0 + r] = from_f32<T>(s);
     }
+}
+
+// V <= 256: a quarter wave (16 lanes) per row, four rows per wave processed
+// side by side. Lane sub of a row holds elements j = u*64 + sub*4 + p (u < 4,
+// p < 4), read as four 16-byte loads (for each u the 16 lanes of a row cover
+// 256 contiguous bytes). The exponentials are summed per lane in (u, p) order,
+// then by a xor butterfly over the 16 lanes (offsets 8, 4, 2, 1); lane 0 of
+// each quarter finishes its row. Every load is issued up front at a clamped
+// in-bounds address.
+template <typename T, bool VEC, bool HAS_BIAS>
+__global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
+    const float* __restrict__ logits, const T* __restrict__ bias,
+    const int64_t* __restrict__ targets, const uint8_t* __restrict__ valid, T* __restrict__ out,
+    int64_t rows, int64_t V, float log_vocab) {
+#pragma clang fp contract(off)
+    const int lane = lane_id();
+    const int sub = lane & 15;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * kRowWaves + threadIdx.x / kWave) * 4 + (lane >> 4);
+    if ((row & ~int64_t(3)) >= rows) return;  // whole wave past the end
+    const int64_t rr = row < rows ? row : rows - 1;
+    const bool live = valid[rr] != 0;
+    const int64_t t = targets[rr];
+    const float* z = logits + rr * V;
+    float v[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t j0 = u * 64 + sub * 4;
+        if constexpr (VEC) {
+            const float4 q = *reinterpret_cast<const float4*>(z + min(j0, V - 4));
+            v[u][0] = q.x; v[u][1] = q.y; v[u][2] = q.z; v[u][3] = q.w;
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) v[u][p] = z[min(j0 + p, V - 1)];
+        }
+    }
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t j0 = u * 64 + sub * 4;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (HAS_BIAS) v[u][p] = v[u][p] + to_f32(bias[min(j0 + p, V - 1)]);
+            if (j0 + p >= V) v[u][p] = -__builtin_inff();
+            m = fmaxf(m, v[u][p]);
+        }
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    // z[target] lives in lane (t % 64) / 4 of the quarter, slot (t / 64, t % 4).
+    float mine = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            if ((t >> 6) == u && (t & 3) == p) mine = v[u][p];
+    const float zt = __shfl(mine, (lane & ~15) | static_cast<int>((t >> 2) & 15), kWave);
+    float sum = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t j0 = u * 64 + sub * 4;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+            if (j0 + p < V) sum = sum + det_expf(v[u][p] - m);
+    }
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
+    if (sub != 0 || row >= rows) return;
+    float s = 0.0f;
+    if (live) {
+        if (t < 0 || t >= V) {
+            s = __builtin_nanf("");
+        } else {
+            const float nll = (det_logf(sum) + m) - zt;
+            s = 1.0f - det_expf(-nll / log_vocab);
+        }
+    }
+    out[row] = from_f32<T>(s);
 }
 
 // d surprise / d logits (surprise_kernel.cu:136-192):
@@ -895,8 +973,19 @@ int launch_rows(const float* logits, const void* bias, const int64_t* targets, c
                                targets, valid, o, rows, V, log_vocab);                                         \
     } while (0)
     if (V <= 256) {
-        if (vec) KOEMI_ROWS_LAUNCH(1, 4, true);
-        else KOEMI_ROWS_LAUNCH(1, 4, false);
+        const dim3 grid(grid_for(rows, kRowWaves * 4));
+#define KOEMI_ROWS16(VEC)                                                                                      \
+    do {                                                                                                       \
+        if (b)                                                                                                 \
+            hipLaunchKernelGGL((surprise_rows16_kernel<T, VEC, true>), grid, block, 0, stream, logits, b, targets, \
+                               valid, o, rows, V, log_vocab);                                                  \
+        else                                                                                                   \
+            hipLaunchKernelGGL((surprise_rows16_kernel<T, VEC, false>), grid, block, 0, stream, logits, b,       \
+                               targets, valid, o, rows, V, log_vocab);                                         \
+    } while (0)
+        if (vec) KOEMI_ROWS16(true);
+        else KOEMI_ROWS16(false);
+#undef KOEMI_ROWS16
     } else if (V <= 1024) {
         if (vec) KOEMI_ROWS_LAUNCH(4, 1, true);
         else KOEMI_ROWS_LAUNCH(4, 1, false);

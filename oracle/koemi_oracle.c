@@ -18,8 +18,10 @@
  *       scores (Cody-Waite + Taylor; log via atanh series), stated step by step
  *   oracle_surprise_rows  model/network.py:677-688 and
  *       think/surprise_kernel.cu:84-134: nll = log(sum exp(z - max)) + max - z_t,
- *       s = 1 - exp(-nll / lnV), invalid -> 0, with the per-lane (chunk,
- *       component) accumulation order and 64-lane pairwise tree of the kernel
+ *       s = 1 - exp(-nll / lnV), invalid -> 0, with the kernel's accumulation
+ *       order: V <= 256, 16 lanes per row (lane l: j = u*64 + l*4 + p in (u, p)
+ *       order) and a 16-lane pairwise tree; longer rows, 64 lanes (lane l:
+ *       j = k*256 + l*4 + p in (k, p) order) and a 64-lane pairwise tree
  *   oracle_quantile  torch.quantile(s, q), linear: rank = q * (n - 1) in
  *       float32, lerp between the two order statistics (torch's lerp form)
  *   oracle_route_learned  model/router.py:46-49 (softmax then topk, ties to the
@@ -175,19 +177,40 @@ void oracle_surprise_rows(const float* logits, const float* bias, const int64_t*
             m = fmaxf(m, zj);
         }
         float lane[64];
-        for (int l = 0; l < 64; ++l) {
-            float acc = 0.0f;
-            for (int64_t k = 0; k < nchunks; ++k)
-                for (int p = 0; p < 4; ++p) {
-                    const int64_t j = k * 256 + (int64_t)l * 4 + p;
-                    if (j < V) {
-                        const float zj = bias ? z[j] + bias[j] : z[j];
-                        acc = acc + oracle_det_expf(zj - m);
+        float sum;
+        if (V <= 256) {
+            /* 16 lanes per row: lane l holds j = u*64 + l*4 + p, summed in (u, p)
+               order, then a 16-lane pairwise tree */
+            for (int l = 0; l < 16; ++l) {
+                float acc = 0.0f;
+                for (int u = 0; u < 4; ++u)
+                    for (int p = 0; p < 4; ++p) {
+                        const int64_t j = (int64_t)u * 64 + (int64_t)l * 4 + p;
+                        if (j < V) {
+                            const float zj = bias ? z[j] + bias[j] : z[j];
+                            acc = acc + oracle_det_expf(zj - m);
+                        }
                     }
-                }
-            lane[l] = acc;
+                lane[l] = acc;
+            }
+            for (int off = 8; off > 0; off >>= 1)
+                for (int l = 0; l < off; ++l) lane[l] = lane[l] + lane[l + off];
+            sum = lane[0];
+        } else {
+            for (int l = 0; l < 64; ++l) {
+                float acc = 0.0f;
+                for (int64_t k = 0; k < nchunks; ++k)
+                    for (int p = 0; p < 4; ++p) {
+                        const int64_t j = k * 256 + (int64_t)l * 4 + p;
+                        if (j < V) {
+                            const float zj = bias ? z[j] + bias[j] : z[j];
+                            acc = acc + oracle_det_expf(zj - m);
+                        }
+                    }
+                lane[l] = acc;
+            }
+            sum = tree64(lane);
         }
-        const float sum = tree64(lane);
         const int64_t t = targets[r];
         if (t < 0 || t >= V) {
             out[r] = NAN;

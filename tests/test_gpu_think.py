@@ -81,7 +81,7 @@ def test_benchmark_reports_synchronized_latency(device):
     assert m.position_count == 14 and m.measured_iterations == 5 and m.latency_milliseconds > 0
 
 
-@pytest.mark.parametrize("vocab", [2, 19, 256, 257, 1000, 1030])
+@pytest.mark.parametrize("vocab", [2, 3, 19, 64, 128, 255, 256, 257, 1000, 1030])
 def test_surprise_rows_bit_identical_to_oracle(device, vocab):
     rng = np.random.default_rng(vocab)
     logits = rng.normal(0, 2, (333, vocab)).astype(np.float32)
