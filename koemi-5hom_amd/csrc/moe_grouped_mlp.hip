@@ -159,7 +159,9 @@ __device__ __forceinline__ uint32_t stage_slot(int r, int g) {
 // Asynchronous 16-byte-per-lane copy global -> LDS (lane l writes M0 + 16 l).
 // Issued through inline assembly so that the compiler does not order every
 // later LDS read after it (it cannot tell the ring stages apart); completion is
-// tracked explicitly with vmcnt. M0 is restored afterwards.
+// tracked explicitly with vmcnt, and ordering against other waves' reads of the
+// stage comes from the barrier (volatile asm is never reordered against other
+// volatile asm). M0 is restored afterwards.
 __device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* src) {
     uint32_t saved;
     asm volatile(
@@ -168,8 +170,7 @@ __device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* sr
         "global_load_lds_dwordx4 %2, off\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds_byte_addr)), "v"(src)
-        : "memory");
+        : "s"(__builtin_amdgcn_readfirstlane(lds_byte_addr)), "v"(src));
 }
 
 // Waits until at most n tiles of this wave's stage copies are outstanding
@@ -200,6 +201,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t slots, int64_t n_tiles,
     int64_t per_xcd) {
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
+    __shared__ float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
 
     const int64_t logical = static_cast<int64_t>(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     const int64_t group = kGroupM * n_tiles;
@@ -277,59 +279,97 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
             bfr[t] = *reinterpret_cast<const bf16x8*>(Bs + stage_slot(b_row[t], kk * 2 + fg));
         }
     };
-    auto multiply = [&](const bf16x8 (&af)[4], const bf16x8 (&bfr)[4]) {
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[nt], af[mt], acc[mt][nt], 0, 0, 0);
+    // Fragment f of a K step, in the order the MFMAs of the step consume them:
+    // A m-tile 0, B n-tiles 0-3, A m-tiles 1-3.
+    auto read_frag = [&](int64_t kt, int kk, int f, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
+        const char* As = lds + (kt % kStages) * kStageBytes;
+        if (f >= 1 && f <= 4)
+            bfr[f - 1] = *reinterpret_cast<const bf16x8*>(As + kOperandBytes + stage_slot(b_row[f - 1], kk * 2 + fg));
+        else {
+            const int t = f == 0 ? 0 : f - 4;
+            af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
+        }
+    };
+    // Copy i of a stage: i < 4 is A chunk i of this wave, i >= 4 B chunk i - 4.
+    auto issue_one = [&](int64_t kt, int stage, int i) {
+        const uint32_t dst = lds0 + stage * kStageBytes + (i >= 4 ? kOperandBytes : 0u) + (wave * 4 + (i & 3)) * 1024;
+        const bf16* src = (i >= 4 ? b_base + b_off[i & 3] : a_base + a_off[i & 3]) + kt * kBK;
+        lds_dma16(dst, src);
+    };
+    auto mfma_one = [&](int j, const bf16x8 (&af)[4], const bf16x8 (&bfr)[4]) {
+        acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j & 3], af[j >> 2], acc[j >> 2][j & 3], 0, 0, 0);
     };
 
-    // K is a multiple of 64, so nk >= 2.
+    // K is a multiple of 64, so nk >= 2. Every iteration issues one stage copy
+    // (past the last tile it repeats the last tile into the stage just
+    // consumed, which is never read again), so exactly one tile is in flight
+    // behind the one waited for at every barrier.
     const int64_t nk = K / kBK;
 #pragma unroll
-    for (int p = 0; p < kStages - 1; ++p)
-        if (p < nk) issue(p, p);
-    wait_tiles_and_sync(min(static_cast<int64_t>(kStages - 2), nk - 1));
+    for (int p = 0; p < kStages - 1; ++p) issue(min(static_cast<int64_t>(p), nk - 1), p);
+    wait_tiles_and_sync(kStages - 2);
     bf16x8 a0[4], b0[4], a1[4], b1[4];
     read_frags(0, 0, a0, b0);
+    // Each MFMA is followed by one other memory instruction (a stage copy or a
+    // fragment read for a later K step), pinned in place by scheduling
+    // barriers, so that the copies and LDS reads issue while the matrix pipe is
+    // busy instead of in a burst that leaves it idle.
     for (int64_t kt = 0; kt < nk; ++kt) {
         // Tile kt + 1 has landed for every wave, and every wave is done with
         // the stage of tile kt - 1, which the next copy overwrites.
-        wait_tiles_and_sync(min(static_cast<int64_t>(kStages - 3), nk - 2 - kt));
-        if (kt + kStages - 1 < nk) issue(kt + kStages - 1, static_cast<int>((kt + kStages - 1) % kStages));
-        read_frags(kt, 1, a1, b1);
-        multiply(a0, b0);
-        if (kt + 1 < nk) read_frags(kt + 1, 0, a0, b0);
-        multiply(a1, b1);
+        wait_tiles_and_sync(kStages - 3);
+        const int64_t kc = min(kt + kStages - 1, nk - 1);
+        const int sc = static_cast<int>((kt + kStages - 1) % kStages);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            mfma_one(j, a0, b0);
+            if (j % 2 == 0) issue_one(kc, sc, j / 2);
+            else read_frag(kt, 1, j / 2, a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        const int64_t kn = min(kt + 1, nk - 1);  // the last iteration re-reads its own stage harmlessly
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            mfma_one(j, a1, b1);
+            if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
-    // Epilogue. Accumulator element v of lane l: row (of the tile) l % 32,
-    // column 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its 32x32 tile. The biases
-    // of the lane's columns are read once, before the row loop.
-    const int col4 = fg * 4;
-    constexpr int kBiasTiles = GLU ? 2 : 4;
-    float b0v[kBiasTiles][16], b1v[GLU ? 2 : 1][16];
-#pragma unroll
-    for (int nt = 0; nt < kBiasTiles; ++nt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t col = (GLU ? n0 + wn * 64 : n0 + wn * 128) + nt * 32 + col4 + (v >> 2) * 8 + (v & 3);
-            const int64_t cc = static_cast<int64_t>(e) * n_out + min(col, n_out - 1);
-            b0v[nt][v] = to_f32(bias0[cc]);
-            if constexpr (GLU) b1v[nt][v] = to_f32(bias1[cc]);
+    // Epilogue through LDS, so that global stores are whole rows: the tile's
+    // biases go to LDS; each wave writes its bias-added (GLU: silu(g) * u)
+    // bf16 outputs into its own LDS region, then reads it back row by row in
+    // 16-byte chunks and stores full 128-byte lines. Accumulator element v of
+    // lane l is row l % 32, column 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its
+    // 32x32 tile. Region rows are kOutCols bf16; the 16-byte chunk c of row r
+    // sits at chunk c ^ (r & kSwz) (conflict-free row reads).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no stage copy may still be writing LDS
+    __syncthreads();                                  // every wave is done reading the stages
+    {
+        float bv;
+        if constexpr (GLU) {
+            const int64_t col = min(n0 + (tid & 127), n_out - 1);
+            bv = to_f32((tid < 128 ? bias0 : bias1)[static_cast<int64_t>(e) * n_out + col]);
+        } else {
+            bv = to_f32(bias0[static_cast<int64_t>(e) * n_out + min(n0 + tid, n_out - 1)]);
         }
+        bias_sh[tid] = bv;
+    }
+    __syncthreads();
+    constexpr int kOutCols = GLU ? 64 : 128;  // columns of a wave's output tile
+    constexpr int kRowBytes = kOutCols * 2;
+    constexpr int kChunks = kRowBytes / 16;   // 16-byte chunks per row
+    constexpr int kSwz = kChunks - 1;
+    char* region = lds + wave * (128 * kRowBytes);
+    const int col_base = GLU ? wn * 64 : wn * 128;  // within the block tile's columns
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-        const int64_t grow = row0 + wm * 128 + mt * 32 + fr;
-        if (grow >= row_end) continue;
-        bf16* crow = C + grow * n_out;
+        const int r = mt * 32 + fr;
 #pragma unroll
-        for (int nt = 0; nt < kBiasTiles; ++nt)
+        for (int nt = 0; nt < (GLU ? 2 : 4); ++nt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int64_t col = (GLU ? n0 + wn * 64 : n0 + wn * 128) + nt * 32 + col4 + j * 8;
-                if (col >= n_out) continue;
+                const int cl = nt * 32 + fg * 4 + j * 8;  // column within the wave tile
                 union {
                     uint2 raw;
                     bf16 e[4];
@@ -337,15 +377,28 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     if constexpr (GLU) {
-                        const float g = acc[mt][nt][j * 4 + q] + b0v[nt][j * 4 + q];
-                        const float u = acc[mt][nt + 2][j * 4 + q] + b1v[nt][j * 4 + q];
+                        const float g = acc[mt][nt][j * 4 + q] + bias_sh[col_base + cl + q];
+                        const float u = acc[mt][nt + 2][j * 4 + q] + bias_sh[128 + col_base + cl + q];
                         o.e[q] = from_f32<bf16>(silu_f(g) * u);
                     } else {
-                        o.e[q] = from_f32<bf16>(acc[mt][nt][j * 4 + q] + b0v[nt][j * 4 + q]);
+                        o.e[q] = from_f32<bf16>(acc[mt][nt][j * 4 + q] + bias_sh[col_base + cl + q]);
                     }
                 }
-                *reinterpret_cast<uint2*>(crow + col) = o.raw;
+                const int chunk = (cl >> 3) ^ (r & kSwz);
+                *reinterpret_cast<uint2*>(region + r * kRowBytes + chunk * 16 + (cl & 4) * 2) = o.raw;
             }
+    }
+    // Row-contiguous read-back (the wave's own region: LDS operations of a wave
+    // complete in order) and full-line stores.
+    const int64_t out_col0 = n0 + col_base;
+#pragma unroll
+    for (int it = 0; it < 128 * kChunks / kWave; ++it) {
+        const int idx = it * kWave + lane;
+        const int r = idx / kChunks, c = idx % kChunks;
+        const uint4 v = *reinterpret_cast<const uint4*>(region + r * kRowBytes + ((c ^ (r & kSwz)) * 16));
+        const int64_t grow = row0 + wm * 128 + r;
+        const int64_t col = out_col0 + c * 8;
+        if (grow < row_end && col < n_out) *reinterpret_cast<uint4*>(C + grow * n_out + col) = v;
     }
 }
 
@@ -493,7 +546,8 @@ extern "C" int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* 
     const bool aligned = reinterpret_cast<uintptr_t>(sorted_context) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(gate_weights) % 16 == 0 &&
                          reinterpret_cast<uintptr_t>(value_weights) % 16 == 0 &&
-                         reinterpret_cast<uintptr_t>(output_weights) % 16 == 0;
+                         reinterpret_cast<uintptr_t>(output_weights) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(output) % 16 == 0;
     if (mfma_shape(width, hidden, dtype) && !aligned)
         return fail(KOEMI_ERR_INVALID, "grouped MLP bf16 operands must be 16-byte aligned");
     if (mfma_shape(width, hidden, dtype))
