@@ -162,15 +162,24 @@ __device__ __forceinline__ uint32_t stage_slot(int r, int g) {
 // tracked explicitly with vmcnt, and ordering against other waves' reads of the
 // stage comes from the barrier (volatile asm is never reordered against other
 // volatile asm). M0 is restored afterwards.
-__device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* src) {
+// The source is a wave-uniform 64-bit base (SGPRs) plus a per-lane 32-bit byte
+// offset, so issuing a copy costs no vector instructions.
+__device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* base, uint32_t byte_off) {
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
         "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %2, off\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
-        : "s"(__builtin_amdgcn_readfirstlane(lds_byte_addr)), "v"(src));
+        : "s"(lds_byte_addr), "v"(byte_off), "s"(base));
+}
+
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t u = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Waits until at most n tiles of this wave's stage copies are outstanding
@@ -229,25 +238,28 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     // (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves 0-1
     // copy gate rows, waves 2-3 value rows.
     const bf16* a_base = A + row0 * K;
-    const bf16* b_base = ((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K;
+    const bf16* b_base = static_cast<const bf16*>(
+        uniform_ptr(((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K));
     const int a_rows = static_cast<int>(row_end - row0);
-    int a_off[4], b_off[4];
+    uint32_t a_off[4], b_off[4];  // byte offsets (the entry point bounds them below 2^32)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = (wave * 4 + i) * 16 + (lane >> 2);
         const int g = (lane & 3) ^ slot_swizzle(r);
-        a_off[i] = min(r, a_rows - 1) * static_cast<int>(K) + g * 8;
+        a_off[i] = (static_cast<uint32_t>(min(r, a_rows - 1)) * static_cast<uint32_t>(K) + g * 8) * 2u;
         const int64_t n = GLU ? min(n0 + (r & 127), n_out - 1) : min(n0 + r, n_out - 1);
-        b_off[i] = static_cast<int>(n) * static_cast<int>(K) + g * 8;
+        b_off[i] = (static_cast<uint32_t>(n) * static_cast<uint32_t>(K) + g * 8) * 2u;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * 4 * 1024);
     auto issue = [&](int64_t kt, int stage) {
-        const uint32_t a_dst = lds0 + stage * kStageBytes + wave * 4 * 1024;
-        const int64_t k0 = kt * kBK;
+        const uint32_t a_dst = wave_lds + stage * kStageBytes;
+        const bf16* ak = a_base + kt * kBK;
+        const bf16* bk = b_base + kt * kBK;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            lds_dma16(a_dst + i * 1024, a_base + a_off[i] + k0);
-            lds_dma16(a_dst + kOperandBytes + i * 1024, b_base + b_off[i] + k0);
+            lds_dma16(a_dst + i * 1024, ak, a_off[i]);
+            lds_dma16(a_dst + kOperandBytes + i * 1024, bk, b_off[i]);
         }
     };
 
@@ -292,9 +304,8 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     };
     // Copy i of a stage: i < 4 is A chunk i of this wave, i >= 4 B chunk i - 4.
     auto issue_one = [&](int64_t kt, int stage, int i) {
-        const uint32_t dst = lds0 + stage * kStageBytes + (i >= 4 ? kOperandBytes : 0u) + (wave * 4 + (i & 3)) * 1024;
-        const bf16* src = (i >= 4 ? b_base + b_off[i & 3] : a_base + a_off[i & 3]) + kt * kBK;
-        lds_dma16(dst, src);
+        const uint32_t dst = wave_lds + stage * kStageBytes + (i >= 4 ? kOperandBytes : 0u) + (i & 3) * 1024;
+        lds_dma16(dst, (i >= 4 ? b_base : a_base) + kt * kBK, i >= 4 ? b_off[i & 3] : a_off[i & 3]);
     };
     auto mfma_one = [&](int j, const bf16x8 (&af)[4], const bf16x8 (&bfr)[4]) {
         acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j & 3], af[j >> 2], acc[j >> 2][j & 3], 0, 0, 0);
@@ -484,7 +495,7 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
     int64_t* slot_end = reinterpret_cast<int64_t*>(base + ws.slot_end_off);
     if (ws.max_slots > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-    if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
+    if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL)  // byte offsets < 2^32 return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
     if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
                                              static_cast<long long>(kMaxScheduleExperts));
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
