@@ -70,6 +70,33 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
     return l == 0 ? 0ull : (~0ull >> (64 - l));
 }
 
+// Exclusive prefix sum of one value per thread over a workgroup of THREADS
+// threads (a multiple of 64): a wave-level shuffle scan, the wave totals
+// scanned by every thread from LDS, two barriers. `wave_tot` is LDS scratch of
+// THREADS / 64 entries. Also returns the workgroup total.
+template <int THREADS, typename V>
+__device__ __forceinline__ V block_exclusive_scan(V v, V* wave_tot, V& total) {
+    const int lane = lane_id(), w = static_cast<int>(threadIdx.x) / kWave;
+    V incl = v;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const V up = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += up;
+    }
+    if (lane == kWave - 1) wave_tot[w] = incl;
+    __syncthreads();
+    V before = 0, all = 0;
+#pragma unroll
+    for (int i = 0; i < THREADS / kWave; ++i) {
+        const V t = wave_tot[i];
+        if (i < w) before += t;
+        all += t;
+    }
+    __syncthreads();
+    total = all;
+    return before + incl - v;
+}
+
 // Number of blocks for `items` work items of `per_block` each, clamped to a grid size
 // the runtime accepts.
 inline unsigned grid_for(int64_t items, int64_t per_block) {

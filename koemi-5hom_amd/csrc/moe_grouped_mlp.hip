@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
     const int64_t* __restrict__ offsets, int64_t E, int64_t pairs, int64_t max_slots,
     int32_t* __restrict__ slot_expert, int64_t* __restrict__ slot_row, int64_t* __restrict__ slot_end) {
     extern __shared__ int32_t first_tile[];  // E + 1 entries
-    __shared__ int32_t span_sum[kSchedThreads];
+    __shared__ int32_t wave_tot[kSchedThreads / kWave];
     const int tid = threadIdx.x;
     const int64_t n = E + 1;
     for (int64_t e = tid; e < E; e += kSchedThreads) {
@@ -110,18 +110,8 @@ __global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
     const int64_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
     int32_t sum = 0;
     for (int64_t e = b0; e < b1; ++e) sum += first_tile[e];
-    span_sum[tid] = sum;
-    __syncthreads();
-    if (tid == 0) {
-        int32_t run = 0;
-        for (int i = 0; i < kSchedThreads; ++i) {
-            const int32_t v = span_sum[i];
-            span_sum[i] = run;
-            run += v;
-        }
-    }
-    __syncthreads();
-    int32_t run = span_sum[tid];
+    int32_t total_tiles;
+    int32_t run = block_exclusive_scan<kSchedThreads>(sum, wave_tot, total_tiles);
     for (int64_t e = b0; e < b1; ++e) {
         const int32_t v = first_tile[e];
         first_tile[e] = run;

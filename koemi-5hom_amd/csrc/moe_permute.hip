@@ -10,7 +10,8 @@
 //                histogram in LDS (counts are order-independent);
 //   2. scan    : one workgroup turns the [chunks, E+1] counts into
 //                segment_offsets and the first destination of every
-//                (chunk, expert) — chunk order then pair order is stability;
+//                (chunk, expert) — chunk order then pair order is stability
+//                (the table is staged in LDS when it fits);
 //   3. scatter : each chunk walks its pairs in order, 64 at a time; lanes with
 //                the same key are grouped with ballots, ranked by popcount of
 //                the lower lanes, and advance an LDS cursor per key. Writes
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __r
                                                                     int64_t* __restrict__ offsets, int64_t chunks,
                                                                     int64_t E) {
     extern __shared__ int64_t key_total[];  // E+1 entries
-    __shared__ int64_t span_sum[kScanThreads];
+    __shared__ int64_t wave_tot[kScanThreads / kWave];
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     constexpr int kWaves = kScanThreads / kWave;
     const int64_t n = E + 1;
@@ -125,18 +126,8 @@ __global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __r
     const int64_t b0 = min(n, tid * per), b1 = min(n, b0 + per);
     int64_t s = 0;
     for (int64_t e = b0; e < b1; ++e) s += key_total[e];
-    span_sum[tid] = s;
-    __syncthreads();
-    if (tid == 0) {
-        int64_t run = 0;
-        for (int i = 0; i < kScanThreads; ++i) {
-            const int64_t v = span_sum[i];
-            span_sum[i] = run;
-            run += v;
-        }
-    }
-    __syncthreads();
-    int64_t run = span_sum[tid];
+    int64_t total;
+    int64_t run = block_exclusive_scan<kScanThreads>(s, wave_tot, total);
     for (int64_t e = b0; e < b1; ++e) {
         const int64_t v = key_total[e];
         key_total[e] = run;
@@ -176,6 +167,74 @@ __global__ __launch_bounds__(kScanThreads) void permute_scan_kernel(int32_t* __r
             base += __shfl(incl, kWave - 1, kWave);
         }
     }
+}
+
+// The same scan with the whole [chunks, E+1] count table staged in LDS (when it
+// fits and E + 1 <= 64): one coalesced read; per key, each lane sums a run of
+// consecutive chunks and one 32-bit wave scan gives every lane's prefix (kept
+// in LDS); the key offsets are scanned; each lane then writes the first
+// destinations of its chunks; one coalesced write.
+constexpr int kScanLdsInts = 12288;  // 48 KiB of counts
+constexpr int kScanLdsKeys = 64;
+
+__global__ __launch_bounds__(kScanThreads) void permute_scan_lds_kernel(int32_t* __restrict__ counts,
+                                                                        int64_t* __restrict__ offsets, int chunks,
+                                                                        int E) {
+    __shared__ int32_t table[kScanLdsInts];
+    __shared__ int32_t lane_prefix[kScanLdsKeys][kWave];
+    __shared__ int32_t key_total[kScanLdsKeys];
+    __shared__ int32_t wave_tot[kScanThreads / kWave];
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    constexpr int kWaves = kScanThreads / kWave;
+    const int n = E + 1;
+    const int total_ints = chunks * n;
+    constexpr int kPer = kScanLdsInts / kScanThreads;
+    {
+        int32_t v[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {  // all loads in flight together, clamped
+            const int i = j * kScanThreads + tid;
+            v[j] = counts[i < total_ints ? i : total_ints - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int i = j * kScanThreads + tid;
+            if (i < total_ints) table[i] = v[j];
+        }
+    }
+    __syncthreads();
+    // Lane l of a key's wave owns chunks [l * run, (l + 1) * run).
+    const int run = (chunks + kWave - 1) / kWave;
+    const int c0 = lane * run, c1 = min(chunks, c0 + run);
+    for (int key = wave; key < n; key += kWaves) {
+        int32_t local = 0;
+        for (int c = c0; c < c1; ++c) local += table[c * n + key];
+        int32_t incl = local;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int32_t up = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += up;
+        }
+        lane_prefix[key][lane] = incl - local;
+        if (lane == kWave - 1) key_total[key] = incl;
+    }
+    __syncthreads();
+    int32_t total;
+    const int32_t excl = block_exclusive_scan<kScanThreads>(tid < n ? key_total[tid] : 0, wave_tot, total);
+    if (tid < n) offsets[tid] = excl;
+    __syncthreads();  // key_total is rewritten below
+    if (tid < n) key_total[tid] = excl;
+    __syncthreads();
+    for (int key = wave; key < n; key += kWaves) {
+        int32_t pos = key_total[key] + lane_prefix[key][lane];
+        for (int c = c0; c < c1; ++c) {
+            const int32_t v = table[c * n + key];
+            table[c * n + key] = pos;
+            pos += v;
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < total_ints; i += kScanThreads) counts[i] = table[i];
 }
 
 template <typename I>
@@ -271,8 +330,12 @@ int run_index_phase(const void* assignments, const uint8_t* valid, const float* 
                        valid, counts, pairs, k, E);
     int st = check_launch("koemi_moe_permute(count)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(kScanThreads), static_cast<size_t>(E + 1) * sizeof(int64_t), s,
-                       counts, offsets, chunks, E);
+    if (chunks * (E + 1) <= kScanLdsInts && E + 1 <= kScanLdsKeys)
+        hipLaunchKernelGGL(permute_scan_lds_kernel, dim3(1), dim3(kScanThreads), 0, s, counts, offsets,
+                           static_cast<int>(chunks), static_cast<int>(E));
+    else
+        hipLaunchKernelGGL(permute_scan_kernel, dim3(1), dim3(kScanThreads), static_cast<size_t>(E + 1) * sizeof(int64_t),
+                           s, counts, offsets, chunks, E);
     st = check_launch("koemi_moe_permute(scan)");
     if (st != KOEMI_OK) return st;
     hipLaunchKernelGGL(permute_scatter_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
