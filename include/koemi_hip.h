@@ -195,6 +195,22 @@ int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* sorted_expe
                           int64_t hidden, int64_t expert_count, int dtype, void* workspace,
                           size_t workspace_bytes, koemi_stream_t stream);
 
+/* Salient-memory ring update, LocalKeyValueMemory.salient_tail of
+ * model/memory.py:431-455. Per batch row, the carried entries [S] followed by
+ * the window's entries [L] (keys/values [*, D] of `dtype`, validity = carried
+ * valid flags then the admission mask). When S + L <= capacity the outputs are
+ * the concatenation ([B, S + L, D], flags unchanged). Otherwise the outputs
+ * are [B, capacity, D]: the latest min(#valid, capacity) valid entries in time
+ * order, and — when fewer than capacity are valid — the latest invalid entries
+ * as filler, all in ascending time order, with the keys and values of invalid
+ * slots zeroed. (The reference takes torch.topk over ranks valid ? t : -1;
+ * which tied invalid filler it picks is unspecified, so this rule fixes it.)
+ * capacity <= 4096. */
+int koemi_salient_tail(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                       const void* keys, const void* values, const uint8_t* admission, void* out_keys,
+                       void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
+                       int64_t width, int64_t capacity, int dtype, koemi_stream_t stream);
+
 /* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
  * without atomics: combined[t] = sum over the valid sorted pairs i of token t,
  * in ascending i, of y_i * w_i in fp32, w_i = pair_weights[i] (sorted order)

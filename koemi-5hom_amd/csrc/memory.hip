@@ -1,0 +1,130 @@
+// Salient-memory ring update for gfx950.
+//
+// Reference: model/memory.py:431-455 (LocalKeyValueMemory.salient_tail): the
+// carried ring entries followed by the window's entries, ranked by
+// (valid ? temporal index : -1), the top `capacity` kept in ascending time
+// order, invalid slots zeroed.
+//
+// One workgroup per batch row. Every position i of the N = S + L entries needs
+// the number of valid and of invalid entries after it; a block-wide prefix of
+// the per-thread valid counts gives both. With m = min(#valid, capacity) a
+// valid entry is kept when fewer than m valid entries follow it, an invalid one
+// when fewer than capacity - m invalid entries follow it (the latest invalid
+// entries are the filler), and its output slot is capacity - 1 minus the number
+// of kept entries after it. The slot -> entry map is built in LDS, then the
+// workgroup copies the kept rows (zero rows for invalid slots).
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+constexpr int kTailThreads = 256;
+constexpr int64_t kMaxCapacity = 4096;
+
+template <typename T>
+__global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
+    const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid, const T* __restrict__ k,
+    const T* __restrict__ v, const uint8_t* __restrict__ adm, T* __restrict__ ok, T* __restrict__ ov,
+    uint8_t* __restrict__ ovalid, int64_t S, int64_t L, int64_t D, int64_t C) {
+    __shared__ int32_t slot_entry[kMaxCapacity];
+    __shared__ uint8_t slot_valid[kMaxCapacity];
+    __shared__ int64_t wave_tot[kTailThreads / kWave];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t N = S + L;
+    const bool concat = N <= C;
+    const int64_t slots = concat ? N : C;
+    auto valid_at = [&](int64_t i) -> bool { return i < S ? cvalid[b * S + i] != 0 : adm[b * L + (i - S)] != 0; };
+    if (concat) {
+        for (int64_t i = tid; i < N; i += kTailThreads) {
+            slot_entry[i] = static_cast<int32_t>(i);
+            slot_valid[i] = valid_at(i) ? 1 : 0;
+        }
+    } else {
+        // Contiguous span of positions per thread.
+        const int64_t per = (N + kTailThreads - 1) / kTailThreads;
+        const int64_t p0 = min(N, tid * per), p1 = min(N, p0 + per);
+        int64_t cnt = 0;
+        for (int64_t i = p0; i < p1; ++i) cnt += valid_at(i) ? 1 : 0;
+        int64_t total_valid;
+        int64_t before = block_exclusive_scan<kTailThreads>(cnt, wave_tot, total_valid);  // valid in [0, p0)
+        const int64_t m = min(total_valid, C);
+        const int64_t total_invalid = N - total_valid;
+        for (int64_t i = p0; i < p1; ++i) {
+            const bool val = valid_at(i);
+            const int64_t valid_after = total_valid - before - (val ? 1 : 0);
+            const int64_t invalid_after = total_invalid - (i - before) - (val ? 0 : 1);
+            const bool keep = val ? valid_after < m : invalid_after < C - m;
+            if (keep) {
+                const int64_t slot = C - 1 - (min(valid_after, m) + min(invalid_after, C - m));
+                slot_entry[slot] = static_cast<int32_t>(i);
+                slot_valid[slot] = val ? 1 : 0;
+            }
+            if (val) ++before;
+        }
+    }
+    __syncthreads();
+    for (int64_t s = tid; s < slots; s += kTailThreads) ovalid[b * slots + s] = slot_valid[s];
+    // Copy the kept rows; invalid slots are zero unless the outputs are the plain concatenation.
+    const int64_t elems = slots * D;
+    for (int64_t x = tid; x < elems; x += kTailThreads) {
+        const int64_t s = x / D, d = x - s * D;
+        const int64_t i = slot_entry[s];
+        const bool zero = !concat && !slot_valid[s];
+        T kk, vv;
+        if (i < S) {
+            kk = ck[(b * S + i) * D + d];
+            vv = cv[(b * S + i) * D + d];
+        } else {
+            kk = k[(b * L + (i - S)) * D + d];
+            vv = v[(b * L + (i - S)) * D + d];
+        }
+        ok[(b * slots + s) * D + d] = zero ? static_cast<T>(0.0f) : kk;
+        ov[(b * slots + s) * D + d] = zero ? static_cast<T>(0.0f) : vv;
+    }
+}
+
+template <typename T>
+int launch_tail(const void* ck, const void* cv, const uint8_t* cvalid, const void* k, const void* v, const uint8_t* adm,
+                void* ok, void* ov, uint8_t* ovalid, int64_t B, int64_t S, int64_t L, int64_t D, int64_t C,
+                hipStream_t s) {
+    hipLaunchKernelGGL(salient_tail_kernel<T>, dim3(static_cast<unsigned>(B)), dim3(kTailThreads), 0, s,
+                       static_cast<const T*>(ck), static_cast<const T*>(cv), cvalid, static_cast<const T*>(k),
+                       static_cast<const T*>(v), adm, static_cast<T*>(ok), static_cast<T*>(ov), ovalid, S, L, D, C);
+    return check_launch("koemi_salient_tail");
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_salient_tail(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                                  const void* keys, const void* values, const uint8_t* admission, void* out_keys,
+                                  void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
+                                  int64_t width, int64_t capacity, int dtype, koemi_stream_t stream) {
+    if (batch < 0 || carried < 0 || length < 0 || width < 1)
+        return fail(KOEMI_ERR_INVALID, "salient_tail sizes must be non-negative with a positive width");
+    if (capacity < 1 || capacity > kMaxCapacity)
+        return fail(KOEMI_ERR_UNSUPPORTED, "salient_tail capacity must be in [1, %lld]", static_cast<long long>(kMaxCapacity));
+    if (batch > 0x7fffffffLL || carried + length > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "salient_tail: too many rows or entries");
+    if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "salient_tail does not support dtype %s", dtype_name(dtype));
+    const int64_t slots = carried + length <= capacity ? carried + length : capacity;
+    if (batch == 0 || slots == 0) return KOEMI_OK;
+    if ((carried > 0 && (!carried_keys || !carried_values || !carried_valid)) ||
+        (length > 0 && (!keys || !values || !admission)) || !out_keys || !out_values || !out_valid)
+        return fail(KOEMI_ERR_INVALID, "salient_tail received a null pointer");
+    hipStream_t s = as_stream(stream);
+    switch (dtype) {
+        case KOEMI_F32:
+            return launch_tail<float>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
+                                      out_values, out_valid, batch, carried, length, width, capacity, s);
+        case KOEMI_F16:
+            return launch_tail<f16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
+                                    out_values, out_valid, batch, carried, length, width, capacity, s);
+        default:
+            return launch_tail<bf16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
+                                     out_values, out_valid, batch, carried, length, width, capacity, s);
+    }
+}

@@ -33,6 +33,7 @@ SOURCES = (
     "moe_permute.hip",
     "moe_grouped_mlp.hip",
     "moe_combine.hip",
+    "memory.hip",
 )
 
 ARCH = "gfx950"

@@ -77,6 +77,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_moe_route_learned": (c_int, (_P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_check_assignments": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_expert_counts": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
+    "koemi_salient_tail": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P),
+    ),
     "koemi_moe_permute_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_moe_permute": (
         c_int,

@@ -1,0 +1,109 @@
+"""Salient (exact-recall) memory ring update on the GPU.
+
+Front for ``LocalKeyValueMemory.salient_tail`` (reference model/memory.py:431-455):
+the carried ring entries followed by the window's entries, the latest
+``capacity`` admitted ones kept in time order, invalid slots zeroed. Runs the
+HIP kernel ``koemi_salient_tail``; there is no torch fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from koemi_amd import _native
+from koemi_amd.think import CudaThinkUnavailableError, CudaThinkValidationError
+
+__all__ = ["salient_tail"]
+
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+_MAX_CAPACITY = 4096
+
+
+def salient_tail(
+    carried_keys: Tensor,
+    carried_values: Tensor,
+    carried_valid: Tensor,
+    keys: Tensor,
+    values: Tensor,
+    admission_mask: Tensor,
+    capacity: int,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Ring update of the salient memory (reference model/memory.py:431-455).
+
+    ``carried_*``: ``[B, S, D]``, ``[B, S, D]``, ``[B, S]`` bool; window
+    ``keys``/``values`` ``[B, L, D]`` and ``admission_mask`` ``[B, L]`` bool.
+    Returns ``(keys, values, valid)`` of ``[B, min(S + L, capacity), ...]``.
+    When ``S + L <= capacity`` they are the concatenations unchanged. Otherwise
+    they hold the latest valid entries (and, when fewer than ``capacity`` are
+    valid, the latest invalid ones as filler) in ascending time order, with the
+    keys and values of invalid slots zeroed. The reference ranks entries with
+    ``torch.topk`` over ``valid ? t : -1``, whose choice among tied invalid
+    entries is unspecified; this front fixes it to the latest ones.
+    """
+
+    tensors = {
+        "carried_keys": carried_keys,
+        "carried_values": carried_values,
+        "carried_valid": carried_valid,
+        "keys": keys,
+        "values": values,
+        "admission_mask": admission_mask,
+    }
+    for name, tensor in tensors.items():
+        if not isinstance(tensor, Tensor):
+            raise CudaThinkValidationError(f"{name} must be a torch.Tensor")
+        if tensor.device.type != "cuda":
+            raise CudaThinkValidationError(f"{name} must be on CUDA")
+    if len({t.device for t in tensors.values()}) != 1:
+        raise CudaThinkValidationError("salient_tail tensors must be on the same CUDA device")
+    if isinstance(capacity, bool) or not isinstance(capacity, int) or capacity < 1:
+        raise CudaThinkValidationError("capacity must be a positive integer")
+    if capacity > _MAX_CAPACITY:
+        raise CudaThinkValidationError(f"capacity must not exceed {_MAX_CAPACITY}")
+    if keys.ndim != 3 or values.shape != keys.shape:
+        raise CudaThinkValidationError("keys and values must have the same shape [batch, length, width]")
+    batch, length, width = keys.shape
+    if carried_keys.ndim != 3 or carried_values.shape != carried_keys.shape:
+        raise CudaThinkValidationError("carried keys and values must have the same shape [batch, carried, width]")
+    if carried_keys.shape[0] != batch or carried_keys.shape[2] != width:
+        raise CudaThinkValidationError("carried entries must match the window's batch and width")
+    carried = carried_keys.shape[1]
+    if carried_valid.shape != (batch, carried) or admission_mask.shape != (batch, length):
+        raise CudaThinkValidationError("carried_valid and admission_mask must be [batch, carried] and [batch, length]")
+    if carried_valid.dtype != torch.bool or admission_mask.dtype != torch.bool:
+        raise CudaThinkValidationError("carried_valid and admission_mask must be torch.bool")
+    if keys.dtype not in _SUPPORTED_DTYPES:
+        raise CudaThinkValidationError("keys must be float32, float16 or bfloat16")
+    if any(t.dtype != keys.dtype for t in (values, carried_keys, carried_values)):
+        raise CudaThinkValidationError("keys, values and the carried entries must share a dtype")
+    if width < 1:
+        raise CudaThinkValidationError("width must be positive")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise CudaThinkUnavailableError(str(error)) from error
+
+    device = keys.device
+    slots = min(carried + length, capacity)
+    out_keys = torch.empty((batch, slots, width), device=device, dtype=keys.dtype)
+    out_values = torch.empty_like(out_keys)
+    out_valid = torch.empty((batch, slots), device=device, dtype=torch.bool)
+    if batch == 0 or slots == 0:
+        return out_keys, out_values, out_valid
+    contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, admission_mask)]
+    _native.call(
+        "koemi_salient_tail",
+        *(_native.ptr(t) if t.numel() else None for t in contiguous),
+        _native.ptr(out_keys),
+        _native.ptr(out_values),
+        _native.ptr(out_valid),
+        batch,
+        carried,
+        length,
+        width,
+        capacity,
+        _native.dtype_code(keys.dtype),
+        _native.stream_of(device),
+    )
+    return out_keys, out_values, out_valid

@@ -223,6 +223,44 @@ def admission(scores: np.ndarray, valid: np.ndarray, *, threshold: float | None 
     return np.asarray(valid, dtype=bool) & (s > np.float32(tau)), tau
 
 
+def salient_tail(
+    carried_keys: np.ndarray,
+    carried_values: np.ndarray,
+    carried_valid: np.ndarray,
+    keys: np.ndarray,
+    values: np.ndarray,
+    admission: np.ndarray,
+    capacity: int,
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Salient ring update (model/memory.py:431-455): concatenate carried and new
+    entries; if they fit, return them unchanged; else keep the entries ranked
+    highest by (valid ? t : -1), in ascending t, zeroing invalid slots. The
+    reference's torch.topk leaves the choice among tied invalid entries
+    unspecified; this restatement (and the kernel) takes the latest ones."""
+
+    all_k = np.concatenate([carried_keys, keys], axis=1)
+    all_v = np.concatenate([carried_values, values], axis=1)
+    all_ok = np.concatenate([carried_valid, admission], axis=1).astype(bool)
+    n = all_k.shape[1]
+    if n <= capacity:
+        return all_k, all_v, all_ok
+    out_k = np.zeros((all_k.shape[0], capacity) + all_k.shape[2:], dtype=all_k.dtype)
+    out_v = np.zeros_like(out_k)
+    out_ok = np.zeros((all_k.shape[0], capacity), dtype=bool)
+    for b in range(all_k.shape[0]):
+        valid_idx = np.flatnonzero(all_ok[b])
+        invalid_idx = np.flatnonzero(~all_ok[b])
+        m = min(valid_idx.size, capacity)
+        chosen = list(valid_idx[valid_idx.size - m:]) + list(invalid_idx[invalid_idx.size - (capacity - m):]
+                                                            if capacity > m else [])
+        sel = np.sort(np.asarray(chosen, dtype=np.int64))
+        ok = all_ok[b, sel]
+        out_ok[b] = ok
+        out_k[b] = np.where(ok[:, None], all_k[b, sel], 0)
+        out_v[b] = np.where(ok[:, None], all_v[b, sel], 0)
+    return out_k, out_v, out_ok
+
+
 # ------------------------------------------------------------------- MoE
 
 TOKEN_HASH_FACTOR = 1_000_003          # experts.py:12

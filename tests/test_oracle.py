@@ -17,6 +17,10 @@ wrong sign, swapped operand, wrong rounding order) fails at least one:
   (network.py:677-688) within a few ulp; uniform logits -> 1 - 1/e; invalid
   -> exactly 0; bias[65] = 12 monotonic known case (test_network.py:61-70).
 * quantile: torch.quantile (linear) on many sizes / q; NaN propagation.
+* salient_tail: the ring KAT (test_salience_memory.py:13-30); the reference's
+  own torch expression (topk over valid ? t : -1, sorted) on every case where
+  it is unambiguous (at least `capacity` valid entries), and its valid slots
+  on every case; fit-in-capacity returns the concatenation unchanged.
 * hash route: the network KAT (test_network.py:95-101) and the dispatch
   properties of test_dispatch.py:50-108; uint32-vs-int64 closed form (E power
   of two agrees, E = 6 does not).
@@ -250,6 +254,57 @@ def test_admission_is_strictly_above_the_threshold():
     s = np.array([0.7, 0.75, 0.8, 0.9], np.float32)
     mask, _ = oracle.admission(s, np.array([True, True, True, False]), threshold=0.75)
     assert mask.tolist() == [False, False, True, False]
+
+
+def _torch_salient_tail(ck, cv, cvalid, k, v, adm, capacity):
+    """The reference expression of model/memory.py:431-455, in torch on the CPU."""
+    all_keys = torch.cat((ck, k), dim=1)
+    all_values = torch.cat((cv, v), dim=1)
+    all_valid = torch.cat((cvalid, adm), dim=1)
+    if all_keys.shape[1] <= capacity:
+        return all_keys, all_values, all_valid
+    t = torch.arange(all_keys.shape[1]).unsqueeze(0).expand_as(all_valid)
+    ranked = torch.where(all_valid, t, torch.full_like(t, -1))
+    sel = ranked.topk(capacity, dim=1, largest=True).indices.sort(dim=1).values
+    ok = all_valid.gather(1, sel)
+    idx = sel.unsqueeze(-1).expand(-1, -1, all_keys.shape[-1])
+    sk = torch.where(ok.unsqueeze(-1), all_keys.gather(1, idx), torch.zeros(()))
+    sv = torch.where(ok.unsqueeze(-1), all_values.gather(1, idx), torch.zeros(()))
+    return sk, sv, ok
+
+
+def test_salient_tail_known_answer():
+    kat = GOLDEN["salient_tail_latest"]
+    adm = np.array([kat["admission"]])
+    keys = np.arange(4 * 3, dtype=np.float32).reshape(1, 4, 3)
+    empty = np.zeros((1, 0, 3), np.float32)
+    k, v, ok = oracle.salient_tail(empty, empty, np.zeros((1, 0), bool), keys, keys + 100, adm, kat["capacity"])
+    np.testing.assert_array_equal(k[0], keys[0, kat["kept_positions"]])
+    np.testing.assert_array_equal(v[0], keys[0, kat["kept_positions"]] + 100)
+    assert ok.tolist() == [[True, True]]
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_salient_tail_matches_the_reference_expression(seed):
+    rng = np.random.default_rng(seed)
+    b, s, length, d = 3, int(rng.integers(0, 6)), int(rng.integers(1, 40)), 5
+    capacity = int(rng.integers(1, 20))
+    p = rng.uniform(0.05, 0.95)
+    ck, cv = rng.normal(size=(b, s, d)).astype(np.float32), rng.normal(size=(b, s, d)).astype(np.float32)
+    k, v = rng.normal(size=(b, length, d)).astype(np.float32), rng.normal(size=(b, length, d)).astype(np.float32)
+    cvalid, adm = rng.random((b, s)) < p, rng.random((b, length)) < p
+    got = oracle.salient_tail(ck, cv, cvalid, k, v, adm, capacity)
+    want = _torch_salient_tail(*(torch.from_numpy(x) for x in (ck, cv, cvalid, k, v, adm)), capacity)
+    valid_counts = np.concatenate([cvalid, adm], axis=1).sum(axis=1)
+    for bi in range(b):
+        if s + length <= capacity or valid_counts[bi] >= capacity:  # no tie: the whole output is fixed
+            for g, w in zip(got, want):
+                np.testing.assert_array_equal(g[bi], w[bi].numpy())
+        else:  # ties among invalid filler: the valid slots, in order, are still fixed
+            gv, wv = got[2][bi], want[2][bi].numpy()
+            np.testing.assert_array_equal(got[0][bi][gv], want[0][bi].numpy()[wv])
+            np.testing.assert_array_equal(got[1][bi][gv], want[1][bi].numpy()[wv])
+            assert not got[0][bi][~gv].any() and not got[1][bi][~gv].any()
 
 
 # ------------------------------------------------------------------------ MoE
