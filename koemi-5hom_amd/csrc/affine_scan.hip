@@ -347,8 +347,9 @@ int launch_forward(const void* a, const void* b, const void* h0, void* h, int64_
                           reinterpret_cast<uintptr_t>(b) % (4 * VEC) == 0 &&
                           reinterpret_cast<uintptr_t>(h) % (4 * VEC) == 0 &&
                           reinterpret_cast<uintptr_t>(h0) % (4 * VEC) == 0;
-        if (wide) {
-            const int64_t tiles = (F / VEC + kWave - 1) / kWave;
+        const int64_t tiles = (F / VEC + kWave - 1) / kWave;
+        // Wider column strips halve the workgroup count; keep at least one per CU.
+        if (wide && B * tiles >= 256) {
             const int64_t blocks = B * tiles;
             if (blocks > 0x7fffffff) return fail(KOEMI_ERR_UNSUPPORTED, "affine scan grid too large");
             hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC>),
