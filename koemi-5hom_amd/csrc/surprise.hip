@@ -561,13 +561,14 @@ __device__ uint32_t select_rank(const Keys& keys, uint32_t lo, uint32_t hi, uint
 }
 
 // Keys of ranks t0 and t1 = t0 or t0 + 1 among the keys in [kmin, kmax].
-template <class Keys>
+template <class Keys, int BUCKET_BITS = 12>
 __device__ void select_two_ranks(const Keys& keys, uint32_t kmin, uint32_t kmax, uint32_t t0, uint32_t t1,
                                  SelShared& sh, uint32_t& key0, uint32_t& key1) {
+    constexpr int kBuckets = 1 << BUCKET_BITS;
     const int tid = threadIdx.x;
     const uint32_t span = kmax - kmin;
-    const int shift = span < kSelBuckets ? 0 : 32 - __builtin_clz(span) - 12;
-    bucket_pass(keys, kmin, kmax, shift, 0, t0, t1, sh);
+    const int shift = span < kBuckets ? 0 : 32 - __builtin_clz(span) - BUCKET_BITS;
+    bucket_pass<Keys, kSelThreads, kBuckets>(keys, kmin, kmax, shift, 0, t0, t1, sh);
     const uint32_t b0 = sh.result[0], below0 = sh.result[1], n0 = sh.result[2];
     const uint32_t b1 = sh.result[3], below1 = sh.result[4], n1 = sh.result[5];
     __syncthreads();
@@ -667,6 +668,7 @@ constexpr int kPartMaxGroups = 32;                           // finish: one slot
 static_assert(kPartMaxGroups * kPartScores <= (1 << 22), "32-bit sample index arithmetic");
 constexpr int kSampleBuckets = 1024;
 constexpr int kFinishCand = 8192;                            // candidates gathered in LDS
+constexpr int kRecordWords = 8;  // per workgroup: below, candidates, NaNs, candidate min / max key
 constexpr int64_t kPartitionMin = 8192;                      // smaller inputs: one workgroup
 
 struct PartWorkspace {
@@ -677,7 +679,7 @@ inline PartWorkspace part_workspace(int64_t n) {
     PartWorkspace w;
     w.header_off = 0;
     w.record_off = 256;
-    w.key_off = w.record_off + ((static_cast<size_t>(groups) * 4 * sizeof(uint32_t) + 255) & ~size_t(255));
+    w.key_off = w.record_off + ((static_cast<size_t>(groups) * kRecordWords * sizeof(uint32_t) + 255) & ~size_t(255));
     w.index_off = w.key_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
     w.total = w.index_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
     return w;
@@ -764,7 +766,7 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
     }
 
     // Classify own scores; decided mask bytes are written now.
-    uint32_t below = 0, nan = 0, cand = 0, cand_bits = 0, out = 0;
+    uint32_t below = 0, nan = 0, cand = 0, cand_bits = 0, out = 0, cmin = 0xffffffffu, cmax = 0;
 #pragma unroll
     for (int c = 0; c < kPartPerThread; ++c) {
         if (base + c >= n) continue;
@@ -778,6 +780,8 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
         } else {
             ++cand;
             cand_bits |= 1u << c;
+            cmin = min(cmin, k);
+            cmax = max(cmax, k);
         }
     }
     if constexpr (VEC) {
@@ -800,20 +804,28 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
     for (int off = 32; off > 0; off >>= 1) {
         below_sum += __shfl_xor(below_sum, off, kWave);
         nan_sum += __shfl_xor(nan_sum, off, kWave);
+        cmin = min(cmin, static_cast<uint32_t>(__shfl_xor(cmin, off, kWave)));
+        cmax = max(cmax, static_cast<uint32_t>(__shfl_xor(cmax, off, kWave)));
     }
     if (lane == kWave - 1) sh.wave_tmp[0][w] = incl;
     if (lane == 0) {
         sh.wave_tmp[1][w] = below_sum;
         sh.wave_tmp[2][w] = nan_sum;
+        sh.list[0][w] = cmin;
+        sh.list[1][w] = cmax;
     }
     __syncthreads();
     uint32_t pos = incl - cand, total = 0, below_total = 0, nan_total = 0;
+    cmin = 0xffffffffu;
+    cmax = 0;
 #pragma unroll
     for (int i = 0; i < kPartThreads / kWave; ++i) {
         if (i < w) pos += sh.wave_tmp[0][i];
         total += sh.wave_tmp[0][i];
         below_total += sh.wave_tmp[1][i];
         nan_total += sh.wave_tmp[2][i];
+        cmin = min(cmin, sh.list[0][i]);
+        cmax = max(cmax, sh.list[1][i]);
     }
     uint32_t* keys_out = cand_key + static_cast<int64_t>(blockIdx.x) * kPartCand;
     uint32_t* index_out = cand_index + static_cast<int64_t>(blockIdx.x) * kPartCand;
@@ -829,10 +841,12 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
         }
     }
     if (tid == 0) {
-        uint32_t* rec = records + static_cast<int64_t>(blockIdx.x) * 4;
+        uint32_t* rec = records + static_cast<int64_t>(blockIdx.x) * kRecordWords;
         rec[0] = below_total;
         rec[1] = total;
         rec[2] = nan_total;
+        rec[3] = cmin;
+        rec[4] = cmax;
     }
 }
 
@@ -850,6 +864,7 @@ struct LdsKeys {
     }
 };
 
+template <int GMAX>
 __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
     const float* __restrict__ s, const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm,
     float* __restrict__ tau_out, int64_t n, int64_t k_lo, int64_t k_hi, float weight,
@@ -860,30 +875,37 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
     const int tid = threadIdx.x;
     // One round trip: lane g of every wave loads record g (vector loads, all in
     // flight together), every thread loads entry `tid` of every slot (in bounds
-    // whatever the counts), and the pivots.
+    // whatever the counts), and the pivots. Totals, and the candidates' key
+    // range, come from the records by wave reductions (no barrier).
     const int lane = lane_id();
     const int rg = lane < groups ? lane : groups - 1;
-    uint32_t rec_below = records[rg * 4 + 0];
-    uint32_t rec_cand = records[rg * 4 + 1];
-    uint32_t rec_nan = records[rg * 4 + 2];
-    uint32_t key[kPartMaxGroups], index[kPartMaxGroups];
+    const uint32_t* rec = records + rg * kRecordWords;
+    uint32_t rec_below = rec[0], rec_cand = rec[1], rec_nan = rec[2], rec_min = rec[3], rec_max = rec[4];
+    uint32_t key[GMAX], index[GMAX];
 #pragma unroll
-    for (int g = 0; g < kPartMaxGroups; ++g) {
+    for (int g = 0; g < GMAX; ++g) {
         const int gc = g < groups ? g : groups - 1;
         key[g] = cand_key[static_cast<int64_t>(gc) * kPartCand + tid];
         index[g] = cand_index[static_cast<int64_t>(gc) * kPartCand + tid];
     }
-    if (lane >= groups) rec_below = rec_cand = rec_nan = 0;
+    if (lane >= groups) {
+        rec_below = rec_cand = rec_nan = 0;
+        rec_min = 0xffffffffu;
+        rec_max = 0;
+    }
     uint32_t below = rec_below, cand = rec_cand, bad = (rec_nan != 0 || rec_cand > kPartCand) ? 1u : 0u;
+    uint32_t kmin = rec_min, kmax = rec_max;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         below += __shfl_xor(below, off, kWave);
         cand += __shfl_xor(cand, off, kWave);
         bad |= __shfl_xor(bad, off, kWave);
+        kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(kmin, off, kWave)));
+        kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(kmax, off, kWave)));
     }
-    uint32_t count[kPartMaxGroups];
+    uint32_t count[GMAX];
 #pragma unroll
-    for (int g = 0; g < kPartMaxGroups; ++g) count[g] = __shfl(rec_cand, g, kWave);  // 0 past `groups`
+    for (int g = 0; g < GMAX; ++g) count[g] = __shfl(rec_cand, g, kWave);  // 0 past `groups`
     const uint32_t p_lo = header[0], p_hi = header[1];
     const bool fast = bad == 0 && cand <= kFinishCand && static_cast<int64_t>(below) <= k_lo &&
                       k_hi < static_cast<int64_t>(below) + static_cast<int64_t>(cand);
@@ -892,22 +914,15 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
     if (fast) {
         uint32_t off = 0;
 #pragma unroll
-        for (int g = 0; g < kPartMaxGroups; ++g) {
+        for (int g = 0; g < GMAX; ++g) {
             if (static_cast<uint32_t>(tid) < count[g]) keys[off + tid] = key[g];
             off += count[g];
         }
         __syncthreads();
         LdsKeys lk{keys, cand};
-        uint32_t cnt = 0, kmin = 0xffffffffu, kmax = 0;
-        lk.visit([&](uint32_t k) {
-            ++cnt;
-            kmin = min(kmin, k);
-            kmax = max(kmax, k);
-        });
-        block_count_min_max(cnt, kmin, kmax, sh);
         uint32_t key_lo, key_hi;
-        select_two_ranks(lk, kmin, kmax, static_cast<uint32_t>(k_lo - below), static_cast<uint32_t>(k_hi - below), sh,
-                         key_lo, key_hi);
+        select_two_ranks<LdsKeys, 10>(lk, kmin, kmax, static_cast<uint32_t>(k_lo - below),
+                                      static_cast<uint32_t>(k_hi - below), sh, key_lo, key_hi);
         const float v_lo = key_to_float(key_lo);
         const float v_hi = key_to_float(key_hi);
         tau = weight < 0.5f ? __builtin_fmaf(weight, v_hi - v_lo, v_lo)
@@ -920,7 +935,7 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
         if (decided) {
             // Mask bytes of the candidates (every other byte was decided by the partition).
 #pragma unroll
-            for (int g = 0; g < kPartMaxGroups; ++g) {
+            for (int g = 0; g < GMAX; ++g) {
                 if (static_cast<uint32_t>(tid) < count[g]) {
                     const int64_t i = static_cast<int64_t>(g) * kPartScores + (index[g] & 0x7fffffffu);
                     adm[i] = ((index[g] >> 31) && key_to_float(key[g]) > tau) ? 1 : 0;
@@ -1117,7 +1132,12 @@ extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* va
                            s, surprise, valid_mask, admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
     const int st = check_launch("koemi_admission_quantile(partition)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL(quantile_finish_kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission,
-                       threshold_out, count, k_lo, k_hi, weight, header, records, cand_key, cand_index, groups);
+    auto finish = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission, threshold_out,
+                           count, k_lo, k_hi, weight, header, records, cand_key, cand_index, groups);
+    };
+    if (groups <= 8) finish(quantile_finish_kernel<8>);
+    else if (groups <= 16) finish(quantile_finish_kernel<16>);
+    else finish(quantile_finish_kernel<kPartMaxGroups>);
     return check_launch("koemi_admission_quantile");
 }
