@@ -39,11 +39,9 @@ __host__ __device__ __forceinline__ uint32_t float_to_bits(float f) {
     return c.u;
 }
 
-__device__ __forceinline__ float det_expf(float x) {
+// e^x for -86 <= x <= 88 (the reduction and polynomial of det_expf).
+__device__ __forceinline__ float det_exp_core(float x) {
 #pragma clang fp contract(off)
-    if (x != x) return x;
-    if (x < -86.0f) return 0.0f;
-    if (x > 88.0f) return __builtin_inff();
     const float n = __builtin_rintf(x * kLog2e);
     float r = __builtin_fmaf(-n, kLn2Hi, x);
     r = __builtin_fmaf(-n, kLn2Lo, r);
@@ -58,6 +56,21 @@ __device__ __forceinline__ float det_expf(float x) {
     const int ni = static_cast<int>(n);
     const float scale = bits_to_float(static_cast<uint32_t>(ni + 127) << 23);
     return p * scale;
+}
+
+__device__ __forceinline__ float det_expf(float x) {
+    if (x != x) return x;
+    if (x < -86.0f) return 0.0f;
+    if (x > 88.0f) return __builtin_inff();
+    return det_exp_core(x);
+}
+
+// det_expf for arguments known not to exceed 0 (x - max(x) terms of a
+// softmax, or NaN): the same bits without the overflow test.
+__device__ __forceinline__ float det_expf_nonpos(float x) {
+    if (x != x) return x;
+    if (x < -86.0f) return 0.0f;
+    return det_exp_core(x);
 }
 
 __device__ __forceinline__ float det_logf(float x) {

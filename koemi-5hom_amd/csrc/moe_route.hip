@@ -69,14 +69,14 @@ __global__ void route_learned_kernel(const float* __restrict__ logits, const uin
     float m = -__builtin_inff();
     for (int64_t j = 0; j < E; ++j) m = fmaxf(m, l[j]);
     float sum = 0.0f;
-    for (int64_t j = 0; j < E; ++j) sum = sum + detmath::det_expf(l[j] - m);
+    for (int64_t j = 0; j < E; ++j) sum = sum + detmath::det_expf_nonpos(l[j] - m);
     float prev_p = __builtin_inff();
     int64_t prev_j = -1;
     for (int64_t s = 0; s < k; ++s) {
         int64_t best = -1;
         float best_p = 0.0f;
         for (int64_t j = 0; j < E; ++j) {
-            const float p = detmath::det_expf(l[j] - m) / sum;
+            const float p = detmath::det_expf_nonpos(l[j] - m) / sum;
             const bool after_prev = (p < prev_p) || (p == prev_p && j > prev_j);
             if (after_prev && (best < 0 || p > best_p)) {
                 best = j;

@@ -16,6 +16,8 @@
 #include "common.hpp"
 #include "detmath.hpp"
 
+#include <type_traits>
+
 namespace koemi {
 namespace {
 
@@ -116,7 +118,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
                 const int64_t j0 = static_cast<int64_t>(k) * 256 + lane * 4;
 #pragma unroll
                 for (int p = 0; p < 4; ++p)
-                    if (j0 + p < V) sum[r] = sum[r] + det_expf(v[r][k][p] - m[r]);
+                    if (j0 + p < V) sum[r] = sum[r] + detmath::det_expf_nonpos(v[r][k][p] - m[r]);
             }
         }
     } else {
@@ -134,7 +136,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
             for (int64_t k = 0; k < nchunks; ++k) {
                 const int64_t j0 = k * 256 + lane * 4;
                 for (int p = 0; p < 4; ++p)
-                    if (j0 + p < V) sum[0] = sum[0] + det_expf((z[j0 + p] + load_bias(bias, j0 + p)) - m[0]);
+                    if (j0 + p < V) sum[0] = sum[0] + detmath::det_expf_nonpos((z[j0 + p] + load_bias(bias, j0 + p)) - m[0]);
             }
         }
         const int64_t t = tgt[0];
@@ -168,13 +170,14 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
 // 256 contiguous bytes). The exponentials are summed per lane in (u, p) order,
 // then by a xor butterfly over the 16 lanes (offsets 8, 4, 2, 1); lane 0 of
 // each quarter finishes its row. Every load is issued up front at a clamped
-// in-bounds address.
-template <typename T, bool VEC, bool HAS_BIAS>
+// in-bounds address. FULL: V == 256 (no element is past the end of its row).
+template <typename T, bool VEC, bool HAS_BIAS, bool FULL>
 __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
     const float* __restrict__ logits, const T* __restrict__ bias,
     const int64_t* __restrict__ targets, const uint8_t* __restrict__ valid, T* __restrict__ out,
-    int64_t rows, int64_t V, float log_vocab) {
+    int64_t rows, int64_t v_runtime, float log_vocab) {
 #pragma clang fp contract(off)
+    const int64_t V = FULL ? 256 : v_runtime;
     const int lane = lane_id();
     const int sub = lane & 15;
     const int64_t row = (static_cast<int64_t>(blockIdx.x) * kRowWaves + threadIdx.x / kWave) * 4 + (lane >> 4);
@@ -202,7 +205,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             if (HAS_BIAS) v[u][p] = v[u][p] + to_f32(bias[min(j0 + p, V - 1)]);
-            if (j0 + p >= V) v[u][p] = -__builtin_inff();
+            if (!FULL && j0 + p >= V) v[u][p] = -__builtin_inff();
             m = fmaxf(m, v[u][p]);
         }
     }
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
         const int64_t j0 = u * 64 + sub * 4;
 #pragma unroll
         for (int p = 0; p < 4; ++p)
-            if (j0 + p < V) sum = sum + det_expf(v[u][p] - m);
+            if (FULL || j0 + p < V) sum = sum + detmath::det_expf_nonpos(v[u][p] - m);
     }
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) sum = sum + __shfl_xor(sum, off, kWave);
@@ -270,7 +273,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_backward_kern
     for (int64_t k = 0; k < nchunks; ++k) {
         const int64_t j0 = k * 256 + lane * 4;
         for (int p = 0; p < 4; ++p)
-            if (j0 + p < V) sum = sum + det_expf((z[j0 + p] + load_bias(bias, j0 + p)) - m);
+            if (j0 + p < V) sum = sum + detmath::det_expf_nonpos((z[j0 + p] + load_bias(bias, j0 + p)) - m);
     }
     sum = wave_sum_xor(sum);
     const float zt = z[t] + load_bias(bias, t);
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_backward_kern
         for (int p = 0; p < 4; ++p) {
             const int64_t j = j0 + p;
             if (j < V) {
-                const float prob = det_expf((z[j] + load_bias(bias, j)) - m) / sum;
+                const float prob = detmath::det_expf_nonpos((z[j] + load_bias(bias, j)) - m) / sum;
                 dz[j] = gnll * (prob - (j == t ? 1.0f : 0.0f));
             }
         }
@@ -451,6 +454,7 @@ struct RegisterKeys {
 };
 
 // Scores re-read from memory in every pass (any n).
+template <int THREADS>
 struct MemoryKeys {
     const float* s;
     const uint8_t* valid;
@@ -463,15 +467,15 @@ struct MemoryKeys {
     template <class F>
     __device__ void visit(F f) const {
         int64_t i = threadIdx.x;
-        for (; i + 3 * kSelThreads < n; i += 4 * kSelThreads) {
+        for (; i + 3 * THREADS < n; i += 4 * THREADS) {
             float v[4];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) v[u] = s[i + u * kSelThreads];
+            for (int u = 0; u < 4; ++u) v[u] = s[i + u * THREADS];
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 if (v[u] == v[u]) f(order_key(v[u]));
         }
-        for (; i < n; i += kSelThreads) {
+        for (; i < n; i += THREADS) {
             const float v = s[i];
             if (v == v) f(order_key(v));
         }
@@ -481,7 +485,7 @@ struct MemoryKeys {
         visit([&](uint32_t k) { f(k, true); });
     }
     __device__ void write_mask(uint8_t* __restrict__ adm, int64_t count, float tau) const {
-        for (int64_t i = threadIdx.x; i < count; i += kSelThreads) adm[i] = (valid[i] && s[i] > tau) ? 1 : 0;
+        for (int64_t i = threadIdx.x; i < count; i += THREADS) adm[i] = (valid[i] && s[i] > tau) ? 1 : 0;
     }
 };
 
@@ -542,13 +546,13 @@ __device__ void bucket_pass(const Keys& keys, uint32_t lo, uint32_t hi, int shif
 
 // Key of the element with 0-based rank `target` among the (non-NaN) keys, by
 // repeated bucket refinement.
-template <class Keys>
+template <class Keys, int THREADS = kSelThreads>
 __device__ uint32_t select_rank(const Keys& keys, uint32_t lo, uint32_t hi, uint32_t target, SelShared& sh) {
     uint32_t below = 0;  // keys < lo
     for (int pass = 0; pass < 8 && lo < hi; ++pass) {
         const uint32_t span = hi - lo;
         const int shift = span < kSelBuckets ? 0 : 32 - __builtin_clz(span) - 12;
-        bucket_pass(keys, lo, hi, shift, below, target, target, sh);
+        bucket_pass<Keys, THREADS>(keys, lo, hi, shift, below, target, target, sh);
         const uint32_t b = sh.result[0];
         below = sh.result[1];
         __syncthreads();
@@ -561,20 +565,20 @@ __device__ uint32_t select_rank(const Keys& keys, uint32_t lo, uint32_t hi, uint
 }
 
 // Keys of ranks t0 and t1 = t0 or t0 + 1 among the keys in [kmin, kmax].
-template <class Keys, int BUCKET_BITS = 12>
+template <class Keys, int BUCKET_BITS = 12, int THREADS = kSelThreads>
 __device__ void select_two_ranks(const Keys& keys, uint32_t kmin, uint32_t kmax, uint32_t t0, uint32_t t1,
                                  SelShared& sh, uint32_t& key0, uint32_t& key1) {
     constexpr int kBuckets = 1 << BUCKET_BITS;
     const int tid = threadIdx.x;
     const uint32_t span = kmax - kmin;
     const int shift = span < kBuckets ? 0 : 32 - __builtin_clz(span) - BUCKET_BITS;
-    bucket_pass<Keys, kSelThreads, kBuckets>(keys, kmin, kmax, shift, 0, t0, t1, sh);
+    bucket_pass<Keys, THREADS, kBuckets>(keys, kmin, kmax, shift, 0, t0, t1, sh);
     const uint32_t b0 = sh.result[0], below0 = sh.result[1], n0 = sh.result[2];
     const uint32_t b1 = sh.result[3], below1 = sh.result[4], n1 = sh.result[5];
     __syncthreads();
     if (n0 > kSelList || n1 > kSelList) {  // crowded bucket: refine
-        key0 = select_rank(keys, kmin, kmax, t0, sh);
-        key1 = (t1 == t0) ? key0 : select_rank(keys, kmin, kmax, t1, sh);
+        key0 = select_rank<Keys, THREADS>(keys, kmin, kmax, t0, sh);
+        key1 = (t1 == t0) ? key0 : select_rank<Keys, THREADS>(keys, kmin, kmax, t1, sh);
         return;
     }
     // Gather the candidates of both buckets (list 1 only when they differ).
@@ -587,13 +591,14 @@ __device__ void select_two_ranks(const Keys& keys, uint32_t kmin, uint32_t kmax,
         else if (b == b1) sh.list[1][atomicAdd(&sh.result[7], 1u)] = k;
     });
     __syncthreads();
-    // Threads [0, 512) rank list 0 for t0, threads [512, 1024) the list of t1.
-    const int half = tid / kSelList;
-    const int idx = tid % kSelList;
+    // The first half of the threads ranks list 0 for t0, the second half the
+    // list of t1 (one entry per thread at 1024 threads).
+    constexpr int kHalf = THREADS / 2;
+    const int half = tid / kHalf;
     const uint32_t* list = (half == 1 && b1 != b0) ? sh.list[1] : sh.list[0];
     const uint32_t m = (half == 1 && b1 != b0) ? n1 : n0;
     const uint32_t r = half == 0 ? t0 - below0 : t1 - below1;
-    if (static_cast<uint32_t>(idx) < m) {
+    for (uint32_t idx = tid % kHalf; idx < m; idx += kHalf) {
         const uint32_t x = list[idx];
         uint32_t less = 0, equal = 0;
         for (uint32_t j = 0; j < m; ++j) {
@@ -643,7 +648,7 @@ __global__ __launch_bounds__(kSelThreads) void quantile_admission_kernel(
 // ----------------------------------------------- two-kernel quantile select ---
 // For larger n the per-element work is spread over many workgroups:
 //
-//   partition (grid, 4096 scores per workgroup): every workgroup reads the same
+//   partition (grid, 4 scores per thread): every workgroup reads the same
 //     strided sample of 1024 scores and, from its bucket histogram, the same
 //     two pivot keys p_lo <= p_hi bracketing sample ranks a few standard
 //     deviations either side of the target ranks. Each workgroup then splits
@@ -660,61 +665,97 @@ __global__ __launch_bounds__(kSelThreads) void quantile_admission_kernel(
 //     bytes. If a check fails (a NaN score, a sample far off the data, too
 //     many candidates) it falls back to the exact single-workgroup select over
 //     all scores and rewrites the whole mask.
-constexpr int kPartThreads = 1024;
+//
+// Both kernels run THREADS threads per workgroup: 256 up to 32768 scores (a
+// workgroup of 4 waves finds room on a CU beside other kernels' workgroups,
+// so the select can overlap independent work on another stream), 1024 above.
+// A workgroup partitions 4 * THREADS scores and keeps up to THREADS
+// candidates; the finish loads one slot entry per thread and workgroup.
 constexpr int kPartPerThread = 4;
-constexpr int kPartScores = kPartThreads * kPartPerThread;  // per workgroup
-constexpr int kPartCand = kPartThreads;                      // candidate slots per workgroup
-constexpr int kPartMaxGroups = 32;                           // finish: one slot entry per thread and group
-static_assert(kPartMaxGroups * kPartScores <= (1 << 22), "32-bit sample index arithmetic");
+constexpr int kPartMaxGroups = 32;
+constexpr int kSampleSize = 1024;
+static_assert(static_cast<int64_t>(kSampleSize) * kPartMaxGroups * 1024 * kPartPerThread <= (int64_t(1) << 32),
+              "32-bit sample index arithmetic");
 constexpr int kSampleBuckets = 1024;
 constexpr int kFinishCand = 8192;                            // candidates gathered in LDS
 constexpr int kRecordWords = 8;  // per workgroup: below, candidates, NaNs, candidate min / max key
 constexpr int64_t kPartitionMin = 8192;                      // smaller inputs: one workgroup
+#ifndef KOEMI_PART_SMALL_MAX
+#define KOEMI_PART_SMALL_MAX (int64_t(kPartMaxGroups) * 256 * kPartPerThread)
+#endif
+constexpr int64_t kPartSmallMax = KOEMI_PART_SMALL_MAX;   // 256-thread path
+constexpr int64_t kPartMax = int64_t(kPartMaxGroups) * 1024 * kPartPerThread;       // 1024-thread path
+
+inline int part_threads(int64_t n) { return n <= kPartSmallMax ? 256 : 1024; }
 
 struct PartWorkspace {
+    int threads, groups;
     size_t header_off, record_off, key_off, index_off, total;
 };
 inline PartWorkspace part_workspace(int64_t n) {
-    const int64_t groups = (n + kPartScores - 1) / kPartScores;
     PartWorkspace w;
+    w.threads = part_threads(n);
+    const int64_t scores = int64_t(w.threads) * kPartPerThread;
+    w.groups = static_cast<int>((n + scores - 1) / scores);
+    const size_t slots = static_cast<size_t>(w.groups) * w.threads * sizeof(uint32_t);
     w.header_off = 0;
     w.record_off = 256;
-    w.key_off = w.record_off + ((static_cast<size_t>(groups) * kRecordWords * sizeof(uint32_t) + 255) & ~size_t(255));
-    w.index_off = w.key_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
-    w.total = w.index_off + ((static_cast<size_t>(groups) * kPartCand * sizeof(uint32_t) + 255) & ~size_t(255));
+    w.key_off = w.record_off + ((static_cast<size_t>(w.groups) * kRecordWords * sizeof(uint32_t) + 255) & ~size_t(255));
+    w.index_off = w.key_off + ((slots + 255) & ~size_t(255));
+    w.total = w.index_off + ((slots + 255) & ~size_t(255));
     return w;
 }
 
-// One sample key per thread: element floor(tid * n / 1024) (n > 1024 and
-// tid * n < 2^32 on the partitioned path, so 32-bit arithmetic is exact).
+// The sample: 256 runs of 4 consecutive scores, run b starting at
+// floor(b * n / 256) rounded down to a multiple of 4 (so a run is one 16-byte
+// line segment and the sample touches 256 cache lines, not 1024); sample
+// element i = 4 b + c is held by thread tid with i = tid + j * THREADS.
+// n > 1024 and b * n < 2^32 on the partitioned path, so 32-bit arithmetic is
+// exact and every run lies inside the scores.
+template <int THREADS>
 struct SampleKeys {
-    uint32_t key;
-    bool present;
+    static constexpr int kPer = kSampleSize / THREADS;
+    uint32_t key[kPer];
+    uint32_t present;  // bit j: key[j] is not NaN
     __device__ void load(const float* __restrict__ s, int64_t n) {
-        const uint32_t src = static_cast<uint32_t>(threadIdx.x) * static_cast<uint32_t>(n) / kPartThreads;
-        const float v = s[src];
-        key = order_key(v);
-        present = v == v;
+        float v[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const uint32_t i = static_cast<uint32_t>(threadIdx.x + j * THREADS);
+            const uint32_t run = ((i >> 2) * static_cast<uint32_t>(n) / (kSampleSize / 4)) & ~3u;
+            v[j] = s[run + (i & 3u)];
+        }
+        present = 0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            key[j] = order_key(v[j]);
+            present |= (v[j] == v[j] ? 1u : 0u) << j;
+        }
     }
     template <class F>
     __device__ void visit(F f) const {
-        if (present) f(key);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j)
+            if ((present >> j) & 1u) f(key[j]);
     }
     template <class F>
     __device__ void visit_all(F f) const {
-        f(key, present);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) f(key[j], ((present >> j) & 1u) != 0);
     }
 };
 
-template <bool VEC>
-__global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
+template <int THREADS, bool VEC>
+__global__ __launch_bounds__(THREADS) void quantile_partition_kernel(
     const float* __restrict__ s, const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm, int64_t n,
     int64_t k_lo, int64_t k_hi, uint32_t* __restrict__ header, uint32_t* __restrict__ records,
     uint32_t* __restrict__ cand_key, uint32_t* __restrict__ cand_index) {
     __shared__ SelShared sh;
+    constexpr int kScores = THREADS * kPartPerThread;  // per workgroup
+    constexpr int kCand = THREADS;                      // candidate slots per workgroup
     const int tid = threadIdx.x;
     // Own scores and the sample are loaded together.
-    const int64_t base = static_cast<int64_t>(blockIdx.x) * kPartScores + static_cast<int64_t>(tid) * kPartPerThread;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kScores + static_cast<int64_t>(tid) * kPartPerThread;
     float v[kPartPerThread];
     uint32_t vw = 0;
     if constexpr (VEC) {
@@ -733,13 +774,17 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
             vw |= static_cast<uint32_t>(valid[i]) << (8 * c);
         }
     }
-    SampleKeys sample;
+    SampleKeys<THREADS> sample;
     sample.load(s, n);
 
     // Pivots from the sample (identical in every workgroup).
-    uint32_t m = sample.present ? 1u : 0u, smin = sample.present ? sample.key : 0xffffffffu,
-             smax = sample.present ? sample.key : 0u;
-    block_count_min_max<kPartThreads>(m, smin, smax, sh);
+    uint32_t m = 0, smin = 0xffffffffu, smax = 0u;
+    sample.visit([&](uint32_t k) {
+        ++m;
+        smin = min(smin, k);
+        smax = max(smax, k);
+    });
+    block_count_min_max<THREADS>(m, smin, smax, sh);
     uint32_t p_lo = 0, p_hi = 0xffffffffu;
     if (m > 0) {
         const float frac0 = static_cast<float>(k_lo) / static_cast<float>(n);
@@ -752,7 +797,7 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
         const uint32_t r1 = r1f >= static_cast<float>(m - 1) ? m - 1 : static_cast<uint32_t>(r1f);
         const uint32_t span = smax - smin;
         const int shift = span < kSampleBuckets ? 0 : 32 - __builtin_clz(span) - 10;
-        bucket_pass<SampleKeys, kPartThreads, kSampleBuckets>(sample, smin, smax, shift, 0, r0, r1, sh);
+        bucket_pass<SampleKeys<THREADS>, THREADS, kSampleBuckets>(sample, smin, smax, shift, 0, r0, r1, sh);
         const uint32_t b0 = sh.result[0], b1 = sh.result[3];
         __syncthreads();
         // Ranks at the sample's ends open the range to the whole key space.
@@ -819,7 +864,7 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
     cmin = 0xffffffffu;
     cmax = 0;
 #pragma unroll
-    for (int i = 0; i < kPartThreads / kWave; ++i) {
+    for (int i = 0; i < THREADS / kWave; ++i) {
         if (i < w) pos += sh.wave_tmp[0][i];
         total += sh.wave_tmp[0][i];
         below_total += sh.wave_tmp[1][i];
@@ -827,12 +872,12 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
         cmin = min(cmin, sh.list[0][i]);
         cmax = max(cmax, sh.list[1][i]);
     }
-    uint32_t* keys_out = cand_key + static_cast<int64_t>(blockIdx.x) * kPartCand;
-    uint32_t* index_out = cand_index + static_cast<int64_t>(blockIdx.x) * kPartCand;
+    uint32_t* keys_out = cand_key + static_cast<int64_t>(blockIdx.x) * kCand;
+    uint32_t* index_out = cand_index + static_cast<int64_t>(blockIdx.x) * kCand;
 #pragma unroll
     for (int c = 0; c < kPartPerThread; ++c) {
         if ((cand_bits >> c) & 1u) {
-            if (pos < kPartCand) {
+            if (pos < kCand) {
                 keys_out[pos] = order_key(v[c]);
                 const uint32_t ok = ((vw >> (8 * c)) & 0xffu) ? 0x80000000u : 0u;
                 index_out[pos] = static_cast<uint32_t>(tid * kPartPerThread + c) | ok;
@@ -851,12 +896,13 @@ __global__ __launch_bounds__(kPartThreads) void quantile_partition_kernel(
 }
 
 // Candidate keys gathered in LDS.
+template <int THREADS>
 struct LdsKeys {
     const uint32_t* key;
     uint32_t m;
     template <class F>
     __device__ void visit(F f) const {
-        for (uint32_t i = threadIdx.x; i < m; i += kSelThreads) f(key[i]);
+        for (uint32_t i = threadIdx.x; i < m; i += THREADS) f(key[i]);
     }
     template <class F>
     __device__ void visit_all(F f) const {
@@ -864,36 +910,46 @@ struct LdsKeys {
     }
 };
 
-template <int GMAX>
+// SLOT: candidate slots per partition workgroup (its thread count), GMAX:
+// the most workgroups this instance reads. Flat slot entry f = g * SLOT + e is
+// loaded by thread f % kSelThreads (E = GMAX * SLOT / kSelThreads per thread).
+template <int SLOT, int GMAX>
 __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
     const float* __restrict__ s, const uint8_t* __restrict__ valid, uint8_t* __restrict__ adm,
     float* __restrict__ tau_out, int64_t n, int64_t k_lo, int64_t k_hi, float weight,
     const uint32_t* __restrict__ header, const uint32_t* __restrict__ records, const uint32_t* __restrict__ cand_key,
     const uint32_t* __restrict__ cand_index, int groups) {
+    constexpr int THREADS = kSelThreads;
+    constexpr int kScores = SLOT * kPartPerThread;  // scores per partition workgroup
+    constexpr int E = GMAX * SLOT / THREADS;
+    static_assert(E >= 1 && GMAX * SLOT % THREADS == 0 && GMAX <= kWave, "slot entry layout");
     __shared__ SelShared sh;
     __shared__ uint32_t keys[kFinishCand];
     const int tid = threadIdx.x;
     // One round trip: lane g of every wave loads record g (vector loads, all in
-    // flight together), every thread loads entry `tid` of every slot (in bounds
-    // whatever the counts), and the pivots. Totals, and the candidates' key
-    // range, come from the records by wave reductions (no barrier).
+    // flight together), every thread loads its E slot entries (in bounds
+    // whatever the counts), and the pivots. Totals, the candidates' key range
+    // and each slot's offset among the gathered candidates come from the
+    // records by wave reductions and a wave scan (no barrier).
     const int lane = lane_id();
     const int rg = lane < groups ? lane : groups - 1;
     const uint32_t* rec = records + rg * kRecordWords;
     uint32_t rec_below = rec[0], rec_cand = rec[1], rec_nan = rec[2], rec_min = rec[3], rec_max = rec[4];
-    uint32_t key[GMAX], index[GMAX];
+    uint32_t key[E], index[E];
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) {
+    for (int k = 0; k < E; ++k) {
+        const int f = tid + k * THREADS;
+        const int g = f / SLOT;
         const int gc = g < groups ? g : groups - 1;
-        key[g] = cand_key[static_cast<int64_t>(gc) * kPartCand + tid];
-        index[g] = cand_index[static_cast<int64_t>(gc) * kPartCand + tid];
+        key[k] = cand_key[static_cast<int64_t>(gc) * SLOT + f % SLOT];
+        index[k] = cand_index[static_cast<int64_t>(gc) * SLOT + f % SLOT];
     }
     if (lane >= groups) {
         rec_below = rec_cand = rec_nan = 0;
         rec_min = 0xffffffffu;
         rec_max = 0;
     }
-    uint32_t below = rec_below, cand = rec_cand, bad = (rec_nan != 0 || rec_cand > kPartCand) ? 1u : 0u;
+    uint32_t below = rec_below, cand = rec_cand, bad = (rec_nan != 0 || rec_cand > SLOT) ? 1u : 0u;
     uint32_t kmin = rec_min, kmax = rec_max;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -903,26 +959,39 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
         kmin = min(kmin, static_cast<uint32_t>(__shfl_xor(kmin, off, kWave)));
         kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(kmax, off, kWave)));
     }
-    uint32_t count[GMAX];
+    uint32_t prefix = rec_cand;  // inclusive scan of the slot counts over the lanes
 #pragma unroll
-    for (int g = 0; g < GMAX; ++g) count[g] = __shfl(rec_cand, g, kWave);  // 0 past `groups`
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint32_t up = __shfl_up(prefix, off, kWave);
+        if (lane >= off) prefix += up;
+    }
+    prefix -= rec_cand;
+    // A wave's 64 entries lie in one slot (SLOT % 64 == 0), so each slot's count
+    // and offset are wave-uniform (scalar registers).
+    static_assert(SLOT % kWave == 0, "one slot per wave and entry");
+    uint32_t count[E], offset[E];
+#pragma unroll
+    for (int k = 0; k < E; ++k) {
+        const int g = __builtin_amdgcn_readfirstlane((tid + k * THREADS) / SLOT);  // < GMAX; count 0 past `groups`
+        count[k] = __builtin_amdgcn_readlane(rec_cand, g);
+        offset[k] = __builtin_amdgcn_readlane(prefix, g);
+    }
     const uint32_t p_lo = header[0], p_hi = header[1];
     const bool fast = bad == 0 && cand <= kFinishCand && static_cast<int64_t>(below) <= k_lo &&
                       k_hi < static_cast<int64_t>(below) + static_cast<int64_t>(cand);
     float tau = 0.0f;
     bool decided = false;
     if (fast) {
-        uint32_t off = 0;
 #pragma unroll
-        for (int g = 0; g < GMAX; ++g) {
-            if (static_cast<uint32_t>(tid) < count[g]) keys[off + tid] = key[g];
-            off += count[g];
+        for (int k = 0; k < E; ++k) {
+            const uint32_t e = static_cast<uint32_t>((tid + k * THREADS) % SLOT);
+            if (e < count[k]) keys[offset[k] + e] = key[k];
         }
         __syncthreads();
-        LdsKeys lk{keys, cand};
+        LdsKeys<THREADS> lk{keys, cand};
         uint32_t key_lo, key_hi;
-        select_two_ranks<LdsKeys, 10>(lk, kmin, kmax, static_cast<uint32_t>(k_lo - below),
-                                      static_cast<uint32_t>(k_hi - below), sh, key_lo, key_hi);
+        select_two_ranks<LdsKeys<THREADS>, 10, THREADS>(lk, kmin, kmax, static_cast<uint32_t>(k_lo - below),
+                                                        static_cast<uint32_t>(k_hi - below), sh, key_lo, key_hi);
         const float v_lo = key_to_float(key_lo);
         const float v_hi = key_to_float(key_hi);
         tau = weight < 0.5f ? __builtin_fmaf(weight, v_hi - v_lo, v_lo)
@@ -935,17 +1004,18 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
         if (decided) {
             // Mask bytes of the candidates (every other byte was decided by the partition).
 #pragma unroll
-            for (int g = 0; g < GMAX; ++g) {
-                if (static_cast<uint32_t>(tid) < count[g]) {
-                    const int64_t i = static_cast<int64_t>(g) * kPartScores + (index[g] & 0x7fffffffu);
-                    adm[i] = ((index[g] >> 31) && key_to_float(key[g]) > tau) ? 1 : 0;
+            for (int k = 0; k < E; ++k) {
+                const int f = tid + k * THREADS;
+                if (static_cast<uint32_t>(f % SLOT) < count[k]) {
+                    const int64_t i = static_cast<int64_t>(f / SLOT) * kScores + (index[k] & 0x7fffffffu);
+                    adm[i] = ((index[k] >> 31) && key_to_float(key[k]) > tau) ? 1 : 0;
                 }
             }
         }
     }
     if (!decided) {
         // Exact select over all scores from memory, and the whole mask.
-        MemoryKeys mk;
+        MemoryKeys<THREADS> mk;
         mk.load(s, valid, n);
         uint32_t counted = 0, kmin = 0xffffffffu, kmax = 0;
         mk.visit([&](uint32_t k) {
@@ -953,13 +1023,13 @@ __global__ __launch_bounds__(kSelThreads) void quantile_finish_kernel(
             kmin = min(kmin, k);
             kmax = max(kmax, k);
         });
-        block_count_min_max(counted, kmin, kmax, sh);
+        block_count_min_max<THREADS>(counted, kmin, kmax, sh);
         if (static_cast<int64_t>(counted) != n) {
             tau = __builtin_nanf("");
         } else {
             uint32_t key_lo, key_hi;
-            select_two_ranks(mk, kmin, kmax, static_cast<uint32_t>(k_lo), static_cast<uint32_t>(k_hi), sh, key_lo,
-                             key_hi);
+            select_two_ranks<MemoryKeys<THREADS>, 12, THREADS>(mk, kmin, kmax, static_cast<uint32_t>(k_lo),
+                                                               static_cast<uint32_t>(k_hi), sh, key_lo, key_hi);
             const float v_lo = key_to_float(key_lo);
             const float v_hi = key_to_float(key_hi);
             tau = weight < 0.5f ? __builtin_fmaf(weight, v_hi - v_lo, v_lo)
@@ -989,18 +1059,19 @@ int launch_rows(const float* logits, const void* bias, const int64_t* targets, c
     } while (0)
     if (V <= 256) {
         const dim3 grid(grid_for(rows, kRowWaves * 4));
-#define KOEMI_ROWS16(VEC)                                                                                      \
-    do {                                                                                                       \
-        if (b)                                                                                                 \
-            hipLaunchKernelGGL((surprise_rows16_kernel<T, VEC, true>), grid, block, 0, stream, logits, b, targets, \
-                               valid, o, rows, V, log_vocab);                                                  \
-        else                                                                                                   \
-            hipLaunchKernelGGL((surprise_rows16_kernel<T, VEC, false>), grid, block, 0, stream, logits, b,       \
-                               targets, valid, o, rows, V, log_vocab);                                         \
-    } while (0)
-        if (vec) KOEMI_ROWS16(true);
-        else KOEMI_ROWS16(false);
-#undef KOEMI_ROWS16
+        auto launch16 = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, block, 0, stream, logits, b, targets, valid, o, rows, V, log_vocab);
+        };
+        if (vec && V == 256) {
+            if (b) launch16(surprise_rows16_kernel<T, true, true, true>);
+            else launch16(surprise_rows16_kernel<T, true, false, true>);
+        } else if (vec) {
+            if (b) launch16(surprise_rows16_kernel<T, true, true, false>);
+            else launch16(surprise_rows16_kernel<T, true, false, false>);
+        } else {
+            if (b) launch16(surprise_rows16_kernel<T, false, true, false>);
+            else launch16(surprise_rows16_kernel<T, false, false, false>);
+        }
     } else if (V <= 1024) {
         if (vec) KOEMI_ROWS_LAUNCH(4, 1, true);
         else KOEMI_ROWS_LAUNCH(4, 1, false);
@@ -1077,7 +1148,7 @@ extern "C" int koemi_admission_threshold(const void* surprise, const uint8_t* va
 
 // Inputs handled by the two-kernel path (more use the single workgroup).
 inline bool partitioned(int64_t count) {
-    return count > kPartitionMin && count <= static_cast<int64_t>(kPartMaxGroups) * kPartScores;
+    return count > kPartitionMin && count <= kPartMax;
 }
 
 extern "C" size_t koemi_admission_quantile_workspace_bytes(int64_t count) {
@@ -1112,32 +1183,39 @@ extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* va
         return check_launch("koemi_admission_quantile");
     }
     if (!partitioned(count)) {
-        launch(quantile_admission_kernel<MemoryKeys>);
+        launch(quantile_admission_kernel<MemoryKeys<kSelThreads>>);
         return check_launch("koemi_admission_quantile");
     }
     const PartWorkspace pw = part_workspace(count);
     if (!workspace || workspace_bytes < pw.total)
         return fail(KOEMI_ERR_INVALID, "quantile admission workspace too small: need %zu bytes", pw.total);
-    const int groups = static_cast<int>((count + kPartScores - 1) / kPartScores);
+    const int groups = pw.groups;
     char* ws = static_cast<char*>(workspace);
     uint32_t* header = reinterpret_cast<uint32_t*>(ws + pw.header_off);
     uint32_t* records = reinterpret_cast<uint32_t*>(ws + pw.record_off);
     uint32_t* cand_key = reinterpret_cast<uint32_t*>(ws + pw.key_off);
     uint32_t* cand_index = reinterpret_cast<uint32_t*>(ws + pw.index_off);
-    if (vec)
-        hipLaunchKernelGGL(quantile_partition_kernel<true>, dim3(static_cast<unsigned>(groups)), dim3(kPartThreads), 0,
-                           s, surprise, valid_mask, admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
-    else
-        hipLaunchKernelGGL(quantile_partition_kernel<false>, dim3(static_cast<unsigned>(groups)), dim3(kPartThreads), 0,
-                           s, surprise, valid_mask, admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
-    const int st = check_launch("koemi_admission_quantile(partition)");
-    if (st != KOEMI_OK) return st;
-    auto finish = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission, threshold_out,
-                           count, k_lo, k_hi, weight, header, records, cand_key, cand_index, groups);
+    auto run = [&](auto threads_tag) -> int {
+        constexpr int T = decltype(threads_tag)::value;
+        auto partition = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(groups)), dim3(T), 0, s, surprise, valid_mask,
+                               admission, count, k_lo, k_hi, header, records, cand_key, cand_index);
+        };
+        if (vec) partition(quantile_partition_kernel<T, true>);
+        else partition(quantile_partition_kernel<T, false>);
+        const int st = check_launch("koemi_admission_quantile(partition)");
+        if (st != KOEMI_OK) return st;
+        auto finish = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(1), dim3(kSelThreads), 0, s, surprise, valid_mask, admission,
+                               threshold_out, count, k_lo, k_hi, weight, header, records, cand_key, cand_index, groups);
+        };
+        if (groups <= 8) finish(quantile_finish_kernel<T, 8>);
+        else if (groups <= 16) finish(quantile_finish_kernel<T, 16>);
+        else finish(quantile_finish_kernel<T, kPartMaxGroups>);
+        return KOEMI_OK;
     };
-    if (groups <= 8) finish(quantile_finish_kernel<8>);
-    else if (groups <= 16) finish(quantile_finish_kernel<16>);
-    else finish(quantile_finish_kernel<kPartMaxGroups>);
+    const int st = pw.threads == 256 ? run(std::integral_constant<int, 256>{})
+                                     : run(std::integral_constant<int, 1024>{});
+    if (st != KOEMI_OK) return st;
     return check_launch("koemi_admission_quantile");
 }

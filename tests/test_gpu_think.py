@@ -128,7 +128,8 @@ def test_config2_surprise_and_quantile_admission_bit_exact(device):
 @pytest.mark.parametrize(
     "case",
     ["single", "pair", "ties", "ties_aligned", "constant", "negative", "wide", "nan", "normal_32k", "odd_32k",
-     "ties_32k", "outliers_32k", "zeros_32k", "sorted_32k", "large"],
+     "ties_32k", "outliers_32k", "zeros_32k", "sorted_32k", "nan_32k", "odd_12k", "normal_100k", "sorted_64k",
+     "large"],
 )
 @pytest.mark.parametrize("q", [0.0, 0.25, 0.9, 1.0])
 def test_quantile_admission_edge_cases(device, case, q):
@@ -148,6 +149,10 @@ def test_quantile_admission_edge_cases(device, case, q):
         "outliers_32k": np.concatenate([rng.normal(0.63, 0.05, 32764), [1e-30, 3e38, -3e38, -0.0]]),
         "zeros_32k": rng.choice(np.array([-0.0, 0.0, 0.5, -1.0]), 32768),
         "sorted_32k": np.sort(rng.normal(0.63, 0.05, 32768)),
+        "nan_32k": np.concatenate([rng.normal(0.63, 0.05, 20000), [np.nan], rng.normal(0.63, 0.05, 12767)]),
+        "odd_12k": rng.normal(0.63, 0.05, 12001),
+        "normal_100k": rng.normal(0.63, 0.05, 100_000),
+        "sorted_64k": np.sort(rng.normal(0.63, 0.05, 65536)),
         "large": rng.uniform(0.5, 0.9, 300_000),
     }[case].astype(np.float32)
     valid = rng.random(scores.size) > 0.2
