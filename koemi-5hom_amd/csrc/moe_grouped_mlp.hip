@@ -18,6 +18,8 @@
 // valid pairs are zero-filled.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace koemi {
 namespace {
 
@@ -41,6 +43,7 @@ constexpr int kBK = 32;
 #define KOEMI_GEMM_STAGES 4
 #endif
 constexpr int kStages = KOEMI_GEMM_STAGES;
+static_assert(kStages == 4, "the prologue fills three stages and each K step waits for one tile");
 constexpr int kGemmThreads = 256;
 constexpr uint32_t kStageBytes = 2u * kBM * kBK * 2u;  // A and B, bf16
 constexpr uint32_t kOperandBytes = kBM * kBK * 2u;
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t slots, int64_t n_tiles,
     int64_t per_xcd) {
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
-    __shared__ float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
+    __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
 
     const int64_t logical = static_cast<int64_t>(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     const int64_t group = kGroupM * n_tiles;
@@ -253,6 +256,21 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         }
     };
 
+    // Fragment rows: A rows of the wave's four m-tiles, B rows of its four
+    // n-tiles (GLU: two gate, two value).
+    const int fr = lane & 31;
+    const int fg = lane >> 5;
+
+    // The tile's biases (one per thread: GLU gate biases of hidden units
+    // [n0, n0 + 128) then their value biases; plain: 256 output columns) are
+    // loaded now and reach LDS at the epilogue, so their latency is hidden
+    // behind the main loop.
+    float bias_mine;
+    {
+        const int64_t col = GLU ? min(n0 + (tid & 127), n_out - 1) : min(n0 + tid, n_out - 1);
+        const bf16* bsrc = (GLU && tid >= 128) ? bias1 : bias0;
+        bias_mine = to_f32(bsrc[static_cast<int64_t>(e) * n_out + col]);
+    }
     f32x16 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -260,11 +278,6 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-    // Fragment rows: A rows of the wave's four m-tiles, B rows of its four
-    // n-tiles (GLU: two gate, two value).
-    const int fr = lane & 31;
-    const int fg = lane >> 5;
     int a_row[4], b_row[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -301,62 +314,68 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j & 3], af[j >> 2], acc[j >> 2][j & 3], 0, 0, 0);
     };
 
-    // K is a multiple of 64, so nk >= 2. Every iteration issues one stage copy
-    // (past the last tile it repeats the last tile into the stage just
-    // consumed, which is never read again), so exactly one tile is in flight
-    // behind the one waited for at every barrier.
+    // K is a multiple of 64, so nk >= 2. Step kt issues the copy of K tile
+    // kt + 3 (while there is one) into the stage consumed by step kt - 1, so at
+    // most one tile is in flight behind the one waited for at every barrier;
+    // no copy is issued past the last tile, so none is outstanding at the
+    // epilogue.
     const int64_t nk = K / kBK;
-#pragma unroll
-    for (int p = 0; p < kStages - 1; ++p) issue(min(static_cast<int64_t>(p), nk - 1), p);
-    wait_tiles_and_sync(kStages - 2);
+    issue(0, 0);
+    issue(1, 1);
+    if (nk >= 3) {
+        issue(2, 2);
+        wait_tiles_and_sync(2);
+    } else {
+        wait_tiles_and_sync(1);
+    }
     bf16x8 a0[4], b0[4], a1[4], b1[4];
     read_frags(0, 0, a0, b0);
     // Each MFMA is followed by one other memory instruction (a stage copy or a
     // fragment read for a later K step), pinned in place by scheduling
     // barriers, so that the copies and LDS reads issue while the matrix pipe is
     // busy instead of in a burst that leaves it idle.
-    for (int64_t kt = 0; kt < nk; ++kt) {
-        // Tile kt + 1 has landed for every wave, and every wave is done with
-        // the stage of tile kt - 1, which the next copy overwrites.
-        wait_tiles_and_sync(kStages - 3);
-        const int64_t kc = min(kt + kStages - 1, nk - 1);
+    auto k_step = [&](int64_t kt, auto copy_tag) {
+        constexpr bool kCopy = decltype(copy_tag)::value;
+        // Tile kt + 1 has landed for every wave (one later copy may still be
+        // in flight: tile kt + 2, if there is one), and every wave is done
+        // with the stage of tile kt - 1, which this step's copy overwrites.
+        if (kCopy || kt + 2 < nk) wait_tiles_and_sync(1);
+        else wait_tiles_and_sync(0);
         const int sc = static_cast<int>((kt + kStages - 1) % kStages);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             mfma_one(j, a0, b0);
-            if (j % 2 == 0) issue_one(kc, sc, j / 2);
-            else read_frag(kt, 1, j / 2, a1, b1);
+            if (j % 2 == 0) {
+                if constexpr (kCopy) issue_one(kt + kStages - 1, sc, j / 2);
+            } else {
+                read_frag(kt, 1, j / 2, a1, b1);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
-        const int64_t kn = min(kt + 1, nk - 1);  // the last iteration re-reads its own stage harmlessly
+        const int64_t kn = min(kt + 1, nk - 1);  // the last step re-reads its own stage harmlessly
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             mfma_one(j, a1, b1);
             if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
             __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
+    int64_t kt = 0;
+    for (; kt + kStages - 1 < nk; ++kt) k_step(kt, std::true_type{});
+    for (; kt < nk; ++kt) k_step(kt, std::false_type{});
 
-    // Epilogue through LDS, so that global stores are whole rows: the tile's
-    // biases go to LDS; each wave writes its bias-added (GLU: silu(g) * u)
-    // bf16 outputs into its own LDS region, then reads it back row by row in
+    // Epilogue through LDS, so that global stores are whole rows: each wave
+    // writes its bias-added bf16 outputs (GLU: silu(g) * u) into its own LDS
+    // region, then reads it back row by row in
     // 16-byte chunks and stores full 128-byte lines. Accumulator element v of
     // lane l is row l % 32, column 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its
     // 32x32 tile. Region rows are kOutCols bf16; the 16-byte chunk c of row r
-    // sits at chunk c ^ (r & kSwz) (conflict-free row reads).
+    // sits at chunk c ^ (r & kSwz) (conflict-free row reads). The GLU products
+    // of a 32x32 tile are formed sixteen at a time, each step over all sixteen
+    // (independent exp and reciprocal latencies overlap).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no stage copy may still be writing LDS
-    __syncthreads();                                  // every wave is done reading the stages
-    {
-        float bv;
-        if constexpr (GLU) {
-            const int64_t col = min(n0 + (tid & 127), n_out - 1);
-            bv = to_f32((tid < 128 ? bias0 : bias1)[static_cast<int64_t>(e) * n_out + col]);
-        } else {
-            bv = to_f32(bias0[static_cast<int64_t>(e) * n_out + min(n0 + tid, n_out - 1)]);
-        }
-        bias_sh[tid] = bv;
-    }
-    __syncthreads();
+    bias_sh[tid] = bias_mine;
+    __syncthreads();  // every wave is done reading the stages; the biases are in LDS
     constexpr int kOutCols = GLU ? 64 : 128;  // columns of a wave's output tile
     constexpr int kRowBytes = kOutCols * 2;
     constexpr int kChunks = kRowBytes / 16;   // 16-byte chunks per row
@@ -364,42 +383,87 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     char* region = lds + wave * (128 * kRowBytes);
     const int col_base = GLU ? wn * 64 : wn * 128;  // within the block tile's columns
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int r = mt * 32 + fr;
+    for (int nt = 0; nt < (GLU ? 2 : 4); ++nt) {
+        // Biases of the 16 columns of n-tile nt (the same for every m-tile):
+        // runs of four at col_base + nt * 32 + fg * 4 + 8 j (GLU value biases
+        // 128 further on).
+        float bias_g[16], bias_u[16];
 #pragma unroll
-        for (int nt = 0; nt < (GLU ? 2 : 4); ++nt)
+        for (int j = 0; j < 4; ++j) {
+            const int cl = col_base + nt * 32 + fg * 4 + j * 8;
+            const float4 bg4 = *reinterpret_cast<const float4*>(&bias_sh[cl]);
+            bias_g[j * 4 + 0] = bg4.x;
+            bias_g[j * 4 + 1] = bg4.y;
+            bias_g[j * 4 + 2] = bg4.z;
+            bias_g[j * 4 + 3] = bg4.w;
+            if constexpr (GLU) {
+                const float4 bu4 = *reinterpret_cast<const float4*>(&bias_sh[128 + cl]);
+                bias_u[j * 4 + 0] = bu4.x;
+                bias_u[j * 4 + 1] = bu4.y;
+                bias_u[j * 4 + 2] = bu4.z;
+                bias_u[j * 4 + 3] = bu4.w;
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            // One 32x32 tile at a time: without the scheduling barrier every
+            // accumulator is copied out of the AGPRs at once and VGPRs spill.
+            __builtin_amdgcn_sched_barrier(0);
+            const int r = mt * 32 + fr;
+            float o[16];
+            if constexpr (GLU) {
+                float g[16], d[16];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) g[v] = acc[mt][nt][v] + bias_g[v];
+#pragma unroll
+                for (int v = 0; v < 16; ++v) d[v] = __builtin_amdgcn_exp2f(g[v] * -1.4426950408889634f);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) d[v] = __builtin_amdgcn_rcpf(1.0f + d[v]);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[v] = (g[v] * d[v]) * (acc[mt][nt + 2][v] + bias_u[v]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) o[v] = acc[mt][nt][v] + bias_g[v];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int cl = nt * 32 + fg * 4 + j * 8;  // column within the wave tile
                 union {
                     uint2 raw;
                     bf16 e[4];
-                } o;
+                } w;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    if constexpr (GLU) {
-                        const float g = acc[mt][nt][j * 4 + q] + bias_sh[col_base + cl + q];
-                        const float u = acc[mt][nt + 2][j * 4 + q] + bias_sh[128 + col_base + cl + q];
-                        o.e[q] = from_f32<bf16>(silu_f(g) * u);
-                    } else {
-                        o.e[q] = from_f32<bf16>(acc[mt][nt][j * 4 + q] + bias_sh[col_base + cl + q]);
-                    }
-                }
+                for (int q = 0; q < 4; ++q) w.e[q] = from_f32<bf16>(o[j * 4 + q]);
                 const int chunk = (cl >> 3) ^ (r & kSwz);
-                *reinterpret_cast<uint2*>(region + r * kRowBytes + chunk * 16 + (cl & 4) * 2) = o.raw;
+                *reinterpret_cast<uint2*>(region + r * kRowBytes + chunk * 16 + (cl & 4) * 2) = w.raw;
             }
+        }
     }
     // Row-contiguous read-back (the wave's own region: LDS operations of a wave
     // complete in order) and full-line stores.
+    // Eight reads are issued before their eight stores, so one LDS latency
+    // covers eight lines.
     const int64_t out_col0 = n0 + col_base;
+    constexpr int kIters = 128 * kChunks / kWave;
+    constexpr int kBatch = 8;
+    static_assert(kIters % kBatch == 0, "read-back batches");
 #pragma unroll
-    for (int it = 0; it < 128 * kChunks / kWave; ++it) {
-        const int idx = it * kWave + lane;
-        const int r = idx / kChunks, c = idx % kChunks;
-        const uint4 v = *reinterpret_cast<const uint4*>(region + r * kRowBytes + ((c ^ (r & kSwz)) * 16));
-        const int64_t grow = row0 + wm * 128 + r;
-        const int64_t col = out_col0 + c * 8;
-        if (grow < row_end && col < n_out) *reinterpret_cast<uint4*>(C + grow * n_out + col) = v;
+    for (int b = 0; b < kIters; b += kBatch) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int idx = (b + i) * kWave + lane;
+            const int r = idx / kChunks, c = idx % kChunks;
+            v[i] = *reinterpret_cast<const uint4*>(region + r * kRowBytes + ((c ^ (r & kSwz)) * 16));
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int idx = (b + i) * kWave + lane;
+            const int r = idx / kChunks, c = idx % kChunks;
+            const int64_t grow = row0 + wm * 128 + r;
+            const int64_t col = out_col0 + c * 8;
+            if (grow < row_end && col < n_out) *reinterpret_cast<uint4*>(C + grow * n_out + col) = v[i];
+        }
     }
 }
 
