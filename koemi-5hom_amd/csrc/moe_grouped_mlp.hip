@@ -70,7 +70,8 @@ inline MlpWorkspace mlp_workspace(int64_t pairs, int64_t width, int64_t hidden, 
     const size_t elem = mfma_shape(width, hidden, dtype) ? 2 : 4;
     w.hidden_off = 0;
     w.slot_expert_off = align256(static_cast<size_t>(pairs > 0 ? pairs : 1) * static_cast<size_t>(hidden) * elem);
-    w.slot_row_off = w.slot_expert_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int32_t));
+    // slot_expert has one more entry: the number of slots in use.
+    w.slot_row_off = w.slot_expert_off + align256(static_cast<size_t>(w.max_slots + 1) * sizeof(int32_t));
     w.slot_end_off = w.slot_row_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int64_t));
     w.total = w.slot_end_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int64_t));
     return w;
@@ -122,6 +123,7 @@ __global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
     }
     __syncthreads();
     const int64_t total = first_tile[E];
+    if (tid == 0) slot_expert[max_slots] = static_cast<int32_t>(total);  // slots in use
     for (int64_t slot = tid; slot < max_slots; slot += kSchedThreads) {
         if (slot >= total) {
             slot_expert[slot] = -1;
@@ -200,16 +202,22 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
-    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t slots, int64_t n_tiles,
-    int64_t per_xcd) {
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles) {
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
     __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
 
+    // The grid covers the most slots the pairs can need; the tiles of the
+    // slots actually in use are spread evenly over the eight XCDs (workgroup
+    // b runs on XCD b % 8), the surplus workgroups exit.
+    const int64_t slots = min(static_cast<int64_t>(slot_expert[max_slots]), max_slots);
+    const int64_t tiles = slots * n_tiles;
+    const int64_t per_xcd = (tiles + 7) / 8;
+    if (static_cast<int64_t>(blockIdx.x >> 3) >= per_xcd) return;
     const int64_t logical = static_cast<int64_t>(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (logical >= tiles) return;
     const int64_t group = kGroupM * n_tiles;
     const int64_t gi = logical / group;
     const int64_t first_slot = gi * kGroupM;
-    if (first_slot >= slots) return;
     const int64_t gm = min(static_cast<int64_t>(kGroupM), slots - first_slot);
     const int64_t within = logical - gi * group;
     const int64_t slot = first_slot + within % gm;
@@ -549,7 +557,8 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
     int64_t* slot_end = reinterpret_cast<int64_t*>(base + ws.slot_end_off);
     if (ws.max_slots > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-    if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL)  // byte offsets < 2^32 return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
+    if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL)  // 32-bit byte offsets in the tiles
+        return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
     if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
                                              static_cast<long long>(kMaxScheduleExperts));
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
@@ -564,8 +573,7 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         if (per_xcd * 8 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kGemmThreads), 0, s, a,
                            static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
-                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
-                           per_xcd);
+                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles);
         return check_launch(what);
     };
     st = launch(grouped_gemm_bf16_kernel<true>, static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D,

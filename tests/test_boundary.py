@@ -66,6 +66,23 @@ def test_workspace_queries():
     assert _native.query("koemi_moe_combine_workspace_bytes", 32768, 2) >= 32768 * 2 * 8
 
 
+def test_grouped_mlp_rejects_shapes_past_its_limits_before_launching():
+    # The pointers are never dereferenced: both shapes fail the entry point's
+    # checks before any kernel is launched.
+    lib = _native.load_library()
+    fake = ctypes.c_void_p(1 << 20)
+
+    def run(width: int, hidden: int, experts: int) -> int:
+        need = _native.query("koemi_moe_grouped_mlp_workspace_bytes", 256, width, hidden, experts, _native.BF16)
+        return lib.koemi_moe_grouped_mlp(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake,
+                                         256, width, hidden, experts, _native.BF16, fake, need, None)
+
+    assert run(65536, 32768, 4) == _native.ERR_UNSUPPORTED  # 32-bit tile offsets
+    assert b"2^31" in lib.koemi_last_error()
+    assert run(1024, 2816, 9000) == _native.ERR_UNSUPPORTED  # LDS-resident tile prefixes
+    assert b"experts" in lib.koemi_last_error()
+
+
 # -------------------------------------------------------------------- dense
 
 
