@@ -53,8 +53,14 @@ constexpr int kKAlign = 64;
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// Split K for the last, sparse round: at most this many partial tiles (fp32
+// 256 x 256 each, 64 MiB in all) per GEMM launch.
+constexpr int kMaxSplitUnits = 256;
+constexpr int kMaxSplit = 8;  // chunks per leftover tile (the fixup reads every chunk)
+constexpr size_t kPartialTileFloats = static_cast<size_t>(kBM) * kBN;
+
 struct MlpWorkspace {
-    size_t hidden_off, slot_expert_off, slot_row_off, slot_end_off, total;
+    size_t hidden_off, slot_expert_off, slot_row_off, slot_end_off, partial_off, total;
     int64_t max_slots;
 };
 
@@ -73,7 +79,9 @@ inline MlpWorkspace mlp_workspace(int64_t pairs, int64_t width, int64_t hidden, 
     // slot_expert has one more entry: the number of slots in use.
     w.slot_row_off = w.slot_expert_off + align256(static_cast<size_t>(w.max_slots + 1) * sizeof(int32_t));
     w.slot_end_off = w.slot_row_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int64_t));
-    w.total = w.slot_end_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int64_t));
+    w.partial_off = w.slot_end_off + align256(static_cast<size_t>(w.max_slots) * sizeof(int64_t));
+    w.total = w.partial_off;
+    if (mfma_shape(width, hidden, dtype)) w.total += kMaxSplitUnits * kPartialTileFloats * sizeof(float);
     return w;
 }
 
@@ -187,6 +195,49 @@ __device__ __forceinline__ void wait_tiles_and_sync(int64_t n) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Logical tile -> (slot, column tile): groups of kGroupM slots, all column
+// tiles of a group before the next.
+// Tile counts stay below 2^31 (the entry point checks), so the index
+// arithmetic is 32-bit.
+__device__ __forceinline__ void tile_coords(uint32_t logical, uint32_t slots, uint32_t n_tiles, uint32_t& slot,
+                                            uint32_t& tile_n) {
+    const uint32_t group = kGroupM * n_tiles;
+    const uint32_t gi = logical / group;
+    const uint32_t first_slot = gi * kGroupM;
+    const uint32_t gm = min(static_cast<uint32_t>(kGroupM), slots - first_slot);
+    const uint32_t within = logical - gi * group;
+    slot = first_slot + within % gm;
+    tile_n = within / gm;
+}
+
+// Work of one GEMM launch: `whole` tiles computed in full, then, when the tiles
+// left over after whole rounds of `cus` workgroups would fill at most half a
+// round, each leftover tile split along K into `split` chunks (at least two K
+// steps each) so that the last round keeps every CU busy. Partial tiles go to
+// the workspace as fp32 and a fixup kernel adds them in chunk order.
+struct SplitPlan {
+    uint32_t whole, units, split;
+};
+
+// float4 index of (wave, m-tile, n-tile, j, lane) in a partial tile.
+__device__ __forceinline__ int partial_slot(int wave, int mt, int t, int j, int lane) {
+    return (((wave * 4 + mt) * 4 + t) * 4 + j) * kWave + lane;
+}
+__device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uint32_t cus) {
+    SplitPlan p{tiles, 0, 1};
+    const uint32_t rem = tiles % cus;
+    if (rem > 0 && rem * 2 <= cus) {
+        const uint32_t s =
+            min(min(min(cus, static_cast<uint32_t>(kMaxSplitUnits)) / rem, nk / 2), static_cast<uint32_t>(kMaxSplit));
+        if (s >= 2) {
+            p.whole = tiles - rem;
+            p.units = rem * s;
+            p.split = s;
+        }
+    }
+    return p;
+}
+
 // One 256x256 tile per workgroup. GLU: B rows 0..127 are gate rows and
 // 128..255 the value rows of hidden units [h0, h0 + 128), so wave (wm, wn) holds
 // gate and value accumulators of the same 128 rows x 64 hidden units and forms
@@ -197,31 +248,40 @@ __device__ __forceinline__ void wait_tiles_and_sync(int64_t n) {
 // renumbered so that every XCD owns a contiguous range, traversed in groups of
 // kGroupM slots (all column tiles of a group before the next), which keeps the
 // A rows and B columns of concurrently running tiles in that XCD's L2.
-template <bool GLU>
+template <bool GLU, bool PARTIAL>
 __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
-    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles) {
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
+    float* __restrict__ partial, uint32_t cus) {
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
     __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
 
-    // The grid covers the most slots the pairs can need; the tiles of the
-    // slots actually in use are spread evenly over the eight XCDs (workgroup
-    // b runs on XCD b % 8), the surplus workgroups exit.
-    const int64_t slots = min(static_cast<int64_t>(slot_expert[max_slots]), max_slots);
-    const int64_t tiles = slots * n_tiles;
-    const int64_t per_xcd = (tiles + 7) / 8;
-    if (static_cast<int64_t>(blockIdx.x >> 3) >= per_xcd) return;
-    const int64_t logical = static_cast<int64_t>(blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (logical >= tiles) return;
-    const int64_t group = kGroupM * n_tiles;
-    const int64_t gi = logical / group;
-    const int64_t first_slot = gi * kGroupM;
-    const int64_t gm = min(static_cast<int64_t>(kGroupM), slots - first_slot);
-    const int64_t within = logical - gi * group;
-    const int64_t slot = first_slot + within % gm;
-    const int64_t tile_n = within / gm;
+    // Whole tiles (PARTIAL false): the grid covers the most tiles the pairs can
+    // need; the whole tiles of the split plan for the slots actually in use are
+    // spread evenly over the eight XCDs (workgroup b runs on XCD b % 8) and the
+    // surplus workgroups exit. Partial tiles (PARTIAL true): workgroup b takes
+    // unit b of the plan, K steps [k_begin, k_end) of its leftover tile.
+    const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
+    const uint32_t nk_all = static_cast<uint32_t>(K / kBK);
+    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), nk_all, cus);
+    uint32_t logical, unit = 0, k_begin = 0, k_end = nk_all;
+    if constexpr (!PARTIAL) {
+        const uint32_t per_xcd = (plan.whole + 7) / 8;
+        if ((blockIdx.x >> 3) >= per_xcd) return;
+        logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+        if (logical >= plan.whole) return;
+    } else {
+        unit = blockIdx.x;
+        if (unit >= plan.units) return;
+        logical = plan.whole + unit / plan.split;
+        const uint32_t chunk = unit % plan.split;
+        k_begin = chunk * nk_all / plan.split;
+        k_end = (chunk + 1) * nk_all / plan.split;
+    }
+    uint32_t slot, tile_n;
+    tile_coords(logical, slots, static_cast<uint32_t>(n_tiles), slot, tile_n);
     const int e = slot_expert[slot];
     if (e < 0) return;
     const int64_t row0 = slot_row[slot];
@@ -230,7 +290,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const int lane = lane_id();
     const int wave = tid / kWave;
     const int wm = wave >> 1, wn = wave & 1;
-    const int64_t n0 = GLU ? tile_n * (kBN / 2) : tile_n * kBN;
+    const int64_t n0 = GLU ? static_cast<int64_t>(tile_n) * (kBN / 2) : static_cast<int64_t>(tile_n) * kBN;
 
     // Stage copies: wave w fills 1 KiB chunks 4w..4w+3 (16 rows each) of A and
     // of B; lane l of a chunk copies row l / 4 of it, K group (l % 4) ^ swizzle.
@@ -238,9 +298,11 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     // discarded outputs). Offsets are 32-bit and relative to per-tile bases
     // (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves 0-1
     // copy gate rows, waves 2-3 value rows.
-    const bf16* a_base = A + row0 * K;
+    // A partial tile runs K steps [k_begin, k_end): the bases start there.
+    const int64_t k0 = static_cast<int64_t>(k_begin) * kBK;
+    const bf16* a_base = static_cast<const bf16*>(uniform_ptr(A + row0 * K + k0));
     const bf16* b_base = static_cast<const bf16*>(
-        uniform_ptr(((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K));
+        uniform_ptr(((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K + k0));
     const int a_rows = static_cast<int>(row_end - row0);
     uint32_t a_off[4], b_off[4];  // byte offsets (the entry point bounds them below 2^32)
 #pragma unroll
@@ -322,12 +384,13 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j & 3], af[j >> 2], acc[j >> 2][j & 3], 0, 0, 0);
     };
 
-    // K is a multiple of 64, so nk >= 2. Step kt issues the copy of K tile
+    // K is a multiple of 64 and a partial tile has at least two K steps, so
+    // nk >= 2. Step kt issues the copy of K tile
     // kt + 3 (while there is one) into the stage consumed by step kt - 1, so at
     // most one tile is in flight behind the one waited for at every barrier;
     // no copy is issued past the last tile, so none is outstanding at the
     // epilogue.
-    const int64_t nk = K / kBK;
+    const int64_t nk = static_cast<int64_t>(k_end - k_begin);
     issue(0, 0);
     issue(1, 1);
     if (nk >= 3) {
@@ -371,6 +434,23 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     int64_t kt = 0;
     for (; kt + kStages - 1 < nk; ++kt) k_step(kt, std::true_type{});
     for (; kt < nk; ++kt) k_step(kt, std::false_type{});
+
+    if constexpr (PARTIAL) {
+        // Partial tile: the fp32 sums go to the workspace in accumulator order,
+        // float4 (wave, mt, t, j, lane) holding elements 4j..4j+3 of n-tile t of
+        // m-tile mt (partial_slot), so that each store writes 1 KiB contiguous.
+        float* pt = partial + static_cast<int64_t>(unit) * kPartialTileFloats;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<float4*>(pt + partial_slot(wave, mt, t, j, lane) * 4) =
+                        make_float4(acc[mt][t][j * 4 + 0], acc[mt][t][j * 4 + 1], acc[mt][t][j * 4 + 2],
+                                    acc[mt][t][j * 4 + 3]);
+        return;
+    }
 
     // Epilogue through LDS, so that global stores are whole rows: each wave
     // writes its bias-added bf16 outputs (GLU: silu(g) * u) into its own LDS
@@ -475,6 +555,93 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     }
 }
 
+// Sums the partial tiles of the split plan in chunk order, adds the biases
+// (GLU: silu(g + b_g) * (u + b_v)) and writes the bf16 outputs. A thread takes
+// one float4 slot of a leftover tile (GLU: a gate slot, n-tile t < 2, and its
+// value slot t + 2), reading the slot in every chunk (coalesced), and writes
+// the four consecutive outputs it holds: row wm * 128 + mt * 32 + lane % 32,
+// columns col_base + t * 32 + 4 (lane / 32) + 8 j (+0..3).
+template <bool GLU>
+__global__ __launch_bounds__(256) void split_fixup_kernel(
+    const float* __restrict__ partial, const bf16* __restrict__ bias0, const bf16* __restrict__ bias1,
+    bf16* __restrict__ C, const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
+    uint32_t cus) {
+    const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
+    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), static_cast<uint32_t>(K / kBK), cus);
+    if (plan.units == 0) return;
+    constexpr uint32_t kSlotsPerTile = GLU ? kPartialTileFloats / 8 : kPartialTileFloats / 4;
+    const uint32_t items = plan.units / plan.split * kSlotsPerTile;
+    for (uint32_t item = blockIdx.x * blockDim.x + threadIdx.x; item < items; item += gridDim.x * blockDim.x) {
+        const uint32_t rt = item / kSlotsPerTile;
+        uint32_t f = item % kSlotsPerTile;
+        const int lane = static_cast<int>(f % kWave);
+        f /= kWave;
+        const int j = static_cast<int>(f % 4);
+        f /= 4;
+        const int t = static_cast<int>(f % (GLU ? 2 : 4));
+        f /= GLU ? 2 : 4;
+        const int mt = static_cast<int>(f % 4);
+        const int wave = static_cast<int>(f / 4);
+        const int wm = wave >> 1, wn = wave & 1;
+        uint32_t slot, tile_n;
+        tile_coords(plan.whole + rt, slots, static_cast<uint32_t>(n_tiles), slot, tile_n);
+        const int e = slot_expert[slot];
+        const int64_t grow = slot_row[slot] + wm * 128 + mt * 32 + (lane & 31);
+        if (e < 0 || grow >= slot_end[slot]) continue;
+        const float* pt = partial + static_cast<int64_t>(rt) * plan.split * kPartialTileFloats;
+        const int64_t s0 = partial_slot(wave, mt, t, j, lane) * 4;
+        // Chunks are loaded eight at a time and added in chunk order; chunks
+        // past the split read as +0, which leaves a sum that starts at +0
+        // unchanged.
+        const int64_t sv = partial_slot(wave, mt, GLU ? t + 2 : t, j, lane) * 4;
+        float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
+        for (uint32_t k0 = 0; k0 < plan.split; k0 += 8) {
+            float4 pg[8], pu[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const bool in = k0 + i < plan.split;
+                const int64_t base = static_cast<int64_t>(in ? k0 + i : 0) * kPartialTileFloats;
+                pg[i] = *reinterpret_cast<const float4*>(pt + base + s0);
+                if (!in) pg[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (GLU) {
+                    pu[i] = *reinterpret_cast<const float4*>(pt + base + sv);
+                    if (!in) pu[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                g.x += pg[i].x;
+                g.y += pg[i].y;
+                g.z += pg[i].z;
+                g.w += pg[i].w;
+                if constexpr (GLU) {
+                    u.x += pu[i].x;
+                    u.y += pu[i].y;
+                    u.z += pu[i].z;
+                    u.w += pu[i].w;
+                }
+            }
+        }
+        const int64_t col = (GLU ? static_cast<int64_t>(tile_n) * (kBN / 2) + wn * 64
+                                 : static_cast<int64_t>(tile_n) * kBN + wn * 128) +
+                            t * 32 + (lane >> 5) * 4 + j * 8;
+        if (col >= n_out) continue;
+        const int64_t bo = static_cast<int64_t>(e) * n_out + col;
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+        union {
+            uint2 raw;
+            bf16 h[4];
+        } w;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if constexpr (GLU) w.h[c] = from_f32<bf16>(silu_f(gv[c] + to_f32(bias0[bo + c])) * (uv[c] + to_f32(bias1[bo + c])));
+            else w.h[c] = from_f32<bf16>(gv[c] + to_f32(bias0[bo + c]));
+        }
+        *reinterpret_cast<uint2*>(C + grow * n_out + col) = w.raw;
+    }
+}
+
 // ------------------------------------------------- fp32-accumulating SIMT path
 // One 256-thread block per sorted pair (the reference's decomposition), used for
 // float32 / float16 weights and for shapes the MFMA tiles do not cover.
@@ -549,6 +716,18 @@ int run_simt(const void* x, const int64_t* experts, const int64_t* offsets, cons
     return check_launch("koemi_moe_grouped_mlp(zero)");
 }
 
+// Compute units of the current device (the rounds of one-workgroup-per-CU tiles).
+int64_t device_cus() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] > 0) return cached[dev];
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 256;
+    cached[dev] = n;
+    return n;
+}
+
 int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* bg, const void* Wv, const void* bv,
              const void* Wo, const void* bo, void* y, int64_t P, int64_t D, int64_t Hd, int64_t E,
              const MlpWorkspace& ws, char* base, hipStream_t s) {
@@ -556,6 +735,7 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int32_t* slot_expert = reinterpret_cast<int32_t*>(base + ws.slot_expert_off);
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
     int64_t* slot_end = reinterpret_cast<int64_t*>(base + ws.slot_end_off);
+    float* partial = reinterpret_cast<float*>(base + ws.partial_off);
     if (ws.max_slots > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
     if (Hd * D > 0x7fffffffLL || 256 * (Hd > D ? Hd : D) > 0x7fffffffLL)  // 32-bit byte offsets in the tiles
         return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
@@ -566,21 +746,39 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int st = check_launch("koemi_moe_grouped_mlp(schedule)");
     if (st != KOEMI_OK) return st;
     const int64_t slots = ws.max_slots;
-    auto launch = [&](auto kernel, const bf16* a, const void* w0, const void* w1, const void* b0, const void* b1,
-                      bf16* c, int64_t n_out, int64_t K, int64_t n_tiles, const char* what) {
-        const int64_t tiles = slots * n_tiles;
-        const int64_t per_xcd = (tiles + 7) / 8;
-        if (per_xcd * 8 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(per_xcd * 8)), dim3(kGemmThreads), 0, s, a,
+    const uint32_t cus = static_cast<uint32_t>(device_cus());
+    // Whole tiles, then the partial tiles of the split plan (if any; every
+    // workgroup exits otherwise), then their sums.
+    auto launch = [&](auto kernel, auto partial_kernel, auto fixup, const bf16* a, const void* w0, const void* w1,
+                      const void* b0, const void* b1, bf16* c, int64_t n_out, int64_t K, int64_t n_tiles,
+                      const char* what) {
+        const int64_t whole_grid = (slots * n_tiles + 7) / 8 * 8;
+        if (whole_grid > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid)), dim3(kGemmThreads), 0, s, a,
                            static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
-                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles);
+                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
+                           partial, cus);
+        int st2 = check_launch(what);
+        if (st2 != KOEMI_OK) return st2;
+        hipLaunchKernelGGL(partial_kernel, dim3(kMaxSplitUnits), dim3(kGemmThreads), 0, s, a,
+                           static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
+                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
+                           partial, cus);
+        st2 = check_launch(what);
+        if (st2 != KOEMI_OK) return st2;
+        // At most kMaxSplitUnits / 2 leftover tiles of 8192 (GLU) or 16384 slots.
+        hipLaunchKernelGGL(fixup, dim3(1024), dim3(256), 0, s, partial, static_cast<const bf16*>(b0),
+                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots,
+                           n_tiles, cus);
         return check_launch(what);
     };
-    st = launch(grouped_gemm_bf16_kernel<true>, static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D,
-                (Hd + kBN / 2 - 1) / (kBN / 2), "koemi_moe_grouped_mlp(gemm1)");
+    st = launch(grouped_gemm_bf16_kernel<true, false>, grouped_gemm_bf16_kernel<true, true>, split_fixup_kernel<true>,
+                static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D, (Hd + kBN / 2 - 1) / (kBN / 2),
+                "koemi_moe_grouped_mlp(gemm1)");
     if (st != KOEMI_OK) return st;
-    st = launch(grouped_gemm_bf16_kernel<false>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd,
-                (D + kBN - 1) / kBN, "koemi_moe_grouped_mlp(gemm2)");
+    st = launch(grouped_gemm_bf16_kernel<false, false>, grouped_gemm_bf16_kernel<false, true>,
+                split_fixup_kernel<false>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd, (D + kBN - 1) / kBN,
+                "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
     hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
                        offsets + E, P, D);
