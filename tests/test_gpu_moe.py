@@ -183,6 +183,28 @@ def test_grouped_mlp_bf16_mfma_ragged_segments(device, sizes):
     assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
 
 
+def test_grouped_mlp_bf16_whole_rounds_and_split_last_round(device):
+    # 130 row slots; width 512 and hidden 256 give 260 tiles in both GEMMs: on a
+    # 256-CU device one whole round plus 4 leftover tiles computed in K chunks
+    # and summed by the fixup kernel (other CU counts take other plans).
+    g = torch.Generator().manual_seed(11)
+    E, D, H = 2, 512, 256
+    sizes = (16640, 16600)
+    offsets = np.concatenate([[0], np.cumsum(sizes)])
+    P = int(offsets[-1]) + 3
+    x = torch.randn((P, D), generator=g).to(torch.bfloat16)
+    experts = torch.full((P,), E, dtype=torch.int64)
+    for e in range(E):
+        experts[offsets[e]:offsets[e + 1]] = e
+    ws = [(0.05 * torch.randn(s, generator=g)).to(torch.bfloat16) for s in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    got = moe.grouped_expert_mlp_inference(x.to(device), experts.to(device), torch.from_numpy(offsets).to(device),
+                                           *(w.to(device) for w in ws))
+    want = oracle.grouped_mlp(x.float().numpy(), experts.numpy(), offsets, *(w.float().numpy() for w in ws),
+                              dtype=np.float32, round_hidden_bf16=True)
+    check_bf16_mlp(got[:offsets[-1]], want[:offsets[-1]], "grouped MLP bf16 whole rounds + split last round")
+    assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
+
+
 def run_config4_pipeline(device, c, learned: bool):
     ctx = c.context.to(device)
     valid = c.valid.to(device)
