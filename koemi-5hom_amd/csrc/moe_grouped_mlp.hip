@@ -43,7 +43,10 @@ constexpr int kBK = 32;
 #define KOEMI_GEMM_STAGES 4
 #endif
 constexpr int kStages = KOEMI_GEMM_STAGES;
-static_assert(kStages == 4, "the prologue fills three stages and each K step waits for one tile");
+static_assert(kStages == 4 || kStages == 5, "stage ring of four or five K tiles");
+// Five stages fill the 160 KiB of LDS; the epilogue's biases then live in the
+// last stage (free once the K loop is done), past the 128 KiB output regions.
+constexpr bool kBiasInStages = kStages >= 5;
 constexpr int kGemmThreads = 256;
 constexpr uint32_t kStageBytes = 2u * kBM * kBK * 2u;  // A and B, bf16
 constexpr uint32_t kOperandBytes = kBM * kBK * 2u;
@@ -256,7 +259,13 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
     float* __restrict__ partial, uint32_t cus) {
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
-    __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];  // the tile's biases (epilogue)
+    float* bias_sh;  // the tile's biases (epilogue)
+    if constexpr (kBiasInStages) {
+        bias_sh = reinterpret_cast<float*>(lds + 4 * kStageBytes);
+    } else {
+        __shared__ __attribute__((aligned(16))) float bias_arr[kGemmThreads];
+        bias_sh = bias_arr;
+    }
 
     // Whole tiles (PARTIAL false): the grid covers the most tiles the pairs can
     // need; the whole tiles of the split plan for the slots actually in use are
@@ -385,20 +394,17 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     };
 
     // K is a multiple of 64 and a partial tile has at least two K steps, so
-    // nk >= 2. Step kt issues the copy of K tile
-    // kt + 3 (while there is one) into the stage consumed by step kt - 1, so at
-    // most one tile is in flight behind the one waited for at every barrier;
-    // no copy is issued past the last tile, so none is outstanding at the
-    // epilogue.
+    // nk >= 2. The prologue issues K tiles 0 .. kStages - 2; step kt issues the
+    // copy of K tile kt + kStages - 1 (while there is one) into the stage
+    // consumed by step kt - 1, so up to kStages - 3 tiles are in flight behind
+    // the one waited for at every barrier; no copy is issued past the last
+    // tile, so none is outstanding at the epilogue.
     const int64_t nk = static_cast<int64_t>(k_end - k_begin);
     issue(0, 0);
     issue(1, 1);
-    if (nk >= 3) {
-        issue(2, 2);
-        wait_tiles_and_sync(2);
-    } else {
-        wait_tiles_and_sync(1);
-    }
+    if (nk >= 3) issue(2, 2);
+    if (kStages >= 5 && nk >= 4) issue(3, 3);
+    wait_tiles_and_sync(min(nk, static_cast<int64_t>(kStages - 1)) - 1);
     bf16x8 a0[4], b0[4], a1[4], b1[4];
     read_frags(0, 0, a0, b0);
     // Each MFMA is followed by one other memory instruction (a stage copy or a
@@ -410,8 +416,9 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         // Tile kt + 1 has landed for every wave (one later copy may still be
         // in flight: tile kt + 2, if there is one), and every wave is done
         // with the stage of tile kt - 1, which this step's copy overwrites.
-        if (kCopy || kt + 2 < nk) wait_tiles_and_sync(1);
-        else wait_tiles_and_sync(0);
+        // Copies issued after tile kt + 1: tiles kt + 2 .. min(kt + kStages - 2, nk - 1).
+        if (kCopy) wait_tiles_and_sync(kStages - 3);
+        else wait_tiles_and_sync(max(min(nk - 2 - kt, static_cast<int64_t>(kStages - 3)), int64_t(0)));
         const int sc = static_cast<int>((kt + kStages - 1) % kStages);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -462,8 +469,14 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     // of a 32x32 tile are formed sixteen at a time, each step over all sixteen
     // (independent exp and reciprocal latencies overlap).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no stage copy may still be writing LDS
-    bias_sh[tid] = bias_mine;
-    __syncthreads();  // every wave is done reading the stages; the biases are in LDS
+    if constexpr (kBiasInStages) {
+        __syncthreads();  // every wave is done reading the stages
+        bias_sh[tid] = bias_mine;
+        __syncthreads();  // the biases are in LDS
+    } else {
+        bias_sh[tid] = bias_mine;
+        __syncthreads();  // every wave is done reading the stages; the biases are in LDS
+    }
     constexpr int kOutCols = GLU ? 64 : 128;  // columns of a wave's output tile
     constexpr int kRowBytes = kOutCols * 2;
     constexpr int kChunks = kRowBytes / 16;   // 16-byte chunks per row
