@@ -10,7 +10,8 @@ Cache cannot hold the working set; the step is captured once per input set in
 a HIP graph and replayed (its three kernels are launch-bound at this size).
 
 Also measured and reported (same JSON line, "kernels"): the C1/C3 affine scan,
-the C3 RMSNorm-SiLU, and the C4 MoE route/permute/grouped-GEMM/combine, each as
+the C3 RMSNorm-SiLU, the C4 MoE route/permute/grouped-GEMM/combine and one
+window's salient read at the C5 model shape ("C5w"), each as
 average kernel time from HIP events, GB/s or TFLOP/s, and the roofline fraction.
 The CPU baseline is the oracle's single-threaded C port of the same C2 step
 (and, as an extra, the reference's PyTorch formulas on all host cores).
@@ -61,7 +62,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,3,4", help="extra configurations to measure (comma list of 1,3,4; '' for none)")
+    ap.add_argument("--configs", default="1,3,4,5",
+                    help="extra configurations to measure (comma list of 1,3,4,5; '' for none)")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -200,7 +202,7 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from koemi_amd import core, dense, moe, think, workloads
+    from koemi_amd import core, dense, memory, moe, think, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     device = torch.device("cuda:0")
@@ -401,6 +403,25 @@ def main() -> int:
         kernels["hipblaslt_reference_gemm"] = {"shape": [C4_PAIRS, C4_D, 2 * C4_H],
                                                "TFLOP/s": round(2 * C4_PAIRS * C4_D * 2 * C4_H / ms / 1e9, 1)}
         del c4, sc, y, a_mat, b_mat
+
+    if "5" in extra:
+        # One window's salient read at the C5 model shape (8 sequences, scan
+        # window 128, 16 salient slots, width 1024, fp32), as network.py:350-358
+        # issues it once per window.
+        log("C5 window salient read")
+        g5 = torch.Generator(device=device).manual_seed(1005)
+        b5, s5, l5, d5 = 8, 16, 128, 1024
+        r5 = lambda *shape: torch.randn(shape, generator=g5, device=device)
+        ck, cv, k5, v5, q5 = r5(b5, s5, d5), r5(b5, s5, d5), r5(b5, l5, d5), r5(b5, l5, d5), r5(b5, l5, d5)
+        cvalid = torch.rand((b5, s5), generator=g5, device=device) < 0.8
+        adm5 = torch.rand((b5, l5), generator=g5, device=device) < 0.1
+        ms = events_ms(lambda: memory.read_salient_window(ck, cv, cvalid, k5, v5, adm5, q5), args.kernel_iters)
+        flop = 4 * b5 * l5 * (s5 + l5) * d5
+        nbytes = 4 * (4 * b5 * l5 * d5 + 2 * b5 * s5 * d5) + b5 * (s5 + l5)
+        kernels["C5w.salient_read"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
+                                       "TFLOP/s": round(flop / ms / 1e9, 2), "shape_b_l_s_d": [b5, l5, s5, d5],
+                                       "note": "two rocBLAS product pairs + the HIP masked softmax, eager launches"}
+        del ck, cv, k5, v5, q5
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

@@ -211,6 +211,25 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
                        void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
                        int64_t width, int64_t capacity, int dtype, koemi_stream_t stream);
 
+/* Salient-memory read, LocalKeyValueMemory.read_salient_window of
+ * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
+ * the reference). For every batch row b and query t < length:
+ *   slots = [carried entries (carried) ; window entries (length)],
+ *   score_s = key_s . query_t / sqrt(width),
+ *   eligible: carried slot s with carried_valid[b, s], window slot j with
+ *   admission[b, j] and j < t,
+ *   out[b, t] = softmax over the eligible slots applied to the values (zero
+ *   when no slot is eligible).
+ * Keys, values and queries are [batch, *, width] in `dtype`, the masks bytes
+ * (0/1); out is [batch, length, width] in `dtype`. Products accumulate in fp32.
+ * carried may be 0 (carried pointers may then be NULL). */
+size_t koemi_salient_read_workspace_bytes(int64_t batch, int64_t carried, int64_t length, int64_t width,
+                                          int dtype);
+int koemi_salient_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                       const void* keys, const void* values, const uint8_t* admission, const void* queries,
+                       void* out, int64_t batch, int64_t carried, int64_t length, int64_t width, int dtype,
+                       void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
 /* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
  * without atomics: combined[t] = sum over the valid sorted pairs i of token t,
  * in ascending i, of y_i * w_i in fp32, w_i = pair_weights[i] (sorted order)

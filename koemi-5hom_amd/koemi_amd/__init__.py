@@ -6,7 +6,7 @@ Module map (reference front -> this package):
 * ``koemi.model.cuda_scan``     -> ``koemi_amd.cuda_scan`` (cuda_affine_scan)
 * ``koemi.cuda_kernels.core``   -> ``koemi_amd.core``      (fused_rmsnorm_silu)
 * ``koemi.cuda_kernels.think``  -> ``koemi_amd.think``     (causal_surprise, ...)
-* ``koemi.model.memory`` (LocalKeyValueMemory.salient_tail) -> ``koemi_amd.memory``
+* ``koemi.model.memory`` (LocalKeyValueMemory.read_salient_window, salient_tail) -> ``koemi_amd.memory``
 * ``koemi.cuda_kernels.moe``    -> ``koemi_amd.moe``       (route/permute/grouped MLP/combine)
 * ``koemi.cuda_kernels.loader`` -> ``koemi_amd.loader``
 
@@ -17,7 +17,7 @@ Every operator runs a hand-written HIP kernel from ``libkoemi_hip.so``
 from koemi_amd.core import fused_rmsnorm_silu, load_core_extension
 from koemi_amd.cuda_scan import cuda_affine_scan, diagnose_cuda_affine_scan
 from koemi_amd.dense import dense_affine_scan, native_cuda_available
-from koemi_amd.memory import salient_tail
+from koemi_amd.memory import read_salient_window, salient_tail
 from koemi_amd.moe import (
     combine_topk,
     expert_activation_counts,
@@ -46,6 +46,7 @@ __all__ = [
     "route_topk_learned",
     "route_topk_valid",
     "salience_admission",
+    "read_salient_window",
     "salient_tail",
     "surprise_from_logits",
 ]

@@ -23,6 +23,7 @@ BUILD_DIR = PACKAGE_DIR.parent / "_build"
 LIBRARY_DIR = PACKAGE_DIR / "_lib"
 LIBRARY_PATH = LIBRARY_DIR / "libkoemi_hip.so"
 INCLUDE_DIR = PACKAGE_DIR.parent.parent / "include"
+ROCM_LIB = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "lib"
 
 SOURCES = (
     "abi.hip",
@@ -34,6 +35,7 @@ SOURCES = (
     "moe_grouped_mlp.hip",
     "moe_combine.hip",
     "memory.hip",
+    "salient_read.hip",
 )
 
 ARCH = "gfx950"
@@ -93,8 +95,10 @@ def build_library(*, verbose: bool = False, jobs: int | None = None) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         list(pool.map(lambda pair: _compile(pair[0], pair[1], verbose), zip(sources, objects)))
     tmp = LIBRARY_PATH.with_suffix(".so.tmp")
+    # rocBLAS (the salient read's plain GEMMs): linked by soname librocblas.so.5, which
+    # resolves at run time to the rocBLAS PyTorch has loaded, on PyTorch's HIP runtime.
     cmd = [hipcc_path(), f"--offload-arch={ARCH}", "-mcode-object-version=5", "-shared", "-fPIC", "-o", str(tmp),
-           *map(str, objects)]
+           *map(str, objects), f"-L{ROCM_LIB}", "-lrocblas"]
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,9 +1,12 @@
-"""Salient (exact-recall) memory ring update on the GPU.
+"""Salient (exact-recall) memory on the GPU: ring read and ring update.
 
-Front for ``LocalKeyValueMemory.salient_tail`` (reference model/memory.py:431-455):
-the carried ring entries followed by the window's entries, the latest
-``capacity`` admitted ones kept in time order, invalid slots zeroed. Runs the
-HIP kernel ``koemi_salient_tail``; there is no torch fallback.
+Fronts for ``LocalKeyValueMemory.read_salient_window`` (reference
+model/memory.py:405-429: each query attends to the carried ring entries and to
+the window's admitted entries at earlier positions) and
+``LocalKeyValueMemory.salient_tail`` (memory.py:431-455: the carried ring
+entries followed by the window's entries, the latest ``capacity`` admitted
+ones kept in time order, invalid slots zeroed). They run ``koemi_salient_read``
+and ``koemi_salient_tail``; there is no torch fallback.
 """
 
 from __future__ import annotations
@@ -14,10 +17,95 @@ from torch import Tensor
 from koemi_amd import _native
 from koemi_amd.think import CudaThinkUnavailableError, CudaThinkValidationError
 
-__all__ = ["salient_tail"]
+__all__ = ["read_salient_window", "salient_tail"]
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _MAX_CAPACITY = 4096
+
+
+def read_salient_window(
+    carried_keys: Tensor,
+    carried_values: Tensor,
+    carried_valid: Tensor,
+    keys: Tensor,
+    values: Tensor,
+    admission_mask: Tensor,
+    queries: Tensor,
+) -> Tensor:
+    """Salient read of one window (reference model/memory.py:405-429).
+
+    ``carried_*``: ``[B, S, D]``, ``[B, S, D]``, ``[B, S]`` bool (the ring);
+    window ``keys``/``values`` ``[B, L, D]``, ``admission_mask`` ``[B, L]`` bool and
+    ``queries`` ``[B, L, D]``. Query t attends, with scores ``key . query /
+    sqrt(D)``, to the valid carried entries and to the admitted window entries
+    at positions before t; rows with no such entry read zeros. Returns
+    ``[B, L, D]`` in the queries' dtype (fp32 accumulation).
+    """
+
+    tensors = {
+        "carried_keys": carried_keys,
+        "carried_values": carried_values,
+        "carried_valid": carried_valid,
+        "keys": keys,
+        "values": values,
+        "admission_mask": admission_mask,
+        "queries": queries,
+    }
+    for name, tensor in tensors.items():
+        if not isinstance(tensor, Tensor):
+            raise CudaThinkValidationError(f"{name} must be a torch.Tensor")
+        if tensor.device.type != "cuda":
+            raise CudaThinkValidationError(f"{name} must be on CUDA")
+    if len({t.device for t in tensors.values()}) != 1:
+        raise CudaThinkValidationError("read_salient_window tensors must be on the same CUDA device")
+    if queries.ndim != 3 or keys.shape != queries.shape or values.shape != queries.shape:
+        raise CudaThinkValidationError("keys, values and queries must have the same shape [batch, length, width]")
+    batch, length, width = queries.shape
+    if carried_keys.ndim != 3 or carried_values.shape != carried_keys.shape:
+        raise CudaThinkValidationError("carried keys and values must have the same shape [batch, carried, width]")
+    if carried_keys.shape[0] != batch or carried_keys.shape[2] != width:
+        raise CudaThinkValidationError("carried entries must match the window's batch and width")
+    carried = carried_keys.shape[1]
+    if carried_valid.shape != (batch, carried) or admission_mask.shape != (batch, length):
+        raise CudaThinkValidationError("carried_valid and admission_mask must be [batch, carried] and [batch, length]")
+    if carried_valid.dtype != torch.bool or admission_mask.dtype != torch.bool:
+        raise CudaThinkValidationError("carried_valid and admission_mask must be torch.bool")
+    if queries.dtype not in _SUPPORTED_DTYPES:
+        raise CudaThinkValidationError("queries must be float32, float16 or bfloat16")
+    if any(t.dtype != queries.dtype for t in (keys, values, carried_keys, carried_values)):
+        raise CudaThinkValidationError("keys, values, queries and the carried entries must share a dtype")
+    if width < 1:
+        raise CudaThinkValidationError("width must be positive")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise CudaThinkUnavailableError(str(error)) from error
+
+    device = queries.device
+    out = torch.empty_like(queries, memory_format=torch.contiguous_format)
+    if batch == 0 or length == 0:
+        return out
+    dtype = _native.dtype_code(queries.dtype)
+    workspace = torch.empty(
+        _native.query("koemi_salient_read_workspace_bytes", batch, carried, length, width, dtype),
+        dtype=torch.uint8,
+        device=device,
+    )
+    contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, admission_mask, queries)]
+    _native.call(
+        "koemi_salient_read",
+        *(_native.ptr(t) if t.numel() else None for t in contiguous),
+        _native.ptr(out),
+        batch,
+        carried,
+        length,
+        width,
+        dtype,
+        _native.ptr(workspace),
+        workspace.numel(),
+        _native.stream_of(device),
+    )
+    return out
 
 
 def salient_tail(

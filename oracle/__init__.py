@@ -223,6 +223,42 @@ def admission(scores: np.ndarray, valid: np.ndarray, *, threshold: float | None 
     return np.asarray(valid, dtype=bool) & (s > np.float32(tau)), tau
 
 
+def read_salient_window(
+    carried_keys: np.ndarray,
+    carried_values: np.ndarray,
+    carried_valid: np.ndarray,
+    keys: np.ndarray,
+    values: np.ndarray,
+    admission: np.ndarray,
+    queries: np.ndarray,
+) -> np.ndarray:
+    """Salient read (model/memory.py:405-429), in float64: scores of every query
+    against [carried keys ; window keys] divided by sqrt(width); carried slot s
+    eligible when carried_valid, window slot j when admitted and j < t; softmax
+    over the eligible slots (rows with none read zeros); weighted sum of
+    [carried values ; window values]."""
+
+    ck = np.asarray(carried_keys, dtype=np.float64)
+    k = np.asarray(keys, dtype=np.float64)
+    q = np.asarray(queries, dtype=np.float64)
+    all_k = np.concatenate([ck, k], axis=1)
+    all_v = np.concatenate([np.asarray(carried_values, np.float64), np.asarray(values, np.float64)], axis=1)
+    b, length, width = q.shape
+    s = ck.shape[1]
+    pos = np.arange(length)
+    current = np.asarray(admission, bool)[:, None, :] & (pos[:, None] > pos[None, :])[None]
+    carried = np.broadcast_to(np.asarray(carried_valid, bool)[:, None, :], (b, length, s))
+    eligible = np.concatenate([carried, current], axis=-1)
+    scores = np.einsum("bsd,btd->bts", all_k, q) / np.sqrt(width)
+    scores = np.where(eligible, scores, -np.inf)
+    any_slot = eligible.any(axis=-1, keepdims=True)
+    m = np.where(any_slot, scores.max(axis=-1, keepdims=True, initial=-np.inf), 0.0)
+    e = np.where(eligible, np.exp(scores - m), 0.0)
+    total = e.sum(axis=-1, keepdims=True)
+    w = np.where(any_slot, e / np.where(total > 0, total, 1.0), 0.0)
+    return np.einsum("bts,bsd->btd", w, all_v)
+
+
 def salient_tail(
     carried_keys: np.ndarray,
     carried_values: np.ndarray,

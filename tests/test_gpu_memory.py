@@ -1,4 +1,5 @@
-"""Salient-memory ring update (model/memory.py:431-455) on the GPU against the oracle, bit for bit."""
+"""Salient memory on the GPU against the oracle: ring update (model/memory.py:431-455)
+bit for bit, ring read (memory.py:405-429) within the tolerances stated below."""
 
 from __future__ import annotations
 
@@ -7,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from koemi_amd import memory
+from koemi_amd import memory, think
 
 pytestmark = pytest.mark.gpu
 
@@ -60,3 +61,55 @@ def test_salient_tail_rejects_bad_inputs(device):
     with pytest.raises(ValueError, match="share a dtype"):
         memory.salient_tail(k[:, :0].half(), k[:, :0].half(), torch.zeros((1, 0), dtype=torch.bool, device=device), k, k,
                             torch.ones((1, 4), dtype=torch.bool, device=device), 2)
+
+
+# ------------------------------------------------------------ salient read
+# read_salient_window (model/memory.py:405-429) against the float64 oracle on
+# the same (rounded) inputs. fp32: rtol 1e-4, atol 1e-5 x max|value| (fp32
+# products on rocBLAS, fp32 softmax). f16/bf16: the weights and the output are
+# rounded to the input dtype as in the reference, so |err| <= 2^-7 x max|value|.
+
+
+def _read_case(seed, b, s, length, d, p, dtype):
+    g = torch.Generator().manual_seed(seed)
+    t = lambda *shape: torch.randn(shape, generator=g).to(dtype)
+    ck, cv, k, v, q = t(b, s, d), t(b, s, d), t(b, length, d), t(b, length, d), t(b, length, d)
+    cvalid, adm = torch.rand((b, s), generator=g) < p, torch.rand((b, length), generator=g) < p
+    return ck, cv, cvalid, k, v, adm, q
+
+
+@pytest.mark.parametrize(
+    "b, s, length, d, p, dtype",
+    [
+        (2, 16, 128, 64, 0.3, torch.float32),      # default model: 16 salient slots, 128-token window
+        (8, 16, 128, 1024, 0.1, torch.float32),    # C5 width
+        (3, 16, 128, 256, 0.5, torch.bfloat16),
+        (2, 5, 37, 24, 0.7, torch.float16),
+        (2, 0, 20, 8, 0.5, torch.float32),         # empty ring
+        (1, 4, 1, 16, 1.0, torch.float32),         # one query: carried slots only
+        (3, 16, 64, 32, 0.0, torch.bfloat16),      # nothing eligible: zeros
+    ],
+)
+def test_read_salient_window_matches_oracle(device, b, s, length, d, p, dtype):
+    case = _read_case(b * 7 + length + d, b, s, length, d, p, dtype)
+    got = memory.read_salient_window(*(x.to(device) for x in case)).float().cpu().numpy()
+    want = oracle.read_salient_window(*(x.float().numpy() if x.is_floating_point() else x.numpy() for x in case))
+    vmax = max(float(case[1].float().abs().max()) if s else 0.0, float(case[4].float().abs().max()))
+    err = np.abs(got - want)
+    print(f"salient read b={b} s={s} L={length} d={d} {dtype}: max_abs={err.max():.3e} max|v|={vmax:.3e}", flush=True)
+    if dtype == torch.float32:
+        assert np.all(err <= 1e-4 * np.abs(want) + 1e-5 * vmax)
+    else:
+        assert np.all(err <= 2.0**-7 * vmax)
+    if p == 0.0:
+        assert np.all(got == 0.0)
+
+
+def test_read_salient_window_rejects_bad_inputs(device):
+    ck, cv, cvalid, k, v, adm, q = (x.to(device) for x in _read_case(1, 2, 3, 5, 4, 0.5, torch.float32))
+    with pytest.raises(think.CudaThinkValidationError, match="share a dtype"):
+        memory.read_salient_window(ck, cv, cvalid, k.half(), v, adm, q)
+    with pytest.raises(think.CudaThinkValidationError, match="must be on CUDA"):
+        memory.read_salient_window(ck, cv, cvalid, k, v, adm, q.cpu())
+    with pytest.raises(think.CudaThinkValidationError, match="same shape"):
+        memory.read_salient_window(ck, cv, cvalid, k[:, :4], v, adm, q)

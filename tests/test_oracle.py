@@ -273,6 +273,74 @@ def _torch_salient_tail(ck, cv, cvalid, k, v, adm, capacity):
     return sk, sv, ok
 
 
+def _torch_read_salient_window(ck, cv, cvalid, k, v, adm, q):
+    """The reference expression of model/memory.py:405-429, in torch on the CPU (float64)."""
+    batch_size, length, width = q.shape
+    carried_length = ck.shape[1]
+    all_keys = torch.cat((ck, k), dim=1)
+    all_values = torch.cat((cv, v), dim=1)
+    carried_eligible = cvalid.unsqueeze(1).expand(batch_size, length, carried_length)
+    positions = torch.arange(length)
+    prior = positions.unsqueeze(1) > positions.unsqueeze(0)
+    current_eligible = adm.unsqueeze(1) & prior.unsqueeze(0)
+    eligible = torch.cat((carried_eligible, current_eligible), dim=-1)
+    scores = torch.einsum("bsd,btd->bts", all_keys, q) / math.sqrt(width)
+    masked = scores.masked_fill(~eligible, float("-inf"))
+    any_slot = eligible.any(dim=-1, keepdim=True)
+    weights = torch.where(any_slot, torch.softmax(masked, dim=-1), torch.zeros(()))
+    return torch.einsum("bts,bsd->btd", weights, all_values)
+
+
+def _read_case(rng, b, s, length, d, p):
+    ck, cv = rng.normal(size=(b, s, d)), rng.normal(size=(b, s, d))
+    k, v, q = rng.normal(size=(b, length, d)), rng.normal(size=(b, length, d)), rng.normal(size=(b, length, d))
+    return ck, cv, rng.random((b, s)) < p, k, v, rng.random((b, length)) < p, q
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_read_salient_window_matches_the_reference_expression(seed):
+    rng = np.random.default_rng(100 + seed)
+    case = _read_case(rng, 2, int(rng.integers(0, 5)), int(rng.integers(1, 24)), int(rng.integers(1, 9)),
+                      rng.uniform(0.0, 1.0))
+    got = oracle.read_salient_window(*case)
+    want = _torch_read_salient_window(*(torch.from_numpy(np.asarray(x)) for x in case)).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_read_salient_window_closed_forms():
+    rng = np.random.default_rng(7)
+    ck, cv, _, k, v, _, q = _read_case(rng, 1, 3, 6, 4, 0.5)
+    none = oracle.read_salient_window(ck, cv, np.zeros((1, 3), bool), k, v, np.zeros((1, 6), bool), q)
+    assert np.all(none == 0.0)  # no eligible slot: zeros
+    # only carried slot 1 valid, nothing admitted: every query reads value 1 exactly
+    one = oracle.read_salient_window(ck, cv, np.array([[False, True, False]]), k, v, np.zeros((1, 6), bool), q)
+    np.testing.assert_array_equal(one[0], np.broadcast_to(cv[0, 1], (6, 4)))
+    # window slot 2 admitted only: queries t <= 2 read zeros, later ones value 2 exactly
+    adm = np.zeros((1, 6), bool)
+    adm[0, 2] = True
+    w2 = oracle.read_salient_window(ck, cv, np.zeros((1, 3), bool), k, v, adm, q)
+    assert np.all(w2[0, :3] == 0.0)
+    np.testing.assert_array_equal(w2[0, 3:], np.broadcast_to(v[0, 2], (3, 4)))
+    # zero queries: equal scores, so the read is the mean of the eligible values
+    cvalid = np.array([[True, False, True]])
+    adm = np.ones((1, 6), bool)
+    mean = oracle.read_salient_window(ck, cv, cvalid, k, v, adm, np.zeros_like(q))
+    for t in range(6):
+        rows = np.concatenate([cv[0, [0, 2]], v[0, :t]], axis=0)
+        np.testing.assert_allclose(mean[0, t], rows.mean(axis=0), rtol=1e-13, atol=1e-13)
+
+
+def test_read_salient_window_is_causal():
+    rng = np.random.default_rng(9)
+    case = list(_read_case(rng, 2, 4, 10, 3, 0.6))
+    base = oracle.read_salient_window(*case)
+    for i in (3, 4, 5):  # keys, values, admission of the window from position 5 on
+        case[i] = case[i].copy()
+        case[i][:, 5:] = rng.normal(size=case[i][:, 5:].shape) if i != 5 else ~case[i][:, 5:]
+    changed = oracle.read_salient_window(*case)
+    np.testing.assert_array_equal(changed[:, :6], base[:, :6])  # query t sees window slots j < t only
+
+
 def test_salient_tail_known_answer():
     kat = GOLDEN["salient_tail_latest"]
     adm = np.array([kat["admission"]])
