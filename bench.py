@@ -107,6 +107,139 @@ TRAFFIC_KERNELS = {
 COPY_BYTES = 512 * 2**20  # the calibration copy reads and writes this many bytes
 
 
+def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
+    """The reference's PyTorch formulas for each measured row, on the host cores.
+
+    Each is timed on a bounded sample of its configuration (median of up to
+    five runs after one warmup, within ``budget_s`` per row) and scaled to the
+    full configuration by the sample's share of the work; the samples have the
+    configuration's shapes and distributions.
+    """
+
+    import statistics
+
+    import torch
+    import torch.nn.functional as F
+
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(99)
+    out = {}
+
+    def median_ms(fn) -> float:
+        fn()
+        times, t0 = [], time.perf_counter()
+        while len(times) < 5 and (not times or time.perf_counter() - t0 < budget_s):
+            t1 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t1)
+        return statistics.median(times) * 1000.0
+
+    def seq_scan(a, b):  # the tests' sequential recurrence (test_dense_cuda.py:21-33)
+        h = torch.zeros_like(a[:, 0])
+        res = torch.empty_like(a)
+        for t in range(a.shape[1]):
+            h = a[:, t] * h + b[:, t]
+            res[:, t] = h
+        return res
+
+    def hillis_steele(a, b):  # the model path, model/scan.py:17-30
+        coef, val, off, n = a, b, 1, a.shape[1]
+        while off < n:
+            sc = torch.cat((torch.ones_like(coef[:, :off]), coef[:, : n - off]), dim=1)
+            sv = torch.cat((torch.zeros_like(val[:, :off]), val[:, : n - off]), dim=1)
+            val = coef * sv + val
+            coef = coef * sc
+            off *= 2
+        return val
+
+    if "1" in extra:
+        a = torch.rand((4, 1024, 256), generator=g) * 0.199 + 0.8
+        b = torch.randn((4, 1024, 256), generator=g)
+        out["C1.affine_scan"] = {"ms": round(median_ms(lambda: seq_scan(a, b)), 3), "sample": "full C1, sequential loop",
+                                 "ms_model_path": round(median_ms(lambda: hillis_steele(a, b)), 3)}
+    if "3" in extra:
+        a = torch.sigmoid(torch.randn((1, 4096, 1024), generator=g) + 2.0)
+        b = 0.5 * torch.randn((1, 4096, 1024), generator=g)
+        out["C3.affine_scan"] = {"ms": round(32 * median_ms(lambda: seq_scan(a, b)), 3),
+                                 "sample": "1 of the 32 sequences, sequential loop, x32",
+                                 "ms_model_path": round(32 * median_ms(lambda: hillis_steele(a, b)), 3)}
+        del a, b
+        x = torch.randn((8192, 1024), generator=g).to(torch.bfloat16)
+        gam = (1 + 0.02 * torch.randn((1024,), generator=g)).to(torch.bfloat16)
+
+        def norm():  # core/rmsnorm_silu.py fallback formula (layers.py:14-16 + F.silu), fp32
+            xf = x.float()
+            return F.silu(xf * torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + 1e-6) * gam.float()).to(x.dtype)
+
+        out["C3.rmsnorm_silu"] = {"ms": round(16 * median_ms(norm), 3), "sample": "8192 of 131072 rows, x16"}
+    if "4" in extra:
+        T, D, H, E, K = C4_T, C4_D, C4_H, C4_E, C4_K
+        tok = torch.randint(0, 256, (T,), generator=g)
+        prev = torch.cat((torch.tensor([256]), tok[:-1]))
+        valid = torch.ones((T,), dtype=torch.bool)
+
+        def route():  # experts.py:30-38, 283-289 (int64)
+            def mix(v):
+                v = ((v >> 16) ^ v) * 0x45D9F3B % (1 << 32)
+                v = ((v >> 16) ^ v) * 0x45D9F3B % (1 << 32)
+                return (v >> 16) ^ v
+            h = mix((tok * 1000003 + prev * 97409) % (1 << 32))
+            e = torch.stack([(h + k * 0x9E3779B9) % E for k in range(K)], dim=-1)
+            return torch.where(valid.unsqueeze(-1), e, torch.full_like(e, -1))
+
+        out["C4.route_hash"] = {"ms": round(median_ms(route), 3), "sample": "full C4"}
+        assign = route()
+        ctx = torch.randn((T, D), generator=g).to(torch.bfloat16)
+
+        def permute():  # experts.py:189-197: stable argsort by expert, gather rows
+            keys = torch.where(assign >= 0, assign, torch.full_like(assign, E)).reshape(-1)
+            order = torch.argsort(keys, stable=True)
+            return ctx[order // K], order
+
+        out["C4.permute"] = {"ms": round(median_ms(permute), 3), "sample": "full C4"}
+        rows_e = 4096 // E  # a slice of the sorted pairs, equal per expert
+        xs = torch.randn((E, rows_e, D), generator=g).to(torch.bfloat16)
+        wg = (0.02 * torch.randn((E, H, D), generator=g)).to(torch.bfloat16)
+        wv = (0.02 * torch.randn((E, H, D), generator=g)).to(torch.bfloat16)
+        wo = (0.02 * torch.randn((E, D, H), generator=g)).to(torch.bfloat16)
+
+        def ffn():  # GatedFeedForward per expert (layers.py:27-29), fp32 on the host
+            for e in range(E):
+                xe = xs[e].float()
+                hgl = F.silu(xe @ wg[e].float().T) * (xe @ wv[e].float().T)
+                _ = hgl @ wo[e].float().T
+
+        out["C4.grouped_glu_ffn"] = {"ms": round(C4_PAIRS / 4096 * median_ms(ffn), 3),
+                                     "sample": "4096 of 65536 pairs (256 per expert), fp32, x16"}
+        y = torch.randn((C4_PAIRS, D), generator=g).to(torch.bfloat16)
+        idx = torch.arange(C4_PAIRS) // K
+
+        def combine():  # moe_kernels.cu:201-229 semantics: sum of y / k per token
+            acc = torch.zeros((T, D), dtype=torch.float32)
+            acc.index_add_(0, idx, y.float() / K)
+            return acc.to(torch.bfloat16)
+
+        out["C4.combine"] = {"ms": round(median_ms(combine), 3), "sample": "full C4"}
+    if "5" in extra:
+        b5, s5, l5, d5 = 8, 16, 128, 1024
+        ck, cv = torch.randn((b5, s5, d5), generator=g), torch.randn((b5, s5, d5), generator=g)
+        k5, v5, q5 = (torch.randn((b5, l5, d5), generator=g) for _ in range(3))
+        cvalid, adm = torch.rand((b5, s5), generator=g) < 0.8, torch.rand((b5, l5), generator=g) < 0.1
+
+        def read():  # model/memory.py:405-429
+            all_k, all_v = torch.cat((ck, k5), dim=1), torch.cat((cv, v5), dim=1)
+            pos = torch.arange(l5)
+            elig = torch.cat((cvalid.unsqueeze(1).expand(b5, l5, s5),
+                              adm.unsqueeze(1) & (pos.unsqueeze(1) > pos.unsqueeze(0)).unsqueeze(0)), dim=-1)
+            sc = torch.einsum("bsd,btd->bts", all_k, q5) / math.sqrt(d5)
+            w = torch.softmax(sc.masked_fill(~elig, float("-inf")), dim=-1)
+            w = torch.where(elig.any(dim=-1, keepdim=True), w, torch.zeros(()))
+            return torch.einsum("bts,bsd->btd", w, all_v)
+
+        out["C5w.salient_read"] = {"ms": round(median_ms(read), 3), "sample": "full C5 window"}
+    return out
+
+
 def traffic_probe() -> int:
     """Launch each HBM kernel at its configuration (and one device copy of known size)."""
 
@@ -464,6 +597,12 @@ def main() -> int:
                 break
         extras["cpu_torch_reference_formulas"] = {"value": round(reps * C2_TOKENS / elapsed, 1), "unit": "tokens/s",
                                                   "cores": threads, "sample": f"{reps} C2 steps, fp32 torch CPU"}
+        log("CPU reference formulas of the other rows")
+        cpu_rows = cpu_reference_times(extra, threads, budget_s=args.cpu_seconds / 4)
+        for key, row in cpu_rows.items():
+            if key in kernels and "ms" in kernels[key]:
+                row["gpu_speedup"] = round(row["ms"] / kernels[key]["ms"], 1)
+        extras["cpu_reference_rows"] = {"cores": threads, "rows": cpu_rows}
 
     result = {
         "metric": "HERM tokens/s on 1 MI355X (C2: fused RMSNorm-SiLU + surprise + 0.9-quantile admission)",
