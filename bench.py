@@ -36,6 +36,7 @@ for _path in (ROOT, ROOT / "koemi-5hom_amd"):
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA
 C2_TOKENS = 16 * 2048
 
 # Algorithmic bytes / FLOPs per launch.
@@ -50,6 +51,7 @@ C4_PAIRS = C4_T * C4_K
 C4_ROUTE_BYTES = C4_T * (8 + 8 + 1) + C4_PAIRS * 8
 C4_PERMUTE_BYTES = C4_T * C4_D * 2 + C4_PAIRS * C4_D * 2 + C4_PAIRS * 8 + C4_T + 2 * C4_PAIRS * 8 + (C4_E + 1) * 8
 C4_GEMM_FLOP = 6 * C4_D * C4_H * C4_PAIRS
+C3G_FLOP = 2 * 2 * 32 * 4096 * 1024 * 1024                              # two width x width products
 C4_COMBINE_BYTES = C4_PAIRS * C4_D * 2 + C4_T * C4_D * 2 + C4_PAIRS * 8 + (C4_E + 1) * 8
 
 
@@ -62,8 +64,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,3,4,5",
-                    help="extra configurations to measure (comma list of 1,3,4,5; '' for none)")
+    ap.add_argument("--configs", default="1,3,4,5,g",
+                    help="extra configurations to measure (comma list of 1,3,4,5,g; '' for none)")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -220,6 +222,16 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
             return acc.to(torch.bfloat16)
 
         out["C4.combine"] = {"ms": round(median_ms(combine), 3), "sample": "full C4"}
+    if "g" in extra:
+        ug = torch.randn((8192, 1024), generator=g)
+        lin_r, lin_c = torch.nn.Linear(1024, 1024), torch.nn.Linear(1024, 1024)
+
+        def gates():  # BoundedRecurrentState.gates, model/memory.py:14-30
+            with torch.no_grad():
+                bounded = 2.0**-8 + ((1.0 - 2.0**-8) - 2.0**-8) * torch.sigmoid(lin_r(ug))
+                return bounded, (1.0 - bounded) * torch.tanh(lin_c(ug))
+
+        out["C3g.recurrent_gates"] = {"ms": round(16 * median_ms(gates), 3), "sample": "8192 of 131072 rows, x16"}
     if "5" in extra:
         b5, s5, l5, d5 = 8, 16, 128, 1024
         ck, cv = torch.randn((b5, s5, d5), generator=g), torch.randn((b5, s5, d5), generator=g)
@@ -335,7 +347,7 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from koemi_amd import core, dense, memory, moe, think, workloads
+    from koemi_amd import core, dense, memory, moe, recurrent, think, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     device = torch.device("cuda:0")
@@ -555,6 +567,24 @@ def main() -> int:
                                        "TFLOP/s": round(flop / ms / 1e9, 2), "shape_b_l_s_d": [b5, l5, s5, d5],
                                        "note": "two rocBLAS product pairs + the HIP masked softmax, eager launches"}
         del ck, cv, k5, v5, q5
+
+    if "g" in extra:
+        # The recurrent gates and the window scan at the C3 shape ([32, 4096, 1024]
+        # fp32), the step before the C3 scan (network.py:306-310).
+        log("C3g recurrent gates + scan (generating 0.5 GiB of inputs)")
+        gg = torch.Generator(device=device).manual_seed(1006)
+        ug = torch.randn((32, 4096, 1024), generator=gg, device=device)
+        wts = [(1024 ** -0.5) * torch.randn(shape, generator=gg, device=device)
+               for shape in ((1024, 1024), (1024,), (1024, 1024), (1024,))]
+        vg = torch.ones((32, 4096), dtype=torch.bool, device=device)
+        ms = events_ms(lambda: recurrent.recurrent_gates(ug, *wts, vg), max(3, args.kernel_iters // 4))
+        kernels["C3g.recurrent_gates"] = {"ms": round(ms, 5), "TFLOP/s": round(C3G_FLOP / ms / 1e9, 1),
+                                          "frac_mfma_fp32": round(C3G_FLOP / ms / 1e9 / FP32_PEAK_TFLOPS, 4),
+                                          "note": "two fp32 rocBLAS products + the HIP gate epilogue"}
+        ms = events_ms(lambda: recurrent.recurrent_scan(ug, *wts, vg), max(3, args.kernel_iters // 4))
+        kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
+                                         "note": "gates then the affine scan (network.py:306-310)"}
+        del ug, wts, vg
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

@@ -211,6 +211,20 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
                        void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
                        int64_t width, int64_t capacity, int dtype, koemi_stream_t stream);
 
+/* Bounded recurrent gates, BoundedRecurrentState.gates of model/memory.py:14-30
+ * with the masking of network.py:306-309 (a torch composite in the
+ * reference): for input rows u (rows x width, `dtype`),
+ *   retention = sigmoid(u W_r^T + b_r), a = 2^-8 + (1 - 2^-7) retention,
+ *   b = (1 - a) tanh(u W_c^T + b_c),
+ * and where `valid` (one byte per row, may be NULL) is 0: a = 1, b = 0.
+ * W_r, W_c are width x width (out x in), biases width; a and b are rows x width
+ * in `dtype`. Products accumulate in fp32. width % 4 == 0. */
+size_t koemi_recurrent_gates_workspace_bytes(int64_t rows, int64_t width);
+int koemi_recurrent_gates(const void* input, const void* retention_weight, const void* retention_bias,
+                          const void* candidate_weight, const void* candidate_bias, const uint8_t* valid,
+                          void* retention_out, void* increment_out, int64_t rows, int64_t width, int dtype,
+                          void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
 /* Salient-memory read, LocalKeyValueMemory.read_salient_window of
  * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
  * the reference). For every batch row b and query t < length:

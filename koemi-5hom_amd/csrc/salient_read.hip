@@ -27,6 +27,11 @@
 #include <mutex>
 
 namespace koemi {
+
+// The rocBLAS handle of a device (blas.hip); callers hold g_blas_mutex.
+rocblas_handle blas_handle(int device);
+extern std::mutex g_blas_mutex;
+
 namespace {
 
 constexpr int kSoftmaxWaves = 4;
@@ -76,11 +81,6 @@ __global__ void fp32_to_dtype_kernel(const float* __restrict__ src, T* __restric
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = from_f32<T>(src[i]);
 }
-
-// One rocBLAS handle per device, created on first use; calls are serialised
-// (a handle carries its stream).
-std::mutex g_blas_mutex;
-rocblas_handle g_blas[64] = {};
 
 rocblas_datatype blas_type(int dtype) {
     switch (dtype) {
@@ -149,13 +149,10 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
     const hipStream_t s = as_stream(stream);
 
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(KOEMI_ERR_LAUNCH, "salient read: no device");
+    if (hipGetDevice(&dev) != hipSuccess) return fail(KOEMI_ERR_LAUNCH, "salient read: no device");
     std::lock_guard<std::mutex> lock(g_blas_mutex);
-    if (!g_blas[dev] && rocblas_create_handle(&g_blas[dev]) != rocblas_status_success) {
-        g_blas[dev] = nullptr;
-        return fail(KOEMI_ERR_LAUNCH, "salient read: rocblas_create_handle failed");
-    }
-    rocblas_handle h = g_blas[dev];
+    rocblas_handle h = blas_handle(dev);
+    if (!h) return fail(KOEMI_ERR_LAUNCH, "salient read: no rocBLAS handle");
     if (rocblas_set_stream(h, s) != rocblas_status_success ||
         rocblas_set_pointer_mode(h, rocblas_pointer_mode_host) != rocblas_status_success)
         return fail(KOEMI_ERR_LAUNCH, "salient read: rocblas stream setup failed");

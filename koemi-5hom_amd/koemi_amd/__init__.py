@@ -7,17 +7,20 @@ Module map (reference front -> this package):
 * ``koemi.cuda_kernels.core``   -> ``koemi_amd.core``      (fused_rmsnorm_silu)
 * ``koemi.cuda_kernels.think``  -> ``koemi_amd.think``     (causal_surprise, ...)
 * ``koemi.model.memory`` (LocalKeyValueMemory.read_salient_window, salient_tail) -> ``koemi_amd.memory``
+* ``koemi.model.memory`` (BoundedRecurrentState.gates, + network.py:306-310 scan) -> ``koemi_amd.recurrent``
 * ``koemi.cuda_kernels.moe``    -> ``koemi_amd.moe``       (route/permute/grouped MLP/combine)
 * ``koemi.cuda_kernels.loader`` -> ``koemi_amd.loader``
 
-Every operator runs a hand-written HIP kernel from ``libkoemi_hip.so``
-(C ABI in ``include/koemi_hip.h``); none falls back to CPU or to PyTorch.
+Every operator runs from ``libkoemi_hip.so`` (C ABI in ``include/koemi_hip.h``):
+hand-written HIP kernels, with rocBLAS for the plain GEMMs of the salient read
+and the recurrent gates; none falls back to CPU or to PyTorch.
 """
 
 from koemi_amd.core import fused_rmsnorm_silu, load_core_extension
 from koemi_amd.cuda_scan import cuda_affine_scan, diagnose_cuda_affine_scan
 from koemi_amd.dense import dense_affine_scan, native_cuda_available
 from koemi_amd.memory import read_salient_window, salient_tail
+from koemi_amd.recurrent import recurrent_gates, recurrent_scan
 from koemi_amd.moe import (
     combine_topk,
     expert_activation_counts,
@@ -47,6 +50,8 @@ __all__ = [
     "route_topk_valid",
     "salience_admission",
     "read_salient_window",
+    "recurrent_gates",
+    "recurrent_scan",
     "salient_tail",
     "surprise_from_logits",
 ]

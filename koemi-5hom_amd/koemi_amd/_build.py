@@ -36,6 +36,8 @@ SOURCES = (
     "moe_combine.hip",
     "memory.hip",
     "salient_read.hip",
+    "gates.hip",
+    "blas.hip",
 )
 
 ARCH = "gfx950"

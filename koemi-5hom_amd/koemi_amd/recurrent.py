@@ -1,0 +1,129 @@
+"""Bounded recurrent state on the GPU: gates and the working-state scan.
+
+Fronts for ``BoundedRecurrentState.gates`` (reference model/memory.py:14-30)
+and the first steps of the HERM window (network.py:306-310: gates, masking of
+invalid positions, affine scan from the carried working state). The gates run
+``koemi_recurrent_gates`` (two rocBLAS products with fp32 accumulation and one
+HIP epilogue kernel); the scan runs the dense affine-scan kernel. There is no
+torch fallback. Inference only (no autograd through the gates).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from koemi_amd import _native
+from koemi_amd.dense import DenseCudaUnavailableError, DenseCudaValidationError, dense_affine_scan
+
+__all__ = ["recurrent_gates", "recurrent_scan"]
+
+_SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def recurrent_gates(
+    input_state: Tensor,
+    retention_weight: Tensor,
+    retention_bias: Tensor,
+    candidate_weight: Tensor,
+    candidate_bias: Tensor,
+    valid_mask: Tensor | None = None,
+) -> tuple[Tensor, Tensor]:
+    """(retention, increment) of ``BoundedRecurrentState.gates`` (memory.py:14-30).
+
+    ``input_state`` ``[..., D]``; the weights ``[D, D]`` and biases ``[D]`` of
+    ``retention_projection`` and ``candidate_projection`` (``nn.Linear``
+    layout: out x in). ``retention = 2^-8 + (1 - 2^-7) * sigmoid(u W_r^T + b_r)``,
+    ``increment = (1 - retention) * tanh(u W_c^T + b_c)``. With ``valid_mask``
+    (``input_state.shape[:-1]``, bool) invalid positions get retention 1 and
+    increment 0, as network.py:307-309 applies them. Outputs in the input
+    dtype; products accumulate in fp32.
+    """
+
+    tensors = {
+        "input_state": input_state,
+        "retention_weight": retention_weight,
+        "retention_bias": retention_bias,
+        "candidate_weight": candidate_weight,
+        "candidate_bias": candidate_bias,
+    }
+    if valid_mask is not None:
+        tensors["valid_mask"] = valid_mask
+    for name, tensor in tensors.items():
+        if not isinstance(tensor, Tensor):
+            raise DenseCudaValidationError(f"{name} must be a torch.Tensor")
+        if tensor.device.type != "cuda":
+            raise DenseCudaValidationError(f"{name} must be on CUDA")
+    if len({t.device for t in tensors.values()}) != 1:
+        raise DenseCudaValidationError("recurrent gate tensors must be on the same CUDA device")
+    if input_state.ndim < 1:
+        raise DenseCudaValidationError("input_state must have a trailing feature dimension")
+    width = input_state.shape[-1]
+    for name in ("retention_weight", "candidate_weight"):
+        if tensors[name].shape != (width, width):
+            raise DenseCudaValidationError(f"{name} must have shape [{width}, {width}]")
+    for name in ("retention_bias", "candidate_bias"):
+        if tensors[name].shape != (width,):
+            raise DenseCudaValidationError(f"{name} must have shape [{width}]")
+    if input_state.dtype not in _SUPPORTED_DTYPES:
+        raise DenseCudaValidationError("unsupported dtype for the recurrent gates (float16, bfloat16, float32)")
+    if any(t.dtype != input_state.dtype for n, t in tensors.items() if n != "valid_mask"):
+        raise DenseCudaValidationError("input_state and the gate parameters must have the same dtype")
+    if valid_mask is not None and (valid_mask.dtype != torch.bool or valid_mask.shape != input_state.shape[:-1]):
+        raise DenseCudaValidationError("valid_mask must be a bool tensor of shape input_state.shape[:-1]")
+    if width % 4 != 0:
+        raise DenseCudaValidationError("the feature width must be a multiple of 4")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise DenseCudaUnavailableError(str(error)) from error
+
+    device = input_state.device
+    rows = input_state.numel() // width if width else 0
+    retention = torch.empty(input_state.shape, device=device, dtype=input_state.dtype)
+    increment = torch.empty_like(retention)
+    if rows == 0:
+        return retention, increment
+    workspace = torch.empty(_native.query("koemi_recurrent_gates_workspace_bytes", rows, width), dtype=torch.uint8,
+                            device=device)
+    u = input_state.contiguous()
+    params = [t.contiguous() for t in (retention_weight, retention_bias, candidate_weight, candidate_bias)]
+    mask = valid_mask.contiguous() if valid_mask is not None else None
+    _native.call(
+        "koemi_recurrent_gates",
+        _native.ptr(u),
+        *(_native.ptr(t) for t in params),
+        _native.ptr(mask) if mask is not None else None,
+        _native.ptr(retention),
+        _native.ptr(increment),
+        rows,
+        width,
+        _native.dtype_code(input_state.dtype),
+        _native.ptr(workspace),
+        workspace.numel(),
+        _native.stream_of(device),
+    )
+    return retention, increment
+
+
+def recurrent_scan(
+    input_state: Tensor,
+    retention_weight: Tensor,
+    retention_bias: Tensor,
+    candidate_weight: Tensor,
+    candidate_bias: Tensor,
+    valid_mask: Tensor,
+    initial: Tensor | None = None,
+) -> Tensor:
+    """Working states of one window (network.py:306-310).
+
+    ``input_state`` ``[B, L, D]``, ``valid_mask`` ``[B, L]``, ``initial``
+    ``[B, D]`` (zeros when omitted): gates with invalid positions masked to
+    (1, 0), then ``h_t = a_t h_{t-1} + b_t`` from ``initial``.
+    """
+
+    if not isinstance(input_state, Tensor) or input_state.ndim != 3:
+        raise DenseCudaValidationError("input_state must be a [batch, length, width] tensor")
+    retention, increment = recurrent_gates(input_state, retention_weight, retention_bias, candidate_weight,
+                                           candidate_bias, valid_mask)
+    return dense_affine_scan(retention, increment, initial)

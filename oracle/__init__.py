@@ -223,6 +223,25 @@ def admission(scores: np.ndarray, valid: np.ndarray, *, threshold: float | None 
     return np.asarray(valid, dtype=bool) & (s > np.float32(tau)), tau
 
 
+def recurrent_gates(u, retention_weight, retention_bias, candidate_weight, candidate_bias, valid=None):
+    """BoundedRecurrentState.gates (model/memory.py:14-30) in float64, with the
+    masking of network.py:307-309 when `valid` is given:
+    a = 2^-8 + ((1 - 2^-8) - 2^-8) sigmoid(u W_r^T + b_r), b = (1 - a) tanh(u W_c^T + b_c),
+    invalid rows a = 1, b = 0."""
+
+    x = np.asarray(u, dtype=np.float64)
+    zr = x @ np.asarray(retention_weight, np.float64).T + np.asarray(retention_bias, np.float64)
+    zc = x @ np.asarray(candidate_weight, np.float64).T + np.asarray(candidate_bias, np.float64)
+    lo, hi = 2.0**-8, 1.0 - 2.0**-8
+    a = lo + (hi - lo) / (1.0 + np.exp(-zr))
+    b = (1.0 - a) * np.tanh(zc)
+    if valid is not None:
+        keep = np.asarray(valid, bool)[..., None]
+        a = np.where(keep, a, 1.0)
+        b = np.where(keep, b, 0.0)
+    return a, b
+
+
 def read_salient_window(
     carried_keys: np.ndarray,
     carried_values: np.ndarray,

@@ -1,0 +1,82 @@
+"""Bounded recurrent gates (model/memory.py:14-30) and the window's working-state
+scan (network.py:306-310) on the GPU against the float64 oracle.
+
+Tolerances: fp32 products accumulate in fp32 over the width, so gates are
+within 2e-5 absolute (|a|, |b| < 1) and the scanned states within 1e-4 (a < 1
+keeps the recurrence contractive); bf16/f16 outputs are rounded to the dtype,
+within 2^-7 absolute of values below 1 and 2^-6 of the scanned states.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from koemi_amd import dense, recurrent
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(seed, b, length, d, p, dtype):
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn((b, length, d), generator=g).to(dtype)
+    scale = d ** -0.5  # nn.Linear's initialisation scale
+    wr, wc = ((scale * torch.randn((d, d), generator=g)).to(dtype) for _ in range(2))
+    br, bc = ((scale * torch.randn((d,), generator=g)).to(dtype) for _ in range(2))
+    valid = torch.rand((b, length), generator=g) < p
+    return u, wr, br, wc, bc, valid
+
+
+def _np(t):
+    return t.float().numpy() if t.is_floating_point() else t.numpy()
+
+
+@pytest.mark.parametrize(
+    "b, length, d, p, dtype",
+    [
+        (2, 128, 64, 0.9, torch.float32),      # default model window (embedding 64, scan window 128)
+        (4, 256, 1024, 0.8, torch.float32),    # C5 width
+        (2, 64, 256, 0.7, torch.bfloat16),
+        (3, 17, 12, 0.5, torch.float16),
+    ],
+)
+def test_recurrent_gates_match_oracle(device, b, length, d, p, dtype):
+    u, wr, br, wc, bc, valid = _case(b * 13 + d, b, length, d, p, dtype)
+    a, inc = recurrent.recurrent_gates(*(t.to(device) for t in (u, wr, br, wc, bc)), valid.to(device))
+    want_a, want_b = oracle.recurrent_gates(*(_np(t) for t in (u, wr, br, wc, bc, valid)))
+    tol = 2e-5 if dtype == torch.float32 else 2.0**-7
+    err_a = np.abs(a.float().cpu().numpy() - want_a).max()
+    err_b = np.abs(inc.float().cpu().numpy() - want_b).max()
+    print(f"gates b={b} L={length} d={d} {dtype}: max_abs a={err_a:.3e} b={err_b:.3e}", flush=True)
+    assert err_a <= tol and err_b <= tol
+    inv = ~valid.numpy()
+    assert np.all(a.float().cpu().numpy()[inv] == 1.0) and np.all(inc.float().cpu().numpy()[inv] == 0.0)
+
+
+@pytest.mark.parametrize("b, length, d, dtype", [(2, 128, 64, torch.float32), (2, 300, 128, torch.bfloat16)])
+def test_recurrent_scan_matches_oracle(device, b, length, d, dtype):
+    u, wr, br, wc, bc, valid = _case(b + length + d, b, length, d, 0.85, dtype)
+    h0 = torch.randn((b, d), generator=torch.Generator().manual_seed(5)).to(dtype)
+    h = recurrent.recurrent_scan(*(t.to(device) for t in (u, wr, br, wc, bc, valid, h0)))
+    a, inc = oracle.recurrent_gates(*(_np(t) for t in (u, wr, br, wc, bc, valid)))
+    if dtype != torch.float32:  # the kernel hands a and b to the scan in the input dtype
+        a = a.astype(np.float32).astype(np.float64) if dtype == torch.float16 else oracle.round_bf16(a.astype(np.float32)).astype(np.float64)
+        inc = inc.astype(np.float32).astype(np.float64) if dtype == torch.float16 else oracle.round_bf16(inc.astype(np.float32)).astype(np.float64)
+    want = oracle.scan_sequential(a, inc, _np(h0).astype(np.float64))
+    err = np.abs(h.float().cpu().numpy() - want).max()
+    print(f"recurrent scan b={b} L={length} d={d} {dtype}: max_abs={err:.3e}", flush=True)
+    assert err <= (1e-4 if dtype == torch.float32 else 2.0**-6)
+
+
+def test_recurrent_gates_reject_bad_inputs(device):
+    u, wr, br, wc, bc, valid = (t.to(device) for t in _case(1, 2, 4, 8, 0.5, torch.float32))
+    with pytest.raises(dense.DenseCudaValidationError, match="must be on CUDA"):
+        recurrent.recurrent_gates(u.cpu(), wr, br, wc, bc)
+    with pytest.raises(dense.DenseCudaValidationError, match="same dtype"):
+        recurrent.recurrent_gates(u, wr.double(), br, wc, bc)
+    with pytest.raises(dense.DenseCudaValidationError, match="shape"):
+        recurrent.recurrent_gates(u, wr[:4], br, wc, bc)
+    with pytest.raises(dense.DenseCudaValidationError, match="valid_mask"):
+        recurrent.recurrent_gates(u, wr, br, wc, bc, valid[:, :2])

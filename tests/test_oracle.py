@@ -341,6 +341,43 @@ def test_read_salient_window_is_causal():
     np.testing.assert_array_equal(changed[:, :6], base[:, :6])  # query t sees window slots j < t only
 
 
+def _torch_gates(u, wr, br, wc, bc):
+    """BoundedRecurrentState.gates (model/memory.py:14-30) with torch.nn on the CPU (float64)."""
+    lin_r, lin_c = torch.nn.Linear(u.shape[-1], u.shape[-1]).double(), torch.nn.Linear(u.shape[-1], u.shape[-1]).double()
+    with torch.no_grad():
+        lin_r.weight.copy_(wr), lin_r.bias.copy_(br), lin_c.weight.copy_(wc), lin_c.bias.copy_(bc)
+        retention = torch.sigmoid(lin_r(u))
+        bounded = 2.0**-8 + ((1.0 - 2.0**-8) - 2.0**-8) * retention
+        return bounded, (1.0 - bounded) * torch.tanh(lin_c(u))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_recurrent_gates_match_the_reference_module(seed):
+    rng = np.random.default_rng(200 + seed)
+    d = int(rng.integers(1, 12))
+    u = rng.normal(size=(3, 5, d))
+    wr, wc = rng.normal(size=(d, d)), rng.normal(size=(d, d))
+    br, bc = rng.normal(size=d), rng.normal(size=d)
+    a, b = oracle.recurrent_gates(u, wr, br, wc, bc)
+    ta, tb = _torch_gates(*(torch.from_numpy(x) for x in (u, wr, br, wc, bc)))
+    np.testing.assert_allclose(a, ta.numpy(), rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(b, tb.numpy(), rtol=1e-13, atol=1e-15)
+
+
+def test_recurrent_gates_closed_forms():
+    d = 4
+    u = np.random.default_rng(3).normal(size=(2, 6, d))
+    zeros = np.zeros((d, d))
+    a, b = oracle.recurrent_gates(u, zeros, np.zeros(d), zeros, np.zeros(d))
+    assert np.all(a == 0.5) and np.all(b == 0.0)  # sigmoid(0) = 1/2: 2^-8 + (1 - 2^-7) / 2 = 1/2
+    a, b = oracle.recurrent_gates(u, zeros, np.full(d, 1e4), zeros, np.full(d, -1e4))
+    assert np.all(a == 1.0 - 2.0**-8) and np.all(b == -(2.0**-8))  # saturated bounds
+    valid = np.array([[True, False, True, True, False, True]] * 2)
+    a, b = oracle.recurrent_gates(u, np.eye(d), np.zeros(d), np.eye(d), np.zeros(d), valid)
+    assert np.all(a[~valid] == 1.0) and np.all(b[~valid] == 0.0)
+    assert np.all((a[valid] >= 2.0**-8) & (a[valid] <= 1.0 - 2.0**-8)) and np.all(np.abs(b[valid]) < 1.0 - a[valid] + 1e-15)
+
+
 def test_salient_tail_known_answer():
     kat = GOLDEN["salient_tail_latest"]
     adm = np.array([kat["admission"]])
