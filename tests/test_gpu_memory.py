@@ -88,6 +88,10 @@ def _read_case(seed, b, s, length, d, p, dtype):
         (2, 0, 20, 8, 0.5, torch.float32),         # empty ring
         (1, 4, 1, 16, 1.0, torch.float32),         # one query: carried slots only
         (3, 16, 64, 32, 0.0, torch.bfloat16),      # nothing eligible: zeros
+        (1, 16, 984, 48, 0.3, torch.float32),      # 1000 slots: the largest LDS weight block of the fused kernels
+        (1, 16, 1100, 40, 0.3, torch.float32),     # 1116 slots: the rocBLAS path
+        (2, 3, 45, 130, 0.6, torch.bfloat16),      # odd slot count and width
+        (2, 7, 33, 12, 0.8, torch.float32),        # width halves of 8 and 4 (four-element loads)
     ],
 )
 def test_read_salient_window_matches_oracle(device, b, s, length, d, p, dtype):
