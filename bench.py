@@ -565,7 +565,7 @@ def main() -> int:
         nbytes = 4 * (4 * b5 * l5 * d5 + 2 * b5 * s5 * d5) + b5 * (s5 + l5)
         kernels["C5w.salient_read"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
                                        "TFLOP/s": round(flop / ms / 1e9, 2), "shape_b_l_s_d": [b5, l5, s5, d5],
-                                       "note": "HIP fp32-MFMA scores kernel + HIP softmax-and-read kernel, eager launches"}
+                                       "note": "HIP fp32-MFMA scores, softmax and weighted-sum kernels, eager launches"}
         del ck, cv, k5, v5, q5
 
     if "g" in extra:

@@ -10,22 +10,16 @@
 //   weight = softmax over the eligible slots (all zero when none is), and
 //   out    = weight . [carried_values ; values]    [B, L, D]
 //
-// Up to kFusedMaxSlots slots (S + L) two kernels on fp32 MFMA
-// (v_mfma_f32_32x32x2f32), every operand converted to fp32:
-//   scores: one workgroup per (32 slots, 32 queries, batch, half of the
-//     width); its four waves split that half further, stage 32 x 64 slices of
-//     queries and keys in LDS (rows padded to 66 floats: conflict-free operand
-//     reads) and sum their partial 32 x 32 products through LDS. Slot tiles that
-//     causality hides from every query of the tile are skipped.
-//   read: one workgroup per (128 output columns, 32 queries, batch). Each
-//     wave owns 8 query rows: it adds the two width halves of their scores,
-//     masks them (eligibility from the valid and admission bytes and the
-//     positions), takes the row maxima on the way and leaves exp(score - max)
-//     in LDS with the row sums. Then each wave multiplies the 32 x K block of
-//     exponentials with a 32-column slice of the values, read straight from
-//     memory two 16-step windows ahead of use (each MFMA's value operand is two
-//     128-byte row segments), and divides by the row sums on the way out
-//     (all-zero rows when nothing is eligible).
+// Up to kFusedMaxSlots slots (S + L) three HIP kernels, products on fp32 MFMA
+// (v_mfma_f32_32x32x2f32) with every operand converted to fp32 and loaded
+// straight from memory into the MFMA operand registers (no LDS staging):
+//   scores: one workgroup per active (32 slots, 32 queries, batch, quarter of
+//     the width) tile, a tile being active when some slot in it is eligible
+//     for some query of it; four fp32 partial score arrays.
+//   softmax: one wave per query row; adds the partials, masks, max, exp, sum
+//     in registers, writes fp32 weights (zero rows when nothing is eligible).
+//   weighted sum: one workgroup per (128 output columns, 32 queries, batch),
+//     slot blocks past the tile's last eligible slot skipped.
 // Longer slot axes use rocBLAS for the two products (fp32 accumulation; the
 // carried and window parts of the key axis as separate strided-batched calls
 // on the caller's tensors) around a masked-softmax kernel. rocBLAS is
@@ -47,9 +41,9 @@ extern std::mutex g_blas_mutex;
 namespace {
 
 constexpr int kSoftmaxWaves = 4;
-constexpr int64_t kFusedMaxSlots = 1024;  // the read kernel keeps 32 rows of exponentials in LDS (32 x 1026 floats)
-constexpr int kSplitD = 2;                // width halves of the scores kernel
-constexpr int kPitch = 66;                // LDS row pitch (floats) of the scores kernel's operands
+constexpr int64_t kFusedMaxSlots = 1024;  // the softmax kernel holds a row in registers (16 slots per lane)
+constexpr int kParts = 4;                 // width parts of the scores kernel (partial sums added by the softmax)
+constexpr int kChunk = 64;                // width columns of one wave task of the scores kernel
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -74,292 +68,244 @@ __device__ __forceinline__ float4 load4_f32(const T* p) {
     }
 }
 
-// Scores of slots [s0, s0 + 32) for queries [q0, q0 + 32) of batch b over the
-// width half h: scores[h][b][t][s] = (sum over the half of key_s . query_t) / sqrt(D).
-// VEC: width % 4 == 0 (four-element loads).
+// Slot tiles (32 slots each) of query tile y that hold an eligible slot for
+// some query of the tile: slot s is eligible for query t only if s < S + t, so
+// tile x is needed when 32 x < S + t_max.
+__host__ __device__ inline int active_slot_tiles(int y, int S, int L, int K) {
+    const int t_max = min(32 * y + 31, L - 1);
+    return min((K + 31) / 32, (S + t_max + 31) / 32);
+}
+
+// Partial scores of one (32 slots, 32 queries, batch, quarter of the width)
+// tile: partial[part][b][t][s] = (sum over the part's width columns of
+// key_s . query_t) / sqrt(D). Only the tiles active_slot_tiles() names are
+// launched; tile groups (batch, part) are laid out contiguously per XCD (the
+// dispatcher deals workgroups to the 8 XCDs in turn) so one XCD's L2 serves
+// every re-read of a batch's queries and keys.
+//
+// The four waves take 64-column chunks of the part in turn. Lane l (row
+// r = l % 32, half h = l / 32) loads, straight from memory, eight four-element
+// groups of query row r and key row r at columns 64 c + 32 blk + 16 h + 4 i;
+// component j of group (blk, i) feeds one v_mfma_f32_32x32x2f32 step. A
+// lane's query and key values sit at the same column and the step's two
+// K-entries (h = 0, 1) at two distinct columns, so the 32 steps of a chunk
+// cover its 64 columns once: the column order inside the sum is permuted,
+// the sum is the same. VEC: width % 4 == 0 (four-element loads).
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void salient_scores_kernel(
-    const T* __restrict__ ck, const T* __restrict__ k, const T* __restrict__ q, float* __restrict__ scores,
-    int64_t B, int64_t S, int64_t L, int64_t D, float inv_sqrt_d) {
-    __shared__ float stage[4][2][32 * kPitch];  // per wave: queries, keys (67.6 KiB: two workgroups per CU)
-    const int64_t K = S + L;
-    const int64_t s0 = static_cast<int64_t>(blockIdx.x) * 32, q0 = static_cast<int64_t>(blockIdx.y) * 32;
-    const int64_t b = blockIdx.z / kSplitD;
-    const int half = static_cast<int>(blockIdx.z % kSplitD);
-    // Window slot j is seen by queries t > j only: skip tiles no query here sees.
-    const int64_t t_max = min(q0 + 31, L - 1);
-    if (s0 >= S && s0 - S >= t_max) return;
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    // Halves start at multiples of 4, so with width % 4 == 0 every four-element
-    // group lies inside one half and one row.
-    const int64_t d_half = ((D + kSplitD - 1) / kSplitD + 3) & ~int64_t(3);
-    const int64_t d_lo = min(D, half * d_half), d_hi = min(D, d_lo + d_half);
-    const int64_t nchunks = (d_hi - d_lo + 63) / 64;
-    // Lane l stages rows l / 16 + 4 i (i < 8), columns 4 (l % 16) .. +3 of a chunk.
-    const T* qrow[8];
-    const T* krow[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = lane / 16 + 4 * i;
-        const int64_t t = min(q0 + r, L - 1), sl = min(s0 + r, K - 1);
-        qrow[i] = q + (b * L + t) * D;
-        krow[i] = sl < S ? ck + (b * S + sl) * D : k + (b * L + (sl - S)) * D;
+    const T* __restrict__ ck, const T* __restrict__ k, const T* __restrict__ q, float* __restrict__ partial,
+    int B, int S, int L, int64_t D, float inv_sqrt_d, int tiles, int total, int per_xcd) {
+    const int pid = static_cast<int>(blockIdx.x);
+    const int logical = (pid & 7) * per_xcd + (pid >> 3);
+    if (logical >= total) return;
+    const int group = logical / tiles;
+    int rem = logical - group * tiles, y = 0;
+    const int K = S + L;
+    for (;; ++y) {
+        const int n = active_slot_tiles(y, S, L, K);
+        if (rem < n) break;
+        rem -= n;
     }
-    const int col = (lane % 16) * 4;
-    float4 qv[8], kv[8];
+    const int b = group / kParts, part = group % kParts;
+    const int s0 = rem * 32, q0 = y * 32;
+    const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
+    const int r = lane & 31, h = lane >> 5;
+    const int64_t nch = (D + kChunk - 1) / kChunk, per_part = (nch + kParts - 1) / kParts;
+    const int64_t c_end = min(nch, (part + 1) * per_part);
+    const T* qrow = q + (static_cast<int64_t>(b) * L + min(q0 + r, L - 1)) * D;
+    const int sl = min(s0 + r, K - 1);
+    const T* krow = sl < S ? ck + (static_cast<int64_t>(b) * S + sl) * D : k + (static_cast<int64_t>(b) * L + (sl - S)) * D;
+
+    float4 qa[8], kb[8];
     auto load_chunk = [&](int64_t c) {
-        const int64_t d = d_lo + c * 64 + col;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            if (VEC) {
-                const bool in = d < d_hi;
-                const int64_t dc = in ? d : d_lo;  // d_lo and d_hi are multiples of 4 here
-                qv[i] = load4_f32(qrow[i] + dc);
-                kv[i] = load4_f32(krow[i] + dc);
-                if (!in) qv[i] = kv[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int g = 0; g < 8; ++g) {
+            const int64_t d = c * kChunk + 32 * (g / 4) + 16 * h + 4 * (g % 4);
+            if constexpr (VEC) {
+                const bool in = d < D;
+                const int64_t dc = in ? d : 0;
+                qa[g] = load4_f32(qrow + dc);
+                kb[g] = load4_f32(krow + dc);
+                if (!in) qa[g] = kb[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             } else {
-                float a[4], e[4];
+                float x[4], z[4];
 #pragma unroll
-                for (int x = 0; x < 4; ++x) {
-                    const bool in = d + x < d_hi;
-                    const int64_t dc = in ? d + x : d_lo;
-                    a[x] = in ? load_f32(qrow[i] + dc) : 0.0f;
-                    e[x] = in ? load_f32(krow[i] + dc) : 0.0f;
+                for (int j = 0; j < 4; ++j) {
+                    const bool in = d + j < D;
+                    const int64_t dc = in ? d + j : 0;
+                    x[j] = load_f32(qrow + dc);
+                    z[j] = load_f32(krow + dc);
+                    if (!in) x[j] = z[j] = 0.0f;
                 }
-                qv[i] = make_float4(a[0], a[1], a[2], a[3]);
-                kv[i] = make_float4(e[0], e[1], e[2], e[3]);
+                qa[g] = make_float4(x[0], x[1], x[2], x[3]);
+                kb[g] = make_float4(z[0], z[1], z[2], z[3]);
             }
         }
     };
-    auto store_chunk = [&]() {
-        float* qs = stage[wave][0];
-        float* ks = stage[wave][1];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = lane / 16 + 4 * i;
-            // rows are 264 bytes apart: 8-byte aligned pairs
-            *reinterpret_cast<float2*>(qs + r * kPitch + col) = make_float2(qv[i].x, qv[i].y);
-            *reinterpret_cast<float2*>(qs + r * kPitch + col + 2) = make_float2(qv[i].z, qv[i].w);
-            *reinterpret_cast<float2*>(ks + r * kPitch + col) = make_float2(kv[i].x, kv[i].y);
-            *reinterpret_cast<float2*>(ks + r * kPitch + col + 2) = make_float2(kv[i].z, kv[i].w);
-        }
-    };
-    // Two accumulators (even and odd K steps) keep two MFMA chains in flight.
+    // Two accumulators keep two MFMA chains in flight.
     f32x16 acc0, acc1;
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc0[v] = acc1[v] = 0.0f;
-    // Wave w takes chunks w, w + 4, ...; the next chunk's loads are in flight
-    // (in registers) while the current one is multiplied from LDS. A wave's LDS
-    // operations complete in order, so the next chunk's stores wait for this
-    // chunk's operand reads.
-    int64_t c = wave;
-    if (c < nchunks) load_chunk(c);
-    for (; c < nchunks; c += 4) {
-        store_chunk();
-        if (c + 4 < nchunks) load_chunk(c + 4);
-        const float* qs = stage[wave][0];
-        const float* ks = stage[wave][1];
-        // Lane l: row l % 32 of each operand, K index 2 kk + l / 32; sixteen
-        // operand pairs are read before their MFMAs (one LDS latency each).
+    for (int64_t c = part * per_part + wave; c < c_end; c += 4) {
+        load_chunk(c);
 #pragma unroll
-        for (int kb = 0; kb < 32; kb += 16) {
-            float a[16], e[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int idx = (lane % 32) * kPitch + 2 * (kb + i) + lane / 32;
-                a[i] = qs[idx];
-                e[i] = ks[idx];
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], e[i], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i + 1], e[i + 1], acc1, 0, 0, 0);
-            }
+        for (int g = 0; g < 8; ++g) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[g].x, kb[g].x, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[g].y, kb[g].y, acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[g].z, kb[g].z, acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[g].w, kb[g].w, acc1, 0, 0, 0);
         }
     }
-    f32x16 acc = acc0 + acc1;
-    // Sum the four waves' partial tiles: element v of lane l is query
+    const f32x16 acc = acc0 + acc1;
+    // Sum the four waves' tiles: element v of lane l is query
     // 8 (v / 4) + 4 (l / 32) + v % 4, slot l % 32.
-    __syncthreads();
-    float* red = &stage[0][0][0];  // 4 x 16 x 64 floats
+    __shared__ float red[4][16][kWave];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) red[(wave * 16 + v) * kWave + lane] = acc[v];
+    for (int v = 0; v < 16; ++v) red[wave][v][lane] = acc[v];
     __syncthreads();
 #pragma unroll
     for (int vv = 0; vv < 4; ++vv) {
         const int v = wave * 4 + vv;
-        const float sum = red[(0 * 16 + v) * kWave + lane] + red[(1 * 16 + v) * kWave + lane] +
-                          red[(2 * 16 + v) * kWave + lane] + red[(3 * 16 + v) * kWave + lane];
-        const int64_t t = q0 + 8 * (v / 4) + 4 * (lane / 32) + v % 4;
-        const int64_t sl = s0 + lane % 32;
-        if (t < L && sl < K) scores[((half * B + b) * L + t) * K + sl] = sum * inv_sqrt_d;
+        const float sum = red[0][v][lane] + red[1][v][lane] + red[2][v][lane] + red[3][v][lane];
+        const int t = q0 + 8 * (v / 4) + 4 * h + v % 4;
+        const int slot = s0 + r;
+        if (t < L && slot < K)
+            partial[((static_cast<int64_t>(part) * B + b) * L + t) * K + slot] = sum * inv_sqrt_d;
     }
 }
 
-// out[b][t][d] for queries [q0, q0 + 32) and columns [d0, d0 + 128).
-template <typename T>
-__global__ __launch_bounds__(256) void salient_read_kernel(
-    const float* __restrict__ scores, const uint8_t* __restrict__ carried_valid, const uint8_t* __restrict__ admission,
-    const T* __restrict__ cv, const T* __restrict__ v, T* __restrict__ out, int64_t B, int64_t S, int64_t L,
-    int64_t D, int pitch) {
-    extern __shared__ float p_sh[];  // 32 x pitch exponentials, then the 32 rows' sums
-    float* row_sum = p_sh + 32 * pitch;
-    // Slot and row indices fit 32 bits (S + L <= kFusedMaxSlots); memory offsets are 64-bit.
-    const int K = static_cast<int>(S + L), Si = static_cast<int>(S), Li = static_cast<int>(L);
-    const int64_t d0 = static_cast<int64_t>(blockIdx.x) * 128;
-    const int q0 = static_cast<int>(blockIdx.y) * 32;
-    const int64_t b = blockIdx.z;
-    const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
-
-    // Wave w computes columns dw .. dw + 31 of out = E (32 x K) . V (K x 32) in
-    // steps of two slots, windows of 16 steps; the value rows of its first two
-    // windows are requested before the softmax, and every later window two
-    // windows ahead of its use.
-    const int64_t dw = d0 + wave * 32;
-    const int64_t dcol = min(dw + lane % 32, D - 1);
-    const T* cv_b = cv + b * S * D + dcol;  // + slot * D (carried slots)
-    const T* v_b = v + b * L * D + dcol;    // + (slot - S) * D (window slots)
-    const int windows = ((K + 1) / 2 + 15) / 16;
-    auto vwindow = [&](float(&dst)[16], int w) {
-        if (w >= windows) return;
+// Masked softmax of one query row per wave (b, t): the four partial scores
+// are added (fixed order), slot s is eligible when its valid or admission
+// byte is set and s < S + t; weights = exp(score - max) / sum over the
+// eligible slots, zero elsewhere and in rows with none, written as fp32 rows
+// of pitch Kp (K rounded up to 32; the padding is zero). NJ x 64 >= Kp.
+template <int NJ>
+__global__ __launch_bounds__(256) void salient_softmax_kernel(
+    const float* __restrict__ partial, const uint8_t* __restrict__ carried_valid,
+    const uint8_t* __restrict__ admission, float* __restrict__ weight, int B, int S, int L, int Kp) {
+    const int lane = lane_id();
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;  // b L + t
+    if (row >= static_cast<int64_t>(B) * L) return;
+    const int b = static_cast<int>(row / L), t = static_cast<int>(row % L);
+    const int K = S + L, lim = S + t;
+    const int64_t part_stride = static_cast<int64_t>(B) * L * K;
+    const float* x0 = partial + row * K;
+    float x[NJ];
+    bool ok[NJ];
+    float m = -INFINITY;
+    bool any = false;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int sl = min(32 * w + 2 * i + lane / 32, K - 1);  // clamped rows carry zero weight
-            dst[i] = load_f32(sl < Si ? cv_b + static_cast<int64_t>(sl) * D : v_b + static_cast<int64_t>(sl - Si) * D);
+    for (int j = 0; j < NJ; ++j) {
+        const int sl = 64 * j + lane;
+        if (64 * j < K) {
+            const int slc = min(sl, K - 1);
+            const bool f = (slc < S ? carried_valid[static_cast<int64_t>(b) * S + slc]
+                                    : admission[static_cast<int64_t>(b) * L + (slc - S)]) != 0;
+            float v = x0[slc];
+#pragma unroll
+            for (int p = 1; p < kParts; ++p) v += x0[p * part_stride + slc];
+            x[j] = v;
+            ok[j] = sl < K && f && sl < lim;
+        } else {
+            x[j] = 0.0f;
+            ok[j] = false;
+        }
+        if (ok[j]) {
+            any = true;
+            m = fmaxf(m, x[j]);
+        }
+    }
+    m = wave_max_xor(m);
+    any = __any(any);
+    if (!any) m = 0.0f;
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        x[j] = ok[j] ? expf(x[j] - m) : 0.0f;
+        sum += x[j];
+    }
+    sum = wave_sum_xor(sum);
+    float* w = weight + row * Kp;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        const int sl = 64 * j + lane;
+        if (64 * j < Kp && sl < Kp) w[sl] = sum > 0.0f ? x[j] / sum : x[j];
+    }
+}
+
+// out[b][t][d] = sum over slots s of weight[b][t][s] . [carried_values ; values][b][s][d]
+// for queries [q0, q0 + 32) and columns [d0, d0 + 128): one wave per 32
+// columns, v_mfma_f32_32x32x2f32 over 32-slot blocks. Lane l (row r, half h)
+// loads four four-element groups of weight row r at slots 32 blk + 16 h + 4 i
+// and the 16 value rows 32 blk + 16 h + s at column d0 + 32 w + r; step
+// s = 4 i + j pairs component j of group i with value row s, so each lane's
+// weight and value refer to the same slot. Blocks past the last slot that is
+// eligible for some query of the tile (S + t_max) are skipped (their weights
+// are zero); value rows are requested two blocks ahead of use.
+template <typename T>
+__global__ __launch_bounds__(256) void salient_pv_kernel(
+    const float* __restrict__ weight, const T* __restrict__ cv, const T* __restrict__ v, T* __restrict__ out,
+    int B, int S, int L, int64_t D, int Kp) {
+    const int64_t d0 = static_cast<int64_t>(blockIdx.x) * 128;
+    const int q0 = static_cast<int>(blockIdx.y) * 32, b = static_cast<int>(blockIdx.z);
+    const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
+    const int r = lane & 31, h = lane >> 5;
+    const int K = S + L;
+    const int t_max = min(q0 + 31, L - 1);
+    const int blocks = (min(K, S + t_max) + 31) / 32;
+    const float* wrow = weight + (static_cast<int64_t>(b) * L + min(q0 + r, L - 1)) * Kp + 16 * h;
+    const int64_t dw = d0 + wave * 32;
+    const int64_t dcol = min(dw + r, D - 1);
+    const T* cv_b = cv + static_cast<int64_t>(b) * S * D + dcol;  // + slot * D (carried slots)
+    const T* v_b = v + static_cast<int64_t>(b) * L * D + dcol;    // + (slot - S) * D (window slots)
+    struct Block {
+        float4 w[4];
+        float val[16];
+    };
+    auto load_block = [&](Block& dst, int blk) {
+        if (blk >= blocks) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst.w[i] = *reinterpret_cast<const float4*>(wrow + 32 * blk + 4 * i);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int sl = min(32 * blk + 16 * h + s, K - 1);  // clamped rows carry zero weight
+            dst.val[s] = load_f32(sl < S ? cv_b + static_cast<int64_t>(sl) * D : v_b + static_cast<int64_t>(sl - S) * D);
         }
     };
-    float va[16], vb[16], vc[16];
-    vwindow(va, 0);
-    vwindow(vb, 1);
-
-    // Wave w owns query rows r0 .. r0 + 7 (r0 = 8 w) of the tile: it adds the
-    // two width halves of their scores, keeps the eligible ones (-inf
-    // elsewhere) in LDS and takes their maxima on the way, 2 x 64 slots per
-    // round trip. Slot sl is eligible for query t < L when its valid or
-    // admission byte is set and sl < S + t.
-    const int r0 = wave * 8;
-    const float* half0 = scores + b * L * K;
-    const float* half1 = half0 + B * L * K;
-    int lim[8], row_off[8];
-    float m[8];
-    bool any[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        const int t = q0 + r0 + r;
-        lim[r] = t < Li ? Si + t : 0;
-        row_off[r] = min(t, Li - 1) * K;
-        m[r] = -INFINITY;
-        any[r] = false;
-    }
-    for (int c = 0; c < K; c += 128) {
-        float x0[2][8], x1[2][8];
-        bool f[2];
-        int col[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            col[j] = c + 64 * j + lane;
-            const int sl = min(col[j], K - 1);
-            f[j] = (sl < Si ? carried_valid[b * S + sl] : admission[b * L + (sl - Si)]) != 0;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                x0[j][r] = half0[row_off[r] + sl];
-                x1[j][r] = half1[row_off[r] + sl];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            if (col[j] >= K) continue;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const bool ok = f[j] && col[j] < lim[r];
-                const float x = x0[j][r] + x1[j][r];
-                p_sh[(r0 + r) * pitch + col[j]] = ok ? x : -INFINITY;
-                if (ok) {
-                    any[r] = true;
-                    m[r] = fmaxf(m[r], x);
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int r = 0; r < 8; ++r) m[r] = fmaxf(m[r], __shfl_xor(m[r], off, kWave));
-    // Exponentials in place (zero past K up to the pitch, and in rows with no
-    // eligible slot); the row sums divide the products at the end. Each lane
-    // reads back only the cells it wrote.
-    float sum[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        any[r] = __any(any[r]);
-        if (!any[r]) m[r] = 0.0f;
-        sum[r] = 0.0f;
-    }
-    for (int sl = lane; sl < pitch; sl += kWave) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            float* cell = p_sh + (r0 + r) * pitch + sl;
-            const float e = sl < K ? expf(*cell - m[r]) : 0.0f;  // exp(-inf) = 0 for ineligible slots
-            *cell = e;
-            sum[r] += e;
-        }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int r = 0; r < 8; ++r) sum[r] += __shfl_xor(sum[r], off, kWave);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < 8; ++r) row_sum[r0 + r] = sum[r];
-    }
-    __syncthreads();
-
-    // E . V: the exponentials of 16 steps are read before their MFMAs; two
-    // accumulators; the steps run to whole windows over the zero exponentials
-    // that pad each row.
     f32x16 acc0, acc1;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc0[i] = acc1[i] = 0.0f;
-    const float* erow = p_sh + (lane % 32) * pitch + lane / 32;
-    auto multiply = [&](const float(&vw)[16], int w) {
-        float ew[16];
+    auto multiply = [&](const Block& src) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ew[i] = erow[32 * w + 2 * i];
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ew[i], vw[i], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ew[i + 1], vw[i + 1], acc1, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(src.w[i].x, src.val[4 * i + 0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(src.w[i].y, src.val[4 * i + 1], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(src.w[i].z, src.val[4 * i + 2], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(src.w[i].w, src.val[4 * i + 3], acc1, 0, 0, 0);
         }
     };
-    for (int w = 0; w < windows; w += 3) {
-        vwindow(vc, w + 2);
-        multiply(va, w);
-        if (w + 1 >= windows) break;
-        vwindow(va, w + 3);
-        multiply(vb, w + 1);
-        if (w + 2 >= windows) break;
-        vwindow(vb, w + 4);
-        multiply(vc, w + 2);
+    Block ba, bb, bc;
+    load_block(ba, 0);
+    load_block(bb, 1);
+    for (int blk = 0; blk < blocks; blk += 3) {
+        load_block(bc, blk + 2);
+        multiply(ba);
+        if (blk + 1 >= blocks) break;
+        load_block(ba, blk + 3);
+        multiply(bb);
+        if (blk + 2 >= blocks) break;
+        load_block(bb, blk + 4);
+        multiply(bc);
     }
     const f32x16 acc = acc0 + acc1;
-    // Element i of lane l: query 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32;
-    // a row whose exponentials sum to zero reads zeros.
+    // Element i of lane l: query 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        const int r = 8 * (i / 4) + 4 * (lane / 32) + i % 4;
-        const int t = q0 + r;
-        const int64_t d = dw + lane % 32;
-        const float total = row_sum[r];
-        const float o = total == 0.0f ? 0.0f : acc[i] / total;  // a NaN sum stays NaN
-        if (t < Li && d < D) out[(b * L + t) * D + d] = from_f32<T>(o);
+        const int t = q0 + 8 * (i / 4) + 4 * h + i % 4;
+        const int64_t d = dw + r;
+        if (t < L && d < D) out[(static_cast<int64_t>(b) * L + t) * D + d] = from_f32<T>(acc[i]);
     }
 }
-
-// Row pitch (floats) of the read kernel's LDS weights: K rounded up to a
-// multiple of 32 (the MFMA loop runs 16 two-slot steps at a time over the zero
-// padding), plus 2 so that pitch / 2 is odd and the 32 rows of a column fall in
-// distinct banks (the odd column of each pair in the other half of the banks).
-inline int read_pitch(int64_t K) { return static_cast<int>((K + 31) / 32 * 32 + 2); }
 
 template <typename T>
 __global__ __launch_bounds__(kWave * kSoftmaxWaves) void masked_softmax_kernel(
@@ -424,8 +370,10 @@ ReadWorkspace read_workspace(int64_t B, int64_t S, int64_t L, int64_t D, int dty
     const size_t scores = rows * static_cast<size_t>(S + L);
     ReadWorkspace w;
     w.score_off = 0;
-    if (S + L <= kFusedMaxSlots) {  // fused kernels: the two width halves of the scores
-        w.weight_off = w.out_off = w.total = align(kSplitD * scores * sizeof(float));
+    if (S + L <= kFusedMaxSlots) {  // the partial scores, then weight rows of pitch Kp
+        const size_t kp = static_cast<size_t>((S + L + 31) / 32 * 32);
+        w.weight_off = align(kParts * scores * sizeof(float));
+        w.out_off = w.total = w.weight_off + align(rows * kp * sizeof(float));
     } else if (dtype == KOEMI_F32) {
         // The weights overwrite the scores (a lane reads each element before
         // writing it) and the second product writes the output directly.
@@ -476,31 +424,48 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
     const hipStream_t s = as_stream(stream);
 
     if (K <= kFusedMaxSlots) {
-        if (batch > 65535 / kSplitD || (length + 31) / 32 > 65535 || (width + 127) / 128 > 0x7fffffffLL)
+        if (batch > 65535 || batch * length > 0x7fffffffLL / kParts || (width + 127) / 128 > 0x7fffffffLL)
             return fail(KOEMI_ERR_UNSUPPORTED, "salient read grid too large");
+        const int Bi = static_cast<int>(batch), Si = static_cast<int>(carried), Li = static_cast<int>(length);
+        const int Ki = static_cast<int>(K), Kp = (Ki + 31) / 32 * 32;
+        int tiles = 0;
+        for (int y = 0; y < (Li + 31) / 32; ++y) tiles += active_slot_tiles(y, Si, Li, Ki);
+        const int64_t total = static_cast<int64_t>(tiles) * Bi * kParts;
+        if (total > 0x3fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "salient read grid too large");
+        const int per_xcd = static_cast<int>((total + 7) / 8);
         const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
-        const dim3 g1(static_cast<unsigned>((K + 31) / 32), static_cast<unsigned>((length + 31) / 32),
-                      static_cast<unsigned>(batch * kSplitD));
-        const dim3 g2(static_cast<unsigned>((width + 127) / 128), static_cast<unsigned>((length + 31) / 32),
-                      static_cast<unsigned>(batch));
-        const int pitch = read_pitch(K);
-        const size_t lds = static_cast<size_t>(32) * (pitch + 1) * sizeof(float);
+        float* weight32 = reinterpret_cast<float*>(base + ws.weight_off);
+        const int64_t rows = batch * length;
         const size_t esize = dtype == KOEMI_F32 ? 4 : 2;
         const bool vec = width % 4 == 0 && reinterpret_cast<uintptr_t>(queries) % (4 * esize) == 0 &&
                          reinterpret_cast<uintptr_t>(keys) % (4 * esize) == 0 &&
                          (carried == 0 || reinterpret_cast<uintptr_t>(carried_keys) % (4 * esize) == 0);
         auto run = [&](auto tag) {
             using T = decltype(tag);
-            auto scores_kernel = [&](auto kernel) {
-                hipLaunchKernelGGL(kernel, g1, dim3(256), 0, s, static_cast<const T*>(carried_keys),
-                                   static_cast<const T*>(keys), static_cast<const T*>(queries), score, batch, carried,
-                                   length, width, inv_sqrt_d);
+            if (total > 0) {
+                auto scores_kernel = [&](auto kernel) {
+                    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(8 * per_xcd)), dim3(256), 0, s,
+                                       static_cast<const T*>(carried_keys), static_cast<const T*>(keys),
+                                       static_cast<const T*>(queries), score, Bi, Si, Li, width, inv_sqrt_d, tiles,
+                                       static_cast<int>(total), per_xcd);
+                };
+                if (vec) scores_kernel(salient_scores_kernel<T, true>);
+                else scores_kernel(salient_scores_kernel<T, false>);
+            }
+            auto softmax = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s, score,
+                                   carried_valid, admission, weight32, Bi, Si, Li, Kp);
             };
-            if (vec) scores_kernel(salient_scores_kernel<T, true>);
-            else scores_kernel(salient_scores_kernel<T, false>);
-            hipLaunchKernelGGL(salient_read_kernel<T>, g2, dim3(256), lds, s, score, carried_valid, admission,
-                               static_cast<const T*>(carried_values), static_cast<const T*>(values),
-                               static_cast<T*>(out), batch, carried, length, width, pitch);
+            if (Kp <= 64) softmax(salient_softmax_kernel<1>);
+            else if (Kp <= 128) softmax(salient_softmax_kernel<2>);
+            else if (Kp <= 256) softmax(salient_softmax_kernel<4>);
+            else if (Kp <= 512) softmax(salient_softmax_kernel<8>);
+            else softmax(salient_softmax_kernel<16>);
+            hipLaunchKernelGGL(salient_pv_kernel<T>,
+                               dim3(static_cast<unsigned>((width + 127) / 128), static_cast<unsigned>((Li + 31) / 32),
+                                    static_cast<unsigned>(Bi)),
+                               dim3(256), 0, s, weight32, static_cast<const T*>(carried_values),
+                               static_cast<const T*>(values), static_cast<T*>(out), Bi, Si, Li, width, Kp);
         };
         if (dtype == KOEMI_F32) run(float{});
         else if (dtype == KOEMI_F16) run(f16{});

@@ -66,7 +66,7 @@ def test_salient_tail_rejects_bad_inputs(device):
 # ------------------------------------------------------------ salient read
 # read_salient_window (model/memory.py:405-429) against the float64 oracle on
 # the same (rounded) inputs. fp32: rtol 1e-4, atol 1e-5 x max|value| (fp32
-# products on rocBLAS, fp32 softmax). f16/bf16: the weights and the output are
+# products on fp32 MFMA or rocBLAS, fp32 softmax). f16/bf16: the weights and the output are
 # rounded to the input dtype as in the reference, so |err| <= 2^-7 x max|value|.
 
 
@@ -88,10 +88,13 @@ def _read_case(seed, b, s, length, d, p, dtype):
         (2, 0, 20, 8, 0.5, torch.float32),         # empty ring
         (1, 4, 1, 16, 1.0, torch.float32),         # one query: carried slots only
         (3, 16, 64, 32, 0.0, torch.bfloat16),      # nothing eligible: zeros
-        (1, 16, 984, 48, 0.3, torch.float32),      # 1000 slots: the largest LDS weight block of the fused kernels
+        (1, 16, 984, 48, 0.3, torch.float32),      # 1000 slots (16 per softmax lane)
+        (1, 24, 1000, 36, 0.3, torch.float32),     # 1024 slots: the largest of the HIP kernels
         (1, 16, 1100, 40, 0.3, torch.float32),     # 1116 slots: the rocBLAS path
-        (2, 3, 45, 130, 0.6, torch.bfloat16),      # odd slot count and width
-        (2, 7, 33, 12, 0.8, torch.float32),        # width halves of 8 and 4 (four-element loads)
+        (2, 3, 45, 130, 0.6, torch.bfloat16),      # odd slot count and width (two-byte scalar loads)
+        (2, 7, 33, 12, 0.8, torch.float32),        # one 64-column chunk, three empty width parts
+        (1, 9, 70, 4100, 0.5, torch.float32),      # 65 chunks: 17 per width part, the last part short
+        (2, 40, 90, 200, 0.9, torch.float16),      # carried slots fill two slot tiles
     ],
 )
 def test_read_salient_window_matches_oracle(device, b, s, length, d, p, dtype):
