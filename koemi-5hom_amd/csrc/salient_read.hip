@@ -234,8 +234,9 @@ __global__ __launch_bounds__(256) void salient_softmax_kernel(
 }
 
 // out[b][t][d] = sum over slots s of weight[b][t][s] . [carried_values ; values][b][s][d]
-// for queries [q0, q0 + 32) and columns [d0, d0 + 128): one wave per 32
-// columns, v_mfma_f32_32x32x2f32 over 32-slot blocks. Lane l (row r, half h)
+// for queries [q0, q0 + 32) and columns [d0, d0 + 128): eight waves, two per
+// 32-column slice, each taking half of the 32-slot blocks (the second half's
+// sums are added through LDS), v_mfma_f32_32x32x2f32. Lane l (row r, half h)
 // loads four four-element groups of weight row r at slots 32 blk + 16 h + 4 i
 // and the 16 value rows 32 blk + 16 h + s at column d0 + 32 w + r; step
 // s = 4 i + j pairs component j of group i with value row s, so each lane's
@@ -243,18 +244,21 @@ __global__ __launch_bounds__(256) void salient_softmax_kernel(
 // eligible for some query of the tile (S + t_max) are skipped (their weights
 // are zero); value rows are requested two blocks ahead of use.
 template <typename T>
-__global__ __launch_bounds__(256) void salient_pv_kernel(
+__global__ __launch_bounds__(512) void salient_pv_kernel(
     const float* __restrict__ weight, const T* __restrict__ cv, const T* __restrict__ v, T* __restrict__ out,
     int B, int S, int L, int64_t D, int Kp) {
     const int64_t d0 = static_cast<int64_t>(blockIdx.x) * 128;
     const int q0 = static_cast<int>(blockIdx.y) * 32, b = static_cast<int>(blockIdx.z);
     const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
+    const int slice = wave & 3, second = wave >> 2;
     const int r = lane & 31, h = lane >> 5;
     const int K = S + L;
     const int t_max = min(q0 + 31, L - 1);
-    const int blocks = (min(K, S + t_max) + 31) / 32;
+    const int all_blocks = (min(K, S + t_max) + 31) / 32;
+    const int first_end = (all_blocks + 1) / 2;
+    const int blk0 = second ? first_end : 0, blocks = second ? all_blocks : first_end;
     const float* wrow = weight + (static_cast<int64_t>(b) * L + min(q0 + r, L - 1)) * Kp + 16 * h;
-    const int64_t dw = d0 + wave * 32;
+    const int64_t dw = d0 + slice * 32;
     const int64_t dcol = min(dw + r, D - 1);
     const T* cv_b = cv + static_cast<int64_t>(b) * S * D + dcol;  // + slot * D (carried slots)
     const T* v_b = v + static_cast<int64_t>(b) * L * D + dcol;    // + (slot - S) * D (window slots)
@@ -285,9 +289,9 @@ __global__ __launch_bounds__(256) void salient_pv_kernel(
         }
     };
     Block ba, bb, bc;
-    load_block(ba, 0);
-    load_block(bb, 1);
-    for (int blk = 0; blk < blocks; blk += 3) {
+    load_block(ba, blk0);
+    load_block(bb, blk0 + 1);
+    for (int blk = blk0; blk < blocks; blk += 3) {
         load_block(bc, blk + 2);
         multiply(ba);
         if (blk + 1 >= blocks) break;
@@ -297,13 +301,20 @@ __global__ __launch_bounds__(256) void salient_pv_kernel(
         load_block(bb, blk + 4);
         multiply(bc);
     }
-    const f32x16 acc = acc0 + acc1;
+    f32x16 acc = acc0 + acc1;
+    __shared__ float red[4][16][kWave];
+    if (second) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[slice][i][lane] = acc[i];
+    }
+    __syncthreads();
+    if (second) return;
     // Element i of lane l: query 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int t = q0 + 8 * (i / 4) + 4 * h + i % 4;
         const int64_t d = dw + r;
-        if (t < L && d < D) out[(static_cast<int64_t>(b) * L + t) * D + d] = from_f32<T>(acc[i]);
+        if (t < L && d < D) out[(static_cast<int64_t>(b) * L + t) * D + d] = from_f32<T>(acc[i] + red[slice][i][lane]);
     }
 }
 
@@ -464,7 +475,7 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
             hipLaunchKernelGGL(salient_pv_kernel<T>,
                                dim3(static_cast<unsigned>((width + 127) / 128), static_cast<unsigned>((Li + 31) / 32),
                                     static_cast<unsigned>(Bi)),
-                               dim3(256), 0, s, weight32, static_cast<const T*>(carried_values),
+                               dim3(512), 0, s, weight32, static_cast<const T*>(carried_values),
                                static_cast<const T*>(values), static_cast<T*>(out), Bi, Si, Li, width, Kp);
         };
         if (dtype == KOEMI_F32) run(float{});
