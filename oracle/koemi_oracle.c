@@ -101,7 +101,9 @@ static uint32_t float_to_bits(float f) {
 }
 
 /* e^x: x = n ln2 + r (n = rint(x log2e), r by two fmaf with the split ln2),
- * e^r = sum_{i<=7} r^i / i! by Horner with fmaf, times 2^n. */
+ * e^r by the degree-6 polynomial c6 .. c0 below (minimax relative error with
+ * each coefficient rounded to fp32 in turn; c1 = c0 = 1) by Horner with fmaf,
+ * times 2^n by ldexpf (exact: the result is normal for -86 <= x <= 88). */
 float oracle_det_expf(float x) {
     if (x != x) return x;
     if (x < -86.0f) return 0.0f;
@@ -109,16 +111,14 @@ float oracle_det_expf(float x) {
     const float n = rintf(x * kLog2e);
     float r = fmaf(-n, kLn2Hi, x);
     r = fmaf(-n, kLn2Lo, r);
-    float p = 1.984127011382952e-04f;
-    p = fmaf(p, r, 1.3888889225199819e-03f);
-    p = fmaf(p, r, 8.333333767950535e-03f);
-    p = fmaf(p, r, 4.16666679084301e-02f);
-    p = fmaf(p, r, 1.666666716337204e-01f);
-    p = fmaf(p, r, 0.5f);
+    float p = 0.0013814611593261361f;   /* 0x3ab51225 */
+    p = fmaf(p, r, 0.008368710055947304f);  /* 0x3c091cea */
+    p = fmaf(p, r, 0.04166838899254799f);   /* 0x3d2aac79 */
+    p = fmaf(p, r, 0.1666652113199234f);    /* 0x3e2aaa49 */
+    p = fmaf(p, r, 0.4999999403953552f);    /* 0x3efffffe */
     p = fmaf(p, r, 1.0f);
     p = fmaf(p, r, 1.0f);
-    const int ni = (int)n;
-    return p * bits_to_float((uint32_t)(ni + 127) << 23);
+    return ldexpf(p, (int)n);
 }
 
 /* log x: x = m 2^e, m in [sqrt(1/2), sqrt(2)); log m = 2 atanh((m-1)/(m+1)). */
