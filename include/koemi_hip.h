@@ -244,6 +244,19 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
                        void* out, int64_t batch, int64_t carried, int64_t length, int64_t width, int dtype,
                        void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
+/* Local-memory read, LocalKeyValueMemory.read_window of model/memory.py:332-362
+ * without the novelty output (a torch composite in the reference; network.py:
+ * 328-336). The read of koemi_salient_read with the sliding window of
+ * memory.py:364-383: slot s (carried entries, then the window's entries) is
+ * eligible for query t when its valid byte (carried_valid, then valid) is set
+ * and carried + t - window <= s < carried + t. Same layouts, dtypes and
+ * workspace (koemi_salient_read_workspace_bytes) as koemi_salient_read;
+ * window >= 1. */
+int koemi_local_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                     const void* keys, const void* values, const uint8_t* valid, const void* queries, void* out,
+                     int64_t batch, int64_t carried, int64_t length, int64_t width, int64_t window, int dtype,
+                     void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
 /* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
  * without atomics: combined[t] = sum over the valid sorted pairs i of token t,
  * in ascending i, of y_i * w_i in fp32, w_i = pair_weights[i] (sorted order)

@@ -20,6 +20,11 @@
 //     in registers, writes fp32 weights (zero rows when nothing is eligible).
 //   weighted sum: one workgroup per (128 output columns, 32 queries, batch),
 //     slot blocks past the tile's last eligible slot skipped.
+// The local memory's read (LocalKeyValueMemory.read_window, memory.py:332-362)
+// is the same masked read with a sliding window: slot s is eligible for query t
+// when its valid byte is set and S + t - window <= s < S + t (the window
+// entries strictly before the query's own entry; memory.py:364-383).
+//
 // Longer slot axes use rocBLAS for the two products (fp32 accumulation; the
 // carried and window parts of the key axis as separate strided-batched calls
 // on the caller's tensors) around a masked-softmax kernel. rocBLAS is
@@ -176,18 +181,19 @@ __global__ __launch_bounds__(256) void salient_scores_kernel(
 
 // Masked softmax of one query row per wave (b, t): the four partial scores
 // are added (fixed order), slot s is eligible when its valid or admission
-// byte is set and s < S + t; weights = exp(score - max) / sum over the
+// byte is set and s < S + t (and s >= S + t - window when window > 0, the
+// local memory's sliding window); weights = exp(score - max) / sum over the
 // eligible slots, zero elsewhere and in rows with none, written as fp32 rows
 // of pitch Kp (K rounded up to 32; the padding is zero). NJ x 64 >= Kp.
 template <int NJ>
 __global__ __launch_bounds__(256) void salient_softmax_kernel(
     const float* __restrict__ partial, const uint8_t* __restrict__ carried_valid,
-    const uint8_t* __restrict__ admission, float* __restrict__ weight, int B, int S, int L, int Kp) {
+    const uint8_t* __restrict__ admission, float* __restrict__ weight, int B, int S, int L, int Kp, int window) {
     const int lane = lane_id();
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;  // b L + t
     if (row >= static_cast<int64_t>(B) * L) return;
     const int b = static_cast<int>(row / L), t = static_cast<int>(row % L);
-    const int K = S + L, lim = S + t;
+    const int K = S + L, lim = S + t, low = window > 0 ? lim - window : 0;
     const int64_t part_stride = static_cast<int64_t>(B) * L * K;
     const float* x0 = partial + row * K;
     float x[NJ];
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(256) void salient_softmax_kernel(
 #pragma unroll
             for (int p = 1; p < kParts; ++p) v += x0[p * part_stride + slc];
             x[j] = v;
-            ok[j] = sl < K && f && sl < lim;
+            ok[j] = sl < K && f && sl < lim && sl >= low;
         } else {
             x[j] = 0.0f;
             ok[j] = false;
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(512) void salient_pv_kernel(
 template <typename T>
 __global__ __launch_bounds__(kWave * kSoftmaxWaves) void masked_softmax_kernel(
     const float* __restrict__ score, const uint8_t* __restrict__ carried_valid, const uint8_t* __restrict__ admission,
-    T* __restrict__ weight, int64_t B, int64_t S, int64_t L) {
+    T* __restrict__ weight, int64_t B, int64_t S, int64_t L, int64_t window) {
     const int lane = lane_id();
     const int64_t row = static_cast<int64_t>(blockIdx.x) * kSoftmaxWaves + threadIdx.x / kWave;  // b * L + t
     if (row >= B * L) return;
@@ -330,6 +336,7 @@ __global__ __launch_bounds__(kWave * kSoftmaxWaves) void masked_softmax_kernel(
     const float* x = score + row * K;
     T* w = weight + row * K;
     auto eligible = [&](int64_t s) -> bool {
+        if (window > 0 && s < S + t - window) return false;
         if (s < S) return carried_valid[b * S + s] != 0;
         const int64_t j = s - S;
         return j < t && admission[b * L + j] != 0;
@@ -410,13 +417,18 @@ extern "C" size_t koemi_salient_read_workspace_bytes(int64_t batch, int64_t carr
     return read_workspace(batch, carried, length, width, dtype).total;
 }
 
-extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
-                                  const void* keys, const void* values, const uint8_t* admission, const void* queries,
-                                  void* out, int64_t batch, int64_t carried, int64_t length, int64_t width, int dtype,
-                                  void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+namespace {
+
+// The masked read shared by the salient read (window 0: no lower bound) and
+// the local memory's sliding-window read (window > 0).
+int memory_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid, const void* keys,
+                const void* values, const uint8_t* admission, const void* queries, void* out, int64_t batch,
+                int64_t carried, int64_t length, int64_t width, int64_t window, int dtype, void* workspace,
+                size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || carried < 0 || length < 0 || width < 1)
         return fail(KOEMI_ERR_INVALID, "salient read needs non-negative batch, carried and length and positive width");
     if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "salient read does not support dtype %s", dtype_name(dtype));
+    if (window < 0 || window > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "memory read window outside [0, 2^31)");
     if (batch == 0 || length == 0) return KOEMI_OK;
     const int64_t K = carried + length;
     const int64_t limit = 0x7fffffffLL;
@@ -465,7 +477,7 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
             }
             auto softmax = [&](auto kernel) {
                 hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s, score,
-                                   carried_valid, admission, weight32, Bi, Si, Li, Kp);
+                                   carried_valid, admission, weight32, Bi, Si, Li, Kp, static_cast<int>(window));
             };
             if (Kp <= 64) softmax(salient_softmax_kernel<1>);
             else if (Kp <= 128) softmax(salient_softmax_kernel<2>);
@@ -532,15 +544,15 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
     switch (dtype) {
         case KOEMI_F32:
             hipLaunchKernelGGL(masked_softmax_kernel<float>, grid, block, 0, s, score, carried_valid, admission,
-                               static_cast<float*>(weight), batch, carried, length);
+                               static_cast<float*>(weight), batch, carried, length, window);
             break;
         case KOEMI_F16:
             hipLaunchKernelGGL(masked_softmax_kernel<f16>, grid, block, 0, s, score, carried_valid, admission,
-                               static_cast<f16*>(weight), batch, carried, length);
+                               static_cast<f16*>(weight), batch, carried, length, window);
             break;
         default:
             hipLaunchKernelGGL(masked_softmax_kernel<bf16>, grid, block, 0, s, score, carried_valid, admission,
-                               static_cast<bf16*>(weight), batch, carried, length);
+                               static_cast<bf16*>(weight), batch, carried, length, window);
     }
     st = check_launch("koemi_salient_read(softmax)");
     if (st != KOEMI_OK) return st;
@@ -578,4 +590,24 @@ extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_
         return check_launch("koemi_salient_read(convert)");
     }
     return KOEMI_OK;
+}
+
+}  // namespace
+
+extern "C" int koemi_salient_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                                  const void* keys, const void* values, const uint8_t* admission, const void* queries,
+                                  void* out, int64_t batch, int64_t carried, int64_t length, int64_t width, int dtype,
+                                  void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    return memory_read(carried_keys, carried_values, carried_valid, keys, values, admission, queries, out, batch,
+                       carried, length, width, 0, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int koemi_local_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                                const void* keys, const void* values, const uint8_t* valid, const void* queries,
+                                void* out, int64_t batch, int64_t carried, int64_t length, int64_t width,
+                                int64_t window, int dtype, void* workspace, size_t workspace_bytes,
+                                koemi_stream_t stream) {
+    if (window < 1) return fail(KOEMI_ERR_INVALID, "local read needs a positive window");
+    return memory_read(carried_keys, carried_values, carried_valid, keys, values, valid, queries, out, batch, carried,
+                       length, width, window, dtype, workspace, workspace_bytes, stream);
 }

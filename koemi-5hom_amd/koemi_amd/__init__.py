@@ -6,7 +6,7 @@ Module map (reference front -> this package):
 * ``koemi.model.cuda_scan``     -> ``koemi_amd.cuda_scan`` (cuda_affine_scan)
 * ``koemi.cuda_kernels.core``   -> ``koemi_amd.core``      (fused_rmsnorm_silu)
 * ``koemi.cuda_kernels.think``  -> ``koemi_amd.think``     (causal_surprise, ...)
-* ``koemi.model.memory`` (LocalKeyValueMemory.read_salient_window, salient_tail) -> ``koemi_amd.memory``
+* ``koemi.model.memory`` (LocalKeyValueMemory.read_salient_window, salient_tail, read_window) -> ``koemi_amd.memory``
 * ``koemi.model.memory`` (BoundedRecurrentState.gates, + network.py:306-310 scan) -> ``koemi_amd.recurrent``
 * ``koemi.cuda_kernels.moe``    -> ``koemi_amd.moe``       (route/permute/grouped MLP/combine)
 * ``koemi.cuda_kernels.loader`` -> ``koemi_amd.loader``
@@ -19,7 +19,7 @@ and the recurrent gates; none falls back to CPU or to PyTorch.
 from koemi_amd.core import fused_rmsnorm_silu, load_core_extension
 from koemi_amd.cuda_scan import cuda_affine_scan, diagnose_cuda_affine_scan
 from koemi_amd.dense import dense_affine_scan, native_cuda_available
-from koemi_amd.memory import read_salient_window, salient_tail
+from koemi_amd.memory import read_local_window, read_salient_window, salient_tail
 from koemi_amd.recurrent import recurrent_gates, recurrent_scan
 from koemi_amd.moe import (
     combine_topk,
@@ -49,6 +49,7 @@ __all__ = [
     "route_topk_learned",
     "route_topk_valid",
     "salience_admission",
+    "read_local_window",
     "read_salient_window",
     "recurrent_gates",
     "recurrent_scan",

@@ -91,6 +91,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),
     ),
+    "koemi_local_read": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),
+    ),
     "koemi_moe_permute_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_moe_permute": (
         c_int,

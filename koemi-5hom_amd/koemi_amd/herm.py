@@ -1,0 +1,400 @@
+"""HERM block window and block stack on the GPU (the end-to-end configuration).
+
+``block_window`` is ``KoemiModel.forward_window`` (reference model/network.py:
+296-441) under the settings the reference runs by default: ablation
+``no_refine`` (the memory value is the fast associative read), hash expert
+routing with the static dispatch (experts.py:109-150), static rings
+(``KoemiState.create_static``, state.py:43-76). Its hot-path operators run on
+this package's HIP kernels:
+
+* gates + masking + scan: ``recurrent.recurrent_scan`` (memory.py:22-26,
+  network.py:306-310);
+* surprise from the prior states: ``think.causal_surprise`` on the content
+  head (network.py:677-698);
+* admission: ``think.salience_admission`` with the fixed threshold (network.py:349);
+* local read: ``memory.read_local_window`` (memory.py:332-383);
+* salient read and ring update: ``memory.read_salient_window``,
+  ``memory.salient_tail`` (memory.py:405-455);
+* experts: ``moe.route_topk_valid``, ``moe.permute_topk``,
+  ``moe.grouped_expert_mlp_inference``, ``moe.combine_topk`` (experts.py:
+  109-150, 283-289; layers.py:19-29).
+
+The projections are plain library GEMMs (``torch.nn.functional.linear`` on
+hipBLASLt) in ``HermSettings.linear_dtype`` with fp32 results; every other
+operation, the recurrent state and the memories are fp32. bf16 matches the
+reference's default GPU precision (``resolve_precision("auto")`` selects bf16
+autocast on CUDA, model/gpu_precision.py:96-121); fp32 is the parity setting.
+The gates run in fp32 whatever ``linear_dtype`` is. The associative memory's
+scan-and-read (memory.py:97-144) and the small elementwise steps are torch
+operations on device. The local read's novelty output, which only the refine
+path reads, is not computed.
+
+The stack (``stack_window``) is this package's composition for the 12-layer
+configuration (the reference model is a single block): layer 0 embeds the
+token ids, layer l > 0 takes layer l - 1's final context in place of the
+embedding (its own input normalizer applied); each layer has its own weights
+and state and uses the token ids for validity, routing and surprise targets;
+the last layer's head gives the logits. Inference only.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import asdict, dataclass
+
+import torch
+from torch import Tensor
+from torch.nn import functional
+
+from koemi_amd import memory, moe, recurrent, think
+
+__all__ = [
+    "DecodeGraph",
+    "HermSettings",
+    "PAD_TOKEN_ID",
+    "block_window",
+    "decode_step",
+    "init_stack",
+    "initial_states",
+    "prefill",
+    "prepare_stack",
+    "stack_window",
+]
+
+PAD_TOKEN_ID = 256             # configuration/settings.py:10-11
+_EPS = 1e-6                    # RootMeanSquareNorm epsilon (layers.py:9)
+_MIN_DECAY = 2.0**-12          # memory.py:74-75
+_MAX_DECAY = 1.0 - 2.0**-12
+_READ_EPSILON = 2.0**-8        # memory.py:77
+
+
+@dataclass(frozen=True)
+class HermSettings:
+    """Model settings (configuration/settings.py:14-32 names) of the stack."""
+
+    width: int = 1024
+    memory_features: int = 16
+    local_memory_size: int = 16
+    salience_memory_size: int = 16
+    salience_threshold: float = 0.75
+    expert_count: int = 16
+    top_k: int = 2
+    vocabulary_size: int = PAD_TOKEN_ID + 1
+    layers: int = 12
+    scan_chunk: int = 128
+    linear_dtype: torch.dtype = torch.bfloat16
+
+    def oracle_config(self) -> dict:
+        keys = ("width", "memory_features", "local_memory_size", "salience_memory_size", "salience_threshold",
+                "expert_count", "top_k")
+        values = asdict(self)
+        return {k: values[k] for k in keys}
+
+
+def _linear_init(generator: torch.Generator, out_features: int, in_features: int) -> tuple[Tensor, Tensor]:
+    """nn.Linear's default initialisation: U(-1/sqrt(in), 1/sqrt(in)) for weight and bias."""
+
+    bound = 1.0 / math.sqrt(in_features)
+    device = generator.device
+    weight = (torch.rand((out_features, in_features), generator=generator, device=device) * 2.0 - 1.0) * bound
+    bias = (torch.rand((out_features,), generator=generator, device=device) * 2.0 - 1.0) * bound
+    return weight, bias
+
+
+def init_stack(settings: HermSettings, seed: int, device: torch.device | str = "cpu") -> list[dict[str, Tensor]]:
+    """Random-initialised fp32 parameters of every layer, from one seeded
+    generator on ``device`` (nn.Embedding ~ N(0, 1) with the padding row zero,
+    nn.Linear uniform, normalizer weights one; network.py:81-106)."""
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    d, m, e, v = settings.width, settings.memory_features, settings.expert_count, settings.vocabulary_size
+    hidden = 2 * d  # GatedFeedForward expands to 2 x width (layers.py:22)
+    layers = []
+    for layer in range(settings.layers):
+        p: dict[str, Tensor] = {}
+        if layer == 0:
+            p["embedding"] = torch.randn((v, d), generator=g, device=device)
+            p["embedding"][PAD_TOKEN_ID] = 0.0
+        p["input_norm"] = torch.ones(d, device=device)
+        for name in ("retention", "candidate", "key", "query", "value", "local_key", "local_value"):
+            p[name + "_w"], p[name + "_b"] = _linear_init(g, d, d)
+        p["feature_w"], p["feature_b"] = _linear_init(g, m, d)
+        p["decay_w"], p["decay_b"] = _linear_init(g, 1, d)
+        p["write_w"], p["write_b"] = _linear_init(g, 1, d)
+        p["fusion_w"], p["fusion_b"] = _linear_init(g, d, 4 * d)
+        p["fusion_norm"] = torch.ones(d, device=device)
+        for name, (o, i) in (("gate", (hidden, d)), ("up", (hidden, d)), ("down", (d, hidden))):
+            pairs = [_linear_init(g, o, i) for _ in range(e)]
+            p[name + "_w"] = torch.stack([w for w, _ in pairs])
+            p[name + "_b"] = torch.stack([b for _, b in pairs])
+        p["expert_norm"] = torch.ones(d, device=device)
+        p["head_w"], p["head_b"] = _linear_init(g, v, d)
+        layers.append(p)
+    return layers
+
+
+def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, device: torch.device) -> list[dict[str, Tensor]]:
+    """Device copies laid out for the kernels: the seven projections of the
+    working states stacked into one GEMM, the GEMM weights in ``linear_dtype``,
+    the gates and the content head in fp32."""
+
+    lin = settings.linear_dtype
+    prepared = []
+    for p in params:
+        q: dict[str, Tensor] = {}
+        to = lambda t, dtype=torch.float32: t.to(device=device, dtype=dtype).contiguous()
+        if "embedding" in p:
+            q["embedding"] = to(p["embedding"])
+        q["input_norm"] = to(p["input_norm"])
+        for name in ("retention", "candidate"):
+            q[name + "_w"], q[name + "_b"] = to(p[name + "_w"]), to(p[name + "_b"])
+        order = ("local_key", "local_value", "key", "value", "query", "decay", "write")
+        q["ws_w"] = to(torch.cat([p[n + "_w"] for n in order]), lin)
+        q["ws_b"] = to(torch.cat([p[n + "_b"] for n in order]), lin)
+        q["feature_w"], q["feature_b"] = to(p["feature_w"], lin), to(p["feature_b"], lin)
+        q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"], lin)
+        q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
+        for name in ("gate", "up", "down"):
+            q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
+        q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"], lin)
+        q["content_w"] = to(p["head_w"][:PAD_TOKEN_ID])
+        q["content_b"] = to(p["head_b"][:PAD_TOKEN_ID])
+        prepared.append(q)
+    return prepared
+
+
+def initial_states(settings: HermSettings, batch: int, device: torch.device) -> list[dict[str, Tensor]]:
+    """KoemiState.create_static (state.py:43-76) per layer: zeros, rings at
+    capacity with every slot invalid, last token PAD."""
+
+    d, m = settings.width, settings.memory_features
+    w, s = settings.local_memory_size, settings.salience_memory_size
+    states = []
+    for _ in range(settings.layers):
+        z = lambda *shape: torch.zeros(shape, device=device)
+        states.append({
+            "working": z(batch, d),
+            "basis": z(batch, d, m),
+            "normalizer": z(batch, m),
+            "local_keys": z(batch, w, d),
+            "local_values": z(batch, w, d),
+            "local_valid": torch.zeros((batch, w), dtype=torch.bool, device=device),
+            "salient_keys": z(batch, s, d),
+            "salient_values": z(batch, s, d),
+            "salient_valid": torch.zeros((batch, s), dtype=torch.bool, device=device),
+            "last_token": torch.full((batch,), PAD_TOKEN_ID, dtype=torch.int64, device=device),
+        })
+    return states
+
+
+def _rms(x: Tensor, weight: Tensor) -> Tensor:
+    """RootMeanSquareNorm.forward (layers.py:14-16)."""
+
+    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + _EPS) * weight
+
+
+def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
+    return functional.linear(x.to(weight.dtype), weight, bias).float()
+
+
+def _previous_token_ids(ids: Tensor, valid: Tensor, carried: Tensor) -> Tensor:
+    """network.py:742-749: the previous valid token, or the carried last token."""
+
+    length = ids.shape[1]
+    index = torch.arange(length, device=ids.device).expand_as(ids)
+    latest = torch.cummax(torch.where(valid, index, torch.full_like(index, -1)), dim=1).values
+    previous = torch.cat((torch.full_like(latest[:, :1], -1), latest[:, :-1]), dim=1)
+    gathered = ids.gather(1, previous.clamp_min(0))
+    return torch.where(previous >= 0, gathered, carried.unsqueeze(1))
+
+
+def _last_valid_token_ids(ids: Tensor, valid: Tensor, carried: Tensor) -> Tensor:
+    """network.py:751-761."""
+
+    index = torch.arange(ids.shape[1], device=ids.device).expand_as(ids)
+    last = torch.where(valid, index, torch.full_like(index, -1)).amax(dim=1)
+    gathered = ids.gather(1, last.clamp_min(0).unsqueeze(1)).squeeze(1)
+    return torch.where(last >= 0, gathered, carried)
+
+
+def _associative_scan_read(basis: Tensor, normalizer: Tensor, decay: Tensor, value: Tensor, features: Tensor,
+                           weight: Tensor, query_features: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """HierarchicalAssociativeMemory.scan_and_read (memory.py:97-144), fp32:
+    reads from the state before each position's write, and the final state."""
+
+    log_decay = torch.log(decay)
+    cumulative = torch.cumsum(log_decay, dim=1)
+    prior = cumulative - log_decay
+    initial = torch.exp(prior)
+    length = decay.shape[1]
+    past = torch.ones((length, length), dtype=torch.bool, device=decay.device).tril(-1)
+    pair = torch.exp((prior.unsqueeze(-1) - cumulative.unsqueeze(1)).masked_fill(~past, float("-inf")))
+    similarity = torch.bmm(query_features, features.transpose(1, 2).contiguous())
+    influence = pair * similarity * weight.unsqueeze(1)
+    numerator = initial.unsqueeze(-1) * torch.bmm(query_features, basis.transpose(1, 2).contiguous())
+    numerator = numerator + torch.bmm(influence, value)
+    denominator = initial * torch.bmm(query_features, normalizer.unsqueeze(-1)).squeeze(-1) + influence.sum(dim=-1)
+    regularized = denominator.unsqueeze(-1) + _READ_EPSILON
+    read = (denominator.unsqueeze(-1) / regularized) * numerator / regularized
+    total = cumulative[:, -1]
+    final_weight = torch.exp(total.unsqueeze(1) - cumulative) * weight
+    scale = torch.exp(total)
+    final_basis = scale[:, None, None] * basis + torch.bmm((value * final_weight.unsqueeze(-1)).transpose(1, 2).contiguous(),
+                                                           features)
+    final_normalizer = scale[:, None] * normalizer + (final_weight.unsqueeze(-1) * features).sum(dim=1)
+    return read, final_basis, final_normalizer
+
+
+def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
+                 context: Tensor | None = None) -> tuple[Tensor, Tensor, dict[str, Tensor], Tensor]:
+    """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
+    int64 on the device; ``context`` the previous layer's final context (None
+    for the embedding layer). Returns (logits, final_context, next_state,
+    surprise)."""
+
+    ids = ids.contiguous()
+    batch, length = ids.shape
+    d = settings.width
+    valid = ids != PAD_TOKEN_ID
+    source = functional.embedding(ids, p["embedding"]) if context is None else context
+    u = _rms(source, p["input_norm"])
+    ws = recurrent.recurrent_scan(u, p["retention_w"], p["retention_b"], p["candidate_w"], p["candidate_b"], valid,
+                                  state["working"])
+    prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
+    targets = torch.where(valid, ids, torch.zeros_like(ids))
+    surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
+
+    projected = _linear(ws, p["ws_w"], p["ws_b"])
+    local_keys, local_values, key, value, query, decay, write = torch.split(projected, [d, d, d, d, d, 1, 1], dim=-1)
+    keep = valid.unsqueeze(-1)
+    local_keys = torch.where(keep, local_keys, torch.zeros_like(local_keys)).contiguous()
+    local_values = torch.where(keep, local_values, torch.zeros_like(local_values)).contiguous()
+    local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
+                                           local_keys, local_values, valid, ws, window=settings.local_memory_size)
+
+    feature_logits = _linear(torch.stack((key, query)), p["feature_w"], p["feature_b"])
+    features, query_features = torch.softmax(feature_logits, dim=-1).unbind(0)
+    value = torch.tanh(value).contiguous()
+    decay = _MIN_DECAY + (_MAX_DECAY - _MIN_DECAY) * torch.sigmoid(decay.squeeze(-1))
+    write = torch.sigmoid(write.squeeze(-1)) * (0.25 + 0.75 * surprise.clamp(0.0, 1.0))
+    decay = torch.where(valid, decay, torch.ones_like(decay))
+    write = torch.where(valid, write, torch.zeros_like(write))
+    fast, basis, normalizer = _associative_scan_read(state["basis"], state["normalizer"], decay, value,
+                                                     features.contiguous(), write, query_features.contiguous())
+
+    admission, _ = think.salience_admission(surprise, valid, threshold=settings.salience_threshold)
+    salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
+                                               local_keys, local_values, admission, ws)
+    fused = _rms(_linear(torch.cat((ws, fast, local_value, salient_value), dim=-1), p["fusion_w"], p["fusion_b"]),
+                 p["fusion_norm"])
+
+    previous = _previous_token_ids(ids, valid, state["last_token"])
+    k = settings.top_k
+    assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
+                                       validate=False)
+    flat = fused.reshape(-1, d)
+    flat_valid = valid.reshape(-1)
+    sorted_context, sorted_rows, sorted_experts, offsets = moe.permute_topk(
+        flat.to(settings.linear_dtype), assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
+        validate=False)
+    expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
+                                                  p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
+    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
+                              validate=False).float()
+    final = torch.where(flat_valid.unsqueeze(-1), _rms(flat + update, p["expert_norm"]), flat).view(batch, length, d)
+    logits = _linear(final, p["head_w"], p["head_b"])
+
+    w = settings.local_memory_size
+    salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
+                                  local_values, admission, settings.salience_memory_size)
+    next_state = {
+        "working": ws[:, -1].contiguous(),
+        "basis": basis,
+        "normalizer": normalizer,
+        "local_keys": torch.cat((state["local_keys"], local_keys), dim=1)[:, -w:].contiguous(),
+        "local_values": torch.cat((state["local_values"], local_values), dim=1)[:, -w:].contiguous(),
+        "local_valid": torch.cat((state["local_valid"], valid), dim=1)[:, -w:].contiguous(),
+        "salient_keys": salient[0],
+        "salient_values": salient[1],
+        "salient_valid": salient[2],
+        "last_token": _last_valid_token_ids(ids, valid, state["last_token"]),
+    }
+    return logits, final, next_state, surprise
+
+
+def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                 states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+    """One window through every layer; returns the last layer's logits and the next states."""
+
+    context = None
+    next_states = []
+    logits = None
+    for p, state in zip(params, states):
+        logits, context, next_state, _ = block_window(p, settings, ids, state, context)
+        next_states.append(next_state)
+    return logits, next_states
+
+
+def prefill(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+            states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+    """forward_parallel (network.py:176-197): windows of ``scan_chunk`` tokens, state carried."""
+
+    pieces = []
+    for start in range(0, ids.shape[1], settings.scan_chunk):
+        logits, states = stack_window(params, settings, ids[:, start:start + settings.scan_chunk].contiguous(), states)
+        pieces.append(logits)
+    return torch.cat(pieces, dim=1), states
+
+
+def decode_step(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+    """One greedy decode step at fixed shapes: ``ids`` ``[B, 1]`` -> the next ids
+    ``[B, 1]`` (argmax of the logits with the padding id removed, as
+    TokenSampler does for a greedy policy, runtime/fast_decode.py:53-55, 82-84)
+    and the next states."""
+
+    logits, states = stack_window(params, settings, ids, states)
+    scores = logits[:, -1].clone()
+    scores[:, PAD_TOKEN_ID] = float("-inf")
+    return scores.argmax(dim=-1, keepdim=True), states
+
+
+class DecodeGraph:
+    """Greedy decode steps replayed from one captured HIP graph.
+
+    The step (``decode_step`` followed by copies of the next ids and states into
+    static buffers) is captured once over private copies of ``ids`` and
+    ``states``; each ``step()`` replays it, advancing ``self.ids`` and
+    ``self.states`` in place. Fixed shapes throughout (static rings), no host
+    synchronisation inside the step. Two eager steps on throwaway copies warm
+    the libraries up before the capture.
+    """
+
+    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                 states: list[dict[str, Tensor]]) -> None:
+        self.params = params
+        self.settings = settings
+        self.ids = ids.clone()
+        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            warm_ids, warm_states = self.ids.clone(), [{k: v.clone() for k, v in st.items()} for st in states]
+            for _ in range(2):
+                warm_ids, warm_states = decode_step(params, settings, warm_ids, warm_states)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+
+    def _step(self) -> None:
+        next_ids, next_states = decode_step(self.params, self.settings, self.ids, self.states)
+        for state, new in zip(self.states, next_states):
+            for key, tensor in state.items():
+                tensor.copy_(new[key])
+        self.ids.copy_(next_ids)
+
+    def step(self) -> Tensor:
+        self.graph.replay()
+        return self.ids

@@ -1,4 +1,4 @@
-"""Salient (exact-recall) memory on the GPU: ring read and ring update.
+"""Salient (exact-recall) and local memory on the GPU: ring reads and ring update.
 
 Fronts for ``LocalKeyValueMemory.read_salient_window`` (reference
 model/memory.py:405-429: each query attends to the carried ring entries and to
@@ -6,7 +6,9 @@ the window's admitted entries at earlier positions) and
 ``LocalKeyValueMemory.salient_tail`` (memory.py:431-455: the carried ring
 entries followed by the window's entries, the latest ``capacity`` admitted
 ones kept in time order, invalid slots zeroed). They run ``koemi_salient_read``
-and ``koemi_salient_tail``; there is no torch fallback.
+and ``koemi_salient_tail``; there is no torch fallback. ``read_local_window``
+is the local memory's sliding-window read (memory.py:332-383) on the same
+kernels (``koemi_local_read``).
 """
 
 from __future__ import annotations
@@ -17,7 +19,7 @@ from torch import Tensor
 from koemi_amd import _native
 from koemi_amd.think import CudaThinkUnavailableError, CudaThinkValidationError
 
-__all__ = ["read_salient_window", "salient_tail"]
+__all__ = ["read_local_window", "read_salient_window", "salient_tail"]
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _MAX_CAPACITY = 4096
@@ -42,13 +44,61 @@ def read_salient_window(
     ``[B, L, D]`` in the queries' dtype (fp32 accumulation).
     """
 
+    return _masked_read(
+        "read_salient_window", "admission_mask", carried_keys, carried_values, carried_valid, keys, values,
+        admission_mask, queries, 0,
+    )
+
+
+def read_local_window(
+    carried_keys: Tensor,
+    carried_values: Tensor,
+    carried_valid: Tensor,
+    keys: Tensor,
+    values: Tensor,
+    valid_mask: Tensor,
+    queries: Tensor,
+    *,
+    window: int,
+) -> Tensor:
+    """Local-memory read of one window: the value output of
+    ``LocalKeyValueMemory.read_window`` (reference model/memory.py:332-362).
+
+    Same layouts as ``read_salient_window`` with the window's ``valid_mask`` in
+    place of the admission mask; query t attends to the valid entries among
+    the ``window`` positions strictly before its own entry in
+    ``[carried ; window entries]`` (``sliding_window_mask``, memory.py:364-383).
+    The novelty output of the reference method is not computed (the refine
+    path that reads it is off under the default ``no_refine`` ablation).
+    """
+
+    if isinstance(window, bool) or not isinstance(window, int) or window < 1:
+        raise CudaThinkValidationError("window must be a positive integer")
+    return _masked_read(
+        "read_local_window", "valid_mask", carried_keys, carried_values, carried_valid, keys, values, valid_mask,
+        queries, window,
+    )
+
+
+def _masked_read(
+    front: str,
+    mask_name: str,
+    carried_keys: Tensor,
+    carried_values: Tensor,
+    carried_valid: Tensor,
+    keys: Tensor,
+    values: Tensor,
+    mask: Tensor,
+    queries: Tensor,
+    window: int,
+) -> Tensor:
     tensors = {
         "carried_keys": carried_keys,
         "carried_values": carried_values,
         "carried_valid": carried_valid,
         "keys": keys,
         "values": values,
-        "admission_mask": admission_mask,
+        mask_name: mask,
         "queries": queries,
     }
     for name, tensor in tensors.items():
@@ -57,7 +107,7 @@ def read_salient_window(
         if tensor.device.type != "cuda":
             raise CudaThinkValidationError(f"{name} must be on CUDA")
     if len({t.device for t in tensors.values()}) != 1:
-        raise CudaThinkValidationError("read_salient_window tensors must be on the same CUDA device")
+        raise CudaThinkValidationError(f"{front} tensors must be on the same CUDA device")
     if queries.ndim != 3 or keys.shape != queries.shape or values.shape != queries.shape:
         raise CudaThinkValidationError("keys, values and queries must have the same shape [batch, length, width]")
     batch, length, width = queries.shape
@@ -66,10 +116,10 @@ def read_salient_window(
     if carried_keys.shape[0] != batch or carried_keys.shape[2] != width:
         raise CudaThinkValidationError("carried entries must match the window's batch and width")
     carried = carried_keys.shape[1]
-    if carried_valid.shape != (batch, carried) or admission_mask.shape != (batch, length):
-        raise CudaThinkValidationError("carried_valid and admission_mask must be [batch, carried] and [batch, length]")
-    if carried_valid.dtype != torch.bool or admission_mask.dtype != torch.bool:
-        raise CudaThinkValidationError("carried_valid and admission_mask must be torch.bool")
+    if carried_valid.shape != (batch, carried) or mask.shape != (batch, length):
+        raise CudaThinkValidationError(f"carried_valid and {mask_name} must be [batch, carried] and [batch, length]")
+    if carried_valid.dtype != torch.bool or mask.dtype != torch.bool:
+        raise CudaThinkValidationError(f"carried_valid and {mask_name} must be torch.bool")
     if queries.dtype not in _SUPPORTED_DTYPES:
         raise CudaThinkValidationError("queries must be float32, float16 or bfloat16")
     if any(t.dtype != queries.dtype for t in (keys, values, carried_keys, carried_values)):
@@ -91,15 +141,14 @@ def read_salient_window(
         dtype=torch.uint8,
         device=device,
     )
-    contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, admission_mask, queries)]
+    contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, mask, queries)]
+    pointers = [_native.ptr(t) if t.numel() else None for t in contiguous]
+    sizes = (batch, carried, length, width) + ((window,) if window else ())
     _native.call(
-        "koemi_salient_read",
-        *(_native.ptr(t) if t.numel() else None for t in contiguous),
+        "koemi_local_read" if window else "koemi_salient_read",
+        *pointers,
         _native.ptr(out),
-        batch,
-        carried,
-        length,
-        width,
+        *sizes,
         dtype,
         _native.ptr(workspace),
         workspace.numel(),

@@ -278,6 +278,82 @@ def read_salient_window(
     return np.einsum("bts,bsd->btd", w, all_v)
 
 
+def read_local_window(
+    carried_keys: np.ndarray,
+    carried_values: np.ndarray,
+    carried_valid: np.ndarray,
+    keys: np.ndarray,
+    values: np.ndarray,
+    valid: np.ndarray,
+    queries: np.ndarray,
+    window: int,
+) -> np.ndarray:
+    """Local read (value output of LocalKeyValueMemory.read_window, model/memory.py:
+    332-362, with sliding_window_mask 364-383), in float64: slot s of
+    [carried ; window entries] is eligible for query t when valid and
+    C + t - window <= s < C + t; softmax of key . query / sqrt(width) over the
+    eligible slots (rows with none read zeros)."""
+
+    ck = np.asarray(carried_keys, dtype=np.float64)
+    all_k = np.concatenate([ck, np.asarray(keys, np.float64)], axis=1)
+    all_v = np.concatenate([np.asarray(carried_values, np.float64), np.asarray(values, np.float64)], axis=1)
+    all_valid = np.concatenate([np.asarray(carried_valid, bool), np.asarray(valid, bool)], axis=1)
+    q = np.asarray(queries, dtype=np.float64)
+    b, length, width = q.shape
+    c = ck.shape[1]
+    own = c + np.arange(length)[:, None]
+    src = np.arange(all_k.shape[1])[None, :]
+    eligible = ((src < own) & (src >= own - window))[None] & all_valid[:, None, :]
+    scores = np.einsum("bsd,btd->bts", all_k, q) / np.sqrt(width)
+    scores = np.where(eligible, scores, -np.inf)
+    any_slot = eligible.any(axis=-1, keepdims=True)
+    m = np.where(any_slot, scores.max(axis=-1, keepdims=True, initial=-np.inf), 0.0)
+    e = np.where(eligible, np.exp(scores - m), 0.0)
+    total = e.sum(axis=-1, keepdims=True)
+    w = np.where(any_slot, e / np.where(total > 0, total, 1.0), 0.0)
+    return np.einsum("bts,bsd->btd", w, all_v)
+
+
+def read_local_sequential(
+    carried_keys: np.ndarray,
+    carried_values: np.ndarray,
+    carried_valid: np.ndarray,
+    keys: np.ndarray,
+    values: np.ndarray,
+    valid: np.ndarray,
+    queries: np.ndarray,
+    window: int,
+) -> np.ndarray:
+    """The same read position by position, as the sequential path does it
+    (LocalKeyValueMemory.read, memory.py:274-295, then append, 457-475): a
+    ring of the last `window` entries, read before the query's own entry is
+    appended. An independent restatement used to pin read_local_window."""
+
+    ring_k = [row for row in np.asarray(carried_keys, np.float64).transpose(1, 0, 2)]
+    ring_v = [row for row in np.asarray(carried_values, np.float64).transpose(1, 0, 2)]
+    ring_ok = [row for row in np.asarray(carried_valid, bool).T]
+    ring_k, ring_v, ring_ok = ring_k[-window:], ring_v[-window:], ring_ok[-window:]
+    q = np.asarray(queries, np.float64)
+    b, length, width = q.shape
+    out = np.zeros_like(q)
+    for t in range(length):
+        if ring_k:
+            k = np.stack(ring_k, 1)
+            v = np.stack(ring_v, 1)
+            ok = np.stack(ring_ok, 1)
+            scores = np.einsum("bsd,bd->bs", k, q[:, t]) / np.sqrt(width)
+            for r in range(b):
+                if ok[r].any():
+                    z = scores[r][ok[r]]
+                    e = np.exp(z - z.max())
+                    out[r, t] = (e / e.sum()) @ v[r][ok[r]]
+        ring_k.append(np.asarray(keys, np.float64)[:, t])
+        ring_v.append(np.asarray(values, np.float64)[:, t])
+        ring_ok.append(np.asarray(valid, bool)[:, t])
+        ring_k, ring_v, ring_ok = ring_k[-window:], ring_v[-window:], ring_ok[-window:]
+    return out
+
+
 def salient_tail(
     carried_keys: np.ndarray,
     carried_values: np.ndarray,

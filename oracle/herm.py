@@ -1,0 +1,256 @@
+"""CPU oracle of one HERM block window and of the block stack, in float64.
+
+TEST INFRASTRUCTURE ONLY (see the package docstring): imported by tests/ and
+nowhere in the product.
+
+Restates KoemiModel.forward_window (reference model/network.py:296-441) under
+the default settings it runs with (ablation "no_refine": memory_value is the
+fast associative read; hash expert routing with the static dispatch of
+experts.py:109-150) from the reference's own formulas:
+
+* embed + input normalizer (network.py:703-707, layers.py:8-16);
+* gates, masking and scan (memory.py:22-26; network.py:306-310; scan.py);
+* previous states and surprise (scan.py:33-34; network.py:677-698);
+* local entries and the local read (memory.py:297-383);
+* associative projection, fast write terms, masking and scan_and_read
+  (memory.py:82-144, 244-255; network.py:734-740);
+* admission, salient read and salient tail (network.py:349; memory.py:405-455);
+* fusion (network.py:723-732), experts (experts.py:109-150, 283-289;
+  layers.py:19-29), token head (network.py:700-701);
+* local tail and last valid token (memory.py:385-403; network.py:751-761).
+
+The block stack is this repository's composition for the 12-layer
+configuration (the reference model is one block): layer 0 embeds the token ids,
+layer l > 0 takes layer l - 1's final context in place of the embedding (its
+own input normalizer applied), every layer keeps its own state and uses the
+token ids for validity, routing and surprise targets; the last layer's head
+gives the logits.
+
+Pinned beyond the formulas by tests/test_oracle_herm.py: the associative
+scan-and-read against the sequential read/update recurrence (memory.py:91-95,
+279-288), the local read against the per-position ring read
+(oracle.read_local_sequential), and the reused oracle functions' own pins.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+import oracle
+
+PAD = oracle.PAD_TOKEN_ID
+EPS = 1e-6                  # RootMeanSquareNorm default epsilon (layers.py:9)
+MIN_DECAY = 2.0**-12        # memory.py:74-75
+MAX_DECAY = 1.0 - 2.0**-12
+READ_EPSILON = 2.0**-8      # memory.py:77
+
+
+def rms(x: np.ndarray, weight: np.ndarray) -> np.ndarray:
+    """RootMeanSquareNorm.forward (layers.py:14-16)."""
+
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + EPS) * weight
+
+
+def linear(x: np.ndarray, weight: np.ndarray, bias: np.ndarray | None) -> np.ndarray:
+    y = x @ np.asarray(weight, np.float64).T
+    return y if bias is None else y + np.asarray(bias, np.float64)
+
+
+def softmax(z: np.ndarray) -> np.ndarray:
+    e = np.exp(z - z.max(axis=-1, keepdims=True))
+    return e / e.sum(axis=-1, keepdims=True)
+
+
+def sigmoid(z: np.ndarray) -> np.ndarray:
+    return 1.0 / (1.0 + np.exp(-z))
+
+
+def confidence_read(numerator: np.ndarray, denominator: np.ndarray) -> np.ndarray:
+    """confidence_weighted_read (memory.py:248-251)."""
+
+    regularized = denominator + READ_EPSILON
+    return (denominator / regularized) * numerator / regularized
+
+
+def associative_scan_read(basis, normalizer, decay, value, features, weight, query_features):
+    """scan_and_read of memory.py:97-144 (parallel form): reads for every
+    position from the state before its own write, and the final state."""
+
+    log_decay = np.log(decay)
+    cumulative = np.cumsum(log_decay, axis=1)
+    prior = cumulative - log_decay
+    initial = np.exp(prior)
+    length = decay.shape[1]
+    past = np.arange(length)[:, None] > np.arange(length)[None, :]
+    pair = np.where(past[None], np.exp(np.where(past[None], prior[:, :, None] - cumulative[:, None, :], 0.0)), 0.0)
+    similarity = np.einsum("bsm,btm->bts", features, query_features)
+    influence = pair * similarity * weight[:, None, :]
+    numerator = initial[..., None] * np.einsum("bdm,btm->btd", basis, query_features)
+    numerator = numerator + np.einsum("bts,bsd->btd", influence, value)
+    denominator = initial * np.einsum("bm,btm->bt", normalizer, query_features) + influence.sum(axis=-1)
+    read = confidence_read(numerator, denominator[..., None])
+    total = cumulative[:, -1]
+    final_weight = np.exp(total[:, None] - cumulative) * weight
+    final_basis = np.exp(total)[:, None, None] * basis + np.einsum("bs,bsd,bsm->bdm", final_weight, value, features)
+    final_normalizer = np.exp(total)[:, None] * normalizer + np.einsum("bs,bsm->bm", final_weight, features)
+    return read, final_basis, final_normalizer
+
+
+def associative_sequential(basis, normalizer, decay, value, features, weight, query_features):
+    """The same reads and final state position by position: read (memory.py:
+    91-95) from the current state, then update (memory.py:279-288)."""
+
+    basis = basis.copy()
+    normalizer = normalizer.copy()
+    reads = np.zeros_like(value)
+    for t in range(value.shape[1]):
+        qf = query_features[:, t]
+        numerator = np.einsum("bdm,bm->bd", basis, qf)
+        denominator = (normalizer * qf).sum(axis=-1, keepdims=True)
+        reads[:, t] = confidence_read(numerator, denominator)
+        d = decay[:, t]
+        basis = d[:, None, None] * basis + weight[:, t, None, None] * (value[:, t, :, None] * features[:, t, None, :])
+        normalizer = d[:, None] * normalizer + weight[:, t, None] * features[:, t]
+    return reads, basis, normalizer
+
+
+def initial_state(batch: int, cfg: dict) -> dict:
+    """KoemiState.create_static (state.py:43-76): zero state, rings at capacity, all slots invalid."""
+
+    d, m, w, s = cfg["width"], cfg["memory_features"], cfg["local_memory_size"], cfg["salience_memory_size"]
+    return {
+        "working": np.zeros((batch, d)),
+        "basis": np.zeros((batch, d, m)),
+        "normalizer": np.zeros((batch, m)),
+        "local_keys": np.zeros((batch, w, d)),
+        "local_values": np.zeros((batch, w, d)),
+        "local_valid": np.zeros((batch, w), bool),
+        "salient_keys": np.zeros((batch, s, d)),
+        "salient_values": np.zeros((batch, s, d)),
+        "salient_valid": np.zeros((batch, s), bool),
+        "last_token": np.full((batch,), PAD, np.int64),
+    }
+
+
+def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray, valid: np.ndarray, cfg: dict):
+    """DeterministicExpertMixture static dispatch (experts.py:109-150): every
+    valid token adds FFN_e(context) / k over its distinct assigned experts, then
+    output_normalizer(context + update) where valid."""
+
+    k, count = cfg["top_k"], cfg["expert_count"]
+    assignments = oracle.route_hash(ids, previous, valid, count, k)
+    b, length, d = context.shape
+    flat = context.reshape(-1, d)
+    update = np.zeros_like(flat)
+    a = assignments.reshape(-1, k)
+    ok = valid.reshape(-1)
+    for t in np.nonzero(ok)[0]:
+        seen = set()
+        for e in a[t]:
+            if e < 0 or e >= count or e in seen:
+                continue
+            seen.add(int(e))
+            x = flat[t]
+            gate = linear(x, p["gate_w"][e], p["gate_b"][e])
+            up = linear(x, p["up_w"][e], p["up_b"][e])
+            update[t] += linear(gate / (1.0 + np.exp(-gate)) * up, p["down_w"][e], p["down_b"][e]) / k
+    mixed = rms(flat + update, p["expert_norm"])
+    out = np.where(ok[:, None], mixed, flat).reshape(b, length, d)
+    return out, assignments
+
+
+def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context: np.ndarray | None = None):
+    """One forward_window of one block. Returns (logits, final_context,
+    next_state, surprise, admission)."""
+
+    f = lambda name: np.asarray(p[name], np.float64)
+    ids = np.asarray(ids, np.int64)
+    valid = ids != PAD
+    source = f("embedding")[ids] if input_context is None else input_context
+    u = rms(source, f("input_norm"))
+    retention, increment = oracle.recurrent_gates(u, f("retention_w"), f("retention_b"), f("candidate_w"),
+                                                  f("candidate_b"), valid)
+    ws = oracle.scan_sequential(np.asarray(retention, np.float64), np.asarray(increment, np.float64), state["working"])
+    prior = np.concatenate([state["working"][:, None], ws[:, :-1]], axis=1)
+
+    content = linear(prior, f("head_w")[:PAD], f("head_b")[:PAD])
+    targets = np.where(valid, ids, 0)
+    zmax = content.max(axis=-1, keepdims=True)
+    lse = np.log(np.exp(content - zmax).sum(axis=-1)) + zmax[..., 0]
+    nll = lse - np.take_along_axis(content, targets[..., None], axis=-1)[..., 0]
+    surprise = np.where(valid, 1.0 - np.exp(-nll / math.log(PAD)), 0.0)
+
+    keep = valid[..., None]
+    local_keys = np.where(keep, linear(ws, f("local_key_w"), f("local_key_b")), 0.0)
+    local_values = np.where(keep, linear(ws, f("local_value_w"), f("local_value_b")), 0.0)
+    local_value = oracle.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
+                                           local_keys, local_values, valid, ws, cfg["local_memory_size"])
+
+    key = linear(ws, f("key_w"), f("key_b"))
+    features = softmax(linear(key, f("feature_w"), f("feature_b")))
+    value = np.tanh(linear(ws, f("value_w"), f("value_b")))
+    decay = MIN_DECAY + (MAX_DECAY - MIN_DECAY) * sigmoid(linear(ws, f("decay_w"), f("decay_b")))[..., 0]
+    write = sigmoid(linear(ws, f("write_w"), f("write_b")))[..., 0] * (0.25 + 0.75 * np.clip(surprise, 0.0, 1.0))
+    decay = np.where(valid, decay, 1.0)
+    write = np.where(valid, write, 0.0)
+    query_features = softmax(linear(linear(ws, f("query_w"), f("query_b")), f("feature_w"), f("feature_b")))
+    fast, basis, normalizer = associative_scan_read(state["basis"], state["normalizer"], decay, value, features,
+                                                    write, query_features)
+
+    admission = valid & (surprise > cfg["salience_threshold"])
+    salient_value = oracle.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
+                                               local_keys, local_values, admission, ws)
+    fused = rms(linear(np.concatenate([ws, fast, local_value, salient_value], axis=-1), f("fusion_w"),
+                       f("fusion_b")), f("fusion_norm"))
+    previous = oracle.previous_token_ids(ids, valid, state["last_token"])
+    final, _ = experts({k: f(k) for k in ("gate_w", "gate_b", "up_w", "up_b", "down_w", "down_b", "expert_norm")},
+                       fused, ids, previous, valid, cfg)
+    logits = linear(final, f("head_w"), f("head_b"))
+
+    w = cfg["local_memory_size"]
+    all_lk = np.concatenate([state["local_keys"], local_keys], axis=1)
+    all_lv = np.concatenate([state["local_values"], local_values], axis=1)
+    all_ok = np.concatenate([state["local_valid"], valid], axis=1)
+    sk, sv, sok = oracle.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"],
+                                      local_keys, local_values, admission, cfg["salience_memory_size"])
+    positions = np.where(valid, np.arange(ids.shape[1])[None, :], -1).max(axis=1)
+    last = np.where(positions >= 0, ids[np.arange(ids.shape[0]), np.maximum(positions, 0)], state["last_token"])
+    next_state = {
+        "working": ws[:, -1],
+        "basis": basis,
+        "normalizer": normalizer,
+        "local_keys": all_lk[:, -w:],
+        "local_values": all_lv[:, -w:],
+        "local_valid": all_ok[:, -w:],
+        "salient_keys": np.asarray(sk, np.float64),
+        "salient_values": np.asarray(sv, np.float64),
+        "salient_valid": np.asarray(sok, bool),
+        "last_token": last,
+    }
+    return logits, final, next_state, surprise, admission
+
+
+def stack_window(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict):
+    """One window through every layer (the composition in the module docstring).
+    Returns (last layer's logits, next states, per-layer surprise)."""
+
+    context = None
+    next_states, surprises = [], []
+    logits = None
+    for p, st in zip(params, states):
+        logits, context, nst, surprise, _ = block_window(p, st, ids, cfg, context)
+        next_states.append(nst)
+        surprises.append(surprise)
+    return logits, next_states, surprises
+
+
+def prefill(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict, window: int):
+    """forward_parallel (network.py:176-197): the sequence in windows of `window`, state carried."""
+
+    pieces = []
+    for start in range(0, ids.shape[1], window):
+        logits, states, _ = stack_window(params, states, ids[:, start:start + window], cfg)
+        pieces.append(logits)
+    return np.concatenate(pieces, axis=1), states

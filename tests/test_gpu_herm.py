@@ -1,0 +1,166 @@
+"""HERM block stack on the GPU (koemi_amd.herm) against the float64 oracle.
+
+Parity setting: fp32 projections (``linear_dtype=torch.float32``), a two-layer
+stack of width 32 run over two windows from the static initial state, then
+greedy decode steps. The admission threshold is placed in a gap of the
+oracle's surprise values (at least 2e-3 from every score), so the GPU's fp32
+surprise (within ~1e-6 of the oracle's) admits exactly the same entries.
+Tolerances: logits and states 1e-4 relative + 1e-4 x max|logit| absolute
+(fp32 products and fp32 state against float64); masks and token ids exact.
+The bf16 setting (the benchmark's) is compared with the fp32 setting with
+admission off, within 5e-2 relative (bf16 rounding of every projection input).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+from koemi_amd import herm
+from oracle import herm as oherm
+
+pytestmark = pytest.mark.gpu
+
+PAD = herm.PAD_TOKEN_ID
+
+
+def _settings(**kw):
+    base = dict(width=32, memory_features=4, local_memory_size=4, salience_memory_size=3, expert_count=4, top_k=2,
+                layers=2, scan_chunk=6, linear_dtype=torch.float32)
+    base.update(kw)
+    return herm.HermSettings(**base)
+
+
+def _params(settings, seed=11):
+    params = herm.init_stack(settings, seed)
+    for p in params:
+        p["head_w"] *= 8.0  # spread the surprise scores over (0, 1)
+    return params
+
+
+def _oracle_params(params):
+    return [{k: v.double().numpy() for k, v in p.items()} for p in params]
+
+
+def _ids(b, length, seed=3):
+    rng = np.random.default_rng(seed)
+    ids = rng.integers(0, 256, (b, length))
+    ids[1, 2] = PAD
+    ids[0, 9] = PAD
+    return ids
+
+
+def _pick_threshold(params_np, ids, settings):
+    """A threshold 2e-3 or more from every surprise score of the oracle run
+    with it, with scores on both sides."""
+
+    cfg = settings.oracle_config()
+    for tau in (0.5, 0.55, 0.6, 0.65, 0.45, 0.7, 0.4):
+        cfg["salience_threshold"] = tau
+        scores = _oracle_scores(params_np, ids, settings, cfg)
+        if np.abs(scores - tau).min() >= 2e-3 and (scores > tau).any() and (scores < tau).any():
+            return tau
+    pytest.skip("no threshold with a 2e-3 margin for this seed")
+
+
+def _oracle_scores(params_np, ids, settings, cfg):
+    states = [oherm.initial_state(ids.shape[0], cfg) for _ in params_np]
+    scores = []
+    for start in range(0, ids.shape[1], settings.scan_chunk):
+        piece = ids[:, start:start + settings.scan_chunk]
+        _, states, surprise = oherm.stack_window(params_np, states, piece, cfg)
+        scores += [s[piece != PAD] for s in surprise]
+    return np.concatenate(scores)
+
+
+def _close(got, want, scale, what):
+    err = np.abs(np.asarray(got, np.float64) - want)
+    bound = 1e-4 * np.abs(want) + 1e-4 * scale
+    print(f"{what}: max_abs={err.max():.3e} scale={scale:.3e}", flush=True)
+    assert np.all(err <= bound), what
+
+
+def test_stack_prefill_and_decode_match_the_oracle(device):
+    b, length = 2, 12
+    settings = _settings()
+    params = _params(settings)
+    params_np = _oracle_params(params)
+    ids = _ids(b, length)
+    tau = _pick_threshold(params_np, ids, settings)
+    settings = dataclasses.replace(settings, salience_threshold=tau)
+    cfg = settings.oracle_config()
+
+    prepared = herm.prepare_stack(params, settings, device)
+    states = herm.initial_states(settings, b, device)
+    logits, states = herm.prefill(prepared, settings, torch.from_numpy(ids).to(device), states)
+    want_states = [oherm.initial_state(b, cfg) for _ in params_np]
+    want_logits, want_states = oherm.prefill(params_np, want_states, ids, cfg, settings.scan_chunk)
+    scale = float(np.abs(want_logits).max())
+    _close(logits.cpu().numpy(), want_logits, scale, "prefill logits")
+    for layer, (got, want) in enumerate(zip(states, want_states)):
+        for key in ("working", "basis", "normalizer", "local_keys", "salient_keys", "salient_values"):
+            _close(got[key].cpu().numpy(), want[key], float(np.abs(want[key]).max()) + 1e-30, f"layer {layer} {key}")
+        for key in ("local_valid", "salient_valid", "last_token"):
+            np.testing.assert_array_equal(got[key].cpu().numpy(), want[key])
+    assert any(w["salient_valid"].any() for w in want_states)  # admission happened
+
+    # three greedy decode steps from the prefill state
+    next_ids = torch.from_numpy(ids[:, -1:]).to(device)
+    want_next = ids[:, -1:]
+    for step in range(3):
+        got_logits, states = herm.stack_window(prepared, settings, next_ids, states)
+        want_step_logits, want_states, _ = oherm.stack_window(params_np, want_states, want_next, cfg)
+        _close(got_logits.cpu().numpy(), want_step_logits, scale, f"decode step {step} logits")
+        scores = want_step_logits[:, -1].copy()
+        scores[:, PAD] = -np.inf
+        want_next = scores.argmax(axis=-1)[:, None]
+        top2 = np.sort(scores, axis=-1)[:, -2:]
+        assert np.all(top2[:, 1] - top2[:, 0] > 1e-3)  # no near-tie in this case
+        got_scores = got_logits[:, -1].clone()
+        got_scores[:, PAD] = float("-inf")
+        next_ids = got_scores.argmax(dim=-1, keepdim=True)
+        np.testing.assert_array_equal(next_ids.cpu().numpy(), want_next)
+
+
+def test_decode_graph_replays_match_eager_steps(device):
+    b = 3
+    settings = _settings(layers=2, salience_threshold=0.55)
+    params = herm.prepare_stack(_params(settings, seed=12), settings, device)
+    states = herm.initial_states(settings, b, device)
+    _, states = herm.prefill(params, settings, torch.from_numpy(_ids(b, 12, seed=4)).to(device), states)
+    ids = torch.tensor([[65], [66], [PAD]], device=device)
+    graph = herm.DecodeGraph(params, settings, ids, states)
+    eager_ids, eager_states = ids, states
+    for step in range(4):
+        eager_ids, eager_states = herm.decode_step(params, settings, eager_ids, eager_states)
+        torch.cuda.synchronize()
+        got = graph.step().clone()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), eager_ids.cpu().numpy())
+        for layer, (g, e) in enumerate(zip(graph.states, eager_states)):
+            for key, tensor in e.items():
+                if tensor.dtype.is_floating_point:
+                    torch.testing.assert_close(g[key], tensor, rtol=1e-5, atol=1e-5,
+                                               msg=lambda m: f"step {step} layer {layer} {key}: {m}")
+                else:
+                    assert torch.equal(g[key], tensor), f"step {step} layer {layer} {key}"
+
+
+def test_bf16_projections_stay_close_to_fp32(device):
+    b = 2
+    base = _settings(width=64, salience_threshold=2.0)  # admission off: no discrete flips
+    params = _params(base, seed=13)
+    ids = torch.from_numpy(_ids(b, 12, seed=5)).to(device)
+    out = {}
+    for dtype in (torch.float32, torch.bfloat16):
+        settings = dataclasses.replace(base, linear_dtype=dtype)
+        prepared = herm.prepare_stack(params, settings, device)
+        logits, _ = herm.prefill(prepared, settings, ids, herm.initial_states(settings, b, device))
+        assert torch.isfinite(logits).all()
+        out[dtype] = logits.double()
+    rel = float((out[torch.bfloat16] - out[torch.float32]).norm() / out[torch.float32].norm())
+    print(f"bf16 vs fp32 projections: relative error {rel:.3e}", flush=True)
+    assert rel < 5e-2
