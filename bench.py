@@ -12,7 +12,10 @@ a HIP graph and replayed (its three kernels are launch-bound at this size).
 Also measured and reported (same JSON line, "kernels"): the C1/C3 affine scan,
 the C3 RMSNorm-SiLU, the C4 MoE route/permute/grouped-GEMM/combine and one
 window's salient read at the C5 model shape ("C5w"), each as
-average kernel time from HIP events, GB/s or TFLOP/s, and the roofline fraction.
+average kernel time from HIP events, GB/s or TFLOP/s, and the roofline fraction,
+and the C5 end-to-end stack ("e": 12 random-initialised HERM blocks of width
+1024, prefill 8 x 2048 byte ids, then 256 greedy decode steps at batch 64),
+prefill and decode tokens/s from HIP-graph replays.
 The CPU baseline is the oracle's single-threaded C port of the same C2 step
 (and, as an extra, the reference's PyTorch formulas on all host cores).
 
@@ -64,8 +67,8 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,3,4,5,g",
-                    help="extra configurations to measure (comma list of 1,3,4,5,g; '' for none)")
+    ap.add_argument("--configs", default="1,3,4,5,g,e",
+                    help="extra configurations to measure (comma list of 1,3,4,5,g,e; '' for none)")
     ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -249,6 +252,22 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
             return torch.einsum("bts,bsd->btd", w, all_v)
 
         out["C5w.salient_read"] = {"ms": round(median_ms(read), 3), "sample": "full C5 window"}
+    if "e" in extra:
+        # One block window (batch 8, 128 tokens, width 1024) with the float64
+        # numpy restatement of forward_window, scaled to 16 windows x 12 layers.
+        import numpy as np
+
+        import oracle.herm as oherm
+        from koemi_amd import herm
+
+        settings = herm.HermSettings(layers=1)
+        params = [{k: v.double().numpy() for k, v in p.items()} for p in herm.init_stack(settings, 1005)]
+        cfg = settings.oracle_config()
+        ids = np.random.default_rng(1005).integers(0, 256, (8, 128))
+        state = oherm.initial_state(8, cfg)
+        window_ms = median_ms(lambda: oherm.block_window(params[0], state, ids, cfg))
+        out["C5.prefill"] = {"ms": round(window_ms * 16 * 12, 3),
+                             "sample": "one layer x one window (8 x 128 tokens), numpy float64 block restatement, x192"}
     return out
 
 
@@ -585,6 +604,48 @@ def main() -> int:
         kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
                                          "note": "gates then the affine scan (network.py:306-310)"}
         del ug, wts, vg
+
+    if "e" in extra:
+        # C5 end to end: 12 HERM blocks, width 1024, 16 experts top-2, byte
+        # vocabulary (+ PAD); prefill 8 x 2048 ids ~ U{0..255} in windows of 128,
+        # then 256 greedy decode steps at batch 64 from the empty static state.
+        log("C5 end-to-end stack (12 layers): graphed prefill and decode")
+        from koemi_amd import herm
+
+        settings = herm.HermSettings()
+        params = herm.prepare_stack(herm.init_stack(settings, 1005, device), settings, device)
+        ge = torch.Generator(device=device).manual_seed(1005)
+        ids = torch.randint(0, 256, (8, 2048), generator=ge, device=device)
+        start = herm.initial_states(settings, 8, device)
+        logits, _, graph = herm.prefill_graphed(params, settings, ids, start)
+        times = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits, _, graph = herm.prefill_graphed(params, settings, ids, start, graph)
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        prefill_s = sorted(times)[1]
+        assert torch.isfinite(logits).all()
+        kernels["C5.prefill"] = {"ms": round(prefill_s * 1e3, 3), "tokens_per_s": round(ids.numel() / prefill_s),
+                                 "shape": "12 layers x [8, 2048], windows of 128",
+                                 "note": "bf16 projections (the reference's default GPU precision), fp32 state; "
+                                         "each window replayed from one HIP graph"}
+        del graph, logits, start
+        dids = torch.randint(0, 256, (64, 1), generator=ge, device=device)
+        decode = herm.DecodeGraph(params, settings, dids, herm.initial_states(settings, 64, device))
+        for _ in range(3):
+            decode.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(256):
+            decode.step()
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+        kernels["C5.decode"] = {"ms": round(decode_s * 1e3, 3), "ms_per_step": round(decode_s * 1e3 / 256, 4),
+                                "tokens_per_s": round(64 * 256 / decode_s), "shape": "12 layers, batch 64, 256 steps",
+                                "note": "greedy, padding id masked; each step replayed from one HIP graph"}
+        del decode, params
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

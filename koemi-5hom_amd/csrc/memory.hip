@@ -15,13 +15,21 @@
 // workgroup copies the kept rows (zero rows for invalid slots).
 #include "common.hpp"
 
+#include <cstring>
+#include <type_traits>
+
 namespace koemi {
 namespace {
 
 constexpr int kTailThreads = 256;
 constexpr int64_t kMaxCapacity = 4096;
+constexpr int kTailSlotsPerBlock = 4;  // output slots copied by one workgroup
 
-template <typename T>
+// One workgroup per (batch row, group of kTailSlotsPerBlock output slots):
+// every workgroup of a row repeats the (cheap) slot selection in LDS, then
+// copies its own slots' key and value rows. VEC: width % 4 == 0 and 16-byte
+// (fp32) or 8-byte (half) aligned rows, copied four elements at a time.
+template <typename T, bool VEC>
 __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
     const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid, const T* __restrict__ k,
     const T* __restrict__ v, const uint8_t* __restrict__ adm, T* __restrict__ ok, T* __restrict__ ov,
@@ -64,23 +72,35 @@ __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
         }
     }
     __syncthreads();
-    for (int64_t s = tid; s < slots; s += kTailThreads) ovalid[b * slots + s] = slot_valid[s];
+    const int64_t s_begin = static_cast<int64_t>(blockIdx.y) * kTailSlotsPerBlock;
+    const int64_t s_end = min(slots, s_begin + kTailSlotsPerBlock);
+    if (s_begin + tid < s_end) ovalid[b * slots + s_begin + tid] = slot_valid[s_begin + tid];
     // Copy the kept rows; invalid slots are zero unless the outputs are the plain concatenation.
-    const int64_t elems = slots * D;
-    for (int64_t x = tid; x < elems; x += kTailThreads) {
-        const int64_t s = x / D, d = x - s * D;
+    for (int64_t s = s_begin; s < s_end; ++s) {
         const int64_t i = slot_entry[s];
         const bool zero = !concat && !slot_valid[s];
-        T kk, vv;
-        if (i < S) {
-            kk = ck[(b * S + i) * D + d];
-            vv = cv[(b * S + i) * D + d];
+        const T* ksrc = i < S ? ck + (b * S + i) * D : k + (b * L + (i - S)) * D;
+        const T* vsrc = i < S ? cv + (b * S + i) * D : v + (b * L + (i - S)) * D;
+        T* kdst = ok + (b * slots + s) * D;
+        T* vdst = ov + (b * slots + s) * D;
+        if constexpr (VEC) {
+            using V = typename std::conditional<sizeof(T) == 4, float4, uint2>::type;
+            const V* ks = reinterpret_cast<const V*>(ksrc);
+            const V* vs = reinterpret_cast<const V*>(vsrc);
+            V* kd = reinterpret_cast<V*>(kdst);
+            V* vd = reinterpret_cast<V*>(vdst);
+            V z;
+            memset(&z, 0, sizeof z);
+            for (int64_t q = tid; q < D / 4; q += kTailThreads) {
+                kd[q] = zero ? z : ks[q];
+                vd[q] = zero ? z : vs[q];
+            }
         } else {
-            kk = k[(b * L + (i - S)) * D + d];
-            vv = v[(b * L + (i - S)) * D + d];
+            for (int64_t d = tid; d < D; d += kTailThreads) {
+                kdst[d] = zero ? static_cast<T>(0.0f) : ksrc[d];
+                vdst[d] = zero ? static_cast<T>(0.0f) : vsrc[d];
+            }
         }
-        ok[(b * slots + s) * D + d] = zero ? static_cast<T>(0.0f) : kk;
-        ov[(b * slots + s) * D + d] = zero ? static_cast<T>(0.0f) : vv;
     }
 }
 
@@ -88,9 +108,18 @@ template <typename T>
 int launch_tail(const void* ck, const void* cv, const uint8_t* cvalid, const void* k, const void* v, const uint8_t* adm,
                 void* ok, void* ov, uint8_t* ovalid, int64_t B, int64_t S, int64_t L, int64_t D, int64_t C,
                 hipStream_t s) {
-    hipLaunchKernelGGL(salient_tail_kernel<T>, dim3(static_cast<unsigned>(B)), dim3(kTailThreads), 0, s,
-                       static_cast<const T*>(ck), static_cast<const T*>(cv), cvalid, static_cast<const T*>(k),
-                       static_cast<const T*>(v), adm, static_cast<T*>(ok), static_cast<T*>(ov), ovalid, S, L, D, C);
+    const int64_t slots = S + L <= C ? S + L : C;
+    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>((slots + kTailSlotsPerBlock - 1) / kTailSlotsPerBlock));
+    const size_t align = sizeof(T) == 4 ? 16 : 8;
+    auto aligned = [&](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % align == 0; };
+    const bool vec = D % 4 == 0 && aligned(ck) && aligned(cv) && aligned(k) && aligned(v) && aligned(ok) && aligned(ov);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kTailThreads), 0, s, static_cast<const T*>(ck), static_cast<const T*>(cv),
+                           cvalid, static_cast<const T*>(k), static_cast<const T*>(v), adm, static_cast<T*>(ok),
+                           static_cast<T*>(ov), ovalid, S, L, D, C);
+    };
+    if (vec) launch(salient_tail_kernel<T, true>);
+    else launch(salient_tail_kernel<T, false>);
     return check_launch("koemi_salient_tail");
 }
 

@@ -53,10 +53,12 @@ __all__ = [
     "HermSettings",
     "PAD_TOKEN_ID",
     "block_window",
+    "WindowGraph",
     "decode_step",
     "init_stack",
     "initial_states",
     "prefill",
+    "prefill_graphed",
     "prepare_stack",
     "stack_window",
 ]
@@ -359,42 +361,86 @@ def decode_step(params: list[dict[str, Tensor]], settings: HermSettings, ids: Te
     return scores.argmax(dim=-1, keepdim=True), states
 
 
-class DecodeGraph:
-    """Greedy decode steps replayed from one captured HIP graph.
+class WindowGraph:
+    """``stack_window`` at a fixed (batch, length) replayed from one captured HIP graph.
 
-    The step (``decode_step`` followed by copies of the next ids and states into
-    static buffers) is captured once over private copies of ``ids`` and
-    ``states``; each ``step()`` replays it, advancing ``self.ids`` and
-    ``self.states`` in place. Fixed shapes throughout (static rings), no host
-    synchronisation inside the step. Two eager steps on throwaway copies warm
-    the libraries up before the capture.
+    The window (every layer, then copies of the next states into static
+    buffers, and with ``greedy`` the next ids of a greedy decode step into the
+    static ids) is captured once over private copies of ``states``; each
+    ``run()`` copies the given ids in (unless greedy), replays, and leaves the
+    last layer's logits in ``self.logits`` and the advanced state in
+    ``self.states``. Fixed shapes (static rings), no host synchronisation and
+    no allocation inside the replay. Two eager windows on throwaway copies
+    warm the libraries up before the capture.
     """
 
-    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
-                 states: list[dict[str, Tensor]]) -> None:
+    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
+                 ids: Tensor, *, greedy: bool = False) -> None:
         self.params = params
         self.settings = settings
-        self.ids = ids.clone()
+        self.greedy = greedy
+        self.ids = ids.clone().contiguous()
         self.states = [{k: v.clone() for k, v in st.items()} for st in states]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             warm_ids, warm_states = self.ids.clone(), [{k: v.clone() for k, v in st.items()} for st in states]
             for _ in range(2):
-                warm_ids, warm_states = decode_step(params, settings, warm_ids, warm_states)
+                _, warm_states = stack_window(params, settings, warm_ids, warm_states)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self._step()
+            self.logits = self._window()
 
-    def _step(self) -> None:
-        next_ids, next_states = decode_step(self.params, self.settings, self.ids, self.states)
+    def _window(self) -> Tensor:
+        logits, next_states = stack_window(self.params, self.settings, self.ids, self.states)
         for state, new in zip(self.states, next_states):
             for key, tensor in state.items():
                 tensor.copy_(new[key])
-        self.ids.copy_(next_ids)
+        if self.greedy:
+            scores = logits[:, -1].clone()
+            scores[:, PAD_TOKEN_ID] = float("-inf")
+            self.ids.copy_(scores.argmax(dim=-1, keepdim=True))
+        return logits
+
+    def run(self, ids: Tensor | None = None) -> Tensor:
+        if ids is not None:
+            self.ids.copy_(ids)
+        self.graph.replay()
+        return self.logits
+
+
+class DecodeGraph(WindowGraph):
+    """Greedy decode steps (``decode_step``) replayed from one captured HIP
+    graph; ``step()`` advances ``self.ids`` ``[B, 1]`` and ``self.states`` in place."""
+
+    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                 states: list[dict[str, Tensor]]) -> None:
+        super().__init__(params, settings, states, ids, greedy=True)
 
     def step(self) -> Tensor:
-        self.graph.replay()
+        self.run()
         return self.ids
+
+
+def prefill_graphed(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                    states: list[dict[str, Tensor]], graph: WindowGraph | None = None
+                    ) -> tuple[Tensor, list[dict[str, Tensor]], WindowGraph]:
+    """``prefill`` with every window replayed from one ``WindowGraph`` (the
+    sequence length a multiple of ``scan_chunk``). Pass the graph of an earlier
+    call to reuse it; its state buffers are reset to ``states`` first."""
+
+    batch, length = ids.shape
+    chunk = settings.scan_chunk
+    if length % chunk:
+        raise ValueError("prefill_graphed needs a length that is a multiple of scan_chunk")
+    if graph is None:
+        graph = WindowGraph(params, settings, states, ids[:, :chunk])
+    for state, start in zip(graph.states, states):
+        for key, tensor in state.items():
+            tensor.copy_(start[key])
+    pieces = []
+    for begin in range(0, length, chunk):
+        pieces.append(graph.run(ids[:, begin:begin + chunk]).clone())
+    return torch.cat(pieces, dim=1), graph.states, graph

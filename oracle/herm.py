@@ -146,16 +146,19 @@ def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray,
     update = np.zeros_like(flat)
     a = assignments.reshape(-1, k)
     ok = valid.reshape(-1)
-    for t in np.nonzero(ok)[0]:
-        seen = set()
-        for e in a[t]:
-            if e < 0 or e >= count or e in seen:
-                continue
-            seen.add(int(e))
-            x = flat[t]
-            gate = linear(x, p["gate_w"][e], p["gate_b"][e])
-            up = linear(x, p["up_w"][e], p["up_b"][e])
-            update[t] += linear(gate / (1.0 + np.exp(-gate)) * up, p["down_w"][e], p["down_b"][e]) / k
+    # a slot counts when the token is valid, the expert in range and not
+    # already taken by an earlier slot of the token (experts.py:120-127, 261-267)
+    take = ok[:, None] & (a >= 0) & (a < count)
+    for slot in range(1, k):
+        take[:, slot] &= ~(a[:, :slot] == a[:, slot:slot + 1]).any(axis=1)
+    for e in range(count):
+        rows = np.nonzero((take & (a == e)).any(axis=1))[0]
+        if rows.size == 0:
+            continue
+        x = flat[rows]
+        gate = linear(x, p["gate_w"][e], p["gate_b"][e])
+        up = linear(x, p["up_w"][e], p["up_b"][e])
+        update[rows] += linear(gate / (1.0 + np.exp(-gate)) * up, p["down_w"][e], p["down_b"][e]) / k
     mixed = rms(flat + update, p["expert_norm"])
     out = np.where(ok[:, None], mixed, flat).reshape(b, length, d)
     return out, assignments

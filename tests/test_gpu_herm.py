@@ -164,3 +164,23 @@ def test_bf16_projections_stay_close_to_fp32(device):
     rel = float((out[torch.bfloat16] - out[torch.float32]).norm() / out[torch.float32].norm())
     print(f"bf16 vs fp32 projections: relative error {rel:.3e}", flush=True)
     assert rel < 5e-2
+
+
+def test_graphed_prefill_matches_the_eager_prefill(device):
+    b = 2
+    settings = _settings(salience_threshold=0.55)
+    params = herm.prepare_stack(_params(settings, seed=14), settings, device)
+    ids = torch.from_numpy(_ids(b, 12, seed=6)).to(device)
+    want_logits, want_states = herm.prefill(params, settings, ids, herm.initial_states(settings, b, device))
+    graph = None
+    for run in range(2):  # the second call reuses the captured window
+        logits, states, graph = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, b, device),
+                                                     graph)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(logits, want_logits, rtol=1e-5, atol=1e-5)
+        for g, e in zip(states, want_states):
+            for key, tensor in e.items():
+                if tensor.dtype.is_floating_point:
+                    torch.testing.assert_close(g[key], tensor, rtol=1e-5, atol=1e-5)
+                else:
+                    assert torch.equal(g[key], tensor), f"run {run} {key}"
