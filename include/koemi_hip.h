@@ -244,6 +244,25 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
                        void* out, int64_t batch, int64_t carried, int64_t length, int64_t width, int dtype,
                        void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
+/* Associative memory of one HERM block window: HierarchicalAssociativeMemory.
+ * project (the feature softmax, value tanh, bounded decay and write weight),
+ * query_features, fast_write_terms and scan_and_read of model/memory.py:82-144,
+ * 244-255, with the write masking of network.py:734-740 (torch composites in
+ * the reference). `projections` is fp32 [batch * length, row_stride] holding,
+ * at the given column offsets, the value pre-activations (width columns), the
+ * feature logits W_f key + b_f and W_f query + b_f (features columns each)
+ * and the decay and write logits (one column each); surprise fp32 and valid
+ * bytes [batch * length]; basis fp32 [batch, width, features], normalizer
+ * [batch, features]. Writes the reads [batch, length, width] and the window's
+ * final basis and normalizer (fp32). features <= 32; the window length is
+ * bounded by LDS ((132 + 2 features) x 4 bytes per position: at most 249
+ * positions with 16 features). No workspace. */
+int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset, int64_t feature_offset,
+                          int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset,
+                          const float* surprise, const uint8_t* valid, const float* basis, const float* normalizer,
+                          float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
+                          int64_t width, int64_t features, koemi_stream_t stream);
+
 /* Local-memory read, LocalKeyValueMemory.read_window of model/memory.py:332-362
  * without the novelty output (a torch composite in the reference; network.py:
  * 328-336). The read of koemi_salient_read with the sliding window of

@@ -38,6 +38,7 @@ SOURCES = (
     "salient_read.hip",
     "gates.hip",
     "blas.hip",
+    "assoc_memory.hip",
 )
 
 ARCH = "gfx950"

@@ -91,6 +91,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),
     ),
+    "koemi_assoc_scan_read": (
+        c_int,
+        (_P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64,
+         c_int64, c_int64, _P),
+    ),
     "koemi_local_read": (
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),

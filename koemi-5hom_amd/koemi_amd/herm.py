@@ -21,11 +21,13 @@ this package's HIP kernels:
 
 The projections are plain library GEMMs (``torch.nn.functional.linear`` on
 hipBLASLt) in ``HermSettings.linear_dtype`` with fp32 results; every other
-operation, the recurrent state and the memories are fp32. bf16 matches the
+operation (the associative memory's feature projection included), the
+recurrent state and the memories are fp32. bf16 matches the
 reference's default GPU precision (``resolve_precision("auto")`` selects bf16
 autocast on CUDA, model/gpu_precision.py:96-121); fp32 is the parity setting.
-The gates run in fp32 whatever ``linear_dtype`` is. The associative memory's
-scan-and-read (memory.py:97-144) and the small elementwise steps are torch
+The gates run in fp32 whatever ``linear_dtype`` is. The associative memory
+(projection tail, write terms, scan-and-read; memory.py:82-144) runs on
+``koemi_assoc_scan_read``; the remaining small elementwise steps are torch
 operations on device. The local read's novelty output, which only the refine
 path reads, is not computed.
 
@@ -46,7 +48,7 @@ import torch
 from torch import Tensor
 from torch.nn import functional
 
-from koemi_amd import memory, moe, recurrent, think
+from koemi_amd import _native, memory, moe, recurrent, think
 
 __all__ = [
     "DecodeGraph",
@@ -54,6 +56,7 @@ __all__ = [
     "PAD_TOKEN_ID",
     "block_window",
     "WindowGraph",
+    "associative_scan_read",
     "decode_step",
     "init_stack",
     "initial_states",
@@ -65,9 +68,6 @@ __all__ = [
 
 PAD_TOKEN_ID = 256             # configuration/settings.py:10-11
 _EPS = 1e-6                    # RootMeanSquareNorm epsilon (layers.py:9)
-_MIN_DECAY = 2.0**-12          # memory.py:74-75
-_MAX_DECAY = 1.0 - 2.0**-12
-_READ_EPSILON = 2.0**-8        # memory.py:77
 
 
 @dataclass(frozen=True)
@@ -136,9 +136,10 @@ def init_stack(settings: HermSettings, seed: int, device: torch.device | str = "
 
 
 def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, device: torch.device) -> list[dict[str, Tensor]]:
-    """Device copies laid out for the kernels: the seven projections of the
-    working states stacked into one GEMM, the GEMM weights in ``linear_dtype``,
-    the gates and the content head in fp32."""
+    """Device copies laid out for the kernels: the projections of the working
+    states stacked into one GEMM (local key, local value, value, the key's and
+    the query's feature logits with W_f folded in, decay, write), the GEMM
+    weights in ``linear_dtype``, the gates and the content head in fp32."""
 
     lin = settings.linear_dtype
     prepared = []
@@ -150,10 +151,17 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         q["input_norm"] = to(p["input_norm"])
         for name in ("retention", "candidate"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"]), to(p[name + "_b"])
-        order = ("local_key", "local_value", "key", "value", "query", "decay", "write")
-        q["ws_w"] = to(torch.cat([p[n + "_w"] for n in order]), lin)
-        q["ws_b"] = to(torch.cat([p[n + "_b"] for n in order]), lin)
-        q["feature_w"], q["feature_b"] = to(p["feature_w"], lin), to(p["feature_b"], lin)
+        # feature logits of the key and of the query are linear in the states:
+        # W_f (W_k x + b_k) + b_f = (W_f W_k) x + (W_f b_k + b_f), formed in float64
+        f64 = lambda name: p[name].double()
+        fk_w = f64("feature_w") @ f64("key_w")
+        fk_b = f64("feature_w") @ f64("key_b") + f64("feature_b")
+        fq_w = f64("feature_w") @ f64("query_w")
+        fq_b = f64("feature_w") @ f64("query_b") + f64("feature_b")
+        weights = [p["local_key_w"], p["local_value_w"], p["value_w"], fk_w, fq_w, p["decay_w"], p["write_w"]]
+        biases = [p["local_key_b"], p["local_value_b"], p["value_b"], fk_b, fq_b, p["decay_b"], p["write_b"]]
+        q["ws_w"] = to(torch.cat([w.double() for w in weights]), lin)
+        q["ws_b"] = to(torch.cat([b.double() for b in biases]), lin)
         q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"], lin)
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
@@ -219,32 +227,37 @@ def _last_valid_token_ids(ids: Tensor, valid: Tensor, carried: Tensor) -> Tensor
     return torch.where(last >= 0, gathered, carried)
 
 
-def _associative_scan_read(basis: Tensor, normalizer: Tensor, decay: Tensor, value: Tensor, features: Tensor,
-                           weight: Tensor, query_features: Tensor) -> tuple[Tensor, Tensor, Tensor]:
-    """HierarchicalAssociativeMemory.scan_and_read (memory.py:97-144), fp32:
-    reads from the state before each position's write, and the final state."""
+def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor, normalizer: Tensor,
+                          *, width: int, features: int) -> tuple[Tensor, Tensor, Tensor]:
+    """The associative memory of one window on ``koemi_assoc_scan_read``:
+    projection tail, fast write terms with the write masking and
+    scan_and_read (memory.py:82-144, 244-255; network.py:734-740).
 
-    log_decay = torch.log(decay)
-    cumulative = torch.cumsum(log_decay, dim=1)
-    prior = cumulative - log_decay
-    initial = torch.exp(prior)
-    length = decay.shape[1]
-    past = torch.ones((length, length), dtype=torch.bool, device=decay.device).tril(-1)
-    pair = torch.exp((prior.unsqueeze(-1) - cumulative.unsqueeze(1)).masked_fill(~past, float("-inf")))
-    similarity = torch.bmm(query_features, features.transpose(1, 2).contiguous())
-    influence = pair * similarity * weight.unsqueeze(1)
-    numerator = initial.unsqueeze(-1) * torch.bmm(query_features, basis.transpose(1, 2).contiguous())
-    numerator = numerator + torch.bmm(influence, value)
-    denominator = initial * torch.bmm(query_features, normalizer.unsqueeze(-1)).squeeze(-1) + influence.sum(dim=-1)
-    regularized = denominator.unsqueeze(-1) + _READ_EPSILON
-    read = (denominator.unsqueeze(-1) / regularized) * numerator / regularized
-    total = cumulative[:, -1]
-    final_weight = torch.exp(total.unsqueeze(1) - cumulative) * weight
-    scale = torch.exp(total)
-    final_basis = scale[:, None, None] * basis + torch.bmm((value * final_weight.unsqueeze(-1)).transpose(1, 2).contiguous(),
-                                                           features)
-    final_normalizer = scale[:, None] * normalizer + (final_weight.unsqueeze(-1) * features).sum(dim=1)
-    return read, final_basis, final_normalizer
+    ``projections`` fp32 ``[B, L, 3 D + 2 M + 2]``, the stacked working-state
+    projection: local key, local value and value pre-activations (D columns
+    each), the feature logits of the key and of the query (M each; W_f W_k and
+    W_f W_q folded into the projection) and the decay and write logits.
+    ``surprise`` ``[B, L]`` fp32, ``valid`` ``[B, L]`` bool, ``basis``
+    ``[B, D, M]``, ``normalizer`` ``[B, M]`` fp32. Returns (reads ``[B, L, D]``,
+    next basis, next normalizer).
+    """
+
+    batch, length, stride = projections.shape
+    d, m = width, features
+    if stride != 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
+        raise ValueError("projections must be contiguous fp32 [batch, length, 3 * width + 2 * features + 2]")
+    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
+    next_basis = torch.empty_like(basis)
+    next_normalizer = torch.empty_like(normalizer)
+    args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
+    _native.call(
+        "koemi_assoc_scan_read",
+        _native.ptr(projections), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        *(_native.ptr(t) for t in args),
+        _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
+        batch, length, d, m, _native.stream_of(projections.device),
+    )
+    return read, next_basis, next_normalizer
 
 
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
@@ -266,23 +279,16 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     targets = torch.where(valid, ids, torch.zeros_like(ids))
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
-    projected = _linear(ws, p["ws_w"], p["ws_b"])
-    local_keys, local_values, key, value, query, decay, write = torch.split(projected, [d, d, d, d, d, 1, 1], dim=-1)
+    projected = _linear(ws, p["ws_w"], p["ws_b"]).contiguous()
+    local_keys, local_values = torch.split(projected[..., : 2 * d], [d, d], dim=-1)
     keep = valid.unsqueeze(-1)
     local_keys = torch.where(keep, local_keys, torch.zeros_like(local_keys)).contiguous()
     local_values = torch.where(keep, local_values, torch.zeros_like(local_values)).contiguous()
     local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
                                            local_keys, local_values, valid, ws, window=settings.local_memory_size)
 
-    feature_logits = _linear(torch.stack((key, query)), p["feature_w"], p["feature_b"])
-    features, query_features = torch.softmax(feature_logits, dim=-1).unbind(0)
-    value = torch.tanh(value).contiguous()
-    decay = _MIN_DECAY + (_MAX_DECAY - _MIN_DECAY) * torch.sigmoid(decay.squeeze(-1))
-    write = torch.sigmoid(write.squeeze(-1)) * (0.25 + 0.75 * surprise.clamp(0.0, 1.0))
-    decay = torch.where(valid, decay, torch.ones_like(decay))
-    write = torch.where(valid, write, torch.zeros_like(write))
-    fast, basis, normalizer = _associative_scan_read(state["basis"], state["normalizer"], decay, value,
-                                                     features.contiguous(), write, query_features.contiguous())
+    fast, basis, normalizer = associative_scan_read(projected, surprise, valid, state["basis"], state["normalizer"],
+                                                    width=d, features=settings.memory_features)
 
     admission, _ = think.salience_admission(surprise, valid, threshold=settings.salience_threshold)
     salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],

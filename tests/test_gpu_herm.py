@@ -184,3 +184,38 @@ def test_graphed_prefill_matches_the_eager_prefill(device):
                     torch.testing.assert_close(g[key], tensor, rtol=1e-5, atol=1e-5)
                 else:
                     assert torch.equal(g[key], tensor), f"run {run} {key}"
+
+
+@pytest.mark.parametrize("b, length, d, m", [(2, 130, 100, 16), (3, 1, 64, 16), (2, 9, 36, 5), (1, 70, 128, 32)])
+def test_associative_kernel_matches_the_oracle(device, b, length, d, m):
+    """koemi_assoc_scan_read (memory.py:82-144, 244-255; network.py:734-740)
+    against oracle/herm.py's float64 scan-and-read fed with the same terms
+    (features = softmax of the given key/query feature logits, value = tanh,
+    bounded decay, surprise-scaled write weight, masking): several 64-row
+    influence tiles, partial 64-column chunks, one position (the decode step)
+    and 5 or 32 features; fp32 tolerance 1e-4 relative + 1e-5 x max|result|."""
+
+    rng = np.random.default_rng(b * 1000 + length)
+    proj = rng.normal(size=(b, length, 3 * d + 2 * m + 2)).astype(np.float32)
+    surprise = rng.random((b, length)).astype(np.float32)
+    valid = rng.random((b, length)) < 0.8
+    basis = rng.normal(size=(b, d, m)).astype(np.float32)
+    normalizer = rng.random((b, m)).astype(np.float32)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    read, nb, nn = herm.associative_scan_read(t(proj), t(surprise), t(valid), t(basis), t(normalizer), width=d,
+                                              features=m)
+    p64 = proj.astype(np.float64)
+    value = np.tanh(p64[..., 2 * d:3 * d])
+    features = oherm.softmax(p64[..., 3 * d:3 * d + m])
+    qf = oherm.softmax(p64[..., 3 * d + m:3 * d + 2 * m])
+    decay = oherm.MIN_DECAY + (oherm.MAX_DECAY - oherm.MIN_DECAY) * oherm.sigmoid(p64[..., 3 * d + 2 * m])
+    weight = oherm.sigmoid(p64[..., 3 * d + 2 * m + 1]) * (0.25 + 0.75 * np.clip(surprise, 0, 1))
+    decay = np.where(valid, decay, 1.0)
+    weight = np.where(valid, weight, 0.0)
+    want = oherm.associative_scan_read(basis.astype(np.float64), normalizer.astype(np.float64), decay, value,
+                                       features, weight, qf)
+    for got, ref, name in zip((read, nb, nn), want, ("read", "basis", "normalizer")):
+        err = np.abs(got.cpu().numpy().astype(np.float64) - ref)
+        scale = float(np.abs(ref).max())
+        print(f"assoc {name} b={b} L={length} d={d} m={m}: max_abs={err.max():.3e} scale={scale:.3e}", flush=True)
+        assert np.all(err <= 1e-4 * np.abs(ref) + 1e-5 * scale), name
