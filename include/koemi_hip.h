@@ -263,6 +263,28 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
                           float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
                           int64_t width, int64_t features, koemi_stream_t stream);
 
+/* Small per-window steps of the HERM block (torch composites in the reference).
+ * koemi_herm_rmsnorm: out = RootMeanSquareNorm(x + residual) * weight
+ * (layers.py:14-16) on rows whose mask byte is set (all rows when mask is
+ * NULL), out = x elsewhere (the expert mixture's valid-row select,
+ * experts.py:134-136); x, weight and out fp32 [rows, width], residual NULL or
+ * [rows, width] in residual_dtype; width a multiple of 4, at most 2048.
+ * koemi_herm_token_context: previous[b, t] = the last valid token before t
+ * (carried_last[b] before the first), last[b] = the window's last valid token
+ * or carried_last[b] (network.py:742-761); int64 ids, valid bytes.
+ * koemi_herm_local_tail: the local ring after a window, the last `window`
+ * entries of [carried (window entries) ; new (length entries)] with their
+ * valid bytes (memory.py:385-403); fp32 keys and values [batch, *, width]. */
+int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
+                       const uint8_t* mask, float* output, int64_t rows, int64_t width, float eps,
+                       koemi_stream_t stream);
+int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
+                             int64_t* previous, int64_t* last, int64_t batch, int64_t length, koemi_stream_t stream);
+int koemi_herm_local_tail(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
+                          const float* keys, const float* values, const uint8_t* valid, float* out_keys,
+                          float* out_values, uint8_t* out_valid, int64_t batch, int64_t window, int64_t length,
+                          int64_t width, koemi_stream_t stream);
+
 /* Local-memory read, LocalKeyValueMemory.read_window of model/memory.py:332-362
  * without the novelty output (a torch composite in the reference; network.py:
  * 328-336). The read of koemi_salient_read with the sliding window of

@@ -1,0 +1,163 @@
+// Small per-window steps of the HERM block for gfx950 (torch composites in
+// the reference), each one kernel:
+//
+//   koemi_herm_rmsnorm: RootMeanSquareNorm (layers.py:14-16) of x (+ an
+//     optional residual), kept only on rows whose mask byte is set (others
+//     copy x): the input normalizer (network.py:703-707), the fusion normalizer
+//     (network.py:723-732) and the expert mixture's output normalizer with its
+//     valid-row select (experts.py:134-136). One wave per row, the row in
+//     registers, fp32 sum of squares, 16-byte loads.
+//   koemi_herm_token_context: the previous valid token of each position and
+//     the last valid token of each row (network.py:742-761). One thread per
+//     row walks its window.
+//   koemi_herm_local_tail: the local ring after a window, the last `window`
+//     entries of [carried ; new] with their valid bytes (memory.py:385-403).
+#include "common.hpp"
+
+namespace koemi {
+namespace {
+
+template <typename R, int NV>
+__global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restrict__ x, const R* __restrict__ residual,
+                                                           const float* __restrict__ w,
+                                                           const uint8_t* __restrict__ mask, float* __restrict__ y,
+                                                           int64_t rows, int H, float eps) {
+    const int lane = lane_id();
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const float* xr = x + row * H;
+    float v[NV][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        if (c < H) {
+            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            v[j][0] = q.x; v[j][1] = q.y; v[j][2] = q.z; v[j][3] = q.w;
+            if (residual != nullptr) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[j][i] += to_f32(residual[row * H + c + i]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[j][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = fmaf(v[j][i], v[j][i], ss);
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    const bool keep = mask == nullptr || mask[row] != 0;
+    const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
+    float* yr = y + row * H;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        if (c >= H) continue;
+        float4 o;
+        if (keep) {
+            const float4 wq = *reinterpret_cast<const float4*>(w + c);
+            o = make_float4(v[j][0] * inv * wq.x, v[j][1] * inv * wq.y, v[j][2] * inv * wq.z, v[j][3] * inv * wq.w);
+        } else {
+            o = *reinterpret_cast<const float4*>(xr + c);
+        }
+        *reinterpret_cast<float4*>(yr + c) = o;
+    }
+}
+
+__global__ void herm_token_context_kernel(const int64_t* __restrict__ ids, const uint8_t* __restrict__ valid,
+                                          const int64_t* __restrict__ carried, int64_t* __restrict__ previous,
+                                          int64_t* __restrict__ last, int64_t B, int64_t L) {
+    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    int64_t latest = carried[b];
+    for (int64_t t = 0; t < L; ++t) {
+        previous[b * L + t] = latest;
+        if (valid[b * L + t]) latest = ids[b * L + t];
+    }
+    last[b] = latest;
+}
+
+__global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float* __restrict__ cv,
+                                       const uint8_t* __restrict__ cvalid, const float* __restrict__ k,
+                                       const float* __restrict__ v, const uint8_t* __restrict__ valid,
+                                       float* __restrict__ ok, float* __restrict__ ov, uint8_t* __restrict__ ovalid,
+                                       int64_t W, int64_t L, int64_t D) {
+    // block (b, slot): output slot s holds entry W + L - (W - s) of [carried (W) ; new (L)]
+    const int64_t b = blockIdx.x, s = blockIdx.y;
+    const int64_t i = L + s;  // index into the concatenation
+    const bool carried_entry = i < W;
+    const float* ks = carried_entry ? ck + (b * W + i) * D : k + (b * L + (i - W)) * D;
+    const float* vs = carried_entry ? cv + (b * W + i) * D : v + (b * L + (i - W)) * D;
+    float* kd = ok + (b * W + s) * D;
+    float* vd = ov + (b * W + s) * D;
+    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+        kd[d] = ks[d];
+        vd[d] = vs[d];
+    }
+    if (threadIdx.x == 0) ovalid[b * W + s] = carried_entry ? cvalid[b * W + i] : valid[b * L + (i - W)];
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
+                                  const uint8_t* mask, float* output, int64_t rows, int64_t width, float eps,
+                                  koemi_stream_t stream) {
+    if (rows < 0 || width < 1) return fail(KOEMI_ERR_INVALID, "herm rmsnorm needs rows >= 0 and a positive width");
+    if (width % 4 != 0 || width > 4 * kWave * 8)
+        return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm needs a width that is a multiple of 4 and at most 2048");
+    if (residual != nullptr && residual_dtype != KOEMI_F32 && residual_dtype != KOEMI_BF16 && residual_dtype != KOEMI_F16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm residual dtype %s", dtype_name(residual_dtype));
+    if (rows == 0) return KOEMI_OK;
+    if (!input || !weight || !output) return fail(KOEMI_ERR_INVALID, "herm rmsnorm received a null pointer");
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+    const hipStream_t s = as_stream(stream);
+    const int H = static_cast<int>(width);
+    auto launch = [&](auto tag) {
+        using R = decltype(tag);
+        const R* r = static_cast<const R*>(residual);
+        if (width <= 4 * kWave * 4)
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 4>), grid, dim3(256), 0, s, input, r, weight, mask, output, rows,
+                               H, eps);
+        else
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 8>), grid, dim3(256), 0, s, input, r, weight, mask, output, rows,
+                               H, eps);
+    };
+    if (residual == nullptr || residual_dtype == KOEMI_F32) launch(float{});
+    else if (residual_dtype == KOEMI_BF16) launch(bf16{});
+    else launch(f16{});
+    return check_launch("koemi_herm_rmsnorm");
+}
+
+extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
+                                        int64_t* previous, int64_t* last, int64_t batch, int64_t length,
+                                        koemi_stream_t stream) {
+    if (batch < 0 || length < 0) return fail(KOEMI_ERR_INVALID, "token context needs non-negative sizes");
+    if (batch == 0) return KOEMI_OK;
+    if (!token_ids || !valid || !carried_last || !previous || !last)
+        return fail(KOEMI_ERR_INVALID, "token context received a null pointer");
+    hipLaunchKernelGGL(herm_token_context_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0,
+                       as_stream(stream), token_ids, valid, carried_last, previous, last, batch, length);
+    return check_launch("koemi_herm_token_context");
+}
+
+extern "C" int koemi_herm_local_tail(const float* carried_keys, const float* carried_values,
+                                     const uint8_t* carried_valid, const float* keys, const float* values,
+                                     const uint8_t* valid, float* out_keys, float* out_values, uint8_t* out_valid,
+                                     int64_t batch, int64_t window, int64_t length, int64_t width,
+                                     koemi_stream_t stream) {
+    if (batch < 0 || window < 1 || length < 0 || width < 1)
+        return fail(KOEMI_ERR_INVALID, "local tail needs batch, length >= 0 and positive window and width");
+    if (window > 65535 || batch > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "local tail grid too large");
+    if (batch == 0) return KOEMI_OK;
+    if (!carried_keys || !carried_values || !carried_valid || (length > 0 && (!keys || !values || !valid)) ||
+        !out_keys || !out_values || !out_valid)
+        return fail(KOEMI_ERR_INVALID, "local tail received a null pointer");
+    hipLaunchKernelGGL(herm_local_tail_kernel, dim3(static_cast<unsigned>(batch), static_cast<unsigned>(window)),
+                       dim3(256), 0, as_stream(stream), carried_keys, carried_values, carried_valid, keys, values,
+                       valid, out_keys, out_values, out_valid, window, length, width);
+    return check_launch("koemi_herm_local_tail");
+}

@@ -39,6 +39,7 @@ SOURCES = (
     "gates.hip",
     "blas.hip",
     "assoc_memory.hip",
+    "herm_glue.hip",
 )
 
 ARCH = "gfx950"

@@ -197,34 +197,57 @@ def initial_states(settings: HermSettings, batch: int, device: torch.device) -> 
     return states
 
 
-def _rms(x: Tensor, weight: Tensor) -> Tensor:
-    """RootMeanSquareNorm.forward (layers.py:14-16)."""
+def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor | None = None) -> Tensor:
+    """RootMeanSquareNorm.forward (layers.py:14-16) of ``x (+ residual)`` on
+    ``koemi_herm_rmsnorm``; with ``mask``, rows whose mask is false keep ``x``
+    (the expert mixture's valid-row select, experts.py:134-136)."""
 
-    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + _EPS) * weight
+    x = x.contiguous()
+    width = x.shape[-1]
+    out = torch.empty_like(x)
+    residual = residual.contiguous() if residual is not None else None
+    mask = mask.contiguous() if mask is not None else None
+    _native.call(
+        "koemi_herm_rmsnorm", _native.ptr(x), _native.ptr(residual) if residual is not None else None,
+        _native.dtype_code(residual.dtype) if residual is not None else 0, _native.ptr(weight),
+        _native.ptr(mask) if mask is not None else None, _native.ptr(out), x.numel() // width, width, _EPS,
+        _native.stream_of(x.device),
+    )
+    return out
 
 
 def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
     return functional.linear(x.to(weight.dtype), weight, bias).float()
 
 
-def _previous_token_ids(ids: Tensor, valid: Tensor, carried: Tensor) -> Tensor:
-    """network.py:742-749: the previous valid token, or the carried last token."""
+def _token_context(ids: Tensor, valid: Tensor, carried: Tensor) -> tuple[Tensor, Tensor]:
+    """The previous valid token of each position and the last valid token of
+    each row (network.py:742-761) on ``koemi_herm_token_context``."""
 
-    length = ids.shape[1]
-    index = torch.arange(length, device=ids.device).expand_as(ids)
-    latest = torch.cummax(torch.where(valid, index, torch.full_like(index, -1)), dim=1).values
-    previous = torch.cat((torch.full_like(latest[:, :1], -1), latest[:, :-1]), dim=1)
-    gathered = ids.gather(1, previous.clamp_min(0))
-    return torch.where(previous >= 0, gathered, carried.unsqueeze(1))
+    batch, length = ids.shape
+    previous = torch.empty_like(ids)
+    last = torch.empty_like(carried)
+    _native.call("koemi_herm_token_context", _native.ptr(ids), _native.ptr(valid), _native.ptr(carried),
+                 _native.ptr(previous), _native.ptr(last), batch, length, _native.stream_of(ids.device))
+    return previous, last
 
 
-def _last_valid_token_ids(ids: Tensor, valid: Tensor, carried: Tensor) -> Tensor:
-    """network.py:751-761."""
+def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: Tensor,
+                window: int) -> tuple[Tensor, Tensor, Tensor]:
+    """LocalKeyValueMemory.tail (memory.py:385-403) of a static ring of
+    ``window`` entries on ``koemi_herm_local_tail``."""
 
-    index = torch.arange(ids.shape[1], device=ids.device).expand_as(ids)
-    last = torch.where(valid, index, torch.full_like(index, -1)).amax(dim=1)
-    gathered = ids.gather(1, last.clamp_min(0).unsqueeze(1)).squeeze(1)
-    return torch.where(last >= 0, gathered, carried)
+    batch, length, width = keys.shape
+    if state["local_keys"].shape[1] != window:
+        raise ValueError("the local ring must hold exactly `window` entries (static state)")
+    out_k = torch.empty_like(state["local_keys"])
+    out_v = torch.empty_like(state["local_values"])
+    out_ok = torch.empty_like(state["local_valid"])
+    _native.call("koemi_herm_local_tail", _native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
+                 _native.ptr(state["local_valid"]), _native.ptr(keys), _native.ptr(values), _native.ptr(valid),
+                 _native.ptr(out_k), _native.ptr(out_v), _native.ptr(out_ok), batch, window, length, width,
+                 _native.stream_of(keys.device))
+    return out_k, out_v, out_ok
 
 
 def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor, normalizer: Tensor,
@@ -276,14 +299,14 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     ws = recurrent.recurrent_scan(u, p["retention_w"], p["retention_b"], p["candidate_w"], p["candidate_b"], valid,
                                   state["working"])
     prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
-    targets = torch.where(valid, ids, torch.zeros_like(ids))
+    targets = torch.where(valid, ids, 0)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
     projected = _linear(ws, p["ws_w"], p["ws_b"]).contiguous()
     local_keys, local_values = torch.split(projected[..., : 2 * d], [d, d], dim=-1)
     keep = valid.unsqueeze(-1)
-    local_keys = torch.where(keep, local_keys, torch.zeros_like(local_keys)).contiguous()
-    local_values = torch.where(keep, local_values, torch.zeros_like(local_values)).contiguous()
+    local_keys = torch.where(keep, local_keys, 0.0)
+    local_values = torch.where(keep, local_values, 0.0)
     local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
                                            local_keys, local_values, valid, ws, window=settings.local_memory_size)
 
@@ -296,7 +319,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     fused = _rms(_linear(torch.cat((ws, fast, local_value, salient_value), dim=-1), p["fusion_w"], p["fusion_b"]),
                  p["fusion_norm"])
 
-    previous = _previous_token_ids(ids, valid, state["last_token"])
+    previous, last_token = _token_context(ids, valid, state["last_token"])
     k = settings.top_k
     assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
                                        validate=False)
@@ -307,25 +330,24 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
         validate=False)
     expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
                                                   p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
-    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
-                              validate=False).float()
-    final = torch.where(flat_valid.unsqueeze(-1), _rms(flat + update, p["expert_norm"]), flat).view(batch, length, d)
+    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k, validate=False)
+    final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
     logits = _linear(final, p["head_w"], p["head_b"])
 
-    w = settings.local_memory_size
+    local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
     salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
                                   local_values, admission, settings.salience_memory_size)
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
         "normalizer": normalizer,
-        "local_keys": torch.cat((state["local_keys"], local_keys), dim=1)[:, -w:].contiguous(),
-        "local_values": torch.cat((state["local_values"], local_values), dim=1)[:, -w:].contiguous(),
-        "local_valid": torch.cat((state["local_valid"], valid), dim=1)[:, -w:].contiguous(),
+        "local_keys": local_ring[0],
+        "local_values": local_ring[1],
+        "local_valid": local_ring[2],
         "salient_keys": salient[0],
         "salient_values": salient[1],
         "salient_valid": salient[2],
-        "last_token": _last_valid_token_ids(ids, valid, state["last_token"]),
+        "last_token": last_token,
     }
     return logits, final, next_state, surprise
 
