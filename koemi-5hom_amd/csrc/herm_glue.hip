@@ -8,8 +8,8 @@
 //     valid-row select (experts.py:134-136). One wave per row, the row in
 //     registers, fp32 sum of squares, 16-byte loads.
 //   koemi_herm_token_context: the previous valid token of each position and
-//     the last valid token of each row (network.py:742-761). One thread per
-//     row walks its window.
+//     the last valid token of each row (network.py:742-761). One workgroup per
+//     row, a max-scan of the valid positions.
 //   koemi_herm_local_tail: the local ring after a window, the last `window`
 //     entries of [carried ; new] with their valid bytes (memory.py:385-403).
 #include "common.hpp"
@@ -65,17 +65,40 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restri
     }
 }
 
-__global__ void herm_token_context_kernel(const int64_t* __restrict__ ids, const uint8_t* __restrict__ valid,
-                                          const int64_t* __restrict__ carried, int64_t* __restrict__ previous,
-                                          int64_t* __restrict__ last, int64_t B, int64_t L) {
-    const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    int64_t latest = carried[b];
-    for (int64_t t = 0; t < L; ++t) {
-        previous[b * L + t] = latest;
-        if (valid[b * L + t]) latest = ids[b * L + t];
+// One workgroup per row: position t takes the latest valid index before it,
+// an exclusive max-scan of (valid ? t : -1) over 256-position chunks (a wave
+// scan, the wave maxima through LDS, the chunk's carry in a register).
+__global__ __launch_bounds__(256) void herm_token_context_kernel(const int64_t* __restrict__ ids,
+                                                                 const uint8_t* __restrict__ valid,
+                                                                 const int64_t* __restrict__ carried,
+                                                                 int64_t* __restrict__ previous,
+                                                                 int64_t* __restrict__ last, int64_t L) {
+    __shared__ int wave_max[4];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    int carry = -1;  // latest valid index before the chunk
+    for (int64_t c0 = 0; c0 < L; c0 += 256) {
+        const int64_t t = c0 + tid;
+        const int mine = (t < L && valid[b * L + t]) ? static_cast<int>(t) : -1;
+        int incl = mine;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int up = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl = max(incl, up);
+        }
+        if (lane == kWave - 1) wave_max[wave] = incl;
+        __syncthreads();
+        int before = carry;
+        for (int w = 0; w < wave; ++w) before = max(before, wave_max[w]);
+        const int left = __shfl_up(incl, 1, kWave);  // every lane takes part
+        const int prev_index = lane > 0 ? max(before, left) : before;
+        if (t < L) previous[b * L + t] = prev_index >= 0 ? ids[b * L + prev_index] : carried[b];
+        int chunk_max = carry;
+        for (int w = 0; w < 4; ++w) chunk_max = max(chunk_max, wave_max[w]);
+        __syncthreads();
+        carry = chunk_max;
     }
-    last[b] = latest;
+    if (tid == 0) last[b] = carry >= 0 ? ids[b * L + carry] : carried[b];
 }
 
 __global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float* __restrict__ cv,
@@ -139,8 +162,9 @@ extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t*
     if (batch == 0) return KOEMI_OK;
     if (!token_ids || !valid || !carried_last || !previous || !last)
         return fail(KOEMI_ERR_INVALID, "token context received a null pointer");
-    hipLaunchKernelGGL(herm_token_context_kernel, dim3(static_cast<unsigned>((batch + 63) / 64)), dim3(64), 0,
-                       as_stream(stream), token_ids, valid, carried_last, previous, last, batch, length);
+    if (batch > 0x7fffffffLL || length > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "token context sizes too large");
+    hipLaunchKernelGGL(herm_token_context_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), 0, as_stream(stream),
+                       token_ids, valid, carried_last, previous, last, length);
     return check_launch("koemi_herm_token_context");
 }
 

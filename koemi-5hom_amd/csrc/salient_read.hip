@@ -73,12 +73,17 @@ __device__ __forceinline__ float4 load4_f32(const T* p) {
     }
 }
 
-// Slot tiles (32 slots each) of query tile y that hold an eligible slot for
-// some query of the tile: slot s is eligible for query t only if s < S + t, so
-// tile x is needed when 32 x < S + t_max.
-__host__ __device__ inline int active_slot_tiles(int y, int S, int L, int K) {
+// Slot tiles (32 slots each) of query tile y that can hold an eligible slot
+// for some query of the tile: slot s is eligible for query t only if
+// s < S + t (and s >= S + t - window with a sliding window), so the tiles
+// x in [first_slot_tile, first_slot_tile + active_slot_tiles) are needed:
+// 32 x < S + t_max and 32 x + 31 >= S + t_min - window.
+__host__ __device__ inline int first_slot_tile(int y, int S, int window) {
+    return window > 0 ? max(0, (S + 32 * y - window) / 32) : 0;
+}
+__host__ __device__ inline int active_slot_tiles(int y, int S, int L, int K, int window) {
     const int t_max = min(32 * y + 31, L - 1);
-    return min((K + 31) / 32, (S + t_max + 31) / 32);
+    return max(0, min((K + 31) / 32, (S + t_max + 31) / 32) - first_slot_tile(y, S, window));
 }
 
 // Partial scores of one (32 slots, 32 queries, batch, quarter of the width)
@@ -99,7 +104,7 @@ __host__ __device__ inline int active_slot_tiles(int y, int S, int L, int K) {
 template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void salient_scores_kernel(
     const T* __restrict__ ck, const T* __restrict__ k, const T* __restrict__ q, float* __restrict__ partial,
-    int B, int S, int L, int64_t D, float inv_sqrt_d, int tiles, int total, int per_xcd) {
+    int B, int S, int L, int64_t D, float inv_sqrt_d, int tiles, int total, int per_xcd, int window) {
     const int pid = static_cast<int>(blockIdx.x);
     const int logical = (pid & 7) * per_xcd + (pid >> 3);
     if (logical >= total) return;
@@ -107,12 +112,12 @@ __global__ __launch_bounds__(256) void salient_scores_kernel(
     int rem = logical - group * tiles, y = 0;
     const int K = S + L;
     for (;; ++y) {
-        const int n = active_slot_tiles(y, S, L, K);
+        const int n = active_slot_tiles(y, S, L, K, window);
         if (rem < n) break;
         rem -= n;
     }
     const int b = group / kParts, part = group % kParts;
-    const int s0 = rem * 32, q0 = y * 32;
+    const int s0 = (first_slot_tile(y, S, window) + rem) * 32, q0 = y * 32;
     const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
     const int r = lane & 31, h = lane >> 5;
     const int64_t nch = (D + kChunk - 1) / kChunk, per_part = (nch + kParts - 1) / kParts;
@@ -247,12 +252,13 @@ __global__ __launch_bounds__(256) void salient_softmax_kernel(
 // and the 16 value rows 32 blk + 16 h + s at column d0 + 32 w + r; step
 // s = 4 i + j pairs component j of group i with value row s, so each lane's
 // weight and value refer to the same slot. Blocks past the last slot that is
-// eligible for some query of the tile (S + t_max) are skipped (their weights
-// are zero); value rows are requested two blocks ahead of use.
+// eligible for some query of the tile (S + t_max), and with a sliding window
+// the blocks before its first one, are skipped (their weights are zero);
+// value rows are requested two blocks ahead of use.
 template <typename T>
 __global__ __launch_bounds__(512) void salient_pv_kernel(
     const float* __restrict__ weight, const T* __restrict__ cv, const T* __restrict__ v, T* __restrict__ out,
-    int B, int S, int L, int64_t D, int Kp) {
+    int B, int S, int L, int64_t D, int Kp, int window) {
     const int64_t d0 = static_cast<int64_t>(blockIdx.x) * 128;
     const int q0 = static_cast<int>(blockIdx.y) * 32, b = static_cast<int>(blockIdx.z);
     const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
@@ -261,8 +267,9 @@ __global__ __launch_bounds__(512) void salient_pv_kernel(
     const int K = S + L;
     const int t_max = min(q0 + 31, L - 1);
     const int all_blocks = (min(K, S + t_max) + 31) / 32;
-    const int first_end = (all_blocks + 1) / 2;
-    const int blk0 = second ? first_end : 0, blocks = second ? all_blocks : first_end;
+    const int lo = min(first_slot_tile(q0 / 32, S, window), all_blocks);
+    const int first_end = lo + (all_blocks - lo + 1) / 2;
+    const int blk0 = second ? first_end : lo, blocks = second ? all_blocks : first_end;
     const float* wrow = weight + (static_cast<int64_t>(b) * L + min(q0 + r, L - 1)) * Kp + 16 * h;
     const int64_t dw = d0 + slice * 32;
     const int64_t dcol = min(dw + r, D - 1);
@@ -452,7 +459,8 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
         const int Bi = static_cast<int>(batch), Si = static_cast<int>(carried), Li = static_cast<int>(length);
         const int Ki = static_cast<int>(K), Kp = (Ki + 31) / 32 * 32;
         int tiles = 0;
-        for (int y = 0; y < (Li + 31) / 32; ++y) tiles += active_slot_tiles(y, Si, Li, Ki);
+        const int win = static_cast<int>(window);
+        for (int y = 0; y < (Li + 31) / 32; ++y) tiles += active_slot_tiles(y, Si, Li, Ki, win);
         const int64_t total = static_cast<int64_t>(tiles) * Bi * kParts;
         if (total > 0x3fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "salient read grid too large");
         const int per_xcd = static_cast<int>((total + 7) / 8);
@@ -470,7 +478,7 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
                     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(8 * per_xcd)), dim3(256), 0, s,
                                        static_cast<const T*>(carried_keys), static_cast<const T*>(keys),
                                        static_cast<const T*>(queries), score, Bi, Si, Li, width, inv_sqrt_d, tiles,
-                                       static_cast<int>(total), per_xcd);
+                                       static_cast<int>(total), per_xcd, win);
                 };
                 if (vec) scores_kernel(salient_scores_kernel<T, true>);
                 else scores_kernel(salient_scores_kernel<T, false>);
@@ -488,7 +496,7 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
                                dim3(static_cast<unsigned>((width + 127) / 128), static_cast<unsigned>((Li + 31) / 32),
                                     static_cast<unsigned>(Bi)),
                                dim3(512), 0, s, weight32, static_cast<const T*>(carried_values),
-                               static_cast<const T*>(values), static_cast<T*>(out), Bi, Si, Li, width, Kp);
+                               static_cast<const T*>(values), static_cast<T*>(out), Bi, Si, Li, width, Kp, win);
         };
         if (dtype == KOEMI_F32) run(float{});
         else if (dtype == KOEMI_F16) run(f16{});

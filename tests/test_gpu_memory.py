@@ -120,3 +120,59 @@ def test_read_salient_window_rejects_bad_inputs(device):
         memory.read_salient_window(ck, cv, cvalid, k, v, adm, q.cpu())
     with pytest.raises(think.CudaThinkValidationError, match="same shape"):
         memory.read_salient_window(ck, cv, cvalid, k[:, :4], v, adm, q)
+
+
+# ------------------------------------------------------------ local read
+# read_local_window (value output of model/memory.py:332-383) against the
+# float64 oracle (itself pinned to the per-position ring read); same
+# tolerances as the salient read.
+
+
+@pytest.mark.parametrize(
+    "b, s, length, d, window, p, dtype",
+    [
+        (8, 16, 128, 64, 16, 0.9, torch.float32),    # C5 shape (width reduced): ring of 16, window of 128
+        (2, 16, 300, 48, 16, 0.8, torch.float32),    # several query tiles: the lower bound skips slot tiles
+        (2, 4, 9, 12, 40, 0.7, torch.float32),       # window longer than the sequence
+        (3, 5, 33, 20, 1, 0.6, torch.bfloat16),      # window of one entry
+        (1, 16, 1100, 40, 24, 0.9, torch.float32),   # 1116 slots: the rocBLAS path
+        (2, 0, 17, 8, 4, 0.5, torch.float16),        # empty ring
+    ],
+)
+def test_read_local_window_matches_oracle(device, b, s, length, d, window, p, dtype):
+    case = _read_case(b * 11 + length + d, b, s, length, d, p, dtype)
+    got = memory.read_local_window(*(x.to(device) for x in case), window=window).float().cpu().numpy()
+    ck, cv, cvalid, k, v, valid, q = (x.float().numpy() if x.is_floating_point() else x.numpy() for x in case)
+    want = oracle.read_local_window(ck, cv, cvalid, k, v, valid, q, window)
+    vmax = max(float(np.abs(cv).max()) if s else 0.0, float(np.abs(v).max()))
+    err = np.abs(got - want)
+    print(f"local read b={b} s={s} L={length} d={d} window={window} {dtype}: max_abs={err.max():.3e}", flush=True)
+    if dtype == torch.float32:
+        assert np.all(err <= 1e-4 * np.abs(want) + 1e-5 * vmax)
+    else:
+        assert np.all(err <= 2.0**-7 * vmax)
+
+
+def test_read_local_window_rejects_a_bad_window(device):
+    case = [x.to(device) for x in _read_case(3, 2, 3, 5, 4, 0.5, torch.float32)]
+    with pytest.raises(think.CudaThinkValidationError, match="positive integer"):
+        memory.read_local_window(*case, window=0)
+
+
+@pytest.mark.parametrize("b, length, p", [(3, 300, 0.7), (2, 1, 0.5), (4, 64, 0.0), (1, 257, 1.0)])
+def test_token_context_matches_the_oracle(device, b, length, p):
+    """koemi_herm_token_context: previous valid token per position and last
+    valid token per row (network.py:742-761) against the oracle's loop, over
+    several 256-position chunks, one position, no valid token and all valid."""
+
+    from koemi_amd import herm
+
+    g = torch.Generator().manual_seed(b * 31 + length)
+    ids = torch.randint(0, 256, (b, length), generator=g)
+    valid = torch.rand((b, length), generator=g) < p
+    carried = torch.randint(0, 257, (b,), generator=g)
+    previous, last = herm._token_context(ids.to(device), valid.to(device), carried.to(device))
+    want = oracle.previous_token_ids(ids.numpy(), valid.numpy(), carried.numpy())
+    np.testing.assert_array_equal(previous.cpu().numpy(), want)
+    want_last = np.array([ids[r][valid[r]][-1].item() if valid[r].any() else carried[r].item() for r in range(b)])
+    np.testing.assert_array_equal(last.cpu().numpy(), want_last)
