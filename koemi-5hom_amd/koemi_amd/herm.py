@@ -139,7 +139,8 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
     """Device copies laid out for the kernels: the projections of the working
     states stacked into one GEMM (local key, local value, value, the key's and
     the query's feature logits with W_f folded in, decay, write), the GEMM
-    weights in ``linear_dtype``, the gates and the content head in fp32."""
+    weights in ``linear_dtype`` with fp32 biases, the gates and the content
+    head in fp32."""
 
     lin = settings.linear_dtype
     prepared = []
@@ -161,12 +162,12 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         weights = [p["local_key_w"], p["local_value_w"], p["value_w"], fk_w, fq_w, p["decay_w"], p["write_w"]]
         biases = [p["local_key_b"], p["local_value_b"], p["value_b"], fk_b, fq_b, p["decay_b"], p["write_b"]]
         q["ws_w"] = to(torch.cat([w.double() for w in weights]), lin)
-        q["ws_b"] = to(torch.cat([b.double() for b in biases]), lin)
-        q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"], lin)
+        q["ws_b"] = to(torch.cat([b.double() for b in biases]))
+        q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"])
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
-        q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"], lin)
+        q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"])
         q["content_w"] = to(p["head_w"][:PAD_TOKEN_ID])
         q["content_b"] = to(p["head_b"][:PAD_TOKEN_ID])
         prepared.append(q)
@@ -217,7 +218,14 @@ def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor
 
 
 def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
-    return functional.linear(x.to(weight.dtype), weight, bias).float()
+    """x W^T + b with fp32 results: one library GEMM (fp32 accumulation, the fp32
+    bias added in its epilogue) for half-precision weights."""
+
+    if weight.dtype == torch.float32:
+        return functional.linear(x, weight, bias)
+    flat = x.reshape(-1, x.shape[-1]).to(weight.dtype)
+    out = torch.addmm(bias, flat, weight.t(), out_dtype=torch.float32)
+    return out.view(*x.shape[:-1], weight.shape[0])
 
 
 def _token_context(ids: Tensor, valid: Tensor, carried: Tensor) -> tuple[Tensor, Tensor]:
