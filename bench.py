@@ -602,7 +602,8 @@ def main() -> int:
                                           "note": "two fp32 rocBLAS products + the HIP gate epilogue"}
         ms = events_ms(lambda: recurrent.recurrent_scan(ug, *wts, vg), max(3, args.kernel_iters // 4))
         kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
-                                         "note": "gates then the affine scan (network.py:306-310)"}
+                                         "note": "the two gate GEMMs, then one kernel forming the gates inside "
+                                                 "the affine scan (network.py:306-310)"}
         del ug, wts, vg
 
     if "e" in extra:

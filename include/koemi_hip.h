@@ -225,6 +225,20 @@ int koemi_recurrent_gates(const void* input, const void* retention_weight, const
                           void* retention_out, void* increment_out, int64_t rows, int64_t width, int dtype,
                           void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
+/* The bounded recurrent state over a window in one call, fp32: the gates of
+ * model/memory.py:14-30 with the masking of network.py:306-309 followed by the
+ * affine scan of network.py:310 (h_t = a_t h_{t-1} + b_t from `initial`),
+ * the gates formed in registers inside the scan rather than written to memory.
+ * input [batch, length, width], weights width x width (out x in), biases
+ * width, valid [batch, length] bytes or NULL, initial [batch, width], states
+ * [batch, length, width]. The workspace is
+ * koemi_recurrent_gates_workspace_bytes(batch * length, width). Results equal
+ * koemi_recurrent_gates followed by koemi_affine_scan_forward. width % 4 == 0. */
+int koemi_recurrent_scan(const float* input, const float* retention_weight, const float* retention_bias,
+                         const float* candidate_weight, const float* candidate_bias, const uint8_t* valid,
+                         const float* initial, float* states, int64_t batch, int64_t length, int64_t width,
+                         void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
 /* Salient-memory read, LocalKeyValueMemory.read_salient_window of
  * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
  * the reference). For every batch row b and query t < length:

@@ -135,6 +135,12 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_kernel(
 template <int VEC>
 struct FloatVec;
 template <>
+struct FloatVec<1> {
+    using type = float;
+    __device__ static void split(const float& v, float (&o)[1]) { o[0] = v; }
+    __device__ static float join(const float (&o)[1]) { return o[0]; }
+};
+template <>
 struct FloatVec<2> {
     using type = float2;
     __device__ static void split(const float2& v, float (&o)[2]) { o[0] = v.x; o[1] = v.y; }
@@ -147,10 +153,23 @@ struct FloatVec<4> {
     __device__ static float4 join(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 
-template <int S, int NSEG, int VEC>
+// Gate inputs of the fused gates + scan (GATES): a and b point at the two
+// fp32 pre-activation products u W_r^T and u W_c^T; the biases and the valid
+// bytes turn them into the gates of BoundedRecurrentState.gates
+// (model/memory.py:22-26) with the masking of network.py:307-309, by the same
+// expressions as the separate gate kernel (gates.hip).
+struct GateInputs {
+    const float* retention_bias;
+    const float* candidate_bias;
+    const uint8_t* valid;  // [B * L] or null
+};
+constexpr float kGateMinRetention = 0.00390625f;        // 2^-8
+constexpr float kGateRetentionSpan = 1.0f - 0.0078125f;  // 1 - 2^-7
+
+template <int S, int NSEG, int VEC, bool GATES = false>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
-    int64_t L, int64_t F, int64_t col_tiles) {
+    int64_t L, int64_t F, int64_t col_tiles, GateInputs gates = GateInputs{nullptr, nullptr, nullptr}) {
     using V = typename FloatVec<VEC>::type;
     constexpr int CH = S * NSEG;
     __shared__ float seg_p[NSEG][VEC][kWave];
@@ -166,6 +185,11 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* b_col = b + bi * L * F + fc;
     float* h_col = h + bi * L * F + fc;
 
+    float gbr[VEC], gbc[VEC];
+    if constexpr (GATES) {
+        FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.retention_bias + fc), gbr);
+        FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.candidate_bias + fc), gbc);
+    }
     float carry[VEC];
     {
         const V c0 = *reinterpret_cast<const V*>(h0 + bi * F + fc);
@@ -183,6 +207,14 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
             va[i] = *reinterpret_cast<const V*>(a_col + tc * F);
             vb[i] = *reinterpret_cast<const V*>(b_col + tc * F);
         }
+        bool keep[S];
+        if constexpr (GATES) {
+#pragma unroll
+            for (int i = 0; i < S; ++i) {
+                const int64_t t = t_first + i;
+                keep[i] = gates.valid == nullptr || gates.valid[bi * L + (t < L ? t : L - 1)] != 0;
+            }
+        }
 #pragma unroll
         for (int i = 0; i < S; ++i) {
             const bool ok = col_ok && t_first + i < L;
@@ -190,6 +222,13 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
             FloatVec<VEC>::split(vb[i], rb[i]);
 #pragma unroll
             for (int c = 0; c < VEC; ++c) {
+                if constexpr (GATES) {
+                    const float retention = 1.0f / (1.0f + expf(-(ra[i][c] + gbr[c])));
+                    const float ga = kGateMinRetention + kGateRetentionSpan * retention;
+                    const float gb = (1.0f - ga) * tanhf(rb[i][c] + gbc[c]);
+                    ra[i][c] = keep[i] ? ga : 1.0f;
+                    rb[i][c] = keep[i] ? gb : 0.0f;
+                }
                 ra[i][c] = ok ? ra[i][c] : 1.0f;
                 rb[i][c] = ok ? rb[i][c] : 0.0f;
             }
@@ -394,6 +433,34 @@ int check_scan_args(const void* a, const void* b, const void* h0, const void* h,
 }
 
 }  // namespace
+
+// The fused gates + scan over fp32 pre-activation products zr, zc [B, L, F]:
+// KOEMI_SCAN_VEC columns per lane where the rows are aligned to it and that
+// still fills the chip, one column per lane otherwise. Returns
+// KOEMI_ERR_UNSUPPORTED without launching when the grid would not fit (the
+// caller then forms the gates separately).
+int launch_gated_scan(const float* zr, const float* zc, const float* retention_bias, const float* candidate_bias,
+                      const uint8_t* valid, const float* h0, float* h, int64_t B, int64_t L, int64_t F,
+                      hipStream_t stream) {
+    constexpr int VEC = KOEMI_SCAN_VEC;
+    const GateInputs gates{retention_bias, candidate_bias, valid};
+    auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % (4 * VEC) == 0; };
+    const int64_t wide_tiles = (F / VEC + kWave - 1) / kWave;
+    if (F % VEC == 0 && aligned(zr) && aligned(zc) && aligned(h) && aligned(h0) && aligned(retention_bias) &&
+        aligned(candidate_bias) && B * wide_tiles >= 256 && B * wide_tiles <= 0x7fffffff) {
+        hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
+                           dim3(static_cast<unsigned>(B * wide_tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc,
+                           h0, h, L, F, wide_tiles, gates);
+        return check_launch("koemi_recurrent_scan");
+    }
+    const int64_t tiles = (F + kWave - 1) / kWave;
+    if (B * tiles > 0x7fffffff) return KOEMI_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true>),
+                       dim3(static_cast<unsigned>(B * tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc, h0, h,
+                       L, F, tiles, gates);
+    return check_launch("koemi_recurrent_scan");
+}
+
 }  // namespace koemi
 
 using namespace koemi;

@@ -12,7 +12,9 @@
 // accumulation, fp32 results in the workspace); one HIP kernel then applies
 // the biases, the bounded sigmoid, tanh and the mask and writes a and b in the
 // input dtype, reading each fp32 product once (16-byte loads, four columns per
-// thread).
+// thread). koemi_recurrent_scan (fp32) hands the two products straight to the
+// affine-scan kernel, which applies the same expressions in registers, so a
+// and b never reach memory.
 #include "common.hpp"
 
 #include <rocblas/rocblas.h>
@@ -21,9 +23,13 @@
 
 namespace koemi {
 
-// The rocBLAS handle of the current device (salient_read.hip owns the table).
+// The rocBLAS handle of a device (blas.hip); callers hold g_blas_mutex.
 rocblas_handle blas_handle(int device);
 extern std::mutex g_blas_mutex;
+// The fused gates + scan kernel (affine_scan.hip).
+int launch_gated_scan(const float* zr, const float* zc, const float* retention_bias, const float* candidate_bias,
+                      const uint8_t* valid, const float* h0, float* h, int64_t B, int64_t L, int64_t F,
+                      hipStream_t stream);
 
 namespace {
 
@@ -66,6 +72,34 @@ size_t gates_workspace(int64_t rows, int64_t D) {
     return 2 * one;
 }
 
+// zr = u W_r^T, zc = u W_c^T (row-major [rows, D], fp32) on rocBLAS: in its
+// column-major terms Z' (D x rows) = W'^T (D x D) . u' (D x rows).
+int gate_products(const void* input, const void* retention_weight, const void* candidate_weight, float* zr,
+                  float* zc, int64_t rows, int64_t width, int dtype, hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(KOEMI_ERR_LAUNCH, "recurrent gates: no device");
+    std::lock_guard<std::mutex> lock(g_blas_mutex);
+    rocblas_handle h = blas_handle(dev);
+    if (!h) return fail(KOEMI_ERR_LAUNCH, "recurrent gates: no rocBLAS handle");
+    if (rocblas_set_stream(h, s) != rocblas_status_success ||
+        rocblas_set_pointer_mode(h, rocblas_pointer_mode_host) != rocblas_status_success)
+        return fail(KOEMI_ERR_LAUNCH, "recurrent gates: rocblas stream setup failed");
+    const rocblas_datatype t = gates_blas_type(dtype);
+    const rocblas_int d = static_cast<rocblas_int>(width), n = static_cast<rocblas_int>(rows);
+    const float one = 1.0f, zero = 0.0f;
+    for (int g = 0; g < 2; ++g) {
+        const void* w = g == 0 ? retention_weight : candidate_weight;
+        float* z = g == 0 ? zr : zc;
+        const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, d, n, d, &one,
+                                                  w, t, d, input, t, d, &zero, z, rocblas_datatype_f32_r, d, z,
+                                                  rocblas_datatype_f32_r, d, rocblas_datatype_f32_r,
+                                                  rocblas_gemm_algo_standard, 0, 0);
+        if (st != rocblas_status_success)
+            return fail(KOEMI_ERR_LAUNCH, "recurrent gates: rocblas_gemm_ex failed (%s)", rocblas_status_to_string(st));
+    }
+    return KOEMI_OK;
+}
+
 }  // namespace
 }  // namespace koemi
 
@@ -96,30 +130,9 @@ extern "C" int koemi_recurrent_gates(const void* input, const void* retention_we
     float* zc = reinterpret_cast<float*>(static_cast<char*>(workspace) + need / 2);
     const hipStream_t s = as_stream(stream);
 
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return fail(KOEMI_ERR_LAUNCH, "recurrent gates: no device");
     {
-        std::lock_guard<std::mutex> lock(g_blas_mutex);
-        rocblas_handle h = blas_handle(dev);
-        if (!h) return fail(KOEMI_ERR_LAUNCH, "recurrent gates: no rocBLAS handle");
-        if (rocblas_set_stream(h, s) != rocblas_status_success ||
-            rocblas_set_pointer_mode(h, rocblas_pointer_mode_host) != rocblas_status_success)
-            return fail(KOEMI_ERR_LAUNCH, "recurrent gates: rocblas stream setup failed");
-        // Row-major Z [rows, D] = u [rows, D] . W^T, W [D_out, D_in]: in rocBLAS's
-        // column-major terms Z' (D x rows) = W'^T (D x D) . u' (D x rows).
-        const rocblas_datatype t = gates_blas_type(dtype);
-        const rocblas_int d = static_cast<rocblas_int>(width), n = static_cast<rocblas_int>(rows);
-        const float one = 1.0f, zero = 0.0f;
-        for (int g = 0; g < 2; ++g) {
-            const void* w = g == 0 ? retention_weight : candidate_weight;
-            float* z = g == 0 ? zr : zc;
-            const rocblas_status st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, d, n, d,
-                                                      &one, w, t, d, input, t, d, &zero, z, rocblas_datatype_f32_r, d,
-                                                      z, rocblas_datatype_f32_r, d, rocblas_datatype_f32_r,
-                                                      rocblas_gemm_algo_standard, 0, 0);
-            if (st != rocblas_status_success)
-                return fail(KOEMI_ERR_LAUNCH, "recurrent gates: rocblas_gemm_ex failed (%s)", rocblas_status_to_string(st));
-        }
+        const int st = gate_products(input, retention_weight, candidate_weight, zr, zc, rows, width, dtype, s);
+        if (st != KOEMI_OK) return st;
     }
     const int64_t quads = rows * (width / 4);
     const dim3 grid(static_cast<unsigned>((quads + 255) / 256)), block(256);
@@ -140,4 +153,30 @@ extern "C" int koemi_recurrent_gates(const void* input, const void* retention_we
                                valid, static_cast<bf16*>(retention_out), static_cast<bf16*>(increment_out), rows, width);
     }
     return check_launch("koemi_recurrent_gates");
+}
+
+extern "C" int koemi_recurrent_scan(const float* input, const float* retention_weight, const float* retention_bias,
+                                    const float* candidate_weight, const float* candidate_bias, const uint8_t* valid,
+                                    const float* initial, float* states, int64_t batch, int64_t length, int64_t width,
+                                    void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    if (batch < 0 || length < 0 || width < 1)
+        return fail(KOEMI_ERR_INVALID, "recurrent scan needs non-negative batch and length and a positive width");
+    if (width % 4 != 0) return fail(KOEMI_ERR_UNSUPPORTED, "recurrent scan needs width % 4 == 0");
+    const int64_t rows = batch * length;
+    if (rows == 0) return KOEMI_OK;
+    if (rows > 0x7fffffffLL || width > 0x7fffffffLL / 4)
+        return fail(KOEMI_ERR_UNSUPPORTED, "recurrent scan sizes exceed 32-bit GEMM dimensions");
+    if (batch * ((width + kWave - 1) / kWave) > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "recurrent scan grid too large");
+    if (!input || !retention_weight || !retention_bias || !candidate_weight || !candidate_bias || !initial || !states)
+        return fail(KOEMI_ERR_INVALID, "recurrent scan received a null pointer");
+    const size_t need = gates_workspace(rows, width);
+    if (!workspace || workspace_bytes < need)
+        return fail(KOEMI_ERR_INVALID, "recurrent scan workspace too small: need %zu bytes", need);
+    float* zr = static_cast<float*>(workspace);
+    float* zc = reinterpret_cast<float*>(static_cast<char*>(workspace) + need / 2);
+    const hipStream_t s = as_stream(stream);
+    int st = gate_products(input, retention_weight, candidate_weight, zr, zc, rows, width, KOEMI_F32, s);
+    if (st != KOEMI_OK) return st;
+    return launch_gated_scan(zr, zc, retention_bias, candidate_bias, valid, initial, states, batch, length, width, s);
 }

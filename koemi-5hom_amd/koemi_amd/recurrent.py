@@ -4,8 +4,11 @@ Fronts for ``BoundedRecurrentState.gates`` (reference model/memory.py:14-30)
 and the first steps of the HERM window (network.py:306-310: gates, masking of
 invalid positions, affine scan from the carried working state). The gates run
 ``koemi_recurrent_gates`` (two rocBLAS products with fp32 accumulation and one
-HIP epilogue kernel); the scan runs the dense affine-scan kernel. There is no
-torch fallback. Inference only (no autograd through the gates).
+HIP epilogue kernel); the fp32 window scan runs ``koemi_recurrent_scan``, the
+same products followed by one HIP kernel that forms the gates in registers
+inside the affine scan; other dtypes run the gates and then the dense
+affine-scan kernel. There is no torch fallback. Inference only (no autograd
+through the gates).
 """
 
 from __future__ import annotations
@@ -40,6 +43,38 @@ def recurrent_gates(
     dtype; products accumulate in fp32.
     """
 
+    _check_gate_arguments(input_state, retention_weight, retention_bias, candidate_weight, candidate_bias, valid_mask)
+    width = input_state.shape[-1]
+    device = input_state.device
+    rows = input_state.numel() // width if width else 0
+    retention = torch.empty(input_state.shape, device=device, dtype=input_state.dtype)
+    increment = torch.empty_like(retention)
+    if rows == 0:
+        return retention, increment
+    workspace = torch.empty(_native.query("koemi_recurrent_gates_workspace_bytes", rows, width), dtype=torch.uint8,
+                            device=device)
+    u = input_state.contiguous()
+    params = [t.contiguous() for t in (retention_weight, retention_bias, candidate_weight, candidate_bias)]
+    mask = valid_mask.contiguous() if valid_mask is not None else None
+    _native.call(
+        "koemi_recurrent_gates",
+        _native.ptr(u),
+        *(_native.ptr(t) for t in params),
+        _native.ptr(mask) if mask is not None else None,
+        _native.ptr(retention),
+        _native.ptr(increment),
+        rows,
+        width,
+        _native.dtype_code(input_state.dtype),
+        _native.ptr(workspace),
+        workspace.numel(),
+        _native.stream_of(device),
+    )
+    return retention, increment
+
+
+def _check_gate_arguments(input_state, retention_weight, retention_bias, candidate_weight, candidate_bias,
+                          valid_mask) -> None:
     tensors = {
         "input_state": input_state,
         "retention_weight": retention_weight,
@@ -78,33 +113,6 @@ def recurrent_gates(
     except _native.NativeLibraryUnavailableError as error:
         raise DenseCudaUnavailableError(str(error)) from error
 
-    device = input_state.device
-    rows = input_state.numel() // width if width else 0
-    retention = torch.empty(input_state.shape, device=device, dtype=input_state.dtype)
-    increment = torch.empty_like(retention)
-    if rows == 0:
-        return retention, increment
-    workspace = torch.empty(_native.query("koemi_recurrent_gates_workspace_bytes", rows, width), dtype=torch.uint8,
-                            device=device)
-    u = input_state.contiguous()
-    params = [t.contiguous() for t in (retention_weight, retention_bias, candidate_weight, candidate_bias)]
-    mask = valid_mask.contiguous() if valid_mask is not None else None
-    _native.call(
-        "koemi_recurrent_gates",
-        _native.ptr(u),
-        *(_native.ptr(t) for t in params),
-        _native.ptr(mask) if mask is not None else None,
-        _native.ptr(retention),
-        _native.ptr(increment),
-        rows,
-        width,
-        _native.dtype_code(input_state.dtype),
-        _native.ptr(workspace),
-        workspace.numel(),
-        _native.stream_of(device),
-    )
-    return retention, increment
-
 
 def recurrent_scan(
     input_state: Tensor,
@@ -124,6 +132,39 @@ def recurrent_scan(
 
     if not isinstance(input_state, Tensor) or input_state.ndim != 3:
         raise DenseCudaValidationError("input_state must be a [batch, length, width] tensor")
-    retention, increment = recurrent_gates(input_state, retention_weight, retention_bias, candidate_weight,
-                                           candidate_bias, valid_mask)
-    return dense_affine_scan(retention, increment, initial)
+    if input_state.dtype != torch.float32:
+        retention, increment = recurrent_gates(input_state, retention_weight, retention_bias, candidate_weight,
+                                               candidate_bias, valid_mask)
+        return dense_affine_scan(retention, increment, initial)
+    _check_gate_arguments(input_state, retention_weight, retention_bias, candidate_weight, candidate_bias, valid_mask)
+    batch, length, width = input_state.shape
+    device = input_state.device
+    if initial is None:
+        initial = torch.zeros((batch, width), device=device, dtype=torch.float32)
+    elif not isinstance(initial, Tensor) or initial.shape != (batch, width) or initial.dtype != torch.float32 \
+            or initial.device != device:
+        raise DenseCudaValidationError("initial must be a float32 [batch, width] tensor on the input's device")
+    states = torch.empty((batch, length, width), device=device, dtype=torch.float32)
+    if states.numel() == 0:
+        return states
+    workspace = torch.empty(_native.query("koemi_recurrent_gates_workspace_bytes", batch * length, width),
+                            dtype=torch.uint8, device=device)
+    u = input_state.contiguous()
+    params = [t.contiguous() for t in (retention_weight, retention_bias, candidate_weight, candidate_bias)]
+    mask = valid_mask.contiguous() if valid_mask is not None else None
+    h0 = initial.contiguous()
+    _native.call(
+        "koemi_recurrent_scan",
+        _native.ptr(u),
+        *(_native.ptr(t) for t in params),
+        _native.ptr(mask) if mask is not None else None,
+        _native.ptr(h0),
+        _native.ptr(states),
+        batch,
+        length,
+        width,
+        _native.ptr(workspace),
+        workspace.numel(),
+        _native.stream_of(device),
+    )
+    return states

@@ -70,6 +70,47 @@ def test_recurrent_scan_matches_oracle(device, b, length, d, dtype):
     assert err <= (1e-4 if dtype == torch.float32 else 2.0**-6)
 
 
+@pytest.mark.parametrize(
+    "b, length, d, p, with_mask",
+    [
+        (64, 40, 512, 0.8, True),    # two columns per lane (64 x 4 column strips fill the chip)
+        (32, 33, 1024, 0.9, False),  # C3 width, no mask
+        (2, 300, 100, 0.7, True),    # one column per lane, a partial column strip
+        (3, 1, 64, 0.5, True),       # one-token window (decode)
+        (8, 129, 1024, 0.85, True),  # C5 batch and width, one column per lane
+    ],
+)
+def test_fused_recurrent_scan_equals_gates_then_scan(device, b, length, d, p, with_mask):
+    """koemi_recurrent_scan forms the gates inside the scan kernel with the
+    gate kernel's expressions: its states match gates + dense_affine_scan to
+    fp32 rounding (the oracle fixes both within 1e-4)."""
+    u, wr, br, wc, bc, valid = _case(b * 7 + length + d, b, length, d, p, torch.float32)
+    h0 = torch.randn((b, d), generator=torch.Generator().manual_seed(9))
+    args = [t.to(device) for t in (u, wr, br, wc, bc)]
+    mask = valid.to(device) if with_mask else None
+    fused = recurrent.recurrent_scan(*args, mask, h0.to(device))
+    a, inc = recurrent.recurrent_gates(*args, mask)
+    split = dense.dense_affine_scan(a, inc, h0.to(device))
+    torch.cuda.synchronize()
+    diff = (fused - split).abs().max().item()
+    print(f"fused scan b={b} L={length} d={d} mask={with_mask}: max_abs vs split={diff:.3e} "
+          f"exact={torch.equal(fused, split)}", flush=True)
+    assert diff <= 1e-6
+    if length * d <= 300 * 128:
+        want = oracle.scan_sequential(*oracle.recurrent_gates(*(_np(t) for t in (u, wr, br, wc, bc, valid if with_mask
+                                                                                  else torch.ones_like(valid)))),
+                                      _np(h0).astype(np.float64))
+        assert np.abs(fused.cpu().numpy() - want).max() <= 1e-4
+
+
+def test_recurrent_scan_rejects_bad_initial(device):
+    u, wr, br, wc, bc, valid = (t.to(device) for t in _case(2, 2, 4, 8, 0.5, torch.float32))
+    with pytest.raises(dense.DenseCudaValidationError, match="initial"):
+        recurrent.recurrent_scan(u, wr, br, wc, bc, valid, torch.zeros((2, 4), device=device))
+    h = recurrent.recurrent_scan(u[:, :0], wr, br, wc, bc, valid[:, :0])
+    assert h.shape == (2, 0, 8)
+
+
 def test_recurrent_gates_reject_bad_inputs(device):
     u, wr, br, wc, bc, valid = (t.to(device) for t in _case(1, 2, 4, 8, 0.5, torch.float32))
     with pytest.raises(dense.DenseCudaValidationError, match="must be on CUDA"):
