@@ -239,6 +239,20 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
                          const float* initial, float* states, int64_t batch, int64_t length, int64_t width,
                          void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
+/* The same gates and scan from precomputed fp32 pre-activations, for callers
+ * that form u W_r^T and u W_c^T themselves (one stacked GEMM): row r of the
+ * batch x length rows holds the retention pre-activations at
+ * preactivations[r * row_stride + retention_offset + f] and the candidate ones
+ * at [... + candidate_offset + f], f < width. The biases (width each) are
+ * added first; NULL means none (already inside the pre-activations). Then
+ * a = 2^-8 + (1 - 2^-7) sigmoid, b = (1 - a) tanh, the valid mask (NULL: all
+ * valid) and h_t = a_t h_{t-1} + b_t from `initial` [batch, width] into
+ * `states` [batch, length, width], as in network.py:306-310. No workspace. */
+int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
+                     int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
+                     const uint8_t* valid, const float* initial, float* states, int64_t batch, int64_t length,
+                     int64_t width, koemi_stream_t stream);
+
 /* Salient-memory read, LocalKeyValueMemory.read_salient_window of
  * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
  * the reference). For every batch row b and query t < length:

@@ -153,23 +153,32 @@ struct FloatVec<4> {
     __device__ static float4 join(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 
-// Gate inputs of the fused gates + scan (GATES): a and b point at the two
-// fp32 pre-activation products u W_r^T and u W_c^T; the biases and the valid
-// bytes turn them into the gates of BoundedRecurrentState.gates
-// (model/memory.py:22-26) with the masking of network.py:307-309, by the same
-// expressions as the separate gate kernel (gates.hip).
-struct GateInputs {
-    const float* retention_bias;
-    const float* candidate_bias;
-    const uint8_t* valid;  // [B * L] or null
-};
 constexpr float kGateMinRetention = 0.00390625f;        // 2^-8
 constexpr float kGateRetentionSpan = 1.0f - 0.0078125f;  // 1 - 2^-7
 
+// Gate inputs of the fused gates + scan (GATES): a and b point at the two
+// fp32 pre-activation products u W_r^T and u W_c^T (rows `stride` floats
+// apart); the biases (null: none) and the valid bytes turn them into the gates
+// of BoundedRecurrentState.gates (model/memory.py:22-26) with the masking of
+// network.py:307-309, by the same expressions as the separate gate kernel
+// (gates.hip).
+struct GateInputs {
+    const float* retention_bias;  // [F] or null
+    const float* candidate_bias;  // [F] or null
+    const uint8_t* valid;         // [B * L] or null
+};
+
+__device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
+    const float retention = 1.0f / (1.0f + expf(-(zr + br)));
+    const float ga = kGateMinRetention + kGateRetentionSpan * retention;
+    const float gb = (1.0f - ga) * tanhf(zc + bc);
+    a = keep ? ga : 1.0f;
+    b = keep ? gb : 0.0f;
+}
 template <int S, int NSEG, int VEC, bool GATES = false>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
-    int64_t L, int64_t F, int64_t col_tiles, GateInputs gates = GateInputs{nullptr, nullptr, nullptr}) {
+    int64_t L, int64_t F, int64_t col_tiles, int64_t stride, GateInputs gates = GateInputs{nullptr, nullptr, nullptr}) {
     using V = typename FloatVec<VEC>::type;
     constexpr int CH = S * NSEG;
     __shared__ float seg_p[NSEG][VEC][kWave];
@@ -181,14 +190,14 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane) * VEC;
     const bool col_ok = f < F;
     const int64_t fc = col_ok ? f : 0;
-    const float* a_col = a + bi * L * F + fc;
-    const float* b_col = b + bi * L * F + fc;
+    const float* a_col = a + bi * L * stride + fc;
+    const float* b_col = b + bi * L * stride + fc;
     float* h_col = h + bi * L * F + fc;
 
-    float gbr[VEC], gbc[VEC];
+    float gbr[VEC] = {}, gbc[VEC] = {};
     if constexpr (GATES) {
-        FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.retention_bias + fc), gbr);
-        FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.candidate_bias + fc), gbc);
+        if (gates.retention_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.retention_bias + fc), gbr);
+        if (gates.candidate_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.candidate_bias + fc), gbc);
     }
     float carry[VEC];
     {
@@ -204,8 +213,8 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
         for (int i = 0; i < S; ++i) {  // unconditional loads at clamped positions
             const int64_t t = t_first + i;
             const int64_t tc = t < L ? t : L - 1;
-            va[i] = *reinterpret_cast<const V*>(a_col + tc * F);
-            vb[i] = *reinterpret_cast<const V*>(b_col + tc * F);
+            va[i] = *reinterpret_cast<const V*>(a_col + tc * stride);
+            vb[i] = *reinterpret_cast<const V*>(b_col + tc * stride);
         }
         bool keep[S];
         if constexpr (GATES) {
@@ -223,11 +232,7 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
 #pragma unroll
             for (int c = 0; c < VEC; ++c) {
                 if constexpr (GATES) {
-                    const float retention = 1.0f / (1.0f + expf(-(ra[i][c] + gbr[c])));
-                    const float ga = kGateMinRetention + kGateRetentionSpan * retention;
-                    const float gb = (1.0f - ga) * tanhf(rb[i][c] + gbc[c]);
-                    ra[i][c] = keep[i] ? ga : 1.0f;
-                    rb[i][c] = keep[i] ? gb : 0.0f;
+                    if (t_first + i < L) gate_pair(ra[i][c], rb[i][c], gbr[c], gbc[c], keep[i], ra[i][c], rb[i][c]);
                 }
                 ra[i][c] = ok ? ra[i][c] : 1.0f;
                 rb[i][c] = ok ? rb[i][c] : 0.0f;
@@ -394,7 +399,7 @@ int launch_forward(const void* a, const void* b, const void* h0, void* h, int64_
             hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC>),
                                dim3(static_cast<unsigned>(blocks)), dim3(kWave * kScanSegments), 0, stream,
                                static_cast<const float*>(a), static_cast<const float*>(b),
-                               static_cast<const float*>(h0), static_cast<float*>(h), L, F, tiles);
+                               static_cast<const float*>(h0), static_cast<float*>(h), L, F, tiles, F);
             return check_launch("koemi_affine_scan_forward");
         }
     }
@@ -434,31 +439,51 @@ int check_scan_args(const void* a, const void* b, const void* h0, const void* h,
 
 }  // namespace
 
-// The fused gates + scan over fp32 pre-activation products zr, zc [B, L, F]:
-// KOEMI_SCAN_VEC columns per lane where the rows are aligned to it and that
-// still fills the chip, one column per lane otherwise. Returns
-// KOEMI_ERR_UNSUPPORTED without launching when the grid would not fit (the
-// caller then forms the gates separately).
-int launch_gated_scan(const float* zr, const float* zc, const float* retention_bias, const float* candidate_bias,
-                      const uint8_t* valid, const float* h0, float* h, int64_t B, int64_t L, int64_t F,
-                      hipStream_t stream) {
+// One-position windows (decode steps): h = a h0 + b per column, the same
+// single rounding the scan makes at its first position.
+__global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict__ zr, const float* __restrict__ zc,
+                                                         int64_t stride, GateInputs gates,
+                                                         const float* __restrict__ h0, float* __restrict__ h,
+                                                         int64_t B, int64_t F) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= B * F) return;
+    const int64_t bi = i / F, f = i - bi * F;
+    const bool keep = gates.valid == nullptr || gates.valid[bi] != 0;
+    float a, b;
+    gate_pair(zr[bi * stride + f], zc[bi * stride + f], gates.retention_bias ? gates.retention_bias[f] : 0.0f,
+              gates.candidate_bias ? gates.candidate_bias[f] : 0.0f, keep, a, b);
+    h[i] = a * h0[i] + b;
+}
+
+// The fused gates + scan over fp32 pre-activation products zr, zc (row r of
+// the B x L rows at r * stride): one position per column for L == 1,
+// otherwise the wide scan with KOEMI_SCAN_VEC columns per lane where the rows
+// are aligned to it and that still fills the chip, one column per lane
+// otherwise. The caller has checked that B * ceil(F / 64) fits the grid.
+int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
+                      const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, int64_t B,
+                      int64_t L, int64_t F, hipStream_t stream) {
     constexpr int VEC = KOEMI_SCAN_VEC;
     const GateInputs gates{retention_bias, candidate_bias, valid};
-    auto aligned = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % (4 * VEC) == 0; };
+    if (L == 1) {
+        hipLaunchKernelGGL(gated_step_kernel, dim3(static_cast<unsigned>((B * F + 255) / 256)), dim3(256), 0, stream,
+                           zr, zc, stride, gates, h0, h, B, F);
+        return check_launch("gated scan (one position)");
+    }
+    auto aligned = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % (4 * VEC) == 0; };
     const int64_t wide_tiles = (F / VEC + kWave - 1) / kWave;
-    if (F % VEC == 0 && aligned(zr) && aligned(zc) && aligned(h) && aligned(h0) && aligned(retention_bias) &&
-        aligned(candidate_bias) && B * wide_tiles >= 256 && B * wide_tiles <= 0x7fffffff) {
+    if (F % VEC == 0 && stride % VEC == 0 && aligned(zr) && aligned(zc) && aligned(h) && aligned(h0) &&
+        aligned(retention_bias) && aligned(candidate_bias) && B * wide_tiles >= 256) {
         hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
                            dim3(static_cast<unsigned>(B * wide_tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc,
-                           h0, h, L, F, wide_tiles, gates);
-        return check_launch("koemi_recurrent_scan");
+                           h0, h, L, F, wide_tiles, stride, gates);
+        return check_launch("gated scan");
     }
     const int64_t tiles = (F + kWave - 1) / kWave;
-    if (B * tiles > 0x7fffffff) return KOEMI_ERR_UNSUPPORTED;
     hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true>),
                        dim3(static_cast<unsigned>(B * tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc, h0, h,
-                       L, F, tiles, gates);
-    return check_launch("koemi_recurrent_scan");
+                       L, F, tiles, stride, gates);
+    return check_launch("gated scan");
 }
 
 }  // namespace koemi
@@ -516,4 +541,22 @@ extern "C" int koemi_affine_scan_backward(const void* retention, const void* ini
         default: return KOEMI_SCAN_BWD(bf16);
     }
 #undef KOEMI_SCAN_BWD
+}
+
+extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
+                                int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
+                                const uint8_t* valid, const float* initial, float* states, int64_t batch,
+                                int64_t length, int64_t width, koemi_stream_t stream) {
+    if (batch < 0 || length < 0 || width < 1)
+        return fail(KOEMI_ERR_INVALID, "gated scan needs non-negative batch and length and a positive width");
+    if (retention_offset < 0 || candidate_offset < 0 || retention_offset + width > row_stride ||
+        candidate_offset + width > row_stride)
+        return fail(KOEMI_ERR_INVALID, "gated scan: the gate columns must lie inside a row");
+    if (batch * length == 0) return KOEMI_OK;
+    if (!preactivations || !initial || !states) return fail(KOEMI_ERR_INVALID, "gated scan received a null pointer");
+    if (batch * ((width + kWave - 1) / kWave) > 0x7fffffffLL || batch * width > 0x7fffffffLL * 256LL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "gated scan grid too large");
+    return launch_gated_scan(preactivations + retention_offset, preactivations + candidate_offset, row_stride,
+                             retention_bias, candidate_bias, valid, initial, states, batch, length, width,
+                             as_stream(stream));
 }

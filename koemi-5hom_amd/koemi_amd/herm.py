@@ -7,8 +7,9 @@ routing with the static dispatch (experts.py:109-150), static rings
 (``KoemiState.create_static``, state.py:43-76). Its hot-path operators run on
 this package's HIP kernels:
 
-* gates + masking + scan: ``recurrent.recurrent_scan`` (memory.py:22-26,
-  network.py:306-310);
+* gates + masking + scan: one stacked GEMM for the two gate projections,
+  then ``recurrent.gated_scan`` (memory.py:22-26, network.py:306-310), which
+  forms the gates inside the scan kernel;
 * surprise from the prior states: ``think.causal_surprise`` on the content
   head (network.py:677-698);
 * admission: ``think.salience_admission`` with the fixed threshold (network.py:349);
@@ -25,7 +26,8 @@ operation (the associative memory's feature projection included), the
 recurrent state and the memories are fp32. bf16 matches the
 reference's default GPU precision (``resolve_precision("auto")`` selects bf16
 autocast on CUDA, model/gpu_precision.py:96-121); fp32 is the parity setting.
-The gates run in fp32 whatever ``linear_dtype`` is. The associative memory
+The gate projections are one of those GEMMs (retention and candidate
+stacked); their nonlinearity, the mask and the scan run in fp32. The associative memory
 (projection tail, write terms, scan-and-read; memory.py:82-144) runs on
 ``koemi_assoc_scan_read``; the remaining small elementwise steps are torch
 operations on device. The local read's novelty output, which only the refine
@@ -138,9 +140,9 @@ def init_stack(settings: HermSettings, seed: int, device: torch.device | str = "
 def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, device: torch.device) -> list[dict[str, Tensor]]:
     """Device copies laid out for the kernels: the projections of the working
     states stacked into one GEMM (local key, local value, value, the key's and
-    the query's feature logits with W_f folded in, decay, write), the GEMM
-    weights in ``linear_dtype`` with fp32 biases, the gates and the content
-    head in fp32."""
+    the query's feature logits with W_f folded in, decay, write), the two gate
+    projections stacked into another, the GEMM weights in ``linear_dtype``
+    with fp32 biases, the content head in fp32."""
 
     lin = settings.linear_dtype
     prepared = []
@@ -150,8 +152,8 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         if "embedding" in p:
             q["embedding"] = to(p["embedding"])
         q["input_norm"] = to(p["input_norm"])
-        for name in ("retention", "candidate"):
-            q[name + "_w"], q[name + "_b"] = to(p[name + "_w"]), to(p[name + "_b"])
+        q["gates_w"] = to(torch.cat((p["retention_w"], p["candidate_w"])), lin)
+        q["gates_b"] = to(torch.cat((p["retention_b"], p["candidate_b"])))
         # feature logits of the key and of the query are linear in the states:
         # W_f (W_k x + b_k) + b_f = (W_f W_k) x + (W_f b_k + b_f), formed in float64
         f64 = lambda name: p[name].double()
@@ -304,8 +306,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     valid = ids != PAD_TOKEN_ID
     source = functional.embedding(ids, p["embedding"]) if context is None else context
     u = _rms(source, p["input_norm"])
-    ws = recurrent.recurrent_scan(u, p["retention_w"], p["retention_b"], p["candidate_w"], p["candidate_b"], valid,
-                                  state["working"])
+    ws = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d)
     prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
     targets = torch.where(valid, ids, 0)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
@@ -431,9 +432,16 @@ class WindowGraph:
 
     def _window(self) -> Tensor:
         logits, next_states = stack_window(self.params, self.settings, self.ids, self.states)
+        # every layer's next state into the static buffers: a few multi-tensor
+        # copy kernels (one per dtype) rather than one copy per tensor
+        groups: dict[torch.dtype, tuple[list[Tensor], list[Tensor]]] = {}
         for state, new in zip(self.states, next_states):
             for key, tensor in state.items():
-                tensor.copy_(new[key])
+                dst, src = groups.setdefault(tensor.dtype, ([], []))
+                dst.append(tensor)
+                src.append(new[key])
+        for dst, src in groups.values():
+            torch._foreach_copy_(dst, src)
         if self.greedy:
             scores = logits[:, -1].clone()
             scores[:, PAD_TOKEN_ID] = float("-inf")

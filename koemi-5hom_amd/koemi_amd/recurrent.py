@@ -19,7 +19,7 @@ from torch import Tensor
 from koemi_amd import _native
 from koemi_amd.dense import DenseCudaUnavailableError, DenseCudaValidationError, dense_affine_scan
 
-__all__ = ["recurrent_gates", "recurrent_scan"]
+__all__ = ["gated_scan", "recurrent_gates", "recurrent_scan"]
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -166,5 +166,52 @@ def recurrent_scan(
         _native.ptr(workspace),
         workspace.numel(),
         _native.stream_of(device),
+    )
+    return states
+
+
+def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
+               retention_offset: int = 0, candidate_offset: int | None = None) -> Tensor:
+    """Working states of one window from precomputed gate pre-activations.
+
+    ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
+    ``u W_r^T + b_r`` in columns ``retention_offset .. + width`` and
+    ``u W_c^T + b_c`` in ``candidate_offset .. + width`` (default: right
+    after the retention columns), as one stacked projection produces them.
+    The gates of memory.py:22-26, the masking of network.py:307-309 and the
+    scan of network.py:310 from ``initial`` ``[B, width]`` run in one kernel
+    (``koemi_gated_scan``). Returns ``[B, L, width]`` fp32.
+    """
+
+    if candidate_offset is None:
+        candidate_offset = retention_offset + width
+    if not isinstance(preactivations, Tensor) or preactivations.ndim != 3 or preactivations.dtype != torch.float32:
+        raise DenseCudaValidationError("preactivations must be a float32 [batch, length, columns] tensor")
+    if preactivations.device.type != "cuda":
+        raise DenseCudaValidationError("preactivations must be on CUDA")
+    batch, length, columns = preactivations.shape
+    if min(retention_offset, candidate_offset) < 0 or max(retention_offset, candidate_offset) + width > columns:
+        raise DenseCudaValidationError("the gate columns must lie inside the pre-activation rows")
+    if not isinstance(initial, Tensor) or initial.shape != (batch, width) or initial.dtype != torch.float32 \
+            or initial.device != preactivations.device:
+        raise DenseCudaValidationError("initial must be a float32 [batch, width] tensor on the same device")
+    if valid_mask is not None and (valid_mask.dtype != torch.bool or valid_mask.shape != (batch, length)
+                                   or valid_mask.device != preactivations.device):
+        raise DenseCudaValidationError("valid_mask must be a bool [batch, length] tensor on the same device")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise DenseCudaUnavailableError(str(error)) from error
+    z = preactivations.contiguous()
+    states = torch.empty((batch, length, width), device=z.device, dtype=torch.float32)
+    if states.numel() == 0:
+        return states
+    mask = valid_mask.contiguous() if valid_mask is not None else None
+    _native.call(
+        "koemi_gated_scan",
+        _native.ptr(z), columns, retention_offset, candidate_offset, None, None,
+        _native.ptr(mask) if mask is not None else None,
+        _native.ptr(initial.contiguous()), _native.ptr(states),
+        batch, length, width, _native.stream_of(z.device),
     )
     return states

@@ -103,6 +103,48 @@ def test_fused_recurrent_scan_equals_gates_then_scan(device, b, length, d, p, wi
         assert np.abs(fused.cpu().numpy() - want).max() <= 1e-4
 
 
+@pytest.mark.parametrize(
+    "b, length, d, r_off, c_off, cols",
+    [
+        (64, 40, 512, 0, 512, 1024),    # stacked gate GEMM output, two columns per lane
+        (8, 129, 1024, 0, 1024, 2048),  # C5 window shape, one column per lane
+        (2, 37, 100, 3, 105, 210),      # odd offsets inside wider rows
+        (64, 1, 1024, 0, 1024, 2048),   # decode step (one-position kernel)
+        (3, 1, 36, 41, 2, 80),          # candidate columns before the retention columns
+    ],
+)
+def test_gated_scan_from_preactivations(device, b, length, d, r_off, c_off, cols):
+    """koemi_gated_scan against the oracle's gates (u = the pre-activation
+    row, W_r and W_c selecting the two column ranges, zero biases) and scan."""
+    g = torch.Generator().manual_seed(b * 1000 + length + d)
+    z = 1.5 * torch.randn((b, length, cols), generator=g)
+    valid = torch.rand((b, length), generator=g) < 0.8
+    h0 = torch.randn((b, d), generator=g)
+    h = recurrent.gated_scan(z.to(device), valid.to(device), h0.to(device), width=d, retention_offset=r_off,
+                             candidate_offset=c_off)
+    select = lambda off: np.eye(cols)[off:off + d]
+    a, inc = oracle.recurrent_gates(z.double().numpy(), select(r_off), np.zeros(d), select(c_off), np.zeros(d),
+                                    valid.numpy())
+    want = oracle.scan_sequential(a, inc, h0.double().numpy())
+    err = np.abs(h.cpu().numpy() - want).max()
+    print(f"gated scan b={b} L={length} d={d} offsets=({r_off},{c_off}): max_abs={err:.3e}", flush=True)
+    assert err <= 1e-4
+    # a one-position call (the decode kernel) reproduces the window's first state bit for bit
+    first = recurrent.gated_scan(z[:, :1].to(device), valid[:, :1].to(device), h0.to(device), width=d,
+                                 retention_offset=r_off, candidate_offset=c_off)
+    assert torch.equal(first, h[:, :1])
+
+
+def test_gated_scan_rejects_bad_columns(device):
+    z = torch.zeros((2, 3, 10), device=device)
+    h0 = torch.zeros((2, 4), device=device)
+    with pytest.raises(dense.DenseCudaValidationError, match="inside"):
+        recurrent.gated_scan(z, None, h0, width=4, retention_offset=0, candidate_offset=7)
+    with pytest.raises(dense.DenseCudaValidationError, match="initial"):
+        recurrent.gated_scan(z, None, h0[:, :3], width=4)
+    assert recurrent.gated_scan(z, None, h0, width=4).shape == (2, 3, 4)
+
+
 def test_recurrent_scan_rejects_bad_initial(device):
     u, wr, br, wc, bc, valid = (t.to(device) for t in _case(2, 2, 4, 8, 0.5, torch.float32))
     with pytest.raises(dense.DenseCudaValidationError, match="initial"):
