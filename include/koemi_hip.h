@@ -253,6 +253,23 @@ int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t re
                      const uint8_t* valid, const float* initial, float* states, int64_t batch, int64_t length,
                      int64_t width, koemi_stream_t stream);
 
+/* nn.Linear over a few rows with bf16 weights (the HERM block's projections
+ * in a decode step: the gate, working-state, fusion and head layers of
+ * model/network.py:296-441 and model/memory.py, which the reference runs as
+ * torch linear layers under bf16 autocast):
+ *   output[r, n] = sum_k bf16(x[r, k]) * weight[n, k] + bias[n],
+ * fp32 accumulation and results. x is `pieces` (1..4) row-major blocks
+ * [rows, piece_width] of `input_dtype` (float32, rounded to bf16 on load, or
+ * bfloat16) that together form K = pieces * piece_width, block i holding
+ * columns [i * piece_width, (i + 1) * piece_width) (network.py:401-405
+ * concatenates four such inputs); unused piece pointers may be NULL. weight
+ * is [out_features, K] bf16, bias [out_features] fp32 or NULL, output
+ * [rows, out_features] fp32. piece_width % 64 == 0, and % 1024 == 0 when
+ * pieces > 1; any rows (each 64-row pass streams the weights once). */
+int koemi_linear_rows(const void* input0, const void* input1, const void* input2, const void* input3, int pieces,
+                      int64_t piece_width, int input_dtype, const void* weight, const float* bias, float* output,
+                      int64_t rows, int64_t out_features, koemi_stream_t stream);
+
 /* Salient-memory read, LocalKeyValueMemory.read_salient_window of
  * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
  * the reference). For every batch row b and query t < length:

@@ -1,0 +1,215 @@
+// Projections of a few rows (a decode step's 64 tokens) on bf16 MFMA.
+//
+// The HERM block's linear layers (nn.Linear in model/network.py and
+// model/memory.py: the stacked working-state projections, the two gate
+// projections, the fusion layer over [working ; memory ; local ; salient] of
+// network.py:401-405 and the head) run on the libraries for a window of many
+// rows. For a handful of rows a library GEMM is a long chain of dependent K
+// steps over few workgroups, and each call needs the fp32 activations cast to
+// bf16 (and the fusion input concatenated) by separate kernels first. Here one
+// kernel streams the weights once: a workgroup owns 32 output features and up
+// to 64 rows per pass (two 32-row MFMA blocks of v_mfma_f32_32x32x16_bf16).
+// The input rows are staged in LDS as bf16, 1024 K values at a time, by
+// coalesced 16-byte loads all issued at once (fp32 inputs rounded to nearest
+// even on the way, as the cast they replace); each of the eight waves takes two
+// 64-wide K steps of the chunk, its weight fragments loaded from global memory while the chunk is
+// staged, and the waves add their partial sums through LDS at the end; the
+// bias is added in the epilogue and the results are fp32. The input may be
+// given as up to four row-major pieces of equal width that together form the
+// K dimension (the concatenation is never built).
+//
+// Fragments use the MFMA register layout with a K permutation shared by both
+// operands: lane l holds row l % 32 and, per step, the 32 contiguous values of
+// half l / 32, of which MFMA j takes values 8j..8j+7, so every product pairs
+// equal k.
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace koemi {
+namespace {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+constexpr int kCols = 32;
+constexpr int kWaves = 8;
+constexpr int kBlocks = 2;  // 32-row MFMA blocks per pass
+constexpr int64_t kMaxRows = 64;
+
+struct Pieces {
+    const void* p[4];
+};
+
+// K values of the input staged in LDS at a time: sixteen 64-wide steps, two
+// per wave, for bf16 inputs (all of K for the 1024-wide layers, so one memory
+// round trip); eight for fp32 inputs, whose staging loads take twice the
+// registers. Rows are padded by 16 bytes so that the 16-byte fragment reads of
+// 16 consecutive rows fall in distinct banks. The cross-wave sums reuse the
+// staging area once the last chunk is multiplied.
+constexpr int kMaxChunk = 2 * kWaves * 64;
+template <typename XT>
+constexpr int chunk_of() { return sizeof(XT) == 2 ? kMaxChunk : kMaxChunk / 2; }
+constexpr int kRowPitch = kMaxChunk + 8;  // bf16 elements
+constexpr int kStageBytes = kBlocks * 32 * kRowPitch * 2;
+constexpr int kRedBytes = kWaves * kBlocks * 16 * kWave * 4;
+static_assert(kRedBytes <= kStageBytes, "the partial sums fit in the staging area");
+
+template <typename XT>
+__global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, int64_t piece_width,
+                                                                     const bf16* __restrict__ w,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ y, int64_t M, int64_t N,
+                                                                     int64_t K) {
+    __shared__ bf16x8 xs_raw[kStageBytes / 16];
+    bf16* xs = reinterpret_cast<bf16*>(xs_raw);
+    auto red = reinterpret_cast<float (*)[kBlocks][16][kWave]>(xs_raw);  // [kWaves][kBlocks][16][kWave]
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kCols;
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int r = lane % 32, half = lane / 32;
+    const int64_t wn = n0 + r < N ? n0 + r : N - 1;  // rows past N are loaded from the last row, never stored
+    const bf16* wr = w + wn * K + 32 * half;
+    constexpr int kVec = 16 / sizeof(XT);  // input elements per 16-byte load
+    constexpr int kChunk = chunk_of<XT>();
+    for (int64_t pass = 0; pass < M; pass += kBlocks * 32) {
+        const int64_t rows = M - pass < kBlocks * 32 ? M - pass : kBlocks * 32;
+        const int blocks = rows > 32 ? 2 : 1;
+        f32x16 acc[kBlocks];
+#pragma unroll
+        for (int rb = 0; rb < kBlocks; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rb][i] = 0.0f;
+        for (int64_t c0 = 0; c0 < K; c0 += kChunk) {
+            const int64_t ck = K - c0 < kChunk ? K - c0 : kChunk;  // a multiple of 64
+            // This wave's weight fragments first (steps wave and wave + 8 of
+            // the chunk), so that they load under the staging.
+            bf16x8 wf[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int64_t kw = 64 * (wave + h * kWaves);
+                if (kw < ck) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) wf[h][j] = *reinterpret_cast<const bf16x8*>(wr + c0 + kw + 8 * j);
+                }
+            }
+            // Stage rows [pass, pass + rows) x k [c0, c0 + ck) as bf16: one
+            // 16-byte input load per thread and iteration, consecutive threads
+            // on consecutive addresses. A load never crosses a piece boundary
+            // (piece_width is a multiple of 64), so its piece is looked up per load.
+            // All of a thread's loads are issued before any is used (a fixed,
+            // unrolled count), so the staging costs one memory round trip. A
+            // chunk lies inside one piece (piece_width is a multiple of the
+            // chunk, or there is one piece), so the piece is found once.
+            constexpr int kPerRow = kChunk / kVec;  // 16-byte loads per staged row
+            constexpr int kLoads = kBlocks * 32 * kPerRow / (kWaves * kWave);
+            using Raw = typename std::conditional<sizeof(XT) == 2, bf16x8, float4>::type;
+            Raw buf[kLoads];
+            const int64_t piece = c0 / piece_width;
+            const XT* base = static_cast<const XT*>(in.p[piece]) + pass * piece_width + (c0 - piece * piece_width);
+            // Unconditional loads (positions past the rows or the chunk read a
+            // valid element and land in staging slots nothing reads), so that
+            // no branch separates them and they are all in flight together.
+            const int last_row = static_cast<int>(rows) - 1, last_k = static_cast<int>(ck) - kVec;
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                const int v = tid + u * kWaves * kWave;
+                const int row = min(v / kPerRow, last_row), kk = min((v % kPerRow) * kVec, last_k);
+                buf[u] = *reinterpret_cast<const Raw*>(base + row * piece_width + kk);
+            }
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                const int v = tid + u * kWaves * kWave;
+                bf16* dst = xs + (v / kPerRow) * kRowPitch + (v % kPerRow) * kVec;
+                if constexpr (sizeof(XT) == 2) {
+                    *reinterpret_cast<bf16x8*>(dst) = buf[u];
+                } else {
+                    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+                    bf16x4 o;
+                    o[0] = static_cast<__bf16>(buf[u].x);
+                    o[1] = static_cast<__bf16>(buf[u].y);
+                    o[2] = static_cast<__bf16>(buf[u].z);
+                    o[3] = static_cast<__bf16>(buf[u].w);
+                    *reinterpret_cast<bf16x4*>(dst) = o;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int kw = 64 * (wave + h * kWaves);
+                if (kw >= ck) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int rb = 0; rb < kBlocks; ++rb) {
+                        if (rb >= blocks) continue;
+                        const int row = rb * 32 + r;
+                        bf16x8 xf = {};
+                        if (row < rows) xf = *reinterpret_cast<const bf16x8*>(xs + row * kRowPitch + kw + 32 * half + 8 * j);
+                        acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xf, wf[h][j], acc[rb], 0, 0, 0);
+                    }
+            }
+            __syncthreads();  // the staging area is rewritten by the next chunk (or holds the sums)
+        }
+#pragma unroll
+        for (int rb = 0; rb < kBlocks; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[wave][rb][i][lane] = acc[rb][i];
+        __syncthreads();
+        // 2 blocks x 16 accumulator entries x 64 lanes, four per thread; entry i
+        // of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4 of its block, column l % 32.
+#pragma unroll
+        for (int q = 0; q < kBlocks * 16 / kWaves; ++q) {
+            const int idx = q * kWaves + wave;  // (block, entry), wave-uniform
+            const int rb = idx / 16, i = idx % 16;
+            const int64_t row = rb * 32 + 8 * (i / 4) + 4 * (lane / 32) + i % 4;
+            const int64_t col = n0 + lane % 32;
+            if (rb >= blocks || row >= rows || col >= N) continue;
+            float v = bias != nullptr ? bias[col] : 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < kWaves; ++w2) v += red[w2][rb][i][lane];
+            y[(pass + row) * N + col] = v;
+        }
+        __syncthreads();  // red is rewritten by the next pass
+    }
+}
+
+}  // namespace
+}  // namespace koemi
+
+using namespace koemi;
+
+extern "C" int koemi_linear_rows(const void* input0, const void* input1, const void* input2, const void* input3,
+                                 int pieces, int64_t piece_width, int input_dtype, const void* weight,
+                                 const float* bias, float* output, int64_t rows, int64_t out_features,
+                                 koemi_stream_t stream) {
+    if (rows < 0 || out_features < 1 || piece_width < 1 || pieces < 1 || pieces > 4)
+        return fail(KOEMI_ERR_INVALID, "linear rows needs rows >= 0, 1 to 4 input pieces and positive widths");
+    if (input_dtype != KOEMI_F32 && input_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows takes float32 or bfloat16 inputs, not %s",
+                    dtype_name(input_dtype));
+    if (piece_width % 64 != 0 || (pieces > 1 && piece_width % kMaxChunk != 0))
+        return fail(KOEMI_ERR_UNSUPPORTED,
+                    "linear rows needs an input width that is a multiple of 64 (of 1024 for several pieces)");
+    if (rows > kMaxRows * 1024 || out_features > 0x7fffffffLL / 2)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows is for a few rows (at most %lld)",
+                    static_cast<long long>(kMaxRows * 1024));
+    if (rows == 0) return KOEMI_OK;
+    const void* in[4] = {input0, input1, input2, input3};
+    const size_t elem = input_dtype == KOEMI_F32 ? 4 : 2;
+    for (int i = 0; i < pieces; ++i)
+        if (!in[i] || reinterpret_cast<uintptr_t>(in[i]) % (8 * elem) != 0)
+            return fail(KOEMI_ERR_INVALID, "linear rows input %d is null or not %zu-byte aligned", i, 8 * elem);
+    if (!weight || reinterpret_cast<uintptr_t>(weight) % 16 != 0 || !output)
+        return fail(KOEMI_ERR_INVALID, "linear rows needs a 16-byte aligned weight and an output");
+    const Pieces p{{in[0], pieces > 1 ? in[1] : in[0], pieces > 2 ? in[2] : in[0], pieces > 3 ? in[3] : in[0]}};
+    const int64_t K = piece_width * pieces;
+    const dim3 grid(static_cast<unsigned>((out_features + kCols - 1) / kCols)), block(kWaves * kWave);
+    const hipStream_t s = as_stream(stream);
+    if (input_dtype == KOEMI_F32)
+        hipLaunchKernelGGL(linear_rows_kernel<float>, grid, block, 0, s, p, piece_width,
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K);
+    else
+        hipLaunchKernelGGL(linear_rows_kernel<bf16>, grid, block, 0, s, p, piece_width,
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K);
+    return check_launch("koemi_linear_rows");
+}

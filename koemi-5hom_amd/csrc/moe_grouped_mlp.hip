@@ -698,6 +698,117 @@ __global__ __launch_bounds__(256) void glu_output_simt_kernel(
     }
 }
 
+// ------------------------------------------------------------ skinny path ---
+// Few rows per expert (a decode step: 64 tokens x top-2 over 16 experts is
+// about 8 rows each). The big tiles above would run 256-row MFMA tiles for 8
+// useful rows, so the step would be bound by wasted matrix work; here it is
+// bound by streaming the expert weights once. A workgroup owns 32 output
+// columns of one expert (GLU: 32 hidden units, their gate and value rows) and
+// every row of that expert, in passes of 32 rows (one MFMA block); its eight
+// waves split K in 64-wide steps, interleaved so that they read adjacent
+// 128-byte pieces of each weight row, keep two steps of loads in flight, and
+// add their partial sums through LDS. Operands come straight from global
+// memory in the MFMA register layout: lane l holds row l % 32 and, per step,
+// the 32 contiguous values of half l / 32, of which MFMA j takes values
+// 8j..8j+7; A and B use the same assignment, so every product pairs equal k.
+// Rows past the segment are not loaded (zero fragments) and not stored.
+constexpr int kSkinnyCols = 32;
+constexpr int kSkinnyWaves = 8;
+constexpr int64_t kSkinnyMaxRowsPerExpert = 64;  // average over experts below which the path is used
+
+template <bool GLU>
+__global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
+    const bf16* __restrict__ a, const bf16* __restrict__ w0, const bf16* __restrict__ w1,
+    const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ c,
+    const int64_t* __restrict__ offsets, int64_t n_out, int64_t K, int64_t col_groups) {
+    constexpr int kMats = GLU ? 2 : 1;
+    __shared__ float red[kSkinnyWaves][kMats][16][kWave];
+    const int64_t e = static_cast<int64_t>(blockIdx.x) / col_groups;
+    const int64_t n0 = (static_cast<int64_t>(blockIdx.x) % col_groups) * kSkinnyCols;
+    const int64_t row0 = offsets[e];
+    const int64_t count = offsets[e + 1] - row0;
+    if (count <= 0) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int r = lane % 32, half = lane / 32;
+    const int64_t steps = K / 64;
+    const bf16* wr0 = w0 + (e * n_out + n0 + r) * K + 32 * half;
+    const bf16* wr1 = GLU ? w1 + (e * n_out + n0 + r) * K + 32 * half : wr0;
+    struct Frags {
+        bf16x8 w[kMats][4];
+        bf16x8 x[4];
+    };
+    for (int64_t pass = 0; pass < count; pass += 32) {
+        const int64_t rows = count - pass < 32 ? count - pass : 32;
+        const bool aok = r < rows;
+        const bf16* ar = a + (row0 + pass + (aok ? r : 0)) * K + 32 * half;
+        f32x16 acc[kMats];
+#pragma unroll
+        for (int m = 0; m < kMats; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[m][i] = 0.0f;
+        auto load = [&](int64_t step, Frags& f) {
+            if (step >= steps) return;
+            const int64_t k = step * 64;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f.w[0][j] = *reinterpret_cast<const bf16x8*>(wr0 + k + 8 * j);
+                if constexpr (GLU) f.w[1][j] = *reinterpret_cast<const bf16x8*>(wr1 + k + 8 * j);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                bf16x8 v = {};
+                if (aok) v = *reinterpret_cast<const bf16x8*>(ar + k + 8 * j);
+                f.x[j] = v;
+            }
+        };
+        auto multiply = [&](int64_t step, const Frags& f) {
+            if (step >= steps) return;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int m = 0; m < kMats; ++m)
+                    acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.x[j], f.w[m][j], acc[m], 0, 0, 0);
+        };
+        // Two register sets, each holding one step's operands: the loads of
+        // the next two steps are in flight while one is multiplied.
+        Frags f0, f1;
+        int64_t s0 = wave;
+        load(s0, f0);
+        load(s0 + kSkinnyWaves, f1);
+        for (; s0 < steps; s0 += 2 * kSkinnyWaves) {
+            multiply(s0, f0);
+            load(s0 + 2 * kSkinnyWaves, f0);
+            multiply(s0 + kSkinnyWaves, f1);
+            load(s0 + 3 * kSkinnyWaves, f1);
+        }
+#pragma unroll
+        for (int m = 0; m < kMats; ++m)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) red[wave][m][i][lane] = acc[m][i];
+        __syncthreads();
+        // 16 accumulator entries x 64 lanes = 1024 outputs, two per thread;
+        // entry i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+#pragma unroll
+        for (int q = 0; q < 16 / kSkinnyWaves; ++q) {
+            const int i = q * kSkinnyWaves + wave;  // wave-uniform
+            const int64_t row = 8 * (i / 4) + 4 * (lane / 32) + i % 4;
+            if (row >= rows) continue;
+            const int64_t col = n0 + lane % 32;
+            float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kSkinnyWaves; ++w) {
+                v0 += red[w][0][i][lane];
+                if constexpr (GLU) v1 += red[w][kMats - 1][i][lane];
+            }
+            float out;
+            if constexpr (GLU) out = silu_f(v0 + to_f32(bias0[e * n_out + col])) * (v1 + to_f32(bias1[e * n_out + col]));
+            else out = v0 + to_f32(bias0[e * n_out + col]);
+            c[(row0 + pass + row) * n_out + col] = from_f32<bf16>(out);
+        }
+        __syncthreads();  // red is rewritten by the next pass
+    }
+}
+
 // Rows past the valid pairs are zero (moe_kernels.cu:512, 167-169); a
 // grid-stride loop over only those rows.
 template <typename T>
@@ -754,6 +865,24 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP needs hidden * width < 2^31");
     if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
                                              static_cast<long long>(kMaxScheduleExperts));
+    if (P <= kSkinnyMaxRowsPerExpert * E && E * ((Hd > D ? Hd : D) / kSkinnyCols) <= 0x7fffffffLL) {
+        const int64_t groups1 = Hd / kSkinnyCols, groups2 = D / kSkinnyCols;
+        hipLaunchKernelGGL(skinny_gemm_kernel<true>, dim3(static_cast<unsigned>(E * groups1)),
+                           dim3(kSkinnyWaves * kWave), 0, s, static_cast<const bf16*>(x), static_cast<const bf16*>(Wg),
+                           static_cast<const bf16*>(Wv), static_cast<const bf16*>(bg), static_cast<const bf16*>(bv),
+                           H, offsets, Hd, D, groups1);
+        int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
+        if (st != KOEMI_OK) return st;
+        hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2)),
+                           dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const bf16*>(Wo),
+                           static_cast<const bf16*>(Wo), static_cast<const bf16*>(bo), static_cast<const bf16*>(bo),
+                           static_cast<bf16*>(y), offsets, D, Hd, groups2);
+        st = check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
+        if (st != KOEMI_OK) return st;
+        hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
+                           offsets + E, P, D);
+        return check_launch("koemi_moe_grouped_mlp(zero)");
+    }
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
                        s, offsets, E, P, ws.max_slots, slot_expert, slot_row, slot_end);
     int st = check_launch("koemi_moe_grouped_mlp(schedule)");

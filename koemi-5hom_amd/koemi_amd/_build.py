@@ -40,6 +40,7 @@ SOURCES = (
     "blas.hip",
     "assoc_memory.hip",
     "herm_glue.hip",
+    "linear_rows.hip",
 )
 
 ARCH = "gfx950"

@@ -94,6 +94,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P),
     ),
+    "koemi_linear_rows": (
+        c_int,
+        (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, _P),
+    ),
     "koemi_salient_read_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64, c_int)),
     "koemi_salient_read": (
         c_int,

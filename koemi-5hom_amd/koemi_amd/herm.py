@@ -50,7 +50,7 @@ import torch
 from torch import Tensor
 from torch.nn import functional
 
-from koemi_amd import _native, memory, moe, recurrent, think
+from koemi_amd import _native, linear, memory, moe, recurrent, think
 
 __all__ = [
     "DecodeGraph",
@@ -225,9 +225,19 @@ def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
 
     if weight.dtype == torch.float32:
         return functional.linear(x, weight, bias)
+    if _few_rows(x, weight):
+        return linear.linear_rows([x], weight, bias)
     flat = x.reshape(-1, x.shape[-1]).to(weight.dtype)
     out = torch.addmm(bias, flat, weight.t(), out_dtype=torch.float32)
     return out.view(*x.shape[:-1], weight.shape[0])
+
+
+def _few_rows(x: Tensor, weight: Tensor) -> bool:
+    """Decode-step projections: a few rows and K <= 1024 (one or two staged
+    chunks; the 4096-wide fusion input stays on the library GEMM)."""
+
+    return (weight.dtype == torch.bfloat16 and x.numel() // x.shape[-1] <= linear.MAX_ROWS
+            and x.shape[-1] % 64 == 0 and x.shape[-1] <= 1024 and x.dtype in (torch.float32, torch.bfloat16))
 
 
 def _token_context(ids: Tensor, valid: Tensor, carried: Tensor) -> tuple[Tensor, Tensor]:
@@ -294,11 +304,13 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
 
 
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
-                 context: Tensor | None = None) -> tuple[Tensor, Tensor, dict[str, Tensor], Tensor]:
+                 context: Tensor | None = None, *, with_logits: bool = True
+                 ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
     for the embedding layer). Returns (logits, final_context, next_state,
-    surprise)."""
+    surprise); logits is None when ``with_logits`` is False (the stack's
+    inner layers, whose head output nothing reads)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
@@ -341,7 +353,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                   p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
     update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k, validate=False)
     final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
-    logits = _linear(final, p["head_w"], p["head_b"])
+    logits = _linear(final, p["head_w"], p["head_b"]) if with_logits else None
 
     local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
     salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
@@ -369,7 +381,8 @@ def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: T
     next_states = []
     logits = None
     for p, state in zip(params, states):
-        logits, context, next_state, _ = block_window(p, settings, ids, state, context)
+        last = len(next_states) == len(params) - 1
+        logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last)
         next_states.append(next_state)
     return logits, next_states
 

@@ -183,6 +183,32 @@ def test_grouped_mlp_bf16_mfma_ragged_segments(device, sizes):
     assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
 
 
+@pytest.mark.parametrize("sizes, D, H", [
+    ((0, 5, 70, 0, 57), 256, 384),          # empty experts, a 70-row expert (two passes), a partial second block
+    ((33, 1, 64, 65), 128, 192),            # 33 rows (one row in the second block), exactly 64, 65
+    ((8, 9, 7, 8, 8, 6, 10, 8, 8, 8, 9, 7, 8, 8, 8, 10), 1024, 2048),  # a C5 decode step: 64 tokens x top-2
+])
+def test_grouped_mlp_bf16_few_rows_per_expert(device, sizes, D, H):
+    """At most 64 pairs per expert on average: the skinny kernels (weights
+    streamed once, K split over the waves) against the float64 loop."""
+    g = torch.Generator().manual_seed(sum(sizes) + D)
+    E = len(sizes)
+    offsets = np.concatenate([[0], np.cumsum(sizes)])
+    P = int(offsets[-1]) + 5  # trailing rows past the valid pairs
+    assert P <= 64 * E
+    x = torch.randn((P, D), generator=g).to(torch.bfloat16)
+    experts = torch.full((P,), E, dtype=torch.int64)
+    for e in range(E):
+        experts[offsets[e]:offsets[e + 1]] = e
+    ws = [(0.05 * torch.randn(s, generator=g)).to(torch.bfloat16) for s in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    got = moe.grouped_expert_mlp_inference(x.to(device), experts.to(device), torch.from_numpy(offsets).to(device),
+                                           *(w.to(device) for w in ws))
+    want = oracle.grouped_mlp(x.float().numpy(), experts.numpy(), offsets, *(w.float().numpy() for w in ws),
+                              dtype=np.float32, round_hidden_bf16=True)
+    check_bf16_mlp(got[:offsets[-1]], want[:offsets[-1]], f"grouped MLP bf16 skinny sizes={sizes}")
+    assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
+
+
 def test_grouped_mlp_bf16_whole_rounds_and_split_last_round(device):
     # 130 row slots; width 512 and hidden 256 give 260 tiles in both GEMMs: on a
     # 256-CU device one whole round plus 4 leftover tiles computed in K chunks
