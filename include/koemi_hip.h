@@ -132,7 +132,8 @@ int koemi_admission_quantile(const float* surprise, const uint8_t* valid_mask, u
  * h = mix32(tok * 1000003 + prev * 97409); a[t, s] = (h + s * 0x9E3779B9) mod E
  * for valid tokens, -1 otherwise. ids are I32 or I64 (`id_dtype`).
  * *duplicate_flag (device int32, caller-zeroed) is set to 1 when a valid token
- * received the same expert in two slots (moe/__init__.py:113-125, 171-175). */
+ * received the same expert in two slots (moe/__init__.py:113-125, 171-175);
+ * NULL skips the check. */
 int koemi_moe_route_hash(const void* token_ids, const void* previous_token_ids,
                          const uint8_t* valid_mask, int id_dtype, int64_t* assignments,
                          int32_t* duplicate_flag, int64_t tokens, int64_t expert_count,

@@ -44,7 +44,7 @@ __global__ void route_hash_kernel(const I* __restrict__ tok, const I* __restrict
         for (int64_t r = 0; r < s; ++r) dup |= (row[r] == e);
         row[s] = e;
     }
-    if (dup) atomicOr(dup_flag, 1);
+    if (dup && dup_flag != nullptr) atomicOr(dup_flag, 1);
 }
 
 // softmax(logits) then top-k in descending probability, ties to the lower index
@@ -155,7 +155,7 @@ extern "C" int koemi_moe_route_hash(const void* token_ids, const void* previous_
         return fail(KOEMI_ERR_INVALID, "route needs 1 <= top_k <= expert_count");
     if (!index_dtype(id_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "token ids must be int32 or int64");
     if (tokens == 0) return KOEMI_OK;
-    if (!token_ids || !previous_token_ids || !valid_mask || !assignments || !duplicate_flag)
+    if (!token_ids || !previous_token_ids || !valid_mask || !assignments)
         return fail(KOEMI_ERR_INVALID, "route received a null pointer");
     const dim3 grid(grid_for(tokens, 256)), block(256);
     hipStream_t s = as_stream(stream);

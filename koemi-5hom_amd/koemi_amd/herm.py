@@ -334,7 +334,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     fast, basis, normalizer = associative_scan_read(projected, surprise, valid, state["basis"], state["normalizer"],
                                                     width=d, features=settings.memory_features)
 
-    admission, _ = think.salience_admission(surprise, valid, threshold=settings.salience_threshold)
+    admission = think.admission_above(surprise, valid, settings.salience_threshold)
     salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                local_keys, local_values, admission, ws)
     fused = _rms(_linear(torch.cat((ws, fast, local_value, salient_value), dim=-1), p["fusion_w"], p["fusion_b"]),

@@ -155,7 +155,8 @@ def route_topk_valid(
     _require_library()
     count = token_ids.numel()
     assignments = torch.empty((count, top_k), device=token_ids.device, dtype=torch.int64)
-    duplicate = torch.zeros((1,), device=token_ids.device, dtype=torch.int32)
+    # the duplicate check's flag only when it is read (validate)
+    duplicate = torch.zeros((1,), device=token_ids.device, dtype=torch.int32) if validate else None
     if count:
         with torch.cuda.device(token_ids.device):
             _native.call(
@@ -165,7 +166,7 @@ def route_topk_valid(
                 valid_mask.data_ptr(),
                 _native.dtype_code(token_ids.dtype),
                 assignments.data_ptr(),
-                duplicate.data_ptr(),
+                duplicate.data_ptr() if duplicate is not None else None,
                 count,
                 expert_count,
                 top_k,

@@ -31,6 +31,7 @@ __all__ = [
     "CudaThinkBenchmark",
     "CudaThinkUnavailableError",
     "CudaThinkValidationError",
+    "admission_above",
     "benchmark_causal_surprise",
     "causal_surprise",
     "salience_admission",
@@ -337,6 +338,32 @@ def surprise_from_logits(
     bias = content_bias.contiguous() if content_bias is not None else None
     out = _rows_forward(flat, bias, target_ids.reshape(-1).contiguous(), valid_mask.reshape(-1).contiguous(), torch.float32)
     return out.view(logits.shape[:-1])
+
+
+def admission_above(surprise: Tensor, valid_mask: Tensor, threshold: float) -> Tensor:
+    """The admission mask alone for a fixed threshold (network.py:349), as
+    ``salience_admission(surprise, valid_mask, threshold=threshold)[0]`` without
+    forming the tau tensor (one kernel)."""
+
+    if not isinstance(surprise, Tensor) or not isinstance(valid_mask, Tensor):
+        raise CudaThinkValidationError("surprise and valid_mask must be torch.Tensors")
+    if surprise.shape != valid_mask.shape or valid_mask.dtype != torch.bool:
+        raise CudaThinkValidationError("valid_mask must be a bool tensor of the surprise's shape")
+    if surprise.dtype not in _SUPPORTED_DTYPES:
+        raise CudaThinkValidationError("surprise dtype must be float16, bfloat16 or float32")
+    if isinstance(threshold, bool) or not isinstance(threshold, (int, float)):
+        raise CudaThinkValidationError("threshold must be a number")
+    if surprise.device.type != "cuda" or valid_mask.device != surprise.device:
+        raise CudaThinkValidationError("all think tensors must be on one CUDA device")
+    _load()
+    scores = surprise.reshape(-1).contiguous()
+    valid = valid_mask.reshape(-1).contiguous()
+    admission = torch.empty((scores.numel(),), device=scores.device, dtype=torch.bool)
+    if scores.numel():
+        _native.call("koemi_admission_threshold", scores.data_ptr(), valid.data_ptr(), admission.data_ptr(),
+                     scores.numel(), float(threshold), _native.dtype_code(scores.dtype),
+                     _native.stream_of(scores.device))
+    return admission.view(surprise.shape)
 
 
 def salience_admission(

@@ -173,3 +173,9 @@ def test_fixed_threshold_admission_is_strict(device):
     for dtype in (torch.bfloat16, torch.float16):
         m, _ = think.salience_admission(s.to(dtype), valid, threshold=0.75)
         assert m.tolist() == [False, False, True, False]
+    assert think.admission_above(s, valid, 0.75).tolist() == [False, False, True, False]
+    g = torch.Generator().manual_seed(4)
+    big = torch.rand((3, 1000), generator=g).to(device)
+    big_valid = (torch.rand((3, 1000), generator=g) < 0.8).to(device)
+    assert torch.equal(think.admission_above(big, big_valid, 0.5),
+                       think.salience_admission(big, big_valid, threshold=0.5)[0])
