@@ -28,11 +28,12 @@
 // one workgroup per (batch row, 64 output columns, 64 query rows): the
 // window's feature softmaxes, decays, cumulative log-decays and write weights
 // are formed while staging them in LDS (each workgroup of a row repeats this
-// small part), then the causal influence rows of its 64 queries go to LDS
-// with their sums (wave reductions), and four waves of 16 rows each
-// accumulate the read of their 64 columns, four slots per LDS load; the
-// workgroups of the first row tile also write the final basis columns and the
-// normalizer.
+// small part); the three products of the window run on fp32 MFMA
+// (v_mfma_f32_32x32x2f32): the feature similarities of the causal influence
+// rows (K = features), the read itself (influence x values, K = slots, with
+// the carried basis term as a few more K values) and, in the workgroups of the
+// first row tile, the final basis columns (K = slots); the denominators and
+// the normalizer are wave reductions.
 #include "common.hpp"
 
 namespace koemi {
@@ -46,15 +47,32 @@ constexpr float kReadEpsilon = 0.00390625f;          // 2^-8
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// LDS floats: the influence rows of the tile (64 x L rounded up to 4, for
-// 16-byte reads) and their denominators (64), cum, log-decay, write weights
-// and final-write weights (4L), features (transposed, [MAXM][L]) and query
-// features ([L][MAXM]) zero-padded to MAXM so every feature loop runs
-// unguarded (2 L MAXM), the value columns (64L).
-inline int64_t assoc_pitch(int64_t L) { return (L + 3) & ~int64_t(3); }
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+// LDS floats: the influence rows of the tile (64 x (Lq + 1), Lq = L rounded up
+// to 32, the odd pitch spreading the MFMA operand reads of 32 rows over the
+// banks); cum, log-decay (then the prior log-weights), write weights and
+// final-write weights (4 Lq); features ([MAXM][L + 1]) and query features
+// ([L][MAXM + 1]), zero-padded to MAXM so the feature products run unguarded;
+// the value columns ([Lq][65]).
+inline int64_t assoc_round(int64_t L) { return (L + 31) & ~int64_t(31); }
 inline int64_t assoc_maxm(int64_t M) { return M <= 16 ? 16 : 32; }
 inline size_t assoc_lds(int64_t L, int64_t M) {
-    return (kAssocRows * assoc_pitch(L) + kAssocRows + 4 * L + 2 * L * assoc_maxm(M) + kAssocCols * L) * sizeof(float);
+    const int64_t Lq = assoc_round(L), X = assoc_maxm(M);
+    return (kAssocRows * (Lq + 1) + 4 * Lq + X * (L + 1) + L * (X + 1) + Lq * (kAssocCols + 1)) * sizeof(float);
+}
+
+// e^x and tanh on the hardware exp2 and reciprocal (about 1 ulp each): the
+// window kernel evaluates them per (query, slot) pair and per staged value.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float fast_tanh(float x) {
+    return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x * 2.8853900817779268f) + 1.0f);
+}
+
+// v_mfma_f32_32x32x2f32: lane l supplies A[l % 32][l / 32] and B[l / 32][l % 32];
+// accumulator entry i of lane l is D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
+__device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
 template <int MAXM>
@@ -64,69 +82,73 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out,
     float* __restrict__ next_basis, float* __restrict__ next_normalizer, int L, int64_t D, int M) {
     extern __shared__ float sh[];
-    const int Lp = (L + 3) & ~3;
-    float* infl = sh;                     // [64][Lp]
-    float* den = infl + kAssocRows * Lp;  // [64]
-    float* cum = den + kAssocRows;        // [L]
-    float* logd = cum + L;                // [L]
-    float* wt = logd + L;                 // [L] write weights
-    float* fwt = wt + L;                  // [L] final-write weights
-    float* f_sh = fwt + L;                // [MAXM][L] (slot-contiguous: lanes read consecutive slots)
-    float* q_sh = f_sh + L * MAXM;        // [L][MAXM]
-    float* val = q_sh + L * MAXM;         // [L][64]
+    constexpr int QP = MAXM + 1;        // query-feature pitch
+    constexpr int VP = kAssocCols + 1;  // value pitch
+    const int Lq = (L + 31) & ~31;
+    const int IP = Lq + 1;  // influence pitch
+    const int FP = L + 1;   // feature pitch
+    float* infl = sh;                      // [64][IP]
+    float* cum = infl + kAssocRows * IP;   // [Lq]
+    float* logd = cum + Lq;                // [Lq]
+    float* wt = logd + Lq;                 // [Lq] write weights
+    float* fwt = wt + Lq;                  // [Lq] final-write weights
+    float* f_sh = fwt + Lq;                // [MAXM][FP]
+    float* q_sh = f_sh + MAXM * FP;        // [L][QP]
+    float* val = q_sh + L * QP;            // [Lq][VP]
     const int64_t b = blockIdx.x;
     const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kAssocCols;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int h = lane >> 5, r32 = lane & 31;
     const float* rows0 = proj + b * L * stride;
-    // per position: the two feature softmaxes, the decay and the write weight
-    for (int t = tid; t < L; t += 256) {
+    // the key's and the query's feature softmax of every position (one per
+    // thread), the decay and the write weight with the key's
+    for (int job = tid; job < 2 * L; job += 256) {
+        const bool query = job >= L;
+        const int t = query ? job - L : job;
         const float* row = rows0 + t * stride;
-        float zk[MAXM], zq[MAXM];
-        float mk = -INFINITY, mq = -INFINITY;
+        const int64_t off = query ? fq_off : fk_off;
+        float z[MAXM];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {  // unconditional loads at clamped columns, then masked
-            zk[m] = row[fk_off + min(m, M - 1)];
-            zq[m] = row[fq_off + min(m, M - 1)];
-        }
+        for (int m = 0; m < MAXM; ++m) z[m] = row[off + min(m, M - 1)];  // unconditional, then masked
 #pragma unroll
         for (int m = 0; m < MAXM; ++m) {
-            if (m >= M) zk[m] = zq[m] = -INFINITY;
-            mk = fmaxf(mk, zk[m]);
-            mq = fmaxf(mq, zq[m]);
+            if (m >= M) z[m] = -INFINITY;
+            mx = fmaxf(mx, z[m]);
         }
-        float sk = 0.0f, sq = 0.0f;
+        float sum = 0.0f;
 #pragma unroll
         for (int m = 0; m < MAXM; ++m) {
-            zk[m] = m < M ? expf(zk[m] - mk) : 0.0f;
-            zq[m] = m < M ? expf(zq[m] - mq) : 0.0f;
-            sk += zk[m];
-            sq += zq[m];
+            z[m] = m < M ? fast_exp(z[m] - mx) : 0.0f;
+            sum += z[m];
         }
+        const float inv = __builtin_amdgcn_rcpf(sum);
+        if (query) {
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            f_sh[m * L + t] = zk[m] / sk;  // zero past M
-            q_sh[t * MAXM + m] = zq[m] / sq;
+            for (int m = 0; m < MAXM; ++m) q_sh[t * QP + m] = z[m] * inv;  // zero past M
+        } else {
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m) f_sh[m * FP + t] = z[m] * inv;
+            const bool ok = valid[b * L + t] != 0;
+            const float decay = kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]);
+            const float sv = fminf(fmaxf(surprise[b * L + t], 0.0f), 1.0f);
+            logd[t] = ok ? logf(decay) : 0.0f;
+            wt[t] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
         }
-        const bool ok = valid[b * L + t] != 0;
-        const float decay = kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]);
-        const float sv = fminf(fmaxf(surprise[b * L + t], 0.0f), 1.0f);
-        logd[t] = ok ? logf(decay) : 0.0f;
-        wt[t] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
     }
     {
-        // wave w stages value rows w, w + 4, ...: eight loads in flight per lane per batch
+        // value rows t < Lq (zero past L): wave w stages rows w, w + 4, ...,
+        // sixteen unconditional loads in flight per lane
         const int64_t dv = c0 + lane;
-        for (int tb = wave; tb < L; tb += 32) {
-            float x[8];
+        const int64_t dc = dv < D ? dv : D - 1;
+        for (int tb = wave; tb < Lq; tb += 64) {
+            float x[16];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int t = tb + 4 * j;
-                x[j] = (t < L && dv < D) ? rows0[t * stride + value_off + dv] : 0.0f;
-            }
+            for (int j = 0; j < 16; ++j) x[j] = rows0[min(tb + 4 * j, L - 1) * stride + value_off + dc];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < 16; ++j) {
                 const int t = tb + 4 * j;
-                if (t < L) val[t * kAssocCols + lane] = dv < D ? tanhf(x[j]) : 0.0f;
+                if (t < Lq) val[t * VP + lane] = (t < L && dv < D) ? fast_tanh(x[j]) : 0.0f;
             }
         }
     }
@@ -157,106 +179,137 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
     }
     __syncthreads();
     const float total = cum[L - 1];
-    for (int s = tid; s < L; s += 256) fwt[s] = expf(total - cum[s]) * wt[s];
-    const int64_t d = c0 + lane;
-    const bool dok = d < D;
-    float brow[MAXM], nrm[MAXM];
-#pragma unroll
-    for (int m = 0; m < MAXM; ++m) {
-        brow[m] = (m < M && dok) ? basis[(b * D + d) * M + m] : 0.0f;
-        nrm[m] = m < M ? normalizer[b * M + m] : 0.0f;
+    float* prior = logd;  // prior_t = cum_t - log decay_t replaces the log-decays from here on
+    for (int s = tid; s < L; s += 256) {
+        fwt[s] = expf(total - cum[s]) * wt[s];
+        prior[s] = cum[s] - logd[s];
     }
+    __syncthreads();
 
-    constexpr int kRowsPerWave = kAssocRows / 4;
     const int t0 = static_cast<int>(blockIdx.z) * kAssocRows;
     const int rows = min(kAssocRows, L - t0);
-    __syncthreads();  // fwt is written
-    // influence of slot s on query t0 + r (zero unless s < t): wave w fills
-    // rows w, w + 4, ...; lanes take consecutive slots; the row sums (the
-    // reads' denominators) by wave reduction.
-    for (int r = wave; r < rows; r += 4) {
-        const int t = t0 + r;
-        const float prior = cum[t] - logd[t];
-        float sum = 0.0f;
-        for (int s = lane; s < t0 + rows; s += kWave) {
-            float v = 0.0f;
-            if (s < t) {
-                float sim = 0.0f;
+    const int s_cnt = t0 + rows;  // slots that can reach these queries (s < t <= t0 + rows - 1)
+    const int nsb = (s_cnt + 31) / 32;
+    // influence of slot s on query t (zero unless s < t): the feature products
+    // q_t . f_s of 32 x 32 blocks on MFMA (K = MAXM), then the decay and write
+    // weights; blocks (query half, slot block) go round-robin over the waves.
+    for (int blk = wave; blk < 2 * nsb; blk += 4) {
+        const int tb = blk / nsb, sb = blk - tb * nsb;
+        const int ta = min(t0 + tb * 32 + r32, L - 1);
+        const int s = sb * 32 + r32, sc = min(s, L - 1);
+        f32x16 acc = {};
 #pragma unroll
-                for (int m = 0; m < MAXM; ++m) sim = fmaf(q_sh[t * MAXM + m], f_sh[m * L + s], sim);
-                v = expf(prior - cum[s]) * sim * wt[s];
-            }
-            infl[r * Lp + s] = v;
-            sum += v;
-        }
+        for (int kk = 0; kk < MAXM / 2; ++kk)
+            acc = mfma2(q_sh[ta * QP + 2 * kk + h], f_sh[(2 * kk + h) * FP + sc], acc);
+        const float cs = cum[sc], ws = wt[sc];
 #pragma unroll
-        for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-        if (lane == 0) {
-            float nq = 0.0f;
-#pragma unroll
-            for (int m = 0; m < MAXM; ++m) nq = fmaf(nrm[m], q_sh[t * MAXM + m], nq);
-            den[r] = expf(prior) * nq + sum;
+        for (int i = 0; i < 16; ++i) {
+            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            const int t = t0 + r;
+            const float v = fast_exp(prior[min(t, L - 1)] - cs) * acc[i] * ws;
+            infl[r * IP + s] = (s < t && t < L) ? v : 0.0f;
         }
     }
     __syncthreads();
-    // wave w: rows w, w + 4, ... of the tile (16 at most), lane = column
-    float acc[kRowsPerWave];
+    {
+        // the reads: wave w owns the 32 x 32 block (query half w / 2, column half w % 2);
+        // sum over slots of influence x value on MFMA, then the carried basis term
+        // e^{prior_t} (q_t . basis_d) as MAXM more K values. The denominators ride
+        // along as a second product with the same A operand and B = 1 (row sums of
+        // the influence), then e^{prior_t} (q_t . normalizer), so every lane holds
+        // the denominator of each of its rows.
+        const int tb = wave >> 1, db = wave & 1;
+        const int k_end = (s_cnt + 1) & ~1;
+        const float* ia = infl + (tb * 32 + r32) * IP + h;
+        const float* vb = val + h * VP + db * 32 + r32;
+        f32x16 acc = {}, accd = {};
+        int s = 0;
+        for (; s + 8 <= k_end; s += 8) {  // four steps' operands loaded together
+            const float a0 = ia[s], a1 = ia[s + 2], a2 = ia[s + 4], a3 = ia[s + 6];
+            const float b0 = vb[s * VP], b1 = vb[(s + 2) * VP], b2 = vb[(s + 4) * VP], b3 = vb[(s + 6) * VP];
+            acc = mfma2(a0, b0, acc);
+            accd = mfma2(a0, 1.0f, accd);
+            acc = mfma2(a1, b1, acc);
+            accd = mfma2(a1, 1.0f, accd);
+            acc = mfma2(a2, b2, acc);
+            accd = mfma2(a2, 1.0f, accd);
+            acc = mfma2(a3, b3, acc);
+            accd = mfma2(a3, 1.0f, accd);
+        }
+        for (; s < k_end; s += 2) {
+            const float a = ia[s];
+            acc = mfma2(a, vb[s * VP], acc);
+            accd = mfma2(a, 1.0f, accd);
+        }
+        const int tq = min(t0 + tb * 32 + r32, L - 1);
+        const float ep = fast_exp(prior[tq]);
+        const int64_t dq = min(c0 + db * 32 + r32, D - 1);
 #pragma unroll
-    for (int j = 0; j < kRowsPerWave; ++j) acc[j] = 0.0f;
-    const int s_end = t0 + rows - 1;  // slots past the tile's last query add zero
-    int s = 0;
-    if (rows == kAssocRows) {
-        for (; s + 4 <= s_end; s += 4) {
-            const float v0 = val[s * kAssocCols + lane], v1 = val[(s + 1) * kAssocCols + lane];
-            const float v2 = val[(s + 2) * kAssocCols + lane], v3 = val[(s + 3) * kAssocCols + lane];
+        for (int kk = 0; kk < MAXM / 2; ++kk) {
+            const int m = 2 * kk + h;
+            const float on = m < M ? 1.0f : 0.0f;
+            const float aq = ep * q_sh[tq * QP + m];
+            acc = mfma2(aq, basis[(b * D + dq) * M + min(m, M - 1)] * on, acc);
+            accd = mfma2(aq, normalizer[b * M + min(m, M - 1)] * on, accd);
+        }
+        const int64_t d = c0 + db * 32 + r32;
 #pragma unroll
-            for (int j = 0; j < kRowsPerWave; ++j) {
-                const float4 iv = *reinterpret_cast<const float4*>(infl + (wave + 4 * j) * Lp + s);
-                acc[j] = fmaf(iv.x, v0, fmaf(iv.y, v1, fmaf(iv.z, v2, fmaf(iv.w, v3, acc[j]))));
+        for (int i = 0; i < 16; ++i) {
+            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            if (r >= rows || d >= D) continue;
+            const float dn = accd[i], reg = dn + kReadEpsilon;
+            out[(b * L + t0 + r) * D + d] = (dn / reg) * acc[i] / reg;
+        }
+    }
+    if (blockIdx.z != 0) return;
+    // final basis columns (64 x M): sum over slots of (final-write weight x value)
+    // x feature on MFMA, slots split in two halves over wave pairs, the halves
+    // added through LDS (the influence rows are no longer read)
+    const float keep = expf(total);
+    const int half = ((L + 1) / 2 + 1) & ~1;
+    {
+        const int db = wave & 1, kh = wave >> 1;
+        const int s_lo = kh * half, s_hi = min(L, s_lo + half);
+        f32x16 acc = {};
+        const float* fm = f_sh + min(r32, MAXM - 1) * FP;
+        const float fon = r32 < MAXM ? 1.0f : 0.0f;
+        const float* vcol = val + db * 32 + r32;
+        for (int s = s_lo; s < s_hi; s += 8) {  // four steps' operands loaded together
+            float a[4], bf[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int sl = s + 2 * q + h, slc = min(sl, L - 1);
+                a[q] = sl < s_hi ? fwt[slc] * vcol[slc * VP] : 0.0f;
+                bf[q] = fm[slc] * fon;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc = mfma2(a[q], bf[q], acc);
+        }
+        __syncthreads();  // the influence area is free
+        float* part = infl + db * 16 * kWave;  // [2][16][64]
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) part[i * kWave + lane] = acc[i];
+        }
+        __syncthreads();
+        if (kh == 0) {
+            const int m = r32;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t d = c0 + db * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+                if (m >= M || d >= D) continue;
+                const int64_t at = (b * D + d) * M + m;
+                next_basis[at] = fmaf(keep, basis[at], acc[i] + part[i * kWave + lane]);
             }
         }
     }
-    for (; s < s_end; ++s) {
-        const float v0 = val[s * kAssocCols + lane];
-#pragma unroll
-        for (int j = 0; j < kRowsPerWave; ++j) {
-            const int r = wave + 4 * j;
-            if (r < rows) acc[j] = fmaf(infl[r * Lp + s], v0, acc[j]);
+    if (blockIdx.y == 0 && wave == 3) {
+        for (int m = 0; m < M; ++m) {
+            float sum = 0.0f;
+            for (int s = lane; s < L; s += kWave) sum = fmaf(fwt[s], f_sh[m * FP + s], sum);
+            sum = wave_sum_xor(sum);
+            if (lane == 0) next_normalizer[b * M + m] = fmaf(keep, normalizer[b * M + m], sum);
         }
-    }
-#pragma unroll
-    for (int j = 0; j < kRowsPerWave; ++j) {
-        const int r = wave + 4 * j;
-        if (r >= rows) continue;
-        const int t = t0 + r;
-        float bq = 0.0f;
-#pragma unroll
-        for (int m = 0; m < MAXM; ++m) bq = fmaf(brow[m], q_sh[t * MAXM + m], bq);
-        const float num = expf(cum[t] - logd[t]) * bq + acc[j];
-        const float dn = den[r], reg = dn + kReadEpsilon;
-        if (dok) out[(b * L + t) * D + d] = (dn / reg) * num / reg;
-    }
-    if (blockIdx.z != 0) return;
-    // final basis columns: wave w takes the features m with m % 4 == w
-    const float keep = expf(total);
-#pragma unroll
-    for (int m = 0; m < MAXM; ++m) {
-        if (m >= M || (m & 3) != wave) continue;
-        float a0 = keep * brow[m], a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-        int s = 0;
-        for (; s + 4 <= L; s += 4) {
-            a0 = fmaf(fwt[s] * val[s * kAssocCols + lane], f_sh[m * L + s], a0);
-            a1 = fmaf(fwt[s + 1] * val[(s + 1) * kAssocCols + lane], f_sh[m * L + s + 1], a1);
-            a2 = fmaf(fwt[s + 2] * val[(s + 2) * kAssocCols + lane], f_sh[m * L + s + 2], a2);
-            a3 = fmaf(fwt[s + 3] * val[(s + 3) * kAssocCols + lane], f_sh[m * L + s + 3], a3);
-        }
-        for (; s < L; ++s) a0 = fmaf(fwt[s] * val[s * kAssocCols + lane], f_sh[m * L + s], a0);
-        if (dok) next_basis[(b * D + d) * M + m] = (a0 + a1) + (a2 + a3);
-    }
-    if (blockIdx.y == 0 && tid < M) {
-        float acc = keep * normalizer[b * M + tid];
-        for (int s = 0; s < L; ++s) acc = fmaf(fwt[s], f_sh[tid * L + s], acc);
-        next_normalizer[b * M + tid] = acc;
     }
 }
 
