@@ -248,11 +248,13 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
  * added first; NULL means none (already inside the pre-activations). Then
  * a = 2^-8 + (1 - 2^-7) sigmoid, b = (1 - a) tanh, the valid mask (NULL: all
  * valid) and h_t = a_t h_{t-1} + b_t from `initial` [batch, width] into
- * `states` [batch, length, width], as in network.py:306-310. No workspace. */
+ * `states` [batch, length, width], as in network.py:306-310; with
+ * `states_bf16` (NULL: none) also a bf16 copy of the states for the next
+ * projection's GEMM. No workspace. */
 int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                      int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
-                     const uint8_t* valid, const float* initial, float* states, int64_t batch, int64_t length,
-                     int64_t width, koemi_stream_t stream);
+                     const uint8_t* valid, const float* initial, float* states, void* states_bf16, int64_t batch,
+                     int64_t length, int64_t width, koemi_stream_t stream);
 
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections
  * in a decode step: the gate, working-state, fusion and head layers of
@@ -314,7 +316,9 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
  * (layers.py:14-16) on rows whose mask byte is set (all rows when mask is
  * NULL), out = x elsewhere (the expert mixture's valid-row select,
  * experts.py:134-136); x, weight and out fp32 [rows, width], residual NULL or
- * [rows, width] in residual_dtype; width a multiple of 4, at most 2048.
+ * [rows, width] in residual_dtype; width a multiple of 4, at most 2048;
+ * `output_bf16` (NULL: none) receives a bf16 copy of out for a following
+ * GEMM, and `output` may then be NULL.
  * koemi_herm_token_context: previous[b, t] = the last valid token before t
  * (carried_last[b] before the first), last[b] = the window's last valid token
  * or carried_last[b] (network.py:742-761); int64 ids, valid bytes.
@@ -322,7 +326,7 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
  * entries of [carried (window entries) ; new (length entries)] with their
  * valid bytes (memory.py:385-403); fp32 keys and values [batch, *, width]. */
 int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
-                       const uint8_t* mask, float* output, int64_t rows, int64_t width, float eps,
+                       const uint8_t* mask, float* output, void* output_bf16, int64_t rows, int64_t width, float eps,
                        koemi_stream_t stream);
 int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
                              int64_t* previous, int64_t* last, int64_t batch, int64_t length, koemi_stream_t stream);
@@ -330,6 +334,13 @@ int koemi_herm_local_tail(const float* carried_keys, const float* carried_values
                           const float* keys, const float* values, const uint8_t* valid, float* out_keys,
                           float* out_values, uint8_t* out_valid, int64_t batch, int64_t window, int64_t length,
                           int64_t width, koemi_stream_t stream);
+
+/* The fusion layer's input [working ; memory ; local ; salient]
+ * (network.py:401-405, a torch.cat in the reference) as one bf16 matrix
+ * [rows, pieces * width] for its GEMM: `pieces` (1..4) fp32 [rows, width]
+ * blocks (16-byte aligned), width % 4 == 0, rounded to nearest even. */
+int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2, const float* input3,
+                           int pieces, int64_t rows, int64_t width, void* output, koemi_stream_t stream);
 
 /* Local-memory read, LocalKeyValueMemory.read_window of model/memory.py:332-362
  * without the novelty output (a torch composite in the reference; network.py:

@@ -166,6 +166,7 @@ struct GateInputs {
     const float* retention_bias;  // [F] or null
     const float* candidate_bias;  // [F] or null
     const uint8_t* valid;         // [B * L] or null
+    __bf16* h16;                  // [B, L, F] bf16 copy of the states, or null
 };
 
 __device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
@@ -178,7 +179,8 @@ __device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc
 template <int S, int NSEG, int VEC, bool GATES = false>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
-    int64_t L, int64_t F, int64_t col_tiles, int64_t stride, GateInputs gates = GateInputs{nullptr, nullptr, nullptr}) {
+    int64_t L, int64_t F, int64_t col_tiles, int64_t stride,
+    GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr}) {
     using V = typename FloatVec<VEC>::type;
     constexpr int CH = S * NSEG;
     __shared__ float seg_p[NSEG][VEC][kWave];
@@ -275,7 +277,16 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
                 float o[VEC];
 #pragma unroll
                 for (int c = 0; c < VEC; ++c) o[c] = ra[i][c] * c_in[c] + rb[i][c];
-                if (t < L) *reinterpret_cast<V*>(h_col + t * F) = FloatVec<VEC>::join(o);
+                if (t < L) {
+                    *reinterpret_cast<V*>(h_col + t * F) = FloatVec<VEC>::join(o);
+                    if constexpr (GATES) {
+                        if (gates.h16 != nullptr) {
+#pragma unroll
+                            for (int c = 0; c < VEC; ++c)
+                                gates.h16[(bi * L + t) * F + f + c] = static_cast<__bf16>(o[c]);
+                        }
+                    }
+                }
             }
         }
         __syncthreads();
@@ -452,7 +463,9 @@ __global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict
     float a, b;
     gate_pair(zr[bi * stride + f], zc[bi * stride + f], gates.retention_bias ? gates.retention_bias[f] : 0.0f,
               gates.candidate_bias ? gates.candidate_bias[f] : 0.0f, keep, a, b);
-    h[i] = a * h0[i] + b;
+    const float hv = a * h0[i] + b;
+    h[i] = hv;
+    if (gates.h16 != nullptr) gates.h16[i] = static_cast<__bf16>(hv);
 }
 
 // The fused gates + scan over fp32 pre-activation products zr, zc (row r of
@@ -461,10 +474,10 @@ __global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict
 // are aligned to it and that still fills the chip, one column per lane
 // otherwise. The caller has checked that B * ceil(F / 64) fits the grid.
 int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
-                      const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, int64_t B,
-                      int64_t L, int64_t F, hipStream_t stream) {
+                      const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
+                      int64_t B, int64_t L, int64_t F, hipStream_t stream) {
     constexpr int VEC = KOEMI_SCAN_VEC;
-    const GateInputs gates{retention_bias, candidate_bias, valid};
+    const GateInputs gates{retention_bias, candidate_bias, valid, static_cast<__bf16*>(h16)};
     if (L == 1) {
         hipLaunchKernelGGL(gated_step_kernel, dim3(static_cast<unsigned>((B * F + 255) / 256)), dim3(256), 0, stream,
                            zr, zc, stride, gates, h0, h, B, F);
@@ -545,8 +558,8 @@ extern "C" int koemi_affine_scan_backward(const void* retention, const void* ini
 
 extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                                 int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
-                                const uint8_t* valid, const float* initial, float* states, int64_t batch,
-                                int64_t length, int64_t width, koemi_stream_t stream) {
+                                const uint8_t* valid, const float* initial, float* states, void* states_bf16,
+                                int64_t batch, int64_t length, int64_t width, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1)
         return fail(KOEMI_ERR_INVALID, "gated scan needs non-negative batch and length and a positive width");
     if (retention_offset < 0 || candidate_offset < 0 || retention_offset + width > row_stride ||
@@ -557,6 +570,6 @@ extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride,
     if (batch * ((width + kWave - 1) / kWave) > 0x7fffffffLL || batch * width > 0x7fffffffLL * 256LL)
         return fail(KOEMI_ERR_UNSUPPORTED, "gated scan grid too large");
     return launch_gated_scan(preactivations + retention_offset, preactivations + candidate_offset, row_stride,
-                             retention_bias, candidate_bias, valid, initial, states, batch, length, width,
-                             as_stream(stream));
+                             retention_bias, candidate_bias, valid, initial, states, states_bf16, batch, length,
+                             width, as_stream(stream));
 }

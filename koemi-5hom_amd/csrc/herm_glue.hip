@@ -12,6 +12,9 @@
 //     row, a max-scan of the valid positions.
 //   koemi_herm_local_tail: the local ring after a window, the last `window`
 //     entries of [carried ; new] with their valid bytes (memory.py:385-403).
+//   koemi_herm_concat_bf16: the fusion layer's input [working ; memory ;
+//     local ; salient] (network.py:401-405) as one bf16 matrix for its GEMM,
+//     the concatenation and the cast in one pass.
 #include "common.hpp"
 
 namespace koemi {
@@ -21,7 +24,7 @@ template <typename R, int NV>
 __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restrict__ x, const R* __restrict__ residual,
                                                            const float* __restrict__ w,
                                                            const uint8_t* __restrict__ mask, float* __restrict__ y,
-                                                           int64_t rows, int H, float eps) {
+                                                           bf16* __restrict__ y16, int64_t rows, int H, float eps) {
     const int lane = lane_id();
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
     if (row >= rows) return;
@@ -49,7 +52,6 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restri
     for (int off = kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
     const bool keep = mask == nullptr || mask[row] != 0;
     const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
-    float* yr = y + row * H;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
@@ -61,7 +63,14 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restri
         } else {
             o = *reinterpret_cast<const float4*>(xr + c);
         }
-        *reinterpret_cast<float4*>(yr + c) = o;
+        if (y != nullptr) *reinterpret_cast<float4*>(y + row * H + c) = o;
+        if (y16 != nullptr) {
+            typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+            bf16x4 q;
+            q[0] = static_cast<__bf16>(o.x); q[1] = static_cast<__bf16>(o.y);
+            q[2] = static_cast<__bf16>(o.z); q[3] = static_cast<__bf16>(o.w);
+            *reinterpret_cast<bf16x4*>(y16 + row * H + c) = q;
+        }
     }
 }
 
@@ -121,33 +130,57 @@ __global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float
     if (threadIdx.x == 0) ovalid[b * W + s] = carried_entry ? cvalid[b * W + i] : valid[b * L + (i - W)];
 }
 
+// [rows, pieces * width] bf16 from `pieces` fp32 [rows, width] blocks; a thread
+// converts four consecutive values (16-byte load, 8-byte store).
+struct ConcatPieces {
+    const float* p[4];
+};
+__global__ __launch_bounds__(256) void herm_concat_bf16_kernel(ConcatPieces in, int pieces, int64_t rows,
+                                                               int64_t width, bf16* __restrict__ out) {
+    const int64_t quads = width / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * pieces * quads) return;
+    const int64_t row = i / (pieces * quads);
+    const int64_t rest = i - row * pieces * quads;
+    const int piece = static_cast<int>(rest / quads);
+    const int64_t c = (rest - piece * quads) * 4;
+    const float4 v = *reinterpret_cast<const float4*>(in.p[piece] + row * width + c);
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+    bf16x4 q;
+    q[0] = static_cast<__bf16>(v.x); q[1] = static_cast<__bf16>(v.y);
+    q[2] = static_cast<__bf16>(v.z); q[3] = static_cast<__bf16>(v.w);
+    *reinterpret_cast<bf16x4*>(out + row * pieces * width + piece * width + c) = q;
+}
+
 }  // namespace
 }  // namespace koemi
 
 using namespace koemi;
 
 extern "C" int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
-                                  const uint8_t* mask, float* output, int64_t rows, int64_t width, float eps,
-                                  koemi_stream_t stream) {
+                                  const uint8_t* mask, float* output, void* output_bf16, int64_t rows, int64_t width,
+                                  float eps, koemi_stream_t stream) {
     if (rows < 0 || width < 1) return fail(KOEMI_ERR_INVALID, "herm rmsnorm needs rows >= 0 and a positive width");
     if (width % 4 != 0 || width > 4 * kWave * 8)
         return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm needs a width that is a multiple of 4 and at most 2048");
     if (residual != nullptr && residual_dtype != KOEMI_F32 && residual_dtype != KOEMI_BF16 && residual_dtype != KOEMI_F16)
         return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm residual dtype %s", dtype_name(residual_dtype));
     if (rows == 0) return KOEMI_OK;
-    if (!input || !weight || !output) return fail(KOEMI_ERR_INVALID, "herm rmsnorm received a null pointer");
+    if (!input || !weight || (!output && !output_bf16))
+        return fail(KOEMI_ERR_INVALID, "herm rmsnorm received a null pointer");
     const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
     const hipStream_t s = as_stream(stream);
     const int H = static_cast<int>(width);
     auto launch = [&](auto tag) {
         using R = decltype(tag);
         const R* r = static_cast<const R*>(residual);
+        bf16* o16 = static_cast<bf16*>(output_bf16);
         if (width <= 4 * kWave * 4)
-            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 4>), grid, dim3(256), 0, s, input, r, weight, mask, output, rows,
-                               H, eps);
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 4>), grid, dim3(256), 0, s, input, r, weight, mask, output, o16,
+                               rows, H, eps);
         else
-            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 8>), grid, dim3(256), 0, s, input, r, weight, mask, output, rows,
-                               H, eps);
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 8>), grid, dim3(256), 0, s, input, r, weight, mask, output, o16,
+                               rows, H, eps);
     };
     if (residual == nullptr || residual_dtype == KOEMI_F32) launch(float{});
     else if (residual_dtype == KOEMI_BF16) launch(bf16{});
@@ -184,4 +217,25 @@ extern "C" int koemi_herm_local_tail(const float* carried_keys, const float* car
                        dim3(256), 0, as_stream(stream), carried_keys, carried_values, carried_valid, keys, values,
                        valid, out_keys, out_values, out_valid, window, length, width);
     return check_launch("koemi_herm_local_tail");
+}
+
+extern "C" int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2,
+                                      const float* input3, int pieces, int64_t rows, int64_t width, void* output,
+                                      koemi_stream_t stream) {
+    if (pieces < 1 || pieces > 4 || rows < 0 || width < 1)
+        return fail(KOEMI_ERR_INVALID, "concat needs 1 to 4 pieces, rows >= 0 and a positive width");
+    if (width % 4 != 0) return fail(KOEMI_ERR_UNSUPPORTED, "concat needs a width that is a multiple of 4");
+    if (rows == 0) return KOEMI_OK;
+    const float* in[4] = {input0, input1, input2, input3};
+    for (int i = 0; i < pieces; ++i)
+        if (!in[i] || reinterpret_cast<uintptr_t>(in[i]) % 16 != 0)
+            return fail(KOEMI_ERR_INVALID, "concat input %d is null or not 16-byte aligned", i);
+    if (!output || reinterpret_cast<uintptr_t>(output) % 8 != 0)
+        return fail(KOEMI_ERR_INVALID, "concat output is null or not 8-byte aligned");
+    const int64_t threads = rows * pieces * (width / 4);
+    if ((threads + 255) / 256 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "concat grid too large");
+    const ConcatPieces p{{in[0], pieces > 1 ? in[1] : in[0], pieces > 2 ? in[2] : in[0], pieces > 3 ? in[3] : in[0]}};
+    hipLaunchKernelGGL(herm_concat_bf16_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), p, pieces, rows, width, static_cast<bf16*>(output));
+    return check_launch("koemi_herm_concat_bf16");
 }

@@ -200,28 +200,37 @@ def initial_states(settings: HermSettings, batch: int, device: torch.device) -> 
     return states
 
 
-def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor | None = None) -> Tensor:
+def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor | None = None, *,
+         fp32: bool = True, low: torch.dtype | None = None) -> Tensor | tuple[Tensor | None, Tensor | None]:
     """RootMeanSquareNorm.forward (layers.py:14-16) of ``x (+ residual)`` on
     ``koemi_herm_rmsnorm``; with ``mask``, rows whose mask is false keep ``x``
-    (the expert mixture's valid-row select, experts.py:134-136)."""
+    (the expert mixture's valid-row select, experts.py:134-136). With ``low``
+    (bf16) the kernel also writes that copy for a following GEMM and the call
+    returns ``(fp32 or None, copy)``; ``fp32=False`` skips the fp32 output."""
 
     x = x.contiguous()
     width = x.shape[-1]
-    out = torch.empty_like(x)
+    out = torch.empty_like(x) if fp32 or low is None else None
+    out16 = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16) if low == torch.bfloat16 else None
     residual = residual.contiguous() if residual is not None else None
     mask = mask.contiguous() if mask is not None else None
     _native.call(
         "koemi_herm_rmsnorm", _native.ptr(x), _native.ptr(residual) if residual is not None else None,
         _native.dtype_code(residual.dtype) if residual is not None else 0, _native.ptr(weight),
-        _native.ptr(mask) if mask is not None else None, _native.ptr(out), x.numel() // width, width, _EPS,
-        _native.stream_of(x.device),
+        _native.ptr(mask) if mask is not None else None, _native.ptr(out), _native.ptr(out16), x.numel() // width,
+        width, _EPS, _native.stream_of(x.device),
     )
-    return out
+    if low is None:
+        return out
+    if out16 is None:  # no kernel-side copy for this dtype
+        return out, out.to(low)
+    return out, out16
 
 
 def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
     """x W^T + b with fp32 results: one library GEMM (fp32 accumulation, the fp32
-    bias added in its epilogue) for half-precision weights."""
+    bias added in its epilogue) for half-precision weights; ``x`` may already
+    be in the weights' dtype (a copy its producer wrote)."""
 
     if weight.dtype == torch.float32:
         return functional.linear(x, weight, bias)
@@ -317,13 +326,20 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     d = settings.width
     valid = ids != PAD_TOKEN_ID
     source = functional.embedding(ids, p["embedding"]) if context is None else context
-    u = _rms(source, p["input_norm"])
-    ws = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d)
+    lin = settings.linear_dtype
+    low = lin if lin == torch.bfloat16 else None  # kernels write bf16 copies of the GEMM inputs
+    if low is None:
+        u = _rms(source, p["input_norm"])
+    else:
+        u = _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
+                                   with_bf16=low is not None)
+    ws, ws_low = scanned if low is not None else (scanned, scanned)
     prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
     targets = torch.where(valid, ids, 0)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
-    projected = _linear(ws, p["ws_w"], p["ws_b"]).contiguous()
+    projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
     local_keys, local_values = torch.split(projected[..., : 2 * d], [d, d], dim=-1)
     keep = valid.unsqueeze(-1)
     local_keys = torch.where(keep, local_keys, 0.0)
@@ -337,8 +353,15 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     admission = think.admission_above(surprise, valid, settings.salience_threshold)
     salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                local_keys, local_values, admission, ws)
-    fused = _rms(_linear(torch.cat((ws, fast, local_value, salient_value), dim=-1), p["fusion_w"], p["fusion_b"]),
-                 p["fusion_norm"])
+    pieces = (ws, fast, local_value, salient_value)
+    if low is None:
+        fusion_in = torch.cat(pieces, dim=-1)
+    else:
+        fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
+        _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4, batch * length, d,
+                     _native.ptr(fusion_in), _native.stream_of(ids.device))
+    fused_pair = _rms(_linear(fusion_in, p["fusion_w"], p["fusion_b"]), p["fusion_norm"], low=low)
+    fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
     previous, last_token = _token_context(ids, valid, state["last_token"])
     k = settings.top_k
@@ -346,9 +369,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                        validate=False)
     flat = fused.reshape(-1, d)
     flat_valid = valid.reshape(-1)
+    moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
     sorted_context, sorted_rows, sorted_experts, offsets = moe.permute_topk(
-        flat.to(settings.linear_dtype), assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
-        validate=False)
+        moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count, validate=False)
     expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
                                                   p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
     update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k, validate=False)

@@ -171,7 +171,8 @@ def recurrent_scan(
 
 
 def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
-               retention_offset: int = 0, candidate_offset: int | None = None) -> Tensor:
+               retention_offset: int = 0, candidate_offset: int | None = None,
+               with_bf16: bool = False) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
     ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
@@ -180,7 +181,9 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     after the retention columns), as one stacked projection produces them.
     The gates of memory.py:22-26, the masking of network.py:307-309 and the
     scan of network.py:310 from ``initial`` ``[B, width]`` run in one kernel
-    (``koemi_gated_scan``). Returns ``[B, L, width]`` fp32.
+    (``koemi_gated_scan``). Returns ``[B, L, width]`` fp32, and with
+    ``with_bf16`` also its bf16 copy (written by the same kernel) for a
+    following bf16 GEMM.
     """
 
     if candidate_offset is None:
@@ -204,14 +207,14 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
         raise DenseCudaUnavailableError(str(error)) from error
     z = preactivations.contiguous()
     states = torch.empty((batch, length, width), device=z.device, dtype=torch.float32)
-    if states.numel() == 0:
-        return states
-    mask = valid_mask.contiguous() if valid_mask is not None else None
-    _native.call(
-        "koemi_gated_scan",
-        _native.ptr(z), columns, retention_offset, candidate_offset, None, None,
-        _native.ptr(mask) if mask is not None else None,
-        _native.ptr(initial.contiguous()), _native.ptr(states),
-        batch, length, width, _native.stream_of(z.device),
-    )
-    return states
+    states16 = torch.empty(states.shape, device=z.device, dtype=torch.bfloat16) if with_bf16 else None
+    if states.numel():
+        mask = valid_mask.contiguous() if valid_mask is not None else None
+        _native.call(
+            "koemi_gated_scan",
+            _native.ptr(z), columns, retention_offset, candidate_offset, None, None,
+            _native.ptr(mask) if mask is not None else None,
+            _native.ptr(initial.contiguous()), _native.ptr(states), _native.ptr(states16),
+            batch, length, width, _native.stream_of(z.device),
+        )
+    return (states, states16) if with_bf16 else states

@@ -219,3 +219,33 @@ def test_associative_kernel_matches_the_oracle(device, b, length, d, m):
         scale = float(np.abs(ref).max())
         print(f"assoc {name} b={b} L={length} d={d} m={m}: max_abs={err.max():.3e} scale={scale:.3e}", flush=True)
         assert np.all(err <= 1e-4 * np.abs(ref) + 1e-5 * scale), name
+
+
+def test_bf16_copies_written_by_the_kernels_equal_the_casts(device):
+    """The bf16 GEMM inputs the block's kernels write beside their fp32 results
+    (RMSNorm, the gated scan, the fusion concatenation) equal torch's
+    round-to-nearest-even casts of those results bit for bit."""
+
+    from koemi_amd import _native, recurrent
+
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn((37, 1024), generator=g).to(device)
+    w = (1.0 + 0.1 * torch.randn((1024,), generator=g)).to(device)
+    out, out16 = herm._rms(x, w, low=torch.bfloat16)
+    assert out16.dtype == torch.bfloat16 and torch.equal(out16, out.to(torch.bfloat16))
+    only16 = herm._rms(x, w, fp32=False, low=torch.bfloat16)
+    assert only16[0] is None and torch.equal(only16[1], out16)
+
+    for length in (1, 40):
+        z = torch.randn((3, length, 2 * 96), generator=g).to(device)
+        h0 = torch.randn((3, 96), generator=g).to(device)
+        valid = (torch.rand((3, length), generator=g) < 0.7).to(device)
+        states, states16 = recurrent.gated_scan(z, valid, h0, width=96, with_bf16=True)
+        assert torch.equal(states, recurrent.gated_scan(z, valid, h0, width=96))
+        assert torch.equal(states16, states.to(torch.bfloat16))
+
+    pieces = [torch.randn((5, 7, 64), generator=g).to(device) for _ in range(4)]
+    cat16 = torch.empty((5, 7, 256), device=device, dtype=torch.bfloat16)
+    _native.call("koemi_herm_concat_bf16", *(_native.ptr(p) for p in pieces), 4, 35, 64, _native.ptr(cat16),
+                 _native.stream_of(device))
+    assert torch.equal(cat16, torch.cat(pieces, dim=-1).to(torch.bfloat16))
