@@ -335,7 +335,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
                                    with_bf16=low is not None)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
+    # the state before each position: the carried one, then the window's own
+    prior = state["working"].unsqueeze(1) if length == 1 else torch.cat((state["working"].unsqueeze(1), ws[:, :-1]),
+                                                                        dim=1)
     targets = torch.where(valid, ids, 0)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
