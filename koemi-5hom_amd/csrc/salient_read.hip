@@ -244,6 +244,127 @@ __global__ __launch_bounds__(256) void salient_softmax_kernel(
     }
 }
 
+// One-position window (a decode step): the query attends to the carried
+// slots only (window entries before position 0: none), those that are valid
+// and, with a sliding window, not older than `window` entries. One workgroup
+// per (batch row, 1024 columns): each wave scores a quarter of the slots over
+// the whole width (four-element loads, all of a slot's loads in flight before
+// the wave reduction), wave 0 forms the softmax in LDS, then each thread sums
+// its four columns over the slots, eight slots' loads at a time. Needs
+// width % 4 == 0 and aligned rows; otherwise the window kernels run.
+constexpr int kStepMaxSlots = 256;
+
+template <typename T>
+struct Vec4 {
+    __device__ static void load(const T* p, float (&o)[4]) {
+        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
+        const t4 v = *reinterpret_cast<const t4*>(p);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = to_f32(v[c]);
+    }
+    __device__ static void store(T* p, const float (&o)[4]) {
+        typedef __attribute__((__vector_size__(4 * sizeof(T)))) T t4;
+        t4 v;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = from_f32<T>(o[c]);
+        *reinterpret_cast<t4*>(p) = v;
+    }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void read_step_kernel(const T* __restrict__ ck, const T* __restrict__ cv,
+                                                        const uint8_t* __restrict__ cvalid,
+                                                        const T* __restrict__ q, T* __restrict__ out, int S,
+                                                        int64_t D, float inv_sqrt_d, int window) {
+    __shared__ float w_sh[kStepMaxSlots];
+    __shared__ float stat[1];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int low = window > 0 ? S - window : 0;
+    const T* qb = q + b * D;
+    // wave w scores slots w, w + 4, w + 8, w + 12 of each round of 16, all
+    // their loads of a 1024-wide stretch in flight together
+    for (int s0 = wave; s0 < S; s0 += 16) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        int64_t d = lane * 4;
+        for (; d + 3 * 256 < D; d += 4 * 256) {
+            float qv[4][4], kv[4][4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) Vec4<T>::load(qb + d + u * 256, qv[u]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int sl = min(s0 + 4 * j, S - 1);  // past S: a valid row, result unused
+#pragma unroll
+                for (int u = 0; u < 4; ++u) Vec4<T>::load(ck + (b * S + sl) * D + d + u * 256, kv[j][u]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[j] = fmaf(kv[j][u][c], qv[u][c], acc[j]);
+        }
+        for (; d < D; d += 256) {
+            float qv[4];
+            Vec4<T>::load(qb + d, qv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float kv[4];
+                Vec4<T>::load(ck + (b * S + min(s0 + 4 * j, S - 1)) * D + d, kv);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[j] = fmaf(kv[c], qv[c], acc[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float sum = wave_sum_xor(acc[j]);
+            const int sl = s0 + 4 * j;
+            if (lane == 0 && sl < S) w_sh[sl] = (cvalid[b * S + sl] != 0 && sl >= low) ? sum * inv_sqrt_d : -INFINITY;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float m = -INFINITY;
+        for (int sl = lane; sl < S; sl += kWave) m = fmaxf(m, w_sh[sl]);
+        m = wave_max_xor(m);
+        float sum = 0.0f;
+        for (int sl = lane; sl < S; sl += kWave) {
+            const float x = w_sh[sl];
+            const float ex = x == -INFINITY ? 0.0f : expf(x - m);
+            w_sh[sl] = ex;
+            sum += ex;
+        }
+        sum = wave_sum_xor(sum);
+        if (lane == 0) stat[0] = sum > 0.0f ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = stat[0];
+    const int64_t d = static_cast<int64_t>(blockIdx.y) * 1024 + tid * 4;
+    if (d >= D) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const T* vcol = cv + b * S * D + d;
+    int sl = 0;
+    for (; sl + 8 <= S; sl += 8) {
+        float v[8][4];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) Vec4<T>::load(vcol + (sl + u) * D, v[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float wgt = w_sh[sl + u] * inv;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[u][c], acc[c]);
+        }
+    }
+    for (; sl < S; ++sl) {
+        float v[4];
+        Vec4<T>::load(vcol + sl * D, v);
+        const float wgt = w_sh[sl] * inv;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[c], acc[c]);
+    }
+    Vec4<T>::store(out + b * D + d, acc);
+}
+
 // out[b][t][d] = sum over slots s of weight[b][t][s] . [carried_values ; values][b][s][d]
 // for queries [q0, q0 + 32) and columns [d0, d0 + 128): eight waves, two per
 // 32-column slice, each taking half of the 32-slot blocks (the second half's
@@ -448,6 +569,28 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
     const ReadWorkspace ws = read_workspace(batch, carried, length, width, dtype);
     if (!workspace || workspace_bytes < ws.total)
         return fail(KOEMI_ERR_INVALID, "salient read workspace too small: need %zu bytes", ws.total);
+    const size_t step_es = dtype == KOEMI_F32 ? 4 : 2;
+    auto step_aligned = [&](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % (4 * step_es) == 0; };
+    if (length == 1 && carried <= kStepMaxSlots && batch <= 65535 && width % 4 == 0 && step_aligned(carried_keys) &&
+        step_aligned(carried_values) && step_aligned(queries) && step_aligned(out)) {
+        // one position: only carried slots can be eligible
+        const hipStream_t s1 = as_stream(stream);
+        const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+        const int Si = static_cast<int>(carried), win = static_cast<int>(window);
+        auto step = [&](auto tag) {
+            using T = decltype(tag);
+            hipLaunchKernelGGL(read_step_kernel<T>,
+                               dim3(static_cast<unsigned>(batch), static_cast<unsigned>((width + 1023) / 1024)),
+                               dim3(256), 0, s1,
+                               static_cast<const T*>(carried_keys), static_cast<const T*>(carried_values),
+                               carried_valid, static_cast<const T*>(queries), static_cast<T*>(out), Si, width,
+                               inv_sqrt_d, win);
+        };
+        if (dtype == KOEMI_F32) step(float{});
+        else if (dtype == KOEMI_F16) step(f16{});
+        else step(bf16{});
+        return check_launch("koemi_salient_read(one position)");
+    }
     char* base = static_cast<char*>(workspace);
     float* score = reinterpret_cast<float*>(base + ws.score_off);
     void* weight = base + ws.weight_off;

@@ -86,7 +86,10 @@ def _read_case(seed, b, s, length, d, p, dtype):
         (3, 16, 128, 256, 0.5, torch.bfloat16),
         (2, 5, 37, 24, 0.7, torch.float16),
         (2, 0, 20, 8, 0.5, torch.float32),         # empty ring
-        (1, 4, 1, 16, 1.0, torch.float32),         # one query: carried slots only
+        (1, 4, 1, 16, 1.0, torch.float32),         # one query: carried slots only (the one-position kernel)
+        (64, 16, 1, 1024, 0.6, torch.float32),     # a C5 decode step
+        (3, 16, 1, 100, 0.0, torch.bfloat16),      # one position, nothing eligible: zeros
+        (2, 0, 1, 8, 0.5, torch.float32),          # one position, empty ring
         (3, 16, 64, 32, 0.0, torch.bfloat16),      # nothing eligible: zeros
         (1, 16, 984, 48, 0.3, torch.float32),      # 1000 slots (16 per softmax lane)
         (1, 24, 1000, 36, 0.3, torch.float32),     # 1024 slots: the largest of the HIP kernels
@@ -137,6 +140,8 @@ def test_read_salient_window_rejects_bad_inputs(device):
         (3, 5, 33, 20, 1, 0.6, torch.bfloat16),      # window of one entry
         (1, 16, 1100, 40, 24, 0.9, torch.float32),   # 1116 slots: the rocBLAS path
         (2, 0, 17, 8, 4, 0.5, torch.float16),        # empty ring
+        (64, 16, 1, 1024, 16, 0.7, torch.float32),   # a C5 decode step (one-position kernel)
+        (3, 20, 1, 72, 6, 0.8, torch.float16),       # one position: only the newest `window` ring slots
     ],
 )
 def test_read_local_window_matches_oracle(device, b, s, length, d, window, p, dtype):
