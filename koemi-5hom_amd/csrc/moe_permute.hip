@@ -319,11 +319,85 @@ __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __re
     }
 }
 
+// Index phase of a small permutation (a decode step's pairs) in one
+// workgroup: wave w keys pairs [64 w, 64 w + 64), counts each key's lanes with
+// ballots (rank = earlier lanes with the same key), the waves' counts meet in
+// LDS, and every pair's destination is
+//   offset[key] + (same-key pairs of earlier waves) + rank,
+// the same stable order as the chunked kernels.
+constexpr int kSmallPairs = 1024;
+constexpr int kSmallKeys = 64;  // E + 1
+
+template <typename I>
+__global__ __launch_bounds__(kSmallPairs) void permute_small_kernel(
+    const I* __restrict__ a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
+    int64_t* __restrict__ sorted_rows, int64_t* __restrict__ sorted_experts, int64_t* __restrict__ offsets,
+    float* __restrict__ sorted_w, int64_t* __restrict__ dest, int64_t pairs, int64_t k, int64_t E) {
+    __shared__ int32_t wcount[kSmallPairs / kWave][kSmallKeys];
+    __shared__ int32_t key_off[kSmallKeys];
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int nkeys = static_cast<int>(E) + 1;
+    for (int i = tid; i < (kSmallPairs / kWave) * kSmallKeys; i += kSmallPairs) (&wcount[0][0])[i] = 0;
+    __syncthreads();
+    const int64_t g = static_cast<int64_t>(wave) * kWave;
+    int32_t key = -1;
+    uint64_t peers = 0;
+    if (g < pairs) {  // wave-uniform
+        key = group_key(a, valid, g, pairs, k, E);
+        const bool active = key >= 0;
+        uint64_t remaining = __ballot(active);
+        while (remaining) {
+            const int leader = __ffsll(static_cast<unsigned long long>(remaining)) - 1;
+            const int32_t lkey = __shfl(key, leader, kWave);
+            const uint64_t same = __ballot(active && key == lkey);
+            if (active && key == lkey) peers = same;
+            remaining &= ~same;
+        }
+        if (active && __popcll(peers & lanemask_lt()) == 0) wcount[wave][key] = __popcll(peers);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // per key: the count of the earlier waves (in place), then the keys' exclusive offsets
+        int32_t total = 0;
+        if (lane < nkeys) {
+            for (int w = 0; w < kSmallPairs / kWave; ++w) {
+                const int32_t c = wcount[w][lane];
+                wcount[w][lane] = total;
+                total += c;
+            }
+        }
+        int32_t incl = total;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int32_t up = __shfl_up(incl, off, kWave);
+            if (lane >= off) incl += up;
+        }
+        if (lane < nkeys) {
+            key_off[lane] = incl - total;
+            offsets[lane] = incl - total;
+        }
+    }
+    __syncthreads();
+    if (key >= 0) {
+        const int64_t p = g + lane;
+        const int64_t d = static_cast<int64_t>(key_off[key]) + wcount[wave][key] + __popcll(peers & lanemask_lt());
+        sorted_rows[d] = p / k;
+        sorted_experts[d] = key;
+        if (sorted_w) sorted_w[d] = (key < E) ? pair_w[p] : 0.0f;
+        dest[p] = d;
+    }
+}
+
 template <typename I>
 int run_index_phase(const void* assignments, const uint8_t* valid, const float* pair_w, int64_t* sorted_rows,
                     int64_t* sorted_experts, int64_t* offsets, float* sorted_w, int32_t* counts, int64_t* dest,
                     int64_t pairs, int64_t k, int64_t E, hipStream_t s) {
     const I* a = static_cast<const I*>(assignments);
+    if (pairs <= kSmallPairs && E + 1 <= kSmallKeys) {
+        hipLaunchKernelGGL(permute_small_kernel<I>, dim3(1), dim3(kSmallPairs), 0, s, a, valid, pair_w, sorted_rows,
+                           sorted_experts, offsets, sorted_w, dest, pairs, k, E);
+        return check_launch("koemi_moe_permute(small)");
+    }
     const int64_t chunks = num_chunks(pairs);
     const size_t hist_bytes = static_cast<size_t>(E + 1) * sizeof(int32_t);
     hipLaunchKernelGGL(permute_count_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,

@@ -109,7 +109,10 @@ def test_permute_known_answer(device):
     "dtype, T, k, E",
     [(torch.float32, 5000, 3, 13), (torch.bfloat16, 5000, 3, 13), (torch.float16, 5000, 3, 13),
      # count tables too large to stage in LDS (and E + 1 > 1024): the global-memory scan
-     (torch.bfloat16, 3000, 2, 1500), (torch.float32, 40000, 2, 24)],
+     (torch.bfloat16, 3000, 2, 1500), (torch.float32, 40000, 2, 24),
+     # at most 1024 pairs and 64 keys: the one-workgroup index phase (a decode step: 64 tokens x top-2)
+     (torch.bfloat16, 64, 2, 16), (torch.float32, 341, 3, 13), (torch.float16, 1024, 1, 63), (torch.float32, 1, 2, 2),
+     (torch.bfloat16, 512, 2, 64)],
 )
 def test_permute_random_with_invalid_and_repeats(device, dtype, T, k, E):
     g = torch.Generator().manual_seed(71)
