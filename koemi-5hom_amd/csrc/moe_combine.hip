@@ -28,6 +28,27 @@ __global__ void zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
     if (i < n) p[i] = 0;
 }
 
+// Steps 1 for a small combine (a decode step) in one workgroup: the
+// per-token counters live in LDS, so no separate zero-fill runs.
+constexpr int kSmallInvertTokens = 8192;
+__global__ __launch_bounds__(1024) void invert_rows_small_kernel(const int64_t* __restrict__ sorted_rows,
+                                                                 const int64_t* __restrict__ valid_end,
+                                                                 int32_t* __restrict__ cnt, int64_t* __restrict__ pos,
+                                                                 int64_t pairs, int64_t tokens, int64_t k) {
+    __shared__ int32_t c_sh[kSmallInvertTokens];
+    for (int64_t t = threadIdx.x; t < tokens; t += 1024) c_sh[t] = 0;
+    __syncthreads();
+    const int64_t valid = min(*valid_end, pairs);
+    for (int64_t i = threadIdx.x; i < valid; i += 1024) {
+        const int64_t t = sorted_rows[i];
+        if (t < 0 || t >= tokens) continue;
+        const int32_t slot = atomicAdd(&c_sh[t], 1);
+        if (slot < k) pos[t * k + slot] = i;
+    }
+    __syncthreads();
+    for (int64_t t = threadIdx.x; t < tokens; t += 1024) cnt[t] = c_sh[t];
+}
+
 __global__ void invert_rows_kernel(const int64_t* __restrict__ sorted_rows, const int64_t* __restrict__ valid_end,
                                    int32_t* __restrict__ cnt, int64_t* __restrict__ pos, int64_t pairs, int64_t tokens,
                                    int64_t k) {
@@ -279,14 +300,22 @@ extern "C" int koemi_moe_combine(const void* expert_outputs, const int64_t* sort
     int32_t* cnt = reinterpret_cast<int32_t*>(base + ws.cnt_off);
     int64_t* pos = reinterpret_cast<int64_t*>(base + ws.pos_off);
     hipStream_t s = as_stream(stream);
-    hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(tokens, 256)), dim3(256), 0, s, cnt, tokens);
-    int st = check_launch("koemi_moe_combine(zero)");
-    if (st != KOEMI_OK) return st;
-    if (pairs > 0) {
-        hipLaunchKernelGGL(invert_rows_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, s, sorted_rows,
+    int st = KOEMI_OK;
+    if (tokens <= kSmallInvertTokens && pairs <= 4096) {
+        hipLaunchKernelGGL(invert_rows_small_kernel, dim3(1), dim3(1024), 0, s, sorted_rows,
                            segment_offsets + num_segments, cnt, pos, pairs, tokens, top_k);
         st = check_launch("koemi_moe_combine(invert)");
         if (st != KOEMI_OK) return st;
+    } else {
+        hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(tokens, 256)), dim3(256), 0, s, cnt, tokens);
+        st = check_launch("koemi_moe_combine(zero)");
+        if (st != KOEMI_OK) return st;
+        if (pairs > 0) {
+            hipLaunchKernelGGL(invert_rows_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, s, sorted_rows,
+                               segment_offsets + num_segments, cnt, pos, pairs, tokens, top_k);
+            st = check_launch("koemi_moe_combine(invert)");
+            if (st != KOEMI_OK) return st;
+        }
     }
     switch (dtype) {
         case KOEMI_F32: return launch_combine_rows<float>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);

@@ -269,3 +269,24 @@ def test_config4_pipeline(device, learned):
     want_out = oracle.combine(y.float().cpu().numpy(), rows.cpu().numpy(), off, c.context.shape[0], 2,
                               None if sw is None else sw.cpu().numpy())
     np.testing.assert_array_equal(out.cpu().view(torch.int16).numpy(), oracle.f32_to_bf16(want_out).view(np.int16))
+
+
+@pytest.mark.parametrize("tokens, k, E, learned", [(64, 2, 16, False), (300, 3, 13, True), (1, 2, 4, False)])
+def test_small_combine_bit_exact(device, tokens, k, E, learned):
+    """A decode-sized combine (the one-workgroup inversion) against the oracle's
+    ascending-order fp32 sums, with and without pair weights."""
+    g = torch.Generator().manual_seed(tokens + k)
+    D = 96
+    a = torch.randint(-1, E + 1, (tokens, k), generator=g)
+    valid = torch.rand((tokens,), generator=g) > 0.2
+    ctx = torch.randn((tokens, D), generator=g).to(torch.bfloat16)
+    w = torch.rand((tokens, k), generator=g) if learned else None
+    perm = moe.permute_topk(ctx.to(device), a.to(device), valid.to(device), expert_count=E,
+                            pair_weights=w.to(device) if w is not None else None, validate=False)
+    sc, rows, offsets = perm[0], perm[1], perm[3]
+    sw = perm[4] if w is not None else None
+    y = (sc.float() * 1.5 + 0.25).to(torch.bfloat16)  # stand-in expert outputs
+    out = moe.combine_topk(y, rows, offsets, token_count=tokens, top_k=k, pair_weights=sw)
+    want = oracle.combine(y.float().cpu().numpy(), rows.cpu().numpy(), offsets.cpu().numpy(), tokens, k,
+                          pair_weights=sw.cpu().numpy() if sw is not None else None)
+    np.testing.assert_array_equal(out.cpu().view(torch.int16).numpy(), oracle.f32_to_bf16(want).view(np.int16))
