@@ -321,7 +321,10 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
  * GEMM, and `output` may then be NULL.
  * koemi_herm_token_context: previous[b, t] = the last valid token before t
  * (carried_last[b] before the first), last[b] = the window's last valid token
- * or carried_last[b] (network.py:742-761); int64 ids, valid bytes.
+ * or carried_last[b] (network.py:742-761); int64 ids, valid bytes. With
+ * `valid` NULL the validity is ids != pad_id (network.py:303) and is written
+ * to `valid_out`; `targets_out` (NULL: none) receives ids where valid and 0
+ * elsewhere (the surprise targets, network.py:335).
  * koemi_herm_local_tail: the local ring after a window, the last `window`
  * entries of [carried (window entries) ; new (length entries)] with their
  * valid bytes (memory.py:385-403); fp32 keys and values [batch, *, width]. */
@@ -329,7 +332,8 @@ int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dt
                        const uint8_t* mask, float* output, void* output_bf16, int64_t rows, int64_t width, float eps,
                        koemi_stream_t stream);
 int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
-                             int64_t* previous, int64_t* last, int64_t batch, int64_t length, koemi_stream_t stream);
+                             int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out, int64_t pad_id,
+                             int64_t batch, int64_t length, koemi_stream_t stream);
 int koemi_herm_local_tail(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
                           const float* keys, const float* values, const uint8_t* valid, float* out_keys,
                           float* out_values, uint8_t* out_valid, int64_t batch, int64_t window, int64_t length,

@@ -77,18 +77,31 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restri
 // One workgroup per row: position t takes the latest valid index before it,
 // an exclusive max-scan of (valid ? t : -1) over 256-position chunks (a wave
 // scan, the wave maxima through LDS, the chunk's carry in a register).
+// With `valid` null the validity is ids != pad_id, written to valid_out, and
+// targets_out (if given) gets ids where valid, 0 elsewhere (network.py:335,
+// the surprise targets).
 __global__ __launch_bounds__(256) void herm_token_context_kernel(const int64_t* __restrict__ ids,
                                                                  const uint8_t* __restrict__ valid,
                                                                  const int64_t* __restrict__ carried,
                                                                  int64_t* __restrict__ previous,
-                                                                 int64_t* __restrict__ last, int64_t L) {
+                                                                 int64_t* __restrict__ last,
+                                                                 uint8_t* __restrict__ valid_out,
+                                                                 int64_t* __restrict__ targets_out, int64_t pad_id,
+                                                                 int64_t L) {
     __shared__ int wave_max[4];
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     int carry = -1;  // latest valid index before the chunk
     for (int64_t c0 = 0; c0 < L; c0 += 256) {
         const int64_t t = c0 + tid;
-        const int mine = (t < L && valid[b * L + t]) ? static_cast<int>(t) : -1;
+        bool ok = false;
+        if (t < L) {
+            const int64_t id = ids[b * L + t];
+            ok = valid != nullptr ? valid[b * L + t] != 0 : id != pad_id;
+            if (valid_out != nullptr) valid_out[b * L + t] = ok ? 1 : 0;
+            if (targets_out != nullptr) targets_out[b * L + t] = ok ? id : 0;
+        }
+        const int mine = ok ? static_cast<int>(t) : -1;
         int incl = mine;
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
@@ -189,15 +202,15 @@ extern "C" int koemi_herm_rmsnorm(const float* input, const void* residual, int 
 }
 
 extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
-                                        int64_t* previous, int64_t* last, int64_t batch, int64_t length,
-                                        koemi_stream_t stream) {
+                                        int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out,
+                                        int64_t pad_id, int64_t batch, int64_t length, koemi_stream_t stream) {
     if (batch < 0 || length < 0) return fail(KOEMI_ERR_INVALID, "token context needs non-negative sizes");
     if (batch == 0) return KOEMI_OK;
-    if (!token_ids || !valid || !carried_last || !previous || !last)
+    if (!token_ids || !carried_last || !previous || !last || (!valid && !valid_out))
         return fail(KOEMI_ERR_INVALID, "token context received a null pointer");
     if (batch > 0x7fffffffLL || length > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "token context sizes too large");
     hipLaunchKernelGGL(herm_token_context_kernel, dim3(static_cast<unsigned>(batch)), dim3(256), 0, as_stream(stream),
-                       token_ids, valid, carried_last, previous, last, length);
+                       token_ids, valid, carried_last, previous, last, valid_out, targets_out, pad_id, length);
     return check_launch("koemi_herm_token_context");
 }
 

@@ -249,16 +249,24 @@ def _few_rows(x: Tensor, weight: Tensor) -> bool:
             and x.shape[-1] % 64 == 0 and x.shape[-1] <= 1024 and x.dtype in (torch.float32, torch.bfloat16))
 
 
-def _token_context(ids: Tensor, valid: Tensor, carried: Tensor) -> tuple[Tensor, Tensor]:
+def _token_context(ids: Tensor, valid: Tensor | None, carried: Tensor
+                   ) -> tuple[Tensor, Tensor] | tuple[Tensor, Tensor, Tensor, Tensor]:
     """The previous valid token of each position and the last valid token of
-    each row (network.py:742-761) on ``koemi_herm_token_context``."""
+    each row (network.py:742-761) on ``koemi_herm_token_context``. With
+    ``valid`` None the kernel also forms the validity ``ids != PAD`` and the
+    surprise targets (ids, 0 where invalid) and the call returns
+    ``(previous, last, valid, targets)``."""
 
     batch, length = ids.shape
     previous = torch.empty_like(ids)
     last = torch.empty_like(carried)
+    formed = valid is None
+    valid_out = torch.empty(ids.shape, device=ids.device, dtype=torch.bool) if formed else None
+    targets = torch.empty_like(ids) if formed else None
     _native.call("koemi_herm_token_context", _native.ptr(ids), _native.ptr(valid), _native.ptr(carried),
-                 _native.ptr(previous), _native.ptr(last), batch, length, _native.stream_of(ids.device))
-    return previous, last
+                 _native.ptr(previous), _native.ptr(last), _native.ptr(valid_out), _native.ptr(targets), PAD_TOKEN_ID,
+                 batch, length, _native.stream_of(ids.device))
+    return (previous, last, valid_out, targets) if formed else (previous, last)
 
 
 def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: Tensor,
@@ -324,7 +332,8 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     ids = ids.contiguous()
     batch, length = ids.shape
     d = settings.width
-    valid = ids != PAD_TOKEN_ID
+    # validity, surprise targets and the routing context of every position in one kernel
+    previous, last_token, valid, targets = _token_context(ids, None, state["last_token"])
     source = functional.embedding(ids, p["embedding"]) if context is None else context
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None  # kernels write bf16 copies of the GEMM inputs
@@ -338,7 +347,6 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     # the state before each position: the carried one, then the window's own
     prior = state["working"].unsqueeze(1) if length == 1 else torch.cat((state["working"].unsqueeze(1), ws[:, :-1]),
                                                                         dim=1)
-    targets = torch.where(valid, ids, 0)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
     projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
@@ -365,7 +373,6 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     fused_pair = _rms(_linear(fusion_in, p["fusion_w"], p["fusion_b"]), p["fusion_norm"], low=low)
     fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
-    previous, last_token = _token_context(ids, valid, state["last_token"])
     k = settings.top_k
     assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
                                        validate=False)

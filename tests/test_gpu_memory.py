@@ -181,3 +181,10 @@ def test_token_context_matches_the_oracle(device, b, length, p):
     np.testing.assert_array_equal(previous.cpu().numpy(), want)
     want_last = np.array([ids[r][valid[r]][-1].item() if valid[r].any() else carried[r].item() for r in range(b)])
     np.testing.assert_array_equal(last.cpu().numpy(), want_last)
+    # the same kernel forming the validity from the padding id, and the surprise targets
+    padded = torch.where(valid, ids, torch.full_like(ids, herm.PAD_TOKEN_ID))
+    previous2, last2, valid2, targets = herm._token_context(padded.to(device), None, carried.to(device))
+    np.testing.assert_array_equal(valid2.cpu().numpy(), valid.numpy())
+    np.testing.assert_array_equal(targets.cpu().numpy(), np.where(valid.numpy(), ids.numpy(), 0))
+    np.testing.assert_array_equal(previous2.cpu().numpy(), want)
+    np.testing.assert_array_equal(last2.cpu().numpy(), want_last)
