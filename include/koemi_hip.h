@@ -343,6 +343,13 @@ int koemi_herm_local_tail(const float* carried_keys, const float* carried_values
  * (network.py:401-405, a torch.cat in the reference) as one bf16 matrix
  * [rows, pieces * width] for its GEMM: `pieces` (1..4) fp32 [rows, width]
  * blocks (16-byte aligned), width % 4 == 0, rounded to nearest even. */
+/* The local keys and values of a window (network.py:337-340: the first two
+ * width-column blocks of the stacked working-state projection, rows of
+ * invalid positions zeroed, a torch.where each in the reference) as two
+ * contiguous fp32 [rows, width] blocks in one kernel; width and row_stride
+ * multiples of 4, 16-byte aligned pointers. */
+int koemi_herm_masked_pair(const float* source, int64_t row_stride, const uint8_t* valid, float* out0, float* out1,
+                           int64_t rows, int64_t width, koemi_stream_t stream);
 int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2, const float* input3,
                            int pieces, int64_t rows, int64_t width, void* output, koemi_stream_t stream);
 

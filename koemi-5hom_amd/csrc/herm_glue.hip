@@ -143,6 +143,25 @@ __global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float
     if (threadIdx.x == 0) ovalid[b * W + s] = carried_entry ? cvalid[b * W + i] : valid[b * L + (i - W)];
 }
 
+// out0 = the first `width` columns of each row, out1 the next `width`, rows
+// whose valid byte is 0 zeroed (the local keys and values of network.py:
+// 337-340 cut from the stacked projection); four columns per thread.
+__global__ __launch_bounds__(256) void herm_masked_pair_kernel(const float* __restrict__ src, int64_t stride,
+                                                               const uint8_t* __restrict__ valid,
+                                                               float* __restrict__ out0, float* __restrict__ out1,
+                                                               int64_t rows, int64_t width) {
+    const int64_t quads = width / 4;
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= rows * 2 * quads) return;
+    const int64_t row = i / (2 * quads);
+    const int64_t rest = i - row * 2 * quads;
+    const int which = rest >= quads ? 1 : 0;
+    const int64_t c = (rest - which * quads) * 4;
+    float4 v = *reinterpret_cast<const float4*>(src + row * stride + which * width + c);
+    if (valid[row] == 0) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    *reinterpret_cast<float4*>((which ? out1 : out0) + row * width + c) = v;
+}
+
 // [rows, pieces * width] bf16 from `pieces` fp32 [rows, width] blocks; a thread
 // converts four consecutive values (16-byte load, 8-byte store).
 struct ConcatPieces {
@@ -251,4 +270,21 @@ extern "C" int koemi_herm_concat_bf16(const float* input0, const float* input1, 
     hipLaunchKernelGGL(herm_concat_bf16_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                        as_stream(stream), p, pieces, rows, width, static_cast<bf16*>(output));
     return check_launch("koemi_herm_concat_bf16");
+}
+
+extern "C" int koemi_herm_masked_pair(const float* source, int64_t row_stride, const uint8_t* valid, float* out0,
+                                      float* out1, int64_t rows, int64_t width, koemi_stream_t stream) {
+    if (rows < 0 || width < 1 || row_stride < 2 * width)
+        return fail(KOEMI_ERR_INVALID, "masked pair needs rows >= 0, a positive width and row_stride >= 2 width");
+    if (width % 4 != 0 || row_stride % 4 != 0)
+        return fail(KOEMI_ERR_UNSUPPORTED, "masked pair needs width and row_stride multiples of 4");
+    if (rows == 0) return KOEMI_OK;
+    if (!source || !valid || !out0 || !out1 || reinterpret_cast<uintptr_t>(source) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(out0) % 16 != 0 || reinterpret_cast<uintptr_t>(out1) % 16 != 0)
+        return fail(KOEMI_ERR_INVALID, "masked pair received a null or unaligned pointer");
+    const int64_t threads = rows * 2 * (width / 4);
+    if ((threads + 255) / 256 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "masked pair grid too large");
+    hipLaunchKernelGGL(herm_masked_pair_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), source, row_stride, valid, out0, out1, rows, width);
+    return check_launch("koemi_herm_masked_pair");
 }

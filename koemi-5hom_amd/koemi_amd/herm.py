@@ -163,8 +163,13 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         fq_b = f64("feature_w") @ f64("query_b") + f64("feature_b")
         weights = [p["local_key_w"], p["local_value_w"], p["value_w"], fk_w, fq_w, p["decay_w"], p["write_w"]]
         biases = [p["local_key_b"], p["local_value_b"], p["value_b"], fk_b, fq_b, p["decay_b"], p["write_b"]]
-        q["ws_w"] = to(torch.cat([w.double() for w in weights]), lin)
-        q["ws_b"] = to(torch.cat([b.double() for b in biases]))
+        # rows padded to a multiple of 4 (zero weights and biases) so every row of
+        # the projection starts 16-byte aligned for the kernels that read it
+        ws_w = torch.cat([w.double() for w in weights])
+        ws_b = torch.cat([b.double() for b in biases])
+        pad = -ws_w.shape[0] % 4
+        q["ws_w"] = to(torch.cat((ws_w, ws_w.new_zeros((pad, ws_w.shape[1])))), lin)
+        q["ws_b"] = to(torch.cat((ws_b, ws_b.new_zeros(pad))))
         q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"])
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
@@ -293,10 +298,11 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     projection tail, fast write terms with the write masking and
     scan_and_read (memory.py:82-144, 244-255; network.py:734-740).
 
-    ``projections`` fp32 ``[B, L, 3 D + 2 M + 2]``, the stacked working-state
-    projection: local key, local value and value pre-activations (D columns
-    each), the feature logits of the key and of the query (M each; W_f W_k and
-    W_f W_q folded into the projection) and the decay and write logits.
+    ``projections`` fp32 ``[B, L, C]``, C >= 3 D + 2 M + 2, the stacked
+    working-state projection: local key, local value and value pre-activations
+    (D columns each), the feature logits of the key and of the query (M each;
+    W_f W_k and W_f W_q folded into the projection) and the decay and write
+    logits; columns past those (row padding) are not read.
     ``surprise`` ``[B, L]`` fp32, ``valid`` ``[B, L]`` bool, ``basis``
     ``[B, D, M]``, ``normalizer`` ``[B, M]`` fp32. Returns (reads ``[B, L, D]``,
     next basis, next normalizer).
@@ -304,8 +310,8 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
 
     batch, length, stride = projections.shape
     d, m = width, features
-    if stride != 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
-        raise ValueError("projections must be contiguous fp32 [batch, length, 3 * width + 2 * features + 2]")
+    if stride < 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
+        raise ValueError("projections must be contiguous fp32 [batch, length, >= 3 * width + 2 * features + 2]")
     read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
@@ -350,10 +356,11 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
     projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
-    local_keys, local_values = torch.split(projected[..., : 2 * d], [d, d], dim=-1)
-    keep = valid.unsqueeze(-1)
-    local_keys = torch.where(keep, local_keys, 0.0)
-    local_values = torch.where(keep, local_values, 0.0)
+    # local keys and values: the first two column blocks, invalid rows zeroed (one kernel)
+    local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
+    local_values = torch.empty_like(local_keys)
+    _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
+                 _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
     local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
                                            local_keys, local_values, valid, ws, window=settings.local_memory_size)
 
