@@ -326,35 +326,32 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x;
     const float* row = proj + b * stride;
-    if (tid == 0) {
-        float zk[MAXM], zq[MAXM], mk = -INFINITY, mq = -INFINITY;
+    if (tid < kWave) {
+        // lanes 0..31: the key's feature softmax, lanes 32..63: the query's
+        // (one feature per lane; max and sum by shuffles within each half)
+        const int lane = tid, m = lane & 31;
+        const bool query = lane >= 32, in = m < M;
+        const float z = in ? row[(query ? fq_off : fk_off) + min(m, M - 1)] : -INFINITY;
+        float mx = z;
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            zk[m] = m < M ? row[fk_off + m] : -INFINITY;
-            zq[m] = m < M ? row[fq_off + m] : -INFINITY;
-            mk = fmaxf(mk, zk[m]);
-            mq = fmaxf(mq, zq[m]);
-        }
-        float sk = 0.0f, sq = 0.0f;
+        for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        const float e = in ? expf(z - mx) : 0.0f;
+        float sum = e;
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            zk[m] = m < M ? expf(zk[m] - mk) : 0.0f;
-            zq[m] = m < M ? expf(zq[m] - mq) : 0.0f;
-            sk += zk[m];
-            sq += zq[m];
-        }
-        float nq = 0.0f;
+        for (int off = 16; off > 0; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+        const float f = e / sum;
+        if (m < MAXM) (query ? q_sh : f_sh)[m] = f;  // zero past M
+        // normalizer . query features over the query half
+        float nq = (query && in) ? normalizer[b * M + m] * f : 0.0f;
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            f_sh[m] = zk[m] / sk;
-            q_sh[m] = zq[m] / sq;
-            if (m < M) nq = fmaf(normalizer[b * M + m], q_sh[m], nq);
+        for (int off = 16; off > 0; off >>= 1) nq += __shfl_xor(nq, off, kWave);
+        if (lane == 32) gate[2] = nq;
+        if (lane == 0) {
+            const bool ok = valid[b] != 0;
+            const float sv = fminf(fmaxf(surprise[b], 0.0f), 1.0f);
+            gate[0] = ok ? kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]) : 1.0f;
+            gate[1] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
         }
-        const bool ok = valid[b] != 0;
-        const float sv = fminf(fmaxf(surprise[b], 0.0f), 1.0f);
-        gate[0] = ok ? kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]) : 1.0f;
-        gate[1] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
-        gate[2] = nq;
     }
     __syncthreads();
     const float decay = gate[0], w = gate[1], dn = gate[2];

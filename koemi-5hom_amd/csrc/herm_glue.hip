@@ -136,9 +136,19 @@ __global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float
     const float* vs = carried_entry ? cv + (b * W + i) * D : v + (b * L + (i - W)) * D;
     float* kd = ok + (b * W + s) * D;
     float* vd = ov + (b * W + s) * D;
-    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-        kd[d] = ks[d];
-        vd[d] = vs[d];
+    if (D % 4 == 0 && reinterpret_cast<uintptr_t>(ks) % 16 == 0 && reinterpret_cast<uintptr_t>(vs) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(kd) % 16 == 0 && reinterpret_cast<uintptr_t>(vd) % 16 == 0) {
+        for (int64_t d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {  // 16-byte copies
+            const float4 kq = *reinterpret_cast<const float4*>(ks + d);
+            const float4 vq = *reinterpret_cast<const float4*>(vs + d);
+            *reinterpret_cast<float4*>(kd + d) = kq;
+            *reinterpret_cast<float4*>(vd + d) = vq;
+        }
+    } else {
+        for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+            kd[d] = ks[d];
+            vd[d] = vs[d];
+        }
     }
     if (threadIdx.x == 0) ovalid[b * W + s] = carried_entry ? cvalid[b * W + i] : valid[b * L + (i - W)];
 }
