@@ -212,6 +212,19 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
                        void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
                        int64_t width, int64_t capacity, int dtype, koemi_stream_t stream);
 
+/* The local and the salient read of a one-position window (a decode step,
+ * network.py:337-358: LocalKeyValueMemory.read_window and
+ * read_salient_window with one query) in one launch: each query [batch, width]
+ * attends, with scores key . query / sqrt(width), to the valid carried slots
+ * of each ring (for the local ring only the newest `window` slots), zero
+ * output when none is eligible. fp32, width % 4 == 0, at most 256 slots per
+ * ring, 16-byte aligned rows. Results equal koemi_local_read and
+ * koemi_salient_read with length 1. */
+int koemi_read_step_pair(const float* local_keys, const float* local_values, const uint8_t* local_valid,
+                         int64_t local_slots, int64_t window, const float* salient_keys, const float* salient_values,
+                         const uint8_t* salient_valid, int64_t salient_slots, const float* queries, float* local_out,
+                         float* salient_out, int64_t batch, int64_t width, koemi_stream_t stream);
+
 /* Bounded recurrent gates, BoundedRecurrentState.gates of model/memory.py:14-30
  * with the masking of network.py:306-309 (a torch composite in the
  * reference): for input rows u (rows x width, `dtype`),

@@ -271,11 +271,42 @@ struct Vec4 {
     }
 };
 
+// One memory of a one-position read; blockIdx.z picks one of two (the HERM
+// block's local and salient reads of the same query in one launch).
+template <typename T>
+struct StepMemory {
+    const T* ck;
+    const T* cv;
+    const uint8_t* cvalid;
+    T* out;
+    int S;
+    int window;
+};
+
+template <typename T>
+__device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
+                               const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
+                               int window);
+
 template <typename T>
 __global__ __launch_bounds__(256) void read_step_kernel(const T* __restrict__ ck, const T* __restrict__ cv,
                                                         const uint8_t* __restrict__ cvalid,
                                                         const T* __restrict__ q, T* __restrict__ out, int S,
                                                         int64_t D, float inv_sqrt_d, int window) {
+    read_step_body<T>(ck, cv, cvalid, q, out, S, D, inv_sqrt_d, window);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void read_step_pair_kernel(StepMemory<T> m0, StepMemory<T> m1,
+                                                             const T* __restrict__ q, int64_t D, float inv_sqrt_d) {
+    const StepMemory<T>& m = blockIdx.z == 0 ? m0 : m1;
+    read_step_body<T>(m.ck, m.cv, m.cvalid, q, m.out, m.S, D, inv_sqrt_d, m.window);
+}
+
+template <typename T>
+__device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
+                               const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
+                               int window) {
     __shared__ float w_sh[kStepMaxSlots];
     __shared__ float stat[1];
     const int64_t b = blockIdx.x;
@@ -761,4 +792,34 @@ extern "C" int koemi_local_read(const void* carried_keys, const void* carried_va
     if (window < 1) return fail(KOEMI_ERR_INVALID, "local read needs a positive window");
     return memory_read(carried_keys, carried_values, carried_valid, keys, values, valid, queries, out, batch, carried,
                        length, width, window, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int koemi_read_step_pair(const float* local_keys, const float* local_values, const uint8_t* local_valid,
+                                    int64_t local_slots, int64_t window, const float* salient_keys,
+                                    const float* salient_values, const uint8_t* salient_valid, int64_t salient_slots,
+                                    const float* queries, float* local_out, float* salient_out, int64_t batch,
+                                    int64_t width, koemi_stream_t stream) {
+    if (batch < 0 || width < 1 || local_slots < 0 || salient_slots < 0 || window < 1)
+        return fail(KOEMI_ERR_INVALID, "read step pair needs non-negative sizes, a positive width and window");
+    if (local_slots > kStepMaxSlots || salient_slots > kStepMaxSlots || width % 4 != 0 || batch > 65535 ||
+        window > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "read step pair needs at most %d slots, width %% 4 == 0 and batch <= 65535",
+                    kStepMaxSlots);
+    if (batch == 0) return KOEMI_OK;
+    auto aligned = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (!queries || !local_out || !salient_out || (local_slots > 0 && (!local_keys || !local_values || !local_valid)) ||
+        (salient_slots > 0 && (!salient_keys || !salient_values || !salient_valid)))
+        return fail(KOEMI_ERR_INVALID, "read step pair received a null pointer");
+    if (!aligned(local_keys) || !aligned(local_values) || !aligned(salient_keys) || !aligned(salient_values) ||
+        !aligned(queries) || !aligned(local_out) || !aligned(salient_out))
+        return fail(KOEMI_ERR_INVALID, "read step pair needs 16-byte aligned rows");
+    const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+    const StepMemory<float> m0{local_keys, local_values, local_valid, local_out, static_cast<int>(local_slots),
+                               static_cast<int>(window)};
+    const StepMemory<float> m1{salient_keys, salient_values, salient_valid, salient_out,
+                               static_cast<int>(salient_slots), 0};
+    hipLaunchKernelGGL(read_step_pair_kernel<float>,
+                       dim3(static_cast<unsigned>(batch), static_cast<unsigned>((width + 1023) / 1024), 2),
+                       dim3(256), 0, as_stream(stream), m0, m1, queries, width, inv_sqrt_d);
+    return check_launch("koemi_read_step_pair");
 }

@@ -361,15 +361,26 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     local_values = torch.empty_like(local_keys)
     _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
                  _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
-    local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
-                                           local_keys, local_values, valid, ws, window=settings.local_memory_size)
+    if length == 1:
+        # a decode step: only the carried slots are eligible, both reads in one launch
+        local_value = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
+        salient_value = torch.empty_like(local_value)
+        _native.call("koemi_read_step_pair", _native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
+                     _native.ptr(state["local_valid"]), state["local_keys"].shape[1], settings.local_memory_size,
+                     _native.ptr(state["salient_keys"]), _native.ptr(state["salient_values"]),
+                     _native.ptr(state["salient_valid"]), state["salient_keys"].shape[1], _native.ptr(ws),
+                     _native.ptr(local_value), _native.ptr(salient_value), batch, d, _native.stream_of(ids.device))
+    else:
+        local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
+                                               local_keys, local_values, valid, ws, window=settings.local_memory_size)
 
     fast, basis, normalizer = associative_scan_read(projected, surprise, valid, state["basis"], state["normalizer"],
                                                     width=d, features=settings.memory_features)
 
     admission = think.admission_above(surprise, valid, settings.salience_threshold)
-    salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
-                                               local_keys, local_values, admission, ws)
+    if length != 1:
+        salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
+                                                   state["salient_valid"], local_keys, local_values, admission, ws)
     pieces = (ws, fast, local_value, salient_value)
     if low is None:
         fusion_in = torch.cat(pieces, dim=-1)

@@ -188,3 +188,30 @@ def test_token_context_matches_the_oracle(device, b, length, p):
     np.testing.assert_array_equal(targets.cpu().numpy(), np.where(valid.numpy(), ids.numpy(), 0))
     np.testing.assert_array_equal(previous2.cpu().numpy(), want)
     np.testing.assert_array_equal(last2.cpu().numpy(), want_last)
+
+
+def test_read_step_pair_equals_the_two_reads(device):
+    """koemi_read_step_pair (the decode step's local and salient reads in one
+    launch) against read_local_window and read_salient_window with one query."""
+    from koemi_amd import _native
+
+    g = torch.Generator().manual_seed(77)
+    b, d, w, s = 5, 96, 16, 12
+    lk, lv = (torch.randn((b, w, d), generator=g).to(device) for _ in range(2))
+    sk, sv = (torch.randn((b, s, d), generator=g).to(device) for _ in range(2))
+    lvalid = (torch.rand((b, w), generator=g) < 0.7).to(device)
+    svalid = (torch.rand((b, s), generator=g) < 0.5).to(device)
+    svalid[0] = False  # a row with nothing eligible
+    q = torch.randn((b, 1, d), generator=g).to(device)
+    new_k, new_v = (torch.randn((b, 1, d), generator=g).to(device) for _ in range(2))
+    one = torch.ones((b, 1), dtype=torch.bool, device=device)
+    for window in (16, 5):
+        lo, so = torch.empty_like(q), torch.empty_like(q)
+        _native.call("koemi_read_step_pair", _native.ptr(lk), _native.ptr(lv), _native.ptr(lvalid), w, window,
+                     _native.ptr(sk), _native.ptr(sv), _native.ptr(svalid), s, _native.ptr(q), _native.ptr(lo),
+                     _native.ptr(so), b, d, _native.stream_of(device))
+        want_l = memory.read_local_window(lk, lv, lvalid, new_k, new_v, one, q, window=window)
+        want_s = memory.read_salient_window(sk, sv, svalid, new_k, new_v, one, q)
+        torch.testing.assert_close(lo, want_l, rtol=1e-6, atol=1e-6)
+        torch.testing.assert_close(so, want_s, rtol=1e-6, atol=1e-6)
+        assert torch.equal(so[0], torch.zeros_like(so[0]))
