@@ -720,9 +720,19 @@ template <bool GLU>
 __global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
     const bf16* __restrict__ a, const bf16* __restrict__ w0, const bf16* __restrict__ w1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ c,
-    const int64_t* __restrict__ offsets, int64_t n_out, int64_t K, int64_t col_groups) {
+    const int64_t* __restrict__ offsets, int64_t n_out, int64_t K, int64_t col_groups, int64_t experts,
+    int64_t pairs) {
     constexpr int kMats = GLU ? 2 : 1;
     __shared__ float red[kSkinnyWaves][kMats][16][kWave];
+    if (static_cast<int64_t>(blockIdx.x) >= experts * col_groups) {
+        // workgroups past the experts' zero the rows past the valid pairs
+        // (moe_kernels.cu:512, 167-169), a grid stride over those rows
+        const int64_t extra = gridDim.x - experts * col_groups;
+        const int64_t start = min(max(offsets[experts], int64_t(0)), pairs);
+        for (int64_t p = start + (blockIdx.x - experts * col_groups); p < pairs; p += extra)
+            for (int64_t q = threadIdx.x; q < n_out; q += blockDim.x) c[p * n_out + q] = from_f32<bf16>(0.0f);
+        return;
+    }
     const int64_t e = static_cast<int64_t>(blockIdx.x) / col_groups;
     const int64_t n0 = (static_cast<int64_t>(blockIdx.x) % col_groups) * kSkinnyCols;
     const int64_t row0 = offsets[e];
@@ -870,18 +880,16 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         hipLaunchKernelGGL(skinny_gemm_kernel<true>, dim3(static_cast<unsigned>(E * groups1)),
                            dim3(kSkinnyWaves * kWave), 0, s, static_cast<const bf16*>(x), static_cast<const bf16*>(Wg),
                            static_cast<const bf16*>(Wv), static_cast<const bf16*>(bg), static_cast<const bf16*>(bv),
-                           H, offsets, Hd, D, groups1);
+                           H, offsets, Hd, D, groups1, E, P);
         int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
         if (st != KOEMI_OK) return st;
-        hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2)),
+        // the output GEMM's launch also zeroes the rows past the valid pairs (extra workgroups)
+        const int64_t tail_wgs = P < 64 ? P : 64;
+        hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2 + tail_wgs)),
                            dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const bf16*>(Wo),
                            static_cast<const bf16*>(Wo), static_cast<const bf16*>(bo), static_cast<const bf16*>(bo),
-                           static_cast<bf16*>(y), offsets, D, Hd, groups2);
-        st = check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
-        if (st != KOEMI_OK) return st;
-        hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
-                           offsets + E, P, D);
-        return check_launch("koemi_moe_grouped_mlp(zero)");
+                           static_cast<bf16*>(y), offsets, D, Hd, groups2, E, P);
+        return check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
     }
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
                        s, offsets, E, P, ws.max_slots, slot_expert, slot_row, slot_end);
