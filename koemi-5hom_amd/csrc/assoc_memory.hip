@@ -361,12 +361,31 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
         float* nbr = next_basis + (b * D + d) * M;
         const float v = tanhf(row[value_off + d]);
         float num = 0.0f;
+        if (M == MAXM && reinterpret_cast<uintptr_t>(br) % 16 == 0 && reinterpret_cast<uintptr_t>(nbr) % 16 == 0) {
+            // the whole basis row at once: MAXM / 4 16-byte loads in flight, then the stores
+            float4 x4[MAXM / 4];
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) {
-            if (m < M) {
-                const float x = br[m];
-                num = fmaf(x, q_sh[m], num);
-                nbr[m] = fmaf(decay, x, w * v * f_sh[m]);
+            for (int j = 0; j < MAXM / 4; ++j) x4[j] = reinterpret_cast<const float4*>(br)[j];
+#pragma unroll
+            for (int j = 0; j < MAXM / 4; ++j) {
+                const float x[4] = {x4[j].x, x4[j].y, x4[j].z, x4[j].w};
+                float o[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int m = 4 * j + c;
+                    num = fmaf(x[c], q_sh[m], num);
+                    o[c] = fmaf(decay, x[c], w * v * f_sh[m]);
+                }
+                reinterpret_cast<float4*>(nbr)[j] = make_float4(o[0], o[1], o[2], o[3]);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < MAXM; ++m) {
+                if (m < M) {
+                    const float x = br[m];
+                    num = fmaf(x, q_sh[m], num);
+                    nbr[m] = fmaf(decay, x, w * v * f_sh[m]);
+                }
             }
         }
         const float reg = dn + kReadEpsilon;
