@@ -671,7 +671,7 @@ def main() -> int:
         cpu_value = reps * C2_TOKENS / elapsed
         cpu_baseline = {"value": round(cpu_value, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
                         "sample": f"{reps} full C2 steps (32768 tokens each) with the oracle's C port, {elapsed:.1f} s"}
-        # the reference's PyTorch formulas on all host cores
+        # the reference's PyTorch formulas (its CPU fallback path) on all host cores
         import torch.nn.functional as F
 
         threads = len(os.sched_getaffinity(0))
