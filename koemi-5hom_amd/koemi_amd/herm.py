@@ -87,10 +87,11 @@ class HermSettings:
     layers: int = 12
     scan_chunk: int = 128
     linear_dtype: torch.dtype = torch.bfloat16
+    expert_routing: str = "hash"   # "hash" (experts.py:109-150) or "learned" (router.py:43-97)
 
     def oracle_config(self) -> dict:
         keys = ("width", "memory_features", "local_memory_size", "salience_memory_size", "salience_threshold",
-                "expert_count", "top_k")
+                "expert_count", "top_k", "expert_routing")
         values = asdict(self)
         return {k: values[k] for k in keys}
 

@@ -4,9 +4,10 @@ TEST INFRASTRUCTURE ONLY (see the package docstring): imported by tests/ and
 nowhere in the product.
 
 Restates KoemiModel.forward_window (reference model/network.py:296-441) under
-the default settings it runs with (ablation "no_refine": memory_value is the
-fast associative read; hash expert routing with the static dispatch of
-experts.py:109-150) from the reference's own formulas:
+the ablation it runs by default ("no_refine": memory_value is the fast
+associative read), with hash expert routing (the static dispatch of
+experts.py:109-150) or learned routing (router.py:43-97), from the
+reference's own formulas:
 
 * embed + input normalizer (network.py:703-707, layers.py:8-16);
 * gates, masking and scan (memory.py:22-26; network.py:306-310; scan.py);
@@ -26,10 +27,20 @@ own input normalizer applied), every layer keeps its own state and uses the
 token ids for validity, routing and surprise targets; the last layer's head
 gives the logits.
 
-Pinned beyond the formulas by tests/test_oracle_herm.py: the associative
-scan-and-read against the sequential read/update recurrence (memory.py:91-95,
-279-288), the local read against the per-position ring read
-(oracle.read_local_sequential), and the reused oracle functions' own pins.
+Pinned against the reference itself by tests/test_oracle_reference_block.py:
+the reference KoemiModel.forward_window at toy size in float64 (hash and
+learned routing, three windows with the state carried, padding, admissions;
+fixtures tests/golden/herm_block_*.npz). Pinned beyond that by
+tests/test_oracle_herm.py: the associative scan-and-read against the
+sequential read/update recurrence (memory.py:91-95, 279-288), the local read
+against the per-position ring read (oracle.read_local_sequential), window-cut
+independence of the stack, and the reused oracle functions' own pins.
+
+``cfg`` keys: the HermSettings names (width, memory_features,
+local_memory_size, salience_memory_size, salience_threshold, expert_count,
+top_k), optionally ``expert_routing`` ("hash" or "learned"; learned needs the
+layer's ``router_w``) and ``memory_log_dtype`` (fp32 by default, as the
+reference forms the memory's log-decays; float64 for exact-arithmetic checks).
 """
 
 from __future__ import annotations
@@ -74,17 +85,31 @@ def confidence_read(numerator: np.ndarray, denominator: np.ndarray) -> np.ndarra
     return (denominator / regularized) * numerator / regularized
 
 
-def associative_scan_read(basis, normalizer, decay, value, features, weight, query_features):
+def associative_scan_read(basis, normalizer, decay, value, features, weight, query_features, *,
+                          log_dtype=np.float32):
     """scan_and_read of memory.py:97-144 (parallel form): reads for every
-    position from the state before its own write, and the final state."""
+    position from the state before its own write, and the final state.
 
-    log_decay = np.log(decay)
-    cumulative = np.cumsum(log_decay, axis=1)
+    The reference forms the log-decays, their cumulative sums and the decay
+    factors in fp32 whatever the model's dtype (``torch.log(decay.float())``,
+    memory.py:106-115, 126-129) and casts the factors back; ``log_dtype``
+    follows that (float64 gives the exact-arithmetic form, used to pin the
+    parallel form against the sequential recurrence)."""
+
+    ld = np.dtype(log_dtype)
+    # log and exp at log_dtype, correctly rounded (evaluated in float64, then
+    # rounded): torch's fp32 log/exp agree with that to within one ulp
+    log = lambda v: np.log(np.asarray(v, ld).astype(np.float64)).astype(ld)
+    exp = lambda v: np.exp(np.asarray(v, np.float64)).astype(ld).astype(np.float64)
+    log_decay = log(decay)
+    # torch's CPU cumsum accumulates fp32 in float64 and rounds each prefix
+    cumulative = np.cumsum(log_decay.astype(np.float64), axis=1).astype(ld)
     prior = cumulative - log_decay
-    initial = np.exp(prior)
+    initial = exp(prior)
     length = decay.shape[1]
     past = np.arange(length)[:, None] > np.arange(length)[None, :]
-    pair = np.where(past[None], np.exp(np.where(past[None], prior[:, :, None] - cumulative[:, None, :], 0.0)), 0.0)
+    pair_log = np.where(past[None], prior[:, :, None] - cumulative[:, None, :], ld.type(0))
+    pair = np.where(past[None], exp(pair_log), 0.0)
     similarity = np.einsum("bsm,btm->bts", features, query_features)
     influence = pair * similarity * weight[:, None, :]
     numerator = initial[..., None] * np.einsum("bdm,btm->btd", basis, query_features)
@@ -92,9 +117,10 @@ def associative_scan_read(basis, normalizer, decay, value, features, weight, que
     denominator = initial * np.einsum("bm,btm->bt", normalizer, query_features) + influence.sum(axis=-1)
     read = confidence_read(numerator, denominator[..., None])
     total = cumulative[:, -1]
-    final_weight = np.exp(total[:, None] - cumulative) * weight
-    final_basis = np.exp(total)[:, None, None] * basis + np.einsum("bs,bsd,bsm->bdm", final_weight, value, features)
-    final_normalizer = np.exp(total)[:, None] * normalizer + np.einsum("bs,bsm->bm", final_weight, features)
+    final_weight = exp(total[:, None] - cumulative) * weight
+    total_factor = exp(total)
+    final_basis = total_factor[:, None, None] * basis + np.einsum("bs,bsd,bsm->bdm", final_weight, value, features)
+    final_normalizer = total_factor[:, None] * normalizer + np.einsum("bs,bsm->bm", final_weight, features)
     return read, final_basis, final_normalizer
 
 
@@ -134,39 +160,66 @@ def initial_state(batch: int, cfg: dict) -> dict:
     }
 
 
+def learned_route(router_w: np.ndarray, context: np.ndarray, valid: np.ndarray, top_k: int):
+    """LearnedExpertMixture.forward's gate (router.py:46-50): the context with
+    invalid rows zeroed through the bias-free gate, the logits rounded to fp32,
+    softmax and top-k in fp32 (oracle.route_learned); invalid rows -1 and 0.
+    Returns (assignments [..., k] int64, weights [..., k] fp32)."""
+
+    gate_context = np.where(valid[..., None], context, 0.0)
+    logits = linear(gate_context, router_w, None).astype(np.float32)
+    return oracle.route_learned(logits, valid, top_k)
+
+
 def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray, valid: np.ndarray, cfg: dict):
-    """DeterministicExpertMixture static dispatch (experts.py:109-150): every
-    valid token adds FFN_e(context) / k over its distinct assigned experts, then
-    output_normalizer(context + update) where valid."""
+    """The expert mixture of a block, then output_normalizer(context + update)
+    where valid (experts.py:134-136; router.py:96-97).
+
+    Hash routing (the default): DeterministicExpertMixture's static dispatch
+    (experts.py:109-150), every valid token adds FFN_e(context) / k over its
+    distinct assigned experts. ``cfg["expert_routing"] == "learned"``:
+    LearnedExpertMixture (router.py:43-97), every valid token adds
+    w_slot * FFN_e(context) over its top-k experts, w the fp32 softmax weight.
+    Returns (context, assignments)."""
 
     k, count = cfg["top_k"], cfg["expert_count"]
-    assignments = oracle.route_hash(ids, previous, valid, count, k)
     b, length, d = context.shape
     flat = context.reshape(-1, d)
-    update = np.zeros_like(flat)
-    a = assignments.reshape(-1, k)
     ok = valid.reshape(-1)
-    # a slot counts when the token is valid, the expert in range and not
-    # already taken by an earlier slot of the token (experts.py:120-127, 261-267)
-    take = ok[:, None] & (a >= 0) & (a < count)
-    for slot in range(1, k):
-        take[:, slot] &= ~(a[:, :slot] == a[:, slot:slot + 1]).any(axis=1)
+    if cfg.get("expert_routing", "hash") == "learned":
+        assignments, weights = learned_route(p["router_w"], context, valid, k)
+        a = assignments.reshape(-1, k)
+        scale = weights.reshape(-1, k).astype(np.float64)
+        take = ok[:, None] & (a >= 0)
+    else:
+        assignments = oracle.route_hash(ids, previous, valid, count, k)
+        a = assignments.reshape(-1, k)
+        scale = np.full(a.shape, 1.0 / k)
+        # a slot counts when the token is valid, the expert in range and not
+        # already taken by an earlier slot of the token (experts.py:120-127, 261-267)
+        take = ok[:, None] & (a >= 0) & (a < count)
+        for slot in range(1, k):
+            take[:, slot] &= ~(a[:, :slot] == a[:, slot:slot + 1]).any(axis=1)
+    update = np.zeros_like(flat)
     for e in range(count):
-        rows = np.nonzero((take & (a == e)).any(axis=1))[0]
+        rows, slots = np.nonzero(take & (a == e))
         if rows.size == 0:
             continue
         x = flat[rows]
         gate = linear(x, p["gate_w"][e], p["gate_b"][e])
         up = linear(x, p["up_w"][e], p["up_b"][e])
-        update[rows] += linear(gate / (1.0 + np.exp(-gate)) * up, p["down_w"][e], p["down_b"][e]) / k
+        y = linear(gate / (1.0 + np.exp(-gate)) * up, p["down_w"][e], p["down_b"][e])
+        np.add.at(update, rows, y * scale[rows, slots][:, None])
     mixed = rms(flat + update, p["expert_norm"])
     out = np.where(ok[:, None], mixed, flat).reshape(b, length, d)
     return out, assignments
 
 
-def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context: np.ndarray | None = None):
+def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context: np.ndarray | None = None, *,
+                 return_assignments: bool = False):
     """One forward_window of one block. Returns (logits, final_context,
-    next_state, surprise, admission)."""
+    next_state, surprise, admission), and the expert assignments [B, L, k]
+    as a sixth item with ``return_assignments``."""
 
     f = lambda name: np.asarray(p[name], np.float64)
     ids = np.asarray(ids, np.int64)
@@ -200,7 +253,8 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
     write = np.where(valid, write, 0.0)
     query_features = softmax(linear(linear(ws, f("query_w"), f("query_b")), f("feature_w"), f("feature_b")))
     fast, basis, normalizer = associative_scan_read(state["basis"], state["normalizer"], decay, value, features,
-                                                    write, query_features)
+                                                    write, query_features,
+                                                    log_dtype=cfg.get("memory_log_dtype", np.float32))
 
     admission = valid & (surprise > cfg["salience_threshold"])
     salient_value = oracle.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
@@ -208,8 +262,8 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
     fused = rms(linear(np.concatenate([ws, fast, local_value, salient_value], axis=-1), f("fusion_w"),
                        f("fusion_b")), f("fusion_norm"))
     previous = oracle.previous_token_ids(ids, valid, state["last_token"])
-    final, _ = experts({k: f(k) for k in ("gate_w", "gate_b", "up_w", "up_b", "down_w", "down_b", "expert_norm")},
-                       fused, ids, previous, valid, cfg)
+    names = ("gate_w", "gate_b", "up_w", "up_b", "down_w", "down_b", "expert_norm", "router_w")
+    final, assignments = experts({k: f(k) for k in names if k in p}, fused, ids, previous, valid, cfg)
     logits = linear(final, f("head_w"), f("head_b"))
 
     w = cfg["local_memory_size"]
@@ -232,6 +286,8 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
         "salient_valid": np.asarray(sok, bool),
         "last_token": last,
     }
+    if return_assignments:
+        return logits, final, next_state, surprise, admission, assignments
     return logits, final, next_state, surprise, admission
 
 

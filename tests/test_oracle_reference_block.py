@@ -1,0 +1,157 @@
+"""The HERM block oracle against the reference's own forward_window.
+
+``tests/golden/herm_block_{hash,learned}.npz`` hold the reference
+``KoemiModel`` (model/network.py:296-441) at toy size in float64: its
+``state_dict``, three windows of ids (11 tokens, 11 more with the state
+carried, one decode position; padding inside and at the end of rows) and every
+output (logits, surprise, admission, expert assignments, each ``KoemiState``
+field after the window). They were written by
+``tests/golden/make_herm_block_fixture.py`` in the CPU container from the
+reference package; nothing from the reference is imported here.
+
+The weights go through ``koemi_amd.checkpoint`` (the reference state-dict and
+``KoemiState`` layout map) into ``oracle.herm.block_window``, so these tests
+pin both the oracle's block composition (fusion order, residuals, norm
+placement, ring updates, routing) and the layout map. Tolerances, relative to
+each output's largest magnitude: 1e-12 for everything the associative memory
+does not feed (working state, surprise, local and salient rings), float64
+against float64; 1e-7 for the basis, normalizer and logits, because the
+reference forms the memory's log-decay factors in fp32 (memory.py:106-129)
+with torch's fp32 log/exp, which differ from the oracle's correctly rounded
+ones by at most an ulp on some inputs (measured: <= 1e-8), and the learned
+gate's fp32 softmax weights (router.py:46) likewise. Assignments, admission
+masks, ring valid bits and last tokens are exact.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from koemi_amd import checkpoint
+from oracle import herm
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+FIELDS = tuple(checkpoint.STATE_FIELDS)
+
+
+def load(routing: str) -> dict[str, np.ndarray]:
+    with np.load(GOLDEN / f"herm_block_{routing}.npz", allow_pickle=False) as data:
+        return {k: data[k] for k in data.files}
+
+
+def params_of(data: dict[str, np.ndarray], expert_count: int = 4) -> dict[str, np.ndarray]:
+    model_state = {k[len("param."):]: torch.from_numpy(v) for k, v in data.items() if k.startswith("param.")}
+    return {k: v.numpy() for k, v in checkpoint.block_parameters(model_state, expert_count).items()}
+
+
+def cfg_of(data: dict[str, np.ndarray], routing: str) -> dict:
+    return dict(width=16, memory_features=4, local_memory_size=4, salience_memory_size=3,
+                salience_threshold=float(data["settings.salience_threshold"]), expert_count=4, top_k=2,
+                expert_routing=routing)
+
+
+def state_in(data: dict[str, np.ndarray], w: int) -> dict[str, np.ndarray]:
+    fields = {name: data[f"w{w}.state_in.{name}"] for name in FIELDS}
+    return {k: np.asarray(v) for k, v in checkpoint.state_from_fields(fields).items()}
+
+
+def close(got, want, rel):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    scale = max(float(np.abs(want).max()), 1e-30)
+    err = float(np.abs(got - want).max()) if want.size else 0.0
+    assert err <= rel * scale, f"max abs err {err:.3e} > {rel:.0e} x scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("routing", ["hash", "learned"])
+def test_block_window_matches_reference_fixture(routing):
+    data = load(routing)
+    p = params_of(data)
+    cfg = cfg_of(data, routing)
+    fine, memory_fed = 1e-12, 1e-7
+    tol = lambda key: memory_fed if key in ("basis", "normalizer") else fine
+    windows = [int(n) for n in data["settings.windows"]]
+    assert windows == [11, 11, 1]
+    state = state_in(data, 0)
+    for w in range(len(windows)):
+        # each window from the reference's own incoming state: errors do not compound
+        if w:
+            carried = state_in(data, w)
+            for key in carried:
+                if carried[key].dtype == bool or carried[key].dtype.kind == "i":
+                    np.testing.assert_array_equal(state[key], carried[key], err_msg=key)
+                else:
+                    close(state[key], carried[key], tol(key))
+            state = carried
+        logits, final, nxt, surprise, admission, assign = herm.block_window(p, state, data[f"w{w}.ids"], cfg,
+                                                                            return_assignments=True)
+        close(logits, data[f"w{w}.logits"], memory_fed)
+        close(surprise, data[f"w{w}.surprise"], fine)
+        np.testing.assert_array_equal(admission, data[f"w{w}.admission"])
+        np.testing.assert_array_equal(assign, data[f"w{w}.assignments"])
+        want = {k: np.asarray(v) for k, v in checkpoint.state_from_fields(
+            {name: data[f"w{w}.state_out.{name}"] for name in FIELDS}).items()}
+        for key, value in want.items():
+            if value.dtype == bool or value.dtype.kind == "i":
+                np.testing.assert_array_equal(nxt[key], value, err_msg=f"window {w} {key}")
+            else:
+                close(nxt[key], value, tol(key))
+        state = nxt
+
+
+def test_fixture_exercises_the_block():
+    """The fixture covers what the pins need: admissions on and off in every
+    window, carried ring entries, padding, both slots of each routing."""
+
+    for routing in ("hash", "learned"):
+        data = load(routing)
+        for w in range(2):
+            adm = data[f"w{w}.admission"]
+            assert adm.any() and not adm.all()
+        assert data["w2.admission"].any()
+        assert data["w1.state_in.salient_valid"].any() and data["w1.state_in.local_valid"].any()
+        assert (data["w0.ids"] == herm.PAD).any() and (data["w1.ids"] == herm.PAD).any()
+        assert (data["w0.assignments"] >= 0).any() and (data["w0.assignments"] == -1).any()
+
+
+def test_layout_map_roundtrip_and_errors():
+    data = load("learned")
+    model_state = {k[len("param."):]: torch.from_numpy(v) for k, v in data.items() if k.startswith("param.")}
+    p = checkpoint.block_parameters(model_state, 4)
+    assert p["gate_w"].shape == (4, 32, 16) and p["down_w"].shape == (4, 16, 32) and p["router_w"].shape == (4, 16)
+    np.testing.assert_array_equal(p["up_w"][2].numpy(), data["param.experts.experts.2.value_projection.weight"])
+    with pytest.raises(KeyError, match="experts.experts.3"):
+        checkpoint.block_parameters({k: v for k, v in model_state.items() if "experts.3." not in k}, 4)
+    with pytest.raises(ValueError, match="without a place"):
+        checkpoint.block_parameters({**model_state, "memory_refine_gate.weight": torch.zeros(1, 64)}, 4)
+    fields = {name: torch.from_numpy(data[f"w1.state_out.{name}"]) for name in
+              (*checkpoint.STATE_FIELDS, *checkpoint.PASSTHROUGH_FIELDS)}
+    back = checkpoint.state_to_fields(checkpoint.state_from_fields(fields), fields, 22)
+    assert back["step_index"] == 22
+    for name, tensor in fields.items():
+        assert back[name] is tensor
+
+
+def test_reference_checkpoint_loads_weights_only(tmp_path):
+    """A format-7 payload (checkpoints.py:36-57) written with torch.save loads
+    through the weights-only loader into the stack layout."""
+
+    data = load("hash")
+    model_state = {k[len("param."):]: torch.from_numpy(v) for k, v in data.items() if k.startswith("param.")}
+    settings = {"vocabulary_size": 257, "embedding_size": 16, "memory_features": 4, "local_memory_size": 4,
+                "salience_memory_size": 3, "salience_threshold": 0.6, "expert_count": 4, "expert_top_k": 2,
+                "scan_chunk": 11, "ablation": "no_refine", "expert_routing": "hash"}
+    path = tmp_path / "model.pt"
+    torch.save({"format_version": 7, "model_settings": settings, "model_state": model_state}, path)
+    hs, params = checkpoint.load_reference_checkpoint(path)
+    assert (hs.width, hs.memory_features, hs.expert_count, hs.top_k, hs.layers) == (16, 4, 4, 2, 1)
+    assert hs.expert_routing == "hash" and hs.scan_chunk == 11
+    torch.testing.assert_close(params[0]["fusion_w"], model_state["fusion_projection.weight"], rtol=0, atol=0)
+    torch.save({"format_version": 6, "model_settings": settings, "model_state": model_state}, path)
+    with pytest.raises(ValueError, match="format version"):
+        checkpoint.load_reference_checkpoint(path)
+    with pytest.raises(ValueError, match="ablation"):
+        checkpoint.settings_from_model_settings({**settings, "ablation": "herm"})
