@@ -1,23 +1,33 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X HERM hot path (one GPU).
 
-Headline ("C2"): one step = fused RMSNorm-SiLU of
-x bf16 [32768, 512] + surprise of 32768 tokens from fp32 logits [32768, 256]
-+ admission above the 0.9 quantile of the scores. ``value`` is HERM tokens/s
-over K steps with every input resident in HBM. Each step reads a different
-one of several input sets (>= 512 MiB in total) so that the 256 MiB Infinity
-Cache cannot hold the working set; the step is captured once per input set in
-a HIP graph and replayed (its three kernels are launch-bound at this size).
+Headline ("C5", the largest single-GPU
+configuration): a random-initialised stack of 12 HERM blocks (width 1024,
+state 1024, 16 experts top-2, byte vocabulary + PAD). One step is one prefill
+of 8 x 2048 byte ids through all 12 layers in windows of 128 tokens (the state
+carried from window to window), with the ids, the weights and the state
+resident in HBM. ``value`` is prefill HERM tokens/s over K steps; greedy
+decode tokens/s (256 steps at batch 64, fixed-shape state) is reported beside
+it under ``kernels["C5.decode"]``.
 
-Also measured and reported (same JSON line, "kernels"): the C1/C3 affine scan,
-the C3 RMSNorm-SiLU, the C4 MoE route/permute/grouped-GEMM/combine and one
-window's salient read at the C5 model shape ("C5w"), each as
-average kernel time from HIP events, GB/s or TFLOP/s, and the roofline fraction,
-and the C5 end-to-end stack ("e": 12 random-initialised HERM blocks of width
-1024, prefill 8 x 2048 byte ids, then 256 greedy decode steps at batch 64),
-prefill and decode tokens/s from HIP-graph replays.
-The CPU baseline is the oracle's single-threaded C port of the same C2 step
-(and, as an extra, the reference's PyTorch formulas on all host cores).
+``roofline`` is the prefill's dominant hand-written kernel, timed live with
+HIP events on its launch stream over graphs of repeated launches at the exact
+per-window shape (its expert segments come from the same ids), with inputs
+and weights rotated so the Infinity Cache cannot hold them.
+
+``cpu_baseline`` is the reference's block window restated in PyTorch on the
+host (oracle/herm_torch.py: the reference's forward_window formulas with its
+sorted-segment expert dispatch), fp32, on all host cores, median of 5 runs
+after a warmup, on one window of the same configuration (8 x 128 tokens, one
+layer), scaled to the 12 layers of the stack.
+
+Also reported under ``kernels``: the C1/C3 affine scan, the C2 step (fused
+RMSNorm-SiLU + surprise + 0.9-quantile admission), the C3 RMSNorm-SiLU, the
+C4 MoE route/permute/grouped-FFN/combine, the C3-shape recurrent gates and
+one C5 window's salient read, each as the median per-launch time from HIP
+events, GB/s or TFLOP/s and the roofline fraction, with inputs rotated over
+more than 256 MiB where the working set would otherwise fit the Infinity
+Cache; and the reference's PyTorch formulas for those rows on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -28,6 +38,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -40,9 +51,18 @@ for _path in (ROOT, ROOT / "koemi-5hom_amd"):
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA
-C2_TOKENS = 16 * 2048
+MALL_BYTES = 256 * 2**20       # Infinity Cache
 
-# Algorithmic bytes / FLOPs per launch.
+# C5: the stack
+C5_LAYERS, C5_WIDTH, C5_HIDDEN, C5_E, C5_K = 12, 1024, 2048, 16, 2
+C5_BATCH, C5_LEN, C5_WINDOW = 8, 2048, 128
+C5_PREFILL_TOKENS = C5_BATCH * C5_LEN
+C5_DECODE_BATCH, C5_DECODE_STEPS = 64, 256
+C5_WINDOW_PAIRS = C5_BATCH * C5_WINDOW * C5_K
+C5_FFN_FLOP = 6 * C5_WIDTH * C5_HIDDEN * C5_WINDOW_PAIRS            # GEMM 1 (gate + value) + GEMM 2, per window
+
+# Algorithmic bytes / FLOPs per launch of the other rows.
+C2_TOKENS = 16 * 2048
 C2_NORM_BYTES = 32768 * 512 * 2 * 2 + 512 * 2 + 32768 * 4            # x read, y write, gamma, inv
 C2_SURPRISE_BYTES = 32768 * 256 * 4 + 32768 * 8 + 32768 + 32768 * 4   # logits, targets, valid, s
 C2_ADMISSION_BYTES = 32768 * 4 + 32768 + 32768 + 4                     # s, valid, mask, tau
@@ -65,13 +85,15 @@ def log(msg: str) -> None:
 def parse_args() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,3,4,5,g,e",
-                    help="extra configurations to measure (comma list of 1,3,4,5,g,e; '' for none)")
+    ap.add_argument("--steps", type=int, default=10, help="timed C5 prefill steps (8 x 2048 tokens, 12 layers each)")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--configs", default="1,2,3,4,5,g",
+                    help="extra rows to measure (comma list of 1,2,3,4,5,g; '' for none)")
     ap.add_argument("--kernel-iters", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="budget of each CPU reference row")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="only the C5 prefill steps (for rocprofv3 runs of the headline alone)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run each HBM kernel a few times at its config plus a device copy of known size, for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (prints nothing else)")
@@ -112,8 +134,60 @@ TRAFFIC_KERNELS = {
 COPY_BYTES = 512 * 2**20  # the calibration copy reads and writes this many bytes
 
 
+def median_s(fn, runs: int = 5, budget_s: float = 1e9) -> tuple[float, int]:
+    """Median wall time of ``fn`` over ``runs`` runs after one warmup (fewer
+    runs, never below one, if ``budget_s`` is spent first)."""
+
+    fn()
+    times, t0 = [], time.perf_counter()
+    while len(times) < runs and (not times or time.perf_counter() - t0 < budget_s):
+        t1 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t1)
+    return statistics.median(times), len(times)
+
+
+def cpu_stack_baseline(threads: int, ids_window, decode_ids) -> dict:
+    """The C5 CPU baseline: oracle/herm_torch.py's block window (the
+    reference's forward_window formulas, fp32) on the host cores, one layer
+    of the stack's shapes with its own seeded fp32 weights; tokens/s of the
+    12-layer stack = window tokens / (12 x the median window time)."""
+
+    import torch
+
+    from koemi_amd import herm
+    from oracle import herm_torch
+
+    torch.set_num_threads(threads)
+    settings = herm.HermSettings(layers=1)
+    p = herm.init_stack(settings, 1005, "cpu")[0]
+    cfg = settings.oracle_config()
+
+    def state(batch):
+        return {k: v.cpu() for k, v in herm.initial_states(settings, batch, torch.device("cpu"))[0].items()}
+
+    prefill_state = state(ids_window.shape[0])
+    decode_state = state(decode_ids.shape[0])
+    with torch.inference_mode():
+        window_s, runs = median_s(lambda: herm_torch.block_window(p, prefill_state, ids_window, cfg), 5)
+        step_s, step_runs = median_s(lambda: herm_torch.block_window(p, decode_state, decode_ids, cfg), 5)
+    tokens = ids_window.numel()
+    return {
+        "value": round(tokens / (C5_LAYERS * window_s), 1),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"one C5 prefill window ({ids_window.shape[0]} x {ids_window.shape[1]} tokens) through one layer, "
+                   f"oracle/herm_torch.py fp32 on {threads} threads, median of {runs} runs after a warmup: "
+                   f"{window_s * 1e3:.1f} ms; value = tokens / (12 layers x that)"),
+        "decode": {"tokens_per_s": round(decode_ids.numel() / (C5_LAYERS * step_s), 1),
+                   "ms_per_layer_step": round(step_s * 1e3, 3), "runs": step_runs,
+                   "sample": f"one decode position at batch {decode_ids.shape[0]} through one layer, x12 layers"},
+    }
+
+
 def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
-    """The reference's PyTorch formulas for each measured row, on the host cores.
+    """The reference's PyTorch formulas for each measured kernel row, on the host cores.
 
     Each is timed on a bounded sample of its configuration (median of up to
     five runs after one warmup, within ``budget_s`` per row) and scaled to the
@@ -121,23 +195,17 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
     configuration's shapes and distributions.
     """
 
-    import statistics
-
     import torch
     import torch.nn.functional as F
+
+    from oracle import herm_torch
 
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(99)
     out = {}
 
     def median_ms(fn) -> float:
-        fn()
-        times, t0 = [], time.perf_counter()
-        while len(times) < 5 and (not times or time.perf_counter() - t0 < budget_s):
-            t1 = time.perf_counter()
-            fn()
-            times.append(time.perf_counter() - t1)
-        return statistics.median(times) * 1000.0
+        return median_s(fn, 5, budget_s)[0] * 1000.0
 
     def seq_scan(a, b):  # the tests' sequential recurrence (test_dense_cuda.py:21-33)
         h = torch.zeros_like(a[:, 0])
@@ -148,20 +216,26 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
         return res
 
     def hillis_steele(a, b):  # the model path, model/scan.py:17-30
-        coef, val, off, n = a, b, 1, a.shape[1]
-        while off < n:
-            sc = torch.cat((torch.ones_like(coef[:, :off]), coef[:, : n - off]), dim=1)
-            sv = torch.cat((torch.zeros_like(val[:, :off]), val[:, : n - off]), dim=1)
-            val = coef * sv + val
-            coef = coef * sc
-            off *= 2
-        return val
+        return herm_torch.window_scan(a, b, torch.zeros_like(a[:, 0]))
 
     if "1" in extra:
         a = torch.rand((4, 1024, 256), generator=g) * 0.199 + 0.8
         b = torch.randn((4, 1024, 256), generator=g)
         out["C1.affine_scan"] = {"ms": round(median_ms(lambda: seq_scan(a, b)), 3), "sample": "full C1, sequential loop",
                                  "ms_model_path": round(median_ms(lambda: hillis_steele(a, b)), 3)}
+    if "2" in extra:
+        from koemi_amd import workloads
+
+        c = workloads.config2()
+        x2, g2 = c.x.float(), c.gamma.float()
+
+        def c2_step():  # layers.py:14-16 + F.silu; network.py:677-688; quantile admission
+            F.silu(x2 * torch.rsqrt(x2.square().mean(dim=-1, keepdim=True) + 1e-6) * g2)
+            nll = F.cross_entropy(c.logits, c.targets, reduction="none")
+            s = torch.where(c.valid, 1.0 - torch.exp(-(nll / math.log(256))), torch.zeros(()))
+            return s > torch.quantile(s, 0.9)
+
+        out["C2.step"] = {"ms": round(median_ms(c2_step), 3), "sample": "full C2 step, fp32"}
     if "3" in extra:
         a = torch.sigmoid(torch.randn((1, 4096, 1024), generator=g) + 2.0)
         b = 0.5 * torch.randn((1, 4096, 1024), generator=g)
@@ -184,13 +258,9 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
         valid = torch.ones((T,), dtype=torch.bool)
 
         def route():  # experts.py:30-38, 283-289 (int64)
-            def mix(v):
-                v = ((v >> 16) ^ v) * 0x45D9F3B % (1 << 32)
-                v = ((v >> 16) ^ v) * 0x45D9F3B % (1 << 32)
-                return (v >> 16) ^ v
-            h = mix((tok * 1000003 + prev * 97409) % (1 << 32))
-            e = torch.stack([(h + k * 0x9E3779B9) % E for k in range(K)], dim=-1)
-            return torch.where(valid.unsqueeze(-1), e, torch.full_like(e, -1))
+            h = herm_torch.content_hash(tok, prev)
+            e = (h.unsqueeze(-1) + torch.arange(K) * herm_torch.SLOT_OFFSET).remainder(E)
+            return e.masked_fill(~valid.unsqueeze(-1), -1)
 
         out["C4.route_hash"] = {"ms": round(median_ms(route), 3), "sample": "full C4"}
         assign = route()
@@ -216,6 +286,7 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
 
         out["C4.grouped_glu_ffn"] = {"ms": round(C4_PAIRS / 4096 * median_ms(ffn), 3),
                                      "sample": "4096 of 65536 pairs (256 per expert), fp32, x16"}
+        del wg, wv, wo
         y = torch.randn((C4_PAIRS, D), generator=g).to(torch.bfloat16)
         idx = torch.arange(C4_PAIRS) // K
 
@@ -240,34 +311,13 @@ def cpu_reference_times(extra: list, threads: int, budget_s: float) -> dict:
         ck, cv = torch.randn((b5, s5, d5), generator=g), torch.randn((b5, s5, d5), generator=g)
         k5, v5, q5 = (torch.randn((b5, l5, d5), generator=g) for _ in range(3))
         cvalid, adm = torch.rand((b5, s5), generator=g) < 0.8, torch.rand((b5, l5), generator=g) < 0.1
-
-        def read():  # model/memory.py:405-429
-            all_k, all_v = torch.cat((ck, k5), dim=1), torch.cat((cv, v5), dim=1)
-            pos = torch.arange(l5)
-            elig = torch.cat((cvalid.unsqueeze(1).expand(b5, l5, s5),
-                              adm.unsqueeze(1) & (pos.unsqueeze(1) > pos.unsqueeze(0)).unsqueeze(0)), dim=-1)
-            sc = torch.einsum("bsd,btd->bts", all_k, q5) / math.sqrt(d5)
-            w = torch.softmax(sc.masked_fill(~elig, float("-inf")), dim=-1)
-            w = torch.where(elig.any(dim=-1, keepdim=True), w, torch.zeros(()))
-            return torch.einsum("bts,bsd->btd", w, all_v)
-
-        out["C5w.salient_read"] = {"ms": round(median_ms(read), 3), "sample": "full C5 window"}
-    if "e" in extra:
-        # One block window (batch 8, 128 tokens, width 1024) with the float64
-        # numpy restatement of forward_window, scaled to 16 windows x 12 layers.
-        import numpy as np
-
-        import oracle.herm as oherm
-        from koemi_amd import herm
-
-        settings = herm.HermSettings(layers=1)
-        params = [{k: v.double().numpy() for k, v in p.items()} for p in herm.init_stack(settings, 1005)]
-        cfg = settings.oracle_config()
-        ids = np.random.default_rng(1005).integers(0, 256, (8, 128))
-        state = oherm.initial_state(8, cfg)
-        window_ms = median_ms(lambda: oherm.block_window(params[0], state, ids, cfg))
-        out["C5.prefill"] = {"ms": round(window_ms * 16 * 12, 3),
-                             "sample": "one layer x one window (8 x 128 tokens), numpy float64 block restatement, x192"}
+        pos = torch.arange(l5)
+        elig = torch.cat((cvalid.unsqueeze(1).expand(b5, l5, s5),
+                          adm.unsqueeze(1) & (pos.unsqueeze(1) > pos.unsqueeze(0)).unsqueeze(0)), dim=-1)
+        all_k, all_v = torch.cat((ck, k5), dim=1), torch.cat((cv, v5), dim=1)
+        out["C5w.salient_read"] = {  # model/memory.py:405-429
+            "ms": round(median_ms(lambda: herm_torch.masked_attention(all_k, all_v, q5, elig)), 3),
+            "sample": "full C5 window"}
     return out
 
 
@@ -312,7 +362,6 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     """profiles/traffic.json from rocprofv3 counter_collection.csv files of FETCH_SIZE and WRITE_SIZE."""
 
     import csv
-    import statistics
 
     def per_kernel(directory: str, counter: str) -> dict:
         rows = []
@@ -351,6 +400,40 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
+class Timer:
+    """Median per-launch GPU time of an operator: ``per_graph`` launches
+    captured in one HIP graph (cycling over input sets), the graph replayed
+    ``reps`` times with an event pair around each replay on the launch
+    stream; every graph gets its own memory pool."""
+
+    def __init__(self, torch, stream):
+        self.torch = torch
+        self.stream = stream
+
+    def per_launch_ms(self, fns: list, per_graph: int, reps: int) -> float:
+        torch = self.torch
+        for fn in fns:  # eager warmup: libraries pick their kernels outside the capture
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(per_graph):
+                fns[i % len(fns)]()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(self.stream)
+            g.replay()
+            end.record(self.stream)
+            end.synchronize()
+            times.append(start.elapsed_time(end) / per_graph)
+        del g
+        return statistics.median(times)
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_pmc:
@@ -359,214 +442,229 @@ def main() -> int:
         return traffic_probe()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures a single GPU: this build has no multi-GPU path and every box has one GPU; "
+        print("bench.py measures a single GPU: this build has no multi-GPU path and every box here has one GPU; "
               "run with --gpus 1", file=sys.stderr, flush=True)
         return 2
 
-    import numpy as np
     import torch
 
-    from koemi_amd import core, dense, memory, moe, recurrent, think, workloads
+    from koemi_amd import core, dense, herm, memory, moe, recurrent, think, workloads
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     stream = torch.cuda.current_stream(device)
+    timer = Timer(torch, stream)
+    kernels: dict = {}
 
-    def events_ms(fn, iters: int, warmup: int = 3) -> float:
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(iters):
-            fn()
-        end.record(stream)
-        end.synchronize()
-        return start.elapsed_time(end) / iters
+    # ------------------------------------------------------------ headline C5
+    log("C5: initialising the 12-layer stack")
+    settings = herm.HermSettings()
+    params = herm.prepare_stack(herm.init_stack(settings, 1005, device), settings, device)
+    c5 = workloads.config5()
+    ids = c5.prefill_ids.to(device)
+    start_states = herm.initial_states(settings, C5_BATCH, device)
 
-    # ------------------------------------------------------------- headline C2
-    log("generating C2 input sets")
-    per_set = C2_NORM_BYTES + C2_SURPRISE_BYTES + C2_ADMISSION_BYTES
-    n_sets = max(2, math.ceil(512 * 2**20 / per_set))
-    sets = []
-    for i in range(n_sets):
-        c = workloads.config2(seed=1002 + i)
-        d = {
-            "x": c.x.to(device), "gamma": c.gamma.to(device), "logits": c.logits.to(device),
-            "targets": c.targets.to(device), "valid": c.valid.to(device),
-        }
-        sets.append(d)
-    eps, q = 1e-6, 0.9
-
-    def step_norm(d):
-        return tuple(core.rmsnorm_silu_forward(d["x"], d["gamma"], eps))
-
-    def step_surprise(d):
-        s = think.surprise_from_logits(d["logits"], d["targets"], d["valid"])
-        return (s, *think.salience_admission(s, d["valid"], quantile=q))
-
-    def step(d):
-        d["out"] = step_norm(d) + step_surprise(d)
-
-    # eager reference outputs for the graph check
-    for d in sets:
-        step(d)
+    log("C5: capturing the window graph; eager first window for the replay check")
+    eager_logits, _ = herm.stack_window(params, settings, ids[:, :C5_WINDOW].contiguous(),
+                                        herm.initial_states(settings, C5_BATCH, device))
+    logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states)
     torch.cuda.synchronize()
-    eager = [tuple(t.clone() for t in d["out"]) for d in sets]
+    first = logits[:, :C5_WINDOW].clone()
+    replay_vs_eager = float((first - eager_logits).abs().max() / eager_logits.abs().max())
+    assert replay_vs_eager < 1e-5, f"graph replay differs from the eager window: {replay_vs_eager:.3e}"
+    assert torch.isfinite(logits).all(), "non-finite prefill logits"
+    reference_logits = logits.clone()
 
-    # One graph holds `per_graph` consecutive steps (two passes over the input
-    # sets) so that the host cost of a graph launch is amortized over many steps.
-    # The RMSNorm-SiLU of a step does not depend on its surprise/admission
-    # chain, so the graph holds the two as separate branches (captured from two
-    # streams of default priority, joined at the end): the GPU may overlap the
-    # gaps between one branch's kernels with the other's.
-    per_graph = 2 * n_sets
-    full_replays, remainder = divmod(args.steps, per_graph)
-    log(f"capturing {per_graph}-step graphs")
-    pool = torch.cuda.graph_pool_handle()
-    branch = torch.cuda.Stream(device)
-
-    keep_alive = []  # outputs of captured steps stay referenced, so no later capture reuses them
-
-    def capture_steps(count: int):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, pool=pool):
-            main = torch.cuda.current_stream(device)
-            branch.wait_stream(main)
-            outs = []
-            for i in range(count):
-                d = sets[i % n_sets]
-                with torch.cuda.stream(branch):
-                    s_out = step_surprise(d)
-                outs.append((d, step_norm(d) + s_out))
-            main.wait_stream(branch)
-        for d, out in outs:
-            d["out"] = out
-            keep_alive.append(out)
-        torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        for i in range(min(n_sets, count)):  # every replay must reproduce the eager outputs
-            for got, want in zip(sets[i]["out"], eager[i]):
-                assert torch.equal(got, want), "graph replay differs from the eager step"
-        return g
-
-    step_graph = capture_steps(per_graph) if full_replays else None
-    tail_graph = capture_steps(remainder) if remainder else None
-
-    for i in range(args.warmup):  # untimed warmup steps
-        step(sets[i % n_sets])
+    log(f"C5: {args.warmup} warmup + {args.steps} timed prefill steps")
+    for _ in range(args.warmup):
+        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
     torch.cuda.synchronize()
-    log(f"timing {args.steps} C2 steps")
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    start_ev, end_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(full_replays):
-        step_graph.replay()
-    if tail_graph is not None:
-        tail_graph.replay()
-    end.record(stream)
+    start_ev.record(stream)
+    for _ in range(args.steps):
+        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
+    end_ev.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(end)
-    steps = args.steps
-    ms_per_step = max(wall * 1000.0, gpu_ms) / steps
-    value = C2_TOKENS / (ms_per_step / 1000.0)
-    for i in range(min(n_sets, remainder if tail_graph is not None else per_graph)):
-        for got, want in zip(sets[i]["out"], eager[i]):
-            assert torch.equal(got, want), "graph replay differs from the eager step after timing"
+    gpu_ms = start_ev.elapsed_time(end_ev)
+    ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
+    value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
+    assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
+    kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
+                             "replay_vs_eager_rel": replay_vs_eager}
+    del graph, logits, reference_logits, eager_logits, first
 
-    # Per-kernel times of the step: each kernel alone, `per_graph` launches per graph.
-    def kernel_graph_ms(fn_for_set) -> float:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, pool=pool):
-            for i in range(per_graph):
-                fn_for_set(sets[i % n_sets])
+    if not args.headline_only:
+        log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
+        decode = herm.DecodeGraph(params, settings, c5.decode_ids.to(device),
+                                  herm.initial_states(settings, C5_DECODE_BATCH, device))
+        for _ in range(3):
+            decode.step()
         torch.cuda.synchronize()
-        reps = max(4, math.ceil(steps / per_graph))
-        return events_ms(g.replay, reps, warmup=2) / per_graph
+        t0 = time.perf_counter()
+        for _ in range(C5_DECODE_STEPS):
+            decode.step()
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+        kernels["C5.decode"] = {"ms_per_step": round(decode_s * 1e3 / C5_DECODE_STEPS, 4),
+                                "tokens_per_s": round(C5_DECODE_BATCH * C5_DECODE_STEPS / decode_s, 1),
+                                "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
+        del decode
 
-    log("timing C2 kernels")
-    for d in sets:
-        d["s"] = d["out"][2]
-    c2_times = {
-        "rmsnorm_silu": kernel_graph_ms(lambda d: core.rmsnorm_silu_forward(d["x"], d["gamma"], eps)),
-        "surprise_rows": kernel_graph_ms(lambda d: think.surprise_from_logits(d["logits"], d["targets"], d["valid"])),
-        "quantile_admission": kernel_graph_ms(lambda d: think.salience_admission(d["s"], d["valid"], quantile=q)),
-    }
-    c2_bytes = {"rmsnorm_silu": C2_NORM_BYTES, "surprise_rows": C2_SURPRISE_BYTES, "quantile_admission": C2_ADMISSION_BYTES}
-    kernels = {}
-    for name, ms in c2_times.items():
-        gbs = c2_bytes[name] / (ms / 1000.0) / 1e9
-        kernels[f"C2.{name}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-    hbm_kernels = ("rmsnorm_silu", "surprise_rows")
-    dominant = max(hbm_kernels, key=c2_times.get)
-    dom_gbs = c2_bytes[dominant] / (c2_times[dominant] / 1000.0) / 1e9
-    eager_ms = events_ms(lambda: step(sets[0]), 20)
-    del step_graph, tail_graph, keep_alive
-    for d in sets:
-        d.pop("out", None)
+    # --------------------------------------------- dominant kernel of C5 prefill
+    # The expert FFN of one layer window at the prefill's exact shape: the
+    # window's ids routed by the hash (as every layer routes them), bf16
+    # contexts, each layer's own weights in turn (two layers' experts, 403 MB,
+    # do not fit the Infinity Cache, as the stack's twelve do not).
+    log("C5: dominant kernel (expert FFN of a layer window), live timing")
+    win = ids[:, :C5_WINDOW].contiguous()
+    valid5 = win != herm.PAD_TOKEN_ID
+    prev5 = torch.cat((torch.full_like(win[:, :1], herm.PAD_TOKEN_ID), win[:, :-1]), dim=1)
+    assign5 = moe.route_topk_valid(win, prev5, valid5, expert_count=C5_E, top_k=C5_K)
+    ffn_sets = []
+    for layer in (0, 1):
+        ctx5 = torch.randn((C5_BATCH * C5_WINDOW, C5_WIDTH), device=device).to(torch.bfloat16)
+        sc, rows, experts, offsets = moe.permute_topk(ctx5, assign5.reshape(-1, C5_K), valid5.reshape(-1),
+                                                      expert_count=C5_E)
+        p = params[layer]
+        ffn_sets.append((sc, experts, offsets, p["gate_w"], p["gate_b"], p["up_w"], p["up_b"], p["down_w"],
+                         p["down_b"]))
+    ffn_ms = timer.per_launch_ms([lambda s=s: moe.grouped_expert_mlp_inference(*s, validate=False) for s in ffn_sets],
+                                 24, max(10, args.kernel_iters))
+    ffn_tflops = C5_FFN_FLOP / ffn_ms / 1e9
+    kernels["C5.expert_ffn_window"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
+                                       "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
+                                       "pairs": C5_WINDOW_PAIRS, "flop": C5_FFN_FLOP}
+    headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", None),
+                         "kernel": "grouped expert GLU FFN of one C5 layer window (grouped_gemm_bf16_kernel launches "
+                                   "of GEMM 1 and GEMM 2 with the device tile schedule)",
+                         "algorithmic_flop": C5_FFN_FLOP, "avg_ms": round(ffn_ms, 5)}
+    del ffn_sets
+    extra = [c for c in args.configs.split(",") if c.strip()] if not args.headline_only else []
+    iters = args.kernel_iters
 
-    # ------------------------------------------------------------ other configs
-    extra = [c for c in args.configs.split(",") if c.strip()]
+    # ---------------------------------------------------------------- C2 step
+    if "2" in extra:
+        log("C2: RMSNorm-SiLU + surprise + 0.9-quantile admission")
+        per_set = C2_NORM_BYTES + C2_SURPRISE_BYTES + C2_ADMISSION_BYTES
+        n_sets = max(2, math.ceil(2 * MALL_BYTES / per_set))
+        sets = []
+        for i in range(n_sets):
+            c = workloads.config2(seed=1002 + i)
+            sets.append({k: getattr(c, k).to(device) for k in ("x", "gamma", "logits", "targets", "valid")})
+        for d in sets:
+            s = think.surprise_from_logits(d["logits"], d["targets"], d["valid"])
+            d["s"] = s
+            d["want"] = tuple(t.clone() for t in (*core.rmsnorm_silu_forward(d["x"], d["gamma"], 1e-6), s,
+                                                  *think.salience_admission(s, d["valid"], quantile=0.9)))
+
+        def c2_step(d):
+            y, inv = core.rmsnorm_silu_forward(d["x"], d["gamma"], 1e-6)
+            s = think.surprise_from_logits(d["logits"], d["targets"], d["valid"])
+            mask, tau = think.salience_admission(s, d["valid"], quantile=0.9)
+            return y, inv, s, mask, tau
+
+        # the step, replayed from one graph of 2 x n_sets steps; outputs compared with the eager ones
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs = [c2_step(sets[i % n_sets]) for i in range(2 * n_sets)]
+        torch.cuda.synchronize()
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        for i, out in enumerate(outs):
+            for got, want in zip(out, sets[i % n_sets]["want"]):
+                assert torch.equal(got, want), "C2 graph replay differs from the eager step"
+        reps = max(5, iters)
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            g.replay()
+            b.record(stream)
+            b.synchronize()
+            times.append(a.elapsed_time(b) / (2 * n_sets))
+        step_ms = statistics.median(times)
+        del g, outs
+        c2_rows = {
+            "rmsnorm_silu": ([lambda d=d: core.rmsnorm_silu_forward(d["x"], d["gamma"], 1e-6) for d in sets],
+                             C2_NORM_BYTES),
+            "surprise_rows": ([lambda d=d: think.surprise_from_logits(d["logits"], d["targets"], d["valid"])
+                               for d in sets], C2_SURPRISE_BYTES),
+            "quantile_admission": ([lambda d=d: think.salience_admission(d["s"], d["valid"], quantile=0.9)
+                                    for d in sets], C2_ADMISSION_BYTES),
+        }
+        kernels["C2.step"] = {"ms": round(step_ms, 5), "tokens_per_s": round(C2_TOKENS / (step_ms / 1e3), 1),
+                              "input_sets": n_sets}
+        for name, (fns, nbytes) in c2_rows.items():
+            ms = timer.per_launch_ms(fns, 2 * n_sets, reps)
+            gbs = nbytes / ms / 1e6
+            kernels[f"C2.{name}"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        del sets
+
     if "1" in extra:
         log("C1 scan")
         c1 = workloads.to_device(workloads.config1(), device)
-        g1 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g1, pool=pool):
-            for _ in range(20):
-                dense.scan_forward(c1.retention, c1.increment, c1.initial)
-        ms = events_ms(g1.replay, 10) / 20
+        ms = timer.per_launch_ms([lambda: dense.scan_forward(c1.retention, c1.increment, c1.initial)], 20, iters)
         kernels["C1.affine_scan"] = {"ms": round(ms, 5), "GB/s": round(C1_SCAN_BYTES / ms / 1e6, 1),
                                      "frac_hbm": round(C1_SCAN_BYTES / ms / 1e6 / HBM_PEAK_GBS, 4),
                                      "note": "12.6 MB working set is launch-bound and fits the Infinity Cache"}
-        del c1, g1
+        del c1
     if "3" in extra:
-        log("C3 scan + norm (generating 1 GiB of inputs)")
+        log("C3 scan + norm (generating 1.6 GB of inputs)")
         c3 = workloads.to_device(workloads.config3(), device)
-        ms = events_ms(lambda: dense.scan_forward(c3.retention, c3.increment, c3.initial), args.kernel_iters)
+        ms = timer.per_launch_ms([lambda: dense.scan_forward(c3.retention, c3.increment, c3.initial)], 4,
+                                 max(5, iters // 2))
         gbs = C3_SCAN_BYTES / ms / 1e6
         kernels["C3.affine_scan"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                      "tokens_per_s": round(32 * 4096 / (ms / 1000.0))}
         h = dense.scan_forward(c3.retention, c3.increment, c3.initial).to(torch.bfloat16).view(-1, 1024)
         del c3
+        hs = [h, h.clone()]  # two 268 MB inputs in turn: the second is not in the Infinity Cache after the first
         gamma = workloads.config3(batch=1, seq=1, width=1024).gamma.to(device)
-        ms = events_ms(lambda: core.rmsnorm_silu_forward(h, gamma, 1e-6), args.kernel_iters)
+        ms = timer.per_launch_ms([lambda x=x: core.rmsnorm_silu_forward(x, gamma, 1e-6) for x in hs], 8, iters)
         gbs = C3_NORM_BYTES / ms / 1e6
-        kernels["C3.rmsnorm_silu"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-        del h
+        kernels["C3.rmsnorm_silu"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                      "note": "two input copies alternate"}
+        del h, hs
     if "4" in extra:
         log("C4 MoE (generating inputs)")
         c4 = workloads.to_device(workloads.config4(), device)
-        ms = events_ms(lambda: moe.route_topk_valid(c4.token_ids, c4.previous_token_ids, c4.valid, expert_count=16,
-                                                    top_k=2, validate=False), args.kernel_iters)
+        ms = timer.per_launch_ms([lambda: moe.route_topk_valid(c4.token_ids, c4.previous_token_ids, c4.valid,
+                                                               expert_count=16, top_k=2, validate=False)], 20, iters)
         kernels["C4.route_hash"] = {"ms": round(ms, 5), "GB/s": round(C4_ROUTE_BYTES / ms / 1e6, 1)}
-        a_l, w_l = moe.route_topk_learned(c4.router_logits, c4.valid, top_k=2)
         assign = moe.route_topk_valid(c4.token_ids, c4.previous_token_ids, c4.valid, expert_count=16, top_k=2)
-        ms = events_ms(lambda: moe.permute_topk(c4.context, assign, c4.valid, expert_count=16, validate=False), args.kernel_iters)
+        ctxs = [c4.context, c4.context.clone(), c4.context.clone()]  # 3 x 67 MB contexts + their 134 MB outputs
+        ms = timer.per_launch_ms([lambda x=x: moe.permute_topk(x, assign, c4.valid, expert_count=16, validate=False)
+                                  for x in ctxs], 6, iters)
         gbs = C4_PERMUTE_BYTES / ms / 1e6
-        kernels["C4.permute"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        kernels["C4.permute"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                 "note": "three context copies in turn"}
+        a_l, w_l = moe.route_topk_learned(c4.router_logits, c4.valid, top_k=2)
         sc, rows, experts, offsets, sw = moe.permute_topk(c4.context, a_l, c4.valid, expert_count=16, pair_weights=w_l)
-        weights = (c4.gate_weights, c4.gate_biases, c4.value_weights, c4.value_biases, c4.output_weights, c4.output_biases)
-        ms = events_ms(lambda: moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights, validate=False),
-                       max(5, args.kernel_iters // 2))
+        del ctxs
+        weights = (c4.gate_weights, c4.gate_biases, c4.value_weights, c4.value_biases, c4.output_weights,
+                   c4.output_biases)
+        ms = timer.per_launch_ms([lambda: moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights,
+                                                                           validate=False)], 4, max(5, iters // 2))
         tflops = C4_GEMM_FLOP / ms / 1e9
         kernels["C4.grouped_glu_ffn"] = {"ms": round(ms, 5), "TFLOP/s": round(tflops, 1),
                                          "frac_mfma_bf16": round(tflops / BF16_PEAK_TFLOPS, 4)}
-        y = moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights, validate=False)
-        ms = events_ms(lambda: moe.combine_topk(y, rows, offsets, token_count=C4_T, top_k=2, pair_weights=sw,
-                                                validate=False), args.kernel_iters)
+        ys = [moe.grouped_expert_mlp_inference(sc, experts, offsets, *weights, validate=False) for _ in range(2)]
+        ms = timer.per_launch_ms([lambda y=y: moe.combine_topk(y, rows, offsets, token_count=C4_T, top_k=2,
+                                                               pair_weights=sw, validate=False) for y in ys], 6, iters)
         gbs = C4_COMBINE_BYTES / ms / 1e6
-        kernels["C4.combine"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        kernels["C4.combine"] = {"ms": round(ms, 5), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                 "note": "two expert-output copies in turn"}
         # practical bf16 GEMM ceiling of the platform library at the same total shape
         a_mat = torch.randn((C4_PAIRS, C4_D), device=device, dtype=torch.bfloat16)
         b_mat = torch.randn((C4_D, 2 * C4_H), device=device, dtype=torch.bfloat16)
-        ms = events_ms(lambda: torch.matmul(a_mat, b_mat), 10)
+        ms = timer.per_launch_ms([lambda: torch.matmul(a_mat, b_mat)], 4, 10)
         kernels["hipblaslt_reference_gemm"] = {"shape": [C4_PAIRS, C4_D, 2 * C4_H],
                                                "TFLOP/s": round(2 * C4_PAIRS * C4_D * 2 * C4_H / ms / 1e9, 1)}
-        del c4, sc, y, a_mat, b_mat
+        del c4, sc, ys, a_mat, b_mat
 
     if "5" in extra:
         # One window's salient read at the C5 model shape (8 sequences, scan
@@ -579,12 +677,10 @@ def main() -> int:
         ck, cv, k5, v5, q5 = r5(b5, s5, d5), r5(b5, s5, d5), r5(b5, l5, d5), r5(b5, l5, d5), r5(b5, l5, d5)
         cvalid = torch.rand((b5, s5), generator=g5, device=device) < 0.8
         adm5 = torch.rand((b5, l5), generator=g5, device=device) < 0.1
-        ms = events_ms(lambda: memory.read_salient_window(ck, cv, cvalid, k5, v5, adm5, q5), args.kernel_iters)
+        ms = timer.per_launch_ms([lambda: memory.read_salient_window(ck, cv, cvalid, k5, v5, adm5, q5)], 20, iters)
         flop = 4 * b5 * l5 * (s5 + l5) * d5
-        nbytes = 4 * (4 * b5 * l5 * d5 + 2 * b5 * s5 * d5) + b5 * (s5 + l5)
-        kernels["C5w.salient_read"] = {"ms": round(ms, 5), "GB/s": round(nbytes / ms / 1e6, 1),
-                                       "TFLOP/s": round(flop / ms / 1e9, 2), "shape_b_l_s_d": [b5, l5, s5, d5],
-                                       "note": "HIP fp32-MFMA scores, softmax and weighted-sum kernels, eager launches"}
+        kernels["C5w.salient_read"] = {"ms": round(ms, 5), "TFLOP/s": round(flop / ms / 1e9, 2),
+                                       "shape_b_l_s_d": [b5, l5, s5, d5]}
         del ck, cv, k5, v5, q5
 
     if "g" in extra:
@@ -596,134 +692,54 @@ def main() -> int:
         wts = [(1024 ** -0.5) * torch.randn(shape, generator=gg, device=device)
                for shape in ((1024, 1024), (1024,), (1024, 1024), (1024,))]
         vg = torch.ones((32, 4096), dtype=torch.bool, device=device)
-        ms = events_ms(lambda: recurrent.recurrent_gates(ug, *wts, vg), max(3, args.kernel_iters // 4))
+        ms = timer.per_launch_ms([lambda: recurrent.recurrent_gates(ug, *wts, vg)], 2, max(3, iters // 4))
         kernels["C3g.recurrent_gates"] = {"ms": round(ms, 5), "TFLOP/s": round(C3G_FLOP / ms / 1e9, 1),
-                                          "frac_mfma_fp32": round(C3G_FLOP / ms / 1e9 / FP32_PEAK_TFLOPS, 4),
-                                          "note": "two fp32 rocBLAS products + the HIP gate epilogue"}
-        ms = events_ms(lambda: recurrent.recurrent_scan(ug, *wts, vg), max(3, args.kernel_iters // 4))
+                                          "frac_mfma_fp32": round(C3G_FLOP / ms / 1e9 / FP32_PEAK_TFLOPS, 4)}
+        ms = timer.per_launch_ms([lambda: recurrent.recurrent_scan(ug, *wts, vg)], 2, max(3, iters // 4))
         kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
-                                         "note": "the two gate GEMMs, then one kernel forming the gates inside "
-                                                 "the affine scan (network.py:306-310)"}
+                                         "note": "the gate GEMMs, then the gates formed inside the affine scan"}
         del ug, wts, vg
-
-    if "e" in extra:
-        # C5 end to end: 12 HERM blocks, width 1024, 16 experts top-2, byte
-        # vocabulary (+ PAD); prefill 8 x 2048 ids ~ U{0..255} in windows of 128,
-        # then 256 greedy decode steps at batch 64 from the empty static state.
-        log("C5 end-to-end stack (12 layers): graphed prefill and decode")
-        from koemi_amd import herm
-
-        settings = herm.HermSettings()
-        params = herm.prepare_stack(herm.init_stack(settings, 1005, device), settings, device)
-        ge = torch.Generator(device=device).manual_seed(1005)
-        ids = torch.randint(0, 256, (8, 2048), generator=ge, device=device)
-        start = herm.initial_states(settings, 8, device)
-        logits, _, graph = herm.prefill_graphed(params, settings, ids, start)
-        times = []
-        for _ in range(3):
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            logits, _, graph = herm.prefill_graphed(params, settings, ids, start, graph)
-            torch.cuda.synchronize()
-            times.append(time.perf_counter() - t0)
-        prefill_s = sorted(times)[1]
-        assert torch.isfinite(logits).all()
-        kernels["C5.prefill"] = {"ms": round(prefill_s * 1e3, 3), "tokens_per_s": round(ids.numel() / prefill_s),
-                                 "shape": "12 layers x [8, 2048], windows of 128",
-                                 "note": "bf16 projections (the reference's default GPU precision), fp32 state; "
-                                         "each window replayed from one HIP graph"}
-        del graph, logits, start
-        dids = torch.randint(0, 256, (64, 1), generator=ge, device=device)
-        decode = herm.DecodeGraph(params, settings, dids, herm.initial_states(settings, 64, device))
-        for _ in range(3):
-            decode.step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(256):
-            decode.step()
-        torch.cuda.synchronize()
-        decode_s = time.perf_counter() - t0
-        kernels["C5.decode"] = {"ms": round(decode_s * 1e3, 3), "ms_per_step": round(decode_s * 1e3 / 256, 4),
-                                "tokens_per_s": round(64 * 256 / decode_s), "shape": "12 layers, batch 64, 256 steps",
-                                "note": "greedy, padding id masked; each step replayed from one HIP graph"}
-        del decode, params
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None
     extras = {}
     if not args.no_cpu_baseline:
-        import oracle
-
-        log("CPU baseline (oracle C port, 1 thread)")
-        c = workloads.config2()
-        x32 = c.x.float().numpy()
-        g32 = c.gamma.float().numpy()
-        logits, targets, valid = c.logits.numpy(), c.targets.numpy(), c.valid.numpy()
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            oracle.rmsnorm_silu_f32(x32, g32, eps)
-            s_cpu = oracle.surprise_rows(logits, targets, valid)
-            oracle.admission(s_cpu, valid, q=q)
-            reps += 1
-            elapsed = time.perf_counter() - t0
-            if elapsed >= args.cpu_seconds or reps >= 1000:
-                break
-        cpu_value = reps * C2_TOKENS / elapsed
-        cpu_baseline = {"value": round(cpu_value, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-                        "sample": f"{reps} full C2 steps (32768 tokens each) with the oracle's C port, {elapsed:.1f} s"}
-        # the reference's PyTorch formulas (its CPU fallback path) on all host cores
-        import torch.nn.functional as F
-
         threads = len(os.sched_getaffinity(0))
-        torch.set_num_threads(threads)
-        x_t, g_t = c.x.float(), c.gamma.float()
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            F.silu(x_t * torch.rsqrt(x_t.square().mean(dim=-1, keepdim=True) + eps) * g_t)
-            nll = F.cross_entropy(c.logits, c.targets, reduction="none")
-            s_t = torch.where(c.valid, 1.0 - torch.exp(-(nll / math.log(256))), torch.zeros(()))
-            s_t > torch.quantile(s_t, q)
-            reps += 1
-            elapsed = time.perf_counter() - t0
-            if elapsed >= args.cpu_seconds / 2 or reps >= 1000:
-                break
-        extras["cpu_torch_reference_formulas"] = {"value": round(reps * C2_TOKENS / elapsed, 1), "unit": "tokens/s",
-                                                  "cores": threads, "sample": f"{reps} C2 steps, fp32 torch CPU"}
-        log("CPU reference formulas of the other rows")
-        cpu_rows = cpu_reference_times(extra, threads, budget_s=args.cpu_seconds / 4)
-        for key, row in cpu_rows.items():
-            if key in kernels and "ms" in kernels[key]:
-                row["gpu_speedup"] = round(row["ms"] / kernels[key]["ms"], 1)
-        extras["cpu_reference_rows"] = {"cores": threads, "rows": cpu_rows}
+        log(f"CPU baseline: torch block window on {threads} threads")
+        cpu_baseline = cpu_stack_baseline(threads, c5.prefill_ids[:, :C5_WINDOW].contiguous(), c5.decode_ids)
+        if extra:
+            log("CPU reference formulas of the kernel rows")
+            rows_cpu = cpu_reference_times(extra, threads, args.cpu_seconds)
+            for key, row in rows_cpu.items():
+                if key in kernels and "ms" in kernels[key]:
+                    row["gpu_speedup"] = round(row["ms"] / kernels[key]["ms"], 1)
+            extras["cpu_reference_rows"] = {"cores": threads, "rows": rows_cpu}
 
     result = {
-        "metric": "HERM tokens/s on 1 MI355X (C2: fused RMSNorm-SiLU + surprise + 0.9-quantile admission)",
+        "metric": "HERM tokens/s on 1 MI355X (C5: 12-layer HERM stack, prefill 8 x 2048)",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "C2: RMSNorm-SiLU of x bf16 [32768,512] (eps 1e-6) + surprise from logits fp32 [32768,256] "
-                        "+ admission above the 0.9 quantile; seeded inputs, rotated over "
-                        f"{n_sets} HBM-resident sets (> Infinity Cache); step = RMSNorm-SiLU on one graph branch, surprise -> "
-                        f"admission (partition + finish) on another (independent work), {per_graph} steps per HIP graph "
-                        "replay",
-            "tokens_per_step": C2_TOKENS,
-            "compute": "bf16 activations, fp32 arithmetic in every kernel",
-            "input_sets": n_sets,
+            "workload": "C5: random-initialised stack of 12 HERM blocks (width 1024, state 1024, 16 experts top-2 "
+                        "hash-routed, local and salient rings of 16, byte vocabulary + PAD); step = prefill of "
+                        "8 x 2048 seeded byte ids in windows of 128 (each window replayed from one HIP graph); "
+                        "decode = 256 greedy steps at batch 64",
+            "tokens_per_step": C5_PREFILL_TOKENS,
+            "decode_tokens_per_s": kernels.get("C5.decode", {}).get("tokens_per_s"),
+            "compute": "bf16 projections and expert FFNs with fp32 accumulation; fp32 state, memories and "
+                       "every other operation",
         },
-        "roofline": {**roofline(dom_gbs, HBM_PEAK_GBS, "GB/s", "hbm", load_traffic(f"C2.{dominant}")),
-                     "kernel": f"C2.{dominant}", "algorithmic_bytes": c2_bytes[dominant],
-                     "avg_ms": round(c2_times[dominant], 5)},
+        "roofline": headline_roofline,
         "cpu_baseline": cpu_baseline,
-        "eager_ms_per_step": round(eager_ms, 5),
         "kernels": kernels,
         **extras,
     }

@@ -15,6 +15,8 @@ kernels see identical bits. Seeds 1001-1005 name configurations C1-C5.
   ~ N(0, 1) fp32 [32768, 16]; W_g, W_v ~ N(0, 0.02^2) bf16 [16, 2816, 1024];
   W_o ~ N(0, 0.02^2) bf16 [16, 1024, 2816]; biases ~ N(0, 0.02^2); top-2.
   Hash variant: tok ~ U{0..255}, prev = tok shifted by one with PAD (256) first.
+* C5 HERM stack end to end: prefill ids ~ U{0..255} [8, 2048], decode ids
+  ~ U{0..255} [64, 1].
 """
 
 from __future__ import annotations
@@ -128,3 +130,19 @@ def to_device(obj, device: torch.device | str):
     fields = {name: getattr(obj, name) for name in obj.__dataclass_fields__}
     moved = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in fields.items()}
     return type(obj)(**moved)
+
+
+@dataclass
+class StackInputs:
+    prefill_ids: torch.Tensor  # int64 [8, 2048], U{0..255}
+    decode_ids: torch.Tensor   # int64 [64, 1], the first decode step's ids
+
+
+def config5(seed: int = 1005) -> StackInputs:
+    """C5 end-to-end: 8 x 2048 prefill byte ids, then greedy decode at batch 64
+    from 64 random first ids (the stack's weights: ``herm.init_stack(settings, seed)``)."""
+
+    g = _gen(seed)
+    prefill = torch.randint(0, 256, (8, 2048), generator=g, dtype=torch.int64)
+    decode = torch.randint(0, 256, (64, 1), generator=g, dtype=torch.int64)
+    return StackInputs(prefill, decode)
