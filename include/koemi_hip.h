@@ -139,6 +139,15 @@ int koemi_moe_route_hash(const void* token_ids, const void* previous_token_ids,
                          int32_t* duplicate_flag, int64_t tokens, int64_t expert_count,
                          int64_t top_k, koemi_stream_t stream);
 
+/* The synthetic "token id mod E" route of the benchmark's C4 hash variant
+ * (BASELINE configs[3]); no counterpart in the reference, whose hash route is
+ * koemi_moe_route_hash above. a[t, s] = (tok[t] + s) mod E (torch.remainder
+ * sign: in [0, E) for negative ids) for valid tokens, -1 otherwise; ids are
+ * I32 or I64. Slots never repeat an expert (s < E). */
+int koemi_moe_route_modulo(const void* token_ids, const uint8_t* valid_mask, int id_dtype,
+                           int64_t* assignments, int64_t tokens, int64_t expert_count, int64_t top_k,
+                           koemi_stream_t stream);
+
 /* Learned top-k gate of model/router.py:46-49: p = softmax(logits) in fp32,
  * (weights, assignments) = topk(p, k) in descending order, ties to the lower
  * expert index; invalid tokens get assignment -1 and weight 0.

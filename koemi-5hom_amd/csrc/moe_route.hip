@@ -47,6 +47,24 @@ __global__ void route_hash_kernel(const I* __restrict__ tok, const I* __restrict
     if (dup && dup_flag != nullptr) atomicOr(dup_flag, 1);
 }
 
+// The synthetic "token id mod E" route of the benchmark's hash variant: slot s
+// of a valid token takes expert (tok + s) mod E, with torch.remainder's sign
+// (the result is in [0, E) for negative ids too); invalid tokens -1. There is
+// no counterpart in the reference (its hash route is route_hash_kernel above).
+template <typename I>
+__global__ void route_modulo_kernel(const I* __restrict__ tok, const uint8_t* __restrict__ valid,
+                                    int64_t* __restrict__ out, int64_t T, int64_t E, int64_t k) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    int64_t* row = out + t * k;
+    const int64_t base = valid[t] ? static_cast<int64_t>(tok[t]) % E : 0;
+    for (int64_t s = 0; s < k; ++s) {
+        int64_t e = (base + s) % E;
+        e += e < 0 ? E : 0;
+        row[s] = valid[t] ? e : -1;
+    }
+}
+
 // softmax(logits) then top-k in descending probability, ties to the lower index
 // (router.py:46-49). Probabilities use the fixed exp of detmath.hpp and a
 // left-to-right sum so that weights are reproducible bit for bit.
@@ -168,6 +186,26 @@ extern "C" int koemi_moe_route_hash(const void* token_ids, const void* previous_
                            static_cast<const int64_t*>(previous_token_ids), valid_mask, assignments, duplicate_flag,
                            tokens, expert_count, top_k);
     return check_launch("koemi_moe_route_hash");
+}
+
+extern "C" int koemi_moe_route_modulo(const void* token_ids, const uint8_t* valid_mask, int id_dtype,
+                                      int64_t* assignments, int64_t tokens, int64_t expert_count, int64_t top_k,
+                                      koemi_stream_t stream) {
+    if (tokens < 0) return fail(KOEMI_ERR_INVALID, "token count must be non-negative");
+    if (expert_count < 1 || top_k < 1 || top_k > expert_count)
+        return fail(KOEMI_ERR_INVALID, "route needs 1 <= top_k <= expert_count");
+    if (!index_dtype(id_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "token ids must be int32 or int64");
+    if (tokens == 0) return KOEMI_OK;
+    if (!token_ids || !valid_mask || !assignments) return fail(KOEMI_ERR_INVALID, "route received a null pointer");
+    const dim3 grid(grid_for(tokens, 256)), block(256);
+    hipStream_t s = as_stream(stream);
+    if (id_dtype == KOEMI_I32)
+        hipLaunchKernelGGL(route_modulo_kernel<int32_t>, grid, block, 0, s, static_cast<const int32_t*>(token_ids),
+                           valid_mask, assignments, tokens, expert_count, top_k);
+    else
+        hipLaunchKernelGGL(route_modulo_kernel<int64_t>, grid, block, 0, s, static_cast<const int64_t*>(token_ids),
+                           valid_mask, assignments, tokens, expert_count, top_k);
+    return check_launch("koemi_moe_route_modulo");
 }
 
 extern "C" int koemi_moe_route_learned(const float* router_logits, const uint8_t* valid_mask,

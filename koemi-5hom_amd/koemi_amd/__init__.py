@@ -28,6 +28,7 @@ from koemi_amd.moe import (
     load_native_extension,
     permute_topk,
     route_topk_learned,
+    route_topk_modulo,
     route_topk_valid,
 )
 from koemi_amd.think import benchmark_causal_surprise, causal_surprise, salience_admission, surprise_from_logits
@@ -47,6 +48,7 @@ __all__ = [
     "native_cuda_available",
     "permute_topk",
     "route_topk_learned",
+    "route_topk_modulo",
     "route_topk_valid",
     "salience_admission",
     "read_local_window",

@@ -1,10 +1,13 @@
 """HERM block window and block stack on the GPU (the end-to-end configuration).
 
 ``block_window`` is ``KoemiModel.forward_window`` (reference model/network.py:
-296-441) under the settings the reference runs by default: ablation
-``no_refine`` (the memory value is the fast associative read), hash expert
-routing with the static dispatch (experts.py:109-150), static rings
-(``KoemiState.create_static``, state.py:43-76). Its hot-path operators run on
+296-441) under the ablation the reference runs by default, ``no_refine`` (the
+memory value is the fast associative read), with hash expert routing (the
+static dispatch, experts.py:109-150) or learned routing
+(``HermSettings.expert_routing = "learned"``: LearnedExpertMixture,
+router.py:43-97) and static rings (``KoemiState.create_static``,
+state.py:43-76). Reference checkpoints and ``KoemiState`` map onto this
+layout through ``koemi_amd.checkpoint``. Its hot-path operators run on
 this package's HIP kernels:
 
 * gates + masking + scan: one stacked GEMM for the two gate projections,
@@ -16,9 +19,11 @@ this package's HIP kernels:
 * local read: ``memory.read_local_window`` (memory.py:332-383);
 * salient read and ring update: ``memory.read_salient_window``,
   ``memory.salient_tail`` (memory.py:405-455);
-* experts: ``moe.route_topk_valid``, ``moe.permute_topk``,
-  ``moe.grouped_expert_mlp_inference``, ``moe.combine_topk`` (experts.py:
-  109-150, 283-289; layers.py:19-29).
+* experts: ``moe.route_topk_valid`` (hash) or the gate GEMM then
+  ``moe.route_topk_learned`` (learned), ``moe.permute_topk``,
+  ``moe.grouped_expert_mlp_inference``, ``moe.combine_topk`` (with the pair
+  weights when learned) (experts.py:109-150, 283-289; router.py:43-97;
+  layers.py:19-29).
 
 The projections are plain library GEMMs (``torch.nn.functional.linear`` on
 hipBLASLt) in ``HermSettings.linear_dtype`` with fp32 results; every other
@@ -133,6 +138,9 @@ def init_stack(settings: HermSettings, seed: int, device: torch.device | str = "
             p[name + "_w"] = torch.stack([w for w, _ in pairs])
             p[name + "_b"] = torch.stack([b for _, b in pairs])
         p["expert_norm"] = torch.ones(d, device=device)
+        if settings.expert_routing == "learned":
+            bound = 1.0 / math.sqrt(d)  # nn.Linear(d, E, bias=False) (router.py:41)
+            p["router_w"] = (torch.rand((e, d), generator=g, device=device) * 2.0 - 1.0) * bound
         p["head_w"], p["head_b"] = _linear_init(g, v, d)
         layers.append(p)
     return layers
@@ -175,6 +183,8 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
+        if "router_w" in p:
+            q["router_w"] = to(p["router_w"])
         q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"])
         q["content_w"] = to(p["head_w"][:PAD_TOKEN_ID])
         q["content_b"] = to(p["head_b"][:PAD_TOKEN_ID])
@@ -393,16 +403,27 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
     k = settings.top_k
-    assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
-                                       validate=False)
     flat = fused.reshape(-1, d)
     flat_valid = valid.reshape(-1)
+    if settings.expert_routing == "learned":
+        # LearnedExpertMixture (router.py:43-97): the bias-free gate on the fp32
+        # context (rows of invalid tokens are routed to -1 whatever their
+        # logits), softmax top-k, each pair weighted by its probability
+        router_logits = functional.linear(flat, p["router_w"])
+        assignments, weights = moe.route_topk_learned(router_logits, flat_valid, top_k=k)
+    else:
+        assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
+                                           validate=False)
+        weights = None
     moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
-    sorted_context, sorted_rows, sorted_experts, offsets = moe.permute_topk(
-        moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count, validate=False)
+    permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
+                                pair_weights=weights, validate=False)
+    sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
+    sorted_weights = permuted[4] if weights is not None else None
     expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
                                                   p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
-    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k, validate=False)
+    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
+                              pair_weights=sorted_weights, validate=False)
     final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
     logits = _linear(final, p["head_w"], p["head_b"]) if with_logits else None
 

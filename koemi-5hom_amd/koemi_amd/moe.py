@@ -178,6 +178,38 @@ def route_topk_valid(
     return assignments
 
 
+def route_topk_modulo(token_ids: Tensor, valid_mask: Tensor, *, expert_count: int, top_k: int) -> Tensor:
+    """The benchmark's synthetic "token id mod E" route (C4 hash variant, no
+    counterpart in the reference): slot ``s`` of a valid token takes expert
+    ``(token_id + s) mod expert_count`` (``torch.remainder`` sign), invalid
+    tokens ``-1``. Returns ``token_ids.shape + (top_k,)`` int64."""
+
+    tensors = {"token_ids": token_ids, "valid_mask": valid_mask}
+    for name, tensor in tensors.items():
+        _require_cuda_tensor(tensor, name)
+    _require_same_cuda_device(tensors)
+    if token_ids.dtype not in (torch.int32, torch.int64):
+        raise CudaMoeValidationError("token_ids must use int32 or int64")
+    if valid_mask.dtype != torch.bool:
+        raise CudaMoeValidationError("valid_mask must use boolean dtype")
+    if token_ids.shape != valid_mask.shape:
+        raise CudaMoeValidationError("routing tensors must have equal shapes")
+    expert_count = _require_positive_bounded(expert_count, "expert_count", 1 << 20)
+    top_k = _require_positive_bounded(top_k, "top_k", 256)
+    if top_k > expert_count:
+        raise CudaMoeValidationError("top_k must not exceed expert_count")
+    _require_library()
+    count = token_ids.numel()
+    assignments = torch.empty((count, top_k), device=token_ids.device, dtype=torch.int64)
+    if count:
+        token_ids, valid_mask = token_ids.contiguous(), valid_mask.contiguous()
+        with torch.cuda.device(token_ids.device):
+            _native.call("koemi_moe_route_modulo", token_ids.data_ptr(), valid_mask.data_ptr(),
+                         _native.dtype_code(token_ids.dtype), assignments.data_ptr(), count, expert_count, top_k,
+                         _native.stream_of(token_ids.device))
+    return assignments.reshape(*token_ids.shape, top_k)
+
+
 def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int) -> tuple[Tensor, Tensor]:
     """Learned softmax top-k gate (router.py:46-49): returns int64 assignments and
     fp32 weights of shape ``router_logits.shape[:-1] + (top_k,)``, descending by

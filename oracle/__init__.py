@@ -424,6 +424,15 @@ def route_hash(token_ids: np.ndarray, previous_token_ids: np.ndarray, valid: np.
     return np.where(np.asarray(valid, dtype=bool)[..., None], a, -1).astype(np.int64)
 
 
+def route_modulo(token_ids: np.ndarray, valid: np.ndarray, expert_count: int, top_k: int) -> np.ndarray:
+    """The benchmark's synthetic "token id mod E" variant (BASELINE configs[3];
+    no reference counterpart): slot s -> (tok + s) mod E with Python's
+    (torch.remainder's) sign; invalid -> -1."""
+
+    a = np.remainder(np.asarray(token_ids, np.int64)[..., None] + np.arange(top_k, dtype=np.int64), expert_count)
+    return np.where(np.asarray(valid, bool)[..., None], a, -1).astype(np.int64)
+
+
 def route_learned(router_logits: np.ndarray, valid: np.ndarray, top_k: int) -> tuple[np.ndarray, np.ndarray]:
     """router.py:46-49 with the kernel's rounding steps: (assignments, weights)."""
 

@@ -1,0 +1,130 @@
+"""The C5 workload on the GPU: 12 HERM blocks, width 1024, state 1024, 16
+experts top-2 (hash-routed), rings of 16, byte vocabulary + PAD, bf16
+projections and expert FFNs, admission threshold 0.75 -- the benchmark's
+configuration, at its shapes.
+
+* The prefill of 8 x 2048 ids (config5) replayed from the window graph:
+  finite logits of the right shape, the carried last tokens equal the last ids,
+  the local rings full of valid entries, the first window's graph replay equal
+  to the eager window (1e-5 of the logit scale: the same kernels; the library
+  GEMMs may be replayed from other algorithms inside the capture), and a
+  second replayed prefill bit-identical to the first.
+* The first layer's first 128-token window and one decode step at batch 64
+  (layer 0 with its token head) against oracle.herm in float64 on every row.
+  Tolerances for the bf16 path against float64: relative Frobenius error of
+  each output <= 2e-2 and max abs error <= 6e-2 of its largest magnitude (bf16
+  rounding, 2^-9 relative, of every GEMM operand: weights and activations of
+  the gate, working-state, fusion, expert and head products); the measured
+  errors are printed. The surprise scores within 2e-3 relative and the
+  admission masks equal wherever the oracle's score is 5e-3 or more from the
+  threshold.
+* Decode steps replayed from the decode graph equal eager steps (ids exact,
+  logits 1e-5 of scale).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+from koemi_amd import herm, workloads
+from oracle import herm as oherm
+
+pytestmark = pytest.mark.gpu
+
+WINDOW = 128
+
+
+@pytest.fixture(scope="module")
+def c5(device):
+    settings = herm.HermSettings()
+    assert (settings.layers, settings.width, settings.expert_count, settings.top_k) == (12, 1024, 16, 2)
+    assert settings.linear_dtype == torch.bfloat16 and settings.salience_threshold == 0.75
+    raw = herm.init_stack(settings, 1005, device)
+    params = herm.prepare_stack(raw, settings, device)
+    return settings, raw, params
+
+
+def _report(name, got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = float(np.abs(want).max()) + 1e-30
+    rel = float(np.linalg.norm(got - want) / (np.linalg.norm(want) + 1e-30))
+    mx = float(np.abs(got - want).max()) / scale
+    print(f"{name}: rel_frobenius={rel:.3e} max_abs/scale={mx:.3e}", flush=True)
+    assert rel <= 2e-2, name
+    assert mx <= 6e-2, name
+
+
+def test_c5_prefill_properties_and_graph_replay(device, c5):
+    settings, _, params = c5
+    ids = workloads.config5().prefill_ids.to(device)
+    batch = ids.shape[0]
+    eager_logits, _ = herm.stack_window(params, settings, ids[:, :WINDOW].contiguous(),
+                                        herm.initial_states(settings, batch, device))
+    logits, states, graph = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, batch, device))
+    torch.cuda.synchronize()
+    assert logits.shape == (batch, ids.shape[1], settings.vocabulary_size)
+    assert torch.isfinite(logits).all()
+    scale = float(eager_logits.abs().max())
+    assert float((logits[:, :WINDOW] - eager_logits).abs().max()) <= 1e-5 * scale
+    first = logits.clone()
+    for layer, st in enumerate(states):
+        assert torch.equal(st["last_token"], ids[:, -1]), f"layer {layer} last token"
+        assert bool(st["local_valid"].all()), f"layer {layer} local ring"
+        assert st["salient_valid"].shape == (batch, settings.salience_memory_size)
+        assert torch.isfinite(st["working"]).all() and torch.isfinite(st["basis"]).all()
+    again, _, graph = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, batch, device), graph)
+    torch.cuda.synchronize()
+    assert torch.equal(again, first)
+
+
+def _oracle_layer(raw_layer):
+    return {k: v.double().cpu().numpy() for k, v in raw_layer.items()}
+
+
+def test_c5_first_layer_window_and_decode_step_match_the_oracle(device, c5):
+    settings, raw, params = c5
+    cfg = settings.oracle_config()
+    p_np = _oracle_layer(raw[0])
+    c = workloads.config5()
+    for name, ids in (("prefill window", c.prefill_ids[:, :WINDOW].contiguous()), ("decode step", c.decode_ids)):
+        batch = ids.shape[0]
+        state = herm.initial_states(dataclasses.replace(settings, layers=1), batch, device)[0]
+        logits, final, nxt, surprise = herm.block_window(params[0], settings, ids.to(device), state)
+        torch.cuda.synchronize()
+        w_logits, w_final, w_next, w_surprise, w_adm = oherm.block_window(p_np, oherm.initial_state(batch, cfg),
+                                                                          ids.numpy(), cfg)
+        _report(f"{name} logits", logits.cpu().numpy(), w_logits)
+        _report(f"{name} final context", final.cpu().numpy(), w_final)
+        for key in ("working", "basis", "normalizer", "local_keys", "local_values"):
+            _report(f"{name} {key}", nxt[key].cpu().numpy(), w_next[key])
+        got_s = surprise.cpu().numpy()
+        assert np.all(np.abs(got_s - w_surprise) <= 2e-3 * np.abs(w_surprise) + 1e-6), name
+        clear = np.abs(w_surprise - settings.salience_threshold) >= 5e-3
+        got_adm = (got_s > settings.salience_threshold) & (ids.numpy() != herm.PAD_TOKEN_ID)
+        np.testing.assert_array_equal(got_adm[clear], w_adm[clear])
+        np.testing.assert_array_equal(nxt["last_token"].cpu().numpy(), w_next["last_token"])
+        np.testing.assert_array_equal(nxt["local_valid"].cpu().numpy(), w_next["local_valid"])
+        print(f"{name}: admitted (oracle) {int(w_adm.sum())} of {w_adm.size}", flush=True)
+
+
+def test_c5_decode_graph_replays_equal_eager_steps(device, c5):
+    settings, _, params = c5
+    ids = workloads.config5().decode_ids.to(device)
+    batch = ids.shape[0]
+    decode = herm.DecodeGraph(params, settings, ids, herm.initial_states(settings, batch, device))
+    eager_ids, eager_states = ids.clone(), herm.initial_states(settings, batch, device)
+    for step in range(4):
+        logits = decode.run().clone()
+        eager_logits, eager_states = herm.stack_window(params, settings, eager_ids, eager_states)
+        torch.cuda.synchronize()
+        scale = float(eager_logits.abs().max())
+        assert float((logits - eager_logits).abs().max()) <= 1e-5 * scale, f"step {step}"
+        scores = eager_logits[:, -1].clone()
+        scores[:, herm.PAD_TOKEN_ID] = float("-inf")
+        eager_ids = scores.argmax(dim=-1, keepdim=True)
+        assert torch.equal(decode.ids, eager_ids), f"step {step}"

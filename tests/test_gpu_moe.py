@@ -64,6 +64,32 @@ def test_config4_hash_route_bit_exact(device, id_dtype):
     np.testing.assert_array_equal(counts.cpu().numpy(), oracle.expert_counts(want, c.valid.numpy(), 16))
 
 
+@pytest.mark.parametrize("id_dtype", [torch.int64, torch.int32])
+def test_config4_modulo_route_bit_exact(device, id_dtype):
+    """The C4 synthetic variant "token id mod 16" (slot k -> (tok + k) mod 16):
+    assignments, counts and the permutation bit-exact against the oracle, with
+    some tokens invalid and, in a second call, negative ids."""
+
+    c = workloads.config4()
+    valid = c.valid.clone()
+    valid[5::113] = False
+    got = moe.route_topk_modulo(c.token_ids.to(device, id_dtype), valid.to(device), expert_count=16, top_k=2)
+    want = oracle.route_modulo(c.token_ids.numpy(), valid.numpy(), 16, 2)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    counts = moe.expert_activation_counts(got, valid.to(device), expert_count=16)
+    np.testing.assert_array_equal(counts.cpu().numpy(), oracle.expert_counts(want, valid.numpy(), 16))
+    sc, rows, experts, offsets = moe.permute_topk(c.context.to(device), got, valid.to(device), expert_count=16)
+    w_sc, w_rows, w_experts, w_off = oracle.permute(bf16_np(c.context), want, valid.numpy(), 16)
+    np.testing.assert_array_equal(rows.cpu().numpy(), w_rows)
+    np.testing.assert_array_equal(experts.cpu().numpy(), w_experts)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), w_off)
+    np.testing.assert_array_equal(bf16_np(sc), w_sc)
+    neg = torch.arange(-40, 40, dtype=id_dtype, device=device)
+    ok = torch.ones(80, dtype=torch.bool, device=device)
+    np.testing.assert_array_equal(moe.route_topk_modulo(neg, ok, expert_count=7, top_k=3).cpu().numpy(),
+                                  oracle.route_modulo(neg.cpu().numpy(), ok.cpu().numpy(), 7, 3))
+
+
 def test_route_rejects_duplicate_slots(device):
     tok = torch.arange(64, device=device)
     with pytest.raises(moe.CudaMoeValidationError, match="duplicate experts"):

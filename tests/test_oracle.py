@@ -424,6 +424,22 @@ def test_network_hash_route_known_answer():
     assert oracle.expert_counts(a, valid, kat["expert_count"]).tolist() == kat["activation_counts"]
 
 
+def test_modulo_route_known_answer_and_torch_expression():
+    """The synthetic "token id mod 16" variant: slot s -> (tok + s) mod 16,
+    hand-computed, and torch.remainder's expression on random ids (negative
+    ids included, for the sign convention)."""
+
+    tok = np.array([0, 15, 16, 17, 255, 256, 3])
+    valid = np.array([True, True, True, True, True, False, True])
+    got = oracle.route_modulo(tok, valid, 16, 2)
+    assert got.tolist() == [[0, 1], [15, 0], [0, 1], [1, 2], [15, 0], [-1, -1], [3, 4]]
+    g = torch.Generator().manual_seed(5)
+    ids = torch.randint(-300, 300, (2048,), generator=g)
+    ok = torch.rand((2048,), generator=g) < 0.9
+    want = (ids.unsqueeze(-1) + torch.arange(3)).remainder(13).masked_fill(~ok.unsqueeze(-1), -1)
+    np.testing.assert_array_equal(oracle.route_modulo(ids.numpy(), ok.numpy(), 13, 3), want.numpy())
+
+
 def test_hash_route_properties_of_the_reference_dispatch_tests():
     six = oracle.route_hash(np.array([[97, 98, 99]]), np.array([[32, 97, 98]]), np.ones((1, 3), bool), 128, 6)
     assert all(len(set(row)) == 6 for row in six[0].tolist())
