@@ -126,6 +126,22 @@ int koemi_admission_quantile(const float* surprise, const uint8_t* valid_mask, u
                              float* threshold_out, int64_t count, float quantile, void* workspace,
                              size_t workspace_bytes, koemi_stream_t stream);
 
+/* koemi_admission_quantile without a caller workspace and without any
+ * allocation: no counterpart in the reference. It is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The partitioned select's records and
+ * candidate slots live in a static device array of 263,424 bytes per GPU
+ * (held until the process ends), enough for every count; counts needing more
+ * are rejected (KOEMI_ERR_UNSUPPORTED). The array's device address is resolved
+ * once per device on the first call there (hipGetSymbolAddress, with that
+ * device current). Every call on one GPU shares its array, and nothing in it
+ * needs to start at zero: calls on one GPU that overlap in time (different
+ * streams without ordering) race and must not be issued. Same inputs, outputs
+ * and results as koemi_admission_quantile. */
+int koemi_admission_quantile_noalloc(const float* surprise, const uint8_t* valid_mask, uint8_t* admission,
+                                     float* threshold_out, int64_t count, float quantile,
+                                     koemi_stream_t stream);
+
 /* ------------------------------------------------------------------ moe --- */
 /* Replaces `route_topk(tok, prev, valid, E, k)` of moe/moe_kernels.cpp:193-201
  * with the int64 semantics of the PyTorch oracle (model/experts.py:283-289):

@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "detmath.hpp"
 
+#include <mutex>
 #include <type_traits>
 
 namespace koemi {
@@ -1151,9 +1152,67 @@ inline bool partitioned(int64_t count) {
     return count > kPartitionMin && count <= kPartMax;
 }
 
+namespace {
+
+// The no-alloc entry point's workspace: one static device array per GPU, sized
+// for the largest partitioned input (32 workgroup records and 2 x 32 x 1024
+// candidate slots: 257 KiB). Inputs outside the partitioned range need no
+// workspace, so every count fits.
+constexpr size_t kQuantileScratchBytes = 256 + ((size_t(kPartMaxGroups) * kRecordWords * 4 + 255) & ~size_t(255)) +
+                                         2 * ((size_t(kPartMaxGroups) * 1024 * 4 + 255) & ~size_t(255));
+__device__ __align__(256) uint8_t scratch[kQuantileScratchBytes];
+
+// Device address of `scratch` on each GPU, resolved once per device (with the
+// device current) by the first no-alloc call there. In host code `scratch`
+// names a host-side stand-in, never the device memory: only these addresses
+// are passed to kernels.
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+void* g_scratch_ptr[kMaxScratchDevices];
+hipError_t g_scratch_status[kMaxScratchDevices];
+
+int scratch_for_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+        return fail(KOEMI_ERR_LAUNCH, "quantile admission (no alloc): no current device");
+    if (dev >= kMaxScratchDevices)
+        return fail(KOEMI_ERR_UNSUPPORTED, "quantile admission (no alloc): device %d beyond the %d supported", dev,
+                    kMaxScratchDevices);
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* p = nullptr;
+        g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = p;
+    });
+    if (g_scratch_status[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
+        return fail(KOEMI_ERR_LAUNCH, "quantile admission (no alloc): hipGetSymbolAddress failed on device %d (%s)", dev,
+                    hipGetErrorString(g_scratch_status[dev]));
+    *out = g_scratch_ptr[dev];
+    return KOEMI_OK;
+}
+
+}  // namespace
+
 extern "C" size_t koemi_admission_quantile_workspace_bytes(int64_t count) {
     if (!partitioned(count)) return 0;
     return part_workspace(count).total;
+}
+
+extern "C" int koemi_admission_quantile_noalloc(const float* surprise, const uint8_t* valid_mask,
+                                                uint8_t* admission, float* threshold_out, int64_t count,
+                                                float quantile, koemi_stream_t stream) {
+    if (count < 1) return fail(KOEMI_ERR_INVALID, "quantile admission needs at least one score");
+    if (count > 0xffffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "quantile admission supports at most 2^32-1 scores");
+    const size_t need = partitioned(count) ? part_workspace(count).total : 0;
+    if (need > kQuantileScratchBytes)
+        return fail(KOEMI_ERR_UNSUPPORTED, "quantile admission (no alloc): %zu workspace bytes exceed the %zu-byte "
+                    "static scratch", need, kQuantileScratchBytes);
+    void* ws = nullptr;
+    if (need) {
+        const int st = scratch_for_current_device(&ws);
+        if (st != KOEMI_OK) return st;
+    }
+    return koemi_admission_quantile(surprise, valid_mask, admission, threshold_out, count, quantile, ws,
+                                    need ? kQuantileScratchBytes : 0, stream);
 }
 
 extern "C" int koemi_admission_quantile(const float* surprise, const uint8_t* valid_mask,

@@ -73,6 +73,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_admission_threshold": (c_int, (_P, _P, _P, c_int64, c_float, c_int, _P)),
     "koemi_admission_quantile_workspace_bytes": (c_size_t, (c_int64,)),
     "koemi_admission_quantile": (c_int, (_P, _P, _P, _P, c_int64, c_float, _P, c_size_t, _P)),
+    "koemi_admission_quantile_noalloc": (c_int, (_P, _P, _P, _P, c_int64, c_float, _P)),
     "koemi_moe_route_hash": (c_int, (_P, _P, _P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_route_modulo": (c_int, (_P, _P, c_int, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_route_learned": (c_int, (_P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
