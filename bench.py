@@ -6,7 +6,10 @@ configuration): a random-initialised stack of 12 HERM blocks (width 1024,
 state 1024, 16 experts top-2, byte vocabulary + PAD). One step is one prefill
 of 8 x 2048 byte ids through all 12 layers in windows of 128 tokens (the state
 carried from window to window), with the ids, the weights and the state
-resident in HBM. ``value`` is prefill HERM tokens/s over K steps; greedy
+resident in HBM; the (layer, window) HIP graphs run as a wavefront over
+per-layer streams (``herm.WavefrontPrefill``), checked bit for bit against the
+window-by-window prefill, whose rate is reported too. ``value`` is prefill
+HERM tokens/s over K steps; greedy
 decode tokens/s (256 steps at batch 64, fixed-shape state) is reported beside
 it under ``kernels["C5.decode"]``.
 
@@ -465,36 +468,54 @@ def main() -> int:
     ids = c5.prefill_ids.to(device)
     start_states = herm.initial_states(settings, C5_BATCH, device)
 
-    log("C5: capturing the window graph; eager first window for the replay check")
+    log("C5: window-by-window graphed prefill (eager first window for the replay check)")
     eager_logits, _ = herm.stack_window(params, settings, ids[:, :C5_WINDOW].contiguous(),
                                         herm.initial_states(settings, C5_BATCH, device))
-    logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states)
+    sequential, _, graph = herm.prefill_graphed(params, settings, ids, start_states)
     torch.cuda.synchronize()
-    first = logits[:, :C5_WINDOW].clone()
-    replay_vs_eager = float((first - eager_logits).abs().max() / eager_logits.abs().max())
+    replay_vs_eager = float((sequential[:, :C5_WINDOW] - eager_logits).abs().max() / eager_logits.abs().max())
     assert replay_vs_eager < 1e-5, f"graph replay differs from the eager window: {replay_vs_eager:.3e}"
-    assert torch.isfinite(logits).all(), "non-finite prefill logits"
-    reference_logits = logits.clone()
+    assert torch.isfinite(sequential).all(), "non-finite prefill logits"
+    seq_steps = 3
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(seq_steps):
+        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
+    torch.cuda.synchronize()
+    seq_ms = (time.perf_counter() - t0) * 1000.0 / seq_steps
+    assert torch.equal(logits, sequential), "window-by-window prefill is not reproducible"
+    kernels["C5.prefill_window_by_window"] = {"ms_per_step": round(seq_ms, 4),
+                                              "tokens_per_s": round(C5_PREFILL_TOKENS / (seq_ms / 1000.0), 1),
+                                              "replay_vs_eager_rel": replay_vs_eager,
+                                              "note": "every layer of a window in one HIP graph, windows in turn"}
+    del graph, logits, eager_logits
+
+    log("C5: wavefront prefill (per-layer streams): capture and equality with the window-by-window prefill")
+    wave = herm.WavefrontPrefill(params, settings, start_states, C5_BATCH, device)
+    logits = wave.run(ids)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, sequential), "wavefront prefill differs from the window-by-window prefill"
 
     log(f"C5: {args.warmup} warmup + {args.steps} timed prefill steps")
     for _ in range(args.warmup):
-        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
+        logits = wave.run(ids)
     torch.cuda.synchronize()
     start_ev, end_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start_ev.record(stream)
     for _ in range(args.steps):
-        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
+        logits = wave.run(ids)
     end_ev.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = start_ev.elapsed_time(end_ev)
     ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
     value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
-    assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
+    assert torch.equal(logits, sequential), "prefill steps are not reproducible"
     kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
-                             "replay_vs_eager_rel": replay_vs_eager}
-    del graph, logits, reference_logits, eager_logits, first
+                             "schedule": "wavefront: layer l's window w on layer l's stream after window w of "
+                                         "layer l - 1; each layer window replayed from a HIP graph"}
+    del wave, logits, sequential
 
     if not args.headline_only:
         log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
@@ -731,8 +752,8 @@ def main() -> int:
         "config": {
             "workload": "C5: random-initialised stack of 12 HERM blocks (width 1024, state 1024, 16 experts top-2 "
                         "hash-routed, local and salient rings of 16, byte vocabulary + PAD); step = prefill of "
-                        "8 x 2048 seeded byte ids in windows of 128 (each window replayed from one HIP graph); "
-                        "decode = 256 greedy steps at batch 64",
+                        "8 x 2048 seeded byte ids in windows of 128, the (layer, window) graphs scheduled as a "
+                        "wavefront over per-layer streams; decode = 256 greedy steps at batch 64",
             "tokens_per_step": C5_PREFILL_TOKENS,
             "decode_tokens_per_s": kernels.get("C5.decode", {}).get("tokens_per_s"),
             "compute": "bf16 projections and expert FFNs with fp32 accumulation; fp32 state, memories and "

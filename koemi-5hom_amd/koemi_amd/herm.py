@@ -62,6 +62,7 @@ __all__ = [
     "HermSettings",
     "PAD_TOKEN_ID",
     "block_window",
+    "WavefrontPrefill",
     "WindowGraph",
     "associative_scan_read",
     "decode_step",
@@ -573,3 +574,109 @@ def prefill_graphed(params: list[dict[str, Tensor]], settings: HermSettings, ids
     for begin in range(0, length, chunk):
         pieces.append(graph.run(ids[:, begin:begin + chunk]).clone())
     return torch.cat(pieces, dim=1), graph.states, graph
+
+
+class WavefrontPrefill:
+    """``prefill`` of the whole stack with the layer windows scheduled as a wavefront.
+
+    Window ``w`` of layer ``l`` needs only window ``w - 1`` of the same layer
+    (the carried state) and window ``w`` of layer ``l - 1`` (its final
+    context), so every (layer, window) pair on an anti-diagonal ``l + w = d``
+    is independent of the others. Each layer runs on its own stream of default
+    priority; window ``w`` of layer ``l`` waits (HIP events) for window ``w`` of
+    layer ``l - 1`` and, before overwriting its output buffer, for window
+    ``w - 2`` of layer ``l + 1``, which read it. Small latency-bound kernels of
+    different layers then overlap on the GPU instead of running one after the
+    other, and the results are those of ``prefill`` bit for bit (the same
+    kernels on the same inputs).
+
+    Each layer's window is captured twice (output buffers alternate by window
+    parity) into HIP graphs with static inputs: the window's ids (copied in on
+    the layer's stream), the previous layer's output of the same parity, and
+    the layer's state, which every replay advances in place. ``run(ids)``
+    resets the state to ``states`` (as given at construction, or the
+    ``states`` argument) and returns the last layer's logits of every window;
+    ``self.states`` holds the final states. Fixed (batch, scan_chunk) shapes;
+    the sequence length must be a multiple of ``scan_chunk``.
+    """
+
+    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
+                 batch: int, device: torch.device) -> None:
+        self.params, self.settings = params, settings
+        self.layers = len(params)
+        chunk = settings.scan_chunk
+        self.start = [{k: v.clone() for k, v in st.items()} for st in states]
+        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
+        self.streams = [torch.cuda.Stream(device) for _ in range(self.layers)]
+        self.ids_in = [[torch.zeros((batch, chunk), dtype=torch.int64, device=device) for _ in range(2)]
+                       for _ in range(self.layers)]
+        # warm the libraries up outside the capture: one eager window on throwaway states
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            warm = [{k: v.clone() for k, v in st.items()} for st in states]
+            for _ in range(2):
+                _, warm = stack_window(params, settings, self.ids_in[0][0], warm)
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize(device)
+        self.graphs: list[list[torch.cuda.CUDAGraph]] = []
+        self.out: list[list[Tensor]] = []
+        self.logits: list[Tensor | None] = [None, None]
+        for layer in range(self.layers):
+            graphs, outs = [], []
+            for parity in range(2):
+                g = torch.cuda.CUDAGraph()
+                context = self.out[layer - 1][parity] if layer else None
+                last = layer == self.layers - 1
+                with torch.cuda.graph(g):
+                    logits, final, nxt, _ = block_window(params[layer], settings, self.ids_in[layer][parity],
+                                                         self.states[layer], context, with_logits=last)
+                    keys = list(self.states[layer])
+                    torch._foreach_copy_([self.states[layer][k] for k in keys], [nxt[k] for k in keys])
+                graphs.append(g)
+                outs.append(final)
+                if last:
+                    self.logits[parity] = logits
+            self.graphs.append(graphs)
+            self.out.append(outs)
+        torch.cuda.synchronize(device)
+
+    def run(self, ids: Tensor, states: list[dict[str, Tensor]] | None = None) -> Tensor:
+        batch, length = ids.shape
+        chunk = self.settings.scan_chunk
+        if length % chunk or batch != self.ids_in[0][0].shape[0]:
+            raise ValueError("WavefrontPrefill.run needs the captured batch and a length that is a multiple of "
+                             "scan_chunk")
+        windows = length // chunk
+        current = torch.cuda.current_stream(ids.device)
+        source = self.start if states is None else states
+        for state, start in zip(self.states, source):
+            for key, tensor in state.items():
+                tensor.copy_(start[key])
+        vocab = self.logits[0].shape[-1]
+        logits = torch.empty((batch, length, vocab), device=ids.device, dtype=self.logits[0].dtype)
+        ready = current.record_event()
+        for stream in self.streams:
+            stream.wait_event(ready)
+        done: list[list[torch.cuda.Event | None]] = [[None] * windows for _ in range(self.layers)]
+        last = self.layers - 1
+        for diagonal in range(windows + self.layers - 1):
+            for layer in range(self.layers):
+                w = diagonal - layer
+                if not 0 <= w < windows:
+                    continue
+                stream, parity = self.streams[layer], w % 2
+                with torch.cuda.stream(stream):
+                    if layer:
+                        stream.wait_event(done[layer - 1][w])
+                    if layer < last and w >= 2:
+                        stream.wait_event(done[layer + 1][w - 2])  # the reader of this parity's output
+                    self.ids_in[layer][parity].copy_(ids[:, w * chunk:(w + 1) * chunk])
+                    self.graphs[layer][parity].replay()
+                    if layer == last:
+                        logits[:, w * chunk:(w + 1) * chunk].copy_(self.logits[parity])
+                    done[layer][w] = stream.record_event()
+        for stream in self.streams:
+            current.wait_stream(stream)
+        logits.record_stream(self.streams[last])
+        return logits

@@ -249,3 +249,24 @@ def test_bf16_copies_written_by_the_kernels_equal_the_casts(device):
     _native.call("koemi_herm_concat_bf16", *(_native.ptr(p) for p in pieces), 4, 35, 64, _native.ptr(cat16),
                  _native.stream_of(device))
     assert torch.equal(cat16, torch.cat(pieces, dim=-1).to(torch.bfloat16))
+
+
+def test_wavefront_prefill_equals_the_window_by_window_prefill(device):
+    """Layer windows scheduled as a wavefront on per-layer streams give the
+    sequential prefill's logits and states bit for bit (same kernels, same
+    inputs), over five windows and three layers, with admissions."""
+
+    b = 2
+    settings = _settings(layers=3, salience_threshold=0.55)
+    params = herm.prepare_stack(_params(settings, seed=21), settings, device)
+    ids = torch.from_numpy(_ids(b, 30, seed=8)).to(device)
+    want_logits, want_states, _ = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, b, device))
+    wave = herm.WavefrontPrefill(params, settings, herm.initial_states(settings, b, device), b, device)
+    for run in range(2):
+        logits = wave.run(ids)
+        torch.cuda.synchronize()
+        assert torch.equal(logits, want_logits), f"run {run}"
+        for got, want in zip(wave.states, want_states):
+            for key, tensor in want.items():
+                assert torch.equal(got[key], tensor), f"run {run} {key}"
+    assert any(bool(st["salient_valid"].any()) for st in want_states)

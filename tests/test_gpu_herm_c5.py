@@ -12,14 +12,19 @@ configuration, at its shapes.
 * The first layer's first 128-token window and one decode step at batch 64
   (layer 0 with its token head) against oracle.herm in float64 on every row.
   Tolerances for the bf16 path against float64: relative Frobenius error of
-  each output <= 2e-2 and max abs error <= 6e-2 of its largest magnitude (bf16
-  rounding, 2^-9 relative, of every GEMM operand: weights and activations of
-  the gate, working-state, fusion, expert and head products); the measured
-  errors are printed. The surprise scores within 2e-3 relative and the
-  admission masks equal wherever the oracle's score is 5e-3 or more from the
-  threshold.
+  each output <= 1e-2 and max abs error <= 1.5e-2 of its largest magnitude,
+  about five bf16 unit roundoffs (2^-9): every GEMM operand (weights and
+  activations of the gate, working-state, fusion, expert and head products)
+  is rounded to bf16 and about two such products feed each output in series
+  (measured: 2.4e-3 to 4.3e-3, normalizer 1e-3). The surprise scores within
+  2e-3 relative and the admission masks equal wherever the oracle's score is
+  5e-3 or more from the threshold (with the random-initialised head every
+  score is near 1 - 1/e, below the 0.75 threshold: nothing is admitted at
+  this configuration; the reference fixtures cover admission).
 * Decode steps replayed from the decode graph equal eager steps (ids exact,
   logits 1e-5 of scale).
+* The wavefront prefill (per-layer streams) equals the window-by-window
+  prefill bit for bit.
 """
 
 from __future__ import annotations
@@ -55,8 +60,8 @@ def _report(name, got, want):
     rel = float(np.linalg.norm(got - want) / (np.linalg.norm(want) + 1e-30))
     mx = float(np.abs(got - want).max()) / scale
     print(f"{name}: rel_frobenius={rel:.3e} max_abs/scale={mx:.3e}", flush=True)
-    assert rel <= 2e-2, name
-    assert mx <= 6e-2, name
+    assert rel <= 1e-2, name
+    assert mx <= 1.5e-2, name
 
 
 def test_c5_prefill_properties_and_graph_replay(device, c5):
@@ -128,3 +133,17 @@ def test_c5_decode_graph_replays_equal_eager_steps(device, c5):
         scores[:, herm.PAD_TOKEN_ID] = float("-inf")
         eager_ids = scores.argmax(dim=-1, keepdim=True)
         assert torch.equal(decode.ids, eager_ids), f"step {step}"
+
+
+def test_c5_wavefront_prefill_equals_the_window_by_window_prefill(device, c5):
+    settings, _, params = c5
+    ids = workloads.config5().prefill_ids.to(device)
+    batch = ids.shape[0]
+    want, want_states, _ = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, batch, device))
+    wave = herm.WavefrontPrefill(params, settings, herm.initial_states(settings, batch, device), batch, device)
+    logits = wave.run(ids)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, want)
+    for got, exp in zip(wave.states, want_states):
+        for key, tensor in exp.items():
+            assert torch.equal(got[key], tensor), key
