@@ -6,17 +6,21 @@ configuration): a random-initialised stack of 12 HERM blocks (width 1024,
 state 1024, 16 experts top-2, byte vocabulary + PAD). One step is one prefill
 of 8 x 2048 byte ids through all 12 layers in windows of 128 tokens (the state
 carried from window to window), with the ids, the weights and the state
-resident in HBM; the (layer, window) HIP graphs run as a wavefront over
-per-layer streams (``herm.WavefrontPrefill``), checked bit for bit against the
-window-by-window prefill, whose rate is reported too. ``value`` is prefill
-HERM tokens/s over K steps; greedy
+resident in HBM. The prefill runs sequence-parallel (``herm.SequencePrefill``:
+each layer over all positions at once, the state carried into every window
+formed by one scan, window rings and a windowed associative memory; the whole
+stack replayed from one HIP graph), checked against the window-by-window
+prefill (within the bf16 path's rounding), whose rate is reported beside it
+with that of the wavefront schedule (``herm.WavefrontPrefill``, bit-identical
+to it). ``value`` is prefill HERM tokens/s over K steps; greedy
 decode tokens/s (256 steps at batch 64, fixed-shape state) is reported beside
 it under ``kernels["C5.decode"]``.
 
-``roofline`` is the prefill's dominant hand-written kernel, timed live with
-HIP events on its launch stream over graphs of repeated launches at the exact
-per-window shape (its expert segments come from the same ids), with inputs
-and weights rotated so the Infinity Cache cannot hold them.
+``roofline`` is the prefill's dominant hand-written kernel, the grouped
+expert FFN of one layer over the whole prefill, timed live with HIP events on
+its launch stream over graphs of repeated launches at the exact shape (its
+expert segments come from the same ids), with weights rotated so the Infinity
+Cache cannot hold them.
 
 ``cpu_baseline`` is the reference's block window restated in PyTorch on the
 host (oracle/herm_torch.py: the reference's forward_window formulas with its
@@ -61,8 +65,8 @@ C5_LAYERS, C5_WIDTH, C5_HIDDEN, C5_E, C5_K = 12, 1024, 2048, 16, 2
 C5_BATCH, C5_LEN, C5_WINDOW = 8, 2048, 128
 C5_PREFILL_TOKENS = C5_BATCH * C5_LEN
 C5_DECODE_BATCH, C5_DECODE_STEPS = 64, 256
-C5_WINDOW_PAIRS = C5_BATCH * C5_WINDOW * C5_K
-C5_FFN_FLOP = 6 * C5_WIDTH * C5_HIDDEN * C5_WINDOW_PAIRS            # GEMM 1 (gate + value) + GEMM 2, per window
+C5_PAIRS = C5_PREFILL_TOKENS * C5_K
+C5_FFN_FLOP = 6 * C5_WIDTH * C5_HIDDEN * C5_PAIRS                   # GEMM 1 (gate + value) + GEMM 2, per layer
 
 # Algorithmic bytes / FLOPs per launch of the other rows.
 C2_TOKENS = 16 * 2048
@@ -403,6 +407,53 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
     return 0
 
 
+def window_by_window_rows(args, herm, params, settings, ids, start_states, kernels: dict):
+    """The C5 prefill window by window (every layer of a window in one HIP
+    graph, windows in turn) and as a wavefront over per-layer streams
+    (bit-identical to it): rates into ``kernels``; returns its logits."""
+
+    import torch
+
+    log("C5: window-by-window graphed prefill (eager first window for the replay check)")
+    eager_logits, _ = herm.stack_window(params, settings, ids[:, :C5_WINDOW].contiguous(),
+                                        herm.initial_states(settings, C5_BATCH, ids.device))
+    sequential, _, graph = herm.prefill_graphed(params, settings, ids, start_states)
+    torch.cuda.synchronize()
+    replay_vs_eager = float((sequential[:, :C5_WINDOW] - eager_logits).abs().max() / eager_logits.abs().max())
+    assert replay_vs_eager < 1e-5, f"graph replay differs from the eager window: {replay_vs_eager:.3e}"
+    assert torch.isfinite(sequential).all(), "non-finite prefill logits"
+    seq_steps = 3
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(seq_steps):
+        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
+    torch.cuda.synchronize()
+    seq_ms = (time.perf_counter() - t0) * 1000.0 / seq_steps
+    assert torch.equal(logits, sequential), "window-by-window prefill is not reproducible"
+    kernels["C5.prefill_window_by_window"] = {"ms_per_step": round(seq_ms, 4),
+                                              "tokens_per_s": round(C5_PREFILL_TOKENS / (seq_ms / 1000.0), 1),
+                                              "replay_vs_eager_rel": replay_vs_eager,
+                                              "note": "every layer of a window in one HIP graph, windows in turn"}
+    del graph, logits, eager_logits
+
+    log("C5: wavefront prefill (per-layer streams): capture and equality with the window-by-window prefill")
+    wave = herm.WavefrontPrefill(params, settings, start_states, C5_BATCH, ids.device)
+    logits = wave.run(ids)
+    torch.cuda.synchronize()
+    assert torch.equal(logits, sequential), "wavefront prefill differs from the window-by-window prefill"
+    t0 = time.perf_counter()
+    for _ in range(seq_steps):
+        logits = wave.run(ids)
+    torch.cuda.synchronize()
+    wave_ms = (time.perf_counter() - t0) * 1000.0 / seq_steps
+    kernels["C5.prefill_wavefront"] = {"ms_per_step": round(wave_ms, 4),
+                                       "tokens_per_s": round(C5_PREFILL_TOKENS / (wave_ms / 1000.0), 1),
+                                       "note": "window-by-window graphs of each layer on per-layer streams, "
+                                               "bit-identical to the window-by-window prefill"}
+    del wave, logits
+    return sequential
+
+
 class Timer:
     """Median per-launch GPU time of an operator: ``per_graph`` launches
     captured in one HIP graph (cycling over input sets), the graph replayed
@@ -468,54 +519,43 @@ def main() -> int:
     ids = c5.prefill_ids.to(device)
     start_states = herm.initial_states(settings, C5_BATCH, device)
 
-    log("C5: window-by-window graphed prefill (eager first window for the replay check)")
-    eager_logits, _ = herm.stack_window(params, settings, ids[:, :C5_WINDOW].contiguous(),
-                                        herm.initial_states(settings, C5_BATCH, device))
-    sequential, _, graph = herm.prefill_graphed(params, settings, ids, start_states)
-    torch.cuda.synchronize()
-    replay_vs_eager = float((sequential[:, :C5_WINDOW] - eager_logits).abs().max() / eager_logits.abs().max())
-    assert replay_vs_eager < 1e-5, f"graph replay differs from the eager window: {replay_vs_eager:.3e}"
-    assert torch.isfinite(sequential).all(), "non-finite prefill logits"
-    seq_steps = 3
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(seq_steps):
-        logits, _, graph = herm.prefill_graphed(params, settings, ids, start_states, graph)
-    torch.cuda.synchronize()
-    seq_ms = (time.perf_counter() - t0) * 1000.0 / seq_steps
-    assert torch.equal(logits, sequential), "window-by-window prefill is not reproducible"
-    kernels["C5.prefill_window_by_window"] = {"ms_per_step": round(seq_ms, 4),
-                                              "tokens_per_s": round(C5_PREFILL_TOKENS / (seq_ms / 1000.0), 1),
-                                              "replay_vs_eager_rel": replay_vs_eager,
-                                              "note": "every layer of a window in one HIP graph, windows in turn"}
-    del graph, logits, eager_logits
+    sequential = None
+    if not args.headline_only:
+        sequential = window_by_window_rows(args, herm, params, settings, ids, start_states, kernels)
 
-    log("C5: wavefront prefill (per-layer streams): capture and equality with the window-by-window prefill")
-    wave = herm.WavefrontPrefill(params, settings, start_states, C5_BATCH, device)
-    logits = wave.run(ids)
+    log("C5: sequence-parallel prefill (one HIP graph): capture and check against the window-by-window prefill")
+    seq = herm.SequencePrefill(params, settings, start_states, ids)
+    logits = seq.run(ids).clone()
     torch.cuda.synchronize()
-    assert torch.equal(logits, sequential), "wavefront prefill differs from the window-by-window prefill"
+    assert torch.isfinite(logits).all(), "non-finite prefill logits"
+    seq_rel = None
+    if sequential is not None:
+        seq_rel = float((logits - sequential).norm() / sequential.norm())
+        assert seq_rel < 1e-2, f"sequence-parallel prefill differs from the window-by-window one: {seq_rel:.3e}"
+    reference_logits = logits
 
     log(f"C5: {args.warmup} warmup + {args.steps} timed prefill steps")
     for _ in range(args.warmup):
-        logits = wave.run(ids)
+        logits = seq.run(ids)
     torch.cuda.synchronize()
     start_ev, end_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start_ev.record(stream)
     for _ in range(args.steps):
-        logits = wave.run(ids)
+        logits = seq.run(ids)
     end_ev.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu_ms = start_ev.elapsed_time(end_ev)
     ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
     value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
-    assert torch.equal(logits, sequential), "prefill steps are not reproducible"
+    assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
     kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
-                             "schedule": "wavefront: layer l's window w on layer l's stream after window w of "
-                                         "layer l - 1; each layer window replayed from a HIP graph"}
-    del wave, logits, sequential
+                             "vs_window_by_window_rel": None if seq_rel is None else round(seq_rel, 6),
+                             "schedule": "sequence-parallel: each layer over all 2048 positions (the windows' "
+                                         "carried states from one scan, window rings and a windowed associative "
+                                         "memory), the whole stack replayed from one HIP graph"}
+    del seq, logits, sequential, reference_logits
 
     if not args.headline_only:
         log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
@@ -535,32 +575,32 @@ def main() -> int:
         del decode
 
     # --------------------------------------------- dominant kernel of C5 prefill
-    # The expert FFN of one layer window at the prefill's exact shape: the
-    # window's ids routed by the hash (as every layer routes them), bf16
+    # The expert FFN of one layer over the whole prefill at its exact shape:
+    # the prefill ids routed by the hash (as every layer routes them), bf16
     # contexts, each layer's own weights in turn (two layers' experts, 403 MB,
     # do not fit the Infinity Cache, as the stack's twelve do not).
-    log("C5: dominant kernel (expert FFN of a layer window), live timing")
-    win = ids[:, :C5_WINDOW].contiguous()
-    valid5 = win != herm.PAD_TOKEN_ID
-    prev5 = torch.cat((torch.full_like(win[:, :1], herm.PAD_TOKEN_ID), win[:, :-1]), dim=1)
-    assign5 = moe.route_topk_valid(win, prev5, valid5, expert_count=C5_E, top_k=C5_K)
+    log("C5: dominant kernel (the expert FFN of one layer over the prefill), live timing")
+    valid5 = ids != herm.PAD_TOKEN_ID
+    prev5 = torch.cat((torch.full_like(ids[:, :1], herm.PAD_TOKEN_ID), ids[:, :-1]), dim=1)
+    assign5 = moe.route_topk_valid(ids, prev5, valid5, expert_count=C5_E, top_k=C5_K)
     ffn_sets = []
     for layer in (0, 1):
-        ctx5 = torch.randn((C5_BATCH * C5_WINDOW, C5_WIDTH), device=device).to(torch.bfloat16)
+        ctx5 = torch.randn((C5_PREFILL_TOKENS, C5_WIDTH), device=device).to(torch.bfloat16)
         sc, rows, experts, offsets = moe.permute_topk(ctx5, assign5.reshape(-1, C5_K), valid5.reshape(-1),
                                                       expert_count=C5_E)
         p = params[layer]
         ffn_sets.append((sc, experts, offsets, p["gate_w"], p["gate_b"], p["up_w"], p["up_b"], p["down_w"],
                          p["down_b"]))
     ffn_ms = timer.per_launch_ms([lambda s=s: moe.grouped_expert_mlp_inference(*s, validate=False) for s in ffn_sets],
-                                 24, max(10, args.kernel_iters))
+                                 4, max(10, args.kernel_iters))
     ffn_tflops = C5_FFN_FLOP / ffn_ms / 1e9
-    kernels["C5.expert_ffn_window"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
-                                       "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
-                                       "pairs": C5_WINDOW_PAIRS, "flop": C5_FFN_FLOP}
+    kernels["C5.expert_ffn_layer"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
+                                      "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
+                                      "pairs": C5_PAIRS, "flop": C5_FFN_FLOP}
     headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", None),
-                         "kernel": "grouped expert GLU FFN of one C5 layer window (grouped_gemm_bf16_kernel launches "
-                                   "of GEMM 1 and GEMM 2 with the device tile schedule)",
+                         "kernel": "grouped expert GLU FFN of one C5 layer over the prefill: grouped_gemm_bf16_kernel "
+                                   "launches of GEMM 1 (gate + value, SiLU-GLU epilogue) and GEMM 2 with the device "
+                                   "tile schedule, split-K partial tiles and their fix-ups",
                          "algorithmic_flop": C5_FFN_FLOP, "avg_ms": round(ffn_ms, 5)}
     del ffn_sets
     extra = [c for c in args.configs.split(",") if c.strip()] if not args.headline_only else []
@@ -752,8 +792,8 @@ def main() -> int:
         "config": {
             "workload": "C5: random-initialised stack of 12 HERM blocks (width 1024, state 1024, 16 experts top-2 "
                         "hash-routed, local and salient rings of 16, byte vocabulary + PAD); step = prefill of "
-                        "8 x 2048 seeded byte ids in windows of 128, the (layer, window) graphs scheduled as a "
-                        "wavefront over per-layer streams; decode = 256 greedy steps at batch 64",
+                        "8 x 2048 seeded byte ids (windows of 128, state carried), computed sequence-parallel and "
+                        "replayed from one HIP graph; decode = 256 greedy steps at batch 64",
             "tokens_per_step": C5_PREFILL_TOKENS,
             "decode_tokens_per_s": kernels.get("C5.decode", {}).get("tokens_per_s"),
             "compute": "bf16 projections and expert FFNs with fp32 accumulation; fp32 state, memories and "

@@ -237,6 +237,24 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
                        void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
                        int64_t width, int64_t capacity, int dtype, koemi_stream_t stream);
 
+/* The rings a sequence-parallel prefill needs (no single reference op: the
+ * state that forward_parallel carries from window to window, network.py:
+ * 176-197, through LocalKeyValueMemory.tail and salient_tail, memory.py:
+ * 385-403, 431-455). For each batch row and r = 0 .. length / window, the ring
+ * as it stands before position r * window of the sequence: entries = the
+ * carried ring [carried] followed by positions 0 .. r * window - 1, each with
+ * its flag. tail != 0: the last `capacity` entries with their flags, rows as
+ * stored (the local ring; flags = valid). tail == 0: the salient_tail rule
+ * above (flags = admission; invalid slots zeroed). Outputs
+ * [batch, length / window + 1, capacity, width] keys and values and
+ * [batch, length / window + 1, capacity] flags; row r = length / window is the
+ * ring after the whole sequence. Requires carried >= capacity (a static ring,
+ * state.py:43-76) and length % window == 0. */
+int koemi_window_rings(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                       const void* keys, const void* values, const uint8_t* flags, void* out_keys, void* out_values,
+                       uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length, int64_t window,
+                       int64_t width, int64_t capacity, int tail, int dtype, koemi_stream_t stream);
+
 /* The local and the salient read of a one-position window (a decode step,
  * network.py:337-358: LocalKeyValueMemory.read_window and
  * read_salient_window with one query) in one launch: each query [batch, width]
@@ -348,6 +366,26 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
                           const float* surprise, const uint8_t* valid, const float* basis, const float* normalizer,
                           float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
                           int64_t width, int64_t features, koemi_stream_t stream);
+
+/* koemi_assoc_scan_read over a whole sequence of `windows` windows of
+ * `window` positions at once (forward_parallel, network.py:176-197, carrying
+ * the memory state from window to window): the same layouts with length =
+ * windows * window. Three launches: every window's own terms of the final
+ * state from a zero carried state, a scan over the windows of
+ * state' = e^{c_{L-1}} state + terms (the kernel's own update, so each
+ * window's carried state equals a window-by-window run's), and the reads of
+ * every window from its carried state. Writes the reads [batch, length,
+ * width] and the state after the last window. window >= 2; workspace of
+ * koemi_assoc_scan_read_windows_workspace_bytes(batch, windows, width,
+ * features) bytes. */
+size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t width, int64_t features);
+int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
+                                  int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
+                                  int64_t write_offset, const float* surprise, const uint8_t* valid,
+                                  const float* basis, const float* normalizer, float* read, float* next_basis,
+                                  float* next_normalizer, int64_t batch, int64_t windows, int64_t window,
+                                  int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
+                                  koemi_stream_t stream);
 
 /* Small per-window steps of the HERM block (torch composites in the reference).
  * koemi_herm_rmsnorm: out = RootMeanSquareNorm(x + residual) * weight

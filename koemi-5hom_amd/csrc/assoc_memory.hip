@@ -75,7 +75,14 @@ __device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <int MAXM>
+// What one launch of assoc_read_kernel computes: the window's reads and its
+// final state (kFull); only the final state's window terms with a zero
+// carried state, sum_s e^{c_{L-1} - c_s} weight_s value_s features_s^T (and
+// for the normalizer), plus e^{c_{L-1}} per row in `out` (kDelta; launched
+// with one row tile); or only the reads (kRead).
+constexpr int kFull = 0, kDelta = 1, kRead = 2;
+
+template <int MAXM, int MODE = kFull>
 __global__ __launch_bounds__(256) void assoc_read_kernel(
     const float* __restrict__ proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
     int64_t decay_off, int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid,
@@ -186,6 +193,7 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
     }
     __syncthreads();
 
+    if constexpr (MODE != kDelta) {
     const int t0 = static_cast<int>(blockIdx.z) * kAssocRows;
     const int rows = min(kAssocRows, L - t0);
     const int s_cnt = t0 + rows;  // slots that can reach these queries (s < t <= t0 + rows - 1)
@@ -261,6 +269,8 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
             out[(b * L + t0 + r) * D + d] = (dn / reg) * acc[i] / reg;
         }
     }
+    }  // MODE != kDelta
+    if constexpr (MODE == kRead) return;
     if (blockIdx.z != 0) return;
     // final basis columns (64 x M): sum over slots of (final-write weight x value)
     // x feature on MFMA, slots split in two halves over wave pairs, the halves
@@ -299,7 +309,8 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
                 const int64_t d = c0 + db * 32 + 8 * (i / 4) + 4 * h + (i % 4);
                 if (m >= M || d >= D) continue;
                 const int64_t at = (b * D + d) * M + m;
-                next_basis[at] = fmaf(keep, basis[at], acc[i] + part[i * kWave + lane]);
+                const float window_terms = acc[i] + part[i * kWave + lane];
+                next_basis[at] = MODE == kDelta ? window_terms : fmaf(keep, basis[at], window_terms);
             }
         }
     }
@@ -308,9 +319,37 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
             float sum = 0.0f;
             for (int s = lane; s < L; s += kWave) sum = fmaf(fwt[s], f_sh[m * FP + s], sum);
             sum = wave_sum_xor(sum);
-            if (lane == 0) next_normalizer[b * M + m] = fmaf(keep, normalizer[b * M + m], sum);
+            if (lane == 0) next_normalizer[b * M + m] = MODE == kDelta ? sum : fmaf(keep, normalizer[b * M + m], sum);
         }
+        if (MODE == kDelta && lane == 0) out[b] = keep;
     }
+}
+
+// The state carried into each of a sequence's windows and the state after the
+// last: for element e of the flattened basis (D x M, then the M normalizer
+// entries) of batch row b, cur = state_0; window w receives cur, then
+// cur = fmaf(keep_w, cur, delta_w), the update assoc_read_kernel applies at the
+// end of a window (so the carried states equal a window-by-window run's).
+__global__ __launch_bounds__(256) void assoc_carry_kernel(
+    const float* __restrict__ delta_basis, const float* __restrict__ delta_norm, const float* __restrict__ keep,
+    const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ carried_basis,
+    float* __restrict__ carried_norm, float* __restrict__ next_basis, float* __restrict__ next_normalizer,
+    int64_t windows, int64_t DM, int64_t M) {
+    const int64_t b = blockIdx.x;
+    const int64_t e = static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x;
+    if (e >= DM + M) return;
+    const bool is_basis = e < DM;
+    const int64_t x = is_basis ? e : e - DM;
+    const int64_t n = is_basis ? DM : M;
+    const float* delta = is_basis ? delta_basis : delta_norm;
+    float* carried = is_basis ? carried_basis : carried_norm;
+    float cur = is_basis ? basis[b * DM + x] : normalizer[b * M + x];
+    for (int64_t w = 0; w < windows; ++w) {
+        const int64_t row = b * windows + w;
+        carried[row * n + x] = cur;
+        cur = fmaf(keep[row], cur, delta[row * n + x]);
+    }
+    (is_basis ? next_basis : next_normalizer)[b * n + x] = cur;
 }
 
 // One-position window (a decode step): read from the carried state, then
@@ -444,4 +483,100 @@ extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_strid
     if (M <= 16) run(assoc_read_kernel<16>);
     else run(assoc_read_kernel<32>);
     return check_launch("koemi_assoc_scan_read");
+}
+
+namespace {
+
+struct WindowsWorkspace {
+    size_t delta_basis, delta_norm, keep, carried_basis, carried_norm, total;
+};
+
+inline size_t align256w(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline WindowsWorkspace windows_workspace(int64_t rows, int64_t width, int64_t features) {
+    WindowsWorkspace w;
+    const size_t basis_bytes = align256w(static_cast<size_t>(rows * width * features) * sizeof(float));
+    const size_t norm_bytes = align256w(static_cast<size_t>(rows * features) * sizeof(float));
+    w.delta_basis = 0;
+    w.delta_norm = w.delta_basis + basis_bytes;
+    w.keep = w.delta_norm + norm_bytes;
+    w.carried_basis = w.keep + align256w(static_cast<size_t>(rows) * sizeof(float));
+    w.carried_norm = w.carried_basis + basis_bytes;
+    w.total = w.carried_norm + norm_bytes;
+    return w;
+}
+
+}  // namespace
+
+extern "C" size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t width,
+                                                                 int64_t features) {
+    if (batch < 0 || windows < 0 || width < 1 || features < 1) return 0;
+    return windows_workspace(batch * windows, width, features).total;
+}
+
+extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
+                                             int64_t feature_offset, int64_t query_feature_offset,
+                                             int64_t decay_offset, int64_t write_offset, const float* surprise,
+                                             const uint8_t* valid, const float* basis, const float* normalizer,
+                                             float* read, float* next_basis, float* next_normalizer, int64_t batch,
+                                             int64_t windows, int64_t window, int64_t width, int64_t features,
+                                             void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    if (batch < 0 || windows < 0 || window < 2 || width < 1 || features < 1)
+        return fail(KOEMI_ERR_INVALID, "windowed associative read needs non-negative batch and windows, a window of at "
+                    "least two positions, positive width and features");
+    if (features > 32) return fail(KOEMI_ERR_UNSUPPORTED, "associative read supports at most 32 memory features");
+    auto inside = [&](int64_t off, int64_t span) { return off >= 0 && off + span <= row_stride; };
+    if (!inside(value_offset, width) || !inside(feature_offset, features) ||
+        !inside(query_feature_offset, features) || !inside(decay_offset, 1) || !inside(write_offset, 1))
+        return fail(KOEMI_ERR_INVALID, "associative read column offsets must lie inside the row stride");
+    const int64_t rows = batch * windows;
+    if (batch == 0) return KOEMI_OK;
+    const size_t lds = assoc_lds(window, features);
+    if (lds > 160 * 1024)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative read window too long (%lld positions)",
+                    static_cast<long long>(window));
+    if (rows > 0x7fffffffLL || (width + kAssocCols - 1) / kAssocCols > 65535 ||
+        (width * features + features + 255) / 256 > 65535)
+        return fail(KOEMI_ERR_UNSUPPORTED, "windowed associative read grid too large");
+    if (!basis || !normalizer || !next_basis || !next_normalizer ||
+        (windows > 0 && (!projections || !surprise || !valid || !read)))
+        return fail(KOEMI_ERR_INVALID, "windowed associative read received a null pointer");
+    const WindowsWorkspace ws = windows_workspace(rows, width, features);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "windowed associative read workspace too small: need %zu bytes", ws.total);
+    char* w = static_cast<char*>(workspace);
+    float* delta_basis = reinterpret_cast<float*>(w + ws.delta_basis);
+    float* delta_norm = reinterpret_cast<float*>(w + ws.delta_norm);
+    float* keep = reinterpret_cast<float*>(w + ws.keep);
+    float* carried_basis = reinterpret_cast<float*>(w + ws.carried_basis);
+    float* carried_norm = reinterpret_cast<float*>(w + ws.carried_norm);
+    const hipStream_t s = as_stream(stream);
+    const int M = static_cast<int>(features);
+    const unsigned col_tiles = static_cast<unsigned>((width + kAssocCols - 1) / kAssocCols);
+    auto launch = [&](auto kernel, unsigned row_tiles, const float* carried_b, const float* carried_n, float* out,
+                      float* nb, float* nn) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(rows), col_tiles, row_tiles), dim3(256), lds, s,
+                           projections, row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
+                           write_offset, surprise, valid, carried_b, carried_n, out, nb, nn, static_cast<int>(window),
+                           width, M);
+    };
+    if (windows > 0) {
+        // 1. every window's own terms of the final state, from a zero carried state
+        if (M <= 16) launch(assoc_read_kernel<16, kDelta>, 1u, nullptr, nullptr, keep, delta_basis, delta_norm);
+        else launch(assoc_read_kernel<32, kDelta>, 1u, nullptr, nullptr, keep, delta_basis, delta_norm);
+        int st = check_launch("koemi_assoc_scan_read_windows(delta)");
+        if (st != KOEMI_OK) return st;
+    }
+    // 2. the state carried into each window, and the final state
+    const int64_t DM = width * features;
+    hipLaunchKernelGGL(assoc_carry_kernel, dim3(static_cast<unsigned>(batch), static_cast<unsigned>((DM + M + 255) / 256)),
+                       dim3(256), 0, s, delta_basis, delta_norm, keep, basis, normalizer, carried_basis, carried_norm,
+                       next_basis, next_normalizer, windows, DM, static_cast<int64_t>(M));
+    int st = check_launch("koemi_assoc_scan_read_windows(carry)");
+    if (st != KOEMI_OK || windows == 0) return st;
+    // 3. the reads of every window from its carried state
+    const unsigned row_tiles = static_cast<unsigned>((window + kAssocRows - 1) / kAssocRows);
+    if (M <= 16) launch(assoc_read_kernel<16, kRead>, row_tiles, carried_basis, carried_norm, read, nullptr, nullptr);
+    else launch(assoc_read_kernel<32, kRead>, row_tiles, carried_basis, carried_norm, read, nullptr, nullptr);
+    return check_launch("koemi_assoc_scan_read_windows(read)");
 }

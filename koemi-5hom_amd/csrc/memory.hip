@@ -25,25 +25,41 @@ constexpr int kTailThreads = 256;
 constexpr int64_t kMaxCapacity = 4096;
 constexpr int kTailSlotsPerBlock = 4;  // output slots copied by one workgroup
 
-// One workgroup per (batch row, group of kTailSlotsPerBlock output slots):
+// One workgroup per (ring row, group of kTailSlotsPerBlock output slots):
 // every workgroup of a row repeats the (cheap) slot selection in LDS, then
 // copies its own slots' key and value rows. VEC: width % 4 == 0 and 16-byte
 // (fp32) or 8-byte (half) aligned rows, copied four elements at a time.
-template <typename T, bool VEC>
+//
+// Ring rows: blockIdx.x = b * R + r. Row r selects over the carried entries
+// and the first Lr = L - (R - 1 - r) * W positions of batch row b, i.e. the
+// ring as it stands before position Lr; R = 1 is the ring after all L
+// positions (salient_tail), R = L / W + 1 the rings carried into each window
+// of W positions plus the final one. TAIL: the last C entries whatever their
+// flags (LocalKeyValueMemory.tail, memory.py:385-403), rows copied as stored;
+// otherwise the salient rule above (flag = admission).
+template <typename T, bool VEC, bool TAIL>
 __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
     const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid, const T* __restrict__ k,
     const T* __restrict__ v, const uint8_t* __restrict__ adm, T* __restrict__ ok, T* __restrict__ ov,
-    uint8_t* __restrict__ ovalid, int64_t S, int64_t L, int64_t D, int64_t C) {
+    uint8_t* __restrict__ ovalid, int64_t S, int64_t L, int64_t D, int64_t C, int64_t R, int64_t W) {
     __shared__ int32_t slot_entry[kMaxCapacity];
     __shared__ uint8_t slot_valid[kMaxCapacity];
     __shared__ int64_t wave_tot[kTailThreads / kWave];
-    const int64_t b = blockIdx.x;
+    const int64_t row = blockIdx.x;
+    const int64_t b = row / R;
+    const int64_t Lr = L - (R - 1 - (row - b * R)) * W;
     const int tid = threadIdx.x;
-    const int64_t N = S + L;
+    const int64_t N = S + Lr;
     const bool concat = N <= C;
     const int64_t slots = concat ? N : C;
     auto valid_at = [&](int64_t i) -> bool { return i < S ? cvalid[b * S + i] != 0 : adm[b * L + (i - S)] != 0; };
-    if (concat) {
+    if (TAIL && !concat) {
+        for (int64_t s = tid; s < C; s += kTailThreads) {
+            const int64_t i = N - C + s;
+            slot_entry[s] = static_cast<int32_t>(i);
+            slot_valid[s] = valid_at(i) ? 1 : 0;
+        }
+    } else if (concat) {
         for (int64_t i = tid; i < N; i += kTailThreads) {
             slot_entry[i] = static_cast<int32_t>(i);
             slot_valid[i] = valid_at(i) ? 1 : 0;
@@ -74,15 +90,16 @@ __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
     __syncthreads();
     const int64_t s_begin = static_cast<int64_t>(blockIdx.y) * kTailSlotsPerBlock;
     const int64_t s_end = min(slots, s_begin + kTailSlotsPerBlock);
-    if (s_begin + tid < s_end) ovalid[b * slots + s_begin + tid] = slot_valid[s_begin + tid];
-    // Copy the kept rows; invalid slots are zero unless the outputs are the plain concatenation.
+    if (s_begin + tid < s_end) ovalid[row * slots + s_begin + tid] = slot_valid[s_begin + tid];
+    // Copy the kept rows; invalid slots are zero unless the outputs are the plain
+    // concatenation or the tail of the entries.
     for (int64_t s = s_begin; s < s_end; ++s) {
         const int64_t i = slot_entry[s];
-        const bool zero = !concat && !slot_valid[s];
+        const bool zero = !TAIL && !concat && !slot_valid[s];
         const T* ksrc = i < S ? ck + (b * S + i) * D : k + (b * L + (i - S)) * D;
         const T* vsrc = i < S ? cv + (b * S + i) * D : v + (b * L + (i - S)) * D;
-        T* kdst = ok + (b * slots + s) * D;
-        T* vdst = ov + (b * slots + s) * D;
+        T* kdst = ok + (row * slots + s) * D;
+        T* vdst = ov + (row * slots + s) * D;
         if constexpr (VEC) {
             using V = typename std::conditional<sizeof(T) == 4, float4, uint2>::type;
             const V* ks = reinterpret_cast<const V*>(ksrc);
@@ -104,23 +121,30 @@ __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
     }
 }
 
+// R ring rows per batch row (see salient_tail_kernel); every row has `slots`
+// output slots (the windowed form requires S >= C, so that every row has C).
 template <typename T>
 int launch_tail(const void* ck, const void* cv, const uint8_t* cvalid, const void* k, const void* v, const uint8_t* adm,
                 void* ok, void* ov, uint8_t* ovalid, int64_t B, int64_t S, int64_t L, int64_t D, int64_t C,
-                hipStream_t s) {
+                int64_t R, int64_t W, bool tail, const char* what, hipStream_t s) {
     const int64_t slots = S + L <= C ? S + L : C;
-    const dim3 grid(static_cast<unsigned>(B), static_cast<unsigned>((slots + kTailSlotsPerBlock - 1) / kTailSlotsPerBlock));
+    const dim3 grid(static_cast<unsigned>(B * R), static_cast<unsigned>((slots + kTailSlotsPerBlock - 1) / kTailSlotsPerBlock));
     const size_t align = sizeof(T) == 4 ? 16 : 8;
     auto aligned = [&](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % align == 0; };
     const bool vec = D % 4 == 0 && aligned(ck) && aligned(cv) && aligned(k) && aligned(v) && aligned(ok) && aligned(ov);
     auto launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(kTailThreads), 0, s, static_cast<const T*>(ck), static_cast<const T*>(cv),
                            cvalid, static_cast<const T*>(k), static_cast<const T*>(v), adm, static_cast<T*>(ok),
-                           static_cast<T*>(ov), ovalid, S, L, D, C);
+                           static_cast<T*>(ov), ovalid, S, L, D, C, R, W);
     };
-    if (vec) launch(salient_tail_kernel<T, true>);
-    else launch(salient_tail_kernel<T, false>);
-    return check_launch("koemi_salient_tail");
+    if (tail) {
+        if (vec) launch(salient_tail_kernel<T, true, true>);
+        else launch(salient_tail_kernel<T, false, true>);
+    } else {
+        if (vec) launch(salient_tail_kernel<T, true, false>);
+        else launch(salient_tail_kernel<T, false, false>);
+    }
+    return check_launch(what);
 }
 
 }  // namespace
@@ -148,12 +172,52 @@ extern "C" int koemi_salient_tail(const void* carried_keys, const void* carried_
     switch (dtype) {
         case KOEMI_F32:
             return launch_tail<float>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                      out_values, out_valid, batch, carried, length, width, capacity, s);
+                                      out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
+                                      "koemi_salient_tail", s);
         case KOEMI_F16:
             return launch_tail<f16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                    out_values, out_valid, batch, carried, length, width, capacity, s);
+                                    out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
+                                    "koemi_salient_tail", s);
         default:
             return launch_tail<bf16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                     out_values, out_valid, batch, carried, length, width, capacity, s);
+                                     out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
+                                     "koemi_salient_tail", s);
+    }
+}
+
+extern "C" int koemi_window_rings(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
+                                  const void* keys, const void* values, const uint8_t* flags, void* out_keys,
+                                  void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
+                                  int64_t window, int64_t width, int64_t capacity, int tail, int dtype,
+                                  koemi_stream_t stream) {
+    if (batch < 0 || length < 0 || width < 1 || window < 1)
+        return fail(KOEMI_ERR_INVALID, "window rings need non-negative sizes, a positive width and window");
+    if (length % window) return fail(KOEMI_ERR_INVALID, "window rings need a length that is a multiple of the window");
+    if (capacity < 1 || capacity > kMaxCapacity || carried < capacity)
+        return fail(KOEMI_ERR_UNSUPPORTED, "window rings need a carried ring at capacity (capacity in [1, %lld])",
+                    static_cast<long long>(kMaxCapacity));
+    const int64_t rows = length / window + 1;
+    if (batch * rows > 0x7fffffffLL || carried + length > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "window rings: too many rows or entries");
+    if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "window rings do not support dtype %s", dtype_name(dtype));
+    if (batch == 0) return KOEMI_OK;
+    if (!carried_keys || !carried_values || !carried_valid || (length > 0 && (!keys || !values || !flags)) ||
+        !out_keys || !out_values || !out_valid)
+        return fail(KOEMI_ERR_INVALID, "window rings received a null pointer");
+    hipStream_t s = as_stream(stream);
+    const bool t = tail != 0;
+    switch (dtype) {
+        case KOEMI_F32:
+            return launch_tail<float>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
+                                      out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
+                                      "koemi_window_rings", s);
+        case KOEMI_F16:
+            return launch_tail<f16>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
+                                    out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
+                                    "koemi_window_rings", s);
+        default:
+            return launch_tail<bf16>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
+                                     out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
+                                     "koemi_window_rings", s);
     }
 }

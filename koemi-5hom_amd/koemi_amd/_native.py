@@ -83,6 +83,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P),
     ),
+    "koemi_window_rings": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_int, _P),
+    ),
     "koemi_recurrent_gates_workspace_bytes": (c_size_t, (c_int64, c_int64)),
     "koemi_recurrent_gates": (
         c_int,
@@ -109,6 +113,12 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64,
          c_int64, c_int64, _P),
+    ),
+    "koemi_assoc_scan_read_windows_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64)),
+    "koemi_assoc_scan_read_windows": (
+        c_int,
+        (_P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64,
+         c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
     "koemi_herm_rmsnorm": (c_int, (_P, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_float, _P)),
     "koemi_herm_concat_bf16": (c_int, (_P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P)),

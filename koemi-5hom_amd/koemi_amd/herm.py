@@ -62,9 +62,14 @@ __all__ = [
     "HermSettings",
     "PAD_TOKEN_ID",
     "block_window",
+    "SequencePrefill",
     "WavefrontPrefill",
     "WindowGraph",
     "associative_scan_read",
+    "associative_scan_read_windows",
+    "block_sequence",
+    "stack_sequence",
+    "window_rings",
     "decode_step",
     "init_stack",
     "initial_states",
@@ -338,6 +343,55 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     return read, next_basis, next_normalizer
 
 
+def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, previous: Tensor, valid: Tensor,
+                      pieces: tuple[Tensor, Tensor, Tensor, Tensor], with_logits: bool) -> tuple[Tensor, Tensor | None]:
+    """The block's position-wise tail: fusion of [working ; memory ; local ;
+    salient] with its normalizer (network.py:723-732), the expert mixture with
+    its output normalizer (experts.py:109-150 or router.py:43-97) and the token
+    head (network.py:700-701). Every position independent of the others, so
+    the rows may span any number of windows. Returns (final context
+    [B, L, D] fp32, logits or None)."""
+
+    batch, length = ids.shape
+    d = settings.width
+    lin = settings.linear_dtype
+    low = lin if lin == torch.bfloat16 else None
+    if low is None:
+        fusion_in = torch.cat(pieces, dim=-1)
+    else:
+        fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
+        _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4, batch * length, d,
+                     _native.ptr(fusion_in), _native.stream_of(ids.device))
+    fused_pair = _rms(_linear(fusion_in, p["fusion_w"], p["fusion_b"]), p["fusion_norm"], low=low)
+    fused, fused_low = fused_pair if low is not None else (fused_pair, None)
+
+    k = settings.top_k
+    flat = fused.reshape(-1, d)
+    flat_valid = valid.reshape(-1)
+    if settings.expert_routing == "learned":
+        # LearnedExpertMixture (router.py:43-97): the bias-free gate on the fp32
+        # context (rows of invalid tokens are routed to -1 whatever their
+        # logits), softmax top-k, each pair weighted by its probability
+        router_logits = functional.linear(flat, p["router_w"])
+        assignments, weights = moe.route_topk_learned(router_logits, flat_valid, top_k=k)
+    else:
+        assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
+                                           validate=False)
+        weights = None
+    moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
+    permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
+                                pair_weights=weights, validate=False)
+    sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
+    sorted_weights = permuted[4] if weights is not None else None
+    expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
+                                                  p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
+    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
+                              pair_weights=sorted_weights, validate=False)
+    final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
+    logits = _linear(final, p["head_w"], p["head_b"]) if with_logits else None
+    return final, logits
+
+
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
                  context: Tensor | None = None, *, with_logits: bool = True
                  ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
@@ -393,40 +447,8 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
                                                    state["salient_valid"], local_keys, local_values, admission, ws)
-    pieces = (ws, fast, local_value, salient_value)
-    if low is None:
-        fusion_in = torch.cat(pieces, dim=-1)
-    else:
-        fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
-        _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4, batch * length, d,
-                     _native.ptr(fusion_in), _native.stream_of(ids.device))
-    fused_pair = _rms(_linear(fusion_in, p["fusion_w"], p["fusion_b"]), p["fusion_norm"], low=low)
-    fused, fused_low = fused_pair if low is not None else (fused_pair, None)
-
-    k = settings.top_k
-    flat = fused.reshape(-1, d)
-    flat_valid = valid.reshape(-1)
-    if settings.expert_routing == "learned":
-        # LearnedExpertMixture (router.py:43-97): the bias-free gate on the fp32
-        # context (rows of invalid tokens are routed to -1 whatever their
-        # logits), softmax top-k, each pair weighted by its probability
-        router_logits = functional.linear(flat, p["router_w"])
-        assignments, weights = moe.route_topk_learned(router_logits, flat_valid, top_k=k)
-    else:
-        assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
-                                           validate=False)
-        weights = None
-    moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
-    permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
-                                pair_weights=weights, validate=False)
-    sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
-    sorted_weights = permuted[4] if weights is not None else None
-    expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
-                                                  p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
-    update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
-                              pair_weights=sorted_weights, validate=False)
-    final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
-    logits = _linear(final, p["head_w"], p["head_b"]) if with_logits else None
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, (ws, fast, local_value, salient_value),
+                                      with_logits)
 
     local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
     salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
@@ -444,6 +466,198 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
         "last_token": last_token,
     }
     return logits, final, next_state, surprise
+
+
+def window_rings(carried_keys: Tensor, carried_values: Tensor, carried_flags: Tensor, keys: Tensor, values: Tensor,
+                 flags: Tensor, *, window: int, capacity: int, tail: bool) -> tuple[Tensor, Tensor, Tensor]:
+    """The ring carried into every window of a sequence and the ring after it
+    (``koemi_window_rings``): ``[B, L / window + 1, capacity, D]`` keys and
+    values, ``[B, L / window + 1, capacity]`` flags. ``tail``: the local ring
+    (the last ``capacity`` entries, LocalKeyValueMemory.tail, memory.py:
+    385-403); otherwise the salient ring (salient_tail, memory.py:431-455)."""
+
+    batch, length, width = keys.shape
+    rows = length // window + 1
+    out_k = torch.empty((batch, rows, capacity, width), device=keys.device, dtype=keys.dtype)
+    out_v = torch.empty_like(out_k)
+    out_ok = torch.empty((batch, rows, capacity), device=keys.device, dtype=torch.bool)
+    args = [t.contiguous() for t in (carried_keys, carried_values, carried_flags, keys, values, flags)]
+    _native.call("koemi_window_rings", *(_native.ptr(t) for t in args), _native.ptr(out_k), _native.ptr(out_v),
+                 _native.ptr(out_ok), batch, carried_keys.shape[1], length, window, width, capacity, int(tail),
+                 _native.dtype_code(keys.dtype), _native.stream_of(keys.device))
+    return out_k, out_v, out_ok
+
+
+def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor,
+                                  normalizer: Tensor, *, width: int, features: int, window: int
+                                  ) -> tuple[Tensor, Tensor, Tensor]:
+    """``associative_scan_read`` over every window of a sequence at once
+    (``koemi_assoc_scan_read_windows``): the same inputs with length = a
+    multiple of ``window``; each window reads from the state the previous
+    windows left (equal to a window-by-window run's), and the state after the
+    last window is returned with the reads."""
+
+    batch, length, stride = projections.shape
+    d, m = width, features
+    if stride < 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
+        raise ValueError("projections must be contiguous fp32 [batch, length, >= 3 * width + 2 * features + 2]")
+    if length % window:
+        raise ValueError("the sequence length must be a multiple of the window")
+    windows = length // window
+    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
+    next_basis = torch.empty_like(basis)
+    next_normalizer = torch.empty_like(normalizer)
+    workspace = torch.empty((_native.query("koemi_assoc_scan_read_windows_workspace_bytes", batch, windows, d, m),),
+                            device=projections.device, dtype=torch.uint8)
+    args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
+    _native.call(
+        "koemi_assoc_scan_read_windows",
+        _native.ptr(projections), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        *(_native.ptr(t) for t in args),
+        _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
+        batch, windows, window, d, m, _native.ptr(workspace), workspace.numel(), _native.stream_of(projections.device),
+    )
+    return read, next_basis, next_normalizer
+
+
+def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
+                   context: Tensor | None = None, *, with_logits: bool = True
+                   ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
+    """One block over a whole sequence of windows at once: forward_parallel
+    (network.py:176-197) of a single block, i.e. ``block_window`` applied to
+    windows of ``scan_chunk`` tokens with the state carried, computed
+    sequence-parallel. ``ids`` ``[B, L]``, L a multiple of ``scan_chunk``,
+    static state rings (``initial_states``).
+
+    No part of a window's carried state (working state, associative basis and
+    normalizer, local and salient rings, last token) depends on the fusion,
+    the experts or the head, so those run once over all positions, and so do
+    the projections, the surprise head and the admission (position-wise).
+    The recurrence runs as one scan over the whole sequence; the local and
+    salient reads of all windows run as one batch of B x L / scan_chunk rows,
+    each with the ring carried into its window (``window_rings``); the
+    associative memory runs per window from the state the previous windows
+    left (``associative_scan_read_windows``). The results equal the
+    window-by-window ones up to floating-point rounding (the library GEMMs
+    see more rows). Returns (logits or None, final context, next state,
+    surprise [B, L]).
+    """
+
+    ids = ids.contiguous()
+    batch, length = ids.shape
+    chunk, d = settings.scan_chunk, settings.width
+    if length % chunk:
+        raise ValueError("block_sequence needs a length that is a multiple of scan_chunk")
+    windows = length // chunk
+    rows = batch * windows
+    previous, last_token, valid, targets = _token_context(ids, None, state["last_token"])
+    source = functional.embedding(ids, p["embedding"]) if context is None else context
+    lin = settings.linear_dtype
+    low = lin if lin == torch.bfloat16 else None
+    u = _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
+                                   with_bf16=low is not None)
+    ws, ws_low = scanned if low is not None else (scanned, scanned)
+    prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
+    surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
+
+    projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
+    local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
+    local_values = torch.empty_like(local_keys)
+    _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
+                 _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
+    cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
+    lk, lv, lok = window_rings(state["local_keys"], state["local_values"], state["local_valid"], local_keys,
+                               local_values, valid, window=chunk, capacity=cap_l, tail=True)
+    per_window = lambda t: t.view(rows, chunk, *t.shape[2:])
+    carried = lambda t: t[:, :windows].reshape(rows, *t.shape[2:])
+    local_value = memory.read_local_window(carried(lk), carried(lv), carried(lok), per_window(local_keys),
+                                           per_window(local_values), per_window(valid), per_window(ws),
+                                           window=cap_l).view(batch, length, d)
+
+    fast, basis, normalizer = associative_scan_read_windows(projected, surprise, valid, state["basis"],
+                                                            state["normalizer"], width=d,
+                                                            features=settings.memory_features, window=chunk)
+    admission = think.admission_above(surprise, valid, settings.salience_threshold)
+    sk, sv, sok = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
+                               local_values, admission, window=chunk, capacity=cap_s, tail=False)
+    salient_value = memory.read_salient_window(carried(sk), carried(sv), carried(sok), per_window(local_keys),
+                                               per_window(local_values), per_window(admission),
+                                               per_window(ws)).view(batch, length, d)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, (ws, fast, local_value, salient_value),
+                                      with_logits)
+    next_state = {
+        "working": ws[:, -1].contiguous(),
+        "basis": basis,
+        "normalizer": normalizer,
+        "local_keys": lk[:, windows].contiguous(),
+        "local_values": lv[:, windows].contiguous(),
+        "local_valid": lok[:, windows].contiguous(),
+        "salient_keys": sk[:, windows].contiguous(),
+        "salient_values": sv[:, windows].contiguous(),
+        "salient_valid": sok[:, windows].contiguous(),
+        "last_token": last_token,
+    }
+    return logits, final, next_state, surprise
+
+
+def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                   states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+    """``prefill`` computed layer by layer with ``block_sequence``: each layer
+    over the whole sequence before the next. Returns the last layer's logits
+    of every position and the next states."""
+
+    context = None
+    next_states = []
+    logits = None
+    for layer, (p, state) in enumerate(zip(params, states)):
+        logits, context, next_state, _ = block_sequence(p, settings, ids, state, context,
+                                                        with_logits=layer == len(params) - 1)
+        next_states.append(next_state)
+    return logits, next_states
+
+
+class SequencePrefill:
+    """``stack_sequence`` at a fixed (batch, length) replayed from one captured
+    HIP graph: ``run(ids, states=None)`` copies the ids in, resets the static
+    state buffers to ``states`` (default: the states given at construction),
+    replays, and returns the logits buffer; ``self.states`` then holds the
+    states after the sequence. Two eager passes on throwaway copies warm the
+    libraries up before the capture."""
+
+    def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
+                 ids: Tensor) -> None:
+        self.params, self.settings = params, settings
+        self.ids = ids.clone().contiguous()
+        self.start = [{k: v.clone() for k, v in st.items()} for st in states]
+        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            warm = [{k: v.clone() for k, v in st.items()} for st in states]
+            for _ in range(2):
+                stack_sequence(params, settings, self.ids, warm)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits, next_states = stack_sequence(params, settings, self.ids, self.states)
+            dst, src = [], []
+            for state, new in zip(self.states, next_states):
+                for key in state:
+                    dst.append(state[key])
+                    src.append(new[key])
+            torch._foreach_copy_(dst, src)
+
+    def run(self, ids: Tensor | None = None, states: list[dict[str, Tensor]] | None = None) -> Tensor:
+        if ids is not None:
+            self.ids.copy_(ids)
+        source = self.start if states is None else states
+        for state, start in zip(self.states, source):
+            for key, tensor in state.items():
+                tensor.copy_(start[key])
+        self.graph.replay()
+        return self.logits
 
 
 def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,

@@ -24,7 +24,8 @@ configuration, at its shapes.
 * Decode steps replayed from the decode graph equal eager steps (ids exact,
   logits 1e-5 of scale).
 * The wavefront prefill (per-layer streams) equals the window-by-window
-  prefill bit for bit.
+  prefill bit for bit; the sequence-parallel prefill equals it within the bf16
+  tolerances (layer 0's state bit for bit).
 """
 
 from __future__ import annotations
@@ -147,3 +148,33 @@ def test_c5_wavefront_prefill_equals_the_window_by_window_prefill(device, c5):
     for got, exp in zip(wave.states, want_states):
         for key, tensor in exp.items():
             assert torch.equal(got[key], tensor), key
+
+
+def test_c5_sequence_prefill_matches_the_window_by_window_prefill(device, c5):
+    """The sequence-parallel prefill (one HIP graph) at C5. Layer 0's carried
+    state does not depend on any product whose rows change with the batching
+    (its expert FFN feeds only the next layer), so it equals the
+    window-by-window state bit for bit; the later layers and the logits carry
+    the bf16 rounding of products computed over other row sets (the split-K
+    expert tiles of a window against whole tiles of the sequence): within the
+    tolerances of the bf16 path above (measured 4.6e-3 relative Frobenius,
+    8.6e-3 max/scale). Ring bits and last tokens exact."""
+
+    settings, _, params = c5
+    ids = workloads.config5().prefill_ids.to(device)
+    batch = ids.shape[0]
+    want, want_states, _ = herm.prefill_graphed(params, settings, ids, herm.initial_states(settings, batch, device))
+    seq = herm.SequencePrefill(params, settings, herm.initial_states(settings, batch, device), ids)
+    got = seq.run(ids)
+    torch.cuda.synchronize()
+    rel = float((got - want).norm() / want.norm())
+    mx = float((got - want).abs().max() / want.abs().max())
+    print(f"C5 sequence-parallel vs window-by-window logits: rel_frobenius={rel:.3e} max/scale={mx:.3e}", flush=True)
+    assert rel <= 1e-2 and mx <= 2e-2
+    for key, tensor in want_states[0].items():
+        assert torch.equal(seq.states[0][key], tensor), f"layer 0 {key}"
+    for layer, (st, exp) in enumerate(zip(seq.states, want_states)):
+        for key in ("local_valid", "salient_valid", "last_token"):
+            assert torch.equal(st[key], exp[key]), f"layer {layer} {key}"
+        for key in ("working", "basis", "local_keys"):
+            assert float((st[key] - exp[key]).norm() / exp[key].norm()) <= 1e-2, f"layer {layer} {key}"

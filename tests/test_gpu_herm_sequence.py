@@ -1,0 +1,153 @@
+"""The sequence-parallel HERM block (koemi_amd.herm.block_sequence, stack_sequence,
+SequencePrefill) against the window-by-window block and the oracle.
+
+* window_rings: the ring carried into every window equals, bit for bit, the
+  ring a window-by-window run carries: the salient ring against
+  oracle.salient_tail applied window after window (memory.py:431-455), the
+  local ring against the tail of [ring ; entries] (memory.py:385-403).
+* associative_scan_read_windows: reads and final state bit-identical to
+  associative_scan_read run window after window with the state carried (the
+  same kernel arithmetic: the per-window terms, then e^{c_{L-1}} state +
+  terms).
+* stack_sequence over a three-layer stack (width 32, fp32 projections, five
+  windows of six tokens with padding and admissions): logits and float states
+  within 1e-5 of the window-by-window prefill's scale, ring bits and last
+  tokens exact; and against oracle.herm's prefill (float64) within 1e-4 (the
+  tolerance of tests/test_gpu_herm.py), the admission threshold placed
+  >= 2e-3 from every oracle score.
+* SequencePrefill (one HIP graph) replays equal the eager stack_sequence
+  (1e-5) and each other (exactly).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from koemi_amd import herm
+from oracle import herm as oherm
+
+from test_gpu_herm import _close, _ids, _oracle_params, _params, _pick_threshold, _settings
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_rings(rng, b, s, length, d, p_flag):
+    ck = rng.normal(size=(b, s, d)).astype(np.float32)
+    cv = rng.normal(size=(b, s, d)).astype(np.float32)
+    cok = rng.random((b, s)) < 0.5
+    ck[~cok] = 0.0
+    cv[~cok] = 0.0
+    k = rng.normal(size=(b, length, d)).astype(np.float32)
+    v = rng.normal(size=(b, length, d)).astype(np.float32)
+    flags = rng.random((b, length)) < p_flag
+    return ck, cv, cok, k, v, flags
+
+
+@pytest.mark.parametrize("p_flag", [0.02, 0.3, 0.9])
+def test_window_rings_equal_the_window_by_window_rings(device, p_flag):
+    rng = np.random.default_rng(int(p_flag * 100))
+    b, s, window, windows, d = 3, 5, 7, 6, 12
+    ck, cv, cok, k, v, flags = _rand_rings(rng, b, s, window * windows, d, p_flag)
+    t = lambda x: torch.from_numpy(x).to(device)
+    for tail in (False, True):
+        got_k, got_v, got_ok = herm.window_rings(t(ck), t(cv), t(cok), t(k), t(v), t(flags), window=window,
+                                                 capacity=s, tail=tail)
+        rk, rv, rok = ck, cv, cok
+        for w in range(windows + 1):
+            np.testing.assert_array_equal(got_ok[:, w].cpu().numpy(), rok, err_msg=f"tail={tail} w={w}")
+            np.testing.assert_array_equal(got_k[:, w].cpu().numpy(), rk, err_msg=f"tail={tail} w={w}")
+            np.testing.assert_array_equal(got_v[:, w].cpu().numpy(), rv, err_msg=f"tail={tail} w={w}")
+            if w == windows:
+                break
+            sl = slice(w * window, (w + 1) * window)
+            if tail:
+                rk = np.concatenate([rk, k[:, sl]], axis=1)[:, -s:]
+                rv = np.concatenate([rv, v[:, sl]], axis=1)[:, -s:]
+                rok = np.concatenate([rok, flags[:, sl]], axis=1)[:, -s:]
+            else:
+                rk, rv, rok = (np.asarray(x) for x in oracle.salient_tail(rk, rv, rok, k[:, sl], v[:, sl],
+                                                                          flags[:, sl], s))
+                rk, rv = rk.astype(np.float32), rv.astype(np.float32)
+
+
+def test_windowed_associative_memory_equals_window_by_window(device):
+    g = torch.Generator(device=device).manual_seed(9)
+    b, windows, window, d, m = 3, 5, 40, 96, 16
+    stride = 3 * d + 2 * m + 2 + 2
+    proj = torch.randn((b, windows * window, stride), generator=g, device=device)
+    surprise = torch.rand((b, windows * window), generator=g, device=device)
+    valid = torch.rand((b, windows * window), generator=g, device=device) < 0.9
+    basis = torch.randn((b, d, m), generator=g, device=device) * 0.1
+    norm = torch.rand((b, m), generator=g, device=device)
+    read, nb, nn = herm.associative_scan_read_windows(proj, surprise, valid, basis, norm, width=d, features=m,
+                                                      window=window)
+    cur_b, cur_n = basis, norm
+    for w in range(windows):
+        sl = slice(w * window, (w + 1) * window)
+        r, cur_b, cur_n = herm.associative_scan_read(proj[:, sl].contiguous(), surprise[:, sl], valid[:, sl], cur_b,
+                                                     cur_n, width=d, features=m)
+        assert torch.equal(read[:, sl], r), f"window {w}"
+    assert torch.equal(nb, cur_b) and torch.equal(nn, cur_n)
+
+
+def test_stack_sequence_matches_window_by_window_and_the_oracle(device):
+    b, length = 2, 30
+    settings = _settings(layers=3, scan_chunk=6)
+    params = _params(settings, seed=23)
+    params_np = _oracle_params(params)
+    ids = _ids(b, length, seed=12)
+    ids[1, 20:23] = herm.PAD_TOKEN_ID
+    tau = _pick_threshold(params_np, ids, settings)
+    settings = dataclasses.replace(settings, salience_threshold=tau)
+    cfg = settings.oracle_config()
+    prepared = herm.prepare_stack(params, settings, device)
+    ids_t = torch.from_numpy(ids).to(device)
+    want_logits, want_states = herm.prefill(prepared, settings, ids_t, herm.initial_states(settings, b, device))
+    logits, states = herm.stack_sequence(prepared, settings, ids_t, herm.initial_states(settings, b, device))
+    torch.cuda.synchronize()
+    scale = float(want_logits.abs().max())
+    assert float((logits - want_logits).abs().max()) <= 1e-5 * scale
+    for layer, (got, want) in enumerate(zip(states, want_states)):
+        for key, tensor in want.items():
+            if tensor.dtype.is_floating_point:
+                tol = 1e-5 * float(tensor.abs().max()) + 1e-7
+                assert float((got[key] - tensor).abs().max()) <= tol, f"layer {layer} {key}"
+            else:
+                assert torch.equal(got[key], tensor), f"layer {layer} {key}"
+    assert any(bool(st["salient_valid"].any()) for st in want_states)
+    o_logits, o_states = oherm.prefill(params_np, [oherm.initial_state(b, cfg) for _ in params_np], ids, cfg,
+                                       settings.scan_chunk)
+    _close(logits.cpu().numpy(), o_logits, float(np.abs(o_logits).max()), "sequence-parallel logits vs oracle")
+    for got, want in zip(states, o_states):
+        for key in ("local_valid", "salient_valid", "last_token"):
+            np.testing.assert_array_equal(got[key].cpu().numpy(), want[key])
+
+
+def test_sequence_prefill_graph_replays_equal_eager(device):
+    b, length = 2, 24
+    settings = _settings(layers=2, scan_chunk=6, salience_threshold=0.55)
+    prepared = herm.prepare_stack(_params(settings, seed=25), settings, device)
+    ids = torch.from_numpy(_ids(b, length, seed=13)).to(device)
+    want, want_states = herm.stack_sequence(prepared, settings, ids, herm.initial_states(settings, b, device))
+    seq = herm.SequencePrefill(prepared, settings, herm.initial_states(settings, b, device), ids)
+    first = None
+    for run in range(2):
+        got = seq.run(ids).clone()
+        torch.cuda.synchronize()
+        # the library GEMMs may be replayed from other algorithms inside the capture
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5 * float(want.abs().max()))
+        for g_state, w_state in zip(seq.states, want_states):
+            for key, tensor in w_state.items():
+                if tensor.dtype.is_floating_point:
+                    torch.testing.assert_close(g_state[key], tensor, rtol=1e-5, atol=1e-6)
+                else:
+                    assert torch.equal(g_state[key], tensor), f"run {run} {key}"
+        if first is None:
+            first = got
+        else:
+            assert torch.equal(got, first)
