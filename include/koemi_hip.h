@@ -245,15 +245,17 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
  * carried ring [carried] followed by positions 0 .. r * window - 1, each with
  * its flag. tail != 0: the last `capacity` entries with their flags, rows as
  * stored (the local ring; flags = valid). tail == 0: the salient_tail rule
- * above (flags = admission; invalid slots zeroed). Outputs
- * [batch, length / window + 1, capacity, width] keys and values and
- * [batch, length / window + 1, capacity] flags; row r = length / window is the
- * ring after the whole sequence. Requires carried >= capacity (a static ring,
- * state.py:43-76) and length % window == 0. */
+ * above (flags = admission; invalid slots zeroed). The rings carried into the
+ * windows r < length / window go to out_* ([batch * length / window,
+ * capacity, width] keys and values, [batch * length / window, capacity]
+ * flags; row b * (length / window) + r), the ring after the whole sequence
+ * to final_* ([batch, capacity, ...]). Requires carried >= capacity (a static
+ * ring, state.py:43-76) and length % window == 0. */
 int koemi_window_rings(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
                        const void* keys, const void* values, const uint8_t* flags, void* out_keys, void* out_values,
-                       uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length, int64_t window,
-                       int64_t width, int64_t capacity, int tail, int dtype, koemi_stream_t stream);
+                       uint8_t* out_valid, void* final_keys, void* final_values, uint8_t* final_valid, int64_t batch,
+                       int64_t carried, int64_t length, int64_t window, int64_t width, int64_t capacity, int tail,
+                       int dtype, koemi_stream_t stream);
 
 /* The local and the salient read of a one-position window (a decode step,
  * network.py:337-358: LocalKeyValueMemory.read_window and

@@ -37,17 +37,28 @@ constexpr int kTailSlotsPerBlock = 4;  // output slots copied by one workgroup
 // of W positions plus the final one. TAIL: the last C entries whatever their
 // flags (LocalKeyValueMemory.tail, memory.py:385-403), rows copied as stored;
 // otherwise the salient rule above (flag = admission).
+// Outputs: ring row r < R - 1 of batch row b goes to row b * (R - 1) + r of
+// (ok, ov, ovalid), row R - 1 to row b of (fk, fv, fvalid); with R = 1 every
+// ring is a final one.
 template <typename T, bool VEC, bool TAIL>
 __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
     const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid, const T* __restrict__ k,
     const T* __restrict__ v, const uint8_t* __restrict__ adm, T* __restrict__ ok, T* __restrict__ ov,
-    uint8_t* __restrict__ ovalid, int64_t S, int64_t L, int64_t D, int64_t C, int64_t R, int64_t W) {
+    uint8_t* __restrict__ ovalid, T* __restrict__ fk, T* __restrict__ fv, uint8_t* __restrict__ fvalid, int64_t S,
+    int64_t L, int64_t D, int64_t C, int64_t R, int64_t W) {
     __shared__ int32_t slot_entry[kMaxCapacity];
     __shared__ uint8_t slot_valid[kMaxCapacity];
     __shared__ int64_t wave_tot[kTailThreads / kWave];
-    const int64_t row = blockIdx.x;
-    const int64_t b = row / R;
-    const int64_t Lr = L - (R - 1 - (row - b * R)) * W;
+    const int64_t b = static_cast<int64_t>(blockIdx.x) / R;
+    const int64_t r_in = static_cast<int64_t>(blockIdx.x) - b * R;
+    const int64_t Lr = L - (R - 1 - r_in) * W;
+    const bool final_ring = r_in == R - 1;
+    const int64_t row = final_ring ? b : b * (R - 1) + r_in;
+    if (final_ring) {
+        ok = fk;
+        ov = fv;
+        ovalid = fvalid;
+    }
     const int tid = threadIdx.x;
     const int64_t N = S + Lr;
     const bool concat = N <= C;
@@ -125,17 +136,19 @@ __global__ __launch_bounds__(kTailThreads) void salient_tail_kernel(
 // output slots (the windowed form requires S >= C, so that every row has C).
 template <typename T>
 int launch_tail(const void* ck, const void* cv, const uint8_t* cvalid, const void* k, const void* v, const uint8_t* adm,
-                void* ok, void* ov, uint8_t* ovalid, int64_t B, int64_t S, int64_t L, int64_t D, int64_t C,
-                int64_t R, int64_t W, bool tail, const char* what, hipStream_t s) {
+                void* ok, void* ov, uint8_t* ovalid, void* fk, void* fv, uint8_t* fvalid, int64_t B, int64_t S,
+                int64_t L, int64_t D, int64_t C, int64_t R, int64_t W, bool tail, const char* what, hipStream_t s) {
     const int64_t slots = S + L <= C ? S + L : C;
     const dim3 grid(static_cast<unsigned>(B * R), static_cast<unsigned>((slots + kTailSlotsPerBlock - 1) / kTailSlotsPerBlock));
     const size_t align = sizeof(T) == 4 ? 16 : 8;
     auto aligned = [&](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % align == 0; };
-    const bool vec = D % 4 == 0 && aligned(ck) && aligned(cv) && aligned(k) && aligned(v) && aligned(ok) && aligned(ov);
+    const bool vec = D % 4 == 0 && aligned(ck) && aligned(cv) && aligned(k) && aligned(v) && aligned(ok) &&
+                     aligned(ov) && aligned(fk) && aligned(fv);
     auto launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(kTailThreads), 0, s, static_cast<const T*>(ck), static_cast<const T*>(cv),
                            cvalid, static_cast<const T*>(k), static_cast<const T*>(v), adm, static_cast<T*>(ok),
-                           static_cast<T*>(ov), ovalid, S, L, D, C, R, W);
+                           static_cast<T*>(ov), ovalid, static_cast<T*>(fk), static_cast<T*>(fv), fvalid, S, L, D, C,
+                           R, W);
     };
     if (tail) {
         if (vec) launch(salient_tail_kernel<T, true, true>);
@@ -172,24 +185,24 @@ extern "C" int koemi_salient_tail(const void* carried_keys, const void* carried_
     switch (dtype) {
         case KOEMI_F32:
             return launch_tail<float>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                      out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
-                                      "koemi_salient_tail", s);
+                                      out_values, out_valid, out_keys, out_values, out_valid, batch, carried, length,
+                                      width, capacity, 1, 0, false, "koemi_salient_tail", s);
         case KOEMI_F16:
             return launch_tail<f16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                    out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
-                                    "koemi_salient_tail", s);
+                                    out_values, out_valid, out_keys, out_values, out_valid, batch, carried, length,
+                                    width, capacity, 1, 0, false, "koemi_salient_tail", s);
         default:
             return launch_tail<bf16>(carried_keys, carried_values, carried_valid, keys, values, admission, out_keys,
-                                     out_values, out_valid, batch, carried, length, width, capacity, 1, 0, false,
-                                     "koemi_salient_tail", s);
+                                     out_values, out_valid, out_keys, out_values, out_valid, batch, carried, length,
+                                     width, capacity, 1, 0, false, "koemi_salient_tail", s);
     }
 }
 
 extern "C" int koemi_window_rings(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
                                   const void* keys, const void* values, const uint8_t* flags, void* out_keys,
-                                  void* out_values, uint8_t* out_valid, int64_t batch, int64_t carried, int64_t length,
-                                  int64_t window, int64_t width, int64_t capacity, int tail, int dtype,
-                                  koemi_stream_t stream) {
+                                  void* out_values, uint8_t* out_valid, void* final_keys, void* final_values,
+                                  uint8_t* final_valid, int64_t batch, int64_t carried, int64_t length, int64_t window,
+                                  int64_t width, int64_t capacity, int tail, int dtype, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1 || window < 1)
         return fail(KOEMI_ERR_INVALID, "window rings need non-negative sizes, a positive width and window");
     if (length % window) return fail(KOEMI_ERR_INVALID, "window rings need a length that is a multiple of the window");
@@ -201,23 +214,23 @@ extern "C" int koemi_window_rings(const void* carried_keys, const void* carried_
         return fail(KOEMI_ERR_UNSUPPORTED, "window rings: too many rows or entries");
     if (!float_dtype(dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "window rings do not support dtype %s", dtype_name(dtype));
     if (batch == 0) return KOEMI_OK;
-    if (!carried_keys || !carried_values || !carried_valid || (length > 0 && (!keys || !values || !flags)) ||
-        !out_keys || !out_values || !out_valid)
+    if (!carried_keys || !carried_values || !carried_valid || (length > 0 && (!keys || !values || !flags ||
+        !out_keys || !out_values || !out_valid)) || !final_keys || !final_values || !final_valid)
         return fail(KOEMI_ERR_INVALID, "window rings received a null pointer");
     hipStream_t s = as_stream(stream);
     const bool t = tail != 0;
     switch (dtype) {
         case KOEMI_F32:
             return launch_tail<float>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
-                                      out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
-                                      "koemi_window_rings", s);
+                                      out_values, out_valid, final_keys, final_values, final_valid, batch, carried,
+                                      length, width, capacity, rows, window, t, "koemi_window_rings", s);
         case KOEMI_F16:
             return launch_tail<f16>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
-                                    out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
-                                    "koemi_window_rings", s);
+                                    out_values, out_valid, final_keys, final_values, final_valid, batch, carried,
+                                    length, width, capacity, rows, window, t, "koemi_window_rings", s);
         default:
             return launch_tail<bf16>(carried_keys, carried_values, carried_valid, keys, values, flags, out_keys,
-                                     out_values, out_valid, batch, carried, length, width, capacity, rows, window, t,
-                                     "koemi_window_rings", s);
+                                     out_values, out_valid, final_keys, final_values, final_valid, batch, carried,
+                                     length, width, capacity, rows, window, t, "koemi_window_rings", s);
     }
 }

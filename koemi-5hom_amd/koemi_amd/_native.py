@@ -85,7 +85,8 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     ),
     "koemi_window_rings": (
         c_int,
-        (_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, c_int, _P),
+        (_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int,
+         c_int, _P),
     ),
     "koemi_recurrent_gates_workspace_bytes": (c_size_t, (c_int64, c_int64)),
     "koemi_recurrent_gates": (

@@ -469,23 +469,32 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
 
 
 def window_rings(carried_keys: Tensor, carried_values: Tensor, carried_flags: Tensor, keys: Tensor, values: Tensor,
-                 flags: Tensor, *, window: int, capacity: int, tail: bool) -> tuple[Tensor, Tensor, Tensor]:
+                 flags: Tensor, *, window: int, capacity: int, tail: bool
+                 ) -> tuple[tuple[Tensor, Tensor, Tensor], tuple[Tensor, Tensor, Tensor]]:
     """The ring carried into every window of a sequence and the ring after it
-    (``koemi_window_rings``): ``[B, L / window + 1, capacity, D]`` keys and
-    values, ``[B, L / window + 1, capacity]`` flags. ``tail``: the local ring
-    (the last ``capacity`` entries, LocalKeyValueMemory.tail, memory.py:
-    385-403); otherwise the salient ring (salient_tail, memory.py:431-455)."""
+    (``koemi_window_rings``): ``((keys, values, flags), (final keys, final
+    values, final flags))`` with ``[B * L / window, capacity, D]`` keys and
+    values and ``[B * L / window, capacity]`` flags (row ``b * L / window +
+    w`` is the ring carried into window ``w`` of batch row ``b``, the layout
+    the batched window reads take), and ``[B, capacity, ...]`` finals.
+    ``tail``: the local ring (the last ``capacity`` entries,
+    LocalKeyValueMemory.tail, memory.py:385-403); otherwise the salient ring
+    (salient_tail, memory.py:431-455)."""
 
     batch, length, width = keys.shape
-    rows = length // window + 1
-    out_k = torch.empty((batch, rows, capacity, width), device=keys.device, dtype=keys.dtype)
+    rows = batch * (length // window)
+    out_k = torch.empty((rows, capacity, width), device=keys.device, dtype=keys.dtype)
     out_v = torch.empty_like(out_k)
-    out_ok = torch.empty((batch, rows, capacity), device=keys.device, dtype=torch.bool)
+    out_ok = torch.empty((rows, capacity), device=keys.device, dtype=torch.bool)
+    fin_k = torch.empty((batch, capacity, width), device=keys.device, dtype=keys.dtype)
+    fin_v = torch.empty_like(fin_k)
+    fin_ok = torch.empty((batch, capacity), device=keys.device, dtype=torch.bool)
     args = [t.contiguous() for t in (carried_keys, carried_values, carried_flags, keys, values, flags)]
     _native.call("koemi_window_rings", *(_native.ptr(t) for t in args), _native.ptr(out_k), _native.ptr(out_v),
-                 _native.ptr(out_ok), batch, carried_keys.shape[1], length, window, width, capacity, int(tail),
-                 _native.dtype_code(keys.dtype), _native.stream_of(keys.device))
-    return out_k, out_v, out_ok
+                 _native.ptr(out_ok), _native.ptr(fin_k), _native.ptr(fin_v), _native.ptr(fin_ok), batch,
+                 carried_keys.shape[1], length, window, width, capacity, int(tail), _native.dtype_code(keys.dtype),
+                 _native.stream_of(keys.device))
+    return (out_k, out_v, out_ok), (fin_k, fin_v, fin_ok)
 
 
 def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor,
@@ -518,6 +527,27 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
         batch, windows, window, d, m, _native.ptr(workspace), workspace.numel(), _native.stream_of(projections.device),
     )
     return read, next_basis, next_normalizer
+
+
+def _surprise_after(p: dict[str, Tensor], ws: Tensor, carried: Tensor, targets: Tensor, valid: Tensor) -> Tensor:
+    """causal_surprise of every position from the state before it (the carried
+    state, then the window's own; network.py:318-325, 677-698) without forming
+    the shifted states: the content logits of the carried state and of every
+    working state (the same fp32 products and row kernel as
+    ``think.causal_surprise``), each working state's row scored against the
+    next position's target. Returns fp32 [B, L]."""
+
+    batch, length, d = ws.shape
+    weight_t = p["content_w"].t()
+    logits = torch.mm(ws.view(batch * length, d), weight_t)
+    first = torch.mm(carried, weight_t)
+    next_targets = torch.cat((targets[:, 1:], targets[:, :1]), dim=1)      # row t scores target t + 1
+    next_valid = torch.cat((valid[:, 1:], torch.zeros_like(valid[:, :1])), dim=1)
+    later = think.surprise_from_logits(logits, next_targets.view(-1), next_valid.view(-1),
+                                       content_bias=p["content_b"]).view(batch, length)
+    start = think.surprise_from_logits(first, targets[:, 0].contiguous(), valid[:, 0].contiguous(),
+                                       content_bias=p["content_b"])
+    return torch.cat((start.unsqueeze(1), later[:, :-1]), dim=1)
 
 
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
@@ -558,8 +588,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
                                    with_bf16=low is not None)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    prior = torch.cat((state["working"].unsqueeze(1), ws[:, :-1]), dim=1)
-    surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
+    surprise = _surprise_after(p, ws, state["working"], targets, valid)
 
     projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
     local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
@@ -567,35 +596,33 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
                  _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
     cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
-    lk, lv, lok = window_rings(state["local_keys"], state["local_values"], state["local_valid"], local_keys,
-                               local_values, valid, window=chunk, capacity=cap_l, tail=True)
+    local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],
+                                            local_keys, local_values, valid, window=chunk, capacity=cap_l, tail=True)
     per_window = lambda t: t.view(rows, chunk, *t.shape[2:])
-    carried = lambda t: t[:, :windows].reshape(rows, *t.shape[2:])
-    local_value = memory.read_local_window(carried(lk), carried(lv), carried(lok), per_window(local_keys),
-                                           per_window(local_values), per_window(valid), per_window(ws),
-                                           window=cap_l).view(batch, length, d)
+    local_value = memory.read_local_window(*local_rings, per_window(local_keys), per_window(local_values),
+                                           per_window(valid), per_window(ws), window=cap_l).view(batch, length, d)
 
     fast, basis, normalizer = associative_scan_read_windows(projected, surprise, valid, state["basis"],
                                                             state["normalizer"], width=d,
                                                             features=settings.memory_features, window=chunk)
     admission = think.admission_above(surprise, valid, settings.salience_threshold)
-    sk, sv, sok = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
-                               local_values, admission, window=chunk, capacity=cap_s, tail=False)
-    salient_value = memory.read_salient_window(carried(sk), carried(sv), carried(sok), per_window(local_keys),
-                                               per_window(local_values), per_window(admission),
-                                               per_window(ws)).view(batch, length, d)
+    salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
+                                                local_keys, local_values, admission, window=chunk, capacity=cap_s,
+                                                tail=False)
+    salient_value = memory.read_salient_window(*salient_rings, per_window(local_keys), per_window(local_values),
+                                               per_window(admission), per_window(ws)).view(batch, length, d)
     final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, (ws, fast, local_value, salient_value),
                                       with_logits)
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
         "normalizer": normalizer,
-        "local_keys": lk[:, windows].contiguous(),
-        "local_values": lv[:, windows].contiguous(),
-        "local_valid": lok[:, windows].contiguous(),
-        "salient_keys": sk[:, windows].contiguous(),
-        "salient_values": sv[:, windows].contiguous(),
-        "salient_valid": sok[:, windows].contiguous(),
+        "local_keys": local_final[0],
+        "local_values": local_final[1],
+        "local_valid": local_final[2],
+        "salient_keys": salient_final[0],
+        "salient_values": salient_final[1],
+        "salient_valid": salient_final[2],
         "last_token": last_token,
     }
     return logits, final, next_state, surprise

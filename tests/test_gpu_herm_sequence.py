@@ -55,8 +55,12 @@ def test_window_rings_equal_the_window_by_window_rings(device, p_flag):
     ck, cv, cok, k, v, flags = _rand_rings(rng, b, s, window * windows, d, p_flag)
     t = lambda x: torch.from_numpy(x).to(device)
     for tail in (False, True):
-        got_k, got_v, got_ok = herm.window_rings(t(ck), t(cv), t(cok), t(k), t(v), t(flags), window=window,
-                                                 capacity=s, tail=tail)
+        rings, final = herm.window_rings(t(ck), t(cv), t(cok), t(k), t(v), t(flags), window=window, capacity=s,
+                                         tail=tail)
+        per_row = [x.view(b, windows, *x.shape[1:]) for x in rings]
+        got_k = torch.cat((per_row[0], final[0].unsqueeze(1)), dim=1)
+        got_v = torch.cat((per_row[1], final[1].unsqueeze(1)), dim=1)
+        got_ok = torch.cat((per_row[2], final[2].unsqueeze(1)), dim=1)
         rk, rv, rok = ck, cv, cok
         for w in range(windows + 1):
             np.testing.assert_array_equal(got_ok[:, w].cpu().numpy(), rok, err_msg=f"tail={tail} w={w}")
