@@ -101,6 +101,9 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the C5 prefill steps (for rocprofv3 runs of the headline alone)")
+    ap.add_argument("--rows-only", action="store_true",
+                    help="only the kernel rows of --configs (for rocprofv3 runs of one configuration's kernels); "
+                         "prints them as JSON")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run each HBM kernel a few times at its config plus a device copy of known size, for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (prints nothing else)")
@@ -488,122 +491,13 @@ class Timer:
         return statistics.median(times)
 
 
-def main() -> int:
-    args = parse_args()
-    if args.summarize_pmc:
-        return summarize_pmc(*args.summarize_pmc)
-    if args.traffic_probe:
-        return traffic_probe()
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures a single GPU: this build has no multi-GPU path and every box here has one GPU; "
-              "run with --gpus 1", file=sys.stderr, flush=True)
-        return 2
+def kernel_rows(args, extra: list, device, stream, timer, kernels: dict) -> None:
+    """The per-kernel rows of the configurations in ``extra`` (1, 2, 3, 4, 5, g) into ``kernels``."""
 
     import torch
 
-    from koemi_amd import core, dense, herm, memory, moe, recurrent, think, workloads
+    from koemi_amd import core, dense, memory, moe, recurrent, think, workloads
 
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    stream = torch.cuda.current_stream(device)
-    timer = Timer(torch, stream)
-    kernels: dict = {}
-
-    # ------------------------------------------------------------ headline C5
-    log("C5: initialising the 12-layer stack")
-    settings = herm.HermSettings()
-    params = herm.prepare_stack(herm.init_stack(settings, 1005, device), settings, device)
-    c5 = workloads.config5()
-    ids = c5.prefill_ids.to(device)
-    start_states = herm.initial_states(settings, C5_BATCH, device)
-
-    sequential = None
-    if not args.headline_only:
-        sequential = window_by_window_rows(args, herm, params, settings, ids, start_states, kernels)
-
-    log("C5: sequence-parallel prefill (one HIP graph): capture and check against the window-by-window prefill")
-    seq = herm.SequencePrefill(params, settings, start_states, ids)
-    logits = seq.run(ids).clone()
-    torch.cuda.synchronize()
-    assert torch.isfinite(logits).all(), "non-finite prefill logits"
-    seq_rel = None
-    if sequential is not None:
-        seq_rel = float((logits - sequential).norm() / sequential.norm())
-        assert seq_rel < 1e-2, f"sequence-parallel prefill differs from the window-by-window one: {seq_rel:.3e}"
-    reference_logits = logits
-
-    log(f"C5: {args.warmup} warmup + {args.steps} timed prefill steps")
-    for _ in range(args.warmup):
-        logits = seq.run(ids)
-    torch.cuda.synchronize()
-    start_ev, end_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start_ev.record(stream)
-    for _ in range(args.steps):
-        logits = seq.run(ids)
-    end_ev.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = start_ev.elapsed_time(end_ev)
-    ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
-    value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
-    assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
-    kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
-                             "vs_window_by_window_rel": None if seq_rel is None else round(seq_rel, 6),
-                             "schedule": "sequence-parallel: each layer over all 2048 positions (the windows' "
-                                         "carried states from one scan, window rings and a windowed associative "
-                                         "memory), the whole stack replayed from one HIP graph"}
-    del seq, logits, sequential, reference_logits
-
-    if not args.headline_only:
-        log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
-        decode = herm.DecodeGraph(params, settings, c5.decode_ids.to(device),
-                                  herm.initial_states(settings, C5_DECODE_BATCH, device))
-        for _ in range(3):
-            decode.step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(C5_DECODE_STEPS):
-            decode.step()
-        torch.cuda.synchronize()
-        decode_s = time.perf_counter() - t0
-        kernels["C5.decode"] = {"ms_per_step": round(decode_s * 1e3 / C5_DECODE_STEPS, 4),
-                                "tokens_per_s": round(C5_DECODE_BATCH * C5_DECODE_STEPS / decode_s, 1),
-                                "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
-        del decode
-
-    # --------------------------------------------- dominant kernel of C5 prefill
-    # The expert FFN of one layer over the whole prefill at its exact shape:
-    # the prefill ids routed by the hash (as every layer routes them), bf16
-    # contexts, each layer's own weights in turn (two layers' experts, 403 MB,
-    # do not fit the Infinity Cache, as the stack's twelve do not).
-    log("C5: dominant kernel (the expert FFN of one layer over the prefill), live timing")
-    valid5 = ids != herm.PAD_TOKEN_ID
-    prev5 = torch.cat((torch.full_like(ids[:, :1], herm.PAD_TOKEN_ID), ids[:, :-1]), dim=1)
-    assign5 = moe.route_topk_valid(ids, prev5, valid5, expert_count=C5_E, top_k=C5_K)
-    ffn_sets = []
-    for layer in (0, 1):
-        ctx5 = torch.randn((C5_PREFILL_TOKENS, C5_WIDTH), device=device).to(torch.bfloat16)
-        sc, rows, experts, offsets = moe.permute_topk(ctx5, assign5.reshape(-1, C5_K), valid5.reshape(-1),
-                                                      expert_count=C5_E)
-        p = params[layer]
-        ffn_sets.append((sc, experts, offsets, p["gate_w"], p["gate_b"], p["up_w"], p["up_b"], p["down_w"],
-                         p["down_b"]))
-    ffn_ms = timer.per_launch_ms([lambda s=s: moe.grouped_expert_mlp_inference(*s, validate=False) for s in ffn_sets],
-                                 4, max(10, args.kernel_iters))
-    ffn_tflops = C5_FFN_FLOP / ffn_ms / 1e9
-    kernels["C5.expert_ffn_layer"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
-                                      "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
-                                      "pairs": C5_PAIRS, "flop": C5_FFN_FLOP}
-    headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", None),
-                         "kernel": "grouped expert GLU FFN of one C5 layer over the prefill: grouped_gemm_bf16_kernel "
-                                   "launches of GEMM 1 (gate + value, SiLU-GLU epilogue) and GEMM 2 with the device "
-                                   "tile schedule, split-K partial tiles and their fix-ups",
-                         "algorithmic_flop": C5_FFN_FLOP, "avg_ms": round(ffn_ms, 5)}
-    del ffn_sets
-    extra = [c for c in args.configs.split(",") if c.strip()] if not args.headline_only else []
     iters = args.kernel_iters
 
     # ---------------------------------------------------------------- C2 step
@@ -760,6 +654,132 @@ def main() -> int:
         kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
                                          "note": "the gate GEMMs, then the gates formed inside the affine scan"}
         del ug, wts, vg
+
+
+
+def main() -> int:
+    args = parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc)
+    if args.traffic_probe:
+        return traffic_probe()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures a single GPU: this build has no multi-GPU path and every box here has one GPU; "
+              "run with --gpus 1", file=sys.stderr, flush=True)
+        return 2
+
+    import torch
+
+    from koemi_amd import core, dense, herm, memory, moe, recurrent, think, workloads
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stream = torch.cuda.current_stream(device)
+    timer = Timer(torch, stream)
+    kernels: dict = {}
+
+    if args.rows_only:
+        extra = [c for c in args.configs.split(",") if c.strip()]
+        kernel_rows(args, extra, device, stream, timer, kernels)
+        print(json.dumps({"kernels": kernels}), flush=True)
+        return 0
+
+    # ------------------------------------------------------------ headline C5
+    log("C5: initialising the 12-layer stack")
+    settings = herm.HermSettings()
+    params = herm.prepare_stack(herm.init_stack(settings, 1005, device), settings, device)
+    c5 = workloads.config5()
+    ids = c5.prefill_ids.to(device)
+    start_states = herm.initial_states(settings, C5_BATCH, device)
+
+    sequential = None
+    if not args.headline_only:
+        sequential = window_by_window_rows(args, herm, params, settings, ids, start_states, kernels)
+
+    log("C5: sequence-parallel prefill (one HIP graph): capture and check against the window-by-window prefill")
+    seq = herm.SequencePrefill(params, settings, start_states, ids)
+    logits = seq.run(ids).clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(logits).all(), "non-finite prefill logits"
+    seq_rel = None
+    if sequential is not None:
+        seq_rel = float((logits - sequential).norm() / sequential.norm())
+        assert seq_rel < 1e-2, f"sequence-parallel prefill differs from the window-by-window one: {seq_rel:.3e}"
+    reference_logits = logits
+
+    log(f"C5: {args.warmup} warmup + {args.steps} timed prefill steps")
+    for _ in range(args.warmup):
+        logits = seq.run(ids)
+    torch.cuda.synchronize()
+    start_ev, end_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start_ev.record(stream)
+    for _ in range(args.steps):
+        logits = seq.run(ids)
+    end_ev.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start_ev.elapsed_time(end_ev)
+    ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
+    value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
+    assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
+    kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
+                             "vs_window_by_window_rel": None if seq_rel is None else round(seq_rel, 6),
+                             "schedule": "sequence-parallel: each layer over all 2048 positions (the windows' "
+                                         "carried states from one scan, window rings and a windowed associative "
+                                         "memory), the whole stack replayed from one HIP graph"}
+    del seq, logits, sequential, reference_logits
+
+    if not args.headline_only:
+        log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
+        decode = herm.DecodeGraph(params, settings, c5.decode_ids.to(device),
+                                  herm.initial_states(settings, C5_DECODE_BATCH, device))
+        for _ in range(3):
+            decode.step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(C5_DECODE_STEPS):
+            decode.step()
+        torch.cuda.synchronize()
+        decode_s = time.perf_counter() - t0
+        kernels["C5.decode"] = {"ms_per_step": round(decode_s * 1e3 / C5_DECODE_STEPS, 4),
+                                "tokens_per_s": round(C5_DECODE_BATCH * C5_DECODE_STEPS / decode_s, 1),
+                                "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
+        del decode
+
+    # --------------------------------------------- dominant kernel of C5 prefill
+    # The expert FFN of one layer over the whole prefill at its exact shape:
+    # the prefill ids routed by the hash (as every layer routes them), bf16
+    # contexts, each layer's own weights in turn (two layers' experts, 403 MB,
+    # do not fit the Infinity Cache, as the stack's twelve do not).
+    log("C5: dominant kernel (the expert FFN of one layer over the prefill), live timing")
+    valid5 = ids != herm.PAD_TOKEN_ID
+    prev5 = torch.cat((torch.full_like(ids[:, :1], herm.PAD_TOKEN_ID), ids[:, :-1]), dim=1)
+    assign5 = moe.route_topk_valid(ids, prev5, valid5, expert_count=C5_E, top_k=C5_K)
+    ffn_sets = []
+    for layer in (0, 1):
+        ctx5 = torch.randn((C5_PREFILL_TOKENS, C5_WIDTH), device=device).to(torch.bfloat16)
+        sc, rows, experts, offsets = moe.permute_topk(ctx5, assign5.reshape(-1, C5_K), valid5.reshape(-1),
+                                                      expert_count=C5_E)
+        p = params[layer]
+        ffn_sets.append((sc, experts, offsets, p["gate_w"], p["gate_b"], p["up_w"], p["up_b"], p["down_w"],
+                         p["down_b"]))
+    ffn_ms = timer.per_launch_ms([lambda s=s: moe.grouped_expert_mlp_inference(*s, validate=False) for s in ffn_sets],
+                                 4, max(10, args.kernel_iters))
+    ffn_tflops = C5_FFN_FLOP / ffn_ms / 1e9
+    kernels["C5.expert_ffn_layer"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
+                                      "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
+                                      "pairs": C5_PAIRS, "flop": C5_FFN_FLOP}
+    headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", None),
+                         "kernel": "grouped expert GLU FFN of one C5 layer over the prefill: grouped_gemm_bf16_kernel "
+                                   "launches of GEMM 1 (gate + value, SiLU-GLU epilogue) and GEMM 2 with the device "
+                                   "tile schedule, split-K partial tiles and their fix-ups",
+                         "algorithmic_flop": C5_FFN_FLOP, "avg_ms": round(ffn_ms, 5)}
+    del ffn_sets
+    extra = [c for c in args.configs.split(",") if c.strip()] if not args.headline_only else []
+    kernel_rows(args, extra, device, stream, timer, kernels)
 
     # ------------------------------------------------------------ CPU baseline
     cpu_baseline = None

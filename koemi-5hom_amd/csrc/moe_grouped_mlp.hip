@@ -39,28 +39,37 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kBK = 32;
-#ifndef KOEMI_GEMM_STAGES
-#define KOEMI_GEMM_STAGES 4
-#endif
-constexpr int kStages = KOEMI_GEMM_STAGES;
-static_assert(kStages == 4 || kStages == 5, "stage ring of four or five K tiles");
-// Five stages fill the 160 KiB of LDS; the epilogue's biases then live in the
-// last stage (free once the K loop is done), past the 128 KiB output regions.
-constexpr bool kBiasInStages = kStages >= 5;
 constexpr int kGemmThreads = 256;
-constexpr uint32_t kStageBytes = 2u * kBM * kBK * 2u;  // A and B, bf16
-constexpr uint32_t kOperandBytes = kBM * kBK * 2u;
+constexpr uint32_t kOperandBytes = kBM * kBK * 2u;  // the A operand of one stage (bf16)
 constexpr int kGroupM = 4;  // tile slots per group in the launch order
+
+// Two tile shapes. BNT = 256: a 256 x 256 tile, 256 accumulators per wave and
+// a ring of four 32 KiB stages (128 KiB of LDS), one workgroup per CU. BNT =
+// 128 (the default): a 256 x 128 tile, 128 accumulators per wave and three
+// 24 KiB stages (72 KiB), so that two workgroups share a CU and one's
+// epilogue, prologue and memory waits overlap the other's matrix work.
+#ifndef KOEMI_GEMM_BN
+#define KOEMI_GEMM_BN 256
+#endif
+template <int BNT>
+struct TileShape {
+    static constexpr int kNT = BNT / 64;                                 // n-tiles (32 wide) per wave
+    static constexpr int kStages = BNT == 256 ? 4 : 3;
+    static constexpr uint32_t kStageBytes = static_cast<uint32_t>(kBM + BNT) * kBK * 2u;
+    static constexpr int kCopies = 4 + kNT;                              // 1 KiB stage copies per wave and tile
+    static constexpr int kWgPerCu = BNT == 256 ? 1 : 2;
+    static constexpr int64_t kPartialFloats = static_cast<int64_t>(kBM) * BNT;
+};
 // Rows are 64 bytes; the K step of the fronts' MFMA shape check.
 constexpr int kKAlign = 64;
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// Split K for the last, sparse round: at most this many partial tiles (fp32
-// 256 x 256 each, 64 MiB in all) per GEMM launch.
+// Split K for the last, sparse round: at most this many partial tiles (fp32,
+// at most 256 x 256 each, 64 MiB in all) per GEMM launch.
 constexpr int kMaxSplitUnits = 256;
 constexpr int kMaxSplit = 8;  // chunks per leftover tile (the fixup reads every chunk)
-constexpr size_t kPartialTileFloats = static_cast<size_t>(kBM) * kBN;
+constexpr size_t kPartialTileFloats = static_cast<size_t>(kBM) * kBN;  // the workspace's room per partial tile
 
 struct MlpWorkspace {
     size_t hidden_off, slot_expert_off, slot_row_off, slot_end_off, partial_off, total;
@@ -189,12 +198,20 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
 }
 
 // Waits until at most n tiles of this wave's stage copies are outstanding
-// (eight copies per tile and wave), then joins the workgroup.
+// (CPT copies per tile and wave: eight for 256-wide tiles, six for 128-wide),
+// then joins the workgroup.
+template <int CPT>
 __device__ __forceinline__ void wait_tiles_and_sync(int64_t n) {
-    if (n >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-    else if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    static_assert(CPT == 8 || CPT == 6, "stage copies per tile");
+    if (CPT == 8) {
+        if (n >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        else if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        if (n >= 1) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
@@ -214,17 +231,20 @@ __device__ __forceinline__ void tile_coords(uint32_t logical, uint32_t slots, ui
 }
 
 // Work of one GEMM launch: `whole` tiles computed in full, then, when the tiles
-// left over after whole rounds of `cus` workgroups would fill at most half a
-// round, each leftover tile split along K into `split` chunks (at least two K
-// steps each) so that the last round keeps every CU busy. Partial tiles go to
+// left over after whole rounds of `cus` workgroups (those that run at once)
+// would fill at most half a round, each leftover tile split along K into
+// `split` chunks (at least two K steps each) so that the last round keeps
+// every CU busy. Partial tiles go to
 // the workspace as fp32 and a fixup kernel adds them in chunk order.
 struct SplitPlan {
     uint32_t whole, units, split;
 };
 
-// float4 index of (wave, m-tile, n-tile, j, lane) in a partial tile.
+// float4 index of (wave, m-tile, n-tile, j, lane) in a partial tile of NT
+// n-tiles per wave.
+template <int NT>
 __device__ __forceinline__ int partial_slot(int wave, int mt, int t, int j, int lane) {
-    return (((wave * 4 + mt) * 4 + t) * 4 + j) * kWave + lane;
+    return (((wave * 4 + mt) * NT + t) * 4 + j) * kWave + lane;
 }
 __device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uint32_t cus) {
     SplitPlan p{tiles, 0, 1};
@@ -241,40 +261,42 @@ __device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uin
     return p;
 }
 
-// One 256x256 tile per workgroup. GLU: B rows 0..127 are gate rows and
-// 128..255 the value rows of hidden units [h0, h0 + 128), so wave (wm, wn) holds
-// gate and value accumulators of the same 128 rows x 64 hidden units and forms
-// silu(g + b_g) * (u + b_v) in registers. Plain: 256 consecutive output
-// columns. The MFMA is issued with the weight fragment as its first operand,
-// so each lane's accumulators are four consecutive output columns of one row
-// (8-byte stores). Launch order: workgroup i runs on XCD i % 8; tiles are
-// renumbered so that every XCD owns a contiguous range, traversed in groups of
-// kGroupM slots (all column tiles of a group before the next), which keeps the
-// A rows and B columns of concurrently running tiles in that XCD's L2.
-template <bool GLU, bool PARTIAL>
-__global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
+// One 256 x BNT tile per workgroup. GLU: B rows 0 .. BNT/2 - 1 are gate rows
+// and the next BNT/2 the value rows of hidden units [h0, h0 + BNT/2), so wave
+// (wm, wn) holds gate and value accumulators of the same 128 rows x BNT/4
+// hidden units and forms silu(g + b_g) * (u + b_v) in registers. Plain: BNT
+// consecutive output columns, BNT/2 per wave. The MFMA is issued with the
+// weight fragment as its first operand, so each lane's accumulators are four
+// consecutive output columns of one row (8-byte stores). Launch order:
+// workgroup i runs on XCD i % 8; tiles are renumbered so that every XCD owns a
+// contiguous range, traversed in groups of kGroupM slots (all column tiles of
+// a group before the next), which keeps the A rows and B columns of
+// concurrently running tiles in that XCD's L2.
+template <bool GLU, bool PARTIAL, int BNT>
+__global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void grouped_gemm_bf16_kernel(
     const bf16* __restrict__ A, const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
-    float* __restrict__ partial, uint32_t cus) {
+    float* __restrict__ partial, uint32_t rounds) {
+    using TS = TileShape<BNT>;
+    constexpr int NT = TS::kNT;
+    constexpr int kStages = TS::kStages;
+    constexpr uint32_t kStageBytes = TS::kStageBytes;
+    constexpr int CPT = TS::kCopies;
     __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
-    float* bias_sh;  // the tile's biases (epilogue)
-    if constexpr (kBiasInStages) {
-        bias_sh = reinterpret_cast<float*>(lds + 4 * kStageBytes);
-    } else {
-        __shared__ __attribute__((aligned(16))) float bias_arr[kGemmThreads];
-        bias_sh = bias_arr;
-    }
+    __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];
 
     // Whole tiles (PARTIAL false): the grid covers the most tiles the pairs can
     // need; the whole tiles of the split plan for the slots actually in use are
     // spread evenly over the eight XCDs (workgroup b runs on XCD b % 8) and the
     // surplus workgroups exit. Partial tiles (PARTIAL true): workgroup b takes
     // unit b of the plan, K steps [k_begin, k_end) of its leftover tile.
+    // `rounds` is the number of workgroups that run at once (CUs x workgroups
+    // per CU).
     const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
     const uint32_t nk_all = static_cast<uint32_t>(K / kBK);
-    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), nk_all, cus);
+    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), nk_all, rounds);
     uint32_t logical, unit = 0, k_begin = 0, k_end = nk_all;
     if constexpr (!PARTIAL) {
         const uint32_t per_xcd = (plan.whole + 7) / 8;
@@ -299,98 +321,102 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     const int lane = lane_id();
     const int wave = tid / kWave;
     const int wm = wave >> 1, wn = wave & 1;
-    const int64_t n0 = GLU ? static_cast<int64_t>(tile_n) * (kBN / 2) : static_cast<int64_t>(tile_n) * kBN;
+    const int64_t n0 = GLU ? static_cast<int64_t>(tile_n) * (BNT / 2) : static_cast<int64_t>(tile_n) * BNT;
 
-    // Stage copies: wave w fills 1 KiB chunks 4w..4w+3 (16 rows each) of A and
-    // of B; lane l of a chunk copies row l / 4 of it, K group (l % 4) ^ swizzle.
-    // Rows past the segment or the output width are clamped (they only feed
-    // discarded outputs). Offsets are 32-bit and relative to per-tile bases
-    // (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves 0-1
-    // copy gate rows, waves 2-3 value rows.
-    // A partial tile runs K steps [k_begin, k_end): the bases start there.
+    // Stage copies: A is 16 chunks of 1 KiB (16 rows each), wave w filling
+    // chunks 4w .. 4w + 3; B is BNT / 16 chunks, wave w filling NT chunks from
+    // NT w. Lane l of a chunk copies row l / 4 of it, K group (l % 4) ^
+    // swizzle. Rows past the segment or the output width are clamped (they only
+    // feed discarded outputs). Offsets are 32-bit and relative to per-tile
+    // bases (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves
+    // 0-1 copy gate rows, waves 2-3 value rows. A partial tile runs K steps
+    // [k_begin, k_end): the bases start there.
     const int64_t k0 = static_cast<int64_t>(k_begin) * kBK;
     const bf16* a_base = static_cast<const bf16*>(uniform_ptr(A + row0 * K + k0));
     const bf16* b_base = static_cast<const bf16*>(
         uniform_ptr(((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K + k0));
     const int a_rows = static_cast<int>(row_end - row0);
-    uint32_t a_off[4], b_off[4];  // byte offsets (the entry point bounds them below 2^32)
+    uint32_t a_off[4], b_off[NT];  // byte offsets (the entry point bounds them below 2^32)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = (wave * 4 + i) * 16 + (lane >> 2);
         const int g = (lane & 3) ^ slot_swizzle(r);
         a_off[i] = (static_cast<uint32_t>(min(r, a_rows - 1)) * static_cast<uint32_t>(K) + g * 8) * 2u;
-        const int64_t n = GLU ? min(n0 + (r & 127), n_out - 1) : min(n0 + r, n_out - 1);
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int r = (wave * NT + i) * 16 + (lane >> 2);
+        const int g = (lane & 3) ^ slot_swizzle(r);
+        const int64_t n = GLU ? min(n0 + (r & (BNT / 2 - 1)), n_out - 1) : min(n0 + r, n_out - 1);
         b_off[i] = (static_cast<uint32_t>(n) * static_cast<uint32_t>(K) + g * 8) * 2u;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
-    const uint32_t wave_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * 4 * 1024);
+    const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * 4 * 1024);
+    const uint32_t b_lds = __builtin_amdgcn_readfirstlane(lds0 + kOperandBytes + wave * NT * 1024);
+    // Copy i of a stage: i < 4 is A chunk i of this wave, i >= 4 B chunk i - 4.
+    auto issue_one = [&](int64_t kt, int stage, int i) {
+        if (i < 4)
+            lds_dma16(a_lds + stage * kStageBytes + i * 1024, a_base + kt * kBK, a_off[i]);
+        else
+            lds_dma16(b_lds + stage * kStageBytes + (i - 4) * 1024, b_base + kt * kBK, b_off[i - 4]);
+    };
     auto issue = [&](int64_t kt, int stage) {
-        const uint32_t a_dst = wave_lds + stage * kStageBytes;
-        const bf16* ak = a_base + kt * kBK;
-        const bf16* bk = b_base + kt * kBK;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            lds_dma16(a_dst + i * 1024, ak, a_off[i]);
-            lds_dma16(a_dst + kOperandBytes + i * 1024, bk, b_off[i]);
-        }
+        for (int i = 0; i < CPT; ++i) issue_one(kt, stage, i);
     };
 
-    // Fragment rows: A rows of the wave's four m-tiles, B rows of its four
-    // n-tiles (GLU: two gate, two value).
+    // Fragment rows: A rows of the wave's four m-tiles, B rows of its NT
+    // n-tiles (GLU: NT / 2 gate, then NT / 2 value).
     const int fr = lane & 31;
     const int fg = lane >> 5;
 
     // The tile's biases (one per thread: GLU gate biases of hidden units
-    // [n0, n0 + 128) then their value biases; plain: 256 output columns) are
-    // loaded now and reach LDS at the epilogue, so their latency is hidden
-    // behind the main loop.
+    // [n0, n0 + BNT/2) then their value biases; plain: BNT output columns;
+    // threads past BNT load a clamped column nobody reads) are loaded now and
+    // reach LDS at the epilogue, so their latency is hidden behind the main
+    // loop.
     float bias_mine;
     {
-        const int64_t col = GLU ? min(n0 + (tid & 127), n_out - 1) : min(n0 + tid, n_out - 1);
-        const bf16* bsrc = (GLU && tid >= 128) ? bias1 : bias0;
+        const int64_t col = GLU ? min(n0 + (tid & (BNT / 2 - 1)), n_out - 1) : min(n0 + min(tid, BNT - 1), n_out - 1);
+        const bf16* bsrc = (GLU && (tid & (BNT - 1)) >= BNT / 2) ? bias1 : bias0;
         bias_mine = to_f32(bsrc[static_cast<int64_t>(e) * n_out + col]);
     }
-    f32x16 acc[4][4];
+    f32x16 acc[4][NT];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    int a_row[4], b_row[4];
+    int a_row[4], b_row[NT];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        a_row[t] = wm * 128 + t * 32 + fr;
-        b_row[t] = (GLU ? ((t < 2) ? wn * 64 + t * 32 : 128 + wn * 64 + (t - 2) * 32) : wn * 128 + t * 32) + fr;
-    }
+    for (int t = 0; t < 4; ++t) a_row[t] = wm * 128 + t * 32 + fr;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        b_row[t] = (GLU ? (t < NT / 2 ? wn * (BNT / 4) + t * 32 : BNT / 2 + wn * (BNT / 4) + (t - NT / 2) * 32)
+                        : wn * (BNT / 2) + t * 32) + fr;
 
-    auto read_frags = [&](int64_t kt, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
+    auto read_frags = [&](int64_t kt, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[NT]) {
         const char* As = lds + (kt % kStages) * kStageBytes;
         const char* Bs = As + kOperandBytes;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
-            bfr[t] = *reinterpret_cast<const bf16x8*>(Bs + stage_slot(b_row[t], kk * 2 + fg));
-        }
+        for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Bs + stage_slot(b_row[t], kk * 2 + fg));
     };
-    // Fragment f of a K step, in the order the MFMAs of the step consume them:
-    // A m-tile 0, B n-tiles 0-3, A m-tiles 1-3.
-    auto read_frag = [&](int64_t kt, int kk, int f, bf16x8 (&af)[4], bf16x8 (&bfr)[4]) {
+    // Fragment f of a K step (4 + NT of them), in the order the MFMAs of the
+    // step consume them: A m-tile 0, B n-tiles 0 .. NT - 1, A m-tiles 1-3.
+    auto read_frag = [&](int64_t kt, int kk, int f, bf16x8 (&af)[4], bf16x8 (&bfr)[NT]) {
         const char* As = lds + (kt % kStages) * kStageBytes;
-        if (f >= 1 && f <= 4)
+        if (f >= 1 && f <= NT)
             bfr[f - 1] = *reinterpret_cast<const bf16x8*>(As + kOperandBytes + stage_slot(b_row[f - 1], kk * 2 + fg));
         else {
-            const int t = f == 0 ? 0 : f - 4;
+            const int t = f == 0 ? 0 : f - NT;
             af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
         }
     };
-    // Copy i of a stage: i < 4 is A chunk i of this wave, i >= 4 B chunk i - 4.
-    auto issue_one = [&](int64_t kt, int stage, int i) {
-        const uint32_t dst = wave_lds + stage * kStageBytes + (i >= 4 ? kOperandBytes : 0u) + (i & 3) * 1024;
-        lds_dma16(dst, (i >= 4 ? b_base : a_base) + kt * kBK, i >= 4 ? b_off[i & 3] : a_off[i & 3]);
-    };
-    auto mfma_one = [&](int j, const bf16x8 (&af)[4], const bf16x8 (&bfr)[4]) {
-        acc[j >> 2][j & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j & 3], af[j >> 2], acc[j >> 2][j & 3], 0, 0, 0);
+    auto mfma_one = [&](int j, const bf16x8 (&af)[4], const bf16x8 (&bfr)[NT]) {
+        acc[j / NT][j % NT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j % NT], af[j / NT], acc[j / NT][j % NT], 0, 0, 0);
     };
 
     // K is a multiple of 64 and a partial tile has at least two K steps, so
@@ -400,41 +426,54 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
     // the one waited for at every barrier; no copy is issued past the last
     // tile, so none is outstanding at the epilogue.
     const int64_t nk = static_cast<int64_t>(k_end - k_begin);
-    issue(0, 0);
-    issue(1, 1);
-    if (nk >= 3) issue(2, 2);
-    if (kStages >= 5 && nk >= 4) issue(3, 3);
-    wait_tiles_and_sync(min(nk, static_cast<int64_t>(kStages - 1)) - 1);
-    bf16x8 a0[4], b0[4], a1[4], b1[4];
+#pragma unroll
+    for (int i = 0; i < kStages - 1; ++i)
+        if (i < nk) issue(i, i);
+    wait_tiles_and_sync<CPT>(min(nk, static_cast<int64_t>(kStages - 1)) - 1);
+    bf16x8 a0[4], b0[NT], a1[4], b1[NT];
     read_frags(0, 0, a0, b0);
-    // Each MFMA is followed by one other memory instruction (a stage copy or a
-    // fragment read for a later K step), pinned in place by scheduling
-    // barriers, so that the copies and LDS reads issue while the matrix pipe is
-    // busy instead of in a burst that leaves it idle.
+    // Each MFMA is followed by memory instructions for later work (stage copies
+    // and fragment reads), pinned in place by scheduling barriers, so that they
+    // issue while the matrix pipe is busy instead of in a burst that leaves it
+    // idle. 256-wide tiles: 16 MFMAs per half step, a copy after every even one
+    // and a fragment read after every odd one. 128-wide: 8 MFMAs per half
+    // step, copy j after MFMA j (six) and fragment j - 2 after MFMA j >= 2.
+    constexpr int MK = 4 * NT;  // MFMAs per half step
     auto k_step = [&](int64_t kt, auto copy_tag) {
         constexpr bool kCopy = decltype(copy_tag)::value;
-        // Tile kt + 1 has landed for every wave (one later copy may still be
-        // in flight: tile kt + 2, if there is one), and every wave is done
-        // with the stage of tile kt - 1, which this step's copy overwrites.
-        // Copies issued after tile kt + 1: tiles kt + 2 .. min(kt + kStages - 2, nk - 1).
-        if (kCopy) wait_tiles_and_sync(kStages - 3);
-        else wait_tiles_and_sync(max(min(nk - 2 - kt, static_cast<int64_t>(kStages - 3)), int64_t(0)));
+        // Tile kt + 1 has landed for every wave (later copies may still be in
+        // flight: tiles kt + 2 .. min(kt + kStages - 2, nk - 1)), and every
+        // wave is done with the stage of tile kt - 1, which this step's copy
+        // overwrites.
+        if (kCopy) wait_tiles_and_sync<CPT>(kStages - 3);
+        else wait_tiles_and_sync<CPT>(max(min(nk - 2 - kt, static_cast<int64_t>(kStages - 3)), int64_t(0)));
         const int sc = static_cast<int>((kt + kStages - 1) % kStages);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < MK; ++j) {
             mfma_one(j, a0, b0);
-            if (j % 2 == 0) {
-                if constexpr (kCopy) issue_one(kt + kStages - 1, sc, j / 2);
+            if constexpr (NT == 4) {
+                if (j % 2 == 0) {
+                    if constexpr (kCopy) issue_one(kt + kStages - 1, sc, j / 2);
+                } else {
+                    read_frag(kt, 1, j / 2, a1, b1);
+                }
             } else {
-                read_frag(kt, 1, j / 2, a1, b1);
+                if constexpr (kCopy) {
+                    if (j < CPT) issue_one(kt + kStages - 1, sc, j);
+                }
+                if (j >= 2) read_frag(kt, 1, j - 2, a1, b1);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         const int64_t kn = min(kt + 1, nk - 1);  // the last step re-reads its own stage harmlessly
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
+        for (int j = 0; j < MK; ++j) {
             mfma_one(j, a1, b1);
-            if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
+            if constexpr (NT == 4) {
+                if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
+            } else {
+                if (j >= 2) read_frag(kn, 0, j - 2, a0, b0);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -446,14 +485,14 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
         // Partial tile: the fp32 sums go to the workspace in accumulator order,
         // float4 (wave, mt, t, j, lane) holding elements 4j..4j+3 of n-tile t of
         // m-tile mt (partial_slot), so that each store writes 1 KiB contiguous.
-        float* pt = partial + static_cast<int64_t>(unit) * kPartialTileFloats;
+        float* pt = partial + static_cast<int64_t>(unit) * TS::kPartialFloats;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    *reinterpret_cast<float4*>(pt + partial_slot(wave, mt, t, j, lane) * 4) =
+                    *reinterpret_cast<float4*>(pt + partial_slot<NT>(wave, mt, t, j, lane) * 4) =
                         make_float4(acc[mt][t][j * 4 + 0], acc[mt][t][j * 4 + 1], acc[mt][t][j * 4 + 2],
                                     acc[mt][t][j * 4 + 3]);
         return;
@@ -461,33 +500,29 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
 
     // Epilogue through LDS, so that global stores are whole rows: each wave
     // writes its bias-added bf16 outputs (GLU: silu(g) * u) into its own LDS
-    // region, then reads it back row by row in
-    // 16-byte chunks and stores full 128-byte lines. Accumulator element v of
-    // lane l is row l % 32, column 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its
-    // 32x32 tile. Region rows are kOutCols bf16; the 16-byte chunk c of row r
-    // sits at chunk c ^ (r & kSwz) (conflict-free row reads). The GLU products
-    // of a 32x32 tile are formed sixteen at a time, each step over all sixteen
-    // (independent exp and reciprocal latencies overlap).
+    // region, then reads it back row by row in 16-byte chunks and stores full
+    // lines. Accumulator element v of lane l is row l % 32, column
+    // 4 * (l / 32) + (v % 4) + 8 * (v / 4) of its 32x32 tile. Region rows are
+    // kOutCols bf16; the 16-byte chunk c of row r sits at chunk c ^ (r & kSwz)
+    // (conflict-free row reads). The GLU products of a 32x32 tile are formed
+    // sixteen at a time, each step over all sixteen (independent exp and
+    // reciprocal latencies overlap).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no stage copy may still be writing LDS
-    if constexpr (kBiasInStages) {
-        __syncthreads();  // every wave is done reading the stages
-        bias_sh[tid] = bias_mine;
-        __syncthreads();  // the biases are in LDS
-    } else {
-        bias_sh[tid] = bias_mine;
-        __syncthreads();  // every wave is done reading the stages; the biases are in LDS
-    }
-    constexpr int kOutCols = GLU ? 64 : 128;  // columns of a wave's output tile
+    bias_sh[tid] = bias_mine;
+    __syncthreads();  // every wave is done reading the stages; the biases are in LDS
+    constexpr int kOutCols = GLU ? BNT / 4 : BNT / 2;  // columns of a wave's output tile
     constexpr int kRowBytes = kOutCols * 2;
     constexpr int kChunks = kRowBytes / 16;   // 16-byte chunks per row
     constexpr int kSwz = kChunks - 1;
+    static_assert(4 * 128 * kRowBytes <= kStages * kStageBytes, "output regions fit the stages");
     char* region = lds + wave * (128 * kRowBytes);
-    const int col_base = GLU ? wn * 64 : wn * 128;  // within the block tile's columns
+    const int col_base = GLU ? wn * (BNT / 4) : wn * (BNT / 2);  // within the block tile's columns
+    constexpr int kOutTiles = GLU ? NT / 2 : NT;
 #pragma unroll
-    for (int nt = 0; nt < (GLU ? 2 : 4); ++nt) {
+    for (int nt = 0; nt < kOutTiles; ++nt) {
         // Biases of the 16 columns of n-tile nt (the same for every m-tile):
         // runs of four at col_base + nt * 32 + fg * 4 + 8 j (GLU value biases
-        // 128 further on).
+        // BNT / 2 further on).
         float bias_g[16], bias_u[16];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -498,7 +533,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
             bias_g[j * 4 + 2] = bg4.z;
             bias_g[j * 4 + 3] = bg4.w;
             if constexpr (GLU) {
-                const float4 bu4 = *reinterpret_cast<const float4*>(&bias_sh[128 + cl]);
+                const float4 bu4 = *reinterpret_cast<const float4*>(&bias_sh[BNT / 2 + cl]);
                 bias_u[j * 4 + 0] = bu4.x;
                 bias_u[j * 4 + 1] = bu4.y;
                 bias_u[j * 4 + 2] = bu4.z;
@@ -521,7 +556,7 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
 #pragma unroll
                 for (int v = 0; v < 16; ++v) d[v] = __builtin_amdgcn_rcpf(1.0f + d[v]);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) o[v] = (g[v] * d[v]) * (acc[mt][nt + 2][v] + bias_u[v]);
+                for (int v = 0; v < 16; ++v) o[v] = (g[v] * d[v]) * (acc[mt][nt + NT / 2][v] + bias_u[v]);
             } else {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) o[v] = acc[mt][nt][v] + bias_g[v];
@@ -574,16 +609,19 @@ __global__ __launch_bounds__(kGemmThreads) void grouped_gemm_bf16_kernel(
 // value slot t + 2), reading the slot in every chunk (coalesced), and writes
 // the four consecutive outputs it holds: row wm * 128 + mt * 32 + lane % 32,
 // columns col_base + t * 32 + 4 (lane / 32) + 8 j (+0..3).
-template <bool GLU>
+template <bool GLU, int BNT>
 __global__ __launch_bounds__(256) void split_fixup_kernel(
     const float* __restrict__ partial, const bf16* __restrict__ bias0, const bf16* __restrict__ bias1,
     bf16* __restrict__ C, const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
-    uint32_t cus) {
+    uint32_t rounds) {
+    using TS = TileShape<BNT>;
+    constexpr int NT = TS::kNT;
+    constexpr int64_t kTileFloats = TS::kPartialFloats;
     const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
-    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), static_cast<uint32_t>(K / kBK), cus);
+    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), static_cast<uint32_t>(K / kBK), rounds);
     if (plan.units == 0) return;
-    constexpr uint32_t kSlotsPerTile = GLU ? kPartialTileFloats / 8 : kPartialTileFloats / 4;
+    constexpr uint32_t kSlotsPerTile = GLU ? kTileFloats / 8 : kTileFloats / 4;
     const uint32_t items = plan.units / plan.split * kSlotsPerTile;
     for (uint32_t item = blockIdx.x * blockDim.x + threadIdx.x; item < items; item += gridDim.x * blockDim.x) {
         const uint32_t rt = item / kSlotsPerTile;
@@ -592,8 +630,8 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(
         f /= kWave;
         const int j = static_cast<int>(f % 4);
         f /= 4;
-        const int t = static_cast<int>(f % (GLU ? 2 : 4));
-        f /= GLU ? 2 : 4;
+        const int t = static_cast<int>(f % (GLU ? NT / 2 : NT));
+        f /= GLU ? NT / 2 : NT;
         const int mt = static_cast<int>(f % 4);
         const int wave = static_cast<int>(f / 4);
         const int wm = wave >> 1, wn = wave & 1;
@@ -602,19 +640,19 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(
         const int e = slot_expert[slot];
         const int64_t grow = slot_row[slot] + wm * 128 + mt * 32 + (lane & 31);
         if (e < 0 || grow >= slot_end[slot]) continue;
-        const float* pt = partial + static_cast<int64_t>(rt) * plan.split * kPartialTileFloats;
-        const int64_t s0 = partial_slot(wave, mt, t, j, lane) * 4;
+        const float* pt = partial + static_cast<int64_t>(rt) * plan.split * kTileFloats;
+        const int64_t s0 = partial_slot<NT>(wave, mt, t, j, lane) * 4;
         // Chunks are loaded eight at a time and added in chunk order; chunks
         // past the split read as +0, which leaves a sum that starts at +0
         // unchanged.
-        const int64_t sv = partial_slot(wave, mt, GLU ? t + 2 : t, j, lane) * 4;
+        const int64_t sv = partial_slot<NT>(wave, mt, GLU ? t + NT / 2 : t, j, lane) * 4;
         float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
         for (uint32_t k0 = 0; k0 < plan.split; k0 += 8) {
             float4 pg[8], pu[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const bool in = k0 + i < plan.split;
-                const int64_t base = static_cast<int64_t>(in ? k0 + i : 0) * kPartialTileFloats;
+                const int64_t base = static_cast<int64_t>(in ? k0 + i : 0) * kTileFloats;
                 pg[i] = *reinterpret_cast<const float4*>(pt + base + s0);
                 if (!in) pg[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if constexpr (GLU) {
@@ -636,8 +674,8 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(
                 }
             }
         }
-        const int64_t col = (GLU ? static_cast<int64_t>(tile_n) * (kBN / 2) + wn * 64
-                                 : static_cast<int64_t>(tile_n) * kBN + wn * 128) +
+        const int64_t col = (GLU ? static_cast<int64_t>(tile_n) * (BNT / 2) + wn * (BNT / 4)
+                                 : static_cast<int64_t>(tile_n) * BNT + wn * (BNT / 2)) +
                             t * 32 + (lane >> 5) * 4 + j * 8;
         if (col >= n_out) continue;
         const int64_t bo = static_cast<int64_t>(e) * n_out + col;
@@ -896,7 +934,8 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     int st = check_launch("koemi_moe_grouped_mlp(schedule)");
     if (st != KOEMI_OK) return st;
     const int64_t slots = ws.max_slots;
-    const uint32_t cus = static_cast<uint32_t>(device_cus());
+    constexpr int BNT = KOEMI_GEMM_BN;
+    const uint32_t rounds = static_cast<uint32_t>(device_cus() * TileShape<BNT>::kWgPerCu);
     // Whole tiles, then the partial tiles of the split plan (if any; every
     // workgroup exits otherwise), then their sums.
     auto launch = [&](auto kernel, auto partial_kernel, auto fixup, const bf16* a, const void* w0, const void* w1,
@@ -907,27 +946,27 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid)), dim3(kGemmThreads), 0, s, a,
                            static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
                            static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
-                           partial, cus);
+                           partial, rounds);
         int st2 = check_launch(what);
         if (st2 != KOEMI_OK) return st2;
         hipLaunchKernelGGL(partial_kernel, dim3(kMaxSplitUnits), dim3(kGemmThreads), 0, s, a,
                            static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
                            static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
-                           partial, cus);
+                           partial, rounds);
         st2 = check_launch(what);
         if (st2 != KOEMI_OK) return st2;
         // At most kMaxSplitUnits / 2 leftover tiles of 8192 (GLU) or 16384 slots.
         hipLaunchKernelGGL(fixup, dim3(1024), dim3(256), 0, s, partial, static_cast<const bf16*>(b0),
                            static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots,
-                           n_tiles, cus);
+                           n_tiles, rounds);
         return check_launch(what);
     };
-    st = launch(grouped_gemm_bf16_kernel<true, false>, grouped_gemm_bf16_kernel<true, true>, split_fixup_kernel<true>,
-                static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D, (Hd + kBN / 2 - 1) / (kBN / 2),
-                "koemi_moe_grouped_mlp(gemm1)");
+    st = launch(grouped_gemm_bf16_kernel<true, false, BNT>, grouped_gemm_bf16_kernel<true, true, BNT>,
+                split_fixup_kernel<true, BNT>, static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D,
+                (Hd + BNT / 2 - 1) / (BNT / 2), "koemi_moe_grouped_mlp(gemm1)");
     if (st != KOEMI_OK) return st;
-    st = launch(grouped_gemm_bf16_kernel<false, false>, grouped_gemm_bf16_kernel<false, true>,
-                split_fixup_kernel<false>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd, (D + kBN - 1) / kBN,
+    st = launch(grouped_gemm_bf16_kernel<false, false, BNT>, grouped_gemm_bf16_kernel<false, true, BNT>,
+                split_fixup_kernel<false, BNT>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd, (D + BNT - 1) / BNT,
                 "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
     hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
