@@ -308,11 +308,16 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
  * valid) and h_t = a_t h_{t-1} + b_t from `initial` [batch, width] into
  * `states` [batch, length, width], as in network.py:306-310; with
  * `states_bf16` (NULL: none) also a bf16 copy of the states for the next
- * projection's GEMM. No workspace. */
+ * projection's GEMM. `workspace` (NULL: none, else at least
+ * koemi_gated_scan_workspace_bytes) lets a batch of a few long rows run as a
+ * two-phase scan: the transfers of every 8-step segment first, then chunks of
+ * the sequence in parallel, each from its carry composed through the segments
+ * before it in order, which gives the same bits as the one-pass scan. */
+size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
 int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                      int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
                      const uint8_t* valid, const float* initial, float* states, void* states_bf16, int64_t batch,
-                     int64_t length, int64_t width, koemi_stream_t stream);
+                     int64_t length, int64_t width, void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections
  * in a decode step: the gate, working-state, fusion and head layers of

@@ -30,6 +30,9 @@ namespace {
 #ifndef KOEMI_SCAN_SEGMENTS
 #define KOEMI_SCAN_SEGMENTS 8
 #endif
+#ifndef KOEMI_SCAN_BUFFERS
+#define KOEMI_SCAN_BUFFERS 3
+#endif
 constexpr int kScanSteps = KOEMI_SCAN_STEPS;        // S: serial steps per wave per chunk
 constexpr int kScanSegments = KOEMI_SCAN_SEGMENTS;  // NSEG: waves per workgroup
 
@@ -153,8 +156,6 @@ struct FloatVec<4> {
     __device__ static float4 join(const float (&o)[4]) { return make_float4(o[0], o[1], o[2], o[3]); }
 };
 
-constexpr float kGateMinRetention = 0.00390625f;        // 2^-8
-constexpr float kGateRetentionSpan = 1.0f - 0.0078125f;  // 1 - 2^-7
 
 // Gate inputs of the fused gates + scan (GATES): a and b point at the two
 // fp32 pre-activation products u W_r^T and u W_c^T (rows `stride` floats
@@ -170,37 +171,220 @@ struct GateInputs {
 };
 
 __device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
-    const float retention = 1.0f / (1.0f + expf(-(zr + br)));
-    const float ga = kGateMinRetention + kGateRetentionSpan * retention;
-    const float gb = (1.0f - ga) * tanhf(zc + bc);
+    const float ga = kGateMinRetention + kGateRetentionSpan * gate_sigmoid(zr + br);
+    const float gb = (1.0f - ga) * gate_tanh(zc + bc);
     a = keep ? ga : 1.0f;
     b = keep ? gb : 0.0f;
 }
-template <int S, int NSEG, int VEC, bool GATES = false>
+// VEC bf16 values in one store (2 VEC bytes, aligned to it).
+template <int VEC>
+__device__ __forceinline__ void store_bf16(__bf16* dst, const float (&o)[VEC]) {
+    if constexpr (VEC == 1) {
+        dst[0] = static_cast<__bf16>(o[0]);
+    } else {
+        uint32_t u[VEC];
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) u[c] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(o[c]));
+        if constexpr (VEC == 2) {
+            *reinterpret_cast<uint32_t*>(dst) = u[0] | (u[1] << 16);
+        } else {
+            static_assert(VEC == 4, "two or four columns per lane");
+            *reinterpret_cast<uint2*>(dst) = make_uint2(u[0] | (u[1] << 16), u[2] | (u[3] << 16));
+        }
+    }
+}
+
+// One chunk's raw inputs of a wave: S steps of VEC columns and the steps'
+// valid bytes, loaded unconditionally at clamped positions so that no branch
+// waits on them; wide_gate turns them into (a, b) pairs when they are used.
+template <int S, int VEC>
+struct WideRaw {
+    typename FloatVec<VEC>::type va[S], vb[S];
+    uint8_t keep[S];
+};
+
+template <int S, int VEC, bool GATES>
+__device__ __forceinline__ void wide_fetch(const float* __restrict__ a_col, const float* __restrict__ b_col,
+                                           int64_t stride, int64_t L, int64_t t_first, int64_t bi,
+                                           const GateInputs& gates, WideRaw<S, VEC>& raw) {
+    using V = typename FloatVec<VEC>::type;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const int64_t t = t_first + i;
+        const int64_t tc = t < L ? t : L - 1;
+        raw.va[i] = *reinterpret_cast<const V*>(a_col + tc * stride);
+        raw.vb[i] = *reinterpret_cast<const V*>(b_col + tc * stride);
+        if constexpr (GATES) raw.keep[i] = gates.valid == nullptr ? 1 : gates.valid[bi * L + tc];
+    }
+}
+
+// (a, b) of the fetched steps: the gates first when GATES, then the identity
+// (1, 0) outside the sequence or the columns.
+template <int S, int VEC, bool GATES>
+__device__ __forceinline__ void wide_gate(const WideRaw<S, VEC>& raw, int64_t L, int64_t t_first, bool col_ok,
+                                          const float (&gbr)[VEC], const float (&gbc)[VEC], float (&ra)[S][VEC],
+                                          float (&rb)[S][VEC]) {
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const bool ok = col_ok && t_first + i < L;
+        FloatVec<VEC>::split(raw.va[i], ra[i]);
+        FloatVec<VEC>::split(raw.vb[i], rb[i]);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+            if constexpr (GATES) gate_pair(ra[i][c], rb[i][c], gbr[c], gbc[c], raw.keep[i] != 0, ra[i][c], rb[i][c]);
+            ra[i][c] = ok ? ra[i][c] : 1.0f;
+            rb[i][c] = ok ? rb[i][c] : 0.0f;
+        }
+    }
+}
+
+template <int VEC, bool GATES>
+__device__ __forceinline__ void gate_biases(const GateInputs& gates, int64_t fc, float (&gbr)[VEC],
+                                            float (&gbc)[VEC]) {
+    using V = typename FloatVec<VEC>::type;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) gbr[c] = gbc[c] = 0.0f;
+    if constexpr (GATES) {
+        if (gates.retention_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.retention_bias + fc), gbr);
+        if (gates.candidate_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.candidate_bias + fc), gbc);
+    }
+}
+
+// Two-phase scan, phase one: the transfer (P, Q) = (prod a, scan from 0) of
+// every S-step segment j (positions j S .. j S + S - 1) of every column, by the
+// operations of the segment pass of scan_forward_wide_kernel in their order,
+// into tp / tq [B, segments, F]. Wave w of workgroup (x, y) takes segment
+// 8 y + w of batch row x / col_tiles.
+template <int S, int VEC, bool GATES>
+__global__ __launch_bounds__(kWave * 8) void scan_segment_transfer_kernel(
+    const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ tp, float* __restrict__ tq,
+    int64_t L, int64_t F, int64_t col_tiles, int64_t stride, int64_t segments, GateInputs gates) {
+    using V = typename FloatVec<VEC>::type;
+    const int lane = lane_id();
+    const int64_t j = static_cast<int64_t>(blockIdx.y) * 8 + static_cast<int>(threadIdx.x) / kWave;
+    if (j >= segments) return;
+    const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
+    const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane) * VEC;
+    const bool col_ok = f < F;
+    const int64_t fc = col_ok ? f : 0;
+    float gbr[VEC], gbc[VEC];
+    gate_biases<VEC, GATES>(gates, fc, gbr, gbc);
+    WideRaw<S, VEC> raw;
+    wide_fetch<S, VEC, GATES>(a + bi * L * stride + fc, b + bi * L * stride + fc, stride, L, j * S, bi, gates, raw);
+    float ra[S][VEC], rb[S][VEC];
+    wide_gate<S, VEC, GATES>(raw, L, j * S, col_ok, gbr, gbc, ra, rb);
+    float po[VEC], qo[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+        float p = 1.0f, q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            q = ra[i][c] * q + rb[i][c];
+            p = p * ra[i][c];
+        }
+        po[c] = p;
+        qo[c] = q;
+    }
+    if (col_ok) {
+        const int64_t o = (bi * segments + j) * F + f;
+        *reinterpret_cast<V*>(tp + o) = FloatVec<VEC>::join(po);
+        *reinterpret_cast<V*>(tq + o) = FloatVec<VEC>::join(qo);
+    }
+}
+
+// Two-phase scan, between the phases: the carried state at the start of every
+// chunk of `spc` segments, c <- P_j c + Q_j over the segments in order from
+// h0, into carries [B, chunks, F] (chunk 0's is h0 itself and is not written).
+// One workgroup per 64 columns of a batch row: in each round of 256 segments,
+// wave w first loads the transfers of segments 32 w .. 32 w + 31 (all loads in
+// flight together), then the waves fold their segments one after the other,
+// handing the carry on through LDS.
+constexpr int kCarrySegs = 32;
+__global__ __launch_bounds__(kWave * 8) void scan_chunk_carry_kernel(
+    const float* __restrict__ tp, const float* __restrict__ tq, const float* __restrict__ h0,
+    float* __restrict__ carries, int64_t F, int64_t col_tiles, int64_t segments, int64_t spc, int64_t chunks) {
+    __shared__ float hand[kWave];
+    const int lane = lane_id();
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
+    const int64_t f = (static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane;
+    const bool col_ok = f < F;
+    const int64_t fc = col_ok ? f : 0;
+    const float* tp_col = tp + bi * segments * F + fc;
+    const float* tq_col = tq + bi * segments * F + fc;
+    float carry = h0[bi * F + fc];
+    for (int64_t r0 = 0; r0 < segments; r0 += 8 * kCarrySegs) {
+        const int64_t j0 = r0 + static_cast<int64_t>(wave) * kCarrySegs;
+        float p[kCarrySegs], q[kCarrySegs];
+#pragma unroll
+        for (int i = 0; i < kCarrySegs; ++i) {
+            const int64_t j = j0 + i < segments ? j0 + i : segments - 1;
+            p[i] = tp_col[j * F];
+            q[i] = tq_col[j * F];
+        }
+        for (int w = 0; w < 8; ++w) {
+            if (wave == w) {
+                if (r0 > 0 || w > 0) carry = hand[lane];
+                // the next chunk start at or after j0 + 1 (chunk starts are multiples of spc)
+                int64_t next = (j0 / spc + 1) * spc;
+                int64_t chunk = next / spc;
+#pragma unroll
+                for (int i = 0; i < kCarrySegs; ++i) {
+                    const int64_t j = j0 + i;
+                    if (j < segments) {
+                        carry = p[i] * carry + q[i];
+                        if (j + 1 == next) {
+                            if (chunk < chunks && col_ok) carries[(bi * chunks + chunk) * F + f] = carry;
+                            next += spc;
+                            ++chunk;
+                        }
+                    }
+                }
+                hand[lane] = carry;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// The scan proper. Without chunk carries one workgroup walks its columns
+// through the whole sequence. With them (phase two of the two-phase scan)
+// workgroup (x, y) walks positions [y span, min(L, (y + 1) span)), span a
+// multiple of NSEG * S, from chunk y's carry (h0 for y = 0): that carry is the
+// state the one-workgroup walk carries into position y span, composed by the
+// same operations in the same order, so both give the same bits.
+//
+// LPC > 1 splits each wave into LPC groups of 64 / LPC lanes: a workgroup then
+// owns 64 / LPC column strips and NSEG * LPC segments per chunk (twice the
+// workgroups for a batch of few rows at LPC = 2). The composition order, and
+// so every result bit, is the same for any LPC and VEC.
+template <int S, int NSEG, int VEC, bool GATES = false, int LPC = 1>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
     int64_t L, int64_t F, int64_t col_tiles, int64_t stride,
-    GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr}) {
+    GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr},
+    const float* __restrict__ chunk_carry = nullptr, int64_t chunks = 0, int64_t span = 0) {
     using V = typename FloatVec<VEC>::type;
-    constexpr int CH = S * NSEG;
-    __shared__ float seg_p[NSEG][VEC][kWave];
-    __shared__ float seg_b[NSEG][VEC][kWave];
+    constexpr int TW = kWave / LPC;    // lanes (column strips) per group
+    constexpr int NS = NSEG * LPC;     // segments per chunk
+    constexpr int CH = S * NS;
+    __shared__ float seg_p[NS][VEC][TW];
+    __shared__ float seg_b[NS][VEC][TW];
 
-    const int lane = lane_id();
-    const int seg = static_cast<int>(threadIdx.x) / kWave;
+    const int lane = lane_id() % TW;
+    const int seg = static_cast<int>(threadIdx.x) / kWave * LPC + lane_id() / TW;
     const int64_t bi = static_cast<int64_t>(blockIdx.x) / col_tiles;
-    const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * kWave + lane) * VEC;
+    const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * TW + lane) * VEC;
     const bool col_ok = f < F;
     const int64_t fc = col_ok ? f : 0;
     const float* a_col = a + bi * L * stride + fc;
     const float* b_col = b + bi * L * stride + fc;
     float* h_col = h + bi * L * F + fc;
+    const int64_t t_begin = chunk_carry != nullptr ? static_cast<int64_t>(blockIdx.y) * span : 0;
+    const int64_t t_end = chunk_carry != nullptr ? (t_begin + span < L ? t_begin + span : L) : L;
 
-    float gbr[VEC] = {}, gbc[VEC] = {};
-    if constexpr (GATES) {
-        if (gates.retention_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.retention_bias + fc), gbr);
-        if (gates.candidate_bias) FloatVec<VEC>::split(*reinterpret_cast<const V*>(gates.candidate_bias + fc), gbc);
-    }
+    float gbr[VEC], gbc[VEC];
+    gate_biases<VEC, GATES>(gates, fc, gbr, gbc);
     float carry[VEC];
     {
         const V c0 = *reinterpret_cast<const V*>(h0 + bi * F + fc);
@@ -208,38 +392,15 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
 #pragma unroll
         for (int c = 0; c < VEC; ++c) carry[c] = col_ok ? carry[c] : 0.0f;
     }
+    if (chunk_carry != nullptr && blockIdx.y > 0) {
+        const V cy = *reinterpret_cast<const V*>(chunk_carry + (bi * chunks + blockIdx.y) * F + fc);
+        FloatVec<VEC>::split(cy, carry);
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) carry[c] = col_ok ? carry[c] : 0.0f;
+    }
 
-    auto load = [&](int64_t t_first, float (&ra)[S][VEC], float (&rb)[S][VEC]) {
-        V va[S], vb[S];
-#pragma unroll
-        for (int i = 0; i < S; ++i) {  // unconditional loads at clamped positions
-            const int64_t t = t_first + i;
-            const int64_t tc = t < L ? t : L - 1;
-            va[i] = *reinterpret_cast<const V*>(a_col + tc * stride);
-            vb[i] = *reinterpret_cast<const V*>(b_col + tc * stride);
-        }
-        bool keep[S];
-        if constexpr (GATES) {
-#pragma unroll
-            for (int i = 0; i < S; ++i) {
-                const int64_t t = t_first + i;
-                keep[i] = gates.valid == nullptr || gates.valid[bi * L + (t < L ? t : L - 1)] != 0;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < S; ++i) {
-            const bool ok = col_ok && t_first + i < L;
-            FloatVec<VEC>::split(va[i], ra[i]);
-            FloatVec<VEC>::split(vb[i], rb[i]);
-#pragma unroll
-            for (int c = 0; c < VEC; ++c) {
-                if constexpr (GATES) {
-                    if (t_first + i < L) gate_pair(ra[i][c], rb[i][c], gbr[c], gbc[c], keep[i], ra[i][c], rb[i][c]);
-                }
-                ra[i][c] = ok ? ra[i][c] : 1.0f;
-                rb[i][c] = ok ? rb[i][c] : 0.0f;
-            }
-        }
+    auto fetch = [&](int64_t t_first, WideRaw<S, VEC>& raw) {
+        wide_fetch<S, VEC, GATES>(a_col, b_col, stride, L, t_first, bi, gates, raw);
     };
 
     auto process = [&](float (&ra)[S][VEC], float (&rb)[S][VEC], int64_t t0) {
@@ -263,7 +424,7 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
         for (int c = 0; c < VEC; ++c) {
             float cc = carry[c], ci = carry[c];
 #pragma unroll
-            for (int j = 0; j < NSEG; ++j) {
+            for (int j = 0; j < NS; ++j) {
                 if (j == seg) ci = cc;
                 cc = seg_p[j][c][lane] * cc + seg_b[j][c][lane];
             }
@@ -277,14 +438,10 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
                 float o[VEC];
 #pragma unroll
                 for (int c = 0; c < VEC; ++c) o[c] = ra[i][c] * c_in[c] + rb[i][c];
-                if (t < L) {
+                if (t < t_end) {
                     *reinterpret_cast<V*>(h_col + t * F) = FloatVec<VEC>::join(o);
                     if constexpr (GATES) {
-                        if (gates.h16 != nullptr) {
-#pragma unroll
-                            for (int c = 0; c < VEC; ++c)
-                                gates.h16[(bi * L + t) * F + f + c] = static_cast<__bf16>(o[c]);
-                        }
+                        if (gates.h16 != nullptr) store_bf16<VEC>(gates.h16 + (bi * L + t) * F + f, o);
                     }
                 }
             }
@@ -292,15 +449,24 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
         __syncthreads();
     };
 
-    float xa[S][VEC], xb[S][VEC], ya[S][VEC], yb[S][VEC];
+    // A ring of NB chunk buffers: the loads of the next NB - 1 chunks are in
+    // flight while one is scanned (buffer indices are compile-time constants
+    // of the unrolled ring, so the buffers stay in registers).
+    constexpr int NB = VEC == 1 ? KOEMI_SCAN_BUFFERS : 2;
+    WideRaw<S, VEC> raw[NB];
     const int64_t seg_off = static_cast<int64_t>(seg) * S;
-    load(seg_off, xa, xb);
-    for (int64_t t0 = 0; t0 < L; t0 += 2 * CH) {
-        load(t0 + CH + seg_off, ya, yb);
-        process(xa, xb, t0);
-        if (t0 + CH >= L) break;
-        load(t0 + 2 * CH + seg_off, xa, xb);
-        process(ya, yb, t0 + CH);
+#pragma unroll
+    for (int k = 0; k + 1 < NB; ++k) fetch(t_begin + k * CH + seg_off, raw[k]);
+    for (int64_t t0 = t_begin; t0 < t_end; t0 += NB * CH) {
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const int64_t tc = t0 + k * CH;
+            if (tc >= t_end) break;
+            fetch(tc + (NB - 1) * CH + seg_off, raw[(k + NB - 1) % NB]);
+            float ra[S][VEC], rb[S][VEC];
+            wide_gate<S, VEC, GATES>(raw[k], L, tc + seg_off, col_ok, gbr, gbc, ra, rb);
+            process(ra, rb, tc);
+        }
     }
 }
 
@@ -468,14 +634,89 @@ __global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict
     if (gates.h16 != nullptr) gates.h16[i] = static_cast<__bf16>(hv);
 }
 
+// Two-phase split of an S-step segmented walk over L positions into chunks of
+// `span` positions (a multiple of NSEG * S): enough chunks that about
+// kTwoPhaseBlocks workgroups run (none when the column tiles alone fill that
+// many, or the sequence is a single chunk).
+constexpr int64_t kTwoPhaseBlocks = 1024;
+struct TwoPhase {
+    int64_t span = 0, chunks = 0, segments = 0;
+};
+inline TwoPhase two_phase_split(int64_t col_blocks, int64_t L) {
+    constexpr int64_t CH = static_cast<int64_t>(kScanSteps) * kScanSegments;
+    TwoPhase tp;
+    const int64_t steps = (L + CH - 1) / CH;
+    int64_t want = (kTwoPhaseBlocks + col_blocks - 1) / col_blocks;
+    if (want > steps) want = steps;
+    if (want < 2) return tp;
+    tp.span = (steps + want - 1) / want * CH;
+    tp.chunks = (L + tp.span - 1) / tp.span;
+    tp.segments = (L + kScanSteps - 1) / kScanSteps;
+    if (tp.chunks < 2 || tp.chunks > 65535 || (tp.segments + 7) / 8 > 65535) tp.chunks = 0;
+    return tp;
+}
+
+// Workspace of the two-phase scan: the segment transfers P and Q, then the
+// chunk carries (at most one chunk per NSEG * S positions).
+size_t gated_scan_workspace(int64_t B, int64_t L, int64_t F) {
+    constexpr int64_t CH = static_cast<int64_t>(kScanSteps) * kScanSegments;
+    const size_t segments = static_cast<size_t>((L + kScanSteps - 1) / kScanSteps);
+    const size_t chunks = static_cast<size_t>((L + CH - 1) / CH);
+    return (2 * segments + chunks) * static_cast<size_t>(B) * static_cast<size_t>(F) * sizeof(float);
+}
+
+#ifndef KOEMI_SCAN_TWO_PHASE_VEC
+#define KOEMI_SCAN_TWO_PHASE_VEC 2
+#endif
+#ifndef KOEMI_SCAN_LPC_MAX
+#define KOEMI_SCAN_LPC_MAX 2
+#endif
+#ifndef KOEMI_SCAN_TWO_PHASE_BELOW
+#define KOEMI_SCAN_TWO_PHASE_BELOW 128
+#endif
+// The one-pass scan runs when it has at least this many workgroups.
+constexpr int64_t kTwoPhaseBelow = KOEMI_SCAN_TWO_PHASE_BELOW;
+
+// The three launches of the two-phase gated scan, VEC columns per lane in the
+// two passes over the pre-activations (the carry pass works column by column
+// on the [B, segments, F] transfers, whatever VEC is).
+template <int VEC>
+int run_two_phase(const float* zr, const float* zc, int64_t stride, const GateInputs& gates, const float* h0, float* h,
+                  int64_t B, int64_t L, int64_t F, int64_t tiles, const TwoPhase& split, float* workspace,
+                  hipStream_t stream) {
+    float* tp = workspace;
+    float* tq = tp + B * split.segments * F;
+    float* carries = tq + B * split.segments * F;
+    hipLaunchKernelGGL((scan_segment_transfer_kernel<kScanSteps, VEC, true>),
+                       dim3(static_cast<unsigned>(B * tiles), static_cast<unsigned>((split.segments + 7) / 8)),
+                       dim3(kWave * 8), 0, stream, zr, zc, tp, tq, L, F, tiles, stride, split.segments, gates);
+    int st = check_launch("gated scan (segment transfers)");
+    if (st != KOEMI_OK) return st;
+    const int64_t carry_tiles = (F + kWave - 1) / kWave;
+    hipLaunchKernelGGL(scan_chunk_carry_kernel, dim3(static_cast<unsigned>(B * carry_tiles)), dim3(kWave * 8), 0,
+                       stream, tp, tq, h0, carries, F, carry_tiles, split.segments, split.span / kScanSteps,
+                       split.chunks);
+    st = check_launch("gated scan (chunk carries)");
+    if (st != KOEMI_OK) return st;
+    hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
+                       dim3(static_cast<unsigned>(B * tiles), static_cast<unsigned>(split.chunks)),
+                       dim3(kWave * kScanSegments), 0, stream, zr, zc, h0, h, L, F, tiles, stride, gates, carries,
+                       split.chunks, split.span);
+    return check_launch("gated scan (chunks)");
+}
+
 // The fused gates + scan over fp32 pre-activation products zr, zc (row r of
 // the B x L rows at r * stride): one position per column for L == 1,
 // otherwise the wide scan with KOEMI_SCAN_VEC columns per lane where the rows
-// are aligned to it and that still fills the chip, one column per lane
-// otherwise. The caller has checked that B * ceil(F / 64) fits the grid.
+// are aligned to it and that still fills the chip; one column per lane
+// otherwise, split into the two-phase scan (segment transfers into the
+// workspace, then chunks of the sequence walked from their carried state) when
+// a workspace of gated_scan_workspace bytes is given and the column tiles
+// alone leave the chip short of workgroups. The caller has checked that
+// B * ceil(F / 64) fits the grid.
 int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
                       const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
-                      int64_t B, int64_t L, int64_t F, hipStream_t stream) {
+                      int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace, size_t workspace_bytes) {
     constexpr int VEC = KOEMI_SCAN_VEC;
     const GateInputs gates{retention_bias, candidate_bias, valid, static_cast<__bf16*>(h16)};
     if (L == 1) {
@@ -486,16 +727,49 @@ int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const fl
     auto aligned = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % (4 * VEC) == 0; };
     const int64_t wide_tiles = (F / VEC + kWave - 1) / kWave;
     if (F % VEC == 0 && stride % VEC == 0 && aligned(zr) && aligned(zc) && aligned(h) && aligned(h0) &&
-        aligned(retention_bias) && aligned(candidate_bias) && B * wide_tiles >= 256) {
+        aligned(retention_bias) && aligned(candidate_bias) && reinterpret_cast<uintptr_t>(h16) % (2 * VEC) == 0 &&
+        B * wide_tiles >= 256) {
         hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
                            dim3(static_cast<unsigned>(B * wide_tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc,
                            h0, h, L, F, wide_tiles, stride, gates);
         return check_launch("gated scan");
     }
-    const int64_t tiles = (F + kWave - 1) / kWave;
-    hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true>),
-                       dim3(static_cast<unsigned>(B * tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc, h0, h,
-                       L, F, tiles, stride, gates);
+    // One column per lane: lane groups of 64 / lpc lanes, lpc = 2 or 4 when
+    // the batch's 64-column strips leave CUs idle.
+    int lpc = 1;
+    while (lpc < KOEMI_SCAN_LPC_MAX && B * ((F + kWave / lpc - 1) / (kWave / lpc)) < 256 && F > kWave / lpc / 2)
+        lpc *= 2;
+    const int64_t tiles = (F + kWave / lpc - 1) / (kWave / lpc);
+    if (workspace != nullptr && workspace_bytes >= gated_scan_workspace(B, L, F) && B * tiles < kTwoPhaseBelow) {
+        constexpr int TV = KOEMI_SCAN_TWO_PHASE_VEC;
+        const bool tv_ok = F % TV == 0 && stride % TV == 0 && reinterpret_cast<uintptr_t>(workspace) % (4 * TV) == 0 &&
+                           reinterpret_cast<uintptr_t>(h16) % (2 * TV) == 0 &&
+                           [&] {
+                               for (const void* p : {static_cast<const void*>(zr), static_cast<const void*>(zc),
+                                                     static_cast<const void*>(h), static_cast<const void*>(h0),
+                                                     static_cast<const void*>(retention_bias),
+                                                     static_cast<const void*>(candidate_bias)})
+                                   if (p != nullptr && reinterpret_cast<uintptr_t>(p) % (4 * TV) != 0) return false;
+                               return true;
+                           }();
+        const int64_t tiles1 = (F + kWave - 1) / kWave;
+        const int64_t tv_tiles = (F / TV + kWave - 1) / kWave;
+        const TwoPhase split = two_phase_split(B * (tv_ok ? tv_tiles : tiles1), L);
+        if (split.chunks >= 2) {
+            if (tv_ok)
+                return run_two_phase<TV>(zr, zc, stride, gates, h0, h, B, L, F, tv_tiles, split,
+                                         static_cast<float*>(workspace), stream);
+            return run_two_phase<1>(zr, zc, stride, gates, h0, h, B, L, F, tiles1, split,
+                                    static_cast<float*>(workspace), stream);
+        }
+    }
+    auto one_pass = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(B * tiles)), dim3(kWave * kScanSegments), 0, stream, zr,
+                           zc, h0, h, L, F, tiles, stride, gates, nullptr, 0, 0);
+    };
+    if (lpc == 4) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 4>);
+    else if (lpc == 2) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 2>);
+    else one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 1>);
     return check_launch("gated scan");
 }
 
@@ -556,10 +830,16 @@ extern "C" int koemi_affine_scan_backward(const void* retention, const void* ini
 #undef KOEMI_SCAN_BWD
 }
 
+extern "C" size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width) {
+    if (batch <= 0 || length <= 1 || width <= 0) return 0;
+    return gated_scan_workspace(batch, length, width);
+}
+
 extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                                 int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
                                 const uint8_t* valid, const float* initial, float* states, void* states_bf16,
-                                int64_t batch, int64_t length, int64_t width, koemi_stream_t stream) {
+                                int64_t batch, int64_t length, int64_t width, void* workspace, size_t workspace_bytes,
+                                koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1)
         return fail(KOEMI_ERR_INVALID, "gated scan needs non-negative batch and length and a positive width");
     if (retention_offset < 0 || candidate_offset < 0 || retention_offset + width > row_stride ||
@@ -569,7 +849,10 @@ extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride,
     if (!preactivations || !initial || !states) return fail(KOEMI_ERR_INVALID, "gated scan received a null pointer");
     if (batch * ((width + kWave - 1) / kWave) > 0x7fffffffLL || batch * width > 0x7fffffffLL * 256LL)
         return fail(KOEMI_ERR_UNSUPPORTED, "gated scan grid too large");
+    if (workspace != nullptr && workspace_bytes < gated_scan_workspace(batch, length, width))
+        return fail(KOEMI_ERR_INVALID, "gated scan workspace too small: need %zu bytes",
+                    gated_scan_workspace(batch, length, width));
     return launch_gated_scan(preactivations + retention_offset, preactivations + candidate_offset, row_stride,
                              retention_bias, candidate_bias, valid, initial, states, states_bf16, batch, length,
-                             width, as_stream(stream));
+                             width, as_stream(stream), workspace, workspace_bytes);
 }

@@ -29,12 +29,11 @@ extern std::mutex g_blas_mutex;
 // The fused gates + scan kernel (affine_scan.hip).
 int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
                       const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
-                      int64_t B, int64_t L, int64_t F, hipStream_t stream);
+                      int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace,
+                      size_t workspace_bytes);
 
 namespace {
 
-constexpr float kMinRetention = 0.00390625f;             // 2^-8
-constexpr float kRetentionSpan = 1.0f - 0.0078125f;       // (1 - 2^-8) - 2^-8 = 1 - 2^-7
 
 template <typename T>
 __global__ __launch_bounds__(256) void gates_epilogue_kernel(
@@ -51,9 +50,8 @@ __global__ __launch_bounds__(256) void gates_epilogue_kernel(
     const bool keep = valid == nullptr || valid[row] != 0;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const float retention = 1.0f / (1.0f + expf(-(r[c] + to_f32(br[c0 + c]))));
-        const float a = kMinRetention + kRetentionSpan * retention;
-        const float b = (1.0f - a) * tanhf(z[c] + to_f32(bc[c0 + c]));
+        const float a = kGateMinRetention + kGateRetentionSpan * gate_sigmoid(r[c] + to_f32(br[c0 + c]));
+        const float b = (1.0f - a) * gate_tanh(z[c] + to_f32(bc[c0 + c]));
         a_out[row * D + c0 + c] = from_f32<T>(keep ? a : 1.0f);
         b_out[row * D + c0 + c] = from_f32<T>(keep ? b : 0.0f);
     }
@@ -179,5 +177,5 @@ extern "C" int koemi_recurrent_scan(const float* input, const float* retention_w
     int st = gate_products(input, retention_weight, candidate_weight, zr, zc, rows, width, KOEMI_F32, s);
     if (st != KOEMI_OK) return st;
     return launch_gated_scan(zr, zc, width, retention_bias, candidate_bias, valid, initial, states, nullptr, batch,
-                             length, width, s);
+                             length, width, s, nullptr, 0);
 }

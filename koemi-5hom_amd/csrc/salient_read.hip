@@ -578,6 +578,201 @@ extern "C" size_t koemi_salient_read_workspace_bytes(int64_t batch, int64_t carr
 
 namespace {
 
+// Fused window read (fp32): one workgroup per (batch row, 32 queries) does
+// the whole masked read of its queries in one launch. The candidate slots of
+// the block (salient: every slot before its last query's own entry; local:
+// the `window` entries before each query's own, a band of at most window + 31
+// slots) are compacted by their flags (carried valid bytes, then the window's
+// admission or valid bytes) into an LDS list, so slots that no query can use
+// cost nothing (a row with nothing eligible only writes zeros). Then:
+//   scores: 32 queries x the listed slots on fp32 MFMA (v_mfma_f32_32x32x2f32),
+//     operands loaded straight from memory in the MFMA layout (a lane's query
+//     and key values at the same width column, the step's two K entries at two
+//     columns 16 apart), the four waves taking 64-column chunks in turn and
+//     leaving their partial sums in LDS;
+//   softmax: the partials added in wave order and scaled by 1/sqrt(D), masked
+//     per query (salient: carried slots and earlier window entries; local:
+//     the window before the query's own entry), max, exp, sum, weights in LDS;
+//   weighted sum: out = weights x values of the listed slots on fp32 MFMA, each
+//     wave taking 32-column tiles in turn, eight slot steps' value loads
+//     issued together.
+// Needs width % 4 == 0, 16-byte aligned rows and at most kWinMaxSlots
+// candidate slots per block; other shapes take the kernels above.
+constexpr int kWinQ = 32;
+constexpr int kWinMaxSlots = 152;  // LDS: 4 x 32 x 153 fp32 partial scores (78 KiB: two workgroups per CU)
+
+__device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <bool LOCAL>
+__global__ __launch_bounds__(256) void window_read_kernel(
+    const float* __restrict__ ck, const float* __restrict__ cv, const uint8_t* __restrict__ cvalid,
+    const float* __restrict__ k, const float* __restrict__ v, const uint8_t* __restrict__ flags,
+    const float* __restrict__ q, float* __restrict__ out, int S, int L, int64_t D, int window, float scale) {
+    __shared__ int list[kWinMaxSlots];
+    __shared__ int wave_cnt[4];
+    __shared__ float sc[4][kWinQ][kWinMaxSlots + 1];
+    const int64_t row = blockIdx.x;
+    const int t0 = static_cast<int>(blockIdx.y) * kWinQ;
+    const int nq = min(kWinQ, L - t0);
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int r = lane & 31, h = lane >> 5;
+    // candidate slots [c_lo, c_hi): before the last query's own entry S + t0 + nq - 1
+    const int c_hi = S + t0 + nq - 1;
+    const int c_lo = LOCAL ? max(0, S + t0 - window) : 0;
+    const int c = c_lo + tid;
+    bool f = false;
+    if (c < c_hi) f = (c < S ? cvalid[row * S + c] : flags[row * L + (c - S)]) != 0;
+    const uint64_t bal = __ballot(f);
+    const int before = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) wave_cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wave_cnt[w];
+    const int n = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    if (f) list[base + before] = c;
+    __syncthreads();
+    float* orow0 = out + (row * L + t0) * D;
+    if (n == 0) {  // nothing eligible for any query of the block: zero rows
+        for (int64_t i = tid; i < nq * D / 4; i += 256) reinterpret_cast<float4*>(orow0)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const int nst = (n + 31) / 32;
+    auto slot_row = [&](int s, const float* carried, const float* window_rows) -> const float* {
+        return s < S ? carried + (row * S + s) * D : window_rows + (row * L + (s - S)) * D;
+    };
+
+    // scores
+    {
+        const float* qrow = q + (row * L + t0 + min(r, nq - 1)) * D;
+        f32x16 acc[5];
+#pragma unroll
+        for (int st = 0; st < 5; ++st)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[st][e] = 0.0f;
+        const int64_t chunks = (D + 63) / 64;
+        for (int64_t ch = wave; ch < chunks; ch += 4) {
+            float4 qa[2][4];
+#pragma unroll
+            for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
+                    qa[blk][i] = col < D ? *reinterpret_cast<const float4*>(qrow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+            for (int st = 0; st < 5; ++st) {
+                if (st >= nst) break;
+                const float* krow = slot_row(list[min(st * 32 + r, n - 1)], ck, k);
+                float4 kb[2][4];
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
+                        kb[blk][i] = col < D ? *reinterpret_cast<const float4*>(krow + col)
+                                             : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+#pragma unroll
+                for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        acc[st] = mfma_f32_32x32x2(qa[blk][i].x, kb[blk][i].x, acc[st]);
+                        acc[st] = mfma_f32_32x32x2(qa[blk][i].y, kb[blk][i].y, acc[st]);
+                        acc[st] = mfma_f32_32x32x2(qa[blk][i].z, kb[blk][i].z, acc[st]);
+                        acc[st] = mfma_f32_32x32x2(qa[blk][i].w, kb[blk][i].w, acc[st]);
+                    }
+            }
+        }
+        // accumulator entry e of lane l: query 8 (e / 4) + 4 h + e % 4, slot st * 32 + l % 32
+#pragma unroll
+        for (int st = 0; st < 5; ++st) {
+            if (st >= nst) break;
+            if (st * 32 + r < n) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) sc[wave][8 * (e / 4) + 4 * h + (e % 4)][st * 32 + r] = acc[st][e];
+            }
+        }
+    }
+    __syncthreads();
+
+    // softmax: wave w takes queries 8 w .. 8 w + 7; weights overwrite sc[0]
+    const int npad = nst * 32;
+    for (int qq = 0; qq < 8; ++qq) {
+        const int m = wave * 8 + qq;
+        const int t = t0 + m;
+        float x[3];
+        bool ok[3];
+        float mx = -INFINITY;
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int idx = j * kWave + lane;
+            x[j] = 0.0f;
+            ok[j] = false;
+            if (idx < n) {
+                const int sl = list[idx];
+                x[j] = (((sc[0][m][idx] + sc[1][m][idx]) + sc[2][m][idx]) + sc[3][m][idx]) * scale;
+                ok[j] = m < nq && sl < S + t && (!LOCAL || sl >= S + t - window);
+            }
+            if (ok[j]) {
+                any = true;
+                mx = fmaxf(mx, x[j]);
+            }
+        }
+        mx = wave_max_xor(mx);
+        any = __any(any);
+        if (!any) mx = 0.0f;
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            x[j] = ok[j] ? expf(x[j] - mx) : 0.0f;
+            sum += x[j];
+        }
+        sum = wave_sum_xor(sum);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int idx = j * kWave + lane;
+            if (idx < n) sc[0][m][idx] = sum > 0.0f ? x[j] / sum : x[j];
+        }
+    }
+    __syncthreads();
+
+    // weighted sum of the listed slots' values
+    const int64_t col_tiles = (D + 31) / 32;
+    for (int64_t ct = wave; ct < col_tiles; ct += 4) {
+        const int64_t col = ct * 32 + r;
+        const int64_t colc = min(col, D - 1);
+        f32x16 o;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = 0.0f;
+        for (int i0 = 0; i0 < npad; i0 += 16) {  // eight MFMA steps of two slots each
+            float a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int li = i0 + 2 * u + h;
+                a[u] = li < n ? sc[0][r][li] : 0.0f;
+                b[u] = li < n ? slot_row(list[li], cv, v)[colc] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) o = mfma_f32_32x32x2(a[u], b[u], o);
+        }
+        if (col < D) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = 8 * (e / 4) + 4 * h + (e % 4);
+                if (m < nq) orow0[m * D + col] = o[e];
+            }
+        }
+    }
+}
+
+inline bool window_read_fits(int64_t carried, int64_t length, int64_t window) {
+    if (carried > kWinMaxSlots) return false;
+    return window > 0 ? window + kWinQ - 1 <= kWinMaxSlots : carried + length - 1 <= kWinMaxSlots;
+}
+
 // The masked read shared by the salient read (window 0: no lower bound) and
 // the local memory's sliding-window read (window > 0).
 int memory_read(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid, const void* keys,
@@ -621,6 +816,24 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
         else if (dtype == KOEMI_F16) step(f16{});
         else step(bf16{});
         return check_launch("koemi_salient_read(one position)");
+    }
+    auto aligned16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (dtype == KOEMI_F32 && width % 4 == 0 && window_read_fits(carried, length, window) && batch <= 0x7fffffffLL &&
+        (length + kWinQ - 1) / kWinQ <= 65535 &&
+        aligned16(carried_keys) && aligned16(carried_values) && aligned16(keys) && aligned16(values) &&
+        aligned16(queries) && aligned16(out)) {
+        const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+        const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((length + kWinQ - 1) / kWinQ));
+        auto launch = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, as_stream(stream), static_cast<const float*>(carried_keys),
+                               static_cast<const float*>(carried_values), carried_valid,
+                               static_cast<const float*>(keys), static_cast<const float*>(values), admission,
+                               static_cast<const float*>(queries), static_cast<float*>(out), static_cast<int>(carried),
+                               static_cast<int>(length), width, static_cast<int>(window), inv_sqrt_d);
+        };
+        if (window > 0) launch(window_read_kernel<true>);
+        else launch(window_read_kernel<false>);
+        return check_launch(window > 0 ? "koemi_local_read" : "koemi_salient_read");
     }
     char* base = static_cast<char*>(workspace);
     float* score = reinterpret_cast<float*>(base + ws.score_off);

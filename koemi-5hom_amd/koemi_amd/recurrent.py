@@ -172,7 +172,7 @@ def recurrent_scan(
 
 def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
                retention_offset: int = 0, candidate_offset: int | None = None,
-               with_bf16: bool = False) -> Tensor | tuple[Tensor, Tensor]:
+               with_bf16: bool = False, two_phase: bool = True) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
     ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
@@ -183,7 +183,10 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     scan of network.py:310 from ``initial`` ``[B, width]`` run in one kernel
     (``koemi_gated_scan``). Returns ``[B, L, width]`` fp32, and with
     ``with_bf16`` also its bf16 copy (written by the same kernel) for a
-    following bf16 GEMM.
+    following bf16 GEMM. With ``two_phase`` the kernel gets the workspace of
+    its two-phase form, which it takes when the batch's columns alone would
+    leave the chip short of workgroups (a few long rows); the result is the
+    same to the bit either way.
     """
 
     if candidate_offset is None:
@@ -210,11 +213,13 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     states16 = torch.empty(states.shape, device=z.device, dtype=torch.bfloat16) if with_bf16 else None
     if states.numel():
         mask = valid_mask.contiguous() if valid_mask is not None else None
+        need = _native.query("koemi_gated_scan_workspace_bytes", batch, length, width) if two_phase else 0
+        workspace = torch.empty(need, device=z.device, dtype=torch.uint8) if need else None
         _native.call(
             "koemi_gated_scan",
             _native.ptr(z), columns, retention_offset, candidate_offset, None, None,
             _native.ptr(mask) if mask is not None else None,
             _native.ptr(initial.contiguous()), _native.ptr(states), _native.ptr(states16),
-            batch, length, width, _native.stream_of(z.device),
+            batch, length, width, _native.ptr(workspace), need, _native.stream_of(z.device),
         )
     return (states, states16) if with_bf16 else states

@@ -135,6 +135,36 @@ def test_gated_scan_from_preactivations(device, b, length, d, r_off, c_off, cols
     assert torch.equal(first, h[:, :1])
 
 
+@pytest.mark.parametrize(
+    "b, length, d, r_off, c_off, cols",
+    [
+        (8, 2048, 1024, 0, 1024, 2048),  # C5 prefill: 128 column tiles, eight chunks of 256 positions
+        (3, 1000, 100, 3, 105, 210),     # ragged: the last chunk and the last column tile short
+        (1, 777, 64, 0, 64, 128),        # one column tile: a chunk of 64 positions per workgroup
+    ],
+)
+def test_two_phase_gated_scan_equals_the_one_pass_scan(device, b, length, d, r_off, c_off, cols):
+    """The two-phase scan (segment transfers, then chunks from their composed
+    carries) gives the one-pass scan's bits, fp32 states and bf16 copy, and
+    stays within 1e-4 of the oracle's float64 scan."""
+    g = torch.Generator().manual_seed(b * 7 + length)
+    z = (1.5 * torch.randn((b, length, cols), generator=g)).to(device)
+    valid = (torch.rand((b, length), generator=g) < 0.8).to(device)
+    h0 = torch.randn((b, d), generator=g).to(device)
+    kw = dict(width=d, retention_offset=r_off, candidate_offset=c_off, with_bf16=True)
+    one, one16 = recurrent.gated_scan(z, valid, h0, two_phase=False, **kw)
+    two, two16 = recurrent.gated_scan(z, valid, h0, two_phase=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two) and torch.equal(one16, two16)
+    select = lambda off: np.eye(cols)[off:off + d]
+    zc = z.double().cpu().numpy()
+    a, inc = oracle.recurrent_gates(zc, select(r_off), np.zeros(d), select(c_off), np.zeros(d), valid.cpu().numpy())
+    want = oracle.scan_sequential(a, inc, h0.double().cpu().numpy())
+    err = np.abs(two.cpu().numpy() - want).max()
+    print(f"two-phase gated scan b={b} L={length} d={d}: max_abs={err:.3e}", flush=True)
+    assert err <= 1e-4
+
+
 def test_gated_scan_rejects_bad_columns(device):
     z = torch.zeros((2, 3, 10), device=device)
     h0 = torch.zeros((2, 4), device=device)
