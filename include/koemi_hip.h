@@ -365,27 +365,35 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
  * and the decay and write logits (one column each); surprise fp32 and valid
  * bytes [batch * length]; basis fp32 [batch, width, features], normalizer
  * [batch, features]. Writes the reads [batch, length, width] and the window's
- * final basis and normalizer (fp32). features <= 32; the window length is
- * bounded by LDS ((132 + 2 features) x 4 bytes per position: at most 249
- * positions with 16 features). No workspace. */
+ * final basis and normalizer (fp32); next_basis and next_normalizer must not
+ * alias basis and normalizer. features <= 32; the window length is bounded by
+ * LDS (at most 480 positions with 16 features, 384 with 32). A window of one
+ * position (a decode step) needs no workspace; longer ones take
+ * koemi_assoc_scan_read_workspace_bytes(batch, length, width, features)
+ * bytes for the per-position weights (features, cumulative log-decays, write
+ * weights) that three launches share: prepare, state, reads. */
+size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width, int64_t features);
 int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset, int64_t feature_offset,
                           int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset,
                           const float* surprise, const uint8_t* valid, const float* basis, const float* normalizer,
                           float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
-                          int64_t width, int64_t features, koemi_stream_t stream);
+                          int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
+                          koemi_stream_t stream);
 
 /* koemi_assoc_scan_read over a whole sequence of `windows` windows of
  * `window` positions at once (forward_parallel, network.py:176-197, carrying
  * the memory state from window to window): the same layouts with length =
- * windows * window. Three launches: every window's own terms of the final
- * state from a zero carried state, a scan over the windows of
- * state' = e^{c_{L-1}} state + terms (the kernel's own update, so each
- * window's carried state equals a window-by-window run's), and the reads of
- * every window from its carried state. Writes the reads [batch, length,
- * width] and the state after the last window. window >= 2; workspace of
- * koemi_assoc_scan_read_windows_workspace_bytes(batch, windows, width,
- * features) bytes. */
-size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t width, int64_t features);
+ * windows * window. Four launches: every window's per-position weights and
+ * its own terms of the final state from a zero carried state, a scan over the
+ * windows of state' = e^{c_{L-1}} state + terms (the one-window update, so
+ * each window's carried state equals a window-by-window run's), and the reads
+ * of every window from its carried state (the one-window read kernel, so the
+ * reads equal a window-by-window run's bit for bit). Writes the reads [batch,
+ * length, width] and the state after the last window. window >= 2; workspace
+ * of koemi_assoc_scan_read_windows_workspace_bytes(batch, windows, window,
+ * width, features) bytes. */
+size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window, int64_t width,
+                                                     int64_t features);
 int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
                                   int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
                                   int64_t write_offset, const float* surprise, const uint8_t* valid,

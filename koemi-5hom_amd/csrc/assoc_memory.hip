@@ -49,21 +49,8 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf
 
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 
-// LDS floats: the influence rows of the tile (64 x (Lq + 1), Lq = L rounded up
-// to 32, the odd pitch spreading the MFMA operand reads of 32 rows over the
-// banks); cum, log-decay (then the prior log-weights), write weights and
-// final-write weights (4 Lq); features ([MAXM][L + 1]) and query features
-// ([L][MAXM + 1]), zero-padded to MAXM so the feature products run unguarded;
-// the value columns ([Lq][65]).
-inline int64_t assoc_round(int64_t L) { return (L + 31) & ~int64_t(31); }
-inline int64_t assoc_maxm(int64_t M) { return M <= 16 ? 16 : 32; }
-inline size_t assoc_lds(int64_t L, int64_t M) {
-    const int64_t Lq = assoc_round(L), X = assoc_maxm(M);
-    return (kAssocRows * (Lq + 1) + 4 * Lq + X * (L + 1) + L * (X + 1) + Lq * (kAssocCols + 1)) * sizeof(float);
-}
-
 // e^x and tanh on the hardware exp2 and reciprocal (about 1 ulp each): the
-// window kernel evaluates them per (query, slot) pair and per staged value.
+// window kernels evaluate them per (query, slot) pair and per value read.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float fast_tanh(float x) {
     return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x * 2.8853900817779268f) + 1.0f);
@@ -75,40 +62,61 @@ __device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// What one launch of assoc_read_kernel computes: the window's reads and its
-// final state (kFull); only the final state's window terms with a zero
-// carried state, sum_s e^{c_{L-1} - c_s} weight_s value_s features_s^T (and
-// for the normalizer), plus e^{c_{L-1}} per row in `out` (kDelta; launched
-// with one row tile); or only the reads (kRead).
-constexpr int kFull = 0, kDelta = 1, kRead = 2;
+inline int64_t assoc_maxm(int64_t M) { return M <= 16 ? 16 : 32; }
 
-template <int MAXM, int MODE = kFull>
-__global__ __launch_bounds__(256) void assoc_read_kernel(
-    const float* __restrict__ proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
-    int64_t decay_off, int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid,
-    const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out,
-    float* __restrict__ next_basis, float* __restrict__ next_normalizer, int L, int64_t D, int M) {
+// Per-position quantities of a window row, formed once by assoc_prep_kernel
+// and read by the delta and read kernels: the key's and the query's feature
+// softmaxes ([rows][L][MAXM], zero past M), the cumulative log-decay c_t, the
+// prior log-weight c_t - log decay_t, the write weight, the final-write weight
+// e^{c_{L-1} - c_t} weight_t, and per row e^{c_{L-1}}.
+struct AssocPrep {
+    float* kf;
+    float* qf;
+    float* cum;
+    float* prior;
+    float* wt;
+    float* fwt;
+    float* keep;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+inline size_t prep_bytes(int64_t rows, int64_t L, int64_t M) {
+    const size_t feat = align256(static_cast<size_t>(rows * L * assoc_maxm(M)) * sizeof(float));
+    const size_t pos = align256(static_cast<size_t>(rows * L) * sizeof(float));
+    return 2 * feat + 4 * pos + align256(static_cast<size_t>(rows) * sizeof(float));
+}
+inline AssocPrep prep_at(void* base, int64_t rows, int64_t L, int64_t M) {
+    char* w = static_cast<char*>(base);
+    const size_t feat = align256(static_cast<size_t>(rows * L * assoc_maxm(M)) * sizeof(float));
+    const size_t pos = align256(static_cast<size_t>(rows * L) * sizeof(float));
+    AssocPrep p;
+    p.kf = reinterpret_cast<float*>(w);
+    p.qf = reinterpret_cast<float*>(w + feat);
+    p.cum = reinterpret_cast<float*>(w + 2 * feat);
+    p.prior = reinterpret_cast<float*>(w + 2 * feat + pos);
+    p.wt = reinterpret_cast<float*>(w + 2 * feat + 2 * pos);
+    p.fwt = reinterpret_cast<float*>(w + 2 * feat + 3 * pos);
+    p.keep = reinterpret_cast<float*>(w + 2 * feat + 4 * pos);
+    return p;
+}
+
+// One workgroup per window row: the 2 L feature softmaxes (one per thread),
+// the decays and write weights with the keys', the cumulative log-decay
+// (memory.py:108; wave 0: each lane sums its run of positions, an inclusive
+// wave scan of the run sums places it), then the prior and final-write
+// weights. Dynamic LDS: 3 L floats.
+template <int MAXM>
+__global__ __launch_bounds__(256) void assoc_prep_kernel(
+    const float* __restrict__ proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
+    int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid, AssocPrep prep, int L,
+    int M) {
     extern __shared__ float sh[];
-    constexpr int QP = MAXM + 1;        // query-feature pitch
-    constexpr int VP = kAssocCols + 1;  // value pitch
-    const int Lq = (L + 31) & ~31;
-    const int IP = Lq + 1;  // influence pitch
-    const int FP = L + 1;   // feature pitch
-    float* infl = sh;                      // [64][IP]
-    float* cum = infl + kAssocRows * IP;   // [Lq]
-    float* logd = cum + Lq;                // [Lq]
-    float* wt = logd + Lq;                 // [Lq] write weights
-    float* fwt = wt + Lq;                  // [Lq] final-write weights
-    float* f_sh = fwt + Lq;                // [MAXM][FP]
-    float* q_sh = f_sh + MAXM * FP;        // [L][QP]
-    float* val = q_sh + L * QP;            // [Lq][VP]
+    float* logd = sh;       // [L]
+    float* cum = sh + L;    // [L]
+    float* wt = sh + 2 * L;  // [L]
     const int64_t b = blockIdx.x;
-    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kAssocCols;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-    const int h = lane >> 5, r32 = lane & 31;
     const float* rows0 = proj + b * L * stride;
-    // the key's and the query's feature softmax of every position (one per
-    // thread), the decay and the write weight with the key's
     for (int job = tid; job < 2 * L; job += 256) {
         const bool query = job >= L;
         const int t = query ? job - L : job;
@@ -130,12 +138,11 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
             sum += z[m];
         }
         const float inv = __builtin_amdgcn_rcpf(sum);
-        if (query) {
+        float* dst = (query ? prep.qf : prep.kf) + (b * L + t) * MAXM;
 #pragma unroll
-            for (int m = 0; m < MAXM; ++m) q_sh[t * QP + m] = z[m] * inv;  // zero past M
-        } else {
-#pragma unroll
-            for (int m = 0; m < MAXM; ++m) f_sh[m * FP + t] = z[m] * inv;
+        for (int m = 0; m < MAXM; m += 4)
+            *reinterpret_cast<float4*>(dst + m) = make_float4(z[m] * inv, z[m + 1] * inv, z[m + 2] * inv, z[m + 3] * inv);
+        if (!query) {
             const bool ok = valid[b * L + t] != 0;
             const float decay = kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]);
             const float sv = fminf(fmaxf(surprise[b * L + t], 0.0f), 1.0f);
@@ -143,26 +150,8 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
             wt[t] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
         }
     }
-    {
-        // value rows t < Lq (zero past L): wave w stages rows w, w + 4, ...,
-        // sixteen unconditional loads in flight per lane
-        const int64_t dv = c0 + lane;
-        const int64_t dc = dv < D ? dv : D - 1;
-        for (int tb = wave; tb < Lq; tb += 64) {
-            float x[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) x[j] = rows0[min(tb + 4 * j, L - 1) * stride + value_off + dc];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int t = tb + 4 * j;
-                if (t < Lq) val[t * VP + lane] = (t < L && dv < D) ? fast_tanh(x[j]) : 0.0f;
-            }
-        }
-    }
     __syncthreads();
     if (wave == 0) {
-        // cumulative log-decay (memory.py:108): lane l sums its run of positions
-        // [l R, l R + R); an inclusive wave scan of the run sums places it.
         const int R = (L + kWave - 1) / kWave;
         float acc = 0.0f;
         for (int j = 0; j < R; ++j) {
@@ -186,150 +175,217 @@ __global__ __launch_bounds__(256) void assoc_read_kernel(
     }
     __syncthreads();
     const float total = cum[L - 1];
-    float* prior = logd;  // prior_t = cum_t - log decay_t replaces the log-decays from here on
     for (int s = tid; s < L; s += 256) {
-        fwt[s] = expf(total - cum[s]) * wt[s];
-        prior[s] = cum[s] - logd[s];
+        prep.cum[b * L + s] = cum[s];
+        prep.prior[b * L + s] = cum[s] - logd[s];
+        prep.wt[b * L + s] = wt[s];
+        prep.fwt[b * L + s] = expf(total - cum[s]) * wt[s];
     }
-    __syncthreads();
+    if (tid == 0) prep.keep[b] = expf(total);
+}
 
-    if constexpr (MODE != kDelta) {
-    const int t0 = static_cast<int>(blockIdx.z) * kAssocRows;
-    const int rows = min(kAssocRows, L - t0);
-    const int s_cnt = t0 + rows;  // slots that can reach these queries (s < t <= t0 + rows - 1)
-    const int nsb = (s_cnt + 31) / 32;
-    // influence of slot s on query t (zero unless s < t): the feature products
-    // q_t . f_s of 32 x 32 blocks on MFMA (K = MAXM), then the decay and write
-    // weights; blocks (query half, slot block) go round-robin over the waves.
-    for (int blk = wave; blk < 2 * nsb; blk += 4) {
-        const int tb = blk / nsb, sb = blk - tb * nsb;
-        const int ta = min(t0 + tb * 32 + r32, L - 1);
-        const int s = sb * 32 + r32, sc = min(s, L - 1);
-        f32x16 acc = {};
+// The window's own terms of the final state of a row, from the prepared
+// weights: terms[d][m] = sum_s fwt_s tanh(v_s[d]) kf_s[m] on fp32 MFMA (A =
+// the weighted values, 32 columns of a wave's half, B = the key features,
+// K = slots, the slots split in two halves over wave pairs and added through
+// LDS), normalizer terms sum_s fwt_s kf_s[m] by a wave reduction. FINAL
+// writes the next state e^{c_{L-1}} state + terms (the fmaf the carry kernel
+// applies between windows); otherwise the terms. Grid (rows, ceil(D / 64)).
+template <int MAXM, bool FINAL>
+__global__ __launch_bounds__(256) void assoc_delta_kernel(
+    const float* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
+    const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ next_basis,
+    float* __restrict__ next_normalizer, int L, int64_t D, int M) {
+    extern __shared__ float sh[];
+    constexpr int QP = MAXM + 1;
+    float* fwt = sh;               // [L]
+    float* kf = fwt + L;           // [L][QP]
+    float* part = kf + L * QP;     // [2][16][64]
+    const int64_t b = blockIdx.x;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int h = lane >> 5, r32 = lane & 31;
+    for (int s = tid; s < L; s += 256) fwt[s] = prep.fwt[b * L + s];
+    for (int i = tid; i < L * MAXM; i += 256) kf[(i / MAXM) * QP + i % MAXM] = prep.kf[b * L * MAXM + i];
+    __syncthreads();
+    const int half = ((L + 1) / 2 + 1) & ~1;
+    const int db = wave & 1, kh = wave >> 1;
+    const int s_lo = kh * half, s_hi = min(L, s_lo + half);
+    const int64_t dv = c0 + db * 32 + r32;
+    const float* vcol = proj + b * L * stride + value_off + (dv < D ? dv : D - 1);
+    const float fon = r32 < MAXM ? 1.0f : 0.0f;
+    const int mf = min(r32, MAXM - 1);
+    f32x16 acc = {};
+    for (int s = s_lo; s < s_hi; s += 8) {  // four steps' operands loaded together
+        float x[4], a[4], bf[4];
 #pragma unroll
-        for (int kk = 0; kk < MAXM / 2; ++kk)
-            acc = mfma2(q_sh[ta * QP + 2 * kk + h], f_sh[(2 * kk + h) * FP + sc], acc);
-        const float cs = cum[sc], ws = wt[sc];
+        for (int q = 0; q < 4; ++q) x[q] = vcol[min(s + 2 * q + h, L - 1) * stride];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-            const int t = t0 + r;
-            const float v = fast_exp(prior[min(t, L - 1)] - cs) * acc[i] * ws;
-            infl[r * IP + s] = (s < t && t < L) ? v : 0.0f;
+        for (int q = 0; q < 4; ++q) {
+            const int sl = s + 2 * q + h, slc = min(sl, L - 1);
+            a[q] = sl < s_hi ? fwt[slc] * fast_tanh(x[q]) : 0.0f;
+            bf[q] = kf[slc * QP + mf] * fon;
         }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc = mfma2(a[q], bf[q], acc);
+    }
+    if (kh == 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) part[(db * 16 + i) * kWave + lane] = acc[i];
     }
     __syncthreads();
-    {
-        // the reads: wave w owns the 32 x 32 block (query half w / 2, column half w % 2);
-        // sum over slots of influence x value on MFMA, then the carried basis term
-        // e^{prior_t} (q_t . basis_d) as MAXM more K values. The denominators ride
-        // along as a second product with the same A operand and B = 1 (row sums of
-        // the influence), then e^{prior_t} (q_t . normalizer), so every lane holds
-        // the denominator of each of its rows.
-        const int tb = wave >> 1, db = wave & 1;
-        const int k_end = (s_cnt + 1) & ~1;
-        const float* ia = infl + (tb * 32 + r32) * IP + h;
-        const float* vb = val + h * VP + db * 32 + r32;
-        f32x16 acc = {}, accd = {};
-        int s = 0;
-        for (; s + 8 <= k_end; s += 8) {  // four steps' operands loaded together
-            const float a0 = ia[s], a1 = ia[s + 2], a2 = ia[s + 4], a3 = ia[s + 6];
-            const float b0 = vb[s * VP], b1 = vb[(s + 2) * VP], b2 = vb[(s + 4) * VP], b3 = vb[(s + 6) * VP];
-            acc = mfma2(a0, b0, acc);
-            accd = mfma2(a0, 1.0f, accd);
-            acc = mfma2(a1, b1, acc);
-            accd = mfma2(a1, 1.0f, accd);
-            acc = mfma2(a2, b2, acc);
-            accd = mfma2(a2, 1.0f, accd);
-            acc = mfma2(a3, b3, acc);
-            accd = mfma2(a3, 1.0f, accd);
-        }
-        for (; s < k_end; s += 2) {
-            const float a = ia[s];
-            acc = mfma2(a, vb[s * VP], acc);
-            accd = mfma2(a, 1.0f, accd);
-        }
-        const int tq = min(t0 + tb * 32 + r32, L - 1);
-        const float ep = fast_exp(prior[tq]);
-        const int64_t dq = min(c0 + db * 32 + r32, D - 1);
-#pragma unroll
-        for (int kk = 0; kk < MAXM / 2; ++kk) {
-            const int m = 2 * kk + h;
-            const float on = m < M ? 1.0f : 0.0f;
-            const float aq = ep * q_sh[tq * QP + m];
-            acc = mfma2(aq, basis[(b * D + dq) * M + min(m, M - 1)] * on, acc);
-            accd = mfma2(aq, normalizer[b * M + min(m, M - 1)] * on, accd);
-        }
-        const int64_t d = c0 + db * 32 + r32;
+    const float keep = prep.keep[b];
+    if (kh == 0) {
+        const int m = r32;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-            if (r >= rows || d >= D) continue;
-            const float dn = accd[i], reg = dn + kReadEpsilon;
-            out[(b * L + t0 + r) * D + d] = (dn / reg) * acc[i] / reg;
-        }
-    }
-    }  // MODE != kDelta
-    if constexpr (MODE == kRead) return;
-    if (blockIdx.z != 0) return;
-    // final basis columns (64 x M): sum over slots of (final-write weight x value)
-    // x feature on MFMA, slots split in two halves over wave pairs, the halves
-    // added through LDS (the influence rows are no longer read)
-    const float keep = expf(total);
-    const int half = ((L + 1) / 2 + 1) & ~1;
-    {
-        const int db = wave & 1, kh = wave >> 1;
-        const int s_lo = kh * half, s_hi = min(L, s_lo + half);
-        f32x16 acc = {};
-        const float* fm = f_sh + min(r32, MAXM - 1) * FP;
-        const float fon = r32 < MAXM ? 1.0f : 0.0f;
-        const float* vcol = val + db * 32 + r32;
-        for (int s = s_lo; s < s_hi; s += 8) {  // four steps' operands loaded together
-            float a[4], bf[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int sl = s + 2 * q + h, slc = min(sl, L - 1);
-                a[q] = sl < s_hi ? fwt[slc] * vcol[slc * VP] : 0.0f;
-                bf[q] = fm[slc] * fon;
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc = mfma2(a[q], bf[q], acc);
-        }
-        __syncthreads();  // the influence area is free
-        float* part = infl + db * 16 * kWave;  // [2][16][64]
-        if (kh == 1) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) part[i * kWave + lane] = acc[i];
-        }
-        __syncthreads();
-        if (kh == 0) {
-            const int m = r32;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int64_t d = c0 + db * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-                if (m >= M || d >= D) continue;
-                const int64_t at = (b * D + d) * M + m;
-                const float window_terms = acc[i] + part[i * kWave + lane];
-                next_basis[at] = MODE == kDelta ? window_terms : fmaf(keep, basis[at], window_terms);
-            }
+            const int64_t d = c0 + db * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            if (m >= M || d >= D) continue;
+            const int64_t at = (b * D + d) * M + m;
+            const float terms = acc[i] + part[(db * 16 + i) * kWave + lane];
+            next_basis[at] = FINAL ? fmaf(keep, basis[at], terms) : terms;
         }
     }
     if (blockIdx.y == 0 && wave == 3) {
         for (int m = 0; m < M; ++m) {
             float sum = 0.0f;
-            for (int s = lane; s < L; s += kWave) sum = fmaf(fwt[s], f_sh[m * FP + s], sum);
+            for (int s = lane; s < L; s += kWave) sum = fmaf(fwt[s], kf[s * QP + m], sum);
             sum = wave_sum_xor(sum);
-            if (lane == 0) next_normalizer[b * M + m] = MODE == kDelta ? sum : fmaf(keep, normalizer[b * M + m], sum);
+            if (lane == 0) next_normalizer[b * M + m] = FINAL ? fmaf(keep, normalizer[b * M + m], sum) : sum;
         }
-        if (MODE == kDelta && lane == 0) out[b] = keep;
+    }
+}
+
+// The reads of a window row from its carried state: one workgroup per (row,
+// group of kReadTiles 64-column tiles, 64 queries). It stages the prepared
+// features and weights of its queries and of the slots that can reach them,
+// forms the influence of slot s on query t,
+//   e^{prior_t - c_s} (q_t . f_s) weight_s  (s < t, else 0),
+// on fp32 MFMA (32 x 32 blocks, K = features) into LDS, and the denominators
+// den_t = sum_s influence + e^{prior_t} (q_t . normalizer) by wave
+// reductions. Then per column tile each wave forms a 32 x 32 block of
+// sum_s influence tanh(v_s[d]) + e^{prior_t} (q_t . basis_d) on MFMA (A from
+// LDS, B the value columns straight from memory, eight steps' loads in flight
+// ahead of their use), and writes read = den/(den + 2^-8) num/(den + 2^-8).
+constexpr int kReadTiles = 4;
+constexpr int kReadRows = 64;
+inline size_t read_lds(int64_t L, int64_t M) {
+    const int64_t Lq = (L + 31) & ~int64_t(31), X = assoc_maxm(M);
+    return static_cast<size_t>(kReadRows * (Lq + 1) + X * (Lq + 1) + kReadRows * (X + 1) + 2 * Lq + 2 * kReadRows) *
+           sizeof(float);
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(256) void assoc_window_read_kernel(
+    const float* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
+    const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out, int L, int64_t D,
+    int M) {
+    extern __shared__ float sh[];
+    constexpr int QP = MAXM + 1;
+    const int Lq = (L + 31) & ~31;
+    const int IP = Lq + 1;
+    float* infl = sh;                     // [64][IP]
+    float* f_sh = infl + kReadRows * IP;  // [MAXM][IP]
+    float* q_sh = f_sh + MAXM * IP;       // [64][QP]
+    float* cum = q_sh + kReadRows * QP;   // [Lq]
+    float* wt = cum + Lq;                 // [Lq]
+    float* pr = wt + Lq;                  // [64] prior of the tile's queries
+    float* den = pr + kReadRows;          // [64]
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const int h = lane >> 5, r32 = lane & 31;
+    const int t0 = static_cast<int>(blockIdx.z) * kReadRows;
+    const int rows = min(kReadRows, L - t0);
+    const int s_cnt = t0 + rows;  // slots that can reach these queries (s < t <= t0 + rows - 1)
+    for (int i = tid; i < s_cnt * MAXM; i += 256) f_sh[(i % MAXM) * IP + i / MAXM] = prep.kf[b * L * MAXM + i];
+    for (int i = tid; i < kReadRows * MAXM; i += 256) {
+        const int r = i / MAXM;
+        q_sh[r * QP + i % MAXM] = r < rows ? prep.qf[(b * L + t0) * MAXM + i] : 0.0f;
+    }
+    for (int s2 = tid; s2 < s_cnt; s2 += 256) {
+        cum[s2] = prep.cum[b * L + s2];
+        wt[s2] = prep.wt[b * L + s2];
+    }
+    if (tid < kReadRows) pr[tid] = tid < rows ? prep.prior[b * L + t0 + tid] : 0.0f;
+    __syncthreads();
+
+    const int nsb = (s_cnt + 31) / 32;
+    for (int blk = wave; blk < 2 * nsb; blk += 4) {
+        const int tb = blk / nsb, sb = blk - tb * nsb;
+        const int ra = tb * 32 + r32;
+        const int s = sb * 32 + r32, sc = min(s, s_cnt - 1);
+        f32x16 acc = {};
+#pragma unroll
+        for (int kk = 0; kk < MAXM / 2; ++kk) acc = mfma2(q_sh[ra * QP + 2 * kk + h], f_sh[(2 * kk + h) * IP + sc], acc);
+        const float cs = cum[sc], ws = wt[sc];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            const float v = fast_exp(pr[r] - cs) * acc[i] * ws;
+            infl[r * IP + s] = (s < t0 + r && r < rows) ? v : 0.0f;
+        }
+    }
+    __syncthreads();
+    for (int rr = 0; rr < kReadRows / 4; ++rr) {
+        const int r = wave * (kReadRows / 4) + rr;
+        float sum = 0.0f;
+        for (int s = lane; s < s_cnt; s += kWave) sum += infl[r * IP + s];
+        float nq = lane < M ? q_sh[r * QP + lane] * normalizer[b * M + lane] : 0.0f;
+        sum = wave_sum_xor(sum);
+        nq = wave_sum_xor(nq);
+        if (lane == 0) den[r] = sum + fast_exp(pr[r]) * nq;
+    }
+    __syncthreads();
+
+    const int tb = wave >> 1, db = wave & 1;
+    const int k_end = (s_cnt + 1) & ~1;
+    const float* ia = infl + (tb * 32 + r32) * IP + h;
+    const float ep = fast_exp(pr[tb * 32 + r32]);
+    const float* vrows = proj + b * L * stride + value_off;
+    for (int ct = 0; ct < kReadTiles; ++ct) {
+        const int64_t d0 = (static_cast<int64_t>(blockIdx.y) * kReadTiles + ct) * 64 + db * 32;
+        if (d0 >= D) break;
+        const int64_t dq = min(d0 + r32, D - 1);
+        const float* vcol = vrows + dq;
+        f32x16 acc = {};
+        float bn[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) bn[u] = vcol[min(2 * u + h, L - 1) * stride];
+        for (int s = 0; s < k_end; s += 16) {
+            float bc[8], av[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bc[u] = bn[u];
+            if (s + 16 < k_end) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) bn[u] = vcol[min(s + 16 + 2 * u + h, L - 1) * stride];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) av[u] = s + 2 * u + h < k_end ? ia[s + 2 * u] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = mfma2(av[u], fast_tanh(bc[u]), acc);
+        }
+#pragma unroll
+        for (int kk = 0; kk < MAXM / 2; ++kk) {
+            const int m = 2 * kk + h;
+            const float on = m < M ? 1.0f : 0.0f;
+            acc = mfma2(ep * q_sh[(tb * 32 + r32) * QP + m], basis[(b * D + dq) * M + min(m, M - 1)] * on, acc);
+        }
+        const int64_t d = d0 + r32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+            if (r >= rows || d >= D) continue;
+            const float dn = den[r], reg = dn + kReadEpsilon;
+            out[(b * L + t0 + r) * D + d] = (dn / reg) * acc[i] / reg;
+        }
     }
 }
 
 // The state carried into each of a sequence's windows and the state after the
 // last: for element e of the flattened basis (D x M, then the M normalizer
 // entries) of batch row b, cur = state_0; window w receives cur, then
-// cur = fmaf(keep_w, cur, delta_w), the update assoc_read_kernel applies at the
-// end of a window (so the carried states equal a window-by-window run's).
+// cur = fmaf(keep_w, cur, delta_w), the update the one-window entry applies at
+// the end of a window (so the carried states equal a window-by-window run's).
 __global__ __launch_bounds__(256) void assoc_carry_kernel(
     const float* __restrict__ delta_basis, const float* __restrict__ delta_norm, const float* __restrict__ keep,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ carried_basis,
@@ -350,6 +406,45 @@ __global__ __launch_bounds__(256) void assoc_carry_kernel(
         cur = fmaf(keep[row], cur, delta[row * n + x]);
     }
     (is_basis ? next_basis : next_normalizer)[b * n + x] = cur;
+}
+
+// The three launches of a window's (or every window's) memory: prepare, the
+// state terms (FINAL: the next state), the reads. Rows are batch rows (one
+// window) or (batch row, window) pairs.
+template <int MAXM>
+int launch_prep(const float* proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
+                int64_t write_off, const float* surprise, const uint8_t* valid, const AssocPrep& prep, int64_t rows,
+                int L, int M, hipStream_t s) {
+    hipLaunchKernelGGL(assoc_prep_kernel<MAXM>, dim3(static_cast<unsigned>(rows)), dim3(256),
+                       3 * static_cast<size_t>(L) * sizeof(float), s, proj, stride, fk_off, fq_off, decay_off,
+                       write_off, surprise, valid, prep, L, M);
+    return check_launch("associative memory (prepare)");
+}
+
+template <int MAXM, bool FINAL>
+int launch_delta(const float* proj, int64_t stride, int64_t value_off, const AssocPrep& prep, const float* basis,
+                 const float* normalizer, float* nb, float* nn, int64_t rows, int L, int64_t D, int M,
+                 hipStream_t s) {
+    const size_t lds = (static_cast<size_t>(L) * (MAXM + 2) + 2 * 16 * kWave) * sizeof(float);
+    hipLaunchKernelGGL((assoc_delta_kernel<MAXM, FINAL>), dim3(static_cast<unsigned>(rows),
+                       static_cast<unsigned>((D + 63) / 64)), dim3(256), lds, s, proj, stride, value_off, prep, basis,
+                       normalizer, nb, nn, L, D, M);
+    return check_launch("associative memory (state terms)");
+}
+
+template <int MAXM>
+int launch_window_read(const float* proj, int64_t stride, int64_t value_off, const AssocPrep& prep,
+                       const float* basis, const float* normalizer, float* out, int64_t rows, int L, int64_t D, int M,
+                       hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((D + 64 * kReadTiles - 1) / (64 * kReadTiles)),
+                    static_cast<unsigned>((L + kReadRows - 1) / kReadRows));
+    hipLaunchKernelGGL(assoc_window_read_kernel<MAXM>, grid, dim3(256), read_lds(L, M), s, proj, stride, value_off,
+                       prep, basis, normalizer, out, L, D, M);
+    return check_launch("associative memory (reads)");
+}
+
+inline size_t delta_lds(int64_t L, int64_t M) {
+    return (static_cast<size_t>(L) * (assoc_maxm(M) + 2) + 2 * 16 * kWave) * sizeof(float);
 }
 
 // One-position window (a decode step): read from the carried state, then
@@ -438,25 +533,79 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
 
 using namespace koemi;
 
-extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset,
-                                     int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
-                                     int64_t write_offset, const float* surprise, const uint8_t* valid,
-                                     const float* basis, const float* normalizer, float* read, float* next_basis,
-                                     float* next_normalizer, int64_t batch, int64_t length, int64_t width,
-                                     int64_t features, koemi_stream_t stream) {
-    if (batch < 0 || length < 0 || width < 1 || features < 1)
-        return fail(KOEMI_ERR_INVALID, "associative read needs non-negative batch and length, positive width and features");
+namespace {
+
+// Largest window the LDS of the read kernel holds (64 influence rows of
+// L + 1 floats plus the staged features and weights).
+inline bool window_fits(int64_t L, int64_t M) { return read_lds(L, M) <= 160 * 1024 && delta_lds(L, M) <= 160 * 1024; }
+
+struct WindowsWorkspace {
+    size_t delta_basis, delta_norm, carried_basis, carried_norm, prep, total;
+};
+
+inline WindowsWorkspace windows_workspace(int64_t rows, int64_t window, int64_t width, int64_t features) {
+    WindowsWorkspace w;
+    const size_t basis_bytes = align256(static_cast<size_t>(rows * width * features) * sizeof(float));
+    const size_t norm_bytes = align256(static_cast<size_t>(rows * features) * sizeof(float));
+    w.delta_basis = 0;
+    w.delta_norm = w.delta_basis + basis_bytes;
+    w.carried_basis = w.delta_norm + norm_bytes;
+    w.carried_norm = w.carried_basis + basis_bytes;
+    w.prep = w.carried_norm + norm_bytes;
+    w.total = w.prep + prep_bytes(rows, window, features);
+    return w;
+}
+
+int check_assoc_args(int64_t row_stride, int64_t value_offset, int64_t feature_offset, int64_t query_feature_offset,
+                     int64_t decay_offset, int64_t write_offset, int64_t width, int64_t features) {
     if (features > 32) return fail(KOEMI_ERR_UNSUPPORTED, "associative read supports at most 32 memory features");
     auto inside = [&](int64_t off, int64_t span) { return off >= 0 && off + span <= row_stride; };
     if (!inside(value_offset, width) || !inside(feature_offset, features) ||
         !inside(query_feature_offset, features) || !inside(decay_offset, 1) || !inside(write_offset, 1))
         return fail(KOEMI_ERR_INVALID, "associative read column offsets must lie inside the row stride");
+    return KOEMI_OK;
+}
+
+// prepare, state terms (FINAL: next state from the given one), reads from the
+// given (carried) state
+template <int MAXM, bool FINAL>
+int run_window_memory(const float* proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
+                      int64_t decay_off, int64_t write_off, const float* surprise, const uint8_t* valid,
+                      const AssocPrep& prep, const float* state_basis, const float* state_norm, float* nb, float* nn,
+                      const float* read_basis, const float* read_norm, float* read, int64_t rows, int L, int64_t D,
+                      int M, hipStream_t s, bool reads) {
+    int st = launch_prep<MAXM>(proj, stride, fk_off, fq_off, decay_off, write_off, surprise, valid, prep, rows, L, M, s);
+    if (st != KOEMI_OK) return st;
+    st = launch_delta<MAXM, FINAL>(proj, stride, value_off, prep, state_basis, state_norm, nb, nn, rows, L, D, M, s);
+    if (st != KOEMI_OK || !reads) return st;
+    return launch_window_read<MAXM>(proj, stride, value_off, prep, read_basis, read_norm, read, rows, L, D, M, s);
+}
+
+}  // namespace
+
+extern "C" size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width,
+                                                         int64_t features) {
+    if (batch <= 0 || length <= 1 || width < 1 || features < 1) return 0;
+    return prep_bytes(batch, length, features);
+}
+
+extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset,
+                                     int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
+                                     int64_t write_offset, const float* surprise, const uint8_t* valid,
+                                     const float* basis, const float* normalizer, float* read, float* next_basis,
+                                     float* next_normalizer, int64_t batch, int64_t length, int64_t width,
+                                     int64_t features, void* workspace, size_t workspace_bytes,
+                                     koemi_stream_t stream) {
+    if (batch < 0 || length < 0 || width < 1 || features < 1)
+        return fail(KOEMI_ERR_INVALID, "associative read needs non-negative batch and length, positive width and features");
+    int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
+                              write_offset, width, features);
+    if (st != KOEMI_OK) return st;
     if (batch == 0 || length == 0) return KOEMI_OK;
-    const size_t lds = assoc_lds(length, features);
-    if (lds > 160 * 1024)
+    if (!window_fits(length, features))
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read window too long (%lld positions)",
                     static_cast<long long>(length));
-    if (batch > 0x7fffffffLL || (width + kAssocCols - 1) / kAssocCols > 65535)
+    if (batch > 0x7fffffffLL || (width + 63) / 64 > 65535)
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read grid too large");
     if (!projections || !surprise || !valid || !basis || !normalizer || !read || !next_basis || !next_normalizer)
         return fail(KOEMI_ERR_INVALID, "associative read received a null pointer");
@@ -473,45 +622,26 @@ extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_strid
         else step(assoc_step_kernel<32>);
         return check_launch("koemi_assoc_scan_read");
     }
-    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((width + kAssocCols - 1) / kAssocCols),
-                    static_cast<unsigned>((length + kAssocRows - 1) / kAssocRows));
-    auto run = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), lds, s, projections, row_stride, value_offset, feature_offset,
-                           query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer, read,
-                           next_basis, next_normalizer, static_cast<int>(length), width, M);
-    };
-    if (M <= 16) run(assoc_read_kernel<16>);
-    else run(assoc_read_kernel<32>);
-    return check_launch("koemi_assoc_scan_read");
+    const size_t need = prep_bytes(batch, length, features);
+    if (!workspace || workspace_bytes < need)
+        return fail(KOEMI_ERR_INVALID, "associative read workspace too small: need %zu bytes", need);
+    const AssocPrep prep = prep_at(workspace, batch, length, features);
+    const int L = static_cast<int>(length);
+    if (M <= 16)
+        return run_window_memory<16, true>(projections, row_stride, value_offset, feature_offset, query_feature_offset,
+                                           decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
+                                           next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M, s,
+                                           true);
+    return run_window_memory<32, true>(projections, row_stride, value_offset, feature_offset, query_feature_offset,
+                                       decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
+                                       next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M, s,
+                                       true);
 }
 
-namespace {
-
-struct WindowsWorkspace {
-    size_t delta_basis, delta_norm, keep, carried_basis, carried_norm, total;
-};
-
-inline size_t align256w(size_t x) { return (x + 255) & ~size_t(255); }
-
-inline WindowsWorkspace windows_workspace(int64_t rows, int64_t width, int64_t features) {
-    WindowsWorkspace w;
-    const size_t basis_bytes = align256w(static_cast<size_t>(rows * width * features) * sizeof(float));
-    const size_t norm_bytes = align256w(static_cast<size_t>(rows * features) * sizeof(float));
-    w.delta_basis = 0;
-    w.delta_norm = w.delta_basis + basis_bytes;
-    w.keep = w.delta_norm + norm_bytes;
-    w.carried_basis = w.keep + align256w(static_cast<size_t>(rows) * sizeof(float));
-    w.carried_norm = w.carried_basis + basis_bytes;
-    w.total = w.carried_norm + norm_bytes;
-    return w;
-}
-
-}  // namespace
-
-extern "C" size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t width,
-                                                                 int64_t features) {
-    if (batch < 0 || windows < 0 || width < 1 || features < 1) return 0;
-    return windows_workspace(batch * windows, width, features).total;
+extern "C" size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window,
+                                                                 int64_t width, int64_t features) {
+    if (batch < 0 || windows < 0 || window < 1 || width < 1 || features < 1) return 0;
+    return windows_workspace(batch * windows, window, width, features).total;
 }
 
 extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
@@ -524,59 +654,54 @@ extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t r
     if (batch < 0 || windows < 0 || window < 2 || width < 1 || features < 1)
         return fail(KOEMI_ERR_INVALID, "windowed associative read needs non-negative batch and windows, a window of at "
                     "least two positions, positive width and features");
-    if (features > 32) return fail(KOEMI_ERR_UNSUPPORTED, "associative read supports at most 32 memory features");
-    auto inside = [&](int64_t off, int64_t span) { return off >= 0 && off + span <= row_stride; };
-    if (!inside(value_offset, width) || !inside(feature_offset, features) ||
-        !inside(query_feature_offset, features) || !inside(decay_offset, 1) || !inside(write_offset, 1))
-        return fail(KOEMI_ERR_INVALID, "associative read column offsets must lie inside the row stride");
+    int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
+                              write_offset, width, features);
+    if (st != KOEMI_OK) return st;
     const int64_t rows = batch * windows;
     if (batch == 0) return KOEMI_OK;
-    const size_t lds = assoc_lds(window, features);
-    if (lds > 160 * 1024)
+    if (!window_fits(window, features))
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read window too long (%lld positions)",
                     static_cast<long long>(window));
-    if (rows > 0x7fffffffLL || (width + kAssocCols - 1) / kAssocCols > 65535 ||
-        (width * features + features + 255) / 256 > 65535)
+    if (rows > 0x7fffffffLL || (width + 63) / 64 > 65535 || (width * features + features + 255) / 256 > 65535)
         return fail(KOEMI_ERR_UNSUPPORTED, "windowed associative read grid too large");
     if (!basis || !normalizer || !next_basis || !next_normalizer ||
         (windows > 0 && (!projections || !surprise || !valid || !read)))
         return fail(KOEMI_ERR_INVALID, "windowed associative read received a null pointer");
-    const WindowsWorkspace ws = windows_workspace(rows, width, features);
+    const WindowsWorkspace ws = windows_workspace(rows, window, width, features);
     if (!workspace || workspace_bytes < ws.total)
         return fail(KOEMI_ERR_INVALID, "windowed associative read workspace too small: need %zu bytes", ws.total);
     char* w = static_cast<char*>(workspace);
     float* delta_basis = reinterpret_cast<float*>(w + ws.delta_basis);
     float* delta_norm = reinterpret_cast<float*>(w + ws.delta_norm);
-    float* keep = reinterpret_cast<float*>(w + ws.keep);
     float* carried_basis = reinterpret_cast<float*>(w + ws.carried_basis);
     float* carried_norm = reinterpret_cast<float*>(w + ws.carried_norm);
+    const AssocPrep prep = prep_at(w + ws.prep, rows, window, features);
     const hipStream_t s = as_stream(stream);
     const int M = static_cast<int>(features);
-    const unsigned col_tiles = static_cast<unsigned>((width + kAssocCols - 1) / kAssocCols);
-    auto launch = [&](auto kernel, unsigned row_tiles, const float* carried_b, const float* carried_n, float* out,
-                      float* nb, float* nn) {
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(rows), col_tiles, row_tiles), dim3(256), lds, s,
-                           projections, row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
-                           write_offset, surprise, valid, carried_b, carried_n, out, nb, nn, static_cast<int>(window),
-                           width, M);
-    };
+    const int L = static_cast<int>(window);
     if (windows > 0) {
-        // 1. every window's own terms of the final state, from a zero carried state
-        if (M <= 16) launch(assoc_read_kernel<16, kDelta>, 1u, nullptr, nullptr, keep, delta_basis, delta_norm);
-        else launch(assoc_read_kernel<32, kDelta>, 1u, nullptr, nullptr, keep, delta_basis, delta_norm);
-        int st = check_launch("koemi_assoc_scan_read_windows(delta)");
+        // 1. every window's prepared weights and own terms of the final state (from a zero state)
+        st = M <= 16 ? run_window_memory<16, false>(projections, row_stride, value_offset, feature_offset,
+                                                    query_feature_offset, decay_offset, write_offset, surprise, valid,
+                                                    prep, nullptr, nullptr, delta_basis, delta_norm, nullptr, nullptr,
+                                                    nullptr, rows, L, width, M, s, false)
+                     : run_window_memory<32, false>(projections, row_stride, value_offset, feature_offset,
+                                                    query_feature_offset, decay_offset, write_offset, surprise, valid,
+                                                    prep, nullptr, nullptr, delta_basis, delta_norm, nullptr, nullptr,
+                                                    nullptr, rows, L, width, M, s, false);
         if (st != KOEMI_OK) return st;
     }
     // 2. the state carried into each window, and the final state
     const int64_t DM = width * features;
     hipLaunchKernelGGL(assoc_carry_kernel, dim3(static_cast<unsigned>(batch), static_cast<unsigned>((DM + M + 255) / 256)),
-                       dim3(256), 0, s, delta_basis, delta_norm, keep, basis, normalizer, carried_basis, carried_norm,
-                       next_basis, next_normalizer, windows, DM, static_cast<int64_t>(M));
-    int st = check_launch("koemi_assoc_scan_read_windows(carry)");
+                       dim3(256), 0, s, delta_basis, delta_norm, prep.keep, basis, normalizer, carried_basis,
+                       carried_norm, next_basis, next_normalizer, windows, DM, static_cast<int64_t>(M));
+    st = check_launch("koemi_assoc_scan_read_windows(carry)");
     if (st != KOEMI_OK || windows == 0) return st;
     // 3. the reads of every window from its carried state
-    const unsigned row_tiles = static_cast<unsigned>((window + kAssocRows - 1) / kAssocRows);
-    if (M <= 16) launch(assoc_read_kernel<16, kRead>, row_tiles, carried_basis, carried_norm, read, nullptr, nullptr);
-    else launch(assoc_read_kernel<32, kRead>, row_tiles, carried_basis, carried_norm, read, nullptr, nullptr);
-    return check_launch("koemi_assoc_scan_read_windows(read)");
+    if (M <= 16)
+        return launch_window_read<16>(projections, row_stride, value_offset, prep, carried_basis, carried_norm, read,
+                                      rows, L, width, M, s);
+    return launch_window_read<32>(projections, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows,
+                                  L, width, M, s);
 }

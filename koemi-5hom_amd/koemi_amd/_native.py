@@ -111,12 +111,13 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),
     ),
+    "koemi_assoc_scan_read_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64)),
     "koemi_assoc_scan_read": (
         c_int,
         (_P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64,
-         c_int64, c_int64, _P),
+         c_int64, c_int64, _P, c_size_t, _P),
     ),
-    "koemi_assoc_scan_read_windows_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64)),
+    "koemi_assoc_scan_read_windows_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64, c_int64)),
     "koemi_assoc_scan_read_windows": (
         c_int,
         (_P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64,

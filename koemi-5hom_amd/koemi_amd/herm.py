@@ -332,13 +332,15 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
+    need = _native.query("koemi_assoc_scan_read_workspace_bytes", batch, length, d, m)
+    workspace = torch.empty((need,), device=projections.device, dtype=torch.uint8) if need else None
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read",
         _native.ptr(projections), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
         *(_native.ptr(t) for t in args),
         _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
-        batch, length, d, m, _native.stream_of(projections.device),
+        batch, length, d, m, _native.ptr(workspace), need, _native.stream_of(projections.device),
     )
     return read, next_basis, next_normalizer
 
@@ -516,8 +518,8 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
-    workspace = torch.empty((_native.query("koemi_assoc_scan_read_windows_workspace_bytes", batch, windows, d, m),),
-                            device=projections.device, dtype=torch.uint8)
+    workspace = torch.empty((_native.query("koemi_assoc_scan_read_windows_workspace_bytes", batch, windows, window, d,
+                                           m),), device=projections.device, dtype=torch.uint8)
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read_windows",
