@@ -599,20 +599,38 @@ namespace {
 // Needs width % 4 == 0, 16-byte aligned rows and at most kWinMaxSlots
 // candidate slots per block; other shapes take the kernels above.
 constexpr int kWinQ = 32;
-constexpr int kWinMaxSlots = 152;  // LDS: 4 x 32 x 153 fp32 partial scores (78 KiB: two workgroups per CU)
+constexpr int kWinMaxSlots = 152;   // salient blocks: LDS 4 x 32 x 153 fp32 partial scores (78 KiB)
+constexpr int kWinLocalSlots = 64;  // local blocks: 4 x 32 x 65 (33 KiB)
 
 __device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-template <bool LOCAL>
+// Four consecutive output columns of one row (16-byte fp32 or 8-byte bf16 store).
+__device__ inline void store4(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ inline void store4(__bf16* p, float a, float b, float c, float d) {
+    const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(a)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+    const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<__bf16>(c)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(d))) << 16);
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
+// out rows are `ostride` elements apart (the reads can land in a column
+// block of a wider matrix, e.g. the fusion input in bf16).
+template <bool LOCAL, int MAXS, typename OutT>
 __global__ __launch_bounds__(256) void window_read_kernel(
     const float* __restrict__ ck, const float* __restrict__ cv, const uint8_t* __restrict__ cvalid,
     const float* __restrict__ k, const float* __restrict__ v, const uint8_t* __restrict__ flags,
-    const float* __restrict__ q, float* __restrict__ out, int S, int L, int64_t D, int window, float scale) {
-    __shared__ int list[kWinMaxSlots];
+    const float* __restrict__ q, OutT* __restrict__ out, int64_t ostride, int S, int L, int64_t D, int window,
+    float scale) {
+    constexpr int NST = (MAXS + 31) / 32;  // slot tiles
+    constexpr int NJ = (MAXS + kWave - 1) / kWave;
+    __shared__ int list[MAXS];
     __shared__ int wave_cnt[4];
-    __shared__ float sc[4][kWinQ][kWinMaxSlots + 1];
+    __shared__ float sc[4][kWinQ][MAXS + 1];
     const int64_t row = blockIdx.x;
     const int t0 = static_cast<int>(blockIdx.y) * kWinQ;
     const int nq = min(kWinQ, L - t0);
@@ -633,9 +651,13 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     const int n = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
     if (f) list[base + before] = c;
     __syncthreads();
-    float* orow0 = out + (row * L + t0) * D;
+    OutT* orow0 = out + (row * L + t0) * ostride;
     if (n == 0) {  // nothing eligible for any query of the block: zero rows
-        for (int64_t i = tid; i < nq * D / 4; i += 256) reinterpret_cast<float4*>(orow0)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        const int64_t quads = D / 4;
+        for (int64_t i = tid; i < nq * quads; i += 256) {
+            const int64_t m = i / quads;
+            store4(orow0 + m * ostride + 4 * (i - m * quads), 0.0f, 0.0f, 0.0f, 0.0f);
+        }
         return;
     }
     const int nst = (n + 31) / 32;
@@ -646,9 +668,9 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     // scores
     {
         const float* qrow = q + (row * L + t0 + min(r, nq - 1)) * D;
-        f32x16 acc[5];
+        f32x16 acc[NST];
 #pragma unroll
-        for (int st = 0; st < 5; ++st)
+        for (int st = 0; st < NST; ++st)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[st][e] = 0.0f;
         const int64_t chunks = (D + 63) / 64;
@@ -662,7 +684,7 @@ __global__ __launch_bounds__(256) void window_read_kernel(
                     qa[blk][i] = col < D ? *reinterpret_cast<const float4*>(qrow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
 #pragma unroll
-            for (int st = 0; st < 5; ++st) {
+            for (int st = 0; st < NST; ++st) {
                 if (st >= nst) break;
                 const float* krow = slot_row(list[min(st * 32 + r, n - 1)], ck, k);
                 float4 kb[2][4];
@@ -687,7 +709,7 @@ __global__ __launch_bounds__(256) void window_read_kernel(
         }
         // accumulator entry e of lane l: query 8 (e / 4) + 4 h + e % 4, slot st * 32 + l % 32
 #pragma unroll
-        for (int st = 0; st < 5; ++st) {
+        for (int st = 0; st < NST; ++st) {
             if (st >= nst) break;
             if (st * 32 + r < n) {
 #pragma unroll
@@ -702,12 +724,12 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     for (int qq = 0; qq < 8; ++qq) {
         const int m = wave * 8 + qq;
         const int t = t0 + m;
-        float x[3];
-        bool ok[3];
+        float x[NJ];
+        bool ok[NJ];
         float mx = -INFINITY;
         bool any = false;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const int idx = j * kWave + lane;
             x[j] = 0.0f;
             ok[j] = false;
@@ -726,51 +748,91 @@ __global__ __launch_bounds__(256) void window_read_kernel(
         if (!any) mx = 0.0f;
         float sum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             x[j] = ok[j] ? expf(x[j] - mx) : 0.0f;
             sum += x[j];
         }
         sum = wave_sum_xor(sum);
 #pragma unroll
-        for (int j = 0; j < 3; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const int idx = j * kWave + lane;
             if (idx < n) sc[0][m][idx] = sum > 0.0f ? x[j] / sum : x[j];
         }
     }
     __syncthreads();
 
-    // weighted sum of the listed slots' values
-    const int64_t col_tiles = (D + 31) / 32;
-    for (int64_t ct = wave; ct < col_tiles; ct += 4) {
-        const int64_t col = ct * 32 + r;
-        const int64_t colc = min(col, D - 1);
-        f32x16 o;
+    // weighted sum of the listed slots' values: a wave covers 128 columns per
+    // pass as four 32-column MFMA tiles, lane (r, h) feeding column 4 r + c of
+    // tile c from one 16-byte load of a value row; eight MFMA steps' loads
+    // are issued ahead of the step that uses them
+    const int64_t passes = (D + 127) / 128;
+    for (int64_t pc = wave; pc < passes; pc += 4) {
+        const int64_t col = pc * 128 + 4 * r;
+        const bool cok = col < D;
+        const int64_t colc = cok ? col : 0;
+        f32x16 o[4];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[e] = 0.0f;
-        for (int i0 = 0; i0 < npad; i0 += 16) {  // eight MFMA steps of two slots each
-            float a[8], b[8];
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) o[cc][e] = 0.0f;
+        float4 bn[8];
+        auto fetch = [&](int i0) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int li = i0 + 2 * u + h;
-                a[u] = li < n ? sc[0][r][li] : 0.0f;
-                b[u] = li < n ? slot_row(list[li], cv, v)[colc] : 0.0f;
+                bn[u] = li < n ? *reinterpret_cast<const float4*>(slot_row(list[li], cv, v) + colc)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+        };
+        fetch(0);
+        for (int i0 = 0; i0 < npad; i0 += 16) {  // eight MFMA steps of two slots each
+            float4 bc[8];
+            float a[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) o = mfma_f32_32x32x2(a[u], b[u], o);
+            for (int u = 0; u < 8; ++u) {
+                bc[u] = bn[u];
+                const int li = i0 + 2 * u + h;
+                a[u] = li < n ? sc[0][r][li] : 0.0f;
+            }
+            if (i0 + 16 < npad) fetch(i0 + 16);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                o[0] = mfma_f32_32x32x2(a[u], bc[u].x, o[0]);
+                o[1] = mfma_f32_32x32x2(a[u], bc[u].y, o[1]);
+                o[2] = mfma_f32_32x32x2(a[u], bc[u].z, o[2]);
+                o[3] = mfma_f32_32x32x2(a[u], bc[u].w, o[3]);
+            }
         }
-        if (col < D) {
+        if (cok) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int m = 8 * (e / 4) + 4 * h + (e % 4);
-                if (m < nq) orow0[m * D + col] = o[e];
+                if (m < nq) store4(orow0 + m * ostride + col, o[0][e], o[1][e], o[2][e], o[3][e]);
             }
         }
     }
 }
 
+// Whether the fused read takes a block: at most MAXS candidate slots.
 inline bool window_read_fits(int64_t carried, int64_t length, int64_t window) {
-    if (carried > kWinMaxSlots) return false;
-    return window > 0 ? window + kWinQ - 1 <= kWinMaxSlots : carried + length - 1 <= kWinMaxSlots;
+    if (window > 0) return carried <= kWinLocalSlots && window + kWinQ - 1 <= kWinLocalSlots;
+    return carried <= kWinMaxSlots && carried + length - 1 <= kWinMaxSlots;
+}
+
+template <typename OutT>
+int launch_window_read(const float* ck, const float* cv, const uint8_t* cvalid, const float* k, const float* v,
+                       const uint8_t* flags, const float* q, OutT* out, int64_t ostride, int64_t batch,
+                       int64_t carried, int64_t length, int64_t width, int64_t window, hipStream_t stream) {
+    const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((length + kWinQ - 1) / kWinQ));
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, ck, cv, cvalid, k, v, flags, q, out, ostride,
+                           static_cast<int>(carried), static_cast<int>(length), width, static_cast<int>(window),
+                           inv_sqrt_d);
+    };
+    if (window > 0) launch(window_read_kernel<true, kWinLocalSlots, OutT>);
+    else launch(window_read_kernel<false, kWinMaxSlots, OutT>);
+    return check_launch(window > 0 ? "koemi_local_read" : "koemi_salient_read");
 }
 
 // The masked read shared by the salient read (window 0: no lower bound) and
@@ -822,18 +884,10 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
         (length + kWinQ - 1) / kWinQ <= 65535 &&
         aligned16(carried_keys) && aligned16(carried_values) && aligned16(keys) && aligned16(values) &&
         aligned16(queries) && aligned16(out)) {
-        const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
-        const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((length + kWinQ - 1) / kWinQ));
-        auto launch = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, as_stream(stream), static_cast<const float*>(carried_keys),
-                               static_cast<const float*>(carried_values), carried_valid,
-                               static_cast<const float*>(keys), static_cast<const float*>(values), admission,
-                               static_cast<const float*>(queries), static_cast<float*>(out), static_cast<int>(carried),
-                               static_cast<int>(length), width, static_cast<int>(window), inv_sqrt_d);
-        };
-        if (window > 0) launch(window_read_kernel<true>);
-        else launch(window_read_kernel<false>);
-        return check_launch(window > 0 ? "koemi_local_read" : "koemi_salient_read");
+        return launch_window_read(static_cast<const float*>(carried_keys), static_cast<const float*>(carried_values),
+                                  carried_valid, static_cast<const float*>(keys), static_cast<const float*>(values),
+                                  admission, static_cast<const float*>(queries), static_cast<float*>(out), width, batch,
+                                  carried, length, width, window, as_stream(stream));
     }
     char* base = static_cast<char*>(workspace);
     float* score = reinterpret_cast<float*>(base + ws.score_off);

@@ -648,18 +648,20 @@ def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids:
 
 class SequencePrefill:
     """``stack_sequence`` at a fixed (batch, length) replayed from one captured
-    HIP graph: ``run(ids, states=None)`` copies the ids in, resets the static
-    state buffers to ``states`` (default: the states given at construction),
-    replays, and returns the logits buffer; ``self.states`` then holds the
-    states after the sequence. Two eager passes on throwaway copies warm the
-    libraries up before the capture."""
+    HIP graph. The graph reads the ids and the starting states from static
+    buffers it never writes (``self.start``: the states given at
+    construction) and writes the logits and the states after the sequence
+    (``self.states``) into buffers of its own, so a replay needs no copies:
+    ``run(ids=None, states=None)`` copies in only what is given (ids other
+    than the static ids buffer; starting states, which then stay the start
+    of later runs), replays, and returns the logits buffer. Two eager passes
+    on throwaway copies warm the libraries up before the capture."""
 
     def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
                  ids: Tensor) -> None:
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
         self.start = [{k: v.clone() for k, v in st.items()} for st in states]
-        self.states = [{k: v.clone() for k, v in st.items()} for st in states]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -670,21 +672,15 @@ class SequencePrefill:
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.logits, next_states = stack_sequence(params, settings, self.ids, self.states)
-            dst, src = [], []
-            for state, new in zip(self.states, next_states):
-                for key in state:
-                    dst.append(state[key])
-                    src.append(new[key])
-            torch._foreach_copy_(dst, src)
+            self.logits, self.states = stack_sequence(params, settings, self.ids, self.start)
 
     def run(self, ids: Tensor | None = None, states: list[dict[str, Tensor]] | None = None) -> Tensor:
-        if ids is not None:
+        if ids is not None and ids.data_ptr() != self.ids.data_ptr():
             self.ids.copy_(ids)
-        source = self.start if states is None else states
-        for state, start in zip(self.states, source):
-            for key, tensor in state.items():
-                tensor.copy_(start[key])
+        if states is not None:
+            dst = [t for st in self.start for t in st.values()]
+            src = [st[k] for st, mine in zip(states, self.start) for k in mine]
+            torch._foreach_copy_(dst, src)
         self.graph.replay()
         return self.logits
 
