@@ -359,7 +359,8 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
  * project (the feature softmax, value tanh, bounded decay and write weight),
  * query_features, fast_write_terms and scan_and_read of model/memory.py:82-144,
  * 244-255, with the write masking of network.py:734-740 (torch composites in
- * the reference). `projections` is fp32 [batch * length, row_stride] holding,
+ * the reference). `projections` is [batch * length, row_stride] in
+ * projection_dtype (KOEMI_F32 or KOEMI_BF16: a bf16 GEMM's own output),
  * at the given column offsets, the value pre-activations (width columns), the
  * feature logits W_f key + b_f and W_f query + b_f (features columns each)
  * and the decay and write logits (one column each); surprise fp32 and valid
@@ -373,8 +374,8 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
  * bytes for the per-position weights (features, cumulative log-decays, write
  * weights) that three launches share: prepare, state, reads. */
 size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width, int64_t features);
-int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset, int64_t feature_offset,
-                          int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset,
+int koemi_assoc_scan_read(const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset,
+                          int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset,
                           const float* surprise, const uint8_t* valid, const float* basis, const float* normalizer,
                           float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
                           int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
@@ -394,7 +395,8 @@ int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t 
  * width, features) bytes. */
 size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window, int64_t width,
                                                      int64_t features);
-int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
+int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype, int64_t row_stride,
+                                  int64_t value_offset,
                                   int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
                                   int64_t write_offset, const float* surprise, const uint8_t* valid,
                                   const float* basis, const float* normalizer, float* read, float* next_basis,
@@ -406,8 +408,9 @@ int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, 
  * koemi_herm_rmsnorm: out = RootMeanSquareNorm(x + residual) * weight
  * (layers.py:14-16) on rows whose mask byte is set (all rows when mask is
  * NULL), out = x elsewhere (the expert mixture's valid-row select,
- * experts.py:134-136); x, weight and out fp32 [rows, width], residual NULL or
- * [rows, width] in residual_dtype; width a multiple of 4, at most 2048;
+ * experts.py:134-136); x [rows, width] in input_dtype (KOEMI_F32 or
+ * KOEMI_BF16), weight and out fp32, residual NULL or [rows, width] in
+ * residual_dtype; width a multiple of 4, at most 2048;
  * `output_bf16` (NULL: none) receives a bf16 copy of out for a following
  * GEMM, and `output` may then be NULL.
  * koemi_herm_token_context: previous[b, t] = the last valid token before t
@@ -419,9 +422,9 @@ int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, 
  * koemi_herm_local_tail: the local ring after a window, the last `window`
  * entries of [carried (window entries) ; new (length entries)] with their
  * valid bytes (memory.py:385-403); fp32 keys and values [batch, *, width]. */
-int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
-                       const uint8_t* mask, float* output, void* output_bf16, int64_t rows, int64_t width, float eps,
-                       koemi_stream_t stream);
+int koemi_herm_rmsnorm(const void* input, int input_dtype, const void* residual, int residual_dtype,
+                       const float* weight, const uint8_t* mask, float* output, void* output_bf16, int64_t rows,
+                       int64_t width, float eps, koemi_stream_t stream);
 int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
                              int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out, int64_t pad_id,
                              int64_t batch, int64_t length, koemi_stream_t stream);
@@ -437,10 +440,11 @@ int koemi_herm_local_tail(const float* carried_keys, const float* carried_values
 /* The local keys and values of a window (network.py:337-340: the first two
  * width-column blocks of the stacked working-state projection, rows of
  * invalid positions zeroed, a torch.where each in the reference) as two
- * contiguous fp32 [rows, width] blocks in one kernel; width and row_stride
- * multiples of 4, 16-byte aligned pointers. */
-int koemi_herm_masked_pair(const float* source, int64_t row_stride, const uint8_t* valid, float* out0, float* out1,
-                           int64_t rows, int64_t width, koemi_stream_t stream);
+ * contiguous fp32 [rows, width] blocks in one kernel; the source in
+ * source_dtype (KOEMI_F32 or KOEMI_BF16); width and row_stride multiples of
+ * 4, 16-byte aligned pointers. */
+int koemi_herm_masked_pair(const void* source, int source_dtype, int64_t row_stride, const uint8_t* valid, float* out0,
+                           float* out1, int64_t rows, int64_t width, koemi_stream_t stream);
 int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2, const float* input3,
                            int pieces, int64_t rows, int64_t width, void* output, koemi_stream_t stream);
 

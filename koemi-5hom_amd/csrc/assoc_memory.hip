@@ -24,17 +24,18 @@
 //
 // Windows of one position (a decode step) take assoc_step_kernel: the read
 // from the carried state, then the state update (memory.py:91-95, 279-288),
-// one thread per (batch row, column). Longer windows take assoc_read_kernel,
-// one workgroup per (batch row, 64 output columns, 64 query rows): the
-// window's feature softmaxes, decays, cumulative log-decays and write weights
-// are formed while staging them in LDS (each workgroup of a row repeats this
-// small part); the three products of the window run on fp32 MFMA
-// (v_mfma_f32_32x32x2f32): the feature similarities of the causal influence
-// rows (K = features), the read itself (influence x values, K = slots, with
-// the carried basis term as a few more K values) and, in the workgroups of the
-// first row tile, the final basis columns (K = slots); the denominators and
-// the normalizer are wave reductions.
+// one thread per (batch row, column). Longer windows take three launches:
+// assoc_prep_kernel forms each row's feature softmaxes, decays, cumulative
+// log-decays and write weights once, into a workspace; assoc_delta_kernel the
+// window's own terms of the final state (fp32 MFMA, K = slots);
+// assoc_window_read_kernel the reads: the causal influence rows of 64 queries
+// (fp32 MFMA, K = features) in LDS, then influence x values plus the carried
+// basis term on MFMA, the denominators as wave reductions. The projection may
+// be fp32 or bf16 (the GEMM's own output dtype); everything after the load is
+// fp32.
 #include "common.hpp"
+
+#include <type_traits>
 
 namespace koemi {
 namespace {
@@ -105,9 +106,9 @@ inline AssocPrep prep_at(void* base, int64_t rows, int64_t L, int64_t M) {
 // (memory.py:108; wave 0: each lane sums its run of positions, an inclusive
 // wave scan of the run sums places it), then the prior and final-write
 // weights. Dynamic LDS: 3 L floats.
-template <int MAXM>
+template <int MAXM, typename PT>
 __global__ __launch_bounds__(256) void assoc_prep_kernel(
-    const float* __restrict__ proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
+    const PT* __restrict__ proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
     int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid, AssocPrep prep, int L,
     int M) {
     extern __shared__ float sh[];
@@ -116,16 +117,16 @@ __global__ __launch_bounds__(256) void assoc_prep_kernel(
     float* wt = sh + 2 * L;  // [L]
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-    const float* rows0 = proj + b * L * stride;
+    const PT* rows0 = proj + b * L * stride;
     for (int job = tid; job < 2 * L; job += 256) {
         const bool query = job >= L;
         const int t = query ? job - L : job;
-        const float* row = rows0 + t * stride;
+        const PT* row = rows0 + t * stride;
         const int64_t off = query ? fq_off : fk_off;
         float z[MAXM];
         float mx = -INFINITY;
 #pragma unroll
-        for (int m = 0; m < MAXM; ++m) z[m] = row[off + min(m, M - 1)];  // unconditional, then masked
+        for (int m = 0; m < MAXM; ++m) z[m] = to_f32(row[off + min(m, M - 1)]);  // unconditional, then masked
 #pragma unroll
         for (int m = 0; m < MAXM; ++m) {
             if (m >= M) z[m] = -INFINITY;
@@ -144,10 +145,10 @@ __global__ __launch_bounds__(256) void assoc_prep_kernel(
             *reinterpret_cast<float4*>(dst + m) = make_float4(z[m] * inv, z[m + 1] * inv, z[m + 2] * inv, z[m + 3] * inv);
         if (!query) {
             const bool ok = valid[b * L + t] != 0;
-            const float decay = kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]);
+            const float decay = kMinDecay + kDecaySpan * sigmoid_f(to_f32(row[decay_off]));
             const float sv = fminf(fmaxf(surprise[b * L + t], 0.0f), 1.0f);
             logd[t] = ok ? logf(decay) : 0.0f;
-            wt[t] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
+            wt[t] = ok ? sigmoid_f(to_f32(row[write_off])) * (0.25f + 0.75f * sv) : 0.0f;
         }
     }
     __syncthreads();
@@ -191,9 +192,9 @@ __global__ __launch_bounds__(256) void assoc_prep_kernel(
 // LDS), normalizer terms sum_s fwt_s kf_s[m] by a wave reduction. FINAL
 // writes the next state e^{c_{L-1}} state + terms (the fmaf the carry kernel
 // applies between windows); otherwise the terms. Grid (rows, ceil(D / 64)).
-template <int MAXM, bool FINAL>
+template <int MAXM, bool FINAL, typename PT>
 __global__ __launch_bounds__(256) void assoc_delta_kernel(
-    const float* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
+    const PT* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ next_basis,
     float* __restrict__ next_normalizer, int L, int64_t D, int M) {
     extern __shared__ float sh[];
@@ -212,14 +213,14 @@ __global__ __launch_bounds__(256) void assoc_delta_kernel(
     const int db = wave & 1, kh = wave >> 1;
     const int s_lo = kh * half, s_hi = min(L, s_lo + half);
     const int64_t dv = c0 + db * 32 + r32;
-    const float* vcol = proj + b * L * stride + value_off + (dv < D ? dv : D - 1);
+    const PT* vcol = proj + b * L * stride + value_off + (dv < D ? dv : D - 1);
     const float fon = r32 < MAXM ? 1.0f : 0.0f;
     const int mf = min(r32, MAXM - 1);
     f32x16 acc = {};
     for (int s = s_lo; s < s_hi; s += 8) {  // four steps' operands loaded together
         float x[4], a[4], bf[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) x[q] = vcol[min(s + 2 * q + h, L - 1) * stride];
+        for (int q = 0; q < 4; ++q) x[q] = to_f32(vcol[min(s + 2 * q + h, L - 1) * stride]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int sl = s + 2 * q + h, slc = min(sl, L - 1);
@@ -275,9 +276,9 @@ inline size_t read_lds(int64_t L, int64_t M) {
            sizeof(float);
 }
 
-template <int MAXM>
+template <int MAXM, typename PT>
 __global__ __launch_bounds__(256) void assoc_window_read_kernel(
-    const float* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
+    const PT* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out, int L, int64_t D,
     int M) {
     extern __shared__ float sh[];
@@ -341,23 +342,23 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     const int k_end = (s_cnt + 1) & ~1;
     const float* ia = infl + (tb * 32 + r32) * IP + h;
     const float ep = fast_exp(pr[tb * 32 + r32]);
-    const float* vrows = proj + b * L * stride + value_off;
+    const PT* vrows = proj + b * L * stride + value_off;
     for (int ct = 0; ct < kReadTiles; ++ct) {
         const int64_t d0 = (static_cast<int64_t>(blockIdx.y) * kReadTiles + ct) * 64 + db * 32;
         if (d0 >= D) break;
         const int64_t dq = min(d0 + r32, D - 1);
-        const float* vcol = vrows + dq;
+        const PT* vcol = vrows + dq;
         f32x16 acc = {};
         float bn[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) bn[u] = vcol[min(2 * u + h, L - 1) * stride];
+        for (int u = 0; u < 8; ++u) bn[u] = to_f32(vcol[min(2 * u + h, L - 1) * stride]);
         for (int s = 0; s < k_end; s += 16) {
             float bc[8], av[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) bc[u] = bn[u];
             if (s + 16 < k_end) {
 #pragma unroll
-                for (int u = 0; u < 8; ++u) bn[u] = vcol[min(s + 16 + 2 * u + h, L - 1) * stride];
+                for (int u = 0; u < 8; ++u) bn[u] = to_f32(vcol[min(s + 16 + 2 * u + h, L - 1) * stride]);
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) av[u] = s + 2 * u + h < k_end ? ia[s + 2 * u] : 0.0f;
@@ -411,34 +412,34 @@ __global__ __launch_bounds__(256) void assoc_carry_kernel(
 // The three launches of a window's (or every window's) memory: prepare, the
 // state terms (FINAL: the next state), the reads. Rows are batch rows (one
 // window) or (batch row, window) pairs.
-template <int MAXM>
-int launch_prep(const float* proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
+template <int MAXM, typename PT>
+int launch_prep(const PT* proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
                 int64_t write_off, const float* surprise, const uint8_t* valid, const AssocPrep& prep, int64_t rows,
                 int L, int M, hipStream_t s) {
-    hipLaunchKernelGGL(assoc_prep_kernel<MAXM>, dim3(static_cast<unsigned>(rows)), dim3(256),
+    hipLaunchKernelGGL((assoc_prep_kernel<MAXM, PT>), dim3(static_cast<unsigned>(rows)), dim3(256),
                        3 * static_cast<size_t>(L) * sizeof(float), s, proj, stride, fk_off, fq_off, decay_off,
                        write_off, surprise, valid, prep, L, M);
     return check_launch("associative memory (prepare)");
 }
 
-template <int MAXM, bool FINAL>
-int launch_delta(const float* proj, int64_t stride, int64_t value_off, const AssocPrep& prep, const float* basis,
+template <int MAXM, bool FINAL, typename PT>
+int launch_delta(const PT* proj, int64_t stride, int64_t value_off, const AssocPrep& prep, const float* basis,
                  const float* normalizer, float* nb, float* nn, int64_t rows, int L, int64_t D, int M,
                  hipStream_t s) {
     const size_t lds = (static_cast<size_t>(L) * (MAXM + 2) + 2 * 16 * kWave) * sizeof(float);
-    hipLaunchKernelGGL((assoc_delta_kernel<MAXM, FINAL>), dim3(static_cast<unsigned>(rows),
+    hipLaunchKernelGGL((assoc_delta_kernel<MAXM, FINAL, PT>), dim3(static_cast<unsigned>(rows),
                        static_cast<unsigned>((D + 63) / 64)), dim3(256), lds, s, proj, stride, value_off, prep, basis,
                        normalizer, nb, nn, L, D, M);
     return check_launch("associative memory (state terms)");
 }
 
-template <int MAXM>
-int launch_window_read(const float* proj, int64_t stride, int64_t value_off, const AssocPrep& prep,
+template <int MAXM, typename PT>
+int launch_window_read(const PT* proj, int64_t stride, int64_t value_off, const AssocPrep& prep,
                        const float* basis, const float* normalizer, float* out, int64_t rows, int L, int64_t D, int M,
                        hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((D + 64 * kReadTiles - 1) / (64 * kReadTiles)),
                     static_cast<unsigned>((L + kReadRows - 1) / kReadRows));
-    hipLaunchKernelGGL(assoc_window_read_kernel<MAXM>, grid, dim3(256), read_lds(L, M), s, proj, stride, value_off,
+    hipLaunchKernelGGL((assoc_window_read_kernel<MAXM, PT>), grid, dim3(256), read_lds(L, M), s, proj, stride, value_off,
                        prep, basis, normalizer, out, L, D, M);
     return check_launch("associative memory (reads)");
 }
@@ -450,22 +451,22 @@ inline size_t delta_lds(int64_t L, int64_t M) {
 // One-position window (a decode step): read from the carried state, then
 // basis' = decay basis + weight value features^T, normalizer' likewise.
 // One thread per (batch row, column); the row's softmaxes and gates in LDS.
-template <int MAXM>
+template <int MAXM, typename PT>
 __global__ __launch_bounds__(256) void assoc_step_kernel(
-    const float* __restrict__ proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
+    const PT* __restrict__ proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
     int64_t decay_off, int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out,
     float* __restrict__ next_basis, float* __restrict__ next_normalizer, int64_t D, int M) {
     __shared__ float f_sh[MAXM], q_sh[MAXM], gate[3];  // decay, weight, normalizer . query features
     const int64_t b = blockIdx.x;
     const int tid = threadIdx.x;
-    const float* row = proj + b * stride;
+    const PT* row = proj + b * stride;
     if (tid < kWave) {
         // lanes 0..31: the key's feature softmax, lanes 32..63: the query's
         // (one feature per lane; max and sum by shuffles within each half)
         const int lane = tid, m = lane & 31;
         const bool query = lane >= 32, in = m < M;
-        const float z = in ? row[(query ? fq_off : fk_off) + min(m, M - 1)] : -INFINITY;
+        const float z = in ? to_f32(row[(query ? fq_off : fk_off) + min(m, M - 1)]) : -INFINITY;
         float mx = z;
 #pragma unroll
         for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
@@ -483,8 +484,8 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
         if (lane == 0) {
             const bool ok = valid[b] != 0;
             const float sv = fminf(fmaxf(surprise[b], 0.0f), 1.0f);
-            gate[0] = ok ? kMinDecay + kDecaySpan * sigmoid_f(row[decay_off]) : 1.0f;
-            gate[1] = ok ? sigmoid_f(row[write_off]) * (0.25f + 0.75f * sv) : 0.0f;
+            gate[0] = ok ? kMinDecay + kDecaySpan * sigmoid_f(to_f32(row[decay_off])) : 1.0f;
+            gate[1] = ok ? sigmoid_f(to_f32(row[write_off])) * (0.25f + 0.75f * sv) : 0.0f;
         }
     }
     __syncthreads();
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
     if (d < D) {
         const float* br = basis + (b * D + d) * M;
         float* nbr = next_basis + (b * D + d) * M;
-        const float v = tanhf(row[value_off + d]);
+        const float v = tanhf(to_f32(row[value_off + d]));
         float num = 0.0f;
         if (M == MAXM && reinterpret_cast<uintptr_t>(br) % 16 == 0 && reinterpret_cast<uintptr_t>(nbr) % 16 == 0) {
             // the whole basis row at once: MAXM / 4 16-byte loads in flight, then the stores
@@ -568,8 +569,8 @@ int check_assoc_args(int64_t row_stride, int64_t value_offset, int64_t feature_o
 
 // prepare, state terms (FINAL: next state from the given one), reads from the
 // given (carried) state
-template <int MAXM, bool FINAL>
-int run_window_memory(const float* proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
+template <int MAXM, bool FINAL, typename PT>
+int run_window_memory(const PT* proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
                       int64_t decay_off, int64_t write_off, const float* surprise, const uint8_t* valid,
                       const AssocPrep& prep, const float* state_basis, const float* state_norm, float* nb, float* nn,
                       const float* read_basis, const float* read_norm, float* read, int64_t rows, int L, int64_t D,
@@ -581,6 +582,13 @@ int run_window_memory(const float* proj, int64_t stride, int64_t value_off, int6
     return launch_window_read<MAXM>(proj, stride, value_off, prep, read_basis, read_norm, read, rows, L, D, M, s);
 }
 
+// Calls f with the projections as the given dtype's pointer (fp32 or bf16).
+template <typename F>
+int with_projection(const void* projections, int dtype, F&& f) {
+    if (dtype == KOEMI_BF16) return f(static_cast<const bf16*>(projections));
+    return f(static_cast<const float*>(projections));
+}
+
 }  // namespace
 
 extern "C" size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width,
@@ -589,7 +597,7 @@ extern "C" size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t l
     return prep_bytes(batch, length, features);
 }
 
-extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_stride, int64_t value_offset,
+extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset,
                                      int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
                                      int64_t write_offset, const float* surprise, const uint8_t* valid,
                                      const float* basis, const float* normalizer, float* read, float* next_basis,
@@ -601,6 +609,8 @@ extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_strid
     int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
                               write_offset, width, features);
     if (st != KOEMI_OK) return st;
+    if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
     if (batch == 0 || length == 0) return KOEMI_OK;
     if (!window_fits(length, features))
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read window too long (%lld positions)",
@@ -613,29 +623,34 @@ extern "C" int koemi_assoc_scan_read(const float* projections, int64_t row_strid
     const int M = static_cast<int>(features);
     if (length == 1) {
         const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((width + 255) / 256));
-        auto step = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, projections, row_stride, value_offset, feature_offset,
-                               query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer,
-                               read, next_basis, next_normalizer, width, M);
-        };
-        if (M <= 16) step(assoc_step_kernel<16>);
-        else step(assoc_step_kernel<32>);
-        return check_launch("koemi_assoc_scan_read");
+        return with_projection(projections, projection_dtype, [&](auto proj) {
+            using PT = std::remove_const_t<std::remove_pointer_t<decltype(proj)>>;
+            auto step = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, proj, row_stride, value_offset, feature_offset,
+                                   query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer,
+                                   read, next_basis, next_normalizer, width, M);
+            };
+            if (M <= 16) step(assoc_step_kernel<16, PT>);
+            else step(assoc_step_kernel<32, PT>);
+            return check_launch("koemi_assoc_scan_read");
+        });
     }
     const size_t need = prep_bytes(batch, length, features);
     if (!workspace || workspace_bytes < need)
         return fail(KOEMI_ERR_INVALID, "associative read workspace too small: need %zu bytes", need);
     const AssocPrep prep = prep_at(workspace, batch, length, features);
     const int L = static_cast<int>(length);
-    if (M <= 16)
-        return run_window_memory<16, true>(projections, row_stride, value_offset, feature_offset, query_feature_offset,
+    return with_projection(projections, projection_dtype, [&](auto proj) {
+        if (M <= 16)
+            return run_window_memory<16, true>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
+                                               decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
+                                               next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M,
+                                               s, true);
+        return run_window_memory<32, true>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
                                            decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
                                            next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M, s,
                                            true);
-    return run_window_memory<32, true>(projections, row_stride, value_offset, feature_offset, query_feature_offset,
-                                       decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
-                                       next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M, s,
-                                       true);
+    });
 }
 
 extern "C" size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window,
@@ -644,7 +659,8 @@ extern "C" size_t koemi_assoc_scan_read_windows_workspace_bytes(int64_t batch, i
     return windows_workspace(batch * windows, window, width, features).total;
 }
 
-extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t row_stride, int64_t value_offset,
+extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype, int64_t row_stride,
+                                             int64_t value_offset,
                                              int64_t feature_offset, int64_t query_feature_offset,
                                              int64_t decay_offset, int64_t write_offset, const float* surprise,
                                              const uint8_t* valid, const float* basis, const float* normalizer,
@@ -657,6 +673,8 @@ extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t r
     int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
                               write_offset, width, features);
     if (st != KOEMI_OK) return st;
+    if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
     const int64_t rows = batch * windows;
     if (batch == 0) return KOEMI_OK;
     if (!window_fits(window, features))
@@ -681,14 +699,17 @@ extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t r
     const int L = static_cast<int>(window);
     if (windows > 0) {
         // 1. every window's prepared weights and own terms of the final state (from a zero state)
-        st = M <= 16 ? run_window_memory<16, false>(projections, row_stride, value_offset, feature_offset,
-                                                    query_feature_offset, decay_offset, write_offset, surprise, valid,
-                                                    prep, nullptr, nullptr, delta_basis, delta_norm, nullptr, nullptr,
-                                                    nullptr, rows, L, width, M, s, false)
-                     : run_window_memory<32, false>(projections, row_stride, value_offset, feature_offset,
+        st = with_projection(projections, projection_dtype, [&](auto proj) {
+            if (M <= 16)
+                return run_window_memory<16, false>(proj, row_stride, value_offset, feature_offset,
                                                     query_feature_offset, decay_offset, write_offset, surprise, valid,
                                                     prep, nullptr, nullptr, delta_basis, delta_norm, nullptr, nullptr,
                                                     nullptr, rows, L, width, M, s, false);
+            return run_window_memory<32, false>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
+                                                decay_offset, write_offset, surprise, valid, prep, nullptr, nullptr,
+                                                delta_basis, delta_norm, nullptr, nullptr, nullptr, rows, L, width, M,
+                                                s, false);
+        });
         if (st != KOEMI_OK) return st;
     }
     // 2. the state carried into each window, and the final state
@@ -699,9 +720,11 @@ extern "C" int koemi_assoc_scan_read_windows(const float* projections, int64_t r
     st = check_launch("koemi_assoc_scan_read_windows(carry)");
     if (st != KOEMI_OK || windows == 0) return st;
     // 3. the reads of every window from its carried state
-    if (M <= 16)
-        return launch_window_read<16>(projections, row_stride, value_offset, prep, carried_basis, carried_norm, read,
-                                      rows, L, width, M, s);
-    return launch_window_read<32>(projections, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows,
-                                  L, width, M, s);
+    return with_projection(projections, projection_dtype, [&](auto proj) {
+        if (M <= 16)
+            return launch_window_read<16>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows,
+                                          L, width, M, s);
+        return launch_window_read<32>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows, L,
+                                      width, M, s);
+    });
 }

@@ -20,22 +20,30 @@
 namespace koemi {
 namespace {
 
-template <typename R, int NV>
-__global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restrict__ x, const R* __restrict__ residual,
+// Four consecutive values as fp32 (one 16- or 8-byte load).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const bf16* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+
+template <typename X, typename R, int NV>
+__global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const X* __restrict__ x, const R* __restrict__ residual,
                                                            const float* __restrict__ w,
                                                            const uint8_t* __restrict__ mask, float* __restrict__ y,
                                                            bf16* __restrict__ y16, int64_t rows, int H, float eps) {
     const int lane = lane_id();
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
     if (row >= rows) return;
-    const float* xr = x + row * H;
+    const X* xr = x + row * H;
     float v[NV][4];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
         if (c < H) {
-            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            const float4 q = load4(xr + c);
             v[j][0] = q.x; v[j][1] = q.y; v[j][2] = q.z; v[j][3] = q.w;
             if (residual != nullptr) {
 #pragma unroll
@@ -61,7 +69,7 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const float* __restri
             const float4 wq = *reinterpret_cast<const float4*>(w + c);
             o = make_float4(v[j][0] * inv * wq.x, v[j][1] * inv * wq.y, v[j][2] * inv * wq.z, v[j][3] * inv * wq.w);
         } else {
-            o = *reinterpret_cast<const float4*>(xr + c);
+            o = load4(xr + c);
         }
         if (y != nullptr) *reinterpret_cast<float4*>(y + row * H + c) = o;
         if (y16 != nullptr) {
@@ -156,7 +164,8 @@ __global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float
 // out0 = the first `width` columns of each row, out1 the next `width`, rows
 // whose valid byte is 0 zeroed (the local keys and values of network.py:
 // 337-340 cut from the stacked projection); four columns per thread.
-__global__ __launch_bounds__(256) void herm_masked_pair_kernel(const float* __restrict__ src, int64_t stride,
+template <typename S>
+__global__ __launch_bounds__(256) void herm_masked_pair_kernel(const S* __restrict__ src, int64_t stride,
                                                                const uint8_t* __restrict__ valid,
                                                                float* __restrict__ out0, float* __restrict__ out1,
                                                                int64_t rows, int64_t width) {
@@ -167,7 +176,7 @@ __global__ __launch_bounds__(256) void herm_masked_pair_kernel(const float* __re
     const int64_t rest = i - row * 2 * quads;
     const int which = rest >= quads ? 1 : 0;
     const int64_t c = (rest - which * quads) * 4;
-    float4 v = *reinterpret_cast<const float4*>(src + row * stride + which * width + c);
+    float4 v = load4(src + row * stride + which * width + c);
     if (valid[row] == 0) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     *reinterpret_cast<float4*>((which ? out1 : out0) + row * width + c) = v;
 }
@@ -199,10 +208,12 @@ __global__ __launch_bounds__(256) void herm_concat_bf16_kernel(ConcatPieces in, 
 
 using namespace koemi;
 
-extern "C" int koemi_herm_rmsnorm(const float* input, const void* residual, int residual_dtype, const float* weight,
-                                  const uint8_t* mask, float* output, void* output_bf16, int64_t rows, int64_t width,
-                                  float eps, koemi_stream_t stream) {
+extern "C" int koemi_herm_rmsnorm(const void* input, int input_dtype, const void* residual, int residual_dtype,
+                                  const float* weight, const uint8_t* mask, float* output, void* output_bf16,
+                                  int64_t rows, int64_t width, float eps, koemi_stream_t stream) {
     if (rows < 0 || width < 1) return fail(KOEMI_ERR_INVALID, "herm rmsnorm needs rows >= 0 and a positive width");
+    if (input_dtype != KOEMI_F32 && input_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm input dtype %s", dtype_name(input_dtype));
     if (width % 4 != 0 || width > 4 * kWave * 8)
         return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm needs a width that is a multiple of 4 and at most 2048");
     if (residual != nullptr && residual_dtype != KOEMI_F32 && residual_dtype != KOEMI_BF16 && residual_dtype != KOEMI_F16)
@@ -213,20 +224,26 @@ extern "C" int koemi_herm_rmsnorm(const float* input, const void* residual, int 
     const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
     const hipStream_t s = as_stream(stream);
     const int H = static_cast<int>(width);
-    auto launch = [&](auto tag) {
+    auto launch = [&](auto xtag, auto tag) {
+        using X = decltype(xtag);
         using R = decltype(tag);
+        const X* x = static_cast<const X*>(input);
         const R* r = static_cast<const R*>(residual);
         bf16* o16 = static_cast<bf16*>(output_bf16);
         if (width <= 4 * kWave * 4)
-            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 4>), grid, dim3(256), 0, s, input, r, weight, mask, output, o16,
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<X, R, 4>), grid, dim3(256), 0, s, x, r, weight, mask, output, o16,
                                rows, H, eps);
         else
-            hipLaunchKernelGGL((herm_rmsnorm_kernel<R, 8>), grid, dim3(256), 0, s, input, r, weight, mask, output, o16,
+            hipLaunchKernelGGL((herm_rmsnorm_kernel<X, R, 8>), grid, dim3(256), 0, s, x, r, weight, mask, output, o16,
                                rows, H, eps);
     };
-    if (residual == nullptr || residual_dtype == KOEMI_F32) launch(float{});
-    else if (residual_dtype == KOEMI_BF16) launch(bf16{});
-    else launch(f16{});
+    auto with_input = [&](auto tag) {
+        if (input_dtype == KOEMI_BF16) launch(bf16{}, tag);
+        else launch(float{}, tag);
+    };
+    if (residual == nullptr || residual_dtype == KOEMI_F32) with_input(float{});
+    else if (residual_dtype == KOEMI_BF16) with_input(bf16{});
+    else with_input(f16{});
     return check_launch("koemi_herm_rmsnorm");
 }
 
@@ -282,8 +299,10 @@ extern "C" int koemi_herm_concat_bf16(const float* input0, const float* input1, 
     return check_launch("koemi_herm_concat_bf16");
 }
 
-extern "C" int koemi_herm_masked_pair(const float* source, int64_t row_stride, const uint8_t* valid, float* out0,
-                                      float* out1, int64_t rows, int64_t width, koemi_stream_t stream) {
+extern "C" int koemi_herm_masked_pair(const void* source, int source_dtype, int64_t row_stride, const uint8_t* valid,
+                                      float* out0, float* out1, int64_t rows, int64_t width, koemi_stream_t stream) {
+    if (source_dtype != KOEMI_F32 && source_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "masked pair source dtype %s", dtype_name(source_dtype));
     if (rows < 0 || width < 1 || row_stride < 2 * width)
         return fail(KOEMI_ERR_INVALID, "masked pair needs rows >= 0, a positive width and row_stride >= 2 width");
     if (width % 4 != 0 || row_stride % 4 != 0)
@@ -294,7 +313,13 @@ extern "C" int koemi_herm_masked_pair(const float* source, int64_t row_stride, c
         return fail(KOEMI_ERR_INVALID, "masked pair received a null or unaligned pointer");
     const int64_t threads = rows * 2 * (width / 4);
     if ((threads + 255) / 256 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "masked pair grid too large");
-    hipLaunchKernelGGL(herm_masked_pair_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                       as_stream(stream), source, row_stride, valid, out0, out1, rows, width);
+    if (source_dtype == KOEMI_BF16)
+        hipLaunchKernelGGL(herm_masked_pair_kernel<bf16>, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                           dim3(256), 0, as_stream(stream), static_cast<const bf16*>(source), row_stride, valid, out0,
+                           out1, rows, width);
+    else
+        hipLaunchKernelGGL(herm_masked_pair_kernel<float>, dim3(static_cast<unsigned>((threads + 255) / 256)),
+                           dim3(256), 0, as_stream(stream), static_cast<const float*>(source), row_stride, valid, out0,
+                           out1, rows, width);
     return check_launch("koemi_herm_masked_pair");
 }

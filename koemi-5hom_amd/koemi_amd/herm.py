@@ -178,14 +178,19 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         fq_b = f64("feature_w") @ f64("query_b") + f64("feature_b")
         weights = [p["local_key_w"], p["local_value_w"], p["value_w"], fk_w, fq_w, p["decay_w"], p["write_w"]]
         biases = [p["local_key_b"], p["local_value_b"], p["value_b"], fk_b, fq_b, p["decay_b"], p["write_b"]]
-        # rows padded to a multiple of 4 (zero weights and biases) so every row of
-        # the projection starts 16-byte aligned for the kernels that read it
+        # rows padded (zero weights and biases) to a multiple of 4, so every row
+        # of the projection starts 16-byte aligned for the kernels that read it,
+        # and for a bf16 GEMM to a multiple of 256, whole tiles of the library's
+        # 256-wide kernels (3108 -> 3328 columns at width 1024: a third less time)
         ws_w = torch.cat([w.double() for w in weights])
         ws_b = torch.cat([b.double() for b in biases])
-        pad = -ws_w.shape[0] % 4
+        pad = -ws_w.shape[0] % (256 if lin == torch.bfloat16 else 4)
         q["ws_w"] = to(torch.cat((ws_w, ws_w.new_zeros((pad, ws_w.shape[1])))), lin)
         q["ws_b"] = to(torch.cat((ws_b, ws_b.new_zeros(pad))))
         q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"])
+        if lin == torch.bfloat16:
+            # the bias of a GEMM with bf16 results (nn.Linear under bf16 autocast)
+            q["ws_b16"], q["fusion_b16"] = q["ws_b"].to(lin), q["fusion_b"].to(lin)
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
@@ -232,12 +237,13 @@ def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor
 
     x = x.contiguous()
     width = x.shape[-1]
-    out = torch.empty_like(x) if fp32 or low is None else None
+    out = torch.empty(x.shape, device=x.device, dtype=torch.float32) if fp32 or low is None else None
     out16 = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16) if low == torch.bfloat16 else None
     residual = residual.contiguous() if residual is not None else None
     mask = mask.contiguous() if mask is not None else None
     _native.call(
-        "koemi_herm_rmsnorm", _native.ptr(x), _native.ptr(residual) if residual is not None else None,
+        "koemi_herm_rmsnorm", _native.ptr(x), _native.dtype_code(x.dtype),
+        _native.ptr(residual) if residual is not None else None,
         _native.dtype_code(residual.dtype) if residual is not None else 0, _native.ptr(weight),
         _native.ptr(mask) if mask is not None else None, _native.ptr(out), _native.ptr(out16), x.numel() // width,
         width, _EPS, _native.stream_of(x.device),
@@ -249,18 +255,43 @@ def _rms(x: Tensor, weight: Tensor, residual: Tensor | None = None, mask: Tensor
     return out, out16
 
 
-def _linear(x: Tensor, weight: Tensor, bias: Tensor) -> Tensor:
-    """x W^T + b with fp32 results: one library GEMM (fp32 accumulation, the fp32
-    bias added in its epilogue) for half-precision weights; ``x`` may already
-    be in the weights' dtype (a copy its producer wrote)."""
+def _linear(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """x W^T (+ b) with fp32 results: for half-precision weights one library
+    GEMM with fp32 accumulation and results, then the fp32 bias added in place
+    (the library's fp32-output GEMM with a bias epilogue first copies the
+    broadcast bias into the output and reads it back); ``x`` may already be in
+    the weights' dtype (a copy its producer wrote). ``bias`` None: none (the
+    gate biases are added inside the scan)."""
 
     if weight.dtype == torch.float32:
         return functional.linear(x, weight, bias)
     if _few_rows(x, weight):
         return linear.linear_rows([x], weight, bias)
     flat = x.reshape(-1, x.shape[-1]).to(weight.dtype)
-    out = torch.addmm(bias, flat, weight.t(), out_dtype=torch.float32)
+    out = torch.mm(flat, weight.t(), out_dtype=torch.float32)
+    if bias is not None:
+        out += bias
     return out.view(*x.shape[:-1], weight.shape[0])
+
+
+def _linear_low(x: Tensor, weight: Tensor, bias_low: Tensor) -> Tensor:
+    """x W^T + b with bf16 results, the bias in the library GEMM's epilogue:
+    nn.Linear under bf16 autocast (the reference's default GPU precision).
+    Used for the working-state projection and the fusion layer of windows
+    (not decode steps), whose consumers read bf16."""
+
+    flat = x.reshape(-1, x.shape[-1])
+    return torch.addmm(bias_low, flat, weight.t()).view(*x.shape[:-1], weight.shape[0])
+
+
+def _projection(x: Tensor, p: dict[str, Tensor], name: str) -> Tensor:
+    """The ``name`` projection (``ws`` or ``fusion``) of x: bf16 results for a
+    bf16 stack outside decode steps, fp32 otherwise."""
+
+    w = p[name + "_w"]
+    if w.dtype == torch.bfloat16 and not _few_rows(x, w):
+        return _linear_low(x, w, p[name + "_b16"])
+    return _linear(x, w, p[name + "_b"]).contiguous()
 
 
 def _few_rows(x: Tensor, weight: Tensor) -> bool:
@@ -327,8 +358,9 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
 
     batch, length, stride = projections.shape
     d, m = width, features
-    if stride < 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
-        raise ValueError("projections must be contiguous fp32 [batch, length, >= 3 * width + 2 * features + 2]")
+    if (stride < 3 * d + 2 * m + 2 or projections.dtype not in (torch.float32, torch.bfloat16)
+            or not projections.is_contiguous()):
+        raise ValueError("projections must be contiguous fp32 or bf16 [batch, length, >= 3 * width + 2 * features + 2]")
     read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
@@ -337,7 +369,7 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read",
-        _native.ptr(projections), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
         *(_native.ptr(t) for t in args),
         _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
         batch, length, d, m, _native.ptr(workspace), need, _native.stream_of(projections.device),
@@ -364,7 +396,7 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
         _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4, batch * length, d,
                      _native.ptr(fusion_in), _native.stream_of(ids.device))
-    fused_pair = _rms(_linear(fusion_in, p["fusion_w"], p["fusion_b"]), p["fusion_norm"], low=low)
+    fused_pair = _rms(_projection(fusion_in, p, "fusion"), p["fusion_norm"], low=low)
     fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
     k = settings.top_k
@@ -415,19 +447,21 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
         u = _rms(source, p["input_norm"])
     else:
         u = _rms(source, p["input_norm"], fp32=False, low=low)[1]
-    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
-                                   with_bf16=low is not None)
+    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
+                                   with_bf16=low is not None, retention_bias=p["gates_b"][:d],
+                                   candidate_bias=p["gates_b"][d:])
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     # the state before each position: the carried one, then the window's own
     prior = state["working"].unsqueeze(1) if length == 1 else torch.cat((state["working"].unsqueeze(1), ws[:, :-1]),
                                                                         dim=1)
     surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
 
-    projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
+    projected = _projection(ws_low, p, "ws")
     # local keys and values: the first two column blocks, invalid rows zeroed (one kernel)
     local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
     local_values = torch.empty_like(local_keys)
-    _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
+    _native.call("koemi_herm_masked_pair", _native.ptr(projected), _native.dtype_code(projected.dtype),
+                 projected.shape[-1], _native.ptr(valid),
                  _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
     if length == 1:
         # a decode step: only the carried slots are eligible, both reads in one launch
@@ -510,8 +544,9 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
 
     batch, length, stride = projections.shape
     d, m = width, features
-    if stride < 3 * d + 2 * m + 2 or projections.dtype != torch.float32 or not projections.is_contiguous():
-        raise ValueError("projections must be contiguous fp32 [batch, length, >= 3 * width + 2 * features + 2]")
+    if (stride < 3 * d + 2 * m + 2 or projections.dtype not in (torch.float32, torch.bfloat16)
+            or not projections.is_contiguous()):
+        raise ValueError("projections must be contiguous fp32 or bf16 [batch, length, >= 3 * width + 2 * features + 2]")
     if length % window:
         raise ValueError("the sequence length must be a multiple of the window")
     windows = length // window
@@ -523,7 +558,7 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read_windows",
-        _native.ptr(projections), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
         *(_native.ptr(t) for t in args),
         _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
         batch, windows, window, d, m, _native.ptr(workspace), workspace.numel(), _native.stream_of(projections.device),
@@ -587,15 +622,17 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
     u = _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
-    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], p["gates_b"]), valid, state["working"], width=d,
-                                   with_bf16=low is not None)
+    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
+                                   with_bf16=low is not None, retention_bias=p["gates_b"][:d],
+                                   candidate_bias=p["gates_b"][d:])
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise = _surprise_after(p, ws, state["working"], targets, valid)
 
-    projected = _linear(ws_low, p["ws_w"], p["ws_b"]).contiguous()
+    projected = _projection(ws_low, p, "ws")
     local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
     local_values = torch.empty_like(local_keys)
-    _native.call("koemi_herm_masked_pair", _native.ptr(projected), projected.shape[-1], _native.ptr(valid),
+    _native.call("koemi_herm_masked_pair", _native.ptr(projected), _native.dtype_code(projected.dtype),
+                 projected.shape[-1], _native.ptr(valid),
                  _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
     cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
     local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],

@@ -172,7 +172,8 @@ def recurrent_scan(
 
 def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
                retention_offset: int = 0, candidate_offset: int | None = None,
-               with_bf16: bool = False, two_phase: bool = True) -> Tensor | tuple[Tensor, Tensor]:
+               with_bf16: bool = False, two_phase: bool = True, retention_bias: Tensor | None = None,
+               candidate_bias: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
     ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
@@ -183,7 +184,9 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     scan of network.py:310 from ``initial`` ``[B, width]`` run in one kernel
     (``koemi_gated_scan``). Returns ``[B, L, width]`` fp32, and with
     ``with_bf16`` also its bf16 copy (written by the same kernel) for a
-    following bf16 GEMM. With ``two_phase`` the kernel gets the workspace of
+    following bf16 GEMM. ``retention_bias`` and ``candidate_bias`` (fp32
+    ``[width]``, None: none) are added to the pre-activations inside the
+    kernel. With ``two_phase`` the kernel gets the workspace of
     its two-phase form, which it takes when the batch's columns alone would
     leave the chip short of workgroups (a few long rows); the result is the
     same to the bit either way.
@@ -204,6 +207,10 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     if valid_mask is not None and (valid_mask.dtype != torch.bool or valid_mask.shape != (batch, length)
                                    or valid_mask.device != preactivations.device):
         raise DenseCudaValidationError("valid_mask must be a bool [batch, length] tensor on the same device")
+    for bias in (retention_bias, candidate_bias):
+        if bias is not None and (not isinstance(bias, Tensor) or bias.shape != (width,) or bias.dtype != torch.float32
+                                 or bias.device != preactivations.device or not bias.is_contiguous()):
+            raise DenseCudaValidationError("gate biases must be contiguous float32 [width] tensors on the same device")
     try:
         _native.load_library()
     except _native.NativeLibraryUnavailableError as error:
@@ -217,7 +224,8 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
         workspace = torch.empty(need, device=z.device, dtype=torch.uint8) if need else None
         _native.call(
             "koemi_gated_scan",
-            _native.ptr(z), columns, retention_offset, candidate_offset, None, None,
+            _native.ptr(z), columns, retention_offset, candidate_offset, _native.ptr(retention_bias),
+            _native.ptr(candidate_bias),
             _native.ptr(mask) if mask is not None else None,
             _native.ptr(initial.contiguous()), _native.ptr(states), _native.ptr(states16),
             batch, length, width, _native.ptr(workspace), need, _native.stream_of(z.device),
