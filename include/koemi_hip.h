@@ -308,7 +308,7 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
  * valid) and h_t = a_t h_{t-1} + b_t from `initial` [batch, width] into
  * `states` [batch, length, width], as in network.py:306-310; with
  * `states_bf16` (NULL: none) also a bf16 copy of the states for the next
- * projection's GEMM. `workspace` (NULL: none, else at least
+ * projection's GEMM, rows bf16_row_stride elements apart (0: width). `workspace` (NULL: none, else at least
  * koemi_gated_scan_workspace_bytes) lets a batch of a few long rows run as a
  * two-phase scan: the transfers of every 8-step segment first, then chunks of
  * the sequence in parallel, each from its carry composed through the segments
@@ -316,8 +316,9 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
 size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
 int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                      int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
-                     const uint8_t* valid, const float* initial, float* states, void* states_bf16, int64_t batch,
-                     int64_t length, int64_t width, void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+                     const uint8_t* valid, const float* initial, float* states, void* states_bf16,
+                     int64_t bf16_row_stride, int64_t batch, int64_t length, int64_t width, void* workspace,
+                     size_t workspace_bytes, koemi_stream_t stream);
 
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections
  * in a decode step: the gate, working-state, fusion and head layers of
@@ -365,7 +366,9 @@ int koemi_salient_read(const void* carried_keys, const void* carried_values, con
  * feature logits W_f key + b_f and W_f query + b_f (features columns each)
  * and the decay and write logits (one column each); surprise fp32 and valid
  * bytes [batch * length]; basis fp32 [batch, width, features], normalizer
- * [batch, features]. Writes the reads [batch, length, width] and the window's
+ * [batch, features]. Writes the reads (read_dtype KOEMI_F32 or KOEMI_BF16,
+ * rows read_row_stride elements apart, 0: width; a one-position window only
+ * fp32 contiguous) and the window's
  * final basis and normalizer (fp32); next_basis and next_normalizer must not
  * alias basis and normalizer. features <= 32; the window length is bounded by
  * LDS (at most 480 positions with 16 features, 384 with 32). A window of one
@@ -377,9 +380,9 @@ size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t length, int6
 int koemi_assoc_scan_read(const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset,
                           int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset,
                           const float* surprise, const uint8_t* valid, const float* basis, const float* normalizer,
-                          float* read, float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
-                          int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
-                          koemi_stream_t stream);
+                          void* read, int read_dtype, int64_t read_row_stride, float* next_basis,
+                          float* next_normalizer, int64_t batch, int64_t length, int64_t width, int64_t features,
+                          void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
 /* koemi_assoc_scan_read over a whole sequence of `windows` windows of
  * `window` positions at once (forward_parallel, network.py:176-197, carrying
@@ -399,10 +402,10 @@ int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype,
                                   int64_t value_offset,
                                   int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
                                   int64_t write_offset, const float* surprise, const uint8_t* valid,
-                                  const float* basis, const float* normalizer, float* read, float* next_basis,
-                                  float* next_normalizer, int64_t batch, int64_t windows, int64_t window,
-                                  int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
-                                  koemi_stream_t stream);
+                                  const float* basis, const float* normalizer, void* read, int read_dtype,
+                                  int64_t read_row_stride, float* next_basis, float* next_normalizer, int64_t batch,
+                                  int64_t windows, int64_t window, int64_t width, int64_t features, void* workspace,
+                                  size_t workspace_bytes, koemi_stream_t stream);
 
 /* Small per-window steps of the HERM block (torch composites in the reference).
  * koemi_herm_rmsnorm: out = RootMeanSquareNorm(x + residual) * weight
@@ -460,6 +463,21 @@ int koemi_local_read(const void* carried_keys, const void* carried_values, const
                      const void* keys, const void* values, const uint8_t* valid, const void* queries, void* out,
                      int64_t batch, int64_t carried, int64_t length, int64_t width, int64_t window, int dtype,
                      void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
+/* The salient (window = 0) or local (window >= 1) read of koemi_salient_read /
+ * koemi_local_read, fp32 inputs, written as out_dtype (KOEMI_F32 or
+ * KOEMI_BF16) rows `out_row_stride` elements apart, so that the read can land
+ * in a column block of a wider matrix (the HERM fusion layer's bf16 input,
+ * network.py:401-405, without a separate concatenation). Only the one-launch
+ * fused read: width % 4 == 0, 16-byte aligned fp32 rows, at most 152
+ * candidate slots per 32 queries (salient: carried + length - 1 <= 152;
+ * local: carried <= 64 and window <= 33); other shapes return
+ * KOEMI_ERR_UNSUPPORTED (take koemi_salient_read / koemi_local_read). No
+ * workspace. */
+int koemi_memory_read_into(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
+                           const float* keys, const float* values, const uint8_t* flags, const float* queries,
+                           void* out, int out_dtype, int64_t out_row_stride, int64_t batch, int64_t carried,
+                           int64_t length, int64_t width, int64_t window, koemi_stream_t stream);
 
 /* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
  * without atomics: combined[t] = sum over the valid sorted pairs i of token t,

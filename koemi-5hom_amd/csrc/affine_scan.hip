@@ -167,7 +167,8 @@ struct GateInputs {
     const float* retention_bias;  // [F] or null
     const float* candidate_bias;  // [F] or null
     const uint8_t* valid;         // [B * L] or null
-    __bf16* h16;                  // [B, L, F] bf16 copy of the states, or null
+    __bf16* h16;                  // bf16 copy of the states, row (b, t) at (b L + t) h16_stride, or null
+    int64_t h16_stride;           // elements between rows of h16 (F when contiguous)
 };
 
 __device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
@@ -362,7 +363,7 @@ template <int S, int NSEG, int VEC, bool GATES = false, int LPC = 1>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
     int64_t L, int64_t F, int64_t col_tiles, int64_t stride,
-    GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr},
+    GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr, 0},
     const float* __restrict__ chunk_carry = nullptr, int64_t chunks = 0, int64_t span = 0) {
     using V = typename FloatVec<VEC>::type;
     constexpr int TW = kWave / LPC;    // lanes (column strips) per group
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
                 if (t < t_end) {
                     *reinterpret_cast<V*>(h_col + t * F) = FloatVec<VEC>::join(o);
                     if constexpr (GATES) {
-                        if (gates.h16 != nullptr) store_bf16<VEC>(gates.h16 + (bi * L + t) * F + f, o);
+                        if (gates.h16 != nullptr) store_bf16<VEC>(gates.h16 + (bi * L + t) * gates.h16_stride + f, o);
                     }
                 }
             }
@@ -631,7 +632,7 @@ __global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict
               gates.candidate_bias ? gates.candidate_bias[f] : 0.0f, keep, a, b);
     const float hv = a * h0[i] + b;
     h[i] = hv;
-    if (gates.h16 != nullptr) gates.h16[i] = static_cast<__bf16>(hv);
+    if (gates.h16 != nullptr) gates.h16[bi * gates.h16_stride + f] = static_cast<__bf16>(hv);
 }
 
 // Two-phase split of an S-step segmented walk over L positions into chunks of
@@ -716,9 +717,10 @@ int run_two_phase(const float* zr, const float* zc, int64_t stride, const GateIn
 // B * ceil(F / 64) fits the grid.
 int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
                       const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
+                      int64_t h16_stride,
                       int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace, size_t workspace_bytes) {
     constexpr int VEC = KOEMI_SCAN_VEC;
-    const GateInputs gates{retention_bias, candidate_bias, valid, static_cast<__bf16*>(h16)};
+    const GateInputs gates{retention_bias, candidate_bias, valid, static_cast<__bf16*>(h16), h16_stride};
     if (L == 1) {
         hipLaunchKernelGGL(gated_step_kernel, dim3(static_cast<unsigned>((B * F + 255) / 256)), dim3(256), 0, stream,
                            zr, zc, stride, gates, h0, h, B, F);
@@ -728,6 +730,7 @@ int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const fl
     const int64_t wide_tiles = (F / VEC + kWave - 1) / kWave;
     if (F % VEC == 0 && stride % VEC == 0 && aligned(zr) && aligned(zc) && aligned(h) && aligned(h0) &&
         aligned(retention_bias) && aligned(candidate_bias) && reinterpret_cast<uintptr_t>(h16) % (2 * VEC) == 0 &&
+        h16_stride % VEC == 0 &&
         B * wide_tiles >= 256) {
         hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
                            dim3(static_cast<unsigned>(B * wide_tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc,
@@ -743,7 +746,7 @@ int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const fl
     if (workspace != nullptr && workspace_bytes >= gated_scan_workspace(B, L, F) && B * tiles < kTwoPhaseBelow) {
         constexpr int TV = KOEMI_SCAN_TWO_PHASE_VEC;
         const bool tv_ok = F % TV == 0 && stride % TV == 0 && reinterpret_cast<uintptr_t>(workspace) % (4 * TV) == 0 &&
-                           reinterpret_cast<uintptr_t>(h16) % (2 * TV) == 0 &&
+                           reinterpret_cast<uintptr_t>(h16) % (2 * TV) == 0 && h16_stride % TV == 0 &&
                            [&] {
                                for (const void* p : {static_cast<const void*>(zr), static_cast<const void*>(zc),
                                                      static_cast<const void*>(h), static_cast<const void*>(h0),
@@ -838,8 +841,8 @@ extern "C" size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length
 extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
                                 int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
                                 const uint8_t* valid, const float* initial, float* states, void* states_bf16,
-                                int64_t batch, int64_t length, int64_t width, void* workspace, size_t workspace_bytes,
-                                koemi_stream_t stream) {
+                                int64_t bf16_row_stride, int64_t batch, int64_t length, int64_t width, void* workspace,
+                                size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1)
         return fail(KOEMI_ERR_INVALID, "gated scan needs non-negative batch and length and a positive width");
     if (retention_offset < 0 || candidate_offset < 0 || retention_offset + width > row_stride ||
@@ -849,10 +852,13 @@ extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride,
     if (!preactivations || !initial || !states) return fail(KOEMI_ERR_INVALID, "gated scan received a null pointer");
     if (batch * ((width + kWave - 1) / kWave) > 0x7fffffffLL || batch * width > 0x7fffffffLL * 256LL)
         return fail(KOEMI_ERR_UNSUPPORTED, "gated scan grid too large");
+    if (bf16_row_stride == 0) bf16_row_stride = width;
+    if (states_bf16 != nullptr && bf16_row_stride < width)
+        return fail(KOEMI_ERR_INVALID, "gated scan: the bf16 row stride is below the width");
     if (workspace != nullptr && workspace_bytes < gated_scan_workspace(batch, length, width))
         return fail(KOEMI_ERR_INVALID, "gated scan workspace too small: need %zu bytes",
                     gated_scan_workspace(batch, length, width));
     return launch_gated_scan(preactivations + retention_offset, preactivations + candidate_offset, row_stride,
-                             retention_bias, candidate_bias, valid, initial, states, states_bf16, batch, length,
-                             width, as_stream(stream), workspace, workspace_bytes);
+                             retention_bias, candidate_bias, valid, initial, states, states_bf16, bf16_row_stride,
+                             batch, length, width, as_stream(stream), workspace, workspace_bytes);
 }

@@ -276,11 +276,11 @@ inline size_t read_lds(int64_t L, int64_t M) {
            sizeof(float);
 }
 
-template <int MAXM, typename PT>
+template <int MAXM, typename PT, typename OutT, bool VEC4>
 __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     const PT* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
-    const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out, int L, int64_t D,
-    int M) {
+    const float* __restrict__ basis, const float* __restrict__ normalizer, OutT* __restrict__ out, int64_t ostride,
+    int L, int64_t D, int M) {
     extern __shared__ float sh[];
     constexpr int QP = MAXM + 1;
     const int Lq = (L + 31) & ~31;
@@ -338,11 +338,69 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     }
     __syncthreads();
 
-    const int tb = wave >> 1, db = wave & 1;
+    const int tb = wave >> 1;
     const int k_end = (s_cnt + 1) & ~1;
     const float* ia = infl + (tb * 32 + r32) * IP + h;
     const float ep = fast_exp(pr[tb * 32 + r32]);
     const PT* vrows = proj + b * L * stride + value_off;
+    if constexpr (VEC4) {
+        // wave (tb, half): 32 queries x 128 columns as four 32x32 MFMA tiles;
+        // lane (r, h) feeds column 4 r + c of tile c from one 4-column load of
+        // a value row (eight steps' loads in flight ahead of their use)
+        const int64_t d0 = static_cast<int64_t>(blockIdx.y) * (kReadTiles * 64) + (wave & 1) * 128;
+        if (d0 >= D) return;
+        const int64_t dcol = d0 + 4 * r32;
+        const bool cok = dcol < D;
+        const int64_t dq = cok ? dcol : 0;
+        const PT* vcol = vrows + dq;
+        f32x16 acc[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
+        float4 bn[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) bn[u] = load4(vcol + min(2 * u + h, L - 1) * stride);
+        for (int s = 0; s < k_end; s += 16) {
+            float4 bc[8];
+            float av[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bc[u] = bn[u];
+            if (s + 16 < k_end) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) bn[u] = load4(vcol + min(s + 16 + 2 * u + h, L - 1) * stride);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) av[u] = s + 2 * u + h < k_end ? ia[s + 2 * u] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                acc[0] = mfma2(av[u], fast_tanh(bc[u].x), acc[0]);
+                acc[1] = mfma2(av[u], fast_tanh(bc[u].y), acc[1]);
+                acc[2] = mfma2(av[u], fast_tanh(bc[u].z), acc[2]);
+                acc[3] = mfma2(av[u], fast_tanh(bc[u].w), acc[3]);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < MAXM / 2; ++kk) {
+            const int m = 2 * kk + h;
+            const float on = m < M ? 1.0f : 0.0f;
+            const float aq = ep * q_sh[(tb * 32 + r32) * QP + m];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                acc[c] = mfma2(aq, basis[(b * D + min(dq + c, D - 1)) * M + min(m, M - 1)] * on, acc[c]);
+        }
+        if (cok) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+                if (r >= rows) continue;
+                const float dn = den[r], reg = dn + kReadEpsilon;
+                const float g = dn / reg;
+                store4(out + (b * L + t0 + r) * ostride + dcol, g * acc[0][i] / reg, g * acc[1][i] / reg,
+                       g * acc[2][i] / reg, g * acc[3][i] / reg);
+            }
+        }
+        return;
+    }
+    const int db = wave & 1;
     for (int ct = 0; ct < kReadTiles; ++ct) {
         const int64_t d0 = (static_cast<int64_t>(blockIdx.y) * kReadTiles + ct) * 64 + db * 32;
         if (d0 >= D) break;
@@ -377,7 +435,7 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
             const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
             if (r >= rows || d >= D) continue;
             const float dn = den[r], reg = dn + kReadEpsilon;
-            out[(b * L + t0 + r) * D + d] = (dn / reg) * acc[i] / reg;
+            out[(b * L + t0 + r) * ostride + d] = from_f32<OutT>((dn / reg) * acc[i] / reg);
         }
     }
 }
@@ -435,12 +493,25 @@ int launch_delta(const PT* proj, int64_t stride, int64_t value_off, const AssocP
 
 template <int MAXM, typename PT>
 int launch_window_read(const PT* proj, int64_t stride, int64_t value_off, const AssocPrep& prep,
-                       const float* basis, const float* normalizer, float* out, int64_t rows, int L, int64_t D, int M,
-                       hipStream_t s) {
+                       const float* basis, const float* normalizer, void* out, int out_dtype, int64_t ostride,
+                       int64_t rows, int L, int64_t D, int M, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((D + 64 * kReadTiles - 1) / (64 * kReadTiles)),
                     static_cast<unsigned>((L + kReadRows - 1) / kReadRows));
-    hipLaunchKernelGGL((assoc_window_read_kernel<MAXM, PT>), grid, dim3(256), read_lds(L, M), s, proj, stride, value_off,
-                       prep, basis, normalizer, out, L, D, M);
+    // four columns per lane where every value row and output row starts at a
+    // multiple of four elements (aligned 4-element loads and stores)
+    const bool vec4 = D % 4 == 0 && stride % 4 == 0 && value_off % 4 == 0 && ostride % 4 == 0 &&
+                      reinterpret_cast<uintptr_t>(proj) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+    auto launch = [&](auto kernel, auto* o) {
+        hipLaunchKernelGGL(kernel, grid, dim3(256), read_lds(L, M), s, proj, stride, value_off, prep, basis,
+                           normalizer, o, ostride, L, D, M);
+    };
+    if (out_dtype == KOEMI_BF16) {
+        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, bf16, true>, static_cast<bf16*>(out));
+        else launch(assoc_window_read_kernel<MAXM, PT, bf16, false>, static_cast<bf16*>(out));
+    } else {
+        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, float, true>, static_cast<float*>(out));
+        else launch(assoc_window_read_kernel<MAXM, PT, float, false>, static_cast<float*>(out));
+    }
     return check_launch("associative memory (reads)");
 }
 
@@ -573,13 +644,14 @@ template <int MAXM, bool FINAL, typename PT>
 int run_window_memory(const PT* proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
                       int64_t decay_off, int64_t write_off, const float* surprise, const uint8_t* valid,
                       const AssocPrep& prep, const float* state_basis, const float* state_norm, float* nb, float* nn,
-                      const float* read_basis, const float* read_norm, float* read, int64_t rows, int L, int64_t D,
-                      int M, hipStream_t s, bool reads) {
+                      const float* read_basis, const float* read_norm, void* read, int read_dtype, int64_t ostride,
+                      int64_t rows, int L, int64_t D, int M, hipStream_t s, bool reads) {
     int st = launch_prep<MAXM>(proj, stride, fk_off, fq_off, decay_off, write_off, surprise, valid, prep, rows, L, M, s);
     if (st != KOEMI_OK) return st;
     st = launch_delta<MAXM, FINAL>(proj, stride, value_off, prep, state_basis, state_norm, nb, nn, rows, L, D, M, s);
     if (st != KOEMI_OK || !reads) return st;
-    return launch_window_read<MAXM>(proj, stride, value_off, prep, read_basis, read_norm, read, rows, L, D, M, s);
+    return launch_window_read<MAXM>(proj, stride, value_off, prep, read_basis, read_norm, read, read_dtype, ostride, rows,
+                                    L, D, M, s);
 }
 
 // Calls f with the projections as the given dtype's pointer (fp32 or bf16).
@@ -600,10 +672,10 @@ extern "C" size_t koemi_assoc_scan_read_workspace_bytes(int64_t batch, int64_t l
 extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset,
                                      int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
                                      int64_t write_offset, const float* surprise, const uint8_t* valid,
-                                     const float* basis, const float* normalizer, float* read, float* next_basis,
-                                     float* next_normalizer, int64_t batch, int64_t length, int64_t width,
-                                     int64_t features, void* workspace, size_t workspace_bytes,
-                                     koemi_stream_t stream) {
+                                     const float* basis, const float* normalizer, void* read, int read_dtype,
+                                     int64_t read_row_stride, float* next_basis, float* next_normalizer, int64_t batch,
+                                     int64_t length, int64_t width, int64_t features, void* workspace,
+                                     size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1 || features < 1)
         return fail(KOEMI_ERR_INVALID, "associative read needs non-negative batch and length, positive width and features");
     int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
@@ -611,6 +683,12 @@ extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dty
     if (st != KOEMI_OK) return st;
     if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
+    if (read_dtype != KOEMI_F32 && read_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative reads must be float32 or bfloat16");
+    if (read_row_stride == 0) read_row_stride = width;
+    if (read_row_stride < width) return fail(KOEMI_ERR_INVALID, "associative read row stride below the width");
+    if (length == 1 && (read_dtype != KOEMI_F32 || read_row_stride != width))
+        return fail(KOEMI_ERR_UNSUPPORTED, "a one-position associative read writes contiguous float32 reads");
     if (batch == 0 || length == 0) return KOEMI_OK;
     if (!window_fits(length, features))
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read window too long (%lld positions)",
@@ -628,7 +706,7 @@ extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dty
             auto step = [&](auto kernel) {
                 hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, proj, row_stride, value_offset, feature_offset,
                                    query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer,
-                                   read, next_basis, next_normalizer, width, M);
+                                   static_cast<float*>(read), next_basis, next_normalizer, width, M);
             };
             if (M <= 16) step(assoc_step_kernel<16, PT>);
             else step(assoc_step_kernel<32, PT>);
@@ -644,12 +722,12 @@ extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dty
         if (M <= 16)
             return run_window_memory<16, true>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
                                                decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
-                                               next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M,
-                                               s, true);
+                                               next_basis, next_normalizer, basis, normalizer, read, read_dtype,
+                                               read_row_stride, batch, L, width, M, s, true);
         return run_window_memory<32, true>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
                                            decay_offset, write_offset, surprise, valid, prep, basis, normalizer,
-                                           next_basis, next_normalizer, basis, normalizer, read, batch, L, width, M, s,
-                                           true);
+                                           next_basis, next_normalizer, basis, normalizer, read, read_dtype,
+                                           read_row_stride, batch, L, width, M, s, true);
     });
 }
 
@@ -664,9 +742,10 @@ extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projec
                                              int64_t feature_offset, int64_t query_feature_offset,
                                              int64_t decay_offset, int64_t write_offset, const float* surprise,
                                              const uint8_t* valid, const float* basis, const float* normalizer,
-                                             float* read, float* next_basis, float* next_normalizer, int64_t batch,
-                                             int64_t windows, int64_t window, int64_t width, int64_t features,
-                                             void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+                                             void* read, int read_dtype, int64_t read_row_stride, float* next_basis,
+                                             float* next_normalizer, int64_t batch, int64_t windows, int64_t window,
+                                             int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
+                                             koemi_stream_t stream) {
     if (batch < 0 || windows < 0 || window < 2 || width < 1 || features < 1)
         return fail(KOEMI_ERR_INVALID, "windowed associative read needs non-negative batch and windows, a window of at "
                     "least two positions, positive width and features");
@@ -675,6 +754,10 @@ extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projec
     if (st != KOEMI_OK) return st;
     if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
         return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
+    if (read_dtype != KOEMI_F32 && read_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative reads must be float32 or bfloat16");
+    if (read_row_stride == 0) read_row_stride = width;
+    if (read_row_stride < width) return fail(KOEMI_ERR_INVALID, "associative read row stride below the width");
     const int64_t rows = batch * windows;
     if (batch == 0) return KOEMI_OK;
     if (!window_fits(window, features))
@@ -704,11 +787,11 @@ extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projec
                 return run_window_memory<16, false>(proj, row_stride, value_offset, feature_offset,
                                                     query_feature_offset, decay_offset, write_offset, surprise, valid,
                                                     prep, nullptr, nullptr, delta_basis, delta_norm, nullptr, nullptr,
-                                                    nullptr, rows, L, width, M, s, false);
+                                                    nullptr, KOEMI_F32, width, rows, L, width, M, s, false);
             return run_window_memory<32, false>(proj, row_stride, value_offset, feature_offset, query_feature_offset,
                                                 decay_offset, write_offset, surprise, valid, prep, nullptr, nullptr,
-                                                delta_basis, delta_norm, nullptr, nullptr, nullptr, rows, L, width, M,
-                                                s, false);
+                                                delta_basis, delta_norm, nullptr, nullptr, nullptr, KOEMI_F32, width,
+                                                rows, L, width, M, s, false);
         });
         if (st != KOEMI_OK) return st;
     }
@@ -722,9 +805,9 @@ extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projec
     // 3. the reads of every window from its carried state
     return with_projection(projections, projection_dtype, [&](auto proj) {
         if (M <= 16)
-            return launch_window_read<16>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows,
-                                          L, width, M, s);
-        return launch_window_read<32>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read, rows, L,
-                                      width, M, s);
+            return launch_window_read<16>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read,
+                                          read_dtype, read_row_stride, rows, L, width, M, s);
+        return launch_window_read<32>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read,
+                                      read_dtype, read_row_stride, rows, L, width, M, s);
     });
 }

@@ -129,6 +129,25 @@ __device__ __forceinline__ float gate_tanh(float x) {
 constexpr float kGateMinRetention = 0.00390625f;        // 2^-8
 constexpr float kGateRetentionSpan = 1.0f - 0.0078125f;  // (1 - 2^-8) - 2^-8 = 1 - 2^-7
 
+// Four consecutive values as fp32 (one 16-byte fp32 or 8-byte bf16 load).
+__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 load4(const bf16* p) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                       __uint_as_float(u.y & 0xffff0000u));
+}
+// Four consecutive outputs (one 16-byte fp32 or 8-byte bf16 store).
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+    const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<bf16>(a)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<bf16>(b))) << 16);
+    const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<bf16>(c)) |
+                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<bf16>(d))) << 16);
+    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
+}
+
 inline unsigned grid_for(int64_t items, int64_t per_block) {
     int64_t b = (items + per_block - 1) / per_block;
     if (b < 1) b = 1;

@@ -29,7 +29,7 @@ extern std::mutex g_blas_mutex;
 // The fused gates + scan kernel (affine_scan.hip).
 int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
                       const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
-                      int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace,
+                      int64_t h16_stride, int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace,
                       size_t workspace_bytes);
 
 namespace {
@@ -176,6 +176,6 @@ extern "C" int koemi_recurrent_scan(const float* input, const float* retention_w
     const hipStream_t s = as_stream(stream);
     int st = gate_products(input, retention_weight, candidate_weight, zr, zc, rows, width, KOEMI_F32, s);
     if (st != KOEMI_OK) return st;
-    return launch_gated_scan(zr, zc, width, retention_bias, candidate_bias, valid, initial, states, nullptr, batch,
-                             length, width, s, nullptr, 0);
+    return launch_gated_scan(zr, zc, width, retention_bias, candidate_bias, valid, initial, states, nullptr, width,
+                             batch, length, width, s, nullptr, 0);
 }

@@ -20,14 +20,6 @@
 namespace koemi {
 namespace {
 
-// Four consecutive values as fp32 (one 16- or 8-byte load).
-__device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-__device__ __forceinline__ float4 load4(const bf16* p) {
-    const uint2 u = *reinterpret_cast<const uint2*>(p);
-    return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
-                       __uint_as_float(u.y & 0xffff0000u));
-}
-
 template <typename X, typename R, int NV>
 __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const X* __restrict__ x, const R* __restrict__ residual,
                                                            const float* __restrict__ w,

@@ -606,18 +606,6 @@ __device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
-// Four consecutive output columns of one row (16-byte fp32 or 8-byte bf16 store).
-__device__ inline void store4(float* p, float a, float b, float c, float d) {
-    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
-}
-__device__ inline void store4(__bf16* p, float a, float b, float c, float d) {
-    const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(a)) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
-    const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<__bf16>(c)) |
-                        (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(d))) << 16);
-    *reinterpret_cast<uint2*>(p) = make_uint2(lo, hi);
-}
-
 // out rows are `ostride` elements apart (the reads can land in a column
 // block of a wider matrix, e.g. the fusion input in bf16).
 template <bool LOCAL, int MAXS, typename OutT>
@@ -1059,6 +1047,35 @@ extern "C" int koemi_local_read(const void* carried_keys, const void* carried_va
     if (window < 1) return fail(KOEMI_ERR_INVALID, "local read needs a positive window");
     return memory_read(carried_keys, carried_values, carried_valid, keys, values, valid, queries, out, batch, carried,
                        length, width, window, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int koemi_memory_read_into(const float* carried_keys, const float* carried_values,
+                                      const uint8_t* carried_valid, const float* keys, const float* values,
+                                      const uint8_t* flags, const float* queries, void* out, int out_dtype,
+                                      int64_t out_row_stride, int64_t batch, int64_t carried, int64_t length,
+                                      int64_t width, int64_t window, koemi_stream_t stream) {
+    if (batch < 0 || carried < 0 || length < 0 || width < 1 || window < 0)
+        return fail(KOEMI_ERR_INVALID, "memory read needs non-negative batch, carried, length and window, positive width");
+    if (out_dtype != KOEMI_F32 && out_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "memory read output must be float32 or bfloat16");
+    if (out_row_stride < width || out_row_stride % 4 != 0)
+        return fail(KOEMI_ERR_INVALID, "memory read output row stride must be a multiple of 4, at least the width");
+    if (batch == 0 || length == 0) return KOEMI_OK;
+    auto aligned16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    if (width % 4 != 0 || !window_read_fits(carried, length, window) || batch > 0x7fffffffLL ||
+        (length + kWinQ - 1) / kWinQ > 65535 || !aligned16(carried_keys) || !aligned16(carried_values) ||
+        !aligned16(keys) || !aligned16(values) || !aligned16(queries) || reinterpret_cast<uintptr_t>(out) % 8 != 0)
+        return fail(KOEMI_ERR_UNSUPPORTED, "memory read into a strided output: shape outside the fused read");
+    if (!keys || !values || !flags || !queries || !out || (carried > 0 && (!carried_keys || !carried_values ||
+                                                                          !carried_valid)))
+        return fail(KOEMI_ERR_INVALID, "memory read received a null pointer");
+    if (out_dtype == KOEMI_BF16)
+        return launch_window_read(carried_keys, carried_values, carried_valid, keys, values, flags, queries,
+                                  static_cast<bf16*>(out), out_row_stride, batch, carried, length, width, window,
+                                  as_stream(stream));
+    return launch_window_read(carried_keys, carried_values, carried_valid, keys, values, flags, queries,
+                              static_cast<float*>(out), out_row_stride, batch, carried, length, width, window,
+                              as_stream(stream));
 }
 
 extern "C" int koemi_read_step_pair(const float* local_keys, const float* local_values, const uint8_t* local_valid,

@@ -100,7 +100,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_gated_scan_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_gated_scan": (
         c_int,
-        (_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
     "koemi_linear_rows": (
         c_int,
@@ -114,14 +114,18 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_assoc_scan_read_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64)),
     "koemi_assoc_scan_read": (
         c_int,
-        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64,
-         c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P,
+         c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
     "koemi_assoc_scan_read_windows_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64, c_int64)),
     "koemi_assoc_scan_read_windows": (
         c_int,
-        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, _P, c_int64,
-         c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P,
+         c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
+    "koemi_memory_read_into": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P),
     ),
     "koemi_herm_rmsnorm": (c_int, (_P, c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_float, _P)),
     "koemi_herm_concat_bf16": (c_int, (_P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P)),

@@ -274,6 +274,24 @@ def _linear(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     return out.view(*x.shape[:-1], weight.shape[0])
 
 
+def _fusion_input(settings: HermSettings, batch: int, length: int, device: torch.device) -> Tensor | None:
+    """The fusion layer's bf16 input [working ; memory ; local ; salient]
+    (network.py:401-405) of a bf16 window of more than one position, written
+    column block by column block by the scan's bf16 copy, the associative
+    read and the two memory reads (no separate concatenation); None for fp32
+    stacks and decode steps (their pieces are concatenated)."""
+
+    if settings.linear_dtype != torch.bfloat16 or length == 1:
+        return None
+    return torch.empty((batch, length, 4 * settings.width), device=device, dtype=torch.bfloat16)
+
+
+def _block(fusion_in: Tensor | None, index: int, width: int) -> Tensor | None:
+    """Column block ``index`` (width columns) of the fusion input, or None."""
+
+    return None if fusion_in is None else fusion_in[..., index * width:(index + 1) * width]
+
+
 def _linear_low(x: Tensor, weight: Tensor, bias_low: Tensor) -> Tensor:
     """x W^T + b with bf16 results, the bias in the library GEMM's epilogue:
     nn.Linear under bf16 autocast (the reference's default GPU precision).
@@ -341,7 +359,7 @@ def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: T
 
 
 def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor, normalizer: Tensor,
-                          *, width: int, features: int) -> tuple[Tensor, Tensor, Tensor]:
+                          *, width: int, features: int, out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """The associative memory of one window on ``koemi_assoc_scan_read``:
     projection tail, fast write terms with the write masking and
     scan_and_read (memory.py:82-144, 244-255; network.py:734-740).
@@ -353,7 +371,8 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     logits; columns past those (row padding) are not read.
     ``surprise`` ``[B, L]`` fp32, ``valid`` ``[B, L]`` bool, ``basis``
     ``[B, D, M]``, ``normalizer`` ``[B, M]`` fp32. Returns (reads ``[B, L, D]``,
-    next basis, next normalizer).
+    next basis, next normalizer); with ``out`` (an fp32 or bf16 ``[B, L, D]``
+    view with evenly spaced rows, L > 1) the reads are written there.
     """
 
     batch, length, stride = projections.shape
@@ -361,7 +380,8 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     if (stride < 3 * d + 2 * m + 2 or projections.dtype not in (torch.float32, torch.bfloat16)
             or not projections.is_contiguous()):
         raise ValueError("projections must be contiguous fp32 or bf16 [batch, length, >= 3 * width + 2 * features + 2]")
-    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
+    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32) if out is None else out
+    read_stride = memory._row_stride(read, (batch, length, d))
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
     need = _native.query("koemi_assoc_scan_read_workspace_bytes", batch, length, d, m)
@@ -369,28 +389,35 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read",
-        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m,
+        3 * d + 2 * m, 3 * d + 2 * m + 1,
         *(_native.ptr(t) for t in args),
-        _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
+        _native.ptr(read), _native.dtype_code(read.dtype), read_stride, _native.ptr(next_basis),
+        _native.ptr(next_normalizer),
         batch, length, d, m, _native.ptr(workspace), need, _native.stream_of(projections.device),
     )
     return read, next_basis, next_normalizer
 
 
 def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, previous: Tensor, valid: Tensor,
-                      pieces: tuple[Tensor, Tensor, Tensor, Tensor], with_logits: bool) -> tuple[Tensor, Tensor | None]:
+                      pieces: tuple[Tensor, Tensor, Tensor, Tensor] | Tensor, with_logits: bool
+                      ) -> tuple[Tensor, Tensor | None]:
     """The block's position-wise tail: fusion of [working ; memory ; local ;
     salient] with its normalizer (network.py:723-732), the expert mixture with
     its output normalizer (experts.py:109-150 or router.py:43-97) and the token
     head (network.py:700-701). Every position independent of the others, so
-    the rows may span any number of windows. Returns (final context
-    [B, L, D] fp32, logits or None)."""
+    the rows may span any number of windows. ``pieces`` are the four fp32
+    inputs, or the bf16 fusion input their producers already wrote
+    ([B, L, 4 D], see ``_fusion_input``). Returns (final context [B, L, D]
+    fp32, logits or None)."""
 
     batch, length = ids.shape
     d = settings.width
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
-    if low is None:
+    if isinstance(pieces, Tensor):
+        fusion_in = pieces
+    elif low is None:
         fusion_in = torch.cat(pieces, dim=-1)
     else:
         fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
@@ -447,9 +474,10 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
         u = _rms(source, p["input_norm"])
     else:
         u = _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    fusion_in = _fusion_input(settings, batch, length, ids.device)
     scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
                                    with_bf16=low is not None, retention_bias=p["gates_b"][:d],
-                                   candidate_bias=p["gates_b"][d:])
+                                   candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     # the state before each position: the carried one, then the window's own
     prior = state["working"].unsqueeze(1) if length == 1 else torch.cat((state["working"].unsqueeze(1), ws[:, :-1]),
@@ -474,17 +502,20 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                      _native.ptr(local_value), _native.ptr(salient_value), batch, d, _native.stream_of(ids.device))
     else:
         local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
-                                               local_keys, local_values, valid, ws, window=settings.local_memory_size)
+                                               local_keys, local_values, valid, ws, window=settings.local_memory_size,
+                                               out=_block(fusion_in, 2, d))
 
     fast, basis, normalizer = associative_scan_read(projected, surprise, valid, state["basis"], state["normalizer"],
-                                                    width=d, features=settings.memory_features)
+                                                    width=d, features=settings.memory_features,
+                                                    out=_block(fusion_in, 1, d))
 
     admission = think.admission_above(surprise, valid, settings.salience_threshold)
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
-                                                   state["salient_valid"], local_keys, local_values, admission, ws)
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, (ws, fast, local_value, salient_value),
-                                      with_logits)
+                                                   state["salient_valid"], local_keys, local_values, admission, ws,
+                                                   out=_block(fusion_in, 3, d))
+    pieces = fusion_in if fusion_in is not None else (ws, fast, local_value, salient_value)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits)
 
     local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
     salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
@@ -534,8 +565,8 @@ def window_rings(carried_keys: Tensor, carried_values: Tensor, carried_flags: Te
 
 
 def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor,
-                                  normalizer: Tensor, *, width: int, features: int, window: int
-                                  ) -> tuple[Tensor, Tensor, Tensor]:
+                                  normalizer: Tensor, *, width: int, features: int, window: int,
+                                  out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """``associative_scan_read`` over every window of a sequence at once
     (``koemi_assoc_scan_read_windows``): the same inputs with length = a
     multiple of ``window``; each window reads from the state the previous
@@ -550,7 +581,8 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     if length % window:
         raise ValueError("the sequence length must be a multiple of the window")
     windows = length // window
-    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
+    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32) if out is None else out
+    read_stride = memory._row_stride(read, (batch, length, d))
     next_basis = torch.empty_like(basis)
     next_normalizer = torch.empty_like(normalizer)
     workspace = torch.empty((_native.query("koemi_assoc_scan_read_windows_workspace_bytes", batch, windows, window, d,
@@ -558,9 +590,11 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
     _native.call(
         "koemi_assoc_scan_read_windows",
-        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+        _native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m,
+        3 * d + 2 * m, 3 * d + 2 * m + 1,
         *(_native.ptr(t) for t in args),
-        _native.ptr(read), _native.ptr(next_basis), _native.ptr(next_normalizer),
+        _native.ptr(read), _native.dtype_code(read.dtype), read_stride, _native.ptr(next_basis),
+        _native.ptr(next_normalizer),
         batch, windows, window, d, m, _native.ptr(workspace), workspace.numel(), _native.stream_of(projections.device),
     )
     return read, next_basis, next_normalizer
@@ -622,9 +656,10 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
     u = _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    fusion_in = _fusion_input(settings, batch, length, ids.device)
     scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
                                    with_bf16=low is not None, retention_bias=p["gates_b"][:d],
-                                   candidate_bias=p["gates_b"][d:])
+                                   candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise = _surprise_after(p, ws, state["working"], targets, valid)
 
@@ -637,21 +672,27 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
     local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],
                                             local_keys, local_values, valid, window=chunk, capacity=cap_l, tail=True)
-    per_window = lambda t: t.view(rows, chunk, *t.shape[2:])
+    per_window = lambda t: None if t is None else t.view(rows, chunk, *t.shape[2:])
     local_value = memory.read_local_window(*local_rings, per_window(local_keys), per_window(local_values),
-                                           per_window(valid), per_window(ws), window=cap_l).view(batch, length, d)
+                                           per_window(valid), per_window(ws), window=cap_l,
+                                           out=per_window(_block(fusion_in, 2, d)))
 
     fast, basis, normalizer = associative_scan_read_windows(projected, surprise, valid, state["basis"],
                                                             state["normalizer"], width=d,
-                                                            features=settings.memory_features, window=chunk)
+                                                            features=settings.memory_features, window=chunk,
+                                                            out=_block(fusion_in, 1, d))
     admission = think.admission_above(surprise, valid, settings.salience_threshold)
     salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                 local_keys, local_values, admission, window=chunk, capacity=cap_s,
                                                 tail=False)
     salient_value = memory.read_salient_window(*salient_rings, per_window(local_keys), per_window(local_values),
-                                               per_window(admission), per_window(ws)).view(batch, length, d)
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, (ws, fast, local_value, salient_value),
-                                      with_logits)
+                                               per_window(admission), per_window(ws),
+                                               out=per_window(_block(fusion_in, 3, d)))
+    if fusion_in is not None:
+        pieces = fusion_in
+    else:
+        pieces = (ws, fast, local_value.view(batch, length, d), salient_value.view(batch, length, d))
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits)
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,

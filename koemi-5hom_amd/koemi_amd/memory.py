@@ -33,6 +33,8 @@ def read_salient_window(
     values: Tensor,
     admission_mask: Tensor,
     queries: Tensor,
+    *,
+    out: Tensor | None = None,
 ) -> Tensor:
     """Salient read of one window (reference model/memory.py:405-429).
 
@@ -41,12 +43,16 @@ def read_salient_window(
     ``queries`` ``[B, L, D]``. Query t attends, with scores ``key . query /
     sqrt(D)``, to the valid carried entries and to the admitted window entries
     at positions before t; rows with no such entry read zeros. Returns
-    ``[B, L, D]`` in the queries' dtype (fp32 accumulation).
+    ``[B, L, D]`` in the queries' dtype (fp32 accumulation). With ``out`` (a
+    float32 or bfloat16 ``[B, L, D]`` view with contiguous columns and evenly
+    spaced rows, e.g. a column block of a wider matrix) the read is written
+    there, by one kernel where ``koemi_memory_read_into`` takes the shape, and
+    ``out`` is returned.
     """
 
     return _masked_read(
         "read_salient_window", "admission_mask", carried_keys, carried_values, carried_valid, keys, values,
-        admission_mask, queries, 0,
+        admission_mask, queries, 0, out,
     )
 
 
@@ -60,6 +66,7 @@ def read_local_window(
     queries: Tensor,
     *,
     window: int,
+    out: Tensor | None = None,
 ) -> Tensor:
     """Local-memory read of one window: the value output of
     ``LocalKeyValueMemory.read_window`` (reference model/memory.py:332-362).
@@ -70,14 +77,37 @@ def read_local_window(
     ``[carried ; window entries]`` (``sliding_window_mask``, memory.py:364-383).
     The novelty output of the reference method is not computed (the refine
     path that reads it is off under the default ``no_refine`` ablation).
+    ``out`` as for ``read_salient_window``.
     """
 
     if isinstance(window, bool) or not isinstance(window, int) or window < 1:
         raise CudaThinkValidationError("window must be a positive integer")
     return _masked_read(
         "read_local_window", "valid_mask", carried_keys, carried_values, carried_valid, keys, values, valid_mask,
-        queries, window,
+        queries, window, out,
     )
+
+
+def _row_stride(out: Tensor, shape: tuple[int, int, int]) -> int:
+    """Row stride of an output view [batch, length, width] whose rows are
+    evenly spaced with contiguous columns (a column block of a wider matrix)."""
+
+    if not isinstance(out, Tensor) or tuple(out.shape) != shape or out.dtype not in (torch.float32, torch.bfloat16):
+        raise CudaThinkValidationError(f"out must be a float32 or bfloat16 tensor of shape {list(shape)}")
+    if out.stride(2) != 1 or out.stride(0) != shape[1] * out.stride(1) or out.stride(1) % 4:
+        raise CudaThinkValidationError("out must have contiguous columns and evenly spaced rows (stride % 4 == 0)")
+    return out.stride(1)
+
+
+def _fused_read_fits(carried: int, length: int, width: int, window: int) -> bool:
+    """Shapes koemi_memory_read_into takes (the one-launch fused read): at
+    most 152 candidate slots per 32 queries (local: 64)."""
+
+    if width % 4:
+        return False
+    if window > 0:
+        return carried <= 64 and window + 31 <= 64
+    return carried <= 152 and carried + length - 1 <= 152
 
 
 def _masked_read(
@@ -91,6 +121,7 @@ def _masked_read(
     mask: Tensor,
     queries: Tensor,
     window: int,
+    out: Tensor | None = None,
 ) -> Tensor:
     tensors = {
         "carried_keys": carried_keys,
@@ -132,6 +163,20 @@ def _masked_read(
         raise CudaThinkUnavailableError(str(error)) from error
 
     device = queries.device
+    if out is not None:
+        stride = _row_stride(out, (batch, length, width))
+        if batch == 0 or length == 0:
+            return out
+        if queries.dtype == torch.float32 and _fused_read_fits(carried, length, width, window):
+            contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, mask,
+                                                   queries)]
+            _native.call("koemi_memory_read_into", *[_native.ptr(t) if t.numel() else None for t in contiguous],
+                         _native.ptr(out), _native.dtype_code(out.dtype), stride, batch, carried, length, width,
+                         window, _native.stream_of(device))
+        else:
+            out.copy_(_masked_read(front, mask_name, carried_keys, carried_values, carried_valid, keys, values, mask,
+                                   queries, window))
+        return out
     out = torch.empty_like(queries, memory_format=torch.contiguous_format)
     if batch == 0 or length == 0:
         return out

@@ -173,7 +173,7 @@ def recurrent_scan(
 def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
                retention_offset: int = 0, candidate_offset: int | None = None,
                with_bf16: bool = False, two_phase: bool = True, retention_bias: Tensor | None = None,
-               candidate_bias: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
+               candidate_bias: Tensor | None = None, out_bf16: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
     ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
@@ -186,7 +186,9 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     ``with_bf16`` also its bf16 copy (written by the same kernel) for a
     following bf16 GEMM. ``retention_bias`` and ``candidate_bias`` (fp32
     ``[width]``, None: none) are added to the pre-activations inside the
-    kernel. With ``two_phase`` the kernel gets the workspace of
+    kernel. ``out_bf16`` (with ``with_bf16``): a bf16 ``[B, L, width]`` view
+    with contiguous columns and evenly spaced rows (a column block of a wider
+    matrix) that receives the bf16 copy. With ``two_phase`` the kernel gets the workspace of
     its two-phase form, which it takes when the batch's columns alone would
     leave the chip short of workgroups (a few long rows); the result is the
     same to the bit either way.
@@ -217,7 +219,13 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
         raise DenseCudaUnavailableError(str(error)) from error
     z = preactivations.contiguous()
     states = torch.empty((batch, length, width), device=z.device, dtype=torch.float32)
-    states16 = torch.empty(states.shape, device=z.device, dtype=torch.bfloat16) if with_bf16 else None
+    states16 = None
+    if with_bf16:
+        states16 = out_bf16 if out_bf16 is not None else torch.empty(states.shape, device=z.device,
+                                                                     dtype=torch.bfloat16)
+        if (states16.shape != states.shape or states16.dtype != torch.bfloat16 or states16.stride(2) != 1
+                or states16.stride(0) != length * states16.stride(1)):
+            raise DenseCudaValidationError("out_bf16 must be a bf16 [batch, length, width] view with evenly spaced rows")
     if states.numel():
         mask = valid_mask.contiguous() if valid_mask is not None else None
         need = _native.query("koemi_gated_scan_workspace_bytes", batch, length, width) if two_phase else 0
@@ -228,6 +236,7 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
             _native.ptr(candidate_bias),
             _native.ptr(mask) if mask is not None else None,
             _native.ptr(initial.contiguous()), _native.ptr(states), _native.ptr(states16),
+            states16.stride(1) if states16 is not None else 0,
             batch, length, width, _native.ptr(workspace), need, _native.stream_of(z.device),
         )
     return (states, states16) if with_bf16 else states

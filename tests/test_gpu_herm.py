@@ -221,6 +221,42 @@ def test_associative_kernel_matches_the_oracle(device, b, length, d, m):
         assert np.all(err <= 1e-4 * np.abs(ref) + 1e-5 * scale), name
 
 
+@pytest.mark.parametrize("length", [130, 128])
+def test_associative_reads_into_a_bf16_block_and_from_bf16_projections(device, length):
+    """The reads written into a bf16 column block of a wider matrix equal the
+    fp32 reads rounded to bf16 (one launch, the same arithmetic), for the
+    one-window and the windowed entry; projections given in bf16 give the
+    reads of their fp32 widening bit for bit (the kernels widen on load)."""
+
+    b, d, m, window = 2, 96, 16, 64
+    g = torch.Generator(device=device).manual_seed(length)
+    # rows padded to a multiple of 4 columns: the four-columns-per-lane read
+    proj = torch.randn((b, length, 3 * d + 2 * m + 4), generator=g, device=device)
+    surprise = torch.rand((b, length), generator=g, device=device)
+    valid = torch.rand((b, length), generator=g, device=device) < 0.8
+    basis = torch.randn((b, d, m), generator=g, device=device) * 0.1
+    norm = torch.rand((b, m), generator=g, device=device)
+    wide = torch.zeros((b, length, 3 * d), device=device, dtype=torch.bfloat16)
+    read, nb, nn = herm.associative_scan_read(proj, surprise, valid, basis, norm, width=d, features=m)
+    got, nb2, nn2 = herm.associative_scan_read(proj, surprise, valid, basis, norm, width=d, features=m,
+                                               out=wide[..., d:2 * d])
+    assert got.data_ptr() == wide[..., d:2 * d].data_ptr()
+    assert torch.equal(wide[..., d:2 * d], read.to(torch.bfloat16))
+    assert torch.equal(nb2, nb) and torch.equal(nn2, nn)
+    assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
+    low = proj.to(torch.bfloat16)
+    r16, b16, n16 = herm.associative_scan_read(low, surprise, valid, basis, norm, width=d, features=m)
+    r32, b32, n32 = herm.associative_scan_read(low.float(), surprise, valid, basis, norm, width=d, features=m)
+    assert torch.equal(r16, r32) and torch.equal(b16, b32) and torch.equal(n16, n32)
+    if length % window == 0:
+        wide.zero_()
+        rw, bw, nw = herm.associative_scan_read_windows(proj, surprise, valid, basis, norm, width=d, features=m,
+                                                        window=window)
+        herm.associative_scan_read_windows(proj, surprise, valid, basis, norm, width=d, features=m, window=window,
+                                           out=wide[..., 2 * d:])
+        assert torch.equal(wide[..., 2 * d:], rw.to(torch.bfloat16))
+
+
 def test_bf16_copies_written_by_the_kernels_equal_the_casts(device):
     """The bf16 GEMM inputs the block's kernels write beside their fp32 results
     (RMSNorm, the gated scan, the fusion concatenation) equal torch's

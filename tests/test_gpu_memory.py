@@ -115,6 +115,28 @@ def test_read_salient_window_matches_oracle(device, b, s, length, d, p, dtype):
         assert np.all(got == 0.0)
 
 
+@pytest.mark.parametrize("window, s, length", [(0, 16, 128), (16, 16, 128), (0, 16, 200), (40, 16, 50)])
+def test_reads_into_a_bf16_block_equal_the_rounded_reads(device, window, s, length):
+    """read_*_window(out=...) writes the read into a bf16 column block of a
+    wider matrix: equal to the fp32 read rounded to bf16, the neighbouring
+    columns untouched. (0, 16, 128) and (16, 16, 128) take the one-launch
+    read (koemi_memory_read_into); (0, 16, 200) (215 candidate slots) and
+    (40, 16, 50) (a window past 33) the fallback through the fp32 read."""
+
+    b, d = 3, 64
+    ck, cv, cvalid, k, v, flags, q = (x.to(device) for x in _read_case(7 + window + length, b, s, length, d, 0.6,
+                                                                       torch.float32))
+    wide = torch.zeros((b, length, 3 * d), device=device, dtype=torch.bfloat16)
+    if window:
+        want = memory.read_local_window(ck, cv, cvalid, k, v, flags, q, window=window)
+        memory.read_local_window(ck, cv, cvalid, k, v, flags, q, window=window, out=wide[..., d:2 * d])
+    else:
+        want = memory.read_salient_window(ck, cv, cvalid, k, v, flags, q)
+        memory.read_salient_window(ck, cv, cvalid, k, v, flags, q, out=wide[..., d:2 * d])
+    assert torch.equal(wide[..., d:2 * d], want.to(torch.bfloat16))
+    assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
+
+
 def test_read_salient_window_rejects_bad_inputs(device):
     ck, cv, cvalid, k, v, adm, q = (x.to(device) for x in _read_case(1, 2, 3, 5, 4, 0.5, torch.float32))
     with pytest.raises(think.CudaThinkValidationError, match="share a dtype"):

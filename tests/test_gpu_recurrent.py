@@ -154,8 +154,13 @@ def test_two_phase_gated_scan_equals_the_one_pass_scan(device, b, length, d, r_o
     kw = dict(width=d, retention_offset=r_off, candidate_offset=c_off, with_bf16=True)
     one, one16 = recurrent.gated_scan(z, valid, h0, two_phase=False, **kw)
     two, two16 = recurrent.gated_scan(z, valid, h0, two_phase=True, **kw)
+    # the bf16 copy written into a column block of a wider matrix
+    wide = torch.zeros((b, length, 3 * d), device=device, dtype=torch.bfloat16)
+    three, _ = recurrent.gated_scan(z, valid, h0, two_phase=True, out_bf16=wide[..., d:2 * d], **kw)
     torch.cuda.synchronize()
     assert torch.equal(one, two) and torch.equal(one16, two16)
+    assert torch.equal(three, one) and torch.equal(wide[..., d:2 * d], one16)
+    assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
     select = lambda off: np.eye(cols)[off:off + d]
     zc = z.double().cpu().numpy()
     a, inc = oracle.recurrent_gates(zc, select(r_off), np.zeros(d), select(c_off), np.zeros(d), valid.cpu().numpy())
