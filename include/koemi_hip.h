@@ -436,6 +436,19 @@ int koemi_herm_local_tail(const float* carried_keys, const float* carried_values
                           float* out_values, uint8_t* out_valid, int64_t batch, int64_t window, int64_t length,
                           int64_t width, koemi_stream_t stream);
 
+/* causal_surprise of a HERM window from the state before each position
+ * (network.py:318-325, 677-698) with the fixed-threshold admission
+ * (network.py:349), one kernel: row (b, t) of the batch x length rows is
+ * scored, as koemi_surprise_rows_forward does (fp32, content_bias `bias`
+ * [vocab] or NULL), on the logits of row (b, t - 1) of `logits`
+ * [batch * length, vocab] (the window's own states), and for t == 0 on row b
+ * of `first` [batch, vocab] (the carried state), against target_ids[b, t];
+ * `admission` (NULL: none) receives valid && surprise > threshold.
+ * vocab == 256; 16-byte aligned logits. */
+int koemi_herm_surprise_shifted(const float* logits, const float* first, const float* bias, const int64_t* target_ids,
+                                const uint8_t* valid_mask, float* surprise, uint8_t* admission, float threshold,
+                                int64_t batch, int64_t length, int64_t vocab, float log_vocab, koemi_stream_t stream);
+
 /* The fusion layer's input [working ; memory ; local ; salient]
  * (network.py:401-405, a torch.cat in the reference) as one bf16 matrix
  * [rows, pieces * width] for its GEMM: `pieces` (1..4) fp32 [rows, width]

@@ -172,11 +172,16 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
 // then by a xor butterfly over the 16 lanes (offsets 8, 4, 2, 1); lane 0 of
 // each quarter finishes its row. Every load is issued up front at a clamped
 // in-bounds address. FULL: V == 256 (no element is past the end of its row).
-template <typename T, bool VEC, bool HAS_BIAS, bool FULL>
+// SHIFT (the HERM block's surprise of every position from the state before
+// it): rows are (b, pos) of a [batch, length] window; row (b, pos) scores the
+// logits of row (b, pos - 1), and for pos == 0 row b of `first` (the carried
+// state's logits). `admission` (null: none) receives valid && s > threshold.
+template <typename T, bool VEC, bool HAS_BIAS, bool FULL, bool SHIFT = false>
 __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
     const float* __restrict__ logits, const T* __restrict__ bias,
     const int64_t* __restrict__ targets, const uint8_t* __restrict__ valid, T* __restrict__ out,
-    int64_t rows, int64_t v_runtime, float log_vocab) {
+    int64_t rows, int64_t v_runtime, float log_vocab, const float* __restrict__ first = nullptr,
+    int64_t length = 1, uint8_t* __restrict__ admission = nullptr, float threshold = 0.0f) {
 #pragma clang fp contract(off)
     const int64_t V = FULL ? 256 : v_runtime;
     const int lane = lane_id();
@@ -187,6 +192,10 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
     const bool live = valid[rr] != 0;
     const int64_t t = targets[rr];
     const float* z = logits + rr * V;
+    if constexpr (SHIFT) {
+        const int64_t pos = rr % length;
+        z = pos == 0 ? first + (rr / length) * V : logits + (rr - 1) * V;
+    }
     float v[4][4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -241,6 +250,7 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
         }
     }
     out[row] = from_f32<T>(s);
+    if (admission != nullptr) admission[row] = (live && to_f32(from_f32<T>(s)) > threshold) ? 1 : 0;
 }
 
 // d surprise / d logits (surprise_kernel.cu:136-192):
@@ -1061,7 +1071,8 @@ int launch_rows(const float* logits, const void* bias, const int64_t* targets, c
     if (V <= 256) {
         const dim3 grid(grid_for(rows, kRowWaves * 4));
         auto launch16 = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, grid, block, 0, stream, logits, b, targets, valid, o, rows, V, log_vocab);
+            hipLaunchKernelGGL(kernel, grid, block, 0, stream, logits, b, targets, valid, o, rows, V, log_vocab,
+                               static_cast<const float*>(nullptr), int64_t(1), static_cast<uint8_t*>(nullptr), 0.0f);
         };
         if (vec && V == 256) {
             if (b) launch16(surprise_rows16_kernel<T, true, true, true>);
@@ -1103,6 +1114,28 @@ extern "C" int koemi_surprise_rows_forward(const float* logits, const void* bias
         case KOEMI_F16: return launch_rows<f16>(logits, bias, target_ids, valid_mask, surprise, rows, vocab, log_vocab, s);
         default: return launch_rows<bf16>(logits, bias, target_ids, valid_mask, surprise, rows, vocab, log_vocab, s);
     }
+}
+
+extern "C" int koemi_herm_surprise_shifted(const float* logits, const float* first, const float* bias,
+                                           const int64_t* target_ids, const uint8_t* valid_mask, float* surprise,
+                                           uint8_t* admission, float threshold, int64_t batch, int64_t length,
+                                           int64_t vocab, float log_vocab, koemi_stream_t stream) {
+    if (batch < 0 || length < 1 || vocab < 1) return fail(KOEMI_ERR_INVALID, "shifted surprise needs length, vocab >= 1");
+    if (vocab != 256) return fail(KOEMI_ERR_UNSUPPORTED, "shifted surprise supports a content vocabulary of 256");
+    if (batch == 0) return KOEMI_OK;
+    if (!logits || !first || !target_ids || !valid_mask || !surprise)
+        return fail(KOEMI_ERR_INVALID, "shifted surprise received a null pointer");
+    if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 || reinterpret_cast<uintptr_t>(first) % 16 != 0)
+        return fail(KOEMI_ERR_INVALID, "shifted surprise needs 16-byte aligned logits");
+    const int64_t rows = batch * length;
+    const dim3 grid(grid_for(rows, kRowWaves * 4));
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kWave * kRowWaves), 0, as_stream(stream), logits, bias, target_ids,
+                           valid_mask, surprise, rows, vocab, log_vocab, first, length, admission, threshold);
+    };
+    if (bias) launch(surprise_rows16_kernel<float, true, true, true, true>);
+    else launch(surprise_rows16_kernel<float, true, false, true, true>);
+    return check_launch("koemi_herm_surprise_shifted");
 }
 
 extern "C" int koemi_surprise_rows_backward(const float* logits, const void* bias,

@@ -127,6 +127,9 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P),
     ),
+    "koemi_herm_surprise_shifted": (
+        c_int, (_P, _P, _P, _P, _P, _P, _P, c_float, c_int64, c_int64, c_int64, c_float, _P),
+    ),
     "koemi_herm_rmsnorm": (c_int, (_P, c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_float, _P)),
     "koemi_herm_concat_bf16": (c_int, (_P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P)),
     "koemi_read_step_pair": (

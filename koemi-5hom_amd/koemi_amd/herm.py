@@ -199,6 +199,8 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"])
         q["content_w"] = to(p["head_w"][:PAD_TOKEN_ID])
         q["content_b"] = to(p["head_b"][:PAD_TOKEN_ID])
+        if lin == torch.bfloat16:
+            q["content_w16"] = q["content_w"].to(lin)
         prepared.append(q)
     return prepared
 
@@ -479,10 +481,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                    with_bf16=low is not None, retention_bias=p["gates_b"][:d],
                                    candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    # the state before each position: the carried one, then the window's own
-    prior = state["working"].unsqueeze(1) if length == 1 else torch.cat((state["working"].unsqueeze(1), ws[:, :-1]),
-                                                                        dim=1)
-    surprise = think.causal_surprise(prior, p["content_w"], p["content_b"], targets, valid, validate_targets=False)
+    surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
     projected = _projection(ws_low, p, "ws")
     # local keys and values: the first two column blocks, invalid rows zeroed (one kernel)
@@ -509,7 +508,6 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                     width=d, features=settings.memory_features,
                                                     out=_block(fusion_in, 1, d))
 
-    admission = think.admission_above(surprise, valid, settings.salience_threshold)
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
                                                    state["salient_valid"], local_keys, local_values, admission, ws,
@@ -600,25 +598,36 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     return read, next_basis, next_normalizer
 
 
-def _surprise_after(p: dict[str, Tensor], ws: Tensor, carried: Tensor, targets: Tensor, valid: Tensor) -> Tensor:
+def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws_low: Tensor, carried: Tensor,
+                    targets: Tensor, valid: Tensor) -> tuple[Tensor, Tensor]:
     """causal_surprise of every position from the state before it (the carried
-    state, then the window's own; network.py:318-325, 677-698) without forming
-    the shifted states: the content logits of the carried state and of every
-    working state (the same fp32 products and row kernel as
-    ``think.causal_surprise``), each working state's row scored against the
-    next position's target. Returns fp32 [B, L]."""
+    state, then the window's own; network.py:318-325, 677-698) and the
+    fixed-threshold admission (network.py:349), without forming the shifted
+    states: the content logits of the carried state and of every working
+    state (fp32 results; bf16 operands for a bf16 stack, the content head under
+    bf16 autocast), then one kernel (``koemi_herm_surprise_shifted``) scoring
+    row t on the logits of row t - 1 (the carried state's for t = 0). Returns
+    (surprise fp32 [B, L], admission bool [B, L])."""
 
     batch, length, d = ws.shape
-    weight_t = p["content_w"].t()
-    logits = torch.mm(ws.view(batch * length, d), weight_t)
-    first = torch.mm(carried, weight_t)
-    next_targets = torch.cat((targets[:, 1:], targets[:, :1]), dim=1)      # row t scores target t + 1
-    next_valid = torch.cat((valid[:, 1:], torch.zeros_like(valid[:, :1])), dim=1)
-    later = think.surprise_from_logits(logits, next_targets.view(-1), next_valid.view(-1),
-                                       content_bias=p["content_b"]).view(batch, length)
-    start = think.surprise_from_logits(first, targets[:, 0].contiguous(), valid[:, 0].contiguous(),
-                                       content_bias=p["content_b"])
-    return torch.cat((start.unsqueeze(1), later[:, :-1]), dim=1)
+    w16 = p.get("content_w16")
+    if w16 is not None:
+        weight_t = w16.t()
+        first = torch.mm(carried.to(torch.bfloat16), weight_t, out_dtype=torch.float32)
+        logits = torch.mm(ws_low.reshape(batch * length, d), weight_t, out_dtype=torch.float32) if length > 1 \
+            else first
+    else:
+        weight_t = p["content_w"].t()
+        first = torch.mm(carried, weight_t)
+        logits = torch.mm(ws.reshape(batch * length, d), weight_t) if length > 1 else first
+    surprise = torch.empty((batch, length), device=ws.device, dtype=torch.float32)
+    admission = torch.empty((batch, length), device=ws.device, dtype=torch.bool)
+    vocab = first.shape[1]
+    _native.call("koemi_herm_surprise_shifted", _native.ptr(logits), _native.ptr(first), _native.ptr(p["content_b"]),
+                 _native.ptr(targets), _native.ptr(valid), _native.ptr(surprise), _native.ptr(admission),
+                 float(settings.salience_threshold), batch, length, vocab, think._log_vocab(vocab),
+                 _native.stream_of(ws.device))
+    return surprise, admission
 
 
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
@@ -661,7 +670,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
                                    with_bf16=low is not None, retention_bias=p["gates_b"][:d],
                                    candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    surprise = _surprise_after(p, ws, state["working"], targets, valid)
+    surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
     projected = _projection(ws_low, p, "ws")
     local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
@@ -681,7 +690,6 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
                                                             state["normalizer"], width=d,
                                                             features=settings.memory_features, window=chunk,
                                                             out=_block(fusion_in, 1, d))
-    admission = think.admission_above(surprise, valid, settings.salience_threshold)
     salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                 local_keys, local_values, admission, window=chunk, capacity=cap_s,
                                                 tail=False)

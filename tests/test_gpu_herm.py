@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 import torch
 
-from koemi_amd import herm
+from koemi_amd import _native, herm, think
 from oracle import herm as oherm
 
 pytestmark = pytest.mark.gpu
@@ -255,6 +255,32 @@ def test_associative_reads_into_a_bf16_block_and_from_bf16_projections(device, l
         herm.associative_scan_read_windows(proj, surprise, valid, basis, norm, width=d, features=m, window=window,
                                            out=wide[..., 2 * d:])
         assert torch.equal(wide[..., 2 * d:], rw.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("b, length", [(3, 130), (64, 1)])
+def test_shifted_surprise_equals_the_row_kernel_on_shifted_logits(device, b, length):
+    """koemi_herm_surprise_shifted scores row t on the logits of row t - 1
+    (the carried state's for t = 0): equal, bit for bit, to
+    koemi_surprise_rows_forward on the explicitly shifted logits, and its
+    admission to valid & (surprise > threshold)."""
+
+    g = torch.Generator(device=device).manual_seed(b + length)
+    logits = torch.randn((b * length, 256), generator=g, device=device) * 2.0
+    first = torch.randn((b, 256), generator=g, device=device) * 2.0
+    bias = torch.randn((256,), generator=g, device=device) * 0.1
+    targets = torch.randint(0, 256, (b, length), generator=g, device=device)
+    valid = torch.rand((b, length), generator=g, device=device) < 0.8
+    surprise = torch.empty((b, length), device=device)
+    admission = torch.empty((b, length), device=device, dtype=torch.bool)
+    threshold = 0.6
+    _native.call("koemi_herm_surprise_shifted", _native.ptr(logits), _native.ptr(first), _native.ptr(bias),
+                 _native.ptr(targets), _native.ptr(valid), _native.ptr(surprise), _native.ptr(admission), threshold,
+                 b, length, 256, think._log_vocab(256), _native.stream_of(device))
+    shifted = torch.cat((first.unsqueeze(1), logits.view(b, length, 256)[:, :-1]), dim=1).reshape(b * length, 256)
+    want = think.surprise_from_logits(shifted.contiguous(), targets.reshape(-1), valid.reshape(-1),
+                                      content_bias=bias).view(b, length)
+    assert torch.equal(surprise, want)
+    assert torch.equal(admission, valid & (want > threshold))
 
 
 def test_bf16_copies_written_by_the_kernels_equal_the_casts(device):
