@@ -298,7 +298,8 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
                          const float* initial, float* states, int64_t batch, int64_t length, int64_t width,
                          void* workspace, size_t workspace_bytes, koemi_stream_t stream);
 
-/* The same gates and scan from precomputed fp32 pre-activations, for callers
+/* The same gates and scan from precomputed pre-activations (fp32, or bf16: a
+ * GEMM's own output dtype, as nn.Linear under bf16 autocast), for callers
  * that form u W_r^T and u W_c^T themselves (one stacked GEMM): row r of the
  * batch x length rows holds the retention pre-activations at
  * preactivations[r * row_stride + retention_offset + f] and the candidate ones
@@ -308,14 +309,15 @@ int koemi_recurrent_scan(const float* input, const float* retention_weight, cons
  * valid) and h_t = a_t h_{t-1} + b_t from `initial` [batch, width] into
  * `states` [batch, length, width], as in network.py:306-310; with
  * `states_bf16` (NULL: none) also a bf16 copy of the states for the next
- * projection's GEMM, rows bf16_row_stride elements apart (0: width). `workspace` (NULL: none, else at least
+ * projection's GEMM, rows bf16_row_stride elements apart (0: width).
+ * `workspace` (NULL: none, else at least
  * koemi_gated_scan_workspace_bytes) lets a batch of a few long rows run as a
  * two-phase scan: the transfers of every 8-step segment first, then chunks of
  * the sequence in parallel, each from its carry composed through the segments
  * before it in order, which gives the same bits as the one-pass scan. */
 size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
-int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
-                     int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
+int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_t row_stride,
+                     int64_t retention_offset, int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
                      const uint8_t* valid, const float* initial, float* states, void* states_bf16,
                      int64_t bf16_row_stride, int64_t batch, int64_t length, int64_t width, void* workspace,
                      size_t workspace_bytes, koemi_stream_t stream);

@@ -198,17 +198,43 @@ __device__ __forceinline__ void store_bf16(__bf16* dst, const float (&o)[VEC]) {
 // One chunk's raw inputs of a wave: S steps of VEC columns and the steps'
 // valid bytes, loaded unconditionally at clamped positions so that no branch
 // waits on them; wide_gate turns them into (a, b) pairs when they are used.
-template <int S, int VEC>
+// VEC consecutive pre-activations as loaded (fp32, or bf16: the GEMM's own
+// output dtype) and their fp32 widening.
+template <typename ZT, int VEC>
+struct ZVec {
+    using type = typename FloatVec<VEC>::type;
+    __device__ static void split(const type& v, float (&o)[VEC]) { FloatVec<VEC>::split(v, o); }
+};
+template <int VEC>
+struct ZVec<__bf16, VEC> {
+    static_assert(VEC == 1 || VEC == 2 || VEC == 4, "one, two or four columns per lane");
+    using type = std::conditional_t<VEC == 1, uint16_t, std::conditional_t<VEC == 2, uint32_t, uint2>>;
+    __device__ static void split(const type& v, float (&o)[VEC]) {
+        if constexpr (VEC == 1) {
+            o[0] = __uint_as_float(static_cast<uint32_t>(v) << 16);
+        } else if constexpr (VEC == 2) {
+            o[0] = __uint_as_float(v << 16);
+            o[1] = __uint_as_float(v & 0xffff0000u);
+        } else {
+            o[0] = __uint_as_float(v.x << 16);
+            o[1] = __uint_as_float(v.x & 0xffff0000u);
+            o[2] = __uint_as_float(v.y << 16);
+            o[3] = __uint_as_float(v.y & 0xffff0000u);
+        }
+    }
+};
+
+template <int S, int VEC, typename ZT = float>
 struct WideRaw {
-    typename FloatVec<VEC>::type va[S], vb[S];
+    typename ZVec<ZT, VEC>::type va[S], vb[S];
     uint8_t keep[S];
 };
 
-template <int S, int VEC, bool GATES>
-__device__ __forceinline__ void wide_fetch(const float* __restrict__ a_col, const float* __restrict__ b_col,
+template <int S, int VEC, bool GATES, typename ZT = float>
+__device__ __forceinline__ void wide_fetch(const ZT* __restrict__ a_col, const ZT* __restrict__ b_col,
                                            int64_t stride, int64_t L, int64_t t_first, int64_t bi,
-                                           const GateInputs& gates, WideRaw<S, VEC>& raw) {
-    using V = typename FloatVec<VEC>::type;
+                                           const GateInputs& gates, WideRaw<S, VEC, ZT>& raw) {
+    using V = typename ZVec<ZT, VEC>::type;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const int64_t t = t_first + i;
@@ -221,15 +247,15 @@ __device__ __forceinline__ void wide_fetch(const float* __restrict__ a_col, cons
 
 // (a, b) of the fetched steps: the gates first when GATES, then the identity
 // (1, 0) outside the sequence or the columns.
-template <int S, int VEC, bool GATES>
-__device__ __forceinline__ void wide_gate(const WideRaw<S, VEC>& raw, int64_t L, int64_t t_first, bool col_ok,
+template <int S, int VEC, bool GATES, typename ZT = float>
+__device__ __forceinline__ void wide_gate(const WideRaw<S, VEC, ZT>& raw, int64_t L, int64_t t_first, bool col_ok,
                                           const float (&gbr)[VEC], const float (&gbc)[VEC], float (&ra)[S][VEC],
                                           float (&rb)[S][VEC]) {
 #pragma unroll
     for (int i = 0; i < S; ++i) {
         const bool ok = col_ok && t_first + i < L;
-        FloatVec<VEC>::split(raw.va[i], ra[i]);
-        FloatVec<VEC>::split(raw.vb[i], rb[i]);
+        ZVec<ZT, VEC>::split(raw.va[i], ra[i]);
+        ZVec<ZT, VEC>::split(raw.vb[i], rb[i]);
 #pragma unroll
         for (int c = 0; c < VEC; ++c) {
             if constexpr (GATES) gate_pair(ra[i][c], rb[i][c], gbr[c], gbc[c], raw.keep[i] != 0, ra[i][c], rb[i][c]);
@@ -256,9 +282,9 @@ __device__ __forceinline__ void gate_biases(const GateInputs& gates, int64_t fc,
 // operations of the segment pass of scan_forward_wide_kernel in their order,
 // into tp / tq [B, segments, F]. Wave w of workgroup (x, y) takes segment
 // 8 y + w of batch row x / col_tiles.
-template <int S, int VEC, bool GATES>
+template <int S, int VEC, bool GATES, typename ZT = float>
 __global__ __launch_bounds__(kWave * 8) void scan_segment_transfer_kernel(
-    const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ tp, float* __restrict__ tq,
+    const ZT* __restrict__ a, const ZT* __restrict__ b, float* __restrict__ tp, float* __restrict__ tq,
     int64_t L, int64_t F, int64_t col_tiles, int64_t stride, int64_t segments, GateInputs gates) {
     using V = typename FloatVec<VEC>::type;
     const int lane = lane_id();
@@ -270,10 +296,11 @@ __global__ __launch_bounds__(kWave * 8) void scan_segment_transfer_kernel(
     const int64_t fc = col_ok ? f : 0;
     float gbr[VEC], gbc[VEC];
     gate_biases<VEC, GATES>(gates, fc, gbr, gbc);
-    WideRaw<S, VEC> raw;
-    wide_fetch<S, VEC, GATES>(a + bi * L * stride + fc, b + bi * L * stride + fc, stride, L, j * S, bi, gates, raw);
+    WideRaw<S, VEC, ZT> raw;
+    wide_fetch<S, VEC, GATES, ZT>(a + bi * L * stride + fc, b + bi * L * stride + fc, stride, L, j * S, bi, gates,
+                                  raw);
     float ra[S][VEC], rb[S][VEC];
-    wide_gate<S, VEC, GATES>(raw, L, j * S, col_ok, gbr, gbc, ra, rb);
+    wide_gate<S, VEC, GATES, ZT>(raw, L, j * S, col_ok, gbr, gbc, ra, rb);
     float po[VEC], qo[VEC];
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
@@ -359,9 +386,9 @@ __global__ __launch_bounds__(kWave * 8) void scan_chunk_carry_kernel(
 // owns 64 / LPC column strips and NSEG * LPC segments per chunk (twice the
 // workgroups for a batch of few rows at LPC = 2). The composition order, and
 // so every result bit, is the same for any LPC and VEC.
-template <int S, int NSEG, int VEC, bool GATES = false, int LPC = 1>
+template <int S, int NSEG, int VEC, bool GATES = false, int LPC = 1, typename ZT = float>
 __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
-    const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
+    const ZT* __restrict__ a, const ZT* __restrict__ b, const float* __restrict__ h0, float* __restrict__ h,
     int64_t L, int64_t F, int64_t col_tiles, int64_t stride,
     GateInputs gates = GateInputs{nullptr, nullptr, nullptr, nullptr, 0},
     const float* __restrict__ chunk_carry = nullptr, int64_t chunks = 0, int64_t span = 0) {
@@ -378,8 +405,8 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     const int64_t f = ((static_cast<int64_t>(blockIdx.x) % col_tiles) * TW + lane) * VEC;
     const bool col_ok = f < F;
     const int64_t fc = col_ok ? f : 0;
-    const float* a_col = a + bi * L * stride + fc;
-    const float* b_col = b + bi * L * stride + fc;
+    const ZT* a_col = a + bi * L * stride + fc;
+    const ZT* b_col = b + bi * L * stride + fc;
     float* h_col = h + bi * L * F + fc;
     const int64_t t_begin = chunk_carry != nullptr ? static_cast<int64_t>(blockIdx.y) * span : 0;
     const int64_t t_end = chunk_carry != nullptr ? (t_begin + span < L ? t_begin + span : L) : L;
@@ -400,8 +427,8 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
         for (int c = 0; c < VEC; ++c) carry[c] = col_ok ? carry[c] : 0.0f;
     }
 
-    auto fetch = [&](int64_t t_first, WideRaw<S, VEC>& raw) {
-        wide_fetch<S, VEC, GATES>(a_col, b_col, stride, L, t_first, bi, gates, raw);
+    auto fetch = [&](int64_t t_first, WideRaw<S, VEC, ZT>& raw) {
+        wide_fetch<S, VEC, GATES, ZT>(a_col, b_col, stride, L, t_first, bi, gates, raw);
     };
 
     auto process = [&](float (&ra)[S][VEC], float (&rb)[S][VEC], int64_t t0) {
@@ -454,7 +481,7 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
     // flight while one is scanned (buffer indices are compile-time constants
     // of the unrolled ring, so the buffers stay in registers).
     constexpr int NB = VEC == 1 ? KOEMI_SCAN_BUFFERS : 2;
-    WideRaw<S, VEC> raw[NB];
+    WideRaw<S, VEC, ZT> raw[NB];
     const int64_t seg_off = static_cast<int64_t>(seg) * S;
 #pragma unroll
     for (int k = 0; k + 1 < NB; ++k) fetch(t_begin + k * CH + seg_off, raw[k]);
@@ -465,7 +492,7 @@ __global__ __launch_bounds__(kWave * NSEG) void scan_forward_wide_kernel(
             if (tc >= t_end) break;
             fetch(tc + (NB - 1) * CH + seg_off, raw[(k + NB - 1) % NB]);
             float ra[S][VEC], rb[S][VEC];
-            wide_gate<S, VEC, GATES>(raw[k], L, tc + seg_off, col_ok, gbr, gbc, ra, rb);
+            wide_gate<S, VEC, GATES, ZT>(raw[k], L, tc + seg_off, col_ok, gbr, gbc, ra, rb);
             process(ra, rb, tc);
         }
     }
@@ -619,7 +646,8 @@ int check_scan_args(const void* a, const void* b, const void* h0, const void* h,
 
 // One-position windows (decode steps): h = a h0 + b per column, the same
 // single rounding the scan makes at its first position.
-__global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict__ zr, const float* __restrict__ zc,
+template <typename ZT>
+__global__ __launch_bounds__(256) void gated_step_kernel(const ZT* __restrict__ zr, const ZT* __restrict__ zc,
                                                          int64_t stride, GateInputs gates,
                                                          const float* __restrict__ h0, float* __restrict__ h,
                                                          int64_t B, int64_t F) {
@@ -628,7 +656,8 @@ __global__ __launch_bounds__(256) void gated_step_kernel(const float* __restrict
     const int64_t bi = i / F, f = i - bi * F;
     const bool keep = gates.valid == nullptr || gates.valid[bi] != 0;
     float a, b;
-    gate_pair(zr[bi * stride + f], zc[bi * stride + f], gates.retention_bias ? gates.retention_bias[f] : 0.0f,
+    gate_pair(to_f32(zr[bi * stride + f]), to_f32(zc[bi * stride + f]),
+              gates.retention_bias ? gates.retention_bias[f] : 0.0f,
               gates.candidate_bias ? gates.candidate_bias[f] : 0.0f, keep, a, b);
     const float hv = a * h0[i] + b;
     h[i] = hv;
@@ -681,14 +710,14 @@ constexpr int64_t kTwoPhaseBelow = KOEMI_SCAN_TWO_PHASE_BELOW;
 // The three launches of the two-phase gated scan, VEC columns per lane in the
 // two passes over the pre-activations (the carry pass works column by column
 // on the [B, segments, F] transfers, whatever VEC is).
-template <int VEC>
-int run_two_phase(const float* zr, const float* zc, int64_t stride, const GateInputs& gates, const float* h0, float* h,
+template <int VEC, typename ZT>
+int run_two_phase(const ZT* zr, const ZT* zc, int64_t stride, const GateInputs& gates, const float* h0, float* h,
                   int64_t B, int64_t L, int64_t F, int64_t tiles, const TwoPhase& split, float* workspace,
                   hipStream_t stream) {
     float* tp = workspace;
     float* tq = tp + B * split.segments * F;
     float* carries = tq + B * split.segments * F;
-    hipLaunchKernelGGL((scan_segment_transfer_kernel<kScanSteps, VEC, true>),
+    hipLaunchKernelGGL((scan_segment_transfer_kernel<kScanSteps, VEC, true, ZT>),
                        dim3(static_cast<unsigned>(B * tiles), static_cast<unsigned>((split.segments + 7) / 8)),
                        dim3(kWave * 8), 0, stream, zr, zc, tp, tq, L, F, tiles, stride, split.segments, gates);
     int st = check_launch("gated scan (segment transfers)");
@@ -699,7 +728,7 @@ int run_two_phase(const float* zr, const float* zc, int64_t stride, const GateIn
                        split.chunks);
     st = check_launch("gated scan (chunk carries)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
+    hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true, 1, ZT>),
                        dim3(static_cast<unsigned>(B * tiles), static_cast<unsigned>(split.chunks)),
                        dim3(kWave * kScanSegments), 0, stream, zr, zc, h0, h, L, F, tiles, stride, gates, carries,
                        split.chunks, split.span);
@@ -715,14 +744,15 @@ int run_two_phase(const float* zr, const float* zc, int64_t stride, const GateIn
 // a workspace of gated_scan_workspace bytes is given and the column tiles
 // alone leave the chip short of workgroups. The caller has checked that
 // B * ceil(F / 64) fits the grid.
-int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
-                      const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
-                      int64_t h16_stride,
-                      int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace, size_t workspace_bytes) {
+template <typename ZT>
+int launch_gated_scan_t(const ZT* zr, const ZT* zc, int64_t stride, const float* retention_bias,
+                        const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
+                        int64_t h16_stride, int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace,
+                        size_t workspace_bytes) {
     constexpr int VEC = KOEMI_SCAN_VEC;
     const GateInputs gates{retention_bias, candidate_bias, valid, static_cast<__bf16*>(h16), h16_stride};
     if (L == 1) {
-        hipLaunchKernelGGL(gated_step_kernel, dim3(static_cast<unsigned>((B * F + 255) / 256)), dim3(256), 0, stream,
+        hipLaunchKernelGGL(gated_step_kernel<ZT>, dim3(static_cast<unsigned>((B * F + 255) / 256)), dim3(256), 0, stream,
                            zr, zc, stride, gates, h0, h, B, F);
         return check_launch("gated scan (one position)");
     }
@@ -732,7 +762,7 @@ int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const fl
         aligned(retention_bias) && aligned(candidate_bias) && reinterpret_cast<uintptr_t>(h16) % (2 * VEC) == 0 &&
         h16_stride % VEC == 0 &&
         B * wide_tiles >= 256) {
-        hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true>),
+        hipLaunchKernelGGL((scan_forward_wide_kernel<kScanSteps, kScanSegments, VEC, true, 1, ZT>),
                            dim3(static_cast<unsigned>(B * wide_tiles)), dim3(kWave * kScanSegments), 0, stream, zr, zc,
                            h0, h, L, F, wide_tiles, stride, gates);
         return check_launch("gated scan");
@@ -760,20 +790,28 @@ int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const fl
         const TwoPhase split = two_phase_split(B * (tv_ok ? tv_tiles : tiles1), L);
         if (split.chunks >= 2) {
             if (tv_ok)
-                return run_two_phase<TV>(zr, zc, stride, gates, h0, h, B, L, F, tv_tiles, split,
-                                         static_cast<float*>(workspace), stream);
-            return run_two_phase<1>(zr, zc, stride, gates, h0, h, B, L, F, tiles1, split,
-                                    static_cast<float*>(workspace), stream);
+                return run_two_phase<TV, ZT>(zr, zc, stride, gates, h0, h, B, L, F, tv_tiles, split,
+                                             static_cast<float*>(workspace), stream);
+            return run_two_phase<1, ZT>(zr, zc, stride, gates, h0, h, B, L, F, tiles1, split,
+                                        static_cast<float*>(workspace), stream);
         }
     }
     auto one_pass = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(B * tiles)), dim3(kWave * kScanSegments), 0, stream, zr,
                            zc, h0, h, L, F, tiles, stride, gates, nullptr, 0, 0);
     };
-    if (lpc == 4) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 4>);
-    else if (lpc == 2) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 2>);
-    else one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 1>);
+    if (lpc == 4) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 4, ZT>);
+    else if (lpc == 2) one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 2, ZT>);
+    else one_pass(scan_forward_wide_kernel<kScanSteps, kScanSegments, 1, true, 1, ZT>);
     return check_launch("gated scan");
+}
+
+int launch_gated_scan(const float* zr, const float* zc, int64_t stride, const float* retention_bias,
+                      const float* candidate_bias, const uint8_t* valid, const float* h0, float* h, void* h16,
+                      int64_t h16_stride, int64_t B, int64_t L, int64_t F, hipStream_t stream, void* workspace,
+                      size_t workspace_bytes) {
+    return launch_gated_scan_t(zr, zc, stride, retention_bias, candidate_bias, valid, h0, h, h16, h16_stride, B, L,
+                               F, stream, workspace, workspace_bytes);
 }
 
 }  // namespace koemi
@@ -838,13 +876,15 @@ extern "C" size_t koemi_gated_scan_workspace_bytes(int64_t batch, int64_t length
     return gated_scan_workspace(batch, length, width);
 }
 
-extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride, int64_t retention_offset,
-                                int64_t candidate_offset, const float* retention_bias, const float* candidate_bias,
-                                const uint8_t* valid, const float* initial, float* states, void* states_bf16,
-                                int64_t bf16_row_stride, int64_t batch, int64_t length, int64_t width, void* workspace,
-                                size_t workspace_bytes, koemi_stream_t stream) {
+extern "C" int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_t row_stride,
+                                int64_t retention_offset, int64_t candidate_offset, const float* retention_bias,
+                                const float* candidate_bias, const uint8_t* valid, const float* initial, float* states,
+                                void* states_bf16, int64_t bf16_row_stride, int64_t batch, int64_t length,
+                                int64_t width, void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1)
         return fail(KOEMI_ERR_INVALID, "gated scan needs non-negative batch and length and a positive width");
+    if (preactivation_dtype != KOEMI_F32 && preactivation_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "gated scan pre-activations must be float32 or bfloat16");
     if (retention_offset < 0 || candidate_offset < 0 || retention_offset + width > row_stride ||
         candidate_offset + width > row_stride)
         return fail(KOEMI_ERR_INVALID, "gated scan: the gate columns must lie inside a row");
@@ -858,7 +898,14 @@ extern "C" int koemi_gated_scan(const float* preactivations, int64_t row_stride,
     if (workspace != nullptr && workspace_bytes < gated_scan_workspace(batch, length, width))
         return fail(KOEMI_ERR_INVALID, "gated scan workspace too small: need %zu bytes",
                     gated_scan_workspace(batch, length, width));
-    return launch_gated_scan(preactivations + retention_offset, preactivations + candidate_offset, row_stride,
-                             retention_bias, candidate_bias, valid, initial, states, states_bf16, bf16_row_stride,
-                             batch, length, width, as_stream(stream), workspace, workspace_bytes);
+    if (preactivation_dtype == KOEMI_BF16) {
+        const bf16* z = static_cast<const bf16*>(preactivations);
+        return launch_gated_scan_t(z + retention_offset, z + candidate_offset, row_stride, retention_bias,
+                                   candidate_bias, valid, initial, states, states_bf16, bf16_row_stride, batch, length,
+                                   width, as_stream(stream), workspace, workspace_bytes);
+    }
+    const float* z = static_cast<const float*>(preactivations);
+    return launch_gated_scan_t(z + retention_offset, z + candidate_offset, row_stride, retention_bias, candidate_bias,
+                               valid, initial, states, states_bf16, bf16_row_stride, batch, length, width,
+                               as_stream(stream), workspace, workspace_bytes);
 }

@@ -100,7 +100,8 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_gated_scan_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_gated_scan": (
         c_int,
-        (_P, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, c_int, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t,
+         _P),
     ),
     "koemi_linear_rows": (
         c_int,

@@ -189,8 +189,8 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         q["ws_b"] = to(torch.cat((ws_b, ws_b.new_zeros(pad))))
         q["fusion_w"], q["fusion_b"] = to(p["fusion_w"], lin), to(p["fusion_b"])
         if lin == torch.bfloat16:
-            # the bias of a GEMM with bf16 results (nn.Linear under bf16 autocast)
-            q["ws_b16"], q["fusion_b16"] = q["ws_b"].to(lin), q["fusion_b"].to(lin)
+            # the biases of GEMMs with bf16 results (nn.Linear under bf16 autocast)
+            q["gates_b16"], q["ws_b16"], q["fusion_b16"] = (q[k].to(lin) for k in ("gates_b", "ws_b", "fusion_b"))
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
@@ -274,6 +274,22 @@ def _linear(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     if bias is not None:
         out += bias
     return out.view(*x.shape[:-1], weight.shape[0])
+
+
+def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor, width: int, with_bf16: bool,
+                out_bf16: Tensor | None):
+    """The gate projection and the fused gates + scan: for a bf16 stack
+    outside decode steps the projection's results are bf16 with the biases in
+    the GEMM epilogue (nn.Linear under bf16 autocast); otherwise fp32 results
+    without bias and the biases added inside the scan kernel."""
+
+    w = p["gates_w"]
+    if w.dtype == torch.bfloat16 and not _few_rows(u, w):
+        return recurrent.gated_scan(_linear_low(u, w, p["gates_b16"]), valid, working, width=width,
+                                    with_bf16=with_bf16, out_bf16=out_bf16)
+    return recurrent.gated_scan(_linear(u, w, None), valid, working, width=width, with_bf16=with_bf16,
+                                retention_bias=p["gates_b"][:width], candidate_bias=p["gates_b"][width:],
+                                out_bf16=out_bf16)
 
 
 def _fusion_input(settings: HermSettings, batch: int, length: int, device: torch.device) -> Tensor | None:
@@ -477,9 +493,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     else:
         u = _rms(source, p["input_norm"], fp32=False, low=low)[1]
     fusion_in = _fusion_input(settings, batch, length, ids.device)
-    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
-                                   with_bf16=low is not None, retention_bias=p["gates_b"][:d],
-                                   candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
+    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
@@ -666,9 +680,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     low = lin if lin == torch.bfloat16 else None
     u = _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
     fusion_in = _fusion_input(settings, batch, length, ids.device)
-    scanned = recurrent.gated_scan(_linear(u, p["gates_w"], None), valid, state["working"], width=d,
-                                   with_bf16=low is not None, retention_bias=p["gates_b"][:d],
-                                   candidate_bias=p["gates_b"][d:], out_bf16=_block(fusion_in, 0, d))
+    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 

@@ -176,7 +176,7 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
                candidate_bias: Tensor | None = None, out_bf16: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
-    ``preactivations`` ``[B, L, C]`` fp32 (last dimension contiguous) holds
+    ``preactivations`` ``[B, L, C]`` fp32 or bf16 (last dimension contiguous) holds
     ``u W_r^T + b_r`` in columns ``retention_offset .. + width`` and
     ``u W_c^T + b_c`` in ``candidate_offset .. + width`` (default: right
     after the retention columns), as one stacked projection produces them.
@@ -196,8 +196,9 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
 
     if candidate_offset is None:
         candidate_offset = retention_offset + width
-    if not isinstance(preactivations, Tensor) or preactivations.ndim != 3 or preactivations.dtype != torch.float32:
-        raise DenseCudaValidationError("preactivations must be a float32 [batch, length, columns] tensor")
+    if (not isinstance(preactivations, Tensor) or preactivations.ndim != 3
+            or preactivations.dtype not in (torch.float32, torch.bfloat16)):
+        raise DenseCudaValidationError("preactivations must be a float32 or bfloat16 [batch, length, columns] tensor")
     if preactivations.device.type != "cuda":
         raise DenseCudaValidationError("preactivations must be on CUDA")
     batch, length, columns = preactivations.shape
@@ -232,7 +233,8 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
         workspace = torch.empty(need, device=z.device, dtype=torch.uint8) if need else None
         _native.call(
             "koemi_gated_scan",
-            _native.ptr(z), columns, retention_offset, candidate_offset, _native.ptr(retention_bias),
+            _native.ptr(z), _native.dtype_code(z.dtype), columns, retention_offset, candidate_offset,
+            _native.ptr(retention_bias),
             _native.ptr(candidate_bias),
             _native.ptr(mask) if mask is not None else None,
             _native.ptr(initial.contiguous()), _native.ptr(states), _native.ptr(states16),

@@ -170,6 +170,25 @@ def test_two_phase_gated_scan_equals_the_one_pass_scan(device, b, length, d, r_o
     assert err <= 1e-4
 
 
+@pytest.mark.parametrize("b, length, d, two_phase", [(8, 256, 1024, True), (64, 40, 512, True), (3, 300, 100, True),
+                                                     (64, 1, 1024, False), (1, 777, 64, True)])
+def test_gated_scan_from_bf16_preactivations_equals_their_widening(device, b, length, d, two_phase):
+    """bf16 pre-activations (a bf16 GEMM's own output) give the states of
+    their exact fp32 widening, bit for bit: every path (wide, lane-group,
+    two-phase, one position) widens on load and computes in fp32."""
+
+    g = torch.Generator(device=device).manual_seed(b + length + d)
+    z = (1.5 * torch.randn((b, length, 2 * d), generator=g, device=device)).to(torch.bfloat16)
+    valid = torch.rand((b, length), generator=g, device=device) < 0.8
+    h0 = torch.randn((b, d), generator=g, device=device)
+    bias = torch.randn((2 * d,), generator=g, device=device) * 0.1
+    kw = dict(width=d, with_bf16=True, two_phase=two_phase, retention_bias=bias[:d], candidate_bias=bias[d:])
+    low, low16 = recurrent.gated_scan(z, valid, h0, **kw)
+    wide, wide16 = recurrent.gated_scan(z.float(), valid, h0, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(low, wide) and torch.equal(low16, wide16)
+
+
 def test_gated_scan_rejects_bad_columns(device):
     z = torch.zeros((2, 3, 10), device=device)
     h0 = torch.zeros((2, 4), device=device)
