@@ -472,19 +472,24 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
 
 
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
-                 context: Tensor | None = None, *, with_logits: bool = True
+                 context: Tensor | None = None, *, with_logits: bool = True,
+                 token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None
                  ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
     for the embedding layer). Returns (logits, final_context, next_state,
     surprise); logits is None when ``with_logits`` is False (the stack's
-    inner layers, whose head output nothing reads)."""
+    inner layers, whose head output nothing reads). ``token_context``:
+    ``_token_context``'s four outputs when the caller formed them (a decode
+    step's stack, once for all layers)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
     d = settings.width
     # validity, surprise targets and the routing context of every position in one kernel
-    previous, last_token, valid, targets = _token_context(ids, None, state["last_token"])
+    if token_context is None:
+        token_context = _token_context(ids, None, state["last_token"])
+    previous, last_token, valid, targets = token_context
     source = functional.embedding(ids, p["embedding"]) if context is None else context
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None  # kernels write bf16 copies of the GEMM inputs
@@ -612,6 +617,29 @@ def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: 
     return read, next_basis, next_normalizer
 
 
+def _surprise_carried(p: dict[str, Tensor], settings: HermSettings, carried: Tensor, targets: Tensor,
+                      valid: Tensor) -> tuple[Tensor, Tensor]:
+    """Surprise and admission of a one-position window ([B, 1]), which depend
+    on the carried working state alone: its content logits (``linear_rows``
+    for bf16 heads, a decode step's few rows) and the shifted surprise kernel
+    at length 1."""
+
+    batch = carried.shape[0]
+    w16 = p.get("content_w16")
+    if w16 is not None:
+        first = linear.linear_rows([carried], w16, None)
+    else:
+        first = torch.mm(carried, p["content_w"].t())
+    surprise = torch.empty((batch, 1), device=carried.device, dtype=torch.float32)
+    admission = torch.empty((batch, 1), device=carried.device, dtype=torch.bool)
+    vocab = first.shape[1]
+    _native.call("koemi_herm_surprise_shifted", _native.ptr(first), _native.ptr(first), _native.ptr(p["content_b"]),
+                 _native.ptr(targets), _native.ptr(valid), _native.ptr(surprise), _native.ptr(admission),
+                 float(settings.salience_threshold), batch, 1, vocab, think._log_vocab(vocab),
+                 _native.stream_of(carried.device))
+    return surprise, admission
+
+
 def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws_low: Tensor, carried: Tensor,
                     targets: Tensor, valid: Tensor) -> tuple[Tensor, Tensor]:
     """causal_surprise of every position from the state before it (the carried
@@ -624,6 +652,8 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
     (surprise fp32 [B, L], admission bool [B, L])."""
 
     batch, length, d = ws.shape
+    if length == 1:
+        return _surprise_carried(p, settings, carried, targets, valid)
     w16 = p.get("content_w16")
     if w16 is not None:
         weight_t = w16.t()
@@ -783,10 +813,33 @@ class SequencePrefill:
         return self.logits
 
 
+def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
+                  states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+    """One decode position ([B, 1] ids) through every layer, the token context
+    formed once for all of them (every layer sees the same ids and carries the
+    same last token): one kernel per step instead of one per layer. Otherwise
+    ``block_window`` layer after layer."""
+
+    ids = ids.contiguous()
+    token_context = _token_context(ids, None, states[0]["last_token"])
+    context = None
+    next_states = []
+    logits = None
+    for layer, (p, state) in enumerate(zip(params, states)):
+        logits, context, next_state, _ = block_window(p, settings, ids, state, context,
+                                                      with_logits=layer == len(params) - 1,
+                                                      token_context=token_context)
+        next_states.append(next_state)
+    return logits, next_states
+
+
 def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
                  states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
-    """One window through every layer; returns the last layer's logits and the next states."""
+    """One window through every layer; returns the last layer's logits and the
+    next states. Decode steps (one position) take ``_stack_decode``."""
 
+    if ids.shape[1] == 1 and ids.device.type == "cuda":
+        return _stack_decode(params, settings, ids, states)
     context = None
     next_states = []
     logits = None
