@@ -322,6 +322,33 @@ int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_
                      int64_t bf16_row_stride, int64_t batch, int64_t length, int64_t width, void* workspace,
                      size_t workspace_bytes, koemi_stream_t stream);
 
+/* BoundedRecurrentState.gates (model/memory.py:14-30: the projections
+ * W_r u + b_r and W_c u + b_c, sigmoid retention and tanh candidate), the
+ * masking of network.py:307-309 and the scan of network.py:310 in one kernel,
+ * for bf16 inputs under autocast (the projection's results rounded to bf16
+ * after the bias, as the reference's autocast GEMM writes them). inputs
+ * [batch * length, input_width] bf16 (rows (b, t), contiguous); weights
+ * [2 * width, input_width] bf16: the retention rows, then the candidate rows;
+ * biases [2 * width] bf16 in the same order, or NULL. valid [batch, length]
+ * (NULL: all valid), initial [batch, width] fp32; writes states [batch,
+ * length, width] fp32 and, with states_bf16 (NULL: none), a bf16 copy whose
+ * rows are bf16_row_stride elements apart (0: width). The projection runs on
+ * bf16 MFMA in tiles of 256 positions x 128 features, whose epilogue forms
+ * the gates and scans them, so the pre-activations never reach memory; each
+ * tile publishes its transfer (the affine map of its positions) and takes
+ * its carry by applying the earlier tiles' transfers to the initial state in
+ * order (bounded waits; the result does not depend on timing). Needs length % 256 == 0, width % 128 == 0,
+ * input_width % 64 == 0 and 16-byte aligned inputs and weights
+ * (KOEMI_ERR_UNSUPPORTED otherwise: take a GEMM and koemi_gated_scan), and a
+ * workspace of koemi_gated_projection_scan_workspace_bytes(batch, length,
+ * width) bytes (0 for unsupported shapes). Calls sharing one workspace must
+ * not overlap in time. */
+size_t koemi_gated_projection_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
+int koemi_gated_projection_scan(const void* inputs, const void* weights, const void* biases, const uint8_t* valid,
+                                const float* initial, float* states, void* states_bf16, int64_t bf16_row_stride,
+                                int64_t batch, int64_t length, int64_t width, int64_t input_width, void* workspace,
+                                size_t workspace_bytes, koemi_stream_t stream);
+
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections
  * in a decode step: the gate, working-state, fusion and head layers of
  * model/network.py:296-441 and model/memory.py, which the reference runs as

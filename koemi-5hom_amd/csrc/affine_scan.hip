@@ -171,12 +171,6 @@ struct GateInputs {
     int64_t h16_stride;           // elements between rows of h16 (F when contiguous)
 };
 
-__device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
-    const float ga = kGateMinRetention + kGateRetentionSpan * gate_sigmoid(zr + br);
-    const float gb = (1.0f - ga) * gate_tanh(zc + bc);
-    a = keep ? ga : 1.0f;
-    b = keep ? gb : 0.0f;
-}
 // VEC bf16 values in one store (2 VEC bytes, aligned to it).
 template <int VEC>
 __device__ __forceinline__ void store_bf16(__bf16* dst, const float (&o)[VEC]) {

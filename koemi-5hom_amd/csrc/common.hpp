@@ -128,6 +128,16 @@ __device__ __forceinline__ float gate_tanh(float x) {
 }
 constexpr float kGateMinRetention = 0.00390625f;        // 2^-8
 constexpr float kGateRetentionSpan = 1.0f - 0.0078125f;  // (1 - 2^-8) - 2^-8 = 1 - 2^-7
+// The working-state gates of one feature (model/memory.py:14-30 with the
+// masking of network.py:307-309): retention a = 2^-8 + (1 - 2^-7) sigmoid(zr +
+// br), candidate b = (1 - a) tanh(zc + bc); a masked position keeps the state
+// (a = 1, b = 0).
+__device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc, bool keep, float& a, float& b) {
+    const float ga = kGateMinRetention + kGateRetentionSpan * gate_sigmoid(zr + br);
+    const float gb = (1.0f - ga) * gate_tanh(zc + bc);
+    a = keep ? ga : 1.0f;
+    b = keep ? gb : 0.0f;
+}
 
 // Four consecutive values as fp32 (one 16-byte fp32 or 8-byte bf16 load).
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }

@@ -17,49 +17,34 @@
 // (no host synchronisation): tile slot -> (expert, first row). Rows past the
 // valid pairs are zero-filled.
 #include "common.hpp"
+#include "mfma_stage.hpp"
 
 #include <type_traits>
 
 namespace koemi {
 namespace {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+using mfma_stage::bf16x8;
+using mfma_stage::f32x16;
+using mfma_stage::kOperandBytes;
+using mfma_stage::slot_swizzle;
+using mfma_stage::TileShape;
+using mfma_stage::uniform_ptr;
 
-// Block tile 256 (pairs) x 256 (B rows), four waves in 2x2, each owning a
-// 128x128 sub-tile as 4x4 MFMA 32x32 tiles (256 fp32 accumulators). K advances
-// in 32-wide tiles through a ring of four LDS stages (32 KiB each: A then B)
-// filled by global_load_lds_dwordx4, which writes each lane's 16 bytes straight
-// into LDS at M0 + 16 * lane without passing through registers; two tiles are
-// in flight while one is multiplied, and the fragments of the next K step are
-// read while the current one is multiplied. A stage row is 64 bytes (four
-// 16-byte K groups); group g of row r sits at slot g ^ ((r >> 2) & 3), so the
-// sixteen rows read by any sixteen consecutive lanes fill 256 distinct bytes
-// of banks (conflict-free 16-byte fragment reads).
-constexpr int kBM = 256;
-constexpr int kBN = 256;
-constexpr int kBK = 32;
-constexpr int kGemmThreads = 256;
-constexpr uint32_t kOperandBytes = kBM * kBK * 2u;  // the A operand of one stage (bf16)
-constexpr int kGroupM = 4;  // tile slots per group in the launch order
-
+// Block tile 256 (pairs) x BNT (B rows), the main loop of mfma_stage.hpp.
 // Two tile shapes. BNT = 256: a 256 x 256 tile, 256 accumulators per wave and
 // a ring of four 32 KiB stages (128 KiB of LDS), one workgroup per CU. BNT =
-// 128 (the default): a 256 x 128 tile, 128 accumulators per wave and three
-// 24 KiB stages (72 KiB), so that two workgroups share a CU and one's
-// epilogue, prologue and memory waits overlap the other's matrix work.
+// 128: a 256 x 128 tile, 128 accumulators per wave and three 24 KiB stages
+// (72 KiB), so that two workgroups share a CU and one's epilogue, prologue and
+// memory waits overlap the other's matrix work.
+constexpr int kBM = mfma_stage::kBM;
+constexpr int kBN = 256;
+constexpr int kBK = mfma_stage::kBK;
+constexpr int kGemmThreads = mfma_stage::kThreads;
+constexpr int kGroupM = 4;  // tile slots per group in the launch order
 #ifndef KOEMI_GEMM_BN
 #define KOEMI_GEMM_BN 256
 #endif
-template <int BNT>
-struct TileShape {
-    static constexpr int kNT = BNT / 64;                                 // n-tiles (32 wide) per wave
-    static constexpr int kStages = BNT == 256 ? 4 : 3;
-    static constexpr uint32_t kStageBytes = static_cast<uint32_t>(kBM + BNT) * kBK * 2u;
-    static constexpr int kCopies = 4 + kNT;                              // 1 KiB stage copies per wave and tile
-    static constexpr int kWgPerCu = BNT == 256 ? 1 : 2;
-    static constexpr int64_t kPartialFloats = static_cast<int64_t>(kBM) * BNT;
-};
 // Rows are 64 bytes; the K step of the fronts' MFMA shape check.
 constexpr int kKAlign = 64;
 
@@ -163,56 +148,6 @@ __global__ __launch_bounds__(kSchedThreads) void build_schedule_kernel(
         slot_row[slot] = lo + (slot - first_tile[lo_e]) * kBM;
         slot_end[slot] = hi;
     }
-}
-
-// Byte offset of K group g (16 bytes) of row r inside one operand stage.
-__device__ __forceinline__ int slot_swizzle(int r) { return (r >> 2) & 3; }
-__device__ __forceinline__ uint32_t stage_slot(int r, int g) {
-    return static_cast<uint32_t>(r * (kBK * 2) + ((g ^ slot_swizzle(r)) << 4));
-}
-
-// Asynchronous 16-byte-per-lane copy global -> LDS (lane l writes M0 + 16 l).
-// Issued through inline assembly so that the compiler does not order every
-// later LDS read after it (it cannot tell the ring stages apart); completion is
-// tracked explicitly with vmcnt, and ordering against other waves' reads of the
-// stage comes from the barrier (volatile asm is never reordered against other
-// volatile asm). M0 is restored afterwards.
-// The source is a wave-uniform 64-bit base (SGPRs) plus a per-lane 32-bit byte
-// offset, so issuing a copy costs no vector instructions.
-__device__ __forceinline__ void lds_dma16(uint32_t lds_byte_addr, const void* base, uint32_t byte_off) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "global_load_lds_dwordx4 %2, %3\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "s"(lds_byte_addr), "v"(byte_off), "s"(base));
-}
-
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-    const uint64_t u = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-    return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// Waits until at most n tiles of this wave's stage copies are outstanding
-// (CPT copies per tile and wave: eight for 256-wide tiles, six for 128-wide),
-// then joins the workgroup.
-template <int CPT>
-__device__ __forceinline__ void wait_tiles_and_sync(int64_t n) {
-    static_assert(CPT == 8 || CPT == 6, "stage copies per tile");
-    if (CPT == 8) {
-        if (n >= 3) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-        else if (n == 2) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-        else if (n == 1) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else {
-        if (n >= 1) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Logical tile -> (slot, column tile): groups of kGroupM slots, all column
@@ -353,18 +288,6 @@ __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void groupe
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
     const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * 4 * 1024);
     const uint32_t b_lds = __builtin_amdgcn_readfirstlane(lds0 + kOperandBytes + wave * NT * 1024);
-    // Copy i of a stage: i < 4 is A chunk i of this wave, i >= 4 B chunk i - 4.
-    auto issue_one = [&](int64_t kt, int stage, int i) {
-        if (i < 4)
-            lds_dma16(a_lds + stage * kStageBytes + i * 1024, a_base + kt * kBK, a_off[i]);
-        else
-            lds_dma16(b_lds + stage * kStageBytes + (i - 4) * 1024, b_base + kt * kBK, b_off[i - 4]);
-    };
-    auto issue = [&](int64_t kt, int stage) {
-#pragma unroll
-        for (int i = 0; i < CPT; ++i) issue_one(kt, stage, i);
-    };
-
     // Fragment rows: A rows of the wave's four m-tiles, B rows of its NT
     // n-tiles (GLU: NT / 2 gate, then NT / 2 value).
     const int fr = lane & 31;
@@ -396,90 +319,8 @@ __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void groupe
         b_row[t] = (GLU ? (t < NT / 2 ? wn * (BNT / 4) + t * 32 : BNT / 2 + wn * (BNT / 4) + (t - NT / 2) * 32)
                         : wn * (BNT / 2) + t * 32) + fr;
 
-    auto read_frags = [&](int64_t kt, int kk, bf16x8 (&af)[4], bf16x8 (&bfr)[NT]) {
-        const char* As = lds + (kt % kStages) * kStageBytes;
-        const char* Bs = As + kOperandBytes;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
-#pragma unroll
-        for (int t = 0; t < NT; ++t) bfr[t] = *reinterpret_cast<const bf16x8*>(Bs + stage_slot(b_row[t], kk * 2 + fg));
-    };
-    // Fragment f of a K step (4 + NT of them), in the order the MFMAs of the
-    // step consume them: A m-tile 0, B n-tiles 0 .. NT - 1, A m-tiles 1-3.
-    auto read_frag = [&](int64_t kt, int kk, int f, bf16x8 (&af)[4], bf16x8 (&bfr)[NT]) {
-        const char* As = lds + (kt % kStages) * kStageBytes;
-        if (f >= 1 && f <= NT)
-            bfr[f - 1] = *reinterpret_cast<const bf16x8*>(As + kOperandBytes + stage_slot(b_row[f - 1], kk * 2 + fg));
-        else {
-            const int t = f == 0 ? 0 : f - NT;
-            af[t] = *reinterpret_cast<const bf16x8*>(As + stage_slot(a_row[t], kk * 2 + fg));
-        }
-    };
-    auto mfma_one = [&](int j, const bf16x8 (&af)[4], const bf16x8 (&bfr)[NT]) {
-        acc[j / NT][j % NT] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j % NT], af[j / NT], acc[j / NT][j % NT], 0, 0, 0);
-    };
-
-    // K is a multiple of 64 and a partial tile has at least two K steps, so
-    // nk >= 2. The prologue issues K tiles 0 .. kStages - 2; step kt issues the
-    // copy of K tile kt + kStages - 1 (while there is one) into the stage
-    // consumed by step kt - 1, so up to kStages - 3 tiles are in flight behind
-    // the one waited for at every barrier; no copy is issued past the last
-    // tile, so none is outstanding at the epilogue.
-    const int64_t nk = static_cast<int64_t>(k_end - k_begin);
-#pragma unroll
-    for (int i = 0; i < kStages - 1; ++i)
-        if (i < nk) issue(i, i);
-    wait_tiles_and_sync<CPT>(min(nk, static_cast<int64_t>(kStages - 1)) - 1);
-    bf16x8 a0[4], b0[NT], a1[4], b1[NT];
-    read_frags(0, 0, a0, b0);
-    // Each MFMA is followed by memory instructions for later work (stage copies
-    // and fragment reads), pinned in place by scheduling barriers, so that they
-    // issue while the matrix pipe is busy instead of in a burst that leaves it
-    // idle. 256-wide tiles: 16 MFMAs per half step, a copy after every even one
-    // and a fragment read after every odd one. 128-wide: 8 MFMAs per half
-    // step, copy j after MFMA j (six) and fragment j - 2 after MFMA j >= 2.
-    constexpr int MK = 4 * NT;  // MFMAs per half step
-    auto k_step = [&](int64_t kt, auto copy_tag) {
-        constexpr bool kCopy = decltype(copy_tag)::value;
-        // Tile kt + 1 has landed for every wave (later copies may still be in
-        // flight: tiles kt + 2 .. min(kt + kStages - 2, nk - 1)), and every
-        // wave is done with the stage of tile kt - 1, which this step's copy
-        // overwrites.
-        if (kCopy) wait_tiles_and_sync<CPT>(kStages - 3);
-        else wait_tiles_and_sync<CPT>(max(min(nk - 2 - kt, static_cast<int64_t>(kStages - 3)), int64_t(0)));
-        const int sc = static_cast<int>((kt + kStages - 1) % kStages);
-#pragma unroll
-        for (int j = 0; j < MK; ++j) {
-            mfma_one(j, a0, b0);
-            if constexpr (NT == 4) {
-                if (j % 2 == 0) {
-                    if constexpr (kCopy) issue_one(kt + kStages - 1, sc, j / 2);
-                } else {
-                    read_frag(kt, 1, j / 2, a1, b1);
-                }
-            } else {
-                if constexpr (kCopy) {
-                    if (j < CPT) issue_one(kt + kStages - 1, sc, j);
-                }
-                if (j >= 2) read_frag(kt, 1, j - 2, a1, b1);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        const int64_t kn = min(kt + 1, nk - 1);  // the last step re-reads its own stage harmlessly
-#pragma unroll
-        for (int j = 0; j < MK; ++j) {
-            mfma_one(j, a1, b1);
-            if constexpr (NT == 4) {
-                if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
-            } else {
-                if (j >= 2) read_frag(kn, 0, j - 2, a0, b0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    int64_t kt = 0;
-    for (; kt + kStages - 1 < nk; ++kt) k_step(kt, std::true_type{});
-    for (; kt < nk; ++kt) k_step(kt, std::false_type{});
+    const int64_t nk = static_cast<int64_t>(k_end - k_begin);  // K is a multiple of 64: nk >= 2
+    mfma_stage::stage_loop<BNT, true>(lds, a_base, b_base, a_off, b_off, a_lds, b_lds, a_row, b_row, nk, acc);
 
     if constexpr (PARTIAL) {
         // Partial tile: the fp32 sums go to the workspace in accumulator order,

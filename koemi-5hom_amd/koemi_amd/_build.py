@@ -41,6 +41,7 @@ SOURCES = (
     "assoc_memory.hip",
     "herm_glue.hip",
     "linear_rows.hip",
+    "gated_projection.hip",
 )
 
 ARCH = "gfx950"

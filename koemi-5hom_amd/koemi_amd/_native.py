@@ -103,6 +103,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         (_P, c_int, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t,
          _P),
     ),
+    "koemi_gated_projection_scan_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
+    "koemi_gated_projection_scan": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
     "koemi_linear_rows": (
         c_int,
         (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, _P),

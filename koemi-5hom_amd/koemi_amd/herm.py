@@ -280,10 +280,15 @@ def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor,
                 out_bf16: Tensor | None):
     """The gate projection and the fused gates + scan: for a bf16 stack
     outside decode steps the projection's results are bf16 with the biases in
-    the GEMM epilogue (nn.Linear under bf16 autocast); otherwise fp32 results
-    without bias and the biases added inside the scan kernel."""
+    the GEMM epilogue (nn.Linear under bf16 autocast) — in one kernel with the
+    gates and the scan where the shape allows (whole 256-position tiles of a
+    sequence), else a library GEMM then the scan kernel; otherwise fp32
+    results without bias and the biases added inside the scan kernel."""
 
     w = p["gates_w"]
+    if w.dtype == torch.bfloat16 and recurrent.gated_projection_fits(u, w):
+        return recurrent.gated_projection_scan(u, w, p["gates_b16"], valid, working, with_bf16=with_bf16,
+                                               out_bf16=out_bf16)
     if w.dtype == torch.bfloat16 and not _few_rows(u, w):
         return recurrent.gated_scan(_linear_low(u, w, p["gates_b16"]), valid, working, width=width,
                                     with_bf16=with_bf16, out_bf16=out_bf16)

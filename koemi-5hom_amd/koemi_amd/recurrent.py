@@ -242,3 +242,71 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
             batch, length, width, _native.ptr(workspace), need, _native.stream_of(z.device),
         )
     return (states, states16) if with_bf16 else states
+
+
+def gated_projection_fits(inputs: Tensor, weight: Tensor) -> bool:
+    """Whether ``gated_projection_scan`` takes these shapes: bf16 ``inputs``
+    ``[B, L, K]`` and stacked ``weight`` ``[2 width, K]`` with L a multiple of
+    256, width of 128 and K of 64."""
+
+    return (inputs.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and inputs.ndim == 3
+            and weight.ndim == 2 and weight.shape[1] == inputs.shape[2] and inputs.shape[1] % 256 == 0
+            and (weight.shape[0] // 2) % 128 == 0 and weight.shape[0] % 2 == 0 and inputs.shape[2] % 64 == 0)
+
+
+def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, valid_mask: Tensor | None,
+                          initial: Tensor, *, with_bf16: bool = False,
+                          out_bf16: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
+    """The gates of model/memory.py:14-30 with their two projections, the
+    masking of network.py:307-309 and the scan of network.py:310, for a bf16
+    window under autocast, in one kernel (``koemi_gated_projection_scan``):
+    ``inputs`` ``[B, L, K]`` bf16, ``weight`` ``[2 width, K]`` bf16 (W_r
+    stacked over W_c), ``bias`` ``[2 width]`` bf16 (b_r then b_c) or None,
+    ``valid_mask`` ``[B, L]`` bool or None, ``initial`` ``[B, width]`` fp32.
+    Returns the states ``[B, L, width]`` fp32 and, with ``with_bf16``, their
+    bf16 copy (into ``out_bf16`` when given: a bf16 ``[B, L, width]`` view with
+    contiguous columns and evenly spaced rows). Shapes outside
+    ``gated_projection_fits`` raise; the projection's results are rounded to
+    bf16 after the bias (the autocast GEMM's output) before the gates."""
+
+    if not gated_projection_fits(inputs, weight):
+        raise DenseCudaValidationError("gated_projection_scan needs bf16 inputs [B, L, K] and weight [2 width, K] "
+                                       "with L % 256 == 0, width % 128 == 0 and K % 64 == 0")
+    if inputs.device.type != "cuda" or weight.device != inputs.device:
+        raise DenseCudaValidationError("inputs and weight must be on the same CUDA device")
+    batch, length, k = inputs.shape
+    width = weight.shape[0] // 2
+    if not isinstance(initial, Tensor) or initial.shape != (batch, width) or initial.dtype != torch.float32 \
+            or initial.device != inputs.device:
+        raise DenseCudaValidationError("initial must be a float32 [batch, width] tensor on the same device")
+    if valid_mask is not None and (valid_mask.dtype != torch.bool or valid_mask.shape != (batch, length)
+                                   or valid_mask.device != inputs.device):
+        raise DenseCudaValidationError("valid_mask must be a bool [batch, length] tensor on the same device")
+    if bias is not None and (bias.shape != (2 * width,) or bias.dtype != torch.bfloat16 or bias.device != inputs.device):
+        raise DenseCudaValidationError("bias must be a bf16 [2 width] tensor on the same device")
+    try:
+        _native.load_library()
+    except _native.NativeLibraryUnavailableError as error:
+        raise DenseCudaUnavailableError(str(error)) from error
+    x = inputs.contiguous()
+    w = weight.contiguous()
+    states = torch.empty((batch, length, width), device=x.device, dtype=torch.float32)
+    states16 = None
+    if with_bf16:
+        states16 = out_bf16 if out_bf16 is not None else torch.empty(states.shape, device=x.device,
+                                                                     dtype=torch.bfloat16)
+        if (states16.shape != states.shape or states16.dtype != torch.bfloat16 or states16.stride(2) != 1
+                or states16.stride(0) != length * states16.stride(1)):
+            raise DenseCudaValidationError("out_bf16 must be a bf16 [batch, length, width] view with evenly spaced rows")
+    if states.numel():
+        need = _native.query("koemi_gated_projection_scan_workspace_bytes", batch, length, width)
+        workspace = torch.empty(need, device=x.device, dtype=torch.uint8)
+        mask = valid_mask.contiguous() if valid_mask is not None else None
+        _native.call(
+            "koemi_gated_projection_scan",
+            _native.ptr(x), _native.ptr(w), _native.ptr(bias.contiguous()) if bias is not None else None,
+            _native.ptr(mask) if mask is not None else None, _native.ptr(initial.contiguous()), _native.ptr(states),
+            _native.ptr(states16), states16.stride(1) if states16 is not None else 0, batch, length, width, k,
+            _native.ptr(workspace), need, _native.stream_of(x.device),
+        )
+    return (states, states16) if with_bf16 else states

@@ -153,12 +153,16 @@ def test_c5_wavefront_prefill_equals_the_window_by_window_prefill(device, c5):
 def test_c5_sequence_prefill_matches_the_window_by_window_prefill(device, c5):
     """The sequence-parallel prefill (one HIP graph) at C5. Layer 0's carried
     state does not depend on any product whose rows change with the batching
-    (its expert FFN feeds only the next layer), so it equals the
-    window-by-window state bit for bit; the later layers and the logits carry
-    the bf16 rounding of products computed over other row sets (the split-K
-    expert tiles of a window against whole tiles of the sequence): within the
-    tolerances of the bf16 path above (measured 4.6e-3 relative Frobenius,
-    8.6e-3 max/scale). Ring bits and last tokens exact."""
+    (its expert FFN feeds only the next layer); the sequence path forms its
+    working state with the fused gate projection + scan kernel (its own MFMA
+    accumulation order, carries composed per 256-position tile) where the
+    window path takes the library GEMM and the scan kernel, so layer 0 agrees
+    within 1e-6 relative (1e-4 for what passes through a bf16 projection of
+    the state) rather than bit for bit. The later layers and the
+    logits carry the bf16 rounding of products computed over other row sets
+    (the split-K expert tiles of a window against whole tiles of the
+    sequence): within the tolerances of the bf16 path above (measured 6.1e-3
+    relative Frobenius, 1.0e-2 max/scale). Ring bits and last tokens exact."""
 
     settings, _, params = c5
     ids = workloads.config5().prefill_ids.to(device)
@@ -172,7 +176,16 @@ def test_c5_sequence_prefill_matches_the_window_by_window_prefill(device, c5):
     print(f"C5 sequence-parallel vs window-by-window logits: rel_frobenius={rel:.3e} max/scale={mx:.3e}", flush=True)
     assert rel <= 1e-2 and mx <= 2e-2
     for key, tensor in want_states[0].items():
-        assert torch.equal(seq.states[0][key], tensor), f"layer 0 {key}"
+        got0 = seq.states[0][key]
+        if tensor.dtype.is_floating_point:
+            rel0 = float((got0 - tensor).norm() / (tensor.norm() + 1e-30))
+            print(f"layer 0 {key}: rel_frobenius={rel0:.3e}", flush=True)
+            # the working state and what the scan feeds in fp32: 1e-6; what passes
+            # through the bf16 copy of the state and a bf16 projection (a value
+            # may round to the neighbouring bf16 value): 1e-4
+            assert rel0 <= (1e-6 if key in ("working", "basis", "normalizer") else 1e-4), f"layer 0 {key}"
+        else:
+            assert torch.equal(got0, tensor), f"layer 0 {key}"
     for layer, (st, exp) in enumerate(zip(seq.states, want_states)):
         for key in ("local_valid", "salient_valid", "last_token"):
             assert torch.equal(st[key], exp[key]), f"layer {layer} {key}"

@@ -189,6 +189,118 @@ def test_gated_scan_from_bf16_preactivations_equals_their_widening(device, b, le
     assert torch.equal(low, wide) and torch.equal(low16, wide16)
 
 
+def _exact_projection_case(seed, b, length, k, d, p, device):
+    """bf16 inputs and weights on grids fine enough that every product and
+    partial sum of the gate projection is exact in fp32 (u in {-3..3} / 8, W
+    in {-3..3} / 64: products are multiples of 2^-9 and |sums| <= 18 for K <=
+    1024, so 15 significant bits), so the projection does not depend on the
+    order of accumulation and every implementation forms the same
+    pre-activations."""
+    g = torch.Generator().manual_seed(seed)
+    u = (torch.randint(-3, 4, (b, length, k), generator=g) / 8.0).to(torch.bfloat16)
+    w = (torch.randint(-3, 4, (2 * d, k), generator=g) / 64.0).to(torch.bfloat16)
+    bias = (torch.randint(-8, 9, (2 * d,), generator=g) / 64.0).to(torch.bfloat16)
+    valid = torch.rand((b, length), generator=g) < p
+    valid[:, 255::256] = False  # masked positions at tile ends
+    h0 = torch.randn((b, d), generator=g)
+    return (t.to(device) for t in (u, w, bias, valid, h0))
+
+
+@pytest.mark.parametrize(
+    "b, length, k, d, p",
+    [
+        (2, 512, 256, 256, 0.9),     # two tiles per sequence, four ticket groups
+        (3, 768, 128, 384, 0.8),     # nine chains: one ticket group
+        (1, 256, 64, 128, 1.0),      # one tile, two K steps
+        (8, 2048, 1024, 1024, 0.9),  # C5 prefill: 512 tiles, two rounds of the chip
+    ],
+)
+def test_gated_projection_scan_matches_oracle(device, b, length, k, d, p):
+    """koemi_gated_projection_scan against the oracle's gates and float64
+    scan of the bf16-rounded pre-activations (exact projection), and against
+    koemi_gated_scan on the same pre-activations: the gates are the same
+    bits, the states differ only by how carries are composed (within 1e-5);
+    the bf16 copy is the states rounded, written into a column block."""
+    u, w, bias, valid, h0 = _exact_projection_case(b * 31 + length + d, b, length, k, d, p, device)
+    z = torch.addmm(bias.float(), u.reshape(-1, k).float(), w.float().t()).view(b, length, 2 * d)
+    z16 = z.to(torch.bfloat16)
+    wide = torch.zeros((b, length, 3 * d), device=device, dtype=torch.bfloat16)
+    got, got16 = recurrent.gated_projection_scan(u, w, bias, valid, h0, with_bf16=True, out_bf16=wide[..., d:2 * d])
+    ref = recurrent.gated_scan(z16, valid, h0, width=d)
+    torch.cuda.synchronize()
+    assert torch.equal(got16, got.to(torch.bfloat16))
+    assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
+    diff = (got - ref).abs().max().item()
+    select = lambda off: np.eye(2 * d)[off:off + d]
+    a, inc = oracle.recurrent_gates(z16.double().cpu().numpy(), select(0), np.zeros(d), select(d), np.zeros(d),
+                                    valid.cpu().numpy())
+    want = oracle.scan_sequential(a, inc, h0.double().cpu().numpy())
+    err = np.abs(got.cpu().numpy() - want).max()
+    print(f"gated projection scan b={b} L={length} K={k} d={d}: max_abs vs oracle {err:.3e}, "
+          f"vs gates+scan {diff:.3e}", flush=True)
+    assert err <= 1e-4
+    assert diff <= 1e-5
+
+
+def test_gated_projection_scan_random_weights_match_library_gemm_then_scan(device):
+    """C5 shape with normal inputs and nn.Linear-scale weights: the fused
+    kernel against hipBLASLt's bf16 GEMM (bias in the epilogue) then
+    koemi_gated_scan. The two GEMMs accumulate in different orders, so a
+    pre-activation can round to the neighbouring bf16 value (2^-8 relative);
+    the states then differ by at most a few 1e-3 and almost everywhere by
+    much less. Two calls in a row (the second with other inputs) check that
+    each call starts from cleared flags."""
+    g = torch.Generator(device=device).manual_seed(5)
+    b, length, k, d = 8, 2048, 1024, 1024
+    w = (torch.randn((2 * d, k), generator=g, device=device) * k ** -0.5).to(torch.bfloat16)
+    bias = (torch.randn((2 * d,), generator=g, device=device) * k ** -0.5).to(torch.bfloat16)
+    h0 = torch.randn((b, d), generator=g, device=device)
+    for call in range(2):
+        u = torch.randn((b, length, k), generator=g, device=device).to(torch.bfloat16)
+        valid = torch.rand((b, length), generator=g, device=device) < 0.9
+        got = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+        z16 = torch.addmm(bias, u.reshape(-1, k), w.t()).view(b, length, 2 * d)
+        ref = recurrent.gated_scan(z16, valid, h0, width=d)
+        torch.cuda.synchronize()
+        diff = (got - ref).abs()
+        big = (diff > 1e-4).float().mean().item()
+        print(f"call {call}: max_abs {diff.max().item():.3e}, mean {diff.mean().item():.3e}, "
+              f"share above 1e-4 {big:.2e}", flush=True)
+        assert diff.max().item() <= 2e-2
+        assert big <= 1e-3
+
+
+def test_gated_projection_scan_graph_replays_equal_eager(device):
+    """The kernel (its flag clearing included) captured in a HIP graph and
+    replayed three times, with eager work between the replays, gives the
+    eager call's bits each time: the carries do not depend on timing."""
+    u, w, bias, valid, h0 = _exact_projection_case(11, 4, 1024, 256, 256, 0.9, device)
+    eager = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    for _ in range(3):
+        recurrent.gated_projection_scan(u, w, bias, valid, h0 * 0.5)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
+def test_gated_projection_scan_rejects_unsupported_shapes(device):
+    u = torch.zeros((2, 200, 64), device=device, dtype=torch.bfloat16)
+    w = torch.zeros((256, 64), device=device, dtype=torch.bfloat16)
+    h0 = torch.zeros((2, 128), device=device)
+    assert not recurrent.gated_projection_fits(u, w)
+    with pytest.raises(dense.DenseCudaValidationError):
+        recurrent.gated_projection_scan(u, w, None, None, h0)
+
+
 def test_gated_scan_rejects_bad_columns(device):
     z = torch.zeros((2, 3, 10), device=device)
     h0 = torch.zeros((2, 4), device=device)
