@@ -10,8 +10,8 @@
 //
 // Here the stacked weight [W_r ; W_c] (bf16, [2F, K]) is multiplied on bf16
 // MFMA (the main loop of mfma_stage.hpp) in block tiles of 256 consecutive
-// positions of one sequence x 128 features: the B tile holds the 128
-// retention rows and the 128 candidate rows of the same features, so a lane's
+// positions of one sequence x 64 (or 128) features: the B tile holds the
+// retention rows and the candidate rows of the same features, so a lane's
 // accumulators hold, for one feature, the retention and candidate
 // pre-activations of sixteen positions, and the epilogue forms the gates and
 // scans them without the pre-activations leaving the registers:
@@ -50,15 +50,24 @@ using mfma_stage::kOperandBytes;
 using mfma_stage::slot_swizzle;
 using mfma_stage::uniform_ptr;
 
-constexpr int kGpRows = 256;      // positions per tile
-constexpr int kGpFeatures = 128;  // state features per tile (256 B rows: retention then candidate)
-constexpr int kGpBN = 2 * kGpFeatures;
+constexpr int kGpRows = 256;  // positions per tile
 constexpr int kGpThreads = mfma_stage::kThreads;
 constexpr int kGpKAlign = 64;
+constexpr int kGpWidthAlign = 128;  // features: a multiple of every tile width
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr int kMaxGroups = 8;
 
-using GpShape = mfma_stage::TileShape<kGpBN>;
+// Tile width: BNT B rows = BNT / 2 features (their retention rows, then their
+// candidate rows). 256 (the default): 128 features, 256 accumulators per wave,
+// one workgroup per CU. 128: 64 features, 128 accumulators per wave and two
+// workgroups per CU (measured no faster at the C5 shape: the two workgroups
+// of a CU run their phases in step, so one's epilogue does not hide under the
+// other's main loop).
+#ifndef KOEMI_GP_BN
+#define KOEMI_GP_BN 256
+#endif
+constexpr int kGpBN = KOEMI_GP_BN;
+static_assert(kGpBN == 128 || kGpBN == 256, "tile width");
 
 // Workspace: kMaxGroups ticket counters (128 bytes apart) and the error word
 // (2 KiB, cleared to zero before every launch), then per tile and feature the
@@ -75,10 +84,11 @@ constexpr int64_t kCounterWords = 512;
 struct GpWorkspace {
     size_t data_off, total;
 };
-inline GpWorkspace gp_workspace(int64_t tiles) {
+// One transfer word per feature of every tile: batch x length / 256 x width.
+inline GpWorkspace gp_workspace(int64_t batch, int64_t length, int64_t width) {
     GpWorkspace w;
     w.data_off = kCounterWords * sizeof(uint32_t);
-    w.total = w.data_off + static_cast<size_t>(tiles) * kGpFeatures * sizeof(uint64_t);
+    w.total = w.data_off + static_cast<size_t>(batch * (length / kGpRows) * width) * sizeof(uint64_t);
     return w;
 }
 
@@ -97,14 +107,16 @@ __device__ __forceinline__ void then(float& A, float& B, float a, float b) {
 }
 
 // The transfers of run q of m-tile mt of n-tile nt (retention accumulators
-// nt, candidate nt + 2, already turned into a and b): lo is the run of the
-// wave's lower half (positions 8q .. 8q + 3 of the m-tile), hi the upper
+// nt, candidate nt + NT / 2, already turned into a and b): lo is the run of
+// the wave's lower half (positions 8q .. 8q + 3 of the m-tile), hi the upper
 // half's (8q + 4 .. 8q + 7), the same in both halves after the swap.
-__device__ __forceinline__ void run_transfer(const f32x16 (&acc)[4][4], int nt, int mt, int q, float& loA, float& loB,
+template <int NT>
+__device__ __forceinline__ void run_transfer(const f32x16 (&acc)[4][NT], int nt, int mt, int q, float& loA, float& loB,
                                              float& hiA, float& hiB) {
-    float A = acc[mt][nt][4 * q], B = acc[mt][nt + 2][4 * q];
+    constexpr int NH = NT / 2;
+    float A = acc[mt][nt][4 * q], B = acc[mt][nt + NH][4 * q];
 #pragma unroll
-    for (int i = 1; i < 4; ++i) then(A, B, acc[mt][nt][4 * q + i], acc[mt][nt + 2][4 * q + i]);
+    for (int i = 1; i < 4; ++i) then(A, B, acc[mt][nt][4 * q + i], acc[mt][nt + NH][4 * q + i]);
     const auto sa = __builtin_amdgcn_permlane32_swap(__float_as_uint(A), __float_as_uint(A), false, false);
     const auto sb = __builtin_amdgcn_permlane32_swap(__float_as_uint(B), __float_as_uint(B), false, false);
     loA = __uint_as_float(sa[0]);
@@ -113,24 +125,28 @@ __device__ __forceinline__ void run_transfer(const f32x16 (&acc)[4][4], int nt, 
     hiB = __uint_as_float(sb[1]);
 }
 
-// One 256-position x 128-feature tile. Wave (wm, wn) holds positions
-// wm * 128 .. + 127 and features wn * 64 .. + 63 of the tile: accumulators
-// [m-tile][0..1] are the retention pre-activations of features wn * 64 + nt *
-// 32 + lane % 32, [m-tile][2..3] the candidate ones of the same features;
-// element v of lane l is position mt * 32 + 8 (v / 4) + 4 (l / 32) + v % 4 of
-// the wave's rows.
-__global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
+// One 256-position x BNT / 2-feature tile. Wave (wm, wn) holds positions
+// wm * 128 .. + 127 and features wn * WF .. + WF - 1 of the tile (WF = BNT / 4):
+// accumulators [m-tile][nt < NT / 2] are the retention pre-activations of
+// features wn * WF + nt * 32 + lane % 32, [m-tile][nt + NT / 2] the candidate
+// ones of the same features; element v of lane l is position mt * 32 +
+// 8 (v / 4) + 4 (l / 32) + v % 4 of the wave's rows.
+template <int BNT>
+__global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) void gated_projection_scan_kernel(
     const bf16* __restrict__ inputs, const bf16* __restrict__ weights, const bf16* __restrict__ biases,
     const uint8_t* __restrict__ valid, const float* __restrict__ initial, float* __restrict__ states,
     bf16* __restrict__ states16, int64_t s16_stride, int64_t L, int64_t F, int64_t K, int32_t n_ft, int32_t n_mt,
     int32_t groups, uint32_t* __restrict__ ws_words, uint64_t* __restrict__ ws_pairs) {
-    constexpr int NT = GpShape::kNT;
-    static_assert(NT == 4, "retention and candidate n-tiles");
-    __shared__ __attribute__((aligned(1024))) char lds[GpShape::kStages * GpShape::kStageBytes];
-    __shared__ float bias_sh[kGpBN];
+    using TS = mfma_stage::TileShape<BNT>;
+    constexpr int NT = TS::kNT;  // n-tiles per wave
+    constexpr int NH = NT / 2;   // of them retention (then as many candidate)
+    constexpr int FEAT = BNT / 2;
+    constexpr int WF = FEAT / 2;  // features per wave
+    __shared__ __attribute__((aligned(1024))) char lds[TS::kStages * TS::kStageBytes];
+    __shared__ float bias_sh[BNT];
     __shared__ uint8_t keep_sh[kGpRows];
-    __shared__ float wave_sh[2][64][2];    // the lower waves' transfers per feature (A, B)
-    __shared__ float carry_sh[2][kGpFeatures];  // the state before rows 0 and 128 of the tile
+    __shared__ float wave_sh[2][WF][2];     // the lower waves' transfers per feature (A, B)
+    __shared__ float carry_sh[2][FEAT];     // the state before rows 0 and 128 of the tile
     __shared__ uint32_t ticket_sh;
 
     const int tid = threadIdx.x;
@@ -151,11 +167,11 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
     const int32_t b = chain / n_ft, ft = chain % n_ft;
     const int64_t tix = static_cast<int64_t>(chain) * n_mt + m;
     const int64_t row0 = static_cast<int64_t>(b) * L + static_cast<int64_t>(m) * kGpRows;
-    const int64_t n0 = static_cast<int64_t>(ft) * kGpFeatures;
+    const int64_t n0 = static_cast<int64_t>(ft) * FEAT;
 
     // Stage copies (as the grouped GEMM's gate/value tile): A rows are the
-    // tile's 256 positions; waves 0-1 copy retention rows n0 .. n0 + 127,
-    // waves 2-3 the candidate rows F + n0 .. of the same features.
+    // tile's 256 positions; waves 0-1 copy the retention rows n0 .. n0 + FEAT
+    // - 1, waves 2-3 the candidate rows F + n0 .. of the same features.
     const bf16* a_base = static_cast<const bf16*>(uniform_ptr(inputs + row0 * K));
     const bf16* b_base = static_cast<const bf16*>(uniform_ptr(weights + ((wave >= 2 ? F : 0) + n0) * K));
     uint32_t a_off[4], b_off[NT];
@@ -169,7 +185,7 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
     for (int i = 0; i < NT; ++i) {
         const int r = (wave * NT + i) * 16 + (lane >> 2);
         const int gk = (lane & 3) ^ slot_swizzle(r);
-        b_off[i] = (static_cast<uint32_t>(r & (kGpFeatures - 1)) * static_cast<uint32_t>(K) + gk * 8) * 2u;
+        b_off[i] = (static_cast<uint32_t>(r & (FEAT - 1)) * static_cast<uint32_t>(K) + gk * 8) * 2u;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
     const uint32_t a_lds = __builtin_amdgcn_readfirstlane(lds0 + wave * 4 * 1024);
@@ -178,13 +194,13 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
 #pragma unroll
     for (int t = 0; t < 4; ++t) a_row[t] = wm * 128 + t * 32 + fl;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) b_row[t] = (t < 2 ? wn * 64 + t * 32 : kGpFeatures + wn * 64 + (t - 2) * 32) + fl;
+    for (int t = 0; t < NT; ++t) b_row[t] = (t < NH ? wn * WF + t * 32 : FEAT + wn * WF + (t - NH) * 32) + fl;
 
-    // Bias (thread t: retention bias of feature n0 + t for t < 128, else the
-    // candidate bias of feature n0 + t - 128) and keep flag of position t, read
-    // now so that their latency hides behind the main loop.
-    const float bias_mine =
-        biases ? to_f32(biases[(tid < kGpFeatures ? n0 + tid : F + n0 + tid - kGpFeatures)]) : 0.0f;
+    // Bias (thread t < FEAT: retention bias of feature n0 + t; FEAT <= t < BNT:
+    // candidate bias of feature n0 + t - FEAT) and keep flag of position t,
+    // read now so that their latency hides behind the main loop.
+    float bias_mine = 0.0f;
+    if (biases != nullptr && tid < BNT) bias_mine = to_f32(biases[tid < FEAT ? n0 + tid : F + n0 + tid - FEAT]);
     const uint8_t keep_mine = valid ? valid[row0 + tid] : uint8_t(1);
 
     f32x16 acc[4][NT];
@@ -194,36 +210,41 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
         for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    mfma_stage::stage_loop<kGpBN, false>(lds, a_base, b_base, a_off, b_off, a_lds, b_lds, a_row, b_row, K / kBK, acc);
+    mfma_stage::stage_loop<BNT, false>(lds, a_base, b_base, a_off, b_off, a_lds, b_lds, a_row, b_row, K / kBK, acc);
 
-    bias_sh[tid] = bias_mine;
+    if (tid < BNT) bias_sh[tid] = bias_mine;
     keep_sh[tid] = keep_mine;
     __syncthreads();
 
-    // 1. Gates in place: acc[mt][nt] <- a, acc[mt][nt + 2] <- b.
+    // 1. Gates in place: acc[mt][nt] <- a, acc[mt][nt + NH] <- b (the keep flag
+    // of a position serves its NH features).
+    float br[NH], bc[NH];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int fi = wn * 64 + nt * 32 + fl;
-        const float br = bias_sh[fi], bc = bias_sh[kGpFeatures + fi];
+    for (int nt = 0; nt < NH; ++nt) {
+        br[nt] = bias_sh[wn * WF + nt * 32 + fl];
+        bc[nt] = bias_sh[FEAT + wn * WF + nt * 32 + fl];
+    }
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            __builtin_amdgcn_sched_barrier(0);
+    for (int mt = 0; mt < 4; ++mt) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int t = wm * 128 + mt * 32 + 8 * (v / 4) + 4 * hf + (v % 4);
+        for (int v = 0; v < 16; ++v) {
+            const bool keep = keep_sh[wm * 128 + mt * 32 + 8 * (v / 4) + 4 * hf + (v % 4)] != 0;
+#pragma unroll
+            for (int nt = 0; nt < NH; ++nt) {
                 float a, bb;
-                gate_pair(round_bf16(acc[mt][nt][v] + br), round_bf16(acc[mt][nt + 2][v] + bc), 0.0f, 0.0f,
-                          keep_sh[t] != 0, a, bb);
+                gate_pair(round_bf16(acc[mt][nt][v] + br[nt]), round_bf16(acc[mt][nt + NH][v] + bc[nt]), 0.0f, 0.0f,
+                          keep, a, bb);
                 acc[mt][nt][v] = a;
-                acc[mt][nt + 2][v] = bb;
+                acc[mt][nt + NH][v] = bb;
             }
         }
     }
 
-    // 2. The wave's transfer over its 128 positions, per feature (both n-tiles).
-    float WA[2], WB[2];
+    // 2. The wave's transfer over its 128 positions, per feature.
+    float WA[NH], WB[NH];
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NH; ++nt) {
         float A = 1.0f, B = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -237,32 +258,32 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
     }
     if (wm == 0 && hf == 0) {
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NH; ++nt) {
             wave_sh[wn][nt * 32 + fl][0] = WA[nt];
             wave_sh[wn][nt * 32 + fl][1] = WB[nt];
         }
     }
     __syncthreads();
 
-    // 3. The carry, by the upper waves: lane l takes feature wn * 64 + l
-    // (n-tile l / 32, the half's own copy of the wave transfer).
-    if (wm == 1) {
-        const int j = lane;                    // feature within the wave's 64
+    // 3. The carry, by the upper waves: lane j < WF takes feature wn * WF + j
+    // (n-tile j / 32, the half's own copy of the wave transfer).
+    const int j = lane;
+    if (wm == 1 && j < WF) {
         const float A0 = wave_sh[wn][j][0], B0 = wave_sh[wn][j][1];
-        const float A1 = hf ? WA[1] : WA[0], B1 = hf ? WB[1] : WB[0];
+        const float A1 = (NH == 2 && hf) ? WA[NH - 1] : WA[0], B1 = (NH == 2 && hf) ? WB[NH - 1] : WB[0];
         const float TA = A0 * A1, TB = fmaf(A1, B0, B1);  // the tile's transfer
+        const int64_t feat = wn * WF + j;
         if (m + 1 < n_mt) {  // the last tile's transfer is nobody's carry
             const uint64_t pair = static_cast<uint64_t>(__float_as_uint(TA)) |
                                   (static_cast<uint64_t>(__float_as_uint(TB)) << 32);
-            __hip_atomic_store(ws_pairs + tix * kGpFeatures + wn * 64 + j, pair, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ws_pairs + tix * FEAT + feat, pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         // The carry: the initial state through the transfers of tiles 0 .. m - 1
         // in order (the same operations whatever the timing, so the states are
         // a deterministic function of the inputs).
-        float C = initial[static_cast<int64_t>(b) * F + n0 + wn * 64 + j];
+        float C = initial[static_cast<int64_t>(b) * F + n0 + feat];
         for (int32_t p = 0; p < m; ++p) {
-            const uint64_t* src = ws_pairs + (static_cast<int64_t>(chain) * n_mt + p) * kGpFeatures + wn * 64 + j;
+            const uint64_t* src = ws_pairs + (static_cast<int64_t>(chain) * n_mt + p) * FEAT + feat;
             uint64_t pair;
             uint32_t spins = 0;
             while ((pair = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == kEmpty &&
@@ -276,16 +297,16 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
             }
             C = fmaf(__uint_as_float(static_cast<uint32_t>(pair)), C, __uint_as_float(static_cast<uint32_t>(pair >> 32)));
         }
-        carry_sh[0][wn * 64 + j] = C;
-        carry_sh[1][wn * 64 + j] = fmaf(A0, C, B0);
+        carry_sh[0][feat] = C;
+        carry_sh[1][feat] = fmaf(A0, C, B0);
     }
     __syncthreads();
 
     // 4. States: each run from its carry (composed from the wave's carry by
     // the run transfers in order), stepped through its four positions.
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-        const int fi = wn * 64 + nt * 32 + fl;
+    for (int nt = 0; nt < NH; ++nt) {
+        const int fi = wn * WF + nt * 32 + fl;
         const int64_t f = n0 + fi;
         float h = carry_sh[wm][fi];
 #pragma unroll
@@ -298,7 +319,7 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int v = 4 * q + i;
-                x = fmaf(acc[mt][nt][v], x, acc[mt][nt + 2][v]);
+                x = fmaf(acc[mt][nt][v], x, acc[mt][nt + NH][v]);
                 const int64_t row = row0 + wm * 128 + mt * 32 + 8 * q + 4 * hf + i;
                 states[row * F + f] = x;
                 if (states16) states16[row * s16_stride + f] = static_cast<bf16>(x);
@@ -314,8 +335,8 @@ __global__ __launch_bounds__(kGpThreads, 1) void gated_projection_scan_kernel(
 using namespace koemi;
 
 extern "C" size_t koemi_gated_projection_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width) {
-    if (batch <= 0 || length <= 0 || width <= 0 || length % kGpRows || width % kGpFeatures) return 0;
-    return gp_workspace(batch * (length / kGpRows) * (width / kGpFeatures)).total;
+    if (batch <= 0 || length <= 0 || width <= 0 || length % kGpRows || width % kGpWidthAlign) return 0;
+    return gp_workspace(batch, length, width).total;
 }
 
 extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weights, const void* biases,
@@ -325,11 +346,11 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
                                            size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1 || input_width < 1)
         return fail(KOEMI_ERR_INVALID, "gated projection scan needs non-negative batch and length and positive widths");
-    if (length % kGpRows || width % kGpFeatures || input_width % kGpKAlign)
+    if (length % kGpRows || width % kGpWidthAlign || input_width % kGpKAlign)
         return fail(KOEMI_ERR_UNSUPPORTED,
                     "gated projection scan needs length %% %d == 0, width %% %d == 0 and input width %% %d == 0 "
                     "(got %lld, %lld, %lld)",
-                    kGpRows, kGpFeatures, kGpKAlign, static_cast<long long>(length), static_cast<long long>(width),
+                    kGpRows, kGpWidthAlign, kGpKAlign, static_cast<long long>(length), static_cast<long long>(width),
                     static_cast<long long>(input_width));
     if (batch * length == 0) return KOEMI_OK;
     if (!inputs || !weights || !initial || !states || !workspace)
@@ -339,11 +360,11 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
     if (bf16_row_stride == 0) bf16_row_stride = width;
     if (states_bf16 != nullptr && bf16_row_stride < width)
         return fail(KOEMI_ERR_INVALID, "gated projection scan: the bf16 row stride is below the width");
-    const int64_t n_mt = length / kGpRows, n_ft = width / kGpFeatures;
+    const int64_t n_mt = length / kGpRows, n_ft = width / (kGpBN / 2);
     const int64_t chains = batch * n_ft, tiles = chains * n_mt;
     if (tiles > 0x7fffffffLL || input_width > (1LL << 22) || width > (1LL << 20))
         return fail(KOEMI_ERR_UNSUPPORTED, "gated projection scan shape too large");
-    const GpWorkspace w = gp_workspace(tiles);
+    const GpWorkspace w = gp_workspace(batch, length, width);
     if (workspace_bytes < w.total)
         return fail(KOEMI_ERR_INVALID, "gated projection scan workspace too small: need %zu bytes", w.total);
     int groups = kMaxGroups;
@@ -354,7 +375,7 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
     hipLaunchKernelGGL(gp_clear_kernel, dim3(static_cast<uint32_t>((clear_words + 255) / 256)), dim3(256), 0, s, words,
                        clear_words);
     if (int st = check_launch("gated projection scan (clear)")) return st;
-    hipLaunchKernelGGL(gated_projection_scan_kernel, dim3(static_cast<uint32_t>(tiles)), dim3(kGpThreads), 0, s,
+    hipLaunchKernelGGL(gated_projection_scan_kernel<kGpBN>, dim3(static_cast<uint32_t>(tiles)), dim3(kGpThreads), 0, s,
                        static_cast<const bf16*>(inputs), static_cast<const bf16*>(weights),
                        static_cast<const bf16*>(biases), valid, initial, states, static_cast<bf16*>(states_bf16),
                        bf16_row_stride, length, width, input_width, static_cast<int32_t>(n_ft),
