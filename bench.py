@@ -653,7 +653,21 @@ def kernel_rows(args, extra: list, device, stream, timer, kernels: dict) -> None
         ms = timer.per_launch_ms([lambda: recurrent.recurrent_scan(ug, *wts, vg)], 2, max(3, iters // 4))
         kernels["C3g.recurrent_scan"] = {"ms": round(ms, 5), "tokens_per_s": round(32 * 4096 / (ms / 1000.0)),
                                          "note": "the gate GEMMs, then the gates formed inside the affine scan"}
-        del ug, wts, vg
+        # The same step for a bf16 window under autocast (the HERM block's case):
+        # the gate projection on bf16 MFMA with the gates and the scan in its
+        # epilogue, the pre-activations never in memory (koemi_gated_projection_scan).
+        ub = ug.to(torch.bfloat16)
+        del ug
+        wb = torch.cat((wts[0], wts[2])).to(torch.bfloat16)
+        bb = torch.cat((wts[1], wts[3])).to(torch.bfloat16)
+        h0g = torch.zeros((32, 1024), device=device)
+        ms = timer.per_launch_ms([lambda: recurrent.gated_projection_scan(ub, wb, bb, vg, h0g, with_bf16=True)], 2,
+                                 max(3, iters // 4))
+        kernels["C3g.gated_projection_scan_bf16"] = {
+            "ms": round(ms, 5), "TFLOP/s": round(C3G_FLOP / ms / 1e9, 1),
+            "frac_mfma_bf16": round(C3G_FLOP / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "note": "bf16 inputs and weights; fp32 states and their bf16 copy written; one kernel (+ its workspace clear)"}
+        del ub, wb, bb, wts, vg
 
 
 

@@ -194,7 +194,9 @@ int koemi_moe_expert_counts(const void* assignments, int assignment_dtype,
  * sorted_experts = key; sorted_context[i] = context[sorted_rows[i]] for
  * i < segment_offsets[E], zero afterwards. pair_weights [tokens, top_k] fp32
  * (or NULL) is permuted the same way into sorted_weights (0 past the valid
- * pairs). Context dtype F32/F16/BF16; assignments I32/I64. expert_count <= 4095. */
+ * pairs). Context dtype F32/F16/BF16; assignments I32/I64. expert_count <= 4095.
+ * sorted_context may be NULL: only the indices are formed (for
+ * koemi_moe_grouped_mlp_indexed, which reads the context rows by sorted_rows). */
 size_t koemi_moe_permute_workspace_bytes(int64_t tokens, int64_t top_k, int64_t expert_count);
 int koemi_moe_permute(const void* context, int context_dtype, const void* assignments,
                       int assignment_dtype, const uint8_t* valid_mask, const float* pair_weights,
@@ -220,6 +222,22 @@ int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* sorted_expe
                           const void* output_biases, void* output, int64_t pairs, int64_t width,
                           int64_t hidden, int64_t expert_count, int dtype, void* workspace,
                           size_t workspace_bytes, koemi_stream_t stream);
+
+/* koemi_moe_grouped_mlp without the sorted copy of the context (no
+ * counterpart in the reference, whose permute_topk always gathers it): pair i
+ * reads row sorted_rows[i] (clamped to [0, tokens)) of context [tokens,
+ * width], as koemi_moe_permute's sorted_rows gives it, straight into the first
+ * GEMM's operand tiles. bf16 only, width and hidden multiples of 64, 16-byte
+ * aligned operands, tokens * width < 2^31; the workspace of
+ * koemi_moe_grouped_mlp_workspace_bytes(pairs, width, hidden, expert_count,
+ * KOEMI_BF16). The outputs equal koemi_moe_grouped_mlp's on the gathered
+ * context bit for bit. */
+int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens, const int64_t* sorted_rows,
+                                  const int64_t* segment_offsets, const void* gate_weights, const void* gate_biases,
+                                  const void* value_weights, const void* value_biases, const void* output_weights,
+                                  const void* output_biases, void* output, int64_t pairs, int64_t width,
+                                  int64_t hidden, int64_t expert_count, void* workspace, size_t workspace_bytes,
+                                  koemi_stream_t stream);
 
 /* Salient-memory ring update, LocalKeyValueMemory.salient_tail of
  * model/memory.py:431-455. Per batch row, the carried entries [S] followed by

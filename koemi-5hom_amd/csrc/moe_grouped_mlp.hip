@@ -209,7 +209,8 @@ __device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uin
 // concurrently running tiles in that XCD's L2.
 template <bool GLU, bool PARTIAL, int BNT>
 __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void grouped_gemm_bf16_kernel(
-    const bf16* __restrict__ A, const bf16* __restrict__ W0, const bf16* __restrict__ W1,
+    const bf16* __restrict__ A, const int64_t* __restrict__ a_index, int64_t a_count,
+    const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
     const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
@@ -266,8 +267,11 @@ __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void groupe
     // bases (the entry point bounds n_out * K; K * 256 is smaller). GLU: waves
     // 0-1 copy gate rows, waves 2-3 value rows. A partial tile runs K steps
     // [k_begin, k_end): the bases start there.
+    // a_index (GEMM 1 reading the unsorted context): A row i of the tile is
+    // context row a_index[row0 + i] (clamped to [0, a_count)), so the sorted
+    // copy of the context is never built; the base is then the context itself.
     const int64_t k0 = static_cast<int64_t>(k_begin) * kBK;
-    const bf16* a_base = static_cast<const bf16*>(uniform_ptr(A + row0 * K + k0));
+    const bf16* a_base = static_cast<const bf16*>(uniform_ptr(A + (a_index ? 0 : row0 * K) + k0));
     const bf16* b_base = static_cast<const bf16*>(
         uniform_ptr(((GLU && wave >= 2) ? W1 : W0) + static_cast<int64_t>(e) * n_out * K + k0));
     const int a_rows = static_cast<int>(row_end - row0);
@@ -276,7 +280,9 @@ __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void groupe
     for (int i = 0; i < 4; ++i) {
         const int r = (wave * 4 + i) * 16 + (lane >> 2);
         const int g = (lane & 3) ^ slot_swizzle(r);
-        a_off[i] = (static_cast<uint32_t>(min(r, a_rows - 1)) * static_cast<uint32_t>(K) + g * 8) * 2u;
+        int64_t ar = min(r, a_rows - 1);
+        if (a_index) ar = min(max(a_index[row0 + ar], int64_t(0)), a_count - 1);
+        a_off[i] = (static_cast<uint32_t>(ar) * static_cast<uint32_t>(K) + g * 8) * 2u;
     }
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
@@ -597,7 +603,8 @@ constexpr int64_t kSkinnyMaxRowsPerExpert = 64;  // average over experts below w
 
 template <bool GLU>
 __global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
-    const bf16* __restrict__ a, const bf16* __restrict__ w0, const bf16* __restrict__ w1,
+    const bf16* __restrict__ a, const int64_t* __restrict__ a_index, int64_t a_count,
+    const bf16* __restrict__ w0, const bf16* __restrict__ w1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ c,
     const int64_t* __restrict__ offsets, int64_t n_out, int64_t K, int64_t col_groups, int64_t experts,
     int64_t pairs) {
@@ -629,7 +636,9 @@ __global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
     for (int64_t pass = 0; pass < count; pass += 32) {
         const int64_t rows = count - pass < 32 ? count - pass : 32;
         const bool aok = r < rows;
-        const bf16* ar = a + (row0 + pass + (aok ? r : 0)) * K + 32 * half;
+        int64_t arow = row0 + pass + (aok ? r : 0);
+        if (a_index) arow = min(max(a_index[arow], int64_t(0)), a_count - 1);  // a row of the unsorted context
+        const bf16* ar = a + arow * K + 32 * half;
         f32x16 acc[kMats];
 #pragma unroll
         for (int m = 0; m < kMats; ++m)
@@ -741,9 +750,10 @@ int64_t device_cus() {
     return n;
 }
 
-int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* bg, const void* Wv, const void* bv,
-             const void* Wo, const void* bo, void* y, int64_t P, int64_t D, int64_t Hd, int64_t E,
-             const MlpWorkspace& ws, char* base, hipStream_t s) {
+// x_index (or null): GEMM 1 reads context row x_index[i] (of x_rows) for pair i.
+int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_t* offsets, const void* Wg,
+             const void* bg, const void* Wv, const void* bv, const void* Wo, const void* bo, void* y, int64_t P,
+             int64_t D, int64_t Hd, int64_t E, const MlpWorkspace& ws, char* base, hipStream_t s) {
     bf16* H = reinterpret_cast<bf16*>(base + ws.hidden_off);
     int32_t* slot_expert = reinterpret_cast<int32_t*>(base + ws.slot_expert_off);
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
@@ -757,7 +767,8 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     if (P <= kSkinnyMaxRowsPerExpert * E && E * ((Hd > D ? Hd : D) / kSkinnyCols) <= 0x7fffffffLL) {
         const int64_t groups1 = Hd / kSkinnyCols, groups2 = D / kSkinnyCols;
         hipLaunchKernelGGL(skinny_gemm_kernel<true>, dim3(static_cast<unsigned>(E * groups1)),
-                           dim3(kSkinnyWaves * kWave), 0, s, static_cast<const bf16*>(x), static_cast<const bf16*>(Wg),
+                           dim3(kSkinnyWaves * kWave), 0, s, static_cast<const bf16*>(x), x_index, x_rows,
+                           static_cast<const bf16*>(Wg),
                            static_cast<const bf16*>(Wv), static_cast<const bf16*>(bg), static_cast<const bf16*>(bv),
                            H, offsets, Hd, D, groups1, E, P);
         int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
@@ -765,7 +776,8 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         // the output GEMM's launch also zeroes the rows past the valid pairs (extra workgroups)
         const int64_t tail_wgs = P < 64 ? P : 64;
         hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2 + tail_wgs)),
-                           dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const bf16*>(Wo),
+                           dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const int64_t*>(nullptr), P,
+                           static_cast<const bf16*>(Wo),
                            static_cast<const bf16*>(Wo), static_cast<const bf16*>(bo), static_cast<const bf16*>(bo),
                            static_cast<bf16*>(y), offsets, D, Hd, groups2, E, P);
         return check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
@@ -779,18 +791,18 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
     const uint32_t rounds = static_cast<uint32_t>(device_cus() * TileShape<BNT>::kWgPerCu);
     // Whole tiles, then the partial tiles of the split plan (if any; every
     // workgroup exits otherwise), then their sums.
-    auto launch = [&](auto kernel, auto partial_kernel, auto fixup, const bf16* a, const void* w0, const void* w1,
-                      const void* b0, const void* b1, bf16* c, int64_t n_out, int64_t K, int64_t n_tiles,
-                      const char* what) {
+    auto launch = [&](auto kernel, auto partial_kernel, auto fixup, const bf16* a, const int64_t* a_index,
+                      int64_t a_count, const void* w0, const void* w1, const void* b0, const void* b1, bf16* c,
+                      int64_t n_out, int64_t K, int64_t n_tiles, const char* what) {
         const int64_t whole_grid = (slots * n_tiles + 7) / 8 * 8;
         if (whole_grid > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid)), dim3(kGemmThreads), 0, s, a,
-                           static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid)), dim3(kGemmThreads), 0, s, a, a_index,
+                           a_count, static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
                            static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
                            partial, rounds);
         int st2 = check_launch(what);
         if (st2 != KOEMI_OK) return st2;
-        hipLaunchKernelGGL(partial_kernel, dim3(kMaxSplitUnits), dim3(kGemmThreads), 0, s, a,
+        hipLaunchKernelGGL(partial_kernel, dim3(kMaxSplitUnits), dim3(kGemmThreads), 0, s, a, a_index, a_count,
                            static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
                            static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
                            partial, rounds);
@@ -803,11 +815,12 @@ int run_mfma(const void* x, const int64_t* offsets, const void* Wg, const void* 
         return check_launch(what);
     };
     st = launch(grouped_gemm_bf16_kernel<true, false, BNT>, grouped_gemm_bf16_kernel<true, true, BNT>,
-                split_fixup_kernel<true, BNT>, static_cast<const bf16*>(x), Wg, Wv, bg, bv, H, Hd, D,
+                split_fixup_kernel<true, BNT>, static_cast<const bf16*>(x), x_index, x_rows, Wg, Wv, bg, bv, H, Hd, D,
                 (Hd + BNT / 2 - 1) / (BNT / 2), "koemi_moe_grouped_mlp(gemm1)");
     if (st != KOEMI_OK) return st;
     st = launch(grouped_gemm_bf16_kernel<false, false, BNT>, grouped_gemm_bf16_kernel<false, true, BNT>,
-                split_fixup_kernel<false, BNT>, H, Wo, Wo, bo, bo, static_cast<bf16*>(y), D, Hd, (D + BNT - 1) / BNT,
+                split_fixup_kernel<false, BNT>, H, static_cast<const int64_t*>(nullptr), P, Wo, Wo, bo, bo,
+                static_cast<bf16*>(y), D, Hd, (D + BNT - 1) / BNT,
                 "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
     hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
@@ -852,8 +865,9 @@ extern "C" int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* 
     if (mfma_shape(width, hidden, dtype) && !aligned)
         return fail(KOEMI_ERR_INVALID, "grouped MLP bf16 operands must be 16-byte aligned");
     if (mfma_shape(width, hidden, dtype))
-        return run_mfma(sorted_context, segment_offsets, gate_weights, gate_biases, value_weights, value_biases,
-                        output_weights, output_biases, output, pairs, width, hidden, expert_count, ws, base, s);
+        return run_mfma(sorted_context, nullptr, pairs, segment_offsets, gate_weights, gate_biases, value_weights,
+                        value_biases, output_weights, output_biases, output, pairs, width, hidden, expert_count, ws,
+                        base, s);
     float* H = reinterpret_cast<float*>(base + ws.hidden_off);
     switch (dtype) {
         case KOEMI_F32:
@@ -869,4 +883,35 @@ extern "C" int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* 
                                   value_weights, value_biases, output_weights, output_biases, output, pairs, width,
                                   hidden, expert_count, H, s);
     }
+}
+
+extern "C" int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens, const int64_t* sorted_rows,
+                                             const int64_t* segment_offsets, const void* gate_weights,
+                                             const void* gate_biases, const void* value_weights,
+                                             const void* value_biases, const void* output_weights,
+                                             const void* output_biases, void* output, int64_t pairs, int64_t width,
+                                             int64_t hidden, int64_t expert_count, void* workspace,
+                                             size_t workspace_bytes, koemi_stream_t stream) {
+    if (pairs < 0 || tokens < 1 || width < 1 || hidden < 1 || expert_count < 1)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP needs positive tokens, width, hidden and expert_count");
+    if (!mfma_shape(width, hidden, KOEMI_BF16))
+        return fail(KOEMI_ERR_UNSUPPORTED, "the indexed grouped MLP needs width and hidden multiples of %d", kKAlign);
+    if (pairs == 0) return KOEMI_OK;
+    if (!context || !sorted_rows || !segment_offsets || !gate_weights || !gate_biases || !value_weights ||
+        !value_biases || !output_weights || !output_biases || !output)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP received a null pointer");
+    if (tokens * width > 0x7fffffffLL)  // 32-bit byte offsets of context rows
+        return fail(KOEMI_ERR_UNSUPPORTED, "the indexed grouped MLP needs tokens * width < 2^31");
+    const MlpWorkspace ws = mlp_workspace(pairs, width, hidden, expert_count, KOEMI_BF16);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP workspace too small: need %zu bytes", ws.total);
+    const bool aligned = reinterpret_cast<uintptr_t>(context) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(gate_weights) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(value_weights) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(output_weights) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(output) % 16 == 0;
+    if (!aligned) return fail(KOEMI_ERR_INVALID, "grouped MLP bf16 operands must be 16-byte aligned");
+    return run_mfma(context, sorted_rows, tokens, segment_offsets, gate_weights, gate_biases, value_weights,
+                    value_biases, output_weights, output_biases, output, pairs, width, hidden, expert_count, ws,
+                    static_cast<char*>(workspace), as_stream(stream));
 }

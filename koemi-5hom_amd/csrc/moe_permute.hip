@@ -456,7 +456,7 @@ extern "C" int koemi_moe_permute(const void* context, int context_dtype, const v
     if (!index_dtype(assignment_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "assignments must be int32 or int64");
     if ((pair_weights == nullptr) != (sorted_weights == nullptr))
         return fail(KOEMI_ERR_INVALID, "pair_weights and sorted_weights must both be given or both be null");
-    if (!context || !assignments || !valid_mask || !sorted_context || !sorted_rows || !sorted_experts || !segment_offsets)
+    if (!context || !assignments || !valid_mask || !sorted_rows || !sorted_experts || !segment_offsets)
         return fail(KOEMI_ERR_INVALID, "permute received a null pointer");
     const PermuteWorkspace ws = permute_workspace(tokens, top_k, expert_count);
     if (!workspace || workspace_bytes < ws.total)
@@ -473,6 +473,7 @@ extern "C" int koemi_moe_permute(const void* context, int context_dtype, const v
                  : run_index_phase<int64_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
                                             segment_offsets, sorted_weights, counts, dest, pairs, top_k, expert_count, s);
     if (st != KOEMI_OK) return st;
+    if (sorted_context == nullptr) return KOEMI_OK;  // the indices only (the caller reads rows by sorted_rows)
     const int64_t* offsets_end = segment_offsets + expert_count;
     switch (context_dtype) {
         case KOEMI_F32: return run_gather<float>(context, dest, offsets_end, sorted_context, tokens, top_k, width, s);

@@ -463,12 +463,20 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
                                            validate=False)
         weights = None
     moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
+    # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
+    # permutation's indices (no sorted copy of the context)
+    indexed = moe_in.dtype == torch.bfloat16 and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
     permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
-                                pair_weights=weights, validate=False)
+                                pair_weights=weights, validate=False, gather=not indexed)
     sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
     sorted_weights = permuted[4] if weights is not None else None
-    expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"], p["gate_b"],
-                                                  p["up_w"], p["up_b"], p["down_w"], p["down_b"], validate=False)
+    if indexed:
+        expert_out = moe.grouped_expert_mlp_indexed(moe_in, sorted_rows, offsets, p["gate_w"], p["gate_b"],
+                                                    p["up_w"], p["up_b"], p["down_w"], p["down_b"])
+    else:
+        expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"],
+                                                      p["gate_b"], p["up_w"], p["up_b"], p["down_w"], p["down_b"],
+                                                      validate=False)
     update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
                               pair_weights=sorted_weights, validate=False)
     final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
@@ -680,7 +688,8 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
 
 
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
-                   context: Tensor | None = None, *, with_logits: bool = True
+                   context: Tensor | None = None, *, with_logits: bool = True,
+                   token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None
                    ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
     """One block over a whole sequence of windows at once: forward_parallel
     (network.py:176-197) of a single block, i.e. ``block_window`` applied to
@@ -698,8 +707,9 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     associative memory runs per window from the state the previous windows
     left (``associative_scan_read_windows``). The results equal the
     window-by-window ones up to floating-point rounding (the library GEMMs
-    see more rows). Returns (logits or None, final context, next state,
-    surprise [B, L]).
+    see more rows). ``token_context``: ``_token_context``'s four outputs when
+    the caller formed them (a stack, once for all layers). Returns (logits or
+    None, final context, next state, surprise [B, L]).
     """
 
     ids = ids.contiguous()
@@ -709,7 +719,9 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
         raise ValueError("block_sequence needs a length that is a multiple of scan_chunk")
     windows = length // chunk
     rows = batch * windows
-    previous, last_token, valid, targets = _token_context(ids, None, state["last_token"])
+    if token_context is None:
+        token_context = _token_context(ids, None, state["last_token"])
+    previous, last_token, valid, targets = token_context
     source = functional.embedding(ids, p["embedding"]) if context is None else context
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
@@ -766,15 +778,20 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
 def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
                    states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
     """``prefill`` computed layer by layer with ``block_sequence``: each layer
-    over the whole sequence before the next. Returns the last layer's logits
-    of every position and the next states."""
+    over the whole sequence before the next. The token context (validity,
+    previous tokens, surprise targets) is formed once for all layers: every
+    layer sees the same ids and carries the same last token. Returns the last
+    layer's logits of every position and the next states."""
 
+    ids = ids.contiguous()
+    token_context = _token_context(ids, None, states[0]["last_token"])
     context = None
     next_states = []
     logits = None
     for layer, (p, state) in enumerate(zip(params, states)):
         logits, context, next_state, _ = block_sequence(p, settings, ids, state, context,
-                                                        with_logits=layer == len(params) - 1)
+                                                        with_logits=layer == len(params) - 1,
+                                                        token_context=token_context)
         next_states.append(next_state)
     return logits, next_states
 

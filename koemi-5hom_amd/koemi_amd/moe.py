@@ -288,6 +288,7 @@ def permute_topk(
     expert_count: int,
     pair_weights: Tensor | None = None,
     validate: bool = True,
+    gather: bool = True,
 ) -> tuple[Tensor, ...]:
     """Sort valid token-expert pairs into stable expert segments
     (reference moe/__init__.py:179-228).
@@ -296,6 +297,9 @@ def permute_topk(
     invalid pairs follow all expert segments with the sentinel expert
     ``expert_count`` and zero context rows. With ``pair_weights`` ([tokens,
     top_k] float32) a fifth tensor, the weights in sorted order, is returned.
+    ``gather=False`` (build-side): the sorted copy of the context is not built
+    and ``sorted_context`` is None (``grouped_expert_mlp_indexed`` reads the
+    context rows by ``sorted_rows``).
     """
 
     tensors = {"context": context, "assignments": assignments, "valid_mask": valid_mask}
@@ -334,7 +338,7 @@ def permute_topk(
     tokens, width = flat.shape
     pairs = tokens * top_k
     device = context.device
-    sorted_context = torch.empty((pairs, width), device=device, dtype=context.dtype)
+    sorted_context = torch.empty((pairs, width), device=device, dtype=context.dtype) if gather else None
     sorted_rows = torch.empty((pairs,), device=device, dtype=torch.int64)
     sorted_experts = torch.empty((pairs,), device=device, dtype=torch.int64)
     segment_offsets = torch.empty((expert_count + 1,), device=device, dtype=torch.int64)
@@ -352,7 +356,7 @@ def permute_topk(
             _native.dtype_code(assignments.dtype),
             valid_mask.data_ptr(),
             _native.ptr(pair_weights),
-            sorted_context.data_ptr(),
+            _native.ptr(sorted_context),
             sorted_rows.data_ptr(),
             sorted_experts.data_ptr(),
             segment_offsets.data_ptr(),
@@ -480,6 +484,53 @@ def grouped_expert_mlp_inference(
             workspace_bytes,
             _native.stream_of(sorted_context.device),
         )
+    return output
+
+
+def grouped_expert_mlp_indexed(
+    context: Tensor,
+    sorted_rows: Tensor,
+    segment_offsets: Tensor,
+    gate_weights: Tensor,
+    gate_biases: Tensor,
+    value_weights: Tensor,
+    value_biases: Tensor,
+    output_weights: Tensor,
+    output_biases: Tensor,
+) -> Tensor:
+    """``grouped_expert_mlp_inference`` on the pairs of ``permute_topk(...,
+    gather=False)`` without the sorted copy of the context: pair i reads row
+    ``sorted_rows[i]`` of ``context`` ([tokens, width] bf16) straight into the
+    first GEMM's operand tiles (``koemi_moe_grouped_mlp_indexed``). The
+    outputs ([pairs, width], pairs = ``sorted_rows.numel()``) equal
+    ``grouped_expert_mlp_inference`` on the gathered rows bit for bit. bf16
+    with width and hidden multiples of 64 only (the MFMA path); no validation
+    of the index tensors beyond their shapes (indices are clamped on the
+    device)."""
+
+    if context.ndim != 2 or context.dtype != torch.bfloat16:
+        raise CudaMoeValidationError("context must be a bf16 [tokens, width] tensor")
+    expert_count, hidden_width, input_width = gate_weights.shape
+    if input_width != context.shape[1] or input_width % 64 or hidden_width % 64:
+        raise CudaMoeValidationError("the indexed grouped MLP needs width and hidden multiples of 64")
+    if sorted_rows.dtype != torch.int64 or sorted_rows.ndim != 1 or segment_offsets.shape != (expert_count + 1,):
+        raise CudaMoeValidationError("sorted_rows must be int64 [pairs] and segment_offsets int64 [experts + 1]")
+    _require_library()
+    pairs = int(sorted_rows.shape[0])
+    output = torch.empty((pairs, input_width), device=context.device, dtype=context.dtype)
+    if pairs == 0:
+        return output
+    x = _aligned(context.contiguous())
+    weights = [_aligned(t.contiguous()) for t in
+               (gate_weights, gate_biases, value_weights, value_biases, output_weights, output_biases)]
+    workspace_bytes = _native.query("koemi_moe_grouped_mlp_workspace_bytes", pairs, input_width, hidden_width,
+                                    expert_count, _native.dtype_code(torch.bfloat16))
+    workspace = torch.empty((workspace_bytes,), device=context.device, dtype=torch.uint8)
+    with torch.cuda.device(context.device):
+        _native.call("koemi_moe_grouped_mlp_indexed", x.data_ptr(), int(x.shape[0]), sorted_rows.data_ptr(),
+                     segment_offsets.data_ptr(), *(w.data_ptr() for w in weights), output.data_ptr(), pairs,
+                     input_width, hidden_width, expert_count, workspace.data_ptr(), workspace_bytes,
+                     _native.stream_of(context.device))
     return output
 
 

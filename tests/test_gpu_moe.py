@@ -297,6 +297,33 @@ def test_config4_pipeline(device, learned):
     np.testing.assert_array_equal(out.cpu().view(torch.int16).numpy(), oracle.f32_to_bf16(want_out).view(np.int16))
 
 
+@pytest.mark.parametrize("tokens, E, D, H, seed", [
+    (32768, 16, 1024, 2816, 0),  # C4: whole rounds of 256 x 256 tiles and a split-K last round
+    (1500, 7, 192, 320, 1),      # ragged segments, partial tiles
+    (64, 16, 1024, 2048, 2),     # a C5 decode step: the few-rows-per-expert kernel
+])
+def test_indexed_grouped_mlp_equals_the_gathered_one(device, tokens, E, D, H, seed):
+    """permute_topk(gather=False) + grouped_expert_mlp_indexed (context rows read
+    by sorted_rows inside the first GEMM) give the same bits as the gathered
+    sorted context through grouped_expert_mlp_inference: the same tiles, the
+    same accumulation order, only the operand addresses differ."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    ctx = torch.randn((tokens, D), generator=g, device=device).to(torch.bfloat16)
+    ids = torch.randint(0, 256, (tokens,), generator=g, device=device)
+    prev = torch.randint(0, 256, (tokens,), generator=g, device=device)
+    valid = torch.rand((tokens,), generator=g, device=device) < 0.95
+    a = moe.route_topk_valid(ids, prev, valid, expert_count=E, top_k=2, validate=False)
+    ws = [(0.05 * torch.randn(shape, generator=g, device=device)).to(torch.bfloat16)
+          for shape in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    sc, rows, experts, offsets = moe.permute_topk(ctx, a, valid, expert_count=E)
+    none, rows2, experts2, offsets2 = moe.permute_topk(ctx, a, valid, expert_count=E, gather=False)
+    assert none is None and torch.equal(rows, rows2) and torch.equal(experts, experts2) and torch.equal(offsets, offsets2)
+    want = moe.grouped_expert_mlp_inference(sc, experts, offsets, *ws)
+    got = moe.grouped_expert_mlp_indexed(ctx, rows2, offsets2, *ws)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("tokens, k, E, learned", [(64, 2, 16, False), (300, 3, 13, True), (1, 2, 4, False)])
 def test_small_combine_bit_exact(device, tokens, k, E, learned):
     """A decode-sized combine (the one-workgroup inversion) against the oracle's
