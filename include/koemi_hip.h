@@ -551,6 +551,26 @@ int koemi_moe_combine(const void* expert_outputs, const int64_t* sorted_rows,
                       int64_t num_segments, int dtype, void* workspace, size_t workspace_bytes,
                       koemi_stream_t stream);
 
+/* The HERM block's expert tail in one pass (no single reference op): the
+ * combine of koemi_moe_combine (bf16 expert outputs [pairs, width], the
+ * ascending-position fp32 sum of each token's pairs scaled by pair_weights or
+ * 1/top_k, rounded once to bf16: combine_topk, moe/__init__.py), the expert
+ * output normalizer RMSNorm(context + update) * expert_norm_weight with rows
+ * whose mask is false keeping the context (experts.py:134-136,
+ * layers.py:14-16), and, with next_norm_weight, the next block's input
+ * RMSNorm of that result (network.py:296-310). Each step rounds as the
+ * separate kernels do (koemi_moe_combine, then koemi_herm_rmsnorm twice), so
+ * the outputs are the same bits. context [tokens, width] fp32; output (NULL:
+ * none) [tokens, width] fp32; next_input_bf16 (NULL: none) [tokens, width]
+ * bf16. top_k <= 8, width % 4 == 0 and <= 2048, 16-byte aligned rows; the
+ * workspace of koemi_moe_combine_workspace_bytes(tokens, top_k). */
+int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_rows, const int64_t* segment_offsets,
+                            const float* pair_weights, const float* context, const uint8_t* mask,
+                            const float* expert_norm_weight, const float* next_norm_weight, float* output,
+                            void* next_input_bf16, int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
+                            int64_t num_segments, float eps, void* workspace, size_t workspace_bytes,
+                            koemi_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

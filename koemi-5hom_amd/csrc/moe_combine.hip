@@ -273,6 +273,110 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
     return check_launch("koemi_moe_combine(rows)");
 }
 
+// The HERM block's expert tail in one pass per token row (a wave per row):
+// the combine above (the k expert outputs in ascending sorted position, each
+// scaled by its weight or by 1/k, summed in fp32 from zero and rounded once to
+// bf16: combine_topk), the expert output normalizer with the residual and the
+// valid-row select (RMSNorm of context + update, rows whose mask is false keep
+// the context: experts.py:134-136, layers.py:14-16) and, with w_next, the next
+// block's input RMSNorm of that result (network.py:296-310), each step with
+// the arithmetic of the separate kernels it replaces (the same bits): lane l
+// holds columns (j * 64 + l) * 4 .. + 3, j < NV; the sum of squares runs in
+// (j, i) order per lane, then over the lanes by xor butterfly.
+template <int KMAX, int NV>
+__global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
+    const bf16* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
+    const float* __restrict__ pair_w, const float* __restrict__ ctx, const uint8_t* __restrict__ mask,
+    const float* __restrict__ w_expert, const float* __restrict__ w_next, float* __restrict__ out,
+    bf16* __restrict__ out_next, int64_t tokens, int64_t k, int H, float eps) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
+    if (t >= tokens) return;
+    const int lane = lane_id();
+    const int n = static_cast<int>(min(static_cast<int64_t>(cnt[t]), k));
+    int64_t p[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+        const int64_t pj = pos[t * k + min(static_cast<int64_t>(j), k - 1)];
+        p[j] = j < n ? pj : INT64_MAX;
+    }
+    sort_positions<KMAX>(p);
+    const float kf = static_cast<float>(k);
+    float w[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) w[j] = (pair_w != nullptr && j < n) ? pair_w[p[j]] : 0.0f;
+    const float* xr = ctx + t * H;
+    float v[NV][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        if (c < H) {
+            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int m = 0; m < KMAX; ++m) {
+                if (m < n) {
+                    const float4 e = load4(y + p[m] * H + c);
+                    const float ev[4] = {e.x, e.y, e.z, e.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i] += pair_w ? ev[i] * w[m] : ev[i] / kf;
+                }
+            }
+            v[j][0] = q.x + to_f32(from_f32<bf16>(acc[0]));
+            v[j][1] = q.y + to_f32(from_f32<bf16>(acc[1]));
+            v[j][2] = q.z + to_f32(from_f32<bf16>(acc[2]));
+            v[j][3] = q.w + to_f32(from_f32<bf16>(acc[3]));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[j][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss = fmaf(v[j][i], v[j][i], ss);
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    const bool keep = mask == nullptr || mask[t] != 0;
+    const float inv = rsqrtf(ss / static_cast<float>(H) + eps);
+    float ss2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        if (c >= H) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[j][i] = 0.0f;
+        } else if (keep) {
+            const float4 wq = *reinterpret_cast<const float4*>(w_expert + c);
+            v[j][0] = v[j][0] * inv * wq.x;
+            v[j][1] = v[j][1] * inv * wq.y;
+            v[j][2] = v[j][2] * inv * wq.z;
+            v[j][3] = v[j][3] * inv * wq.w;
+        } else {
+            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            v[j][0] = q.x; v[j][1] = q.y; v[j][2] = q.z; v[j][3] = q.w;
+        }
+        if (out != nullptr && c < H) *reinterpret_cast<float4*>(out + t * H + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ss2 = fmaf(v[j][i], v[j][i], ss2);
+    }
+    if (w_next == nullptr || out_next == nullptr) return;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) ss2 += __shfl_xor(ss2, off, kWave);
+    const float inv2 = rsqrtf(ss2 / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        if (c >= H) continue;
+        const float4 wq = *reinterpret_cast<const float4*>(w_next + c);
+        typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+        bf16x4 q;
+        q[0] = static_cast<__bf16>(v[j][0] * inv2 * wq.x);
+        q[1] = static_cast<__bf16>(v[j][1] * inv2 * wq.y);
+        q[2] = static_cast<__bf16>(v[j][2] * inv2 * wq.z);
+        q[3] = static_cast<__bf16>(v[j][3] * inv2 * wq.w);
+        *reinterpret_cast<bf16x4*>(out_next + t * H + c) = q;
+    }
+}
+
 }  // namespace
 }  // namespace koemi
 
@@ -322,4 +426,61 @@ extern "C" int koemi_moe_combine(const void* expert_outputs, const int64_t* sort
         case KOEMI_F16: return launch_combine_rows<f16>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);
         default: return launch_combine_rows<bf16>(expert_outputs, cnt, pos, pair_weights, combined, tokens, top_k, width, s);
     }
+}
+
+
+extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_rows,
+                                       const int64_t* segment_offsets, const float* pair_weights, const float* context,
+                                       const uint8_t* mask, const float* expert_norm_weight,
+                                       const float* next_norm_weight, float* output, void* next_input_bf16,
+                                       int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
+                                       int64_t num_segments, float eps, void* workspace, size_t workspace_bytes,
+                                       koemi_stream_t stream) {
+    if (tokens < 1 || width < 1 || pairs < 0) return fail(KOEMI_ERR_INVALID, "combine norm needs tokens, width >= 1");
+    if (top_k < 1 || top_k > 8) return fail(KOEMI_ERR_UNSUPPORTED, "combine norm takes top_k in [1, 8]");
+    if (num_segments < 1) return fail(KOEMI_ERR_INVALID, "segment_offsets must have at least two entries");
+    if (width % 4 != 0 || width > 4 * kWave * 8)
+        return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs a width that is a multiple of 4 and at most 2048");
+    if (!segment_offsets || !context || !expert_norm_weight || (pairs > 0 && (!expert_outputs || !sorted_rows)))
+        return fail(KOEMI_ERR_INVALID, "combine norm received a null pointer");
+    if (!output && !(next_norm_weight && next_input_bf16))
+        return fail(KOEMI_ERR_INVALID, "combine norm has no output");
+    if ((reinterpret_cast<uintptr_t>(expert_outputs) | reinterpret_cast<uintptr_t>(context) |
+         reinterpret_cast<uintptr_t>(output) | reinterpret_cast<uintptr_t>(next_input_bf16)) % 16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs 16-byte aligned rows");
+    const CombineWorkspace ws = combine_workspace(tokens, top_k);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "combine norm workspace too small: need %zu bytes", ws.total);
+    char* base = static_cast<char*>(workspace);
+    int32_t* cnt = reinterpret_cast<int32_t*>(base + ws.cnt_off);
+    int64_t* pos = reinterpret_cast<int64_t*>(base + ws.pos_off);
+    hipStream_t s = as_stream(stream);
+    int st = KOEMI_OK;
+    if (tokens <= kSmallInvertTokens && pairs <= 4096) {
+        hipLaunchKernelGGL(invert_rows_small_kernel, dim3(1), dim3(1024), 0, s, sorted_rows,
+                           segment_offsets + num_segments, cnt, pos, pairs, tokens, top_k);
+        st = check_launch("koemi_herm_combine_norm(invert)");
+    } else {
+        hipLaunchKernelGGL(zero_i32_kernel, dim3(grid_for(tokens, 256)), dim3(256), 0, s, cnt, tokens);
+        st = check_launch("koemi_herm_combine_norm(zero)");
+        if (st == KOEMI_OK && pairs > 0) {
+            hipLaunchKernelGGL(invert_rows_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, s, sorted_rows,
+                               segment_offsets + num_segments, cnt, pos, pairs, tokens, top_k);
+            st = check_launch("koemi_herm_combine_norm(invert)");
+        }
+    }
+    if (st != KOEMI_OK) return st;
+    const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+    const bf16* y = static_cast<const bf16*>(expert_outputs);
+    bf16* o16 = static_cast<bf16*>(next_input_bf16);
+    const int H = static_cast<int>(width);
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, y, cnt, pos, pair_weights, context, mask, expert_norm_weight,
+                           next_norm_weight, output, o16, tokens, top_k, H, eps);
+        return check_launch("koemi_herm_combine_norm(rows)");
+    };
+    const bool wide = width > 4 * kWave * 4;
+    if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8>) : launch(combine_norm_kernel<2, 4>);
+    if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8>) : launch(combine_norm_kernel<4, 4>);
+    return wide ? launch(combine_norm_kernel<8, 8>) : launch(combine_norm_kernel<8, 4>);
 }

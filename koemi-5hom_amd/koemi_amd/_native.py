@@ -168,6 +168,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),
     ),
+    "koemi_herm_combine_norm": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_float, _P, c_size_t,
+         _P),
+    ),
 }
 
 EXPORTED_SYMBOLS: tuple[str, ...] = tuple(_SIGNATURES)

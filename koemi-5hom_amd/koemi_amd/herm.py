@@ -50,6 +50,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import asdict, dataclass
+from typing import NamedTuple
 
 import torch
 from torch import Tensor
@@ -422,9 +423,29 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     return read, next_basis, next_normalizer
 
 
+class NextInput(NamedTuple):
+    """A block's output handed to the next block of a stack already through
+    that block's input RMSNorm: ``normalized`` [B, L, D] bf16, written by the
+    fused expert tail (``koemi_herm_combine_norm``) in place of the fp32 final
+    context, which nothing else reads between two blocks."""
+
+    normalized: Tensor
+
+
+def _input_norm(p: dict[str, Tensor], ids: Tensor, context, low) -> Tensor:
+    """The block's input RMSNorm of its context (the embedding of the ids for
+    the first block; a ``NextInput`` is already normalized): fp32, or the bf16
+    copy for a bf16 stack."""
+
+    if isinstance(context, NextInput):
+        return context.normalized
+    source = functional.embedding(ids, p["embedding"]) if context is None else context
+    return _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
+
+
 def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, previous: Tensor, valid: Tensor,
-                      pieces: tuple[Tensor, Tensor, Tensor, Tensor] | Tensor, with_logits: bool
-                      ) -> tuple[Tensor, Tensor | None]:
+                      pieces: tuple[Tensor, Tensor, Tensor, Tensor] | Tensor, with_logits: bool,
+                      next_norm: Tensor | None = None) -> tuple[Tensor | NextInput, Tensor | None]:
     """The block's position-wise tail: fusion of [working ; memory ; local ;
     salient] with its normalizer (network.py:723-732), the expert mixture with
     its output normalizer (experts.py:109-150 or router.py:43-97) and the token
@@ -432,7 +453,10 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     the rows may span any number of windows. ``pieces`` are the four fp32
     inputs, or the bf16 fusion input their producers already wrote
     ([B, L, 4 D], see ``_fusion_input``). Returns (final context [B, L, D]
-    fp32, logits or None)."""
+    fp32, logits or None). With ``next_norm`` (the next block's input norm
+    weight) and a bf16 stack, the combine, this block's expert normalizer and
+    the next block's input norm run as one kernel and the context returned is
+    that ``NextInput`` (no fp32 context unless logits are asked for too)."""
 
     batch, length = ids.shape
     d = settings.width
@@ -477,6 +501,19 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"],
                                                       p["gate_b"], p["up_w"], p["up_b"], p["down_w"], p["down_b"],
                                                       validate=False)
+    if next_norm is not None and low is not None and k <= 8 and d % 4 == 0 and d <= 2048:
+        tokens = flat.shape[0]
+        final = torch.empty((tokens, d), device=flat.device, dtype=torch.float32) if with_logits else None
+        u_next = torch.empty((tokens, d), device=flat.device, dtype=torch.bfloat16)
+        need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k)
+        workspace = torch.empty((need,), device=flat.device, dtype=torch.uint8)
+        _native.call("koemi_herm_combine_norm", _native.ptr(expert_out), _native.ptr(sorted_rows),
+                     _native.ptr(offsets), _native.ptr(sorted_weights), _native.ptr(flat.contiguous()),
+                     _native.ptr(flat_valid), _native.ptr(p["expert_norm"]), _native.ptr(next_norm),
+                     _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]), d, tokens, k,
+                     settings.expert_count, _EPS, _native.ptr(workspace), need, _native.stream_of(flat.device))
+        logits = _linear(final.view(batch, length, d), p["head_w"], p["head_b"]) if with_logits else None
+        return NextInput(u_next.view(batch, length, d)), logits
     update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
                               pair_weights=sorted_weights, validate=False)
     final = _rms(flat, p["expert_norm"], residual=update, mask=flat_valid).view(batch, length, d)
@@ -485,16 +522,20 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
 
 
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
-                 context: Tensor | None = None, *, with_logits: bool = True,
-                 token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None
-                 ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
+                 context: Tensor | NextInput | None = None, *, with_logits: bool = True,
+                 token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
+                 next_norm: Tensor | None = None
+                 ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
-    for the embedding layer). Returns (logits, final_context, next_state,
-    surprise); logits is None when ``with_logits`` is False (the stack's
-    inner layers, whose head output nothing reads). ``token_context``:
+    for the embedding layer; a ``NextInput`` is taken as this block's
+    normalized input). Returns (logits, final_context, next_state, surprise);
+    logits is None when ``with_logits`` is False (the stack's inner layers,
+    whose head output nothing reads). ``token_context``:
     ``_token_context``'s four outputs when the caller formed them (a decode
-    step's stack, once for all layers)."""
+    step's stack, once for all layers). ``next_norm``: the next block's input
+    norm weight, for a stack; the context returned is then a ``NextInput``
+    (see ``_fuse_mix_predict``)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
@@ -503,13 +544,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     if token_context is None:
         token_context = _token_context(ids, None, state["last_token"])
     previous, last_token, valid, targets = token_context
-    source = functional.embedding(ids, p["embedding"]) if context is None else context
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None  # kernels write bf16 copies of the GEMM inputs
-    if low is None:
-        u = _rms(source, p["input_norm"])
-    else:
-        u = _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    u = _input_norm(p, ids, context, low)
     fusion_in = _fusion_input(settings, batch, length, ids.device)
     scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
@@ -545,7 +582,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                    state["salient_valid"], local_keys, local_values, admission, ws,
                                                    out=_block(fusion_in, 3, d))
     pieces = fusion_in if fusion_in is not None else (ws, fast, local_value, salient_value)
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
 
     local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
     salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
@@ -688,9 +725,10 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
 
 
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
-                   context: Tensor | None = None, *, with_logits: bool = True,
-                   token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None
-                   ) -> tuple[Tensor | None, Tensor, dict[str, Tensor], Tensor]:
+                   context: Tensor | NextInput | None = None, *, with_logits: bool = True,
+                   token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
+                   next_norm: Tensor | None = None
+                   ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One block over a whole sequence of windows at once: forward_parallel
     (network.py:176-197) of a single block, i.e. ``block_window`` applied to
     windows of ``scan_chunk`` tokens with the state carried, computed
@@ -708,8 +746,9 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     left (``associative_scan_read_windows``). The results equal the
     window-by-window ones up to floating-point rounding (the library GEMMs
     see more rows). ``token_context``: ``_token_context``'s four outputs when
-    the caller formed them (a stack, once for all layers). Returns (logits or
-    None, final context, next state, surprise [B, L]).
+    the caller formed them (a stack, once for all layers); ``context`` and
+    ``next_norm`` as in ``block_window``. Returns (logits or None, final
+    context, next state, surprise [B, L]).
     """
 
     ids = ids.contiguous()
@@ -722,10 +761,9 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     if token_context is None:
         token_context = _token_context(ids, None, state["last_token"])
     previous, last_token, valid, targets = token_context
-    source = functional.embedding(ids, p["embedding"]) if context is None else context
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
-    u = _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
+    u = _input_norm(p, ids, context, low)
     fusion_in = _fusion_input(settings, batch, length, ids.device)
     scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
     ws, ws_low = scanned if low is not None else (scanned, scanned)
@@ -759,7 +797,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
         pieces = fusion_in
     else:
         pieces = (ws, fast, local_value.view(batch, length, d), salient_value.view(batch, length, d))
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
@@ -789,9 +827,10 @@ def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids:
     next_states = []
     logits = None
     for layer, (p, state) in enumerate(zip(params, states)):
-        logits, context, next_state, _ = block_sequence(p, settings, ids, state, context,
-                                                        with_logits=layer == len(params) - 1,
-                                                        token_context=token_context)
+        last = layer == len(params) - 1
+        logits, context, next_state, _ = block_sequence(p, settings, ids, state, context, with_logits=last,
+                                                        token_context=token_context,
+                                                        next_norm=None if last else params[layer + 1]["input_norm"])
         next_states.append(next_state)
     return logits, next_states
 
@@ -848,9 +887,10 @@ def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: 
     next_states = []
     logits = None
     for layer, (p, state) in enumerate(zip(params, states)):
-        logits, context, next_state, _ = block_window(p, settings, ids, state, context,
-                                                      with_logits=layer == len(params) - 1,
-                                                      token_context=token_context)
+        last = layer == len(params) - 1
+        logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
+                                                      token_context=token_context,
+                                                      next_norm=None if last else params[layer + 1]["input_norm"])
         next_states.append(next_state)
     return logits, next_states
 
@@ -865,9 +905,10 @@ def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: T
     context = None
     next_states = []
     logits = None
-    for p, state in zip(params, states):
-        last = len(next_states) == len(params) - 1
-        logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last)
+    for layer, (p, state) in enumerate(zip(params, states)):
+        last = layer == len(params) - 1
+        logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
+                                                      next_norm=None if last else params[layer + 1]["input_norm"])
         next_states.append(next_state)
     return logits, next_states
 

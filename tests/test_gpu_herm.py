@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 import torch
 
-from koemi_amd import _native, herm, think
+from koemi_amd import _native, herm, moe, think
 from oracle import herm as oherm
 
 pytestmark = pytest.mark.gpu
@@ -332,3 +332,45 @@ def test_wavefront_prefill_equals_the_window_by_window_prefill(device):
             for key, tensor in want.items():
                 assert torch.equal(got[key], tensor), f"run {run} {key}"
     assert any(bool(st["salient_valid"].any()) for st in want_states)
+
+
+@pytest.mark.parametrize("tokens, learned", [(4096, False), (64, False), (300, True)])
+def test_combine_norm_equals_combine_then_the_two_norms(device, tokens, learned):
+    """koemi_herm_combine_norm (the expert tail of a stack's inner block: the
+    combine, the expert normalizer with its residual and valid-row select, the
+    next block's input norm) gives the bits of combine_topk followed by the
+    two herm_rmsnorm calls it replaces, for hash (mean of the k outputs) and
+    learned (weighted) mixtures, at prefill and decode row counts."""
+    g = torch.Generator(device=device).manual_seed(tokens + learned)
+    d, E, k, hidden = 1024, 16, 2, 256
+    ctx = torch.randn((tokens, d), generator=g, device=device).to(torch.bfloat16)
+    valid = torch.rand((tokens,), generator=g, device=device) < 0.9
+    if learned:
+        a, w = moe.route_topk_learned(torch.randn((tokens, E), generator=g, device=device), valid, top_k=k)
+    else:
+        ids = torch.randint(0, 256, (tokens,), generator=g, device=device)
+        a = moe.route_topk_valid(ids, torch.roll(ids, 1), valid, expert_count=E, top_k=k, validate=False)
+        w = None
+    permuted = moe.permute_topk(ctx, a, valid, expert_count=E, pair_weights=w, gather=False)
+    _, rows, _, offsets = permuted[:4]
+    sw = permuted[4] if learned else None
+    ws = [(0.05 * torch.randn(shape, generator=g, device=device)).to(torch.bfloat16)
+          for shape in ((E, hidden, d), (E, hidden), (E, hidden, d), (E, hidden), (E, d, hidden), (E, d))]
+    y = moe.grouped_expert_mlp_indexed(ctx, rows, offsets, *ws)
+    flat = torch.randn((tokens, d), generator=g, device=device)
+    w_e = 1.0 + 0.1 * torch.randn((d,), generator=g, device=device)
+    w_n = 1.0 + 0.1 * torch.randn((d,), generator=g, device=device)
+    update = moe.combine_topk(y, rows, offsets, token_count=tokens, top_k=k, pair_weights=sw, validate=False)
+    want_final = herm._rms(flat, w_e, residual=update, mask=valid)
+    want_next = herm._rms(want_final, w_n, fp32=False, low=torch.bfloat16)[1]
+    final = torch.empty_like(flat)
+    nxt = torch.empty((tokens, d), device=device, dtype=torch.bfloat16)
+    need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k)
+    workspace = torch.empty((need,), device=device, dtype=torch.uint8)
+    _native.call("koemi_herm_combine_norm", _native.ptr(y), _native.ptr(rows), _native.ptr(offsets), _native.ptr(sw),
+                 _native.ptr(flat), _native.ptr(valid), _native.ptr(w_e), _native.ptr(w_n), _native.ptr(final),
+                 _native.ptr(nxt), int(y.shape[0]), d, tokens, k, E, herm._EPS, _native.ptr(workspace), need,
+                 _native.stream_of(device))
+    torch.cuda.synchronize()
+    assert torch.equal(final, want_final)
+    assert torch.equal(nxt, want_next)
