@@ -349,8 +349,10 @@ int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_
  * [2 * width, input_width] bf16: the retention rows, then the candidate rows;
  * biases [2 * width] bf16 in the same order, or NULL. valid [batch, length]
  * (NULL: all valid), initial [batch, width] fp32; writes states [batch,
- * length, width] fp32 and, with states_bf16 (NULL: none), a bf16 copy whose
- * rows are bf16_row_stride elements apart (0: width). The projection runs on
+ * length, width] fp32, with states_bf16 (NULL: none) a bf16 copy whose rows
+ * are bf16_row_stride elements apart (0: width), and with final_states (NULL:
+ * none) the last position's states again as [batch, width] (the carried
+ * state). The projection runs on
  * bf16 MFMA in tiles of 256 positions x 128 features, whose epilogue forms
  * the gates and scans them, so the pre-activations never reach memory; each
  * tile publishes its transfer (the affine map of its positions) and takes
@@ -364,7 +366,7 @@ int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_
 size_t koemi_gated_projection_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
 int koemi_gated_projection_scan(const void* inputs, const void* weights, const void* biases, const uint8_t* valid,
                                 const float* initial, float* states, void* states_bf16, int64_t bf16_row_stride,
-                                int64_t batch, int64_t length, int64_t width, int64_t input_width, void* workspace,
+                                float* final_states, int64_t batch, int64_t length, int64_t width, int64_t input_width, void* workspace,
                                 size_t workspace_bytes, koemi_stream_t stream);
 
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections

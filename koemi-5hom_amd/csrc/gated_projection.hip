@@ -135,8 +135,9 @@ template <int BNT>
 __global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) void gated_projection_scan_kernel(
     const bf16* __restrict__ inputs, const bf16* __restrict__ weights, const bf16* __restrict__ biases,
     const uint8_t* __restrict__ valid, const float* __restrict__ initial, float* __restrict__ states,
-    bf16* __restrict__ states16, int64_t s16_stride, int64_t L, int64_t F, int64_t K, int32_t n_ft, int32_t n_mt,
-    int32_t groups, uint32_t* __restrict__ ws_words, uint64_t* __restrict__ ws_pairs) {
+    bf16* __restrict__ states16, int64_t s16_stride, float* __restrict__ final_states, int64_t L, int64_t F,
+    int64_t K, int32_t n_ft, int32_t n_mt, int32_t groups, uint32_t* __restrict__ ws_words,
+    uint64_t* __restrict__ ws_pairs) {
     using TS = mfma_stage::TileShape<BNT>;
     constexpr int NT = TS::kNT;  // n-tiles per wave
     constexpr int NH = NT / 2;   // of them retention (then as many candidate)
@@ -323,6 +324,9 @@ __global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) v
                 const int64_t row = row0 + wm * 128 + mt * 32 + 8 * q + 4 * hf + i;
                 states[row * F + f] = x;
                 if (states16) states16[row * s16_stride + f] = static_cast<bf16>(x);
+                // the sequence's last state, also on its own (the carried state)
+                if (final_states && mt == 3 && q == 3 && i == 3 && hf == 1 && wm == 1 && m == n_mt - 1)
+                    final_states[static_cast<int64_t>(b) * F + f] = x;
             }
             h = fmaf(hiA, hmid, hiB);
         }
@@ -341,7 +345,8 @@ extern "C" size_t koemi_gated_projection_scan_workspace_bytes(int64_t batch, int
 
 extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weights, const void* biases,
                                            const uint8_t* valid, const float* initial, float* states,
-                                           void* states_bf16, int64_t bf16_row_stride, int64_t batch,
+                                           void* states_bf16, int64_t bf16_row_stride, float* final_states,
+                                           int64_t batch,
                                            int64_t length, int64_t width, int64_t input_width, void* workspace,
                                            size_t workspace_bytes, koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1 || input_width < 1)
@@ -378,7 +383,7 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
     hipLaunchKernelGGL(gated_projection_scan_kernel<kGpBN>, dim3(static_cast<uint32_t>(tiles)), dim3(kGpThreads), 0, s,
                        static_cast<const bf16*>(inputs), static_cast<const bf16*>(weights),
                        static_cast<const bf16*>(biases), valid, initial, states, static_cast<bf16*>(states_bf16),
-                       bf16_row_stride, length, width, input_width, static_cast<int32_t>(n_ft),
+                       bf16_row_stride, final_states, length, width, input_width, static_cast<int32_t>(n_ft),
                        static_cast<int32_t>(n_mt), static_cast<int32_t>(groups), words,
                        reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + w.data_off));
     return check_launch("gated projection scan");

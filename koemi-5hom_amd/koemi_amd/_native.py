@@ -106,7 +106,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_gated_projection_scan_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_gated_projection_scan": (
         c_int,
-        (_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
     "koemi_linear_rows": (
         c_int,

@@ -277,19 +277,28 @@ def _linear(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     return out.view(*x.shape[:-1], weight.shape[0])
 
 
+def _fused_gates(p: dict[str, Tensor], u: Tensor) -> bool:
+    """Whether the gate projection and the scan run as the one fused kernel."""
+
+    return p["gates_w"].dtype == torch.bfloat16 and recurrent.gated_projection_fits(u, p["gates_w"])
+
+
 def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor, width: int, with_bf16: bool,
-                out_bf16: Tensor | None):
+                out_bf16: Tensor | None, final_out: Tensor | None = None):
     """The gate projection and the fused gates + scan: for a bf16 stack
     outside decode steps the projection's results are bf16 with the biases in
     the GEMM epilogue (nn.Linear under bf16 autocast) — in one kernel with the
     gates and the scan where the shape allows (whole 256-position tiles of a
     sequence), else a library GEMM then the scan kernel; otherwise fp32
-    results without bias and the biases added inside the scan kernel."""
+    results without bias and the biases added inside the scan kernel.
+    ``final_out``: where the fused kernel writes the last position's states
+    (the next carried state), when that kernel runs; the caller checks
+    ``_fused_gates(p, u)``."""
 
     w = p["gates_w"]
-    if w.dtype == torch.bfloat16 and recurrent.gated_projection_fits(u, w):
+    if _fused_gates(p, u):
         return recurrent.gated_projection_scan(u, w, p["gates_b16"], valid, working, with_bf16=with_bf16,
-                                               out_bf16=out_bf16)
+                                               out_bf16=out_bf16, final_out=final_out)
     if w.dtype == torch.bfloat16 and not _few_rows(u, w):
         return recurrent.gated_scan(_linear_low(u, w, p["gates_b16"]), valid, working, width=width,
                                     with_bf16=with_bf16, out_bf16=out_bf16)
@@ -707,7 +716,9 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
     w16 = p.get("content_w16")
     if w16 is not None:
         weight_t = w16.t()
-        first = torch.mm(carried.to(torch.bfloat16), weight_t, out_dtype=torch.float32)
+        # the carried state's few rows: one kernel (fp32 rows rounded to bf16 as staged)
+        first = linear.linear_rows([carried], w16, None) if _few_rows(carried, w16) else \
+            torch.mm(carried.to(torch.bfloat16), weight_t, out_dtype=torch.float32)
         logits = torch.mm(ws_low.reshape(batch * length, d), weight_t, out_dtype=torch.float32) if length > 1 \
             else first
     else:
@@ -765,7 +776,8 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     low = lin if lin == torch.bfloat16 else None
     u = _input_norm(p, ids, context, low)
     fusion_in = _fusion_input(settings, batch, length, ids.device)
-    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
+    working_next = torch.empty((batch, d), device=ids.device, dtype=torch.float32) if _fused_gates(p, u) else None
+    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d), working_next)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
@@ -799,7 +811,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
         pieces = (ws, fast, local_value.view(batch, length, d), salient_value.view(batch, length, d))
     final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
     next_state = {
-        "working": ws[:, -1].contiguous(),
+        "working": working_next if working_next is not None else ws[:, -1].contiguous(),
         "basis": basis,
         "normalizer": normalizer,
         "local_keys": local_final[0],

@@ -255,8 +255,8 @@ def gated_projection_fits(inputs: Tensor, weight: Tensor) -> bool:
 
 
 def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, valid_mask: Tensor | None,
-                          initial: Tensor, *, with_bf16: bool = False,
-                          out_bf16: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
+                          initial: Tensor, *, with_bf16: bool = False, out_bf16: Tensor | None = None,
+                          final_out: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
     """The gates of model/memory.py:14-30 with their two projections, the
     masking of network.py:307-309 and the scan of network.py:310, for a bf16
     window under autocast, in one kernel (``koemi_gated_projection_scan``):
@@ -265,9 +265,11 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
     ``valid_mask`` ``[B, L]`` bool or None, ``initial`` ``[B, width]`` fp32.
     Returns the states ``[B, L, width]`` fp32 and, with ``with_bf16``, their
     bf16 copy (into ``out_bf16`` when given: a bf16 ``[B, L, width]`` view with
-    contiguous columns and evenly spaced rows). Shapes outside
-    ``gated_projection_fits`` raise; the projection's results are rounded to
-    bf16 after the bias (the autocast GEMM's output) before the gates."""
+    contiguous columns and evenly spaced rows). ``final_out`` (a contiguous
+    fp32 ``[B, width]`` tensor, or None) receives the last position's states
+    as well (the carried state). Shapes outside ``gated_projection_fits``
+    raise; the projection's results are rounded to bf16 after the bias (the
+    autocast GEMM's output) before the gates."""
 
     if not gated_projection_fits(inputs, weight):
         raise DenseCudaValidationError("gated_projection_scan needs bf16 inputs [B, L, K] and weight [2 width, K] "
@@ -298,6 +300,9 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
         if (states16.shape != states.shape or states16.dtype != torch.bfloat16 or states16.stride(2) != 1
                 or states16.stride(0) != length * states16.stride(1)):
             raise DenseCudaValidationError("out_bf16 must be a bf16 [batch, length, width] view with evenly spaced rows")
+    if final_out is not None and (final_out.shape != (batch, width) or final_out.dtype != torch.float32
+                                  or not final_out.is_contiguous() or final_out.device != inputs.device):
+        raise DenseCudaValidationError("final_out must be a contiguous float32 [batch, width] tensor")
     if states.numel():
         need = _native.query("koemi_gated_projection_scan_workspace_bytes", batch, length, width)
         workspace = torch.empty(need, device=x.device, dtype=torch.uint8)
@@ -306,7 +311,8 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
             "koemi_gated_projection_scan",
             _native.ptr(x), _native.ptr(w), _native.ptr(bias.contiguous()) if bias is not None else None,
             _native.ptr(mask) if mask is not None else None, _native.ptr(initial.contiguous()), _native.ptr(states),
-            _native.ptr(states16), states16.stride(1) if states16 is not None else 0, batch, length, width, k,
+            _native.ptr(states16), states16.stride(1) if states16 is not None else 0, _native.ptr(final_out),
+            batch, length, width, k,
             _native.ptr(workspace), need, _native.stream_of(x.device),
         )
     return (states, states16) if with_bf16 else states

@@ -225,10 +225,13 @@ def test_gated_projection_scan_matches_oracle(device, b, length, k, d, p):
     z = torch.addmm(bias.float(), u.reshape(-1, k).float(), w.float().t()).view(b, length, 2 * d)
     z16 = z.to(torch.bfloat16)
     wide = torch.zeros((b, length, 3 * d), device=device, dtype=torch.bfloat16)
-    got, got16 = recurrent.gated_projection_scan(u, w, bias, valid, h0, with_bf16=True, out_bf16=wide[..., d:2 * d])
+    fin = torch.full((b, d), float("nan"), device=device)
+    got, got16 = recurrent.gated_projection_scan(u, w, bias, valid, h0, with_bf16=True, out_bf16=wide[..., d:2 * d],
+                                                 final_out=fin)
     ref = recurrent.gated_scan(z16, valid, h0, width=d)
     torch.cuda.synchronize()
     assert torch.equal(got16, got.to(torch.bfloat16))
+    assert torch.equal(fin, got[:, -1])
     assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
     diff = (got - ref).abs().max().item()
     select = lambda off: np.eye(2 * d)[off:off + d]
