@@ -197,6 +197,15 @@ int koemi_moe_expert_counts(const void* assignments, int assignment_dtype,
  * pairs). Context dtype F32/F16/BF16; assignments I32/I64. expert_count <= 4095.
  * sorted_context may be NULL: only the indices are formed (for
  * koemi_moe_grouped_mlp_indexed, which reads the context rows by sorted_rows). */
+/* The index phase of koemi_moe_permute alone (no context; a build-side entry
+ * for the HERM block), which also hands over its pair -> position map:
+ * pair_positions[t * top_k + s] = the sorted position of pair (t, s) (valid
+ * pairs below segment_offsets[E]). Same workspace as koemi_moe_permute. */
+int koemi_moe_permute_indices(const void* assignments, int assignment_dtype, const uint8_t* valid_mask,
+                              const float* pair_weights, int64_t* sorted_rows, int64_t* sorted_experts,
+                              int64_t* segment_offsets, float* sorted_weights, int64_t* pair_positions,
+                              int64_t tokens, int64_t top_k, int64_t expert_count, void* workspace,
+                              size_t workspace_bytes, koemi_stream_t stream);
 size_t koemi_moe_permute_workspace_bytes(int64_t tokens, int64_t top_k, int64_t expert_count);
 int koemi_moe_permute(const void* context, int context_dtype, const void* assignments,
                       int assignment_dtype, const uint8_t* valid_mask, const float* pair_weights,
@@ -230,8 +239,9 @@ int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* sorted_expe
  * GEMM's operand tiles. bf16 only, width and hidden multiples of 64, 16-byte
  * aligned operands, tokens * width < 2^31; the workspace of
  * koemi_moe_grouped_mlp_workspace_bytes(pairs, width, hidden, expert_count,
- * KOEMI_BF16). The outputs equal koemi_moe_grouped_mlp's on the gathered
- * context bit for bit. */
+ * KOEMI_BF16). The rows of the valid pairs equal koemi_moe_grouped_mlp's
+ * on the gathered context bit for bit; the rows past them (pairs >=
+ * segment_offsets[E]) are not written. */
 int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens, const int64_t* sorted_rows,
                                   const int64_t* segment_offsets, const void* gate_weights, const void* gate_biases,
                                   const void* value_weights, const void* value_biases, const void* output_weights,
@@ -564,10 +574,14 @@ int koemi_moe_combine(const void* expert_outputs, const int64_t* sorted_rows,
  * separate kernels do (koemi_moe_combine, then koemi_herm_rmsnorm twice), so
  * the outputs are the same bits. context [tokens, width] fp32; output (NULL:
  * none) [tokens, width] fp32; next_input_bf16 (NULL: none) [tokens, width]
- * bf16. top_k <= 8, width % 4 == 0 and <= 2048, 16-byte aligned rows; the
- * workspace of koemi_moe_combine_workspace_bytes(tokens, top_k). */
-int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_rows, const int64_t* segment_offsets,
-                            const float* pair_weights, const float* context, const uint8_t* mask,
+ * bf16. top_k <= 8, width % 4 == 0 and <= 2048, 16-byte aligned rows. The
+ * pairs of each token come from pair_positions when given (the permutation's
+ * pair -> sorted position map of koemi_moe_permute_indices; no workspace),
+ * else from inverting sorted_rows (the workspace of
+ * koemi_moe_combine_workspace_bytes(tokens, top_k)). */
+int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_rows, const int64_t* pair_positions,
+                            const int64_t* segment_offsets, const float* pair_weights, const float* context,
+                            const uint8_t* mask,
                             const float* expert_norm_weight, const float* next_norm_weight, float* output,
                             void* next_input_bf16, int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
                             int64_t num_segments, float eps, void* workspace, size_t workspace_bytes,

@@ -283,21 +283,37 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
 // the arithmetic of the separate kernels it replaces (the same bits): lane l
 // holds columns (j * 64 + l) * 4 .. + 3, j < NV; the sum of squares runs in
 // (j, i) order per lane, then over the lanes by xor butterfly.
-template <int KMAX, int NV>
+// POS: pos holds every pair's sorted position (the permutation's own
+// pair -> position map, k per token; a pair is valid when its position is
+// below *valid_end) and cnt is unused; otherwise cnt / pos come from the
+// inversion above (the first cnt[t] entries of the token's row).
+template <int KMAX, int NV, bool POS>
 __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     const bf16* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
-    const float* __restrict__ pair_w, const float* __restrict__ ctx, const uint8_t* __restrict__ mask,
-    const float* __restrict__ w_expert, const float* __restrict__ w_next, float* __restrict__ out,
-    bf16* __restrict__ out_next, int64_t tokens, int64_t k, int H, float eps) {
+    const int64_t* __restrict__ valid_end, const float* __restrict__ pair_w, const float* __restrict__ ctx,
+    const uint8_t* __restrict__ mask, const float* __restrict__ w_expert, const float* __restrict__ w_next,
+    float* __restrict__ out, bf16* __restrict__ out_next, int64_t tokens, int64_t k, int H, float eps) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
     if (t >= tokens) return;
     const int lane = lane_id();
-    const int n = static_cast<int>(min(static_cast<int64_t>(cnt[t]), k));
+    int n = 0;
     int64_t p[KMAX];
+    if constexpr (POS) {
+        const int64_t end = *valid_end;
 #pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-        const int64_t pj = pos[t * k + min(static_cast<int64_t>(j), k - 1)];
-        p[j] = j < n ? pj : INT64_MAX;
+        for (int j = 0; j < KMAX; ++j) {
+            const int64_t pj = j < k ? pos[t * k + j] : INT64_MAX;
+            const bool ok = pj >= 0 && pj < end;
+            p[j] = ok ? pj : INT64_MAX;
+            n += ok ? 1 : 0;
+        }
+    } else {
+        n = static_cast<int>(min(static_cast<int64_t>(cnt[t]), k));
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            const int64_t pj = pos[t * k + min(static_cast<int64_t>(j), k - 1)];
+            p[j] = j < n ? pj : INT64_MAX;
+        }
     }
     sort_positions<KMAX>(p);
     const float kf = static_cast<float>(k);
@@ -430,7 +446,8 @@ extern "C" int koemi_moe_combine(const void* expert_outputs, const int64_t* sort
 
 
 extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_rows,
-                                       const int64_t* segment_offsets, const float* pair_weights, const float* context,
+                                       const int64_t* pair_positions, const int64_t* segment_offsets,
+                                       const float* pair_weights, const float* context,
                                        const uint8_t* mask, const float* expert_norm_weight,
                                        const float* next_norm_weight, float* output, void* next_input_bf16,
                                        int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
@@ -441,20 +458,40 @@ extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t
     if (num_segments < 1) return fail(KOEMI_ERR_INVALID, "segment_offsets must have at least two entries");
     if (width % 4 != 0 || width > 4 * kWave * 8)
         return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs a width that is a multiple of 4 and at most 2048");
-    if (!segment_offsets || !context || !expert_norm_weight || (pairs > 0 && (!expert_outputs || !sorted_rows)))
+    if (!segment_offsets || !context || !expert_norm_weight ||
+        (pairs > 0 && (!expert_outputs || (!sorted_rows && !pair_positions))))
         return fail(KOEMI_ERR_INVALID, "combine norm received a null pointer");
     if (!output && !(next_norm_weight && next_input_bf16))
         return fail(KOEMI_ERR_INVALID, "combine norm has no output");
     if ((reinterpret_cast<uintptr_t>(expert_outputs) | reinterpret_cast<uintptr_t>(context) |
          reinterpret_cast<uintptr_t>(output) | reinterpret_cast<uintptr_t>(next_input_bf16)) % 16)
         return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs 16-byte aligned rows");
+    hipStream_t s = as_stream(stream);
+    const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+    const bf16* y = static_cast<const bf16*>(expert_outputs);
+    bf16* o16 = static_cast<bf16*>(next_input_bf16);
+    const int H = static_cast<int>(width);
+    const bool wide = width > 4 * kWave * 4;
+    const int64_t* valid_end = segment_offsets + num_segments;
+    auto launch = [&](auto kernel, const int32_t* cnt, const int64_t* pos) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, y, cnt, pos, valid_end, pair_weights, context, mask,
+                           expert_norm_weight, next_norm_weight, output, o16, tokens, top_k, H, eps);
+        return check_launch("koemi_herm_combine_norm(rows)");
+    };
+    if (pair_positions != nullptr) {  // the permutation's own map: no inversion
+        if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8, true>, nullptr, pair_positions)
+                                    : launch(combine_norm_kernel<2, 4, true>, nullptr, pair_positions);
+        if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8, true>, nullptr, pair_positions)
+                                    : launch(combine_norm_kernel<4, 4, true>, nullptr, pair_positions);
+        return wide ? launch(combine_norm_kernel<8, 8, true>, nullptr, pair_positions)
+                    : launch(combine_norm_kernel<8, 4, true>, nullptr, pair_positions);
+    }
     const CombineWorkspace ws = combine_workspace(tokens, top_k);
     if (!workspace || workspace_bytes < ws.total)
         return fail(KOEMI_ERR_INVALID, "combine norm workspace too small: need %zu bytes", ws.total);
     char* base = static_cast<char*>(workspace);
     int32_t* cnt = reinterpret_cast<int32_t*>(base + ws.cnt_off);
     int64_t* pos = reinterpret_cast<int64_t*>(base + ws.pos_off);
-    hipStream_t s = as_stream(stream);
     int st = KOEMI_OK;
     if (tokens <= kSmallInvertTokens && pairs <= 4096) {
         hipLaunchKernelGGL(invert_rows_small_kernel, dim3(1), dim3(1024), 0, s, sorted_rows,
@@ -470,17 +507,10 @@ extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t
         }
     }
     if (st != KOEMI_OK) return st;
-    const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
-    const bf16* y = static_cast<const bf16*>(expert_outputs);
-    bf16* o16 = static_cast<bf16*>(next_input_bf16);
-    const int H = static_cast<int>(width);
-    auto launch = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, block, 0, s, y, cnt, pos, pair_weights, context, mask, expert_norm_weight,
-                           next_norm_weight, output, o16, tokens, top_k, H, eps);
-        return check_launch("koemi_herm_combine_norm(rows)");
-    };
-    const bool wide = width > 4 * kWave * 4;
-    if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8>) : launch(combine_norm_kernel<2, 4>);
-    if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8>) : launch(combine_norm_kernel<4, 4>);
-    return wide ? launch(combine_norm_kernel<8, 8>) : launch(combine_norm_kernel<8, 4>);
+    if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8, false>, cnt, pos)
+                                : launch(combine_norm_kernel<2, 4, false>, cnt, pos);
+    if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8, false>, cnt, pos)
+                                : launch(combine_norm_kernel<4, 4, false>, cnt, pos);
+    return wide ? launch(combine_norm_kernel<8, 8, false>, cnt, pos)
+                : launch(combine_norm_kernel<8, 4, false>, cnt, pos);
 }

@@ -167,10 +167,12 @@ __device__ __forceinline__ void tile_coords(uint32_t logical, uint32_t slots, ui
 
 // Work of one GEMM launch: `whole` tiles computed in full, then, when the tiles
 // left over after whole rounds of `cus` workgroups (those that run at once)
-// would fill at most half a round, each leftover tile split along K into
-// `split` chunks (at least two K steps each) so that the last round keeps
-// every CU busy. Partial tiles go to
-// the workspace as fp32 and a fixup kernel adds them in chunk order.
+// would fill at most a third of a round, each leftover tile split along K into
+// `split` >= 3 chunks (at least two K steps each) so that the last round keeps
+// every CU busy. Partial tiles go to the workspace as fp32 and a fixup kernel
+// adds them in chunk order. (A two-way split measured slower than the
+// half-empty round it replaces: its fp32 partials and the fix-up launch cost
+// more than the half tile it saves.)
 struct SplitPlan {
     uint32_t whole, units, split;
 };
@@ -184,10 +186,10 @@ __device__ __forceinline__ int partial_slot(int wave, int mt, int t, int j, int 
 __device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uint32_t cus) {
     SplitPlan p{tiles, 0, 1};
     const uint32_t rem = tiles % cus;
-    if (rem > 0 && rem * 2 <= cus) {
+    if (rem > 0 && rem * 3 <= cus) {
         const uint32_t s =
             min(min(min(cus, static_cast<uint32_t>(kMaxSplitUnits)) / rem, nk / 2), static_cast<uint32_t>(kMaxSplit));
-        if (s >= 2) {
+        if (s >= 3) {
             p.whole = tiles - rem;
             p.units = rem * s;
             p.split = s;
@@ -751,9 +753,11 @@ int64_t device_cus() {
 }
 
 // x_index (or null): GEMM 1 reads context row x_index[i] (of x_rows) for pair i.
+// zero_tail: the rows past the valid pairs are zeroed (the reference's output
+// contract); the indexed entry leaves them, as nothing reads them.
 int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_t* offsets, const void* Wg,
              const void* bg, const void* Wv, const void* bv, const void* Wo, const void* bo, void* y, int64_t P,
-             int64_t D, int64_t Hd, int64_t E, const MlpWorkspace& ws, char* base, hipStream_t s) {
+             int64_t D, int64_t Hd, int64_t E, const MlpWorkspace& ws, char* base, hipStream_t s, bool zero_tail) {
     bf16* H = reinterpret_cast<bf16*>(base + ws.hidden_off);
     int32_t* slot_expert = reinterpret_cast<int32_t*>(base + ws.slot_expert_off);
     int64_t* slot_row = reinterpret_cast<int64_t*>(base + ws.slot_row_off);
@@ -774,7 +778,7 @@ int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_
         int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
         if (st != KOEMI_OK) return st;
         // the output GEMM's launch also zeroes the rows past the valid pairs (extra workgroups)
-        const int64_t tail_wgs = P < 64 ? P : 64;
+        const int64_t tail_wgs = zero_tail ? (P < 64 ? P : 64) : 0;
         hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2 + tail_wgs)),
                            dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const int64_t*>(nullptr), P,
                            static_cast<const bf16*>(Wo),
@@ -823,6 +827,7 @@ int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_
                 static_cast<bf16*>(y), D, Hd, (D + BNT - 1) / BNT,
                 "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
+    if (!zero_tail) return KOEMI_OK;
     hipLaunchKernelGGL(zero_tail_rows_kernel<bf16>, dim3(tail_blocks(P)), dim3(256), 0, s, static_cast<bf16*>(y),
                        offsets + E, P, D);
     return check_launch("koemi_moe_grouped_mlp(zero)");
@@ -867,7 +872,7 @@ extern "C" int koemi_moe_grouped_mlp(const void* sorted_context, const int64_t* 
     if (mfma_shape(width, hidden, dtype))
         return run_mfma(sorted_context, nullptr, pairs, segment_offsets, gate_weights, gate_biases, value_weights,
                         value_biases, output_weights, output_biases, output, pairs, width, hidden, expert_count, ws,
-                        base, s);
+                        base, s, true);
     float* H = reinterpret_cast<float*>(base + ws.hidden_off);
     switch (dtype) {
         case KOEMI_F32:
@@ -913,5 +918,5 @@ extern "C" int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens
     if (!aligned) return fail(KOEMI_ERR_INVALID, "grouped MLP bf16 operands must be 16-byte aligned");
     return run_mfma(context, sorted_rows, tokens, segment_offsets, gate_weights, gate_biases, value_weights,
                     value_biases, output_weights, output_biases, output, pairs, width, hidden, expert_count, ws,
-                    static_cast<char*>(workspace), as_stream(stream));
+                    static_cast<char*>(workspace), as_stream(stream), false);
 }

@@ -481,3 +481,33 @@ extern "C" int koemi_moe_permute(const void* context, int context_dtype, const v
         default: return run_gather<bf16>(context, dest, offsets_end, sorted_context, tokens, top_k, width, s);
     }
 }
+
+extern "C" int koemi_moe_permute_indices(const void* assignments, int assignment_dtype, const uint8_t* valid_mask,
+                                         const float* pair_weights, int64_t* sorted_rows, int64_t* sorted_experts,
+                                         int64_t* segment_offsets, float* sorted_weights, int64_t* pair_positions,
+                                         int64_t tokens, int64_t top_k, int64_t expert_count, void* workspace,
+                                         size_t workspace_bytes, koemi_stream_t stream) {
+    if (tokens < 1) return fail(KOEMI_ERR_INVALID, "permute needs tokens >= 1");
+    if (top_k < 1 || top_k > 256) return fail(KOEMI_ERR_INVALID, "assignments top_k is outside [1, 256]");
+    if (expert_count < 1 || top_k > expert_count) return fail(KOEMI_ERR_INVALID, "top_k must not exceed expert_count");
+    if (expert_count > kMaxExperts) return fail(KOEMI_ERR_UNSUPPORTED, "permute supports at most %d experts", kMaxExperts);
+    if (!index_dtype(assignment_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "assignments must be int32 or int64");
+    if ((pair_weights == nullptr) != (sorted_weights == nullptr))
+        return fail(KOEMI_ERR_INVALID, "pair_weights and sorted_weights must both be given or both be null");
+    if (!assignments || !valid_mask || !sorted_rows || !sorted_experts || !segment_offsets || !pair_positions)
+        return fail(KOEMI_ERR_INVALID, "permute received a null pointer");
+    const PermuteWorkspace ws = permute_workspace(tokens, top_k, expert_count);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "permute workspace too small: need %zu bytes", ws.total);
+    if (num_chunks(tokens * top_k) > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many pairs");
+    int32_t* counts = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ws.counts_off);
+    hipStream_t s = as_stream(stream);
+    const int64_t pairs = tokens * top_k;
+    return (assignment_dtype == KOEMI_I32)
+               ? run_index_phase<int32_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                                          segment_offsets, sorted_weights, counts, pair_positions, pairs, top_k,
+                                          expert_count, s)
+               : run_index_phase<int64_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                                          segment_offsets, sorted_weights, counts, pair_positions, pairs, top_k,
+                                          expert_count, s);
+}

@@ -499,10 +499,15 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
     # permutation's indices (no sorted copy of the context)
     indexed = moe_in.dtype == torch.bfloat16 and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
-    permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count,
-                                pair_weights=weights, validate=False, gather=not indexed)
-    sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
-    sorted_weights = permuted[4] if weights is not None else None
+    pair_positions = None
+    if indexed:
+        sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = moe.permute_indices(
+            assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count, pair_weights=weights)
+    else:
+        permuted = moe.permute_topk(moe_in, assignments.reshape(-1, k), flat_valid,
+                                    expert_count=settings.expert_count, pair_weights=weights, validate=False)
+        sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
+        sorted_weights = permuted[4] if weights is not None else None
     if indexed:
         expert_out = moe.grouped_expert_mlp_indexed(moe_in, sorted_rows, offsets, p["gate_w"], p["gate_b"],
                                                     p["up_w"], p["up_b"], p["down_w"], p["down_b"])
@@ -514,10 +519,11 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         tokens = flat.shape[0]
         final = torch.empty((tokens, d), device=flat.device, dtype=torch.float32) if with_logits else None
         u_next = torch.empty((tokens, d), device=flat.device, dtype=torch.bfloat16)
-        need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k)
-        workspace = torch.empty((need,), device=flat.device, dtype=torch.uint8)
+        need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k) if pair_positions is None else 0
+        workspace = torch.empty((need,), device=flat.device, dtype=torch.uint8) if need else None
         _native.call("koemi_herm_combine_norm", _native.ptr(expert_out), _native.ptr(sorted_rows),
-                     _native.ptr(offsets), _native.ptr(sorted_weights), _native.ptr(flat.contiguous()),
+                     _native.ptr(pair_positions), _native.ptr(offsets), _native.ptr(sorted_weights),
+                     _native.ptr(flat.contiguous()),
                      _native.ptr(flat_valid), _native.ptr(p["expert_norm"]), _native.ptr(next_norm),
                      _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]), d, tokens, k,
                      settings.expert_count, _EPS, _native.ptr(workspace), need, _native.stream_of(flat.device))

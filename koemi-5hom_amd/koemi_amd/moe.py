@@ -487,6 +487,41 @@ def grouped_expert_mlp_inference(
     return output
 
 
+def permute_indices(assignments: Tensor, valid_mask: Tensor, *, expert_count: int,
+                    pair_weights: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor, Tensor | None, Tensor]:
+    """The index phase of ``permute_topk`` without a context
+    (``koemi_moe_permute_indices``, build-side): returns ``(sorted_rows,
+    sorted_experts, segment_offsets, sorted_weights or None,
+    pair_positions)``, the first four as ``permute_topk`` forms them and
+    ``pair_positions`` [tokens * top_k] int64 the sorted position of each pair
+    (valid pairs below ``segment_offsets[-1]``). No validation beyond shapes
+    (the HERM block's own routing)."""
+
+    if assignments.ndim != 2 or assignments.dtype not in (torch.int32, torch.int64):
+        raise CudaMoeValidationError("assignments must be an int32 or int64 [token_count, top_k] tensor")
+    tokens, top_k = assignments.shape
+    if valid_mask.shape != (tokens,) or top_k > expert_count or expert_count > _MAX_PERMUTE_EXPERTS:
+        raise CudaMoeValidationError("valid_mask must be [token_count] and top_k <= expert_count <= the permute limit")
+    _require_library()
+    device = assignments.device
+    pairs = tokens * top_k
+    sorted_rows = torch.empty((pairs,), device=device, dtype=torch.int64)
+    sorted_experts = torch.empty((pairs,), device=device, dtype=torch.int64)
+    segment_offsets = torch.empty((expert_count + 1,), device=device, dtype=torch.int64)
+    sorted_weights = torch.empty((pairs,), device=device, dtype=torch.float32) if pair_weights is not None else None
+    pair_positions = torch.empty((pairs,), device=device, dtype=torch.int64)
+    need = _native.query("koemi_moe_permute_workspace_bytes", tokens, top_k, expert_count)
+    workspace = torch.empty((need,), device=device, dtype=torch.uint8)
+    with torch.cuda.device(device):
+        _native.call("koemi_moe_permute_indices", assignments.contiguous().data_ptr(),
+                     _native.dtype_code(assignments.dtype), valid_mask.contiguous().data_ptr(),
+                     _native.ptr(pair_weights.contiguous() if pair_weights is not None else None),
+                     sorted_rows.data_ptr(), sorted_experts.data_ptr(), segment_offsets.data_ptr(),
+                     _native.ptr(sorted_weights), pair_positions.data_ptr(), tokens, top_k, expert_count,
+                     workspace.data_ptr(), need, _native.stream_of(device))
+    return sorted_rows, sorted_experts, segment_offsets, sorted_weights, pair_positions
+
+
 def grouped_expert_mlp_indexed(
     context: Tensor,
     sorted_rows: Tensor,
@@ -502,8 +537,9 @@ def grouped_expert_mlp_indexed(
     gather=False)`` without the sorted copy of the context: pair i reads row
     ``sorted_rows[i]`` of ``context`` ([tokens, width] bf16) straight into the
     first GEMM's operand tiles (``koemi_moe_grouped_mlp_indexed``). The
-    outputs ([pairs, width], pairs = ``sorted_rows.numel()``) equal
-    ``grouped_expert_mlp_inference`` on the gathered rows bit for bit. bf16
+    output rows of the valid pairs ([pairs, width], pairs =
+    ``sorted_rows.numel()``) equal ``grouped_expert_mlp_inference`` on the
+    gathered rows bit for bit; the rows past them are left unwritten. bf16
     with width and hidden multiples of 64 only (the MFMA path); no validation
     of the index tensors beyond their shapes (indices are clamped on the
     device)."""

@@ -363,14 +363,19 @@ def test_combine_norm_equals_combine_then_the_two_norms(device, tokens, learned)
     update = moe.combine_topk(y, rows, offsets, token_count=tokens, top_k=k, pair_weights=sw, validate=False)
     want_final = herm._rms(flat, w_e, residual=update, mask=valid)
     want_next = herm._rms(want_final, w_n, fp32=False, low=torch.bfloat16)[1]
-    final = torch.empty_like(flat)
-    nxt = torch.empty((tokens, d), device=device, dtype=torch.bfloat16)
     need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k)
     workspace = torch.empty((need,), device=device, dtype=torch.uint8)
-    _native.call("koemi_herm_combine_norm", _native.ptr(y), _native.ptr(rows), _native.ptr(offsets), _native.ptr(sw),
-                 _native.ptr(flat), _native.ptr(valid), _native.ptr(w_e), _native.ptr(w_n), _native.ptr(final),
-                 _native.ptr(nxt), int(y.shape[0]), d, tokens, k, E, herm._EPS, _native.ptr(workspace), need,
-                 _native.stream_of(device))
-    torch.cuda.synchronize()
-    assert torch.equal(final, want_final)
-    assert torch.equal(nxt, want_next)
+    # pairs from the inversion of sorted_rows, and from the permutation's own map
+    rows3, _, offsets3, sw3, positions = moe.permute_indices(a, valid, expert_count=E, pair_weights=w)
+    assert torch.equal(rows3, rows) and torch.equal(offsets3, offsets)
+    for by_position in (False, True):
+        final = torch.empty_like(flat)
+        nxt = torch.empty((tokens, d), device=device, dtype=torch.bfloat16)
+        _native.call("koemi_herm_combine_norm", _native.ptr(y), _native.ptr(rows),
+                     _native.ptr(positions if by_position else None), _native.ptr(offsets), _native.ptr(sw),
+                     _native.ptr(flat), _native.ptr(valid), _native.ptr(w_e), _native.ptr(w_n), _native.ptr(final),
+                     _native.ptr(nxt), int(y.shape[0]), d, tokens, k, E, herm._EPS, _native.ptr(workspace), need,
+                     _native.stream_of(device))
+        torch.cuda.synchronize()
+        assert torch.equal(final, want_final), by_position
+        assert torch.equal(nxt, want_next), by_position

@@ -304,9 +304,10 @@ def test_config4_pipeline(device, learned):
 ])
 def test_indexed_grouped_mlp_equals_the_gathered_one(device, tokens, E, D, H, seed):
     """permute_topk(gather=False) + grouped_expert_mlp_indexed (context rows read
-    by sorted_rows inside the first GEMM) give the same bits as the gathered
-    sorted context through grouped_expert_mlp_inference: the same tiles, the
-    same accumulation order, only the operand addresses differ."""
+    by sorted_rows inside the first GEMM) give the same bits, on the valid
+    pairs, as the gathered sorted context through grouped_expert_mlp_inference:
+    the same tiles, the same accumulation order, only the operand addresses
+    differ."""
     g = torch.Generator(device=device).manual_seed(seed)
     ctx = torch.randn((tokens, D), generator=g, device=device).to(torch.bfloat16)
     ids = torch.randint(0, 256, (tokens,), generator=g, device=device)
@@ -321,7 +322,8 @@ def test_indexed_grouped_mlp_equals_the_gathered_one(device, tokens, E, D, H, se
     want = moe.grouped_expert_mlp_inference(sc, experts, offsets, *ws)
     got = moe.grouped_expert_mlp_indexed(ctx, rows2, offsets2, *ws)
     torch.cuda.synchronize()
-    assert torch.equal(got, want)
+    n = int(offsets[-1])  # the rows past the valid pairs are not written by the indexed form
+    assert torch.equal(got[:n], want[:n])
 
 
 @pytest.mark.parametrize("tokens, k, E, learned", [(64, 2, 16, False), (300, 3, 13, True), (1, 2, 4, False)])
