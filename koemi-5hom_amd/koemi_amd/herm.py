@@ -284,7 +284,7 @@ def _fused_gates(p: dict[str, Tensor], u: Tensor) -> bool:
 
 
 def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor, width: int, with_bf16: bool,
-                out_bf16: Tensor | None, final_out: Tensor | None = None):
+                out_bf16: Tensor | None, final_out: Tensor | None = None, states_out: Tensor | None = None):
     """The gate projection and the fused gates + scan: for a bf16 stack
     outside decode steps the projection's results are bf16 with the biases in
     the GEMM epilogue (nn.Linear under bf16 autocast) — in one kernel with the
@@ -293,7 +293,8 @@ def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor,
     results without bias and the biases added inside the scan kernel.
     ``final_out``: where the fused kernel writes the last position's states
     (the next carried state), when that kernel runs; the caller checks
-    ``_fused_gates(p, u)``."""
+    ``_fused_gates(p, u)``. ``states_out``: the buffer for the states on the
+    other paths (a decode graph's static state)."""
 
     w = p["gates_w"]
     if _fused_gates(p, u):
@@ -301,10 +302,10 @@ def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor,
                                                out_bf16=out_bf16, final_out=final_out)
     if w.dtype == torch.bfloat16 and not _few_rows(u, w):
         return recurrent.gated_scan(_linear_low(u, w, p["gates_b16"]), valid, working, width=width,
-                                    with_bf16=with_bf16, out_bf16=out_bf16)
+                                    with_bf16=with_bf16, out_bf16=out_bf16, out=states_out)
     return recurrent.gated_scan(_linear(u, w, None), valid, working, width=width, with_bf16=with_bf16,
                                 retention_bias=p["gates_b"][:width], candidate_bias=p["gates_b"][width:],
-                                out_bf16=out_bf16)
+                                out_bf16=out_bf16, out=states_out)
 
 
 def _fusion_input(settings: HermSettings, batch: int, length: int, device: torch.device) -> Tensor | None:
@@ -353,17 +354,18 @@ def _few_rows(x: Tensor, weight: Tensor) -> bool:
             and x.shape[-1] % 64 == 0 and x.shape[-1] <= 1024 and x.dtype in (torch.float32, torch.bfloat16))
 
 
-def _token_context(ids: Tensor, valid: Tensor | None, carried: Tensor
+def _token_context(ids: Tensor, valid: Tensor | None, carried: Tensor, last_out: Tensor | None = None
                    ) -> tuple[Tensor, Tensor] | tuple[Tensor, Tensor, Tensor, Tensor]:
     """The previous valid token of each position and the last valid token of
     each row (network.py:742-761) on ``koemi_herm_token_context``. With
     ``valid`` None the kernel also forms the validity ``ids != PAD`` and the
     surprise targets (ids, 0 where invalid) and the call returns
-    ``(previous, last, valid, targets)``."""
+    ``(previous, last, valid, targets)``. ``last_out``: the buffer that
+    receives the last tokens (a graph's static state)."""
 
     batch, length = ids.shape
     previous = torch.empty_like(ids)
-    last = torch.empty_like(carried)
+    last = torch.empty_like(carried) if last_out is None else last_out
     formed = valid is None
     valid_out = torch.empty(ids.shape, device=ids.device, dtype=torch.bool) if formed else None
     targets = torch.empty_like(ids) if formed else None
@@ -374,16 +376,20 @@ def _token_context(ids: Tensor, valid: Tensor | None, carried: Tensor
 
 
 def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: Tensor,
-                window: int) -> tuple[Tensor, Tensor, Tensor]:
+                window: int, out: dict[str, Tensor] | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """LocalKeyValueMemory.tail (memory.py:385-403) of a static ring of
-    ``window`` entries on ``koemi_herm_local_tail``."""
+    ``window`` entries on ``koemi_herm_local_tail``; with ``out`` (a state
+    dict) into its ring buffers."""
 
     batch, length, width = keys.shape
     if state["local_keys"].shape[1] != window:
         raise ValueError("the local ring must hold exactly `window` entries (static state)")
-    out_k = torch.empty_like(state["local_keys"])
-    out_v = torch.empty_like(state["local_values"])
-    out_ok = torch.empty_like(state["local_valid"])
+    if out is not None:
+        out_k, out_v, out_ok = out["local_keys"], out["local_values"], out["local_valid"]
+    else:
+        out_k = torch.empty_like(state["local_keys"])
+        out_v = torch.empty_like(state["local_values"])
+        out_ok = torch.empty_like(state["local_valid"])
     _native.call("koemi_herm_local_tail", _native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
                  _native.ptr(state["local_valid"]), _native.ptr(keys), _native.ptr(values), _native.ptr(valid),
                  _native.ptr(out_k), _native.ptr(out_v), _native.ptr(out_ok), batch, window, length, width,
@@ -392,7 +398,8 @@ def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: T
 
 
 def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor, normalizer: Tensor,
-                          *, width: int, features: int, out: Tensor | None = None) -> tuple[Tensor, Tensor, Tensor]:
+                          *, width: int, features: int, out: Tensor | None = None,
+                          next_out: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor, Tensor]:
     """The associative memory of one window on ``koemi_assoc_scan_read``:
     projection tail, fast write terms with the write masking and
     scan_and_read (memory.py:82-144, 244-255; network.py:734-740).
@@ -405,7 +412,8 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     ``surprise`` ``[B, L]`` fp32, ``valid`` ``[B, L]`` bool, ``basis``
     ``[B, D, M]``, ``normalizer`` ``[B, M]`` fp32. Returns (reads ``[B, L, D]``,
     next basis, next normalizer); with ``out`` (an fp32 or bf16 ``[B, L, D]``
-    view with evenly spaced rows, L > 1) the reads are written there.
+    view with evenly spaced rows, L > 1) the reads are written there, with
+    ``next_out`` (contiguous buffers) the next basis and normalizer.
     """
 
     batch, length, stride = projections.shape
@@ -415,8 +423,8 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
         raise ValueError("projections must be contiguous fp32 or bf16 [batch, length, >= 3 * width + 2 * features + 2]")
     read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32) if out is None else out
     read_stride = memory._row_stride(read, (batch, length, d))
-    next_basis = torch.empty_like(basis)
-    next_normalizer = torch.empty_like(normalizer)
+    next_basis, next_normalizer = next_out if next_out is not None else (torch.empty_like(basis),
+                                                                         torch.empty_like(normalizer))
     need = _native.query("koemi_assoc_scan_read_workspace_bytes", batch, length, d, m)
     workspace = torch.empty((need,), device=projections.device, dtype=torch.uint8) if need else None
     args = [t.contiguous() for t in (surprise, valid, basis, normalizer)]
@@ -539,7 +547,7 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
                  context: Tensor | NextInput | None = None, *, with_logits: bool = True,
                  token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
-                 next_norm: Tensor | None = None
+                 next_norm: Tensor | None = None, out_state: dict[str, Tensor] | None = None
                  ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
@@ -550,7 +558,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     ``_token_context``'s four outputs when the caller formed them (a decode
     step's stack, once for all layers). ``next_norm``: the next block's input
     norm weight, for a stack; the context returned is then a ``NextInput``
-    (see ``_fuse_mix_predict``)."""
+    (see ``_fuse_mix_predict``). ``out_state`` (a decode step, one position):
+    a state dict whose buffers receive the next state (a decode graph's other
+    static state; ``last_token`` is the caller's, from the token context)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
@@ -563,7 +573,11 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     low = lin if lin == torch.bfloat16 else None  # kernels write bf16 copies of the GEMM inputs
     u = _input_norm(p, ids, context, low)
     fusion_in = _fusion_input(settings, batch, length, ids.device)
-    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d))
+    if out_state is not None and (length != 1 or _fused_gates(p, u)):
+        raise ValueError("out_state is for decode steps (one position)")
+    states_out = out_state["working"].view(batch, 1, d) if out_state is not None else None
+    scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d),
+                          states_out=states_out)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
@@ -588,9 +602,10 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                local_keys, local_values, valid, ws, window=settings.local_memory_size,
                                                out=_block(fusion_in, 2, d))
 
-    fast, basis, normalizer = associative_scan_read(projected, surprise, valid, state["basis"], state["normalizer"],
-                                                    width=d, features=settings.memory_features,
-                                                    out=_block(fusion_in, 1, d))
+    fast, basis, normalizer = associative_scan_read(
+        projected, surprise, valid, state["basis"], state["normalizer"], width=d, features=settings.memory_features,
+        out=_block(fusion_in, 1, d),
+        next_out=(out_state["basis"], out_state["normalizer"]) if out_state is not None else None)
 
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
@@ -599,9 +614,12 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     pieces = fusion_in if fusion_in is not None else (ws, fast, local_value, salient_value)
     final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
 
-    local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size)
-    salient = memory.salient_tail(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
-                                  local_values, admission, settings.salience_memory_size)
+    local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size, out=out_state)
+    salient = memory.salient_tail(
+        state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys, local_values, admission,
+        settings.salience_memory_size,
+        out=(out_state["salient_keys"], out_state["salient_values"], out_state["salient_valid"])
+        if out_state is not None else None)
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
@@ -893,14 +911,17 @@ class SequencePrefill:
 
 
 def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
-                  states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+                  states: list[dict[str, Tensor]], out_states: list[dict[str, Tensor]] | None = None
+                  ) -> tuple[Tensor, list[dict[str, Tensor]]]:
     """One decode position ([B, 1] ids) through every layer, the token context
     formed once for all of them (every layer sees the same ids and carries the
     same last token): one kernel per step instead of one per layer. Otherwise
-    ``block_window`` layer after layer."""
+    ``block_window`` layer after layer. ``out_states``: state dicts whose
+    buffers receive the next states (all layers' ``last_token`` one buffer)."""
 
     ids = ids.contiguous()
-    token_context = _token_context(ids, None, states[0]["last_token"])
+    token_context = _token_context(ids, None, states[0]["last_token"],
+                                   out_states[0]["last_token"] if out_states is not None else None)
     context = None
     next_states = []
     logits = None
@@ -908,7 +929,8 @@ def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: 
         last = layer == len(params) - 1
         logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
                                                       token_context=token_context,
-                                                      next_norm=None if last else params[layer + 1]["input_norm"])
+                                                      next_norm=None if last else params[layer + 1]["input_norm"],
+                                                      out_state=out_states[layer] if out_states is not None else None)
         next_states.append(next_state)
     return logits, next_states
 
@@ -1012,13 +1034,62 @@ class WindowGraph:
         return self.logits
 
 
-class DecodeGraph(WindowGraph):
-    """Greedy decode steps (``decode_step``) replayed from one captured HIP
-    graph; ``step()`` advances ``self.ids`` ``[B, 1]`` and ``self.states`` in place."""
+class DecodeGraph:
+    """Greedy decode steps (``decode_step``) replayed from two captured HIP
+    graphs over two static state sets: step n reads set n % 2 and its kernels
+    write the next state straight into set (n + 1) % 2 (``out_state``), so no
+    state is copied between steps (the rings alone are 4 x 4 MiB per layer at
+    the C5 batch). ``step()`` advances ``self.ids`` ``[B, 1]`` in place and
+    ``self.states`` to the new set; ``run()`` does the same and returns the
+    step's logits. Every layer of a set shares one ``last_token`` buffer (the
+    stack's layers carry the same last token). Two eager steps on throwaway
+    copies warm the libraries up before the captures."""
 
     def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
                  states: list[dict[str, Tensor]]) -> None:
-        super().__init__(params, settings, states, ids, greedy=True)
+        self.params, self.settings = params, settings
+        self.ids = ids.clone().contiguous()
+        self._sets = []
+        for _ in range(2):
+            copy = [{k: v.clone() for k, v in st.items()} for st in states]
+            for st in copy[1:]:
+                st["last_token"] = copy[0]["last_token"]
+            self._sets.append(copy)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            warm_ids, warm_states = self.ids.clone(), [{k: v.clone() for k, v in st.items()} for st in states]
+            for _ in range(2):
+                _, warm_states = stack_window(params, settings, warm_ids, warm_states)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self._graphs, self._logits = [], []
+        for parity in (0, 1):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._logits.append(self._step(self._sets[parity], self._sets[1 - parity]))
+            self._graphs.append(graph)
+        self._parity = 0
+
+    def _step(self, src: list[dict[str, Tensor]], dst: list[dict[str, Tensor]]) -> Tensor:
+        logits, _ = _stack_decode(self.params, self.settings, self.ids, src, dst)
+        scores = logits[:, -1].clone()
+        scores[:, PAD_TOKEN_ID] = float("-inf")
+        self.ids.copy_(scores.argmax(dim=-1, keepdim=True))
+        return logits
+
+    @property
+    def states(self) -> list[dict[str, Tensor]]:
+        return self._sets[self._parity]
+
+    @property
+    def logits(self) -> Tensor:
+        return self._logits[1 - self._parity]
+
+    def run(self) -> Tensor:
+        self._graphs[self._parity].replay()
+        self._parity ^= 1
+        return self.logits
 
     def step(self) -> Tensor:
         self.run()

@@ -210,6 +210,8 @@ def salient_tail(
     values: Tensor,
     admission_mask: Tensor,
     capacity: int,
+    *,
+    out: tuple[Tensor, Tensor, Tensor] | None = None,
 ) -> tuple[Tensor, Tensor, Tensor]:
     """Ring update of the salient memory (reference model/memory.py:431-455).
 
@@ -221,7 +223,9 @@ def salient_tail(
     valid, the latest invalid ones as filler) in ascending time order, with the
     keys and values of invalid slots zeroed. The reference ranks entries with
     ``torch.topk`` over ``valid ? t : -1``, whose choice among tied invalid
-    entries is unspecified; this front fixes it to the latest ones.
+    entries is unspecified; this front fixes it to the latest ones. ``out``
+    (build-side): contiguous buffers of those shapes that receive the result
+    (a graph's static state), not overlapping the inputs.
     """
 
     tensors = {
@@ -268,9 +272,18 @@ def salient_tail(
 
     device = keys.device
     slots = min(carried + length, capacity)
-    out_keys = torch.empty((batch, slots, width), device=device, dtype=keys.dtype)
-    out_values = torch.empty_like(out_keys)
-    out_valid = torch.empty((batch, slots), device=device, dtype=torch.bool)
+    if out is not None:
+        out_keys, out_values, out_valid = out
+        if (out_keys.shape != (batch, slots, width) or out_values.shape != out_keys.shape
+                or out_valid.shape != (batch, slots) or out_keys.dtype != keys.dtype
+                or out_values.dtype != keys.dtype or out_valid.dtype != torch.bool
+                or not all(t.is_contiguous() for t in out)):
+            raise CudaThinkValidationError("out must be contiguous [batch, slots, width] keys and values and "
+                                           "[batch, slots] bool flags")
+    else:
+        out_keys = torch.empty((batch, slots, width), device=device, dtype=keys.dtype)
+        out_values = torch.empty_like(out_keys)
+        out_valid = torch.empty((batch, slots), device=device, dtype=torch.bool)
     if batch == 0 or slots == 0:
         return out_keys, out_values, out_valid
     contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, admission_mask)]

@@ -173,7 +173,8 @@ def recurrent_scan(
 def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tensor, *, width: int,
                retention_offset: int = 0, candidate_offset: int | None = None,
                with_bf16: bool = False, two_phase: bool = True, retention_bias: Tensor | None = None,
-               candidate_bias: Tensor | None = None, out_bf16: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
+               candidate_bias: Tensor | None = None, out_bf16: Tensor | None = None,
+               out: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
     """Working states of one window from precomputed gate pre-activations.
 
     ``preactivations`` ``[B, L, C]`` fp32 or bf16 (last dimension contiguous) holds
@@ -191,7 +192,9 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     matrix) that receives the bf16 copy. With ``two_phase`` the kernel gets the workspace of
     its two-phase form, which it takes when the batch's columns alone would
     leave the chip short of workgroups (a few long rows); the result is the
-    same to the bit either way.
+    same to the bit either way. ``out``: a contiguous fp32 ``[B, L, width]``
+    tensor that receives the states (a graph's static state), not
+    overlapping the inputs.
     """
 
     if candidate_offset is None:
@@ -219,7 +222,10 @@ def gated_scan(preactivations: Tensor, valid_mask: Tensor | None, initial: Tenso
     except _native.NativeLibraryUnavailableError as error:
         raise DenseCudaUnavailableError(str(error)) from error
     z = preactivations.contiguous()
-    states = torch.empty((batch, length, width), device=z.device, dtype=torch.float32)
+    if out is not None and (out.shape != (batch, length, width) or out.dtype != torch.float32
+                            or not out.is_contiguous() or out.device != z.device):
+        raise DenseCudaValidationError("out must be a contiguous float32 [batch, length, width] tensor")
+    states = out if out is not None else torch.empty((batch, length, width), device=z.device, dtype=torch.float32)
     states16 = None
     if with_bf16:
         states16 = out_bf16 if out_bf16 is not None else torch.empty(states.shape, device=z.device,
