@@ -201,6 +201,17 @@ int koemi_moe_expert_counts(const void* assignments, int assignment_dtype,
  * for the HERM block), which also hands over its pair -> position map:
  * pair_positions[t * top_k + s] = the sorted position of pair (t, s) (valid
  * pairs below segment_offsets[E]). Same workspace as koemi_moe_permute. */
+/* koemi_moe_route_hash followed by koemi_moe_permute_indices in the same
+ * launches, the assignments never stored (a build-side entry for the HERM
+ * block's hash-routed experts): each pair's expert is hashed from its token
+ * and previous token inside the permutation. The same outputs as those two
+ * calls. ids I32 or I64 (id_dtype); the workspace of
+ * koemi_moe_permute_workspace_bytes. */
+int koemi_moe_permute_hash_indices(const void* token_ids, const void* previous_token_ids, int id_dtype,
+                                   const uint8_t* valid_mask, int64_t* sorted_rows, int64_t* sorted_experts,
+                                   int64_t* segment_offsets, int64_t* pair_positions, int64_t tokens, int64_t top_k,
+                                   int64_t expert_count, void* workspace, size_t workspace_bytes,
+                                   koemi_stream_t stream);
 int koemi_moe_permute_indices(const void* assignments, int assignment_dtype, const uint8_t* valid_mask,
                               const float* pair_weights, int64_t* sorted_rows, int64_t* sorted_experts,
                               int64_t* segment_offsets, float* sorted_weights, int64_t* pair_positions,

@@ -24,6 +24,7 @@
 // Every destination is computed, none is claimed by an atomic, so the output
 // does not depend on scheduling.
 #include "common.hpp"
+#include "moe_hash.hpp"
 
 namespace koemi {
 namespace {
@@ -49,34 +50,55 @@ inline PermuteWorkspace permute_workspace(int64_t tokens, int64_t k, int64_t E) 
     return w;
 }
 
+// Where a pair's expert comes from: an assignments array [tokens, k] (ReadSrc)
+// or the content hash of the pair's token and previous token, computed in place
+// (HashSrc: the hash route of experts.py:283-289, so the assignments are never
+// stored). Either way pair p is (token p / k, slot p % k).
+template <typename I>
+struct ReadSrc {
+    const I* a;
+    __device__ int64_t operator()(int64_t p) const { return static_cast<int64_t>(a[p]); }
+};
+template <typename I>
+struct HashSrc {
+    const I* tok;
+    const I* prev;
+    int64_t k, E;
+    __device__ int64_t operator()(int64_t p) const {
+        const int64_t t = p / k;
+        const uint64_t h = content_hash(static_cast<int64_t>(tok[t]), static_cast<int64_t>(prev[t]));
+        return hash_slot_expert(h, p - t * k, E);
+    }
+};
+
 // Pair key (moe_kernels.cu:68-91) of pair g + lane: the expert for a valid token
 // whose slot holds an in-range expert not already used by an earlier slot of the
 // same token, else the sentinel E; -1 for lanes past p1. Earlier slots of a
 // token are read from the lanes that hold them (pairs are token-major), with a
 // memory read only when a token straddles the start of the 64-pair group.
-template <typename I>
-__device__ __forceinline__ int32_t group_key(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+template <typename Src>
+__device__ __forceinline__ int32_t group_key(const Src a, const uint8_t* __restrict__ valid,
                                              int64_t g, int64_t p1, int64_t k, int64_t E) {
     const int lane = lane_id();
     const int64_t p = g + lane;
     const bool active = p < p1;
     const int64_t pc = active ? p : p1 - 1;
-    const int64_t e = static_cast<int64_t>(a[pc]);
+    const int64_t e = a(pc);
     const int64_t t = pc / k;
     const int64_t s = pc - t * k;
     bool ok = active && valid[t] && e >= 0 && e < E;
     for (int64_t r = 1; r < k; ++r) {
         const int64_t above = __shfl_up(e, static_cast<unsigned>(r < kWave ? r : 0), kWave);
         if (r <= s) {
-            const int64_t earlier = (r < kWave && lane >= r) ? above : static_cast<int64_t>(a[pc - r]);
+            const int64_t earlier = (r < kWave && lane >= r) ? above : a(pc - r);
             ok = ok && earlier != e;
         }
     }
     return active ? static_cast<int32_t>(ok ? e : E) : -1;
 }
 
-template <typename I>
-__global__ __launch_bounds__(kWave) void permute_count_kernel(const I* __restrict__ a, const uint8_t* __restrict__ valid,
+template <typename Src>
+__global__ __launch_bounds__(kWave) void permute_count_kernel(const Src a, const uint8_t* __restrict__ valid,
                                                               int32_t* __restrict__ counts, int64_t pairs, int64_t k,
                                                               int64_t E) {
     extern __shared__ int32_t hist[];
@@ -237,9 +259,9 @@ __global__ __launch_bounds__(kScanThreads) void permute_scan_lds_kernel(int32_t*
     for (int i = tid; i < total_ints; i += kScanThreads) counts[i] = table[i];
 }
 
-template <typename I>
+template <typename Src>
 __global__ __launch_bounds__(kWave) void permute_scatter_kernel(
-    const I* __restrict__ a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
+    const Src a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
     const int32_t* __restrict__ bases, int64_t* __restrict__ sorted_rows, int64_t* __restrict__ sorted_experts,
     float* __restrict__ sorted_w, int64_t* __restrict__ dest, int64_t pairs, int64_t k, int64_t E) {
     extern __shared__ int32_t cursor[];
@@ -328,9 +350,9 @@ __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __re
 constexpr int kSmallPairs = 1024;
 constexpr int kSmallKeys = 64;  // E + 1
 
-template <typename I>
+template <typename Src>
 __global__ __launch_bounds__(kSmallPairs) void permute_small_kernel(
-    const I* __restrict__ a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
+    const Src a, const uint8_t* __restrict__ valid, const float* __restrict__ pair_w,
     int64_t* __restrict__ sorted_rows, int64_t* __restrict__ sorted_experts, int64_t* __restrict__ offsets,
     float* __restrict__ sorted_w, int64_t* __restrict__ dest, int64_t pairs, int64_t k, int64_t E) {
     __shared__ int32_t wcount[kSmallPairs / kWave][kSmallKeys];
@@ -388,19 +410,18 @@ __global__ __launch_bounds__(kSmallPairs) void permute_small_kernel(
     }
 }
 
-template <typename I>
-int run_index_phase(const void* assignments, const uint8_t* valid, const float* pair_w, int64_t* sorted_rows,
+template <typename Src>
+int run_index_phase(const Src a, const uint8_t* valid, const float* pair_w, int64_t* sorted_rows,
                     int64_t* sorted_experts, int64_t* offsets, float* sorted_w, int32_t* counts, int64_t* dest,
                     int64_t pairs, int64_t k, int64_t E, hipStream_t s) {
-    const I* a = static_cast<const I*>(assignments);
     if (pairs <= kSmallPairs && E + 1 <= kSmallKeys) {
-        hipLaunchKernelGGL(permute_small_kernel<I>, dim3(1), dim3(kSmallPairs), 0, s, a, valid, pair_w, sorted_rows,
+        hipLaunchKernelGGL(permute_small_kernel<Src>, dim3(1), dim3(kSmallPairs), 0, s, a, valid, pair_w, sorted_rows,
                            sorted_experts, offsets, sorted_w, dest, pairs, k, E);
         return check_launch("koemi_moe_permute(small)");
     }
     const int64_t chunks = num_chunks(pairs);
     const size_t hist_bytes = static_cast<size_t>(E + 1) * sizeof(int32_t);
-    hipLaunchKernelGGL(permute_count_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
+    hipLaunchKernelGGL(permute_count_kernel<Src>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
                        valid, counts, pairs, k, E);
     int st = check_launch("koemi_moe_permute(count)");
     if (st != KOEMI_OK) return st;
@@ -412,7 +433,7 @@ int run_index_phase(const void* assignments, const uint8_t* valid, const float* 
                            s, counts, offsets, chunks, E);
     st = check_launch("koemi_moe_permute(scan)");
     if (st != KOEMI_OK) return st;
-    hipLaunchKernelGGL(permute_scatter_kernel<I>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
+    hipLaunchKernelGGL(permute_scatter_kernel<Src>, dim3(static_cast<unsigned>(chunks)), dim3(kWave), hist_bytes, s, a,
                        valid, pair_w, counts, sorted_rows, sorted_experts, sorted_w, dest, pairs, k, E);
     return check_launch("koemi_moe_permute(scatter)");
 }
@@ -468,9 +489,9 @@ extern "C" int koemi_moe_permute(const void* context, int context_dtype, const v
     hipStream_t s = as_stream(stream);
     const int64_t pairs = tokens * top_k;
     int st = (assignment_dtype == KOEMI_I32)
-                 ? run_index_phase<int32_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                 ? run_index_phase(ReadSrc<int32_t>{static_cast<const int32_t*>(assignments)}, valid_mask, pair_weights, sorted_rows, sorted_experts,
                                             segment_offsets, sorted_weights, counts, dest, pairs, top_k, expert_count, s)
-                 : run_index_phase<int64_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+                 : run_index_phase(ReadSrc<int64_t>{static_cast<const int64_t*>(assignments)}, valid_mask, pair_weights, sorted_rows, sorted_experts,
                                             segment_offsets, sorted_weights, counts, dest, pairs, top_k, expert_count, s);
     if (st != KOEMI_OK) return st;
     if (sorted_context == nullptr) return KOEMI_OK;  // the indices only (the caller reads rows by sorted_rows)
@@ -504,10 +525,42 @@ extern "C" int koemi_moe_permute_indices(const void* assignments, int assignment
     hipStream_t s = as_stream(stream);
     const int64_t pairs = tokens * top_k;
     return (assignment_dtype == KOEMI_I32)
-               ? run_index_phase<int32_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+               ? run_index_phase(ReadSrc<int32_t>{static_cast<const int32_t*>(assignments)}, valid_mask, pair_weights, sorted_rows, sorted_experts,
                                           segment_offsets, sorted_weights, counts, pair_positions, pairs, top_k,
                                           expert_count, s)
-               : run_index_phase<int64_t>(assignments, valid_mask, pair_weights, sorted_rows, sorted_experts,
+               : run_index_phase(ReadSrc<int64_t>{static_cast<const int64_t*>(assignments)}, valid_mask, pair_weights, sorted_rows, sorted_experts,
                                           segment_offsets, sorted_weights, counts, pair_positions, pairs, top_k,
                                           expert_count, s);
+}
+
+extern "C" int koemi_moe_permute_hash_indices(const void* token_ids, const void* previous_token_ids, int id_dtype,
+                                              const uint8_t* valid_mask, int64_t* sorted_rows,
+                                              int64_t* sorted_experts, int64_t* segment_offsets,
+                                              int64_t* pair_positions, int64_t tokens, int64_t top_k,
+                                              int64_t expert_count, void* workspace, size_t workspace_bytes,
+                                              koemi_stream_t stream) {
+    if (tokens < 1) return fail(KOEMI_ERR_INVALID, "permute needs tokens >= 1");
+    if (top_k < 1 || top_k > 256) return fail(KOEMI_ERR_INVALID, "top_k is outside [1, 256]");
+    if (expert_count < 1 || top_k > expert_count) return fail(KOEMI_ERR_INVALID, "top_k must not exceed expert_count");
+    if (expert_count > kMaxExperts) return fail(KOEMI_ERR_UNSUPPORTED, "permute supports at most %d experts", kMaxExperts);
+    if (!index_dtype(id_dtype)) return fail(KOEMI_ERR_UNSUPPORTED, "token ids must be int32 or int64");
+    if (!token_ids || !previous_token_ids || !valid_mask || !sorted_rows || !sorted_experts || !segment_offsets ||
+        !pair_positions)
+        return fail(KOEMI_ERR_INVALID, "permute received a null pointer");
+    const PermuteWorkspace ws = permute_workspace(tokens, top_k, expert_count);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "permute workspace too small: need %zu bytes", ws.total);
+    if (num_chunks(tokens * top_k) > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many pairs");
+    int32_t* counts = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + ws.counts_off);
+    hipStream_t s = as_stream(stream);
+    const int64_t pairs = tokens * top_k;
+    if (id_dtype == KOEMI_I32)
+        return run_index_phase(HashSrc<int32_t>{static_cast<const int32_t*>(token_ids),
+                                                static_cast<const int32_t*>(previous_token_ids), top_k, expert_count},
+                               valid_mask, nullptr, sorted_rows, sorted_experts, segment_offsets, nullptr, counts,
+                               pair_positions, pairs, top_k, expert_count, s);
+    return run_index_phase(HashSrc<int64_t>{static_cast<const int64_t*>(token_ids),
+                                            static_cast<const int64_t*>(previous_token_ids), top_k, expert_count},
+                           valid_mask, nullptr, sorted_rows, sorted_experts, segment_offsets, nullptr, counts,
+                           pair_positions, pairs, top_k, expert_count, s);
 }

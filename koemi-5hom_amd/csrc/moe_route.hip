@@ -8,22 +8,10 @@
 // 16-wide softmax per token: one thread per token, no HBM-heavy traffic.
 #include "common.hpp"
 #include "detmath.hpp"
+#include "moe_hash.hpp"
 
 namespace koemi {
 namespace {
-
-// mix32 of experts.py:30-38. The product tok * 1000003 + prev * 97409 is taken
-// modulo 2^64 (the int64 tensor arithmetic of the reference) and only its low
-// 32 bits are used, so unsigned 64-bit arithmetic gives the same bits.
-__device__ __forceinline__ uint32_t content_hash(int64_t token, int64_t previous) {
-    const uint64_t mixed = static_cast<uint64_t>(token) * 1000003ull + static_cast<uint64_t>(previous) * 97409ull;
-    uint32_t v = static_cast<uint32_t>(mixed);
-    v ^= v >> 16;
-    v *= 0x45D9F3Bu;
-    v ^= v >> 16;
-    v *= 0x45D9F3Bu;
-    return v ^ (v >> 16);
-}
 
 template <typename I>
 __global__ void route_hash_kernel(const I* __restrict__ tok, const I* __restrict__ prev,
@@ -39,8 +27,7 @@ __global__ void route_hash_kernel(const I* __restrict__ tok, const I* __restrict
     const uint64_t h = content_hash(static_cast<int64_t>(tok[t]), static_cast<int64_t>(prev[t]));
     bool dup = false;
     for (int64_t s = 0; s < k; ++s) {
-        // int64 sum of experts.py:288 (no 32-bit wraparound): h < 2^32, s * 0x9E3779B9 < 2^40.
-        const int64_t e = static_cast<int64_t>((h + static_cast<uint64_t>(s) * 0x9E3779B9ull) % static_cast<uint64_t>(E));
+        const int64_t e = hash_slot_expert(h, s, E);
         for (int64_t r = 0; r < s; ++r) dup |= (row[r] == e);
         row[s] = e;
     }

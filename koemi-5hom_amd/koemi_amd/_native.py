@@ -173,6 +173,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         (_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_float, _P,
          c_size_t, _P),
     ),
+    "koemi_moe_permute_hash_indices": (
+        c_int,
+        (_P, _P, c_int, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
     "koemi_moe_permute_indices": (
         c_int,
         (_P, c_int, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, c_size_t, _P),

@@ -493,22 +493,27 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     k = settings.top_k
     flat = fused.reshape(-1, d)
     flat_valid = valid.reshape(-1)
+    moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
+    # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
+    # permutation's indices (no sorted copy of the context); hash routing is
+    # then done inside the permutation (no assignments tensor)
+    indexed = moe_in.dtype == torch.bfloat16 and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
+    hashed = indexed and settings.expert_routing != "learned"
     if settings.expert_routing == "learned":
         # LearnedExpertMixture (router.py:43-97): the bias-free gate on the fp32
         # context (rows of invalid tokens are routed to -1 whatever their
         # logits), softmax top-k, each pair weighted by its probability
         router_logits = functional.linear(flat, p["router_w"])
         assignments, weights = moe.route_topk_learned(router_logits, flat_valid, top_k=k)
-    else:
+    elif not hashed:
         assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
                                            validate=False)
         weights = None
-    moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
-    # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
-    # permutation's indices (no sorted copy of the context)
-    indexed = moe_in.dtype == torch.bfloat16 and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
     pair_positions = None
-    if indexed:
+    if hashed:
+        sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = moe.permute_hash_indices(
+            ids, previous, flat_valid, expert_count=settings.expert_count, top_k=k)
+    elif indexed:
         sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = moe.permute_indices(
             assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count, pair_weights=weights)
     else:

@@ -522,6 +522,39 @@ def permute_indices(assignments: Tensor, valid_mask: Tensor, *, expert_count: in
     return sorted_rows, sorted_experts, segment_offsets, sorted_weights, pair_positions
 
 
+def permute_hash_indices(token_ids: Tensor, previous_token_ids: Tensor, valid_mask: Tensor, *, expert_count: int,
+                         top_k: int) -> tuple[Tensor, Tensor, Tensor, None, Tensor]:
+    """``route_topk_valid`` then ``permute_indices`` in the same launches
+    (``koemi_moe_permute_hash_indices``, build-side): each pair's expert is
+    hashed from its token and previous token inside the permutation, the
+    assignments never stored. Returns what ``permute_indices`` returns (no
+    weights: the hash route has none)."""
+
+    ids = token_ids.reshape(-1)
+    prev = previous_token_ids.reshape(-1)
+    tokens = ids.shape[0]
+    if ids.dtype not in (torch.int32, torch.int64) or prev.dtype != ids.dtype or prev.shape != ids.shape:
+        raise CudaMoeValidationError("token ids must be int32 or int64 tensors of one shape")
+    if valid_mask.reshape(-1).shape != (tokens,) or top_k > expert_count or expert_count > _MAX_PERMUTE_EXPERTS:
+        raise CudaMoeValidationError("valid_mask must be [token_count] and top_k <= expert_count <= the permute limit")
+    _require_library()
+    device = ids.device
+    pairs = tokens * top_k
+    sorted_rows = torch.empty((pairs,), device=device, dtype=torch.int64)
+    sorted_experts = torch.empty((pairs,), device=device, dtype=torch.int64)
+    segment_offsets = torch.empty((expert_count + 1,), device=device, dtype=torch.int64)
+    pair_positions = torch.empty((pairs,), device=device, dtype=torch.int64)
+    need = _native.query("koemi_moe_permute_workspace_bytes", tokens, top_k, expert_count)
+    workspace = torch.empty((need,), device=device, dtype=torch.uint8)
+    with torch.cuda.device(device):
+        _native.call("koemi_moe_permute_hash_indices", ids.contiguous().data_ptr(), prev.contiguous().data_ptr(),
+                     _native.dtype_code(ids.dtype), valid_mask.reshape(-1).contiguous().data_ptr(),
+                     sorted_rows.data_ptr(), sorted_experts.data_ptr(), segment_offsets.data_ptr(),
+                     pair_positions.data_ptr(), tokens, top_k, expert_count, workspace.data_ptr(), need,
+                     _native.stream_of(device))
+    return sorted_rows, sorted_experts, segment_offsets, None, pair_positions
+
+
 def grouped_expert_mlp_indexed(
     context: Tensor,
     sorted_rows: Tensor,

@@ -326,6 +326,25 @@ def test_indexed_grouped_mlp_equals_the_gathered_one(device, tokens, E, D, H, se
     assert torch.equal(got[:n], want[:n])
 
 
+@pytest.mark.parametrize("tokens, k, E, id_dtype", [(32768, 2, 16, torch.int64), (64, 2, 16, torch.int64),
+                                                     (5000, 3, 13, torch.int32), (1, 2, 4, torch.int64)])
+def test_hash_routed_permutation_equals_route_then_permute(device, tokens, k, E, id_dtype):
+    """permute_hash_indices (the hash route computed inside the permutation)
+    gives the bits of route_topk_valid followed by permute_indices: rows,
+    experts, offsets and pair positions, small (one-workgroup) and chunked."""
+    g = torch.Generator(device=device).manual_seed(tokens + k)
+    ids = torch.randint(-5, 300, (tokens,), generator=g, device=device).to(id_dtype)
+    prev = torch.randint(0, 256, (tokens,), generator=g, device=device).to(id_dtype)
+    valid = torch.rand((tokens,), generator=g, device=device) < 0.9
+    a = moe.route_topk_valid(ids, prev, valid, expert_count=E, top_k=k, validate=False)
+    want = moe.permute_indices(a, valid, expert_count=E)
+    got = moe.permute_hash_indices(ids, prev, valid, expert_count=E, top_k=k)
+    torch.cuda.synchronize()
+    for name, w, x in zip(("rows", "experts", "offsets"), want[:3], got[:3]):
+        assert torch.equal(w, x), name
+    assert torch.equal(want[4], got[4]), "pair positions"
+
+
 @pytest.mark.parametrize("tokens, k, E, learned", [(64, 2, 16, False), (300, 3, 13, True), (1, 2, 4, False)])
 def test_small_combine_bit_exact(device, tokens, k, E, learned):
     """A decode-sized combine (the one-workgroup inversion) against the oracle's
