@@ -289,9 +289,21 @@ int koemi_salient_tail(const void* carried_keys, const void* carried_values, con
  * capacity, width] keys and values, [batch * length / window, capacity]
  * flags; row b * (length / window) + r), the ring after the whole sequence
  * to final_* ([batch, capacity, ...]). Requires carried >= capacity (a static
- * ring, state.py:43-76) and length % window == 0. */
+ * ring, state.py:43-76) and length % window == 0.
+ * The sequence's keys and values are rows key_row_stride elements apart
+ * (0: width) of key_dtype: dtype itself, or KOEMI_BF16 into fp32 rings (the
+ * bf16 columns of the block's key/value projection read in place, widened
+ * exactly). key_valid (optional, [batch, length]): a position whose byte is
+ * 0 enters the ring with zero key and value, which is the reference's masking
+ * of the projected keys and values by the validity mask (network.py:337-340)
+ * done on the way (reads need no such masking: only valid entries are ever
+ * eligible). out_keys, out_values and out_valid all NULL: only the final
+ * ring is built (LocalKeyValueMemory.tail or salient_tail of one window), of
+ * min(carried + length, capacity) slots, any carried >= 0. Entries of
+ * another dtype, stride or with key_valid require fp32 rings. */
 int koemi_window_rings(const void* carried_keys, const void* carried_values, const uint8_t* carried_valid,
-                       const void* keys, const void* values, const uint8_t* flags, void* out_keys, void* out_values,
+                       const void* keys, const void* values, int key_dtype, int64_t key_row_stride,
+                       const uint8_t* key_valid, const uint8_t* flags, void* out_keys, void* out_values,
                        uint8_t* out_valid, void* final_keys, void* final_values, uint8_t* final_valid, int64_t batch,
                        int64_t carried, int64_t length, int64_t window, int64_t width, int64_t capacity, int tail,
                        int dtype, koemi_stream_t stream);
@@ -491,20 +503,13 @@ int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype,
  * or carried_last[b] (network.py:742-761); int64 ids, valid bytes. With
  * `valid` NULL the validity is ids != pad_id (network.py:303) and is written
  * to `valid_out`; `targets_out` (NULL: none) receives ids where valid and 0
- * elsewhere (the surprise targets, network.py:335).
- * koemi_herm_local_tail: the local ring after a window, the last `window`
- * entries of [carried (window entries) ; new (length entries)] with their
- * valid bytes (memory.py:385-403); fp32 keys and values [batch, *, width]. */
+ * elsewhere (the surprise targets, network.py:335). */
 int koemi_herm_rmsnorm(const void* input, int input_dtype, const void* residual, int residual_dtype,
                        const float* weight, const uint8_t* mask, float* output, void* output_bf16, int64_t rows,
                        int64_t width, float eps, koemi_stream_t stream);
 int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
                              int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out, int64_t pad_id,
                              int64_t batch, int64_t length, koemi_stream_t stream);
-int koemi_herm_local_tail(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
-                          const float* keys, const float* values, const uint8_t* valid, float* out_keys,
-                          float* out_values, uint8_t* out_valid, int64_t batch, int64_t window, int64_t length,
-                          int64_t width, koemi_stream_t stream);
 
 /* causal_surprise of a HERM window from the state before each position
  * (network.py:318-325, 677-698) with the fixed-threshold admission
@@ -523,14 +528,6 @@ int koemi_herm_surprise_shifted(const float* logits, const float* first, const f
  * (network.py:401-405, a torch.cat in the reference) as one bf16 matrix
  * [rows, pieces * width] for its GEMM: `pieces` (1..4) fp32 [rows, width]
  * blocks (16-byte aligned), width % 4 == 0, rounded to nearest even. */
-/* The local keys and values of a window (network.py:337-340: the first two
- * width-column blocks of the stacked working-state projection, rows of
- * invalid positions zeroed, a torch.where each in the reference) as two
- * contiguous fp32 [rows, width] blocks in one kernel; the source in
- * source_dtype (KOEMI_F32 or KOEMI_BF16); width and row_stride multiples of
- * 4, 16-byte aligned pointers. */
-int koemi_herm_masked_pair(const void* source, int source_dtype, int64_t row_stride, const uint8_t* valid, float* out0,
-                           float* out1, int64_t rows, int64_t width, koemi_stream_t stream);
 int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2, const float* input3,
                            int pieces, int64_t rows, int64_t width, void* output, koemi_stream_t stream);
 
@@ -556,11 +553,16 @@ int koemi_local_read(const void* carried_keys, const void* carried_values, const
  * candidate slots per 32 queries (salient: carried + length - 1 <= 152;
  * local: carried <= 64 and window <= 33); other shapes return
  * KOEMI_ERR_UNSUPPORTED (take koemi_salient_read / koemi_local_read). No
- * workspace. */
+ * workspace. The window's keys and values are rows key_row_stride elements
+ * apart (0: width, else a multiple of 4) of key_dtype KOEMI_F32 or
+ * KOEMI_BF16 (the bf16 columns of the block's key/value projection read in
+ * place, widened exactly; 8-byte aligned). Every slot a query can see is
+ * flagged valid, so masking the window's invalid entries changes nothing. */
 int koemi_memory_read_into(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
-                           const float* keys, const float* values, const uint8_t* flags, const float* queries,
-                           void* out, int out_dtype, int64_t out_row_stride, int64_t batch, int64_t carried,
-                           int64_t length, int64_t width, int64_t window, koemi_stream_t stream);
+                           const void* keys, const void* values, int key_dtype, int64_t key_row_stride,
+                           const uint8_t* flags, const float* queries, void* out, int out_dtype,
+                           int64_t out_row_stride, int64_t batch, int64_t carried, int64_t length, int64_t width,
+                           int64_t window, koemi_stream_t stream);
 
 /* Replaces `combine_topk(y, rows, offsets, T, k)` of moe/moe_kernels.cu:560-582
  * without atomics: combined[t] = sum over the valid sorted pairs i of token t,

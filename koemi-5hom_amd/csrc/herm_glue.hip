@@ -10,8 +10,6 @@
 //   koemi_herm_token_context: the previous valid token of each position and
 //     the last valid token of each row (network.py:742-761). One workgroup per
 //     row, a max-scan of the valid positions.
-//   koemi_herm_local_tail: the local ring after a window, the last `window`
-//     entries of [carried ; new] with their valid bytes (memory.py:385-403).
 //   koemi_herm_concat_bf16: the fusion layer's input [working ; memory ;
 //     local ; salient] (network.py:401-405) as one bf16 matrix for its GEMM,
 //     the concatenation and the cast in one pass.
@@ -123,56 +121,6 @@ __global__ __launch_bounds__(256) void herm_token_context_kernel(const int64_t* 
     if (tid == 0) last[b] = carry >= 0 ? ids[b * L + carry] : carried[b];
 }
 
-__global__ void herm_local_tail_kernel(const float* __restrict__ ck, const float* __restrict__ cv,
-                                       const uint8_t* __restrict__ cvalid, const float* __restrict__ k,
-                                       const float* __restrict__ v, const uint8_t* __restrict__ valid,
-                                       float* __restrict__ ok, float* __restrict__ ov, uint8_t* __restrict__ ovalid,
-                                       int64_t W, int64_t L, int64_t D) {
-    // block (b, slot): output slot s holds entry W + L - (W - s) of [carried (W) ; new (L)]
-    const int64_t b = blockIdx.x, s = blockIdx.y;
-    const int64_t i = L + s;  // index into the concatenation
-    const bool carried_entry = i < W;
-    const float* ks = carried_entry ? ck + (b * W + i) * D : k + (b * L + (i - W)) * D;
-    const float* vs = carried_entry ? cv + (b * W + i) * D : v + (b * L + (i - W)) * D;
-    float* kd = ok + (b * W + s) * D;
-    float* vd = ov + (b * W + s) * D;
-    if (D % 4 == 0 && reinterpret_cast<uintptr_t>(ks) % 16 == 0 && reinterpret_cast<uintptr_t>(vs) % 16 == 0 &&
-        reinterpret_cast<uintptr_t>(kd) % 16 == 0 && reinterpret_cast<uintptr_t>(vd) % 16 == 0) {
-        for (int64_t d = threadIdx.x * 4; d < D; d += blockDim.x * 4) {  // 16-byte copies
-            const float4 kq = *reinterpret_cast<const float4*>(ks + d);
-            const float4 vq = *reinterpret_cast<const float4*>(vs + d);
-            *reinterpret_cast<float4*>(kd + d) = kq;
-            *reinterpret_cast<float4*>(vd + d) = vq;
-        }
-    } else {
-        for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-            kd[d] = ks[d];
-            vd[d] = vs[d];
-        }
-    }
-    if (threadIdx.x == 0) ovalid[b * W + s] = carried_entry ? cvalid[b * W + i] : valid[b * L + (i - W)];
-}
-
-// out0 = the first `width` columns of each row, out1 the next `width`, rows
-// whose valid byte is 0 zeroed (the local keys and values of network.py:
-// 337-340 cut from the stacked projection); four columns per thread.
-template <typename S>
-__global__ __launch_bounds__(256) void herm_masked_pair_kernel(const S* __restrict__ src, int64_t stride,
-                                                               const uint8_t* __restrict__ valid,
-                                                               float* __restrict__ out0, float* __restrict__ out1,
-                                                               int64_t rows, int64_t width) {
-    const int64_t quads = width / 4;
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= rows * 2 * quads) return;
-    const int64_t row = i / (2 * quads);
-    const int64_t rest = i - row * 2 * quads;
-    const int which = rest >= quads ? 1 : 0;
-    const int64_t c = (rest - which * quads) * 4;
-    float4 v = load4(src + row * stride + which * width + c);
-    if (valid[row] == 0) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    *reinterpret_cast<float4*>((which ? out1 : out0) + row * width + c) = v;
-}
-
 // [rows, pieces * width] bf16 from `pieces` fp32 [rows, width] blocks; a thread
 // converts four consecutive values (16-byte load, 8-byte store).
 struct ConcatPieces {
@@ -252,24 +200,6 @@ extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t*
     return check_launch("koemi_herm_token_context");
 }
 
-extern "C" int koemi_herm_local_tail(const float* carried_keys, const float* carried_values,
-                                     const uint8_t* carried_valid, const float* keys, const float* values,
-                                     const uint8_t* valid, float* out_keys, float* out_values, uint8_t* out_valid,
-                                     int64_t batch, int64_t window, int64_t length, int64_t width,
-                                     koemi_stream_t stream) {
-    if (batch < 0 || window < 1 || length < 0 || width < 1)
-        return fail(KOEMI_ERR_INVALID, "local tail needs batch, length >= 0 and positive window and width");
-    if (window > 65535 || batch > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "local tail grid too large");
-    if (batch == 0) return KOEMI_OK;
-    if (!carried_keys || !carried_values || !carried_valid || (length > 0 && (!keys || !values || !valid)) ||
-        !out_keys || !out_values || !out_valid)
-        return fail(KOEMI_ERR_INVALID, "local tail received a null pointer");
-    hipLaunchKernelGGL(herm_local_tail_kernel, dim3(static_cast<unsigned>(batch), static_cast<unsigned>(window)),
-                       dim3(256), 0, as_stream(stream), carried_keys, carried_values, carried_valid, keys, values,
-                       valid, out_keys, out_values, out_valid, window, length, width);
-    return check_launch("koemi_herm_local_tail");
-}
-
 extern "C" int koemi_herm_concat_bf16(const float* input0, const float* input1, const float* input2,
                                       const float* input3, int pieces, int64_t rows, int64_t width, void* output,
                                       koemi_stream_t stream) {
@@ -289,29 +219,4 @@ extern "C" int koemi_herm_concat_bf16(const float* input0, const float* input1, 
     hipLaunchKernelGGL(herm_concat_bf16_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
                        as_stream(stream), p, pieces, rows, width, static_cast<bf16*>(output));
     return check_launch("koemi_herm_concat_bf16");
-}
-
-extern "C" int koemi_herm_masked_pair(const void* source, int source_dtype, int64_t row_stride, const uint8_t* valid,
-                                      float* out0, float* out1, int64_t rows, int64_t width, koemi_stream_t stream) {
-    if (source_dtype != KOEMI_F32 && source_dtype != KOEMI_BF16)
-        return fail(KOEMI_ERR_UNSUPPORTED, "masked pair source dtype %s", dtype_name(source_dtype));
-    if (rows < 0 || width < 1 || row_stride < 2 * width)
-        return fail(KOEMI_ERR_INVALID, "masked pair needs rows >= 0, a positive width and row_stride >= 2 width");
-    if (width % 4 != 0 || row_stride % 4 != 0)
-        return fail(KOEMI_ERR_UNSUPPORTED, "masked pair needs width and row_stride multiples of 4");
-    if (rows == 0) return KOEMI_OK;
-    if (!source || !valid || !out0 || !out1 || reinterpret_cast<uintptr_t>(source) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(out0) % 16 != 0 || reinterpret_cast<uintptr_t>(out1) % 16 != 0)
-        return fail(KOEMI_ERR_INVALID, "masked pair received a null or unaligned pointer");
-    const int64_t threads = rows * 2 * (width / 4);
-    if ((threads + 255) / 256 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "masked pair grid too large");
-    if (source_dtype == KOEMI_BF16)
-        hipLaunchKernelGGL(herm_masked_pair_kernel<bf16>, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                           dim3(256), 0, as_stream(stream), static_cast<const bf16*>(source), row_stride, valid, out0,
-                           out1, rows, width);
-    else
-        hipLaunchKernelGGL(herm_masked_pair_kernel<float>, dim3(static_cast<unsigned>((threads + 255) / 256)),
-                           dim3(256), 0, as_stream(stream), static_cast<const float*>(source), row_stride, valid, out0,
-                           out1, rows, width);
-    return check_launch("koemi_herm_masked_pair");
 }

@@ -36,6 +36,7 @@
 
 #include <cmath>
 #include <mutex>
+#include <type_traits>
 
 namespace koemi {
 
@@ -607,17 +608,19 @@ __device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
 }
 
 // out rows are `ostride` elements apart (the reads can land in a column
-// block of a wider matrix, e.g. the fusion input in bf16).
-template <bool LOCAL, int MAXS, typename OutT>
+// block of a wider matrix, e.g. the fusion input in bf16). The window's keys
+// and values are rows `kstride` elements apart of type KT (fp32, or the bf16
+// columns of the block's projection read in place, widened exactly).
+template <bool LOCAL, int MAXS, typename OutT, typename KT>
 __global__ __launch_bounds__(256) void window_read_kernel(
     const float* __restrict__ ck, const float* __restrict__ cv, const uint8_t* __restrict__ cvalid,
-    const float* __restrict__ k, const float* __restrict__ v, const uint8_t* __restrict__ flags,
+    const KT* __restrict__ k, const KT* __restrict__ v, int64_t kstride, const uint8_t* __restrict__ flags,
     const float* __restrict__ q, OutT* __restrict__ out, int64_t ostride, int S, int L, int64_t D, int window,
     float scale) {
     constexpr int NST = (MAXS + 31) / 32;  // slot tiles
     constexpr int NJ = (MAXS + kWave - 1) / kWave;
     __shared__ int list[MAXS];
-    __shared__ int wave_cnt[4];
+    __shared__ int wave_cnt[4], wave_carried[4];
     __shared__ float sc[4][kWinQ][MAXS + 1];
     const int64_t row = blockIdx.x;
     const int t0 = static_cast<int>(blockIdx.y) * kWinQ;
@@ -632,11 +635,17 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     if (c < c_hi) f = (c < S ? cvalid[row * S + c] : flags[row * L + (c - S)]) != 0;
     const uint64_t bal = __ballot(f);
     const int before = __popcll(bal & ((1ull << lane) - 1ull));
-    if (lane == 0) wave_cnt[wave] = __popcll(bal);
+    const uint64_t bal_carried = __ballot(f && c < S);
+    if (lane == 0) {
+        wave_cnt[wave] = __popcll(bal);
+        wave_carried[wave] = __popcll(bal_carried);
+    }
     __syncthreads();
     int base = 0;
     for (int w = 0; w < wave; ++w) base += wave_cnt[w];
     const int n = wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    // the list is ascending: its first nc slots are carried ones
+    const int nc = wave_carried[0] + wave_carried[1] + wave_carried[2] + wave_carried[3];
     if (f) list[base + before] = c;
     __syncthreads();
     OutT* orow0 = out + (row * L + t0) * ostride;
@@ -649,10 +658,13 @@ __global__ __launch_bounds__(256) void window_read_kernel(
         return;
     }
     const int nst = (n + 31) / 32;
-    auto slot_row = [&](int s, const float* carried, const float* window_rows) -> const float* {
-        return s < S ? carried + (row * S + s) * D : window_rows + (row * L + (s - S)) * D;
-    };
-
+    // Rows of listed slots: carried rows (fp32, D apart) or window rows (KT,
+    // kstride apart). Loads of a group of listed slots [i_lo, i_hi] take one
+    // path when the group is all carried or all window (uniform: nc splits
+    // the list), a per-lane choice only in the group that straddles nc.
+    auto carried_row = [&](const float* base_rows, int s) { return base_rows + (row * S + s) * D; };
+    auto window_row = [&](const KT* base_rows, int s) { return base_rows + (row * L + (s - S)) * kstride; };
+    auto group_kind = [&](int i_lo, int i_hi) { return i_lo >= nc ? 1 : (min(i_hi, n - 1) < nc ? 0 : 2); };
     // scores
     {
         const float* qrow = q + (row * L + t0 + min(r, nq - 1)) * D;
@@ -674,16 +686,24 @@ __global__ __launch_bounds__(256) void window_read_kernel(
 #pragma unroll
             for (int st = 0; st < NST; ++st) {
                 if (st >= nst) break;
-                const float* krow = slot_row(list[min(st * 32 + r, n - 1)], ck, k);
+                const int ks = list[min(st * 32 + r, n - 1)];
                 float4 kb[2][4];
+                auto fetch_keys = [&](const auto* krow) {
 #pragma unroll
-                for (int blk = 0; blk < 2; ++blk)
+                    for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
-                        kb[blk][i] = col < D ? *reinterpret_cast<const float4*>(krow + col)
-                                             : make_float4(0.f, 0.f, 0.f, 0.f);
-                    }
+                        for (int i = 0; i < 4; ++i) {
+                            const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
+                            kb[blk][i] = col < D ? load4(krow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                        }
+                };
+                if constexpr (std::is_same<KT, float>::value) {
+                    fetch_keys(ks < S ? carried_row(ck, ks) : window_row(k, ks));
+                } else {
+                    const int kind = group_kind(st * 32, st * 32 + 31);
+                    if (kind == 0 || (kind == 2 && ks < S)) fetch_keys(carried_row(ck, ks));
+                    else fetch_keys(window_row(k, ks));
+                }
 #pragma unroll
                 for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
@@ -765,11 +785,23 @@ __global__ __launch_bounds__(256) void window_read_kernel(
             for (int e = 0; e < 16; ++e) o[cc][e] = 0.0f;
         float4 bn[8];
         auto fetch = [&](int i0) {
+            auto fetch_with = [&](auto load_slot) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int li = i0 + 2 * u + h;
-                bn[u] = li < n ? *reinterpret_cast<const float4*>(slot_row(list[li], cv, v) + colc)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int u = 0; u < 8; ++u) {
+                    const int li = i0 + 2 * u + h;
+                    bn[u] = li < n ? load_slot(list[li]) : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            };
+            if constexpr (std::is_same<KT, float>::value) {
+                fetch_with([&](int sl) { return load4((sl < S ? carried_row(cv, sl) : window_row(v, sl)) + colc); });
+            } else {
+                const int kind = group_kind(i0, i0 + 15);
+                if (kind == 0) fetch_with([&](int sl) { return load4(carried_row(cv, sl) + colc); });
+                else if (kind == 1) fetch_with([&](int sl) { return load4(window_row(v, sl) + colc); });
+                else
+                    fetch_with([&](int sl) {
+                        return sl < S ? load4(carried_row(cv, sl) + colc) : load4(window_row(v, sl) + colc);
+                    });
             }
         };
         fetch(0);
@@ -807,19 +839,21 @@ inline bool window_read_fits(int64_t carried, int64_t length, int64_t window) {
     return carried <= kWinMaxSlots && carried + length - 1 <= kWinMaxSlots;
 }
 
-template <typename OutT>
-int launch_window_read(const float* ck, const float* cv, const uint8_t* cvalid, const float* k, const float* v,
+template <typename OutT, typename KT = float>
+int launch_window_read(const float* ck, const float* cv, const uint8_t* cvalid, const KT* k, const KT* v,
                        const uint8_t* flags, const float* q, OutT* out, int64_t ostride, int64_t batch,
-                       int64_t carried, int64_t length, int64_t width, int64_t window, hipStream_t stream) {
+                       int64_t carried, int64_t length, int64_t width, int64_t window, hipStream_t stream,
+                       int64_t kstride = 0) {
     const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
     const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((length + kWinQ - 1) / kWinQ));
+    if (kstride == 0) kstride = width;
     auto launch = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, ck, cv, cvalid, k, v, flags, q, out, ostride,
+        hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, ck, cv, cvalid, k, v, kstride, flags, q, out, ostride,
                            static_cast<int>(carried), static_cast<int>(length), width, static_cast<int>(window),
                            inv_sqrt_d);
     };
-    if (window > 0) launch(window_read_kernel<true, kWinLocalSlots, OutT>);
-    else launch(window_read_kernel<false, kWinMaxSlots, OutT>);
+    if (window > 0) launch(window_read_kernel<true, kWinLocalSlots, OutT, KT>);
+    else launch(window_read_kernel<false, kWinMaxSlots, OutT, KT>);
     return check_launch(window > 0 ? "koemi_local_read" : "koemi_salient_read");
 }
 
@@ -1050,32 +1084,43 @@ extern "C" int koemi_local_read(const void* carried_keys, const void* carried_va
 }
 
 extern "C" int koemi_memory_read_into(const float* carried_keys, const float* carried_values,
-                                      const uint8_t* carried_valid, const float* keys, const float* values,
-                                      const uint8_t* flags, const float* queries, void* out, int out_dtype,
-                                      int64_t out_row_stride, int64_t batch, int64_t carried, int64_t length,
-                                      int64_t width, int64_t window, koemi_stream_t stream) {
+                                      const uint8_t* carried_valid, const void* keys, const void* values,
+                                      int key_dtype, int64_t key_row_stride, const uint8_t* flags,
+                                      const float* queries, void* out, int out_dtype, int64_t out_row_stride,
+                                      int64_t batch, int64_t carried, int64_t length, int64_t width, int64_t window,
+                                      koemi_stream_t stream) {
     if (batch < 0 || carried < 0 || length < 0 || width < 1 || window < 0)
         return fail(KOEMI_ERR_INVALID, "memory read needs non-negative batch, carried, length and window, positive width");
     if (out_dtype != KOEMI_F32 && out_dtype != KOEMI_BF16)
         return fail(KOEMI_ERR_UNSUPPORTED, "memory read output must be float32 or bfloat16");
     if (out_row_stride < width || out_row_stride % 4 != 0)
         return fail(KOEMI_ERR_INVALID, "memory read output row stride must be a multiple of 4, at least the width");
+    if (key_dtype != KOEMI_F32 && key_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "memory read keys and values must be float32 or bfloat16");
+    if (key_row_stride == 0) key_row_stride = width;
+    if (key_row_stride < width || key_row_stride % 4 != 0)
+        return fail(KOEMI_ERR_INVALID, "memory read key row stride must be a multiple of 4, at least the width");
     if (batch == 0 || length == 0) return KOEMI_OK;
     auto aligned16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     if (width % 4 != 0 || !window_read_fits(carried, length, window) || batch > 0x7fffffffLL ||
         (length + kWinQ - 1) / kWinQ > 65535 || !aligned16(carried_keys) || !aligned16(carried_values) ||
-        !aligned16(keys) || !aligned16(values) || !aligned16(queries) || reinterpret_cast<uintptr_t>(out) % 8 != 0)
+        reinterpret_cast<uintptr_t>(keys) % (key_dtype == KOEMI_F32 ? 16 : 8) != 0 ||
+        reinterpret_cast<uintptr_t>(values) % (key_dtype == KOEMI_F32 ? 16 : 8) != 0 || !aligned16(queries) ||
+        reinterpret_cast<uintptr_t>(out) % 8 != 0)
         return fail(KOEMI_ERR_UNSUPPORTED, "memory read into a strided output: shape outside the fused read");
     if (!keys || !values || !flags || !queries || !out || (carried > 0 && (!carried_keys || !carried_values ||
                                                                           !carried_valid)))
         return fail(KOEMI_ERR_INVALID, "memory read received a null pointer");
-    if (out_dtype == KOEMI_BF16)
-        return launch_window_read(carried_keys, carried_values, carried_valid, keys, values, flags, queries,
-                                  static_cast<bf16*>(out), out_row_stride, batch, carried, length, width, window,
-                                  as_stream(stream));
-    return launch_window_read(carried_keys, carried_values, carried_valid, keys, values, flags, queries,
-                              static_cast<float*>(out), out_row_stride, batch, carried, length, width, window,
-                              as_stream(stream));
+    auto run = [&](auto out_tag, auto key_tag) {
+        using OutT = decltype(out_tag);
+        using KT = decltype(key_tag);
+        return launch_window_read(carried_keys, carried_values, carried_valid, static_cast<const KT*>(keys),
+                                  static_cast<const KT*>(values), flags, queries, static_cast<OutT*>(out),
+                                  out_row_stride, batch, carried, length, width, window, as_stream(stream),
+                                  key_row_stride);
+    };
+    if (out_dtype == KOEMI_BF16) return key_dtype == KOEMI_BF16 ? run(bf16{}, bf16{}) : run(bf16{}, float{});
+    return key_dtype == KOEMI_BF16 ? run(float{}, bf16{}) : run(float{}, float{});
 }
 
 extern "C" int koemi_read_step_pair(const float* local_keys, const float* local_values, const uint8_t* local_valid,

@@ -85,8 +85,8 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     ),
     "koemi_window_rings": (
         c_int,
-        (_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int,
-         c_int, _P),
+        (_P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
+         c_int64, c_int64, c_int, c_int, _P),
     ),
     "koemi_recurrent_gates_workspace_bytes": (c_size_t, (c_int64, c_int64)),
     "koemi_recurrent_gates": (
@@ -131,7 +131,8 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     ),
     "koemi_memory_read_into": (
         c_int,
-        (_P, _P, _P, _P, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P),
+        (_P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+         _P),
     ),
     "koemi_herm_surprise_shifted": (
         c_int, (_P, _P, _P, _P, _P, _P, _P, c_float, c_int64, c_int64, c_int64, c_float, _P),
@@ -142,9 +143,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P),
     ),
-    "koemi_herm_masked_pair": (c_int, (_P, c_int, c_int64, _P, _P, _P, c_int64, c_int64, _P)),
     "koemi_herm_token_context": (c_int, (_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
-    "koemi_herm_local_tail": (c_int, (_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P)),
     "koemi_local_read": (
         c_int,
         (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, c_int, _P, c_size_t, _P),

@@ -17,8 +17,11 @@ this package's HIP kernels:
   head (network.py:677-698);
 * admission: ``think.salience_admission`` with the fixed threshold (network.py:349);
 * local read: ``memory.read_local_window`` (memory.py:332-383);
-* salient read and ring update: ``memory.read_salient_window``,
-  ``memory.salient_tail`` (memory.py:405-455);
+* salient read: ``memory.read_salient_window`` (memory.py:405-429);
+* ring updates: ``window_rings`` (LocalKeyValueMemory.tail and salient_tail,
+  memory.py:385-403, 431-455); the reads and the rings take the local keys
+  and values in place from the projection, the rings zeroing the entries
+  of invalid positions (network.py:337-340) on the way;
 * experts: ``moe.route_topk_valid`` (hash) or the gate GEMM then
   ``moe.route_topk_learned`` (learned), ``moe.permute_topk``,
   ``moe.grouped_expert_mlp_inference``, ``moe.combine_topk`` (with the pair
@@ -375,28 +378,6 @@ def _token_context(ids: Tensor, valid: Tensor | None, carried: Tensor, last_out:
     return (previous, last, valid_out, targets) if formed else (previous, last)
 
 
-def _local_tail(state: dict[str, Tensor], keys: Tensor, values: Tensor, valid: Tensor,
-                window: int, out: dict[str, Tensor] | None = None) -> tuple[Tensor, Tensor, Tensor]:
-    """LocalKeyValueMemory.tail (memory.py:385-403) of a static ring of
-    ``window`` entries on ``koemi_herm_local_tail``; with ``out`` (a state
-    dict) into its ring buffers."""
-
-    batch, length, width = keys.shape
-    if state["local_keys"].shape[1] != window:
-        raise ValueError("the local ring must hold exactly `window` entries (static state)")
-    if out is not None:
-        out_k, out_v, out_ok = out["local_keys"], out["local_values"], out["local_valid"]
-    else:
-        out_k = torch.empty_like(state["local_keys"])
-        out_v = torch.empty_like(state["local_values"])
-        out_ok = torch.empty_like(state["local_valid"])
-    _native.call("koemi_herm_local_tail", _native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
-                 _native.ptr(state["local_valid"]), _native.ptr(keys), _native.ptr(values), _native.ptr(valid),
-                 _native.ptr(out_k), _native.ptr(out_v), _native.ptr(out_ok), batch, window, length, width,
-                 _native.stream_of(keys.device))
-    return out_k, out_v, out_ok
-
-
 def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor, normalizer: Tensor,
                           *, width: int, features: int, out: Tensor | None = None,
                           next_out: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor, Tensor]:
@@ -587,12 +568,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
     projected = _projection(ws_low, p, "ws")
-    # local keys and values: the first two column blocks, invalid rows zeroed (one kernel)
-    local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
-    local_values = torch.empty_like(local_keys)
-    _native.call("koemi_herm_masked_pair", _native.ptr(projected), _native.dtype_code(projected.dtype),
-                 projected.shape[-1], _native.ptr(valid),
-                 _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
+    # local keys and values: the first two column blocks, read in place (the
+    # rings zero invalid entries on the way; the reads never see them)
+    local_keys, local_values = projected[..., :d], projected[..., d:2 * d]
     if length == 1:
         # a decode step: only the carried slots are eligible, both reads in one launch
         local_value = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
@@ -619,12 +597,16 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     pieces = fusion_in if fusion_in is not None else (ws, fast, local_value, salient_value)
     final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
 
-    local_ring = _local_tail(state, local_keys, local_values, valid, settings.local_memory_size, out=out_state)
-    salient = memory.salient_tail(
-        state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys, local_values, admission,
-        settings.salience_memory_size,
-        out=(out_state["salient_keys"], out_state["salient_values"], out_state["salient_valid"])
-        if out_state is not None else None)
+    ring_out = lambda name: (None if out_state is None else
+                             tuple(out_state[name + part] for part in ("_keys", "_values", "_valid")))
+    if state["local_keys"].shape[1] != settings.local_memory_size:
+        raise ValueError("the local ring must hold exactly `local_memory_size` entries (static state)")
+    _, local_ring = window_rings(state["local_keys"], state["local_values"], state["local_valid"], local_keys,
+                                 local_values, valid, window=length, capacity=settings.local_memory_size, tail=True,
+                                 key_valid=valid, final_only=True, final_out=ring_out("local"))
+    _, salient = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
+                              local_values, admission, window=length, capacity=settings.salience_memory_size,
+                              tail=False, key_valid=valid, final_only=True, final_out=ring_out("salient"))
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
@@ -641,8 +623,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
 
 
 def window_rings(carried_keys: Tensor, carried_values: Tensor, carried_flags: Tensor, keys: Tensor, values: Tensor,
-                 flags: Tensor, *, window: int, capacity: int, tail: bool
-                 ) -> tuple[tuple[Tensor, Tensor, Tensor], tuple[Tensor, Tensor, Tensor]]:
+                 flags: Tensor, *, window: int, capacity: int, tail: bool, key_valid: Tensor | None = None,
+                 final_only: bool = False, final_out: tuple[Tensor, Tensor, Tensor] | None = None
+                 ) -> tuple[tuple[Tensor, Tensor, Tensor] | None, tuple[Tensor, Tensor, Tensor]]:
     """The ring carried into every window of a sequence and the ring after it
     (``koemi_window_rings``): ``((keys, values, flags), (final keys, final
     values, final flags))`` with ``[B * L / window, capacity, D]`` keys and
@@ -651,22 +634,51 @@ def window_rings(carried_keys: Tensor, carried_values: Tensor, carried_flags: Te
     the batched window reads take), and ``[B, capacity, ...]`` finals.
     ``tail``: the local ring (the last ``capacity`` entries,
     LocalKeyValueMemory.tail, memory.py:385-403); otherwise the salient ring
-    (salient_tail, memory.py:431-455)."""
+    (salient_tail, memory.py:431-455).
+
+    ``keys``/``values`` ``[B, L, D]`` may be views with evenly spaced rows
+    (column blocks of the block's projection, fp32 or bf16, read in place
+    into fp32 rings); ``key_valid`` ``[B, L]`` zeroes the entries of invalid
+    positions on the way (network.py:337-340). ``final_only``: only the ring
+    after the sequence (the first result is None); ``final_out``: buffers
+    that receive it (a decode graph's static state)."""
 
     batch, length, width = keys.shape
     rows = batch * (length // window)
-    out_k = torch.empty((rows, capacity, width), device=keys.device, dtype=keys.dtype)
-    out_v = torch.empty_like(out_k)
-    out_ok = torch.empty((rows, capacity), device=keys.device, dtype=torch.bool)
-    fin_k = torch.empty((batch, capacity, width), device=keys.device, dtype=keys.dtype)
-    fin_v = torch.empty_like(fin_k)
-    fin_ok = torch.empty((batch, capacity), device=keys.device, dtype=torch.bool)
-    args = [t.contiguous() for t in (carried_keys, carried_values, carried_flags, keys, values, flags)]
-    _native.call("koemi_window_rings", *(_native.ptr(t) for t in args), _native.ptr(out_k), _native.ptr(out_v),
-                 _native.ptr(out_ok), _native.ptr(fin_k), _native.ptr(fin_v), _native.ptr(fin_ok), batch,
-                 carried_keys.shape[1], length, window, width, capacity, int(tail), _native.dtype_code(keys.dtype),
-                 _native.stream_of(keys.device))
-    return (out_k, out_v, out_ok), (fin_k, fin_v, fin_ok)
+    ring_dtype = carried_keys.dtype
+    strided = keys.dtype != ring_dtype or not keys.is_contiguous() or not values.is_contiguous()
+    if strided or key_valid is not None:
+        stride = keys.stride(1)
+        if (keys.stride(2) != 1 or keys.stride(0) != length * stride or values.stride() != keys.stride()
+                or values.dtype != keys.dtype):
+            raise ValueError("window ring entries must be views with contiguous columns and evenly spaced rows")
+    else:
+        keys, values = keys.contiguous(), values.contiguous()
+        stride = width
+    if final_only:
+        out_k = out_v = out_ok = None
+    else:
+        out_k = torch.empty((rows, capacity, width), device=keys.device, dtype=ring_dtype)
+        out_v = torch.empty_like(out_k)
+        out_ok = torch.empty((rows, capacity), device=keys.device, dtype=torch.bool)
+    slots = min(carried_keys.shape[1] + length, capacity)
+    if final_out is not None:
+        fin_k, fin_v, fin_ok = final_out
+        if fin_k.shape != (batch, slots, width) or fin_ok.shape != (batch, slots) or not all(
+                t.is_contiguous() for t in final_out):
+            raise ValueError("final_out must be contiguous [B, slots, D], [B, slots, D] and [B, slots] buffers")
+    else:
+        fin_k = torch.empty((batch, slots, width), device=keys.device, dtype=ring_dtype)
+        fin_v = torch.empty_like(fin_k)
+        fin_ok = torch.empty((batch, slots), device=keys.device, dtype=torch.bool)
+    ck, cv, cf, fl = (t.contiguous() for t in (carried_keys, carried_values, carried_flags, flags))
+    kv = None if key_valid is None else key_valid.contiguous()
+    _native.call("koemi_window_rings", _native.ptr(ck), _native.ptr(cv), _native.ptr(cf), _native.ptr(keys),
+                 _native.ptr(values), _native.dtype_code(keys.dtype), stride, _native.ptr(kv), _native.ptr(fl),
+                 _native.ptr(out_k), _native.ptr(out_v), _native.ptr(out_ok), _native.ptr(fin_k), _native.ptr(fin_v),
+                 _native.ptr(fin_ok), batch, carried_keys.shape[1], length, window, width, capacity, int(tail),
+                 _native.dtype_code(ring_dtype), _native.stream_of(keys.device))
+    return (None if final_only else (out_k, out_v, out_ok)), (fin_k, fin_v, fin_ok)
 
 
 def associative_scan_read_windows(projections: Tensor, surprise: Tensor, valid: Tensor, basis: Tensor,
@@ -811,14 +823,12 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
     projected = _projection(ws_low, p, "ws")
-    local_keys = torch.empty((batch, length, d), device=ids.device, dtype=torch.float32)
-    local_values = torch.empty_like(local_keys)
-    _native.call("koemi_herm_masked_pair", _native.ptr(projected), _native.dtype_code(projected.dtype),
-                 projected.shape[-1], _native.ptr(valid),
-                 _native.ptr(local_keys), _native.ptr(local_values), batch * length, d, _native.stream_of(ids.device))
+    # local keys and values read in place from the projection (see block_window)
+    local_keys, local_values = projected[..., :d], projected[..., d:2 * d]
     cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
     local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],
-                                            local_keys, local_values, valid, window=chunk, capacity=cap_l, tail=True)
+                                            local_keys, local_values, valid, window=chunk, capacity=cap_l, tail=True,
+                                            key_valid=valid)
     per_window = lambda t: None if t is None else t.view(rows, chunk, *t.shape[2:])
     local_value = memory.read_local_window(*local_rings, per_window(local_keys), per_window(local_values),
                                            per_window(valid), per_window(ws), window=cap_l,
@@ -830,7 +840,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
                                                             out=_block(fusion_in, 1, d))
     salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                 local_keys, local_values, admission, window=chunk, capacity=cap_s,
-                                                tail=False)
+                                                tail=False, key_valid=valid)
     salient_value = memory.read_salient_window(*salient_rings, per_window(local_keys), per_window(local_values),
                                                per_window(admission), per_window(ws),
                                                out=per_window(_block(fusion_in, 3, d)))

@@ -47,7 +47,10 @@ def read_salient_window(
     float32 or bfloat16 ``[B, L, D]`` view with contiguous columns and evenly
     spaced rows, e.g. a column block of a wider matrix) the read is written
     there, by one kernel where ``koemi_memory_read_into`` takes the shape, and
-    ``out`` is returned.
+    ``out`` is returned; that kernel also takes fp32 queries with bfloat16
+    ``keys``/``values`` viewed in place (contiguous columns, evenly spaced
+    rows, e.g. column blocks of the block's key/value projection), widened
+    exactly.
     """
 
     return _masked_read(
@@ -88,14 +91,15 @@ def read_local_window(
     )
 
 
-def _row_stride(out: Tensor, shape: tuple[int, int, int]) -> int:
-    """Row stride of an output view [batch, length, width] whose rows are
-    evenly spaced with contiguous columns (a column block of a wider matrix)."""
+def _row_stride(out: Tensor, shape: tuple[int, int, int], name: str = "out", any_dtype: bool = False) -> int:
+    """Row stride of a view [batch, length, width] whose rows are evenly
+    spaced with contiguous columns (a column block of a wider matrix)."""
 
-    if not isinstance(out, Tensor) or tuple(out.shape) != shape or out.dtype not in (torch.float32, torch.bfloat16):
-        raise CudaThinkValidationError(f"out must be a float32 or bfloat16 tensor of shape {list(shape)}")
+    if not isinstance(out, Tensor) or tuple(out.shape) != shape or (
+            not any_dtype and out.dtype not in (torch.float32, torch.bfloat16)):
+        raise CudaThinkValidationError(f"{name} must be a float32 or bfloat16 tensor of shape {list(shape)}")
     if out.stride(2) != 1 or out.stride(0) != shape[1] * out.stride(1) or out.stride(1) % 4:
-        raise CudaThinkValidationError("out must have contiguous columns and evenly spaced rows (stride % 4 == 0)")
+        raise CudaThinkValidationError(f"{name} must have contiguous columns and evenly spaced rows (stride % 4 == 0)")
     return out.stride(1)
 
 
@@ -153,8 +157,21 @@ def _masked_read(
         raise CudaThinkValidationError(f"carried_valid and {mask_name} must be torch.bool")
     if queries.dtype not in _SUPPORTED_DTYPES:
         raise CudaThinkValidationError("queries must be float32, float16 or bfloat16")
-    if any(t.dtype != queries.dtype for t in (keys, values, carried_keys, carried_values)):
-        raise CudaThinkValidationError("keys, values, queries and the carried entries must share a dtype")
+    # bf16 window entries read in place by the fused fp32 read
+    in_place = (keys.dtype == torch.bfloat16 and queries.dtype == torch.float32 and out is not None
+                and _fused_read_fits(carried_keys.shape[1], length, width, window))
+    widen = keys.dtype == torch.bfloat16 and queries.dtype == torch.float32 and not in_place
+    if any(t.dtype != queries.dtype for t in (carried_keys, carried_values)) or values.dtype != keys.dtype or (
+            keys.dtype != queries.dtype and not (keys.dtype == torch.bfloat16 and queries.dtype == torch.float32)):
+        raise CudaThinkValidationError("keys, values, queries and the carried entries must share a dtype "
+                                       "(or bfloat16 keys and values with fp32 queries)")
+    if widen:  # bf16 entries for a read that cannot take them in place: widened (exactly) first
+        keys, values = keys.float(), values.float()
+    key_stride = width
+    if in_place:
+        key_stride = _row_stride(keys, (batch, length, width), "keys", any_dtype=True)
+        if _row_stride(values, (batch, length, width), "values", any_dtype=True) != key_stride:
+            raise CudaThinkValidationError("keys and values must have the same row stride")
     if width < 1:
         raise CudaThinkValidationError("width must be positive")
     try:
@@ -168,11 +185,15 @@ def _masked_read(
         if batch == 0 or length == 0:
             return out
         if queries.dtype == torch.float32 and _fused_read_fits(carried, length, width, window):
-            contiguous = [t.contiguous() for t in (carried_keys, carried_values, carried_valid, keys, values, mask,
-                                                   queries)]
-            _native.call("koemi_memory_read_into", *[_native.ptr(t) if t.numel() else None for t in contiguous],
-                         _native.ptr(out), _native.dtype_code(out.dtype), stride, batch, carried, length, width,
-                         window, _native.stream_of(device))
+            ck, cv, cvalid, fl, qs = (t.contiguous() for t in (carried_keys, carried_values, carried_valid, mask,
+                                                               queries))
+            if not in_place:
+                keys, values = keys.contiguous(), values.contiguous()
+            ptr = lambda t: _native.ptr(t) if t.numel() else None
+            _native.call("koemi_memory_read_into", ptr(ck), ptr(cv), ptr(cvalid), ptr(keys), ptr(values),
+                         _native.dtype_code(keys.dtype), key_stride, ptr(fl), ptr(qs), _native.ptr(out),
+                         _native.dtype_code(out.dtype), stride, batch, carried, length, width, window,
+                         _native.stream_of(device))
         else:
             out.copy_(_masked_read(front, mask_name, carried_keys, carried_values, carried_valid, keys, values, mask,
                                    queries, window))

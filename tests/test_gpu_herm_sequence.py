@@ -79,6 +79,63 @@ def test_window_rings_equal_the_window_by_window_rings(device, p_flag):
                 rk, rv = rk.astype(np.float32), rv.astype(np.float32)
 
 
+@pytest.mark.parametrize("key_dtype", [torch.bfloat16, torch.float32])
+def test_window_rings_read_projection_columns_in_place(device, key_dtype):
+    """Keys and values read in place from column blocks of a wider projection
+    (bf16 or fp32, rows C apart) with key_valid give the same ring bits as the
+    contiguous fp32 entries with invalid rows zeroed (network.py:337-340);
+    final_only (with and without final_out buffers) gives the final ring of
+    the full call, and with a carried ring below capacity the rings of
+    oracle.salient_tail and of the tail of [ring ; entries]."""
+
+    rng = np.random.default_rng(11)
+    b, s, window, windows, d = 3, 5, 7, 4, 12
+    length, c = window * windows, 2 * d + 8
+    ck, cv, cok, _, _, flags = _rand_rings(rng, b, s, length, d, 0.4)
+    valid = rng.random((b, length)) < 0.7
+    flags &= valid
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    projected = torch.randn((b, length, c), device=device).to(key_dtype)
+    keys, values = projected[..., :d], projected[..., d:2 * d]
+    vmask = t(valid)
+    masked = [torch.where(vmask[..., None], x.float(), torch.zeros((), device=device)).contiguous()
+              for x in (keys, values)]
+    for tail, fl in ((True, valid), (False, flags)):
+        want_rings, want_final = herm.window_rings(t(ck), t(cv), t(cok), *masked, t(fl), window=window, capacity=s,
+                                                   tail=tail)
+        got_rings, got_final = herm.window_rings(t(ck), t(cv), t(cok), keys, values, t(fl), window=window,
+                                                 capacity=s, tail=tail, key_valid=vmask)
+        for w, g in zip(want_rings + want_final, got_rings + got_final):
+            assert torch.equal(w, g), f"tail={tail}"
+        none, final = herm.window_rings(t(ck), t(cv), t(cok), keys, values, t(fl), window=length, capacity=s,
+                                        tail=tail, key_valid=vmask, final_only=True)
+        assert none is None
+        for w, g in zip(want_final, final):
+            assert torch.equal(w, g), f"final_only tail={tail}"
+        bufs = tuple(torch.full_like(x, 1) for x in want_final)
+        herm.window_rings(t(ck), t(cv), t(cok), keys, values, t(fl), window=length, capacity=s, tail=tail,
+                          key_valid=vmask, final_only=True, final_out=bufs)
+        for w, g in zip(want_final, bufs):
+            assert torch.equal(w, g), f"final_out tail={tail}"
+        # a carried ring below capacity (two entries, capacity 9)
+        cap, short = 9, 2
+        head = projected[:, :window].contiguous()
+        _, final = herm.window_rings(t(ck[:, :short]), t(cv[:, :short]), t(cok[:, :short]), head[..., :d],
+                                     head[..., d:2 * d], t(fl[:, :window]), window=window, capacity=cap, tail=tail,
+                                     key_valid=vmask[:, :window].contiguous(), final_only=True)
+        mk, mv = (m[:, :window].cpu().numpy() for m in masked)
+        if tail:
+            rk = np.concatenate([ck[:, :short], mk], axis=1)[:, -cap:]
+            rv = np.concatenate([cv[:, :short], mv], axis=1)[:, -cap:]
+            rok = np.concatenate([cok[:, :short], fl[:, :window]], axis=1)[:, -cap:]
+        else:
+            rk, rv, rok = (np.asarray(x) for x in oracle.salient_tail(ck[:, :short], cv[:, :short], cok[:, :short],
+                                                                      mk, mv, fl[:, :window], cap))
+        np.testing.assert_array_equal(final[2].cpu().numpy(), rok, err_msg=f"short tail={tail}")
+        np.testing.assert_array_equal(final[0].cpu().numpy(), rk.astype(np.float32), err_msg=f"short tail={tail}")
+        np.testing.assert_array_equal(final[1].cpu().numpy(), rv.astype(np.float32), err_msg=f"short tail={tail}")
+
+
 def test_windowed_associative_memory_equals_window_by_window(device):
     g = torch.Generator(device=device).manual_seed(9)
     b, windows, window, d, m = 3, 5, 40, 96, 16

@@ -137,6 +137,36 @@ def test_reads_into_a_bf16_block_equal_the_rounded_reads(device, window, s, leng
     assert not wide[..., :d].any() and not wide[..., 2 * d:].any()
 
 
+@pytest.mark.parametrize("window", [0, 16])
+def test_reads_of_bf16_projection_columns_equal_the_widened_reads(device, window):
+    """The fused read with the window's keys and values as bf16 column blocks
+    of a wider projection (rows 2 D + 8 apart, read in place) equals, bit for
+    bit, the read of the same entries widened to contiguous fp32; entries of
+    positions the flags exclude do not matter (garbage there changes
+    nothing)."""
+
+    b, s, length, d = 3, 16, 64, 64
+    ck, cv, cvalid, _, _, flags, q = (x.to(device) for x in _read_case(31 + window, b, s, length, d, 0.6,
+                                                                       torch.float32))
+    projected = torch.randn((b, length, 2 * d + 8), device=device).to(torch.bfloat16)
+    keys, values = projected[..., :d], projected[..., d:2 * d]
+    read = memory.read_local_window if window else memory.read_salient_window
+    kw = {"window": window} if window else {}
+    want = torch.zeros((b, length, d), device=device, dtype=torch.float32)
+    read(ck, cv, cvalid, keys.float(), values.float(), flags, q, out=want, **kw)
+    got = torch.zeros_like(want)
+    read(ck, cv, cvalid, keys, values, flags, q, out=got, **kw)
+    assert torch.equal(got, want)
+    # a read that cannot take them in place (no out) widens them first
+    assert torch.equal(read(ck, cv, cvalid, keys, values, flags, q, **kw),
+                       read(ck, cv, cvalid, keys.float(), values.float(), flags, q, **kw))
+    # the fused read lists only flagged slots: what the others hold is never read
+    projected[..., :2 * d].masked_fill_(~flags[..., None], float("nan"))
+    got2 = torch.zeros_like(want)
+    read(ck, cv, cvalid, keys, values, flags, q, out=got2, **kw)
+    assert torch.equal(got2, want)
+
+
 def test_read_salient_window_rejects_bad_inputs(device):
     ck, cv, cvalid, k, v, adm, q = (x.to(device) for x in _read_case(1, 2, 3, 5, 4, 0.5, torch.float32))
     with pytest.raises(think.CudaThinkValidationError, match="share a dtype"):
