@@ -321,6 +321,27 @@ int koemi_read_step_pair(const float* local_keys, const float* local_values, con
                          const uint8_t* salient_valid, int64_t salient_slots, const float* queries, float* local_out,
                          float* salient_out, int64_t batch, int64_t width, koemi_stream_t stream);
 
+/* koemi_read_step_pair and the two rings after the position in the same
+ * launch (a decode step's memory: network.py:337-358, 410-414 with
+ * LocalKeyValueMemory.tail and salient_tail, memory.py:385-403, 431-455):
+ * next_local_* = the last local_slots entries of [local ring ; entry] with
+ * their valid bytes, rows as stored; next_salient_* = the salient_tail rule
+ * of koemi_salient_tail over [salient ring ; entry] with capacity
+ * salient_slots and the admission byte as the entry's flag (invalid slots
+ * zeroed). The entry of batch row b is row b of keys / values (key_dtype
+ * KOEMI_F32 or KOEMI_BF16, rows key_row_stride elements apart, 0: width;
+ * the block's projection read in place), zeroed where valid[b] == 0
+ * (network.py:337-340). Static rings (both slot counts >= 1); the next
+ * rings must not overlap the carried ones. */
+int koemi_read_step_pair_rings(const float* local_keys, const float* local_values, const uint8_t* local_valid,
+                               int64_t local_slots, int64_t window, const float* salient_keys,
+                               const float* salient_values, const uint8_t* salient_valid, int64_t salient_slots,
+                               const float* queries, float* local_out, float* salient_out, const void* keys,
+                               const void* values, int key_dtype, int64_t key_row_stride, const uint8_t* valid,
+                               const uint8_t* admission, float* next_local_keys, float* next_local_values,
+                               uint8_t* next_local_valid, float* next_salient_keys, float* next_salient_values,
+                               uint8_t* next_salient_valid, int64_t batch, int64_t width, koemi_stream_t stream);
+
 /* Bounded recurrent gates, BoundedRecurrentState.gates of model/memory.py:14-30
  * with the masking of network.py:306-309 (a torch composite in the
  * reference): for input rows u (rows x width, `dtype`),

@@ -284,10 +284,40 @@ struct StepMemory {
     int window;
 };
 
-template <typename T>
+__device__ __forceinline__ void load4_any(const float* p, float (&o)[4]) { Vec4<float>::load(p, o); }
+__device__ __forceinline__ void load4_any(const bf16* p, float (&o)[4]) {
+    const float4 x = load4(p);
+    o[0] = x.x;
+    o[1] = x.y;
+    o[2] = x.z;
+    o[3] = x.w;
+}
+
+// The ring of one memory after a one-position window (fp32 rings of S == the
+// capacity slots, the position's entry in KT rows kstride elements apart):
+// tail = the last S entries of [ring ; entry] (LocalKeyValueMemory.tail,
+// memory.py:385-403), rows as stored; otherwise the salient_tail rule of
+// memory.py:431-455 (flag = admission, invalid slots zeroed). An entry whose
+// kvalid byte is 0 enters as zeros (network.py:337-340).
+template <typename KT>
+struct StepRing {
+    const KT* k;
+    const KT* v;
+    int64_t kstride;
+    const uint8_t* kvalid;
+    const uint8_t* flag;
+    float* ok;
+    float* ov;
+    uint8_t* ovalid;
+    bool tail;
+};
+
+struct NoRing {};
+
+template <typename T, typename Ring = NoRing>
 __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
                                const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
-                               int window);
+                               int window, const Ring& ring = Ring{});
 
 template <typename T>
 __global__ __launch_bounds__(256) void read_step_kernel(const T* __restrict__ ck, const T* __restrict__ cv,
@@ -304,10 +334,21 @@ __global__ __launch_bounds__(256) void read_step_pair_kernel(StepMemory<T> m0, S
     read_step_body<T>(m.ck, m.cv, m.cvalid, q, m.out, m.S, D, inv_sqrt_d, m.window);
 }
 
-template <typename T>
+// read_step_pair_kernel that also writes both rings after the position
+// (z = 0 the local ring, z = 1 the salient ring).
+template <typename KT>
+__global__ __launch_bounds__(256) void read_step_rings_kernel(StepMemory<float> m0, StepMemory<float> m1,
+                                                              StepRing<KT> r0, StepRing<KT> r1,
+                                                              const float* __restrict__ q, int64_t D,
+                                                              float inv_sqrt_d) {
+    if (blockIdx.z == 0) read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, r0);
+    else read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, r1);
+}
+
+template <typename T, typename Ring>
 __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
                                const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
-                               int window) {
+                               int window, const Ring& ring) {
     __shared__ float w_sh[kStepMaxSlots];
     __shared__ float stat[1];
     const int64_t b = blockIdx.x;
@@ -372,29 +413,91 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
     __syncthreads();
     const float inv = stat[0];
     const int64_t d = static_cast<int64_t>(blockIdx.y) * 1024 + tid * 4;
-    if (d >= D) return;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const T* vcol = cv + b * S * D + d;
-    int sl = 0;
-    for (; sl + 8 <= S; sl += 8) {
-        float v[8][4];
+    if (d < D) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const T* vcol = cv + b * S * D + d;
+        int sl = 0;
+        for (; sl + 8 <= S; sl += 8) {
+            float v[8][4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) Vec4<T>::load(vcol + (sl + u) * D, v[u]);
+            for (int u = 0; u < 8; ++u) Vec4<T>::load(vcol + (sl + u) * D, v[u]);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float wgt = w_sh[sl + u] * inv;
+            for (int u = 0; u < 8; ++u) {
+                const float wgt = w_sh[sl + u] * inv;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[u][c], acc[c]);
+                for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[u][c], acc[c]);
+            }
+        }
+        for (; sl < S; ++sl) {
+            float v[4];
+            Vec4<T>::load(vcol + sl * D, v);
+            const float wgt = w_sh[sl] * inv;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[c], acc[c]);
+        }
+        Vec4<T>::store(out + b * D + d, acc);
+    }
+    if constexpr (!std::is_same<Ring, NoRing>::value) {
+        // the ring after the position: S slots from the N = S + 1 entries [ring ; entry]
+        __shared__ uint8_t fl[kStepMaxSlots + 1];
+        __shared__ int16_t slot_src[kStepMaxSlots];
+        __shared__ uint8_t slot_flag[kStepMaxSlots];
+        const int N = S + 1, C = S;
+        for (int i = tid; i < N; i += 256) fl[i] = (i < S ? cvalid[b * S + i] : ring.flag[b]) != 0 ? 1 : 0;
+        __syncthreads();
+        if (ring.tail) {
+            for (int s = tid; s < C; s += 256) {
+                slot_src[s] = static_cast<int16_t>(s + 1);
+                slot_flag[s] = fl[s + 1];
+            }
+        } else {
+            int total = 0;
+            for (int j = 0; j < N; ++j) total += fl[j];
+            const int m = min(total, C);
+            for (int i = tid; i < N; i += 256) {
+                int va = 0;
+                for (int j = i + 1; j < N; ++j) va += fl[j];
+                const int ia = (N - 1 - i) - va;
+                const bool keep = fl[i] ? va < m : ia < C - m;
+                if (keep) {
+                    const int slot = C - 1 - (min(va, m) + min(ia, C - m));
+                    slot_src[slot] = static_cast<int16_t>(i);
+                    slot_flag[slot] = fl[i];
+                }
+            }
+        }
+        __syncthreads();
+        if (blockIdx.y == 0)
+            for (int s = tid; s < C; s += 256) ring.ovalid[b * C + s] = slot_flag[s];
+        if (d < D) {
+            const bool entry_zero = ring.kvalid != nullptr && ring.kvalid[b] == 0;
+            float ek[4], ev[4];
+            load4_any(ring.k + b * ring.kstride + d, ek);
+            load4_any(ring.v + b * ring.kstride + d, ev);
+#pragma unroll 4
+            for (int s = 0; s < C; ++s) {
+                const int i = slot_src[s];
+                const bool zero = (!ring.tail && !slot_flag[s]) || (i == S && entry_zero);
+                float kq[4], vq[4];
+                if (i < S) {
+                    Vec4<float>::load(ck + (b * S + i) * D + d, kq);
+                    Vec4<float>::load(cv + (b * S + i) * D + d, vq);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        kq[c] = ek[c];
+                        vq[c] = ev[c];
+                    }
+                }
+                if (zero) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) kq[c] = vq[c] = 0.0f;
+                }
+                Vec4<float>::store(ring.ok + (b * C + s) * D + d, kq);
+                Vec4<float>::store(ring.ov + (b * C + s) * D + d, vq);
+            }
         }
     }
-    for (; sl < S; ++sl) {
-        float v[4];
-        Vec4<T>::load(vcol + sl * D, v);
-        const float wgt = w_sh[sl] * inv;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[c], acc[c]);
-    }
-    Vec4<T>::store(out + b * D + d, acc);
 }
 
 // out[b][t][d] = sum over slots s of weight[b][t][s] . [carried_values ; values][b][s][d]
@@ -1151,4 +1254,55 @@ extern "C" int koemi_read_step_pair(const float* local_keys, const float* local_
                        dim3(static_cast<unsigned>(batch), static_cast<unsigned>((width + 1023) / 1024), 2),
                        dim3(256), 0, as_stream(stream), m0, m1, queries, width, inv_sqrt_d);
     return check_launch("koemi_read_step_pair");
+}
+
+extern "C" int koemi_read_step_pair_rings(
+    const float* local_keys, const float* local_values, const uint8_t* local_valid, int64_t local_slots,
+    int64_t window, const float* salient_keys, const float* salient_values, const uint8_t* salient_valid,
+    int64_t salient_slots, const float* queries, float* local_out, float* salient_out, const void* keys,
+    const void* values, int key_dtype, int64_t key_row_stride, const uint8_t* valid, const uint8_t* admission,
+    float* next_local_keys, float* next_local_values, uint8_t* next_local_valid, float* next_salient_keys,
+    float* next_salient_values, uint8_t* next_salient_valid, int64_t batch, int64_t width, koemi_stream_t stream) {
+    if (batch < 0 || width < 1 || local_slots < 1 || salient_slots < 1 || window < 1)
+        return fail(KOEMI_ERR_INVALID, "read step rings need non-negative batch, positive width, window and slots");
+    if (local_slots > kStepMaxSlots || salient_slots > kStepMaxSlots || width % 4 != 0 || batch > 65535 ||
+        window > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "read step rings need at most %d slots, width %% 4 == 0, batch <= 65535",
+                    kStepMaxSlots);
+    if (key_dtype != KOEMI_F32 && key_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "read step rings take float32 or bfloat16 keys and values");
+    if (key_row_stride == 0) key_row_stride = width;
+    if (key_row_stride < width || key_row_stride % 4 != 0)
+        return fail(KOEMI_ERR_INVALID, "read step rings: key row stride must be a multiple of 4, at least the width");
+    if (batch == 0) return KOEMI_OK;
+    if (!queries || !local_out || !salient_out || !local_keys || !local_values || !local_valid || !salient_keys ||
+        !salient_values || !salient_valid || !keys || !values || !valid || !admission || !next_local_keys ||
+        !next_local_values || !next_local_valid || !next_salient_keys || !next_salient_values || !next_salient_valid)
+        return fail(KOEMI_ERR_INVALID, "read step rings received a null pointer");
+    auto aligned = [](const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+    const size_t ka = key_dtype == KOEMI_F32 ? 16 : 8;
+    if (!aligned(local_keys, 16) || !aligned(local_values, 16) || !aligned(salient_keys, 16) ||
+        !aligned(salient_values, 16) || !aligned(queries, 16) || !aligned(local_out, 16) ||
+        !aligned(salient_out, 16) || !aligned(next_local_keys, 16) || !aligned(next_local_values, 16) ||
+        !aligned(next_salient_keys, 16) || !aligned(next_salient_values, 16) || !aligned(keys, ka) ||
+        !aligned(values, ka))
+        return fail(KOEMI_ERR_INVALID, "read step rings need aligned rows");
+    const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+    const StepMemory<float> m0{local_keys, local_values, local_valid, local_out, static_cast<int>(local_slots),
+                               static_cast<int>(window)};
+    const StepMemory<float> m1{salient_keys, salient_values, salient_valid, salient_out,
+                               static_cast<int>(salient_slots), 0};
+    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((width + 1023) / 1024), 2);
+    auto launch = [&](auto tag) {
+        using KT = decltype(tag);
+        const StepRing<KT> r0{static_cast<const KT*>(keys), static_cast<const KT*>(values), key_row_stride, valid,
+                              valid, next_local_keys, next_local_values, next_local_valid, true};
+        const StepRing<KT> r1{static_cast<const KT*>(keys), static_cast<const KT*>(values), key_row_stride, valid,
+                              admission, next_salient_keys, next_salient_values, next_salient_valid, false};
+        hipLaunchKernelGGL(read_step_rings_kernel<KT>, grid, dim3(256), 0, as_stream(stream), m0, m1, r0, r1,
+                           queries, width, inv_sqrt_d);
+    };
+    if (key_dtype == KOEMI_BF16) launch(bf16{});
+    else launch(float{});
+    return check_launch("koemi_read_step_pair_rings");
 }

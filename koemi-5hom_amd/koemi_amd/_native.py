@@ -143,6 +143,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P),
     ),
+    "koemi_read_step_pair_rings": (
+        c_int,
+        (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, _P, _P,
+         _P, _P, _P, c_int64, c_int64, _P),
+    ),
     "koemi_herm_token_context": (c_int, (_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_local_read": (
         c_int,

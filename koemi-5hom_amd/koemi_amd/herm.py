@@ -443,7 +443,8 @@ def _input_norm(p: dict[str, Tensor], ids: Tensor, context, low) -> Tensor:
 
 def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, previous: Tensor, valid: Tensor,
                       pieces: tuple[Tensor, Tensor, Tensor, Tensor] | Tensor, with_logits: bool,
-                      next_norm: Tensor | None = None) -> tuple[Tensor | NextInput, Tensor | None]:
+                      next_norm: Tensor | None = None, routing: dict | None = None
+                      ) -> tuple[Tensor | NextInput, Tensor | None]:
     """The block's position-wise tail: fusion of [working ; memory ; local ;
     salient] with its normalizer (network.py:723-732), the expert mixture with
     its output normalizer (experts.py:109-150 or router.py:43-97) and the token
@@ -454,7 +455,10 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     fp32, logits or None). With ``next_norm`` (the next block's input norm
     weight) and a bf16 stack, the combine, this block's expert normalizer and
     the next block's input norm run as one kernel and the context returned is
-    that ``NextInput`` (no fp32 context unless logits are asked for too)."""
+    that ``NextInput`` (no fp32 context unless logits are asked for too).
+    ``routing``: a dict shared by the layers of one stack pass; the hash
+    route depends only on the ids and the validity (experts.py:283-289), so
+    the first layer's permutation is kept there and reused by the others."""
 
     batch, length = ids.shape
     d = settings.width
@@ -492,8 +496,12 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         weights = None
     pair_positions = None
     if hashed:
-        sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = moe.permute_hash_indices(
-            ids, previous, flat_valid, expert_count=settings.expert_count, top_k=k)
+        route = routing.get("hash") if routing is not None else None
+        if route is None:
+            route = moe.permute_hash_indices(ids, previous, flat_valid, expert_count=settings.expert_count, top_k=k)
+            if routing is not None:
+                routing["hash"] = route
+        sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = route
     elif indexed:
         sorted_rows, sorted_experts, offsets, sorted_weights, pair_positions = moe.permute_indices(
             assignments.reshape(-1, k), flat_valid, expert_count=settings.expert_count, pair_weights=weights)
@@ -533,7 +541,8 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
 def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
                  context: Tensor | NextInput | None = None, *, with_logits: bool = True,
                  token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
-                 next_norm: Tensor | None = None, out_state: dict[str, Tensor] | None = None
+                 next_norm: Tensor | None = None, out_state: dict[str, Tensor] | None = None,
+                 routing: dict | None = None
                  ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
@@ -546,7 +555,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     norm weight, for a stack; the context returned is then a ``NextInput``
     (see ``_fuse_mix_predict``). ``out_state`` (a decode step, one position):
     a state dict whose buffers receive the next state (a decode graph's other
-    static state; ``last_token`` is the caller's, from the token context)."""
+    static state; ``last_token`` is the caller's, from the token context).
+    ``routing``: shared by the layers of a stack pass (see
+    ``_fuse_mix_predict``)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
@@ -571,15 +582,34 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     # local keys and values: the first two column blocks, read in place (the
     # rings zero invalid entries on the way; the reads never see them)
     local_keys, local_values = projected[..., :d], projected[..., d:2 * d]
+    ring_out = lambda name: (None if out_state is None else
+                             tuple(out_state[name + part] for part in ("_keys", "_values", "_valid")))
+    if state["local_keys"].shape[1] != settings.local_memory_size:
+        raise ValueError("the local ring must hold exactly `local_memory_size` entries (static state)")
+    step_rings = (length == 1 and state["salient_keys"].shape[1] == settings.salience_memory_size
+                  and all(state[k].is_contiguous() for k in ("local_keys", "local_values", "local_valid",
+                                                              "salient_keys", "salient_values", "salient_valid")))
     if length == 1:
-        # a decode step: only the carried slots are eligible, both reads in one launch
+        # a decode step: only the carried slots are eligible, both reads in one
+        # launch, with both rings after the step when they are static
         local_value = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
         salient_value = torch.empty_like(local_value)
-        _native.call("koemi_read_step_pair", _native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
-                     _native.ptr(state["local_valid"]), state["local_keys"].shape[1], settings.local_memory_size,
-                     _native.ptr(state["salient_keys"]), _native.ptr(state["salient_values"]),
-                     _native.ptr(state["salient_valid"]), state["salient_keys"].shape[1], _native.ptr(ws),
-                     _native.ptr(local_value), _native.ptr(salient_value), batch, d, _native.stream_of(ids.device))
+        common = (_native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
+                  _native.ptr(state["local_valid"]), state["local_keys"].shape[1], settings.local_memory_size,
+                  _native.ptr(state["salient_keys"]), _native.ptr(state["salient_values"]),
+                  _native.ptr(state["salient_valid"]), state["salient_keys"].shape[1], _native.ptr(ws),
+                  _native.ptr(local_value), _native.ptr(salient_value))
+        if step_rings:
+            local_ring = ring_out("local") or tuple(torch.empty_like(state["local" + part])
+                                                    for part in ("_keys", "_values", "_valid"))
+            salient = ring_out("salient") or tuple(torch.empty_like(state["salient" + part])
+                                                   for part in ("_keys", "_values", "_valid"))
+            _native.call("koemi_read_step_pair_rings", *common, _native.ptr(local_keys), _native.ptr(local_values),
+                         _native.dtype_code(local_keys.dtype), local_keys.stride(1), _native.ptr(valid),
+                         _native.ptr(admission), *(_native.ptr(t) for t in local_ring + salient), batch, d,
+                         _native.stream_of(ids.device))
+        else:
+            _native.call("koemi_read_step_pair", *common, batch, d, _native.stream_of(ids.device))
     else:
         local_value = memory.read_local_window(state["local_keys"], state["local_values"], state["local_valid"],
                                                local_keys, local_values, valid, ws, window=settings.local_memory_size,
@@ -595,18 +625,16 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                    state["salient_valid"], local_keys, local_values, admission, ws,
                                                    out=_block(fusion_in, 3, d))
     pieces = fusion_in if fusion_in is not None else (ws, fast, local_value, salient_value)
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm, routing)
 
-    ring_out = lambda name: (None if out_state is None else
-                             tuple(out_state[name + part] for part in ("_keys", "_values", "_valid")))
-    if state["local_keys"].shape[1] != settings.local_memory_size:
-        raise ValueError("the local ring must hold exactly `local_memory_size` entries (static state)")
-    _, local_ring = window_rings(state["local_keys"], state["local_values"], state["local_valid"], local_keys,
-                                 local_values, valid, window=length, capacity=settings.local_memory_size, tail=True,
-                                 key_valid=valid, final_only=True, final_out=ring_out("local"))
-    _, salient = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"], local_keys,
-                              local_values, admission, window=length, capacity=settings.salience_memory_size,
-                              tail=False, key_valid=valid, final_only=True, final_out=ring_out("salient"))
+    if not step_rings:
+        _, local_ring = window_rings(state["local_keys"], state["local_values"], state["local_valid"], local_keys,
+                                     local_values, valid, window=length, capacity=settings.local_memory_size,
+                                     tail=True, key_valid=valid, final_only=True, final_out=ring_out("local"))
+        _, salient = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
+                                  local_keys, local_values, admission, window=length,
+                                  capacity=settings.salience_memory_size, tail=False, key_valid=valid,
+                                  final_only=True, final_out=ring_out("salient"))
     next_state = {
         "working": ws[:, -1].contiguous(),
         "basis": basis,
@@ -779,7 +807,7 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
                    context: Tensor | NextInput | None = None, *, with_logits: bool = True,
                    token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
-                   next_norm: Tensor | None = None
+                   next_norm: Tensor | None = None, routing: dict | None = None
                    ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One block over a whole sequence of windows at once: forward_parallel
     (network.py:176-197) of a single block, i.e. ``block_window`` applied to
@@ -798,8 +826,8 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     left (``associative_scan_read_windows``). The results equal the
     window-by-window ones up to floating-point rounding (the library GEMMs
     see more rows). ``token_context``: ``_token_context``'s four outputs when
-    the caller formed them (a stack, once for all layers); ``context`` and
-    ``next_norm`` as in ``block_window``. Returns (logits or None, final
+    the caller formed them (a stack, once for all layers); ``context``,
+    ``next_norm`` and ``routing`` as in ``block_window``. Returns (logits or None, final
     context, next state, surprise [B, L]).
     """
 
@@ -848,7 +876,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
         pieces = fusion_in
     else:
         pieces = (ws, fast, local_value.view(batch, length, d), salient_value.view(batch, length, d))
-    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm)
+    final, logits = _fuse_mix_predict(p, settings, ids, previous, valid, pieces, with_logits, next_norm, routing)
     next_state = {
         "working": working_next if working_next is not None else ws[:, -1].contiguous(),
         "basis": basis,
@@ -877,11 +905,13 @@ def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids:
     context = None
     next_states = []
     logits = None
+    routing: dict = {}  # the hash route, formed by the first layer for all of them
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
         logits, context, next_state, _ = block_sequence(p, settings, ids, state, context, with_logits=last,
                                                         token_context=token_context,
-                                                        next_norm=None if last else params[layer + 1]["input_norm"])
+                                                        next_norm=None if last else params[layer + 1]["input_norm"],
+                                                        routing=routing)
         next_states.append(next_state)
     return logits, next_states
 
@@ -940,12 +970,14 @@ def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: 
     context = None
     next_states = []
     logits = None
+    routing: dict = {}  # the hash route, formed by the first layer for all of them
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
         logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
                                                       token_context=token_context,
                                                       next_norm=None if last else params[layer + 1]["input_norm"],
-                                                      out_state=out_states[layer] if out_states is not None else None)
+                                                      out_state=out_states[layer] if out_states is not None else None,
+                                                      routing=routing)
         next_states.append(next_state)
     return logits, next_states
 
@@ -960,10 +992,12 @@ def stack_window(params: list[dict[str, Tensor]], settings: HermSettings, ids: T
     context = None
     next_states = []
     logits = None
+    routing: dict = {}  # the hash route, formed by the first layer for all of them
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
         logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
-                                                      next_norm=None if last else params[layer + 1]["input_norm"])
+                                                      next_norm=None if last else params[layer + 1]["input_norm"],
+                                                      routing=routing)
         next_states.append(next_state)
     return logits, next_states
 

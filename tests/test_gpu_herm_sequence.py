@@ -136,6 +136,48 @@ def test_window_rings_read_projection_columns_in_place(device, key_dtype):
         np.testing.assert_array_equal(final[1].cpu().numpy(), rv.astype(np.float32), err_msg=f"short tail={tail}")
 
 
+@pytest.mark.parametrize("key_dtype, slots", [(torch.bfloat16, 16), (torch.float32, 5)])
+def test_read_step_with_rings_equals_the_read_and_the_two_rings(device, key_dtype, slots):
+    """koemi_read_step_pair_rings (a decode step's reads and both ring
+    updates, one launch) equals koemi_read_step_pair plus window_rings of the
+    local (tail) and salient rings, bit for bit; the entries are column blocks
+    of a wider projection, some positions invalid, some admitted."""
+
+    from koemi_amd import _native
+
+    rng = np.random.default_rng(slots)
+    b, d = 37, 64
+    c = 2 * d + 8
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    lk, lv, lok, _, _, _ = _rand_rings(rng, b, slots, 1, d, 0.5)
+    sk, sv, sok, _, _, _ = _rand_rings(rng, b, slots, 1, d, 0.5)
+    valid = rng.random((b, 1)) < 0.8
+    admission = valid & (rng.random((b, 1)) < 0.5)
+    projected = torch.randn((b, 1, c), device=device).to(key_dtype)
+    keys, values = projected[..., :d], projected[..., d:2 * d]
+    q = torch.randn((b, d), device=device)
+    lk, lv, lok, sk, sv, sok, vmask, amask = (t(x) for x in (lk, lv, lok, sk, sv, sok, valid, admission))
+    stream = _native.stream_of(q.device)
+    common = lambda lo, so: (_native.ptr(lk), _native.ptr(lv), _native.ptr(lok), slots, slots, _native.ptr(sk),
+                             _native.ptr(sv), _native.ptr(sok), slots, _native.ptr(q), _native.ptr(lo),
+                             _native.ptr(so))
+    want_l, want_s = torch.empty_like(q), torch.empty_like(q)
+    _native.call("koemi_read_step_pair", *common(want_l, want_s), b, d, stream)
+    _, want_lr = herm.window_rings(lk, lv, lok, keys, values, vmask, window=1, capacity=slots, tail=True,
+                                   key_valid=vmask, final_only=True)
+    _, want_sr = herm.window_rings(sk, sv, sok, keys, values, amask, window=1, capacity=slots, tail=False,
+                                   key_valid=vmask, final_only=True)
+    got_l, got_s = torch.full_like(q, 7.0), torch.full_like(q, 7.0)
+    got_lr = tuple(torch.full_like(x, 1) for x in want_lr)
+    got_sr = tuple(torch.full_like(x, 1) for x in want_sr)
+    _native.call("koemi_read_step_pair_rings", *common(got_l, got_s), _native.ptr(keys), _native.ptr(values),
+                 _native.dtype_code(key_dtype), keys.stride(1), _native.ptr(vmask), _native.ptr(amask),
+                 *(_native.ptr(x) for x in got_lr + got_sr), b, d, stream)
+    assert torch.equal(got_l, want_l) and torch.equal(got_s, want_s)
+    for w, g in zip(want_lr + want_sr, got_lr + got_sr):
+        assert torch.equal(w, g)
+
+
 def test_windowed_associative_memory_equals_window_by_window(device):
     g = torch.Generator(device=device).manual_seed(9)
     b, windows, window, d, m = 3, 5, 40, 96, 16
