@@ -440,6 +440,29 @@ int koemi_linear_rows(const void* input0, const void* input1, const void* input2
                       int64_t piece_width, int input_dtype, const void* weight, const float* bias, float* output,
                       int64_t rows, int64_t out_features, koemi_stream_t stream);
 
+/* koemi_linear_rows with K split over `splits` workgroup columns (a decode
+ * step's 4096-wide fusion layer, network.py:401-405, spread over the chip):
+ * block s of `partials` ([splits, rows, out_features] fp32) = the products
+ * of K values [s K / splits, (s + 1) K / splits), the bias (fp32 or NULL)
+ * added to block 0 only; the sum of the blocks in order is the projection
+ * (koemi_herm_rmsnorm_parts adds them). piece_width % 1024 == 0 and
+ * K / splits a multiple of 512 (fp32 inputs) or 1024 (bf16 inputs). */
+int koemi_linear_rows_split(const void* input0, const void* input1, const void* input2, const void* input3,
+                            int pieces, int64_t piece_width, int input_dtype, const void* weight, const float* bias,
+                            float* partials, int64_t rows, int64_t out_features, int splits, koemi_stream_t stream);
+
+/* `count` (1..32) independent koemi_linear_rows projections of one shape in
+ * one launch (a decode step's content heads of every layer, network.py:
+ * 318-325, 677-698, each on its own layer's carried working state):
+ * output[e] ([rows, out_features] fp32 blocks, one after another) =
+ * bf16(inputs[e]) weights[e]^T + biases[e]; inputs[e] [rows, in_features] of
+ * input_dtype, weights[e] [out_features, in_features] bf16, `biases` NULL or
+ * an array whose entries may be NULL. The pointer arrays are host arrays,
+ * read during the call. in_features % 64 == 0. */
+int koemi_linear_rows_batched(const void* const* inputs, int input_dtype, const void* const* weights,
+                              const float* const* biases, float* output, int count, int64_t rows,
+                              int64_t in_features, int64_t out_features, koemi_stream_t stream);
+
 /* Salient-memory read, LocalKeyValueMemory.read_salient_window of
  * model/memory.py:405-429 (called at network.py:350-358; a torch composite in
  * the reference). For every batch row b and query t < length:
@@ -528,6 +551,14 @@ int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype,
 int koemi_herm_rmsnorm(const void* input, int input_dtype, const void* residual, int residual_dtype,
                        const float* weight, const uint8_t* mask, float* output, void* output_bf16, int64_t rows,
                        int64_t width, float eps, koemi_stream_t stream);
+/* koemi_herm_rmsnorm of a split projection's result: the input is the sum,
+ * in block order, of `parts` (1..8) fp32 blocks [rows, width] one after another
+ * (koemi_linear_rows_split's partials), plus add_bias (fp32 [width] or
+ * NULL), rounded to bf16 when round_bf16 != 0 (the projection's bf16 output
+ * under autocast); no residual or mask. */
+int koemi_herm_rmsnorm_parts(const float* parts_input, int parts, const float* add_bias, int round_bf16,
+                             const float* weight, float* output, void* output_bf16, int64_t rows, int64_t width,
+                             float eps, koemi_stream_t stream);
 int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,
                              int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out, int64_t pad_id,
                              int64_t batch, int64_t length, koemi_stream_t stream);
@@ -544,6 +575,18 @@ int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, con
 int koemi_herm_surprise_shifted(const float* logits, const float* first, const float* bias, const int64_t* target_ids,
                                 const uint8_t* valid_mask, float* surprise, uint8_t* admission, float threshold,
                                 int64_t batch, int64_t length, int64_t vocab, float log_vocab, koemi_stream_t stream);
+
+/* The surprise and admission of a decode step in every layer at once (each
+ * layer's one position scored on its carried state's content logits,
+ * network.py:318-325, 349, 677-698): row (l, b) of logits [layers * batch,
+ * vocab] is scored with the content bias biases[l] (a host array of `layers`
+ * fp32 [vocab] pointers, read during the call) against target_ids[b] and
+ * valid_mask[b], into surprise[l * batch + b] and admission[l * batch + b]
+ * (NULL: none); the arithmetic of koemi_herm_surprise_shifted at length 1.
+ * layers <= 32, vocab == 256. */
+int koemi_herm_surprise_layers(const float* logits, const float* const* biases, const int64_t* target_ids,
+                               const uint8_t* valid_mask, float* surprise, uint8_t* admission, float threshold,
+                               int layers, int64_t batch, int64_t vocab, float log_vocab, koemi_stream_t stream);
 
 /* The fusion layer's input [working ; memory ; local ; salient]
  * (network.py:401-405, a torch.cat in the reference) as one bf16 matrix

@@ -72,6 +72,71 @@ __global__ __launch_bounds__(256) void herm_rmsnorm_kernel(const X* __restrict__
     }
 }
 
+// koemi_herm_rmsnorm_parts: one workgroup per row, thread t on columns
+// 4 t + 1024 i. The input is the sum of `parts` fp32 blocks part_stride
+// elements apart, added in block order (a split projection's partial sums;
+// every block's load issued before the sums), plus add_bias, optionally
+// rounded to bf16; the row's sum of squares is reduced over the wave, then
+// over the four waves in order.
+constexpr int kMaxParts = 8;
+
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_parts_kernel(const float* __restrict__ x, int parts,
+                                                            int64_t part_stride, const float* __restrict__ add_bias,
+                                                            int round16, const float* __restrict__ w,
+                                                            float* __restrict__ y, bf16* __restrict__ y16, int H,
+                                                            float eps) {
+    __shared__ float wave_ss[4];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    const float* xr = x + row * H;
+    float v[NV][4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * 256 + tid) * 4;
+        if (c < H) {
+            float4 r4[kMaxParts];
+#pragma unroll
+            for (int pt = 0; pt < kMaxParts; ++pt) r4[pt] = load4(xr + min(pt, parts - 1) * part_stride + c);
+            v[j][0] = r4[0].x; v[j][1] = r4[0].y; v[j][2] = r4[0].z; v[j][3] = r4[0].w;
+#pragma unroll
+            for (int pt = 1; pt < kMaxParts; ++pt) {
+                const bool on = pt < parts;
+                v[j][0] += on ? r4[pt].x : 0.0f; v[j][1] += on ? r4[pt].y : 0.0f;
+                v[j][2] += on ? r4[pt].z : 0.0f; v[j][3] += on ? r4[pt].w : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (add_bias != nullptr) v[j][i] += add_bias[c + i];
+                if (round16) v[j][i] = static_cast<float>(static_cast<__bf16>(v[j][i]));
+                ss = fmaf(v[j][i], v[j][i], ss);
+            }
+        }
+    }
+    ss = wave_sum_xor(ss);
+    if (lane == 0) wave_ss[wave] = ss;
+    __syncthreads();
+    const float total = ((wave_ss[0] + wave_ss[1]) + wave_ss[2]) + wave_ss[3];
+    const float inv = rsqrtf(total / static_cast<float>(H) + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * 256 + tid) * 4;
+        if (c >= H) continue;
+        const float4 wq = *reinterpret_cast<const float4*>(w + c);
+        const float4 o = make_float4(v[j][0] * inv * wq.x, v[j][1] * inv * wq.y, v[j][2] * inv * wq.z,
+                                     v[j][3] * inv * wq.w);
+        if (y != nullptr) *reinterpret_cast<float4*>(y + row * H + c) = o;
+        if (y16 != nullptr) {
+            typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+            bf16x4 q;
+            q[0] = static_cast<__bf16>(o.x); q[1] = static_cast<__bf16>(o.y);
+            q[2] = static_cast<__bf16>(o.z); q[3] = static_cast<__bf16>(o.w);
+            *reinterpret_cast<bf16x4*>(y16 + row * H + c) = q;
+        }
+    }
+}
+
 // One workgroup per row: position t takes the latest valid index before it,
 // an exclusive max-scan of (valid ? t : -1) over 256-position chunks (a wave
 // scan, the wave maxima through LDS, the chunk's carry in a register).
@@ -185,6 +250,31 @@ extern "C" int koemi_herm_rmsnorm(const void* input, int input_dtype, const void
     else if (residual_dtype == KOEMI_BF16) with_input(bf16{});
     else with_input(f16{});
     return check_launch("koemi_herm_rmsnorm");
+}
+
+extern "C" int koemi_herm_rmsnorm_parts(const float* parts_input, int parts, const float* add_bias, int round_bf16,
+                                        const float* weight, float* output, void* output_bf16, int64_t rows,
+                                        int64_t width, float eps, koemi_stream_t stream) {
+    if (rows < 0 || width < 1 || parts < 1)
+        return fail(KOEMI_ERR_INVALID, "herm rmsnorm parts needs rows >= 0, a positive width and parts >= 1");
+    if (parts > kMaxParts) return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm parts adds at most %d blocks", kMaxParts);
+    if (width % 4 != 0 || width > 2048)
+        return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm needs a width that is a multiple of 4 and at most 2048");
+    if (rows == 0) return KOEMI_OK;
+    if (rows > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "herm rmsnorm parts: too many rows");
+    if (!parts_input || !weight || (!output && !output_bf16) || reinterpret_cast<uintptr_t>(parts_input) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(weight) % 16 != 0)
+        return fail(KOEMI_ERR_INVALID, "herm rmsnorm parts received a null or unaligned pointer");
+    const int H = static_cast<int>(width);
+    bf16* o16 = static_cast<bf16*>(output_bf16);
+    const dim3 grid(static_cast<unsigned>(rows));
+    if (width <= 1024)
+        hipLaunchKernelGGL(rmsnorm_parts_kernel<1>, grid, dim3(256), 0, as_stream(stream), parts_input, parts,
+                           rows * width, add_bias, round_bf16, weight, output, o16, H, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_parts_kernel<2>, grid, dim3(256), 0, as_stream(stream), parts_input, parts,
+                           rows * width, add_bias, round_bf16, weight, output, o16, H, eps);
+    return check_launch("koemi_herm_rmsnorm_parts");
 }
 
 extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,

@@ -55,12 +55,43 @@ constexpr int kStageBytes = kBlocks * 32 * kRowPitch * 2;
 constexpr int kRedBytes = kWaves * kBlocks * 16 * kWave * 4;
 static_assert(kRedBytes <= kStageBytes, "the partial sums fit in the staging area");
 
-template <typename XT>
+// Independent projections of the same shape in one launch (a decode step's
+// content heads of every layer): with a RowsBatch, blockIdx.y picks entry e,
+// whose input (one piece), weight and bias replace the arguments and whose
+// output is block e of y ([M, N] blocks one after another).
+constexpr int kMaxBatch = 32;
+struct RowsBatch {
+    const void* x[kMaxBatch];
+    const bf16* w[kMaxBatch];
+    const float* bias[kMaxBatch];
+};
+struct NoBatch {};
+
+// Split K (k_len < K, no RowsBatch): blockIdx.y = split s takes K values
+// [s k_len, (s + 1) k_len) and writes its partial sums to block s of y
+// ([M, N] blocks one after another), the bias added by split 0 only; the
+// consumer adds the blocks in split order.
+template <typename XT, typename Batch = NoBatch>
 __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, int64_t piece_width,
                                                                      const bf16* __restrict__ w,
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ y, int64_t M, int64_t N,
-                                                                     int64_t K) {
+                                                                     int64_t K, Batch batch, int64_t k_len) {
+    int64_t k_begin = 0, k_end = K;
+    if constexpr (std::is_same<Batch, RowsBatch>::value) {
+        const int e = blockIdx.y;
+        in = Pieces{{batch.x[e], batch.x[e], batch.x[e], batch.x[e]}};
+        piece_width = K;
+        w = batch.w[e];
+        bias = batch.bias[e];
+        y += static_cast<int64_t>(e) * M * N;
+    } else {
+        const int64_t split = blockIdx.y;
+        k_begin = split * k_len;
+        k_end = k_begin + k_len;
+        y += split * M * N;
+        if (split > 0) bias = nullptr;
+    }
     __shared__ bf16x8 xs_raw[kStageBytes / 16];
     bf16* xs = reinterpret_cast<bf16*>(xs_raw);
     auto red = reinterpret_cast<float (*)[kBlocks][16][kWave]>(xs_raw);  // [kWaves][kBlocks][16][kWave]
@@ -79,8 +110,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, 
         for (int rb = 0; rb < kBlocks; ++rb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[rb][i] = 0.0f;
-        for (int64_t c0 = 0; c0 < K; c0 += kChunk) {
-            const int64_t ck = K - c0 < kChunk ? K - c0 : kChunk;  // a multiple of 64
+        for (int64_t c0 = k_begin; c0 < k_end; c0 += kChunk) {
+            const int64_t ck = k_end - c0 < kChunk ? k_end - c0 : kChunk;  // a multiple of 64
             // This wave's weight fragments first (steps wave and wave + 8 of
             // the chunk), so that they load under the staging.
             bf16x8 wf[2][4];
@@ -207,9 +238,90 @@ extern "C" int koemi_linear_rows(const void* input0, const void* input1, const v
     const hipStream_t s = as_stream(stream);
     if (input_dtype == KOEMI_F32)
         hipLaunchKernelGGL(linear_rows_kernel<float>, grid, block, 0, s, p, piece_width,
-                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K);
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K);
     else
         hipLaunchKernelGGL(linear_rows_kernel<bf16>, grid, block, 0, s, p, piece_width,
-                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K);
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K);
     return check_launch("koemi_linear_rows");
+}
+
+extern "C" int koemi_linear_rows_split(const void* input0, const void* input1, const void* input2,
+                                       const void* input3, int pieces, int64_t piece_width, int input_dtype,
+                                       const void* weight, const float* bias, float* partials, int64_t rows,
+                                       int64_t out_features, int splits, koemi_stream_t stream) {
+    if (rows < 0 || out_features < 1 || piece_width < 1 || pieces < 1 || pieces > 4 || splits < 1)
+        return fail(KOEMI_ERR_INVALID, "split linear rows needs rows >= 0, 1 to 4 pieces, positive widths and splits");
+    if (input_dtype != KOEMI_F32 && input_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows takes float32 or bfloat16 inputs, not %s",
+                    dtype_name(input_dtype));
+    const int64_t K = piece_width * pieces;
+    const int64_t chunk = input_dtype == KOEMI_F32 ? chunk_of<float>() : chunk_of<bf16>();
+    if (piece_width % kMaxChunk != 0 || K % splits != 0 || (K / splits) % chunk != 0 || splits > 65535)
+        return fail(KOEMI_ERR_UNSUPPORTED,
+                    "split linear rows needs pieces of a multiple of 1024 and K / splits a multiple of %lld",
+                    static_cast<long long>(chunk));
+    if (rows > kMaxRows * 1024 || out_features > 0x7fffffffLL / 2)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows is for a few rows (at most %lld)",
+                    static_cast<long long>(kMaxRows * 1024));
+    if (rows == 0) return KOEMI_OK;
+    const void* in[4] = {input0, input1, input2, input3};
+    const size_t elem = input_dtype == KOEMI_F32 ? 4 : 2;
+    for (int i = 0; i < pieces; ++i)
+        if (!in[i] || reinterpret_cast<uintptr_t>(in[i]) % (8 * elem) != 0)
+            return fail(KOEMI_ERR_INVALID, "linear rows input %d is null or not %zu-byte aligned", i, 8 * elem);
+    if (!weight || reinterpret_cast<uintptr_t>(weight) % 16 != 0 || !partials)
+        return fail(KOEMI_ERR_INVALID, "linear rows needs a 16-byte aligned weight and an output");
+    const Pieces p{{in[0], pieces > 1 ? in[1] : in[0], pieces > 2 ? in[2] : in[0], pieces > 3 ? in[3] : in[0]}};
+    const dim3 grid(static_cast<unsigned>((out_features + kCols - 1) / kCols), static_cast<unsigned>(splits));
+    const hipStream_t s = as_stream(stream);
+    if (input_dtype == KOEMI_F32)
+        hipLaunchKernelGGL(linear_rows_kernel<float>, grid, dim3(kWaves * kWave), 0, s, p, piece_width,
+                           static_cast<const bf16*>(weight), bias, partials, rows, out_features, K, NoBatch{},
+                           K / splits);
+    else
+        hipLaunchKernelGGL(linear_rows_kernel<bf16>, grid, dim3(kWaves * kWave), 0, s, p, piece_width,
+                           static_cast<const bf16*>(weight), bias, partials, rows, out_features, K, NoBatch{},
+                           K / splits);
+    return check_launch("koemi_linear_rows_split");
+}
+
+extern "C" int koemi_linear_rows_batched(const void* const* inputs, int input_dtype, const void* const* weights,
+                                         const float* const* biases, float* output, int count, int64_t rows,
+                                         int64_t in_features, int64_t out_features, koemi_stream_t stream) {
+    if (count < 1 || rows < 0 || out_features < 1 || in_features < 1)
+        return fail(KOEMI_ERR_INVALID, "batched linear rows needs count >= 1, rows >= 0 and positive widths");
+    if (count > kMaxBatch)
+        return fail(KOEMI_ERR_UNSUPPORTED, "batched linear rows takes at most %d projections", kMaxBatch);
+    if (input_dtype != KOEMI_F32 && input_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows takes float32 or bfloat16 inputs, not %s",
+                    dtype_name(input_dtype));
+    if (in_features % 64 != 0)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows needs an input width that is a multiple of 64");
+    if (rows > kMaxRows * 1024 || out_features > 0x7fffffffLL / 2)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows is for a few rows (at most %lld)",
+                    static_cast<long long>(kMaxRows * 1024));
+    if (rows == 0) return KOEMI_OK;
+    if (!inputs || !weights || !output) return fail(KOEMI_ERR_INVALID, "batched linear rows received a null pointer");
+    const size_t elem = input_dtype == KOEMI_F32 ? 4 : 2;
+    RowsBatch b{};
+    for (int e = 0; e < count; ++e) {
+        if (!inputs[e] || reinterpret_cast<uintptr_t>(inputs[e]) % (8 * elem) != 0 || !weights[e] ||
+            reinterpret_cast<uintptr_t>(weights[e]) % 16 != 0)
+            return fail(KOEMI_ERR_INVALID, "batched linear rows: projection %d has a null or unaligned operand", e);
+        b.x[e] = inputs[e];
+        b.w[e] = static_cast<const bf16*>(weights[e]);
+        b.bias[e] = biases != nullptr ? biases[e] : nullptr;
+    }
+    const Pieces none{{nullptr, nullptr, nullptr, nullptr}};
+    const dim3 grid(static_cast<unsigned>((out_features + kCols - 1) / kCols), static_cast<unsigned>(count));
+    const hipStream_t s = as_stream(stream);
+    if (input_dtype == KOEMI_F32)
+        hipLaunchKernelGGL((linear_rows_kernel<float, RowsBatch>), grid, dim3(kWaves * kWave), 0, s, none,
+                           in_features, static_cast<const bf16*>(nullptr), static_cast<const float*>(nullptr), output,
+                           rows, out_features, in_features, b, in_features);
+    else
+        hipLaunchKernelGGL((linear_rows_kernel<bf16, RowsBatch>), grid, dim3(kWaves * kWave), 0, s, none,
+                           in_features, static_cast<const bf16*>(nullptr), static_cast<const float*>(nullptr), output,
+                           rows, out_features, in_features, b, in_features);
+    return check_launch("koemi_linear_rows_batched");
 }

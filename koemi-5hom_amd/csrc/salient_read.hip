@@ -474,27 +474,37 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
             float ek[4], ev[4];
             load4_any(ring.k + b * ring.kstride + d, ek);
             load4_any(ring.v + b * ring.kstride + d, ev);
-#pragma unroll 4
-            for (int s = 0; s < C; ++s) {
-                const int i = slot_src[s];
-                const bool zero = (!ring.tail && !slot_flag[s]) || (i == S && entry_zero);
-                float kq[4], vq[4];
-                if (i < S) {
-                    Vec4<float>::load(ck + (b * S + i) * D + d, kq);
-                    Vec4<float>::load(cv + (b * S + i) * D + d, vq);
-                } else {
+            // sixteen slots at a time: every load in flight before the stores
+            constexpr int kGroup = 16;
+            for (int s0 = 0; s0 < C; s0 += kGroup) {
+                float kq[kGroup][4], vq[kGroup][4];
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        kq[c] = ek[c];
-                        vq[c] = ev[c];
+                for (int u = 0; u < kGroup; ++u) {
+                    const int s = s0 + u;
+                    const int i = s < C ? slot_src[s] : S;
+                    if (i < S) {
+                        Vec4<float>::load(ck + (b * S + i) * D + d, kq[u]);
+                        Vec4<float>::load(cv + (b * S + i) * D + d, vq[u]);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            kq[u][c] = ek[c];
+                            vq[u][c] = ev[c];
+                        }
                     }
                 }
-                if (zero) {
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) kq[c] = vq[c] = 0.0f;
+                for (int u = 0; u < kGroup; ++u) {
+                    const int s = s0 + u;
+                    if (s >= C) break;
+                    const bool zero = (!ring.tail && !slot_flag[s]) || (slot_src[s] == S && entry_zero);
+                    if (zero) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) kq[u][c] = vq[u][c] = 0.0f;
+                    }
+                    Vec4<float>::store(ring.ok + (b * C + s) * D + d, kq[u]);
+                    Vec4<float>::store(ring.ov + (b * C + s) * D + d, vq[u]);
                 }
-                Vec4<float>::store(ring.ok + (b * C + s) * D + d, kq);
-                Vec4<float>::store(ring.ov + (b * C + s) * D + d, vq);
             }
         }
     }

@@ -176,12 +176,22 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows_kernel(
 // it): rows are (b, pos) of a [batch, length] window; row (b, pos) scores the
 // logits of row (b, pos - 1), and for pos == 0 row b of `first` (the carried
 // state's logits). `admission` (null: none) receives valid && s > threshold.
-template <typename T, bool VEC, bool HAS_BIAS, bool FULL, bool SHIFT = false>
+// LAYERED (a decode step's surprise of every layer at once): rows are
+// (layer, b) of [layers, layer_rows]; row (l, b) takes the targets and
+// validity of b and the content bias of layer l (layer_bias.p[l]).
+constexpr int kMaxLayers = 32;
+template <typename T>
+struct LayerBias {
+    const T* p[kMaxLayers];
+};
+
+template <typename T, bool VEC, bool HAS_BIAS, bool FULL, bool SHIFT = false, bool LAYERED = false>
 __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
     const float* __restrict__ logits, const T* __restrict__ bias,
     const int64_t* __restrict__ targets, const uint8_t* __restrict__ valid, T* __restrict__ out,
     int64_t rows, int64_t v_runtime, float log_vocab, const float* __restrict__ first = nullptr,
-    int64_t length = 1, uint8_t* __restrict__ admission = nullptr, float threshold = 0.0f) {
+    int64_t length = 1, uint8_t* __restrict__ admission = nullptr, float threshold = 0.0f,
+    LayerBias<T> layer_bias = {}, int64_t layer_rows = 1) {
 #pragma clang fp contract(off)
     const int64_t V = FULL ? 256 : v_runtime;
     const int lane = lane_id();
@@ -189,8 +199,10 @@ __global__ __launch_bounds__(kWave * kRowWaves) void surprise_rows16_kernel(
     const int64_t row = (static_cast<int64_t>(blockIdx.x) * kRowWaves + threadIdx.x / kWave) * 4 + (lane >> 4);
     if ((row & ~int64_t(3)) >= rows) return;  // whole wave past the end
     const int64_t rr = row < rows ? row : rows - 1;
-    const bool live = valid[rr] != 0;
-    const int64_t t = targets[rr];
+    const int64_t tr = LAYERED ? rr % layer_rows : rr;  // the row of targets and valid
+    if constexpr (LAYERED) bias = layer_bias.p[rr / layer_rows];
+    const bool live = valid[tr] != 0;
+    const int64_t t = targets[tr];
     const float* z = logits + rr * V;
     if constexpr (SHIFT) {
         const int64_t pos = rr % length;
@@ -1072,7 +1084,8 @@ int launch_rows(const float* logits, const void* bias, const int64_t* targets, c
         const dim3 grid(grid_for(rows, kRowWaves * 4));
         auto launch16 = [&](auto kernel) {
             hipLaunchKernelGGL(kernel, grid, block, 0, stream, logits, b, targets, valid, o, rows, V, log_vocab,
-                               static_cast<const float*>(nullptr), int64_t(1), static_cast<uint8_t*>(nullptr), 0.0f);
+                               static_cast<const float*>(nullptr), int64_t(1), static_cast<uint8_t*>(nullptr), 0.0f,
+                               LayerBias<T>{}, int64_t(1));
         };
         if (vec && V == 256) {
             if (b) launch16(surprise_rows16_kernel<T, true, true, true>);
@@ -1131,11 +1144,38 @@ extern "C" int koemi_herm_surprise_shifted(const float* logits, const float* fir
     const dim3 grid(grid_for(rows, kRowWaves * 4));
     auto launch = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, dim3(kWave * kRowWaves), 0, as_stream(stream), logits, bias, target_ids,
-                           valid_mask, surprise, rows, vocab, log_vocab, first, length, admission, threshold);
+                           valid_mask, surprise, rows, vocab, log_vocab, first, length, admission, threshold,
+                           LayerBias<float>{}, int64_t(1));
     };
     if (bias) launch(surprise_rows16_kernel<float, true, true, true, true>);
     else launch(surprise_rows16_kernel<float, true, false, true, true>);
     return check_launch("koemi_herm_surprise_shifted");
+}
+
+extern "C" int koemi_herm_surprise_layers(const float* logits, const float* const* biases,
+                                          const int64_t* target_ids, const uint8_t* valid_mask, float* surprise,
+                                          uint8_t* admission, float threshold, int layers, int64_t batch,
+                                          int64_t vocab, float log_vocab, koemi_stream_t stream) {
+    if (batch < 0 || layers < 1 || vocab < 1)
+        return fail(KOEMI_ERR_INVALID, "layered surprise needs batch >= 0, layers and vocab >= 1");
+    if (vocab != 256) return fail(KOEMI_ERR_UNSUPPORTED, "layered surprise supports a content vocabulary of 256");
+    if (layers > kMaxLayers) return fail(KOEMI_ERR_UNSUPPORTED, "layered surprise takes at most %d layers", kMaxLayers);
+    if (batch == 0) return KOEMI_OK;
+    if (!logits || !biases || !target_ids || !valid_mask || !surprise)
+        return fail(KOEMI_ERR_INVALID, "layered surprise received a null pointer");
+    if (reinterpret_cast<uintptr_t>(logits) % 16 != 0)
+        return fail(KOEMI_ERR_INVALID, "layered surprise needs 16-byte aligned logits");
+    LayerBias<float> lb{};
+    for (int l = 0; l < layers; ++l) {
+        if (!biases[l]) return fail(KOEMI_ERR_INVALID, "layered surprise: bias %d is null", l);
+        lb.p[l] = biases[l];
+    }
+    const int64_t rows = batch * layers;
+    const dim3 grid(grid_for(rows, kRowWaves * 4));
+    hipLaunchKernelGGL((surprise_rows16_kernel<float, true, true, true, true, true>), grid, dim3(kWave * kRowWaves), 0,
+                       as_stream(stream), logits, nullptr, target_ids, valid_mask, surprise, rows, vocab, log_vocab,
+                       logits, int64_t{1}, admission, threshold, lb, batch);
+    return check_launch("koemi_herm_surprise_layers");
 }
 
 extern "C" int koemi_surprise_rows_backward(const float* logits, const void* bias,

@@ -112,6 +112,14 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, _P),
     ),
+    "koemi_linear_rows_split": (
+        c_int,
+        (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, c_int, _P),
+    ),
+    "koemi_linear_rows_batched": (
+        c_int,
+        (_P, c_int, _P, _P, _P, c_int, c_int64, c_int64, c_int64, _P),
+    ),
     "koemi_salient_read_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64, c_int)),
     "koemi_salient_read": (
         c_int,
@@ -137,7 +145,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_herm_surprise_shifted": (
         c_int, (_P, _P, _P, _P, _P, _P, _P, c_float, c_int64, c_int64, c_int64, c_float, _P),
     ),
+    "koemi_herm_surprise_layers": (
+        c_int, (_P, _P, _P, _P, _P, _P, c_float, c_int, c_int64, c_int64, c_float, _P),
+    ),
     "koemi_herm_rmsnorm": (c_int, (_P, c_int, _P, c_int, _P, _P, _P, _P, c_int64, c_int64, c_float, _P)),
+    "koemi_herm_rmsnorm_parts": (c_int, (_P, c_int, _P, c_int, _P, _P, _P, c_int64, c_int64, c_float, _P)),
     "koemi_herm_concat_bf16": (c_int, (_P, _P, _P, _P, c_int, c_int64, c_int64, _P, _P)),
     "koemi_read_step_pair": (
         c_int,
@@ -249,6 +261,13 @@ def stream_of(device: torch.device) -> int:
     """Raw hipStream_t of torch's current stream on `device`."""
 
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr_array(tensors: list[torch.Tensor | None]) -> ctypes.Array:
+    """A host array of device addresses (None for absent entries), for the
+    entry points that take one pointer per layer."""
+
+    return (c_void_p * len(tensors))(*(ptr(t) for t in tensors))
 
 
 def call(name: str, *args: Any) -> None:

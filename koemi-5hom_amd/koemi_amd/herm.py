@@ -195,6 +195,7 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
         if lin == torch.bfloat16:
             # the biases of GEMMs with bf16 results (nn.Linear under bf16 autocast)
             q["gates_b16"], q["ws_b16"], q["fusion_b16"] = (q[k].to(lin) for k in ("gates_b", "ws_b", "fusion_b"))
+            q["fusion_b16f"] = q["fusion_b16"].float()  # the bf16 bias as the split fusion layer adds it
         q["fusion_norm"], q["expert_norm"] = to(p["fusion_norm"]), to(p["expert_norm"])
         for name in ("gate", "up", "down"):
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
@@ -441,6 +442,46 @@ def _input_norm(p: dict[str, Tensor], ids: Tensor, context, low) -> Tensor:
     return _rms(source, p["input_norm"]) if low is None else _rms(source, p["input_norm"], fp32=False, low=low)[1]
 
 
+_FUSION_SPLITS = 8  # K = 4 x 1024 fp32 inputs in 512-wide chunks: 8 x 32 workgroups
+
+
+def _fusion_split_fits(p: dict[str, Tensor], pieces: tuple[Tensor, ...], d: int) -> bool:
+    """Whether the fusion layer of a bf16 stack runs as a split-K projection
+    of its four fp32 pieces (a decode step's few rows)."""
+
+    w = p["fusion_w"]
+    rows = pieces[0].numel() // d
+    return (w.dtype == torch.bfloat16 and "fusion_b16" in p and len(pieces) == 4 and d % 1024 == 0
+            and w.shape == (d, 4 * d) and rows <= linear.MAX_ROWS
+            and all(t.dtype == torch.float32 and t.is_contiguous() and t.numel() == rows * d for t in pieces))
+
+
+def _fusion_split(p: dict[str, Tensor], pieces: tuple[Tensor, ...], d: int) -> tuple[Tensor, Tensor]:
+    """The fusion layer and its normalizer (network.py:401-405, 723-732) for a
+    few rows: the four fp32 pieces [working ; memory ; local ; salient] are
+    the K blocks of a split-K projection (no concatenation, the rows rounded
+    to bf16 as staged), whose partial sums the norm kernel adds with the bf16
+    bias and rounds to the bf16 result before normalizing. Returns (fp32,
+    bf16) normalized rows in the pieces' shape."""
+
+    shape = pieces[0].shape
+    rows = pieces[0].numel() // d
+    device = pieces[0].device
+    partials = torch.empty((_FUSION_SPLITS, rows, d), device=device, dtype=torch.float32)
+    stream = _native.stream_of(device)
+    _native.call("koemi_linear_rows_split", *(_native.ptr(t) for t in pieces), 4, d,
+                 _native.dtype_code(torch.float32), _native.ptr(p["fusion_w"]), None, _native.ptr(partials), rows, d,
+                 _FUSION_SPLITS, stream)
+    bias = p.get("fusion_b16f")
+    if bias is None:
+        bias = p["fusion_b16"].float()
+    out = torch.empty(shape, device=device, dtype=torch.float32)
+    out16 = torch.empty(shape, device=device, dtype=torch.bfloat16)
+    _native.call("koemi_herm_rmsnorm_parts", _native.ptr(partials), _FUSION_SPLITS, _native.ptr(bias), 1,
+                 _native.ptr(p["fusion_norm"]), _native.ptr(out), _native.ptr(out16), rows, d, _EPS, stream)
+    return out, out16
+
+
 def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, previous: Tensor, valid: Tensor,
                       pieces: tuple[Tensor, Tensor, Tensor, Tensor] | Tensor, with_logits: bool,
                       next_norm: Tensor | None = None, routing: dict | None = None
@@ -464,16 +505,19 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     d = settings.width
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
-    if isinstance(pieces, Tensor):
-        fusion_in = pieces
-    elif low is None:
-        fusion_in = torch.cat(pieces, dim=-1)
+    if not isinstance(pieces, Tensor) and _fusion_split_fits(p, pieces, d):
+        fused, fused_low = _fusion_split(p, pieces, d)
     else:
-        fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
-        _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4, batch * length, d,
-                     _native.ptr(fusion_in), _native.stream_of(ids.device))
-    fused_pair = _rms(_projection(fusion_in, p, "fusion"), p["fusion_norm"], low=low)
-    fused, fused_low = fused_pair if low is not None else (fused_pair, None)
+        if isinstance(pieces, Tensor):
+            fusion_in = pieces
+        elif low is None:
+            fusion_in = torch.cat(pieces, dim=-1)
+        else:
+            fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
+            _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4,
+                         batch * length, d, _native.ptr(fusion_in), _native.stream_of(ids.device))
+        fused_pair = _rms(_projection(fusion_in, p, "fusion"), p["fusion_norm"], low=low)
+        fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
     k = settings.top_k
     flat = fused.reshape(-1, d)
@@ -542,7 +586,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                  context: Tensor | NextInput | None = None, *, with_logits: bool = True,
                  token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
                  next_norm: Tensor | None = None, out_state: dict[str, Tensor] | None = None,
-                 routing: dict | None = None
+                 routing: dict | None = None, surprise_in: tuple[Tensor, Tensor] | None = None
                  ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One forward_window of one block (network.py:296-441). ``ids`` ``[B, L]``
     int64 on the device; ``context`` the previous layer's final context (None
@@ -557,7 +601,9 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     a state dict whose buffers receive the next state (a decode graph's other
     static state; ``last_token`` is the caller's, from the token context).
     ``routing``: shared by the layers of a stack pass (see
-    ``_fuse_mix_predict``)."""
+    ``_fuse_mix_predict``). ``surprise_in``: this layer's (surprise,
+    admission) [B, 1] when the caller formed them (a decode step's stack, all
+    layers at once: they depend on the carried states alone)."""
 
     ids = ids.contiguous()
     batch, length = ids.shape
@@ -576,7 +622,10 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d),
                           states_out=states_out)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
+    if surprise_in is not None and length == 1:
+        surprise, admission = surprise_in
+    else:
+        surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
 
     projected = _projection(ws_low, p, "ws")
     # local keys and values: the first two column blocks, read in place (the
@@ -766,6 +815,42 @@ def _surprise_carried(p: dict[str, Tensor], settings: HermSettings, carried: Ten
                  float(settings.salience_threshold), batch, 1, vocab, think._log_vocab(vocab),
                  _native.stream_of(carried.device))
     return surprise, admission
+
+
+def _surprise_layers(params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
+                     targets: Tensor, valid: Tensor) -> list[tuple[Tensor, Tensor]] | None:
+    """A decode step's surprise and admission in every layer at once: each
+    depends only on the layer's carried working state (``_surprise_carried``),
+    so the content heads of all layers run as one batched projection
+    (``koemi_linear_rows_batched``) and the scoring as one kernel
+    (``koemi_herm_surprise_layers``). None when the stack does not fit them
+    (fp32 heads, another vocabulary, more than 32 layers)."""
+
+    layers = len(params)
+    w16 = [p.get("content_w16") for p in params]
+    carried = [st["working"] for st in states]
+    if layers > 32 or any(w is None for w in w16) or targets.shape[1] != 1:
+        return None
+    batch, d = carried[0].shape
+    vocab = w16[0].shape[0]
+    if (vocab != 256 or d % 64 or batch > linear.MAX_ROWS
+            or any(w.shape != (vocab, d) or not w.is_contiguous() for w in w16)
+            or any(c.shape != (batch, d) or c.dtype != torch.float32 or not c.is_contiguous() for c in carried)):
+        return None
+    biases = [p["content_b"] for p in params]
+    if any(b.shape != (vocab,) or b.dtype != torch.float32 or not b.is_contiguous() for b in biases):
+        return None
+    device = carried[0].device
+    logits = torch.empty((layers, batch, vocab), device=device, dtype=torch.float32)
+    stream = _native.stream_of(device)
+    _native.call("koemi_linear_rows_batched", _native.ptr_array(carried), _native.dtype_code(torch.float32),
+                 _native.ptr_array(w16), None, _native.ptr(logits), layers, batch, d, vocab, stream)
+    surprise = torch.empty((layers, batch, 1), device=device, dtype=torch.float32)
+    admission = torch.empty((layers, batch, 1), device=device, dtype=torch.bool)
+    _native.call("koemi_herm_surprise_layers", _native.ptr(logits), _native.ptr_array(biases),
+                 _native.ptr(targets), _native.ptr(valid), _native.ptr(surprise), _native.ptr(admission),
+                 float(settings.salience_threshold), layers, batch, vocab, think._log_vocab(vocab), stream)
+    return [(surprise[layer], admission[layer]) for layer in range(layers)]
 
 
 def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws_low: Tensor, carried: Tensor,
@@ -971,13 +1056,15 @@ def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: 
     next_states = []
     logits = None
     routing: dict = {}  # the hash route, formed by the first layer for all of them
+    surprises = _surprise_layers(params, settings, states, token_context[3], token_context[2])
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
         logits, context, next_state, _ = block_window(p, settings, ids, state, context, with_logits=last,
                                                       token_context=token_context,
                                                       next_norm=None if last else params[layer + 1]["input_norm"],
                                                       out_state=out_states[layer] if out_states is not None else None,
-                                                      routing=routing)
+                                                      routing=routing,
+                                                      surprise_in=surprises[layer] if surprises else None)
         next_states.append(next_state)
     return logits, next_states
 

@@ -149,6 +149,27 @@ def test_decode_graph_replays_match_eager_steps(device):
                     assert torch.equal(g[key], tensor), f"step {step} layer {layer} {key}"
 
 
+def test_decode_surprise_of_all_layers_equals_the_per_layer_surprise(device):
+    """A decode step's surprise and admission of every layer, formed at once
+    (one batched content-head launch, one scoring launch), equal the
+    per-layer path (koemi_linear_rows + koemi_herm_surprise_shifted) bit for
+    bit: the same arithmetic per row."""
+
+    b = 5
+    settings = _settings(width=64, layers=3, linear_dtype=torch.bfloat16, salience_threshold=0.5)
+    params = herm.prepare_stack(_params(settings, seed=21), settings, device)
+    gen = torch.Generator().manual_seed(5)
+    states = [{"working": torch.randn((b, 64), generator=gen).to(device)} for _ in range(3)]
+    targets = torch.tensor([[3], [250], [0], [77], [128]], device=device)
+    valid = torch.tensor([[True], [True], [False], [True], [True]], device=device)
+    got = herm._surprise_layers(params, settings, states, targets, valid)
+    assert got is not None
+    for p, st, (s_got, a_got) in zip(params, states, got):
+        s_want, a_want = herm._surprise_carried(p, settings, st["working"], targets, valid)
+        assert torch.equal(s_got, s_want) and torch.equal(a_got, a_want)
+    assert bool(valid.logical_not().logical_or(got[0][0] > 0).all())
+
+
 def test_bf16_projections_stay_close_to_fp32(device):
     b = 2
     base = _settings(width=64, salience_threshold=2.0)  # admission off: no discrete flips

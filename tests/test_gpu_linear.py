@@ -53,3 +53,62 @@ def test_linear_rows_rejects_bad_inputs(device):
     with pytest.raises(dense.DenseCudaValidationError, match="float32"):
         linear.linear_rows([x], w, torch.zeros(8, device=device, dtype=torch.float64))
     assert linear.linear_rows([x[:0]], w, None).shape == (0, 8)
+
+
+@pytest.mark.parametrize("rows, splits, dtype", [(64, 8, torch.float32), (37, 4, torch.float32),
+                                                  (16, 4, torch.bfloat16)])
+def test_split_linear_rows_partials_sum_to_the_projection(device, rows, splits, dtype):
+    """koemi_linear_rows_split: the partial blocks, added in order, equal the
+    float64 product of the bf16-rounded operands (the tolerance above), the
+    bias in block 0 only; each block alone is the product over its K range."""
+
+    from koemi_amd import _native
+
+    width, pieces, n_out = 1024, 4, 1024
+    g = torch.Generator().manual_seed(rows + splits)
+    xs = [torch.randn((rows, width), generator=g).to(dtype).to(device) for _ in range(pieces)]
+    w = (torch.randn((n_out, width * pieces), generator=g) * (width * pieces) ** -0.5).to(torch.bfloat16).to(device)
+    b = torch.randn((n_out,), generator=g).to(device)
+    partials = torch.empty((splits, rows, n_out), device=device)
+    _native.call("koemi_linear_rows_split", *(_native.ptr(x) for x in xs), pieces, width, _native.dtype_code(dtype),
+                 _native.ptr(w), _native.ptr(b), _native.ptr(partials), rows, n_out, splits,
+                 _native.stream_of(partials.device))
+    x64 = torch.cat([x.to(torch.bfloat16).double() for x in xs], dim=-1).cpu()
+    w64 = w.double().cpu()
+    k = width * pieces // splits
+    for s in range(splits):
+        want = x64[:, s * k:(s + 1) * k] @ w64[:, s * k:(s + 1) * k].T + (b.double().cpu() if s == 0 else 0.0)
+        err = (partials[s].double().cpu() - want).abs().max().item()
+        assert err <= 1e-5 * want.abs().max().item() + 1e-6, f"block {s}"
+    total = partials.double().sum(0).cpu()
+    want = x64 @ w64.T + b.double().cpu()
+    assert (total - want).abs().max().item() <= 1e-5 * want.abs().max().item() + 1e-6
+
+
+def test_split_fusion_and_norm_match_the_concatenated_projection(device):
+    """The decode-step fusion layer as a split projection of its four fp32
+    pieces plus the parts-summing norm (bf16 bias, bf16 rounding of the
+    result) against float64: the projection of the bf16-rounded pieces plus
+    the bf16 bias, rounded to bf16 (the autocast result), then the RMS norm.
+    A rounding boundary may fall either way in fp32 accumulation, so an
+    element may differ by one bf16 step of the pre-norm value (2^-8
+    relative) and the norm by as much; the fp32 and bf16 outputs agree."""
+
+    from koemi_amd import herm
+
+    rows, d = 64, 1024
+    g = torch.Generator().manual_seed(9)
+    pieces = tuple(torch.randn((rows, 1, d), generator=g).to(device) for _ in range(4))
+    p = {"fusion_w": (torch.randn((d, 4 * d), generator=g) * (4 * d) ** -0.5).to(torch.bfloat16).to(device),
+         "fusion_b16": torch.randn((d,), generator=g).to(torch.bfloat16).to(device),
+         "fusion_norm": (1.0 + 0.1 * torch.randn((d,), generator=g)).to(device)}
+    assert herm._fusion_split_fits(p, pieces, d)
+    out, out16 = herm._fusion_split(p, pieces, d)
+    x64 = torch.cat([t.to(torch.bfloat16).double().cpu() for t in pieces], dim=-1).reshape(rows, 4 * d)
+    y = (x64 @ p["fusion_w"].double().cpu().T + p["fusion_b16"].double().cpu()).to(torch.bfloat16).double()
+    want = y * torch.rsqrt((y * y).mean(-1, keepdim=True) + herm._EPS) * p["fusion_norm"].double().cpu()
+    got = out.reshape(rows, d).double().cpu()
+    err = (got - want).abs()
+    assert (err <= 2.0**-7 * want.abs() + 1e-5).all(), err.max().item()
+    assert (err > 1e-5 + 1e-6 * want.abs()).float().mean().item() < 0.01  # rounding flips are rare
+    assert torch.equal(out16, out.to(torch.bfloat16))
