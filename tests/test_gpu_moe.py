@@ -216,6 +216,7 @@ def test_grouped_mlp_bf16_mfma_ragged_segments(device, sizes):
     ((0, 5, 70, 0, 57), 256, 384),          # empty experts, a 70-row expert (two passes), a partial second block
     ((33, 1, 64, 65), 128, 192),            # 33 rows (one row in the second block), exactly 64, 65
     ((8, 9, 7, 8, 8, 6, 10, 8, 8, 8, 9, 7, 8, 8, 8, 10), 1024, 2048),  # a C5 decode step: 64 tokens x top-2
+    ((0, 40, 70, 0, 3, 100, 0, 1), 1024, 2048),  # C5 widths: empty experts, two to four 32-row passes
 ])
 def test_grouped_mlp_bf16_few_rows_per_expert(device, sizes, D, H):
     """At most 64 pairs per expert on average: the skinny kernels (weights
