@@ -440,6 +440,22 @@ int koemi_linear_rows(const void* input0, const void* input1, const void* input2
                       int64_t piece_width, int input_dtype, const void* weight, const float* bias, float* output,
                       int64_t rows, int64_t out_features, koemi_stream_t stream);
 
+/* A decode step's gate projections with the gates and the one-position scan
+ * in the epilogue (memory.py:14-30, network.py:306-310; nn.Linear then
+ * BoundedRecurrentState.gates and one scan step in the reference):
+ * weight [2 width, in_features] bf16 stacks the retention rows over the
+ * candidate rows (no GEMM bias); with zr, zc the two products of row r's
+ * input (rounded to bf16, as koemi_linear_rows), states[r, f] = a
+ * initial[r, f] + b where (a, b) are the gates of zr + retention_bias[f] and
+ * zc + candidate_bias[f] (biases fp32 or NULL), a = 1, b = 0 where
+ * valid[r] == 0 (valid NULL: all valid); states_bf16 (NULL: none) receives
+ * the bf16 copy, rows bf16_row_stride apart. Equal to koemi_linear_rows then
+ * koemi_gated_scan at length 1. in_features % 64 == 0. */
+int koemi_linear_rows_gated(const void* input, int input_dtype, const void* weight, const float* retention_bias,
+                            const float* candidate_bias, const uint8_t* valid, const float* initial, float* states,
+                            void* states_bf16, int64_t bf16_row_stride, int64_t rows, int64_t width,
+                            int64_t in_features, koemi_stream_t stream);
+
 /* koemi_linear_rows with K split over `splits` workgroup columns (a decode
  * step's 4096-wide fusion layer, network.py:401-405, spread over the chip):
  * block s of `partials` ([splits, rows, out_features] fp32) = the products

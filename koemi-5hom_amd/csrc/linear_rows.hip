@@ -67,16 +67,38 @@ struct RowsBatch {
 };
 struct NoBatch {};
 
+// The gate projections of a decode step with the gates and the one-position
+// scan in the epilogue (memory.py:14-30 with network.py:306-310): weight
+// rows [0, F) are the retention projection, [F, 2F) the candidate one; a
+// workgroup takes features [16 x, 16 x + 16) as its 32 MFMA columns (16
+// retention rows, then the 16 matching candidate rows), and the thread of
+// feature f finishes it: h = a h0 + b with (a, b) = gate_pair of the two
+// sums (no GEMM bias; the gate biases and the validity inside gate_pair),
+// as koemi_gated_scan does at one position.
+struct NoGates {};
+struct GatedStep {
+    const float* retention_bias;  // [F] or null
+    const float* candidate_bias;  // [F] or null
+    const uint8_t* valid;         // [rows] or null
+    const float* h0;              // [rows, F]
+    float* h;                     // [rows, F]
+    bf16* h16;                    // bf16 copy of h, rows h16_stride apart, or null
+    int64_t h16_stride;
+    int64_t F;
+};
+
 // Split K (k_len < K, no RowsBatch): blockIdx.y = split s takes K values
 // [s k_len, (s + 1) k_len) and writes its partial sums to block s of y
 // ([M, N] blocks one after another), the bias added by split 0 only; the
 // consumer adds the blocks in split order.
-template <typename XT, typename Batch = NoBatch>
+template <typename XT, typename Batch = NoBatch, typename Gates = NoGates>
 __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, int64_t piece_width,
                                                                      const bf16* __restrict__ w,
                                                                      const float* __restrict__ bias,
                                                                      float* __restrict__ y, int64_t M, int64_t N,
-                                                                     int64_t K, Batch batch, int64_t k_len) {
+                                                                     int64_t K, Batch batch, int64_t k_len,
+                                                                     Gates gates = Gates{}) {
+    constexpr bool kGated = std::is_same<Gates, GatedStep>::value;
     int64_t k_begin = 0, k_end = K;
     if constexpr (std::is_same<Batch, RowsBatch>::value) {
         const int e = blockIdx.y;
@@ -98,10 +120,36 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, 
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kCols;
     const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const int r = lane % 32, half = lane / 32;
-    const int64_t wn = n0 + r < N ? n0 + r : N - 1;  // rows past N are loaded from the last row, never stored
+    int64_t wn = n0 + r < N ? n0 + r : N - 1;  // rows past N are loaded from the last row, never stored
+    if constexpr (kGated) {
+        const int64_t f = static_cast<int64_t>(blockIdx.x) * 16 + r % 16;
+        wn = (r < 16 ? 0 : gates.F) + (f < gates.F ? f : gates.F - 1);
+    }
     const bf16* wr = w + wn * K + 32 * half;
     constexpr int kVec = 16 / sizeof(XT);  // input elements per 16-byte load
     constexpr int kChunk = chunk_of<XT>();
+    // gated epilogue: this thread's carried states, validity and biases,
+    // loaded before the partial sums go through LDS (their latency hides
+    // under the exchange)
+    constexpr int kEpi = kBlocks * 16 / kWaves;  // epilogue entries per thread
+    float pre_h0[kEpi], pre_br = 0.0f, pre_bc = 0.0f;
+    bool pre_keep[kEpi];
+    auto preload = [&](int64_t pass) {
+        if constexpr (kGated) {
+            const int64_t f = static_cast<int64_t>(blockIdx.x) * 16 + lane % 32;
+            const int64_t fc = f < gates.F ? f : gates.F - 1;
+            pre_br = gates.retention_bias ? gates.retention_bias[fc] : 0.0f;
+            pre_bc = gates.candidate_bias ? gates.candidate_bias[fc] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < kEpi; ++q) {
+                const int idx = q * kWaves + wave;
+                const int64_t row = (idx / 16) * 32 + 8 * ((idx % 16) / 4) + 4 * (lane / 32) + (idx % 16) % 4;
+                const int64_t br = pass + row < M ? pass + row : M - 1;
+                pre_h0[q] = gates.h0[br * gates.F + fc];
+                pre_keep[q] = gates.valid == nullptr || gates.valid[br] != 0;
+            }
+        }
+    };
     for (int64_t pass = 0; pass < M; pass += kBlocks * 32) {
         const int64_t rows = M - pass < kBlocks * 32 ? M - pass : kBlocks * 32;
         const int blocks = rows > 32 ? 2 : 1;
@@ -181,6 +229,7 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, 
             }
             __syncthreads();  // the staging area is rewritten by the next chunk (or holds the sums)
         }
+        preload(pass);
 #pragma unroll
         for (int rb = 0; rb < kBlocks; ++rb)
 #pragma unroll
@@ -193,6 +242,24 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_rows_kernel(Pieces in, 
             const int idx = q * kWaves + wave;  // (block, entry), wave-uniform
             const int rb = idx / 16, i = idx % 16;
             const int64_t row = rb * 32 + 8 * (i / 4) + 4 * (lane / 32) + i % 4;
+            if constexpr (kGated) {
+                // lane c < 16 (of its half) holds retention feature 16 x + c, lane c + 16 its candidate
+                const int64_t f = static_cast<int64_t>(blockIdx.x) * 16 + lane % 32;
+                if (rb >= blocks || row >= rows || lane % 32 >= 16 || f >= gates.F) continue;
+                float zr = 0.0f, zc = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < kWaves; ++w2) {
+                    zr += red[w2][rb][i][lane];
+                    zc += red[w2][rb][i][lane + 16];
+                }
+                const int64_t br = pass + row;
+                float a, b;
+                gate_pair(zr, zc, pre_br, pre_bc, pre_keep[q], a, b);
+                const float hv = a * pre_h0[q] + b;
+                gates.h[br * gates.F + f] = hv;
+                if (gates.h16 != nullptr) gates.h16[br * gates.h16_stride + f] = static_cast<__bf16>(hv);
+                continue;
+            }
             const int64_t col = n0 + lane % 32;
             if (rb >= blocks || row >= rows || col >= N) continue;
             float v = bias != nullptr ? bias[col] : 0.0f;
@@ -238,11 +305,50 @@ extern "C" int koemi_linear_rows(const void* input0, const void* input1, const v
     const hipStream_t s = as_stream(stream);
     if (input_dtype == KOEMI_F32)
         hipLaunchKernelGGL(linear_rows_kernel<float>, grid, block, 0, s, p, piece_width,
-                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K);
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K, NoGates{});
     else
         hipLaunchKernelGGL(linear_rows_kernel<bf16>, grid, block, 0, s, p, piece_width,
-                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K);
+                           static_cast<const bf16*>(weight), bias, output, rows, out_features, K, NoBatch{}, K, NoGates{});
     return check_launch("koemi_linear_rows");
+}
+
+extern "C" int koemi_linear_rows_gated(const void* input, int input_dtype, const void* weight,
+                                       const float* retention_bias, const float* candidate_bias,
+                                       const uint8_t* valid, const float* initial, float* states, void* states_bf16,
+                                       int64_t bf16_row_stride, int64_t rows, int64_t width, int64_t in_features,
+                                       koemi_stream_t stream) {
+    if (rows < 0 || width < 1 || in_features < 1)
+        return fail(KOEMI_ERR_INVALID, "gated linear rows needs rows >= 0 and positive widths");
+    if (input_dtype != KOEMI_F32 && input_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows takes float32 or bfloat16 inputs, not %s",
+                    dtype_name(input_dtype));
+    if (in_features % 64 != 0)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows needs an input width that is a multiple of 64");
+    if (rows > kMaxRows * 1024 || width > 0x7fffffffLL / 32)
+        return fail(KOEMI_ERR_UNSUPPORTED, "linear rows is for a few rows (at most %lld)",
+                    static_cast<long long>(kMaxRows * 1024));
+    if (states_bf16 != nullptr && bf16_row_stride < width)
+        return fail(KOEMI_ERR_INVALID, "gated linear rows: the bf16 row stride is below the width");
+    if (rows == 0) return KOEMI_OK;
+    const size_t elem = input_dtype == KOEMI_F32 ? 4 : 2;
+    if (!input || reinterpret_cast<uintptr_t>(input) % (8 * elem) != 0 || !weight ||
+        reinterpret_cast<uintptr_t>(weight) % 16 != 0 || !initial || !states)
+        return fail(KOEMI_ERR_INVALID, "gated linear rows received a null or unaligned pointer");
+    const Pieces p{{input, input, input, input}};
+    const GatedStep g{retention_bias, candidate_bias, valid, initial, states, static_cast<bf16*>(states_bf16),
+                      bf16_row_stride, width};
+    const dim3 grid(static_cast<unsigned>((width + 15) / 16));
+    const hipStream_t s = as_stream(stream);
+    const float* none = nullptr;
+    if (input_dtype == KOEMI_F32)
+        hipLaunchKernelGGL((linear_rows_kernel<float, NoBatch, GatedStep>), grid, dim3(kWaves * kWave), 0, s, p,
+                           in_features, static_cast<const bf16*>(weight), none, states, rows, 2 * width,
+                           in_features, NoBatch{}, in_features, g);
+    else
+        hipLaunchKernelGGL((linear_rows_kernel<bf16, NoBatch, GatedStep>), grid, dim3(kWaves * kWave), 0, s, p,
+                           in_features, static_cast<const bf16*>(weight), none, states, rows, 2 * width,
+                           in_features, NoBatch{}, in_features, g);
+    return check_launch("koemi_linear_rows_gated");
 }
 
 extern "C" int koemi_linear_rows_split(const void* input0, const void* input1, const void* input2,
@@ -277,11 +383,11 @@ extern "C" int koemi_linear_rows_split(const void* input0, const void* input1, c
     if (input_dtype == KOEMI_F32)
         hipLaunchKernelGGL(linear_rows_kernel<float>, grid, dim3(kWaves * kWave), 0, s, p, piece_width,
                            static_cast<const bf16*>(weight), bias, partials, rows, out_features, K, NoBatch{},
-                           K / splits);
+                           K / splits, NoGates{});
     else
         hipLaunchKernelGGL(linear_rows_kernel<bf16>, grid, dim3(kWaves * kWave), 0, s, p, piece_width,
                            static_cast<const bf16*>(weight), bias, partials, rows, out_features, K, NoBatch{},
-                           K / splits);
+                           K / splits, NoGates{});
     return check_launch("koemi_linear_rows_split");
 }
 
@@ -318,10 +424,10 @@ extern "C" int koemi_linear_rows_batched(const void* const* inputs, int input_dt
     if (input_dtype == KOEMI_F32)
         hipLaunchKernelGGL((linear_rows_kernel<float, RowsBatch>), grid, dim3(kWaves * kWave), 0, s, none,
                            in_features, static_cast<const bf16*>(nullptr), static_cast<const float*>(nullptr), output,
-                           rows, out_features, in_features, b, in_features);
+                           rows, out_features, in_features, b, in_features, NoGates{});
     else
         hipLaunchKernelGGL((linear_rows_kernel<bf16, RowsBatch>), grid, dim3(kWaves * kWave), 0, s, none,
                            in_features, static_cast<const bf16*>(nullptr), static_cast<const float*>(nullptr), output,
-                           rows, out_features, in_features, b, in_features);
+                           rows, out_features, in_features, b, in_features, NoGates{});
     return check_launch("koemi_linear_rows_batched");
 }

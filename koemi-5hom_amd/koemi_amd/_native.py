@@ -112,6 +112,10 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, _P),
     ),
+    "koemi_linear_rows_gated": (
+        c_int,
+        (_P, c_int, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P),
+    ),
     "koemi_linear_rows_split": (
         c_int,
         (_P, _P, _P, _P, c_int, c_int64, c_int, _P, _P, _P, c_int64, c_int64, c_int, _P),

@@ -304,6 +304,22 @@ def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor,
     if _fused_gates(p, u):
         return recurrent.gated_projection_scan(u, w, p["gates_b16"], valid, working, with_bf16=with_bf16,
                                                out_bf16=out_bf16, final_out=final_out)
+    if u.shape[1] == 1 and w.dtype == torch.bfloat16 and _few_rows(u, w) and w.shape == (2 * width, u.shape[-1]):
+        # a decode step: the gates and the one-position scan in the projection's epilogue
+        batch = u.shape[0]
+        states = states_out if states_out is not None else torch.empty((batch, 1, width), device=u.device,
+                                                                        dtype=torch.float32)
+        states16 = None
+        if with_bf16:
+            states16 = out_bf16 if out_bf16 is not None else torch.empty((batch, 1, width), device=u.device,
+                                                                         dtype=torch.bfloat16)
+        x = u.contiguous()
+        _native.call("koemi_linear_rows_gated", _native.ptr(x), _native.dtype_code(x.dtype), _native.ptr(w),
+                     _native.ptr(p["gates_b"][:width]), _native.ptr(p["gates_b"][width:]), _native.ptr(valid),
+                     _native.ptr(working.contiguous()), _native.ptr(states), _native.ptr(states16),
+                     states16.stride(1) if states16 is not None else 0, batch, width, x.shape[-1],
+                     _native.stream_of(u.device))
+        return (states, states16) if with_bf16 else states
     if w.dtype == torch.bfloat16 and not _few_rows(u, w):
         return recurrent.gated_scan(_linear_low(u, w, p["gates_b16"]), valid, working, width=width,
                                     with_bf16=with_bf16, out_bf16=out_bf16, out=states_out)

@@ -112,3 +112,33 @@ def test_split_fusion_and_norm_match_the_concatenated_projection(device):
     assert (err <= 2.0**-7 * want.abs() + 1e-5).all(), err.max().item()
     assert (err > 1e-5 + 1e-6 * want.abs()).float().mean().item() < 0.01  # rounding flips are rare
     assert torch.equal(out16, out.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("rows, width, k, dtype", [(64, 1024, 1024, torch.bfloat16), (5, 40, 64, torch.float32),
+                                                   (70, 96, 128, torch.bfloat16)])
+def test_gated_linear_rows_equal_the_projection_then_the_gated_step(device, rows, width, k, dtype):
+    """koemi_linear_rows_gated (a decode step's gate projections with the
+    gates and the one-position scan in the epilogue) equals, bit for bit,
+    koemi_linear_rows followed by the gated scan at length 1: the same sums
+    in the same order, then the same gate arithmetic; invalid rows carry the
+    state."""
+
+    from koemi_amd import _native, recurrent
+
+    g = torch.Generator().manual_seed(rows + width)
+    u = torch.randn((rows, 1, k), generator=g).to(dtype).to(device)
+    w = (torch.randn((2 * width, k), generator=g) * k ** -0.5).to(torch.bfloat16).to(device)
+    bias = torch.randn((2 * width,), generator=g).to(device)
+    h0 = torch.randn((rows, width), generator=g).to(device)
+    valid = (torch.rand((rows, 1), generator=g) < 0.8).to(device)
+    z = linear.linear_rows([u.reshape(rows, k)], w, None).reshape(rows, 1, 2 * width)
+    want, want16 = recurrent.gated_scan(z, valid, h0, width=width, with_bf16=True, retention_bias=bias[:width],
+                                        candidate_bias=bias[width:])
+    got = torch.full((rows, 1, width), 7.0, device=device)
+    wide16 = torch.zeros((rows, 1, width + 8), device=device, dtype=torch.bfloat16)
+    _native.call("koemi_linear_rows_gated", _native.ptr(u), _native.dtype_code(dtype), _native.ptr(w),
+                 _native.ptr(bias[:width]), _native.ptr(bias[width:]), _native.ptr(valid), _native.ptr(h0),
+                 _native.ptr(got), _native.ptr(wide16), width + 8, rows, width, k, _native.stream_of(got.device))
+    assert torch.equal(got, want)
+    assert torch.equal(wide16[..., :width], want16) and not wide16[..., width:].any()
+    assert torch.equal(got[~valid.reshape(-1)].reshape(-1, width), h0[~valid.reshape(-1)])
