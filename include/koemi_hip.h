@@ -342,6 +342,31 @@ int koemi_read_step_pair_rings(const float* local_keys, const float* local_value
                                uint8_t* next_local_valid, float* next_salient_keys, float* next_salient_values,
                                uint8_t* next_salient_valid, int64_t batch, int64_t width, koemi_stream_t stream);
 
+/* A decode step's whole memory in one launch: koemi_read_step_pair_rings
+ * with the entries read from `projections` (rows row_stride elements apart
+ * of projection_dtype, KOEMI_F32 or KOEMI_BF16: local keys at column
+ * key_offset, local values at value_offset), and the one-position
+ * associative read and update of koemi_assoc_scan_read (memory.py:82-144,
+ * 244-255; network.py:734-740) on the same rows: value pre-activations at
+ * assoc_value_offset, the key's and the query's feature logits at
+ * feature_offset and query_feature_offset (`features` <= 32 columns each),
+ * the decay and write logits at decay_offset and write_offset; surprise
+ * [batch], the carried basis [batch, width, features] and normalizer
+ * [batch, features] in, the read [batch, width] and the next basis and
+ * normalizer out. The results equal the two separate entries'. */
+int koemi_decode_memory_step(const float* local_keys, const float* local_values, const uint8_t* local_valid,
+                             int64_t local_slots, int64_t window, const float* salient_keys,
+                             const float* salient_values, const uint8_t* salient_valid, int64_t salient_slots,
+                             const float* queries, float* local_out, float* salient_out, const void* projections,
+                             int projection_dtype, int64_t row_stride, int64_t key_offset, int64_t value_offset,
+                             const uint8_t* valid, const uint8_t* admission, float* next_local_keys,
+                             float* next_local_values, uint8_t* next_local_valid, float* next_salient_keys,
+                             float* next_salient_values, uint8_t* next_salient_valid, int64_t assoc_value_offset,
+                             int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
+                             int64_t write_offset, const float* surprise, const float* basis, const float* normalizer,
+                             float* assoc_read, float* next_basis, float* next_normalizer, int64_t features,
+                             int64_t batch, int64_t width, koemi_stream_t stream);
+
 /* Bounded recurrent gates, BoundedRecurrentState.gates of model/memory.py:14-30
  * with the masking of network.py:306-309 (a torch composite in the
  * reference): for input rows u (rows x width, `dtype`),

@@ -296,6 +296,18 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
     if (t >= tokens) return;
     const int lane = lane_id();
+    // the row's context and both norm weights first: they do not wait on the
+    // pair positions, so their loads overlap that chain
+    const float* xr = ctx + t * H;
+    float4 xq[NV], wq_e[NV], wq_n[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * kWave + lane) * 4;
+        const int cc = c < H ? c : 0;
+        xq[j] = *reinterpret_cast<const float4*>(xr + cc);
+        wq_e[j] = *reinterpret_cast<const float4*>(w_expert + cc);
+        wq_n[j] = w_next != nullptr ? *reinterpret_cast<const float4*>(w_next + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     int n = 0;
     int64_t p[KMAX];
     if constexpr (POS) {
@@ -320,14 +332,13 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     float w[KMAX];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) w[j] = (pair_w != nullptr && j < n) ? pair_w[p[j]] : 0.0f;
-    const float* xr = ctx + t * H;
     float v[NV][4];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
         if (c < H) {
-            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            const float4 q = xq[j];
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int m = 0; m < KMAX; ++m) {
@@ -361,13 +372,13 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[j][i] = 0.0f;
         } else if (keep) {
-            const float4 wq = *reinterpret_cast<const float4*>(w_expert + c);
+            const float4 wq = wq_e[j];
             v[j][0] = v[j][0] * inv * wq.x;
             v[j][1] = v[j][1] * inv * wq.y;
             v[j][2] = v[j][2] * inv * wq.z;
             v[j][3] = v[j][3] * inv * wq.w;
         } else {
-            const float4 q = *reinterpret_cast<const float4*>(xr + c);
+            const float4 q = xq[j];
             v[j][0] = q.x; v[j][1] = q.y; v[j][2] = q.z; v[j][3] = q.w;
         }
         if (out != nullptr && c < H) *reinterpret_cast<float4*>(out + t * H + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
@@ -382,7 +393,7 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
         if (c >= H) continue;
-        const float4 wq = *reinterpret_cast<const float4*>(w_next + c);
+        const float4 wq = wq_n[j];
         typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
         bf16x4 q;
         q[0] = static_cast<__bf16>(v[j][0] * inv2 * wq.x);

@@ -31,6 +31,7 @@
 // column-major: a row-major [rows, cols] matrix is its [cols, rows]
 // column-major view, so score^T = K'^T Q' and out' = V' P'.
 #include "common.hpp"
+#include "step_memory.hpp"
 
 #include <rocblas/rocblas.h>
 
@@ -314,24 +315,27 @@ struct StepRing {
 
 struct NoRing {};
 
+// Batch row b, columns [1024 col_block, + 1024) of the read (the scores
+// always run over the whole width).
 template <typename T, typename Ring = NoRing>
 __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
                                const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
-                               int window, const Ring& ring = Ring{});
+                               int window, int64_t b, int col_block, const Ring& ring = Ring{});
 
 template <typename T>
 __global__ __launch_bounds__(256) void read_step_kernel(const T* __restrict__ ck, const T* __restrict__ cv,
                                                         const uint8_t* __restrict__ cvalid,
                                                         const T* __restrict__ q, T* __restrict__ out, int S,
                                                         int64_t D, float inv_sqrt_d, int window) {
-    read_step_body<T>(ck, cv, cvalid, q, out, S, D, inv_sqrt_d, window);
+    read_step_body<T>(ck, cv, cvalid, q, out, S, D, inv_sqrt_d, window, blockIdx.x, static_cast<int>(blockIdx.y));
 }
 
 template <typename T>
 __global__ __launch_bounds__(256) void read_step_pair_kernel(StepMemory<T> m0, StepMemory<T> m1,
                                                              const T* __restrict__ q, int64_t D, float inv_sqrt_d) {
     const StepMemory<T>& m = blockIdx.z == 0 ? m0 : m1;
-    read_step_body<T>(m.ck, m.cv, m.cvalid, q, m.out, m.S, D, inv_sqrt_d, m.window);
+    read_step_body<T>(m.ck, m.cv, m.cvalid, q, m.out, m.S, D, inv_sqrt_d, m.window, blockIdx.x,
+                      static_cast<int>(blockIdx.y));
 }
 
 // read_step_pair_kernel that also writes both rings after the position
@@ -341,17 +345,56 @@ __global__ __launch_bounds__(256) void read_step_rings_kernel(StepMemory<float> 
                                                               StepRing<KT> r0, StepRing<KT> r1,
                                                               const float* __restrict__ q, int64_t D,
                                                               float inv_sqrt_d) {
-    if (blockIdx.z == 0) read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, r0);
-    else read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, r1);
+    const int cb = static_cast<int>(blockIdx.y);
+    if (blockIdx.z == 0)
+        read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, blockIdx.x, cb, r0);
+    else read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, blockIdx.x, cb, r1);
+}
+
+// A decode step's whole memory in one launch: the two reads with their ring
+// updates (read_step_rings_kernel) and the associative memory's read and
+// update (step::assoc_step_body). Batch row blockIdx.x; blockIdx.y < 2 R (R =
+// 1024-column blocks of the reads): memory y / R, column block y % R; past
+// those, associative column block y - 2 R (256 columns each). The parts read
+// nothing the others write.
+struct AssocStep {
+    int64_t stride, value_off, fk_off, fq_off, decay_off, write_off;
+    const float* surprise;
+    const uint8_t* valid;
+    const float* basis;
+    const float* normalizer;
+    float* out;
+    float* next_basis;
+    float* next_normalizer;
+    int M;
+};
+
+template <typename KT, int MAXM, typename PT>
+__global__ __launch_bounds__(256) void decode_memory_kernel(StepMemory<float> m0, StepMemory<float> m1,
+                                                            StepRing<KT> r0, StepRing<KT> r1,
+                                                            const float* __restrict__ q, int64_t D, float inv_sqrt_d,
+                                                            const PT* __restrict__ proj, AssocStep as, int R) {
+    const int y = static_cast<int>(blockIdx.y);
+    if (y < 2 * R) {
+        if (y < R)
+            read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, blockIdx.x, y,
+                                  r0);
+        else
+            read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, blockIdx.x,
+                                  y - R, r1);
+    } else {
+        step::assoc_step_body<MAXM, PT>(proj, as.stride, as.value_off, as.fk_off, as.fq_off, as.decay_off,
+                                        as.write_off, as.surprise, as.valid, as.basis, as.normalizer, as.out,
+                                        as.next_basis, as.next_normalizer, D, as.M, blockIdx.x, y - 2 * R);
+    }
 }
 
 template <typename T, typename Ring>
 __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ cv, const uint8_t* __restrict__ cvalid,
                                const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
-                               int window, const Ring& ring) {
+                               int window, int64_t b, int col_block, const Ring& ring) {
     __shared__ float w_sh[kStepMaxSlots];
     __shared__ float stat[1];
-    const int64_t b = blockIdx.x;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     const int low = window > 0 ? S - window : 0;
     const T* qb = q + b * D;
@@ -412,7 +455,7 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
     }
     __syncthreads();
     const float inv = stat[0];
-    const int64_t d = static_cast<int64_t>(blockIdx.y) * 1024 + tid * 4;
+    const int64_t d = static_cast<int64_t>(col_block) * 1024 + tid * 4;
     if (d < D) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const T* vcol = cv + b * S * D + d;
@@ -467,7 +510,7 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
             }
         }
         __syncthreads();
-        if (blockIdx.y == 0)
+        if (col_block == 0)
             for (int s = tid; s < C; s += 256) ring.ovalid[b * C + s] = slot_flag[s];
         if (d < D) {
             const bool entry_zero = ring.kvalid != nullptr && ring.kvalid[b] == 0;
@@ -1315,4 +1358,75 @@ extern "C" int koemi_read_step_pair_rings(
     if (key_dtype == KOEMI_BF16) launch(bf16{});
     else launch(float{});
     return check_launch("koemi_read_step_pair_rings");
+}
+
+extern "C" int koemi_decode_memory_step(
+    const float* local_keys, const float* local_values, const uint8_t* local_valid, int64_t local_slots,
+    int64_t window, const float* salient_keys, const float* salient_values, const uint8_t* salient_valid,
+    int64_t salient_slots, const float* queries, float* local_out, float* salient_out, const void* projections,
+    int projection_dtype, int64_t row_stride, int64_t key_offset, int64_t value_offset, const uint8_t* valid,
+    const uint8_t* admission, float* next_local_keys, float* next_local_values, uint8_t* next_local_valid,
+    float* next_salient_keys, float* next_salient_values, uint8_t* next_salient_valid,
+    int64_t assoc_value_offset, int64_t feature_offset, int64_t query_feature_offset, int64_t decay_offset,
+    int64_t write_offset, const float* surprise, const float* basis, const float* normalizer, float* assoc_read,
+    float* next_basis, float* next_normalizer, int64_t features, int64_t batch, int64_t width,
+    koemi_stream_t stream) {
+    if (batch < 0 || width < 1 || local_slots < 1 || salient_slots < 1 || window < 1 || features < 1)
+        return fail(KOEMI_ERR_INVALID, "decode memory step needs positive width, window, slots and features");
+    if (local_slots > kStepMaxSlots || salient_slots > kStepMaxSlots || width % 4 != 0 || batch > 65535 ||
+        window > 0x7fffffffLL || features > 32)
+        return fail(KOEMI_ERR_UNSUPPORTED,
+                    "decode memory step needs at most %d slots, width %% 4 == 0, batch <= 65535, features <= 32",
+                    kStepMaxSlots);
+    if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "decode memory step takes a float32 or bfloat16 projection");
+    const int64_t cols = row_stride;
+    auto inside = [&](int64_t off, int64_t n) { return off >= 0 && off + n <= cols; };
+    if (row_stride % 4 != 0 || !inside(key_offset, width) || !inside(value_offset, width) ||
+        !inside(assoc_value_offset, width) || !inside(feature_offset, features) ||
+        !inside(query_feature_offset, features) || !inside(decay_offset, 1) || !inside(write_offset, 1) ||
+        key_offset % 4 != 0 || value_offset % 4 != 0)
+        return fail(KOEMI_ERR_INVALID, "decode memory step: projection columns outside the rows or misaligned");
+    if (batch == 0) return KOEMI_OK;
+    const void* ptrs[] = {queries, local_out, salient_out, local_keys, local_values, local_valid, salient_keys,
+                          salient_values, salient_valid, projections, valid, admission, next_local_keys,
+                          next_local_values, next_local_valid, next_salient_keys, next_salient_values,
+                          next_salient_valid, surprise, basis, normalizer, assoc_read, next_basis, next_normalizer};
+    for (const void* p : ptrs)
+        if (!p) return fail(KOEMI_ERR_INVALID, "decode memory step received a null pointer");
+    auto aligned = [](const void* p, size_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; };
+    const size_t es = projection_dtype == KOEMI_F32 ? 4 : 2;
+    if (!aligned(local_keys, 16) || !aligned(local_values, 16) || !aligned(salient_keys, 16) ||
+        !aligned(salient_values, 16) || !aligned(queries, 16) || !aligned(local_out, 16) ||
+        !aligned(salient_out, 16) || !aligned(next_local_keys, 16) || !aligned(next_local_values, 16) ||
+        !aligned(next_salient_keys, 16) || !aligned(next_salient_values, 16) || !aligned(projections, 4 * es))
+        return fail(KOEMI_ERR_INVALID, "decode memory step needs aligned rows");
+    const float inv_sqrt_d = 1.0f / std::sqrt(static_cast<float>(width));
+    const StepMemory<float> m0{local_keys, local_values, local_valid, local_out, static_cast<int>(local_slots),
+                               static_cast<int>(window)};
+    const StepMemory<float> m1{salient_keys, salient_values, salient_valid, salient_out,
+                               static_cast<int>(salient_slots), 0};
+    const AssocStep as{row_stride, assoc_value_offset, feature_offset, query_feature_offset, decay_offset,
+                       write_offset, surprise, valid, basis, normalizer, assoc_read, next_basis, next_normalizer,
+                       static_cast<int>(features)};
+    const int R = static_cast<int>((width + 1023) / 1024);
+    const int assoc_blocks = static_cast<int>((width + 255) / 256);
+    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>(2 * R + assoc_blocks));
+    auto launch = [&](auto tag) {
+        using KT = decltype(tag);
+        const KT* base = static_cast<const KT*>(projections);
+        const StepRing<KT> r0{base + key_offset, base + value_offset, row_stride, valid, valid, next_local_keys,
+                              next_local_values, next_local_valid, true};
+        const StepRing<KT> r1{base + key_offset, base + value_offset, row_stride, valid, admission,
+                              next_salient_keys, next_salient_values, next_salient_valid, false};
+        if (features <= 16)
+            hipLaunchKernelGGL((decode_memory_kernel<KT, 16, KT>), grid, dim3(256), 0, as_stream(stream), m0, m1, r0,
+                               r1, queries, width, inv_sqrt_d, base, as, R);
+        else
+            hipLaunchKernelGGL((decode_memory_kernel<KT, 32, KT>), grid, dim3(256), 0, as_stream(stream), m0, m1, r0,
+                               r1, queries, width, inv_sqrt_d, base, as, R);
+    };
+    if (projection_dtype == KOEMI_BF16) launch(bf16{});
+    else launch(float{});
+    return check_launch("koemi_decode_memory_step");
 }

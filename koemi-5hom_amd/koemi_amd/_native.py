@@ -159,6 +159,12 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64, _P),
     ),
+    "koemi_decode_memory_step": (
+        c_int,
+        (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, c_int, c_int64, c_int64, c_int64, _P,
+         _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, _P,
+         c_int64, c_int64, c_int64, _P),
+    ),
     "koemi_read_step_pair_rings": (
         c_int,
         (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, _P, _P,

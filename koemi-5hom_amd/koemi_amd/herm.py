@@ -654,9 +654,11 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
     step_rings = (length == 1 and state["salient_keys"].shape[1] == settings.salience_memory_size
                   and all(state[k].is_contiguous() for k in ("local_keys", "local_values", "local_valid",
                                                               "salient_keys", "salient_values", "salient_valid")))
+    assoc_done = False
     if length == 1:
         # a decode step: only the carried slots are eligible, both reads in one
-        # launch, with both rings after the step when they are static
+        # launch, with both rings after the step when they are static (and
+        # then the associative memory's step as well)
         local_value = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
         salient_value = torch.empty_like(local_value)
         common = (_native.ptr(state["local_keys"]), _native.ptr(state["local_values"]),
@@ -669,10 +671,25 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                     for part in ("_keys", "_values", "_valid"))
             salient = ring_out("salient") or tuple(torch.empty_like(state["salient" + part])
                                                    for part in ("_keys", "_values", "_valid"))
-            _native.call("koemi_read_step_pair_rings", *common, _native.ptr(local_keys), _native.ptr(local_values),
-                         _native.dtype_code(local_keys.dtype), local_keys.stride(1), _native.ptr(valid),
-                         _native.ptr(admission), *(_native.ptr(t) for t in local_ring + salient), batch, d,
-                         _native.stream_of(ids.device))
+            m = settings.memory_features
+            if projected.is_contiguous() and m <= 32 and projected.shape[-1] >= 3 * d + 2 * m + 2:
+                # the associative memory's step joins the same launch
+                fast = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
+                basis, normalizer = ((out_state["basis"], out_state["normalizer"]) if out_state is not None
+                                     else (torch.empty_like(state["basis"]), torch.empty_like(state["normalizer"])))
+                _native.call("koemi_decode_memory_step", *common, _native.ptr(projected),
+                             _native.dtype_code(projected.dtype), projected.shape[-1], 0, d, _native.ptr(valid),
+                             _native.ptr(admission), *(_native.ptr(t) for t in local_ring + salient), 2 * d, 3 * d,
+                             3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1, _native.ptr(surprise.contiguous()),
+                             _native.ptr(state["basis"].contiguous()), _native.ptr(state["normalizer"].contiguous()),
+                             _native.ptr(fast), _native.ptr(basis), _native.ptr(normalizer), m, batch, d,
+                             _native.stream_of(ids.device))
+                assoc_done = True
+            else:
+                _native.call("koemi_read_step_pair_rings", *common, _native.ptr(local_keys),
+                             _native.ptr(local_values), _native.dtype_code(local_keys.dtype), local_keys.stride(1),
+                             _native.ptr(valid), _native.ptr(admission), *(_native.ptr(t) for t in local_ring + salient),
+                             batch, d, _native.stream_of(ids.device))
         else:
             _native.call("koemi_read_step_pair", *common, batch, d, _native.stream_of(ids.device))
     else:
@@ -680,10 +697,11 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                local_keys, local_values, valid, ws, window=settings.local_memory_size,
                                                out=_block(fusion_in, 2, d))
 
-    fast, basis, normalizer = associative_scan_read(
-        projected, surprise, valid, state["basis"], state["normalizer"], width=d, features=settings.memory_features,
-        out=_block(fusion_in, 1, d),
-        next_out=(out_state["basis"], out_state["normalizer"]) if out_state is not None else None)
+    if not assoc_done:
+        fast, basis, normalizer = associative_scan_read(
+            projected, surprise, valid, state["basis"], state["normalizer"], width=d,
+            features=settings.memory_features, out=_block(fusion_in, 1, d),
+            next_out=(out_state["basis"], out_state["normalizer"]) if out_state is not None else None)
 
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],

@@ -178,6 +178,58 @@ def test_read_step_with_rings_equals_the_read_and_the_two_rings(device, key_dtyp
         assert torch.equal(w, g)
 
 
+@pytest.mark.parametrize("proj_dtype, m", [(torch.bfloat16, 16), (torch.float32, 5)])
+def test_decode_memory_step_equals_the_reads_rings_and_associative_step(device, proj_dtype, m):
+    """koemi_decode_memory_step (the two reads, both ring updates and the
+    associative memory's one-position step in one launch) equals
+    koemi_read_step_pair_rings plus associative_scan_read at length 1, bit
+    for bit, on a stacked projection [local keys ; local values ; values ;
+    feature logits ; decay ; write] with padding columns."""
+
+    from koemi_amd import _native
+
+    rng = np.random.default_rng(m)
+    b, d, slots = 19, 64, 16
+    c = 3 * d + 2 * m + 2
+    c += -c % 4
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(device)
+    lk, lv, lok, _, _, _ = _rand_rings(rng, b, slots, 1, d, 0.5)
+    sk, sv, sok, _, _, _ = _rand_rings(rng, b, slots, 1, d, 0.5)
+    valid = rng.random((b, 1)) < 0.8
+    admission = valid & (rng.random((b, 1)) < 0.5)
+    lk, lv, lok, sk, sv, sok, vmask, amask = (t(x) for x in (lk, lv, lok, sk, sv, sok, valid, admission))
+    projected = torch.randn((b, 1, c), device=device).to(proj_dtype)
+    q = torch.randn((b, d), device=device)
+    surprise = torch.rand((b, 1), device=device)
+    basis = torch.randn((b, d, m), device=device) * 0.1
+    normalizer = torch.rand((b, m), device=device)
+    stream = _native.stream_of(q.device)
+    common = lambda lo, so: (_native.ptr(lk), _native.ptr(lv), _native.ptr(lok), slots, slots, _native.ptr(sk),
+                             _native.ptr(sv), _native.ptr(sok), slots, _native.ptr(q), _native.ptr(lo),
+                             _native.ptr(so))
+    rings = lambda: tuple(torch.full_like(x, 1) for x in (lk, lv, lok, sk, sv, sok))
+    want_l, want_s, want_r = torch.empty_like(q), torch.empty_like(q), rings()
+    keys, values = projected[..., :d], projected[..., d:2 * d]
+    _native.call("koemi_read_step_pair_rings", *common(want_l, want_s), _native.ptr(keys), _native.ptr(values),
+                 _native.dtype_code(proj_dtype), c, _native.ptr(vmask), _native.ptr(amask),
+                 *(_native.ptr(x) for x in want_r), b, d, stream)
+    want_fast, want_basis, want_norm = herm.associative_scan_read(projected, surprise, vmask, basis, normalizer,
+                                                                  width=d, features=m)
+    got_l, got_s, got_r = torch.full_like(q, 7.0), torch.full_like(q, 7.0), rings()
+    got_fast = torch.full((b, 1, d), 7.0, device=device)
+    got_basis, got_norm = torch.full_like(basis, 7.0), torch.full_like(normalizer, 7.0)
+    _native.call("koemi_decode_memory_step", *common(got_l, got_s), _native.ptr(projected),
+                 _native.dtype_code(proj_dtype), c, 0, d, _native.ptr(vmask), _native.ptr(amask),
+                 *(_native.ptr(x) for x in got_r), 2 * d, 3 * d, 3 * d + m, 3 * d + 2 * m, 3 * d + 2 * m + 1,
+                 _native.ptr(surprise), _native.ptr(basis), _native.ptr(normalizer), _native.ptr(got_fast),
+                 _native.ptr(got_basis), _native.ptr(got_norm), m, b, d, stream)
+    assert torch.equal(got_l, want_l) and torch.equal(got_s, want_s)
+    for w, g in zip(want_r, got_r):
+        assert torch.equal(w, g)
+    assert torch.equal(got_fast, want_fast)
+    assert torch.equal(got_basis, want_basis) and torch.equal(got_norm, want_norm)
+
+
 def test_windowed_associative_memory_equals_window_by_window(device):
     g = torch.Generator(device=device).manual_seed(9)
     b, windows, window, d, m = 3, 5, 40, 96, 16
