@@ -322,6 +322,85 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
                                const T* __restrict__ q, T* __restrict__ out, int S, int64_t D, float inv_sqrt_d,
                                int window, int64_t b, int col_block, const Ring& ring = Ring{});
 
+// The ring after a one-position window (see StepRing): slots [s_begin, s_end)
+// of batch row b, columns [col_begin, col_end) (the slot selection is made
+// over the whole ring by every workgroup that calls this; valid bytes are
+// written by the one with col_begin == 0). 256 threads, four columns each.
+template <typename KT>
+__device__ void ring_step_body(const float* __restrict__ ck, const float* __restrict__ cv,
+                               const uint8_t* __restrict__ cvalid, int S, int64_t D, int64_t b, int s_begin,
+                               int s_end, int64_t col_begin, int64_t col_end, const StepRing<KT>& ring) {
+    __shared__ uint8_t fl[kStepMaxSlots + 1];
+    __shared__ int16_t slot_src[kStepMaxSlots];
+    __shared__ uint8_t slot_flag[kStepMaxSlots];
+    const int tid = threadIdx.x;
+    const int N = S + 1, C = S;
+    for (int i = tid; i < N; i += 256) fl[i] = (i < S ? cvalid[b * S + i] : ring.flag[b]) != 0 ? 1 : 0;
+    __syncthreads();
+    if (ring.tail) {
+        for (int s = tid; s < C; s += 256) {
+            slot_src[s] = static_cast<int16_t>(s + 1);
+            slot_flag[s] = fl[s + 1];
+        }
+    } else {
+        int total = 0;
+        for (int j = 0; j < N; ++j) total += fl[j];
+        const int m = min(total, C);
+        for (int i = tid; i < N; i += 256) {
+            int va = 0;
+            for (int j = i + 1; j < N; ++j) va += fl[j];
+            const int ia = (N - 1 - i) - va;
+            const bool keep = fl[i] ? va < m : ia < C - m;
+            if (keep) {
+                const int slot = C - 1 - (min(va, m) + min(ia, C - m));
+                slot_src[slot] = static_cast<int16_t>(i);
+                slot_flag[slot] = fl[i];
+            }
+        }
+    }
+    __syncthreads();
+    if (col_begin == 0)
+        for (int s = s_begin + tid; s < s_end; s += 256) ring.ovalid[b * C + s] = slot_flag[s];
+    const bool entry_zero = ring.kvalid != nullptr && ring.kvalid[b] == 0;
+    for (int64_t d = col_begin + tid * 4; d < col_end; d += 1024) {
+        float ek[4], ev[4];
+        load4_any(ring.k + b * ring.kstride + d, ek);
+        load4_any(ring.v + b * ring.kstride + d, ev);
+        // sixteen slots at a time: every load in flight before the stores
+        constexpr int kGroup = 16;
+        for (int s0 = s_begin; s0 < s_end; s0 += kGroup) {
+            float kq[kGroup][4], vq[kGroup][4];
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                const int s = s0 + u;
+                const int i = s < s_end ? slot_src[s] : S;
+                if (i < S) {
+                    Vec4<float>::load(ck + (b * S + i) * D + d, kq[u]);
+                    Vec4<float>::load(cv + (b * S + i) * D + d, vq[u]);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        kq[u][c] = ek[c];
+                        vq[u][c] = ev[c];
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                const int s = s0 + u;
+                if (s >= s_end) break;
+                const bool zero = (!ring.tail && !slot_flag[s]) || (slot_src[s] == S && entry_zero);
+                if (zero) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) kq[u][c] = vq[u][c] = 0.0f;
+                }
+                Vec4<float>::store(ring.ok + (b * C + s) * D + d, kq[u]);
+                Vec4<float>::store(ring.ov + (b * C + s) * D + d, vq[u]);
+            }
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void read_step_kernel(const T* __restrict__ ck, const T* __restrict__ cv,
                                                         const uint8_t* __restrict__ cvalid,
@@ -369,23 +448,29 @@ struct AssocStep {
     int M;
 };
 
+constexpr int kRingSlotsPerBlock = 4;  // ring slots copied by one workgroup of the combined launch
+
 template <typename KT, int MAXM, typename PT>
 __global__ __launch_bounds__(256) void decode_memory_kernel(StepMemory<float> m0, StepMemory<float> m1,
                                                             StepRing<KT> r0, StepRing<KT> r1,
                                                             const float* __restrict__ q, int64_t D, float inv_sqrt_d,
-                                                            const PT* __restrict__ proj, AssocStep as, int R) {
+                                                            const PT* __restrict__ proj, AssocStep as, int R, int G) {
     const int y = static_cast<int>(blockIdx.y);
+    const int64_t b = blockIdx.x;
     if (y < 2 * R) {
-        if (y < R)
-            read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, blockIdx.x, y,
-                                  r0);
-        else
-            read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, blockIdx.x,
-                                  y - R, r1);
+        if (y < R) read_step_body<float>(m0.ck, m0.cv, m0.cvalid, q, m0.out, m0.S, D, inv_sqrt_d, m0.window, b, y);
+        else read_step_body<float>(m1.ck, m1.cv, m1.cvalid, q, m1.out, m1.S, D, inv_sqrt_d, m1.window, b, y - R);
+    } else if (y < 2 * R + 2 * G) {
+        const int g = (y - 2 * R) % G, s0 = g * kRingSlotsPerBlock;
+        const StepMemory<float>& m = y - 2 * R < G ? m0 : m1;
+        if (s0 >= m.S) return;  // uniform: this memory has fewer slot groups
+        const int s1 = min(m.S, s0 + kRingSlotsPerBlock);
+        if (y - 2 * R < G) ring_step_body(m0.ck, m0.cv, m0.cvalid, m0.S, D, b, s0, s1, 0, D, r0);
+        else ring_step_body(m1.ck, m1.cv, m1.cvalid, m1.S, D, b, s0, s1, 0, D, r1);
     } else {
         step::assoc_step_body<MAXM, PT>(proj, as.stride, as.value_off, as.fk_off, as.fq_off, as.decay_off,
                                         as.write_off, as.surprise, as.valid, as.basis, as.normalizer, as.out,
-                                        as.next_basis, as.next_normalizer, D, as.M, blockIdx.x, y - 2 * R);
+                                        as.next_basis, as.next_normalizer, D, as.M, b, y - 2 * R - 2 * G);
     }
 }
 
@@ -480,77 +565,9 @@ __device__ void read_step_body(const T* __restrict__ ck, const T* __restrict__ c
         }
         Vec4<T>::store(out + b * D + d, acc);
     }
-    if constexpr (!std::is_same<Ring, NoRing>::value) {
-        // the ring after the position: S slots from the N = S + 1 entries [ring ; entry]
-        __shared__ uint8_t fl[kStepMaxSlots + 1];
-        __shared__ int16_t slot_src[kStepMaxSlots];
-        __shared__ uint8_t slot_flag[kStepMaxSlots];
-        const int N = S + 1, C = S;
-        for (int i = tid; i < N; i += 256) fl[i] = (i < S ? cvalid[b * S + i] : ring.flag[b]) != 0 ? 1 : 0;
-        __syncthreads();
-        if (ring.tail) {
-            for (int s = tid; s < C; s += 256) {
-                slot_src[s] = static_cast<int16_t>(s + 1);
-                slot_flag[s] = fl[s + 1];
-            }
-        } else {
-            int total = 0;
-            for (int j = 0; j < N; ++j) total += fl[j];
-            const int m = min(total, C);
-            for (int i = tid; i < N; i += 256) {
-                int va = 0;
-                for (int j = i + 1; j < N; ++j) va += fl[j];
-                const int ia = (N - 1 - i) - va;
-                const bool keep = fl[i] ? va < m : ia < C - m;
-                if (keep) {
-                    const int slot = C - 1 - (min(va, m) + min(ia, C - m));
-                    slot_src[slot] = static_cast<int16_t>(i);
-                    slot_flag[slot] = fl[i];
-                }
-            }
-        }
-        __syncthreads();
-        if (col_block == 0)
-            for (int s = tid; s < C; s += 256) ring.ovalid[b * C + s] = slot_flag[s];
-        if (d < D) {
-            const bool entry_zero = ring.kvalid != nullptr && ring.kvalid[b] == 0;
-            float ek[4], ev[4];
-            load4_any(ring.k + b * ring.kstride + d, ek);
-            load4_any(ring.v + b * ring.kstride + d, ev);
-            // sixteen slots at a time: every load in flight before the stores
-            constexpr int kGroup = 16;
-            for (int s0 = 0; s0 < C; s0 += kGroup) {
-                float kq[kGroup][4], vq[kGroup][4];
-#pragma unroll
-                for (int u = 0; u < kGroup; ++u) {
-                    const int s = s0 + u;
-                    const int i = s < C ? slot_src[s] : S;
-                    if (i < S) {
-                        Vec4<float>::load(ck + (b * S + i) * D + d, kq[u]);
-                        Vec4<float>::load(cv + (b * S + i) * D + d, vq[u]);
-                    } else {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            kq[u][c] = ek[c];
-                            vq[u][c] = ev[c];
-                        }
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < kGroup; ++u) {
-                    const int s = s0 + u;
-                    if (s >= C) break;
-                    const bool zero = (!ring.tail && !slot_flag[s]) || (slot_src[s] == S && entry_zero);
-                    if (zero) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) kq[u][c] = vq[u][c] = 0.0f;
-                    }
-                    Vec4<float>::store(ring.ok + (b * C + s) * D + d, kq[u]);
-                    Vec4<float>::store(ring.ov + (b * C + s) * D + d, vq[u]);
-                }
-            }
-        }
-    }
+    if constexpr (!std::is_same<Ring, NoRing>::value)
+        ring_step_body(ck, cv, cvalid, S, D, b, 0, S, static_cast<int64_t>(col_block) * 1024,
+                       min(D, static_cast<int64_t>(col_block) * 1024 + 1024), ring);
 }
 
 // out[b][t][d] = sum over slots s of weight[b][t][s] . [carried_values ; values][b][s][d]
@@ -1410,8 +1427,10 @@ extern "C" int koemi_decode_memory_step(
                        write_offset, surprise, valid, basis, normalizer, assoc_read, next_basis, next_normalizer,
                        static_cast<int>(features)};
     const int R = static_cast<int>((width + 1023) / 1024);
+    const int G = static_cast<int>(((local_slots > salient_slots ? local_slots : salient_slots) +
+                                    kRingSlotsPerBlock - 1) / kRingSlotsPerBlock);
     const int assoc_blocks = static_cast<int>((width + 255) / 256);
-    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>(2 * R + assoc_blocks));
+    const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>(2 * R + 2 * G + assoc_blocks));
     auto launch = [&](auto tag) {
         using KT = decltype(tag);
         const KT* base = static_cast<const KT*>(projections);
@@ -1421,10 +1440,10 @@ extern "C" int koemi_decode_memory_step(
                               next_salient_keys, next_salient_values, next_salient_valid, false};
         if (features <= 16)
             hipLaunchKernelGGL((decode_memory_kernel<KT, 16, KT>), grid, dim3(256), 0, as_stream(stream), m0, m1, r0,
-                               r1, queries, width, inv_sqrt_d, base, as, R);
+                               r1, queries, width, inv_sqrt_d, base, as, R, G);
         else
             hipLaunchKernelGGL((decode_memory_kernel<KT, 32, KT>), grid, dim3(256), 0, as_stream(stream), m0, m1, r0,
-                               r1, queries, width, inv_sqrt_d, base, as, R);
+                               r1, queries, width, inv_sqrt_d, base, as, R, G);
     };
     if (projection_dtype == KOEMI_BF16) launch(bf16{});
     else launch(float{});
