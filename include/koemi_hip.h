@@ -604,6 +604,14 @@ int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, con
                              int64_t* previous, int64_t* last, uint8_t* valid_out, int64_t* targets_out, int64_t pad_id,
                              int64_t batch, int64_t length, koemi_stream_t stream);
 
+/* A greedy decode step's next tokens (TokenSampler with the greedy policy,
+ * runtime/fast_decode.py:53-55, 82-84: argmax of the logits with the
+ * padding id removed): ids[r] = the first column of maximal logits[r, :]
+ * (rows row_stride apart, fp32 [rows, vocab]) with column exclude_id scored
+ * -inf, a NaN counting as the maximum (torch.argmax's rule). */
+int koemi_herm_greedy_tokens(const float* logits, int64_t row_stride, int64_t rows, int64_t vocab, int64_t exclude_id,
+                             int64_t* ids, koemi_stream_t stream);
+
 /* causal_surprise of a HERM window from the state before each position
  * (network.py:318-325, 677-698) with the fixed-threshold admission
  * (network.py:349), one kernel: row (b, t) of the batch x length rows is

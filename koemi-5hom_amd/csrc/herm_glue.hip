@@ -137,6 +137,45 @@ __global__ __launch_bounds__(256) void rmsnorm_parts_kernel(const float* __restr
     }
 }
 
+// Greedy next tokens: one wave per row, the first maximum of the row with
+// `exclude` scored -inf (a NaN counts as the maximum, as torch.argmax treats
+// it); each lane scans columns lane, lane + 64, ..., then a shuffle
+// reduction keeps the better (value, index) pair, ties to the lower index.
+__device__ __forceinline__ bool greedy_better(float av, int64_t ai, float bv, int64_t bi) {
+    const bool an = av != av, bn = bv != bv;
+    if (an != bn) return an;
+    if (!an && av != bv) return av > bv;
+    return ai < bi;
+}
+
+__global__ __launch_bounds__(256) void greedy_tokens_kernel(const float* __restrict__ logits, int64_t row_stride,
+                                                            int64_t rows, int64_t V, int64_t exclude,
+                                                            int64_t* __restrict__ ids) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const int lane = lane_id();
+    const float* z = logits + row * row_stride;
+    float bv = -INFINITY;
+    int64_t bi = V;  // past every column: loses every comparison
+    for (int64_t j = lane; j < V; j += kWave) {
+        const float v = j == exclude ? -INFINITY : z[j];
+        if (greedy_better(v, j, bv, bi)) {
+            bv = v;
+            bi = j;
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, kWave);
+        const int64_t oi = __shfl_xor(bi, off, kWave);
+        if (greedy_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) ids[row] = bi < V ? bi : 0;
+}
+
 // One workgroup per row: position t takes the latest valid index before it,
 // an exclusive max-scan of (valid ? t : -1) over 256-position chunks (a wave
 // scan, the wave maxima through LDS, the chunk's carry in a register).
@@ -275,6 +314,18 @@ extern "C" int koemi_herm_rmsnorm_parts(const float* parts_input, int parts, con
         hipLaunchKernelGGL(rmsnorm_parts_kernel<2>, grid, dim3(256), 0, as_stream(stream), parts_input, parts,
                            rows * width, add_bias, round_bf16, weight, output, o16, H, eps);
     return check_launch("koemi_herm_rmsnorm_parts");
+}
+
+extern "C" int koemi_herm_greedy_tokens(const float* logits, int64_t row_stride, int64_t rows, int64_t vocab,
+                                        int64_t exclude_id, int64_t* ids, koemi_stream_t stream) {
+    if (rows < 0 || vocab < 1 || row_stride < vocab)
+        return fail(KOEMI_ERR_INVALID, "greedy tokens need rows >= 0, vocab >= 1 and row_stride >= vocab");
+    if (rows == 0) return KOEMI_OK;
+    if (!logits || !ids) return fail(KOEMI_ERR_INVALID, "greedy tokens received a null pointer");
+    if ((rows + 3) / 4 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "greedy tokens: too many rows");
+    hipLaunchKernelGGL(greedy_tokens_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                       as_stream(stream), logits, row_stride, rows, vocab, exclude_id, ids);
+    return check_launch("koemi_herm_greedy_tokens");
 }
 
 extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,

@@ -170,6 +170,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         (_P, _P, _P, c_int64, c_int64, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, _P, _P,
          _P, _P, _P, c_int64, c_int64, _P),
     ),
+    "koemi_herm_greedy_tokens": (c_int, (_P, c_int64, c_int64, c_int64, c_int64, _P, _P)),
     "koemi_herm_token_context": (c_int, (_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_local_read": (
         c_int,

@@ -577,10 +577,13 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"],
                                                       p["gate_b"], p["up_w"], p["up_b"], p["down_w"], p["down_b"],
                                                       validate=False)
-    if next_norm is not None and low is not None and k <= 8 and d % 4 == 0 and d <= 2048:
+    if low is not None and k <= 8 and d % 4 == 0 and d <= 2048:
+        # the combine, the expert normalizer and (inside a stack) the next
+        # block's input norm in one kernel
         tokens = flat.shape[0]
-        final = torch.empty((tokens, d), device=flat.device, dtype=torch.float32) if with_logits else None
-        u_next = torch.empty((tokens, d), device=flat.device, dtype=torch.bfloat16)
+        final = (torch.empty((tokens, d), device=flat.device, dtype=torch.float32)
+                 if with_logits or next_norm is None else None)
+        u_next = torch.empty((tokens, d), device=flat.device, dtype=torch.bfloat16) if next_norm is not None else None
         need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k) if pair_positions is None else 0
         workspace = torch.empty((need,), device=flat.device, dtype=torch.uint8) if need else None
         _native.call("koemi_herm_combine_norm", _native.ptr(expert_out), _native.ptr(sorted_rows),
@@ -590,6 +593,8 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
                      _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]), d, tokens, k,
                      settings.expert_count, _EPS, _native.ptr(workspace), need, _native.stream_of(flat.device))
         logits = _linear(final.view(batch, length, d), p["head_w"], p["head_b"]) if with_logits else None
+        if next_norm is None:
+            return final.view(batch, length, d), logits
         return NextInput(u_next.view(batch, length, d)), logits
     update = moe.combine_topk(expert_out, sorted_rows, offsets, token_count=flat.shape[0], top_k=k,
                               pair_weights=sorted_weights, validate=False)
@@ -1142,9 +1147,22 @@ def decode_step(params: list[dict[str, Tensor]], settings: HermSettings, ids: Te
     and the next states."""
 
     logits, states = stack_window(params, settings, ids, states)
-    scores = logits[:, -1].clone()
-    scores[:, PAD_TOKEN_ID] = float("-inf")
-    return scores.argmax(dim=-1, keepdim=True), states
+    return _greedy_tokens(logits), states
+
+
+def _greedy_tokens(logits: Tensor, out: Tensor | None = None) -> Tensor:
+    """argmax over the vocabulary of the last position's logits with the
+    padding id excluded (its score taken as -inf, the first maximum winning,
+    as ``torch.argmax`` after masking does), [B, 1] int64, one kernel
+    (``koemi_herm_greedy_tokens``)."""
+
+    batch, length, vocab = logits.shape
+    if logits.dtype != torch.float32 or logits.stride(2) != 1:
+        logits = logits.float().contiguous()
+    ids = out if out is not None else torch.empty((batch, 1), device=logits.device, dtype=torch.int64)
+    _native.call("koemi_herm_greedy_tokens", _native.ptr(logits[:, -1]), logits.stride(0), batch, vocab,
+                 PAD_TOKEN_ID, _native.ptr(ids), _native.stream_of(logits.device))
+    return ids
 
 
 class WindowGraph:
@@ -1192,9 +1210,7 @@ class WindowGraph:
         for dst, src in groups.values():
             torch._foreach_copy_(dst, src)
         if self.greedy:
-            scores = logits[:, -1].clone()
-            scores[:, PAD_TOKEN_ID] = float("-inf")
-            self.ids.copy_(scores.argmax(dim=-1, keepdim=True))
+            _greedy_tokens(logits, out=self.ids)
         return logits
 
     def run(self, ids: Tensor | None = None) -> Tensor:
@@ -1243,9 +1259,7 @@ class DecodeGraph:
 
     def _step(self, src: list[dict[str, Tensor]], dst: list[dict[str, Tensor]]) -> Tensor:
         logits, _ = _stack_decode(self.params, self.settings, self.ids, src, dst)
-        scores = logits[:, -1].clone()
-        scores[:, PAD_TOKEN_ID] = float("-inf")
-        self.ids.copy_(scores.argmax(dim=-1, keepdim=True))
+        _greedy_tokens(logits, out=self.ids)
         return logits
 
     @property

@@ -170,6 +170,28 @@ def test_decode_surprise_of_all_layers_equals_the_per_layer_surprise(device):
     assert bool(valid.logical_not().logical_or(got[0][0] > 0).all())
 
 
+def test_greedy_tokens_equal_the_masked_argmax(device):
+    """koemi_herm_greedy_tokens equals torch's argmax of the last position's
+    logits with the padding id set to -inf: random rows, ties (the first
+    maximum wins), the padding id holding the maximum, an all -inf row and a
+    row with NaNs (torch.argmax takes the first NaN)."""
+
+    g = torch.Generator().manual_seed(8)
+    b, length, vocab = 9, 2, 257
+    logits = torch.randn((b, length, vocab), generator=g)
+    logits[1, -1, [3, 77, 200]] = 9.0              # a three-way tie
+    logits[2, -1, PAD] = 50.0                        # the padding id holds the maximum
+    logits[3, -1, :] = float("-inf")                 # nothing but -inf
+    logits[4, -1, [10, 20]] = float("nan")           # NaNs
+    logits[5, -1, :] = 1.5                           # a constant row
+    logits = logits.to(device)
+    got = herm._greedy_tokens(logits)
+    scores = logits[:, -1].clone()
+    scores[:, PAD] = float("-inf")
+    want = scores.cpu().argmax(dim=-1, keepdim=True)
+    assert torch.equal(got.cpu(), want), (got.cpu().reshape(-1), want.reshape(-1))
+
+
 def test_bf16_projections_stay_close_to_fp32(device):
     b = 2
     base = _settings(width=64, salience_threshold=2.0)  # admission off: no discrete flips
