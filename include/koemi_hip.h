@@ -662,14 +662,14 @@ int koemi_local_read(const void* carried_keys, const void* carried_values, const
  * KOEMI_BF16) rows `out_row_stride` elements apart, so that the read can land
  * in a column block of a wider matrix (the HERM fusion layer's bf16 input,
  * network.py:401-405, without a separate concatenation). Only the one-launch
- * fused read: width % 4 == 0, 16-byte aligned fp32 rows, at most 152
+ * fused read: width % 8 == 0, 16-byte aligned fp32 rows, at most 152
  * candidate slots per 32 queries (salient: carried + length - 1 <= 152;
  * local: carried <= 64 and window <= 33); other shapes return
  * KOEMI_ERR_UNSUPPORTED (take koemi_salient_read / koemi_local_read). No
  * workspace. The window's keys and values are rows key_row_stride elements
- * apart (0: width, else a multiple of 4) of key_dtype KOEMI_F32 or
- * KOEMI_BF16 (the bf16 columns of the block's key/value projection read in
- * place, widened exactly; 8-byte aligned). Every slot a query can see is
+ * apart (0: width, else a multiple of 4; of 8 for bf16) of key_dtype
+ * KOEMI_F32 or KOEMI_BF16 (the bf16 columns of the block's key/value
+ * projection read in place, widened exactly; keys 16-byte aligned). Every slot a query can see is
  * flagged valid, so masking the window's invalid entries changes nothing. */
 int koemi_memory_read_into(const float* carried_keys, const float* carried_values, const uint8_t* carried_valid,
                            const void* keys, const void* values, int key_dtype, int64_t key_row_stride,

@@ -287,7 +287,11 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
 // pair -> position map, k per token; a pair is valid when its position is
 // below *valid_end) and cnt is unused; otherwise cnt / pos come from the
 // inversion above (the first cnt[t] entries of the token's row).
-template <int KMAX, int NV, bool POS>
+// PRE (a decode step's few rows): the row's context and both norm weights
+// are loaded first, ahead of the pair-position chain they do not depend on;
+// many rows (a prefill) load them where they are used, which keeps the
+// registers, and the occupancy, of a bandwidth-bound pass.
+template <int KMAX, int NV, bool POS, bool PRE = false>
 __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     const bf16* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ valid_end, const float* __restrict__ pair_w, const float* __restrict__ ctx,
@@ -296,18 +300,22 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
     if (t >= tokens) return;
     const int lane = lane_id();
-    // the row's context and both norm weights first: they do not wait on the
-    // pair positions, so their loads overlap that chain
     const float* xr = ctx + t * H;
     float4 xq[NV], wq_e[NV], wq_n[NV];
+    if constexpr (PRE) {
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int c = (j * kWave + lane) * 4;
-        const int cc = c < H ? c : 0;
-        xq[j] = *reinterpret_cast<const float4*>(xr + cc);
-        wq_e[j] = *reinterpret_cast<const float4*>(w_expert + cc);
-        wq_n[j] = w_next != nullptr ? *reinterpret_cast<const float4*>(w_next + cc) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < NV; ++j) {
+            const int c = (j * kWave + lane) * 4;
+            const int cc = c < H ? c : 0;
+            xq[j] = *reinterpret_cast<const float4*>(xr + cc);
+            wq_e[j] = *reinterpret_cast<const float4*>(w_expert + cc);
+            wq_n[j] = w_next != nullptr ? *reinterpret_cast<const float4*>(w_next + cc)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
     }
+    auto ctx4 = [&](int j, int c) { return PRE ? xq[j] : *reinterpret_cast<const float4*>(xr + c); };
+    auto we4 = [&](int j, int c) { return PRE ? wq_e[j] : *reinterpret_cast<const float4*>(w_expert + c); };
+    auto wn4 = [&](int j, int c) { return PRE ? wq_n[j] : *reinterpret_cast<const float4*>(w_next + c); };
     int n = 0;
     int64_t p[KMAX];
     if constexpr (POS) {
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
         if (c < H) {
-            const float4 q = xq[j];
+            const float4 q = ctx4(j, c);
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int m = 0; m < KMAX; ++m) {
@@ -372,13 +380,13 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[j][i] = 0.0f;
         } else if (keep) {
-            const float4 wq = wq_e[j];
+            const float4 wq = we4(j, c);
             v[j][0] = v[j][0] * inv * wq.x;
             v[j][1] = v[j][1] * inv * wq.y;
             v[j][2] = v[j][2] * inv * wq.z;
             v[j][3] = v[j][3] * inv * wq.w;
         } else {
-            const float4 q = xq[j];
+            const float4 q = ctx4(j, c);
             v[j][0] = q.x; v[j][1] = q.y; v[j][2] = q.z; v[j][3] = q.w;
         }
         if (out != nullptr && c < H) *reinterpret_cast<float4*>(out + t * H + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     for (int j = 0; j < NV; ++j) {
         const int c = (j * kWave + lane) * 4;
         if (c >= H) continue;
-        const float4 wq = wq_n[j];
+        const float4 wq = wn4(j, c);
         typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
         bf16x4 q;
         q[0] = static_cast<__bf16>(v[j][0] * inv2 * wq.x);
@@ -490,6 +498,8 @@ extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t
         return check_launch("koemi_herm_combine_norm(rows)");
     };
     if (pair_positions != nullptr) {  // the permutation's own map: no inversion
+        if (top_k <= 2 && !wide && tokens <= 1024)
+            return launch(combine_norm_kernel<2, 4, true, true>, nullptr, pair_positions);
         if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8, true>, nullptr, pair_positions)
                                     : launch(combine_norm_kernel<2, 4, true>, nullptr, pair_positions);
         if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8, true>, nullptr, pair_positions)

@@ -776,6 +776,49 @@ constexpr int kWinQ = 32;
 constexpr int kWinMaxSlots = 152;   // salient blocks: LDS 4 x 32 x 153 fp32 partial scores (78 KiB)
 constexpr int kWinLocalSlots = 64;  // local blocks: 4 x 32 x 65 (33 KiB)
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// x = hi + mid + lo exactly (fp32 into three bf16 parts, each the nearest to
+// what the parts before it leave; the residuals are exact in fp32), so the
+// products of the parts with a bf16 operand are exact in fp32 and the sum of
+// the three partial dot products is the fp32 dot product up to the order of
+// the additions.
+__device__ __forceinline__ void split3(const float (&x)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 a = static_cast<__bf16>(x[i]);
+        const float r1 = x[i] - static_cast<float>(a);
+        const __bf16 b = static_cast<__bf16>(r1);
+        const float r2 = r1 - static_cast<float>(b);
+        hi[i] = a;
+        mid[i] = b;
+        lo[i] = static_cast<__bf16>(r2);
+    }
+}
+
+// eight values from column col (a multiple of 8) of a row, zeros past D (a
+// multiple of 8)
+__device__ __forceinline__ void load8(const float* row, int64_t col, int64_t D, float (&x)[8]) {
+    if (col < D) {
+        const float4 a = *reinterpret_cast<const float4*>(row + col);
+        const float4 b = *reinterpret_cast<const float4*>(row + col + 4);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.0f;
+    }
+}
+__device__ __forceinline__ void load8(const bf16* row, int64_t col, int64_t D, float (&x)[8]) {
+    if (col < D) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + col);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = static_cast<float>(v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.0f;
+    }
+}
+
 __device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
@@ -785,7 +828,7 @@ __device__ inline f32x16 mfma_f32_32x32x2(float a, float b, f32x16 c) {
 // and values are rows `kstride` elements apart of type KT (fp32, or the bf16
 // columns of the block's projection read in place, widened exactly).
 template <bool LOCAL, int MAXS, typename OutT, typename KT>
-__global__ __launch_bounds__(256) void window_read_kernel(
+__global__ __launch_bounds__(256, LOCAL ? 2 : 1) void window_read_kernel(
     const float* __restrict__ ck, const float* __restrict__ cv, const uint8_t* __restrict__ cvalid,
     const KT* __restrict__ k, const KT* __restrict__ v, int64_t kstride, const uint8_t* __restrict__ flags,
     const float* __restrict__ q, OutT* __restrict__ out, int64_t ostride, int S, int L, int64_t D, int window,
@@ -846,46 +889,86 @@ __global__ __launch_bounds__(256) void window_read_kernel(
         for (int st = 0; st < NST; ++st)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[st][e] = 0.0f;
+        // 64-column chunks; k step j of a chunk is columns 16 j .. 16 j + 15, of
+        // which lane (r, h) holds the eight from 8 h (rows = queries, columns =
+        // slots). The local read runs on bf16 MFMA with the queries split in
+        // three (split3: exact products), three products per k step for bf16
+        // window rows (keys read in place), six for fp32 rows; the salient read
+        // (mostly carried slots) on fp32 MFMA, one product per column.
         const int64_t chunks = (D + 63) / 64;
         for (int64_t ch = wave; ch < chunks; ch += 4) {
-            float4 qa[2][4];
+            if constexpr (LOCAL) {
+                // the queries as three bf16 parts (their sum is the query exactly)
+                bf16x8 qh[4], qm[4], ql[4];
 #pragma unroll
-            for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
-                    qa[blk][i] = col < D ? *reinterpret_cast<const float4*>(qrow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int j = 0; j < 4; ++j) {
+                    float x[8];
+                    load8(qrow, 64 * ch + 16 * j + 8 * h, D, x);
+                    split3(x, qh[j], qm[j], ql[j]);
                 }
 #pragma unroll
-            for (int st = 0; st < NST; ++st) {
-                if (st >= nst) break;
-                const int ks = list[min(st * 32 + r, n - 1)];
-                float4 kb[2][4];
-                auto fetch_keys = [&](const auto* krow) {
+                for (int st = 0; st < NST; ++st) {
+                    if (st >= nst) break;
+                    const int ks = list[min(st * 32 + r, n - 1)];
+                    bool window_only = false;
+                    if constexpr (!std::is_same<KT, float>::value) window_only = group_kind(st * 32, st * 32 + 31) == 1;
+                    if (window_only) {
+                        // bf16 keys: three products per k step
+                        const KT* krow = window_row(k, ks);
 #pragma unroll
-                    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int64_t col = 64 * ch + 32 * blk + 16 * h + 4 * i;
-                            kb[blk][i] = col < D ? load4(krow + col) : make_float4(0.f, 0.f, 0.f, 0.f);
+                        for (int j = 0; j < 4; ++j) {
+                            const int64_t col = 64 * ch + 16 * j + 8 * h;
+                            bf16x8 kb = {};
+                            if (col < D) kb = *reinterpret_cast<const bf16x8*>(krow + col);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qh[j], kb, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qm[j], kb, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ql[j], kb, acc[st], 0, 0, 0);
                         }
-                };
-                if constexpr (std::is_same<KT, float>::value) {
-                    fetch_keys(ks < S ? carried_row(ck, ks) : window_row(k, ks));
-                } else {
-                    const int kind = group_kind(st * 32, st * 32 + 31);
-                    if (kind == 0 || (kind == 2 && ks < S)) fetch_keys(carried_row(ck, ks));
-                    else fetch_keys(window_row(k, ks));
-                }
+                    } else {
+                        // fp32 keys (carried slots) split as well: six products
+                        // per k step (the three dropped are below 2^-24 of the
+                        // product; for bf16 keys the last three add exact zeros)
+                        float kx[4][8];
 #pragma unroll
-                for (int blk = 0; blk < 2; ++blk)
+                        for (int j = 0; j < 4; ++j) {
+                            const int64_t col = 64 * ch + 16 * j + 8 * h;
+                            if (ks < S) load8(carried_row(ck, ks), col, D, kx[j]);
+                            else load8(window_row(k, ks), col, D, kx[j]);
+                        }
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        acc[st] = mfma_f32_32x32x2(qa[blk][i].x, kb[blk][i].x, acc[st]);
-                        acc[st] = mfma_f32_32x32x2(qa[blk][i].y, kb[blk][i].y, acc[st]);
-                        acc[st] = mfma_f32_32x32x2(qa[blk][i].z, kb[blk][i].z, acc[st]);
-                        acc[st] = mfma_f32_32x32x2(qa[blk][i].w, kb[blk][i].w, acc[st]);
+                        for (int j = 0; j < 4; ++j) {
+                            bf16x8 kh, km, kl;
+                            split3(kx[j], kh, km, kl);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qh[j], kh, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qm[j], kh, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ql[j], kh, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qh[j], km, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qm[j], km, acc[st], 0, 0, 0);
+                            acc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qh[j], kl, acc[st], 0, 0, 0);
+                        }
                     }
+                }
+            } else {
+                // the salient read (mostly carried slots): fp32 MFMA, one product per column
+                float qx[4][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) load8(qrow, 64 * ch + 16 * j + 8 * h, D, qx[j]);
+#pragma unroll
+                for (int st = 0; st < NST; ++st) {
+                    if (st >= nst) break;
+                    const int ks = list[min(st * 32 + r, n - 1)];
+                    float kx[4][8];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int64_t col = 64 * ch + 16 * j + 8 * h;
+                        if (ks < S) load8(carried_row(ck, ks), col, D, kx[j]);
+                        else load8(window_row(k, ks), col, D, kx[j]);
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) acc[st] = mfma_f32_32x32x2(qx[j][m], kx[j][m], acc[st]);
+                }
             }
         }
         // accumulator entry e of lane l: query 8 (e / 4) + 4 h + e % 4, slot st * 32 + l % 32
@@ -901,7 +984,6 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     __syncthreads();
 
     // softmax: wave w takes queries 8 w .. 8 w + 7; weights overwrite sc[0]
-    const int npad = nst * 32;
     for (int qq = 0; qq < 8; ++qq) {
         const int m = wave * 8 + qq;
         const int t = t0 + m;
@@ -943,9 +1025,12 @@ __global__ __launch_bounds__(256) void window_read_kernel(
     __syncthreads();
 
     // weighted sum of the listed slots' values: a wave covers 128 columns per
-    // pass as four 32-column MFMA tiles, lane (r, h) feeding column 4 r + c of
-    // tile c from one 16-byte load of a value row; eight MFMA steps' loads
-    // are issued ahead of the step that uses them
+    // pass as four 32-column MFMA tiles (rows = queries, K = slots), lane
+    // (r, h) feeding column 4 r + c of tile c; per group of 16 listed slots a
+    // lane loads the 16-byte pieces (columns 4 r .. 4 r + 3) of slots 8 h ..
+    // 8 h + 7, one group ahead of its use. The local read runs on bf16 MFMA
+    // with the weights split in three (split3): three products for bf16 window
+    // rows, six for fp32 rows (split as well); the salient read on fp32 MFMA.
     const int64_t passes = (D + 127) / 128;
     for (int64_t pc = wave; pc < passes; pc += 4) {
         const int64_t col = pc * 128 + 4 * r;
@@ -961,7 +1046,7 @@ __global__ __launch_bounds__(256) void window_read_kernel(
             auto fetch_with = [&](auto load_slot) {
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const int li = i0 + 2 * u + h;
+                    const int li = i0 + 8 * h + u;
                     bn[u] = li < n ? load_slot(list[li]) : make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             };
@@ -978,22 +1063,56 @@ __global__ __launch_bounds__(256) void window_read_kernel(
             }
         };
         fetch(0);
-        for (int i0 = 0; i0 < npad; i0 += 16) {  // eight MFMA steps of two slots each
+        // groups of 16 listed slots up to the last listed one (past it the
+        // weights are zero: those groups would add exact zeros)
+        for (int i0 = 0; i0 < n; i0 += 16) {
             float4 bc[8];
-            float a[8];
+            float wv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 bc[u] = bn[u];
-                const int li = i0 + 2 * u + h;
-                a[u] = li < n ? sc[0][r][li] : 0.0f;
+                const int li = i0 + 8 * h + u;
+                wv[u] = li < n ? sc[0][r][li] : 0.0f;
             }
-            if (i0 + 16 < npad) fetch(i0 + 16);
+            if (i0 + 16 < n) fetch(i0 + 16);
+            if constexpr (LOCAL) {
+                bool bf16_rows = false;
+                if constexpr (!std::is_same<KT, float>::value) bf16_rows = group_kind(i0, i0 + 15) == 1;
+                bf16x8 wh, wm, wl;
+                split3(wv, wh, wm, wl);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                o[0] = mfma_f32_32x32x2(a[u], bc[u].x, o[0]);
-                o[1] = mfma_f32_32x32x2(a[u], bc[u].y, o[1]);
-                o[2] = mfma_f32_32x32x2(a[u], bc[u].z, o[2]);
-                o[3] = mfma_f32_32x32x2(a[u], bc[u].w, o[3]);
+                for (int cc = 0; cc < 4; ++cc) {
+                    float vv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        vv[u] = cc == 0 ? bc[u].x : cc == 1 ? bc[u].y : cc == 2 ? bc[u].z : bc[u].w;
+                    if (bf16_rows) {
+                        bf16x8 vb;  // exact: the rows hold bf16 values
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) vb[u] = static_cast<__bf16>(vv[u]);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh, vb, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wm, vb, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl, vb, o[cc], 0, 0, 0);
+                    } else {
+                        bf16x8 vh, vm, vl;
+                        split3(vv, vh, vm, vl);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh, vh, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wm, vh, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wl, vh, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh, vm, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wm, vm, o[cc], 0, 0, 0);
+                        o[cc] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wh, vl, o[cc], 0, 0, 0);
+                    }
+                }
+            } else {
+                // fp32 rows: one fp32 MFMA step per slot pair (slot 8 h + u of lane h)
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    o[0] = mfma_f32_32x32x2(wv[u], bc[u].x, o[0]);
+                    o[1] = mfma_f32_32x32x2(wv[u], bc[u].y, o[1]);
+                    o[2] = mfma_f32_32x32x2(wv[u], bc[u].z, o[2]);
+                    o[3] = mfma_f32_32x32x2(wv[u], bc[u].w, o[3]);
+                }
             }
         }
         if (cok) {
@@ -1007,7 +1126,8 @@ __global__ __launch_bounds__(256) void window_read_kernel(
 }
 
 // Whether the fused read takes a block: at most MAXS candidate slots.
-inline bool window_read_fits(int64_t carried, int64_t length, int64_t window) {
+inline bool window_read_fits(int64_t carried, int64_t length, int64_t window, int64_t width) {
+    if (width % 8 != 0) return false;  // the scores' eight-column loads
     if (window > 0) return carried <= kWinLocalSlots && window + kWinQ - 1 <= kWinLocalSlots;
     return carried <= kWinMaxSlots && carried + length - 1 <= kWinMaxSlots;
 }
@@ -1075,7 +1195,7 @@ int memory_read(const void* carried_keys, const void* carried_values, const uint
         return check_launch("koemi_salient_read(one position)");
     }
     auto aligned16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    if (dtype == KOEMI_F32 && width % 4 == 0 && window_read_fits(carried, length, window) && batch <= 0x7fffffffLL &&
+    if (dtype == KOEMI_F32 && width % 4 == 0 && window_read_fits(carried, length, window, width) && batch <= 0x7fffffffLL &&
         (length + kWinQ - 1) / kWinQ <= 65535 &&
         aligned16(carried_keys) && aligned16(carried_values) && aligned16(keys) && aligned16(values) &&
         aligned16(queries) && aligned16(out)) {
@@ -1275,10 +1395,10 @@ extern "C" int koemi_memory_read_into(const float* carried_keys, const float* ca
         return fail(KOEMI_ERR_INVALID, "memory read key row stride must be a multiple of 4, at least the width");
     if (batch == 0 || length == 0) return KOEMI_OK;
     auto aligned16 = [](const void* p) { return p == nullptr || reinterpret_cast<uintptr_t>(p) % 16 == 0; };
-    if (width % 4 != 0 || !window_read_fits(carried, length, window) || batch > 0x7fffffffLL ||
+    if (width % 4 != 0 || !window_read_fits(carried, length, window, width) || batch > 0x7fffffffLL ||
         (length + kWinQ - 1) / kWinQ > 65535 || !aligned16(carried_keys) || !aligned16(carried_values) ||
-        reinterpret_cast<uintptr_t>(keys) % (key_dtype == KOEMI_F32 ? 16 : 8) != 0 ||
-        reinterpret_cast<uintptr_t>(values) % (key_dtype == KOEMI_F32 ? 16 : 8) != 0 || !aligned16(queries) ||
+        !aligned16(keys) || reinterpret_cast<uintptr_t>(values) % (key_dtype == KOEMI_F32 ? 16 : 8) != 0 ||
+        (key_dtype == KOEMI_BF16 && key_row_stride % 8 != 0) || !aligned16(queries) ||
         reinterpret_cast<uintptr_t>(out) % 8 != 0)
         return fail(KOEMI_ERR_UNSUPPORTED, "memory read into a strided output: shape outside the fused read");
     if (!keys || !values || !flags || !queries || !out || (carried > 0 && (!carried_keys || !carried_values ||

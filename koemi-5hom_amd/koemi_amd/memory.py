@@ -107,7 +107,7 @@ def _fused_read_fits(carried: int, length: int, width: int, window: int) -> bool
     """Shapes koemi_memory_read_into takes (the one-launch fused read): at
     most 152 candidate slots per 32 queries (local: 64)."""
 
-    if width % 4:
+    if width % 8:
         return False
     if window > 0:
         return carried <= 64 and window + 31 <= 64
@@ -159,7 +159,8 @@ def _masked_read(
         raise CudaThinkValidationError("queries must be float32, float16 or bfloat16")
     # bf16 window entries read in place by the fused fp32 read
     in_place = (keys.dtype == torch.bfloat16 and queries.dtype == torch.float32 and out is not None
-                and _fused_read_fits(carried_keys.shape[1], length, width, window))
+                and _fused_read_fits(carried_keys.shape[1], length, width, window)
+                and keys.stride(1) % 8 == 0 and keys.data_ptr() % 16 == 0)
     widen = keys.dtype == torch.bfloat16 and queries.dtype == torch.float32 and not in_place
     if any(t.dtype != queries.dtype for t in (carried_keys, carried_values)) or values.dtype != keys.dtype or (
             keys.dtype != queries.dtype and not (keys.dtype == torch.bfloat16 and queries.dtype == torch.float32)):

@@ -140,10 +140,12 @@ def test_reads_into_a_bf16_block_equal_the_rounded_reads(device, window, s, leng
 @pytest.mark.parametrize("window", [0, 16])
 def test_reads_of_bf16_projection_columns_equal_the_widened_reads(device, window):
     """The fused read with the window's keys and values as bf16 column blocks
-    of a wider projection (rows 2 D + 8 apart, read in place) equals, bit for
-    bit, the read of the same entries widened to contiguous fp32; entries of
-    positions the flags exclude do not matter (garbage there changes
-    nothing)."""
+    of a wider projection (rows 2 D + 8 apart, read in place) equals the read
+    of the same entries widened to contiguous fp32 to fp32 rounding (1e-6 of
+    the output scale: the bf16 rows run on bf16 MFMA with the fp32 operand
+    split in three parts, exact products; fp32 rows on fp32 MFMA); entries of
+    positions the flags exclude do not matter (garbage there changes nothing,
+    bit for bit)."""
 
     b, s, length, d = 3, 16, 64, 64
     ck, cv, cvalid, _, _, flags, q = (x.to(device) for x in _read_case(31 + window, b, s, length, d, 0.6,
@@ -156,7 +158,9 @@ def test_reads_of_bf16_projection_columns_equal_the_widened_reads(device, window
     read(ck, cv, cvalid, keys.float(), values.float(), flags, q, out=want, **kw)
     got = torch.zeros_like(want)
     read(ck, cv, cvalid, keys, values, flags, q, out=got, **kw)
-    assert torch.equal(got, want)
+    err = (got - want).abs().max().item()
+    print(f"bf16 in place vs widened fp32 (window {window}): max_abs={err:.3e}", flush=True)
+    assert err <= 1e-6 * want.abs().max().item()
     # a read that cannot take them in place (no out) widens them first
     assert torch.equal(read(ck, cv, cvalid, keys, values, flags, q, **kw),
                        read(ck, cv, cvalid, keys.float(), values.float(), flags, q, **kw))
@@ -164,7 +168,7 @@ def test_reads_of_bf16_projection_columns_equal_the_widened_reads(device, window
     projected[..., :2 * d].masked_fill_(~flags[..., None], float("nan"))
     got2 = torch.zeros_like(want)
     read(ck, cv, cvalid, keys, values, flags, q, out=got2, **kw)
-    assert torch.equal(got2, want)
+    assert torch.equal(got2, got)
 
 
 def test_read_salient_window_rejects_bad_inputs(device):
