@@ -101,6 +101,9 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the C5 prefill steps (for rocprofv3 runs of the headline alone)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the C5 greedy decode steps (for rocprofv3 runs of the decode step alone); prints them "
+                         "as JSON")
     ap.add_argument("--rows-only", action="store_true",
                     help="only the kernel rows of --configs (for rocprofv3 runs of one configuration's kernels); "
                          "prints them as JSON")
@@ -671,6 +674,28 @@ def kernel_rows(args, extra: list, device, stream, timer, kernels: dict) -> None
 
 
 
+def decode_rows(herm, params, settings, c5, device, kernels: dict) -> None:
+    """C5 greedy decode at batch 64: DecodeGraph steps, 3 untimed then
+    C5_DECODE_STEPS timed, into kernels["C5.decode"]."""
+
+    import torch
+
+    log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
+    decode = herm.DecodeGraph(params, settings, c5.decode_ids.to(device),
+                              herm.initial_states(settings, C5_DECODE_BATCH, device))
+    for _ in range(3):
+        decode.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(C5_DECODE_STEPS):
+        decode.step()
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    kernels["C5.decode"] = {"ms_per_step": round(decode_s * 1e3 / C5_DECODE_STEPS, 4),
+                            "tokens_per_s": round(C5_DECODE_BATCH * C5_DECODE_STEPS / decode_s, 1),
+                            "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_pmc:
@@ -707,6 +732,11 @@ def main() -> int:
     c5 = workloads.config5()
     ids = c5.prefill_ids.to(device)
     start_states = herm.initial_states(settings, C5_BATCH, device)
+
+    if args.decode_only:
+        decode_rows(herm, params, settings, c5, device, kernels)
+        print(json.dumps({"kernels": kernels}), flush=True)
+        return 0
 
     sequential = None
     if not args.headline_only:
@@ -747,21 +777,7 @@ def main() -> int:
     del seq, logits, sequential, reference_logits
 
     if not args.headline_only:
-        log(f"C5: greedy decode, batch {C5_DECODE_BATCH}, {C5_DECODE_STEPS} steps")
-        decode = herm.DecodeGraph(params, settings, c5.decode_ids.to(device),
-                                  herm.initial_states(settings, C5_DECODE_BATCH, device))
-        for _ in range(3):
-            decode.step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(C5_DECODE_STEPS):
-            decode.step()
-        torch.cuda.synchronize()
-        decode_s = time.perf_counter() - t0
-        kernels["C5.decode"] = {"ms_per_step": round(decode_s * 1e3 / C5_DECODE_STEPS, 4),
-                                "tokens_per_s": round(C5_DECODE_BATCH * C5_DECODE_STEPS / decode_s, 1),
-                                "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
-        del decode
+        decode_rows(herm, params, settings, c5, device, kernels)
 
     # --------------------------------------------- dominant kernel of C5 prefill
     # The expert FFN of one layer over the whole prefill at its exact shape:
