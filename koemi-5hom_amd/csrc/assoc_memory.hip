@@ -339,7 +339,10 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     __syncthreads();
 
     const int tb = wave >> 1;
-    const int k_end = (s_cnt + 1) & ~1;
+    // The wave's queries are t0 + tb * 32 .. + 31, and slot s reaches query t
+    // only for s < t: past slot t0 + tb * 32 + 31 every influence is zero, so
+    // the wave's products stop there (exactly the sums of the full range).
+    const int k_end = min((s_cnt + 1) & ~1, t0 + tb * 32 + 32);
     const float* ia = infl + (tb * 32 + r32) * IP + h;
     const float ep = fast_exp(pr[tb * 32 + r32]);
     const PT* vrows = proj + b * L * stride + value_off;
