@@ -298,6 +298,28 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     const int t0 = static_cast<int>(blockIdx.z) * kReadRows;
     const int rows = min(kReadRows, L - t0);
     const int s_cnt = t0 + rows;  // slots that can reach these queries (s < t <= t0 + rows - 1)
+    // bf16 path: this lane's value columns, and the loads of its first eight
+    // K steps, issued before the staging so that their latency passes under
+    // it.
+    const PT* vrows = proj + b * L * stride + value_off;
+    const int64_t v_d0 = static_cast<int64_t>(blockIdx.y) * (kReadTiles * 64) + wave * 64;
+    const int64_t v_dcol = v_d0 + 2 * r32;
+    const int64_t v_dq = v_dcol < D ? v_dcol : 0;
+    auto load2 = [&](const PT* p) {
+        if constexpr (std::is_same<PT, float>::value) {
+            return *reinterpret_cast<const float2*>(p);
+        } else {
+            const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+            return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+        }
+    };
+    float2 bn[8];
+    if constexpr (VEC4) {
+        if (v_d0 < D) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bn[u] = load2(vrows + v_dq + min(2 * u + h, L - 1) * stride);
+        }
+    }
     for (int i = tid; i < s_cnt * MAXM; i += 256) f_sh[(i % MAXM) * IP + i / MAXM] = prep.kf[b * L * MAXM + i];
     for (int i = tid; i < kReadRows * MAXM; i += 256) {
         const int r = i / MAXM;
@@ -338,71 +360,85 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     }
     __syncthreads();
 
+    const int kfull = (s_cnt + 1) & ~1;
+    if constexpr (VEC4) {
+        // Wave w: all 64 queries (m-tiles tb = 0, 1) x 64 columns d0 + 2 r + c
+        // (n-tile c = 0, 1) as four 32x32 MFMA tiles, so each value's tanh is
+        // formed once per workgroup; lane (r, h) feeds columns 2 r, 2 r + 1 of
+        // one 2-column load of a value row (eight steps' loads in flight ahead
+        // of their use). Slot s reaches query t only for s < t, so m-tile 0
+        // (queries t0 .. t0 + 31) stops at slot t0 + 32 (exactly the sums of
+        // the full range).
+        if (v_d0 >= D) return;
+        const int64_t dcol = v_dcol;
+        const bool cok = dcol < D;  // D is a multiple of 4, so dcol + 1 < D too
+        const PT* vcol = vrows + v_dq;
+        const int k_end0 = min(kfull, t0 + 32);
+        const float* ia0 = infl + r32 * IP + h;
+        const float* ia1 = infl + (32 + r32) * IP + h;
+        f32x16 acc[2][2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[m][c] = f32x16{};
+        for (int s = 0; s < kfull; s += 16) {
+            float2 bc[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bc[u] = bn[u];
+            if (s + 16 < kfull) {
+#pragma unroll
+                for (int u = 0; u < 8; ++u) bn[u] = load2(vcol + min(s + 16 + 2 * u + h, L - 1) * stride);
+            }
+            const bool first = s < k_end0;  // wave-uniform
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float tx = fast_tanh(bc[u].x), ty = fast_tanh(bc[u].y);
+                if (first) {
+                    const float a0 = s + 2 * u + h < k_end0 ? ia0[s + 2 * u] : 0.0f;
+                    acc[0][0] = mfma2(a0, tx, acc[0][0]);
+                    acc[0][1] = mfma2(a0, ty, acc[0][1]);
+                }
+                const float a1 = s + 2 * u + h < kfull ? ia1[s + 2 * u] : 0.0f;
+                acc[1][0] = mfma2(a1, tx, acc[1][0]);
+                acc[1][1] = mfma2(a1, ty, acc[1][1]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const float ep = fast_exp(pr[m * 32 + r32]);
+#pragma unroll
+            for (int kk = 0; kk < MAXM / 2; ++kk) {
+                const int mm = 2 * kk + h;
+                const float on = mm < M ? 1.0f : 0.0f;
+                const float aq = ep * q_sh[(m * 32 + r32) * QP + mm];
+#pragma unroll
+                for (int c = 0; c < 2; ++c)
+                    acc[m][c] = mfma2(aq, basis[(b * D + min(v_dq + c, D - 1)) * M + min(mm, M - 1)] * on, acc[m][c]);
+            }
+        }
+        if (cok) {
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int rr = m * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+                    if (rr >= rows) continue;
+                    const float dn = den[rr], reg = dn + kReadEpsilon;
+                    const float g = dn / reg;
+                    OutT* o = out + (b * L + t0 + rr) * ostride + dcol;
+                    o[0] = from_f32<OutT>(g * acc[m][0][i] / reg);
+                    o[1] = from_f32<OutT>(g * acc[m][1][i] / reg);
+                }
+        }
+        return;
+    }
     const int tb = wave >> 1;
     // The wave's queries are t0 + tb * 32 .. + 31, and slot s reaches query t
     // only for s < t: past slot t0 + tb * 32 + 31 every influence is zero, so
     // the wave's products stop there (exactly the sums of the full range).
-    const int k_end = min((s_cnt + 1) & ~1, t0 + tb * 32 + 32);
+    const int k_end = min(kfull, t0 + tb * 32 + 32);
     const float* ia = infl + (tb * 32 + r32) * IP + h;
     const float ep = fast_exp(pr[tb * 32 + r32]);
-    const PT* vrows = proj + b * L * stride + value_off;
-    if constexpr (VEC4) {
-        // wave (tb, half): 32 queries x 128 columns as four 32x32 MFMA tiles;
-        // lane (r, h) feeds column 4 r + c of tile c from one 4-column load of
-        // a value row (eight steps' loads in flight ahead of their use)
-        const int64_t d0 = static_cast<int64_t>(blockIdx.y) * (kReadTiles * 64) + (wave & 1) * 128;
-        if (d0 >= D) return;
-        const int64_t dcol = d0 + 4 * r32;
-        const bool cok = dcol < D;
-        const int64_t dq = cok ? dcol : 0;
-        const PT* vcol = vrows + dq;
-        f32x16 acc[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] = f32x16{};
-        float4 bn[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) bn[u] = load4(vcol + min(2 * u + h, L - 1) * stride);
-        for (int s = 0; s < k_end; s += 16) {
-            float4 bc[8];
-            float av[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) bc[u] = bn[u];
-            if (s + 16 < k_end) {
-#pragma unroll
-                for (int u = 0; u < 8; ++u) bn[u] = load4(vcol + min(s + 16 + 2 * u + h, L - 1) * stride);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) av[u] = s + 2 * u + h < k_end ? ia[s + 2 * u] : 0.0f;
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                acc[0] = mfma2(av[u], fast_tanh(bc[u].x), acc[0]);
-                acc[1] = mfma2(av[u], fast_tanh(bc[u].y), acc[1]);
-                acc[2] = mfma2(av[u], fast_tanh(bc[u].z), acc[2]);
-                acc[3] = mfma2(av[u], fast_tanh(bc[u].w), acc[3]);
-            }
-        }
-#pragma unroll
-        for (int kk = 0; kk < MAXM / 2; ++kk) {
-            const int m = 2 * kk + h;
-            const float on = m < M ? 1.0f : 0.0f;
-            const float aq = ep * q_sh[(tb * 32 + r32) * QP + m];
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                acc[c] = mfma2(aq, basis[(b * D + min(dq + c, D - 1)) * M + min(m, M - 1)] * on, acc[c]);
-        }
-        if (cok) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-                if (r >= rows) continue;
-                const float dn = den[r], reg = dn + kReadEpsilon;
-                const float g = dn / reg;
-                store4(out + (b * L + t0 + r) * ostride + dcol, g * acc[0][i] / reg, g * acc[1][i] / reg,
-                       g * acc[2][i] / reg, g * acc[3][i] / reg);
-            }
-        }
-        return;
-    }
     const int db = wave & 1;
     for (int ct = 0; ct < kReadTiles; ++ct) {
         const int64_t d0 = (static_cast<int64_t>(blockIdx.y) * kReadTiles + ct) * 64 + db * 32;
