@@ -53,7 +53,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 // Split K for the last, sparse round: at most this many partial tiles (fp32,
 // at most 256 x 256 each, 64 MiB in all) per GEMM launch.
 constexpr int kMaxSplitUnits = 256;
-constexpr int kMaxSplit = 8;  // chunks per leftover tile (the fixup reads every chunk)
+constexpr int kMaxSplit = 4;  // chunks per leftover tile (the fixup reads every chunk)
 constexpr size_t kPartialTileFloats = static_cast<size_t>(kBM) * kBN;  // the workspace's room per partial tile
 
 struct MlpWorkspace {
@@ -168,11 +168,13 @@ __device__ __forceinline__ void tile_coords(uint32_t logical, uint32_t slots, ui
 // Work of one GEMM launch: `whole` tiles computed in full, then, when the tiles
 // left over after whole rounds of `cus` workgroups (those that run at once)
 // would fill at most a third of a round, each leftover tile split along K into
-// `split` >= 3 chunks (at least two K steps each) so that the last round keeps
-// every CU busy. Partial tiles go to the workspace as fp32 and a fixup kernel
-// adds them in chunk order. (A two-way split measured slower than the
+// `split` chunks, 3 or 4 (at least two K steps each), so that the last round
+// keeps most CUs busy. Partial tiles go to the workspace as fp32 and a fixup
+// kernel adds them in chunk order. (A two-way split measured slower than the
 // half-empty round it replaces: its fp32 partials and the fix-up launch cost
-// more than the half tile it saves.)
+// more than the half tile it saves. Up to eight chunks filled more CUs but
+// wrote and re-read twice the fp32 partials: 11.7 against 7.9 us of fix-up
+// per C5 layer, 1.16 against 1.12 ms for the C4 FFN.)
 struct SplitPlan {
     uint32_t whole, units, split;
 };
