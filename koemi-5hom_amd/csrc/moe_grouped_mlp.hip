@@ -41,7 +41,7 @@ constexpr int kBM = mfma_stage::kBM;
 constexpr int kBN = 256;
 constexpr int kBK = mfma_stage::kBK;
 constexpr int kGemmThreads = mfma_stage::kThreads;
-constexpr int kGroupM = 4;  // tile slots per group in the launch order
+constexpr int kGroupM = 4;  // tile slots per group in the launch order (2 and 8 measured no better)
 #ifndef KOEMI_GEMM_BN
 #define KOEMI_GEMM_BN 256
 #endif
@@ -174,7 +174,7 @@ __device__ __forceinline__ void tile_coords(uint32_t logical, uint32_t slots, ui
 // half-empty round it replaces: its fp32 partials and the fix-up launch cost
 // more than the half tile it saves. Up to eight chunks filled more CUs but
 // wrote and re-read twice the fp32 partials: 11.7 against 7.9 us of fix-up
-// per C5 layer, 1.16 against 1.12 ms for the C4 FFN.)
+// per C5 layer, the partial tiles themselves unchanged.)
 struct SplitPlan {
     uint32_t whole, units, split;
 };
