@@ -229,14 +229,19 @@ def test_graphed_prefill_matches_the_eager_prefill(device):
                     assert torch.equal(g[key], tensor), f"run {run} {key}"
 
 
-@pytest.mark.parametrize("b, length, d, m", [(2, 130, 100, 16), (3, 1, 64, 16), (2, 9, 36, 5), (1, 70, 128, 32)])
+@pytest.mark.parametrize("b, length, d, m", [(2, 130, 100, 16), (3, 1, 64, 16), (2, 9, 36, 5), (1, 70, 128, 32),
+                                              (2, 130, 100, 5), (1, 130, 264, 15)])
 def test_associative_kernel_matches_the_oracle(device, b, length, d, m):
     """koemi_assoc_scan_read (memory.py:82-144, 244-255; network.py:734-740)
     against oracle/herm.py's float64 scan-and-read fed with the same terms
     (features = softmax of the given key/query feature logits, value = tanh,
     bounded decay, surprise-scaled write weight, masking): several 64-row
     influence tiles, partial 64-column chunks, one position (the decode step)
-    and 5 or 32 features; fp32 tolerance 1e-4 relative + 1e-5 x max|result|."""
+    and 5 or 32 features; fp32 tolerance 1e-4 relative + 1e-5 x max|result|.
+    The last two cases have row strides and widths that are multiples of four
+    (the reads' two-columns-per-lane layout with its causal stop): a last
+    query tile of two rows, a partly filled 64-column wave tile, and two
+    256-column groups."""
 
     rng = np.random.default_rng(b * 1000 + length)
     proj = rng.normal(size=(b, length, 3 * d + 2 * m + 2)).astype(np.float32)
