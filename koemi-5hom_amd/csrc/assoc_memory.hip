@@ -423,11 +423,14 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
                 for (int i = 0; i < 16; ++i) {
                     const int rr = m * 32 + 8 * (i / 4) + 4 * h + (i % 4);
                     if (rr >= rows) continue;
+                    // read = den / reg * num / reg, reg = den + 2^-8: the
+                    // row's scale once (two divisions, no overflow of reg^2)
+                    // for every column.
                     const float dn = den[rr], reg = dn + kReadEpsilon;
-                    const float g = dn / reg;
+                    const float sc = (dn / reg) / reg;
                     OutT* o = out + (b * L + t0 + rr) * ostride + dcol;
-                    o[0] = from_f32<OutT>(g * acc[m][0][i] / reg);
-                    o[1] = from_f32<OutT>(g * acc[m][1][i] / reg);
+                    o[0] = from_f32<OutT>(acc[m][0][i] * sc);
+                    o[1] = from_f32<OutT>(acc[m][1][i] * sc);
                 }
         }
         return;
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
             const int r = tb * 32 + 8 * (i / 4) + 4 * h + (i % 4);
             if (r >= rows || d >= D) continue;
             const float dn = den[r], reg = dn + kReadEpsilon;
-            out[(b * L + t0 + r) * ostride + d] = from_f32<OutT>((dn / reg) * acc[i] / reg);
+            out[(b * L + t0 + r) * ostride + d] = from_f32<OutT>(acc[i] * ((dn / reg) / reg));
         }
     }
 }
