@@ -239,13 +239,15 @@ def test_grouped_mlp_bf16_few_rows_per_expert(device, sizes, D, H):
     assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
 
 
-def test_grouped_mlp_bf16_whole_rounds_and_split_last_round(device):
-    # 130 row slots; width 512 and hidden 256 give 260 tiles in both GEMMs: on a
-    # 256-CU device one whole round plus 4 leftover tiles computed in K chunks
-    # and summed by the fixup kernel (other CU counts take other plans).
+@pytest.mark.parametrize("sizes", [(16640, 16600), (20992, 21208)])
+def test_grouped_mlp_bf16_whole_rounds_and_split_last_round(device, sizes):
+    # Width 512 and hidden 256 give two tiles per row slot in both GEMMs. On a
+    # 256-CU device (other CU counts take other plans): 130 slots, one whole
+    # round plus 4 leftover tiles in four K chunks each; 165 slots (the last
+    # one partly filled), one whole round plus 74 leftover tiles in three K
+    # chunks each; the fixup kernel sums the chunks in order.
     g = torch.Generator().manual_seed(11)
     E, D, H = 2, 512, 256
-    sizes = (16640, 16600)
     offsets = np.concatenate([[0], np.cumsum(sizes)])
     P = int(offsets[-1]) + 3
     x = torch.randn((P, D), generator=g).to(torch.bfloat16)
