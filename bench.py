@@ -67,6 +67,11 @@ C5_PREFILL_TOKENS = C5_BATCH * C5_LEN
 C5_DECODE_BATCH, C5_DECODE_STEPS = 64, 256
 C5_PAIRS = C5_PREFILL_TOKENS * C5_K
 C5_FFN_FLOP = 6 * C5_WIDTH * C5_HIDDEN * C5_PAIRS                   # GEMM 1 (gate + value) + GEMM 2, per layer
+# Algorithmic HBM bytes of that FFN (bf16): the sorted context read, the gate
+# and value weights, the hidden rows written and read back, the output weights
+# and the output rows.
+C5_FFN_BYTES = 2 * (C5_PAIRS * C5_WIDTH + 2 * C5_E * C5_HIDDEN * C5_WIDTH + 2 * C5_PAIRS * C5_HIDDEN
+                    + C5_E * C5_WIDTH * C5_HIDDEN + C5_PAIRS * C5_WIDTH)
 
 # Algorithmic bytes / FLOPs per launch of the other rows.
 C2_TOKENS = 16 * 2048
@@ -143,6 +148,13 @@ TRAFFIC_KERNELS = {
     ("rmsnorm_silu_fwd_groupIDF16bLi4ELi32ELb1E",): ("C3.rmsnorm_silu", C3_NORM_BYTES),
     ("permute_gather_kernel",): ("C4.permute_gather", C4_T * C4_D * 2 + C4_PAIRS * C4_D * 2 + C4_PAIRS * 8),
     ("combine_rows_small_kernel",): ("C4.combine_rows", C4_PAIRS * C4_D * 2 + C4_T * C4_D * 2 + C4_PAIRS * 8),
+}
+# Groups of the traffic probe: every launch of these kernels belongs to one of
+# `calls` calls of the group's operation -> bench key, calls, algorithmic bytes
+# per call.
+TRAFFIC_GROUPS = {
+    ("grouped_gemm_bf16_kernel", "split_fixup_kernel", "build_schedule_kernel", "zero_tail_rows_kernel"):
+        ("C5.expert_ffn_layer", 3, C5_FFN_BYTES),
 }
 COPY_BYTES = 512 * 2**20  # the calibration copy reads and writes this many bytes
 
@@ -367,6 +379,26 @@ def traffic_probe() -> int:
         sc, rows, experts, offsets, sw = moe.permute_topk(c4.context, a_l, c4.valid, expert_count=16, pair_weights=w_l)
     for _ in range(3):
         moe.combine_topk(sc, rows, offsets, token_count=C4_T, top_k=2, pair_weights=sw)
+    del c4, sc, rows, experts, offsets, sw
+    # The C5 expert FFN of one layer over the prefill, as the bench times it:
+    # hash-routed byte ids, the sorted bf16 context, one layer's weights
+    # (N(0, 0.02)); TRAFFIC_GROUPS counts its three calls.
+    from koemi_amd import herm
+
+    g = torch.Generator(device=device).manual_seed(5)
+    ids = torch.randint(0, 256, (C5_BATCH, C5_LEN), generator=g, device=device)
+    valid5 = ids != herm.PAD_TOKEN_ID
+    prev5 = torch.cat((torch.full_like(ids[:, :1], herm.PAD_TOKEN_ID), ids[:, :-1]), dim=1)
+    assign5 = moe.route_topk_valid(ids, prev5, valid5, expert_count=C5_E, top_k=C5_K)
+    ctx5 = torch.randn((C5_PREFILL_TOKENS, C5_WIDTH), generator=g, device=device).to(torch.bfloat16)
+    sc5, _, experts5, offsets5 = moe.permute_topk(ctx5, assign5.reshape(-1, C5_K), valid5.reshape(-1),
+                                                  expert_count=C5_E)
+    shapes = ((C5_E, C5_HIDDEN, C5_WIDTH), (C5_E, C5_HIDDEN), (C5_E, C5_HIDDEN, C5_WIDTH), (C5_E, C5_HIDDEN),
+              (C5_E, C5_WIDTH, C5_HIDDEN), (C5_E, C5_WIDTH))
+    w5 = [(0.02 * torch.randn(shape, generator=g, device=device)).to(torch.bfloat16) for shape in shapes]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        moe.grouped_expert_mlp_inference(sc5, experts5, offsets5, *w5, validate=False)
     torch.cuda.synchronize()
     return 0
 
@@ -407,6 +439,17 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> int:
         write_b = w * 1024.0 * write_scale
         result[key] = {"fetch_kib": f, "write_kib": w, "bytes_per_launch": round(read_b + write_b),
                        "algorithmic_bytes": algorithmic, "ratio": round((read_b + write_b) / algorithmic, 4)}
+    for fragments, (key, calls, algorithmic) in TRAFFIC_GROUPS.items():
+        f = sum(v for name, vs in fetch.items() if any(x in name for x in fragments) for v in vs)
+        w = sum(v for name, vs in write.items() if any(x in name for x in fragments) for v in vs)
+        if f == 0 or w == 0:
+            continue
+        read_b = f * 1024.0 * fetch_scale / calls
+        write_b = w * 1024.0 * write_scale / calls
+        result[key] = {"fetch_kib": round(f / calls, 1), "write_kib": round(w / calls, 1),
+                       "bytes_per_launch": round(read_b + write_b), "algorithmic_bytes": algorithmic,
+                       "ratio": round((read_b + write_b) / algorithmic, 4),
+                       "note": f"sum over the {', '.join(fragments)} launches of one call"}
     out = ROOT / "profiles" / "traffic.json"
     out.write_text(json.dumps(result, indent=1) + "\n")
     print(json.dumps(result, indent=1))
@@ -802,7 +845,8 @@ def main() -> int:
     kernels["C5.expert_ffn_layer"] = {"ms": round(ffn_ms, 5), "TFLOP/s": round(ffn_tflops, 1),
                                       "frac_mfma_bf16": round(ffn_tflops / BF16_PEAK_TFLOPS, 4),
                                       "pairs": C5_PAIRS, "flop": C5_FFN_FLOP}
-    headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", None),
+    headline_roofline = {**roofline(ffn_tflops, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma",
+                                    load_traffic("C5.expert_ffn_layer")),
                          "kernel": "grouped expert GLU FFN of one C5 layer over the prefill: grouped_gemm_bf16_kernel "
                                    "launches of GEMM 1 (gate + value, SiLU-GLU epilogue) and GEMM 2 with the device "
                                    "tile schedule, split-K partial tiles and their fix-ups",
