@@ -789,6 +789,7 @@ def main() -> int:
     seq = herm.SequencePrefill(params, settings, start_states, ids)
     logits = seq.run(ids).clone()
     torch.cuda.synchronize()
+    seq.check()  # the fused gate kernel's status word: no carry wait timed out
     assert torch.isfinite(logits).all(), "non-finite prefill logits"
     seq_rel = None
     if sequential is not None:
@@ -811,6 +812,7 @@ def main() -> int:
     gpu_ms = start_ev.elapsed_time(end_ev)
     ms_per_step = max(wall * 1000.0, gpu_ms) / args.steps
     value = C5_PREFILL_TOKENS / (ms_per_step / 1000.0)
+    seq.check()
     assert torch.equal(logits, reference_logits), "prefill steps are not reproducible"
     kernels["C5.prefill"] = {"ms_per_step": round(ms_per_step, 4), "tokens_per_s": round(value, 1),
                              "vs_window_by_window_rel": None if seq_rel is None else round(seq_rel, 6),

@@ -172,6 +172,31 @@ int koemi_moe_route_learned(const float* router_logits, const uint8_t* valid_mas
                             int64_t* assignments, float* weights, int64_t tokens,
                             int64_t expert_count, int64_t top_k, koemi_stream_t stream);
 
+/* LearnedExpertMixture.forward's route with its RouterStatistics
+ * (model/router.py:11-22, 43-59): assignments and weights as
+ * koemi_moe_route_learned (the same bits), and, as device fp32 values,
+ * probability_mass [expert_count] = the sum of the valid tokens' softmax
+ * probabilities, assignment_counts [expert_count] = the valid assignments per
+ * expert (exact integers), valid_count [1] = the number of valid tokens, and
+ * (balance_loss != NULL) balance_loss [1] = RouterStatistics.balance_loss,
+ * E * sum_e (mass_e / max(valid, 1)) * (counts_e / max(sum counts, 1)).
+ * Sums run in a fixed order (tokens in workgroups of 256, then workgroups in
+ * order), so the results do not depend on timing. Workspace:
+ * koemi_moe_route_learned_stats_workspace_bytes(tokens, expert_count) bytes;
+ * no zeroing needed. tokens == 0 gives zero statistics. */
+size_t koemi_moe_route_learned_stats_workspace_bytes(int64_t tokens, int64_t expert_count);
+int koemi_moe_route_learned_stats(const float* router_logits, const uint8_t* valid_mask, int64_t* assignments,
+                                  float* weights, float* probability_mass, float* assignment_counts,
+                                  float* valid_count, float* balance_loss, int64_t tokens, int64_t expert_count,
+                                  int64_t top_k, void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
+/* RouterStatistics.balance_loss (model/router.py:17-22) of given statistics
+ * (e.g. merged over windows by merge_router_statistics, router.py:25-32), in
+ * fp32 and expert order, as koemi_moe_route_learned_stats computes it. */
+int koemi_moe_router_balance_loss(const float* probability_mass, const float* assignment_counts,
+                                  const float* valid_count, int64_t expert_count, float* balance_loss,
+                                  koemi_stream_t stream);
+
 /* Contract checks of moe/__init__.py:113-125, 213-220 on device:
  * flags[0] |= 1 if a valid assignment is outside [0, expert_count),
  * flags[1] |= 1 if a valid token repeats an expert. flags: caller-zeroed int32[2]. */
@@ -441,12 +466,25 @@ int koemi_gated_scan(const void* preactivations, int preactivation_dtype, int64_
  * (KOEMI_ERR_UNSUPPORTED otherwise: take a GEMM and koemi_gated_scan), and a
  * workspace of koemi_gated_projection_scan_workspace_bytes(batch, length,
  * width) bytes (0 for unsupported shapes). Calls sharing one workspace must
- * not overlap in time. */
+ * not overlap in time.
+ *
+ * Every wait for an earlier tile's transfer is bounded by spin_limit polls
+ * (0: the default, 2^22). A wait that runs out sets *status to 1 (a device
+ * int32 the kernel never clears: the caller zeroes it and reads it after the
+ * launch has completed; NULL: the workspace's word at byte offset 1024,
+ * cleared by every launch) and makes that tile's carry NaN, so its states,
+ * the final states and everything computed from them are NaN, never silently
+ * wrong; the launch itself returns KOEMI_OK, as the failure is only known on
+ * the device. spin_limit | KOEMI_GP_WITHHOLD_TRANSFERS makes no tile publish
+ * its transfer, so every tile past the first of its sequence times out after
+ * (spin_limit & ~KOEMI_GP_WITHHOLD_TRANSFERS) polls: the host's way to test
+ * the timeout path with every wave still exiting normally. */
+#define KOEMI_GP_WITHHOLD_TRANSFERS 0x80000000u
 size_t koemi_gated_projection_scan_workspace_bytes(int64_t batch, int64_t length, int64_t width);
 int koemi_gated_projection_scan(const void* inputs, const void* weights, const void* biases, const uint8_t* valid,
                                 const float* initial, float* states, void* states_bf16, int64_t bf16_row_stride,
                                 float* final_states, int64_t batch, int64_t length, int64_t width, int64_t input_width, void* workspace,
-                                size_t workspace_bytes, koemi_stream_t stream);
+                                size_t workspace_bytes, int32_t* status, uint32_t spin_limit, koemi_stream_t stream);
 
 /* nn.Linear over a few rows with bf16 weights (the HERM block's projections
  * in a decode step: the gate, working-state, fusion and head layers of

@@ -34,9 +34,11 @@
 // blockIdx % G group, tiles in position-major order within a group), so a
 // workgroup only waits for tiles whose workgroups already hold lower tickets
 // and are running, and those publish before they wait for anything: the
-// waits always end. Every wait is also bounded (a transfer not seen after
-// about 2^22 polls sets an error word in the workspace and the tile goes on
-// with the carry it has), so no launch can hang.
+// waits always end. Every wait is also bounded: a transfer not seen after
+// the spin limit (2^22 polls by default) sets a sticky status word to 1 and
+// the tile's carry to NaN, so its states and everything computed from them
+// are NaN, never silently wrong, and the caller learns of it from the status
+// word; no launch can hang.
 #include "common.hpp"
 #include "mfma_stage.hpp"
 
@@ -55,6 +57,7 @@ constexpr int kGpThreads = mfma_stage::kThreads;
 constexpr int kGpKAlign = 64;
 constexpr int kGpWidthAlign = 128;  // features: a multiple of every tile width
 constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr uint32_t kWithhold = 1u << 31;  // KOEMI_GP_WITHHOLD_TRANSFERS
 constexpr int kMaxGroups = 8;
 
 // Tile width: BNT B rows = BNT / 2 features (their retention rows, then their
@@ -69,8 +72,9 @@ constexpr int kMaxGroups = 8;
 constexpr int kGpBN = KOEMI_GP_BN;
 static_assert(kGpBN == 128 || kGpBN == 256, "tile width");
 
-// Workspace: kMaxGroups ticket counters (128 bytes apart) and the error word
-// (2 KiB, cleared to zero before every launch), then per tile and feature the
+// Workspace: kMaxGroups ticket counters (128 bytes apart) and the status word
+// used when the caller passes none (word 256, byte offset 1024; 2 KiB in all,
+// cleared to zero before every launch), then per tile and feature the
 // published transfer as one 64-bit word (A in the low half, B in the high
 // half), filled with kEmpty before every launch. A word is written once, by one
 // 64-bit store, and read by 64-bit loads, so a reader sees either kEmpty or
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) v
     const uint8_t* __restrict__ valid, const float* __restrict__ initial, float* __restrict__ states,
     bf16* __restrict__ states16, int64_t s16_stride, float* __restrict__ final_states, int64_t L, int64_t F,
     int64_t K, int32_t n_ft, int32_t n_mt, int32_t groups, uint32_t* __restrict__ ws_words,
-    uint64_t* __restrict__ ws_pairs) {
+    uint64_t* __restrict__ ws_pairs, int32_t* __restrict__ status, uint32_t spin_limit) {
     using TS = mfma_stage::TileShape<BNT>;
     constexpr int NT = TS::kNT;  // n-tiles per wave
     constexpr int NH = NT / 2;   // of them retention (then as many candidate)
@@ -274,7 +278,7 @@ __global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) v
         const float A1 = (NH == 2 && hf) ? WA[NH - 1] : WA[0], B1 = (NH == 2 && hf) ? WB[NH - 1] : WB[0];
         const float TA = A0 * A1, TB = fmaf(A1, B0, B1);  // the tile's transfer
         const int64_t feat = wn * WF + j;
-        if (m + 1 < n_mt) {  // the last tile's transfer is nobody's carry
+        if (m + 1 < n_mt && !(spin_limit & kWithhold)) {  // the last tile's transfer is nobody's carry
             const uint64_t pair = static_cast<uint64_t>(__float_as_uint(TA)) |
                                   (static_cast<uint64_t>(__float_as_uint(TB)) << 32);
             __hip_atomic_store(ws_pairs + tix * FEAT + feat, pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -283,17 +287,19 @@ __global__ __launch_bounds__(kGpThreads, mfma_stage::TileShape<BNT>::kWgPerCu) v
         // in order (the same operations whatever the timing, so the states are
         // a deterministic function of the inputs).
         float C = initial[static_cast<int64_t>(b) * F + n0 + feat];
+        const uint32_t limit = spin_limit & ~kWithhold;
         for (int32_t p = 0; p < m; ++p) {
             const uint64_t* src = ws_pairs + (static_cast<int64_t>(chain) * n_mt + p) * FEAT + feat;
             uint64_t pair;
             uint32_t spins = 0;
             while ((pair = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == kEmpty &&
-                   spins < kSpinLimit) {
+                   spins < limit) {
                 ++spins;
                 __builtin_amdgcn_s_sleep(2);
             }
-            if (pair == kEmpty) {  // timed out: keep the carry so far, flag the error
-                __hip_atomic_store(ws_words + kMaxGroups * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (pair == kEmpty) {  // timed out: report it, and poison the carry so no state is silently wrong
+                __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                C = __builtin_nanf("");
                 break;
             }
             C = fmaf(__uint_as_float(static_cast<uint32_t>(pair)), C, __uint_as_float(static_cast<uint32_t>(pair >> 32)));
@@ -348,7 +354,8 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
                                            void* states_bf16, int64_t bf16_row_stride, float* final_states,
                                            int64_t batch,
                                            int64_t length, int64_t width, int64_t input_width, void* workspace,
-                                           size_t workspace_bytes, koemi_stream_t stream) {
+                                           size_t workspace_bytes, int32_t* status, uint32_t spin_limit,
+                                           koemi_stream_t stream) {
     if (batch < 0 || length < 0 || width < 1 || input_width < 1)
         return fail(KOEMI_ERR_INVALID, "gated projection scan needs non-negative batch and length and positive widths");
     if (length % kGpRows || width % kGpWidthAlign || input_width % kGpKAlign)
@@ -385,6 +392,8 @@ extern "C" int koemi_gated_projection_scan(const void* inputs, const void* weigh
                        static_cast<const bf16*>(biases), valid, initial, states, static_cast<bf16*>(states_bf16),
                        bf16_row_stride, final_states, length, width, input_width, static_cast<int32_t>(n_ft),
                        static_cast<int32_t>(n_mt), static_cast<int32_t>(groups), words,
-                       reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + w.data_off));
+                       reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + w.data_off),
+                       status ? status : reinterpret_cast<int32_t*>(words + kMaxGroups * 32),
+                       (spin_limit & ~kWithhold) ? spin_limit : (spin_limit | kSpinLimit));
     return check_launch("gated projection scan");
 }

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from ctypes import c_double, c_float, c_int, c_int64, c_size_t, c_void_p
+from ctypes import c_double, c_float, c_int, c_int64, c_size_t, c_uint32, c_void_p
 from typing import Any
 
 import torch
@@ -77,6 +77,12 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_moe_route_hash": (c_int, (_P, _P, _P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_route_modulo": (c_int, (_P, _P, c_int, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_route_learned": (c_int, (_P, _P, _P, _P, c_int64, c_int64, c_int64, _P)),
+    "koemi_moe_route_learned_stats_workspace_bytes": (c_size_t, (c_int64, c_int64)),
+    "koemi_moe_route_learned_stats": (
+        c_int,
+        (_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
+    "koemi_moe_router_balance_loss": (c_int, (_P, _P, _P, c_int64, _P, _P)),
     "koemi_moe_check_assignments": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_expert_counts": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_salient_tail": (
@@ -106,7 +112,8 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     "koemi_gated_projection_scan_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64)),
     "koemi_gated_projection_scan": (
         c_int,
-        (_P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+        (_P, _P, _P, _P, _P, _P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P, c_uint32,
+         _P),
     ),
     "koemi_linear_rows": (
         c_int,

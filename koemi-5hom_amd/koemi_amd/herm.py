@@ -281,6 +281,38 @@ def _linear(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
     return out.view(*x.shape[:-1], weight.shape[0])
 
 
+_GATE_STATUS: dict[int, Tensor] = {}
+
+
+def gate_status(device: torch.device | str) -> Tensor:
+    """The device's status word for the fused gate kernel inside captured
+    graphs: ``recurrent.gated_projection_scan`` sets it to 1 when a tile's
+    bounded wait for an earlier tile runs out (that tile's states are then
+    NaN), and nothing clears it. Allocated on first use, which must come before
+    any capture: every graph class of this module calls this in its
+    constructor. Eager calls need no word (the front checks its own after the
+    launch)."""
+
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    word = _GATE_STATUS.get(index)
+    if word is None:
+        word = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", index))
+        _GATE_STATUS[index] = word
+    return word
+
+
+def check_gate_status(device: torch.device | str) -> None:
+    """Raise ``recurrent.GatedScanTimeoutError`` if a captured fused gate
+    kernel on ``device`` has reported a timed-out wait (a host sync)."""
+
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    word = _GATE_STATUS.get(index)
+    if word is not None:
+        recurrent.check_gated_scan_status(word)
+
+
 def _fused_gates(p: dict[str, Tensor], u: Tensor) -> bool:
     """Whether the gate projection and the scan run as the one fused kernel."""
 
@@ -302,8 +334,15 @@ def _gated_scan(p: dict[str, Tensor], u: Tensor, valid: Tensor, working: Tensor,
 
     w = p["gates_w"]
     if _fused_gates(p, u):
+        status = None  # eager: the front checks its own status word after the launch
+        if torch.cuda.is_current_stream_capturing():
+            index = u.device.index if u.device.index is not None else torch.cuda.current_device()
+            status = _GATE_STATUS.get(index)
+            if status is None:
+                raise RuntimeError("the fused gate kernel under graph capture needs herm.gate_status(device) "
+                                   "allocated before the capture")
         return recurrent.gated_projection_scan(u, w, p["gates_b16"], valid, working, with_bf16=with_bf16,
-                                               out_bf16=out_bf16, final_out=final_out)
+                                               out_bf16=out_bf16, final_out=final_out, status=status)
     if u.shape[1] == 1 and w.dtype == torch.bfloat16 and _few_rows(u, w) and w.shape == (2 * width, u.shape[-1]):
         # a decode step: the gates and the one-position scan in the projection's epilogue
         batch = u.shape[0]
@@ -515,7 +554,11 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
     that ``NextInput`` (no fp32 context unless logits are asked for too).
     ``routing``: a dict shared by the layers of one stack pass; the hash
     route depends only on the ids and the validity (experts.py:283-289), so
-    the first layer's permutation is kept there and reused by the others."""
+    the first layer's permutation is kept there and reused by the others.
+    With learned routing every call appends its ``moe.RouterStatistics``
+    (router.py:50-58) to ``routing["statistics"]`` (the reference's
+    KoemiOutput.router_statistics of a window; merge them with
+    ``moe.merge_router_statistics``)."""
 
     batch, length = ids.shape
     d = settings.width
@@ -549,7 +592,10 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         # context (rows of invalid tokens are routed to -1 whatever their
         # logits), softmax top-k, each pair weighted by its probability
         router_logits = functional.linear(flat, p["router_w"])
-        assignments, weights = moe.route_topk_learned(router_logits, flat_valid, top_k=k)
+        assignments, weights, statistics = moe.route_topk_learned(router_logits, flat_valid, top_k=k,
+                                                                  return_statistics=True)
+        if routing is not None:  # the caller's RouterStatistics, one per learned block call
+            routing.setdefault("statistics", []).append(statistics)
     elif not hashed:
         assignments = moe.route_topk_valid(ids, previous, valid, expert_count=settings.expert_count, top_k=k,
                                            validate=False)
@@ -1049,12 +1095,16 @@ class SequencePrefill:
     ``run(ids=None, states=None)`` copies in only what is given (ids other
     than the static ids buffer; starting states, which then stay the start
     of later runs), replays, and returns the logits buffer. Two eager passes
-    on throwaway copies warm the libraries up before the capture."""
+    on throwaway copies warm the libraries up before the capture. The fused
+    gate kernel reports a timed-out wait into ``self.status`` (NaN states,
+    never silently wrong ones): ``check()`` raises if that happened in any
+    replay so far."""
 
     def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, states: list[dict[str, Tensor]],
                  ids: Tensor) -> None:
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
+        self.status = gate_status(self.ids.device)
         self.start = [{k: v.clone() for k, v in st.items()} for st in states]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -1077,6 +1127,12 @@ class SequencePrefill:
             torch._foreach_copy_(dst, src)
         self.graph.replay()
         return self.logits
+
+    def check(self) -> None:
+        """Raise ``recurrent.GatedScanTimeoutError`` if a replay's fused gate
+        kernel timed out waiting for a carry (reads the status word: a sync)."""
+
+        recurrent.check_gated_scan_status(self.status)
 
 
 def _stack_decode(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
@@ -1184,6 +1240,7 @@ class WindowGraph:
         self.settings = settings
         self.greedy = greedy
         self.ids = ids.clone().contiguous()
+        gate_status(self.ids.device)
         self.states = [{k: v.clone() for k, v in st.items()} for st in states]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -1235,6 +1292,7 @@ class DecodeGraph:
                  states: list[dict[str, Tensor]]) -> None:
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
+        gate_status(self.ids.device)
         self._sets = []
         for _ in range(2):
             copy = [{k: v.clone() for k, v in st.items()} for st in states]
@@ -1330,6 +1388,7 @@ class WavefrontPrefill:
                  batch: int, device: torch.device) -> None:
         self.params, self.settings = params, settings
         self.layers = len(params)
+        gate_status(device)
         chunk = settings.scan_chunk
         self.start = [{k: v.clone() for k, v in st.items()} for st in states]
         self.states = [{k: v.clone() for k, v in st.items()} for st in states]

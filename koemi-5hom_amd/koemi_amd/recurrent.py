@@ -19,7 +19,27 @@ from torch import Tensor
 from koemi_amd import _native
 from koemi_amd.dense import DenseCudaUnavailableError, DenseCudaValidationError, dense_affine_scan
 
-__all__ = ["gated_scan", "recurrent_gates", "recurrent_scan"]
+__all__ = ["GatedScanTimeoutError", "check_gated_scan_status", "gated_scan", "recurrent_gates", "recurrent_scan"]
+
+# koemi_gated_projection_scan: spin_limit bit that stops tiles publishing their
+# transfers (include/koemi_hip.h KOEMI_GP_WITHHOLD_TRANSFERS), so the host can
+# drive the bounded waits to their timeout in a test.
+GP_WITHHOLD_TRANSFERS = 0x80000000
+
+
+class GatedScanTimeoutError(RuntimeError):
+    """A tile of ``gated_projection_scan`` gave up waiting for an earlier
+    tile's transfer: its states (and what was computed from them) are NaN."""
+
+
+def check_gated_scan_status(status: Tensor) -> None:
+    """Raise ``GatedScanTimeoutError`` when the device status word that
+    ``gated_projection_scan`` (``status=``) reports into is set. Reads it to the
+    host, so it waits for the work queued before it on the current stream."""
+
+    if int(status.reshape(-1)[0].item()) != 0:
+        raise GatedScanTimeoutError("gated projection scan: a tile timed out waiting for an earlier tile's carry; "
+                                    "its states are NaN")
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -262,7 +282,8 @@ def gated_projection_fits(inputs: Tensor, weight: Tensor) -> bool:
 
 def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, valid_mask: Tensor | None,
                           initial: Tensor, *, with_bf16: bool = False, out_bf16: Tensor | None = None,
-                          final_out: Tensor | None = None) -> Tensor | tuple[Tensor, Tensor]:
+                          final_out: Tensor | None = None, status: Tensor | None = None,
+                          spin_limit: int = 0) -> Tensor | tuple[Tensor, Tensor]:
     """The gates of model/memory.py:14-30 with their two projections, the
     masking of network.py:307-309 and the scan of network.py:310, for a bf16
     window under autocast, in one kernel (``koemi_gated_projection_scan``):
@@ -275,7 +296,16 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
     fp32 ``[B, width]`` tensor, or None) receives the last position's states
     as well (the carried state). Shapes outside ``gated_projection_fits``
     raise; the projection's results are rounded to bf16 after the bias (the
-    autocast GEMM's output) before the gates."""
+    autocast GEMM's output) before the gates.
+
+    Each tile's wait for the tiles before it is bounded (``spin_limit`` polls,
+    0 = the kernel's default). A wait that runs out makes that tile's states
+    NaN and is reported: with ``status`` (an int32 device tensor of one
+    element the caller zeroed) the kernel sets it to 1 and nothing syncs — the
+    caller checks it later with ``check_gated_scan_status``, which is how a
+    captured graph uses this; without it the front reads a status word of its
+    own after the launch (a host sync) and raises ``GatedScanTimeoutError``.
+    Under graph capture ``status`` is required."""
 
     if not gated_projection_fits(inputs, weight):
         raise DenseCudaValidationError("gated_projection_scan needs bf16 inputs [B, L, K] and weight [2 width, K] "
@@ -292,6 +322,14 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
         raise DenseCudaValidationError("valid_mask must be a bool [batch, length] tensor on the same device")
     if bias is not None and (bias.shape != (2 * width,) or bias.dtype != torch.bfloat16 or bias.device != inputs.device):
         raise DenseCudaValidationError("bias must be a bf16 [2 width] tensor on the same device")
+    if status is not None and (status.dtype != torch.int32 or status.numel() != 1 or status.device != inputs.device
+                               or not status.is_contiguous()):
+        raise DenseCudaValidationError("status must be a contiguous int32 tensor of one element on the same device")
+    if not 0 <= int(spin_limit) <= 0xFFFFFFFF:
+        raise DenseCudaValidationError("spin_limit must fit in 32 bits")
+    own_status = status is None
+    if own_status and torch.cuda.is_current_stream_capturing():
+        raise DenseCudaValidationError("gated_projection_scan under graph capture needs status= (checked after replay)")
     try:
         _native.load_library()
     except _native.NativeLibraryUnavailableError as error:
@@ -312,6 +350,8 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
     if states.numel():
         need = _native.query("koemi_gated_projection_scan_workspace_bytes", batch, length, width)
         workspace = torch.empty(need, device=x.device, dtype=torch.uint8)
+        if own_status:
+            status = torch.zeros(1, device=x.device, dtype=torch.int32)
         mask = valid_mask.contiguous() if valid_mask is not None else None
         _native.call(
             "koemi_gated_projection_scan",
@@ -319,6 +359,8 @@ def gated_projection_scan(inputs: Tensor, weight: Tensor, bias: Tensor | None, v
             _native.ptr(mask) if mask is not None else None, _native.ptr(initial.contiguous()), _native.ptr(states),
             _native.ptr(states16), states16.stride(1) if states16 is not None else 0, _native.ptr(final_out),
             batch, length, width, k,
-            _native.ptr(workspace), need, _native.stream_of(x.device),
+            _native.ptr(workspace), need, _native.ptr(status), int(spin_limit), _native.stream_of(x.device),
         )
+        if own_status:
+            check_gated_scan_status(status)
     return (states, states16) if with_bf16 else states

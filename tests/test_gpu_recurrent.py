@@ -276,23 +276,64 @@ def test_gated_projection_scan_random_weights_match_library_gemm_then_scan(devic
 def test_gated_projection_scan_graph_replays_equal_eager(device):
     """The kernel (its flag clearing included) captured in a HIP graph and
     replayed three times, with eager work between the replays, gives the
-    eager call's bits each time: the carries do not depend on timing."""
+    eager call's bits each time: the carries do not depend on timing. Under
+    capture the timeout is reported into a caller's status word, read after
+    the replays."""
     u, w, bias, valid, h0 = _exact_projection_case(11, 4, 1024, 256, 256, 0.9, device)
     eager = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        recurrent.gated_projection_scan(u, w, bias, valid, h0)
+        recurrent.gated_projection_scan(u, w, bias, valid, h0, status=status)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+        out = recurrent.gated_projection_scan(u, w, bias, valid, h0, status=status)
     for _ in range(3):
         recurrent.gated_projection_scan(u, w, bias, valid, h0 * 0.5)
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+    recurrent.check_gated_scan_status(status)
+    assert int(status.item()) == 0
+
+
+def test_gated_projection_scan_timeout_is_an_error(device):
+    """The bounded carry wait, driven to its timeout from the host: with
+    KOEMI_GP_WITHHOLD_TRANSFERS no tile publishes its transfer, so every tile
+    past the first of its sequence gives up after 64 polls (every wave still
+    exits normally). The status word reads 1, the front raises, the first
+    tile's states equal a normal call's and every later state is NaN (never
+    silently wrong); a normal call afterwards is unaffected."""
+    u, w, bias, valid, h0 = _exact_projection_case(12, 2, 768, 256, 256, 0.9, device)
+    good = recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    final = torch.empty((2, 256), device=device)
+    got = recurrent.gated_projection_scan(u, w, bias, valid, h0, status=status, final_out=final,
+                                          spin_limit=recurrent.GP_WITHHOLD_TRANSFERS | 64)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1
+    with pytest.raises(recurrent.GatedScanTimeoutError, match="timed out"):
+        recurrent.check_gated_scan_status(status)
+    assert torch.equal(got[:, :256], good[:, :256])
+    assert torch.isnan(got[:, 256:]).all() and torch.isnan(final).all()
+    with pytest.raises(recurrent.GatedScanTimeoutError):
+        recurrent.gated_projection_scan(u, w, bias, valid, h0, spin_limit=recurrent.GP_WITHHOLD_TRANSFERS | 64)
+    assert torch.equal(recurrent.gated_projection_scan(u, w, bias, valid, h0), good)
+
+
+def test_gated_projection_scan_needs_status_under_capture(device):
+    """Under graph capture the front cannot read a status word back, so it
+    refuses to run without the caller's."""
+    u, w, bias, valid, h0 = _exact_projection_case(13, 1, 256, 64, 128, 1.0, device)
+    recurrent.gated_projection_scan(u, w, bias, valid, h0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(dense.DenseCudaValidationError, match="status"):
+        with torch.cuda.graph(graph):
+            recurrent.gated_projection_scan(u, w, bias, valid, h0)
 
 
 def test_gated_projection_scan_rejects_unsupported_shapes(device):
