@@ -14,12 +14,15 @@ Build-side keyword-only extensions (absent from the reference signatures):
   into sorted order, for the learned gate;
 * ``combine_topk(..., pair_weights=None)`` weighs each sorted pair by its gate
   probability (router.py:73) instead of ``1 / top_k`` (moe_kernels.cu:226-228);
-* ``route_topk_learned`` — softmax top-k gate of router.py:46-49;
+* ``route_topk_learned`` — softmax top-k gate of router.py:46-49, with
+  ``return_statistics=True`` also its ``RouterStatistics`` (router.py:11-22,
+  50-58; ``merge_router_statistics`` router.py:25-32);
 * ``expert_activation_counts`` — per-expert counts of network.py:48-70.
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass, field
 from typing import Any
 
 import torch
@@ -30,10 +33,12 @@ from koemi_amd import _native
 __all__ = [
     "CudaMoeUnavailableError",
     "CudaMoeValidationError",
+    "RouterStatistics",
     "combine_topk",
     "expert_activation_counts",
     "grouped_expert_mlp_inference",
     "load_native_extension",
+    "merge_router_statistics",
     "permute_topk",
     "route_topk_learned",
     "route_topk_valid",
@@ -210,10 +215,65 @@ def route_topk_modulo(token_ids: Tensor, valid_mask: Tensor, *, expert_count: in
     return assignments.reshape(*token_ids.shape, top_k)
 
 
-def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int) -> tuple[Tensor, Tensor]:
+@dataclass(frozen=True)
+class RouterStatistics:
+    """The learned gate's statistics of one forward (router.py:11-22): fp32
+    device tensors ``probability_mass`` ``[E]`` (the valid tokens' softmax
+    probabilities summed per expert), ``assignment_counts`` ``[E]`` (valid
+    assignments per expert) and ``valid_count`` (0-dim, the valid tokens).
+    ``balance_loss`` (0-dim fp32 device tensor) is
+    ``E * sum((mass / max(valid, 1)) * (counts / max(sum(counts), 1)))``, formed
+    on the device (``koemi_moe_router_balance_loss``) unless the route kernel
+    already formed it."""
+
+    probability_mass: Tensor
+    assignment_counts: Tensor
+    valid_count: Tensor
+    _loss: Tensor | None = field(default=None, repr=False, compare=False)
+
+    @property
+    def balance_loss(self) -> Tensor:
+        if self._loss is not None:
+            return self._loss
+        mass, counts = self.probability_mass.contiguous(), self.assignment_counts.contiguous()
+        valid = self.valid_count.reshape(1).contiguous()
+        tensors = {"probability_mass": mass, "assignment_counts": counts, "valid_count": valid}
+        for name, tensor in tensors.items():
+            _require_cuda_tensor(tensor, name)
+            if tensor.dtype != torch.float32:
+                raise CudaMoeValidationError(f"{name} must use float32")
+        _require_same_cuda_device(tensors)
+        if mass.ndim != 1 or counts.shape != mass.shape or mass.numel() < 1:
+            raise CudaMoeValidationError("probability_mass and assignment_counts must be [expert_count]")
+        _require_library()
+        loss = torch.empty((), device=mass.device, dtype=torch.float32)
+        with torch.cuda.device(mass.device):
+            _native.call("koemi_moe_router_balance_loss", mass.data_ptr(), counts.data_ptr(), valid.data_ptr(),
+                         mass.numel(), loss.data_ptr(), _native.stream_of(mass.device))
+        return loss
+
+
+def merge_router_statistics(statistics: list[RouterStatistics]) -> RouterStatistics | None:
+    """Field-wise sums of several forwards' statistics (router.py:25-32: the
+    windows of a sequence, network.py:835-837); None for an empty list."""
+
+    if not statistics:
+        return None
+    return RouterStatistics(
+        sum(item.probability_mass for item in statistics),
+        sum(item.assignment_counts for item in statistics),
+        sum(item.valid_count for item in statistics),
+    )
+
+
+def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int, return_statistics: bool = False
+                       ) -> tuple[Tensor, Tensor] | tuple[Tensor, Tensor, RouterStatistics]:
     """Learned softmax top-k gate (router.py:46-49): returns int64 assignments and
     fp32 weights of shape ``router_logits.shape[:-1] + (top_k,)``, descending by
-    probability (ties to the lower expert index); invalid rows get -1 and 0."""
+    probability (ties to the lower expert index); invalid rows get -1 and 0.
+    With ``return_statistics`` also the ``RouterStatistics`` of router.py:50-58
+    (one launch more: the route and the per-workgroup partials in one kernel,
+    then a one-workgroup finisher that also forms the balance loss)."""
 
     tensors = {"router_logits": router_logits, "valid_mask": valid_mask}
     for name, tensor in tensors.items():
@@ -233,6 +293,23 @@ def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int)
     count = valid_mask.numel()
     assignments = torch.empty((count, top_k), device=router_logits.device, dtype=torch.int64)
     weights = torch.empty((count, top_k), device=router_logits.device, dtype=torch.float32)
+    shape = (*valid_mask.shape, top_k)
+    if return_statistics:
+        device = router_logits.device
+        mass = torch.empty((expert_count,), device=device, dtype=torch.float32)
+        counts = torch.empty((expert_count,), device=device, dtype=torch.float32)
+        valid_count = torch.empty((), device=device, dtype=torch.float32)
+        loss = torch.empty((), device=device, dtype=torch.float32)
+        need = _native.query("koemi_moe_route_learned_stats_workspace_bytes", count, expert_count)
+        workspace = torch.empty((max(need, 1),), device=device, dtype=torch.uint8)
+        logits_c, valid_c = router_logits.contiguous(), valid_mask.contiguous()
+        with torch.cuda.device(device):
+            _native.call("koemi_moe_route_learned_stats", logits_c.data_ptr(),
+                         valid_c.data_ptr(), assignments.data_ptr(), weights.data_ptr(),
+                         mass.data_ptr(), counts.data_ptr(), valid_count.data_ptr(), loss.data_ptr(), count,
+                         expert_count, top_k, workspace.data_ptr(), need, _native.stream_of(device))
+        statistics = RouterStatistics(mass, counts, valid_count, loss)
+        return assignments.reshape(shape), weights.reshape(shape), statistics
     if count:
         with torch.cuda.device(router_logits.device):
             _native.call(
@@ -246,7 +323,6 @@ def route_topk_learned(router_logits: Tensor, valid_mask: Tensor, *, top_k: int)
                 top_k,
                 _native.stream_of(router_logits.device),
             )
-    shape = (*valid_mask.shape, top_k)
     return assignments.reshape(shape), weights.reshape(shape)
 
 

@@ -447,6 +447,53 @@ def route_learned(router_logits: np.ndarray, valid: np.ndarray, top_k: int) -> t
     return idx.reshape(shape), w.reshape(shape)
 
 
+def router_statistics(router_logits: np.ndarray, valid: np.ndarray, assignments: np.ndarray) -> dict:
+    """RouterStatistics of LearnedExpertMixture.forward (router.py:11-22, 50-58)
+    in float64: ``probability_mass`` [E] = the softmax probabilities of the
+    valid tokens summed per expert, ``assignment_counts`` [E] = the valid
+    (token, slot) assignments per expert (scatter_add of the valid flags over
+    the assignments clamped at 0), ``valid_count`` = the valid tokens, and
+    ``balance_loss`` (``balance_loss`` below)."""
+
+    z = np.asarray(router_logits, np.float64)
+    E = z.shape[-1]
+    z = z.reshape(-1, E)
+    ok = np.asarray(valid, bool).reshape(-1)
+    a = np.asarray(assignments, np.int64).reshape(ok.size, -1)
+    e = np.exp(z - z.max(axis=1, keepdims=True))
+    p = e / e.sum(axis=1, keepdims=True)
+    mass = (p * ok[:, None]).sum(axis=0)
+    counts = np.zeros(E, np.float64)
+    np.add.at(counts, np.maximum(a, 0).reshape(-1), np.repeat(ok, a.shape[1]).astype(np.float64))
+    valid_count = float(ok.sum())
+    return {"probability_mass": mass, "assignment_counts": counts, "valid_count": valid_count,
+            "balance_loss": balance_loss(mass, counts, valid_count)}
+
+
+def balance_loss(probability_mass: np.ndarray, assignment_counts: np.ndarray, valid_count: float) -> float:
+    """RouterStatistics.balance_loss (router.py:17-22) in float64:
+    E * sum((mass / max(valid, 1)) * (counts / max(sum(counts), 1)))."""
+
+    mass = np.asarray(probability_mass, np.float64)
+    counts = np.asarray(assignment_counts, np.float64)
+    importance = mass / max(float(valid_count), 1.0)
+    load = counts / max(float(counts.sum()), 1.0)
+    return float(mass.size * (importance * load).sum())
+
+
+def merge_router_statistics(statistics: list[dict]) -> dict | None:
+    """merge_router_statistics (router.py:25-32): field-wise sums (None when
+    empty), the balance loss formed again from the sums."""
+
+    if not statistics:
+        return None
+    mass = sum(np.asarray(item["probability_mass"], np.float64) for item in statistics)
+    counts = sum(np.asarray(item["assignment_counts"], np.float64) for item in statistics)
+    valid_count = float(sum(float(item["valid_count"]) for item in statistics))
+    return {"probability_mass": mass, "assignment_counts": counts, "valid_count": valid_count,
+            "balance_loss": balance_loss(mass, counts, valid_count)}
+
+
 def expert_counts(assignments: np.ndarray, valid: np.ndarray, expert_count: int) -> np.ndarray:
     """network.py:48-70: counts of valid, in-range assignments per expert."""
 

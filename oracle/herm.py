@@ -164,11 +164,13 @@ def learned_route(router_w: np.ndarray, context: np.ndarray, valid: np.ndarray, 
     """LearnedExpertMixture.forward's gate (router.py:46-50): the context with
     invalid rows zeroed through the bias-free gate, the logits rounded to fp32,
     softmax and top-k in fp32 (oracle.route_learned); invalid rows -1 and 0.
-    Returns (assignments [..., k] int64, weights [..., k] fp32)."""
+    Returns (assignments [..., k] int64, weights [..., k] fp32, the
+    RouterStatistics of router.py:50-58 as ``oracle.router_statistics``)."""
 
     gate_context = np.where(valid[..., None], context, 0.0)
     logits = linear(gate_context, router_w, None).astype(np.float32)
-    return oracle.route_learned(logits, valid, top_k)
+    assignments, weights = oracle.route_learned(logits, valid, top_k)
+    return assignments, weights, oracle.router_statistics(logits, valid, assignments)
 
 
 def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray, valid: np.ndarray, cfg: dict):
@@ -180,14 +182,16 @@ def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray,
     distinct assigned experts. ``cfg["expert_routing"] == "learned"``:
     LearnedExpertMixture (router.py:43-97), every valid token adds
     w_slot * FFN_e(context) over its top-k experts, w the fp32 softmax weight.
-    Returns (context, assignments)."""
+    Returns (context, assignments, router statistics or None for hash
+    routing)."""
 
     k, count = cfg["top_k"], cfg["expert_count"]
     b, length, d = context.shape
     flat = context.reshape(-1, d)
     ok = valid.reshape(-1)
+    statistics = None
     if cfg.get("expert_routing", "hash") == "learned":
-        assignments, weights = learned_route(p["router_w"], context, valid, k)
+        assignments, weights, statistics = learned_route(p["router_w"], context, valid, k)
         a = assignments.reshape(-1, k)
         scale = weights.reshape(-1, k).astype(np.float64)
         take = ok[:, None] & (a >= 0)
@@ -212,14 +216,16 @@ def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray,
         np.add.at(update, rows, y * scale[rows, slots][:, None])
     mixed = rms(flat + update, p["expert_norm"])
     out = np.where(ok[:, None], mixed, flat).reshape(b, length, d)
-    return out, assignments
+    return out, assignments, statistics
 
 
 def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context: np.ndarray | None = None, *,
-                 return_assignments: bool = False):
+                 return_assignments: bool = False, return_statistics: bool = False):
     """One forward_window of one block. Returns (logits, final_context,
-    next_state, surprise, admission), and the expert assignments [B, L, k]
-    as a sixth item with ``return_assignments``."""
+    next_state, surprise, admission), the expert assignments [B, L, k] as a
+    further item with ``return_assignments``, and the learned gate's router
+    statistics (``oracle.router_statistics``; None for hash routing) as the
+    last item with ``return_statistics``."""
 
     f = lambda name: np.asarray(p[name], np.float64)
     ids = np.asarray(ids, np.int64)
@@ -263,7 +269,7 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
                        f("fusion_b")), f("fusion_norm"))
     previous = oracle.previous_token_ids(ids, valid, state["last_token"])
     names = ("gate_w", "gate_b", "up_w", "up_b", "down_w", "down_b", "expert_norm", "router_w")
-    final, assignments = experts({k: f(k) for k in names if k in p}, fused, ids, previous, valid, cfg)
+    final, assignments, statistics = experts({k: f(k) for k in names if k in p}, fused, ids, previous, valid, cfg)
     logits = linear(final, f("head_w"), f("head_b"))
 
     w = cfg["local_memory_size"]
@@ -286,9 +292,12 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
         "salient_valid": np.asarray(sok, bool),
         "last_token": last,
     }
+    out = (logits, final, next_state, surprise, admission)
     if return_assignments:
-        return logits, final, next_state, surprise, admission, assignments
-    return logits, final, next_state, surprise, admission
+        out += (assignments,)
+    if return_statistics:
+        out += (statistics,)
+    return out
 
 
 def stack_window(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict):

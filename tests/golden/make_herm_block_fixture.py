@@ -12,7 +12,8 @@ token head by 8 so that surprise spreads around the admission threshold, and
 runs three windows from ``KoemiState.create_static``: 11 tokens, 11 more
 (state carried, both with padding inside), then one decode position. The
 weights, ids and every output (logits, surprise, admission, expert
-assignments, each next state field) go to ``herm_block_<routing>.npz`` beside
+assignments, each next state field and, for learned routing, the window's
+RouterStatistics with its balance loss) go to ``herm_block_<routing>.npz`` beside
 this script, once with hash routing and once with learned routing. Only data
 is written; nothing from the reference is copied. The GPU box never runs this.
 
@@ -77,6 +78,12 @@ def make(routing: str) -> dict[str, np.ndarray]:
                                     else result.expert_indices.unsqueeze(-1)).numpy()
         for field in KOEMI_STATE_FIELDS:
             out[f"w{w}.state_out.{field}"] = getattr(result.state, field).detach().numpy().copy()
+        stats = result.router_statistics
+        if stats is not None:  # learned routing: RouterStatistics of the window (router.py:50-58)
+            out[f"w{w}.router.probability_mass"] = stats.probability_mass.detach().numpy().copy()
+            out[f"w{w}.router.assignment_counts"] = stats.assignment_counts.detach().numpy().copy()
+            out[f"w{w}.router.valid_count"] = stats.valid_count.detach().numpy().copy()
+            out[f"w{w}.router.balance_loss"] = stats.balance_loss.detach().numpy().copy()
         state = result.state
     return out
 

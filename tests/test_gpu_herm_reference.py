@@ -42,9 +42,21 @@ def test_gpu_block_window_matches_reference_fixture(device, routing):
         state = {k: (v.float() if v.is_floating_point() else v).to(device).contiguous()
                  for k, v in checkpoint.state_from_fields(fields).items()}
         ids = torch.from_numpy(data[f"w{w}.ids"]).to(device)
-        logits, _, nxt, surprise = herm.block_window(params[0], settings, ids, state)
+        routing_out: dict = {}
+        logits, _, nxt, surprise = herm.block_window(params[0], settings, ids, state, routing=routing_out)
         torch.cuda.synchronize()
         close(logits.cpu().numpy(), data[f"w{w}.logits"], 1e-4)
+        if routing == "learned":
+            # the window's RouterStatistics (router.py:50-58): fp32 sums over fp32
+            # probabilities; counts and the valid count exact
+            (stats,) = routing_out["statistics"]
+            close(stats.probability_mass.cpu().numpy(), data[f"w{w}.router.probability_mass"], 1e-4)
+            np.testing.assert_array_equal(stats.assignment_counts.cpu().numpy(),
+                                          data[f"w{w}.router.assignment_counts"])
+            assert float(stats.valid_count) == float(data[f"w{w}.router.valid_count"])
+            close(stats.balance_loss.cpu().numpy(), data[f"w{w}.router.balance_loss"], 1e-4)
+        else:
+            assert "statistics" not in routing_out
         close(surprise.cpu().numpy(), data[f"w{w}.surprise"], 1e-4)
         want = checkpoint.state_from_fields({n: data[f"w{w}.state_out.{n}"] for n in FIELDS})
         for key, value in want.items():

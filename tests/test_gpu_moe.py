@@ -110,6 +110,87 @@ def test_config4_learned_route_bit_exact(device):
     np.testing.assert_allclose(w.cpu().numpy()[v], ref_w.numpy()[v], rtol=1e-6)
 
 
+def _check_router_statistics(stats, want, tokens):
+    """RouterStatistics on the device against the float64 oracle. The mass is
+    an fp32 sum of positive terms, 256 tokens per workgroup in order, then
+    the workgroups in order, each term within 4 ulp (fixed exp, one division):
+    relative error <= (256 + workgroups + 4) * 2^-24 per expert; counts and the
+    valid count are exact integers; the loss adds its own fp32 steps."""
+    u = 2.0 ** -24
+    rel = (256 + (tokens + 255) // 256 + 4) * u
+    mass = stats.probability_mass.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(mass - want["probability_mass"]) <= rel * want["probability_mass"] + 1e-30), \
+        f"mass err {np.abs(mass - want['probability_mass']).max():.3e}"
+    np.testing.assert_array_equal(stats.assignment_counts.cpu().numpy(), want["assignment_counts"])
+    assert float(stats.valid_count) == want["valid_count"]
+    assert stats.valid_count.shape == () and stats.balance_loss.shape == ()
+    loss = float(stats.balance_loss)
+    E = mass.size
+    assert abs(loss - want["balance_loss"]) <= (rel + (2 * E + 8) * u) * max(want["balance_loss"], 1e-30), \
+        f"loss {loss!r} vs {want['balance_loss']!r}"
+
+
+def test_config4_router_statistics(device):
+    """LearnedExpertMixture.forward's statistics at C4 (router.py:50-58): the
+    route's bits equal the plain learned route's, the statistics match the
+    float64 oracle, and the balance loss formed by the standalone kernel from
+    the same statistics equals the fused one bit for bit."""
+    c = workloads.config4()
+    valid = c.valid.clone()
+    valid[::97] = False
+    logits = c.router_logits.to(device)
+    idx, w, stats = moe.route_topk_learned(logits, valid.to(device), top_k=2, return_statistics=True)
+    idx0, w0 = moe.route_topk_learned(logits, valid.to(device), top_k=2)
+    assert torch.equal(idx, idx0) and torch.equal(w, w0)
+    want = oracle.router_statistics(c.router_logits.numpy(), valid.numpy(), idx.cpu().numpy())
+    _check_router_statistics(stats, want, c.router_logits.shape[0])
+    again = moe.RouterStatistics(stats.probability_mass, stats.assignment_counts, stats.valid_count)
+    assert torch.equal(again.balance_loss, stats.balance_loss)
+    # deterministic: a second call gives the same bits
+    _, _, stats2 = moe.route_topk_learned(logits, valid.to(device), top_k=2, return_statistics=True)
+    assert torch.equal(stats2.probability_mass, stats.probability_mass)
+
+
+@pytest.mark.parametrize("tokens, experts, k", [(1000, 100, 3), (257, 4, 2), (5, 1024, 8), (3000, 16, 1)])
+def test_router_statistics_shapes(device, tokens, experts, k):
+    """A last workgroup of a few tokens, experts beyond one 64-expert chunk
+    (100: two chunks, 1024: sixteen), k from 1 to 8, a fifth of the tokens
+    invalid."""
+    g = torch.Generator().manual_seed(tokens + experts)
+    logits = 2.0 * torch.randn((tokens, experts), generator=g)
+    valid = torch.rand((tokens,), generator=g) > 0.2
+    idx, w, stats = moe.route_topk_learned(logits.to(device), valid.to(device), top_k=k, return_statistics=True)
+    want_idx, want_w = oracle.route_learned(logits.numpy(), valid.numpy(), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_idx)
+    np.testing.assert_array_equal(w.cpu().numpy(), want_w)
+    _check_router_statistics(stats, oracle.router_statistics(logits.numpy(), valid.numpy(), want_idx), tokens)
+
+
+def test_router_statistics_empty_and_merged(device):
+    """An empty mask gives zero statistics and a zero loss
+    (test_learned_router.py:82-87); no tokens at all as well; statistics of
+    two halves merged (router.py:25-32) match the oracle's merge, their loss
+    formed on the device."""
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn((600, 16), generator=g)
+    none = torch.zeros((600,), dtype=torch.bool)
+    _, _, stats = moe.route_topk_learned(logits.to(device), none.to(device), top_k=2, return_statistics=True)
+    assert float(stats.valid_count) == 0 and float(stats.balance_loss) == 0.0
+    assert not stats.probability_mass.any() and not stats.assignment_counts.any()
+    idx, _, stats = moe.route_topk_learned(logits[:0].to(device), none[:0].to(device), top_k=2,
+                                           return_statistics=True)
+    assert idx.shape == (0, 2) and float(stats.valid_count) == 0 and float(stats.balance_loss) == 0.0
+    valid = torch.rand((600,), generator=g) > 0.3
+    halves = [moe.route_topk_learned(logits[s].to(device), valid[s].to(device), top_k=2, return_statistics=True)
+              for s in (slice(0, 300), slice(300, 600))]
+    merged = moe.merge_router_statistics([h[2] for h in halves])
+    want = oracle.merge_router_statistics([
+        oracle.router_statistics(logits[s].numpy(), valid[s].numpy(), h[0].cpu().numpy())
+        for s, h in zip((slice(0, 300), slice(300, 600)), halves)])
+    _check_router_statistics(merged, want, 600)
+    assert moe.merge_router_statistics([]) is None
+
+
 # ----------------------------------------------------------------- permute
 
 

@@ -25,6 +25,13 @@ wrong sign, swapped operand, wrong rounding order) fails at least one:
   properties of test_dispatch.py:50-108; uint32-vs-int64 closed form (E power
   of two agrees, E = 6 does not).
 * learned route: torch softmax + topk indices, weights to 1e-6; exact ties.
+* router statistics / balance loss: the reference's own forward_window
+  statistics (tests/test_oracle_reference_block.py); closed forms (uniform
+  gate with balanced counts -> loss 1; all mass and every assignment on one
+  expert -> loss E; an empty mask -> loss 0, test_learned_router.py:82-87);
+  invariants (the mass sums to the valid count, the counts to k x valid,
+  test_learned_router.py:34); a brute-force Python loop over tokens; merging
+  two halves equals the statistics of the whole.
 * permute: the stable-pairs KAT and torch.argsort(stable=True) on random data.
 * grouped_mlp / combine: torch per-row loops of test_moe_cuda.py:79-113.
 """
@@ -500,6 +507,70 @@ def test_learned_route_ties_go_to_the_lower_index():
     logits[0, [2, 5, 6]] = 1.0
     idx, w = oracle.route_learned(logits, np.ones(1, bool), 3)
     assert idx[0].tolist() == [2, 5, 6] and w[0, 0] == w[0, 1] == w[0, 2]
+
+
+def _router_loop(logits, valid, assignments):
+    """RouterStatistics by a plain loop over tokens (router.py:50-58)."""
+    T, E = logits.shape
+    mass, counts, n = [0.0] * E, [0.0] * E, 0
+    for t in range(T):
+        if not valid[t]:
+            continue
+        n += 1
+        z = [float(x) for x in logits[t]]
+        top = max(z)
+        ex = [math.exp(x - top) for x in z]
+        total = sum(ex)
+        for e in range(E):
+            mass[e] += ex[e] / total
+        for e in assignments[t]:
+            counts[int(e)] += 1.0
+    loss = E * sum((mass[e] / max(n, 1)) * (counts[e] / max(sum(counts), 1.0)) for e in range(E))
+    return mass, counts, n, loss
+
+
+def test_router_statistics_brute_force_and_invariants():
+    g = torch.Generator().manual_seed(43)
+    logits = (2.0 * torch.randn((300, 6), generator=g)).numpy()
+    valid = (torch.rand((300,), generator=g) > 0.2).numpy()
+    idx, _ = oracle.route_learned(logits, valid, 2)
+    stats = oracle.router_statistics(logits, valid, idx)
+    mass, counts, n, loss = _router_loop(logits, valid, idx)
+    np.testing.assert_allclose(stats["probability_mass"], mass, rtol=1e-12)
+    np.testing.assert_array_equal(stats["assignment_counts"], counts)
+    assert stats["valid_count"] == n == valid.sum()
+    assert abs(stats["balance_loss"] - loss) <= 1e-12 * loss
+    assert abs(stats["probability_mass"].sum() - n) <= 1e-9 * n
+    assert stats["assignment_counts"].sum() == 2 * n
+    # merging the two halves gives the statistics of the whole (router.py:25-32)
+    halves = [oracle.router_statistics(logits[s], valid[s], idx[s]) for s in (slice(0, 150), slice(150, 300))]
+    merged = oracle.merge_router_statistics(halves)
+    np.testing.assert_allclose(merged["probability_mass"], stats["probability_mass"], rtol=1e-12)
+    np.testing.assert_array_equal(merged["assignment_counts"], stats["assignment_counts"])
+    assert merged["valid_count"] == stats["valid_count"]
+    assert abs(merged["balance_loss"] - stats["balance_loss"]) <= 1e-12
+    assert oracle.merge_router_statistics([]) is None
+
+
+def test_router_statistics_closed_forms():
+    # uniform gate, every expert taken equally often: importance = load = 1/E -> loss 1
+    E, k = 8, 2
+    logits = np.zeros((64, E), np.float32)
+    valid = np.ones(64, bool)
+    balanced = np.stack([np.arange(64) % E, (np.arange(64) + 1) % E], axis=1)
+    stats = oracle.router_statistics(logits, valid, balanced)
+    assert abs(stats["balance_loss"] - 1.0) < 1e-12
+    np.testing.assert_allclose(stats["probability_mass"], np.full(E, 64 / E), rtol=1e-12)
+    # every token certain of expert 3 and routed there alone: importance_3 = load_3 = 1 -> loss E
+    peaked = np.full((32, E), -1e4, np.float32)
+    peaked[:, 3] = 0.0
+    stats = oracle.router_statistics(peaked, np.ones(32, bool), np.full((32, 1), 3))
+    assert abs(stats["balance_loss"] - E) < 1e-9
+    # an empty mask: zero statistics and zero loss (test_learned_router.py:82-87)
+    empty = oracle.router_statistics(np.random.default_rng(0).normal(size=(10, 4)).astype(np.float32),
+                                     np.zeros(10, bool), np.full((10, 2), -1))
+    assert empty["valid_count"] == 0 and empty["balance_loss"] == 0.0
+    assert not empty["probability_mass"].any() and not empty["assignment_counts"].any()
 
 
 def test_permute_known_answer():

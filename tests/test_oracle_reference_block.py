@@ -86,9 +86,18 @@ def test_block_window_matches_reference_fixture(routing):
                 else:
                     close(state[key], carried[key], tol(key))
             state = carried
-        logits, final, nxt, surprise, admission, assign = herm.block_window(p, state, data[f"w{w}.ids"], cfg,
-                                                                            return_assignments=True)
+        logits, final, nxt, surprise, admission, assign, stats = herm.block_window(
+            p, state, data[f"w{w}.ids"], cfg, return_assignments=True, return_statistics=True)
         close(logits, data[f"w{w}.logits"], memory_fed)
+        if routing == "learned":
+            # RouterStatistics (router.py:50-58): the reference's are fp32 sums of
+            # fp32 probabilities; counts and the valid count are exact
+            close(stats["probability_mass"], data[f"w{w}.router.probability_mass"], 1e-6)
+            np.testing.assert_array_equal(stats["assignment_counts"], data[f"w{w}.router.assignment_counts"])
+            assert stats["valid_count"] == float(data[f"w{w}.router.valid_count"])
+            close(stats["balance_loss"], data[f"w{w}.router.balance_loss"], 1e-6)
+        else:
+            assert stats is None
         close(surprise, data[f"w{w}.surprise"], fine)
         np.testing.assert_array_equal(admission, data[f"w{w}.admission"])
         np.testing.assert_array_equal(assign, data[f"w{w}.assignments"])
@@ -115,6 +124,11 @@ def test_fixture_exercises_the_block():
         assert data["w1.state_in.salient_valid"].any() and data["w1.state_in.local_valid"].any()
         assert (data["w0.ids"] == herm.PAD).any() and (data["w1.ids"] == herm.PAD).any()
         assert (data["w0.assignments"] >= 0).any() and (data["w0.assignments"] == -1).any()
+    learned = load("learned")
+    for w in range(3):  # statistics with padding excluded (windows 0 and 1 hold padding)
+        if w < 2:
+            assert float(learned[f"w{w}.router.valid_count"]) < learned[f"w{w}.ids"].size
+        assert learned[f"w{w}.router.assignment_counts"].sum() == 2 * float(learned[f"w{w}.router.valid_count"])
 
 
 def test_layout_map_roundtrip_and_errors():
