@@ -1063,12 +1063,15 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
 
 
 def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
-                   states: list[dict[str, Tensor]]) -> tuple[Tensor, list[dict[str, Tensor]]]:
+                   states: list[dict[str, Tensor]], surprise_out: list[Tensor] | None = None
+                   ) -> tuple[Tensor, list[dict[str, Tensor]]]:
     """``prefill`` computed layer by layer with ``block_sequence``: each layer
     over the whole sequence before the next. The token context (validity,
     previous tokens, surprise targets) is formed once for all layers: every
     layer sees the same ids and carries the same last token. Returns the last
-    layer's logits of every position and the next states."""
+    layer's logits of every position and the next states; ``surprise_out``
+    (a list) receives every layer's surprise [B, L] (the admission mask is
+    ``valid & (surprise > threshold)``, network.py:349)."""
 
     ids = ids.contiguous()
     token_context = _token_context(ids, None, states[0]["last_token"])
@@ -1078,11 +1081,12 @@ def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids:
     routing: dict = {}  # the hash route, formed by the first layer for all of them
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
-        logits, context, next_state, _ = block_sequence(p, settings, ids, state, context, with_logits=last,
-                                                        token_context=token_context,
-                                                        next_norm=None if last else params[layer + 1]["input_norm"],
-                                                        routing=routing)
+        logits, context, next_state, surprise = block_sequence(
+            p, settings, ids, state, context, with_logits=last, token_context=token_context,
+            next_norm=None if last else params[layer + 1]["input_norm"], routing=routing)
         next_states.append(next_state)
+        if surprise_out is not None:
+            surprise_out.append(surprise)
     return logits, next_states
 
 
@@ -1094,7 +1098,8 @@ class SequencePrefill:
     (``self.states``) into buffers of its own, so a replay needs no copies:
     ``run(ids=None, states=None)`` copies in only what is given (ids other
     than the static ids buffer; starting states, which then stay the start
-    of later runs), replays, and returns the logits buffer. Two eager passes
+    of later runs), replays, and returns the logits buffer; ``self.surprise``
+    holds every layer's surprise of the last replay. Two eager passes
     on throwaway copies warm the libraries up before the capture. The fused
     gate kernel reports a timed-out wait into ``self.status`` (NaN states,
     never silently wrong ones): ``check()`` raises if that happened in any
@@ -1115,8 +1120,9 @@ class SequencePrefill:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.graph = torch.cuda.CUDAGraph()
+        self.surprise: list[Tensor] = []
         with torch.cuda.graph(self.graph):
-            self.logits, self.states = stack_sequence(params, settings, self.ids, self.start)
+            self.logits, self.states = stack_sequence(params, settings, self.ids, self.start, self.surprise)
 
     def run(self, ids: Tensor | None = None, states: list[dict[str, Tensor]] | None = None) -> Tensor:
         if ids is not None and ids.data_ptr() != self.ids.data_ptr():

@@ -220,12 +220,17 @@ def experts(p: dict, context: np.ndarray, ids: np.ndarray, previous: np.ndarray,
 
 
 def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context: np.ndarray | None = None, *,
-                 return_assignments: bool = False, return_statistics: bool = False):
+                 return_assignments: bool = False, return_statistics: bool = False,
+                 admission_in: np.ndarray | None = None):
     """One forward_window of one block. Returns (logits, final_context,
     next_state, surprise, admission), the expert assignments [B, L, k] as a
     further item with ``return_assignments``, and the learned gate's router
     statistics (``oracle.router_statistics``; None for hash routing) as the
-    last item with ``return_statistics``."""
+    last item with ``return_statistics``. ``admission_in`` ([B, L] bool, or
+    None) replaces the admission decision ``valid & (surprise > threshold)``
+    (network.py:349), so that a checker can follow another implementation's
+    decision for scores that lie within rounding distance of the threshold;
+    the returned admission is then ``admission_in``."""
 
     f = lambda name: np.asarray(p[name], np.float64)
     ids = np.asarray(ids, np.int64)
@@ -263,6 +268,8 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
                                                     log_dtype=cfg.get("memory_log_dtype", np.float32))
 
     admission = valid & (surprise > cfg["salience_threshold"])
+    if admission_in is not None:
+        admission = np.asarray(admission_in, bool).reshape(admission.shape)
     salient_value = oracle.read_salient_window(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                local_keys, local_values, admission, ws)
     fused = rms(linear(np.concatenate([ws, fast, local_value, salient_value], axis=-1), f("fusion_w"),
@@ -300,25 +307,45 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
     return out
 
 
-def stack_window(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict):
+def stack_window(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict,
+                 admissions: list[np.ndarray] | None = None, *, return_admissions: bool = False):
     """One window through every layer (the composition in the module docstring).
-    Returns (last layer's logits, next states, per-layer surprise)."""
+    Returns (last layer's logits, next states, per-layer surprise), and the
+    per-layer admission masks with ``return_admissions``. ``admissions``: per
+    layer the ``admission_in`` of ``block_window`` (or None)."""
 
     context = None
-    next_states, surprises = [], []
+    next_states, surprises, admitted = [], [], []
     logits = None
-    for p, st in zip(params, states):
-        logits, context, nst, surprise, _ = block_window(p, st, ids, cfg, context)
+    for layer, (p, st) in enumerate(zip(params, states)):
+        forced = None if admissions is None else admissions[layer]
+        logits, context, nst, surprise, admission = block_window(p, st, ids, cfg, context, admission_in=forced)
         next_states.append(nst)
         surprises.append(surprise)
+        admitted.append(admission)
+    if return_admissions:
+        return logits, next_states, surprises, admitted
     return logits, next_states, surprises
 
 
-def prefill(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict, window: int):
-    """forward_parallel (network.py:176-197): the sequence in windows of `window`, state carried."""
+def prefill(params: list[dict], states: list[dict], ids: np.ndarray, cfg: dict, window: int,
+            admissions: list[np.ndarray] | None = None, *, return_layers: bool = False):
+    """forward_parallel (network.py:176-197): the sequence in windows of `window`, state carried.
+    Returns (logits, final states), and with ``return_layers`` also every
+    layer's surprise and admission over the whole sequence ([B, L] each).
+    ``admissions``: per layer a [B, L] mask replacing the admission decision
+    (``block_window``'s ``admission_in``), or None."""
 
-    pieces = []
+    pieces, surprise, admitted = [], [], []
     for start in range(0, ids.shape[1], window):
-        logits, states, _ = stack_window(params, states, ids[:, start:start + window], cfg)
+        forced = None if admissions is None else [a[:, start:start + window] for a in admissions]
+        logits, states, s, a = stack_window(params, states, ids[:, start:start + window], cfg, forced,
+                                            return_admissions=True)
         pieces.append(logits)
-    return np.concatenate(pieces, axis=1), states
+        surprise.append(s)
+        admitted.append(a)
+    logits = np.concatenate(pieces, axis=1)
+    if not return_layers:
+        return logits, states
+    per_layer = lambda parts: [np.concatenate([w[layer] for w in parts], axis=1) for layer in range(len(params))]
+    return logits, states, per_layer(surprise), per_layer(admitted)
