@@ -565,6 +565,66 @@ def grouped_mlp(sorted_context: np.ndarray, sorted_experts: np.ndarray, offsets:
     return out
 
 
+def round_bf16_f64(x: np.ndarray) -> np.ndarray:
+    """float64 values rounded to the nearest bfloat16 (8 significant bits,
+    ties to even), kept in float64; one rounding, no detour through float32."""
+
+    m, ex = np.frexp(np.asarray(x, np.float64))
+    return np.ldexp(np.round(np.ldexp(m, 8)), ex - 8)
+
+
+def grouped_mlp_bound(sorted_context: np.ndarray, offsets: np.ndarray, gate_w, gate_b, value_w, value_b, out_w,
+                      out_b) -> tuple[np.ndarray, np.ndarray]:
+    """The bf16 grouped GLU FFN (moe_kernels.cu:147-199 contract) in float64
+    with the hidden activations stored as bf16 (one rounding), and for every
+    output the error a bf16-operand, fp32-accumulating implementation is
+    allowed against it. Returns (y [P, D] float64, bound [P, D]); rows past
+    offsets[-1] are zero with bound 0.
+
+    bound = ulp(y) / 2 + 2^-7 sqrt(sum_k (h_k W_o[j, k])^2)
+            + 4 sqrt(H) 2^-24 (sum_k |h_k W_o[j, k]| + |b_o[j]|)
+
+    * ulp(y) / 2: the output's rounding to bf16 (ulp of bf16 at |y|);
+    * the hidden term: a stored hidden value may round to the neighbouring
+      bf16 value where the implementation's fp32 sums of the first GEMM land
+      on the other side of a rounding boundary, a change of at most one bf16
+      ulp (2^-7 |h_k|); such changes have independent signs, so their effect
+      on an output is bounded by the root of the sum of squares (if every
+      hidden value moved by a full ulp), not by the sum;
+    * the accumulation term: the second GEMM's fp32 sum over H terms in any
+      order, Higham's sqrt(n) rounding-error model with a factor of 4.
+
+    A worst-case bound (gamma_n = n u for both GEMMs and every hidden value
+    that could round either way taken at its full ulp in the same direction)
+    is above 0.19 |y| at C4, which checks nothing. The largest ratio of
+    |y_gpu - y| to this bound measured at C4 (65,536 pairs x 1024 outputs)
+    is 0.33."""
+
+    u = 2.0 ** -24
+    x = np.asarray(sorted_context, np.float64)
+    D = np.asarray(out_w).shape[1]
+    y = np.zeros((x.shape[0], D), np.float64)
+    bound = np.zeros_like(y)
+    off = np.asarray(offsets, np.int64)
+    for e in range(off.shape[0] - 1):
+        lo, hi = int(off[e]), int(off[e + 1])
+        if hi <= lo:
+            continue
+        xe = x[lo:hi]
+        wg, wv, wo = (np.asarray(w[e], np.float64) for w in (gate_w, value_w, out_w))
+        bg, bv, bo = (np.asarray(b[e], np.float64) for b in (gate_b, value_b, out_b))
+        g = xe @ wg.T + bg
+        v = xe @ wv.T + bv
+        hb = round_bf16_f64(g / (1.0 + np.exp(-g)) * v)
+        ye = hb @ wo.T + bo
+        rms = np.sqrt((hb * hb).astype(np.float32) @ (wo * wo).T.astype(np.float32))
+        s2 = np.abs(hb).astype(np.float32) @ np.abs(wo).T.astype(np.float32) + np.abs(bo)
+        _, ex = np.frexp(ye)
+        y[lo:hi] = ye
+        bound[lo:hi] = np.ldexp(1.0, ex - 9) + 2.0 ** -7 * rms + 4.0 * math.sqrt(hb.shape[1]) * u * s2
+    return y, bound
+
+
 def combine(expert_outputs: np.ndarray, sorted_rows: np.ndarray, offsets: np.ndarray, token_count: int,
             top_k: int, pair_weights: np.ndarray | None = None) -> np.ndarray:
     """combine_topk (moe_kernels.cu:201-229; router.py:73): out[t] = sum over valid

@@ -363,18 +363,26 @@ def run_config4_pipeline(device, c, learned: bool):
 
 @pytest.mark.parametrize("learned", [False, True])
 def test_config4_pipeline(device, learned):
+    """C4 end to end. The grouped GLU FFN is checked on every one of the
+    65,536 pair rows (all 1024 outputs) against the float64 oracle with bf16
+    hidden activations, within oracle.grouped_mlp_bound's per-output bound
+    (half an output ulp + one hidden-value ulp of independent sign per term +
+    an fp32 accumulation term over K = 2816; its docstring gives the model);
+    the rows past the valid pairs are zero."""
     c = workloads.config4()
     sc, rows, experts, offsets, sw, y, out = run_config4_pipeline(device, c, learned)
     off = offsets.cpu().numpy()
-    # sampled rows of the expert outputs against the oracle (fp32 numpy matmul)
-    sample = np.concatenate([np.arange(off[e], min(off[e] + 96, off[e + 1])) for e in range(16)])
-    sample = np.concatenate([sample, np.arange(max(0, off[-1] - 64), off[-1])])
-    x = sc.float().cpu().numpy()[sample]
-    sub_experts = experts.cpu().numpy()[sample]
-    sub_offsets = np.concatenate([[0], np.cumsum(np.bincount(sub_experts, minlength=16)[:16])])
     ws = [t.float().numpy() for t in (c.gate_weights, c.gate_biases, c.value_weights, c.value_biases, c.output_weights, c.output_biases)]
-    want = oracle.grouped_mlp(x, sub_experts, sub_offsets, *ws, dtype=np.float32, round_hidden_bf16=True)
-    check_bf16_mlp(y[torch.from_numpy(sample).to(device)], want, f"C4 grouped MLP ({'learned' if learned else 'hash'})")
+    want, bound = oracle.grouped_mlp_bound(sc.float().cpu().numpy(), off, *ws)
+    got = y.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - want)
+    _, ex = np.frexp(want)
+    half_ulp = np.ldexp(1.0, ex - 9)
+    name = f"C4 grouped MLP ({'learned' if learned else 'hash'})"
+    print(f"{name}: all {got.shape[0]} rows: max err {err.max():.3e}, max err / bound {(err / bound).max():.3f}, "
+          f"share above half an ulp {(err > half_ulp).mean():.2e}", flush=True)
+    assert np.all(err <= bound), f"{name}: {int((err > bound).sum())} outputs beyond the bound"
+    assert not got[int(off[-1]):].any()
     # combine bit-exact against the oracle on the kernel's own expert outputs
     want_out = oracle.combine(y.float().cpu().numpy(), rows.cpu().numpy(), off, c.context.shape[0], 2,
                               None if sw is None else sw.cpu().numpy())

@@ -34,6 +34,11 @@ wrong sign, swapped operand, wrong rounding order) fails at least one:
   two halves equals the statistics of the whole.
 * permute: the stable-pairs KAT and torch.argsort(stable=True) on random data.
 * grouped_mlp / combine: torch per-row loops of test_moe_cuda.py:79-113.
+* grouped_mlp_bound: its values equal grouped_mlp's with bf16 hidden values;
+  a torch fp32 implementation with bf16 operands (another summation order)
+  stays inside the bound; a dropped output bias or swapped gate and value
+  projections fall outside it; round_bf16_f64 equals torch's float32 ->
+  bfloat16 rounding on float32 inputs.
 """
 
 from __future__ import annotations
@@ -635,3 +640,43 @@ def test_grouped_mlp_and_combine_match_the_reference_loops():
     for pair in range(8):
         expected[sorted_rows[pair]] += y[pair] / 2.0
     np.testing.assert_array_equal(combined, expected.numpy())
+
+
+def test_grouped_mlp_bound_accepts_fp32_and_rejects_slips():
+    g = torch.Generator().manual_seed(71)
+    E, D, H, P = 3, 128, 256, 300
+    sizes = [100, 0, 200]
+    off = np.concatenate([[0], np.cumsum(sizes)])
+    bf = lambda *shape, s=1.0: (s * torch.randn(shape, generator=g)).to(torch.bfloat16).float()
+    x = bf(P, D)
+    gw, gb, vw, vb = bf(E, H, D, s=0.05), bf(E, H, s=0.05), bf(E, H, D, s=0.05), bf(E, H, s=0.05)
+    ow, ob = bf(E, D, H, s=0.05), bf(E, D, s=0.05)
+    ws = [t.numpy() for t in (gw, gb, vw, vb, ow, ob)]
+    y, bound = oracle.grouped_mlp_bound(x.numpy(), off, *ws)
+    want = oracle.grouped_mlp(x.numpy(), np.repeat(np.arange(E), sizes), off, *ws, round_hidden_bf16=True)
+    assert np.abs(y - want).max() <= 1e-2 * np.abs(want).max() * 2.0 ** -7  # double rounding of a few h only
+
+    def fp32_impl(gate_w, value_w, out_b):
+        out = torch.zeros((P, D))
+        for e in range(E):
+            lo, hi = int(off[e]), int(off[e + 1])
+            xe = x[lo:hi]
+            hg = xe @ gate_w[e].T + gb[e]
+            hv = xe @ value_w[e].T + vb[e]
+            h = (torch.nn.functional.silu(hg) * hv).to(torch.bfloat16).float()
+            out[lo:hi] = (h.flip(1) @ ow[e].flip(1).T + out_b[e]).to(torch.bfloat16).float()
+        return out.double().numpy()
+
+    assert np.all(np.abs(fp32_impl(gw, vw, ob) - y) <= bound)
+    assert not np.all(np.abs(fp32_impl(gw, vw, torch.zeros_like(ob)) - y) <= bound)
+    assert not np.all(np.abs(fp32_impl(vw, gw, ob) - y) <= bound)
+
+
+def test_round_bf16_f64_is_one_rounding():
+    x = torch.randn(200000, generator=torch.Generator().manual_seed(3)) * 7
+    np.testing.assert_array_equal(oracle.round_bf16_f64(x.double().numpy()),
+                                  x.to(torch.bfloat16).double().numpy())
+    # a float64 value just above a bf16 midpoint rounds up (torch's float64
+    # conversion first rounds to float32, which lands on the midpoint and ties to even)
+    mid = 1.0 + 2.0 ** -8 + 2.0 ** -40
+    assert oracle.round_bf16_f64(np.array([mid]))[0] == 1.0 + 2.0 ** -7
