@@ -26,6 +26,7 @@ other ablations raise.
 
 from __future__ import annotations
 
+import math
 from collections.abc import Mapping
 from pathlib import Path
 
@@ -133,29 +134,91 @@ def block_parameters(model_state: Mapping[str, Tensor], expert_count: int) -> di
     return out
 
 
+# ModelSettings fields (configuration/settings.py:16-32) and their defaults.
+_MODEL_SETTINGS_DEFAULTS = {
+    "vocabulary_size": 257, "embedding_size": 64, "memory_features": 16, "local_memory_size": 16,
+    "salience_memory_size": 16, "salience_threshold": 0.75, "expert_count": 0, "expert_top_k": 1,
+    "expert_dispatch": "loop", "cache_capacity": 256, "scan_chunk": 128, "activation_checkpointing": False,
+    "compile_forward": False, "refine_decay_rate": 0.0625, "ablation": "no_refine", "expert_routing": "hash",
+    "expert_load_balance_weight": 0.01,
+}
+
+
+def _validate_model_settings(v: Mapping) -> None:
+    """The checks of ModelSettings.__post_init__ (configuration/settings.py:
+    34-75), with its messages, so a payload the reference would refuse is
+    refused here too."""
+
+    checks = (
+        (v["vocabulary_size"] < 257, ValueError, "vocabulary_size must cover every byte value and the padding token"),
+        (v["embedding_size"] < 8, ValueError, "embedding_size must be at least 8"),
+        (v["memory_features"] < 2, ValueError, "memory_features must be at least 2"),
+        (v["local_memory_size"] < 1, ValueError, "local_memory_size must be at least 1"),
+        (v["salience_memory_size"] < 1, ValueError, "salience_memory_size must be at least 1"),
+        (not 0.0 <= v["salience_threshold"] <= 1.0, ValueError, "salience_threshold must be between zero and one"),
+        (v["scan_chunk"] < 1, ValueError, "scan_chunk must be at least 1"),
+        (not 0 <= v["expert_count"] <= 128, ValueError, "expert_count must be between 0 and 128"),
+        (v["expert_top_k"] < 1, ValueError, "expert_top_k must be at least 1"),
+        (v["expert_count"] > 0 and v["expert_top_k"] > v["expert_count"], ValueError,
+         "expert_top_k must not exceed expert_count"),
+        (v["expert_dispatch"] not in {"loop", "segments"}, ValueError, "expert_dispatch must be loop or segments"),
+        (v["expert_routing"] not in {"hash", "learned"}, ValueError, "expert_routing must be hash or learned"),
+        (v["expert_routing"] == "learned" and (v["expert_count"] < 1 or v["ablation"] == "affine"), ValueError,
+         "learned routing requires experts and a non-affine ablation"),
+        (not math.isfinite(v["expert_load_balance_weight"]) or v["expert_load_balance_weight"] < 0, ValueError,
+         "expert_load_balance_weight must be finite and non-negative"),
+        (not isinstance(v["activation_checkpointing"], bool), TypeError, "activation_checkpointing must be a boolean"),
+        (not isinstance(v["compile_forward"], bool), TypeError, "compile_forward must be a boolean"),
+        (v["cache_capacity"] < 1, ValueError, "cache_capacity must be at least 1"),
+        (not 0.0 < v["refine_decay_rate"] <= 1.0, ValueError,
+         "refine_decay_rate must be greater than zero and at most one"),
+        (v["ablation"] not in {"herm", "no_refine", "no_surprise", "affine"}, ValueError,
+         "ablation must be herm, no_refine, no_surprise or affine"),
+    )
+    for failed, kind, message in checks:
+        if failed:
+            raise kind(message)
+
+
 def settings_from_model_settings(values: Mapping, *, layers: int = 1, linear_dtype: torch.dtype = torch.float32):
     """``herm.HermSettings`` for a reference ``ModelSettings.to_dict()`` payload
-    (configuration/settings.py:14-32)."""
+    (configuration/settings.py:14-32). Unknown fields raise ``TypeError``
+    (``ModelSettings.from_dict``'s ``cls(**values)``) and the values are checked
+    as ``ModelSettings.__post_init__`` checks them. Fields that do not change
+    this path's arithmetic are validated and then not carried:
+    ``expert_dispatch`` (loop or segment dispatch of the same sums),
+    ``cache_capacity`` (the runtime's token cache), ``activation_checkpointing``
+    and ``compile_forward`` (training and compilation switches),
+    ``refine_decay_rate`` (the refine memory, which the no_refine ablation does
+    not build) and ``expert_load_balance_weight`` (the factor the caller applies
+    to ``moe.RouterStatistics.balance_loss`` for ``router_loss``,
+    network.py:42-46). Only the ``no_refine`` ablation and at least one expert
+    are mapped (``ValueError`` otherwise)."""
 
     from koemi_amd.herm import HermSettings
 
-    ablation = values.get("ablation", "no_refine")
+    unknown = sorted(set(values) - set(_MODEL_SETTINGS_DEFAULTS))
+    if unknown:
+        raise TypeError(f"unknown ModelSettings fields: {unknown}")
+    merged = {**_MODEL_SETTINGS_DEFAULTS, **values}
+    _validate_model_settings(merged)
+    ablation = merged["ablation"]
     if ablation != "no_refine":
         raise ValueError(f"only the no_refine ablation is mapped, not {ablation!r}")
-    routing = values.get("expert_routing", "hash")
-    if routing not in ("hash", "learned"):
-        raise ValueError(f"unknown expert routing {routing!r}")
+    if merged["expert_count"] < 1:
+        raise ValueError("the HERM block is mapped with experts only (expert_count >= 1)")
+    routing = merged["expert_routing"]
     return HermSettings(
-        width=int(values.get("embedding_size", 64)),
-        memory_features=int(values.get("memory_features", 16)),
-        local_memory_size=int(values.get("local_memory_size", 16)),
-        salience_memory_size=int(values.get("salience_memory_size", 16)),
-        salience_threshold=float(values.get("salience_threshold", 0.75)),
-        expert_count=int(values.get("expert_count", 0)),
-        top_k=int(values.get("expert_top_k", 1)),
-        vocabulary_size=int(values.get("vocabulary_size", 257)),
+        width=int(merged["embedding_size"]),
+        memory_features=int(merged["memory_features"]),
+        local_memory_size=int(merged["local_memory_size"]),
+        salience_memory_size=int(merged["salience_memory_size"]),
+        salience_threshold=float(merged["salience_threshold"]),
+        expert_count=int(merged["expert_count"]),
+        top_k=int(merged["expert_top_k"]),
+        vocabulary_size=int(merged["vocabulary_size"]),
         layers=layers,
-        scan_chunk=int(values.get("scan_chunk", 128)),
+        scan_chunk=int(merged["scan_chunk"]),
         linear_dtype=linear_dtype,
         expert_routing=routing,
     )
@@ -175,6 +238,10 @@ def load_reference_checkpoint(path: str | Path, *, linear_dtype: torch.dtype = t
         raise ValueError("checkpoint model settings are invalid")
     if not isinstance(raw.get("model_state"), dict):
         raise ValueError("checkpoint model state is invalid")
+    if raw.get("vocabulary") is not None and not isinstance(raw["vocabulary"], dict):
+        raise ValueError("checkpoint vocabulary payload is invalid")
+    if raw.get("identity") is not None and not isinstance(raw["identity"], dict):
+        raise ValueError("checkpoint identity payload is invalid")
     settings = settings_from_model_settings(raw["model_settings"], linear_dtype=linear_dtype)
     params = block_parameters(raw["model_state"], settings.expert_count)
     if settings.expert_routing == "learned" and "router_w" not in params:

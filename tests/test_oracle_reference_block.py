@@ -169,3 +169,36 @@ def test_reference_checkpoint_loads_weights_only(tmp_path):
         checkpoint.load_reference_checkpoint(path)
     with pytest.raises(ValueError, match="ablation"):
         checkpoint.settings_from_model_settings({**settings, "ablation": "herm"})
+    # CheckpointStore.validate_checkpoint's optional payload types (checkpoints.py:87-92)
+    for key in ("vocabulary", "identity"):
+        torch.save({"format_version": 7, "model_settings": settings, "model_state": model_state, key: [1, 2]}, path)
+        with pytest.raises(ValueError, match=f"{key} payload is invalid"):
+            checkpoint.load_reference_checkpoint(path)
+    torch.save({"format_version": 7, "model_settings": settings, "model_state": model_state,
+                "vocabulary": None, "identity": {"name": "x"}}, path)
+    assert checkpoint.load_reference_checkpoint(path)[0].width == 16
+
+
+@pytest.mark.parametrize("change, kind, message", [
+    ({"expert_top_k": 5}, ValueError, "must not exceed expert_count"),
+    ({"salience_threshold": 1.5}, ValueError, "between zero and one"),
+    ({"embedding_size": 4}, ValueError, "at least 8"),
+    ({"expert_dispatch": "scatter"}, ValueError, "loop or segments"),
+    ({"expert_routing": "learned", "ablation": "affine"}, ValueError, "non-affine"),
+    ({"compile_forward": 1}, TypeError, "boolean"),
+    ({"refine_decay_rate": 0.0}, ValueError, "refine_decay_rate"),
+    ({"expert_load_balance_weight": float("nan")}, ValueError, "finite"),
+    ({"not_a_field": 1}, TypeError, "unknown ModelSettings fields"),
+    ({"expert_count": 0, "expert_top_k": 1}, ValueError, "experts only"),
+])
+def test_model_settings_checks_follow_the_reference(change, kind, message):
+    """ModelSettings.__post_init__ (configuration/settings.py:34-75) refuses
+    these payloads, and so does the settings map (the last two: a field
+    ModelSettings does not have, and a block without experts, which the map
+    does not carry)."""
+    settings = {"vocabulary_size": 257, "embedding_size": 16, "memory_features": 4, "expert_count": 4,
+                "expert_top_k": 2, "ablation": "no_refine", "expert_routing": "hash"}
+    with pytest.raises(kind, match=message):
+        checkpoint.settings_from_model_settings({**settings, **change})
+    ok = checkpoint.settings_from_model_settings({**settings, "expert_dispatch": "segments", "cache_capacity": 8})
+    assert (ok.width, ok.expert_count, ok.top_k, ok.local_memory_size) == (16, 4, 2, 16)
