@@ -105,9 +105,10 @@ struct TileShape {
 // work (stage copies and fragment reads), pinned in place by scheduling
 // barriers, so that they issue while the matrix pipe is busy instead of in a
 // burst that leaves it idle. 256-wide tiles: 16 MFMAs per half step, a copy
-// after every even one and a fragment read after every odd one. 128-wide: 8
-// MFMAs per half step, copy j after MFMA j (six) and fragment j - 2 after MFMA
-// j >= 2.
+// after every fourth one in both halves (eight per step, evenly spaced: the
+// copies of a step land in the stage of tile kt - 1, free for the whole step)
+// and a fragment read after every odd one. 128-wide: 8 MFMAs per half step,
+// copy j after MFMA j (six) and fragment j - 2 after MFMA j >= 2.
 template <int BNT, bool WEIGHTS_FIRST>
 __device__ __forceinline__ void stage_loop(char* lds, const bf16* a_base, const bf16* b_base,
                                            const uint32_t (&a_off)[4], const uint32_t (&b_off)[BNT / 64],
@@ -182,7 +183,9 @@ __device__ __forceinline__ void stage_loop(char* lds, const bf16* a_base, const 
             mfma_one(j, a0, b0);
             if constexpr (NT == 4) {
                 if (j % 2 == 0) {
-                    if constexpr (kCopy) issue_one(kt + kStages - 1, sc, j / 2);
+                    if constexpr (kCopy) {
+                        if (j % 4 == 0) issue_one(kt + kStages - 1, sc, j / 4);
+                    }
                 } else {
                     read_frag(kt, 1, j / 2, a1, b1);
                 }
@@ -199,6 +202,9 @@ __device__ __forceinline__ void stage_loop(char* lds, const bf16* a_base, const 
         for (int j = 0; j < MK; ++j) {
             mfma_one(j, a1, b1);
             if constexpr (NT == 4) {
+                if constexpr (kCopy) {
+                    if (j % 4 == 0) issue_one(kt + kStages - 1, sc, 4 + j / 4);
+                }
                 if (j % 2 == 1) read_frag(kn, 0, j / 2, a0, b0);
             } else {
                 if (j >= 2) read_frag(kn, 0, j - 2, a0, b0);
