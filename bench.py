@@ -115,6 +115,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run each HBM kernel a few times at its config plus a device copy of known size, for "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (prints nothing else)")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="sweep the launch shape of a plain streaming read (koemi_stream_read) over the C2 "
+                         "surprise and RMSNorm-SiLU byte counts, six rotating input sets each, and print the "
+                         "fastest shapes as JSON (the floor the memory-bound C2 kernels are judged against)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn the two --pmc passes over --traffic-probe into profiles/traffic.json")
     return ap.parse_args()
@@ -739,12 +743,72 @@ def decode_rows(herm, params, settings, c5, device, kernels: dict) -> None:
                             "shape": "12 layers, batch 64, 256 greedy steps, PAD masked, one HIP graph per step"}
 
 
+def read_floor() -> int:
+    """The fastest plain read of the C2 surprise input (34,013,184 bytes) and of
+    the C2 RMSNorm-SiLU input (33,554,432 bytes read of its 67 MB) over a
+    sweep of launch shapes (16-byte loads, 1-8 per thread per pass, 256-1024
+    threads per workgroup, 256 workgroups up to one pass over the data), six
+    rotating input sets (204 MB, beyond the 256 MB Infinity Cache's reach for
+    any one set between its uses), timed with HIP events over 120 launches
+    after 12 untimed ones; the median of five such runs per shape."""
+
+    import torch
+
+    from koemi_amd import _native
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    stream = torch.cuda.current_stream(device)
+    lib_stream = _native.stream_of(device)
+    _native.load_library()
+    out: dict = {}
+    for name, nbytes in (("C2.surprise_rows_bytes", 34013184), ("C2.rmsnorm_silu_read_bytes", 33554432)):
+        sets = [torch.empty(nbytes // 4, device=device, dtype=torch.float32).uniform_() for _ in range(6)]
+        sink = torch.empty(2 ** 23, device=device, dtype=torch.float32)
+        results = []
+        n16 = nbytes // 16
+        for unroll in (1, 2, 4, 8):
+            for block in (256, 512, 1024):
+                one_pass = -(-n16 // (block * unroll))
+                for grid in sorted({256, 512, 1024, 2048, 4096, 8192, one_pass}):
+                    if grid > one_pass or grid * block > sink.numel():
+                        continue
+
+                    def run(i, unroll=unroll, block=block, grid=grid):
+                        _native.call("koemi_stream_read", sets[i % 6].data_ptr(), nbytes, unroll, block, grid,
+                                     sink.data_ptr(), lib_stream)
+
+                    for i in range(12):
+                        run(i)
+                    times = []
+                    for _ in range(5):
+                        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        start.record(stream)
+                        for i in range(120):
+                            run(i)
+                        end.record(stream)
+                        end.synchronize()
+                        times.append(start.elapsed_time(end) / 120)
+                    ms = sorted(times)[2]
+                    results.append({"unroll": unroll, "block": block, "grid": grid, "us": round(ms * 1e3, 3),
+                                    "GB/s": round(nbytes / ms / 1e6, 1), "frac_hbm": round(nbytes / ms / 1e6 / 8000, 4)})
+        results.sort(key=lambda r: r["us"])
+        out[name] = {"bytes": nbytes, "best": results, "shapes": len(results),
+                     "one_pass_256x1": next(r for r in results if r["unroll"] == 1 and r["block"] == 256
+                                            and r["grid"] == -(-n16 // 256))}
+        del sets, sink
+    print(json.dumps({"read_floor": out}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_pmc:
         return summarize_pmc(*args.summarize_pmc)
     if args.traffic_probe:
         return traffic_probe()
+    if args.read_floor:
+        return read_floor()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures a single GPU: this build has no multi-GPU path and every box here has one GPU; "

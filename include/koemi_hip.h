@@ -751,6 +751,16 @@ int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_ro
                             int64_t num_segments, float eps, void* workspace, size_t workspace_bytes,
                             koemi_stream_t stream);
 
+/* Measurement only (no counterpart in the reference): reads `bytes` (a
+ * multiple of 16) from `src` with `grid` workgroups of `block` threads, each
+ * thread issuing `unroll` (1, 2, 4 or 8) 16-byte loads per pass of a
+ * grid-stride loop; `sink` (grid * block floats) is written only for a sum
+ * the benchmark never produces. bench.py --read-floor sweeps the launch shape
+ * to find the fastest plain read of a given size on the chip, the floor the
+ * memory-bound kernels are judged against. */
+int koemi_stream_read(const void* src, int64_t bytes, int unroll, int block, int64_t grid, float* sink,
+                      koemi_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,7 @@ SOURCES = (
     "herm_glue.hip",
     "linear_rows.hip",
     "gated_projection.hip",
+    "stream_probe.hip",
 )
 
 ARCH = "gfx950"
