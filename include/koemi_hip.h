@@ -612,6 +612,76 @@ int koemi_assoc_scan_read_windows(const void* projections, int projection_dtype,
                                   int64_t windows, int64_t window, int64_t width, int64_t features, void* workspace,
                                   size_t workspace_bytes, koemi_stream_t stream);
 
+/* The refine memory of the herm ablation (model/network.py:359-384; the write
+ * terms of memory.py:257-268, masked as network.py:733-739; scan_and_read of
+ * memory.py:97-144 over the refine basis and normalizer). The projections and
+ * their column layout are those of koemi_assoc_scan_read (features, query
+ * features, decay and write logits, value pre-activations); per position the
+ * refine terms are decay' = min(1 - (1 - decay) refine_decay_rate, 1 - 2^-16),
+ * weight' = sigmoid(w) clamp(surprise, 0, 1) clamp(novelty, 0, 1) (novelty
+ * [batch, length] fp32, from koemi_local_novelty) and value' =
+ * clamp(tanh(v) - fast_read, -2, 2), fast_read being the position's fast
+ * associative read ([batch, length, width] of fast_dtype F32 or BF16, rows
+ * fast_row_stride apart; 0: width); invalid positions decay 1, weight 0.
+ * Reads go to `read` and the next refine state to next_basis /
+ * next_normalizer as for koemi_assoc_scan_read (a one-position window takes
+ * and writes contiguous fp32). Workspace:
+ * koemi_assoc_refine_scan_read_workspace_bytes (the prepared weights and the
+ * refine values). */
+size_t koemi_assoc_refine_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width, int64_t features);
+int koemi_assoc_refine_scan_read(const void* projections, int projection_dtype, int64_t row_stride,
+                                 int64_t value_offset, int64_t feature_offset, int64_t query_feature_offset,
+                                 int64_t decay_offset, int64_t write_offset, const float* surprise,
+                                 const uint8_t* valid, const float* novelty, float refine_decay_rate,
+                                 const void* fast_read, int fast_dtype, int64_t fast_row_stride, const float* basis,
+                                 const float* normalizer, void* read, int read_dtype, int64_t read_row_stride,
+                                 float* next_basis, float* next_normalizer, int64_t batch, int64_t length,
+                                 int64_t width, int64_t features, void* workspace, size_t workspace_bytes,
+                                 koemi_stream_t stream);
+
+/* koemi_assoc_refine_scan_read over a sequence of windows, as
+ * koemi_assoc_scan_read_windows runs the fast memory (every window's terms,
+ * the carried refine state of each window, every window's reads). */
+size_t koemi_assoc_refine_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window,
+                                                            int64_t width, int64_t features);
+int koemi_assoc_refine_scan_read_windows(const void* projections, int projection_dtype, int64_t row_stride,
+                                         int64_t value_offset, int64_t feature_offset, int64_t query_feature_offset,
+                                         int64_t decay_offset, int64_t write_offset, const float* surprise,
+                                         const uint8_t* valid, const float* novelty, float refine_decay_rate,
+                                         const void* fast_read, int fast_dtype, int64_t fast_row_stride,
+                                         const float* basis, const float* normalizer, void* read, int read_dtype,
+                                         int64_t read_row_stride, float* next_basis, float* next_normalizer,
+                                         int64_t batch, int64_t windows, int64_t window, int64_t width,
+                                         int64_t features, void* workspace, size_t workspace_bytes,
+                                         koemi_stream_t stream);
+
+/* Novelty output of LocalKeyValueMemory.read_window (model/memory.py:354-361)
+ * for `rows` window rows of `length` queries: over the slots of [carried
+ * (capacity) ; window (length)] eligible for query t (valid and among the
+ * `window` positions strictly before its own, memory.py:364-383), the largest
+ * cosine similarity k . q / (max(|k|, 1e-12) max(|q|, 1e-12)); novelty =
+ * clamp(1 - largest, 0, 1), 1 without an eligible slot. carried_keys [rows,
+ * capacity, width] fp32 with carried_valid [rows, capacity]; keys [rows,
+ * length, width] (F32 or BF16, rows key_row_stride apart) with key_valid;
+ * queries fp32 (rows query_row_stride apart); novelty [rows, length] fp32. */
+int koemi_local_novelty(const float* carried_keys, const uint8_t* carried_valid, const void* keys, int key_dtype,
+                        int64_t key_row_stride, const uint8_t* key_valid, const float* queries,
+                        int64_t query_row_stride, float* novelty, int64_t rows, int64_t capacity, int64_t length,
+                        int64_t width, int64_t window, koemi_stream_t stream);
+
+/* The refine gate (KoemiModel.refine_memory, model/network.py:714-721): per
+ * position, pre = W [working; fast; refine; local] + b (weight [4 width], bias
+ * [1] fp32), g = sigmoid(pre), out = fast + g refine. round_bf16 != 0 (a bf16
+ * stack: nn.Linear under bf16 autocast) rounds every input and the weight to
+ * bf16 (weight BF16) and the pre-activation to bf16 after the bias; otherwise
+ * every tensor is F32. working, fast and refine fp32; local F32 or BF16; out
+ * F32 or BF16; every row stride 0 means width. */
+int koemi_herm_refine_gate(const float* working, int64_t working_row_stride, const float* fast,
+                           int64_t fast_row_stride, const float* refine, int64_t refine_row_stride, const void* local,
+                           int local_dtype, int64_t local_row_stride, const void* weight, int weight_dtype,
+                           const float* bias, int round_bf16, void* out, int out_dtype, int64_t out_row_stride,
+                           int64_t rows, int64_t width, koemi_stream_t stream);
+
 /* Small per-window steps of the HERM block (torch composites in the reference).
  * koemi_herm_rmsnorm: out = RootMeanSquareNorm(x + residual) * weight
  * (layers.py:14-16) on rows whose mask byte is set (all rows when mask is

@@ -110,7 +110,7 @@ template <int MAXM, typename PT>
 __global__ __launch_bounds__(256) void assoc_prep_kernel(
     const PT* __restrict__ proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
     int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid, AssocPrep prep, int L,
-    int M) {
+    int M, const float* __restrict__ novelty, float refine_rate) {
     extern __shared__ float sh[];
     float* logd = sh;       // [L]
     float* cum = sh + L;    // [L]
@@ -145,10 +145,17 @@ __global__ __launch_bounds__(256) void assoc_prep_kernel(
             *reinterpret_cast<float4*>(dst + m) = make_float4(z[m] * inv, z[m + 1] * inv, z[m + 2] * inv, z[m + 3] * inv);
         if (!query) {
             const bool ok = valid[b * L + t] != 0;
-            const float decay = kMinDecay + kDecaySpan * sigmoid_f(to_f32(row[decay_off]));
+            float decay = kMinDecay + kDecaySpan * sigmoid_f(to_f32(row[decay_off]));
             const float sv = fminf(fmaxf(surprise[b * L + t], 0.0f), 1.0f);
+            float w = sigmoid_f(to_f32(row[write_off]));
+            if (novelty != nullptr) {  // the refine terms (memory.py:257-268)
+                decay = step::refine_decay(decay, refine_rate);
+                w = w * sv * fminf(fmaxf(novelty[b * L + t], 0.0f), 1.0f);
+            } else {
+                w = w * (0.25f + 0.75f * sv);
+            }
             logd[t] = ok ? logf(decay) : 0.0f;
-            wt[t] = ok ? sigmoid_f(to_f32(row[write_off])) * (0.25f + 0.75f * sv) : 0.0f;
+            wt[t] = ok ? w : 0.0f;
         }
     }
     __syncthreads();
@@ -192,7 +199,7 @@ __global__ __launch_bounds__(256) void assoc_prep_kernel(
 // LDS), normalizer terms sum_s fwt_s kf_s[m] by a wave reduction. FINAL
 // writes the next state e^{c_{L-1}} state + terms (the fmaf the carry kernel
 // applies between windows); otherwise the terms. Grid (rows, ceil(D / 64)).
-template <int MAXM, bool FINAL, typename PT>
+template <int MAXM, bool FINAL, typename PT, bool TANH = true>
 __global__ __launch_bounds__(256) void assoc_delta_kernel(
     const PT* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ next_basis,
@@ -224,7 +231,7 @@ __global__ __launch_bounds__(256) void assoc_delta_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int sl = s + 2 * q + h, slc = min(sl, L - 1);
-            a[q] = sl < s_hi ? fwt[slc] * fast_tanh(x[q]) : 0.0f;
+            a[q] = sl < s_hi ? fwt[slc] * (TANH ? fast_tanh(x[q]) : x[q]) : 0.0f;
             bf[q] = kf[slc * QP + mf] * fon;
         }
 #pragma unroll
@@ -276,7 +283,7 @@ inline size_t read_lds(int64_t L, int64_t M) {
            sizeof(float);
 }
 
-template <int MAXM, typename PT, typename OutT, bool VEC4>
+template <int MAXM, typename PT, typename OutT, bool VEC4, bool TANH = true>
 __global__ __launch_bounds__(256) void assoc_window_read_kernel(
     const PT* __restrict__ proj, int64_t stride, int64_t value_off, AssocPrep prep,
     const float* __restrict__ basis, const float* __restrict__ normalizer, OutT* __restrict__ out, int64_t ostride,
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
             const bool first = s < k_end0;  // wave-uniform
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const float tx = fast_tanh(bc[u].x), ty = fast_tanh(bc[u].y);
+                const float tx = TANH ? fast_tanh(bc[u].x) : bc[u].x, ty = TANH ? fast_tanh(bc[u].y) : bc[u].y;
                 if (first) {
                     const float a0 = s + 2 * u + h < k_end0 ? ia0[s + 2 * u] : 0.0f;
                     acc[0][0] = mfma2(a0, tx, acc[0][0]);
@@ -463,7 +470,7 @@ __global__ __launch_bounds__(256) void assoc_window_read_kernel(
 #pragma unroll
             for (int u = 0; u < 8; ++u) av[u] = s + 2 * u + h < k_end ? ia[s + 2 * u] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc = mfma2(av[u], fast_tanh(bc[u]), acc);
+            for (int u = 0; u < 8; ++u) acc = mfma2(av[u], TANH ? fast_tanh(bc[u]) : bc[u], acc);
         }
 #pragma unroll
         for (int kk = 0; kk < MAXM / 2; ++kk) {
@@ -515,25 +522,25 @@ __global__ __launch_bounds__(256) void assoc_carry_kernel(
 template <int MAXM, typename PT>
 int launch_prep(const PT* proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
                 int64_t write_off, const float* surprise, const uint8_t* valid, const AssocPrep& prep, int64_t rows,
-                int L, int M, hipStream_t s) {
+                int L, int M, hipStream_t s, const float* novelty = nullptr, float refine_rate = 0.0f) {
     hipLaunchKernelGGL((assoc_prep_kernel<MAXM, PT>), dim3(static_cast<unsigned>(rows)), dim3(256),
                        3 * static_cast<size_t>(L) * sizeof(float), s, proj, stride, fk_off, fq_off, decay_off,
-                       write_off, surprise, valid, prep, L, M);
+                       write_off, surprise, valid, prep, L, M, novelty, refine_rate);
     return check_launch("associative memory (prepare)");
 }
 
-template <int MAXM, bool FINAL, typename PT>
+template <int MAXM, bool FINAL, typename PT, bool TANH = true>
 int launch_delta(const PT* proj, int64_t stride, int64_t value_off, const AssocPrep& prep, const float* basis,
                  const float* normalizer, float* nb, float* nn, int64_t rows, int L, int64_t D, int M,
                  hipStream_t s) {
     const size_t lds = (static_cast<size_t>(L) * (MAXM + 2) + 2 * 16 * kWave) * sizeof(float);
-    hipLaunchKernelGGL((assoc_delta_kernel<MAXM, FINAL, PT>), dim3(static_cast<unsigned>(rows),
+    hipLaunchKernelGGL((assoc_delta_kernel<MAXM, FINAL, PT, TANH>), dim3(static_cast<unsigned>(rows),
                        static_cast<unsigned>((D + 63) / 64)), dim3(256), lds, s, proj, stride, value_off, prep, basis,
                        normalizer, nb, nn, L, D, M);
     return check_launch("associative memory (state terms)");
 }
 
-template <int MAXM, typename PT>
+template <int MAXM, typename PT, bool TANH = true>
 int launch_window_read(const PT* proj, int64_t stride, int64_t value_off, const AssocPrep& prep,
                        const float* basis, const float* normalizer, void* out, int out_dtype, int64_t ostride,
                        int64_t rows, int L, int64_t D, int M, hipStream_t s) {
@@ -548,11 +555,11 @@ int launch_window_read(const PT* proj, int64_t stride, int64_t value_off, const 
                            normalizer, o, ostride, L, D, M);
     };
     if (out_dtype == KOEMI_BF16) {
-        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, bf16, true>, static_cast<bf16*>(out));
-        else launch(assoc_window_read_kernel<MAXM, PT, bf16, false>, static_cast<bf16*>(out));
+        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, bf16, true, TANH>, static_cast<bf16*>(out));
+        else launch(assoc_window_read_kernel<MAXM, PT, bf16, false, TANH>, static_cast<bf16*>(out));
     } else {
-        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, float, true>, static_cast<float*>(out));
-        else launch(assoc_window_read_kernel<MAXM, PT, float, false>, static_cast<float*>(out));
+        if (vec4) launch(assoc_window_read_kernel<MAXM, PT, float, true, TANH>, static_cast<float*>(out));
+        else launch(assoc_window_read_kernel<MAXM, PT, float, false, TANH>, static_cast<float*>(out));
     }
     return check_launch("associative memory (reads)");
 }
@@ -567,10 +574,27 @@ __global__ __launch_bounds__(256) void assoc_step_kernel(
     const PT* __restrict__ proj, int64_t stride, int64_t value_off, int64_t fk_off, int64_t fq_off,
     int64_t decay_off, int64_t write_off, const float* __restrict__ surprise, const uint8_t* __restrict__ valid,
     const float* __restrict__ basis, const float* __restrict__ normalizer, float* __restrict__ out,
-    float* __restrict__ next_basis, float* __restrict__ next_normalizer, int64_t D, int M) {
+    float* __restrict__ next_basis, float* __restrict__ next_normalizer, int64_t D, int M,
+    const float* __restrict__ novelty = nullptr, float refine_rate = 0.0f, const float* __restrict__ fast = nullptr) {
     step::assoc_step_body<MAXM, PT>(proj, stride, value_off, fk_off, fq_off, decay_off, write_off, surprise, valid,
                                     basis, normalizer, out, next_basis, next_normalizer, D, M, blockIdx.x,
-                                    static_cast<int>(blockIdx.y));
+                                    static_cast<int>(blockIdx.y), novelty, refine_rate, fast);
+}
+
+// The refine memory's values (memory.py:266-267 with network.py:358): the
+// value tanh(v) of each position (the same fast_tanh as the fast reads)
+// minus the position's fast read, clamped to [-2, 2], as a dense fp32 [rows,
+// D] array the state-terms and read kernels take in place of the projection's
+// value columns (their TANH = false instances).
+template <typename PT, typename FT>
+__global__ __launch_bounds__(256) void refine_error_kernel(const PT* __restrict__ proj, int64_t stride,
+                                                           int64_t value_off, const FT* __restrict__ fast,
+                                                           int64_t fstride, float* __restrict__ err, int64_t rows,
+                                                           int64_t D) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= rows * D) return;
+    const int64_t r = i / D, d = i - r * D;
+    err[i] = step::refine_value(fast_tanh(to_f32(proj[r * stride + value_off + d])), to_f32(fast[r * fstride + d]));
 }
 
 }  // namespace
@@ -679,7 +703,8 @@ extern "C" int koemi_assoc_scan_read(const void* projections, int projection_dty
             auto step = [&](auto kernel) {
                 hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, proj, row_stride, value_offset, feature_offset,
                                    query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer,
-                                   static_cast<float*>(read), next_basis, next_normalizer, width, M);
+                                   static_cast<float*>(read), next_basis, next_normalizer, width, M,
+                                   static_cast<const float*>(nullptr), 0.0f, static_cast<const float*>(nullptr));
             };
             if (M <= 16) step(assoc_step_kernel<16, PT>);
             else step(assoc_step_kernel<32, PT>);
@@ -783,4 +808,227 @@ extern "C" int koemi_assoc_scan_read_windows(const void* projections, int projec
         return launch_window_read<32>(proj, row_stride, value_offset, prep, carried_basis, carried_norm, read,
                                       read_dtype, read_row_stride, rows, L, width, M, s);
     });
+}
+
+// ----------------------------------------------------------- refine memory ---
+// The refine memory of the herm ablation (network.py:359-384): the same
+// projection, features and query features as the fast memory, the refine
+// write terms (memory.py:257-268: decay 1 - (1 - decay) rate capped at
+// 1 - 2^-16, weight sigmoid(w) clamp(surprise) clamp(novelty), value
+// clamp(tanh(v) - fast read, -2, 2), masked like the fast terms), read from
+// and written into the refine basis and normalizer.
+namespace {
+
+// The refine values of `rows` x `length` positions into `err` (fp32, dense).
+int launch_refine_error(const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset,
+                        const void* fast, int fast_dtype, int64_t fast_row_stride, float* err, int64_t positions,
+                        int64_t width, hipStream_t s) {
+    const int64_t n = positions * width;
+    if (n == 0) return KOEMI_OK;
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
+    return with_projection(projections, projection_dtype, [&](auto proj) {
+        using PT = std::remove_const_t<std::remove_pointer_t<decltype(proj)>>;
+        if (fast_dtype == KOEMI_BF16)
+            hipLaunchKernelGGL((refine_error_kernel<PT, bf16>), grid, dim3(256), 0, s, proj, row_stride, value_offset,
+                               static_cast<const bf16*>(fast), fast_row_stride, err, positions, width);
+        else
+            hipLaunchKernelGGL((refine_error_kernel<PT, float>), grid, dim3(256), 0, s, proj, row_stride, value_offset,
+                               static_cast<const float*>(fast), fast_row_stride, err, positions, width);
+        return check_launch("refine memory (values)");
+    });
+}
+
+// prepare (refine terms), state terms from the refine values (FINAL: next
+// state from the given one), reads from the given (carried) state.
+template <int MAXM, bool FINAL, typename PT>
+int run_refine_window_memory(const PT* proj, int64_t stride, int64_t fk_off, int64_t fq_off, int64_t decay_off,
+                             int64_t write_off, const float* surprise, const uint8_t* valid, const float* novelty,
+                             float rate, const float* err, const AssocPrep& prep, const float* state_basis,
+                             const float* state_norm, float* nb, float* nn, const float* read_basis,
+                             const float* read_norm, void* read, int read_dtype, int64_t ostride, int64_t rows, int L,
+                             int64_t D, int M, hipStream_t s, bool reads) {
+    int st = launch_prep<MAXM>(proj, stride, fk_off, fq_off, decay_off, write_off, surprise, valid, prep, rows, L, M, s,
+                               novelty, rate);
+    if (st != KOEMI_OK) return st;
+    st = launch_delta<MAXM, FINAL, float, false>(err, D, 0, prep, state_basis, state_norm, nb, nn, rows, L, D, M, s);
+    if (st != KOEMI_OK || !reads) return st;
+    return launch_window_read<MAXM, float, false>(err, D, 0, prep, read_basis, read_norm, read, read_dtype, ostride,
+                                                  rows, L, D, M, s);
+}
+
+int check_refine_args(const float* novelty, float rate, const void* fast, int fast_dtype, int64_t fast_row_stride,
+                      int64_t width) {
+    if (!(rate > 0.0f && rate <= 1.0f)) return fail(KOEMI_ERR_INVALID, "refine decay rate must be in (0, 1]");
+    if (fast_dtype != KOEMI_F32 && fast_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "the fast reads must be float32 or bfloat16");
+    if (fast_row_stride < width) return fail(KOEMI_ERR_INVALID, "fast read row stride below the width");
+    if (!novelty || !fast) return fail(KOEMI_ERR_INVALID, "refine memory received a null pointer");
+    return KOEMI_OK;
+}
+
+}  // namespace
+
+extern "C" size_t koemi_assoc_refine_scan_read_workspace_bytes(int64_t batch, int64_t length, int64_t width,
+                                                                int64_t features) {
+    if (batch <= 0 || length <= 1 || width < 1 || features < 1) return 0;
+    return prep_bytes(batch, length, features) + align256(static_cast<size_t>(batch * length * width) * sizeof(float));
+}
+
+extern "C" int koemi_assoc_refine_scan_read(
+    const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset, int64_t feature_offset,
+    int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset, const float* surprise,
+    const uint8_t* valid, const float* novelty, float refine_decay_rate, const void* fast_read, int fast_dtype,
+    int64_t fast_row_stride, const float* basis, const float* normalizer, void* read, int read_dtype,
+    int64_t read_row_stride, float* next_basis, float* next_normalizer, int64_t batch, int64_t length, int64_t width,
+    int64_t features, void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    if (batch < 0 || length < 0 || width < 1 || features < 1)
+        return fail(KOEMI_ERR_INVALID, "refine read needs non-negative batch and length, positive width and features");
+    int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
+                              write_offset, width, features);
+    if (st != KOEMI_OK) return st;
+    if (fast_row_stride == 0) fast_row_stride = width;
+    if (batch > 0 && length > 0 &&
+        (st = check_refine_args(novelty, refine_decay_rate, fast_read, fast_dtype, fast_row_stride, width)) != KOEMI_OK)
+        return st;
+    if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
+    if (read_dtype != KOEMI_F32 && read_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative reads must be float32 or bfloat16");
+    if (read_row_stride == 0) read_row_stride = width;
+    if (read_row_stride < width) return fail(KOEMI_ERR_INVALID, "associative read row stride below the width");
+    if (length == 1 && (read_dtype != KOEMI_F32 || read_row_stride != width || fast_dtype != KOEMI_F32 ||
+                        fast_row_stride != width))
+        return fail(KOEMI_ERR_UNSUPPORTED, "a one-position refine read takes and writes contiguous float32 reads");
+    if (batch == 0 || length == 0) return KOEMI_OK;
+    if (!window_fits(length, features))
+        return fail(KOEMI_ERR_UNSUPPORTED, "refine read window too long (%lld positions)", static_cast<long long>(length));
+    if (batch > 0x7fffffffLL || (width + 63) / 64 > 65535 || batch * length * width > 0x7fffffffLL * 256)
+        return fail(KOEMI_ERR_UNSUPPORTED, "refine read grid too large");
+    if (!projections || !surprise || !valid || !basis || !normalizer || !read || !next_basis || !next_normalizer)
+        return fail(KOEMI_ERR_INVALID, "refine read received a null pointer");
+    const hipStream_t s = as_stream(stream);
+    const int M = static_cast<int>(features);
+    if (length == 1) {
+        const dim3 grid(static_cast<unsigned>(batch), static_cast<unsigned>((width + 255) / 256));
+        return with_projection(projections, projection_dtype, [&](auto proj) {
+            using PT = std::remove_const_t<std::remove_pointer_t<decltype(proj)>>;
+            auto step = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, proj, row_stride, value_offset, feature_offset,
+                                   query_feature_offset, decay_offset, write_offset, surprise, valid, basis, normalizer,
+                                   static_cast<float*>(read), next_basis, next_normalizer, width, M, novelty,
+                                   refine_decay_rate, static_cast<const float*>(fast_read));
+            };
+            if (M <= 16) step(assoc_step_kernel<16, PT>);
+            else step(assoc_step_kernel<32, PT>);
+            return check_launch("koemi_assoc_refine_scan_read");
+        });
+    }
+    const size_t pb = prep_bytes(batch, length, features);
+    const size_t need = koemi_assoc_refine_scan_read_workspace_bytes(batch, length, width, features);
+    if (!workspace || workspace_bytes < need)
+        return fail(KOEMI_ERR_INVALID, "refine read workspace too small: need %zu bytes", need);
+    const AssocPrep prep = prep_at(workspace, batch, length, features);
+    float* err = reinterpret_cast<float*>(static_cast<char*>(workspace) + pb);
+    st = launch_refine_error(projections, projection_dtype, row_stride, value_offset, fast_read, fast_dtype,
+                             fast_row_stride, err, batch * length, width, s);
+    if (st != KOEMI_OK) return st;
+    const int L = static_cast<int>(length);
+    return with_projection(projections, projection_dtype, [&](auto proj) {
+        if (M <= 16)
+            return run_refine_window_memory<16, true>(proj, row_stride, feature_offset, query_feature_offset,
+                                                      decay_offset, write_offset, surprise, valid, novelty,
+                                                      refine_decay_rate, err, prep, basis, normalizer, next_basis,
+                                                      next_normalizer, basis, normalizer, read, read_dtype,
+                                                      read_row_stride, batch, L, width, M, s, true);
+        return run_refine_window_memory<32, true>(proj, row_stride, feature_offset, query_feature_offset, decay_offset,
+                                                  write_offset, surprise, valid, novelty, refine_decay_rate, err, prep,
+                                                  basis, normalizer, next_basis, next_normalizer, basis, normalizer,
+                                                  read, read_dtype, read_row_stride, batch, L, width, M, s, true);
+    });
+}
+
+extern "C" size_t koemi_assoc_refine_scan_read_windows_workspace_bytes(int64_t batch, int64_t windows, int64_t window,
+                                                                        int64_t width, int64_t features) {
+    if (batch < 0 || windows < 0 || window < 1 || width < 1 || features < 1) return 0;
+    return windows_workspace(batch * windows, window, width, features).total +
+           align256(static_cast<size_t>(batch * windows * window * width) * sizeof(float));
+}
+
+extern "C" int koemi_assoc_refine_scan_read_windows(
+    const void* projections, int projection_dtype, int64_t row_stride, int64_t value_offset, int64_t feature_offset,
+    int64_t query_feature_offset, int64_t decay_offset, int64_t write_offset, const float* surprise,
+    const uint8_t* valid, const float* novelty, float refine_decay_rate, const void* fast_read, int fast_dtype,
+    int64_t fast_row_stride, const float* basis, const float* normalizer, void* read, int read_dtype,
+    int64_t read_row_stride, float* next_basis, float* next_normalizer, int64_t batch, int64_t windows, int64_t window,
+    int64_t width, int64_t features, void* workspace, size_t workspace_bytes, koemi_stream_t stream) {
+    if (batch < 0 || windows < 0 || window < 2 || width < 1 || features < 1)
+        return fail(KOEMI_ERR_INVALID, "windowed refine read needs non-negative batch and windows, a window of at "
+                    "least two positions, positive width and features");
+    int st = check_assoc_args(row_stride, value_offset, feature_offset, query_feature_offset, decay_offset,
+                              write_offset, width, features);
+    if (st != KOEMI_OK) return st;
+    if (fast_row_stride == 0) fast_row_stride = width;
+    if (batch > 0 && windows > 0 &&
+        (st = check_refine_args(novelty, refine_decay_rate, fast_read, fast_dtype, fast_row_stride, width)) != KOEMI_OK)
+        return st;
+    if (projection_dtype != KOEMI_F32 && projection_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative read projections must be float32 or bfloat16");
+    if (read_dtype != KOEMI_F32 && read_dtype != KOEMI_BF16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "associative reads must be float32 or bfloat16");
+    if (read_row_stride == 0) read_row_stride = width;
+    if (read_row_stride < width) return fail(KOEMI_ERR_INVALID, "associative read row stride below the width");
+    const int64_t rows = batch * windows;
+    if (batch == 0) return KOEMI_OK;
+    if (!window_fits(window, features))
+        return fail(KOEMI_ERR_UNSUPPORTED, "refine read window too long (%lld positions)", static_cast<long long>(window));
+    if (rows > 0x7fffffffLL || (width + 63) / 64 > 65535 || (width * features + features + 255) / 256 > 65535 ||
+        rows * window * width > 0x7fffffffLL * 256)
+        return fail(KOEMI_ERR_UNSUPPORTED, "windowed refine read grid too large");
+    if (!basis || !normalizer || !next_basis || !next_normalizer ||
+        (windows > 0 && (!projections || !surprise || !valid || !read)))
+        return fail(KOEMI_ERR_INVALID, "windowed refine read received a null pointer");
+    const WindowsWorkspace ws = windows_workspace(rows, window, width, features);
+    const size_t need = koemi_assoc_refine_scan_read_windows_workspace_bytes(batch, windows, window, width, features);
+    if (!workspace || workspace_bytes < need)
+        return fail(KOEMI_ERR_INVALID, "windowed refine read workspace too small: need %zu bytes", need);
+    char* w = static_cast<char*>(workspace);
+    float* delta_basis = reinterpret_cast<float*>(w + ws.delta_basis);
+    float* delta_norm = reinterpret_cast<float*>(w + ws.delta_norm);
+    float* carried_basis = reinterpret_cast<float*>(w + ws.carried_basis);
+    float* carried_norm = reinterpret_cast<float*>(w + ws.carried_norm);
+    float* err = reinterpret_cast<float*>(w + ws.total);
+    const AssocPrep prep = prep_at(w + ws.prep, rows, window, features);
+    const hipStream_t s = as_stream(stream);
+    const int M = static_cast<int>(features);
+    const int L = static_cast<int>(window);
+    if (windows > 0) {
+        st = launch_refine_error(projections, projection_dtype, row_stride, value_offset, fast_read, fast_dtype,
+                                 fast_row_stride, err, rows * window, width, s);
+        if (st != KOEMI_OK) return st;
+        st = with_projection(projections, projection_dtype, [&](auto proj) {
+            if (M <= 16)
+                return run_refine_window_memory<16, false>(proj, row_stride, feature_offset, query_feature_offset,
+                                                           decay_offset, write_offset, surprise, valid, novelty,
+                                                           refine_decay_rate, err, prep, nullptr, nullptr,
+                                                           delta_basis, delta_norm, nullptr, nullptr, nullptr,
+                                                           KOEMI_F32, width, rows, L, width, M, s, false);
+            return run_refine_window_memory<32, false>(proj, row_stride, feature_offset, query_feature_offset,
+                                                       decay_offset, write_offset, surprise, valid, novelty,
+                                                       refine_decay_rate, err, prep, nullptr, nullptr, delta_basis,
+                                                       delta_norm, nullptr, nullptr, nullptr, KOEMI_F32, width, rows,
+                                                       L, width, M, s, false);
+        });
+        if (st != KOEMI_OK) return st;
+    }
+    const int64_t DM = width * features;
+    hipLaunchKernelGGL(assoc_carry_kernel, dim3(static_cast<unsigned>(batch), static_cast<unsigned>((DM + M + 255) / 256)),
+                       dim3(256), 0, s, delta_basis, delta_norm, prep.keep, basis, normalizer, carried_basis,
+                       carried_norm, next_basis, next_normalizer, windows, DM, static_cast<int64_t>(M));
+    st = check_launch("koemi_assoc_refine_scan_read_windows(carry)");
+    if (st != KOEMI_OK || windows == 0) return st;
+    if (M <= 16)
+        return launch_window_read<16, float, false>(err, width, 0, prep, carried_basis, carried_norm, read, read_dtype,
+                                                    read_row_stride, rows, L, width, M, s);
+    return launch_window_read<32, float, false>(err, width, 0, prep, carried_basis, carried_norm, read, read_dtype,
+                                                read_row_stride, rows, L, width, M, s);
 }

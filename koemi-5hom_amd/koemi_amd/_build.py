@@ -43,6 +43,7 @@ SOURCES = (
     "linear_rows.hip",
     "gated_projection.hip",
     "stream_probe.hip",
+    "refine.hip",
 )
 
 ARCH = "gfx950"

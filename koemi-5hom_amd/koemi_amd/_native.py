@@ -149,6 +149,27 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, _P, _P, c_int, c_int64, _P, _P,
          c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
+    "koemi_assoc_refine_scan_read_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64)),
+    "koemi_assoc_refine_scan_read": (
+        c_int,
+        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_float, _P, c_int, c_int64, _P,
+         _P, _P, c_int, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
+    "koemi_assoc_refine_scan_read_windows_workspace_bytes": (c_size_t, (c_int64, c_int64, c_int64, c_int64, c_int64)),
+    "koemi_assoc_refine_scan_read_windows": (
+        c_int,
+        (_P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P, _P, c_float, _P, c_int, c_int64, _P,
+         _P, _P, c_int, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
+    "koemi_local_novelty": (
+        c_int,
+        (_P, _P, _P, c_int, c_int64, _P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P),
+    ),
+    "koemi_herm_refine_gate": (
+        c_int,
+        (_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int, c_int64, _P, c_int, _P, c_int, _P, c_int, c_int64, c_int64,
+         c_int64, _P),
+    ),
     "koemi_memory_read_into": (
         c_int,
         (_P, _P, _P, _P, _P, c_int, c_int64, _P, _P, _P, c_int, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,

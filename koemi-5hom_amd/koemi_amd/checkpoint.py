@@ -20,8 +20,8 @@ This module maps both onto the layout of ``koemi_amd.herm``:
   per-layer state dict of ``herm.initial_states``; the refine memory, which
   the ``no_refine`` block neither reads nor writes, passes through unchanged.
 
-Only the ``no_refine`` ablation and the two expert routings are mapped;
-other ablations raise.
+The ``no_refine`` and ``herm`` ablations and the two expert routings are
+mapped; other ablations raise.
 """
 
 from __future__ import annotations
@@ -37,6 +37,8 @@ __all__ = [
     "BLOCK_PARAMETERS",
     "CHECKPOINT_FORMAT_VERSION",
     "EXPERT_PARAMETERS",
+    "REFINE_GATE_PARAMETERS",
+    "REFINE_STATE_FIELDS",
     "STATE_FIELDS",
     "block_parameters",
     "load_reference_checkpoint",
@@ -80,6 +82,11 @@ BLOCK_PARAMETERS: dict[str, str] = {
     "token_predictor.bias": "head_b",
 }
 ROUTER_PARAMETER = ("experts.gate.weight", "router_w")  # LearnedExpertMixture.gate (router.py:41), no bias
+# the refine gate of the "herm" ablation (network.py:94-96: nn.Linear(4 width, 1))
+REFINE_GATE_PARAMETERS: dict[str, str] = {
+    "memory_refine_gate.weight": "refine_gate_w",
+    "memory_refine_gate.bias": "refine_gate_b",
+}
 
 # GatedFeedForward submodule (layers.py:19-29) -> stacked key prefix
 EXPERT_PARAMETERS: dict[str, str] = {
@@ -102,14 +109,17 @@ STATE_FIELDS: dict[str, str] = {
     "last_token_ids": "last_token",
 }
 PASSTHROUGH_FIELDS = ("refine_basis", "refine_normalizer")
+# with the refine memory ("herm" ablation) those two are part of the layer state
+REFINE_STATE_FIELDS: dict[str, str] = {"refine_basis": "refine_basis", "refine_normalizer": "refine_normalizer"}
 
 
 def block_parameters(model_state: Mapping[str, Tensor], expert_count: int) -> dict[str, Tensor]:
     """One layer's parameters from a reference ``KoemiModel.state_dict()``.
 
     Raises ``KeyError`` naming the first reference parameter that is missing
-    and ``ValueError`` for parameters this layout does not know (for example
-    the refine gate of a non-``no_refine`` model)."""
+    and ``ValueError`` for parameters this layout does not know. The learned
+    router's gate and the refine gate of a ``herm`` model are mapped when
+    present (the refine gate's weight and bias together)."""
 
     out: dict[str, Tensor] = {}
     for name, key in BLOCK_PARAMETERS.items():
@@ -128,6 +138,12 @@ def block_parameters(model_state: Mapping[str, Tensor], expert_count: int) -> di
     if ROUTER_PARAMETER[0] in model_state:
         out[ROUTER_PARAMETER[1]] = model_state[ROUTER_PARAMETER[0]]
         known.add(ROUTER_PARAMETER[0])
+    if any(name in model_state for name in REFINE_GATE_PARAMETERS):
+        for name, key in REFINE_GATE_PARAMETERS.items():
+            if name not in model_state:
+                raise KeyError(f"reference parameter {name!r} is missing")
+            out[key] = model_state[name]
+            known.add(name)
     unknown = sorted(set(model_state) - known)
     if unknown:
         raise ValueError(f"reference parameters without a place in the HERM layout: {unknown[:4]}")
@@ -189,11 +205,11 @@ def settings_from_model_settings(values: Mapping, *, layers: int = 1, linear_dty
     ``expert_dispatch`` (loop or segment dispatch of the same sums),
     ``cache_capacity`` (the runtime's token cache), ``activation_checkpointing``
     and ``compile_forward`` (training and compilation switches),
-    ``refine_decay_rate`` (the refine memory, which the no_refine ablation does
-    not build) and ``expert_load_balance_weight`` (the factor the caller applies
+    and ``expert_load_balance_weight`` (the factor the caller applies
     to ``moe.RouterStatistics.balance_loss`` for ``router_loss``,
-    network.py:42-46). Only the ``no_refine`` ablation and at least one expert
-    are mapped (``ValueError`` otherwise)."""
+    network.py:42-46). The ``no_refine`` and ``herm`` ablations (with
+    ``refine_decay_rate``) and at least one expert are mapped (``ValueError``
+    otherwise)."""
 
     from koemi_amd.herm import HermSettings
 
@@ -203,8 +219,8 @@ def settings_from_model_settings(values: Mapping, *, layers: int = 1, linear_dty
     merged = {**_MODEL_SETTINGS_DEFAULTS, **values}
     _validate_model_settings(merged)
     ablation = merged["ablation"]
-    if ablation != "no_refine":
-        raise ValueError(f"only the no_refine ablation is mapped, not {ablation!r}")
+    if ablation not in ("no_refine", "herm"):
+        raise ValueError(f"only the no_refine and herm ablations are mapped, not {ablation!r}")
     if merged["expert_count"] < 1:
         raise ValueError("the HERM block is mapped with experts only (expert_count >= 1)")
     routing = merged["expert_routing"]
@@ -221,6 +237,8 @@ def settings_from_model_settings(values: Mapping, *, layers: int = 1, linear_dty
         scan_chunk=int(merged["scan_chunk"]),
         linear_dtype=linear_dtype,
         expert_routing=routing,
+        ablation=ablation,
+        refine_decay_rate=float(merged["refine_decay_rate"]),
     )
 
 
@@ -246,27 +264,31 @@ def load_reference_checkpoint(path: str | Path, *, linear_dtype: torch.dtype = t
     params = block_parameters(raw["model_state"], settings.expert_count)
     if settings.expert_routing == "learned" and "router_w" not in params:
         raise KeyError(f"reference parameter {ROUTER_PARAMETER[0]!r} is missing")
+    if (settings.ablation == "herm") != ("refine_gate_w" in params):
+        raise ValueError("the refine gate parameters are present exactly for the herm ablation")
     return settings, [params]
 
 
-def state_from_fields(fields: Mapping[str, Tensor]) -> dict[str, Tensor]:
+def state_from_fields(fields: Mapping[str, Tensor], *, refine: bool = False) -> dict[str, Tensor]:
     """A herm layer state from ``KoemiState`` fields (a static state: the
-    rings at their capacity, state.py:43-76)."""
+    rings at their capacity, state.py:43-76); with ``refine`` (a ``herm``
+    ablation stack) the refine basis and normalizer as well."""
 
-    missing = [name for name in STATE_FIELDS if name not in fields]
+    names = {**STATE_FIELDS, **(REFINE_STATE_FIELDS if refine else {})}
+    missing = [name for name in names if name not in fields]
     if missing:
         raise KeyError(f"KoemiState field {missing[0]!r} is missing")
-    return {key: fields[name] for name, key in STATE_FIELDS.items()}
+    return {key: fields[name] for name, key in names.items()}
 
 
 def state_to_fields(state: Mapping[str, Tensor], carried: Mapping[str, Tensor], step_index: int) -> dict:
     """``KoemiState`` fields (and ``step_index``) from a herm layer state; the
-    refine basis and normalizer come from ``carried`` (the state before the
-    window), as forward_window passes them on under ``no_refine``
-    (network.py:368-371)."""
+    refine basis and normalizer come from the state when it holds them (the
+    ``herm`` ablation), else from ``carried`` (the state before the window),
+    as forward_window passes them on under ``no_refine`` (network.py:368-371)."""
 
     out = {name: state[key] for name, key in STATE_FIELDS.items()}
     for name in PASSTHROUGH_FIELDS:
-        out[name] = carried[name]
+        out[name] = state[REFINE_STATE_FIELDS[name]] if REFINE_STATE_FIELDS[name] in state else carried[name]
     out["step_index"] = int(step_index)
     return out

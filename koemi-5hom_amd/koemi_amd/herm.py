@@ -103,10 +103,22 @@ class HermSettings:
     scan_chunk: int = 128
     linear_dtype: torch.dtype = torch.bfloat16
     expert_routing: str = "hash"   # "hash" (experts.py:109-150) or "learned" (router.py:43-97)
+    ablation: str = "no_refine"    # "no_refine" (the default) or "herm" (the refine memory, network.py:359-384)
+    refine_decay_rate: float = 0.0625  # configuration/settings.py:29
+
+    def __post_init__(self) -> None:
+        if self.ablation not in ("no_refine", "herm"):
+            raise ValueError(f"ablation must be no_refine or herm, not {self.ablation!r}")
+        if not 0.0 < self.refine_decay_rate <= 1.0:
+            raise ValueError("refine_decay_rate must be greater than zero and at most one")
+
+    @property
+    def refine(self) -> bool:
+        return self.ablation == "herm"
 
     def oracle_config(self) -> dict:
         keys = ("width", "memory_features", "local_memory_size", "salience_memory_size", "salience_threshold",
-                "expert_count", "top_k", "expert_routing")
+                "expert_count", "top_k", "expert_routing", "ablation", "refine_decay_rate")
         values = asdict(self)
         return {k: values[k] for k in keys}
 
@@ -152,6 +164,8 @@ def init_stack(settings: HermSettings, seed: int, device: torch.device | str = "
             bound = 1.0 / math.sqrt(d)  # nn.Linear(d, E, bias=False) (router.py:41)
             p["router_w"] = (torch.rand((e, d), generator=g, device=device) * 2.0 - 1.0) * bound
         p["head_w"], p["head_b"] = _linear_init(g, v, d)
+        if settings.refine:  # memory_refine_gate = nn.Linear(4 width, 1) (network.py:94-96)
+            p["refine_gate_w"], p["refine_gate_b"] = _linear_init(g, 1, 4 * d)
         layers.append(p)
     return layers
 
@@ -201,6 +215,10 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
             q[name + "_w"], q[name + "_b"] = to(p[name + "_w"], lin), to(p[name + "_b"], lin)
         if "router_w" in p:
             q["router_w"] = to(p["router_w"])
+        if "refine_gate_w" in p:
+            # the refine gate's [4 width] weight in the projections' dtype, its bias fp32
+            q["refine_gate_w"] = to(p["refine_gate_w"].reshape(-1), lin)
+            q["refine_gate_b"] = to(p["refine_gate_b"].reshape(1))
         q["head_w"], q["head_b"] = to(p["head_w"], lin), to(p["head_b"])
         q["content_w"] = to(p["head_w"][:PAD_TOKEN_ID])
         q["content_b"] = to(p["head_b"][:PAD_TOKEN_ID])
@@ -212,14 +230,17 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
 
 def initial_states(settings: HermSettings, batch: int, device: torch.device) -> list[dict[str, Tensor]]:
     """KoemiState.create_static (state.py:43-76) per layer: zeros, rings at
-    capacity with every slot invalid, last token PAD."""
+    capacity with every slot invalid, last token PAD; with the herm ablation
+    also the zero refine basis and normalizer."""
 
     d, m = settings.width, settings.memory_features
     w, s = settings.local_memory_size, settings.salience_memory_size
     states = []
     for _ in range(settings.layers):
         z = lambda *shape: torch.zeros(shape, device=device)
+        refine = {"refine_basis": z(batch, d, m), "refine_normalizer": z(batch, m)} if settings.refine else {}
         states.append({
+            **refine,
             "working": z(batch, d),
             "basis": z(batch, d, m),
             "normalizer": z(batch, m),
@@ -477,6 +498,78 @@ def associative_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, 
     return read, next_basis, next_normalizer
 
 
+def associative_refine_scan_read(projections: Tensor, surprise: Tensor, valid: Tensor, novelty: Tensor,
+                                 fast: Tensor, basis: Tensor, normalizer: Tensor, *, width: int, features: int,
+                                 rate: float, window: int | None = None,
+                                 next_out: tuple[Tensor, Tensor] | None = None) -> tuple[Tensor, Tensor, Tensor]:
+    """The refine memory of the herm ablation (network.py:359-384) on
+    ``koemi_assoc_refine_scan_read`` (or, with ``window``, over every window of
+    a sequence on ``koemi_assoc_refine_scan_read_windows``): the write terms of
+    memory.py:257-268 from the same ``projections`` as
+    ``associative_scan_read``, ``surprise``, the local read's ``novelty``
+    [B, L] fp32 and the fast reads ``fast`` [B, L, D] (fp32 or bf16, rows
+    evenly spaced; the reconstruction error is clamp(tanh(v) - fast, -2, 2)),
+    read from and written into the refine state ``basis`` [B, D, M] /
+    ``normalizer`` [B, M]. Returns (refine reads [B, L, D] fp32, next basis,
+    next normalizer); ``next_out`` as for ``associative_scan_read``."""
+
+    batch, length, stride = projections.shape
+    d, m = width, features
+    if (stride < 3 * d + 2 * m + 2 or projections.dtype not in (torch.float32, torch.bfloat16)
+            or not projections.is_contiguous()):
+        raise ValueError("projections must be contiguous fp32 or bf16 [batch, length, >= 3 * width + 2 * features + 2]")
+    if length == 1 and (fast.dtype != torch.float32 or not fast.is_contiguous()):
+        fast = fast.float().contiguous()
+    fast_stride = memory._row_stride(fast, (batch, length, d))
+    read = torch.empty((batch, length, d), device=projections.device, dtype=torch.float32)
+    next_basis, next_normalizer = next_out if next_out is not None else (torch.empty_like(basis),
+                                                                         torch.empty_like(normalizer))
+    args = [t.contiguous() for t in (surprise, valid, novelty)]
+    state = [basis.contiguous(), normalizer.contiguous()]
+    head = (_native.ptr(projections), _native.dtype_code(projections.dtype), stride, 2 * d, 3 * d, 3 * d + m,
+            3 * d + 2 * m, 3 * d + 2 * m + 1, *(_native.ptr(t) for t in args), float(rate), _native.ptr(fast),
+            _native.dtype_code(fast.dtype), fast_stride, *(_native.ptr(t) for t in state), _native.ptr(read),
+            _native.dtype_code(read.dtype), d, _native.ptr(next_basis), _native.ptr(next_normalizer))
+    if window is None:
+        need = _native.query("koemi_assoc_refine_scan_read_workspace_bytes", batch, length, d, m)
+        workspace = torch.empty((need,), device=projections.device, dtype=torch.uint8) if need else None
+        _native.call("koemi_assoc_refine_scan_read", *head, batch, length, d, m, _native.ptr(workspace), need,
+                     _native.stream_of(projections.device))
+    else:
+        if length % window:
+            raise ValueError("the sequence length must be a multiple of the window")
+        windows = length // window
+        need = _native.query("koemi_assoc_refine_scan_read_windows_workspace_bytes", batch, windows, window, d, m)
+        workspace = torch.empty((need,), device=projections.device, dtype=torch.uint8)
+        _native.call("koemi_assoc_refine_scan_read_windows", *head, batch, windows, window, d, m,
+                     _native.ptr(workspace), need, _native.stream_of(projections.device))
+    return read, next_basis, next_normalizer
+
+
+def _refine_gate(p: dict[str, Tensor], ws: Tensor, fast: Tensor, refine: Tensor, local: Tensor,
+                 out: Tensor | None, low) -> Tensor:
+    """KoemiModel.refine_memory (network.py:714-721) on
+    ``koemi_herm_refine_gate``: the memory value fast + sigmoid(W_g [ws; fast;
+    refine; local] + b_g) refine, [B, L, D], into ``out`` (the fusion input's
+    memory block) or a new fp32 tensor. ``low`` (bf16 stacks) rounds the
+    gate's inputs and pre-activation to bf16 (nn.Linear under autocast)."""
+
+    batch, length, d = ws.shape
+    value = torch.empty((batch, length, d), device=ws.device, dtype=torch.float32) if out is None else out
+    pieces = (ws, fast, refine, local)
+    if any(t.dtype != torch.float32 for t in pieces[:3]):
+        raise ValueError("the refine gate takes fp32 working states, fast and refine reads")
+    strides = [memory._row_stride(t, (batch, length, d)) for t in pieces] + [memory._row_stride(value,
+                                                                                                (batch, length, d))]
+    w = p["refine_gate_w"]
+    _native.call("koemi_herm_refine_gate", _native.ptr(ws), strides[0], _native.ptr(fast), strides[1],
+                 _native.ptr(refine), strides[2], _native.ptr(local), _native.dtype_code(local.dtype), strides[3],
+                 _native.ptr(w), _native.dtype_code(w.dtype), _native.ptr(p["refine_gate_b"]), int(low is not None),
+                 _native.ptr(value), _native.dtype_code(value.dtype), strides[4], batch * length, d,
+                 _native.stream_of(ws.device))
+    return value
+
+
 class NextInput(NamedTuple):
     """A block's output handed to the next block of a stack already through
     that block's input RMSNorm: ``normalized`` [B, L, D] bf16, written by the
@@ -723,7 +816,8 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
             salient = ring_out("salient") or tuple(torch.empty_like(state["salient" + part])
                                                    for part in ("_keys", "_values", "_valid"))
             m = settings.memory_features
-            if projected.is_contiguous() and m <= 32 and projected.shape[-1] >= 3 * d + 2 * m + 2:
+            if (projected.is_contiguous() and m <= 32 and projected.shape[-1] >= 3 * d + 2 * m + 2
+                    and not settings.refine):
                 # the associative memory's step joins the same launch
                 fast = torch.empty((batch, 1, d), device=ids.device, dtype=torch.float32)
                 basis, normalizer = ((out_state["basis"], out_state["normalizer"]) if out_state is not None
@@ -749,10 +843,25 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
                                                out=_block(fusion_in, 2, d))
 
     if not assoc_done:
+        # with the refine memory the fast reads stay fp32 for the reconstruction
+        # error and the gate; the memory value goes to the fusion input instead
         fast, basis, normalizer = associative_scan_read(
             projected, surprise, valid, state["basis"], state["normalizer"], width=d,
-            features=settings.memory_features, out=_block(fusion_in, 1, d),
+            features=settings.memory_features, out=None if settings.refine else _block(fusion_in, 1, d),
             next_out=(out_state["basis"], out_state["normalizer"]) if out_state is not None else None)
+    refine_next = {}
+    if settings.refine:
+        # network.py:359-384: the local read's novelty, the refine terms and
+        # their scan-and-read over the refine state, the refine gate
+        novelty = memory.local_novelty(state["local_keys"], state["local_valid"], local_keys, valid, ws,
+                                       window=settings.local_memory_size)
+        refine, refine_basis, refine_normalizer = associative_refine_scan_read(
+            projected, surprise, valid, novelty, fast, state["refine_basis"], state["refine_normalizer"], width=d,
+            features=settings.memory_features, rate=settings.refine_decay_rate,
+            next_out=(out_state["refine_basis"], out_state["refine_normalizer"]) if out_state is not None else None)
+        local_in = local_value if fusion_in is None or length == 1 else _block(fusion_in, 2, d)
+        fast = _refine_gate(p, ws, fast, refine, local_in, _block(fusion_in, 1, d), low)
+        refine_next = {"refine_basis": refine_basis, "refine_normalizer": refine_normalizer}
 
     if length != 1:
         salient_value = memory.read_salient_window(state["salient_keys"], state["salient_values"],
@@ -780,6 +889,7 @@ def block_window(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, stat
         "salient_values": salient[1],
         "salient_valid": salient[2],
         "last_token": last_token,
+        **refine_next,
     }
     return logits, final, next_state, surprise
 
@@ -1035,7 +1145,19 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     fast, basis, normalizer = associative_scan_read_windows(projected, surprise, valid, state["basis"],
                                                             state["normalizer"], width=d,
                                                             features=settings.memory_features, window=chunk,
-                                                            out=_block(fusion_in, 1, d))
+                                                            out=None if settings.refine else _block(fusion_in, 1, d))
+    refine_next = {}
+    if settings.refine:
+        # the refine memory (network.py:359-384) of every window at once: each
+        # window's novelty against the local ring it receives, the refine
+        # terms' scan-and-read carried over the windows, the gate
+        novelty = memory.local_novelty(local_rings[0], local_rings[2], per_window(local_keys), per_window(valid),
+                                       per_window(ws), window=cap_l).view(batch, length)
+        refine, refine_basis, refine_normalizer = associative_refine_scan_read(
+            projected, surprise, valid, novelty, fast, state["refine_basis"], state["refine_normalizer"], width=d,
+            features=settings.memory_features, rate=settings.refine_decay_rate, window=chunk)
+        fast = _refine_gate(p, ws, fast, refine, local_value.view(batch, length, d), _block(fusion_in, 1, d), low)
+        refine_next = {"refine_basis": refine_basis, "refine_normalizer": refine_normalizer}
     salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
                                                 local_keys, local_values, admission, window=chunk, capacity=cap_s,
                                                 tail=False, key_valid=valid)
@@ -1058,6 +1180,7 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
         "salient_values": salient_final[1],
         "salient_valid": salient_final[2],
         "last_token": last_token,
+        **refine_next,
     }
     return logits, final, next_state, surprise
 

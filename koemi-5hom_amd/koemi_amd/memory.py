@@ -19,7 +19,7 @@ from torch import Tensor
 from koemi_amd import _native
 from koemi_amd.think import CudaThinkUnavailableError, CudaThinkValidationError
 
-__all__ = ["read_local_window", "read_salient_window", "salient_tail"]
+__all__ = ["local_novelty", "read_local_window", "read_salient_window", "salient_tail"]
 
 _SUPPORTED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _MAX_CAPACITY = 4096
@@ -89,6 +89,37 @@ def read_local_window(
         "read_local_window", "valid_mask", carried_keys, carried_values, carried_valid, keys, values, valid_mask,
         queries, window, out,
     )
+
+
+def local_novelty(carried_keys: Tensor, carried_valid: Tensor, keys: Tensor, valid_mask: Tensor, queries: Tensor, *,
+                  window: int) -> Tensor:
+    """The novelty output of ``LocalKeyValueMemory.read_window`` (reference
+    model/memory.py:354-361) on ``koemi_local_novelty``: per query, 1 minus the
+    largest cosine similarity with a key of its sliding window (the slots
+    ``read_local_window`` attends to), clamped to [0, 1]; 1 with no eligible
+    slot. ``carried_keys`` fp32 [B, C, D] with ``carried_valid`` [B, C] bool;
+    ``keys`` [B, L, D] fp32 or bf16 (evenly spaced rows, e.g. a column block
+    of the block's projection) with ``valid_mask`` [B, L] bool; ``queries``
+    fp32 [B, L, D] (evenly spaced rows). Returns [B, L] fp32."""
+
+    if isinstance(window, bool) or not isinstance(window, int) or window < 1:
+        raise CudaThinkValidationError("window must be a positive integer")
+    batch, length, width = queries.shape
+    cap = carried_keys.shape[1]
+    if carried_keys.shape != (batch, cap, width) or carried_keys.dtype != torch.float32:
+        raise CudaThinkValidationError("carried_keys must be float32 [batch, capacity, width]")
+    if carried_valid.shape != (batch, cap) or valid_mask.shape != (batch, length):
+        raise CudaThinkValidationError("carried_valid and valid_mask must match the keys")
+    if queries.dtype != torch.float32:
+        raise CudaThinkValidationError("queries must be float32")
+    key_stride = _row_stride(keys, (batch, length, width), "keys")
+    query_stride = _row_stride(queries, (batch, length, width), "queries")
+    novelty = torch.empty((batch, length), device=queries.device, dtype=torch.float32)
+    ck, cv, vm = carried_keys.contiguous(), carried_valid.contiguous(), valid_mask.contiguous()
+    _native.call("koemi_local_novelty", _native.ptr(ck), _native.ptr(cv), _native.ptr(keys),
+                 _native.dtype_code(keys.dtype), key_stride, _native.ptr(vm), _native.ptr(queries), query_stride,
+                 _native.ptr(novelty), batch, cap, length, width, window, _native.stream_of(queries.device))
+    return novelty
 
 
 def _row_stride(out: Tensor, shape: tuple[int, int, int], name: str = "out", any_dtype: bool = False) -> int:

@@ -314,6 +314,37 @@ def read_local_window(
     return np.einsum("bts,bsd->btd", w, all_v)
 
 
+def local_novelty(
+    carried_keys: np.ndarray,
+    carried_valid: np.ndarray,
+    keys: np.ndarray,
+    valid: np.ndarray,
+    queries: np.ndarray,
+    window: int,
+) -> np.ndarray:
+    """Novelty output of LocalKeyValueMemory.read_window (model/memory.py:
+    354-361), in float64: over the slots eligible for query t (the local
+    read's sliding window, memory.py:364-383), the largest cosine similarity
+    of the query with a key (both normalised as functional.normalize does,
+    x / max(|x|, 1e-12)); novelty = clamp(1 - largest, 0, 1), and 1 for a
+    query with no eligible slot. Returns [B, L]."""
+
+    all_k = np.concatenate([np.asarray(carried_keys, np.float64), np.asarray(keys, np.float64)], axis=1)
+    all_valid = np.concatenate([np.asarray(carried_valid, bool), np.asarray(valid, bool)], axis=1)
+    q = np.asarray(queries, dtype=np.float64)
+    length = q.shape[1]
+    c = np.asarray(carried_keys).shape[1]
+    own = c + np.arange(length)[:, None]
+    src = np.arange(all_k.shape[1])[None, :]
+    eligible = ((src < own) & (src >= own - window))[None] & all_valid[:, None, :]
+    nk = all_k / np.maximum(np.linalg.norm(all_k, axis=-1, keepdims=True), 1e-12)
+    nq = q / np.maximum(np.linalg.norm(q, axis=-1, keepdims=True), 1e-12)
+    similarity = np.where(eligible, np.einsum("bsd,btd->bts", nk, nq), -np.inf)
+    any_slot = eligible.any(axis=-1)
+    highest = similarity.max(axis=-1, initial=-np.inf)
+    return np.clip(np.where(any_slot, 1.0 - highest, 1.0), 0.0, 1.0)
+
+
 def read_local_sequential(
     carried_keys: np.ndarray,
     carried_values: np.ndarray,

@@ -5,7 +5,10 @@ nowhere in the product.
 
 Restates KoemiModel.forward_window (reference model/network.py:296-441) under
 the ablation it runs by default ("no_refine": memory_value is the fast
-associative read), with hash expert routing (the static dispatch of
+associative read) or, with ``cfg["ablation"] == "herm"``, with the refine
+memory (memory.py:257-268 refine write terms from the reconstruction error
+and the local read's novelty, a second scan_and_read over the refine state,
+the refine gate of network.py:714-721), with hash expert routing (the static dispatch of
 experts.py:109-150) or learned routing (router.py:43-97), from the
 reference's own formulas:
 
@@ -39,7 +42,10 @@ independence of the stack, and the reused oracle functions' own pins.
 ``cfg`` keys: the HermSettings names (width, memory_features,
 local_memory_size, salience_memory_size, salience_threshold, expert_count,
 top_k), optionally ``expert_routing`` ("hash" or "learned"; learned needs the
-layer's ``router_w``) and ``memory_log_dtype`` (fp32 by default, as the
+layer's ``router_w``), ``ablation`` ("no_refine" or "herm"; herm needs the
+layer's ``refine_gate_w`` [1, 4 width] and ``refine_gate_b`` [1], the state's
+``refine_basis`` and ``refine_normalizer``, and ``refine_decay_rate``) and
+``memory_log_dtype`` (fp32 by default, as the
 reference forms the memory's log-decays; float64 for exact-arithmetic checks).
 """
 
@@ -55,6 +61,7 @@ PAD = oracle.PAD_TOKEN_ID
 EPS = 1e-6                  # RootMeanSquareNorm default epsilon (layers.py:9)
 MIN_DECAY = 2.0**-12        # memory.py:74-75
 MAX_DECAY = 1.0 - 2.0**-12
+MAX_REFINE_DECAY = 1.0 - 2.0**-16   # memory.py:79
 READ_EPSILON = 2.0**-8      # memory.py:77
 
 
@@ -143,10 +150,14 @@ def associative_sequential(basis, normalizer, decay, value, features, weight, qu
 
 
 def initial_state(batch: int, cfg: dict) -> dict:
-    """KoemiState.create_static (state.py:43-76): zero state, rings at capacity, all slots invalid."""
+    """KoemiState.create_static (state.py:43-76): zero state, rings at capacity,
+    all slots invalid; with the refine ablation also the zero refine basis
+    and normalizer."""
 
     d, m, w, s = cfg["width"], cfg["memory_features"], cfg["local_memory_size"], cfg["salience_memory_size"]
-    return {
+    refine = {"refine_basis": np.zeros((batch, d, m)), "refine_normalizer": np.zeros((batch, m))} \
+        if cfg.get("ablation", "no_refine") == "herm" else {}
+    return {**refine,
         "working": np.zeros((batch, d)),
         "basis": np.zeros((batch, d, m)),
         "normalizer": np.zeros((batch, m)),
@@ -267,6 +278,28 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
                                                     write, query_features,
                                                     log_dtype=cfg.get("memory_log_dtype", np.float32))
 
+    refine_next = {}
+    if cfg.get("ablation", "no_refine") == "herm":
+        # the refine memory (network.py:359-384): write terms from the
+        # reconstruction error and the local read's novelty (memory.py:257-268),
+        # masked as the fast terms, a second scan_and_read over the refine
+        # state with the same query features, and the refine gate
+        # (network.py:714-721) mixing it into the memory value
+        novelty = oracle.local_novelty(state["local_keys"], state["local_valid"], local_keys, valid, ws,
+                                       cfg["local_memory_size"])
+        bounded = MIN_DECAY + (MAX_DECAY - MIN_DECAY) * sigmoid(linear(ws, f("decay_w"), f("decay_b")))[..., 0]
+        refine_decay = np.minimum(1.0 - (1.0 - bounded) * cfg["refine_decay_rate"], MAX_REFINE_DECAY)
+        refine_weight = (sigmoid(linear(ws, f("write_w"), f("write_b")))[..., 0] * np.clip(surprise, 0.0, 1.0)
+                         * np.clip(novelty, 0.0, 1.0))
+        error = np.clip(value - fast, -2.0, 2.0)
+        refine, refine_basis, refine_normalizer = associative_scan_read(
+            state["refine_basis"], state["refine_normalizer"], np.where(valid, refine_decay, 1.0), error, features,
+            np.where(valid, refine_weight, 0.0), query_features, log_dtype=cfg.get("memory_log_dtype", np.float32))
+        gate_in = np.concatenate([ws, fast, refine, local_value], axis=-1)
+        gate = sigmoid(linear(gate_in, f("refine_gate_w"), f("refine_gate_b")))
+        fast = fast + gate * refine
+        refine_next = {"refine_basis": refine_basis, "refine_normalizer": refine_normalizer}
+
     admission = valid & (surprise > cfg["salience_threshold"])
     if admission_in is not None:
         admission = np.asarray(admission_in, bool).reshape(admission.shape)
@@ -298,6 +331,7 @@ def block_window(p: dict, state: dict, ids: np.ndarray, cfg: dict, input_context
         "salient_values": np.asarray(sv, np.float64),
         "salient_valid": np.asarray(sok, bool),
         "last_token": last,
+        **refine_next,
     }
     out = (logits, final, next_state, surprise, admission)
     if return_assignments:

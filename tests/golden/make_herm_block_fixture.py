@@ -14,7 +14,9 @@ runs three windows from ``KoemiState.create_static``: 11 tokens, 11 more
 weights, ids and every output (logits, surprise, admission, expert
 assignments, each next state field and, for learned routing, the window's
 RouterStatistics with its balance loss) go to ``herm_block_<routing>.npz`` beside
-this script, once with hash routing and once with learned routing. Only data
+this script: with hash routing, with learned routing, and with hash routing
+under the ``herm`` ablation (the refine memory, its gate and the local read's
+novelty; ``herm_block_refine.npz``). Only data
 is written; nothing from the reference is copied. The GPU box never runs this.
 
 Reference: model/network.py:296-441 (forward_window), state.py:43-76
@@ -46,14 +48,14 @@ def _ids(rng: np.random.Generator, length: int, pad: int) -> np.ndarray:
     return ids
 
 
-def make(routing: str) -> dict[str, np.ndarray]:
+def make(routing: str, ablation: str = "no_refine") -> dict[str, np.ndarray]:
     from koemi.configuration.settings import PAD_TOKEN_ID, ModelSettings
     from koemi.model.network import KoemiModel
     from koemi.model.state import KOEMI_STATE_FIELDS, KoemiState
 
     settings = ModelSettings(embedding_size=16, memory_features=4, local_memory_size=4, salience_memory_size=3,
                              salience_threshold=0.6, expert_count=4, expert_top_k=2, scan_chunk=11,
-                             ablation="no_refine", expert_routing=routing)
+                             ablation=ablation, expert_routing=routing)
     torch.manual_seed(SEED)
     model = KoemiModel(settings).double().eval()
     with torch.no_grad():
@@ -93,9 +95,10 @@ def main() -> int:
     if src not in sys.path:
         sys.path.insert(0, src)
     torch.set_num_threads(1)
-    for routing in ("hash", "learned"):
-        data = make(routing)
-        path = HERE / f"herm_block_{routing}.npz"
+    for name, routing, ablation in (("hash", "hash", "no_refine"), ("learned", "learned", "no_refine"),
+                                    ("refine", "hash", "herm")):
+        data = make(routing, ablation)
+        path = HERE / f"herm_block_{name}.npz"
         np.savez_compressed(path, **data)
         print(f"wrote {path} ({path.stat().st_size} bytes, {len(data)} arrays)")
     return 0

@@ -35,7 +35,7 @@ from koemi_amd import checkpoint
 from oracle import herm
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-FIELDS = tuple(checkpoint.STATE_FIELDS)
+FIELDS = tuple(checkpoint.STATE_FIELDS) + tuple(checkpoint.REFINE_STATE_FIELDS)
 
 
 def load(routing: str) -> dict[str, np.ndarray]:
@@ -49,14 +49,18 @@ def params_of(data: dict[str, np.ndarray], expert_count: int = 4) -> dict[str, n
 
 
 def cfg_of(data: dict[str, np.ndarray], routing: str) -> dict:
+    """``routing``: the fixture name ("hash", "learned", or "refine": hash
+    routing under the herm ablation, refine_decay_rate at the reference's
+    default 0.0625)."""
     return dict(width=16, memory_features=4, local_memory_size=4, salience_memory_size=3,
                 salience_threshold=float(data["settings.salience_threshold"]), expert_count=4, top_k=2,
-                expert_routing=routing)
+                expert_routing="learned" if routing == "learned" else "hash",
+                ablation="herm" if routing == "refine" else "no_refine", refine_decay_rate=0.0625)
 
 
-def state_in(data: dict[str, np.ndarray], w: int) -> dict[str, np.ndarray]:
+def state_in(data: dict[str, np.ndarray], w: int, refine: bool = False) -> dict[str, np.ndarray]:
     fields = {name: data[f"w{w}.state_in.{name}"] for name in FIELDS}
-    return {k: np.asarray(v) for k, v in checkpoint.state_from_fields(fields).items()}
+    return {k: np.asarray(v) for k, v in checkpoint.state_from_fields(fields, refine=refine).items()}
 
 
 def close(got, want, rel):
@@ -66,20 +70,21 @@ def close(got, want, rel):
     assert err <= rel * scale, f"max abs err {err:.3e} > {rel:.0e} x scale {scale:.3e}"
 
 
-@pytest.mark.parametrize("routing", ["hash", "learned"])
+@pytest.mark.parametrize("routing", ["hash", "learned", "refine"])
 def test_block_window_matches_reference_fixture(routing):
     data = load(routing)
     p = params_of(data)
     cfg = cfg_of(data, routing)
+    refine = routing == "refine"
     fine, memory_fed = 1e-12, 1e-7
-    tol = lambda key: memory_fed if key in ("basis", "normalizer") else fine
+    tol = lambda key: memory_fed if key in ("basis", "normalizer", "refine_basis", "refine_normalizer") else fine
     windows = [int(n) for n in data["settings.windows"]]
     assert windows == [11, 11, 1]
-    state = state_in(data, 0)
+    state = state_in(data, 0, refine)
     for w in range(len(windows)):
         # each window from the reference's own incoming state: errors do not compound
         if w:
-            carried = state_in(data, w)
+            carried = state_in(data, w, refine)
             for key in carried:
                 if carried[key].dtype == bool or carried[key].dtype.kind == "i":
                     np.testing.assert_array_equal(state[key], carried[key], err_msg=key)
@@ -102,7 +107,7 @@ def test_block_window_matches_reference_fixture(routing):
         np.testing.assert_array_equal(admission, data[f"w{w}.admission"])
         np.testing.assert_array_equal(assign, data[f"w{w}.assignments"])
         want = {k: np.asarray(v) for k, v in checkpoint.state_from_fields(
-            {name: data[f"w{w}.state_out.{name}"] for name in FIELDS}).items()}
+            {name: data[f"w{w}.state_out.{name}"] for name in FIELDS}, refine=refine).items()}
         for key, value in want.items():
             if value.dtype == bool or value.dtype.kind == "i":
                 np.testing.assert_array_equal(nxt[key], value, err_msg=f"window {w} {key}")
@@ -140,7 +145,13 @@ def test_layout_map_roundtrip_and_errors():
     with pytest.raises(KeyError, match="experts.experts.3"):
         checkpoint.block_parameters({k: v for k, v in model_state.items() if "experts.3." not in k}, 4)
     with pytest.raises(ValueError, match="without a place"):
+        checkpoint.block_parameters({**model_state, "memory_refine_extra.weight": torch.zeros(1, 64)}, 4)
+    with pytest.raises(KeyError, match="memory_refine_gate.bias"):
         checkpoint.block_parameters({**model_state, "memory_refine_gate.weight": torch.zeros(1, 64)}, 4)
+    refine = load("refine")
+    refine_state = {k[len("param."):]: torch.from_numpy(v) for k, v in refine.items() if k.startswith("param.")}
+    rp = checkpoint.block_parameters(refine_state, 4)
+    assert rp["refine_gate_w"].shape == (1, 64) and rp["refine_gate_b"].shape == (1,)
     fields = {name: torch.from_numpy(data[f"w1.state_out.{name}"]) for name in
               (*checkpoint.STATE_FIELDS, *checkpoint.PASSTHROUGH_FIELDS)}
     back = checkpoint.state_to_fields(checkpoint.state_from_fields(fields), fields, 22)
@@ -168,7 +179,13 @@ def test_reference_checkpoint_loads_weights_only(tmp_path):
     with pytest.raises(ValueError, match="format version"):
         checkpoint.load_reference_checkpoint(path)
     with pytest.raises(ValueError, match="ablation"):
-        checkpoint.settings_from_model_settings({**settings, "ablation": "herm"})
+        checkpoint.settings_from_model_settings({**settings, "ablation": "no_surprise"})
+    hs_refine = checkpoint.settings_from_model_settings({**settings, "ablation": "herm", "refine_decay_rate": 0.125})
+    assert hs_refine.refine and hs_refine.refine_decay_rate == 0.125
+    torch.save({"format_version": 7, "model_settings": {**settings, "ablation": "herm"}, "model_state": model_state},
+               path)
+    with pytest.raises(ValueError, match="exactly for the herm ablation"):
+        checkpoint.load_reference_checkpoint(path)
     # CheckpointStore.validate_checkpoint's optional payload types (checkpoints.py:87-92)
     for key in ("vocabulary", "identity"):
         torch.save({"format_version": 7, "model_settings": settings, "model_state": model_state, key: [1, 2]}, path)
