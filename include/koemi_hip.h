@@ -720,6 +720,18 @@ int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, con
 int koemi_herm_greedy_tokens(const float* logits, int64_t row_stride, int64_t rows, int64_t vocab, int64_t exclude_id,
                              int64_t* ids, koemi_stream_t stream);
 
+/* TokenSampler's non-greedy draw (runtime/fast_decode.py:57-95) for `rows`
+ * rows of fp32 logits (rows row_stride apart; 0: vocab): the exclude_id
+ * column (PAD) removed, with top_k > 0 every score below the min(top_k,
+ * vocab)-th largest removed (ties kept), p = softmax(score / temperature),
+ * ids[r] the first column whose cumulative p (column order) exceeds
+ * uniforms[r] in [0, 1) (the last column with p > 0 when rounding leaves
+ * none). probabilities (NULL: none) receives p [rows, vocab]. The caller
+ * draws the uniforms; vocab <= 4096. */
+int koemi_herm_sample_tokens(const float* logits, int64_t row_stride, int64_t rows, int64_t vocab,
+                             int64_t exclude_id, float temperature, int64_t top_k, const float* uniforms,
+                             int64_t* ids, float* probabilities, koemi_stream_t stream);
+
 /* causal_surprise of a HERM window from the state before each position
  * (network.py:318-325, 677-698) with the fixed-threshold admission
  * (network.py:349), one kernel: row (b, t) of the batch x length rows is

@@ -176,6 +176,119 @@ __global__ __launch_bounds__(256) void greedy_tokens_kernel(const float* __restr
     if (lane == 0) ids[row] = bi < V ? bi : 0;
 }
 
+// TokenSampler's non-greedy draw (runtime/fast_decode.py:57-95): one
+// workgroup per row of fp32 scores (column `exclude`, the PAD id, at -inf),
+// kept = min(top_k, V) and, when kept < V, every score below the kept-th
+// largest (duplicates counted, ties kept) set to -inf; y = score /
+// temperature; p = softmax(y) (max, exp, sum in a fixed order); the draw is
+// the first column whose cumulative probability (in column order) exceeds the
+// row's uniform u in [0, 1), or, when rounding leaves u at or above the last
+// cumulative value, the last column with p > 0. `probs` (null: none) receives
+// p. The caller supplies the uniforms, so a captured graph draws
+// reproducibly from whatever random numbers it is given.
+constexpr int kSampleThreads = 256;
+constexpr int kSampleMaxV = 4096;
+
+__device__ __forceinline__ float block_reduce(float v, float* sh, bool is_max) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, kWave);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    __syncthreads();  // sh may still be read from an earlier reduction
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int w = 1; w < kSampleThreads / kWave; ++w) r = is_max ? fmaxf(r, sh[w]) : r + sh[w];
+    return r;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void sample_tokens_kernel(
+    const float* __restrict__ logits, int64_t row_stride, int64_t V, int64_t exclude, float temperature,
+    int64_t top_k, const float* __restrict__ uniforms, int64_t* __restrict__ ids, float* __restrict__ probs) {
+    __shared__ float sc[kSampleMaxV];
+    __shared__ float red[kSampleThreads / kWave];
+    __shared__ float thr_sh;
+    __shared__ float scan_sh[kSampleThreads];
+    __shared__ int first_sh, last_sh;
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const float* z = logits + row * row_stride;
+    for (int64_t j = tid; j < V; j += kSampleThreads) sc[j] = j == exclude ? -INFINITY : z[j];
+    if (tid == 0) {
+        thr_sh = -INFINITY;
+        first_sh = static_cast<int>(V);
+        last_sh = -1;
+    }
+    __syncthreads();
+    const int64_t kept = top_k > 0 ? (top_k < V ? top_k : V) : V;
+    if (kept < V) {
+        for (int64_t j = tid; j < V; j += kSampleThreads) {
+            const float x = sc[j];
+            int64_t gt = 0, ge = 0;
+            for (int64_t i = 0; i < V; ++i) {
+                gt += sc[i] > x;
+                ge += sc[i] >= x;
+            }
+            if (gt < kept && ge >= kept) thr_sh = x;  // every such column holds the same value
+        }
+    }
+    __syncthreads();
+    const float thr = thr_sh;
+    float mx = -INFINITY;
+    for (int64_t j = tid; j < V; j += kSampleThreads) {
+        const float y = (sc[j] < thr ? -INFINITY : sc[j]) / temperature;
+        sc[j] = y;
+        mx = fmaxf(mx, y);
+    }
+    mx = block_reduce(mx, red, true);
+    float sum = 0.0f;
+    for (int64_t j = tid; j < V; j += kSampleThreads) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = block_reduce(sum, red, false);
+    // probabilities, then the inverse CDF: thread t owns columns [t c, t c + c)
+    const int64_t c = (V + kSampleThreads - 1) / kSampleThreads;
+    const int64_t j0 = tid * c, j1 = j0 + c < V ? j0 + c : V;
+    float local = 0.0f;
+    for (int64_t j = j0; j < j1; ++j) {
+        const float pj = sc[j] / sum;
+        sc[j] = pj;
+        local += pj;
+        if (probs) probs[row * V + j] = pj;
+    }
+    scan_sh[tid] = local;
+    __syncthreads();
+    if (tid == 0) {  // exclusive prefix of the threads' sums, in column order
+        float run = 0.0f;
+        for (int t = 0; t < kSampleThreads; ++t) {
+            const float v = scan_sh[t];
+            scan_sh[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    const float u = uniforms[row];
+    float cum = scan_sh[tid];
+    for (int64_t j = j0; j < j1; ++j) {
+        cum += sc[j];
+        if (cum > u) {
+            atomicMin(&first_sh, static_cast<int>(j));
+            break;
+        }
+    }
+    for (int64_t j = j1 - 1; j >= j0; --j)
+        if (sc[j] > 0.0f) {
+            atomicMax(&last_sh, static_cast<int>(j));
+            break;
+        }
+    __syncthreads();
+    if (tid == 0) ids[row] = first_sh < V ? first_sh : (last_sh >= 0 ? last_sh : 0);
+}
+
 // One workgroup per row: position t takes the latest valid index before it,
 // an exclusive max-scan of (valid ? t : -1) over 256-position chunks (a wave
 // scan, the wave maxima through LDS, the chunk's carry in a register).
@@ -326,6 +439,24 @@ extern "C" int koemi_herm_greedy_tokens(const float* logits, int64_t row_stride,
     hipLaunchKernelGGL(greedy_tokens_kernel, dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
                        as_stream(stream), logits, row_stride, rows, vocab, exclude_id, ids);
     return check_launch("koemi_herm_greedy_tokens");
+}
+
+extern "C" int koemi_herm_sample_tokens(const float* logits, int64_t row_stride, int64_t rows, int64_t vocab,
+                                        int64_t exclude_id, float temperature, int64_t top_k, const float* uniforms,
+                                        int64_t* ids, float* probabilities, koemi_stream_t stream) {
+    if (rows < 0 || vocab < 1) return fail(KOEMI_ERR_INVALID, "token sampling needs rows >= 0 and a positive vocabulary");
+    if (!(temperature > 0.0f)) return fail(KOEMI_ERR_INVALID, "temperature must be positive");
+    if (top_k < 0) return fail(KOEMI_ERR_INVALID, "top_k must be a positive integer (0: none)");
+    if (vocab > kSampleMaxV) return fail(KOEMI_ERR_UNSUPPORTED, "token sampling supports at most %d columns", kSampleMaxV);
+    if (row_stride == 0) row_stride = vocab;
+    if (row_stride < vocab) return fail(KOEMI_ERR_INVALID, "token sampling row stride below the vocabulary");
+    if (rows == 0) return KOEMI_OK;
+    if (!logits || !uniforms || !ids) return fail(KOEMI_ERR_INVALID, "token sampling received a null pointer");
+    if (rows > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "token sampling: too many rows");
+    hipLaunchKernelGGL(sample_tokens_kernel, dim3(static_cast<unsigned>(rows)), dim3(kSampleThreads), 0,
+                       as_stream(stream), logits, row_stride, vocab, exclude_id, temperature, top_k, uniforms, ids,
+                       probabilities);
+    return check_launch("koemi_herm_sample_tokens");
 }
 
 extern "C" int koemi_herm_token_context(const int64_t* token_ids, const uint8_t* valid, const int64_t* carried_last,

@@ -84,6 +84,7 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
     ),
     "koemi_moe_router_balance_loss": (c_int, (_P, _P, _P, c_int64, _P, _P)),
     "koemi_stream_read": (c_int, (_P, c_int64, c_int, c_int, c_int64, _P, _P)),
+    "koemi_herm_sample_tokens": (c_int, (_P, c_int64, c_int64, c_int64, c_int64, c_float, c_int64, _P, _P, _P, _P)),
     "koemi_moe_check_assignments": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_moe_expert_counts": (c_int, (_P, c_int, _P, _P, c_int64, c_int64, c_int64, _P)),
     "koemi_salient_tail": (

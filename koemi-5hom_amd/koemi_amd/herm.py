@@ -1415,13 +1415,21 @@ class DecodeGraph:
     ``self.states`` to the new set; ``run()`` does the same and returns the
     step's logits. Every layer of a set shares one ``last_token`` buffer (the
     stack's layers carry the same last token). Two eager steps on throwaway
-    copies warm the libraries up before the captures."""
+    copies warm the libraries up before the captures. The next ids are the
+    greedy pick, or with a non-greedy ``policy`` (``sampling.SamplingPolicy``)
+    TokenSampler's draw (fast_decode.py:76-95) from uniforms that ``run()``
+    draws from ``generator`` into a static buffer before each replay."""
 
     def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
-                 states: list[dict[str, Tensor]]) -> None:
+                 states: list[dict[str, Tensor]], *, policy=None, generator: torch.Generator | None = None) -> None:
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
         gate_status(self.ids.device)
+        # non-greedy sampling.SamplingPolicy: the captured step draws from
+        # self.uniforms, refilled from `generator` before every replay
+        self.policy = policy if policy is not None and not policy.greedy else None
+        self.generator = generator
+        self.uniforms = torch.zeros((self.ids.shape[0],), device=self.ids.device, dtype=torch.float32)
         self._sets = []
         for _ in range(2):
             copy = [{k: v.clone() for k, v in st.items()} for st in states]
@@ -1446,7 +1454,13 @@ class DecodeGraph:
 
     def _step(self, src: list[dict[str, Tensor]], dst: list[dict[str, Tensor]]) -> Tensor:
         logits, _ = _stack_decode(self.params, self.settings, self.ids, src, dst)
-        _greedy_tokens(logits, out=self.ids)
+        if self.policy is None:
+            _greedy_tokens(logits, out=self.ids)
+        else:
+            last = logits[:, -1]
+            _native.call("koemi_herm_sample_tokens", _native.ptr(last), logits.stride(0), last.shape[0],
+                         last.shape[1], PAD_TOKEN_ID, float(self.policy.temperature), int(self.policy.top_k or 0),
+                         _native.ptr(self.uniforms), _native.ptr(self.ids), None, _native.stream_of(logits.device))
         return logits
 
     @property
@@ -1458,6 +1472,8 @@ class DecodeGraph:
         return self._logits[1 - self._parity]
 
     def run(self) -> Tensor:
+        if self.policy is not None:
+            self.uniforms.uniform_(0.0, 1.0, generator=self.generator)
         self._graphs[self._parity].replay()
         self._parity ^= 1
         return self.logits

@@ -525,6 +525,29 @@ def merge_router_statistics(statistics: list[dict]) -> dict | None:
             "balance_loss": balance_loss(mass, counts, valid_count)}
 
 
+def sample_tokens(logits: np.ndarray, exclude: int, temperature: float, top_k: int | None,
+                  uniforms: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """TokenSampler's non-greedy draw (runtime/fast_decode.py:57-95) in
+    float64 from the fp32 scores: the excluded (PAD) column at -inf, with
+    top_k every score below the min(top_k, V)-th largest at -inf (ties kept),
+    p = softmax(score / temperature), the id the first column whose
+    cumulative p exceeds the row's uniform. Returns (ids [rows], p [rows, V])."""
+
+    s = np.asarray(logits, np.float32).astype(np.float64).copy()
+    s[:, exclude] = -np.inf
+    rows, vocab = s.shape
+    if top_k is not None and top_k < vocab:
+        thr = np.sort(s, axis=1)[:, vocab - top_k][:, None]
+        s = np.where(s < thr, -np.inf, s)
+    y = s / temperature
+    e = np.exp(y - y.max(axis=1, keepdims=True))
+    p = e / e.sum(axis=1, keepdims=True)
+    cum = np.cumsum(p, axis=1)
+    ids = np.array([int(np.argmax(cum[r] > uniforms[r])) if (cum[r] > uniforms[r]).any()
+                    else int(np.nonzero(p[r] > 0)[0][-1]) for r in range(rows)])
+    return ids, p
+
+
 def expert_counts(assignments: np.ndarray, valid: np.ndarray, expert_count: int) -> np.ndarray:
     """network.py:48-70: counts of valid, in-range assignments per expert."""
 

@@ -34,6 +34,14 @@ wrong sign, swapped operand, wrong rounding order) fails at least one:
   two halves equals the statistics of the whole.
 * permute: the stable-pairs KAT and torch.argsort(stable=True) on random data.
 * grouped_mlp / combine: torch per-row loops of test_moe_cuda.py:79-113.
+* sample_tokens: the reference's own torch expression (index_fill PAD,
+  topk threshold, softmax of scores / temperature; fast_decode.py:57-95) for
+  the probabilities; top_k = 1 -> the masked argmax; u = 0 -> the first
+  column with p > 0; a hand-made three-column case.
+* local_novelty: a brute-force loop over each query's sliding window of
+  cosine similarities; closed forms (a query parallel to an eligible key ->
+  0, no eligible slot -> 1, a query orthogonal to every key -> 1); the
+  reference's refine-ablation forward_window fixture (through the block).
 * grouped_mlp_bound: its values equal grouped_mlp's with bf16 hidden values;
   a torch fp32 implementation with bf16 operands (another summation order)
   stays inside the bound; a dropped output bias or swapped gate and value
@@ -680,3 +688,67 @@ def test_round_bf16_f64_is_one_rounding():
     # conversion first rounds to float32, which lands on the midpoint and ties to even)
     mid = 1.0 + 2.0 ** -8 + 2.0 ** -40
     assert oracle.round_bf16_f64(np.array([mid]))[0] == 1.0 + 2.0 ** -7
+
+
+def test_local_novelty_brute_force_and_closed_forms():
+    rng = np.random.default_rng(8)
+    b, cap, length, d, window = 3, 4, 7, 6, 3
+    ck = rng.normal(size=(b, cap, d))
+    cv = rng.random((b, cap)) < 0.6
+    k = rng.normal(size=(b, length, d))
+    kv = rng.random((b, length)) < 0.7
+    q = rng.normal(size=(b, length, d))
+    got = oracle.local_novelty(ck, cv, k, kv, q, window)
+    for bi in range(b):
+        allk = np.concatenate([ck[bi], k[bi]])
+        allv = np.concatenate([cv[bi], kv[bi]])
+        for t in range(length):
+            sims = [float(allk[s] @ q[bi, t] / (np.linalg.norm(allk[s]) * np.linalg.norm(q[bi, t])))
+                    for s in range(max(cap + t - window, 0), cap + t) if allv[s]]
+            want = min(max(1.0 - max(sims), 0.0), 1.0) if sims else 1.0
+            assert abs(got[bi, t] - want) <= 1e-12
+    # closed forms: parallel -> 0, none eligible -> 1, orthogonal -> 1
+    e = np.eye(4)[None]
+    keys = np.stack([e[0, 0], e[0, 1]])[None]
+    qs = np.stack([3.0 * e[0, 0], e[0, 2]])[None]
+    nov = oracle.local_novelty(np.zeros((1, 0, 4)), np.zeros((1, 0), bool), keys, np.ones((1, 2), bool), qs, 2)
+    assert nov[0, 0] == 1.0  # no slot before the first entry
+    assert nov[0, 1] == 1.0  # e2 is orthogonal to e0
+    qs2 = np.stack([e[0, 1], 2.0 * e[0, 0]])[None]
+    assert oracle.local_novelty(np.zeros((1, 0, 4)), np.zeros((1, 0), bool), keys, np.ones((1, 2), bool), qs2,
+                                2)[0, 1] == 0.0
+
+
+@pytest.mark.parametrize("temperature, top_k", [(1.0, None), (0.7, 5), (2.5, 40), (1.0, 300)])
+def test_sample_tokens_probabilities_match_the_torch_expression(temperature, top_k):
+    g = torch.Generator().manual_seed(12)
+    logits = 3.0 * torch.randn((16, 257), generator=g)
+    logits[3, 10] = logits[3, 11] = 50.0  # a tie at the top
+    scores = logits.float().index_fill(-1, torch.tensor([256]), float("-inf"))
+    if top_k is not None:
+        kept = min(top_k, scores.shape[-1])
+        thr = torch.topk(scores, kept, dim=-1).values[..., -1:]
+        scores = scores.masked_fill(scores < thr, float("-inf"))
+    want = torch.softmax(scores / temperature, dim=-1).double().numpy()
+    u = torch.rand((16,), generator=g).numpy()
+    ids, p = oracle.sample_tokens(logits.numpy(), 256, temperature, top_k, u)
+    np.testing.assert_allclose(p, want, rtol=1e-5, atol=1e-7)
+    assert p[:, 256].max() == 0.0
+    cum = np.cumsum(p, axis=1)
+    for r in range(16):
+        assert cum[r, ids[r]] > u[r] and (ids[r] == 0 or cum[r, ids[r] - 1] <= u[r])
+
+
+def test_sample_tokens_closed_forms():
+    logits = np.array([[0.0, np.log(2.0), np.log(5.0), 99.0]], np.float32)
+    ids, p = oracle.sample_tokens(logits, 3, 1.0, None, np.array([0.0]))
+    np.testing.assert_allclose(p[0], [1 / 8, 2 / 8, 5 / 8, 0.0], rtol=1e-7)
+    assert ids[0] == 0  # u = 0: the first column with p > 0
+    assert oracle.sample_tokens(logits, 3, 1.0, None, np.array([0.2]))[0][0] == 1  # 1/8 <= 0.2 < 3/8
+    assert oracle.sample_tokens(logits, 3, 1.0, None, np.array([0.999]))[0][0] == 2
+    # top_k = 1: the masked argmax, whatever the uniform
+    rng = np.random.default_rng(3)
+    big = rng.normal(size=(8, 257)).astype(np.float32)
+    for u in (0.0, 0.5, 0.999):
+        ids, _ = oracle.sample_tokens(big, 256, 1.3, 1, np.full(8, u))
+        np.testing.assert_array_equal(ids, big[:, :256].argmax(axis=1))
