@@ -711,8 +711,10 @@ def kernel_rows(args, extra: list, device, stream, timer, kernels: dict) -> None
         wb = torch.cat((wts[0], wts[2])).to(torch.bfloat16)
         bb = torch.cat((wts[1], wts[3])).to(torch.bfloat16)
         h0g = torch.zeros((32, 1024), device=device)
-        ms = timer.per_launch_ms([lambda: recurrent.gated_projection_scan(ub, wb, bb, vg, h0g, with_bf16=True)], 2,
-                                 max(3, iters // 4))
+        gp_status = torch.zeros(1, device=device, dtype=torch.int32)  # a timed-out carry wait reports here
+        ms = timer.per_launch_ms([lambda: recurrent.gated_projection_scan(ub, wb, bb, vg, h0g, with_bf16=True,
+                                                                          status=gp_status)], 2, max(3, iters // 4))
+        recurrent.check_gated_scan_status(gp_status)
         kernels["C3g.gated_projection_scan_bf16"] = {
             "ms": round(ms, 5), "TFLOP/s": round(C3G_FLOP / ms / 1e9, 1),
             "frac_mfma_bf16": round(C3G_FLOP / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
