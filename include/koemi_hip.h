@@ -285,6 +285,31 @@ int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens, const int
                                   int64_t hidden, int64_t expert_count, void* workspace, size_t workspace_bytes,
                                   koemi_stream_t stream);
 
+/* Expert weights in fragment order, for koemi_moe_grouped_mlp_fragments (no
+ * counterpart in the reference, whose grouped_expert_mlp of
+ * moe/moe_kernels.cu:501-558 reads row-major weights): weights [matrices,
+ * rows, cols] bf16 (rows a multiple of 32, cols of 64; e.g. the gate weights
+ * [E, hidden, width] as E x hidden rows) into fragments of the same size,
+ * each 32-row block stored as [cols / 64][4][64][8]: element (32 b + r, c)
+ * goes to block b at ((c / 64) * 4 + (c % 32) / 8) * 512 + (32 * ((c % 64) /
+ * 32) + r) * 8 + c % 8. Not in place; 16-byte aligned. */
+int koemi_moe_weights_to_fragments(const void* weights, void* fragments, int64_t matrices, int64_t rows,
+                                   int64_t cols, koemi_stream_t stream);
+
+/* koemi_moe_grouped_mlp_indexed for a few rows per expert (a decode step:
+ * pairs <= 64 * expert_count, KOEMI_ERR_UNSUPPORTED otherwise) with the
+ * three weight tensors in fragment order (koemi_moe_weights_to_fragments of
+ * gate and value [E, hidden, width] and output [E, width, hidden]; biases as
+ * they are): every weight load of the kernels reads contiguous memory. Same
+ * arguments, workspace and results as koemi_moe_grouped_mlp_indexed, bit for
+ * bit (the same products in the same order). */
+int koemi_moe_grouped_mlp_fragments(const void* context, int64_t tokens, const int64_t* sorted_rows,
+                                    const int64_t* segment_offsets, const void* gate_fragments,
+                                    const void* gate_biases, const void* value_fragments, const void* value_biases,
+                                    const void* output_fragments, const void* output_biases, void* output,
+                                    int64_t pairs, int64_t width, int64_t hidden, int64_t expert_count,
+                                    void* workspace, size_t workspace_bytes, koemi_stream_t stream);
+
 /* Salient-memory ring update, LocalKeyValueMemory.salient_tail of
  * model/memory.py:431-455. Per batch row, the carried entries [S] followed by
  * the window's entries [L] (keys/values [*, D] of `dtype`, validity = carried

@@ -591,48 +591,75 @@ __global__ __launch_bounds__(256) void glu_output_simt_kernel(
 // Few rows per expert (a decode step: 64 tokens x top-2 over 16 experts is
 // about 8 rows each). The big tiles above would run 256-row MFMA tiles for 8
 // useful rows, so the step would be bound by wasted matrix work; here it is
-// bound by streaming the expert weights once. A workgroup owns 32 output
-// columns of one expert (GLU: 32 hidden units, their gate and value rows) and
-// every row of that expert, in passes of 32 rows (one MFMA block); its eight
-// waves split K in 64-wide steps, interleaved so that they read adjacent
-// 128-byte pieces of each weight row, keep two steps of loads in flight, and
-// add their partial sums through LDS. Operands come straight from global
+// bound by streaming the expert weights once. A task is 32 output columns of
+// one expert (GLU: 32 hidden units, their gate and value rows) over every row
+// of that expert, in passes of 32 rows (one MFMA block). S waves share a task
+// by K, in interleaved 64-wide steps (adjacent 128-byte pieces of each weight
+// row), and add their partial sums through LDS; with S = 1 a wave owns its
+// task alone, G tasks per workgroup, with no LDS and no barrier, and the
+// epilogue reads its accumulators directly. Each wave keeps PF steps of loads
+// in flight (a ring of PF register sets). Operands come straight from global
 // memory in the MFMA register layout: lane l holds row l % 32 and, per step,
 // the 32 contiguous values of half l / 32, of which MFMA j takes values
 // 8j..8j+7; A and B use the same assignment, so every product pairs equal k.
 // Rows past the segment are not loaded (zero fragments) and not stored.
+//
+// FRAG: the weights are in fragment order (koemi_moe_weights_to_fragments):
+// each 32-row block of a weight matrix is stored as [K / 64 steps][4 loads]
+// [64 lanes][8 values], so that every load instruction of a wave reads 1 KB
+// of contiguous memory and a task streams its 32 x K block front to back
+// (with row-major weights each load touches 32 rows, 32 bytes apiece). The
+// same products in the same order: results equal the row-major path's bit for
+// bit.
 constexpr int kSkinnyCols = 32;
-constexpr int kSkinnyWaves = 8;
 constexpr int64_t kSkinnyMaxRowsPerExpert = 64;  // average over experts below which the path is used
+#ifndef KOEMI_SKINNY_GLU
+#define KOEMI_SKINNY_GLU 2, 1, 2  // S, G, PF of the GLU (first) GEMM
+#endif
+#ifndef KOEMI_SKINNY_OUT
+#define KOEMI_SKINNY_OUT 4, 1, 2  // S, G, PF of the output GEMM
+#endif
 
-template <bool GLU>
-__global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
+template <bool GLU, bool FRAG, int S, int G, int PF>
+__global__ __launch_bounds__(S * G * kWave) void skinny_gemm_kernel(
     const bf16* __restrict__ a, const int64_t* __restrict__ a_index, int64_t a_count,
     const bf16* __restrict__ w0, const bf16* __restrict__ w1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ c,
     const int64_t* __restrict__ offsets, int64_t n_out, int64_t K, int64_t col_groups, int64_t experts,
     int64_t pairs) {
+    static_assert(S == 1 || G == 1, "waves that split K share one task per workgroup (the barriers)");
     constexpr int kMats = GLU ? 2 : 1;
-    __shared__ float red[kSkinnyWaves][kMats][16][kWave];
-    if (static_cast<int64_t>(blockIdx.x) >= experts * col_groups) {
-        // workgroups past the experts' zero the rows past the valid pairs
+    __shared__ float red[S > 1 ? S : 1][kMats][S > 1 ? 16 : 1][kWave];
+    const int64_t task_blocks = (experts * col_groups + G - 1) / G;
+    if (static_cast<int64_t>(blockIdx.x) >= task_blocks) {
+        // workgroups past the tasks zero the rows past the valid pairs
         // (moe_kernels.cu:512, 167-169), a grid stride over those rows
-        const int64_t extra = gridDim.x - experts * col_groups;
+        const int64_t extra = gridDim.x - task_blocks;
         const int64_t start = min(max(offsets[experts], int64_t(0)), pairs);
-        for (int64_t p = start + (blockIdx.x - experts * col_groups); p < pairs; p += extra)
+        for (int64_t p = start + (blockIdx.x - task_blocks); p < pairs; p += extra)
             for (int64_t q = threadIdx.x; q < n_out; q += blockDim.x) c[p * n_out + q] = from_f32<bf16>(0.0f);
         return;
     }
-    const int64_t e = static_cast<int64_t>(blockIdx.x) / col_groups;
-    const int64_t n0 = (static_cast<int64_t>(blockIdx.x) % col_groups) * kSkinnyCols;
+    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int split = wave % S;
+    const int64_t task = static_cast<int64_t>(blockIdx.x) * G + wave / S;
+    if (task >= experts * col_groups) return;  // S == 1 here (G > 1): no barrier follows
+    const int64_t e = task / col_groups;
+    const int64_t n0 = (task % col_groups) * kSkinnyCols;
     const int64_t row0 = offsets[e];
     const int64_t count = offsets[e + 1] - row0;
-    if (count <= 0) return;  // uniform over the workgroup
-    const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    if (count <= 0) return;  // uniform over the task's waves
     const int r = lane % 32, half = lane / 32;
     const int64_t steps = K / 64;
-    const bf16* wr0 = w0 + (e * n_out + n0 + r) * K + 32 * half;
-    const bf16* wr1 = GLU ? w1 + (e * n_out + n0 + r) * K + 32 * half : wr0;
+    // this lane's first weight value: row r, values [32 half, + 32) of each
+    // step; in fragment order the lane's 16 bytes of load j of step k start
+    // at (4 k + j) 512 + 8 lane within the 32-row block
+    const int64_t w_lane = FRAG ? 8 * lane : r * K + 32 * half;
+    const bf16* wr0 = w0 + (e * n_out + n0) * K + w_lane;
+    const bf16* wr1 = GLU ? w1 + (e * n_out + n0) * K + w_lane : wr0;
+    const int64_t col = n0 + r;
+    const float b0 = to_f32(bias0[e * n_out + col]);
+    const float b1 = GLU ? to_f32(bias1[e * n_out + col]) : 0.0f;
     struct Frags {
         bf16x8 w[kMats][4];
         bf16x8 x[4];
@@ -653,8 +680,9 @@ __global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
             const int64_t k = step * 64;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                f.w[0][j] = *reinterpret_cast<const bf16x8*>(wr0 + k + 8 * j);
-                if constexpr (GLU) f.w[1][j] = *reinterpret_cast<const bf16x8*>(wr1 + k + 8 * j);
+                const int64_t at = FRAG ? (step * 4 + j) * 512 : k + 8 * j;
+                f.w[0][j] = *reinterpret_cast<const bf16x8*>(wr0 + at);
+                if constexpr (GLU) f.w[1][j] = *reinterpret_cast<const bf16x8*>(wr1 + at);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -671,44 +699,103 @@ __global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(
                 for (int m = 0; m < kMats; ++m)
                     acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.x[j], f.w[m][j], acc[m], 0, 0, 0);
         };
-        // Two register sets, each holding one step's operands: the loads of
-        // the next two steps are in flight while one is multiplied.
-        Frags f0, f1;
-        int64_t s0 = wave;
-        load(s0, f0);
-        load(s0 + kSkinnyWaves, f1);
-        for (; s0 < steps; s0 += 2 * kSkinnyWaves) {
-            multiply(s0, f0);
-            load(s0 + 2 * kSkinnyWaves, f0);
-            multiply(s0 + kSkinnyWaves, f1);
-            load(s0 + 3 * kSkinnyWaves, f1);
-        }
+        // this wave's steps are split, split + S, ...; set p of the ring holds
+        // the step p (mod PF) of them, loaded PF steps before its multiply
+        Frags f[PF];
 #pragma unroll
-        for (int m = 0; m < kMats; ++m)
+        for (int p = 0; p < PF; ++p) load(split + p * S, f[p]);
+        for (int64_t s0 = split; s0 < steps; s0 += PF * S) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) red[wave][m][i][lane] = acc[m][i];
-        __syncthreads();
-        // 16 accumulator entries x 64 lanes = 1024 outputs, two per thread;
-        // entry i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
-#pragma unroll
-        for (int q = 0; q < 16 / kSkinnyWaves; ++q) {
-            const int i = q * kSkinnyWaves + wave;  // wave-uniform
-            const int64_t row = 8 * (i / 4) + 4 * (lane / 32) + i % 4;
-            if (row >= rows) continue;
-            const int64_t col = n0 + lane % 32;
-            float v0 = 0.0f, v1 = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kSkinnyWaves; ++w) {
-                v0 += red[w][0][i][lane];
-                if constexpr (GLU) v1 += red[w][kMats - 1][i][lane];
+            for (int p = 0; p < PF; ++p) {
+                multiply(s0 + p * S, f[p]);
+                load(s0 + (p + PF) * S, f[p]);
             }
-            float out;
-            if constexpr (GLU) out = silu_f(v0 + to_f32(bias0[e * n_out + col])) * (v1 + to_f32(bias1[e * n_out + col]));
-            else out = v0 + to_f32(bias0[e * n_out + col]);
-            c[(row0 + pass + row) * n_out + col] = from_f32<bf16>(out);
         }
-        __syncthreads();  // red is rewritten by the next pass
+        // entry i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32
+        if constexpr (S == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int64_t row = 8 * (i / 4) + 4 * half + i % 4;
+                if (row >= rows) continue;
+                float out;
+                if constexpr (GLU) out = silu_f(acc[0][i] + b0) * (acc[kMats - 1][i] + b1);
+                else out = acc[0][i] + b0;
+                c[(row0 + pass + row) * n_out + col] = from_f32<bf16>(out);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < kMats; ++m)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) red[split][m][i][lane] = acc[m][i];
+            __syncthreads();
+            // 16 accumulator entries x 64 lanes = 1024 outputs, 16 / S per thread
+#pragma unroll
+            for (int q = 0; q < 16 / S; ++q) {
+                const int i = q * S + split;  // wave-uniform
+                const int64_t row = 8 * (i / 4) + 4 * half + i % 4;
+                if (row >= rows) continue;
+                float v0 = 0.0f, v1 = 0.0f;
+#pragma unroll
+                for (int w = 0; w < S; ++w) {
+                    v0 += red[w][0][i][lane];
+                    if constexpr (GLU) v1 += red[w][kMats - 1][i][lane];
+                }
+                float out;
+                if constexpr (GLU) out = silu_f(v0 + b0) * (v1 + b1);
+                else out = v0 + b0;
+                c[(row0 + pass + row) * n_out + col] = from_f32<bf16>(out);
+            }
+            __syncthreads();  // red is rewritten by the next pass
+        }
     }
+}
+
+// Launch of skinny_gemm_kernel<GLU, FRAG, S, G, PF> over every task (plus
+// `tail_wgs` workgroups that zero the rows past the valid pairs).
+template <bool GLU, bool FRAG, int S, int G, int PF>
+void launch_skinny(const bf16* a, const int64_t* a_index, int64_t a_count, const bf16* w0, const bf16* w1,
+                   const bf16* bias0, const bf16* bias1, bf16* c, const int64_t* offsets, int64_t n_out, int64_t K,
+                   int64_t experts, int64_t pairs, int64_t tail_wgs, hipStream_t s) {
+    const int64_t groups = n_out / kSkinnyCols;
+    const int64_t blocks = (experts * groups + G - 1) / G + tail_wgs;
+    hipLaunchKernelGGL((skinny_gemm_kernel<GLU, FRAG, S, G, PF>), dim3(static_cast<unsigned>(blocks)), dim3(S * G * kWave),
+                       0, s, a, a_index, a_count, w0, w1, bias0, bias1, c, offsets, n_out, K, groups, experts, pairs);
+}
+
+// Both GEMMs of the skinny path: GEMM 1 into the bf16 hidden rows H, GEMM 2
+// into y (with zero_tail, extra workgroups of its launch zero the rows past
+// the valid pairs).
+template <bool FRAG>
+int run_skinny(const void* x, const int64_t* x_index, int64_t x_rows, const int64_t* offsets, const void* Wg,
+               const void* bg, const void* Wv, const void* bv, const void* Wo, const void* bo, void* y, int64_t P,
+               int64_t D, int64_t Hd, int64_t E, bf16* H, hipStream_t s, bool zero_tail) {
+    launch_skinny<true, FRAG, KOEMI_SKINNY_GLU>(static_cast<const bf16*>(x), x_index, x_rows, static_cast<const bf16*>(Wg),
+                                                static_cast<const bf16*>(Wv), static_cast<const bf16*>(bg),
+                                                static_cast<const bf16*>(bv), H, offsets, Hd, D, E, P, 0, s);
+    int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
+    if (st != KOEMI_OK) return st;
+    const int64_t tail_wgs = zero_tail ? (P < 64 ? P : 64) : 0;
+    launch_skinny<false, FRAG, KOEMI_SKINNY_OUT>(H, nullptr, P, static_cast<const bf16*>(Wo),
+                                                 static_cast<const bf16*>(Wo), static_cast<const bf16*>(bo),
+                                                 static_cast<const bf16*>(bo), static_cast<bf16*>(y), offsets, D, Hd, E,
+                                                 P, tail_wgs, s);
+    return check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
+}
+
+// Weights [matrices, rows, cols] bf16 into fragment order: thread t writes
+// the 16 bytes of chunk t of the destination, which in its 32-row block is
+// lane l = t % 64 of load j = (t / 64) % 4 of step k = t / 256: row l % 32 of
+// the block, columns 64 k + 32 (l / 32) + 8 j .. + 8.
+__global__ void weights_to_fragments_kernel(const bf16x8* __restrict__ src, bf16x8* __restrict__ dst,
+                                            int64_t chunks, int64_t cols) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= chunks) return;
+    const int64_t block_chunks = 4 * cols;  // 32 rows x cols values / 8
+    const int64_t block = t / block_chunks, c = t % block_chunks;
+    const int64_t lane = c % 64, j = (c / 64) % 4, step = c / 256;
+    const int64_t row = block * 32 + lane % 32;
+    const int64_t col = step * 64 + 32 * (lane / 32) + 8 * j;
+    dst[t] = src[(row * cols + col) / 8];
 }
 
 // Rows past the valid pairs are zero (moe_kernels.cu:512, 167-169); a
@@ -771,22 +858,7 @@ int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_
     if (E > kMaxScheduleExperts) return fail(KOEMI_ERR_UNSUPPORTED, "grouped MLP supports at most %lld experts",
                                              static_cast<long long>(kMaxScheduleExperts));
     if (P <= kSkinnyMaxRowsPerExpert * E && E * ((Hd > D ? Hd : D) / kSkinnyCols) <= 0x7fffffffLL) {
-        const int64_t groups1 = Hd / kSkinnyCols, groups2 = D / kSkinnyCols;
-        hipLaunchKernelGGL(skinny_gemm_kernel<true>, dim3(static_cast<unsigned>(E * groups1)),
-                           dim3(kSkinnyWaves * kWave), 0, s, static_cast<const bf16*>(x), x_index, x_rows,
-                           static_cast<const bf16*>(Wg),
-                           static_cast<const bf16*>(Wv), static_cast<const bf16*>(bg), static_cast<const bf16*>(bv),
-                           H, offsets, Hd, D, groups1, E, P);
-        int st = check_launch("koemi_moe_grouped_mlp(skinny gemm1)");
-        if (st != KOEMI_OK) return st;
-        // the output GEMM's launch also zeroes the rows past the valid pairs (extra workgroups)
-        const int64_t tail_wgs = zero_tail ? (P < 64 ? P : 64) : 0;
-        hipLaunchKernelGGL(skinny_gemm_kernel<false>, dim3(static_cast<unsigned>(E * groups2 + tail_wgs)),
-                           dim3(kSkinnyWaves * kWave), 0, s, H, static_cast<const int64_t*>(nullptr), P,
-                           static_cast<const bf16*>(Wo),
-                           static_cast<const bf16*>(Wo), static_cast<const bf16*>(bo), static_cast<const bf16*>(bo),
-                           static_cast<bf16*>(y), offsets, D, Hd, groups2, E, P);
-        return check_launch("koemi_moe_grouped_mlp(skinny gemm2)");
+        return run_skinny<false>(x, x_index, x_rows, offsets, Wg, bg, Wv, bv, Wo, bo, y, P, D, Hd, E, H, s, zero_tail);
     }
     hipLaunchKernelGGL(build_schedule_kernel, dim3(1), dim3(kSchedThreads), static_cast<size_t>(E + 1) * sizeof(int32_t),
                        s, offsets, E, P, ws.max_slots, slot_expert, slot_row, slot_end);
@@ -921,4 +993,56 @@ extern "C" int koemi_moe_grouped_mlp_indexed(const void* context, int64_t tokens
     return run_mfma(context, sorted_rows, tokens, segment_offsets, gate_weights, gate_biases, value_weights,
                     value_biases, output_weights, output_biases, output, pairs, width, hidden, expert_count, ws,
                     static_cast<char*>(workspace), as_stream(stream), false);
+}
+
+extern "C" int koemi_moe_weights_to_fragments(const void* weights, void* fragments, int64_t matrices, int64_t rows,
+                                              int64_t cols, koemi_stream_t stream) {
+    if (matrices < 1 || rows < 1 || cols < 1 || rows % 32 != 0 || cols % 64 != 0)
+        return fail(KOEMI_ERR_INVALID, "fragment order needs rows a multiple of 32 and cols a multiple of 64");
+    if (!weights || !fragments) return fail(KOEMI_ERR_INVALID, "fragment order received a null pointer");
+    if (reinterpret_cast<uintptr_t>(weights) % 16 != 0 || reinterpret_cast<uintptr_t>(fragments) % 16 != 0)
+        return fail(KOEMI_ERR_INVALID, "fragment order needs 16-byte aligned weights");
+    if (weights == fragments) return fail(KOEMI_ERR_INVALID, "fragment order cannot run in place");
+    const int64_t chunks = matrices * rows * cols / 8;
+    if (chunks / 256 + 1 > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many weights to reorder");
+    hipLaunchKernelGGL(weights_to_fragments_kernel, dim3(static_cast<unsigned>((chunks + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), static_cast<const bf16x8*>(weights), static_cast<bf16x8*>(fragments), chunks,
+                       cols);
+    return check_launch("koemi_moe_weights_to_fragments");
+}
+
+extern "C" int koemi_moe_grouped_mlp_fragments(const void* context, int64_t tokens, const int64_t* sorted_rows,
+                                               const int64_t* segment_offsets, const void* gate_fragments,
+                                               const void* gate_biases, const void* value_fragments,
+                                               const void* value_biases, const void* output_fragments,
+                                               const void* output_biases, void* output, int64_t pairs, int64_t width,
+                                               int64_t hidden, int64_t expert_count, void* workspace,
+                                               size_t workspace_bytes, koemi_stream_t stream) {
+    if (pairs < 0 || tokens < 1 || width < 1 || hidden < 1 || expert_count < 1)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP needs positive tokens, width, hidden and expert_count");
+    if (!mfma_shape(width, hidden, KOEMI_BF16))
+        return fail(KOEMI_ERR_UNSUPPORTED, "the fragment-order grouped MLP needs width and hidden multiples of %d",
+                    kKAlign);
+    if (pairs > kSkinnyMaxRowsPerExpert * expert_count)
+        return fail(KOEMI_ERR_UNSUPPORTED, "the fragment-order grouped MLP takes at most %lld pairs per expert on "
+                    "average (the few-rows path)", static_cast<long long>(kSkinnyMaxRowsPerExpert));
+    if (pairs == 0) return KOEMI_OK;
+    if (!context || !sorted_rows || !segment_offsets || !gate_fragments || !gate_biases || !value_fragments ||
+        !value_biases || !output_fragments || !output_biases || !output)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP received a null pointer");
+    if (tokens * width > 0x7fffffffLL)
+        return fail(KOEMI_ERR_UNSUPPORTED, "the indexed grouped MLP needs tokens * width < 2^31");
+    const MlpWorkspace ws = mlp_workspace(pairs, width, hidden, expert_count, KOEMI_BF16);
+    if (!workspace || workspace_bytes < ws.total)
+        return fail(KOEMI_ERR_INVALID, "grouped MLP workspace too small: need %zu bytes", ws.total);
+    const bool aligned = reinterpret_cast<uintptr_t>(context) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(gate_fragments) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(value_fragments) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(output_fragments) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(output) % 16 == 0;
+    if (!aligned) return fail(KOEMI_ERR_INVALID, "grouped MLP bf16 operands must be 16-byte aligned");
+    bf16* H = reinterpret_cast<bf16*>(static_cast<char*>(workspace) + ws.hidden_off);
+    return run_skinny<true>(context, sorted_rows, tokens, segment_offsets, gate_fragments, gate_biases, value_fragments,
+                            value_biases, output_fragments, output_biases, output, pairs, width, hidden, expert_count,
+                            H, as_stream(stream), false);
 }

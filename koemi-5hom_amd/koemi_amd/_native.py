@@ -220,6 +220,11 @@ _SIGNATURES: dict[str, tuple[Any, tuple[Any, ...]]] = {
         c_int,
         (_P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
     ),
+    "koemi_moe_weights_to_fragments": (c_int, (_P, _P, c_int64, c_int64, c_int64, _P)),
+    "koemi_moe_grouped_mlp_fragments": (
+        c_int,
+        (_P, c_int64, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_int64, c_int64, _P, c_size_t, _P),
+    ),
     "koemi_moe_combine_workspace_bytes": (c_size_t, (c_int64, c_int64)),
     "koemi_moe_combine": (
         c_int,

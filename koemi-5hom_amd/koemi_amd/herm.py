@@ -228,6 +228,23 @@ def prepare_stack(params: list[dict[str, Tensor]], settings: HermSettings, devic
     return prepared
 
 
+def add_decode_fragments(prepared: list[dict[str, Tensor]]) -> None:
+    """Adds to each layer of a bf16 ``prepare_stack`` result the expert
+    weights in fragment order (``gate_wf``, ``up_wf``, ``down_wf``; see
+    ``moe.weights_to_fragments``), which the decode step's expert GEMMs then
+    stream with contiguous loads. A second copy of the expert weights (the
+    prefill keeps the row-major ones); results are unchanged bit for bit.
+    Layers that already hold them, or whose experts are not bf16 MFMA shapes,
+    are left as they are."""
+
+    for q in prepared:
+        w = q["gate_w"]
+        if "gate_wf" in q or w.dtype != torch.bfloat16 or w.shape[1] % 64 or w.shape[2] % 64:
+            continue
+        for name in ("gate", "up", "down"):
+            q[name + "_wf"] = moe.weights_to_fragments(q[name + "_w"])
+
+
 def initial_states(settings: HermSettings, batch: int, device: torch.device) -> list[dict[str, Tensor]]:
     """KoemiState.create_static (state.py:43-76) per layer: zeros, rings at
     capacity with every slot invalid, last token PAD; with the herm ablation
@@ -709,7 +726,12 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
                                     expert_count=settings.expert_count, pair_weights=weights, validate=False)
         sorted_context, sorted_rows, sorted_experts, offsets = permuted[:4]
         sorted_weights = permuted[4] if weights is not None else None
-    if indexed:
+    if indexed and "gate_wf" in p and sorted_rows.shape[0] <= moe.FEW_PAIRS_PER_EXPERT * settings.expert_count:
+        # a decode step's few rows per expert: the weights in fragment order
+        # (add_decode_fragments), the same results as the indexed call below
+        expert_out = moe.grouped_expert_mlp_fragments(moe_in, sorted_rows, offsets, p["gate_wf"], p["gate_b"],
+                                                      p["up_wf"], p["up_b"], p["down_wf"], p["down_b"])
+    elif indexed:
         expert_out = moe.grouped_expert_mlp_indexed(moe_in, sorted_rows, offsets, p["gate_w"], p["gate_b"],
                                                     p["up_w"], p["up_b"], p["down_w"], p["down_b"])
     else:
@@ -1418,10 +1440,13 @@ class DecodeGraph:
     copies warm the libraries up before the captures. The next ids are the
     greedy pick, or with a non-greedy ``policy`` (``sampling.SamplingPolicy``)
     TokenSampler's draw (fast_decode.py:76-95) from uniforms that ``run()``
-    draws from ``generator`` into a static buffer before each replay."""
+    draws from ``generator`` into a static buffer before each replay. The
+    expert weights of ``params`` are given their fragment-order copies first
+    (``add_decode_fragments``, in place)."""
 
     def __init__(self, params: list[dict[str, Tensor]], settings: HermSettings, ids: Tensor,
                  states: list[dict[str, Tensor]], *, policy=None, generator: torch.Generator | None = None) -> None:
+        add_decode_fragments(params)
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
         gate_status(self.ids.device)

@@ -36,12 +36,14 @@ __all__ = [
     "RouterStatistics",
     "combine_topk",
     "expert_activation_counts",
+    "grouped_expert_mlp_fragments",
     "grouped_expert_mlp_inference",
     "load_native_extension",
     "merge_router_statistics",
     "permute_topk",
     "route_topk_learned",
     "route_topk_valid",
+    "weights_to_fragments",
 ]
 
 _MAX_PERMUTE_EXPERTS = 4095
@@ -673,6 +675,76 @@ def grouped_expert_mlp_indexed(
     workspace = torch.empty((workspace_bytes,), device=context.device, dtype=torch.uint8)
     with torch.cuda.device(context.device):
         _native.call("koemi_moe_grouped_mlp_indexed", x.data_ptr(), int(x.shape[0]), sorted_rows.data_ptr(),
+                     segment_offsets.data_ptr(), *(w.data_ptr() for w in weights), output.data_ptr(), pairs,
+                     input_width, hidden_width, expert_count, workspace.data_ptr(), workspace_bytes,
+                     _native.stream_of(context.device))
+    return output
+
+
+FEW_PAIRS_PER_EXPERT = 64  # pairs per expert on average up to which the skinny (decode) path runs
+
+
+def weights_to_fragments(weights: Tensor) -> Tensor:
+    """Expert weights [experts, rows, cols] bf16 (rows a multiple of 32, cols
+    of 64) in the fragment order of ``grouped_expert_mlp_fragments``
+    (``koemi_moe_weights_to_fragments``): each 32-row block stored as
+    [cols / 64][4][64][8], so that every weight load of the few-rows kernels
+    reads contiguous memory. A new tensor of the same shape whose element
+    order alone differs."""
+
+    if weights.ndim != 3 or weights.dtype != torch.bfloat16:
+        raise CudaMoeValidationError("fragment order takes bf16 [experts, rows, cols] weights")
+    matrices, rows, cols = weights.shape
+    if rows % 32 or cols % 64:
+        raise CudaMoeValidationError("fragment order needs rows a multiple of 32 and cols a multiple of 64")
+    _require_library()
+    src = _aligned(weights.contiguous())
+    out = torch.empty_like(src)
+    with torch.cuda.device(weights.device):
+        _native.call("koemi_moe_weights_to_fragments", src.data_ptr(), out.data_ptr(), matrices, rows, cols,
+                     _native.stream_of(weights.device))
+    return out
+
+
+def grouped_expert_mlp_fragments(
+    context: Tensor,
+    sorted_rows: Tensor,
+    segment_offsets: Tensor,
+    gate_fragments: Tensor,
+    gate_biases: Tensor,
+    value_fragments: Tensor,
+    value_biases: Tensor,
+    output_fragments: Tensor,
+    output_biases: Tensor,
+) -> Tensor:
+    """``grouped_expert_mlp_indexed`` for a few rows per expert (a decode
+    step; at most ``FEW_PAIRS_PER_EXPERT`` pairs per expert on average) with
+    the three weight tensors given by ``weights_to_fragments``
+    (``koemi_moe_grouped_mlp_fragments``). The same outputs bit for bit."""
+
+    if context.ndim != 2 or context.dtype != torch.bfloat16:
+        raise CudaMoeValidationError("context must be a bf16 [tokens, width] tensor")
+    expert_count, hidden_width, input_width = gate_fragments.shape
+    if input_width != context.shape[1] or input_width % 64 or hidden_width % 64:
+        raise CudaMoeValidationError("the fragment-order grouped MLP needs width and hidden multiples of 64")
+    if sorted_rows.dtype != torch.int64 or sorted_rows.ndim != 1 or segment_offsets.shape != (expert_count + 1,):
+        raise CudaMoeValidationError("sorted_rows must be int64 [pairs] and segment_offsets int64 [experts + 1]")
+    pairs = int(sorted_rows.shape[0])
+    if pairs > FEW_PAIRS_PER_EXPERT * expert_count:
+        raise CudaMoeValidationError("the fragment-order grouped MLP takes at most "
+                                     f"{FEW_PAIRS_PER_EXPERT} pairs per expert on average")
+    _require_library()
+    output = torch.empty((pairs, input_width), device=context.device, dtype=context.dtype)
+    if pairs == 0:
+        return output
+    x = _aligned(context.contiguous())
+    weights = [_aligned(t.contiguous()) for t in
+               (gate_fragments, gate_biases, value_fragments, value_biases, output_fragments, output_biases)]
+    workspace_bytes = _native.query("koemi_moe_grouped_mlp_workspace_bytes", pairs, input_width, hidden_width,
+                                    expert_count, _native.dtype_code(torch.bfloat16))
+    workspace = torch.empty((workspace_bytes,), device=context.device, dtype=torch.uint8)
+    with torch.cuda.device(context.device):
+        _native.call("koemi_moe_grouped_mlp_fragments", x.data_ptr(), int(x.shape[0]), sorted_rows.data_ptr(),
                      segment_offsets.data_ptr(), *(w.data_ptr() for w in weights), output.data_ptr(), pairs,
                      input_width, hidden_width, expert_count, workspace.data_ptr(), workspace_bytes,
                      _native.stream_of(context.device))

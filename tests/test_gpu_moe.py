@@ -418,6 +418,55 @@ def test_indexed_grouped_mlp_equals_the_gathered_one(device, tokens, E, D, H, se
     assert torch.equal(got[:n], want[:n])
 
 
+@pytest.mark.parametrize("E, rows, cols", [(16, 2048, 1024), (16, 1024, 2048), (3, 96, 192), (1, 32, 64)])
+def test_weights_to_fragments_order(device, E, rows, cols):
+    """koemi_moe_weights_to_fragments against the layout its declaration
+    states: the torch permutation of [E, rows / 32, 32 r, cols / 64 k, 2 half,
+    4 j, 8] into [E, rows / 32, k, j, half, r, 8], and the stated offset of
+    single elements."""
+    g = torch.Generator(device=device).manual_seed(rows + cols)
+    w = torch.randn((E, rows, cols), generator=g, device=device).to(torch.bfloat16)
+    got = moe.weights_to_fragments(w)
+    want = w.view(E, rows // 32, 32, cols // 64, 2, 4, 8).permute(0, 1, 3, 5, 4, 2, 6).reshape(E, rows, cols)
+    assert torch.equal(got, want)
+    flat_w, flat_got = w.view(-1, cols).cpu(), got.view(-1).cpu()
+    for row, c in ((0, 0), (1, 8), (31, 33), (rows - 1, cols - 1), (E * rows - 1, 63), (E * rows // 2 + 5, cols // 2 + 17)):
+        b, r = divmod(row, 32)
+        at = b * 32 * cols + ((c // 64) * 4 + (c % 32) // 8) * 512 + (32 * ((c % 64) // 32) + r) * 8 + c % 8
+        assert flat_got[at] == flat_w[row, c], (row, c)
+
+
+@pytest.mark.parametrize("sizes, D, H", [
+    ((8, 9, 7, 8, 8, 6, 10, 8, 8, 8, 9, 7, 8, 8, 8, 10), 1024, 2048),  # a C5 decode step: 64 tokens x top-2
+    ((0, 40, 70, 0, 3, 100, 0, 1), 1024, 2048),  # empty experts, two to four 32-row passes
+    ((33, 1, 64, 65), 128, 192),                 # a row in a second block, exactly 64, 65
+    ((0, 0, 0, 0), 256, 384),                    # no valid pair
+])
+def test_fragment_grouped_mlp_equals_the_indexed_one(device, sizes, D, H):
+    """grouped_expert_mlp_fragments (weights in fragment order) gives the bits
+    of grouped_expert_mlp_indexed on the same pairs: the same products in the
+    same order, only the weight addresses differ; the row-major skinny path is
+    itself checked against the float64 oracle above."""
+    g = torch.Generator(device=device).manual_seed(sum(sizes) + H)
+    E = len(sizes)
+    tokens = 97
+    offsets = torch.tensor(np.concatenate([[0], np.cumsum(sizes)]), dtype=torch.int64, device=device)
+    P = int(offsets[-1]) + 3  # rows past the valid pairs, written by neither
+    ctx = torch.randn((tokens, D), generator=g, device=device).to(torch.bfloat16)
+    rows = torch.randint(0, tokens, (P,), generator=g, device=device)
+    ws = [(0.05 * torch.randn(shape, generator=g, device=device)).to(torch.bfloat16)
+          for shape in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    frags = [moe.weights_to_fragments(ws[i]) for i in (0, 2, 4)]
+    want = moe.grouped_expert_mlp_indexed(ctx, rows, offsets, *ws)
+    got = moe.grouped_expert_mlp_fragments(ctx, rows, offsets, frags[0], ws[1], frags[1], ws[3], frags[2], ws[5])
+    torch.cuda.synchronize()
+    n = int(offsets[-1])
+    assert torch.equal(got[:n], want[:n])
+    with pytest.raises(moe.CudaMoeValidationError):
+        moe.grouped_expert_mlp_fragments(ctx, torch.zeros(64 * E + 1, dtype=torch.int64, device=device), offsets,
+                                         frags[0], ws[1], frags[1], ws[3], frags[2], ws[5])
+
+
 @pytest.mark.parametrize("tokens, k, E, id_dtype", [(32768, 2, 16, torch.int64), (64, 2, 16, torch.int64),
                                                      (5000, 3, 13, torch.int32), (1, 2, 4, torch.int64)])
 def test_hash_routed_permutation_equals_route_then_permute(device, tokens, k, E, id_dtype):
