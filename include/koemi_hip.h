@@ -858,6 +858,22 @@ int koemi_herm_combine_norm(const void* expert_outputs, const int64_t* sorted_ro
                             int64_t num_segments, float eps, void* workspace, size_t workspace_bytes,
                             koemi_stream_t stream);
 
+/* koemi_herm_combine_norm with the context formed in place (no reference
+ * counterpart; a build-side fusion of the HERM block's tail): the context is
+ * the fusion normalizer's output RMSNorm(fusion_rows) * fusion_norm_weight
+ * (network.py:723-732) of the bf16 fusion rows [tokens, width] (the fusion
+ * layer's output, bias included), with the arithmetic of koemi_herm_rmsnorm
+ * on those rows, so the outputs equal koemi_herm_rmsnorm followed by
+ * koemi_herm_combine_norm on its fp32 result bit for bit, and the fp32
+ * context never goes through memory. Pairs by pair_positions only; the
+ * other arguments as koemi_herm_combine_norm. */
+int koemi_herm_combine_norm_fusion(const void* expert_outputs, const int64_t* pair_positions,
+                                   const int64_t* segment_offsets, const float* pair_weights,
+                                   const void* fusion_rows, const float* fusion_norm_weight, const uint8_t* mask,
+                                   const float* expert_norm_weight, const float* next_norm_weight, float* output,
+                                   void* next_input_bf16, int64_t pairs, int64_t width, int64_t tokens,
+                                   int64_t top_k, int64_t num_segments, float eps, koemi_stream_t stream);
+
 /* Measurement only (no counterpart in the reference): reads `bytes` (a
  * multiple of 16) from `src` with `grid` workgroups of `block` threads, each
  * thread issuing `unroll` (1, 2, 4 or 8) 16-byte loads per pass of a

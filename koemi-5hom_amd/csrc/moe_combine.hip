@@ -291,29 +291,62 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
 // are loaded first, ahead of the pair-position chain they do not depend on;
 // many rows (a prefill) load them where they are used, which keeps the
 // registers, and the occupancy, of a bandwidth-bound pass.
-template <int KMAX, int NV, bool POS, bool PRE = false>
+// FN: the context is not read; it is the fusion normalizer's output
+// RMSNorm(fusion) * w_fusion (network.py:723-732), formed here from the bf16
+// fusion rows with the arithmetic of herm_rmsnorm_kernel (the same lanes,
+// the same sum-of-squares order: the same bits as the fp32 rows that kernel
+// writes), so that no fp32 copy of it goes through memory.
+template <int KMAX, int NV, bool POS, bool PRE = false, bool FN = false>
 __global__ __launch_bounds__(kWave * kCombineWaves) void combine_norm_kernel(
     const bf16* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ valid_end, const float* __restrict__ pair_w, const float* __restrict__ ctx,
     const uint8_t* __restrict__ mask, const float* __restrict__ w_expert, const float* __restrict__ w_next,
-    float* __restrict__ out, bf16* __restrict__ out_next, int64_t tokens, int64_t k, int H, float eps) {
+    float* __restrict__ out, bf16* __restrict__ out_next, int64_t tokens, int64_t k, int H, float eps,
+    const bf16* __restrict__ fusion, const float* __restrict__ w_fusion) {
     const int64_t t = static_cast<int64_t>(blockIdx.x) * kCombineWaves + threadIdx.x / kWave;
     if (t >= tokens) return;
     const int lane = lane_id();
     const float* xr = ctx + t * H;
     float4 xq[NV], wq_e[NV], wq_n[NV];
+    if constexpr (FN) {
+        float fv[NV][4];
+        float ssf = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = (j * kWave + lane) * 4;
+            if (c < H) {
+                const float4 q = load4(fusion + t * H + c);
+                fv[j][0] = q.x; fv[j][1] = q.y; fv[j][2] = q.z; fv[j][3] = q.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) fv[j][i] = 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ssf = fmaf(fv[j][i], fv[j][i], ssf);
+        }
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) ssf += __shfl_xor(ssf, off, kWave);
+        const float invf = rsqrtf(ssf / static_cast<float>(H) + eps);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = (j * kWave + lane) * 4;
+            const float4 wq = *reinterpret_cast<const float4*>(w_fusion + (c < H ? c : 0));
+            xq[j] = make_float4(fv[j][0] * invf * wq.x, fv[j][1] * invf * wq.y, fv[j][2] * invf * wq.z,
+                                fv[j][3] * invf * wq.w);
+        }
+    }
     if constexpr (PRE) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = (j * kWave + lane) * 4;
             const int cc = c < H ? c : 0;
-            xq[j] = *reinterpret_cast<const float4*>(xr + cc);
+            if constexpr (!FN) xq[j] = *reinterpret_cast<const float4*>(xr + cc);
             wq_e[j] = *reinterpret_cast<const float4*>(w_expert + cc);
             wq_n[j] = w_next != nullptr ? *reinterpret_cast<const float4*>(w_next + cc)
                                         : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
-    auto ctx4 = [&](int j, int c) { return PRE ? xq[j] : *reinterpret_cast<const float4*>(xr + c); };
+    auto ctx4 = [&](int j, int c) { return (PRE || FN) ? xq[j] : *reinterpret_cast<const float4*>(xr + c); };
     auto we4 = [&](int j, int c) { return PRE ? wq_e[j] : *reinterpret_cast<const float4*>(w_expert + c); };
     auto wn4 = [&](int j, int c) { return PRE ? wq_n[j] : *reinterpret_cast<const float4*>(w_next + c); };
     int n = 0;
@@ -494,7 +527,8 @@ extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t
     const int64_t* valid_end = segment_offsets + num_segments;
     auto launch = [&](auto kernel, const int32_t* cnt, const int64_t* pos) {
         hipLaunchKernelGGL(kernel, grid, block, 0, s, y, cnt, pos, valid_end, pair_weights, context, mask,
-                           expert_norm_weight, next_norm_weight, output, o16, tokens, top_k, H, eps);
+                           expert_norm_weight, next_norm_weight, output, o16, tokens, top_k, H, eps,
+                           static_cast<const bf16*>(nullptr), static_cast<const float*>(nullptr));
         return check_launch("koemi_herm_combine_norm(rows)");
     };
     if (pair_positions != nullptr) {  // the permutation's own map: no inversion
@@ -534,4 +568,47 @@ extern "C" int koemi_herm_combine_norm(const void* expert_outputs, const int64_t
                                 : launch(combine_norm_kernel<4, 4, false>, cnt, pos);
     return wide ? launch(combine_norm_kernel<8, 8, false>, cnt, pos)
                 : launch(combine_norm_kernel<8, 4, false>, cnt, pos);
+}
+
+extern "C" int koemi_herm_combine_norm_fusion(const void* expert_outputs, const int64_t* pair_positions,
+                                              const int64_t* segment_offsets, const float* pair_weights,
+                                              const void* fusion_rows, const float* fusion_norm_weight,
+                                              const uint8_t* mask, const float* expert_norm_weight,
+                                              const float* next_norm_weight, float* output, void* next_input_bf16,
+                                              int64_t pairs, int64_t width, int64_t tokens, int64_t top_k,
+                                              int64_t num_segments, float eps, koemi_stream_t stream) {
+    if (tokens < 1 || width < 1 || pairs < 0) return fail(KOEMI_ERR_INVALID, "combine norm needs tokens, width >= 1");
+    if (top_k < 1 || top_k > 8) return fail(KOEMI_ERR_UNSUPPORTED, "combine norm takes top_k in [1, 8]");
+    if (num_segments < 1) return fail(KOEMI_ERR_INVALID, "segment_offsets must have at least two entries");
+    if (width % 4 != 0 || width > 4 * kWave * 8)
+        return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs a width that is a multiple of 4 and at most 2048");
+    if (!segment_offsets || !fusion_rows || !fusion_norm_weight || !expert_norm_weight || !pair_positions ||
+        (pairs > 0 && !expert_outputs))
+        return fail(KOEMI_ERR_INVALID, "combine norm received a null pointer");
+    if (!output && !(next_norm_weight && next_input_bf16))
+        return fail(KOEMI_ERR_INVALID, "combine norm has no output");
+    if ((reinterpret_cast<uintptr_t>(expert_outputs) | reinterpret_cast<uintptr_t>(fusion_rows) |
+         reinterpret_cast<uintptr_t>(fusion_norm_weight) | reinterpret_cast<uintptr_t>(output) |
+         reinterpret_cast<uintptr_t>(next_input_bf16)) % 16)
+        return fail(KOEMI_ERR_UNSUPPORTED, "combine norm needs 16-byte aligned rows");
+    hipStream_t s = as_stream(stream);
+    const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+    const bf16* y = static_cast<const bf16*>(expert_outputs);
+    bf16* o16 = static_cast<bf16*>(next_input_bf16);
+    const bf16* fr = static_cast<const bf16*>(fusion_rows);
+    const int H = static_cast<int>(width);
+    const bool wide = width > 4 * kWave * 4;
+    const int64_t* valid_end = segment_offsets + num_segments;
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, y, static_cast<const int32_t*>(nullptr), pair_positions,
+                           valid_end, pair_weights, static_cast<const float*>(nullptr), mask, expert_norm_weight,
+                           next_norm_weight, output, o16, tokens, top_k, H, eps, fr, fusion_norm_weight);
+        return check_launch("koemi_herm_combine_norm_fusion");
+    };
+    if (top_k <= 2) return wide ? launch(combine_norm_kernel<2, 8, true, false, true>)
+                                : launch(combine_norm_kernel<2, 4, true, false, true>);
+    if (top_k <= 4) return wide ? launch(combine_norm_kernel<4, 8, true, false, true>)
+                                : launch(combine_norm_kernel<4, 4, true, false, true>);
+    return wide ? launch(combine_norm_kernel<8, 8, true, false, true>)
+                : launch(combine_norm_kernel<8, 4, true, false, true>);
 }

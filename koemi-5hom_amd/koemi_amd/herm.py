@@ -672,8 +672,16 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
 
     batch, length = ids.shape
     d = settings.width
+    k = settings.top_k
     lin = settings.linear_dtype
     low = lin if lin == torch.bfloat16 else None
+    # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
+    # permutation's indices (no sorted copy of the context); hash routing is
+    # then done inside the permutation (no assignments tensor)
+    indexed = low is not None and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
+    hashed = indexed and settings.expert_routing != "learned"
+    tail = low is not None and k <= 8 and d % 4 == 0 and d <= 2048  # the combined expert tail below
+    fusion_rows = None  # bf16 fusion output whose fp32 normalized copy the expert tail forms itself
     if not isinstance(pieces, Tensor) and _fusion_split_fits(p, pieces, d):
         fused, fused_low = _fusion_split(p, pieces, d)
     else:
@@ -685,18 +693,20 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
             fusion_in = torch.empty((batch, length, 4 * d), device=ids.device, dtype=low)
             _native.call("koemi_herm_concat_bf16", *(_native.ptr(t.contiguous()) for t in pieces), 4,
                          batch * length, d, _native.ptr(fusion_in), _native.stream_of(ids.device))
-        fused_pair = _rms(_projection(fusion_in, p, "fusion"), p["fusion_norm"], low=low)
-        fused, fused_low = fused_pair if low is not None else (fused_pair, None)
+        projected = _projection(fusion_in, p, "fusion")
+        if hashed and tail and projected.dtype == torch.bfloat16:
+            # only the bf16 normalized rows are written here (the experts'
+            # input); koemi_herm_combine_norm_fusion forms the fp32 ones
+            fusion_rows = projected.reshape(-1, d)
+            fused, fused_low = None, _rms(projected, p["fusion_norm"], fp32=False, low=low)[1]
+        else:
+            fused_pair = _rms(projected, p["fusion_norm"], low=low)
+            fused, fused_low = fused_pair if low is not None else (fused_pair, None)
 
-    k = settings.top_k
-    flat = fused.reshape(-1, d)
+    flat = fused.reshape(-1, d) if fused is not None else None
+    tokens = batch * length
     flat_valid = valid.reshape(-1)
     moe_in = fused_low.reshape(-1, d) if fused_low is not None else flat.to(lin)
-    # bf16 MFMA shapes: the first expert GEMM reads the context rows by the
-    # permutation's indices (no sorted copy of the context); hash routing is
-    # then done inside the permutation (no assignments tensor)
-    indexed = moe_in.dtype == torch.bfloat16 and d % 64 == 0 and p["gate_w"].shape[1] % 64 == 0
-    hashed = indexed and settings.expert_routing != "learned"
     if settings.expert_routing == "learned":
         # LearnedExpertMixture (router.py:43-97): the bias-free gate on the fp32
         # context (rows of invalid tokens are routed to -1 whatever their
@@ -738,21 +748,30 @@ def _fuse_mix_predict(p: dict[str, Tensor], settings: HermSettings, ids: Tensor,
         expert_out = moe.grouped_expert_mlp_inference(sorted_context, sorted_experts, offsets, p["gate_w"],
                                                       p["gate_b"], p["up_w"], p["up_b"], p["down_w"], p["down_b"],
                                                       validate=False)
-    if low is not None and k <= 8 and d % 4 == 0 and d <= 2048:
+    if tail:
         # the combine, the expert normalizer and (inside a stack) the next
         # block's input norm in one kernel
-        tokens = flat.shape[0]
-        final = (torch.empty((tokens, d), device=flat.device, dtype=torch.float32)
+        device = ids.device
+        final = (torch.empty((tokens, d), device=device, dtype=torch.float32)
                  if with_logits or next_norm is None else None)
-        u_next = torch.empty((tokens, d), device=flat.device, dtype=torch.bfloat16) if next_norm is not None else None
-        need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k) if pair_positions is None else 0
-        workspace = torch.empty((need,), device=flat.device, dtype=torch.uint8) if need else None
-        _native.call("koemi_herm_combine_norm", _native.ptr(expert_out), _native.ptr(sorted_rows),
-                     _native.ptr(pair_positions), _native.ptr(offsets), _native.ptr(sorted_weights),
-                     _native.ptr(flat.contiguous()),
-                     _native.ptr(flat_valid), _native.ptr(p["expert_norm"]), _native.ptr(next_norm),
-                     _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]), d, tokens, k,
-                     settings.expert_count, _EPS, _native.ptr(workspace), need, _native.stream_of(flat.device))
+        u_next = torch.empty((tokens, d), device=device, dtype=torch.bfloat16) if next_norm is not None else None
+        if fusion_rows is not None and pair_positions is not None:
+            _native.call("koemi_herm_combine_norm_fusion", _native.ptr(expert_out), _native.ptr(pair_positions),
+                         _native.ptr(offsets), _native.ptr(sorted_weights), _native.ptr(fusion_rows),
+                         _native.ptr(p["fusion_norm"]), _native.ptr(flat_valid), _native.ptr(p["expert_norm"]),
+                         _native.ptr(next_norm), _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]),
+                         d, tokens, k, settings.expert_count, _EPS, _native.stream_of(device))
+        else:
+            if flat is None:  # the fp32 normalized fusion rows after all
+                flat = _rms(fusion_rows, p["fusion_norm"])
+            need = _native.query("koemi_moe_combine_workspace_bytes", tokens, k) if pair_positions is None else 0
+            workspace = torch.empty((need,), device=device, dtype=torch.uint8) if need else None
+            _native.call("koemi_herm_combine_norm", _native.ptr(expert_out), _native.ptr(sorted_rows),
+                         _native.ptr(pair_positions), _native.ptr(offsets), _native.ptr(sorted_weights),
+                         _native.ptr(flat.contiguous()),
+                         _native.ptr(flat_valid), _native.ptr(p["expert_norm"]), _native.ptr(next_norm),
+                         _native.ptr(final), _native.ptr(u_next), int(expert_out.shape[0]), d, tokens, k,
+                         settings.expert_count, _EPS, _native.ptr(workspace), need, _native.stream_of(device))
         logits = _linear(final.view(batch, length, d), p["head_w"], p["head_b"]) if with_logits else None
         if next_norm is None:
             return final.view(batch, length, d), logits

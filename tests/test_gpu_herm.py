@@ -427,3 +427,42 @@ def test_combine_norm_equals_combine_then_the_two_norms(device, tokens, learned)
         torch.cuda.synchronize()
         assert torch.equal(final, want_final), by_position
         assert torch.equal(nxt, want_next), by_position
+
+
+@pytest.mark.parametrize("tokens, d, k", [(4096, 1024, 2), (300, 1024, 2), (64, 2048, 3), (129, 256, 1)])
+def test_combine_norm_fusion_equals_the_fusion_norm_then_combine_norm(device, tokens, d, k):
+    """koemi_herm_combine_norm_fusion (the fusion normalizer formed inside the
+    expert tail from the bf16 fusion rows) gives the bits of herm_rmsnorm on
+    those rows followed by koemi_herm_combine_norm on its fp32 result, with
+    all three outputs (final, next input) and invalid rows."""
+    g = torch.Generator(device=device).manual_seed(tokens + d + k)
+    E, hidden = 8, 128
+    ctx = torch.randn((tokens, d), generator=g, device=device).to(torch.bfloat16)
+    valid = torch.rand((tokens,), generator=g, device=device) < 0.9
+    ids = torch.randint(0, 256, (tokens,), generator=g, device=device)
+    a = moe.route_topk_valid(ids, torch.roll(ids, 1), valid, expert_count=E, top_k=k, validate=False)
+    rows, _, offsets, _, positions = moe.permute_indices(a, valid, expert_count=E)
+    ws = [(0.05 * torch.randn(shape, generator=g, device=device)).to(torch.bfloat16)
+          for shape in ((E, hidden, d), (E, hidden), (E, hidden, d), (E, hidden), (E, d, hidden), (E, d))]
+    y = moe.grouped_expert_mlp_indexed(ctx, rows, offsets, *ws)
+    fusion = (3.0 * torch.randn((tokens, d), generator=g, device=device)).to(torch.bfloat16)
+    w_f, w_e, w_n = (1.0 + 0.1 * torch.randn((d,), generator=g, device=device) for _ in range(3))
+    flat = herm._rms(fusion, w_f)
+    outs = []
+    for fused_form in (False, True):
+        final = torch.empty((tokens, d), device=device, dtype=torch.float32)
+        nxt = torch.empty((tokens, d), device=device, dtype=torch.bfloat16)
+        if fused_form:
+            _native.call("koemi_herm_combine_norm_fusion", _native.ptr(y), _native.ptr(positions),
+                         _native.ptr(offsets), None, _native.ptr(fusion), _native.ptr(w_f), _native.ptr(valid),
+                         _native.ptr(w_e), _native.ptr(w_n), _native.ptr(final), _native.ptr(nxt),
+                         int(y.shape[0]), d, tokens, k, E, herm._EPS, _native.stream_of(device))
+        else:
+            _native.call("koemi_herm_combine_norm", _native.ptr(y), _native.ptr(rows), _native.ptr(positions),
+                         _native.ptr(offsets), None, _native.ptr(flat), _native.ptr(valid), _native.ptr(w_e),
+                         _native.ptr(w_n), _native.ptr(final), _native.ptr(nxt), int(y.shape[0]), d, tokens, k, E,
+                         herm._EPS, None, 0, _native.stream_of(device))
+        outs.append((final, nxt))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert not valid.all() and torch.equal(outs[1][0][~valid], flat[~valid])  # invalid rows keep the context
