@@ -340,6 +340,27 @@ def gate_status(device: torch.device | str) -> Tensor:
     return word
 
 
+_BRANCH_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def branch_stream(device: torch.device | str) -> torch.cuda.Stream:
+    """The device's second stream (default priority) for the independent
+    branches of a captured ``block_sequence``: the local and salient rings and
+    reads run on it beside the associative memory on the capture stream, as
+    parallel branches of the graph that join before the fusion layer.
+    Created on first use, which must come before any capture (the graph
+    classes call it in their constructors); a capture on a device without it
+    runs the branches in turn."""
+
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _BRANCH_STREAMS.get(index)
+    if stream is None:
+        stream = torch.cuda.Stream(device=torch.device("cuda", index))
+        _BRANCH_STREAMS[index] = stream
+    return stream
+
+
 def check_gate_status(device: torch.device | str) -> None:
     """Raise ``recurrent.GatedScanTimeoutError`` if a captured fused gate
     kernel on ``device`` has reported a timed-out wait (a host sync)."""
@@ -1175,18 +1196,43 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     # local keys and values read in place from the projection (see block_window)
     local_keys, local_values = projected[..., :d], projected[..., d:2 * d]
     cap_l, cap_s = settings.local_memory_size, settings.salience_memory_size
-    local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],
-                                            local_keys, local_values, valid, window=chunk, capacity=cap_l, tail=True,
-                                            key_valid=valid)
     per_window = lambda t: None if t is None else t.view(rows, chunk, *t.shape[2:])
-    local_value = memory.read_local_window(*local_rings, per_window(local_keys), per_window(local_values),
-                                           per_window(valid), per_window(ws), window=cap_l,
-                                           out=per_window(_block(fusion_in, 2, d)))
+    # Under capture the local and salient memories (rings and reads) form a
+    # branch of the graph on the branch stream beside the associative memory
+    # (the refine memory reads the local ring, so that ablation stays in turn).
+    main = torch.cuda.current_stream(ids.device)
+    side = None
+    if not settings.refine and torch.cuda.is_current_stream_capturing():
+        side = _BRANCH_STREAMS.get(ids.device.index if ids.device.index is not None else torch.cuda.current_device())
+    if side is not None:
+        side.wait_stream(main)
 
+    def rings_and_reads():
+        local_rings, local_final = window_rings(state["local_keys"], state["local_values"], state["local_valid"],
+                                                local_keys, local_values, valid, window=chunk, capacity=cap_l,
+                                                tail=True, key_valid=valid)
+        local_value = memory.read_local_window(*local_rings, per_window(local_keys), per_window(local_values),
+                                               per_window(valid), per_window(ws), window=cap_l,
+                                               out=per_window(_block(fusion_in, 2, d)))
+        salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"],
+                                                    state["salient_valid"], local_keys, local_values, admission,
+                                                    window=chunk, capacity=cap_s, tail=False, key_valid=valid)
+        salient_value = memory.read_salient_window(*salient_rings, per_window(local_keys), per_window(local_values),
+                                                   per_window(admission), per_window(ws),
+                                                   out=per_window(_block(fusion_in, 3, d)))
+        return local_rings, local_final, local_value, salient_final, salient_value
+
+    if side is not None:
+        with torch.cuda.stream(side):
+            local_rings, local_final, local_value, salient_final, salient_value = rings_and_reads()
+    else:
+        local_rings, local_final, local_value, salient_final, salient_value = rings_and_reads()
     fast, basis, normalizer = associative_scan_read_windows(projected, surprise, valid, state["basis"],
                                                             state["normalizer"], width=d,
                                                             features=settings.memory_features, window=chunk,
                                                             out=None if settings.refine else _block(fusion_in, 1, d))
+    if side is not None:
+        main.wait_stream(side)
     refine_next = {}
     if settings.refine:
         # the refine memory (network.py:359-384) of every window at once: each
@@ -1199,12 +1245,6 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
             features=settings.memory_features, rate=settings.refine_decay_rate, window=chunk)
         fast = _refine_gate(p, ws, fast, refine, local_value.view(batch, length, d), _block(fusion_in, 1, d), low)
         refine_next = {"refine_basis": refine_basis, "refine_normalizer": refine_normalizer}
-    salient_rings, salient_final = window_rings(state["salient_keys"], state["salient_values"], state["salient_valid"],
-                                                local_keys, local_values, admission, window=chunk, capacity=cap_s,
-                                                tail=False, key_valid=valid)
-    salient_value = memory.read_salient_window(*salient_rings, per_window(local_keys), per_window(local_values),
-                                               per_window(admission), per_window(ws),
-                                               out=per_window(_block(fusion_in, 3, d)))
     if fusion_in is not None:
         pieces = fusion_in
     else:
@@ -1274,6 +1314,7 @@ class SequencePrefill:
         self.params, self.settings = params, settings
         self.ids = ids.clone().contiguous()
         self.status = gate_status(self.ids.device)
+        branch_stream(self.ids.device)
         self.start = [{k: v.clone() for k, v in st.items()} for st in states]
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
