@@ -127,6 +127,17 @@ __device__ __forceinline__ void gate_pair(float zr, float zc, float br, float bc
 }
 
 // Four consecutive values as fp32 (one 16-byte fp32 or 8-byte bf16 load).
+// 16 bytes stored with a non-temporal hint: outputs written once and far
+// larger than the caches (above KOEMI_NT_STORE_BYTES) skip them.
+#ifndef KOEMI_NT_STORE_BYTES
+#define KOEMI_NT_STORE_BYTES (int64_t(16) << 20)
+#endif
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+    typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+    const u32x4_nt w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4_nt*>(p));
+}
+
 __device__ __forceinline__ float4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 __device__ __forceinline__ float4 load4(const bf16* p) {
     const uint2 u = *reinterpret_cast<const uint2*>(p);

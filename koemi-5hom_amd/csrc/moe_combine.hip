@@ -155,7 +155,7 @@ __device__ __forceinline__ void sort_positions(int64_t (&p)[KMAX]) {
         }
 }
 
-template <typename T, int KMAX, bool VEC>
+template <typename T, int KMAX, bool VEC, bool NTS = false>
 __global__ __launch_bounds__(kWave * kCombineWaves) void combine_rows_small_kernel(
     const T* __restrict__ y, const int32_t* __restrict__ cnt, const int64_t* __restrict__ pos,
     const float* __restrict__ pair_w, T* __restrict__ out, int64_t tokens, int64_t k, int64_t D) {
@@ -214,7 +214,8 @@ __global__ __launch_bounds__(kWave * kCombineWaves) void combine_rows_small_kern
                 V o;
 #pragma unroll
                 for (int q = 0; q < N; ++q) o.e[q] = from_f32<T>(acc[q]);
-                reinterpret_cast<uint4*>(orow)[v] = o.raw;
+                if constexpr (NTS) store16_nt(reinterpret_cast<uint4*>(orow) + v, o.raw);
+                else reinterpret_cast<uint4*>(orow)[v] = o.raw;
             }
         }
     } else {
@@ -250,9 +251,13 @@ int launch_combine_rows(const void* y, const int32_t* cnt, const int64_t* pos, c
     const bool vec = (D * static_cast<int64_t>(sizeof(T))) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 16 == 0;
     const dim3 grid(grid_for(tokens, kCombineWaves)), block(kWave * kCombineWaves);
+    const bool nts = tokens * D * static_cast<int64_t>(sizeof(T)) > KOEMI_NT_STORE_BYTES;  // written once, far beyond the caches
 #define KOEMI_COMBINE_SMALL(KMAX)                                                                                   \
     if (k <= KMAX) {                                                                                                \
-        if (vec)                                                                                                    \
+        if (vec && nts)                                                                                             \
+            hipLaunchKernelGGL((combine_rows_small_kernel<T, KMAX, true, true>), grid, block, 0, s,                 \
+                               static_cast<const T*>(y), cnt, pos, pair_w, static_cast<T*>(out), tokens, k, D);      \
+        else if (vec)                                                                                               \
             hipLaunchKernelGGL((combine_rows_small_kernel<T, KMAX, true>), grid, block, 0, s,                       \
                                static_cast<const T*>(y), cnt, pos, pair_w, static_cast<T*>(out), tokens, k, D);      \
         else                                                                                                        \

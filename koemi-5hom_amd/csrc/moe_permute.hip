@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kWave) void permute_scatter_kernel(
     }
 }
 
-template <typename T, bool VEC>
+template <typename T, bool VEC, bool NTS = false>
 __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __restrict__ ctx,
                                                                    const int64_t* __restrict__ dest,
                                                                    const int64_t* __restrict__ offsets_end,
@@ -328,7 +328,11 @@ __global__ __launch_bounds__(kWave * 4) void permute_gather_kernel(const T* __re
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int64_t v = v0 + u * kWave + lane;
-                    if (v < nvec) dst[v] = keep ? buf[u] : make_uint4(0, 0, 0, 0);
+                    if (v < nvec) {
+                        const uint4 val = keep ? buf[u] : make_uint4(0, 0, 0, 0);
+                        if constexpr (NTS) store16_nt(dst + v, val);
+                        else dst[v] = val;
+                    }
                 }
             }
         }
@@ -444,7 +448,11 @@ int run_gather(const void* ctx, const int64_t* dest, const int64_t* offsets_end,
     const bool vec = (D * static_cast<int64_t>(sizeof(T))) % 16 == 0 && reinterpret_cast<uintptr_t>(ctx) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(out) % 16 == 0;
     const dim3 grid(grid_for(tokens, 4)), block(kWave * 4);
-    if (vec)
+    // the sorted context is written once and is far larger than the caches
+    if (vec && tokens * k * D * static_cast<int64_t>(sizeof(T)) > KOEMI_NT_STORE_BYTES)
+        hipLaunchKernelGGL((permute_gather_kernel<T, true, true>), grid, block, 0, s, static_cast<const T*>(ctx), dest,
+                           offsets_end, static_cast<T*>(out), tokens, k, D);
+    else if (vec)
         hipLaunchKernelGGL((permute_gather_kernel<T, true>), grid, block, 0, s, static_cast<const T*>(ctx), dest,
                            offsets_end, static_cast<T*>(out), tokens, k, D);
     else

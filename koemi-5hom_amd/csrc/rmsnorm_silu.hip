@@ -13,6 +13,14 @@ namespace koemi {
 namespace {
 
 constexpr int kNormWaves = 4;
+// Cache policy of the grouped forward by the size of x: non-temporal loads of
+// x above KOEMI_NORM_NT_LOAD_BYTES, else non-temporal stores of y above
+// KOEMI_NT_STORE_BYTES (measured at C2, [32768, 512] bf16: 13.4 -> 11.5 us in
+// isolation; non-temporal loads and stores together were slower at both C2
+// and C3).
+#ifndef KOEMI_NORM_NT_LOAD_BYTES
+#define KOEMI_NORM_NT_LOAD_BYTES (int64_t(128) << 20)
+#endif
 
 __device__ __forceinline__ float silu(float v) {
     // v * sigmoid(v) with the hardware exp2 and reciprocal (1 ulp each).
@@ -124,7 +132,7 @@ __device__ __forceinline__ uint4 load16(const void* p) {
     }
 }
 
-template <typename T, int NV, int LPR, bool STREAM>
+template <typename T, int NV, int LPR, bool STREAM, bool NT_STORE>
 __global__ __launch_bounds__(kWave * kNormWaves) void rmsnorm_silu_fwd_group(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y, float* __restrict__ inv_out,
     int64_t rows, int H, float eps) {
@@ -173,7 +181,8 @@ __global__ __launch_bounds__(kWave * kNormWaves) void rmsnorm_silu_fwd_group(
             Vec16<T> o;
 #pragma unroll
             for (int i = 0; i < N; ++i) o.e[i] = from_f32<T>(silu(to_f32(xv[v].e[i]) * inv * to_f32(wv[v].e[i])));
-            *reinterpret_cast<uint4*>(yr + c) = o.raw;
+            if constexpr (NT_STORE) store16_nt(yr + c, o.raw);
+            else *reinterpret_cast<uint4*>(yr + c) = o.raw;
         }
     }
 }
@@ -284,17 +293,23 @@ int launch_forward(const void* x, const void* w, void* y, float* inv, int64_t ro
     hipLaunchKernelGGL((rmsnorm_silu_fwd_wave<T, NV, ROWS>), dim3(grid_for(rows, kNormWaves * ROWS)), wblock, 0, \
                        stream, xp, wp, yp, inv, rows, Hi, eps);                                           \
     return check_launch("koemi_rmsnorm_silu_forward")
-        const bool stream_x = rows * H * static_cast<int64_t>(sizeof(T)) > (int64_t(128) << 20);
+        const int64_t bytes = rows * H * static_cast<int64_t>(sizeof(T));
+        const bool stream_x = bytes > KOEMI_NORM_NT_LOAD_BYTES;
+        const bool nt_store = bytes > KOEMI_NT_STORE_BYTES && !stream_x;  // both together measured slower
 #define KOEMI_NORM_GROUP(NV, LPR)                                                                        \
-    if (stream_x)                                                                                        \
-        hipLaunchKernelGGL((rmsnorm_silu_fwd_group<T, NV, LPR, true>),                                   \
-                           dim3(grid_for(rows, kNormWaves * (kWave / LPR))), wblock, 0, stream, xp, wp, yp, \
-                           inv, rows, Hi, eps);                                                          \
-    else                                                                                                 \
-        hipLaunchKernelGGL((rmsnorm_silu_fwd_group<T, NV, LPR, false>),                                  \
-                           dim3(grid_for(rows, kNormWaves * (kWave / LPR))), wblock, 0, stream, xp, wp, yp, \
-                           inv, rows, Hi, eps);                                                          \
-    return check_launch("koemi_rmsnorm_silu_forward")
+    {                                                                                                    \
+        const dim3 g(grid_for(rows, kNormWaves * (kWave / LPR)));                                        \
+        if (stream_x)                                                                                    \
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_group<T, NV, LPR, true, false>), g, wblock, 0, stream, xp, wp, yp, \
+                               inv, rows, Hi, eps);                                                      \
+        else if (nt_store)                                                                               \
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_group<T, NV, LPR, false, true>), g, wblock, 0, stream, xp, wp, yp, \
+                               inv, rows, Hi, eps);                                                      \
+        else                                                                                             \
+            hipLaunchKernelGGL((rmsnorm_silu_fwd_group<T, NV, LPR, false, false>), g, wblock, 0, stream, xp, wp, yp, \
+                               inv, rows, Hi, eps);                                                      \
+        return check_launch("koemi_rmsnorm_silu_forward");                                              \
+    }
         if (vecs <= 16) { KOEMI_NORM_GROUP(1, 16); }
         if (vecs <= 32) { KOEMI_NORM_GROUP(2, 16); }
         if (vecs <= kWave * 1) { KOEMI_NORM_GROUP(4, 16); }
