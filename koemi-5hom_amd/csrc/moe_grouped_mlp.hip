@@ -211,46 +211,25 @@ __device__ __forceinline__ SplitPlan split_plan(uint32_t tiles, uint32_t nk, uin
 // contiguous range, traversed in groups of kGroupM slots (all column tiles of
 // a group before the next), which keeps the A rows and B columns of
 // concurrently running tiles in that XCD's L2.
+//
+// gemm_tile is one tile: whole (PARTIAL false: all K steps, the epilogue) or
+// a partial unit (K steps [k_begin, k_end), fp32 sums to the workspace); its
+// two instances are inlined into separate branches of the kernel, so each
+// keeps its own register allocation.
 template <bool GLU, bool PARTIAL, int BNT>
-__global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void grouped_gemm_bf16_kernel(
+__device__ __forceinline__ void gemm_tile(
     const bf16* __restrict__ A, const int64_t* __restrict__ a_index, int64_t a_count,
     const bf16* __restrict__ W0, const bf16* __restrict__ W1,
     const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
     const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
-    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
-    float* __restrict__ partial, uint32_t rounds) {
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t n_tiles,
+    float* __restrict__ partial, char* lds, float* bias_sh, uint32_t logical, uint32_t slots, uint32_t unit,
+    uint32_t k_begin, uint32_t k_end) {
     using TS = TileShape<BNT>;
     constexpr int NT = TS::kNT;
     constexpr int kStages = TS::kStages;
     constexpr uint32_t kStageBytes = TS::kStageBytes;
     constexpr int CPT = TS::kCopies;
-    __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
-    __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];
-
-    // Whole tiles (PARTIAL false): the grid covers the most tiles the pairs can
-    // need; the whole tiles of the split plan for the slots actually in use are
-    // spread evenly over the eight XCDs (workgroup b runs on XCD b % 8) and the
-    // surplus workgroups exit. Partial tiles (PARTIAL true): workgroup b takes
-    // unit b of the plan, K steps [k_begin, k_end) of its leftover tile.
-    // `rounds` is the number of workgroups that run at once (CUs x workgroups
-    // per CU).
-    const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
-    const uint32_t nk_all = static_cast<uint32_t>(K / kBK);
-    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), nk_all, rounds);
-    uint32_t logical, unit = 0, k_begin = 0, k_end = nk_all;
-    if constexpr (!PARTIAL) {
-        const uint32_t per_xcd = (plan.whole + 7) / 8;
-        if ((blockIdx.x >> 3) >= per_xcd) return;
-        logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-        if (logical >= plan.whole) return;
-    } else {
-        unit = blockIdx.x;
-        if (unit >= plan.units) return;
-        logical = plan.whole + unit / plan.split;
-        const uint32_t chunk = unit % plan.split;
-        k_begin = chunk * nk_all / plan.split;
-        k_end = (chunk + 1) * nk_all / plan.split;
-    }
     uint32_t slot, tile_n;
     tile_coords(logical, slots, static_cast<uint32_t>(n_tiles), slot, tile_n);
     const int e = slot_expert[slot];
@@ -451,6 +430,52 @@ __global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void groupe
             const int64_t col = out_col0 + c * 8;
             if (grow < row_end && col < n_out) *reinterpret_cast<uint4*>(C + grow * n_out + col) = v[i];
         }
+    }
+}
+
+template <bool GLU, int BNT>
+__global__ __launch_bounds__(kGemmThreads, TileShape<BNT>::kWgPerCu) void grouped_gemm_bf16_kernel(
+    const bf16* __restrict__ A, const int64_t* __restrict__ a_index, int64_t a_count,
+    const bf16* __restrict__ W0, const bf16* __restrict__ W1,
+    const bf16* __restrict__ bias0, const bf16* __restrict__ bias1, bf16* __restrict__ C,
+    const int32_t* __restrict__ slot_expert, const int64_t* __restrict__ slot_row,
+    const int64_t* __restrict__ slot_end, int64_t n_out, int64_t K, int64_t max_slots, int64_t n_tiles,
+    float* __restrict__ partial, uint32_t rounds) {
+    using TS = TileShape<BNT>;
+    constexpr int kStages = TS::kStages;
+    constexpr uint32_t kStageBytes = TS::kStageBytes;
+    __shared__ __attribute__((aligned(1024))) char lds[kStages * kStageBytes];
+    __shared__ __attribute__((aligned(16))) float bias_sh[kGemmThreads];
+
+    // One launch covers both kinds of workgroup. Whole tiles (blockIdx.x <
+    // whole_grid, the most whole tiles the pairs can need, a multiple of 8):
+    // the whole tiles of the split plan for the slots actually in use are
+    // spread evenly over the eight XCDs (workgroup b runs on XCD b % 8) and the
+    // surplus workgroups exit. Partial tiles (the kMaxSplitUnits workgroups
+    // after them, dispatched as the last whole tiles run): workgroup
+    // whole_grid + u takes unit u of the plan, K steps [k_begin, k_end) of its
+    // leftover tile. `rounds` is the number of workgroups that run at once
+    // (CUs x workgroups per CU).
+    const uint32_t slots = static_cast<uint32_t>(min(static_cast<int64_t>(slot_expert[max_slots]), max_slots));
+    const uint32_t nk_all = static_cast<uint32_t>(K / kBK);
+    const SplitPlan plan = split_plan(slots * static_cast<uint32_t>(n_tiles), nk_all, rounds);
+    const uint32_t whole_grid = static_cast<uint32_t>((max_slots * n_tiles + 7) / 8 * 8);
+    const bool partial_unit = blockIdx.x >= whole_grid;
+    if (!partial_unit) {
+        const uint32_t per_xcd = (plan.whole + 7) / 8;
+        if ((blockIdx.x >> 3) >= per_xcd) return;
+        const uint32_t logical = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+        if (logical >= plan.whole) return;
+        gemm_tile<GLU, false, BNT>(A, a_index, a_count, W0, W1, bias0, bias1, C, slot_expert, slot_row, slot_end,
+                                   n_out, K, n_tiles, partial, lds, bias_sh, logical, slots, 0, 0, nk_all);
+    } else {
+        const uint32_t unit = blockIdx.x - whole_grid;
+        if (unit >= plan.units) return;
+        const uint32_t logical = plan.whole + unit / plan.split;
+        const uint32_t chunk = unit % plan.split;
+        gemm_tile<GLU, true, BNT>(A, a_index, a_count, W0, W1, bias0, bias1, C, slot_expert, slot_row, slot_end,
+                                  n_out, K, n_tiles, partial, lds, bias_sh, logical, slots, unit,
+                                  chunk * nk_all / plan.split, (chunk + 1) * nk_all / plan.split);
     }
 }
 
@@ -869,22 +894,17 @@ int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_
     const uint32_t rounds = static_cast<uint32_t>(device_cus() * TileShape<BNT>::kWgPerCu);
     // Whole tiles, then the partial tiles of the split plan (if any; every
     // workgroup exits otherwise), then their sums.
-    auto launch = [&](auto kernel, auto partial_kernel, auto fixup, const bf16* a, const int64_t* a_index,
+    auto launch = [&](auto kernel, auto fixup, const bf16* a, const int64_t* a_index,
                       int64_t a_count, const void* w0, const void* w1, const void* b0, const void* b1, bf16* c,
                       int64_t n_out, int64_t K, int64_t n_tiles, const char* what) {
+        // whole tiles, then the partial units, in one launch
         const int64_t whole_grid = (slots * n_tiles + 7) / 8 * 8;
-        if (whole_grid > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
-        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid)), dim3(kGemmThreads), 0, s, a, a_index,
-                           a_count, static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
-                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
-                           partial, rounds);
+        if (whole_grid + kMaxSplitUnits > 0x7fffffffLL) return fail(KOEMI_ERR_UNSUPPORTED, "too many tiles");
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(whole_grid + kMaxSplitUnits)), dim3(kGemmThreads), 0, s,
+                           a, a_index, a_count, static_cast<const bf16*>(w0), static_cast<const bf16*>(w1),
+                           static_cast<const bf16*>(b0), static_cast<const bf16*>(b1), c, slot_expert, slot_row,
+                           slot_end, n_out, K, slots, n_tiles, partial, rounds);
         int st2 = check_launch(what);
-        if (st2 != KOEMI_OK) return st2;
-        hipLaunchKernelGGL(partial_kernel, dim3(kMaxSplitUnits), dim3(kGemmThreads), 0, s, a, a_index, a_count,
-                           static_cast<const bf16*>(w0), static_cast<const bf16*>(w1), static_cast<const bf16*>(b0),
-                           static_cast<const bf16*>(b1), c, slot_expert, slot_row, slot_end, n_out, K, slots, n_tiles,
-                           partial, rounds);
-        st2 = check_launch(what);
         if (st2 != KOEMI_OK) return st2;
         // At most kMaxSplitUnits / 2 leftover tiles of 8192 (GLU) or 16384 slots.
         hipLaunchKernelGGL(fixup, dim3(1024), dim3(256), 0, s, partial, static_cast<const bf16*>(b0),
@@ -892,12 +912,10 @@ int run_mfma(const void* x, const int64_t* x_index, int64_t x_rows, const int64_
                            n_tiles, rounds);
         return check_launch(what);
     };
-    st = launch(grouped_gemm_bf16_kernel<true, false, BNT>, grouped_gemm_bf16_kernel<true, true, BNT>,
-                split_fixup_kernel<true, BNT>, static_cast<const bf16*>(x), x_index, x_rows, Wg, Wv, bg, bv, H, Hd, D,
+    st = launch(grouped_gemm_bf16_kernel<true, BNT>, split_fixup_kernel<true, BNT>, static_cast<const bf16*>(x), x_index, x_rows, Wg, Wv, bg, bv, H, Hd, D,
                 (Hd + BNT / 2 - 1) / (BNT / 2), "koemi_moe_grouped_mlp(gemm1)");
     if (st != KOEMI_OK) return st;
-    st = launch(grouped_gemm_bf16_kernel<false, false, BNT>, grouped_gemm_bf16_kernel<false, true, BNT>,
-                split_fixup_kernel<false, BNT>, H, static_cast<const int64_t*>(nullptr), P, Wo, Wo, bo, bo,
+    st = launch(grouped_gemm_bf16_kernel<false, BNT>, split_fixup_kernel<false, BNT>, H, static_cast<const int64_t*>(nullptr), P, Wo, Wo, bo, bo,
                 static_cast<bf16*>(y), D, Hd, (D + BNT - 1) / BNT,
                 "koemi_moe_grouped_mlp(gemm2)");
     if (st != KOEMI_OK) return st;
