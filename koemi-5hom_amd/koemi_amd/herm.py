@@ -1110,8 +1110,34 @@ def _surprise_layers(params: list[dict[str, Tensor]], settings: HermSettings, st
     return [(surprise[layer], admission[layer]) for layer in range(layers)]
 
 
+def _carried_logits(params: list[dict[str, Tensor]], states: list[dict[str, Tensor]]) -> list[Tensor] | None:
+    """Every layer's content logits of its carried working state (the
+    surprise of a sequence's first position, network.py:318-325), one batched
+    projection for the stack (``koemi_linear_rows_batched``: the arithmetic of
+    the per-layer ``linear_rows`` call, so the same bits) in place of a launch
+    per layer. None when the stack does not fit it (fp32 heads, more than 32
+    layers, rows the projection does not take)."""
+
+    w16 = [p.get("content_w16") for p in params]
+    carried = [st["working"] for st in states]
+    if len(params) > 32 or any(w is None for w in w16):
+        return None
+    batch, d = carried[0].shape
+    vocab = w16[0].shape[0]
+    if (d % 64 or d > 1024 or batch > linear.MAX_ROWS
+            or any(w.shape != (vocab, d) or not w.is_contiguous() for w in w16)
+            or any(c.shape != (batch, d) or c.dtype != torch.float32 or not c.is_contiguous() for c in carried)):
+        return None
+    device = carried[0].device
+    logits = torch.empty((len(params), batch, vocab), device=device, dtype=torch.float32)
+    _native.call("koemi_linear_rows_batched", _native.ptr_array(carried), _native.dtype_code(torch.float32),
+                 _native.ptr_array(w16), None, _native.ptr(logits), len(params), batch, d, vocab,
+                 _native.stream_of(device))
+    return [logits[layer] for layer in range(len(params))]
+
+
 def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws_low: Tensor, carried: Tensor,
-                    targets: Tensor, valid: Tensor) -> tuple[Tensor, Tensor]:
+                    targets: Tensor, valid: Tensor, first: Tensor | None = None) -> tuple[Tensor, Tensor]:
     """causal_surprise of every position from the state before it (the carried
     state, then the window's own; network.py:318-325, 677-698) and the
     fixed-threshold admission (network.py:349), without forming the shifted
@@ -1119,7 +1145,8 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
     state (fp32 results; bf16 operands for a bf16 stack, the content head under
     bf16 autocast), then one kernel (``koemi_herm_surprise_shifted``) scoring
     row t on the logits of row t - 1 (the carried state's for t = 0). Returns
-    (surprise fp32 [B, L], admission bool [B, L])."""
+    (surprise fp32 [B, L], admission bool [B, L]). ``first``: the carried
+    state's content logits when the caller formed them (``_carried_logits``)."""
 
     batch, length, d = ws.shape
     if length == 1:
@@ -1128,8 +1155,9 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
     if w16 is not None:
         weight_t = w16.t()
         # the carried state's few rows: one kernel (fp32 rows rounded to bf16 as staged)
-        first = linear.linear_rows([carried], w16, None) if _few_rows(carried, w16) else \
-            torch.mm(carried.to(torch.bfloat16), weight_t, out_dtype=torch.float32)
+        if first is None:
+            first = linear.linear_rows([carried], w16, None) if _few_rows(carried, w16) else \
+                torch.mm(carried.to(torch.bfloat16), weight_t, out_dtype=torch.float32)
         logits = torch.mm(ws_low.reshape(batch * length, d), weight_t, out_dtype=torch.float32) if length > 1 \
             else first
     else:
@@ -1149,7 +1177,8 @@ def _surprise_after(p: dict[str, Tensor], settings: HermSettings, ws: Tensor, ws
 def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, state: dict[str, Tensor],
                    context: Tensor | NextInput | None = None, *, with_logits: bool = True,
                    token_context: tuple[Tensor, Tensor, Tensor, Tensor] | None = None,
-                   next_norm: Tensor | None = None, routing: dict | None = None
+                   next_norm: Tensor | None = None, routing: dict | None = None,
+                   carried_logits: Tensor | None = None
                    ) -> tuple[Tensor | None, Tensor | NextInput, dict[str, Tensor], Tensor]:
     """One block over a whole sequence of windows at once: forward_parallel
     (network.py:176-197) of a single block, i.e. ``block_window`` applied to
@@ -1169,8 +1198,10 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     window-by-window ones up to floating-point rounding (the library GEMMs
     see more rows). ``token_context``: ``_token_context``'s four outputs when
     the caller formed them (a stack, once for all layers); ``context``,
-    ``next_norm`` and ``routing`` as in ``block_window``. Returns (logits or None, final
-    context, next state, surprise [B, L]).
+    ``next_norm`` and ``routing`` as in ``block_window``; ``carried_logits``:
+    the content logits of ``state["working"]`` when the caller formed them
+    (``_carried_logits``, one launch for a stack). Returns (logits or None,
+    final context, next state, surprise [B, L]).
     """
 
     ids = ids.contiguous()
@@ -1190,7 +1221,8 @@ def block_sequence(p: dict[str, Tensor], settings: HermSettings, ids: Tensor, st
     working_next = torch.empty((batch, d), device=ids.device, dtype=torch.float32) if _fused_gates(p, u) else None
     scanned = _gated_scan(p, u, valid, state["working"], d, low is not None, _block(fusion_in, 0, d), working_next)
     ws, ws_low = scanned if low is not None else (scanned, scanned)
-    surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid)
+    surprise, admission = _surprise_after(p, settings, ws, ws_low, state["working"], targets, valid,
+                                          carried_logits)
 
     projected = _projection(ws_low, p, "ws")
     # local keys and values read in place from the projection (see block_window)
@@ -1283,11 +1315,15 @@ def stack_sequence(params: list[dict[str, Tensor]], settings: HermSettings, ids:
     next_states = []
     logits = None
     routing: dict = {}  # the hash route, formed by the first layer for all of them
+    # every layer's carried-state content logits in one launch (they depend
+    # only on the starting states)
+    carried = _carried_logits(params, states) if ids.shape[1] > 1 else None
     for layer, (p, state) in enumerate(zip(params, states)):
         last = layer == len(params) - 1
         logits, context, next_state, surprise = block_sequence(
             p, settings, ids, state, context, with_logits=last, token_context=token_context,
-            next_norm=None if last else params[layer + 1]["input_norm"], routing=routing)
+            next_norm=None if last else params[layer + 1]["input_norm"], routing=routing,
+            carried_logits=None if carried is None else carried[layer])
         next_states.append(next_state)
         if surprise_out is not None:
             surprise_out.append(surprise)
