@@ -320,6 +320,33 @@ def test_grouped_mlp_bf16_few_rows_per_expert(device, sizes, D, H):
     assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
 
 
+@pytest.mark.parametrize("E", [64, 65, 90])
+def test_grouped_mlp_bf16_many_experts(device, E):
+    """Many experts, with empty, one-row, whole-tile and ragged segments among
+    them: the tile schedule (per-expert tile counts, their prefix, the
+    expert of every slot) and the tiles against the float64 loop."""
+    g = torch.Generator().manual_seed(E)
+    D, H = 128, 192
+    sizes = torch.randint(0, 420, (E,), generator=g)
+    sizes[::7] = 0
+    sizes[3::11] = 1
+    sizes[5::13] = 256
+    offsets = np.concatenate([[0], np.cumsum(sizes.numpy())])
+    P = int(offsets[-1]) + 6
+    assert P > 64 * E  # the tiled path
+    x = torch.randn((P, D), generator=g).to(torch.bfloat16)
+    experts = torch.full((P,), E, dtype=torch.int64)
+    for e in range(E):
+        experts[offsets[e]:offsets[e + 1]] = e
+    ws = [(0.05 * torch.randn(s, generator=g)).to(torch.bfloat16) for s in ((E, H, D), (E, H), (E, H, D), (E, H), (E, D, H), (E, D))]
+    got = moe.grouped_expert_mlp_inference(x.to(device), experts.to(device), torch.from_numpy(offsets).to(device),
+                                           *(w.to(device) for w in ws))
+    want = oracle.grouped_mlp(x.float().numpy(), experts.numpy(), offsets, *(w.float().numpy() for w in ws),
+                              dtype=np.float32, round_hidden_bf16=True)
+    check_bf16_mlp(got[:offsets[-1]], want[:offsets[-1]], f"grouped MLP bf16 E={E}")
+    assert torch.equal(got[offsets[-1]:].cpu(), torch.zeros_like(got[offsets[-1]:].cpu()))
+
+
 @pytest.mark.parametrize("sizes", [(16640, 16600), (20992, 21208)])
 def test_grouped_mlp_bf16_whole_rounds_and_split_last_round(device, sizes):
     # Width 512 and hidden 256 give two tiles per row slot in both GEMMs. On a
